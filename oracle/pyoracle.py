@@ -1,0 +1,183 @@
+"""ctypes front-end for the two CPU oracles (TEST INFRASTRUCTURE).
+
+  OracleEnv : oracle/liboracle.so, this repo's C restatement of csim
+  RefEnv    : oracle/_ref/libcsim_ref.so, the reference csim compiled from
+              /root/reference (present only where that build ran)
+
+Both expose the same per-env protocol (the reference CPU env's puf_reset /
+puf_step, complete_port/pufferlib_cpu_env.h:187-257) and a threaded batch runner
+used as the CPU baseline. Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import this module.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ORACLE_SO = HERE / "liboracle.so"
+REF_SO = HERE / "_ref" / "libcsim_ref.so"
+SB_OBS, SB_CONT, SB_DISC = 1024, 256, 16
+P = ctypes.c_void_p
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(P)
+
+
+class _Lib:
+    def __init__(self, path: Path, prefix: str):
+        self.lib = ctypes.CDLL(str(path))
+        self.prefix = prefix
+        L = self.lib
+        if prefix == "ref":
+            L.ref_open.restype = P
+            L.ref_open.argtypes = [ctypes.c_char_p, ctypes.c_uint32, ctypes.c_int, ctypes.c_int]
+            self.open_fn = L.ref_open
+            self.close_fn = L.ref_close
+            self.reset_fn, self.step_fn, self.state_fn = L.ref_reset, L.ref_step, L.ref_state
+            self.batch_fn = L.ref_run_batch
+            self.row_fn = L.ref_action_row
+            L.ref_last_reward_f64.restype = ctypes.c_double
+            L.ref_last_reward_f64.argtypes = [P]
+            for f in (L.ref_obs_len, L.ref_n_cont, L.ref_n_disc, L.ref_n_cvs):
+                f.argtypes = [P]
+            L.ref_native.argtypes = [P, P]
+            L.ref_parts.argtypes = [P, P]
+            L.ref_log.argtypes = [P, P]
+            L.ref_clear_log.argtypes = [P]
+        else:
+            L.sbo_scen_open.argtypes = [P, ctypes.c_char_p]
+            L.sbo_scen_close.argtypes = [P]
+            L.sbo_env_new.restype = P
+            L.sbo_env_new.argtypes = [P, ctypes.c_uint32, ctypes.c_int, ctypes.c_int]
+            self.close_fn = L.sbo_env_free
+            self.reset_fn, self.step_fn, self.state_fn = L.sbo_env_reset, L.sbo_env_step, L.sbo_env_state
+            self.batch_fn = L.sbo_run_batch
+            self.row_fn = L.sbo_action_row
+            L.sbo_mt_seed.argtypes = [P, ctypes.c_uint32]
+            L.sbo_mt_u32.argtypes = [P]
+            L.sbo_mt_u32.restype = ctypes.c_uint32
+            L.sbo_mt_double.argtypes = [P]
+            L.sbo_mt_double.restype = ctypes.c_double
+        self.close_fn.argtypes = [P]
+        self.reset_fn.argtypes = [P, P]
+        self.step_fn.argtypes = [P, P, P, P, P]
+        self.step_fn.restype = ctypes.c_int
+        self.state_fn.argtypes = [P, P]
+        self.state_fn.restype = ctypes.c_int
+        self.batch_fn.argtypes = [P, P, ctypes.c_int, ctypes.c_int, ctypes.c_uint64, ctypes.c_int, P]
+        self.batch_fn.restype = ctypes.c_double
+        self.row_fn.argtypes = [ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32,
+                                ctypes.c_int, ctypes.c_int, P]
+
+
+_LIBS: dict[str, _Lib] = {}
+
+
+def lib(kind: str) -> _Lib:
+    if kind not in _LIBS:
+        path = REF_SO if kind == "ref" else ORACLE_SO
+        if not path.exists():
+            raise FileNotFoundError(f"{path} is not built (run __graft_entry__.build())")
+        _LIBS[kind] = _Lib(path, "ref" if kind == "ref" else "sbo")
+    return _LIBS[kind]
+
+
+def ref_available() -> bool:
+    return REF_SO.exists()
+
+
+class _Scen:
+    """Keeps one oracle scenario (SboScen) alive for the envs that share it."""
+
+    SIZE = 65536
+
+    def __init__(self, path: str):
+        self.buf = ctypes.create_string_buffer(self.SIZE)
+        L = lib("oracle").lib
+        if L.sbo_scen_open(ctypes.addressof(self.buf), str(path).encode()) != 0:
+            raise RuntimeError(f"oracle cannot open {path}")
+        self.path = str(path)
+
+    def __del__(self):
+        try:
+            lib("oracle").lib.sbo_scen_close(ctypes.addressof(self.buf))
+        except Exception:
+            pass
+
+
+_SCEN_CACHE: dict[str, _Scen] = {}
+
+
+def scenario(path) -> _Scen:
+    key = str(path)
+    if key not in _SCEN_CACHE:
+        _SCEN_CACHE[key] = _Scen(key)
+    return _SCEN_CACHE[key]
+
+
+class CpuEnv:
+    """One env of either oracle, stepping with the reference CPU env protocol."""
+
+    def __init__(self, kind: str, path, occ_seed: int, start: int = 0, max_steps: int = 8640):
+        self.kind = kind
+        self.L = lib(kind)
+        if kind == "ref":
+            self.h = self.L.open_fn(str(path).encode(), occ_seed, start, max_steps)
+            self.n_cont = self.L.lib.ref_n_cont(self.h)
+            self.n_disc = self.L.lib.ref_n_disc(self.h)
+        else:
+            self.scen = scenario(path)
+            self.h = self.L.lib.sbo_env_new(ctypes.addressof(self.scen.buf), occ_seed, start, max_steps)
+            # n_cont / n_disc from the blob through the action table
+            from neurips2026_smart_building_challenge_amd.scenario.sbb import read_sbb
+            d = read_sbb(path)
+            disc = d["act_is_discrete"]
+            self.n_cont = int((disc == 0).sum())
+            self.n_disc = int((disc == 1).sum())
+        if not self.h:
+            raise RuntimeError(f"cannot open env on {path}")
+        self.obs = np.zeros(SB_OBS, np.float32)
+        self._r = np.zeros(1, np.float32)
+        self._t = np.zeros(1, np.float32)
+        self._st = np.zeros(8192, np.float64)
+
+    def close(self):
+        if self.h:
+            self.L.close_fn(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+    def reset(self) -> np.ndarray:
+        self.L.reset_fn(self.h, _ptr(self.obs))
+        return self.obs.copy()
+
+    def step(self, action_row: np.ndarray):
+        a = np.ascontiguousarray(action_row, dtype=np.float32)
+        done = self.L.step_fn(self.h, _ptr(a), _ptr(self.obs), _ptr(self._r), _ptr(self._t))
+        return self.obs.copy(), float(self._r[0]), float(self._t[0]), bool(done)
+
+    def state(self) -> np.ndarray:
+        n = self.L.state_fn(self.h, _ptr(self._st))
+        return self._st[:n].copy()
+
+
+def action_row(seed: int, env: int, step: int, n_cont: int, n_disc: int, kind: str = "oracle") -> np.ndarray:
+    row = np.zeros(SB_CONT + SB_DISC, np.float32)
+    lib(kind).row_fn(seed, env, step, n_cont, n_disc, _ptr(row))
+    return row
+
+
+def run_batch(envs: list[CpuEnv], env_ids, steps: int, seed: int, nthreads: int) -> tuple[float, float]:
+    """Steps every env `steps` times on `nthreads` threads; returns (seconds, reward_sum)."""
+    kind = envs[0].kind
+    arr = (P * len(envs))(*[e.h for e in envs])
+    ids = np.ascontiguousarray(env_ids, dtype=np.int32)
+    acc = np.zeros(1, np.float64)
+    secs = lib(kind).batch_fn(ctypes.cast(arr, P), _ptr(ids), len(envs), steps, seed, nthreads, _ptr(acc))
+    return float(secs), float(acc[0])

@@ -1,0 +1,158 @@
+/* sbo: a plain-C restatement of the reference CPU core ("csim") for the
+ * Smart Buildings env step, used as the parity oracle of the HIP path.
+ *
+ * TEST INFRASTRUCTURE. Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load liboracle.so; the product never links it.
+ *
+ * Scope: the synthetic RC scenarios of this repo (every cell solved, rooms made
+ * of cells, air side given as applied/sensed sparse columns, convection off).
+ * Each function cites the reference function it restates, and keeps that
+ * function's floating-point operation order so that the result is bit-identical
+ * to the reference compiled with the same compiler flags (checked against
+ * oracle/_ref and the committed golden fixtures).
+ */
+#ifndef SBO_H
+#define SBO_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SBO_OBS 1024
+#define SBO_CONT 256
+#define SBO_DISC 16
+
+/* ---------------- blob ---------------- */
+typedef struct {
+    const char* name;
+    uint32_t dtype;
+    uint64_t count;
+    const void* data;
+} SboSec;
+
+typedef struct {
+    uint8_t* bytes;
+    uint64_t size;
+    int n;
+    SboSec* sec;
+} SboBlob;
+
+int sbo_blob_load(SboBlob* b, const char* path);
+void sbo_blob_free(SboBlob* b);
+const SboSec* sbo_sec(const SboBlob* b, const char* name);
+const double* sbo_f64(const SboBlob* b, const char* name);
+const int64_t* sbo_i64(const SboBlob* b, const char* name);
+const int32_t* sbo_i32(const SboBlob* b, const char* name);
+const uint8_t* sbo_u8(const SboBlob* b, const char* name);
+double sbo_f64_1(const SboBlob* b, const char* name, double dflt);
+int64_t sbo_i64_1(const SboBlob* b, const char* name, int64_t dflt);
+
+/* ---------------- scenario (read-only, shared by the envs of a blob) -------- */
+typedef struct {
+    SboBlob blob;
+    int nr, nc, n_cvs, n, k, n_ahu, n_vav, n_zones, n_rooms, n_act, n_dev, n_aux;
+    const int64_t* solved;
+    const double *cap, *dir, *mcoup, *mret, *mgain, *temp_init, *mass_init;
+    const double *horiz, *vert, *cond, *face0, *face1;
+    double h;
+    /* baked LU (SuperLU convention) */
+    const int32_t *Lp, *Li, *Up, *Ui;
+    const double *Lx, *Ux;
+    int *Ldiag, *Udiag, *ir, *pc;
+    /* air side */
+    const int32_t *ap_p, *ap_i, *sn_p, *sn_i;
+    const double *ap_x, *sn_x;
+    double* S;        /* k x k sensed * A^-1 * applied */
+    /* HVAC topology / constants */
+    const int32_t *vz_off, *vz_idx, *vav_ahu, *coupled, *phys_room, *room_off, *room_cells;
+    const int32_t *zv_off, *zv_idx;
+    const double *zone_area, *ahu_c, *vav_c;
+    double boiler_c[10], pump_head0, pump_eff, header_res;
+    double internal_w_m2, standby_frac, occupant_w, cv_area, dt_sec;
+    /* actions */
+    const uint8_t *act_kind, *act_act, *act_disc;
+    const int32_t* act_idx;
+    const double *act_mn, *act_mx, *act_mnr, *act_mxr;
+    int n_cont, n_disc;
+    /* calendar / weather */
+    const double *amb, *comfort, *heat_sp, *cool_sp, *solar_i, *solar_c, *aux_time;
+    const int64_t *occ_hour, *hour_m1, *rew_hour, *rew_month;
+    const uint8_t *occ_work, *work_m1, *rew_work;
+    int occ_assign, occ_ea, occ_la, occ_ed, occ_ld;
+    double p_arr, p_dep;
+    int64_t occ_seed;
+    /* observation */
+    const uint8_t *f_kind, *f_id;
+    const int32_t* f_idx;
+    const double *f_mean, *f_var;
+    /* reward */
+    const double *rw, *elec_wk, *elec_we, *elec_co2, *gas_price;
+    double gas_co2;
+    uint8_t* is_room;
+    int episode_steps;
+} SboScen;
+
+int sbo_scen_open(SboScen* s, const char* path);
+void sbo_scen_close(SboScen* s);
+
+/* ---------------- per-env state ---------------- */
+typedef struct {
+    uint32_t mt[624];
+    int idx;
+} SboMt;
+
+typedef struct {
+    const SboScen* sc;
+    /* field */
+    double *T, *M;
+    /* AHU */
+    int *ahu_run, *ahu_coolreq;
+    double *ahu_recirc, *ahu_sat, *ahu_fan, *ahu_flow, *ahu_wsum, *ahu_atotal, *ahu_satv;
+    /* VAV */
+    double *damper, *reheat, *ratio, *heatsp, *coolsp, *dcmd, *rcmd, *sensing, *vav_area;
+    int *mode, *prev_valid, *dcmd_set, *rcmd_set;
+    /* zones / coupled columns */
+    double *avg_temp, *zone_q, *input_q, *air_g, *air_T, *coil;
+    /* plant */
+    double flow_factor_sum, pump_head, total_reheat;
+    int hws_requests, hws_run, pump_run;
+    double boiler_sp, boiler_ret, boiler_cur, boiler_dstep;
+    int step_index;
+    /* occupancy */
+    uint8_t* occ_state;
+    double* occV;
+    SboMt mt;
+    /* scratch */
+    double *rhs, *y, *yr, *r, *work, *power, *mat;
+    /* bookkeeping (pufferlib_cpu_env.h Env) */
+    int step, max_steps, start;
+    float log[6];
+    double native[SBO_CONT + SBO_DISC];
+    double parts[12];
+    double last_rew;
+    float obs[SBO_OBS];
+} SboEnv;
+
+SboEnv* sbo_env_new(const SboScen* sc, uint32_t occ_seed, int start, int max_steps);
+void sbo_env_free(SboEnv* e);
+void sbo_env_reset(SboEnv* e, float* obs_out);
+int sbo_env_step(SboEnv* e, const float* actions, float* obs_out, float* reward, float* terminal);
+int sbo_env_state(const SboEnv* e, double* out);
+
+/* core pieces (exposed for unit tests) */
+void sbo_mt_seed(SboMt* r, uint32_t seed);
+uint32_t sbo_mt_u32(SboMt* r);
+double sbo_mt_double(SboMt* r);
+void sbo_decode(const SboScen* sc, const double* cont, const double* disc, double* native);
+void sbo_lu_solve(const SboScen* sc, const double* b, double* x, double* work);
+int sbo_dense_solve(int k, double* M, double* b);
+
+double sbo_run_batch(SboEnv** envs, const int* env_ids, int n, int steps, uint64_t seed,
+                     int nthreads, double* reward_sum);
+void sbo_action_row(uint64_t seed, uint32_t env, uint32_t step, int n_cont, int n_disc, float* row);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
