@@ -1,0 +1,188 @@
+"""Benchmark of the MI355X env step: env-steps/s at 960 mixed envs (fp64 physics).
+
+    python bench.py [--steps K] [--warmup W] [--config 1] [--gpus 1] [--no-cpu]
+
+Workload (BASELINE config index 1): 960 envs over 30 seeded synthetic scenarios
+(6 layouts of 41..81 zones x 5 climates, 32 envs each), Beta(2,2) actions from
+the on-device counter RNG, fp64 physics. One timed step = sbx_gen_actions (the
+policy stand-in) + puf_step over all envs, inputs resident in HBM. K defaults to
+a full 8,640-step episode.
+
+roofline: algorithmic HBM bytes of one puf_step (per-env state record read and
+written, action row read, observation row + reward + terminal written; the
+shared per-layout/per-scenario tables are cache-resident and not counted)
+divided by the step kernel's average duration from HIP events recorded around
+back-to-back launches on the bound stream. traffic: measured HBM bytes per
+launch from rocprofv3 FETCH_SIZE/WRITE_SIZE when profiles/ holds them.
+
+cpu_baseline: the reference csim core (oracle/_ref, compiled from the
+reference sources) or, where it was not built, this repo's C restatement,
+stepping the same 960 envs on the host's cores (whole envs per thread) for a
+bounded number of steps.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import tempfile
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "env-steps/sec at 960 mixed envs (fp64 physics); % of HBM roofline"
+HBM_PEAK_GBS = 8000.0
+SEED = 20260601
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def scenario_dir(config: int) -> Path:
+    from neurips2026_smart_building_challenge_amd.scenario import generate as G
+
+    d = Path(tempfile.gettempdir()) / f"sbenv_bench_cfg{config}"
+    G.write_config(config, d)
+    return d
+
+
+def measured_traffic(config: int):
+    p = ROOT / "profiles" / f"step_kernel_traffic_cfg{config}.json"
+    if p.exists():
+        try:
+            return float(json.loads(p.read_text())["hbm_bytes_per_launch"])
+        except Exception:
+            return None
+    return None
+
+
+def cpu_baseline(blob_dir: Path, n_envs: int, groups: int, target_s: float, threads: int) -> dict:
+    sys.path.insert(0, str(ROOT / "oracle"))
+    import pyoracle as po
+    from neurips2026_smart_building_challenge_amd.scenario import generate as G
+    from neurips2026_smart_building_challenge_amd.scenario.sbb import read_sbb
+
+    kind = "ref" if po.ref_available() else "oracle"
+    paths = sorted(blob_dir.glob("*.sbb"))
+    # same assignment as the GPU vec: round-robin over buildings, n/G envs per scenario
+    blds = []
+    for p in paths:
+        b = p.name.split("__")[0]
+        if b not in blds:
+            blds.append(b)
+    ordered, used = [], set()
+    while len(ordered) < len(paths):
+        for b in blds:
+            for p in paths:
+                if p not in used and p.name.split("__")[0] == b:
+                    ordered.append(p)
+                    used.add(p)
+                    break
+    ordered = ordered[:groups]
+    envs, ids = [], []
+    for g, p in enumerate(ordered):
+        seed0 = int(read_sbb(p)["occ_seed"][0])
+        cnt = n_envs // groups + (1 if g < n_envs % groups else 0)
+        for j in range(cnt):
+            e = po.CpuEnv(kind, p, seed0 + j, start=0, max_steps=G.EPISODE_STEPS)
+            e.reset()
+            envs.append(e)
+            ids.append(len(ids))
+    secs, _ = po.run_batch(envs, ids, 4, SEED, threads)          # calibration
+    per_step = secs / 4
+    steps = max(4, min(G.EPISODE_STEPS, int(target_s / max(per_step, 1e-9))))
+    secs, _ = po.run_batch(envs, ids, steps, SEED + 1, threads)
+    for e in envs:
+        e.close()
+    return {"value": n_envs * steps / secs, "unit": "env-steps/s", "cores": threads,
+            "kind": "reference" if kind == "ref" else "port",
+            "sample": f"{n_envs} envs of the same workload x {steps} steps ({secs:.1f} s) on {threads} threads, "
+                      f"{'reference csim compiled from its sources' if kind == 'ref' else 'C restatement of csim'}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=8640)
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--config", type=int, default=1)
+    ap.add_argument("--kernel-iters", type=int, default=1000)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        log("bench.py measures one GPU: the env step has no cross-GPU exchange and this build runs "
+            "on a single MI355X; --gpus above 1 is not supported")
+        return 2
+
+    import torch
+
+    from neurips2026_smart_building_challenge_amd import env as E
+    from neurips2026_smart_building_challenge_amd.scenario import generate as G
+
+    scen, n_envs, desync = G.config_scenarios(args.config)
+    groups = len(scen)
+    t0 = time.time()
+    blob_dir = scenario_dir(args.config)
+    log(f"scenarios ready in {time.time() - t0:.1f}s: {blob_dir}")
+    vec = E.VecEnv(n_envs, blob_dir=str(blob_dir), groups=groups, desync=int(desync))
+    info = vec.info()
+    vec.reset()
+    for s in range(args.warmup):
+        vec.gen_actions(SEED, s)
+        vec.step()
+    torch.cuda.synchronize()
+    log(f"warmup done ({args.warmup} steps)")
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    for s in range(args.steps):
+        vec.gen_actions(SEED, args.warmup + s)
+        vec.step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1)
+    ms_per_step = ms / args.steps
+    value = n_envs * args.steps / (ms / 1e3)
+    log(f"timed {args.steps} steps: {ms_per_step * 1e3:.1f} us/step, {value:.4g} env-steps/s")
+    k_iters = max(1, args.kernel_iters)
+    k_ms = vec.time_step(k_iters) / k_iters
+    achieved = info.bytes_per_step / (k_ms * 1e-3) / 1e9
+    log(f"step kernel: {k_ms * 1e3:.1f} us/launch, {info.bytes_per_step / 1e6:.2f} MB algorithmic -> "
+        f"{achieved:.1f} GB/s")
+    traffic = measured_traffic(args.config)
+    vec.close()
+
+    cpu = None
+    if not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        log(f"cpu baseline on {threads} threads ...")
+        cpu = cpu_baseline(blob_dir, n_envs, groups, args.cpu_seconds, threads)
+        log(f"cpu baseline: {cpu['value']:.4g} env-steps/s ({cpu['kind']})")
+
+    out = {
+        "metric": METRIC, "value": value, "unit": "env-steps/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f64", "data": "synthetic",
+        "config": {"workload": f"BASELINE config {args.config}: {n_envs} envs, {groups} scenarios "
+                               f"({len({s[0].zones for s in scen})} layouts x {len({s[1].name for s in scen})} "
+                               f"climates), Beta(2,2) actions, fp64 physics"
+                               + (", desynchronised starts" if desync else ""),
+                   "n_envs": n_envs, "scenarios": groups, "episode_steps": G.EPISODE_STEPS,
+                   "block": info.block, "lds_bytes": info.lds_bytes},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "kernel_us": k_ms * 1e3, "algorithmic_bytes": info.bytes_per_step},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,195 @@
+/* sbenv: MI355X-native batched Smart Buildings environment step.
+ *
+ * C ABI of the PufferLib "ocean" env binding for the Smart Buildings env, GPU
+ * backend (PUF_BACKEND == PUF_GPU). Every entry point below replaces the
+ * reference function of the same name:
+ *
+ *   puf_vec_create  complete_port/gpu/smart_buildings.cu:2497 (impl), :3311 (export)
+ *   puf_bind_stream complete_port/gpu/smart_buildings.cu:2887, :3314
+ *   puf_init        complete_port/gpu/smart_buildings.cu:2891, :3315
+ *                   (CPU env: complete_port/pufferlib_cpu_env.h:293)
+ *   puf_reset       complete_port/gpu/smart_buildings.cu:2896, :3316
+ *                   (CPU env: complete_port/pufferlib_cpu_env.h:187)
+ *   puf_step        complete_port/gpu/smart_buildings.cu:2979, :3317
+ *                   (CPU env: complete_port/pufferlib_cpu_env.h:211)
+ *   puf_render      complete_port/gpu/smart_buildings.cu:3318 (no-op)
+ *   puf_close       complete_port/gpu/smart_buildings.cu:3319
+ *   puf_log         complete_port/gpu/smart_buildings.cu:3320
+ *                   (CPU env keys: complete_port/pufferlib_cpu_env.h:284-291)
+ *   puf_live_log    complete_port/gpu/smart_buildings.cu:3069, :3321
+ *   puf_mask_init   complete_port/gpu/smart_buildings.cu:3230, :3322
+ *
+ * Buffers: the trainer owns obs [n x SB_OBS] f32, actions [n x (SB_CONT+SB_DISC)]
+ * f32, rewards [n] f32 and terminals [n] f32, all device memory; the env writes
+ * them in place. All device work runs on the stream given to puf_bind_stream
+ * (hipStream_t; NULL = the null stream) and puf_step neither allocates nor
+ * synchronises, so it can be captured in a hipGraph. Errors print to stderr and
+ * abort(), as the reference does (pufferlib_cpu_env.h:189-190, 316-321).
+ *
+ * PufferLib's own pufferenv.h is not part of the reference; the Agent / Dict
+ * layouts here carry the fields the reference env uses (observations, actions,
+ * rewards, terminals, action_mask, policy; dict_find / dict_set) and are this
+ * build's stated assumption about that header.
+ */
+#ifndef SBENV_H
+#define SBENV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SB_OBS 1024
+#define SB_CONT 256
+#define SB_DISC 16
+#define SB_ACT (SB_CONT + SB_DISC)
+#define SB_MASK_WIDTH (SB_CONT + 2 * SB_DISC)
+#define OBS_SIZE SB_OBS
+#define NUM_ATNS SB_ACT
+
+typedef float obs_t;
+
+/* Episode log, complete_port/pufferlib_cpu_env.h:82-89 (n is the last field). */
+typedef struct Log {
+    float perf;
+    float score;
+    float episode_return;
+    float episode_length;
+    float reward_mean;
+    float n;
+} Log;
+
+typedef struct Agent {
+    obs_t* observations;
+    float* actions;
+    float* rewards;
+    float* terminals;
+    unsigned char* action_mask;
+    int policy;
+} Agent;
+
+/* complete_port/pufferlib_cpu_env.h:91-121 (Log first, no pointers into Env). */
+typedef struct Env {
+    Log log;
+    Agent agents[1];
+    int num_agents;
+    int tag;
+    int boundary_reached;
+    int step;
+    int max_steps;
+    int start_offset;
+    int n_act, n_cont, n_disc;
+    int loaded;
+    unsigned int rng;
+    int seed;
+    int index;          /* position in the vec */
+    void* vec;          /* owning vec (opaque) */
+} Env;
+
+typedef struct DictItem {
+    const char* key;
+    float value;
+    const char* str;
+} DictItem;
+
+typedef struct Dict {
+    DictItem* items;
+    int size;
+    int capacity;
+} Dict;
+
+/* Dict helpers with the semantics the reference env relies on. */
+DictItem* dict_find(Dict* d, const char* key);
+void dict_set(Dict* d, const char* key, float value);
+
+/* ---- PufferLib env ABI ---- */
+Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions,
+                    float* rewards, float* terminals);
+void puf_bind_stream(void* stream /* hipStream_t */);
+void puf_init(Env* env, Dict* kwargs);
+void puf_reset(Env* envs);
+void puf_step(Env* envs);
+void puf_render(Env* env);
+void puf_close(Env* envs);
+void puf_log(Log* log, Dict* out);
+void puf_live_log(Env* envs, Dict* out);
+void puf_mask_init(unsigned char* mask, int width, int nagents);
+
+/* ---- extras (no reference counterpart) ---- */
+
+/* Writes one Beta(2,2) action row per env into the vec's action buffer on the
+ * bound stream: Philox4x32-10 keyed by `seed`, counter (env, step, slot, 0),
+ * median of three U(0,1); continuous slots get 2x-1, discrete slots x > 0.5.
+ * The synthetic stand-in for a policy in benchmarks and parity tests. */
+void sbx_gen_actions(Env* envs, uint64_t seed, uint32_t step);
+
+typedef struct SbxVecInfo {
+    int n_envs;
+    int n_layouts;
+    int n_scenarios;
+    int block;              /* threads per env workgroup */
+    int lds_bytes;          /* dynamic LDS per workgroup */
+    int max_nodes;
+    double bytes_per_step;  /* algorithmic HBM bytes of one puf_step (all envs) */
+    double flops_per_step;  /* fp64 flops of one puf_step's solves (all envs) */
+} SbxVecInfo;
+void sbx_vec_info(Env* envs, SbxVecInfo* out);
+
+/* Synchronous snapshot of env `i` in the oracle's state order (temp, mass,
+ * VAV damper/reheat/ratio/sensing, AHU flow/sat/recirc/fan, air_g, air_T,
+ * occupancy, boiler current/return/setpoint, pump head, calendar index),
+ * followed by two extras: the f64 sum of rewards and the number of steps since
+ * puf_reset. air_g / air_T are not kept between steps and read as NaN.
+ * Returns the number of doubles written (<= cap), or -1. */
+int sbx_env_state(Env* envs, int i, double* out, int cap);
+
+/* Launches the step kernel `iters` times back to back between two HIP events
+ * on the bound stream and returns the elapsed milliseconds (synchronises). */
+float sbx_time_step(Env* envs, int iters);
+
+/* Scenario of env i (index into the sorted, round-robin ordered blob list),
+ * its calendar start offset and occupancy seed. */
+int sbx_env_meta(Env* envs, int i, int* scenario, int* start, uint32_t* occ_seed);
+const char* sbx_scenario_path(Env* envs, int scenario);
+
+/* Host-side solve plan of one blob's layout (no GPU needed): the level
+ * schedule the step kernel runs for the numeric LU of A + diag(g) plus both
+ * triangular solves. Pass p is pass_info[8p..8p+4] = {hdr_off, word_off, nact,
+ * maxcnt, row_off}: lanes 0..nact-1 run the tasks hdr[hdr_off + lane]
+ * (target | divisor << 16 | count << 32), and term m of lane l is
+ * words[word_off + row_off_m + l] with row_off_m = row_off[row_off + m].
+ * Arrays are owned by the library until sbx_plan_free. */
+typedef struct SbxPlan {
+    int n;               /* unknowns */
+    int width;           /* lanes per pass */
+    int n_slots;         /* LDS value slots: 0 = zero, 1 = sink, LU, vector */
+    int vec_base;        /* first vector slot */
+    int n_pass;
+    int n_levels;
+    int n_tasks;
+    int kmax;            /* max terms per task */
+    long long n_pairs;   /* multiply-subtract terms */
+    int n_hdr, n_words, n_rows;
+    const int* pass_info;        /* [n_pass * 8] */
+    const int* row_off;          /* [n_rows] */
+    const uint64_t* hdr;         /* [n_hdr] */
+    const uint32_t* words;       /* [n_words]: a | b << 16 */
+    const double* slot_init;     /* [n_slots] A values at LU slots, 0 elsewhere */
+    const int* pos;              /* [n] node -> permuted position */
+    const int* air_slot;         /* [k] LU slot of the coupled air diagonal */
+    const int* air_node;         /* [k] node of coupled column c */
+    int k;
+} SbxPlan;
+int sbx_plan_layout(const char* blob_path, int width, SbxPlan* out);
+void sbx_plan_free(SbxPlan* p);
+
+/* Message of the last failing sbx_* call. */
+const char* sbx_last_error(void);
+const char* sbx_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,73 @@
+"""Builds the HIP env library (gfx950) and, for tests only, the CPU oracles.
+
+    python -m neurips2026_smart_building_challenge_amd.build
+
+Outputs, in-tree so they travel with the repository snapshot:
+    neurips2026_smart_building_challenge_amd/libsbenv.so   product (HIP + C ABI)
+    oracle/liboracle.so                                    C restatement (tests)
+    oracle/_ref/libcsim_ref.so                             reference csim (tests,
+                                                           only where /root/reference exists)
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+CSRC = PKG / "csrc"
+LIB = PKG / "libsbenv.so"
+ARCH = os.environ.get("SBENV_ARCH", "gfx950")
+REF_CSIM = Path("/root/reference/complete_port/csim")
+
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function",
+]
+
+
+def _run(cmd: list[str], cwd: Path | None = None) -> None:
+    r = subprocess.run(cmd, cwd=cwd, capture_output=True, text=True)
+    if r.returncode != 0:
+        sys.stderr.write(r.stdout + r.stderr)
+        raise RuntimeError(f"build step failed: {' '.join(cmd[:3])} ...")
+
+
+def build_product() -> Path:
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    objs = []
+    tmp = PKG / "_build"
+    tmp.mkdir(exist_ok=True)
+    inc = ["-I", str(ROOT / "include"), "-I", str(CSRC)]
+    for src in ["step_kernel.hip"]:
+        o = tmp / (Path(src).stem + ".o")
+        _run([hipcc, *HIP_FLAGS, *inc, "-c", str(CSRC / src), "-o", str(o)])
+        objs.append(o)
+    for src in ["vec.cpp", "plan.cpp", "sbb_reader.cpp"]:
+        o = tmp / (Path(src).stem + ".o")
+        _run([hipcc, "-O2", "-std=c++17", "-fPIC", "-Wall", *inc, "-c", str(CSRC / src), "-o", str(o)])
+        objs.append(o)
+    out_tmp = LIB.with_suffix(".so.tmp")
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(out_tmp)])
+    out_tmp.replace(LIB)
+    return LIB
+
+
+def build_oracles() -> None:
+    _run(["make", "-s", "-C", str(ROOT / "oracle"), "oracle"])
+    if REF_CSIM.is_dir():
+        _run(["make", "-s", "-C", str(ROOT / "oracle"), "ref", f"REF={REF_CSIM}"])
+
+
+def build() -> None:
+    build_product()
+    build_oracles()
+
+
+if __name__ == "__main__":
+    build()
+    print("built", LIB)

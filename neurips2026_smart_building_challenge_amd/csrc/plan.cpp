@@ -1,0 +1,283 @@
+// Solve planner.
+//
+// The reference csim replays baked factors of A (complete_port/csim/sb_lu.c)
+// and folds the air side in with a dense k x k solve (sb_fdm.c:153-181). The
+// device instead refactorizes S = P (A + P_a G S_a) P^T every step in the
+// baked permutation P, whose fill pattern equals the baked one because G only
+// touches diagonal entries. Each entry of L and U is one "task" (Crout form):
+//
+//   U[i][j] = S[i][j] - sum_{k<i} L[i][k] U[k][j]             (i <= j)
+//   L[i][j] = (S[i][j] - sum_{k<j} L[i][k] U[k][j]) / U[j][j]  (i >  j)
+//
+// and the solves reuse the same machinery on a vector of slots:
+//
+//   y_i = w_i - sum_{k<i} L[i][k] y_k                          (forward)
+//   x_i = (y_i - sum_{j>i} U[i][j] x_j) / U[i][i]              (backward, in place)
+//
+// A task's level is one more than the levels of everything it reads; tasks of
+// one level are independent, sorted by term count (descending) and cut into
+// passes of `width` lanes. A pass stores one 64-bit header per active lane and
+// its terms row by row: row m holds term m of every lane whose count exceeds m
+// (a prefix of the lanes, by the sort), so each row is one coalesced read.
+// Dot products longer than kPlanKmax terms become a chain of tasks on the same
+// slot; only the last one divides.
+#include "plan.h"
+
+#include <algorithm>
+#include <unordered_map>
+
+namespace sbh {
+
+namespace {
+
+struct Task {
+    int target;
+    int divisor;      // 0 = none
+    int level;
+    std::vector<std::pair<int, int>> terms;
+};
+
+bool fail(std::string* err, const std::string& msg) {
+    *err = msg;
+    return false;
+}
+
+}  // namespace
+
+bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
+    SolvePlan& P = *out;
+    P = SolvePlan();
+    P.width = width;
+    uint64_t ns = 0, cnt = 0;
+    const int64_t* solved = b.i64("solved", &ns);
+    const int64_t* grid = b.i64("grid");
+    if (!solved || !grid) return fail(err, "blob lacks grid/solved");
+    const int n = (int)ns;
+    if ((int64_t)n != grid[0] * grid[1]) return fail(err, "only blobs with every cell solved are supported");
+    for (int t = 0; t < n; t++)
+        if (solved[t] != t) return fail(err, "solved cells must be 0..n-1 in order");
+    P.n = n;
+
+    const int32_t* Ap = b.i32("A_system_indptr", &cnt);
+    if (!Ap || (int)cnt != n + 1) return fail(err, "blob lacks A_system (CSC n x n)");
+    const int32_t* Ai = b.i32("A_system_indices");
+    const double* Ax = b.f64("A_system_data");
+    const int32_t* pr = b.i32("lu_perm_r", &cnt);
+    const int32_t* pc = b.i32("lu_perm_c");
+    if (!pr || !pc || (int)cnt != n) return fail(err, "blob lacks lu_perm_r/lu_perm_c");
+    P.pos.assign(pc, pc + n);
+    std::vector<int> q(n, -1);
+    for (int t = 0; t < n; t++) {
+        if (pr[t] != pc[t]) return fail(err, "row and column permutations differ (pivoting is not supported)");
+        if (pc[t] < 0 || pc[t] >= n || q[pc[t]] >= 0) return fail(err, "lu_perm_c is not a permutation");
+        q[pc[t]] = t;
+    }
+    const int32_t* Lp = b.i32("lu_L_indptr", &cnt);
+    if (!Lp || (int)cnt != n + 1) return fail(err, "blob lacks lu_L");
+    const int32_t* Li = b.i32("lu_L_indices");
+    const int32_t* Up = b.i32("lu_U_indptr", &cnt);
+    if (!Up || (int)cnt != n + 1) return fail(err, "blob lacks lu_U");
+    const int32_t* Ui = b.i32("lu_U_indices");
+
+    // structural pattern in permuted coordinates
+    std::vector<std::vector<int>> Lcol(n), Lrow(n), Ucol(n), Urow(n);   // strict parts
+    for (int j = 0; j < n; j++) {
+        bool diagL = false, diagU = false;
+        for (int p = Lp[j]; p < Lp[j + 1]; p++) {
+            int i = Li[p];
+            if (i == j) diagL = true;
+            else if (i > j && i < n) { Lcol[j].push_back(i); Lrow[i].push_back(j); }
+            else return fail(err, "lu_L has an entry above the diagonal");
+        }
+        for (int p = Up[j]; p < Up[j + 1]; p++) {
+            int i = Ui[p];
+            if (i == j) diagU = true;
+            else if (i < j && i >= 0) { Ucol[j].push_back(i); Urow[i].push_back(j); }
+            else return fail(err, "lu_U has an entry below the diagonal");
+        }
+        if (!diagL || !diagU) return fail(err, "lu_L/lu_U lack a diagonal entry");
+    }
+    for (int i = 0; i < n; i++) {
+        std::sort(Lcol[i].begin(), Lcol[i].end());
+        std::sort(Lrow[i].begin(), Lrow[i].end());
+        std::sort(Ucol[i].begin(), Ucol[i].end());
+        std::sort(Urow[i].begin(), Urow[i].end());
+    }
+
+    // slots: 0 zero, 1 sink, then per k: U row k (diagonal first), L column k
+    std::unordered_map<long long, int> slot;
+    slot.reserve(8 * n);
+    auto key = [n](int i, int j) { return (long long)i * n + j; };
+    int ns_ = 2;
+    for (int k = 0; k < n; k++) {
+        slot[key(k, k)] = ns_++;
+        for (int j : Urow[k]) slot[key(k, j)] = ns_++;
+        for (int i : Lcol[k]) slot[key(i, k)] = ns_++;
+    }
+    P.vec_base = ns_;
+    P.n_slots = ns_ + n;
+    if (P.n_slots > 65535) return fail(err, "system too large for 16-bit slots");
+
+    // fill closure: every update target must be structural
+    for (int k = 0; k < n; k++)
+        for (int i : Lcol[k])
+            for (int j : Urow[k])
+                if (!slot.count(key(i, j))) return fail(err, "baked LU pattern is not closed under elimination");
+
+    // initial values: permuted A
+    P.slot_init.assign(P.n_slots, 0.0);
+    for (int c = 0; c < n; c++)
+        for (int p = Ap[c]; p < Ap[c + 1]; p++) {
+            int r = Ai[p];
+            auto it = slot.find(key(P.pos[r], P.pos[c]));
+            if (it == slot.end()) return fail(err, "A_system entry outside the LU pattern");
+            P.slot_init[it->second] = Ax[p];
+        }
+
+    // air side: one unit entry per applied column and sensed row, same node
+    const int64_t* sshape = b.i64("sensed_shape");
+    const int k = sshape ? (int)sshape[0] : 0;
+    P.k = k;
+    const int32_t* ap = b.i32("applied_indptr");
+    const int32_t* ai = b.i32("applied_indices");
+    const double* ax = b.f64("applied_data");
+    const int32_t* sp = b.i32("sensed_indptr");
+    const int32_t* si = b.i32("sensed_indices");
+    const double* sx = b.f64("sensed_data");
+    if (k > 0 && (!ap || !ai || !ax || !sp || !si || !sx)) return fail(err, "blob lacks applied/sensed");
+    std::vector<char> seen(n, 0);
+    for (int c = 0; c < k; c++) {
+        if (ap[c + 1] - ap[c] != 1 || sp[c + 1] - sp[c] != 1)
+            return fail(err, "air side must have one applied and one sensed entry per column");
+        int t = ai[ap[c]];
+        if (si[sp[c]] != t || ax[ap[c]] != 1.0 || sx[sp[c]] != 1.0 || t < 0 || t >= n || seen[t])
+            return fail(err, "air side must couple each column to its own node with unit weight");
+        seen[t] = 1;
+        P.air_node.push_back(t);
+        P.air_slot.push_back(slot[key(P.pos[t], P.pos[t])]);
+    }
+
+    // tasks
+    std::vector<int> slot_level(P.n_slots, 0);
+    std::vector<Task> tasks;
+    auto intersect = [](const std::vector<int>& a, const std::vector<int>& b, int lim,
+                        std::vector<int>& o) {
+        o.clear();
+        size_t x = 0, y = 0;
+        while (x < a.size() && y < b.size()) {
+            if (a[x] >= lim || b[y] >= lim) break;
+            if (a[x] < b[y]) x++;
+            else if (a[x] > b[y]) y++;
+            else { o.push_back(a[x]); x++; y++; }
+        }
+    };
+    std::vector<int> ks;
+    auto add_task = [&](int target, int divisor, std::vector<std::pair<int, int>>&& terms, int extra_level) {
+        // split into chains of at most kPlanKmax terms
+        size_t nt = terms.size();
+        size_t pieces = nt == 0 ? 1 : (nt + kPlanKmax - 1) / kPlanKmax;
+        int prev = extra_level;
+        for (size_t pc = 0; pc < pieces; pc++) {
+            size_t lo = pc * kPlanKmax, hi = std::min(nt, lo + (size_t)kPlanKmax);
+            std::vector<std::pair<int, int>> part(terms.begin() + lo, terms.begin() + hi);
+            int lv = prev;
+            for (auto& t : part) lv = std::max(lv, std::max(slot_level[t.first], slot_level[t.second]));
+            const bool last = pc + 1 == pieces;
+            if (last && divisor) lv = std::max(lv, slot_level[divisor]);
+            lv += 1;
+            slot_level[target] = lv;
+            prev = lv;
+            tasks.push_back(Task{target, last ? divisor : 0, lv, std::move(part)});
+        }
+    };
+    for (int r = 0; r < n; r++) {
+        // U row r (j >= r): terms over k < r
+        std::vector<int> ucols;
+        ucols.push_back(r);
+        ucols.insert(ucols.end(), Urow[r].begin(), Urow[r].end());
+        for (int j : ucols) {
+            intersect(Lrow[r], Ucol[j], r, ks);
+            if (ks.empty()) continue;   // slot already holds its value
+            std::vector<std::pair<int, int>> terms;
+            for (int m : ks) terms.push_back({slot[key(r, m)], slot[key(m, j)]});
+            add_task(slot[key(r, j)], 0, std::move(terms), 0);
+        }
+        // L column r (i > r): terms over k < r, divided by U[r][r]
+        for (int i : Lcol[r]) {
+            intersect(Lrow[i], Ucol[r], r, ks);
+            std::vector<std::pair<int, int>> terms;
+            for (int m : ks) terms.push_back({slot[key(i, m)], slot[key(m, r)]});
+            add_task(slot[key(i, r)], slot[key(r, r)], std::move(terms), 0);
+        }
+    }
+    const int vb = P.vec_base;
+    // forward solve
+    std::vector<int> y_read_max(n, 0);
+    for (int i = 0; i < n; i++) {
+        if (Lrow[i].empty()) continue;
+        std::vector<std::pair<int, int>> terms;
+        for (int m : Lrow[i]) {
+            terms.push_back({slot[key(i, m)], vb + m});
+        }
+        add_task(vb + i, 0, std::move(terms), 0);
+        for (int m : Lrow[i]) y_read_max[m] = std::max(y_read_max[m], slot_level[vb + i]);
+    }
+    // backward solve, in place over y; a slot is overwritten only after its
+    // last forward reader
+    for (int i = n - 1; i >= 0; i--) {
+        std::vector<std::pair<int, int>> terms;
+        for (int j : Urow[i]) terms.push_back({slot[key(i, j)], vb + j});
+        int lv0 = std::max(slot_level[vb + i], y_read_max[i]);
+        add_task(vb + i, slot[key(i, i)], std::move(terms), lv0);
+    }
+
+    // levels -> passes
+    int maxlv = 0;
+    for (auto& t : tasks) maxlv = std::max(maxlv, t.level);
+    P.n_levels = maxlv;
+    P.n_tasks = (int)tasks.size();
+    std::vector<std::vector<int>> by_level(maxlv + 1);
+    for (int t = 0; t < (int)tasks.size(); t++) by_level[tasks[t].level].push_back(t);
+    long long npairs = 0, ndiv = 0;
+    for (int lv = 1; lv <= maxlv; lv++) {
+        auto& ids = by_level[lv];
+        std::stable_sort(ids.begin(), ids.end(), [&](int a, int c) {
+            if (tasks[a].terms.size() != tasks[c].terms.size()) return tasks[a].terms.size() > tasks[c].terms.size();
+            return tasks[a].target < tasks[c].target;
+        });
+        for (size_t s = 0; s < ids.size(); s += (size_t)width) {
+            size_t e = std::min(ids.size(), s + (size_t)width);
+            PassInfo pi{};
+            pi.hdr_off = (int)P.hdr.size();
+            pi.word_off = (int)P.words.size();
+            pi.nact = (int)(e - s);
+            pi.maxcnt = (int)tasks[ids[s]].terms.size();
+            pi.row_off = (int)P.row_off.size();
+            for (size_t id = s; id < e; id++) {
+                const Task& t = tasks[ids[id]];
+                P.hdr.push_back((uint64_t)(uint32_t)t.target | ((uint64_t)(uint32_t)t.divisor << 16)
+                                | ((uint64_t)t.terms.size() << 32));
+                npairs += (long long)t.terms.size();
+                ndiv += t.divisor ? 1 : 0;
+            }
+            int ro = 0;
+            for (int m = 0; m < pi.maxcnt; m++) {
+                P.row_off.push_back(ro);
+                for (size_t id = s; id < e; id++) {
+                    const Task& t = tasks[ids[id]];
+                    if ((int)t.terms.size() > m) {
+                        P.words.push_back((uint32_t)t.terms[m].first | ((uint32_t)t.terms[m].second << 16));
+                        ro++;
+                    }
+                }
+            }
+            P.row_off.push_back(ro);
+            P.passes.push_back(pi);
+        }
+    }
+    P.n_pairs = npairs;
+    P.n_divs = ndiv;
+    return true;
+}
+
+}  // namespace sbh

@@ -1,0 +1,177 @@
+// Internal layout shared by the host planner (vec.cpp, plan.cpp) and the HIP
+// step kernel (step_kernel.hip). Not part of the public ABI.
+#pragma once
+#include <stdint.h>
+
+#define SBK_MAX_AHU 16
+#define SBK_MT_N 624
+#define SBK_NAUX_MAX 16
+#define SBK_KMAX 48      // terms per lane per pass (matches the planner)
+
+namespace sbk {
+
+// Per-env state record, identical in HBM and in LDS (one bulk copy each way).
+// Byte offsets are per layout (sizes differ), all 16-byte aligned.
+struct StateLayout {
+    int bytes;        // size of the bulk-copied image (multiple of 16)
+    // f64 arrays
+    int T, M;                                   // [n]
+    int damper, reheat, ratio, heatsp, coolsp, dcmd, rcmd, sensing;  // [nv]
+    int recirc, sat, fan, flow;                 // [na]
+    int plant;                                  // f64[8], see PF_*
+    // i32 arrays
+    int run, coolreq;                           // [na]
+    int iplant;                                 // i32[8], see PI_*
+    // u8 arrays
+    int mode, prev_valid, dcmd_set, rcmd_set;   // [nv]
+    int occ_state;                              // [nz * nassign]
+    int occV;                                   // [nz]
+    // MT19937 words live after the image in HBM (loaded only when drawn from)
+    int mt;                                     // u32[624], HBM offset
+    int record_bytes;                           // image + mt, 256-byte aligned
+};
+
+enum { PF_PUMP_HEAD = 0, PF_BOILER_SP, PF_BOILER_RET, PF_BOILER_CUR, PF_BOILER_DSTEP,
+       PF_REW_SUM, PF_SPARE0, PF_SPARE1 };
+enum { PI_HWS_RUN = 0, PI_PUMP_RUN, PI_HWS_REQ, PI_STEP_INDEX, PI_STEP, PI_MT_IDX,
+       PI_STEPS_TOTAL, PI_EPISODES };
+
+// LDS carve-up (byte offsets from the dynamic shared base).
+struct LdsLayout {
+    int state;        // state image (StateLayout offsets are relative to this)
+    int slots;        // f64[n_slots]: 0 zero, 1 sink, LU entries, vector
+    int mt;           // u32[625]; aliases the slot region (used after the solve)
+    int zq;           // f64[nz] zone heat / zone mean temperature
+    int vtmp;         // f64[3 * nv]: unrestricted flow, flow demand, reheat energy
+    int g;            // f64[k] air-side conductance
+    int tair;         // f64[k] supply air temperature
+    int atmp;         // f64[8 * na]: wsum, atotal, satv, demand, fd sum, count
+    int red;          // f64[64] reduction scratch
+    int misc;         // f64[32] scalars
+    int iscr;         // i32[W + 8] scan scratch
+    int bytes;
+};
+
+enum { MS_FFS = 0, MS_TOTAL_REHEAT, MS_TF, MS_REWARD, MS_COMFORT, MS_AMB };
+
+// One layout (building structure): solve plan + HVAC topology + constant tables.
+struct DevLayout {
+    int n, nz, nv, na, k, n_act, n_cont, n_disc, n_dev, n_aux, nassign;
+    int n_slots, vec_base, n_pass, width;
+    int max_room_cells;
+    StateLayout st;
+    LdsLayout lds;
+    // solve plan
+    const int* pinfo;            // [n_pass * 8]: hdr_off, word_off, nact, maxcnt, row_off
+    const int* row_off;          // cumulative row starts (maxcnt + 1 per pass)
+    const uint64_t* hdr;         // per active lane: target | divisor << 16 | count << 32
+    const uint32_t* words;       // term words: a | b << 16
+    const double* slot_init;     // [n_slots]
+    const int* pos;              // [n]
+    const int* air_slot;         // [k]
+    const int* air_node;         // [k]
+    // field
+    const double* cap;           // [n]
+    const double* mcoup;         // [n]
+    const double* mret;          // [n]
+    const double* mgain;         // [n]
+    const double* solar_c;       // [n]
+    const uint8_t* is_room;      // [n]
+    // zones / rooms (rooms flattened to node lists)
+    const int* zone_cell_off;    // [nz + 1]
+    const int* zone_cells;       // node ids
+    const double* zone_area;     // [nz]
+    const int* vz_off;           // [nv + 1]
+    const int* vz_idx;
+    const double* vav_area;      // [nv] (constant: sum of its zones' areas)
+    const int* vav_ahu;          // [nv]
+    const int* coupled;          // [k] col -> vav
+    const int* zone_col_off;     // [nz + 1] coupled columns feeding zone z
+    const int* zone_cols;
+    const double* vav_c;         // [nv * 9]
+    const double* ahu_c;         // [na * 9]
+    // actions
+    const uint8_t* act_kind;
+    const uint8_t* act_act;
+    const uint8_t* act_disc;
+    const int* act_idx;
+    const int* act_src;          // column in the trainer row (cont block or SB_CONT + d)
+    const double* act_mn;
+    const double* act_mx;
+    const double* act_mnr;
+    const double* act_mxr;
+    // observation map
+    const uint8_t* f_kind;
+    const uint8_t* f_id;
+    const int* f_idx;
+    const double* f_mean;
+    const double* f_sd;          // sqrt(var) or 0 when var <= 0
+    // bytes of algorithmic traffic per env-step
+    double bytes_per_step;
+    double solve_flops;
+};
+
+// One scenario (blob): calendar, weather, prices, scalar constants.
+struct DevScen {
+    int layout;
+    int n1;                      // calendar rows
+    const double* amb;
+    const double* solar_i;
+    const double* comfort;
+    const double* heat_sp;
+    const double* cool_sp;
+    const double* aux_time;      // [n1 * (n_aux - 1)]
+    const uint8_t* occ_hour;
+    const uint8_t* occ_work;
+    const uint8_t* hour_m1;
+    const uint8_t* work_m1;
+    const uint8_t* rew_hour;
+    const uint8_t* rew_month;
+    const uint8_t* rew_work;
+    const double* dirx;          // [n] dirichlet + exposure(h)
+    const double* temp_init;     // [n]
+    const double* mass_init;     // [n]
+    const double* elec_wk;       // [24]
+    const double* elec_we;       // [24]
+    const double* elec_co2;      // [24]
+    const double* gas_price;     // [12]
+    double gas_co2;
+    double rw[8];
+    double boiler_c[10];
+    double diss_den;             // log(r2/c6)/c8 + 1/c4/r2, host libm
+    double pump_eff, pump_head0, header_res;
+    double internal_w_m2, standby_frac, occupant_w, cv_area, dt_sec;
+    double p_arr, p_dep;
+    int ea, la, ed, ld;
+    int conv_tmean;              // 1 if some AHU may need the field mean
+};
+
+struct EnvDesc {
+    int scen;
+    int layout;
+    long long state_off;         // byte offset of the env's record
+    int start;                   // calendar start offset
+    int max_steps;
+};
+
+enum { KMODE_STEP = 0, KMODE_RESET = 1 };
+
+struct KParams {
+    const EnvDesc* envs;
+    const int* order;            // block -> env
+    const DevLayout* layouts;
+    const DevScen* scens;
+    unsigned char* state;
+    const float* actions;
+    float* obs;
+    float* rewards;
+    float* terminals;
+    void* host_env;              // Env array (host-coherent), or null
+    int env_stride;              // sizeof(Env)
+    int log_offset;              // offsetof(Env, log)
+    int n_envs;
+    int mode;
+    float reward_scale;
+};
+
+}  // namespace sbk

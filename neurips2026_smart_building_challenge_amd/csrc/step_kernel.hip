@@ -1,0 +1,1177 @@
+// Fused Smart Buildings env step for MI355X (gfx950).
+//
+// One workgroup of W lanes owns one env for one step. The env's state record
+// is copied HBM -> LDS in one coalesced pass, every phase of the step runs out
+// of LDS, and the record is copied back at the end:
+//
+//   decode + apply     complete_port/csim/sb_sim.c:557-576, :220-244
+//   HVAC pre           sb_sim.c:357-457 (lanes over VAVs / zones, block sums)
+//   field solve        sb_fdm.c:142-188 restated as (A + P G S) y = b + P G T_air
+//                      (Woodbury form of csim's air-side step): numeric LU of
+//                      the permuted system, forward and backward solves, all as
+//                      one host-built level schedule over LDS slots
+//   post               sb_sim.c:489-521 (boiler return, ramp)
+//   observation        complete_port/csim/sb_obs.c:49-64
+//   occupancy          sb_occup.c:36-61, MT19937 draws assigned by prefix sum
+//   reward             sb_reward.c:31-155
+//   bookkeeping        complete_port/pufferlib_cpu_env.h:243-256 (+ auto-reset)
+#include <hip/hip_runtime.h>
+
+#include "sbenv.h"
+#include "sbenv_internal.h"
+
+namespace sbk {
+
+#define RHO_AIR 1.2
+#define CP_AIR 1006.0
+#define RHO_W 1000.0
+#define CP_W 4180.0
+#define GRAV 9.8
+#define PA_PER_BAR 100000.0
+#define PI_D 3.14159265358979323846
+
+enum { M_OFF = 0, M_HEAT = 1, M_COOL = 2, M_PASSIVE = 3 };
+
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ double wave_min(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmin(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+__device__ __forceinline__ double wave_max(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmax(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+__device__ __forceinline__ int wave_isum(int v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Block-wide reductions; every lane receives the same value. The combination
+// order is fixed, so results are deterministic.
+template <int W>
+__device__ __forceinline__ double bsum(double v, double* red) {
+    v = wave_sum(v);
+    if constexpr (W == 64) {
+        return v;
+    } else {
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+        __syncthreads();
+        double s = red[0];
+#pragma unroll
+        for (int i = 1; i < W / 64; i++) s += red[i];
+        return s;
+    }
+}
+
+template <int W>
+__device__ __forceinline__ double bmin(double v, double* red) {
+    v = wave_min(v);
+    if constexpr (W == 64) {
+        return v;
+    } else {
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+        __syncthreads();
+        double s = red[0];
+#pragma unroll
+        for (int i = 1; i < W / 64; i++) s = fmin(s, red[i]);
+        return s;
+    }
+}
+
+template <int W>
+__device__ __forceinline__ double bmax(double v, double* red) {
+    v = wave_max(v);
+    if constexpr (W == 64) {
+        return v;
+    } else {
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+        __syncthreads();
+        double s = red[0];
+#pragma unroll
+        for (int i = 1; i < W / 64; i++) s = fmax(s, red[i]);
+        return s;
+    }
+}
+
+template <int W>
+__device__ __forceinline__ int bisum(int v, double* red) {
+    v = wave_isum(v);
+    if constexpr (W == 64) {
+        return v;
+    } else {
+        int* r = reinterpret_cast<int*>(red);
+        __syncthreads();
+        if ((threadIdx.x & 63) == 0) r[threadIdx.x >> 6] = v;
+        __syncthreads();
+        int s = 0;
+#pragma unroll
+        for (int i = 0; i < W / 64; i++) s += r[i];
+        return s;
+    }
+}
+
+// Block exclusive prefix sum of an int per lane; returns the prefix, *total
+// receives the sum.
+template <int W>
+__device__ __forceinline__ int bscan(int v, int* scr, int* total) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int inc = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        int t = __shfl_up(inc, off, 64);
+        if (lane >= off) inc += t;
+    }
+    __syncthreads();
+    if (lane == 63) scr[w] = inc;
+    __syncthreads();
+    int base = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < W / 64; i++) {
+        if (i < w) base += scr[i];
+        tot += scr[i];
+    }
+    *total = tot;
+    return base + inc - v;
+}
+
+struct Ctx {
+    const DevLayout* L;
+    const DevScen* S;
+    unsigned char* rec;      // HBM record of this env
+    double *T, *M, *damper, *reheat, *ratio, *heatsp, *coolsp, *dcmd, *rcmd, *sensing;
+    double *recirc, *sat, *fan, *flow, *plant;
+    int *run, *coolreq, *ip;
+    uint8_t *mode, *prev_valid, *dcmd_set, *rcmd_set, *occ_state, *occV;
+    double *slots, *zq, *unres, *fdem, *rwen, *g, *tair;
+    double *wsum, *atotal, *satv, *demand, *fdsum, *red, *misc;
+    uint32_t* mt;
+    int* iscr;
+};
+
+__device__ __forceinline__ void bind(Ctx& c, unsigned char* lds) {
+    const DevLayout* L = c.L;
+    unsigned char* s = lds + L->lds.state;
+    const StateLayout& st = L->st;
+    c.T = (double*)(s + st.T);
+    c.M = (double*)(s + st.M);
+    c.damper = (double*)(s + st.damper);
+    c.reheat = (double*)(s + st.reheat);
+    c.ratio = (double*)(s + st.ratio);
+    c.heatsp = (double*)(s + st.heatsp);
+    c.coolsp = (double*)(s + st.coolsp);
+    c.dcmd = (double*)(s + st.dcmd);
+    c.rcmd = (double*)(s + st.rcmd);
+    c.sensing = (double*)(s + st.sensing);
+    c.recirc = (double*)(s + st.recirc);
+    c.sat = (double*)(s + st.sat);
+    c.fan = (double*)(s + st.fan);
+    c.flow = (double*)(s + st.flow);
+    c.plant = (double*)(s + st.plant);
+    c.run = (int*)(s + st.run);
+    c.coolreq = (int*)(s + st.coolreq);
+    c.ip = (int*)(s + st.iplant);
+    c.mode = s + st.mode;
+    c.prev_valid = s + st.prev_valid;
+    c.dcmd_set = s + st.dcmd_set;
+    c.rcmd_set = s + st.rcmd_set;
+    c.occ_state = s + st.occ_state;
+    c.occV = s + st.occV;
+    const LdsLayout& l = L->lds;
+    c.slots = (double*)(lds + l.slots);
+    c.mt = (uint32_t*)(lds + l.mt);
+    c.zq = (double*)(lds + l.zq);
+    c.unres = (double*)(lds + l.vtmp);
+    c.fdem = c.unres + L->nv;
+    c.rwen = c.fdem + L->nv;
+    c.g = (double*)(lds + l.g);
+    c.tair = (double*)(lds + l.tair);
+    double* a = (double*)(lds + l.atmp);
+    c.wsum = a;
+    c.atotal = a + L->na;
+    c.satv = a + 2 * L->na;
+    c.demand = a + 3 * L->na;
+    c.fdsum = a + 4 * L->na;
+    c.red = (double*)(lds + l.red);
+    c.misc = (double*)(lds + l.misc);
+    c.iscr = (int*)(lds + l.iscr);
+}
+
+// ------------------------------------------------------------------ helpers
+__device__ __forceinline__ double ahu_static(const Ctx& c, int a) {
+    if (c.run[a] != 1) return 0.0;
+    double sp = c.fan[a], mn = c.L->ahu_c[a * 9 + 2];
+    return sp > mn ? sp : mn;
+}
+
+__device__ __forceinline__ double vav_unrestricted(const Ctx& c, int v) {
+    const double* vc = c.L->vav_c + v * 9;
+    double d = c.damper[v] * vc[0] * sqrt(ahu_static(c, c.L->vav_ahu[v]) / vc[4]);
+    return d > 0.00001 ? d : 0.00001;
+}
+
+__device__ __forceinline__ double total_flow_rate(const Ctx& c) {
+    double ff = c.misc[MS_FFS];
+    double dp = (c.ip[PI_PUMP_RUN] != 1) ? 0.0 : GRAV * RHO_W * c.plant[PF_PUMP_HEAD] / PA_PER_BAR;
+    return ff * sqrt(dp / (1.0 + ff * ff * c.S->header_res)) / 3600.0;
+}
+
+__device__ __forceinline__ int default_mode(int cur, double zt, double hsp, double csp) {
+    double mid = 0.5 * (csp - hsp) + hsp;
+    if (zt < hsp) return M_HEAT;
+    if (zt > csp) return M_COOL;
+    if (zt < mid && cur == M_HEAT) return M_HEAT;
+    if (zt > mid && cur == M_COOL) return M_COOL;
+    return M_OFF;
+}
+
+// zone means of room cells (ascending), sb_sim.c:149-160
+template <int W>
+__device__ __forceinline__ void zone_means(Ctx& c, double* out) {
+    const DevLayout* L = c.L;
+    for (int z = threadIdx.x; z < L->nz; z += W) {
+        int a = L->zone_cell_off[z], b = L->zone_cell_off[z + 1];
+        double sum = 0.0;
+        for (int t = a; t < b; t++) sum += c.T[L->zone_cells[t]];
+        out[z] = sum / (double)(b - a);
+    }
+}
+
+// area-weighted VAV temperature from zone means (sb_sim.c:163-175)
+__device__ __forceinline__ double vav_temp(const Ctx& c, const double* zmean, int v, double* area_out) {
+    const DevLayout* L = c.L;
+    double area = 0.0, wt = 0.0;
+    for (int t = L->vz_off[v]; t < L->vz_off[v + 1]; t++) {
+        int z = L->vz_idx[t];
+        area += L->zone_area[z];
+        wt += zmean[z] * L->zone_area[z];
+    }
+    *area_out = area;
+    return (area > 0.0) ? wt / area : 0.0;
+}
+
+// ------------------------------------------------------------------ observation
+__device__ __forceinline__ double obs_value(const Ctx& c, int kind, int idx, int id, int j) {
+    if (kind == 0) {
+        switch (id) {
+        case 0: return (double)c.coolreq[idx];
+        case 1: return ahu_static(c, idx);
+        case 2: return (c.run[idx] == 1) ? c.flow[idx] : 0.0;
+        case 3: return c.sat[idx];
+        case 4: return (double)c.run[idx];
+        case 5: return c.flow[idx] / c.L->ahu_c[idx * 9 + 1];
+        case 6: return (1.0 - c.recirc[idx]) * c.flow[idx];
+        case 7: return (double)c.run[idx];
+        case 8: return c.recirc[idx];
+        default: return c.S->amb[j];
+        }
+    }
+    if (kind == 1) {
+        switch (id) {
+        case 0: return c.reheat[idx];
+        case 1: return c.damper[idx];
+        case 2: return c.L->vav_c[idx * 9];
+        case 3: return c.coolsp[idx];
+        case 4: return c.heatsp[idx];
+        default: return c.sensing[idx];
+        }
+    }
+    double dp = (c.ip[PI_PUMP_RUN] == 1) ? 9.8 * 1000.0 * c.plant[PF_PUMP_HEAD] / 100000.0 : 0.0;
+    switch (id) {
+    case 0: return dp;
+    case 1: return c.plant[PF_BOILER_CUR];
+    case 2: return dp;
+    case 3: return (double)c.ip[PI_HWS_RUN];
+    case 4: return (double)c.ip[PI_HWS_REQ];
+    case 5: return (double)c.ip[PI_HWS_RUN];
+    default: return c.plant[PF_BOILER_SP];
+    }
+}
+
+template <int W>
+__device__ __forceinline__ void write_obs(Ctx& c, int j, float* row) {
+#pragma clang fp contract(off)
+    const DevLayout* L = c.L;
+    for (int i = threadIdx.x; i < L->n_dev; i += W) {
+        double v = obs_value(c, L->f_kind[i], L->f_idx[i], L->f_id[i], j);
+        double sd = L->f_sd[i];
+        float v32 = (float)v;
+        row[i] = (float)((sd > 0.0) ? ((double)v32 - L->f_mean[i]) / sd : 0.0);
+    }
+    const int na = L->n_aux;
+    const double* aux = c.S->aux_time + (size_t)j * (na - 1);
+    for (int i = threadIdx.x; i < na - 1; i += W) row[L->n_dev + i] = (float)aux[i];
+    int occ = 0;
+    for (int z = threadIdx.x; z < L->nz; z += W) occ += c.occV[z];
+    occ = bisum<W>(occ, c.red);
+    if (threadIdx.x == 0) row[L->n_dev + na - 1] = (float)occ;
+    for (int i = L->n_dev + na + threadIdx.x; i < 1024; i += W) row[i] = 0.0f;
+}
+
+// ------------------------------------------------------------------ occupancy
+__device__ __forceinline__ uint32_t mt_temper(uint32_t y) {
+    y ^= y >> 11;
+    y ^= (y << 7) & 0x9d2c5680u;
+    y ^= (y << 15) & 0xefc60000u;
+    y ^= y >> 18;
+    return y;
+}
+
+__device__ __forceinline__ uint32_t mt_mix(uint32_t cur, uint32_t nxt, uint32_t far) {
+    uint32_t x = (cur & 0x80000000u) | (nxt & 0x7fffffffu);
+    uint32_t xa = x >> 1;
+    if (x & 1u) xa ^= 0x9908b0dfu;
+    return far ^ xa;
+}
+
+// MT19937 twist of the 624-word state in LDS, in three dependency phases:
+// words [0,227) read only old words, [227,454) read phase-1 words at i-227,
+// [454,624) read phase-2 words (and word 623 reads the new word 0).
+template <int W>
+__device__ __forceinline__ void mt_twist(uint32_t* mt) {
+    constexpr int PER = (227 + W - 1) / W;
+    uint32_t v[PER];
+#pragma unroll
+    for (int ph = 0; ph < 3; ph++) {
+        const int lo = ph * 227, hi = ph == 2 ? 624 : lo + 227;
+#pragma unroll
+        for (int r = 0; r < PER; r++) {
+            int i = lo + threadIdx.x + r * W;
+            if (i < hi) {
+                uint32_t nxt = (i == 623) ? mt[0] : mt[i + 1];
+                uint32_t far = (ph == 0) ? mt[i + 397] : mt[i - 227];
+                v[r] = mt_mix(mt[i], nxt, far);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < PER; r++) {
+            int i = lo + threadIdx.x + r * W;
+            if (i < hi) mt[i] = v[r];
+        }
+        __syncthreads();
+    }
+}
+
+// One interval of the RandomizedArrivalDeparture chains (sb_occup.c:36-61).
+// Occupant o = z * nassign + a draws iff it is at home in the arrival window
+// or at work in the departure window of a workday; draws are taken from the
+// MT stream in occupant order, so occupant o uses the words at
+// 2 * (number of drawing occupants before o).
+template <int W>
+__device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday) {
+    const DevLayout* L = c.L;
+    const DevScen* S = c.S;
+    const int nocc = L->nz * L->nassign;
+    constexpr int MAXC = 8;   // occupants per lane (nocc <= 8 * W, checked on the host)
+    const int per = (nocc + W - 1) / W;
+    const int o0 = threadIdx.x * per;
+    int need[MAXC];
+    int cnt = 0;
+#pragma unroll
+    for (int r = 0; r < MAXC; r++) {
+        need[r] = 0;
+        int o = o0 + r;
+        if (r < per && o < nocc && workday) {
+            int st = c.occ_state[o];
+            if (st == 0) need[r] = (hour >= S->ea && hour <= S->la);
+            else need[r] = (hour >= S->ed && hour < S->ld);
+        }
+        cnt += need[r];
+    }
+    int total;
+    int first = bscan<W>(cnt, c.iscr, &total);
+    const int idx = c.ip[PI_MT_IDX];
+    const int words = 2 * total;
+    uint32_t* hbm_mt = (uint32_t*)(c.rec + L->st.mt);
+    bool twisted = false;
+    if (total > 0) {
+        if (idx + words > SBK_MT_N) {
+            // needs the rest of the current block and the start of the next
+            for (int i = threadIdx.x; i < SBK_MT_N; i += W) c.mt[i] = hbm_mt[i];
+            __syncthreads();
+            twisted = true;
+        }
+    }
+    // gather the tempered words: stream position s -> old[idx + s] or new[idx + s - 624]
+    // Words before the twist are read from the old state first, then the twist.
+    uint32_t w_old[2 * MAXC];
+    int d = first;
+#pragma unroll
+    for (int r = 0; r < MAXC; r++) {
+        w_old[2 * r] = 0;
+        w_old[2 * r + 1] = 0;
+        if (need[r]) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                int pos = idx + 2 * d + h;
+                if (pos < SBK_MT_N) w_old[2 * r + h] = mt_temper(twisted ? c.mt[pos] : hbm_mt[pos]);
+            }
+            d++;
+        }
+    }
+    if (twisted) {
+        __syncthreads();
+        mt_twist<W>(c.mt);
+        d = first;
+#pragma unroll
+        for (int r = 0; r < MAXC; r++) {
+            if (need[r]) {
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    int pos = idx + 2 * d + h;
+                    if (pos >= SBK_MT_N) w_old[2 * r + h] = mt_temper(c.mt[pos - SBK_MT_N]);
+                }
+                d++;
+            }
+        }
+        for (int i = threadIdx.x; i < SBK_MT_N; i += W) hbm_mt[i] = c.mt[i];
+    }
+    // apply the chain updates
+#pragma unroll
+    for (int r = 0; r < MAXC; r++) {
+        int o = o0 + r;
+        if (r < per && o < nocc) {
+            int st = c.occ_state[o];
+            if (!workday) {
+                st = 0;
+            } else if (st == 0) {
+                if (need[r]) {
+                    double u = ((w_old[2 * r] >> 5) * 67108864.0 + (w_old[2 * r + 1] >> 6)) / 9007199254740992.0;
+                    if (u < S->p_arr) st = 1;
+                }
+            } else if (hour < S->ed) {
+            } else if (hour >= S->ld) {
+                st = 0;
+            } else if (need[r]) {
+                double u = ((w_old[2 * r] >> 5) * 67108864.0 + (w_old[2 * r + 1] >> 6)) / 9007199254740992.0;
+                if (u < S->p_dep) st = 0;
+            }
+            c.occ_state[o] = (uint8_t)st;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x == 0 && total > 0) {
+        int ni = idx + words;
+        c.ip[PI_MT_IDX] = twisted ? ni - SBK_MT_N : ni;
+    }
+    for (int z = threadIdx.x; z < L->nz; z += W) {
+        int s = 0;
+        for (int a = 0; a < L->nassign; a++) s += c.occ_state[z * L->nassign + a];
+        c.occV[z] = (uint8_t)s;
+    }
+    __syncthreads();
+}
+
+// ------------------------------------------------------------------ reset
+// sb_sim_reset (sb_sim.c:177-218) on the LDS image; pump head is not reset.
+template <int W>
+__device__ __forceinline__ void sim_reset(Ctx& c, int start) {
+    const DevLayout* L = c.L;
+    const DevScen* S = c.S;
+    for (int a = threadIdx.x; a < L->na; a += W) {
+        const double* ac = L->ahu_c + a * 9;
+        c.run[a] = (int)ac[8];
+        c.recirc[a] = ac[0];
+        c.sat[a] = ac[6];
+        c.fan[a] = ac[7];
+        c.flow[a] = 0.0;
+        c.coolreq[a] = 0;
+    }
+    for (int v = threadIdx.x; v < L->nv; v += W) {
+        const double* vc = L->vav_c + v * 9;
+        c.damper[v] = vc[7];
+        c.reheat[v] = vc[8];
+        c.ratio[v] = 1.0;
+        c.heatsp[v] = vc[5];
+        c.coolsp[v] = vc[6];
+        c.mode[v] = M_OFF;
+        c.prev_valid[v] = 0;
+        c.dcmd_set[v] = 0;
+        c.rcmd_set[v] = 0;
+        c.dcmd[v] = 0.0;
+        c.rcmd[v] = 0.0;
+    }
+    for (int t = threadIdx.x; t < L->n; t += W) {
+        c.T[t] = S->temp_init[t];
+        c.M[t] = S->mass_init[t];
+    }
+    if (threadIdx.x == 0) {
+        c.ip[PI_HWS_REQ] = 0;
+        c.ip[PI_HWS_RUN] = 1;
+        c.ip[PI_PUMP_RUN] = 1;
+        c.plant[PF_BOILER_SP] = S->boiler_c[0];
+        c.plant[PF_BOILER_RET] = S->boiler_c[1];
+        c.plant[PF_BOILER_CUR] = S->boiler_c[0];
+        c.plant[PF_BOILER_DSTEP] = 0.0;
+        c.ip[PI_STEP_INDEX] = start;
+        c.ip[PI_STEP] = 0;
+    }
+    __syncthreads();
+    zone_means<W>(c, c.zq);
+    __syncthreads();
+    for (int v = threadIdx.x; v < L->nv; v += W) {
+        double area;
+        c.sensing[v] = vav_temp(c, c.zq, v, &area);
+    }
+    __syncthreads();
+}
+
+// puf_reset sequence (pufferlib_cpu_env.h:187-208) at the env's start offset.
+template <int W>
+__device__ __forceinline__ void env_reset(Ctx& c, int start, float* obs_row) {
+    const DevScen* S = c.S;
+    sim_reset<W>(c, start);
+    occupancy_advance<W>(c, S->hour_m1[start], S->work_m1[start]);
+    write_obs<W>(c, start, obs_row);
+    occupancy_advance<W>(c, S->occ_hour[start], S->occ_work[start]);
+}
+
+// ------------------------------------------------------------------ step
+template <int W>
+__device__ __forceinline__ void decode_apply(Ctx& c, const float* act) {
+#pragma clang fp contract(off)
+    const DevLayout* L = c.L;
+    for (int i = threadIdx.x; i < L->n_act; i += W) {
+        double nat;
+        float a = act[L->act_src[i]];
+        if (L->act_disc[i]) {
+            double dv = (double)a;
+            double m = (dv == 1.0) ? 1.0 : -1.0;
+            nat = (m - L->act_mnr[i]) / (L->act_mxr[i] - L->act_mnr[i]) * (L->act_mx[i] - L->act_mn[i])
+                  + L->act_mn[i];
+        } else {
+            float m = a > 1.0f ? 1.0f : (a < -1.0f ? -1.0f : a);
+            float span_in = (float)(L->act_mxr[i] - L->act_mnr[i]);
+            float span_out = (float)(L->act_mx[i] - L->act_mn[i]);
+            float r = (m - (float)L->act_mnr[i]) / span_in * span_out + (float)L->act_mn[i];
+            nat = (double)r;
+        }
+        const int idx = L->act_idx[i], ak = L->act_act[i];
+        switch (L->act_kind[i]) {
+        case 0:
+            if (ak == 0) c.sat[idx] = nat;
+            else if (ak == 1) c.fan[idx] = nat;
+            else if (ak == 2) {
+                double hi = L->ahu_c[idx * 9 + 3];
+                c.recirc[idx] = nat < 0.0 ? 0.0 : (nat > hi ? hi : nat);
+            } else c.run[idx] = (nat == 1.0) ? 1 : 0;
+            break;
+        case 1: {
+            double cl = nat < 0.0 ? 0.0 : (nat > 1.0 ? 1.0 : nat);
+            if (ak == 0) { c.dcmd[idx] = cl; c.dcmd_set[idx] = 1; }
+            else { c.rcmd[idx] = cl; c.rcmd_set[idx] = 1; }
+            break;
+        }
+        default:
+            if (ak == 0) c.plant[PF_BOILER_SP] = nat;
+            else if (ak == 1) c.plant[PF_PUMP_HEAD] = nat / (GRAV * RHO_W / PA_PER_BAR);
+            else { int on = (nat == 1.0) ? 1 : 0; c.ip[PI_HWS_RUN] = on; c.ip[PI_PUMP_RUN] = on; }
+        }
+    }
+    __syncthreads();
+}
+
+template <int W>
+__device__ __forceinline__ void step_pre(Ctx& c) {
+    const DevLayout* L = c.L;
+    const DevScen* S = c.S;
+    const int kk = c.ip[PI_STEP_INDEX];
+    const double ambient = S->amb[kk];
+    const int comfort = (S->comfort[kk] != 0.0);
+    const int na = L->na, nv = L->nv;
+    zone_means<W>(c, c.zq);
+    __syncthreads();
+    // sensing + thermostat + VAV settings (sb_sim.c:368-384, :316-355)
+    for (int v = threadIdx.x; v < nv; v += W) {
+        double area;
+        double sensing = vav_temp(c, c.zq, v, &area);
+        c.sensing[v] = sensing;
+        if (area <= 0.0) continue;
+        const double* vc = L->vav_c + v * 9;
+        double hsp = S->heat_sp[kk], csp = S->cool_sp[kk];
+        c.heatsp[v] = hsp;
+        c.coolsp[v] = csp;
+        int mode = c.mode[v];
+        if (comfort) mode = default_mode(mode, sensing, hsp, csp);
+        else if (c.prev_valid[v] && S->comfort[kk - 1] != 0.0) mode = M_PASSIVE;
+        else if (mode == M_PASSIVE && sensing > hsp && sensing < csp) mode = M_PASSIVE;
+        else mode = default_mode(mode, sensing, hsp, csp);
+        c.mode[v] = (uint8_t)mode;
+        c.prev_valid[v] = 1;
+        double damper, reheat;
+        if (mode == M_HEAT) { damper = 1.0; reheat = 1.0; }
+        else if (mode == M_COOL) { damper = 1.0; reheat = 0.0; }
+        else { damper = vc[2]; reheat = 0.0; }
+        if (c.dcmd_set[v]) damper = c.dcmd[v];
+        if (c.rcmd_set[v]) reheat = c.rcmd[v];
+        c.damper[v] = damper > vc[2] ? damper : vc[2];
+        c.reheat[v] = reheat;
+    }
+    __syncthreads();
+    // AHU return-air means and supply temperatures (sb_sim.c:382-387, :253-265)
+    double tmean = 0.0;
+    if (S->conv_tmean) {
+        double s = 0.0;
+        for (int t = threadIdx.x; t < L->n; t += W) s += c.T[t];
+        tmean = bsum<W>(s, c.red) / (double)L->n;
+    }
+    double ffs_part = 0.0;
+    for (int v = threadIdx.x; v < nv; v += W) {
+        ffs_part += c.reheat[v] * L->vav_c[v * 9 + 1];
+        c.unres[v] = vav_unrestricted(c, v);
+    }
+    const double ffs = bsum<W>(ffs_part, c.red);
+    for (int a = 0; a < na; a++) {
+        double ws = 0.0, at = 0.0, dm = 0.0;
+        for (int v = threadIdx.x; v < nv; v += W) {
+            if (L->vav_ahu[v] != a) continue;
+            double area = L->vav_area[v];
+            if (area > 0.0) {
+                ws += c.sensing[v] * area;
+                at += area;
+            }
+            dm += c.unres[v];
+        }
+        ws = bsum<W>(ws, c.red);
+        at = bsum<W>(at, c.red);
+        dm = bsum<W>(dm, c.red);
+        if (threadIdx.x == 0) {
+            double rt = (at > 0.0) ? ws / at : tmean;
+            double mixed = c.recirc[a] * rt + (1.0 - c.recirc[a]) * ambient;
+            c.satv[a] = (mixed > c.sat[a] && c.run[a] == 1) ? c.sat[a] : mixed;
+            c.demand[a] = dm;
+        }
+    }
+    if (threadIdx.x == 0) {
+        c.misc[MS_FFS] = ffs;
+        c.ip[PI_HWS_REQ] = nv;
+    }
+    __syncthreads();
+    for (int v = threadIdx.x; v < nv; v += W) {
+        int a = L->vav_ahu[v];
+        double dm = c.demand[a];
+        if (dm > 0.0) {
+            double r = L->ahu_c[a * 9 + 1] / dm;
+            c.ratio[v] = r < 1.0 ? r : 1.0;
+        } else {
+            c.ratio[v] = 1.0;
+        }
+    }
+    __syncthreads();
+    const double tf = total_flow_rate(c);
+    const double iwt = c.plant[PF_BOILER_CUR];
+    // coupled columns: reheat energy, air-side conductance, AHU flow (sb_sim.c:410-436)
+    double rw_part = 0.0;
+    for (int col = threadIdx.x; col < L->k; col += W) {
+        int v = L->coupled[col];
+        double g = 0.0, ta = 0.0, rw = 0.0, fd = 0.0;
+        if (L->vav_area[v] > 0.0) {
+            const double* vc = L->vav_c + v * 9;
+            int a = L->vav_ahu[v];
+            double sat = c.satv[a];
+            ta = sat;
+            fd = c.unres[v] * c.ratio[v];
+            // reheat_eff / reheat_energy (sb_sim.c:289-314)
+            double eff;
+            double air_cap = CP_AIR * RHO_AIR * fd;
+            if (air_cap <= 0.0) {
+                eff = 0.0;
+            } else {
+                double wflow = 0.0;
+                if (ffs != 0.0) wflow = tf * ((c.reheat[v] * vc[1]) / ffs);
+                double water_cap = CP_W * RHO_W * wflow;
+                eff = water_cap / air_cap;
+                if (eff > 1.0) eff = 1.0;
+                double gap = iwt - sat;
+                if (gap > 0.0) {
+                    double headroom = vc[3] - sat;
+                    if (headroom <= 0.0) eff = 0.0;
+                    else {
+                        double hr = headroom / gap;
+                        if (hr < eff) eff = hr;
+                    }
+                }
+            }
+            rw = eff * CP_AIR * RHO_AIR * fd * (iwt - sat);
+            if (c.damper[v] > 0.0 && vc[0] > 0.0) g = fd * RHO_AIR * CP_AIR;
+        }
+        c.g[col] = g;
+        c.tair[col] = ta;
+        c.rwen[col] = rw;
+        c.fdem[col] = fd;
+        rw_part += rw;
+    }
+    const double total_rw = bsum<W>(rw_part, c.red);
+    // coil extreme for the boiler return temperature (sb_sim.c:495-499)
+    double cmin = 1e308, cmax = -1e308;
+    for (int col = threadIdx.x; col < L->k; col += W) {
+        int v = L->coupled[col];
+        (void)v;
+        cmin = fmin(cmin, c.tair[col]);
+        cmax = fmax(cmax, c.tair[col]);
+    }
+    cmin = bmin<W>(cmin, c.red);
+    cmax = bmax<W>(cmax, c.red);
+    for (int a = 0; a < na; a++) {
+        double f = 0.0;
+        int cnt = 0;
+        for (int col = threadIdx.x; col < L->k; col += W) {
+            int v = L->coupled[col];
+            if (L->vav_ahu[v] == a && L->vav_area[v] > 0.0 && c.fdem[col] > 0.0) {
+                f += c.fdem[col];
+                cnt++;
+            }
+        }
+        f = bsum<W>(f, c.red);
+        cnt = bisum<W>(cnt, c.red);
+        if (threadIdx.x == 0) {
+            double mf = L->ahu_c[a * 9 + 1];
+            c.flow[a] = f > mf ? mf : f;
+            c.coolreq[a] = cnt;
+        }
+    }
+    if (threadIdx.x == 0) {
+        c.misc[MS_TOTAL_REHEAT] = total_rw;
+        c.misc[MS_TF] = tf;
+        c.misc[6] = cmin;
+        c.misc[7] = cmax;
+        c.misc[MS_AMB] = ambient;
+        c.misc[MS_COMFORT] = comfort;
+    }
+    // zone heat: reheat share, internal and occupant gains (sb_sim.c:420-447)
+    const double frac = comfort ? 1.0 : S->standby_frac;
+    const double wpc = S->internal_w_m2 * S->cv_area * frac;
+    for (int z = threadIdx.x; z < L->nz; z += W) {
+        double q = 0.0;
+        for (int t = L->zone_col_off[z]; t < L->zone_col_off[z + 1]; t++) {
+            int col = L->zone_cols[t];
+            int v = L->coupled[col];
+            if (L->vav_area[v] > 0.0 && c.damper[v] > 0.0 && L->vav_c[v * 9] > 0.0)
+                q += c.rwen[col] * L->zone_area[z] / L->vav_area[v];
+        }
+        int ncell = L->zone_cell_off[z + 1] - L->zone_cell_off[z];
+        if (S->internal_w_m2 > 0.0) q += wpc * (double)ncell;
+        if (S->occupant_w > 0.0) q += (double)c.occV[z] * S->occupant_w;
+        c.zq[z] = q / (double)ncell;
+    }
+    __syncthreads();
+}
+
+// ------------------------------------------------------------------ solve plan
+// Orders this wave's LDS accesses before and after the point (the wave's DS
+// operations complete in issue order) without waiting for global loads, so
+// the next pass's term words stay in flight across the synchronisation.
+__device__ __forceinline__ void wave_lds_sync() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0), vmcnt/expcnt untouched
+    __builtin_amdgcn_wave_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+struct PassRegs {
+    uint64_t h;
+    int nact, maxcnt;
+    uint32_t w[SBK_KMAX];
+};
+
+// Loads pass p's header and term words into registers (lane l gets term m of
+// its task from row m, which holds the lanes whose count exceeds m).
+__device__ __forceinline__ void fetch_pass(const DevLayout* L, int p, PassRegs& r) {
+    const int* pi = L->pinfo + 8 * p;
+    const int hdr_off = pi[0], word_off = pi[1], nact = pi[2], maxcnt = pi[3], ro = pi[4];
+    const int lane = threadIdx.x;
+    r.nact = nact;
+    r.maxcnt = maxcnt;
+    r.h = lane < nact ? L->hdr[hdr_off + lane] : 1ull;   // sink slot, no divisor
+    const int* rows = L->row_off + ro;
+#pragma unroll
+    for (int m = 0; m < SBK_KMAX; m++) {
+        uint32_t v = 0;
+        if (m < maxcnt) {
+            const int a = rows[m], b = rows[m + 1];
+            if (lane < b - a) v = L->words[word_off + a + lane];
+        }
+        r.w[m] = v;
+    }
+}
+
+// One pass: every active lane computes slot[target] = (slot[target] - sum of
+// its terms) [/ slot[divisor]]. Missing terms are (0, 0) and read slot 0 = 0.
+__device__ __forceinline__ void run_pass(double* slots, const PassRegs& r) {
+    constexpr int CH = 8;
+    const int tgt = (int)(r.h & 0xffffu), dv = (int)((r.h >> 16) & 0xffffu);
+    double acc = slots[tgt];
+#pragma unroll
+    for (int m0 = 0; m0 < SBK_KMAX; m0 += CH) {
+        if (m0 >= r.maxcnt) break;
+        double x[CH], y[CH];
+#pragma unroll
+        for (int j = 0; j < CH; j++) {
+            const uint32_t w = r.w[m0 + j];
+            x[j] = slots[w & 0xffffu];
+            y[j] = slots[w >> 16];
+        }
+#pragma unroll
+        for (int j = 0; j < CH; j++) acc -= x[j] * y[j];
+    }
+    if (dv) acc = acc / slots[dv];
+    if ((int)threadIdx.x < r.nact) slots[tgt] = acc;
+}
+
+// All passes, pass p+1's words prefetched while pass p computes.
+template <int W>
+__device__ __forceinline__ void run_plan(const DevLayout* L, double* slots) {
+    static_assert(W == 64, "the solve plan runs on one wavefront");
+    const int np = L->n_pass;
+    if (np == 0) return;
+    PassRegs A, B;
+    fetch_pass(L, 0, A);
+    for (int p = 0; p < np; p += 2) {
+        if (p + 1 < np) fetch_pass(L, p + 1, B);
+        run_pass(slots, A);
+        wave_lds_sync();
+        if (p + 1 >= np) break;
+        if (p + 2 < np) fetch_pass(L, p + 2, A);
+        run_pass(slots, B);
+        wave_lds_sync();
+    }
+}
+
+// Field step: b = cap T + q + amb dirx + mc M (+ solar, + g T_air at the air
+// nodes), then (A + diag(g)) y = b by the plan; mass and field update.
+template <int W>
+__device__ __forceinline__ void field_step(Ctx& c) {
+    const DevLayout* L = c.L;
+    const DevScen* S = c.S;
+    const int kk = c.ip[PI_STEP_INDEX];
+    const double ambient = S->amb[kk];
+    const double irr = S->solar_i[kk];
+    const int n = L->n;
+    double* slots = c.slots;
+    const int vb = L->vec_base;
+    for (int s = threadIdx.x; s < vb; s += W) slots[s] = L->slot_init[s];
+    // room cells carry their zone's heat; every node then gets its solar gain
+    for (int z = threadIdx.x; z < L->nz; z += W) {
+        double qz = c.zq[z];
+        for (int t = L->zone_cell_off[z]; t < L->zone_cell_off[z + 1]; t++) c.slots[vb + L->pos[L->zone_cells[t]]] = qz;
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < n; t += W) {
+        const int ps = vb + L->pos[t];
+        double qin = L->is_room[t] ? slots[ps] + L->solar_c[t] * irr : L->solar_c[t] * irr;
+        slots[ps] = L->cap[t] * c.T[t] + qin + ambient * S->dirx[t] + L->mcoup[t] * c.M[t];
+    }
+    __syncthreads();
+    for (int col = threadIdx.x; col < L->k; col += W) {
+        double g = c.g[col];
+        slots[L->air_slot[col]] += g;
+        slots[vb + L->pos[L->air_node[col]]] += g * c.tair[col];
+    }
+    __syncthreads();
+    // level schedule: LU of the permuted system, forward and backward solves
+    run_plan<W>(L, slots);
+    for (int t = threadIdx.x; t < n; t += W) {
+        double y = slots[vb + L->pos[t]];
+        c.M[t] = c.M[t] * L->mret[t] + L->mgain[t] * y;
+        c.T[t] = y;
+    }
+    __syncthreads();
+}
+
+// sb_sim_step_post (sb_sim.c:489-521), convection off.
+template <int W>
+__device__ __forceinline__ void step_post(Ctx& c) {
+    if (threadIdx.x == 0) {
+        const DevScen* S = c.S;
+        const double total_rw = c.misc[MS_TOTAL_REHEAT];
+        double wcap = CP_W * RHO_W * c.misc[MS_TF];
+        if (wcap > 0.0 && c.L->k > 0) {
+            double supply = c.plant[PF_BOILER_CUR];
+            double rt = supply - total_rw / wcap;
+            double at = total_rw >= 0.0 ? c.misc[6] : c.misc[7];
+            double lo = supply < at ? supply : at;
+            double hi = supply > at ? supply : at;
+            if (rt < lo) rt = lo;
+            if (rt > hi) rt = hi;
+            c.plant[PF_BOILER_RET] = rt;
+        }
+        double begin = c.plant[PF_BOILER_CUR], sp = c.plant[PF_BOILER_SP];
+        double dt_min = S->dt_sec / 60.0;
+        double cur;
+        if (sp > begin) {
+            double v = begin + S->boiler_c[2] * dt_min;
+            cur = v < sp ? v : sp;
+        } else if (sp < begin) {
+            double v = begin - S->boiler_c[3] * dt_min;
+            cur = v > sp ? v : sp;
+        } else {
+            cur = sp;
+        }
+        c.plant[PF_BOILER_CUR] = cur;
+        c.plant[PF_BOILER_DSTEP] = cur - begin;
+        c.ip[PI_STEP_INDEX] += 1;
+    }
+    __syncthreads();
+}
+
+// 3C reward (sb_reward.c:31-155) on the post-step state and new occupancy.
+template <int W>
+__device__ __forceinline__ double reward(Ctx& c, int kv) {
+    const DevLayout* L = c.L;
+    const DevScen* S = c.S;
+    const double dt = S->dt_sec, inv_hour = 1.0 / 3600.0;
+    zone_means<W>(c, c.zq);
+    __syncthreads();
+    const double ambient = S->amb[kv];
+    const int hour = S->rew_hour[kv], month = S->rew_month[kv], wd = S->rew_work[kv];
+    double tmean = 0.0;
+    if (S->conv_tmean) {
+        double s = 0.0;
+        for (int t = threadIdx.x; t < L->n; t += W) s += c.T[t];
+        tmean = bsum<W>(s, c.red) / (double)L->n;
+    }
+    double intake = 0.0, exhaust = 0.0, cooling = 0.0;
+    for (int a = 0; a < L->na; a++) {
+        double ws = 0.0, at = 0.0;
+        for (int v = threadIdx.x; v < L->nv; v += W) {
+            if (L->vav_ahu[v] != a) continue;
+            double area;
+            double tv = vav_temp(c, c.zq, v, &area);
+            if (area > 0.0) {
+                ws += tv * area;
+                at += area;
+            }
+        }
+        ws = bsum<W>(ws, c.red);
+        at = bsum<W>(at, c.red);
+        double rc = (at > 0.0) ? ws / at : tmean;
+        double st = ahu_static(c, a);
+        double fe = L->ahu_c[a * 9 + 5];
+        double flow = (c.run[a] == 1) ? c.flow[a] : 0.0;
+        intake += flow * st / fe;
+        exhaust += flow * (1.0 - c.recirc[a]) * st / fe;
+        double mixed = c.recirc[a] * rc + (1.0 - c.recirc[a]) * ambient;
+        double sat = (mixed > c.sat[a] && c.run[a] == 1) ? c.sat[a] : mixed;
+        cooling += flow * RHO_AIR * CP_AIR * (sat - mixed) / L->ahu_c[a * 9 + 4];
+    }
+    const double blower = intake + exhaust;
+    const double tf = total_flow_rate(c);
+    // boiler gas rate (sb_reward.c:12-29); log(r2/c6)/c8 + 1/c4/r2 from the host
+    double gas_rate;
+    {
+        const double* bc = S->boiler_c;
+        double rwt = c.plant[PF_BOILER_RET];
+        double bsp = c.plant[PF_BOILER_SP];
+        double supply = (bsp > rwt) ? bsp : rwt;
+        double flow = CP_W * RHO_W * tf * (supply - rwt);
+        double diss = 0.0;
+        if (supply >= ambient) diss = bc[5] * 2.0 * PI_D * (supply - ambient) / S->diss_den;
+        double tank = 0.0;
+        if (dt > 0.0) tank = CP_W * RHO_W * bc[7] * c.plant[PF_BOILER_DSTEP] / dt;
+        double tot = flow + diss + tank;
+        gas_rate = tot > 0.0 ? tot : 0.0;
+    }
+    const double pump_e = tf * RHO_W * GRAV * c.plant[PF_PUMP_HEAD] / S->pump_eff;
+    const double max_pph = S->rw[0], min_pph = S->rw[1], ref = S->rw[2];
+    const double hsp = S->heat_sp[kv], csp = S->cool_sp[kv];
+    double occ_part = 0.0, cum_part = 0.0;
+    for (int z = threadIdx.x; z < L->nz; z += W) {
+        double occ = (double)c.occV[z];
+        occ_part += occ;
+        double zt = c.zq[z];
+        double dev = zt - csp;
+        if (hsp - zt > dev) dev = hsp - zt;
+        if (dev < 0.0) dev = 0.0;
+        double sh = (dev <= ref) ? dev / ref : 1.0 + ((dev - ref) / ref) * ((dev - ref) / ref);
+        cum_part += max_pph * (1.0 - sh) * occ * dt * inv_hour;
+    }
+    const double total_occ = bsum<W>(occ_part, c.red);
+    const double cum = bsum<W>(cum_part, c.red);
+    const double max_prod = max_pph * total_occ * dt * inv_hour;
+    const double min_prod = min_pph * total_occ * dt * inv_hour;
+    double npr = 0.0;
+    if (total_occ > 0.0 && (max_prod - min_prod) != 0.0) npr = (cum - min_prod) / (max_prod - min_prod) - 1.0;
+    const double elec_rate = blower + fabs(cooling) + pump_e;
+    const double price = wd ? S->elec_wk[hour] : S->elec_we[hour];
+    const double crate = S->elec_co2[hour];
+    const double elec_cost = price * fabs(elec_rate) * dt;
+    const double elec_cost_max = price * S->rw[3] * dt;
+    const double elec_carb = crate * fabs(elec_rate) * dt;
+    const double elec_carb_max = crate * S->rw[3] * dt;
+    const double gprice = S->gas_price[month - 1];
+    const double gg = gas_rate > 0.0 ? gas_rate : 0.0;
+    const double gas_cost = gprice * gg * dt;
+    const double gas_cost_max = gprice * S->rw[4] * dt;
+    const double gas_carb = S->gas_co2 * gg * dt;
+    const double gas_carb_max = S->gas_co2 * S->rw[4] * dt;
+    const double den_e = elec_cost_max + gas_cost_max;
+    const double nec = (den_e > 0.0) ? (elec_cost + gas_cost) / den_e : 0.0;
+    const double den_c = elec_carb_max + gas_carb_max;
+    const double ncar = (den_c > 0.0) ? (elec_carb + gas_carb) / den_c : 0.0;
+    const double pw = S->rw[5], ew = S->rw[6], cw = S->rw[7];
+    const double raw = npr * pw - nec * ew - ncar * cw;
+    return raw / (pw + ew + cw);
+}
+
+// Loads/stores of the state image, 16 bytes per lane.
+template <int W>
+__device__ __forceinline__ void copy16(unsigned char* dst, const unsigned char* src, int bytes) {
+    const int n16 = bytes >> 4;
+    for (int i = threadIdx.x; i < n16; i += W)
+        reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+}
+
+template <int W>
+__global__ __launch_bounds__(W) void step_kernel(KParams P) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int e = P.order[blockIdx.x];
+    const EnvDesc ed = P.envs[e];
+    Ctx c;
+    c.L = P.layouts + ed.layout;
+    c.S = P.scens + ed.scen;
+    c.rec = P.state + ed.state_off;
+    bind(c, lds);
+    const DevLayout* L = c.L;
+    copy16<W>(lds + L->lds.state, c.rec, L->st.bytes);
+    __syncthreads();
+    float* obs_row = P.obs + (size_t)e * 1024;
+    if (P.mode == KMODE_RESET) {
+        env_reset<W>(c, ed.start, obs_row);
+        if (threadIdx.x == 0) {
+            c.ip[PI_STEP] = 0;
+            c.ip[PI_STEPS_TOTAL] = 0;
+            c.ip[PI_EPISODES] = 0;
+            c.plant[PF_REW_SUM] = 0.0;
+        }
+        __syncthreads();
+        copy16<W>(c.rec, lds + L->lds.state, L->st.bytes);
+        return;
+    }
+    // host-visible log fields (trainer may clear them between steps)
+    Log* hlog = nullptr;
+    float lg_ret = 0.f, lg_mean = 0.f;
+    if (P.host_env && threadIdx.x == 0) {
+        hlog = reinterpret_cast<Log*>(reinterpret_cast<unsigned char*>(P.host_env) + (size_t)e * P.env_stride
+                                      + P.log_offset);
+        lg_ret = __hip_atomic_load(&hlog->episode_return, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        lg_mean = __hip_atomic_load(&hlog->reward_mean, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    decode_apply<W>(c, P.actions + (size_t)e * 272);
+    step_pre<W>(c);
+    field_step<W>(c);
+    step_post<W>(c);
+    const int step = c.ip[PI_STEP] + 1;
+    const int j = ed.start + step;
+    write_obs<W>(c, j, obs_row);
+    __syncthreads();
+    occupancy_advance<W>(c, c.S->occ_hour[j], c.S->occ_work[j]);
+    const double rew = reward<W>(c, j);
+    const float r = (float)rew;
+    const int done = step >= ed.max_steps;
+    if (threadIdx.x == 0) {
+        P.rewards[e] = r * P.reward_scale;
+        P.terminals[e] = done ? 1.0f : 0.0f;
+        c.ip[PI_STEP] = step;
+        c.plant[PF_REW_SUM] += rew;
+        c.ip[PI_STEPS_TOTAL] += 1;
+        if (hlog) {
+            float ret = lg_ret + r;
+            float mean = lg_mean + (r - lg_mean) / (float)step;
+            __hip_atomic_store(&hlog->episode_return, ret, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(&hlog->reward_mean, mean, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            if (done) {
+                float m = ret / (float)step;
+                float* lf = reinterpret_cast<float*>(hlog);
+                float perf = __hip_atomic_load(&lf[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                float score = __hip_atomic_load(&lf[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                float elen = __hip_atomic_load(&lf[3], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                float nn = __hip_atomic_load(&lf[5], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(&lf[0], perf + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(&lf[1], score + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(&lf[3], elen + (float)step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(&lf[5], nn + 1.0f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            }
+        }
+        if (done) c.ip[PI_EPISODES] += 1;
+    }
+    __syncthreads();
+    if (done) env_reset<W>(c, ed.start, obs_row);
+    __syncthreads();
+    copy16<W>(c.rec, lds + L->lds.state, L->st.bytes);
+}
+
+// Beta(2,2) action rows (see sbx_gen_actions in sbenv.h).
+__device__ __forceinline__ float u24(uint32_t x) { return ((float)(x >> 8) + 0.5f) * (1.0f / 16777216.0f); }
+
+__device__ __forceinline__ float beta22(uint64_t seed, uint32_t env, uint32_t step, uint32_t slot) {
+    uint32_t c0 = env, c1 = step, c2 = slot, c3 = 0u;
+    uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+#pragma unroll
+    for (int r = 0; r < 10; r++) {
+        uint32_t hi0 = __umulhi(0xD2511F53u, c0), lo0 = 0xD2511F53u * c0;
+        uint32_t hi1 = __umulhi(0xCD9E8D57u, c2), lo1 = 0xCD9E8D57u * c2;
+        uint32_t n0 = hi1 ^ c1 ^ k0;
+        uint32_t n2 = hi0 ^ c3 ^ k1;
+        c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+    }
+    float a = u24(c0), b = u24(c1), d = u24(c2);
+    float lo = a < b ? a : b, hi = a < b ? b : a;
+    return d < lo ? lo : (d > hi ? hi : d);
+}
+
+__global__ void gen_actions_kernel(float* actions, const int* n_cont, const int* n_disc, int n_envs,
+                                   uint64_t seed, uint32_t step) {
+#pragma clang fp contract(off)
+    const int e = blockIdx.x;
+    if (e >= n_envs) return;
+    const int nc = n_cont[e], nd = n_disc[e];
+    float* row = actions + (size_t)e * 272;
+    for (int i = threadIdx.x; i < 272; i += blockDim.x) {
+        float v = 0.0f;
+        if (i < 256) {
+            if (i < nc) v = 2.0f * beta22(seed, (uint32_t)e, step, (uint32_t)i) - 1.0f;
+        } else {
+            int d = i - 256;
+            if (d < nd) v = beta22(seed, (uint32_t)e, step, (uint32_t)i) > 0.5f ? 1.0f : 0.0f;
+        }
+        row[i] = v;
+    }
+}
+
+}  // namespace sbk
+
+// ---------------------------------------------------------------- launchers
+extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int width, int lds_bytes, hipStream_t s) {
+    using namespace sbk;
+    if (width != 64) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(step_kernel<64>, dim3(n_blocks), dim3(64), lds_bytes, s, *p);
+    return (int)hipGetLastError();
+}
+
+extern "C" int sbk_set_lds_limit(int width, int bytes) {
+    using namespace sbk;
+    if (width != 64) return (int)hipErrorInvalidValue;
+    return (int)hipFuncSetAttribute((const void*)step_kernel<64>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+}
+
+extern "C" int sbk_launch_gen_actions(float* actions, const int* n_cont, const int* n_disc, int n_envs,
+                                      uint64_t seed, uint32_t step, hipStream_t s) {
+    hipLaunchKernelGGL(sbk::gen_actions_kernel, dim3(n_envs), dim3(64), 0, s, actions, n_cont, n_disc, n_envs,
+                       seed, step);
+    return (int)hipGetLastError();
+}

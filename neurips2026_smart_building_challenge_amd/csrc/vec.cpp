@@ -1,0 +1,1076 @@
+// PufferLib env ABI for the MI355X env step (host side).
+//
+// puf_vec_create mirrors the reference GPU vec (complete_port/gpu/
+// smart_buildings.cu:2497-2880): scenarios come from env.blob or every *.sbb of
+// env.blob_dir (sorted, then round-robin over buildings, :2435-2459), G groups
+// (env.groups, default n/32) get n/G envs each, and every env then steps in one
+// fused kernel launch per puf_step. Unlike the reference there is no per-group
+// solver (no SB_NE cap, no weather merging): envs of different layouts and
+// climates share one launch and read their own tables.
+#include <dirent.h>
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "plan.h"
+#include "sbb_reader.h"
+#include "sbenv.h"
+#include "sbenv_internal.h"
+
+extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int width, int lds_bytes, hipStream_t s);
+extern "C" int sbk_set_lds_limit(int width, int bytes);
+extern "C" int sbk_launch_gen_actions(float* actions, const int* n_cont, const int* n_disc, int n_envs,
+                                      uint64_t seed, uint32_t step, hipStream_t s);
+
+namespace {
+
+hipStream_t g_stream = nullptr;
+std::string g_err;
+struct Vec;
+Vec* g_last = nullptr;
+
+[[noreturn]] void die(const std::string& msg) {
+    fprintf(stderr, "smart_buildings: %s\n", msg.c_str());
+    abort();
+}
+
+void hip_ok(hipError_t e, const char* what) {
+    if (e != hipSuccess) die(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// ---------------------------------------------------------------- arena
+struct Arena {
+    std::vector<unsigned char> host;
+    size_t add(const void* p, size_t bytes) {
+        size_t off = (host.size() + 255) & ~(size_t)255;
+        host.resize(off + bytes + 1, 0);
+        if (bytes) memcpy(host.data() + off, p, bytes);
+        return off;
+    }
+    template <class T>
+    size_t vec(const std::vector<T>& v) { return add(v.data(), v.size() * sizeof(T)); }
+};
+
+template <class T>
+const T* at(unsigned char* base, size_t off) { return reinterpret_cast<const T*>(base + off); }
+
+int align_up(int x, int a) { return (x + a - 1) / a * a; }
+
+uint64_t splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+// ---------------------------------------------------------------- layouts
+// Host-side tables of one layout; offsets into the arena.
+struct HostLayout {
+    std::string key;
+    sbh::SolvePlan plan;
+    sbk::DevLayout dev{};   // sizes + layouts; pointers patched after upload
+    std::map<std::string, size_t> off;
+};
+
+struct HostScen {
+    std::string path;
+    int layout = -1;
+    sbk::DevScen dev{};
+    std::map<std::string, size_t> off;
+    int n1 = 0;
+    int episode_steps = 0;
+    int64_t occ_seed = 17321;
+    int hour_m1_rows = 0;
+    int n_cont = 0, n_disc = 0;
+};
+
+const char* kStructural[] = {
+    "grid", "solved", "A_system_indptr", "A_system_indices", "A_system_data", "lu_perm_r", "lu_perm_c",
+    "lu_L_indptr", "lu_L_indices", "lu_U_indptr", "lu_U_indices", "capacitance_rate", "mass_coupling",
+    "mass_retained", "mass_gained", "solar_gain_coeff", "applied_indptr", "applied_indices", "applied_data",
+    "sensed_indptr", "sensed_indices", "sensed_data", "zone_area", "phys_room_idx", "room_offsets",
+    "room_cells", "vav_zone_offsets", "vav_zone_idx", "vav_ahu_idx", "coupled_vav_idx", "ahu_const",
+    "vav_const", "act_owner_kind", "act_owner_index", "act_actuator", "act_is_discrete", "act_min_native",
+    "act_max_native", "act_min_norm", "act_max_norm", "f_dev_kind", "f_dev_idx", "f_obs_id", "f_norm_mean",
+    "f_norm_var", "n_dev", "n_aux", "occ_params", nullptr};
+
+std::string structural_key(const sbh::Blob& b) {
+    std::string k;
+    for (int i = 0; kStructural[i]; i++) {
+        std::string s = b.bytes(kStructural[i]);
+        k += std::to_string(s.size()) + ":" + s;
+    }
+    return k;
+}
+
+template <class T>
+std::vector<T> take(const T* p, uint64_t n) { return p ? std::vector<T>(p, p + n) : std::vector<T>(); }
+
+// Builds one layout's tables (everything shared by its scenarios).
+bool make_layout(const sbh::Blob& b, int width, HostLayout* H, Arena& A, std::string* err) {
+    if (!sbh::build_plan(b, width, &H->plan, err)) return false;
+    const sbh::SolvePlan& P = H->plan;
+    sbk::DevLayout& D = H->dev;
+    uint64_t cnt = 0;
+    const int n = P.n;
+    const int64_t* grid = b.i64("grid");
+    const int nc_grid = (int)grid[1];
+    const double* ahu_c = b.f64("ahu_const", &cnt);
+    if (!ahu_c || cnt % 9) return (*err = "ahu_const missing"), false;
+    const int na = (int)(cnt / 9);
+    const int32_t* vz_off = b.i32("vav_zone_offsets", &cnt);
+    if (!vz_off) return (*err = "vav_zone_offsets missing"), false;
+    const int nv = (int)cnt - 1;
+    const double* zone_area = b.f64("zone_area", &cnt);
+    const int nz = (int)cnt;
+    const int32_t* vz_idx = b.i32("vav_zone_idx");
+    const int32_t* vav_ahu = b.i32("vav_ahu_idx");
+    const int32_t* coupled = b.i32("coupled_vav_idx");
+    const int32_t* phys = b.i32("phys_room_idx");
+    const int32_t* room_off = b.i32("room_offsets");
+    const int32_t* room_cells = b.i32("room_cells");
+    const double* vav_c = b.f64("vav_const");
+    if (!zone_area || !vz_idx || !vav_ahu || !phys || !room_off || !room_cells || !vav_c)
+        return (*err = "HVAC topology sections missing"), false;
+    if (na > SBK_MAX_AHU) return (*err = "too many AHUs"), false;
+    const int k = P.k;
+    if (k > 0 && !coupled) return (*err = "coupled_vav_idx missing"), false;
+    if (k > nv) return (*err = "more coupled columns than VAVs"), false;
+    for (int c = 0; c < k; c++)
+        if (coupled[c] < 0 || coupled[c] >= nv) return (*err = "coupled_vav_idx out of range"), false;
+    for (int v = 0; v < nv; v++)
+        if (vav_ahu[v] < 0 || vav_ahu[v] >= na) return (*err = "vav_ahu_idx out of range"), false;
+    // zones -> cells
+    std::vector<int> zoff(1, 0), zcells;
+    std::vector<uint8_t> is_room(n, 0);
+    int max_cells = 0;
+    for (int z = 0; z < nz; z++) {
+        int rm = phys[z];
+        for (int t = room_off[rm]; t < room_off[rm + 1]; t++) {
+            int p = room_cells[2 * t] * nc_grid + room_cells[2 * t + 1];
+            if (p < 0 || p >= n) return (*err = "room cell outside the grid"), false;
+            zcells.push_back(p);
+            is_room[p] = 1;
+        }
+        zoff.push_back((int)zcells.size());
+        max_cells = std::max(max_cells, zoff[z + 1] - zoff[z]);
+        if (zoff[z + 1] == zoff[z]) return (*err = "zone without cells"), false;
+    }
+    std::vector<double> vav_area(nv, 0.0);
+    for (int v = 0; v < nv; v++) {
+        double a = 0.0;
+        for (int t = vz_off[v]; t < vz_off[v + 1]; t++) a += zone_area[vz_idx[t]];
+        vav_area[v] = a;
+        if (!(a > 0.0)) return (*err = "VAVs without zone area are not supported"), false;
+    }
+    // zone -> coupled columns feeding it, ascending column
+    std::vector<int> zcol_off(1, 0), zcols;
+    {
+        std::vector<std::vector<int>> per(nz);
+        for (int c = 0; c < k; c++) {
+            int v = coupled[c];
+            for (int t = vz_off[v]; t < vz_off[v + 1]; t++) per[vz_idx[t]].push_back(c);
+        }
+        for (int z = 0; z < nz; z++) {
+            zcols.insert(zcols.end(), per[z].begin(), per[z].end());
+            zcol_off.push_back((int)zcols.size());
+        }
+    }
+    // actions
+    const uint8_t* kind = b.u8("act_owner_kind", &cnt);
+    const int n_act = (int)cnt;
+    const uint8_t* act = b.u8("act_actuator");
+    const uint8_t* disc = b.u8("act_is_discrete");
+    const int32_t* aidx = b.i32("act_owner_index");
+    const double* mn = b.f64("act_min_native");
+    const double* mx = b.f64("act_max_native");
+    const double* mnr = b.f64("act_min_norm");
+    const double* mxr = b.f64("act_max_norm");
+    if (!kind || !act || !disc || !aidx || !mn || !mx || !mnr || !mxr) return (*err = "action tables missing"), false;
+    std::vector<int> src(n_act);
+    int ncont = 0, ndisc = 0;
+    std::map<long long, int> targets;
+    for (int i = 0; i < n_act; i++) {
+        src[i] = disc[i] ? SB_CONT + ndisc++ : ncont++;
+        long long key = ((long long)kind[i] << 40) | ((long long)aidx[i] << 8) | act[i];
+        if (targets.count(key)) return (*err = "two actions drive the same actuator"), false;
+        targets[key] = i;
+    }
+    if (ncont > SB_CONT || ndisc > SB_DISC) return (*err = "scenario has more actions than SB_CONT/SB_DISC"), false;
+    // observation
+    const int n_dev = (int)b.i64_1("n_dev", 0), n_aux = (int)b.i64_1("n_aux", 0);
+    if (n_aux < 1 || n_aux > SBK_NAUX_MAX) return (*err = "n_aux out of range"), false;
+    if (n_dev + n_aux > SB_OBS) return (*err = "observation larger than OBS_SIZE"), false;
+    const uint8_t* fk = b.u8("f_dev_kind");
+    const uint8_t* fo = b.u8("f_obs_id");
+    const int32_t* fi = b.i32("f_dev_idx");
+    const double* fm = b.f64("f_norm_mean");
+    const double* fv = b.f64("f_norm_var");
+    if (n_dev && (!fk || !fo || !fi || !fm || !fv)) return (*err = "observation map missing"), false;
+    std::vector<double> fsd(n_dev);
+    for (int i = 0; i < n_dev; i++) fsd[i] = fv[i] > 0.0 ? sqrt(fv[i]) : 0.0;
+    // occupancy
+    const double* op = b.f64("occ_params");
+    if (!op) return (*err = "occ_params missing"), false;
+    const int nassign = (int)op[0];
+    if (nassign < 0 || nz * nassign > 312 || nz * nassign > 8 * width)
+        return (*err = "too many occupants per env"), false;
+    if (b.f64_1("conv_p", 0.0) != 0.0) return (*err = "stochastic convection (conv_p > 0) is not supported"), false;
+
+    D.n = n; D.nz = nz; D.nv = nv; D.na = na; D.k = k; D.n_act = n_act; D.n_cont = ncont; D.n_disc = ndisc;
+    D.n_dev = n_dev; D.n_aux = n_aux; D.nassign = nassign;
+    D.n_slots = P.n_slots; D.vec_base = P.vec_base; D.n_pass = P.n_pass(); D.width = width;
+    D.max_room_cells = max_cells;
+    // state record
+    sbk::StateLayout& S = D.st;
+    int o = 0;
+    auto f64a = [&](int count) { int r = o; o += 8 * count; return r; };
+    S.T = f64a(n); S.M = f64a(n);
+    S.damper = f64a(nv); S.reheat = f64a(nv); S.ratio = f64a(nv); S.heatsp = f64a(nv);
+    S.coolsp = f64a(nv); S.dcmd = f64a(nv); S.rcmd = f64a(nv); S.sensing = f64a(nv);
+    S.recirc = f64a(na); S.sat = f64a(na); S.fan = f64a(na); S.flow = f64a(na);
+    S.plant = f64a(8);
+    S.run = o; o += 4 * na; S.coolreq = o; o += 4 * na; S.iplant = o; o += 32;
+    S.mode = o; o += nv; S.prev_valid = o; o += nv; S.dcmd_set = o; o += nv; S.rcmd_set = o; o += nv;
+    S.occ_state = o; o += nz * nassign; S.occV = o; o += nz;
+    S.bytes = align_up(o, 16);
+    S.mt = S.bytes;
+    S.record_bytes = align_up(S.bytes + 4 * SBK_MT_N, 256);
+    // LDS
+    sbk::LdsLayout& Ls = D.lds;
+    int l = 0;
+    Ls.state = 0; l = S.bytes;
+    Ls.slots = l; Ls.mt = l; l += std::max(8 * P.n_slots, 4 * (SBK_MT_N + 1)); l = align_up(l, 16);
+    Ls.zq = l; l += 8 * nz;
+    Ls.vtmp = l; l += 8 * 3 * nv;
+    Ls.g = l; l += 8 * std::max(k, 1);
+    Ls.tair = l; l += 8 * std::max(k, 1);
+    Ls.atmp = l; l += 8 * 8 * na;
+    Ls.red = l; l += 8 * 64;
+    Ls.misc = l; l += 8 * 32;
+    Ls.iscr = l; l += 4 * (width / 64 + 8);
+    Ls.bytes = align_up(l, 16);
+    D.bytes_per_step = 2.0 * S.bytes + 4.0 * (ncont + ndisc) + 4.0 * SB_OBS + 8.0;
+    D.solve_flops = 2.0 * (double)P.n_pairs + (double)P.n_divs;
+
+    auto& O = H->off;
+    O["pinfo"] = A.add(P.passes.data(), P.passes.size() * sizeof(sbh::PassInfo));
+    O["row_off"] = A.vec(P.row_off);
+    O["hdr"] = A.vec(P.hdr);
+    O["words"] = A.vec(P.words);
+    O["slot_init"] = A.vec(P.slot_init);
+    O["pos"] = A.vec(P.pos);
+    O["air_slot"] = A.vec(P.air_slot);
+    O["air_node"] = A.vec(P.air_node);
+    O["cap"] = A.vec(take(b.f64("capacitance_rate"), n));
+    O["mcoup"] = A.vec(take(b.f64("mass_coupling"), n));
+    O["mret"] = A.vec(take(b.f64("mass_retained"), n));
+    O["mgain"] = A.vec(take(b.f64("mass_gained"), n));
+    {
+        uint64_t c2 = 0;
+        const double* sc = b.f64("solar_gain_coeff", &c2);
+        std::vector<double> v(n, 0.0);
+        if (sc && (int)c2 == n) v.assign(sc, sc + n);
+        O["solar_c"] = A.vec(v);
+    }
+    if (!b.f64("capacitance_rate") || !b.f64("mass_coupling") || !b.f64("mass_retained") || !b.f64("mass_gained"))
+        return (*err = "field sections missing"), false;
+    O["is_room"] = A.vec(is_room);
+    O["zone_cell_off"] = A.vec(zoff);
+    O["zone_cells"] = A.vec(zcells);
+    O["zone_area"] = A.vec(take(zone_area, nz));
+    O["vz_off"] = A.vec(take(vz_off, nv + 1));
+    O["vz_idx"] = A.vec(take(vz_idx, vz_off[nv]));
+    O["vav_area"] = A.vec(vav_area);
+    O["vav_ahu"] = A.vec(take(vav_ahu, nv));
+    O["coupled"] = A.vec(take(coupled, k));
+    O["zone_col_off"] = A.vec(zcol_off);
+    O["zone_cols"] = A.vec(zcols);
+    O["vav_c"] = A.vec(take(vav_c, 9 * nv));
+    O["ahu_c"] = A.vec(take(ahu_c, 9 * na));
+    O["act_kind"] = A.vec(take(kind, n_act));
+    O["act_act"] = A.vec(take(act, n_act));
+    O["act_disc"] = A.vec(take(disc, n_act));
+    O["act_idx"] = A.vec(take(aidx, n_act));
+    O["act_src"] = A.vec(src);
+    O["act_mn"] = A.vec(take(mn, n_act));
+    O["act_mx"] = A.vec(take(mx, n_act));
+    O["act_mnr"] = A.vec(take(mnr, n_act));
+    O["act_mxr"] = A.vec(take(mxr, n_act));
+    O["f_kind"] = A.vec(take(fk, n_dev));
+    O["f_id"] = A.vec(take(fo, n_dev));
+    O["f_idx"] = A.vec(take(fi, n_dev));
+    O["f_mean"] = A.vec(take(fm, n_dev));
+    O["f_sd"] = A.vec(fsd);
+    return true;
+}
+
+void patch_layout(HostLayout* H, unsigned char* d) {
+    sbk::DevLayout& D = H->dev;
+    auto& O = H->off;
+    D.pinfo = at<int>(d, O["pinfo"]);
+    D.row_off = at<int>(d, O["row_off"]);
+    D.hdr = at<uint64_t>(d, O["hdr"]);
+    D.words = at<uint32_t>(d, O["words"]);
+    D.slot_init = at<double>(d, O["slot_init"]);
+    D.pos = at<int>(d, O["pos"]);
+    D.air_slot = at<int>(d, O["air_slot"]);
+    D.air_node = at<int>(d, O["air_node"]);
+    D.cap = at<double>(d, O["cap"]);
+    D.mcoup = at<double>(d, O["mcoup"]);
+    D.mret = at<double>(d, O["mret"]);
+    D.mgain = at<double>(d, O["mgain"]);
+    D.solar_c = at<double>(d, O["solar_c"]);
+    D.is_room = at<uint8_t>(d, O["is_room"]);
+    D.zone_cell_off = at<int>(d, O["zone_cell_off"]);
+    D.zone_cells = at<int>(d, O["zone_cells"]);
+    D.zone_area = at<double>(d, O["zone_area"]);
+    D.vz_off = at<int>(d, O["vz_off"]);
+    D.vz_idx = at<int>(d, O["vz_idx"]);
+    D.vav_area = at<double>(d, O["vav_area"]);
+    D.vav_ahu = at<int>(d, O["vav_ahu"]);
+    D.coupled = at<int>(d, O["coupled"]);
+    D.zone_col_off = at<int>(d, O["zone_col_off"]);
+    D.zone_cols = at<int>(d, O["zone_cols"]);
+    D.vav_c = at<double>(d, O["vav_c"]);
+    D.ahu_c = at<double>(d, O["ahu_c"]);
+    D.act_kind = at<uint8_t>(d, O["act_kind"]);
+    D.act_act = at<uint8_t>(d, O["act_act"]);
+    D.act_disc = at<uint8_t>(d, O["act_disc"]);
+    D.act_idx = at<int>(d, O["act_idx"]);
+    D.act_src = at<int>(d, O["act_src"]);
+    D.act_mn = at<double>(d, O["act_mn"]);
+    D.act_mx = at<double>(d, O["act_mx"]);
+    D.act_mnr = at<double>(d, O["act_mnr"]);
+    D.act_mxr = at<double>(d, O["act_mxr"]);
+    D.f_kind = at<uint8_t>(d, O["f_kind"]);
+    D.f_id = at<uint8_t>(d, O["f_id"]);
+    D.f_idx = at<int>(d, O["f_idx"]);
+    D.f_mean = at<double>(d, O["f_mean"]);
+    D.f_sd = at<double>(d, O["f_sd"]);
+}
+
+std::vector<uint8_t> to_u8(const int64_t* p, uint64_t n) {
+    std::vector<uint8_t> v(n);
+    for (uint64_t i = 0; i < n; i++) v[i] = (uint8_t)p[i];
+    return v;
+}
+
+// Builds one scenario's tables (calendar, weather, prices, scalars).
+bool make_scen(const sbh::Blob& b, const HostLayout& Lh, HostScen* H, Arena& A, std::string* err) {
+    const sbk::DevLayout& L = Lh.dev;
+    sbk::DevScen& D = H->dev;
+    uint64_t c_amb = 0, c = 0;
+    const double* amb = b.f64("weather_ambient", &c_amb);
+    if (!amb) return (*err = "weather_ambient missing"), false;
+    uint64_t n1 = c_amb;
+    const char* f64_rows[] = {"sched_comfort", "sched_heat_sp", "sched_cool_sp", nullptr};
+    for (int i = 0; f64_rows[i]; i++) {
+        if (!b.f64(f64_rows[i], &c)) return (*err = std::string(f64_rows[i]) + " missing"), false;
+        n1 = std::min(n1, c);
+    }
+    const char* i64_rows[] = {"occ_hour", "rew_hour", "rew_month", nullptr};
+    for (int i = 0; i64_rows[i]; i++) {
+        if (!b.i64(i64_rows[i], &c)) return (*err = std::string(i64_rows[i]) + " missing"), false;
+        n1 = std::min(n1, c);
+    }
+    const char* u8_rows[] = {"occ_workday", "rew_workday", nullptr};
+    for (int i = 0; u8_rows[i]; i++) {
+        if (!b.u8(u8_rows[i], &c)) return (*err = std::string(u8_rows[i]) + " missing"), false;
+        n1 = std::min(n1, c);
+    }
+    const double* aux = b.f64("aux_time", &c);
+    if (!aux && L.n_aux > 1) return (*err = "aux_time missing"), false;
+    if (L.n_aux > 1) n1 = std::min(n1, c / (uint64_t)(L.n_aux - 1));
+    H->n1 = (int)n1;
+    uint64_t c_solar = 0;
+    const double* solar = b.f64("solar_irradiance", &c_solar);
+    std::vector<double> sol(n1, 0.0);
+    if (solar) for (uint64_t i = 0; i < n1 && i < c_solar; i++) sol[i] = solar[i];
+    uint64_t cm1 = 0;
+    const int64_t* hm1 = b.i64("occ_hour_m1", &cm1);
+    uint64_t cw1 = 0;
+    const uint8_t* wm1 = b.u8("occ_workday_m1", &cw1);
+    if (!hm1 || !wm1) return (*err = "occ_hour_m1/occ_workday_m1 missing"), false;
+    H->hour_m1_rows = (int)std::min(cm1, cw1);
+    const int n = L.n;
+    // Dirichlet + ambient exposure at the scenario's convection coefficient
+    // (complete_port/csim/sb_fdm.c:126-140)
+    const double* dir = b.f64("dirichlet_conductance");
+    const double* f0 = b.f64("ambient_face_areas_0");
+    const double* f1 = b.f64("ambient_face_areas_1");
+    const double* hz = b.f64("horizontal");
+    const double* vt = b.f64("vertical");
+    const double* cd = b.f64("solver_conductivity");
+    if (!dir || !f0 || !f1 || !hz || !vt || !cd) return (*err = "field sections missing"), false;
+    const double h = b.f64_1("convection_coefficient", 8.8);
+    std::vector<double> dirx(n);
+    for (int t = 0; t < n; t++) {
+        double e = 0.0;
+        if (f0[t] > 0.0) e += h * f0[t] / (1.0 + h * 0.5 * hz[t] / cd[t]);
+        if (f1[t] > 0.0) e += h * f1[t] / (1.0 + h * 0.5 * vt[t] / cd[t]);
+        dirx[t] = dir[t] + e;
+    }
+    const double* ti = b.f64("temp_init");
+    const double* mi = b.f64("mass_temp_init");
+    if (!ti || !mi) return (*err = "temp_init/mass_temp_init missing"), false;
+    const double* rw = b.f64("reward_scalars", &c);
+    if (!rw || c < 8) return (*err = "reward_scalars missing"), false;
+    const double* ewk = b.f64("elec_weekday_price");
+    const double* ewe = b.f64("elec_weekend_price");
+    const double* eco = b.f64("elec_carbon_rate");
+    const double* gp = b.f64("gas_month_price");
+    if (!ewk || !ewe || !eco || !gp) return (*err = "price tables missing"), false;
+    auto& O = H->off;
+    O["amb"] = A.vec(take(amb, n1));
+    O["solar_i"] = A.vec(sol);
+    O["comfort"] = A.vec(take(b.f64("sched_comfort"), n1));
+    O["heat_sp"] = A.vec(take(b.f64("sched_heat_sp"), n1));
+    O["cool_sp"] = A.vec(take(b.f64("sched_cool_sp"), n1));
+    O["aux_time"] = A.vec(take(aux, n1 * (uint64_t)std::max(L.n_aux - 1, 0)));
+    O["occ_hour"] = A.vec(to_u8(b.i64("occ_hour"), n1));
+    O["occ_work"] = A.vec(take(b.u8("occ_workday"), n1));
+    O["hour_m1"] = A.vec(to_u8(hm1, H->hour_m1_rows));
+    O["work_m1"] = A.vec(take(wm1, (uint64_t)H->hour_m1_rows));
+    O["rew_hour"] = A.vec(to_u8(b.i64("rew_hour"), n1));
+    O["rew_month"] = A.vec(to_u8(b.i64("rew_month"), n1));
+    O["rew_work"] = A.vec(take(b.u8("rew_workday"), n1));
+    O["dirx"] = A.vec(dirx);
+    O["temp_init"] = A.vec(take(ti, n));
+    O["mass_init"] = A.vec(take(mi, n));
+    O["elec_wk"] = A.vec(take(ewk, 24));
+    O["elec_we"] = A.vec(take(ewe, 24));
+    O["elec_co2"] = A.vec(take(eco, 24));
+    O["gas_price"] = A.vec(take(gp, 12));
+    D.n1 = (int)n1;
+    D.gas_co2 = b.f64_1("gas_carbon_rate", 0.0);
+    for (int i = 0; i < 8; i++) D.rw[i] = rw[i];
+    const double* bc = b.f64("boiler_const");
+    for (int i = 0; i < 10; i++) D.boiler_c[i] = bc ? bc[i] : 0.0;
+    {
+        // log(r2/c6)/c8 + 1/c4/r2 of the boiler tank loss (sb_reward.c:20-24)
+        const double* q = D.boiler_c;
+        double r2 = q[6] + q[9];
+        double cond = log(r2 / q[6]) / q[8];
+        double conv = 1.0 / q[4] / r2;
+        D.diss_den = cond + conv;
+    }
+    const double* pc = b.f64("pump_const");
+    D.pump_head0 = pc ? pc[0] : 0.0;
+    D.pump_eff = pc ? pc[1] : 1.0;
+    D.header_res = b.f64_1("hws_header_resistance", 0.0);
+    D.internal_w_m2 = b.f64_1("internal_gain_w_per_m2", 0.0);
+    D.standby_frac = b.f64_1("internal_gain_standby_fraction", 1.0);
+    D.occupant_w = b.f64_1("occupant_sensible_heat_w", 0.0);
+    {
+        double cv = b.f64_1("cv_size_cm", 20.0) / 100.0;
+        D.cv_area = cv * cv;
+    }
+    const double* op = b.f64("occ_params");
+    D.dt_sec = op[5];
+    D.ea = (int)op[1]; D.la = (int)op[2]; D.ed = (int)op[3]; D.ld = (int)op[4];
+    D.p_arr = 1.0 / ((D.la - D.ea) * 3600.0 / op[5] / 2.0);
+    D.p_dep = 1.0 / ((D.ld - D.ed) * 3600.0 / op[5] / 2.0);
+    {
+        // the field mean is needed only when an AHU serves no zone area
+        const int32_t* vav_ahu = b.i32("vav_ahu_idx");
+        std::vector<int> has(L.na, 0);
+        for (int v = 0; v < L.nv; v++) has[vav_ahu[v]] = 1;
+        D.conv_tmean = 0;
+        for (int a = 0; a < L.na; a++) if (!has[a]) D.conv_tmean = 1;
+    }
+    const double* meta = b.f64("obs_meta", &c);
+    H->episode_steps = (meta && c >= 4) ? (int)meta[3] : 0;
+    H->occ_seed = b.i64_1("occ_seed", 17321);
+    H->n_cont = L.n_cont;
+    H->n_disc = L.n_disc;
+    return true;
+}
+
+void patch_scen(HostScen* H, unsigned char* d) {
+    sbk::DevScen& D = H->dev;
+    auto& O = H->off;
+    D.amb = at<double>(d, O["amb"]);
+    D.solar_i = at<double>(d, O["solar_i"]);
+    D.comfort = at<double>(d, O["comfort"]);
+    D.heat_sp = at<double>(d, O["heat_sp"]);
+    D.cool_sp = at<double>(d, O["cool_sp"]);
+    D.aux_time = at<double>(d, O["aux_time"]);
+    D.occ_hour = at<uint8_t>(d, O["occ_hour"]);
+    D.occ_work = at<uint8_t>(d, O["occ_work"]);
+    D.hour_m1 = at<uint8_t>(d, O["hour_m1"]);
+    D.work_m1 = at<uint8_t>(d, O["work_m1"]);
+    D.rew_hour = at<uint8_t>(d, O["rew_hour"]);
+    D.rew_month = at<uint8_t>(d, O["rew_month"]);
+    D.rew_work = at<uint8_t>(d, O["rew_work"]);
+    D.dirx = at<double>(d, O["dirx"]);
+    D.temp_init = at<double>(d, O["temp_init"]);
+    D.mass_init = at<double>(d, O["mass_init"]);
+    D.elec_wk = at<double>(d, O["elec_wk"]);
+    D.elec_we = at<double>(d, O["elec_we"]);
+    D.elec_co2 = at<double>(d, O["elec_co2"]);
+    D.gas_price = at<double>(d, O["gas_price"]);
+}
+
+// ---------------------------------------------------------------- vec
+struct Vec {
+    int n = 0, width = 64, lds_bytes = 0;
+    float reward_scale = 1.0f;
+    Env* envs = nullptr;
+    std::vector<std::string> paths;           // ordered scenario list
+    std::vector<HostLayout> layouts;
+    std::vector<HostScen> scens;
+    std::vector<sbk::EnvDesc> desc;
+    std::vector<int> order;
+    std::vector<uint32_t> seeds;
+    std::vector<int> env_scen_local;
+    unsigned char* d_arena = nullptr;
+    unsigned char* d_state = nullptr;
+    size_t state_bytes = 0;
+    sbk::DevLayout* d_layouts = nullptr;
+    sbk::DevScen* d_scens = nullptr;
+    sbk::EnvDesc* d_envs = nullptr;
+    int* d_order = nullptr;
+    int* d_ncont = nullptr;
+    int* d_ndisc = nullptr;
+    float* obs = nullptr;
+    float* actions = nullptr;
+    float* rewards = nullptr;
+    float* terminals = nullptr;
+    double bytes_per_step = 0.0, flops_per_step = 0.0;
+};
+
+sbk::KParams params(Vec* v, int mode) {
+    sbk::KParams p{};
+    p.envs = v->d_envs;
+    p.order = v->d_order;
+    p.layouts = v->d_layouts;
+    p.scens = v->d_scens;
+    p.state = v->d_state;
+    p.actions = v->actions;
+    p.obs = v->obs;
+    p.rewards = v->rewards;
+    p.terminals = v->terminals;
+    p.host_env = v->envs;
+    p.env_stride = (int)sizeof(Env);
+    p.log_offset = (int)offsetof(Env, log);
+    p.n_envs = v->n;
+    p.mode = mode;
+    p.reward_scale = v->reward_scale;
+    return p;
+}
+
+void launch(Vec* v, int mode) {
+    sbk::KParams p = params(v, mode);
+    int rc = sbk_launch_step(&p, v->n, v->width, v->lds_bytes, g_stream);
+    if (rc != 0) die(std::string("step kernel launch failed: ") + hipGetErrorString((hipError_t)rc));
+}
+
+Vec* vec_of(Env* envs) {
+    if (!envs || !envs[0].vec) die("env array was not created by puf_vec_create");
+    return static_cast<Vec*>(envs[0].vec);
+}
+
+bool ends_with(const std::string& s, const std::string& suf) {
+    return s.size() >= suf.size() && s.compare(s.size() - suf.size(), suf.size(), suf) == 0;
+}
+
+std::vector<std::string> list_blobs(const std::string& dir) {
+    std::vector<std::string> out;
+    DIR* d = opendir(dir.c_str());
+    if (!d) return out;
+    while (dirent* e = readdir(d)) {
+        std::string nm = e->d_name;
+        if (ends_with(nm, ".sbb")) out.push_back(dir + "/" + nm);
+    }
+    closedir(d);
+    std::sort(out.begin(), out.end());
+    return out;
+}
+
+// all buildings' first weather, then all buildings' second weather, ...
+// (building = file name up to "__"), complete_port/gpu/smart_buildings.cu:2435-2459
+std::vector<std::string> round_robin(const std::vector<std::string>& p) {
+    std::vector<std::string> keys, blds, out;
+    for (auto& f : p) {
+        std::string base = f.substr(f.find_last_of('/') + 1);
+        std::string b = base.substr(0, base.find("__"));
+        keys.push_back(b);
+        if (std::find(blds.begin(), blds.end(), b) == blds.end()) blds.push_back(b);
+    }
+    std::vector<int> used(p.size(), 0);
+    while (out.size() < p.size())
+        for (auto& b : blds)
+            for (size_t i = 0; i < p.size(); i++)
+                if (!used[i] && keys[i] == b) { out.push_back(p[i]); used[i] = 1; break; }
+    return out;
+}
+
+float kw(Dict* d, const char* key, float dflt) {
+    DictItem* it = d ? dict_find(d, key) : nullptr;
+    return it ? it->value : dflt;
+}
+
+const char* kws(Dict* d, const char* key) {
+    DictItem* it = d ? dict_find(d, key) : nullptr;
+    return (it && it->str && it->str[0]) ? it->str : nullptr;
+}
+
+void mt_seed(uint32_t* mt, uint32_t seed) {
+    mt[0] = seed;
+    for (int i = 1; i < SBK_MT_N; i++) mt[i] = 1812433253u * (mt[i - 1] ^ (mt[i - 1] >> 30)) + (uint32_t)i;
+}
+
+}  // namespace
+
+// ================================================================== C ABI
+extern "C" {
+
+DictItem* dict_find(Dict* d, const char* key) {
+    if (!d || !key) return nullptr;
+    for (int i = 0; i < d->size; i++)
+        if (d->items[i].key && strcmp(d->items[i].key, key) == 0) return &d->items[i];
+    return nullptr;
+}
+
+void dict_set(Dict* d, const char* key, float value) {
+    if (!d) return;
+    DictItem* it = dict_find(d, key);
+    if (it) { it->value = value; return; }
+    if (d->size < d->capacity) {
+        d->items[d->size].key = key;
+        d->items[d->size].value = value;
+        d->items[d->size].str = nullptr;
+        d->size++;
+    }
+}
+
+Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, float* rewards, float* terminals) {
+    if (n <= 0) die("puf_vec_create: n must be positive");
+    if (!observations || !actions || !rewards || !terminals) die("puf_vec_create: null trainer buffer");
+    auto v = std::make_unique<Vec>();
+    v->n = n;
+    v->obs = observations;
+    v->actions = actions;
+    v->rewards = rewards;
+    v->terminals = terminals;
+    v->width = (int)kw(kwargs, "block", 64.0f);
+    if (v->width != 64) die("env.block must be 64 (one wavefront per env)");
+    v->reward_scale = kw(kwargs, "reward_scale", 1.0f);
+    // ---- scenario list
+    std::vector<std::string> files;
+    if (const char* one = kws(kwargs, "blob")) {
+        files.push_back(one);
+    } else {
+        const char* dir = kws(kwargs, "blob_dir");
+        if (!dir) dir = getenv("SB_BLOB_DIR");
+        if (dir && dir[0]) files = round_robin(list_blobs(dir));
+        if (files.empty()) die("no scenario. Set env.blob or env.blob_dir (or SB_BLOB_DIR).");
+    }
+    int G = (int)kw(kwargs, "groups", 0.0f);
+    if (G <= 0) G = n / 32;
+    G = std::min(G, (int)files.size());
+    G = std::max(G, 1);
+    G = std::min(G, n);
+    files.resize(G);
+    v->paths = files;
+    std::vector<int> scnt(G);
+    for (int i = 0; i < G; i++) scnt[i] = n / G + (i < n % G ? 1 : 0);
+    // ---- layouts + scenarios
+    Arena A;
+    std::map<std::string, int> layout_of_key;
+    for (int i = 0; i < G; i++) {
+        sbh::Blob b;
+        std::string err;
+        if (!b.open(files[i], &err)) die(err);
+        std::string key = structural_key(b);
+        int li;
+        auto it = layout_of_key.find(key);
+        if (it == layout_of_key.end()) {
+            HostLayout H;
+            H.key = key;
+            if (!make_layout(b, v->width, &H, A, &err)) die(files[i] + ": " + err);
+            li = (int)v->layouts.size();
+            v->layouts.push_back(std::move(H));
+            layout_of_key[key] = li;
+        } else {
+            li = it->second;
+        }
+        HostScen S;
+        S.path = files[i];
+        S.layout = li;
+        if (!make_scen(b, v->layouts[li], &S, A, &err)) die(files[i] + ": " + err);
+        S.dev.layout = li;
+        v->scens.push_back(std::move(S));
+    }
+    // ---- envs
+    const int max_steps_kw = (int)kw(kwargs, "max_steps", 0.0f);
+    const int desync = (int)kw(kwargs, "desync", 0.0f);
+    const uint64_t desync_seed = (uint64_t)kw(kwargs, "desync_seed", 7.0f);
+    const int per_env_seed = (int)kw(kwargs, "per_env_seed", 1.0f);
+    size_t state_off = 0;
+    int e = 0;
+    for (int i = 0; i < G; i++) {
+        const HostScen& S = v->scens[i];
+        const HostLayout& L = v->layouts[S.layout];
+        int ms = max_steps_kw > 0 ? max_steps_kw : S.episode_steps;
+        if (ms <= 0) ms = S.n1 - 1;
+        for (int j = 0; j < scnt[i]; j++, e++) {
+            sbk::EnvDesc d{};
+            d.scen = i;
+            d.layout = S.layout;
+            d.max_steps = ms;
+            d.state_off = (long long)state_off;
+            int start = 0;
+            if (desync) {
+                int range = S.n1 - 1 - ms + 1;
+                if (range < 1) die(S.path + ": calendar too short for desynchronised starts");
+                range = std::min(range, std::max(S.episode_steps, 1));
+                start = (int)(splitmix64(desync_seed * 0x100000001B3ull + (uint64_t)e) % (uint64_t)range);
+            }
+            if (start + ms > S.n1 - 1) die(S.path + ": calendar tables shorter than the episode");
+            if (start >= S.hour_m1_rows) die(S.path + ": occ_hour_m1 has no row for the start offset");
+            d.start = start;
+            v->desc.push_back(d);
+            v->seeds.push_back((uint32_t)(S.occ_seed + (per_env_seed ? j : 0)));
+            v->env_scen_local.push_back(j);
+            state_off += (size_t)L.dev.st.record_bytes;
+        }
+    }
+    v->state_bytes = state_off;
+    // launch order: largest layouts first
+    v->order.resize(n);
+    for (int i = 0; i < n; i++) v->order[i] = i;
+    std::stable_sort(v->order.begin(), v->order.end(), [&](int a, int b) {
+        return v->layouts[v->desc[a].layout].dev.lds.bytes > v->layouts[v->desc[b].layout].dev.lds.bytes;
+    });
+    // ---- upload tables
+    hip_ok(hipMalloc(&v->d_arena, A.host.size()), "hipMalloc(tables)");
+    hip_ok(hipMemcpy(v->d_arena, A.host.data(), A.host.size(), hipMemcpyHostToDevice), "upload tables");
+    std::vector<sbk::DevLayout> dl;
+    int lds = 0;
+    for (auto& L : v->layouts) {
+        patch_layout(&L, v->d_arena);
+        dl.push_back(L.dev);
+        lds = std::max(lds, L.dev.lds.bytes);
+    }
+    std::vector<sbk::DevScen> ds;
+    for (auto& S : v->scens) {
+        patch_scen(&S, v->d_arena);
+        ds.push_back(S.dev);
+    }
+    v->lds_bytes = lds;
+    if (lds > 160 * 1024) die("layout needs more LDS than a workgroup has");
+    if (lds > 64 * 1024) hip_ok((hipError_t)sbk_set_lds_limit(v->width, lds), "LDS limit");
+    hip_ok(hipMalloc(&v->d_layouts, sizeof(sbk::DevLayout) * dl.size()), "hipMalloc(layouts)");
+    hip_ok(hipMemcpy(v->d_layouts, dl.data(), sizeof(sbk::DevLayout) * dl.size(), hipMemcpyHostToDevice), "upload");
+    hip_ok(hipMalloc(&v->d_scens, sizeof(sbk::DevScen) * ds.size()), "hipMalloc(scens)");
+    hip_ok(hipMemcpy(v->d_scens, ds.data(), sizeof(sbk::DevScen) * ds.size(), hipMemcpyHostToDevice), "upload");
+    hip_ok(hipMalloc(&v->d_envs, sizeof(sbk::EnvDesc) * n), "hipMalloc(envs)");
+    hip_ok(hipMemcpy(v->d_envs, v->desc.data(), sizeof(sbk::EnvDesc) * n, hipMemcpyHostToDevice), "upload");
+    hip_ok(hipMalloc(&v->d_order, sizeof(int) * n), "hipMalloc(order)");
+    hip_ok(hipMemcpy(v->d_order, v->order.data(), sizeof(int) * n, hipMemcpyHostToDevice), "upload");
+    {
+        std::vector<int> nc(n), nd(n);
+        for (int i = 0; i < n; i++) {
+            nc[i] = v->layouts[v->desc[i].layout].dev.n_cont;
+            nd[i] = v->layouts[v->desc[i].layout].dev.n_disc;
+        }
+        hip_ok(hipMalloc(&v->d_ncont, sizeof(int) * n), "hipMalloc");
+        hip_ok(hipMalloc(&v->d_ndisc, sizeof(int) * n), "hipMalloc");
+        hip_ok(hipMemcpy(v->d_ncont, nc.data(), sizeof(int) * n, hipMemcpyHostToDevice), "upload");
+        hip_ok(hipMemcpy(v->d_ndisc, nd.data(), sizeof(int) * n, hipMemcpyHostToDevice), "upload");
+    }
+    // ---- initial state records: pump head, seeded MT19937 (index 624)
+    {
+        std::vector<unsigned char> rec(v->state_bytes, 0);
+        for (int i = 0; i < n; i++) {
+            const sbk::EnvDesc& d = v->desc[i];
+            const sbk::DevLayout& L = v->layouts[d.layout].dev;
+            unsigned char* r = rec.data() + d.state_off;
+            reinterpret_cast<double*>(r + L.st.plant)[sbk::PF_PUMP_HEAD] = v->scens[d.scen].dev.pump_head0;
+            reinterpret_cast<int*>(r + L.st.iplant)[sbk::PI_MT_IDX] = SBK_MT_N;
+            mt_seed(reinterpret_cast<uint32_t*>(r + L.st.mt), v->seeds[i]);
+            v->bytes_per_step += L.bytes_per_step;
+            v->flops_per_step += L.solve_flops;
+        }
+        hip_ok(hipMalloc(&v->d_state, v->state_bytes), "hipMalloc(state)");
+        hip_ok(hipMemcpy(v->d_state, rec.data(), v->state_bytes, hipMemcpyHostToDevice), "upload state");
+    }
+    // ---- Env array (host memory the device can write: logs)
+    void* envmem = nullptr;
+    hip_ok(hipHostMalloc(&envmem, sizeof(Env) * (size_t)n, hipHostMallocCoherent), "hipHostMalloc(envs)");
+    memset(envmem, 0, sizeof(Env) * (size_t)n);
+    v->envs = static_cast<Env*>(envmem);
+    for (int i = 0; i < n; i++) {
+        Env& E = v->envs[i];
+        const sbk::DevLayout& L = v->layouts[v->desc[i].layout].dev;
+        E.agents[0].observations = observations + (size_t)i * SB_OBS;
+        E.agents[0].actions = actions + (size_t)i * SB_ACT;
+        E.agents[0].rewards = rewards + i;
+        E.agents[0].terminals = terminals + i;
+        E.num_agents = 1;
+        E.max_steps = v->desc[i].max_steps;
+        E.start_offset = v->desc[i].start;
+        E.n_act = L.n_act;
+        E.n_cont = L.n_cont;
+        E.n_disc = L.n_disc;
+        E.loaded = 1;
+        E.index = i;
+        E.vec = v.get();
+    }
+    hip_ok(hipDeviceSynchronize(), "sync after create");
+    g_last = v.get();
+    Env* out = v->envs;
+    v.release();
+    return out;
+}
+
+void puf_bind_stream(void* s) {
+    if (s == nullptr) return;
+    g_stream = (hipStream_t)s;
+}
+
+void puf_init(Env* env, Dict* kwargs) {
+    (void)kwargs;
+    if (!env) return;
+    memset(&env->log, 0, sizeof(env->log));
+}
+
+void puf_reset(Env* envs) {
+    Vec* v = vec_of(envs);
+    for (int i = 0; i < v->n; i++) {
+        v->envs[i].step = 0;
+        unsigned char* m = v->envs[i].agents[0].action_mask;
+        if (m) {
+            for (int h = 0; h < SB_CONT; h++) m[h] = (h < v->envs[i].n_cont) ? 1 : 0;
+            for (int h = 0; h < SB_DISC; h++) {
+                unsigned char b = (h < v->envs[i].n_disc) ? 1 : 0;
+                m[SB_CONT + 2 * h] = b;
+                m[SB_CONT + 2 * h + 1] = b;
+            }
+        }
+    }
+    launch(v, sbk::KMODE_RESET);
+    hip_ok(hipStreamSynchronize(g_stream), "reset");
+}
+
+void puf_step(Env* envs) { launch(vec_of(envs), sbk::KMODE_STEP); }
+
+void puf_render(Env* env) { (void)env; }
+
+void puf_close(Env* envs) {
+    if (!envs) return;
+    Vec* v = vec_of(envs);
+    (void)hipStreamSynchronize(g_stream);
+    (void)hipFree(v->d_arena);
+    (void)hipFree(v->d_state);
+    (void)hipFree(v->d_layouts);
+    (void)hipFree(v->d_scens);
+    (void)hipFree(v->d_envs);
+    (void)hipFree(v->d_order);
+    (void)hipFree(v->d_ncont);
+    (void)hipFree(v->d_ndisc);
+    (void)hipHostFree(v->envs);
+    if (g_last == v) g_last = nullptr;
+    delete v;
+}
+
+void puf_log(Log* log, Dict* out) {
+    dict_set(out, "perf", log->perf);
+    dict_set(out, "score", log->score);
+    dict_set(out, "episode_return", log->episode_return);
+    dict_set(out, "episode_length", log->episode_length);
+    dict_set(out, "reward_mean", log->reward_mean);
+    dict_set(out, "n", log->n);
+}
+
+void puf_live_log(Env* envs, Dict* out) {
+    Vec* v = vec_of(envs);
+    hip_ok(hipStreamSynchronize(g_stream), "live log");
+    double rs = 0.0;
+    long long st = 0, eps = 0;
+    std::vector<unsigned char> img;
+    for (int i = 0; i < v->n; i++) {
+        const sbk::EnvDesc& d = v->desc[i];
+        const sbk::DevLayout& L = v->layouts[d.layout].dev;
+        double pf[8];
+        int ip[8];
+        hip_ok(hipMemcpy(pf, v->d_state + d.state_off + L.st.plant, sizeof(pf), hipMemcpyDeviceToHost), "copy");
+        hip_ok(hipMemcpy(ip, v->d_state + d.state_off + L.st.iplant, sizeof(ip), hipMemcpyDeviceToHost), "copy");
+        rs += pf[sbk::PF_REW_SUM];
+        st += ip[sbk::PI_STEPS_TOTAL];
+        eps += ip[sbk::PI_EPISODES];
+    }
+    dict_set(out, "env_steps", (float)st);
+    dict_set(out, "episodes", (float)eps);
+    dict_set(out, "reward_mean", st ? (float)(rs / (double)st) : 0.0f);
+}
+
+void puf_mask_init(unsigned char* mask, int width, int nagents) {
+    Vec* v = g_last;
+    if (!v || !mask) return;
+    for (int a = 0; a < nagents; a++) {
+        unsigned char* m = mask + (size_t)a * width;
+        const Env& E = v->envs[a < v->n ? a : v->n - 1];
+        for (int h = 0; h < width; h++) m[h] = 0;
+        for (int h = 0; h < SB_CONT && h < width; h++) m[h] = (h < E.n_cont) ? 1 : 0;
+        for (int h = 0; h < SB_DISC && SB_CONT + 2 * h + 1 < width; h++) {
+            unsigned char b = (h < E.n_disc) ? 1 : 0;
+            m[SB_CONT + 2 * h] = b;
+            m[SB_CONT + 2 * h + 1] = b;
+        }
+    }
+}
+
+void sbx_gen_actions(Env* envs, uint64_t seed, uint32_t step) {
+    Vec* v = vec_of(envs);
+    int rc = sbk_launch_gen_actions(v->actions, v->d_ncont, v->d_ndisc, v->n, seed, step, g_stream);
+    if (rc != 0) die("action kernel launch failed");
+}
+
+void sbx_vec_info(Env* envs, SbxVecInfo* out) {
+    Vec* v = vec_of(envs);
+    memset(out, 0, sizeof(*out));
+    out->n_envs = v->n;
+    out->n_layouts = (int)v->layouts.size();
+    out->n_scenarios = (int)v->scens.size();
+    out->block = v->width;
+    out->lds_bytes = v->lds_bytes;
+    for (auto& L : v->layouts) out->max_nodes = std::max(out->max_nodes, L.dev.n);
+    out->bytes_per_step = v->bytes_per_step;
+    out->flops_per_step = v->flops_per_step;
+}
+
+int sbx_env_state(Env* envs, int i, double* out, int cap) {
+    Vec* v = vec_of(envs);
+    if (i < 0 || i >= v->n) return -1;
+    const sbk::EnvDesc& d = v->desc[i];
+    const sbk::DevLayout& L = v->layouts[d.layout].dev;
+    std::vector<unsigned char> r(L.st.bytes);
+    hip_ok(hipStreamSynchronize(g_stream), "state sync");
+    hip_ok(hipMemcpy(r.data(), v->d_state + d.state_off, r.size(), hipMemcpyDeviceToHost), "state copy");
+    const unsigned char* s = r.data();
+    auto f = [&](int off) { return reinterpret_cast<const double*>(s + off); };
+    std::vector<double> o;
+    for (int t = 0; t < L.n; t++) o.push_back(f(L.st.T)[t]);
+    for (int t = 0; t < L.n; t++) o.push_back(f(L.st.M)[t]);
+    for (int x = 0; x < L.nv; x++) o.push_back(f(L.st.damper)[x]);
+    for (int x = 0; x < L.nv; x++) o.push_back(f(L.st.reheat)[x]);
+    for (int x = 0; x < L.nv; x++) o.push_back(f(L.st.ratio)[x]);
+    for (int x = 0; x < L.nv; x++) o.push_back(f(L.st.sensing)[x]);
+    for (int a = 0; a < L.na; a++) o.push_back(f(L.st.flow)[a]);
+    for (int a = 0; a < L.na; a++) o.push_back(f(L.st.sat)[a]);
+    for (int a = 0; a < L.na; a++) o.push_back(f(L.st.recirc)[a]);
+    for (int a = 0; a < L.na; a++) o.push_back(f(L.st.fan)[a]);
+    for (int c = 0; c < 2 * L.k; c++) o.push_back(NAN);   // air_g / air_T are not kept between steps
+    for (int z = 0; z < L.nz; z++) o.push_back((double)s[L.st.occV + z]);
+    const double* pf = f(L.st.plant);
+    const int* ip = reinterpret_cast<const int*>(s + L.st.iplant);
+    o.push_back(pf[sbk::PF_BOILER_CUR]);
+    o.push_back(pf[sbk::PF_BOILER_RET]);
+    o.push_back(pf[sbk::PF_BOILER_SP]);
+    o.push_back(pf[sbk::PF_PUMP_HEAD]);
+    o.push_back((double)ip[sbk::PI_STEP_INDEX]);
+    // extras after the oracle's layout: f64 reward sum since puf_reset, steps since puf_reset
+    o.push_back(pf[sbk::PF_REW_SUM]);
+    o.push_back((double)ip[sbk::PI_STEPS_TOTAL]);
+    if ((int)o.size() > cap) return -1;
+    memcpy(out, o.data(), o.size() * sizeof(double));
+    return (int)o.size();
+}
+
+float sbx_time_step(Env* envs, int iters) {
+    Vec* v = vec_of(envs);
+    hipEvent_t a, b;
+    hip_ok(hipEventCreate(&a), "event");
+    hip_ok(hipEventCreate(&b), "event");
+    hip_ok(hipEventRecord(a, g_stream), "event");
+    for (int i = 0; i < iters; i++) launch(v, sbk::KMODE_STEP);
+    hip_ok(hipEventRecord(b, g_stream), "event");
+    hip_ok(hipEventSynchronize(b), "event sync");
+    float ms = 0.f;
+    hip_ok(hipEventElapsedTime(&ms, a, b), "elapsed");
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    return ms;
+}
+
+int sbx_env_meta(Env* envs, int i, int* scenario, int* start, uint32_t* occ_seed) {
+    Vec* v = vec_of(envs);
+    if (i < 0 || i >= v->n) return -1;
+    if (scenario) *scenario = v->desc[i].scen;
+    if (start) *start = v->desc[i].start;
+    if (occ_seed) *occ_seed = v->seeds[i];
+    return 0;
+}
+
+const char* sbx_scenario_path(Env* envs, int s) {
+    Vec* v = vec_of(envs);
+    if (s < 0 || s >= (int)v->paths.size()) return nullptr;
+    return v->paths[s].c_str();
+}
+
+struct PlanHolder {
+    sbh::SolvePlan plan;
+};
+static std::map<const void*, PlanHolder*> g_plans;
+
+int sbx_plan_layout(const char* blob_path, int width, SbxPlan* out) {
+    if (!blob_path || !out) return -1;
+    if (width != 64 && width != 128 && width != 256) { g_err = "width must be 64, 128 or 256"; return -1; }
+    sbh::Blob b;
+    std::string err;
+    if (!b.open(blob_path, &err)) { g_err = err; return -1; }
+    auto* h = new PlanHolder();
+    if (!sbh::build_plan(b, width, &h->plan, &err)) { g_err = err; delete h; return -2; }
+    const sbh::SolvePlan& P = h->plan;
+    memset(out, 0, sizeof(*out));
+    out->n = P.n;
+    out->width = P.width;
+    out->n_slots = P.n_slots;
+    out->vec_base = P.vec_base;
+    out->n_pass = P.n_pass();
+    out->n_levels = P.n_levels;
+    out->n_tasks = P.n_tasks;
+    out->n_pairs = P.n_pairs;
+    out->kmax = sbh::kPlanKmax;
+    out->n_hdr = (int)P.hdr.size();
+    out->n_words = (int)P.words.size();
+    out->n_rows = (int)P.row_off.size();
+    out->pass_info = reinterpret_cast<const int*>(P.passes.data());
+    out->row_off = P.row_off.data();
+    out->hdr = P.hdr.data();
+    out->words = P.words.data();
+    out->slot_init = P.slot_init.data();
+    out->pos = P.pos.data();
+    out->air_slot = P.air_slot.data();
+    out->air_node = P.air_node.data();
+    out->k = P.k;
+    g_plans[out->hdr] = h;
+    return 0;
+}
+
+void sbx_plan_free(SbxPlan* p) {
+    if (!p) return;
+    auto it = g_plans.find(p->hdr);
+    if (it != g_plans.end()) {
+        delete it->second;
+        g_plans.erase(it);
+    }
+    memset(p, 0, sizeof(*p));
+}
+
+const char* sbx_last_error(void) { return g_err.c_str(); }
+
+const char* sbx_version(void) { return "sbenv 0.1 gfx950"; }
+
+}  // extern "C"

@@ -1,0 +1,243 @@
+"""Python front-end of libsbenv.so (the MI355X env step) over its C ABI.
+
+Mirrors the PufferLib GPU env binding the reference exports
+(complete_port/gpu/smart_buildings.cu:3307-3323): `VecEnv` owns the trainer-side
+device buffers (torch tensors on the GPU), creates the env vec through
+puf_vec_create with the same kwargs (blob / blob_dir / groups / max_steps /
+desync / reward_scale ...), and steps it with puf_step on a bound stream.
+
+There is no CPU fallback: loading fails loudly when libsbenv.so is missing.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+PKG = Path(__file__).resolve().parent
+LIB_PATH = PKG / "libsbenv.so"
+SB_OBS, SB_CONT, SB_DISC = 1024, 256, 16
+SB_ACT = SB_CONT + SB_DISC
+P = ctypes.c_void_p
+
+
+class Log(ctypes.Structure):
+    _fields_ = [("perf", ctypes.c_float), ("score", ctypes.c_float),
+                ("episode_return", ctypes.c_float), ("episode_length", ctypes.c_float),
+                ("reward_mean", ctypes.c_float), ("n", ctypes.c_float)]
+
+
+class Agent(ctypes.Structure):
+    _fields_ = [("observations", P), ("actions", P), ("rewards", P), ("terminals", P),
+                ("action_mask", P), ("policy", ctypes.c_int)]
+
+
+class Env(ctypes.Structure):
+    _fields_ = [("log", Log), ("agents", Agent * 1), ("num_agents", ctypes.c_int),
+                ("tag", ctypes.c_int), ("boundary_reached", ctypes.c_int), ("step", ctypes.c_int),
+                ("max_steps", ctypes.c_int), ("start_offset", ctypes.c_int),
+                ("n_act", ctypes.c_int), ("n_cont", ctypes.c_int), ("n_disc", ctypes.c_int),
+                ("loaded", ctypes.c_int), ("rng", ctypes.c_uint), ("seed", ctypes.c_int),
+                ("index", ctypes.c_int), ("vec", P)]
+
+
+class DictItem(ctypes.Structure):
+    _fields_ = [("key", ctypes.c_char_p), ("value", ctypes.c_float), ("str", ctypes.c_char_p)]
+
+
+class Dict(ctypes.Structure):
+    _fields_ = [("items", ctypes.POINTER(DictItem)), ("size", ctypes.c_int), ("capacity", ctypes.c_int)]
+
+
+class SbxVecInfo(ctypes.Structure):
+    _fields_ = [("n_envs", ctypes.c_int), ("n_layouts", ctypes.c_int), ("n_scenarios", ctypes.c_int),
+                ("block", ctypes.c_int), ("lds_bytes", ctypes.c_int), ("max_nodes", ctypes.c_int),
+                ("bytes_per_step", ctypes.c_double), ("flops_per_step", ctypes.c_double)]
+
+
+class SbxPlan(ctypes.Structure):
+    _fields_ = [("n", ctypes.c_int), ("width", ctypes.c_int), ("n_slots", ctypes.c_int),
+                ("vec_base", ctypes.c_int), ("n_pass", ctypes.c_int), ("n_levels", ctypes.c_int),
+                ("n_tasks", ctypes.c_int), ("kmax", ctypes.c_int), ("n_pairs", ctypes.c_longlong),
+                ("n_hdr", ctypes.c_int), ("n_words", ctypes.c_int), ("n_rows", ctypes.c_int),
+                ("pass_info", ctypes.POINTER(ctypes.c_int)), ("row_off", ctypes.POINTER(ctypes.c_int)),
+                ("hdr", ctypes.POINTER(ctypes.c_uint64)), ("words", ctypes.POINTER(ctypes.c_uint32)),
+                ("slot_init", ctypes.POINTER(ctypes.c_double)), ("pos", ctypes.POINTER(ctypes.c_int)),
+                ("air_slot", ctypes.POINTER(ctypes.c_int)), ("air_node", ctypes.POINTER(ctypes.c_int)),
+                ("k", ctypes.c_int)]
+
+
+# every symbol include/sbenv.h declares
+EXPORTS = [
+    "dict_find", "dict_set", "puf_vec_create", "puf_bind_stream", "puf_init", "puf_reset", "puf_step",
+    "puf_render", "puf_close", "puf_log", "puf_live_log", "puf_mask_init", "sbx_gen_actions",
+    "sbx_vec_info", "sbx_env_state", "sbx_time_step", "sbx_env_meta", "sbx_scenario_path",
+    "sbx_plan_layout", "sbx_plan_free", "sbx_last_error", "sbx_version",
+]
+
+_LIB = None
+
+
+def lib() -> ctypes.CDLL:
+    """Loads libsbenv.so (raises if it has not been built)."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with "
+                               "python -m neurips2026_smart_building_challenge_amd.build")
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.dict_find.restype = ctypes.POINTER(DictItem)
+        L.dict_find.argtypes = [ctypes.POINTER(Dict), ctypes.c_char_p]
+        L.dict_set.argtypes = [ctypes.POINTER(Dict), ctypes.c_char_p, ctypes.c_float]
+        L.puf_vec_create.restype = ctypes.POINTER(Env)
+        L.puf_vec_create.argtypes = [ctypes.c_int, ctypes.POINTER(Dict), P, P, P, P]
+        L.puf_bind_stream.argtypes = [P]
+        for f in (L.puf_reset, L.puf_step, L.puf_close, L.puf_render):
+            f.argtypes = [ctypes.POINTER(Env)]
+        L.puf_init.argtypes = [ctypes.POINTER(Env), ctypes.POINTER(Dict)]
+        L.puf_log.argtypes = [ctypes.POINTER(Log), ctypes.POINTER(Dict)]
+        L.puf_live_log.argtypes = [ctypes.POINTER(Env), ctypes.POINTER(Dict)]
+        L.puf_mask_init.argtypes = [P, ctypes.c_int, ctypes.c_int]
+        L.sbx_gen_actions.argtypes = [ctypes.POINTER(Env), ctypes.c_uint64, ctypes.c_uint32]
+        L.sbx_vec_info.argtypes = [ctypes.POINTER(Env), ctypes.POINTER(SbxVecInfo)]
+        L.sbx_env_state.argtypes = [ctypes.POINTER(Env), ctypes.c_int, P, ctypes.c_int]
+        L.sbx_env_state.restype = ctypes.c_int
+        L.sbx_time_step.argtypes = [ctypes.POINTER(Env), ctypes.c_int]
+        L.sbx_time_step.restype = ctypes.c_float
+        L.sbx_env_meta.argtypes = [ctypes.POINTER(Env), ctypes.c_int, ctypes.POINTER(ctypes.c_int),
+                                   ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_uint32)]
+        L.sbx_scenario_path.argtypes = [ctypes.POINTER(Env), ctypes.c_int]
+        L.sbx_scenario_path.restype = ctypes.c_char_p
+        L.sbx_plan_layout.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(SbxPlan)]
+        L.sbx_plan_free.argtypes = [ctypes.POINTER(SbxPlan)]
+        L.sbx_last_error.restype = ctypes.c_char_p
+        L.sbx_version.restype = ctypes.c_char_p
+        _LIB = L
+    return _LIB
+
+
+class Kwargs:
+    """A Dict of env kwargs kept alive for the duration of the call."""
+
+    def __init__(self, **kw):
+        self._keep = []
+        items = (DictItem * max(len(kw), 1))()
+        for i, (k, v) in enumerate(kw.items()):
+            kb = k.encode()
+            self._keep.append(kb)
+            items[i].key = kb
+            if isinstance(v, (str, Path)):
+                sb = str(v).encode()
+                self._keep.append(sb)
+                items[i].str = sb
+                items[i].value = 0.0
+            else:
+                items[i].value = float(v)
+                items[i].str = None
+        self.items = items
+        self.d = Dict(ctypes.cast(items, ctypes.POINTER(DictItem)), len(kw), len(kw))
+
+    def ptr(self):
+        return ctypes.byref(self.d)
+
+
+def read_dict(d: Dict) -> dict[str, float]:
+    return {d.items[i].key.decode(): d.items[i].value for i in range(d.size)}
+
+
+def plan_layout(blob: str | Path, width: int = 64) -> dict[str, np.ndarray]:
+    """Solve plan of a blob's layout as numpy arrays (host only, no GPU)."""
+    L = lib()
+    p = SbxPlan()
+    rc = L.sbx_plan_layout(str(blob).encode(), width, ctypes.byref(p))
+    if rc != 0:
+        raise ValueError(L.sbx_last_error().decode())
+    try:
+        def arr(ptr, n):
+            return np.ctypeslib.as_array(ptr, (n,)).copy() if n else np.zeros(0)
+        out = {
+            "n": p.n, "width": p.width, "n_slots": p.n_slots, "vec_base": p.vec_base,
+            "n_pass": p.n_pass, "n_levels": p.n_levels, "n_tasks": p.n_tasks, "n_pairs": p.n_pairs,
+            "kmax": p.kmax, "k": p.k,
+            "pass_info": arr(p.pass_info, 8 * p.n_pass).reshape(-1, 8),
+            "row_off": arr(p.row_off, p.n_rows),
+            "hdr": arr(p.hdr, p.n_hdr),
+            "words": arr(p.words, p.n_words),
+            "slot_init": arr(p.slot_init, p.n_slots),
+            "pos": arr(p.pos, p.n),
+            "air_slot": arr(p.air_slot, p.k).astype(np.int64),
+            "air_node": arr(p.air_node, p.k).astype(np.int64),
+        }
+    finally:
+        L.sbx_plan_free(ctypes.byref(p))
+    return out
+
+
+class VecEnv:
+    """n envs of the GPU env behind the PufferLib ABI, with torch-owned buffers."""
+
+    def __init__(self, n: int, device: str = "cuda", **kwargs):
+        import torch
+
+        self.torch = torch
+        self.n = n
+        self.obs = torch.zeros((n, SB_OBS), dtype=torch.float32, device=device)
+        self.actions = torch.zeros((n, SB_ACT), dtype=torch.float32, device=device)
+        self.rewards = torch.zeros((n,), dtype=torch.float32, device=device)
+        self.terminals = torch.zeros((n,), dtype=torch.float32, device=device)
+        self.L = lib()
+        self.stream = torch.cuda.current_stream()
+        self.L.puf_bind_stream(ctypes.c_void_p(self.stream.cuda_stream))
+        self._kw = Kwargs(**kwargs)
+        self.envs = self.L.puf_vec_create(n, self._kw.ptr(), self.obs.data_ptr(), self.actions.data_ptr(),
+                                          self.rewards.data_ptr(), self.terminals.data_ptr())
+        for i in range(n):
+            self.L.puf_init(ctypes.byref(self.envs[i]), self._kw.ptr())
+
+    def info(self) -> SbxVecInfo:
+        out = SbxVecInfo()
+        self.L.sbx_vec_info(self.envs, ctypes.byref(out))
+        return out
+
+    def reset(self):
+        self.L.puf_reset(self.envs)
+        return self.obs
+
+    def gen_actions(self, seed: int, step: int):
+        self.L.sbx_gen_actions(self.envs, seed, step)
+
+    def step(self):
+        self.L.puf_step(self.envs)
+
+    def state(self, i: int) -> np.ndarray:
+        buf = np.zeros(16384, np.float64)
+        m = self.L.sbx_env_state(self.envs, i, buf.ctypes.data_as(P), buf.size)
+        if m < 0:
+            raise RuntimeError("sbx_env_state failed")
+        return buf[:m].copy()
+
+    def meta(self, i: int) -> tuple[str, int, int]:
+        s, st, sd = ctypes.c_int(), ctypes.c_int(), ctypes.c_uint32()
+        self.L.sbx_env_meta(self.envs, i, ctypes.byref(s), ctypes.byref(st), ctypes.byref(sd))
+        return self.L.sbx_scenario_path(self.envs, s.value).decode(), st.value, sd.value
+
+    def log(self, i: int) -> dict[str, float]:
+        items = (DictItem * 8)()
+        d = Dict(ctypes.cast(items, ctypes.POINTER(DictItem)), 0, 8)
+        self.L.puf_log(ctypes.byref(self.envs[i].log), ctypes.byref(d))
+        return read_dict(d)
+
+    def time_step(self, iters: int) -> float:
+        return float(self.L.sbx_time_step(self.envs, iters))
+
+    def close(self):
+        if self.envs:
+            self.L.puf_close(self.envs)
+            self.envs = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -95,8 +95,10 @@ def factorize(A_csc) -> dict:
             Ui.append(r); Ux.append(LU[r, j])
         Ui.append(j); Ux.append(LU[j, j])
         Up.append(len(Ui))
-    perm_c = q.astype(np.int32)
-    perm_r = pos.astype(np.int32)             # row q[k] of A goes to row k
+    # B = A[q][:, q] = Pr A Pc. Pr[perm_r[i], i] = 1 moves row i of A to row
+    # pos[i]; Pc[i, perm_c[i]] = 1 moves column i to column pos[i].
+    perm_r = pos.astype(np.int32)
+    perm_c = pos.astype(np.int32)
     return {
         "perm_r": perm_r, "perm_c": perm_c,
         "L_indptr": np.asarray(Lp, np.int32), "L_indices": np.asarray(Li, np.int32),

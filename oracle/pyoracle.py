@@ -57,6 +57,11 @@ class _Lib:
             self.reset_fn, self.step_fn, self.state_fn = L.sbo_env_reset, L.sbo_env_step, L.sbo_env_state
             self.batch_fn = L.sbo_run_batch
             self.row_fn = L.sbo_action_row
+            L.sbo_env_last_reward.argtypes = [P]
+            L.sbo_env_last_reward.restype = ctypes.c_double
+            for f in (L.sbo_env_obs_len, L.sbo_env_n_cont, L.sbo_env_n_disc):
+                f.argtypes = [P]
+            L.sbo_env_log.argtypes = [P, P]
             L.sbo_mt_seed.argtypes = [P, ctypes.c_uint32]
             L.sbo_mt_u32.argtypes = [P]
             L.sbo_mt_u32.restype = ctypes.c_uint32
@@ -132,12 +137,9 @@ class CpuEnv:
         else:
             self.scen = scenario(path)
             self.h = self.L.lib.sbo_env_new(ctypes.addressof(self.scen.buf), occ_seed, start, max_steps)
-            # n_cont / n_disc from the blob through the action table
-            from neurips2026_smart_building_challenge_amd.scenario.sbb import read_sbb
-            d = read_sbb(path)
-            disc = d["act_is_discrete"]
-            self.n_cont = int((disc == 0).sum())
-            self.n_disc = int((disc == 1).sum())
+            if self.h:
+                self.n_cont = self.L.lib.sbo_env_n_cont(self.h)
+                self.n_disc = self.L.lib.sbo_env_n_disc(self.h)
         if not self.h:
             raise RuntimeError(f"cannot open env on {path}")
         self.obs = np.zeros(SB_OBS, np.float32)
@@ -161,6 +163,25 @@ class CpuEnv:
         a = np.ascontiguousarray(action_row, dtype=np.float32)
         done = self.L.step_fn(self.h, _ptr(a), _ptr(self.obs), _ptr(self._r), _ptr(self._t))
         return self.obs.copy(), float(self._r[0]), float(self._t[0]), bool(done)
+
+    @property
+    def obs_len(self) -> int:
+        if self.kind == "ref":
+            return int(self.L.lib.ref_obs_len(self.h))
+        return int(self.L.lib.sbo_env_obs_len(self.h))
+
+    def last_reward_f64(self) -> float:
+        if self.kind == "ref":
+            return float(self.L.lib.ref_last_reward_f64(self.h))
+        return float(self.L.lib.sbo_env_last_reward(self.h))
+
+    def log(self) -> np.ndarray:
+        out = np.zeros(6, np.float32)
+        if self.kind == "ref":
+            self.L.lib.ref_log(self.h, _ptr(out))
+        else:
+            self.L.lib.sbo_env_log(self.h, _ptr(out))
+        return out
 
     def state(self) -> np.ndarray:
         n = self.L.state_fn(self.h, _ptr(self._st))

@@ -139,6 +139,11 @@ void sbo_env_free(SboEnv* e);
 void sbo_env_reset(SboEnv* e, float* obs_out);
 int sbo_env_step(SboEnv* e, const float* actions, float* obs_out, float* reward, float* terminal);
 int sbo_env_state(const SboEnv* e, double* out);
+double sbo_env_last_reward(const SboEnv* e);
+int sbo_env_obs_len(const SboEnv* e);
+int sbo_env_n_cont(const SboEnv* e);
+int sbo_env_n_disc(const SboEnv* e);
+void sbo_env_log(const SboEnv* e, float* out);
 
 /* core pieces (exposed for unit tests) */
 void sbo_mt_seed(SboMt* r, uint32_t seed);

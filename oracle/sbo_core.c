@@ -977,3 +977,9 @@ int sbo_env_state(const SboEnv* e, double* out) {
     out[c++] = (double)e->step_index;
     return c;
 }
+
+double sbo_env_last_reward(const SboEnv* e) { return e->last_rew; }
+int sbo_env_obs_len(const SboEnv* e) { return e->sc->n_dev + e->sc->n_aux; }
+int sbo_env_n_cont(const SboEnv* e) { return e->sc->n_cont; }
+int sbo_env_n_disc(const SboEnv* e) { return e->sc->n_disc; }
+void sbo_env_log(const SboEnv* e, float* out) { memcpy(out, e->log, sizeof(e->log)); }

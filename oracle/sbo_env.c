@@ -60,3 +60,6 @@ double sbo_run_batch(SboEnv** envs, const int* ids, int n, int steps, uint64_t s
     free(th);
     return (double)(t1.tv_sec - t0.tv_sec) + 1e-9 * (double)(t1.tv_nsec - t0.tv_nsec);
 }
+
+/* Philox4x32-10 block function, exported for known-answer tests. */
+void sbo_philox4x32_10_ext(uint32_t ctr[4], uint32_t k0, uint32_t k1) { sbo_philox4x32_10(ctr, k0, k1); }

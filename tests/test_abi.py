@@ -1,0 +1,45 @@
+"""The C-ABI library loads on a machine without a GPU and exports every symbol
+include/sbenv.h declares; the host-only helpers work without device calls."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+from neurips2026_smart_building_challenge_amd import env as E
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "sbenv.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = re.findall(r"^[A-Za-z_][\w\s\*]*?\b([a-z_][a-z0-9_]*)\s*\(", text, flags=re.M)
+    return sorted(set(n for n in names if n not in {"sizeof"}))
+
+
+def test_header_symbols_exported():
+    lib = E.lib()
+    names = declared_functions()
+    assert set(E.EXPORTS) == set(names), set(E.EXPORTS) ^ set(names)
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_dict_helpers():
+    kw = E.Kwargs(blob="/x.sbb", max_steps=100, desync=1)
+    it = E.lib().dict_find(kw.ptr(), b"max_steps")
+    assert it and it.contents.value == 100.0
+    assert not E.lib().dict_find(kw.ptr(), b"nope")
+    items = (E.DictItem * 4)()
+    d = E.Dict(ctypes.cast(items, ctypes.POINTER(E.DictItem)), 0, 4)
+    log = E.Log(1.0, 2.0, 3.0, 4.0, 5.0, 6.0)
+    E.lib().puf_log(ctypes.byref(log), ctypes.byref(d))
+    assert d.size == 4                          # capacity bound respected
+    assert E.read_dict(d) == {"perf": 1.0, "score": 2.0, "episode_return": 3.0, "episode_length": 4.0}
+
+
+def test_struct_layout_matches_header():
+    assert ctypes.sizeof(E.Log) == 24
+    assert E.Env.log.offset == 0
+    assert E.lib().sbx_version().startswith(b"sbenv")

@@ -1,0 +1,347 @@
+"""Parity of the HIP env step (libsbenv.so through its C ABI) with the CPU oracle.
+
+Bars (from the hot-path contract):
+  - action generation, reset observations, action decode and observation
+    indexing: bit-exact;
+  - fp64 physics: per-step state within 1e-9 relative; 8,640-step episode
+    reward totals within 1e-6 relative (also against the reference core's
+    total stored in the golden fixtures);
+  - observations computed from physics: equal up to the float32 quantization
+    the reference applies before normalizing (sb_obs.c:55-56), i.e. at most one
+    float32 step of the raw value divided by the normalizer's sigma, plus one
+    float32 step of the result.
+
+The GPU solves (A + P G S) y = b + P G T_air by refactorization while csim
+replays fixed factors and a dense k x k correction (sb_fdm.c:153-181); the two
+agree to round-off, hence tolerances on physics and exactness elsewhere.
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+import pyoracle as po
+from conftest import golden_blob
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+from neurips2026_smart_building_challenge_amd import env as E  # noqa: E402
+from neurips2026_smart_building_challenge_amd.scenario.sbb import read_sbb  # noqa: E402
+
+SEED = 424242
+STATE_RTOL = 1e-9
+
+
+def say(msg: str) -> None:
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    torch.cuda.init()
+    yield
+    torch.cuda.synchronize()
+
+
+class Twin:
+    """Oracle env mirroring GPU env i of a vec (same scenario, seed, start)."""
+
+    def __init__(self, vec: E.VecEnv, i: int, max_steps: int):
+        path, start, seed = vec.meta(i)
+        self.i = i
+        self.path = path
+        self.cpu = po.CpuEnv("oracle", path, seed, start=start, max_steps=max_steps)
+        d = read_sbb(path)
+        self.obs_len = int(d["n_dev"][0] + d["n_aux"][0])
+        self.n_dev = int(d["n_dev"][0])
+        kind, oid = d["f_dev_kind"], d["f_obs_id"]
+        exact = np.ones(self.obs_len, bool)
+        for f in range(self.n_dev):
+            if (kind[f] == 1 and oid[f] == 5) or (kind[f] == 0 and oid[f] in (2, 5, 6)):
+                exact[f] = False      # zone temperatures and AHU flow sums
+        self.exact = exact
+        self.mean = np.zeros(self.obs_len)
+        self.sd = np.ones(self.obs_len)
+        self.mean[:self.n_dev] = d["f_norm_mean"]
+        self.sd[:self.n_dev] = np.sqrt(np.maximum(d["f_norm_var"], 0.0))
+        self.rew_sum = 0.0
+        # state snapshot layout (oracle order): T, M, damper, reheat, ratio, sensing,
+        # flow, sat, recirc, fan, air_g, air_T, occupancy, boiler cur/ret/sp, pump head, index
+        n = int(d["solved"].size)
+        nv = int(d["vav_zone_offsets"].size - 1)
+        na = int(d["ahu_const"].size // 9)
+        k = int(d["sensed_shape"][0])
+        nz = int(d["zone_area"].size)
+        o = 2 * n
+        exact = []
+        exact += list(range(o, o + 2 * nv))                  # damper, reheat (decoded commands)
+        o += 4 * nv
+        exact += list(range(o + na, o + 4 * na))             # AHU sat, recirc, fan (decoded)
+        o += 4 * na + 2 * k
+        exact += list(range(o, o + nz))                      # occupancy counts
+        o += nz
+        exact += [o, o + 2, o + 3, o + 4]                    # boiler current, setpoint, pump head, index
+        self.exact_state = np.array(exact)
+        self.state_len = o + 5
+
+    def step(self, seed, s):
+        row = po.action_row(seed, self.i, s, self.cpu.n_cont, self.cpu.n_disc)
+        ob, r, t, _ = self.cpu.step(row)
+        self.rew_sum += self.cpu.last_reward_f64()
+        return ob, r, t
+
+
+def obs_close(gpu_row: np.ndarray, twin: Twin, cpu_row: np.ndarray, where: str) -> None:
+    n = twin.obs_len
+    g, c = gpu_row[:n], cpu_row[:n]
+    assert np.all(gpu_row[n:] == 0.0), f"{where}: padding not zero"
+    ex = twin.exact
+    bad = np.nonzero(g[ex].view(np.uint32) != c[ex].view(np.uint32))[0]
+    assert bad.size == 0, f"{where}: exact obs fields differ at {np.nonzero(ex)[0][bad][:8]}"
+    raw = c.astype(np.float64) * twin.sd + twin.mean
+    ulp_raw = np.spacing(np.abs(raw).astype(np.float32)).astype(np.float64)
+    tol = ulp_raw / np.where(twin.sd > 0, twin.sd, 1.0) + 2 * np.spacing(np.abs(c)).astype(np.float64) + 1e-30
+    err = np.abs(g.astype(np.float64) - c.astype(np.float64))
+    worst = np.max(err[~ex] / tol[~ex]) if (~ex).any() else 0.0
+    assert worst <= 1.0, f"{where}: obs beyond float32 quantization (x{worst:.2f})"
+
+
+def state_close(gs: np.ndarray, cs: np.ndarray, where: str) -> None:
+    m = len(cs)
+    g = gs[:m]
+    fin = ~np.isnan(g)
+    err = np.abs(g[fin] - cs[fin]) / np.maximum(np.abs(cs[fin]), 1.0)
+    assert err.max() <= STATE_RTOL, f"{where}: state rel err {err.max():.3e} at {np.nonzero(fin)[0][err.argmax()]}"
+
+
+def host(t) -> np.ndarray:
+    return t.detach().cpu().numpy()
+
+
+def test_gpu_action_rows_match_oracle(mixed_dir):
+    vec = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30)
+    for step in (0, 1, 12345):
+        vec.gen_actions(SEED, step)
+        a = host(vec.actions)
+        for i in range(vec.n):
+            e = vec.envs[i]
+            want = po.action_row(SEED, i, step, e.n_cont, e.n_disc)
+            assert np.array_equal(a[i].view(np.uint32), want.view(np.uint32)), (i, step)
+    vec.close()
+
+
+def test_gpu_reset_obs_bit_exact(mixed_dir):
+    vec = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30)
+    vec.reset()
+    torch.cuda.synchronize()
+    obs = host(vec.obs)
+    for i in range(vec.n):
+        tw = Twin(vec, i, 8640)
+        o = tw.cpu.reset()
+        assert np.array_equal(obs[i].view(np.uint32), o.view(np.uint32)), f"env {i} {tw.path}"
+        state_close(vec.state(i), tw.cpu.state(), f"reset env {i}")
+    vec.close()
+
+
+def _run_parity(vec, twins, steps, label):
+    vec.reset()
+    for tw in twins:
+        tw.cpu.reset()
+    for s in range(steps):
+        vec.gen_actions(SEED, s)
+        vec.step()
+        torch.cuda.synchronize()
+        obs, rew, term = host(vec.obs), host(vec.rewards), host(vec.terminals)
+        for tw in twins:
+            ob, r, t = tw.step(SEED, s)
+            where = f"{label} step {s} env {tw.i} {tw.path.rsplit('/', 1)[-1]}"
+            assert term[tw.i] == t, where
+            assert abs(float(rew[tw.i]) - r) <= 2 * np.spacing(np.float32(abs(r))) + 1e-12, where
+            obs_close(obs[tw.i], tw, ob, where)
+            gs = vec.state(tw.i)
+            cs = tw.cpu.state()
+            assert len(cs) == tw.state_len
+            state_close(gs, cs, where)
+            # decoded commands, occupancy and the boiler ramp carry no physics: exact
+            ix = tw.exact_state
+            bad = ix[gs[ix] != cs[ix]]
+            assert bad.size == 0, f"{where}: exact state fields differ at {bad[:8]}"
+
+
+def test_gpu_step_parity_mixed_layouts(mixed_dir):
+    """30 scenarios (6 layouts x 5 climates), episodes of 60 steps, 130 steps (two auto-resets)."""
+    say("parity: 30 envs, one per scenario, 130 steps")
+    vec = E.VecEnv(30, blob_dir=str(mixed_dir), groups=30, max_steps=60)
+    twins = [Twin(vec, i, 60) for i in range(vec.n)]
+    _run_parity(vec, twins, 130, "mixed")
+    vec.close()
+
+
+def test_gpu_step_parity_desync(mixed_dir):
+    """Desynchronised calendar starts: every env at its own seeded offset."""
+    say("parity: 60 envs, desync, 90 steps")
+    vec = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=40, desync=1, desync_seed=99)
+    starts = {vec.meta(i)[1] for i in range(vec.n)}
+    assert len(starts) > 40
+    twins = [Twin(vec, i, 40) for i in range(0, vec.n, 3)]
+    _run_parity(vec, twins, 90, "desync")
+    vec.close()
+
+
+def test_gpu_occupancy_exact(mixed_dir):
+    """Occupant counts (and so the observation's occupancy feature) match exactly over a
+    workday morning, when arrival draws happen every step."""
+    say("occupancy: 30 envs, steps 0..300 of a Monday")
+    vec = E.VecEnv(30, blob_dir=str(mixed_dir), groups=30, max_steps=400)
+    twins = [Twin(vec, i, 400) for i in range(vec.n)]
+    vec.reset()
+    for tw in twins:
+        tw.cpu.reset()
+    for s in range(300):
+        vec.gen_actions(SEED, s)
+        vec.step()
+        for tw in twins:
+            tw.step(SEED, s)
+        if s % 10 == 9:
+            torch.cuda.synchronize()
+            obs = host(vec.obs)
+            for tw in twins:
+                n = tw.obs_len
+                assert obs[tw.i][n - 1] == tw.cpu.obs[n - 1], (s, tw.i)
+    vec.close()
+
+
+def test_gpu_episode_total_vs_reference(golden_index, tmp_path):
+    """Full 8,640-step episode of the 41-zone config: f64 reward total within 1e-6 relative of
+    both the oracle and the reference csim core (golden fixture), final state within 1e-9."""
+    case = golden_index["cases"]["cfg0_episode"]
+    path, sha = golden_blob(case["layout"], case["climate"], tmp_path)
+    assert sha == case["blob_sha256"]
+    say("episode: 1 env, 8640 steps")
+    vec = E.VecEnv(1, blob=str(path), max_steps=8640)
+    vec.reset()
+    seed = golden_index["action_seed"]
+    for s in range(8640):
+        vec.gen_actions(seed, s)
+        vec.step()
+    torch.cuda.synchronize()
+    gs = vec.state(0)
+    gpu_total = gs[-2]
+    assert gs[-1] == 8640
+    ref_total = case["total"]
+    assert abs(gpu_total - ref_total) <= 1e-6 * abs(ref_total), (gpu_total, ref_total)
+    tw = po.CpuEnv("oracle", path, case["occ_seed"], max_steps=8640)
+    tw.reset()
+    tot = 0.0
+    for s in range(8640):
+        tw.step(po.action_row(seed, 0, s, tw.n_cont, tw.n_disc))
+        tot += tw.last_reward_f64()
+    assert abs(gpu_total - tot) <= 1e-6 * abs(tot)
+    state_close(gs, tw.state(), "end of episode")
+    fx = np.load(str(__import__("pathlib").Path(__file__).parent / "golden" / "cfg0_episode.npz"))
+    obs = host(vec.obs)[0]
+    assert np.array_equal(obs[:case["obs_len"]].view(np.uint32), fx["obs_8640"].view(np.uint32))
+    vec.close()
+
+
+def test_gpu_batch_invariance(mixed_dir):
+    """An env steps bit-identically alone and inside a 60-env mixed batch."""
+    say("batch invariance")
+    big = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=50)
+    path, _, _ = big.meta(0)
+    small = E.VecEnv(1, blob=path, max_steps=50)
+    big.reset()
+    small.reset()
+    for s in range(70):
+        small.gen_actions(SEED, s)
+        big.actions[0].copy_(small.actions[0])
+        small.step()
+        big.step()
+        torch.cuda.synchronize()
+        assert torch.equal(big.obs[0], small.obs[0]), s
+        assert torch.equal(big.rewards[0], small.rewards[0]), s
+        assert np.array_equal(big.state(0)[:-2], small.state(0)[:-2], equal_nan=True), s
+    big.close()
+    small.close()
+
+
+def test_gpu_graph_replay_matches_eager(mixed_dir):
+    """puf_step captured in a hipGraph and replayed equals eager stepping on every replay."""
+    say("graph replay")
+    eager = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=30)
+    graph = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=30)
+    eager.reset()
+    graph.reset()
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        graph.L.puf_bind_stream(E.P(torch.cuda.current_stream().cuda_stream))
+        graph.step()
+    graph.L.puf_bind_stream(E.P(torch.cuda.current_stream().cuda_stream))
+    # capture ran no kernel: state is still the reset state
+    for s in range(45):
+        eager.gen_actions(SEED, s)
+        graph.actions.copy_(eager.actions)
+        torch.cuda.synchronize()
+        eager.step()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(eager.obs, graph.obs), s
+        assert torch.equal(eager.rewards, graph.rewards), s
+        assert torch.equal(eager.terminals, graph.terminals), s
+    eager.close()
+    graph.close()
+
+
+def test_gpu_log_matches_oracle(cfg0_dir):
+    say("episode logs")
+    vec = E.VecEnv(1, blob_dir=str(cfg0_dir), max_steps=25)
+    tw = Twin(vec, 0, 25)
+    vec.reset()
+    tw.cpu.reset()
+    for s in range(60):
+        vec.gen_actions(SEED, s)
+        vec.step()
+        tw.step(SEED, s)
+    torch.cuda.synchronize()
+    got = vec.log(0)
+    want = tw.cpu.log()
+    names = ["perf", "score", "episode_return", "episode_length", "reward_mean", "n"]
+    for k, name in enumerate(names):
+        assert abs(got[name] - float(want[k])) <= 1e-5 * max(1.0, abs(float(want[k]))), (name, got, want)
+    assert got["n"] == 2.0 and got["episode_length"] == 50.0
+    vec.close()
+
+
+@pytest.mark.parametrize("config", [2, 3])
+def test_gpu_full_size_properties(config, tmp_path):
+    """BASELINE sizes (4,096 x 81 zones; 16,384 mixed desync): finite outputs, zero padding,
+    deterministic replay of the same vec configuration."""
+    from neurips2026_smart_building_challenge_amd.scenario import generate as G
+
+    say(f"full size config {config}")
+    G.write_config(config, tmp_path)
+    scen, n, desync = G.config_scenarios(config)
+    outs = []
+    for rep in range(2):
+        vec = E.VecEnv(n, blob_dir=str(tmp_path), desync=int(desync))
+        vec.reset()
+        for s in range(6):
+            vec.gen_actions(SEED, s)
+            vec.step()
+        torch.cuda.synchronize()
+        obs = host(vec.obs)
+        rew = host(vec.rewards)
+        assert np.isfinite(obs).all() and np.isfinite(rew).all()
+        assert not host(vec.terminals).any()
+        lens = np.array([vec.envs[i].n_cont for i in range(n)])
+        assert lens.min() > 0
+        outs.append((obs.copy(), rew.copy()))
+        vec.close()
+    assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
