@@ -156,6 +156,9 @@ def main() -> int:
     log(f"step kernel: {k_ms * 1e3:.1f} us/launch, {info.bytes_per_step / 1e6:.2f} MB algorithmic -> "
         f"{achieved:.1f} GB/s")
     traffic = measured_traffic(args.config)
+    phases = vec.phase_times()
+    log("phase us (mean / max over workgroups): " +
+        ", ".join(f"{k} {m:.1f}/{x:.1f}" for k, (m, x) in phases.items()))
     vec.close()
 
     cpu = None
@@ -177,7 +180,8 @@ def main() -> int:
                    "block": info.block, "lds_bytes": info.lds_bytes},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel_us": k_ms * 1e3, "algorithmic_bytes": info.bytes_per_step},
+                     "kernel_us": k_ms * 1e3, "algorithmic_bytes": info.bytes_per_step,
+                     "phase_us_max": {k: round(x, 2) for k, (m, x) in phases.items()}},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -149,6 +149,17 @@ int sbx_env_state(Env* envs, int i, double* out, int cap);
  * on the bound stream and returns the elapsed milliseconds (synchronises). */
 float sbx_time_step(Env* envs, int iters);
 
+/* Runs one step with per-phase wall-clock stamps and reports, for phases
+ * 0..n-1 (load, decode, HVAC pre, solve setup, solve, solve epilogue, post,
+ * observation, occupancy, reward, bookkeeping, store), the mean and max
+ * duration over workgroups in microseconds. Advances the envs by one step and
+ * synchronises. Returns the number of phases written. */
+int sbx_phase_times(Env* envs, double* mean_us, double* max_us, int n_phases);
+
+/* Runs one step recording the shader-clock duration of every solve pass of
+ * env `env`'s workgroup. Returns the number of passes written (<= cap). */
+int sbx_pass_times(Env* envs, int env, long long* cycles, int cap);
+
 /* Scenario of env i (index into the sorted, round-robin ordered blob list),
  * its calendar start offset and occupancy seed. */
 int sbx_env_meta(Env* envs, int i, int* scenario, int* start, uint32_t* occ_seed);
@@ -156,24 +167,28 @@ const char* sbx_scenario_path(Env* envs, int scenario);
 
 /* Host-side solve plan of one blob's layout (no GPU needed): the level
  * schedule the step kernel runs for the numeric LU of A + diag(g) plus both
- * triangular solves. Pass p is pass_info[8p..8p+4] = {hdr_off, word_off, nact,
- * maxcnt, row_off}: lanes 0..nact-1 run the tasks hdr[hdr_off + lane]
- * (target | divisor << 16 | count << 32), and term m of lane l is
- * words[word_off + row_off_m + l] with row_off_m = row_off[row_off + m].
+ * triangular solves. Slot 0 holds 0.0, slot 1 is a write sink, slot 2 holds
+ * 1.0; inv_base.. hold pivot reciprocals. Pass p is pass_info[4p..4p+3] =
+ * {hdr_off, word_off, nact | maxcnt << 8 | has_pivot << 16, 0}: lane l < nact runs task
+ * hdr[hdr_off + l] = target | mul << 16 | inv_target << 32 | count << 48 as
+ * slot[target] = (slot[target] - sum_m slot[a_m] * slot[b_m]) * slot[mul],
+ * then, when has_pivot, slot[inv_target] = 1 / slot[target]; term m is
+ * words[word_off + m * nact + l] = a_m | b_m << 16 ((0, 0) past the count).
  * Arrays are owned by the library until sbx_plan_free. */
 typedef struct SbxPlan {
     int n;               /* unknowns */
     int width;           /* lanes per pass */
     int n_slots;         /* LDS value slots: 0 = zero, 1 = sink, LU, vector */
     int vec_base;        /* first vector slot */
+    int inv_base;        /* first pivot-reciprocal slot */
     int n_pass;
     int n_levels;
     int n_tasks;
     int kmax;            /* max terms per task */
     long long n_pairs;   /* multiply-subtract terms */
-    int n_hdr, n_words, n_rows;
-    const int* pass_info;        /* [n_pass * 8] */
-    const int* row_off;          /* [n_rows] */
+    int n_hdr, n_words, n_rows;  /* n_rows: unused, 0 */
+    const int* pass_info;        /* [n_pass * 4] */
+    const int* row_off;          /* unused, NULL */
     const uint64_t* hdr;         /* [n_hdr] */
     const uint32_t* words;       /* [n_words]: a | b << 16 */
     const double* slot_init;     /* [n_slots] A values at LU slots, 0 elsewhere */

@@ -47,9 +47,12 @@ def build_product() -> Path:
         o = tmp / (Path(src).stem + ".o")
         _run([hipcc, *HIP_FLAGS, *inc, "-c", str(CSRC / src), "-o", str(o)])
         objs.append(o)
+    rocm = Path(hipcc).resolve().parent.parent
     for src in ["vec.cpp", "plan.cpp", "sbb_reader.cpp"]:
+        # host-only C++ (HIP runtime API calls, no device code)
         o = tmp / (Path(src).stem + ".o")
-        _run([hipcc, "-O2", "-std=c++17", "-fPIC", "-Wall", *inc, "-c", str(CSRC / src), "-o", str(o)])
+        _run(["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__",
+              "-I", str(rocm / "include"), *inc, "-c", str(CSRC / src), "-o", str(o)])
         objs.append(o)
     out_tmp = LIB.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(out_tmp)])

@@ -7,18 +7,26 @@
 // touches diagonal entries. Each entry of L and U is one "task" (Crout form):
 //
 //   U[i][j] = S[i][j] - sum_{k<i} L[i][k] U[k][j]             (i <= j)
-//   L[i][j] = (S[i][j] - sum_{k<j} L[i][k] U[k][j]) / U[j][j]  (i >  j)
+//   L[i][j] = (S[i][j] - sum_{k<j} L[i][k] U[k][j]) * r_j      (i >  j)
+//   r_j     = 1 / U[j][j]   (written by the task of U[j][j])
 //
 // and the solves reuse the same machinery on a vector of slots:
 //
 //   y_i = w_i - sum_{k<i} L[i][k] y_k                          (forward)
-//   x_i = (y_i - sum_{j>i} U[i][j] x_j) / U[i][i]              (backward, in place)
+//   x_i = (y_i - sum_{j>i} U[i][j] x_j) * r_i                  (backward, in place)
+//
+// Every task multiplies its result by a slot (the pivot reciprocal, or the
+// constant 1.0), so a pass runs without divergent branches; a pass holding a
+// diagonal task also computes the reciprocal of every lane's result and
+// stores it to the lane's reciprocal slot (the sink for other tasks).
 //
 // A task's level is one more than the levels of everything it reads; tasks of
 // one level are independent, sorted by term count (descending) and cut into
 // passes of `width` lanes. A pass stores one 64-bit header per active lane and
-// its terms row by row: row m holds term m of every lane whose count exceeds m
-// (a prefix of the lanes, by the sort), so each row is one coalesced read.
+// its terms row by row: row m holds term m of every active lane (lanes whose
+// count is m or less hold the (0, 0) term, which reads the zero slot), so term
+// m of lane l sits at word_off + m * nact + l and each row is one coalesced read
+// whose address needs nothing but the pass record.
 // Dot products longer than kPlanKmax terms become a chain of tasks on the same
 // slot; only the last one divides.
 #include "plan.h"
@@ -32,7 +40,8 @@ namespace {
 
 struct Task {
     int target;
-    int divisor;      // 0 = none
+    int mul;          // slot multiplying the result (reciprocal or kSlotOne)
+    int inv_target;   // slot receiving 1/result (kSlotSink unless a pivot)
     int level;
     std::vector<std::pair<int, int>> terms;
 };
@@ -104,18 +113,20 @@ bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
         std::sort(Urow[i].begin(), Urow[i].end());
     }
 
-    // slots: 0 zero, 1 sink, then per k: U row k (diagonal first), L column k
+    // slots: 0 zero, 1 sink, 2 one, then per k: U row k (diagonal first),
+    // L column k; then the n pivot reciprocals; then the vector
     std::unordered_map<long long, int> slot;
     slot.reserve(8 * n);
     auto key = [n](int i, int j) { return (long long)i * n + j; };
-    int ns_ = 2;
+    int ns_ = 3;
     for (int k = 0; k < n; k++) {
         slot[key(k, k)] = ns_++;
         for (int j : Urow[k]) slot[key(k, j)] = ns_++;
         for (int i : Lcol[k]) slot[key(i, k)] = ns_++;
     }
-    P.vec_base = ns_;
-    P.n_slots = ns_ + n;
+    P.inv_base = ns_;
+    P.vec_base = ns_ + n;
+    P.n_slots = ns_ + 2 * n;
     if (P.n_slots > 65535) return fail(err, "system too large for 16-bit slots");
 
     // fill closure: every update target must be structural
@@ -126,6 +137,7 @@ bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
 
     // initial values: permuted A
     P.slot_init.assign(P.n_slots, 0.0);
+    P.slot_init[kSlotOne] = 1.0;
     for (int c = 0; c < n; c++)
         for (int p = Ap[c]; p < Ap[c + 1]; p++) {
             int r = Ai[p];
@@ -172,8 +184,12 @@ bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
         }
     };
     std::vector<int> ks;
-    auto add_task = [&](int target, int divisor, std::vector<std::pair<int, int>>&& terms, int extra_level) {
-        // split into chains of at most kPlanKmax terms
+    // target, multiplier slot (reciprocal to depend on, or kSlotOne), reciprocal
+    // slot to produce (or kSlotSink), terms, extra dependency level
+    auto add_task = [&](int target, int mul, int inv_target, std::vector<std::pair<int, int>>&& terms,
+                        int extra_level) {
+        // split into chains of at most kPlanKmax terms; the last piece scales
+        // and produces the reciprocal
         size_t nt = terms.size();
         size_t pieces = nt == 0 ? 1 : (nt + kPlanKmax - 1) / kPlanKmax;
         int prev = extra_level;
@@ -183,43 +199,45 @@ bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
             int lv = prev;
             for (auto& t : part) lv = std::max(lv, std::max(slot_level[t.first], slot_level[t.second]));
             const bool last = pc + 1 == pieces;
-            if (last && divisor) lv = std::max(lv, slot_level[divisor]);
+            if (last) lv = std::max(lv, slot_level[mul]);
             lv += 1;
             slot_level[target] = lv;
+            if (last && inv_target != kSlotSink) slot_level[inv_target] = lv;
             prev = lv;
-            tasks.push_back(Task{target, last ? divisor : 0, lv, std::move(part)});
+            tasks.push_back(Task{target, last ? mul : kSlotOne, last ? inv_target : kSlotSink, lv,
+                                 std::move(part)});
         }
     };
+    const int vb = P.vec_base, ib = P.inv_base;
     for (int r = 0; r < n; r++) {
-        // U row r (j >= r): terms over k < r
+        // U row r (j >= r): terms over k < r; the diagonal task always runs
+        // (it produces the reciprocal even without terms)
         std::vector<int> ucols;
         ucols.push_back(r);
         ucols.insert(ucols.end(), Urow[r].begin(), Urow[r].end());
         for (int j : ucols) {
             intersect(Lrow[r], Ucol[j], r, ks);
-            if (ks.empty()) continue;   // slot already holds its value
+            const bool diag = j == r;
+            if (ks.empty() && !diag) continue;   // slot already holds its value
             std::vector<std::pair<int, int>> terms;
             for (int m : ks) terms.push_back({slot[key(r, m)], slot[key(m, j)]});
-            add_task(slot[key(r, j)], 0, std::move(terms), 0);
+            add_task(slot[key(r, j)], kSlotOne, diag ? ib + r : kSlotSink, std::move(terms), 0);
         }
-        // L column r (i > r): terms over k < r, divided by U[r][r]
+        // L column r (i > r): terms over k < r, scaled by 1/U[r][r]
         for (int i : Lcol[r]) {
             intersect(Lrow[i], Ucol[r], r, ks);
             std::vector<std::pair<int, int>> terms;
             for (int m : ks) terms.push_back({slot[key(i, m)], slot[key(m, r)]});
-            add_task(slot[key(i, r)], slot[key(r, r)], std::move(terms), 0);
+            add_task(slot[key(i, r)], ib + r, kSlotSink, std::move(terms), 0);
         }
     }
-    const int vb = P.vec_base;
     // forward solve
     std::vector<int> y_read_max(n, 0);
     for (int i = 0; i < n; i++) {
         if (Lrow[i].empty()) continue;
         std::vector<std::pair<int, int>> terms;
-        for (int m : Lrow[i]) {
-            terms.push_back({slot[key(i, m)], vb + m});
-        }
-        add_task(vb + i, 0, std::move(terms), 0);
+        for (int m : Lrow[i]) terms.push_back({slot[key(i, m)], vb + m});
+        add_task(vb + i, kSlotOne, kSlotSink, std::move(terms), 0);
         for (int m : Lrow[i]) y_read_max[m] = std::max(y_read_max[m], slot_level[vb + i]);
     }
     // backward solve, in place over y; a slot is overwritten only after its
@@ -228,7 +246,7 @@ bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
         std::vector<std::pair<int, int>> terms;
         for (int j : Urow[i]) terms.push_back({slot[key(i, j)], vb + j});
         int lv0 = std::max(slot_level[vb + i], y_read_max[i]);
-        add_task(vb + i, slot[key(i, i)], std::move(terms), lv0);
+        add_task(vb + i, ib + i, kSlotSink, std::move(terms), lv0);
     }
 
     // levels -> passes
@@ -250,31 +268,30 @@ bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
             PassInfo pi{};
             pi.hdr_off = (int)P.hdr.size();
             pi.word_off = (int)P.words.size();
-            pi.nact = (int)(e - s);
-            pi.maxcnt = (int)tasks[ids[s]].terms.size();
-            pi.row_off = (int)P.row_off.size();
+            const int nact = (int)(e - s);
+            const int maxcnt = (int)tasks[ids[s]].terms.size();
+            int piv = 0;
             for (size_t id = s; id < e; id++) {
                 const Task& t = tasks[ids[id]];
-                P.hdr.push_back((uint64_t)(uint32_t)t.target | ((uint64_t)(uint32_t)t.divisor << 16)
-                                | ((uint64_t)t.terms.size() << 32));
+                P.hdr.push_back((uint64_t)(uint32_t)t.target | ((uint64_t)(uint32_t)t.mul << 16)
+                                | ((uint64_t)(uint32_t)t.inv_target << 32) | ((uint64_t)t.terms.size() << 48));
                 npairs += (long long)t.terms.size();
-                ndiv += t.divisor ? 1 : 0;
+                ndiv += t.inv_target != kSlotSink ? 1 : 0;
+                if (t.inv_target != kSlotSink) piv = 1;
             }
-            int ro = 0;
-            for (int m = 0; m < pi.maxcnt; m++) {
-                P.row_off.push_back(ro);
+            pi.packed = nact | (maxcnt << 8) | (piv << 16);
+            for (int m = 0; m < maxcnt; m++) {
                 for (size_t id = s; id < e; id++) {
                     const Task& t = tasks[ids[id]];
-                    if ((int)t.terms.size() > m) {
-                        P.words.push_back((uint32_t)t.terms[m].first | ((uint32_t)t.terms[m].second << 16));
-                        ro++;
-                    }
+                    P.words.push_back((int)t.terms.size() > m
+                                      ? (uint32_t)t.terms[m].first | ((uint32_t)t.terms[m].second << 16)
+                                      : 0u);
                 }
             }
-            P.row_off.push_back(ro);
             P.passes.push_back(pi);
         }
     }
+    P.words.resize(P.words.size() + (size_t)kWordTailRows * width, 0u);
     P.n_pairs = npairs;
     P.n_divs = ndiv;
     return true;

@@ -15,23 +15,30 @@ namespace sbh {
 // registers, so this bounds its register arrays.
 constexpr int kPlanKmax = 48;
 
-// Per-pass record: hdr_off, word_off, nact, maxcnt, row_off, 0, 0, 0.
+// Per-pass record, 16 bytes: hdr_off, word_off, nact | maxcnt << 8 | has_pivot << 16, 0.
 struct PassInfo {
-    int hdr_off, word_off, nact, maxcnt, row_off, pad0, pad1, pad2;
+    int hdr_off, word_off, packed, pad;
+    int nact() const { return packed & 0xff; }
+    int maxcnt() const { return (packed >> 8) & 0xff; }
+    int has_pivot() const { return (packed >> 16) & 1; }
 };
+
+// Fixed slots: 0 holds 0.0 (padding terms read it), 1 is a write sink, 2 holds 1.0.
+constexpr int kSlotZero = 0, kSlotSink = 1, kSlotOne = 2;
+// Rows of padding after the last pass, so chunked reads of 8 rows stay inside the array.
+constexpr int kWordTailRows = 8;
 
 struct SolvePlan {
     int n = 0, k = 0, width = 0;
-    int n_slots = 0, vec_base = 0, n_levels = 0, n_tasks = 0;
+    int n_slots = 0, vec_base = 0, inv_base = 0, n_levels = 0, n_tasks = 0;
     long long n_pairs = 0;           // multiply-subtract terms
     long long n_divs = 0;
     std::vector<int> pos;            // node -> permuted position
     std::vector<double> slot_init;   // [n_slots]
     std::vector<int> air_slot, air_node;   // [k]
     std::vector<PassInfo> passes;
-    std::vector<int> row_off;        // per pass: maxcnt + 1 cumulative row starts
-    std::vector<uint64_t> hdr;       // per active lane: target | divisor << 16 | count << 32
-    std::vector<uint32_t> words;     // rows: row m of a pass holds the m-th term of every lane with count > m
+    std::vector<uint64_t> hdr;       // per active lane: target | mul << 16 | inv_target << 32 | count << 48
+    std::vector<uint32_t> words;     // rows of nact words: term m of lane l at word_off + m * nact + l
     int n_pass() const { return (int)passes.size(); }
 };
 

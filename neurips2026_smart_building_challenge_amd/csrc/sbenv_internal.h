@@ -3,10 +3,20 @@
 #pragma once
 #include <stdint.h>
 
+// Read-only device tables live in the constant address space when compiled for
+// the device: uniform reads become scalar loads, divergent ones global loads,
+// and neither is a flat access (flat loads also hold the LDS wait counter).
+#if defined(__HIP_DEVICE_COMPILE__)
+#define SBK_C __attribute__((address_space(4)))
+#else
+#define SBK_C
+#endif
+
 #define SBK_MAX_AHU 16
 #define SBK_MT_N 624
 #define SBK_NAUX_MAX 16
 #define SBK_KMAX 48      // terms per lane per pass (matches the planner)
+#define SBK_NSTAMP 16    // phase stamps per workgroup when phase timing is on
 
 namespace sbk {
 
@@ -49,6 +59,7 @@ struct LdsLayout {
     int red;          // f64[64] reduction scratch
     int misc;         // f64[32] scalars
     int iscr;         // i32[W + 8] scan scratch
+    int prec;         // int4[n_pass] solve pass records (copied at kernel start)
     int bytes;
 };
 
@@ -62,50 +73,49 @@ struct DevLayout {
     StateLayout st;
     LdsLayout lds;
     // solve plan
-    const int* pinfo;            // [n_pass * 8]: hdr_off, word_off, nact, maxcnt, row_off
-    const int* row_off;          // cumulative row starts (maxcnt + 1 per pass)
-    const uint64_t* hdr;         // per active lane: target | divisor << 16 | count << 32
-    const uint32_t* words;       // term words: a | b << 16
-    const double* slot_init;     // [n_slots]
-    const int* pos;              // [n]
-    const int* air_slot;         // [k]
-    const int* air_node;         // [k]
+    const SBK_C int* pinfo;            // [n_pass * 4]: hdr_off, word_off, nact | maxcnt << 8 | pivot << 16, 0
+    const SBK_C uint64_t* hdr;         // per active lane: target | mul << 16 | inv_target << 32 | count << 48
+    const SBK_C uint32_t* words;       // term words a | b << 16, rows of nact words
+    const SBK_C double* slot_init;     // [n_slots]
+    const SBK_C int* pos;              // [n]
+    const SBK_C int* air_slot;         // [k]
+    const SBK_C int* air_node;         // [k]
     // field
-    const double* cap;           // [n]
-    const double* mcoup;         // [n]
-    const double* mret;          // [n]
-    const double* mgain;         // [n]
-    const double* solar_c;       // [n]
-    const uint8_t* is_room;      // [n]
+    const SBK_C double* cap;           // [n]
+    const SBK_C double* mcoup;         // [n]
+    const SBK_C double* mret;          // [n]
+    const SBK_C double* mgain;         // [n]
+    const SBK_C double* solar_c;       // [n]
+    const SBK_C uint8_t* is_room;      // [n]
     // zones / rooms (rooms flattened to node lists)
-    const int* zone_cell_off;    // [nz + 1]
-    const int* zone_cells;       // node ids
-    const double* zone_area;     // [nz]
-    const int* vz_off;           // [nv + 1]
-    const int* vz_idx;
-    const double* vav_area;      // [nv] (constant: sum of its zones' areas)
-    const int* vav_ahu;          // [nv]
-    const int* coupled;          // [k] col -> vav
-    const int* zone_col_off;     // [nz + 1] coupled columns feeding zone z
-    const int* zone_cols;
-    const double* vav_c;         // [nv * 9]
-    const double* ahu_c;         // [na * 9]
+    const SBK_C int* zone_cell_off;    // [nz + 1]
+    const SBK_C int* zone_cells;       // node ids
+    const SBK_C double* zone_area;     // [nz]
+    const SBK_C int* vz_off;           // [nv + 1]
+    const SBK_C int* vz_idx;
+    const SBK_C double* vav_area;      // [nv] (constant: sum of its zones' areas)
+    const SBK_C int* vav_ahu;          // [nv]
+    const SBK_C int* coupled;          // [k] col -> vav
+    const SBK_C int* zone_col_off;     // [nz + 1] coupled columns feeding zone z
+    const SBK_C int* zone_cols;
+    const SBK_C double* vav_c;         // [nv * 9]
+    const SBK_C double* ahu_c;         // [na * 9]
     // actions
-    const uint8_t* act_kind;
-    const uint8_t* act_act;
-    const uint8_t* act_disc;
-    const int* act_idx;
-    const int* act_src;          // column in the trainer row (cont block or SB_CONT + d)
-    const double* act_mn;
-    const double* act_mx;
-    const double* act_mnr;
-    const double* act_mxr;
+    const SBK_C uint8_t* act_kind;
+    const SBK_C uint8_t* act_act;
+    const SBK_C uint8_t* act_disc;
+    const SBK_C int* act_idx;
+    const SBK_C int* act_src;          // column in the trainer row (cont block or SB_CONT + d)
+    const SBK_C double* act_mn;
+    const SBK_C double* act_mx;
+    const SBK_C double* act_mnr;
+    const SBK_C double* act_mxr;
     // observation map
-    const uint8_t* f_kind;
-    const uint8_t* f_id;
-    const int* f_idx;
-    const double* f_mean;
-    const double* f_sd;          // sqrt(var) or 0 when var <= 0
+    const SBK_C uint8_t* f_kind;
+    const SBK_C uint8_t* f_id;
+    const SBK_C int* f_idx;
+    const SBK_C double* f_mean;
+    const SBK_C double* f_sd;          // sqrt(var) or 0 when var <= 0
     // bytes of algorithmic traffic per env-step
     double bytes_per_step;
     double solve_flops;
@@ -115,26 +125,26 @@ struct DevLayout {
 struct DevScen {
     int layout;
     int n1;                      // calendar rows
-    const double* amb;
-    const double* solar_i;
-    const double* comfort;
-    const double* heat_sp;
-    const double* cool_sp;
-    const double* aux_time;      // [n1 * (n_aux - 1)]
-    const uint8_t* occ_hour;
-    const uint8_t* occ_work;
-    const uint8_t* hour_m1;
-    const uint8_t* work_m1;
-    const uint8_t* rew_hour;
-    const uint8_t* rew_month;
-    const uint8_t* rew_work;
-    const double* dirx;          // [n] dirichlet + exposure(h)
-    const double* temp_init;     // [n]
-    const double* mass_init;     // [n]
-    const double* elec_wk;       // [24]
-    const double* elec_we;       // [24]
-    const double* elec_co2;      // [24]
-    const double* gas_price;     // [12]
+    const SBK_C double* amb;
+    const SBK_C double* solar_i;
+    const SBK_C double* comfort;
+    const SBK_C double* heat_sp;
+    const SBK_C double* cool_sp;
+    const SBK_C double* aux_time;      // [n1 * (n_aux - 1)]
+    const SBK_C uint8_t* occ_hour;
+    const SBK_C uint8_t* occ_work;
+    const SBK_C uint8_t* hour_m1;
+    const SBK_C uint8_t* work_m1;
+    const SBK_C uint8_t* rew_hour;
+    const SBK_C uint8_t* rew_month;
+    const SBK_C uint8_t* rew_work;
+    const SBK_C double* dirx;          // [n] dirichlet + exposure(h)
+    const SBK_C double* temp_init;     // [n]
+    const SBK_C double* mass_init;     // [n]
+    const SBK_C double* elec_wk;       // [24]
+    const SBK_C double* elec_we;       // [24]
+    const SBK_C double* elec_co2;      // [24]
+    const SBK_C double* gas_price;     // [12]
     double gas_co2;
     double rw[8];
     double boiler_c[10];
@@ -172,6 +182,9 @@ struct KParams {
     int n_envs;
     int mode;
     float reward_scale;
+    unsigned long long* phase_ts;   // null, or [n_blocks * SBK_NSTAMP] wall-clock stamps
+    unsigned long long* pass_ts;    // null, or [n_pass + 1] shader-clock stamps of one workgroup
+    int pass_ts_block;              // workgroup whose solve passes are stamped
 };
 
 }  // namespace sbk

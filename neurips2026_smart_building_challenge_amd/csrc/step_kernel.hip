@@ -32,6 +32,13 @@ namespace sbk {
 
 enum { M_OFF = 0, M_HEAT = 1, M_COOL = 2, M_PASSIVE = 3 };
 
+// Phase stamp (wall clock, written by lane 0 only when phase timing is on).
+#define STAMP(i)                                                                        \
+    do {                                                                                \
+        if (P.phase_ts && threadIdx.x == 0)                                             \
+            P.phase_ts[(size_t)blockIdx.x * SBK_NSTAMP + (i)] = wall_clock64();        \
+    } while (0)
+
 __device__ __forceinline__ double wave_sum(double v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -159,6 +166,7 @@ struct Ctx {
     double *wsum, *atotal, *satv, *demand, *fdsum, *red, *misc;
     uint32_t* mt;
     int* iscr;
+    unsigned char* prec;     // LDS copy of the solve pass records
 };
 
 __device__ __forceinline__ void bind(Ctx& c, unsigned char* lds) {
@@ -207,6 +215,7 @@ __device__ __forceinline__ void bind(Ctx& c, unsigned char* lds) {
     c.red = (double*)(lds + l.red);
     c.misc = (double*)(lds + l.misc);
     c.iscr = (int*)(lds + l.iscr);
+    c.prec = lds + l.prec;
 }
 
 // ------------------------------------------------------------------ helpers
@@ -365,6 +374,26 @@ __device__ __forceinline__ void mt_twist(uint32_t* mt) {
     }
 }
 
+// Tempered words at stream positions idx + 2d, idx + 2d + 1 (below 624) for
+// each drawing occupant of this lane; d counts draws from `first`.
+template <int MAXC, class Ptr>
+__device__ __forceinline__ void gather_words(Ptr src, int idx, int first, const int* need, uint32_t* w) {
+    int d = first;
+#pragma unroll
+    for (int r = 0; r < MAXC; r++) {
+        w[2 * r] = 0;
+        w[2 * r + 1] = 0;
+        if (need[r]) {
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int pos = idx + 2 * d + h;
+                if (pos < SBK_MT_N) w[2 * r + h] = mt_temper(src[pos]);
+            }
+            d++;
+        }
+    }
+}
+
 // One interval of the RandomizedArrivalDeparture chains (sb_occup.c:36-61).
 // Occupant o = z * nassign + a draws iff it is at home in the arrival window
 // or at work in the departure window of a workday; draws are taken from the
@@ -408,24 +437,12 @@ __device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday)
     // gather the tempered words: stream position s -> old[idx + s] or new[idx + s - 624]
     // Words before the twist are read from the old state first, then the twist.
     uint32_t w_old[2 * MAXC];
-    int d = first;
-#pragma unroll
-    for (int r = 0; r < MAXC; r++) {
-        w_old[2 * r] = 0;
-        w_old[2 * r + 1] = 0;
-        if (need[r]) {
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                int pos = idx + 2 * d + h;
-                if (pos < SBK_MT_N) w_old[2 * r + h] = mt_temper(twisted ? c.mt[pos] : hbm_mt[pos]);
-            }
-            d++;
-        }
-    }
+    if (twisted) gather_words<MAXC>(c.mt, idx, first, need, w_old);     // LDS copy of the state
+    else gather_words<MAXC>(hbm_mt, idx, first, need, w_old);           // HBM record
     if (twisted) {
         __syncthreads();
         mt_twist<W>(c.mt);
-        d = first;
+        int d = first;
 #pragma unroll
         for (int r = 0; r < MAXC; r++) {
             if (need[r]) {
@@ -783,37 +800,73 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 struct PassRegs {
     uint64_t h;
-    int nact, maxcnt;
+    int nact, maxcnt, piv;
     uint32_t w[SBK_KMAX];
 };
 
-// Loads pass p's header and term words into registers (lane l gets term m of
-// its task from row m, which holds the lanes whose count exceeds m).
-__device__ __forceinline__ void fetch_pass(const DevLayout* L, int p, PassRegs& r) {
-    const int* pi = L->pinfo + 8 * p;
-    const int hdr_off = pi[0], word_off = pi[1], nact = pi[2], maxcnt = pi[3], ro = pi[4];
+// Issues the loads of one pass's header and term words into registers. Term m
+// of lane l is at word_off + m * nact + l: every address comes from the pass
+// record alone, so all loads of a pass go out back to back. Rows are read in
+// chunks of 8 without per-row branches; rows past maxcnt (the next pass's
+// words, or the array's tail padding) and lanes past nact read in-bounds words
+// that are then replaced by the (0, 0) term.
+__device__ __forceinline__ void fetch_pass(const DevLayout* L, int4 pi, PassRegs& r) {
+    const int hdr_off = pi.x, word_off = pi.y;
+    const int nact = pi.z & 0xff, maxcnt = (pi.z >> 8) & 0xff, has_pivot = (pi.z >> 16) & 1;
     const int lane = threadIdx.x;
+    const bool act = lane < nact;
     r.nact = nact;
     r.maxcnt = maxcnt;
-    r.h = lane < nact ? L->hdr[hdr_off + lane] : 1ull;   // sink slot, no divisor
-    const int* rows = L->row_off + ro;
+    r.piv = has_pivot;
+    const uint64_t hv = L->hdr[hdr_off + (act ? lane : 0)];
+    // idle lanes: target and reciprocal target both the sink (slot 1), multiplier slot 0
+    r.h = act ? hv : 0x0000000100000001ull;
+    const SBK_C uint32_t* wp = L->words + word_off + lane;
 #pragma unroll
-    for (int m = 0; m < SBK_KMAX; m++) {
-        uint32_t v = 0;
-        if (m < maxcnt) {
-            const int a = rows[m], b = rows[m + 1];
-            if (lane < b - a) v = L->words[word_off + a + lane];
+    for (int m0 = 0; m0 < SBK_KMAX; m0 += 8) {
+        if (m0 < maxcnt) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int m = m0 + j;
+                const uint32_t v = wp[m * nact];
+                r.w[m] = (m < maxcnt && act) ? v : 0u;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) r.w[m0 + j] = 0;
         }
-        r.w[m] = v;
     }
 }
 
+// Waits for a fetched pass here: the empty asm "uses" every register, so the
+// compiler places the memory wait at this point instead of at the first use
+// inside the next pass (where the loads of the pass after it are in flight).
+__device__ __forceinline__ void settle_pass(PassRegs& r) {
+    asm volatile("" : "+v"(r.h));
+#pragma unroll
+    for (int m = 0; m < SBK_KMAX; m++) asm volatile("" : "+v"(r.w[m]));
+}
+
+// 1/x from the hardware reciprocal and two Newton steps (about 1 ulp).
+__device__ __forceinline__ double recip(double x) {
+    double r = __builtin_amdgcn_rcp(x);
+    double e = fma(-x, r, 1.0);
+    r = fma(r, e, r);
+    e = fma(-x, r, 1.0);
+    return fma(r, e, r);
+}
+
 // One pass: every active lane computes slot[target] = (slot[target] - sum of
-// its terms) [/ slot[divisor]]. Missing terms are (0, 0) and read slot 0 = 0.
+// its terms) * slot[mul]; in a pass holding pivots, lanes also store the
+// reciprocal of their result to slot[inv_target] (the sink for non-pivots).
+// Missing terms are (0, 0) and read slot 0 = 0.
 __device__ __forceinline__ void run_pass(double* slots, const PassRegs& r) {
     constexpr int CH = 8;
-    const int tgt = (int)(r.h & 0xffffu), dv = (int)((r.h >> 16) & 0xffffu);
+    const int tgt = (int)(r.h & 0xffffu);
+    const int mul = (int)((r.h >> 16) & 0xffffu);
+    const int invt = (int)((r.h >> 32) & 0xffffu);
     double acc = slots[tgt];
+    const double scale = slots[mul];
 #pragma unroll
     for (int m0 = 0; m0 < SBK_KMAX; m0 += CH) {
         if (m0 >= r.maxcnt) break;
@@ -827,33 +880,46 @@ __device__ __forceinline__ void run_pass(double* slots, const PassRegs& r) {
 #pragma unroll
         for (int j = 0; j < CH; j++) acc -= x[j] * y[j];
     }
-    if (dv) acc = acc / slots[dv];
+    acc *= scale;
     if ((int)threadIdx.x < r.nact) slots[tgt] = acc;
+    if (r.piv) slots[invt] = recip(acc);
 }
 
-// All passes, pass p+1's words prefetched while pass p computes.
+// All passes. Pass p+1's words are loaded while pass p computes and settled
+// after it; pass records are read two passes ahead.
 template <int W>
-__device__ __forceinline__ void run_plan(const DevLayout* L, double* slots) {
+__device__ __forceinline__ void run_plan(const DevLayout* L, double* slots, const int4* rec,
+                                         unsigned long long* pts) {
     static_assert(W == 64, "the solve plan runs on one wavefront");
     const int np = L->n_pass;
     if (np == 0) return;
+    const int last = np - 1;
     PassRegs A, B;
-    fetch_pass(L, 0, A);
+    int4 q1 = rec[min(1, last)];
+    fetch_pass(L, rec[0], A);
+    settle_pass(A);
     for (int p = 0; p < np; p += 2) {
-        if (p + 1 < np) fetch_pass(L, p + 1, B);
+        if (pts) pts[p] = clock64();
+        const int4 q2 = rec[min(p + 2, last)];
+        if (p + 1 < np) fetch_pass(L, q1, B);
         run_pass(slots, A);
         wave_lds_sync();
         if (p + 1 >= np) break;
-        if (p + 2 < np) fetch_pass(L, p + 2, A);
+        settle_pass(B);
+        const int4 q3 = rec[min(p + 3, last)];
+        if (p + 2 < np) fetch_pass(L, q2, A);
         run_pass(slots, B);
         wave_lds_sync();
+        settle_pass(A);
+        q1 = q3;
     }
+    if (pts) pts[np] = clock64();
 }
 
 // Field step: b = cap T + q + amb dirx + mc M (+ solar, + g T_air at the air
 // nodes), then (A + diag(g)) y = b by the plan; mass and field update.
 template <int W>
-__device__ __forceinline__ void field_step(Ctx& c) {
+__device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
     const DevLayout* L = c.L;
     const DevScen* S = c.S;
     const int kk = c.ip[PI_STEP_INDEX];
@@ -862,7 +928,7 @@ __device__ __forceinline__ void field_step(Ctx& c) {
     const int n = L->n;
     double* slots = c.slots;
     const int vb = L->vec_base;
-    for (int s = threadIdx.x; s < vb; s += W) slots[s] = L->slot_init[s];
+    for (int s = threadIdx.x; s < vb; s += W) slots[s] = L->slot_init[s];   // incl. 0.0 and 1.0 slots
     // room cells carry their zone's heat; every node then gets its solar gain
     for (int z = threadIdx.x; z < L->nz; z += W) {
         double qz = c.zq[z];
@@ -881,8 +947,11 @@ __device__ __forceinline__ void field_step(Ctx& c) {
         slots[vb + L->pos[L->air_node[col]]] += g * c.tair[col];
     }
     __syncthreads();
+    STAMP(4);
     // level schedule: LU of the permuted system, forward and backward solves
-    run_plan<W>(L, slots);
+    unsigned long long* pts = (P.pass_ts && blockIdx.x == P.pass_ts_block && threadIdx.x == 0) ? P.pass_ts : nullptr;
+    run_plan<W>(L, slots, reinterpret_cast<const int4*>(c.prec), pts);
+    STAMP(5);
     for (int t = threadIdx.x; t < n; t += W) {
         double y = slots[vb + L->pos[t]];
         c.M[t] = c.M[t] * L->mret[t] + L->mgain[t] * y;
@@ -1045,8 +1114,14 @@ __global__ __launch_bounds__(W) void step_kernel(KParams P) {
     c.rec = P.state + ed.state_off;
     bind(c, lds);
     const DevLayout* L = c.L;
+    STAMP(0);
     copy16<W>(lds + L->lds.state, c.rec, L->st.bytes);
+    if (P.mode == KMODE_STEP) {
+        const SBK_C uint4* src = reinterpret_cast<const SBK_C uint4*>(L->pinfo);
+        for (int i = threadIdx.x; i < L->n_pass; i += W) reinterpret_cast<uint4*>(c.prec)[i] = src[i];
+    }
     __syncthreads();
+    STAMP(1);
     float* obs_row = P.obs + (size_t)e * 1024;
     if (P.mode == KMODE_RESET) {
         env_reset<W>(c, ed.start, obs_row);
@@ -1070,15 +1145,22 @@ __global__ __launch_bounds__(W) void step_kernel(KParams P) {
         lg_mean = __hip_atomic_load(&hlog->reward_mean, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
     decode_apply<W>(c, P.actions + (size_t)e * 272);
+    STAMP(2);
     step_pre<W>(c);
-    field_step<W>(c);
+    STAMP(3);
+    field_step<W>(c, P);
+    STAMP(6);
     step_post<W>(c);
+    STAMP(7);
     const int step = c.ip[PI_STEP] + 1;
     const int j = ed.start + step;
     write_obs<W>(c, j, obs_row);
     __syncthreads();
+    STAMP(8);
     occupancy_advance<W>(c, c.S->occ_hour[j], c.S->occ_work[j]);
+    STAMP(9);
     const double rew = reward<W>(c, j);
+    STAMP(10);
     const float r = (float)rew;
     const int done = step >= ed.max_steps;
     if (threadIdx.x == 0) {
@@ -1110,7 +1192,9 @@ __global__ __launch_bounds__(W) void step_kernel(KParams P) {
     __syncthreads();
     if (done) env_reset<W>(c, ed.start, obs_row);
     __syncthreads();
+    STAMP(11);
     copy16<W>(c.rec, lds + L->lds.state, L->st.bytes);
+    STAMP(12);
 }
 
 // Beta(2,2) action rows (see sbx_gen_actions in sbenv.h).

@@ -8,7 +8,7 @@
 // solver (no SB_NE cap, no weather merging): envs of different layouts and
 // climates share one launch and read their own tables.
 #include <dirent.h>
-#include <hip/hip_runtime.h>
+#include <hip/hip_runtime_api.h>
 #include <math.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -257,13 +257,14 @@ bool make_layout(const sbh::Blob& b, int width, HostLayout* H, Arena& A, std::st
     Ls.red = l; l += 8 * 64;
     Ls.misc = l; l += 8 * 32;
     Ls.iscr = l; l += 4 * (width / 64 + 8);
+    l = align_up(l, 16);
+    Ls.prec = l; l += 16 * P.n_pass();
     Ls.bytes = align_up(l, 16);
     D.bytes_per_step = 2.0 * S.bytes + 4.0 * (ncont + ndisc) + 4.0 * SB_OBS + 8.0;
     D.solve_flops = 2.0 * (double)P.n_pairs + (double)P.n_divs;
 
     auto& O = H->off;
     O["pinfo"] = A.add(P.passes.data(), P.passes.size() * sizeof(sbh::PassInfo));
-    O["row_off"] = A.vec(P.row_off);
     O["hdr"] = A.vec(P.hdr);
     O["words"] = A.vec(P.words);
     O["slot_init"] = A.vec(P.slot_init);
@@ -317,7 +318,6 @@ void patch_layout(HostLayout* H, unsigned char* d) {
     sbk::DevLayout& D = H->dev;
     auto& O = H->off;
     D.pinfo = at<int>(d, O["pinfo"]);
-    D.row_off = at<int>(d, O["row_off"]);
     D.hdr = at<uint64_t>(d, O["hdr"]);
     D.words = at<uint32_t>(d, O["words"]);
     D.slot_init = at<double>(d, O["slot_init"]);
@@ -988,6 +988,69 @@ int sbx_env_state(Env* envs, int i, double* out, int cap) {
     return (int)o.size();
 }
 
+int sbx_phase_times(Env* envs, double* mean_us, double* max_us, int n_phases) {
+    Vec* v = vec_of(envs);
+    if (n_phases > SBK_NSTAMP - 1) n_phases = SBK_NSTAMP - 1;
+    unsigned long long* d = nullptr;
+    const size_t count = (size_t)v->n * SBK_NSTAMP;
+    hip_ok(hipMalloc(&d, count * sizeof(unsigned long long)), "hipMalloc(stamps)");
+    hip_ok(hipMemset(d, 0, count * sizeof(unsigned long long)), "memset(stamps)");
+    sbk::KParams p = params(v, sbk::KMODE_STEP);
+    p.phase_ts = d;
+    int rc = sbk_launch_step(&p, v->n, v->width, v->lds_bytes, g_stream);
+    if (rc != 0) die("step kernel launch failed");
+    hip_ok(hipStreamSynchronize(g_stream), "stamps sync");
+    std::vector<unsigned long long> h(count);
+    hip_ok(hipMemcpy(h.data(), d, count * sizeof(unsigned long long), hipMemcpyDeviceToHost), "stamps copy");
+    (void)hipFree(d);
+    int dev = 0, khz = 0;
+    (void)hipGetDevice(&dev);
+    hip_ok(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev), "wall clock rate");
+    const double us_per_tick = 1e3 / (double)khz;
+    for (int k = 0; k < n_phases; k++) {
+        double sum = 0.0, mx = 0.0;
+        for (int b = 0; b < v->n; b++) {
+            const unsigned long long* t = &h[(size_t)b * SBK_NSTAMP];
+            double dt = (t[k + 1] >= t[k]) ? (double)(t[k + 1] - t[k]) * us_per_tick : 0.0;
+            sum += dt;
+            mx = std::max(mx, dt);
+        }
+        mean_us[k] = sum / v->n;
+        max_us[k] = mx;
+    }
+    return n_phases;
+}
+
+int sbx_pass_times(Env* envs, int env, long long* cycles, int cap) {
+    Vec* v = vec_of(envs);
+    if (env < 0 || env >= v->n) return -1;
+    const int np = v->layouts[v->desc[env].layout].dev.n_pass;
+    if (cap < np) return -1;
+    int block = -1;
+    for (int b = 0; b < v->n; b++)
+        if (v->order[b] == env) block = b;
+    unsigned long long* d = nullptr;
+    hip_ok(hipMalloc(&d, (size_t)(np + 1) * sizeof(unsigned long long)), "hipMalloc(pass stamps)");
+    hip_ok(hipMemset(d, 0, (size_t)(np + 1) * sizeof(unsigned long long)), "memset(pass stamps)");
+    sbk::KParams p = params(v, sbk::KMODE_STEP);
+    p.pass_ts = d;
+    p.pass_ts_block = block;
+    int rc = sbk_launch_step(&p, v->n, v->width, v->lds_bytes, g_stream);
+    if (rc != 0) die("step kernel launch failed");
+    hip_ok(hipStreamSynchronize(g_stream), "pass stamps sync");
+    std::vector<unsigned long long> h(np + 1);
+    hip_ok(hipMemcpy(h.data(), d, h.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost), "copy");
+    (void)hipFree(d);
+    // stamps are taken at even passes (and after the last): split each
+    // two-pass interval evenly
+    for (int i = 0; i < np; i += 2) {
+        const int j = std::min(i + 2, np);
+        const long long dt = (long long)(h[j] - h[i]);
+        for (int k = i; k < j; k++) cycles[k] = dt / (j - i);
+    }
+    return np;
+}
+
 float sbx_time_step(Env* envs, int iters) {
     Vec* v = vec_of(envs);
     hipEvent_t a, b;
@@ -1038,6 +1101,7 @@ int sbx_plan_layout(const char* blob_path, int width, SbxPlan* out) {
     out->width = P.width;
     out->n_slots = P.n_slots;
     out->vec_base = P.vec_base;
+    out->inv_base = P.inv_base;
     out->n_pass = P.n_pass();
     out->n_levels = P.n_levels;
     out->n_tasks = P.n_tasks;
@@ -1045,9 +1109,9 @@ int sbx_plan_layout(const char* blob_path, int width, SbxPlan* out) {
     out->kmax = sbh::kPlanKmax;
     out->n_hdr = (int)P.hdr.size();
     out->n_words = (int)P.words.size();
-    out->n_rows = (int)P.row_off.size();
+    out->n_rows = 0;
     out->pass_info = reinterpret_cast<const int*>(P.passes.data());
-    out->row_off = P.row_off.data();
+    out->row_off = nullptr;
     out->hdr = P.hdr.data();
     out->words = P.words.data();
     out->slot_init = P.slot_init.data();

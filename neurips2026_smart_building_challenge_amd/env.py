@@ -58,7 +58,8 @@ class SbxVecInfo(ctypes.Structure):
 
 class SbxPlan(ctypes.Structure):
     _fields_ = [("n", ctypes.c_int), ("width", ctypes.c_int), ("n_slots", ctypes.c_int),
-                ("vec_base", ctypes.c_int), ("n_pass", ctypes.c_int), ("n_levels", ctypes.c_int),
+                ("vec_base", ctypes.c_int), ("inv_base", ctypes.c_int), ("n_pass", ctypes.c_int),
+                ("n_levels", ctypes.c_int),
                 ("n_tasks", ctypes.c_int), ("kmax", ctypes.c_int), ("n_pairs", ctypes.c_longlong),
                 ("n_hdr", ctypes.c_int), ("n_words", ctypes.c_int), ("n_rows", ctypes.c_int),
                 ("pass_info", ctypes.POINTER(ctypes.c_int)), ("row_off", ctypes.POINTER(ctypes.c_int)),
@@ -72,7 +73,7 @@ class SbxPlan(ctypes.Structure):
 EXPORTS = [
     "dict_find", "dict_set", "puf_vec_create", "puf_bind_stream", "puf_init", "puf_reset", "puf_step",
     "puf_render", "puf_close", "puf_log", "puf_live_log", "puf_mask_init", "sbx_gen_actions",
-    "sbx_vec_info", "sbx_env_state", "sbx_time_step", "sbx_env_meta", "sbx_scenario_path",
+    "sbx_vec_info", "sbx_env_state", "sbx_time_step", "sbx_phase_times", "sbx_pass_times", "sbx_env_meta", "sbx_scenario_path",
     "sbx_plan_layout", "sbx_plan_free", "sbx_last_error", "sbx_version",
 ]
 
@@ -105,6 +106,10 @@ def lib() -> ctypes.CDLL:
         L.sbx_env_state.restype = ctypes.c_int
         L.sbx_time_step.argtypes = [ctypes.POINTER(Env), ctypes.c_int]
         L.sbx_time_step.restype = ctypes.c_float
+        L.sbx_phase_times.argtypes = [ctypes.POINTER(Env), P, P, ctypes.c_int]
+        L.sbx_phase_times.restype = ctypes.c_int
+        L.sbx_pass_times.argtypes = [ctypes.POINTER(Env), ctypes.c_int, P, ctypes.c_int]
+        L.sbx_pass_times.restype = ctypes.c_int
         L.sbx_env_meta.argtypes = [ctypes.POINTER(Env), ctypes.c_int, ctypes.POINTER(ctypes.c_int),
                                    ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_uint32)]
         L.sbx_scenario_path.argtypes = [ctypes.POINTER(Env), ctypes.c_int]
@@ -157,11 +162,10 @@ def plan_layout(blob: str | Path, width: int = 64) -> dict[str, np.ndarray]:
         def arr(ptr, n):
             return np.ctypeslib.as_array(ptr, (n,)).copy() if n else np.zeros(0)
         out = {
-            "n": p.n, "width": p.width, "n_slots": p.n_slots, "vec_base": p.vec_base,
+            "n": p.n, "width": p.width, "n_slots": p.n_slots, "vec_base": p.vec_base, "inv_base": p.inv_base,
             "n_pass": p.n_pass, "n_levels": p.n_levels, "n_tasks": p.n_tasks, "n_pairs": p.n_pairs,
             "kmax": p.kmax, "k": p.k,
-            "pass_info": arr(p.pass_info, 8 * p.n_pass).reshape(-1, 8),
-            "row_off": arr(p.row_off, p.n_rows),
+            "pass_info": arr(p.pass_info, 4 * p.n_pass).reshape(-1, 4),
             "hdr": arr(p.hdr, p.n_hdr),
             "words": arr(p.words, p.n_words),
             "slot_init": arr(p.slot_init, p.n_slots),
@@ -227,6 +231,22 @@ class VecEnv:
         d = Dict(ctypes.cast(items, ctypes.POINTER(DictItem)), 0, 8)
         self.L.puf_log(ctypes.byref(self.envs[i].log), ctypes.byref(d))
         return read_dict(d)
+
+    PHASES = ["load", "decode", "hvac_pre", "solve_setup", "solve", "solve_epilogue", "post",
+              "observation", "occupancy", "reward", "bookkeeping", "store"]
+
+    def phase_times(self) -> dict[str, tuple[float, float]]:
+        """(mean, max) microseconds per kernel phase over workgroups, for one step."""
+        k = len(self.PHASES)
+        mean, mx = np.zeros(k), np.zeros(k)
+        n = self.L.sbx_phase_times(self.envs, mean.ctypes.data_as(P), mx.ctypes.data_as(P), k)
+        return {self.PHASES[i]: (float(mean[i]), float(mx[i])) for i in range(n)}
+
+    def pass_times(self, i: int) -> np.ndarray:
+        """Shader-clock cycles of each solve pass of env i for one step."""
+        buf = np.zeros(65536, np.int64)
+        n = self.L.sbx_pass_times(self.envs, i, buf.ctypes.data_as(P), buf.size)
+        return buf[:max(n, 0)].copy()
 
     def time_step(self, iters: int) -> float:
         return float(self.L.sbx_time_step(self.envs, iters))
