@@ -157,8 +157,19 @@ float sbx_time_step(Env* envs, int iters);
 int sbx_phase_times(Env* envs, double* mean_us, double* max_us, int n_phases);
 
 /* Runs one step recording the shader-clock duration of every solve pass of
- * env `env`'s workgroup. Returns the number of passes written (<= cap). */
+ * env `env`'s workgroup (for a layout on the relaxation solver: the setup,
+ * then every sweep). Returns the number of entries written (<= cap). */
 int sbx_pass_times(Env* envs, int env, long long* cycles, int cap);
+
+/* Field solver of env i's layout and its counters: out[0] solver (0 LU plan,
+ * 1 relaxation), out[1] the certified contraction bound rho (relaxation; 0
+ * otherwise), out[2] relaxation sweeps of the env's last step, out[3] steps of
+ * the env that stopped at the sweep cap (64) without meeting the error bound.
+ * The solver is chosen per vec by kwargs "solver": "auto" (default:
+ * relaxation for every layout where it is certified, rho <= 0.5, at most 256
+ * solved cells and 8 off-diagonal entries per row), "lu" or "relax". Returns
+ * 4, or -1. Synchronous. */
+int sbx_solve_info(Env* envs, int i, double* out);
 
 /* Scenario of env i (index into the sorted, round-robin ordered blob list),
  * its calendar start offset and occupancy seed. */
@@ -186,9 +197,8 @@ typedef struct SbxPlan {
     int n_tasks;
     int kmax;            /* max terms per task */
     long long n_pairs;   /* multiply-subtract terms */
-    int n_hdr, n_words, n_rows;  /* n_rows: unused, 0 */
+    int n_hdr, n_words;
     const int* pass_info;        /* [n_pass * 4] */
-    const int* row_off;          /* unused, NULL */
     const uint64_t* hdr;         /* [n_hdr] */
     const uint32_t* words;       /* [n_words]: a | b << 16 */
     const double* slot_init;     /* [n_slots] A values at LU slots, 0 elsewhere */
@@ -196,6 +206,16 @@ typedef struct SbxPlan {
     const int* air_slot;         /* [k] LU slot of the coupled air diagonal */
     const int* air_node;         /* [k] node of coupled column c */
     int k;
+    /* relaxation form: rows padded to rx_rows; entry m of row i at m * rx_rows + i
+     * of rx_val / rx_col, (0.0, 0) past the row; x_i <- (b_i - sum_m rx_val *
+     * x[rx_col]) / (rx_diag_i + g of air column rx_air_i, if >= 0) */
+    int rx_ok;                   /* 1 when the relaxation form is certified */
+    int rx_rows, rx_terms_max, rx_terms;
+    double rx_rho;               /* max_i sum_j |a_ij| / a_ii */
+    const double* rx_diag;       /* [rx_rows] */
+    const int* rx_air;           /* [rx_rows] */
+    const double* rx_val;        /* [rx_terms_max * rx_rows] */
+    const int* rx_col;           /* [rx_terms_max * rx_rows] */
 } SbxPlan;
 int sbx_plan_layout(const char* blob_path, int width, SbxPlan* out);
 void sbx_plan_free(SbxPlan* p);

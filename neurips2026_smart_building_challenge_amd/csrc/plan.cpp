@@ -29,9 +29,13 @@
 // whose address needs nothing but the pass record.
 // Dot products longer than kPlanKmax terms become a chain of tasks on the same
 // slot; only the last one divides.
+//
+// build_relax prepares the alternative used for strongly diagonally dominant
+// systems: Jacobi sweeps with a certified contraction bound (see plan.h).
 #include "plan.h"
 
 #include <algorithm>
+#include <cmath>
 #include <unordered_map>
 
 namespace sbh {
@@ -295,6 +299,63 @@ bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
     P.n_pairs = npairs;
     P.n_divs = ndiv;
     return true;
+}
+
+void build_relax(const Blob& b, const SolvePlan& lu, RelaxPlan* out) {
+    RelaxPlan& R = *out;
+    R = RelaxPlan();
+    const int n = lu.n;
+    R.n = n;
+    auto no = [&](const std::string& why) { R.ok = false; R.why = why; };
+    if (n > kRelaxRows) return no("more than " + std::to_string(kRelaxRows) + " solved cells");
+    uint64_t cnt = 0;
+    const int32_t* Ap = b.i32("A_system_indptr", &cnt);
+    const int32_t* Ai = b.i32("A_system_indices");
+    const double* Ax = b.f64("A_system_data");
+    if (!Ap || !Ai || !Ax || (int)cnt != n + 1) return no("blob lacks A_system");
+    // CSC -> rows (duplicates summed, explicit zeros dropped)
+    std::vector<std::vector<std::pair<int, double>>> rows(n);
+    std::vector<double> diag(n, 0.0);
+    for (int c = 0; c < n; c++)
+        for (int p = Ap[c]; p < Ap[c + 1]; p++) {
+            const int r = Ai[p];
+            if (r < 0 || r >= n) return no("A_system row index out of range");
+            if (r == c) { diag[r] += Ax[p]; continue; }
+            bool merged = false;
+            for (auto& e : rows[r])
+                if (e.first == c) { e.second += Ax[p]; merged = true; }
+            if (!merged) rows[r].push_back({c, Ax[p]});
+        }
+    double rho = 0.0;
+    int terms = 0;
+    for (int i = 0; i < n; i++) {
+        auto& row = rows[i];
+        row.erase(std::remove_if(row.begin(), row.end(), [](const std::pair<int, double>& e) { return e.second == 0.0; }),
+                  row.end());
+        std::sort(row.begin(), row.end());
+        if (!(diag[i] > 0.0)) return no("a diagonal entry of A is not positive");
+        double off = 0.0;
+        for (auto& e : row) off += std::fabs(e.second);
+        rho = std::max(rho, off / diag[i]);
+        terms = std::max(terms, (int)row.size());
+    }
+    R.rho = rho;
+    R.terms = terms;
+    if (terms > kRelaxTerms) return no("a row of A has more than " + std::to_string(kRelaxTerms) + " off-diagonal entries");
+    if (!(rho <= kRelaxRhoMax)) return no("A is not diagonally dominant enough (rho " + std::to_string(rho) + ")");
+    R.diag.assign(kRelaxRows, 1.0);
+    R.air_col.assign(kRelaxRows, -1);
+    R.val.assign((size_t)kRelaxTerms * kRelaxRows, 0.0);
+    R.col.assign((size_t)kRelaxTerms * kRelaxRows, 0);
+    for (int i = 0; i < n; i++) {
+        R.diag[i] = diag[i];
+        for (size_t m = 0; m < rows[i].size(); m++) {
+            R.val[m * kRelaxRows + i] = rows[i][m].second;
+            R.col[m * kRelaxRows + i] = rows[i][m].first;
+        }
+    }
+    for (int c = 0; c < lu.k; c++) R.air_col[lu.air_node[c]] = c;
+    R.ok = true;
 }
 
 }  // namespace sbh

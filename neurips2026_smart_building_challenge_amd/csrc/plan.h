@@ -48,4 +48,34 @@ struct SolvePlan {
 // pattern closed under elimination, one unit applied/sensed entry per column.
 bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err);
 
+// Relaxation (Jacobi) form of the same solve, x <- D^-1 (b - O x) with
+// D = diag(A) + g and O the off-diagonal part of A. It converges for every
+// step when A has positive diagonal entries and
+//   rho = max_i sum_{j != i} |a_ij| / a_ii < 1,
+// because g >= 0 only enlarges D: rho bounds the infinity norm of the
+// iteration matrix for every g, and after sweep m
+//   |x* - x_m|_inf <= rho / (1 - rho) * |x_m - x_{m-1}|_inf,
+// which the kernel uses as its stopping test. Row i of the device table is
+// handled by lane i % 64 as its (i / 64)-th row.
+constexpr int kRelaxRowsPerLane = 4;
+constexpr int kRelaxRows = 64 * kRelaxRowsPerLane;   // padded row count
+constexpr int kRelaxTerms = 8;                       // off-diagonal entries per row
+constexpr double kRelaxRhoMax = 0.5;                 // larger bounds use the LU plan
+
+struct RelaxPlan {
+    bool ok = false;
+    std::string why;                 // reason when not eligible
+    int n = 0, terms = 0;            // terms: longest off-diagonal row
+    double rho = 0.0;
+    std::vector<double> diag;        // [kRelaxRows], padding 1.0
+    std::vector<int> air_col;        // [kRelaxRows] air-side column of the node, or -1
+    std::vector<double> val;         // [kRelaxTerms * kRelaxRows]: entry m of row i at m * kRelaxRows + i
+    std::vector<int> col;            // same layout; padding entries are (0.0, column 0)
+};
+
+// Fills *out from the blob's A_system and the air-side columns of the LU plan
+// (built first, it validates the air side). Never fails: out->ok says whether
+// the relaxation form applies and out->why why not.
+void build_relax(const Blob& b, const SolvePlan& lu, RelaxPlan* out);
+
 }  // namespace sbh

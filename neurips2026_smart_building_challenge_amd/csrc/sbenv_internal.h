@@ -17,6 +17,11 @@
 #define SBK_NAUX_MAX 16
 #define SBK_KMAX 48      // terms per lane per pass (matches the planner)
 #define SBK_NSTAMP 16    // phase stamps per workgroup when phase timing is on
+#define SBK_RX_RPL 4     // relaxation rows per lane (matches the planner)
+#define SBK_RX_ROWS 256  // padded relaxation rows
+#define SBK_RX_TERMS 8   // relaxation off-diagonal entries per row
+#define SBK_RX_MAXIT 64  // sweep cap (rho <= 1/2 contracts by 2^-64 before it)
+#define SBK_RX_TOL 1e-13 // stop when the error bound is below TOL * max |T|
 
 namespace sbk {
 
@@ -41,8 +46,11 @@ struct StateLayout {
     int record_bytes;                           // image + mt, 256-byte aligned
 };
 
+// PF_SWEEPS: relaxation sweeps of the last step; PF_CAPPED: steps that hit the sweep cap
 enum { PF_PUMP_HEAD = 0, PF_BOILER_SP, PF_BOILER_RET, PF_BOILER_CUR, PF_BOILER_DSTEP,
-       PF_REW_SUM, PF_SPARE0, PF_SPARE1 };
+       PF_REW_SUM, PF_SWEEPS, PF_CAPPED };
+
+enum { SOLVER_LU = 0, SOLVER_RELAX = 1 };
 enum { PI_HWS_RUN = 0, PI_PUMP_RUN, PI_HWS_REQ, PI_STEP_INDEX, PI_STEP, PI_MT_IDX,
        PI_STEPS_TOTAL, PI_EPISODES };
 
@@ -70,8 +78,16 @@ struct DevLayout {
     int n, nz, nv, na, k, n_act, n_cont, n_disc, n_dev, n_aux, nassign;
     int n_slots, vec_base, n_pass, width;
     int max_room_cells;
+    int solver;                        // SOLVER_LU or SOLVER_RELAX
+    int rx_terms;                      // longest off-diagonal row (relaxation)
+    double rx_stop;                    // rho / (1 - rho)
     StateLayout st;
     LdsLayout lds;
+    // relaxation tables, rows padded to SBK_RX_ROWS
+    const SBK_C double* rx_diag;       // [SBK_RX_ROWS]
+    const SBK_C int* rx_air;           // [SBK_RX_ROWS] air-side column or -1
+    const SBK_C double* rx_val;        // [SBK_RX_TERMS * SBK_RX_ROWS]
+    const SBK_C int* rx_col;           // [SBK_RX_TERMS * SBK_RX_ROWS]
     // solve plan
     const SBK_C int* pinfo;            // [n_pass * 4]: hdr_off, word_off, nact | maxcnt << 8 | pivot << 16, 0
     const SBK_C uint64_t* hdr;         // per active lane: target | mul << 16 | inv_target << 32 | count << 48
@@ -167,10 +183,10 @@ struct EnvDesc {
 enum { KMODE_STEP = 0, KMODE_RESET = 1 };
 
 struct KParams {
-    const EnvDesc* envs;
-    const int* order;            // block -> env
-    const DevLayout* layouts;
-    const DevScen* scens;
+    const SBK_C EnvDesc* envs;
+    const SBK_C int* order;      // block -> env
+    const SBK_C DevLayout* layouts;
+    const SBK_C DevScen* scens;
     unsigned char* state;
     const float* actions;
     float* obs;

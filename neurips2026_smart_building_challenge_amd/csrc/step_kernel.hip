@@ -155,8 +155,8 @@ __device__ __forceinline__ int bscan(int v, int* scr, int* total) {
 }
 
 struct Ctx {
-    const DevLayout* L;
-    const DevScen* S;
+    const SBK_C DevLayout* L;
+    const SBK_C DevScen* S;
     unsigned char* rec;      // HBM record of this env
     double *T, *M, *damper, *reheat, *ratio, *heatsp, *coolsp, *dcmd, *rcmd, *sensing;
     double *recirc, *sat, *fan, *flow, *plant;
@@ -170,9 +170,9 @@ struct Ctx {
 };
 
 __device__ __forceinline__ void bind(Ctx& c, unsigned char* lds) {
-    const DevLayout* L = c.L;
+    const SBK_C DevLayout* L = c.L;
     unsigned char* s = lds + L->lds.state;
-    const StateLayout& st = L->st;
+    const StateLayout st = L->st;
     c.T = (double*)(s + st.T);
     c.M = (double*)(s + st.M);
     c.damper = (double*)(s + st.damper);
@@ -197,7 +197,7 @@ __device__ __forceinline__ void bind(Ctx& c, unsigned char* lds) {
     c.rcmd_set = s + st.rcmd_set;
     c.occ_state = s + st.occ_state;
     c.occV = s + st.occV;
-    const LdsLayout& l = L->lds;
+    const LdsLayout l = L->lds;
     c.slots = (double*)(lds + l.slots);
     c.mt = (uint32_t*)(lds + l.mt);
     c.zq = (double*)(lds + l.zq);
@@ -249,7 +249,7 @@ __device__ __forceinline__ int default_mode(int cur, double zt, double hsp, doub
 // zone means of room cells (ascending), sb_sim.c:149-160
 template <int W>
 __device__ __forceinline__ void zone_means(Ctx& c, double* out) {
-    const DevLayout* L = c.L;
+    const SBK_C DevLayout* L = c.L;
     for (int z = threadIdx.x; z < L->nz; z += W) {
         int a = L->zone_cell_off[z], b = L->zone_cell_off[z + 1];
         double sum = 0.0;
@@ -260,7 +260,7 @@ __device__ __forceinline__ void zone_means(Ctx& c, double* out) {
 
 // area-weighted VAV temperature from zone means (sb_sim.c:163-175)
 __device__ __forceinline__ double vav_temp(const Ctx& c, const double* zmean, int v, double* area_out) {
-    const DevLayout* L = c.L;
+    const SBK_C DevLayout* L = c.L;
     double area = 0.0, wt = 0.0;
     for (int t = L->vz_off[v]; t < L->vz_off[v + 1]; t++) {
         int z = L->vz_idx[t];
@@ -312,7 +312,7 @@ __device__ __forceinline__ double obs_value(const Ctx& c, int kind, int idx, int
 template <int W>
 __device__ __forceinline__ void write_obs(Ctx& c, int j, float* row) {
 #pragma clang fp contract(off)
-    const DevLayout* L = c.L;
+    const SBK_C DevLayout* L = c.L;
     for (int i = threadIdx.x; i < L->n_dev; i += W) {
         double v = obs_value(c, L->f_kind[i], L->f_idx[i], L->f_id[i], j);
         double sd = L->f_sd[i];
@@ -401,8 +401,8 @@ __device__ __forceinline__ void gather_words(Ptr src, int idx, int first, const 
 // 2 * (number of drawing occupants before o).
 template <int W>
 __device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday) {
-    const DevLayout* L = c.L;
-    const DevScen* S = c.S;
+    const SBK_C DevLayout* L = c.L;
+    const SBK_C DevScen* S = c.S;
     const int nocc = L->nz * L->nassign;
     constexpr int MAXC = 8;   // occupants per lane (nocc <= 8 * W, checked on the host)
     const int per = (nocc + W - 1) / W;
@@ -496,8 +496,8 @@ __device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday)
 // sb_sim_reset (sb_sim.c:177-218) on the LDS image; pump head is not reset.
 template <int W>
 __device__ __forceinline__ void sim_reset(Ctx& c, int start) {
-    const DevLayout* L = c.L;
-    const DevScen* S = c.S;
+    const SBK_C DevLayout* L = c.L;
+    const SBK_C DevScen* S = c.S;
     for (int a = threadIdx.x; a < L->na; a += W) {
         const double* ac = L->ahu_c + a * 9;
         c.run[a] = (int)ac[8];
@@ -549,7 +549,7 @@ __device__ __forceinline__ void sim_reset(Ctx& c, int start) {
 // puf_reset sequence (pufferlib_cpu_env.h:187-208) at the env's start offset.
 template <int W>
 __device__ __forceinline__ void env_reset(Ctx& c, int start, float* obs_row) {
-    const DevScen* S = c.S;
+    const SBK_C DevScen* S = c.S;
     sim_reset<W>(c, start);
     occupancy_advance<W>(c, S->hour_m1[start], S->work_m1[start]);
     write_obs<W>(c, start, obs_row);
@@ -560,7 +560,7 @@ __device__ __forceinline__ void env_reset(Ctx& c, int start, float* obs_row) {
 template <int W>
 __device__ __forceinline__ void decode_apply(Ctx& c, const float* act) {
 #pragma clang fp contract(off)
-    const DevLayout* L = c.L;
+    const SBK_C DevLayout* L = c.L;
     for (int i = threadIdx.x; i < L->n_act; i += W) {
         double nat;
         float a = act[L->act_src[i]];
@@ -603,8 +603,8 @@ __device__ __forceinline__ void decode_apply(Ctx& c, const float* act) {
 
 template <int W>
 __device__ __forceinline__ void step_pre(Ctx& c) {
-    const DevLayout* L = c.L;
-    const DevScen* S = c.S;
+    const SBK_C DevLayout* L = c.L;
+    const SBK_C DevScen* S = c.S;
     const int kk = c.ip[PI_STEP_INDEX];
     const double ambient = S->amb[kk];
     const int comfort = (S->comfort[kk] != 0.0);
@@ -810,7 +810,7 @@ struct PassRegs {
 // chunks of 8 without per-row branches; rows past maxcnt (the next pass's
 // words, or the array's tail padding) and lanes past nact read in-bounds words
 // that are then replaced by the (0, 0) term.
-__device__ __forceinline__ void fetch_pass(const DevLayout* L, int4 pi, PassRegs& r) {
+__device__ __forceinline__ void fetch_pass(const SBK_C DevLayout* L, int4 pi, PassRegs& r) {
     const int hdr_off = pi.x, word_off = pi.y;
     const int nact = pi.z & 0xff, maxcnt = (pi.z >> 8) & 0xff, has_pivot = (pi.z >> 16) & 1;
     const int lane = threadIdx.x;
@@ -888,7 +888,7 @@ __device__ __forceinline__ void run_pass(double* slots, const PassRegs& r) {
 // All passes. Pass p+1's words are loaded while pass p computes and settled
 // after it; pass records are read two passes ahead.
 template <int W>
-__device__ __forceinline__ void run_plan(const DevLayout* L, double* slots, const int4* rec,
+__device__ __forceinline__ void run_plan(const SBK_C DevLayout* L, double* slots, const int4* rec,
                                          unsigned long long* pts) {
     static_assert(W == 64, "the solve plan runs on one wavefront");
     const int np = L->n_pass;
@@ -916,17 +916,141 @@ __device__ __forceinline__ void run_plan(const DevLayout* L, double* slots, cons
     if (pts) pts[np] = clock64();
 }
 
+// ------------------------------------------------------------------ relaxation
+// (A + diag(g)) y = b by Jacobi sweeps, for layouts whose host-computed bound
+// rho = max_i sum_j |a_ij| / a_ii is at most 1/2 (g >= 0 only strengthens the
+// diagonal, so rho bounds every step's iteration matrix in the infinity norm).
+// Lane l owns rows l, l + 64, l + 128, l + 192: their right-hand sides,
+// reciprocal diagonals and off-diagonal entries stay in registers, the iterate
+// lives in LDS (in the state image's T array, which starts as the previous
+// step's solution). A sweep reads every neighbour value before any lane writes
+// (one wavefront; its LDS operations complete in issue order), so it is a true
+// Jacobi sweep. It stops once rho / (1 - rho) * max|x_m - x_{m-1}|, a bound on
+// the distance to the exact solution, is at most SBK_RX_TOL * max|T|.
+// Sweeps with K off-diagonal terms per row (the tables are padded with
+// (0.0, column 0) entries, so every load is unconditional and a sweep issues
+// all its LDS reads back to back). Returns the number of sweeps.
+template <int K>
+__device__ __forceinline__ int relax_sweeps(const SBK_C DevLayout* L, double* x, int n, const double* bv,
+                                            const double* iv, double* xv, double atol,
+                                            unsigned long long* pts) {
+    const int lane = threadIdx.x;
+    double av[SBK_RX_RPL][K];
+    int ci[SBK_RX_RPL][K];
+#pragma unroll
+    for (int j = 0; j < SBK_RX_RPL; j++) {
+        const int t = lane + 64 * j;   // < SBK_RX_ROWS: tables are padded
+#pragma unroll
+        for (int m = 0; m < K; m++) {
+            av[j][m] = L->rx_val[m * SBK_RX_ROWS + t];
+            ci[j][m] = L->rx_col[m * SBK_RX_ROWS + t];
+        }
+    }
+    const double stop = L->rx_stop;
+    if (pts) pts[1] = clock64();
+    int it = 0;
+    bool done = false;
+    while (!done) {
+        double xn[SBK_RX_RPL];
+#pragma unroll
+        for (int j = 0; j < SBK_RX_RPL; j++) {
+            double acc = bv[j];
+#pragma unroll
+            for (int m = 0; m < K; m++) acc -= av[j][m] * x[ci[j][m]];
+            xn[j] = acc * iv[j];
+        }
+        double dmax = 0.0;
+#pragma unroll
+        for (int j = 0; j < SBK_RX_RPL; j++) {
+            const int t = lane + 64 * j;
+            if (t < n) {
+                dmax = fmax(dmax, fabs(xn[j] - xv[j]));
+                xv[j] = xn[j];
+                x[t] = xn[j];
+            }
+        }
+        wave_lds_sync();
+        ++it;
+        done = __all(stop * dmax <= atol) || it >= SBK_RX_MAXIT;
+        if (pts) pts[1 + it] = clock64();
+    }
+    return it;
+}
+
+template <int W>
+__device__ __forceinline__ void relax_solve(Ctx& c, double ambient, double irr, unsigned long long* pts) {
+    static_assert(W == 64, "the relaxation sweep runs on one wavefront");
+    const SBK_C DevLayout* L = c.L;
+    const SBK_C DevScen* S = c.S;
+    const int n = L->n;
+    const int lane = threadIdx.x;
+    if (pts) pts[0] = clock64();
+    double bv[SBK_RX_RPL], iv[SBK_RX_RPL], xv[SBK_RX_RPL];
+    double xabs = 0.0;
+#pragma unroll
+    for (int j = 0; j < SBK_RX_RPL; j++) {
+        const int t = lane + 64 * j;
+        bv[j] = 0.0;
+        iv[j] = 0.0;
+        xv[j] = 0.0;
+        if (t < n) {
+            const double qin = L->is_room[t] ? c.slots[t] + L->solar_c[t] * irr : L->solar_c[t] * irr;
+            double b = L->cap[t] * c.T[t] + qin + ambient * S->dirx[t] + L->mcoup[t] * c.M[t];
+            double d = L->rx_diag[t];
+            const int col = L->rx_air[t];
+            if (col >= 0) {
+                const double g = c.g[col];
+                b += g * c.tair[col];
+                d += g;
+            }
+            bv[j] = b;
+            iv[j] = recip(d);
+            xv[j] = c.T[t];
+            xabs = fmax(xabs, fabs(xv[j]));
+        }
+    }
+    const double atol = SBK_RX_TOL * wave_max(xabs);
+    const int nt = L->rx_terms;
+    const int it = nt <= 4   ? relax_sweeps<4>(L, c.T, n, bv, iv, xv, atol, pts)
+                   : nt <= 6 ? relax_sweeps<6>(L, c.T, n, bv, iv, xv, atol, pts)
+                             : relax_sweeps<SBK_RX_TERMS>(L, c.T, n, bv, iv, xv, atol, pts);
+    if (lane == 0) {
+        c.plant[PF_SWEEPS] = (double)it;
+        if (it >= SBK_RX_MAXIT) c.plant[PF_CAPPED] += 1.0;
+    }
+#pragma unroll
+    for (int j = 0; j < SBK_RX_RPL; j++) {
+        const int t = lane + 64 * j;
+        if (t < n) c.M[t] = c.M[t] * L->mret[t] + L->mgain[t] * xv[j];
+    }
+    __syncthreads();
+}
+
 // Field step: b = cap T + q + amb dirx + mc M (+ solar, + g T_air at the air
-// nodes), then (A + diag(g)) y = b by the plan; mass and field update.
+// nodes), then (A + diag(g)) y = b by the plan (or by relaxation); mass and
+// field update.
 template <int W>
 __device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
-    const DevLayout* L = c.L;
-    const DevScen* S = c.S;
+    const SBK_C DevLayout* L = c.L;
+    const SBK_C DevScen* S = c.S;
     const int kk = c.ip[PI_STEP_INDEX];
     const double ambient = S->amb[kk];
     const double irr = S->solar_i[kk];
     const int n = L->n;
     double* slots = c.slots;
+    if (L->solver == SOLVER_RELAX) {
+        // room cells carry their zone's heat (node-indexed scratch in the slot region)
+        for (int z = threadIdx.x; z < L->nz; z += W) {
+            double qz = c.zq[z];
+            for (int t = L->zone_cell_off[z]; t < L->zone_cell_off[z + 1]; t++) slots[L->zone_cells[t]] = qz;
+        }
+        __syncthreads();
+        STAMP(4);
+        unsigned long long* pts = (P.pass_ts && blockIdx.x == P.pass_ts_block && threadIdx.x == 0) ? P.pass_ts : nullptr;
+        relax_solve<W>(c, ambient, irr, pts);
+        STAMP(5);
+        return;
+    }
     const int vb = L->vec_base;
     for (int s = threadIdx.x; s < vb; s += W) slots[s] = L->slot_init[s];   // incl. 0.0 and 1.0 slots
     // room cells carry their zone's heat; every node then gets its solar gain
@@ -964,7 +1088,7 @@ __device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
 template <int W>
 __device__ __forceinline__ void step_post(Ctx& c) {
     if (threadIdx.x == 0) {
-        const DevScen* S = c.S;
+        const SBK_C DevScen* S = c.S;
         const double total_rw = c.misc[MS_TOTAL_REHEAT];
         double wcap = CP_W * RHO_W * c.misc[MS_TF];
         if (wcap > 0.0 && c.L->k > 0) {
@@ -999,8 +1123,8 @@ __device__ __forceinline__ void step_post(Ctx& c) {
 // 3C reward (sb_reward.c:31-155) on the post-step state and new occupancy.
 template <int W>
 __device__ __forceinline__ double reward(Ctx& c, int kv) {
-    const DevLayout* L = c.L;
-    const DevScen* S = c.S;
+    const SBK_C DevLayout* L = c.L;
+    const SBK_C DevScen* S = c.S;
     const double dt = S->dt_sec, inv_hour = 1.0 / 3600.0;
     zone_means<W>(c, c.zq);
     __syncthreads();
@@ -1113,7 +1237,7 @@ __global__ __launch_bounds__(W) void step_kernel(KParams P) {
     c.S = P.scens + ed.scen;
     c.rec = P.state + ed.state_off;
     bind(c, lds);
-    const DevLayout* L = c.L;
+    const SBK_C DevLayout* L = c.L;
     STAMP(0);
     copy16<W>(lds + L->lds.state, c.rec, L->st.bytes);
     if (P.mode == KMODE_STEP) {

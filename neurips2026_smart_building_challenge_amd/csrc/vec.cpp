@@ -76,6 +76,7 @@ uint64_t splitmix64(uint64_t x) {
 struct HostLayout {
     std::string key;
     sbh::SolvePlan plan;
+    sbh::RelaxPlan relax;
     sbk::DevLayout dev{};   // sizes + layouts; pointers patched after upload
     std::map<std::string, size_t> off;
 };
@@ -114,10 +115,18 @@ std::string structural_key(const sbh::Blob& b) {
 template <class T>
 std::vector<T> take(const T* p, uint64_t n) { return p ? std::vector<T>(p, p + n) : std::vector<T>(); }
 
-// Builds one layout's tables (everything shared by its scenarios).
-bool make_layout(const sbh::Blob& b, int width, HostLayout* H, Arena& A, std::string* err) {
+enum { SOLVE_AUTO = 0, SOLVE_LU = 1, SOLVE_RELAX = 2 };
+
+// Builds one layout's tables (everything shared by its scenarios). `solve`
+// picks the field solver: the relaxation form where it is certified (AUTO),
+// or the one named.
+bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena& A, std::string* err) {
     if (!sbh::build_plan(b, width, &H->plan, err)) return false;
     const sbh::SolvePlan& P = H->plan;
+    sbh::build_relax(b, P, &H->relax);
+    const sbh::RelaxPlan& R = H->relax;
+    if (solve == SOLVE_RELAX && !R.ok) return (*err = "relaxation solver not applicable: " + R.why), false;
+    const bool relax = solve == SOLVE_RELAX || (solve == SOLVE_AUTO && R.ok);
     sbk::DevLayout& D = H->dev;
     uint64_t cnt = 0;
     const int n = P.n;
@@ -229,6 +238,10 @@ bool make_layout(const sbh::Blob& b, int width, HostLayout* H, Arena& A, std::st
     D.n_dev = n_dev; D.n_aux = n_aux; D.nassign = nassign;
     D.n_slots = P.n_slots; D.vec_base = P.vec_base; D.n_pass = P.n_pass(); D.width = width;
     D.max_room_cells = max_cells;
+    D.solver = relax ? sbk::SOLVER_RELAX : sbk::SOLVER_LU;
+    D.rx_terms = relax ? R.terms : 0;
+    D.rx_stop = relax ? R.rho / (1.0 - R.rho) : 0.0;
+    if (relax) D.n_pass = 0;
     // state record
     sbk::StateLayout& S = D.st;
     int o = 0;
@@ -248,7 +261,8 @@ bool make_layout(const sbh::Blob& b, int width, HostLayout* H, Arena& A, std::st
     sbk::LdsLayout& Ls = D.lds;
     int l = 0;
     Ls.state = 0; l = S.bytes;
-    Ls.slots = l; Ls.mt = l; l += std::max(8 * P.n_slots, 4 * (SBK_MT_N + 1)); l = align_up(l, 16);
+    // slots: the LU entries and vector, or (relaxation) the node heat inputs
+    Ls.slots = l; Ls.mt = l; l += std::max(8 * (relax ? n : P.n_slots), 4 * (SBK_MT_N + 1)); l = align_up(l, 16);
     Ls.zq = l; l += 8 * nz;
     Ls.vtmp = l; l += 8 * 3 * nv;
     Ls.g = l; l += 8 * std::max(k, 1);
@@ -258,12 +272,22 @@ bool make_layout(const sbh::Blob& b, int width, HostLayout* H, Arena& A, std::st
     Ls.misc = l; l += 8 * 32;
     Ls.iscr = l; l += 4 * (width / 64 + 8);
     l = align_up(l, 16);
-    Ls.prec = l; l += 16 * P.n_pass();
+    Ls.prec = l; l += 16 * D.n_pass;
     Ls.bytes = align_up(l, 16);
     D.bytes_per_step = 2.0 * S.bytes + 4.0 * (ncont + ndisc) + 4.0 * SB_OBS + 8.0;
     D.solve_flops = 2.0 * (double)P.n_pairs + (double)P.n_divs;
+    if (relax) {   // per sweep: one multiply-subtract per off-diagonal entry, one scaling per row
+        long long nnz = 0;
+        for (int i = 0; i < n; i++)
+            for (int m = 0; m < sbh::kRelaxTerms; m++) nnz += R.val[(size_t)m * sbh::kRelaxRows + i] != 0.0;
+        D.solve_flops = 2.0 * (double)nnz + (double)n;
+    }
 
     auto& O = H->off;
+    O["rx_diag"] = A.vec(R.ok ? R.diag : std::vector<double>(sbh::kRelaxRows, 1.0));
+    O["rx_air"] = A.vec(R.ok ? R.air_col : std::vector<int>(sbh::kRelaxRows, -1));
+    O["rx_val"] = A.vec(R.ok ? R.val : std::vector<double>((size_t)sbh::kRelaxTerms * sbh::kRelaxRows, 0.0));
+    O["rx_col"] = A.vec(R.ok ? R.col : std::vector<int>((size_t)sbh::kRelaxTerms * sbh::kRelaxRows, 0));
     O["pinfo"] = A.add(P.passes.data(), P.passes.size() * sizeof(sbh::PassInfo));
     O["hdr"] = A.vec(P.hdr);
     O["words"] = A.vec(P.words);
@@ -317,6 +341,10 @@ bool make_layout(const sbh::Blob& b, int width, HostLayout* H, Arena& A, std::st
 void patch_layout(HostLayout* H, unsigned char* d) {
     sbk::DevLayout& D = H->dev;
     auto& O = H->off;
+    D.rx_diag = at<double>(d, O["rx_diag"]);
+    D.rx_air = at<int>(d, O["rx_air"]);
+    D.rx_val = at<double>(d, O["rx_val"]);
+    D.rx_col = at<int>(d, O["rx_col"]);
     D.pinfo = at<int>(d, O["pinfo"]);
     D.hdr = at<uint64_t>(d, O["hdr"]);
     D.words = at<uint32_t>(d, O["words"]);
@@ -684,6 +712,13 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
     v->paths = files;
     std::vector<int> scnt(G);
     for (int i = 0; i < G; i++) scnt[i] = n / G + (i < n % G ? 1 : 0);
+    // ---- field solver: "auto" (relaxation where certified), "lu" or "relax"
+    int solve = SOLVE_AUTO;
+    if (const char* sv = kws(kwargs, "solver")) {
+        if (!strcmp(sv, "lu")) solve = SOLVE_LU;
+        else if (!strcmp(sv, "relax")) solve = SOLVE_RELAX;
+        else if (strcmp(sv, "auto")) die(std::string("env.solver must be auto, lu or relax, not ") + sv);
+    }
     // ---- layouts + scenarios
     Arena A;
     std::map<std::string, int> layout_of_key;
@@ -697,7 +732,7 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
         if (it == layout_of_key.end()) {
             HostLayout H;
             H.key = key;
-            if (!make_layout(b, v->width, &H, A, &err)) die(files[i] + ": " + err);
+            if (!make_layout(b, v->width, solve, &H, A, &err)) die(files[i] + ": " + err);
             li = (int)v->layouts.size();
             v->layouts.push_back(std::move(H));
             layout_of_key[key] = li;
@@ -1024,7 +1059,9 @@ int sbx_phase_times(Env* envs, double* mean_us, double* max_us, int n_phases) {
 int sbx_pass_times(Env* envs, int env, long long* cycles, int cap) {
     Vec* v = vec_of(envs);
     if (env < 0 || env >= v->n) return -1;
-    const int np = v->layouts[v->desc[env].layout].dev.n_pass;
+    const bool relax = v->layouts[v->desc[env].layout].dev.solver == sbk::SOLVER_RELAX;
+    // relaxation: a stamp at entry, after the setup and after every sweep
+    const int np = relax ? SBK_RX_MAXIT + 1 : v->layouts[v->desc[env].layout].dev.n_pass;
     if (cap < np) return -1;
     int block = -1;
     for (int b = 0; b < v->n; b++)
@@ -1041,6 +1078,14 @@ int sbx_pass_times(Env* envs, int env, long long* cycles, int cap) {
     std::vector<unsigned long long> h(np + 1);
     hip_ok(hipMemcpy(h.data(), d, h.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost), "copy");
     (void)hipFree(d);
+    if (relax) {
+        int m = 0;
+        while (m < np && h[m + 1] != 0) {
+            cycles[m] = (long long)(h[m + 1] - h[m]);
+            m++;
+        }
+        return m;
+    }
     // stamps are taken at even passes (and after the last): split each
     // two-pass interval evenly
     for (int i = 0; i < np; i += 2) {
@@ -1067,6 +1112,22 @@ float sbx_time_step(Env* envs, int iters) {
     return ms;
 }
 
+int sbx_solve_info(Env* envs, int i, double* out) {
+    Vec* v = vec_of(envs);
+    if (i < 0 || i >= v->n || !out) return -1;
+    const sbk::EnvDesc& d = v->desc[i];
+    const HostLayout& H = v->layouts[d.layout];
+    double pf[8];
+    hip_ok(hipStreamSynchronize(g_stream), "state sync");
+    hip_ok(hipMemcpy(pf, v->d_state + d.state_off + H.dev.st.plant, sizeof(pf), hipMemcpyDeviceToHost), "copy");
+    const bool relax = H.dev.solver == sbk::SOLVER_RELAX;
+    out[0] = relax ? 1.0 : 0.0;
+    out[1] = relax ? H.relax.rho : 0.0;
+    out[2] = pf[sbk::PF_SWEEPS];
+    out[3] = pf[sbk::PF_CAPPED];
+    return 4;
+}
+
 int sbx_env_meta(Env* envs, int i, int* scenario, int* start, uint32_t* occ_seed) {
     Vec* v = vec_of(envs);
     if (i < 0 || i >= v->n) return -1;
@@ -1084,6 +1145,7 @@ const char* sbx_scenario_path(Env* envs, int s) {
 
 struct PlanHolder {
     sbh::SolvePlan plan;
+    sbh::RelaxPlan relax;
 };
 static std::map<const void*, PlanHolder*> g_plans;
 
@@ -1109,9 +1171,7 @@ int sbx_plan_layout(const char* blob_path, int width, SbxPlan* out) {
     out->kmax = sbh::kPlanKmax;
     out->n_hdr = (int)P.hdr.size();
     out->n_words = (int)P.words.size();
-    out->n_rows = 0;
     out->pass_info = reinterpret_cast<const int*>(P.passes.data());
-    out->row_off = nullptr;
     out->hdr = P.hdr.data();
     out->words = P.words.data();
     out->slot_init = P.slot_init.data();
@@ -1119,6 +1179,19 @@ int sbx_plan_layout(const char* blob_path, int width, SbxPlan* out) {
     out->air_slot = P.air_slot.data();
     out->air_node = P.air_node.data();
     out->k = P.k;
+    sbh::build_relax(b, P, &h->relax);
+    const sbh::RelaxPlan& R = h->relax;
+    out->rx_ok = R.ok ? 1 : 0;
+    out->rx_rows = sbh::kRelaxRows;
+    out->rx_terms_max = sbh::kRelaxTerms;
+    out->rx_terms = R.terms;
+    out->rx_rho = R.rho;
+    if (R.ok) {
+        out->rx_diag = R.diag.data();
+        out->rx_air = R.air_col.data();
+        out->rx_val = R.val.data();
+        out->rx_col = R.col.data();
+    }
     g_plans[out->hdr] = h;
     return 0;
 }

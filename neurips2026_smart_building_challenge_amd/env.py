@@ -61,19 +61,24 @@ class SbxPlan(ctypes.Structure):
                 ("vec_base", ctypes.c_int), ("inv_base", ctypes.c_int), ("n_pass", ctypes.c_int),
                 ("n_levels", ctypes.c_int),
                 ("n_tasks", ctypes.c_int), ("kmax", ctypes.c_int), ("n_pairs", ctypes.c_longlong),
-                ("n_hdr", ctypes.c_int), ("n_words", ctypes.c_int), ("n_rows", ctypes.c_int),
-                ("pass_info", ctypes.POINTER(ctypes.c_int)), ("row_off", ctypes.POINTER(ctypes.c_int)),
+                ("n_hdr", ctypes.c_int), ("n_words", ctypes.c_int),
+                ("pass_info", ctypes.POINTER(ctypes.c_int)),
                 ("hdr", ctypes.POINTER(ctypes.c_uint64)), ("words", ctypes.POINTER(ctypes.c_uint32)),
                 ("slot_init", ctypes.POINTER(ctypes.c_double)), ("pos", ctypes.POINTER(ctypes.c_int)),
                 ("air_slot", ctypes.POINTER(ctypes.c_int)), ("air_node", ctypes.POINTER(ctypes.c_int)),
-                ("k", ctypes.c_int)]
+                ("k", ctypes.c_int),
+                ("rx_ok", ctypes.c_int), ("rx_rows", ctypes.c_int), ("rx_terms_max", ctypes.c_int),
+                ("rx_terms", ctypes.c_int), ("rx_rho", ctypes.c_double),
+                ("rx_diag", ctypes.POINTER(ctypes.c_double)), ("rx_air", ctypes.POINTER(ctypes.c_int)),
+                ("rx_val", ctypes.POINTER(ctypes.c_double)), ("rx_col", ctypes.POINTER(ctypes.c_int))]
 
 
 # every symbol include/sbenv.h declares
 EXPORTS = [
     "dict_find", "dict_set", "puf_vec_create", "puf_bind_stream", "puf_init", "puf_reset", "puf_step",
     "puf_render", "puf_close", "puf_log", "puf_live_log", "puf_mask_init", "sbx_gen_actions",
-    "sbx_vec_info", "sbx_env_state", "sbx_time_step", "sbx_phase_times", "sbx_pass_times", "sbx_env_meta", "sbx_scenario_path",
+    "sbx_vec_info", "sbx_env_state", "sbx_time_step", "sbx_phase_times", "sbx_pass_times", "sbx_solve_info",
+    "sbx_env_meta", "sbx_scenario_path",
     "sbx_plan_layout", "sbx_plan_free", "sbx_last_error", "sbx_version",
 ]
 
@@ -110,6 +115,8 @@ def lib() -> ctypes.CDLL:
         L.sbx_phase_times.restype = ctypes.c_int
         L.sbx_pass_times.argtypes = [ctypes.POINTER(Env), ctypes.c_int, P, ctypes.c_int]
         L.sbx_pass_times.restype = ctypes.c_int
+        L.sbx_solve_info.argtypes = [ctypes.POINTER(Env), ctypes.c_int, P]
+        L.sbx_solve_info.restype = ctypes.c_int
         L.sbx_env_meta.argtypes = [ctypes.POINTER(Env), ctypes.c_int, ctypes.POINTER(ctypes.c_int),
                                    ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_uint32)]
         L.sbx_scenario_path.argtypes = [ctypes.POINTER(Env), ctypes.c_int]
@@ -172,7 +179,14 @@ def plan_layout(blob: str | Path, width: int = 64) -> dict[str, np.ndarray]:
             "pos": arr(p.pos, p.n),
             "air_slot": arr(p.air_slot, p.k).astype(np.int64),
             "air_node": arr(p.air_node, p.k).astype(np.int64),
+            "rx_ok": bool(p.rx_ok), "rx_rho": p.rx_rho, "rx_terms": p.rx_terms, "rx_rows": p.rx_rows,
         }
+        if p.rx_ok:
+            rows, tm = p.rx_rows, p.rx_terms_max
+            out["rx_diag"] = arr(p.rx_diag, rows)
+            out["rx_air"] = arr(p.rx_air, rows).astype(np.int64)
+            out["rx_val"] = arr(p.rx_val, tm * rows).reshape(tm, rows)
+            out["rx_col"] = arr(p.rx_col, tm * rows).reshape(tm, rows).astype(np.int64)
     finally:
         L.sbx_plan_free(ctypes.byref(p))
     return out
@@ -225,6 +239,14 @@ class VecEnv:
         s, st, sd = ctypes.c_int(), ctypes.c_int(), ctypes.c_uint32()
         self.L.sbx_env_meta(self.envs, i, ctypes.byref(s), ctypes.byref(st), ctypes.byref(sd))
         return self.L.sbx_scenario_path(self.envs, s.value).decode(), st.value, sd.value
+
+    def solve_info(self, i: int) -> dict[str, float]:
+        """Field solver of env i: kind ("lu"/"relax"), rho, sweeps of the last step, capped steps."""
+        out = np.zeros(4, np.float64)
+        if self.L.sbx_solve_info(self.envs, i, out.ctypes.data_as(P)) != 4:
+            raise RuntimeError("sbx_solve_info failed")
+        return {"solver": "relax" if out[0] == 1.0 else "lu", "rho": float(out[1]),
+                "sweeps": int(out[2]), "capped": int(out[3])}
 
     def log(self, i: int) -> dict[str, float]:
         items = (DictItem * 8)()

@@ -11,9 +11,12 @@ Bars (from the hot-path contract):
     float32 step of the raw value divided by the normalizer's sigma, plus one
     float32 step of the result.
 
-The GPU solves (A + P G S) y = b + P G T_air by refactorization while csim
-replays fixed factors and a dense k x k correction (sb_fdm.c:153-181); the two
-agree to round-off, hence tolerances on physics and exactness elsewhere.
+The GPU solves (A + P G S) y = b + P G T_air either by refactorization (the
+"lu" solver) or by Jacobi sweeps stopped at a certified error bound of 1e-13 of
+the largest temperature (the "relax" solver, chosen by default where the host
+certifies it), while csim replays fixed factors and a dense k x k correction
+(sb_fdm.c:153-181); they agree to round-off or to that bound, hence tolerances
+on physics and exactness elsewhere. The physics tests run under both solvers.
 """
 from __future__ import annotations
 
@@ -174,19 +177,35 @@ def _run_parity(vec, twins, steps, label):
             assert bad.size == 0, f"{where}: exact state fields differ at {bad[:8]}"
 
 
-def test_gpu_step_parity_mixed_layouts(mixed_dir):
+def check_solver(vec, solver):
+    """Every env runs the requested solver; relaxation never hit its sweep cap."""
+    for i in range(vec.n):
+        info = vec.solve_info(i)
+        assert info["solver"] == solver, (i, info)
+        assert info["capped"] == 0, (i, info)
+        if solver == "relax":
+            assert 0.0 < info["rho"] <= 0.5 and 1 <= info["sweeps"] < 64, (i, info)
+
+
+SOLVERS = ["relax", "lu"]
+
+
+@pytest.mark.parametrize("solver", SOLVERS)
+def test_gpu_step_parity_mixed_layouts(mixed_dir, solver):
     """30 scenarios (6 layouts x 5 climates), episodes of 60 steps, 130 steps (two auto-resets)."""
-    say("parity: 30 envs, one per scenario, 130 steps")
-    vec = E.VecEnv(30, blob_dir=str(mixed_dir), groups=30, max_steps=60)
+    say(f"parity ({solver}): 30 envs, one per scenario, 130 steps")
+    vec = E.VecEnv(30, blob_dir=str(mixed_dir), groups=30, max_steps=60, solver=solver)
     twins = [Twin(vec, i, 60) for i in range(vec.n)]
     _run_parity(vec, twins, 130, "mixed")
+    check_solver(vec, solver)
     vec.close()
 
 
-def test_gpu_step_parity_desync(mixed_dir):
+@pytest.mark.parametrize("solver", SOLVERS)
+def test_gpu_step_parity_desync(mixed_dir, solver):
     """Desynchronised calendar starts: every env at its own seeded offset."""
-    say("parity: 60 envs, desync, 90 steps")
-    vec = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=40, desync=1, desync_seed=99)
+    say(f"parity ({solver}): 60 envs, desync, 90 steps")
+    vec = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=40, desync=1, desync_seed=99, solver=solver)
     starts = {vec.meta(i)[1] for i in range(vec.n)}
     assert len(starts) > 40
     twins = [Twin(vec, i, 40) for i in range(0, vec.n, 3)]
@@ -217,14 +236,15 @@ def test_gpu_occupancy_exact(mixed_dir):
     vec.close()
 
 
-def test_gpu_episode_total_vs_reference(golden_index, tmp_path):
+@pytest.mark.parametrize("solver", SOLVERS)
+def test_gpu_episode_total_vs_reference(golden_index, tmp_path, solver):
     """Full 8,640-step episode of the 41-zone config: f64 reward total within 1e-6 relative of
     both the oracle and the reference csim core (golden fixture), final state within 1e-9."""
     case = golden_index["cases"]["cfg0_episode"]
     path, sha = golden_blob(case["layout"], case["climate"], tmp_path)
     assert sha == case["blob_sha256"]
-    say("episode: 1 env, 8640 steps")
-    vec = E.VecEnv(1, blob=str(path), max_steps=8640)
+    say(f"episode ({solver}): 1 env, 8640 steps")
+    vec = E.VecEnv(1, blob=str(path), max_steps=8640, solver=solver)
     vec.reset()
     seed = golden_index["action_seed"]
     for s in range(8640):
@@ -247,15 +267,17 @@ def test_gpu_episode_total_vs_reference(golden_index, tmp_path):
     fx = np.load(str(__import__("pathlib").Path(__file__).parent / "golden" / "cfg0_episode.npz"))
     obs = host(vec.obs)[0]
     assert np.array_equal(obs[:case["obs_len"]].view(np.uint32), fx["obs_8640"].view(np.uint32))
+    check_solver(vec, solver)
     vec.close()
 
 
-def test_gpu_batch_invariance(mixed_dir):
+@pytest.mark.parametrize("solver", SOLVERS)
+def test_gpu_batch_invariance(mixed_dir, solver):
     """An env steps bit-identically alone and inside a 60-env mixed batch."""
-    say("batch invariance")
-    big = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=50)
+    say(f"batch invariance ({solver})")
+    big = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=50, solver=solver)
     path, _, _ = big.meta(0)
-    small = E.VecEnv(1, blob=path, max_steps=50)
+    small = E.VecEnv(1, blob=path, max_steps=50, solver=solver)
     big.reset()
     small.reset()
     for s in range(70):

@@ -104,3 +104,88 @@ def test_plan_rejects_unsupported(tmp_path):
     _rewrite(p, bad2, lu_L_indptr=Lp2, lu_L_indices=Li[keep], lu_L_data=Lx[keep])
     with pytest.raises(ValueError):
         E.plan_layout(bad2, 64)
+
+
+def relax_solve(pl, g, b, x0, tol=1e-13, cap=64):
+    """The kernel's relaxation solve in numpy: Jacobi sweeps over the exported
+    ELL rows, stopped by rho / (1 - rho) * max|x_m - x_m-1| <= tol * max|x0|."""
+    n = pl["n"]
+    d = pl["rx_diag"][:n].copy()
+    bb = b.copy()
+    air = pl["rx_air"][:n]
+    m = air >= 0
+    d[m] += g[air[m]]
+    val, col = pl["rx_val"][:, :n], pl["rx_col"][:, :n]
+    stop = pl["rx_rho"] / (1.0 - pl["rx_rho"])
+    atol = tol * np.max(np.abs(x0))
+    x = x0.copy()
+    for it in range(1, cap + 1):
+        xn = (bb - (val * x[col]).sum(0)) / d
+        delta = np.max(np.abs(xn - x))
+        x = xn
+        if stop * delta <= atol:
+            return x, it, stop * delta
+    return x, cap, stop * delta
+
+
+@pytest.mark.parametrize("zones,ahus", G.LAYOUTS)
+def test_relax_tables_and_bound(zones, ahus, tmp_path):
+    """The ELL tables rebuild A exactly; rho is A's row dominance ratio; the sweep
+    with the kernel's stopping rule lands within its own certified bound of the
+    exact solution of A + diag(g) for g = 0 and random g >= 0."""
+    import scipy.sparse as sp
+
+    p, _ = golden_blob((zones, ahus), (10.0, 8.0, 499), tmp_path)
+    pl = E.plan_layout(p, 64)
+    assert pl["rx_ok"]
+    d = read_sbb(p)
+    n = pl["n"]
+    A = sp.csc_matrix((d["A_system_data"], d["A_system_indices"], d["A_system_indptr"]), shape=(n, n)).toarray()
+    R = np.zeros((n, n))
+    val, col = pl["rx_val"][:, :n], pl["rx_col"][:, :n]
+    for m in range(val.shape[0]):
+        np.add.at(R, (np.arange(n), col[m]), val[m])
+    R[np.arange(n), np.arange(n)] += pl["rx_diag"][:n]
+    assert np.array_equal(R, A)
+    assert np.all(pl["rx_val"][:, n:] == 0.0) and np.all(pl["rx_diag"][n:] == 1.0)
+    off = np.abs(A).sum(1) - np.abs(np.diag(A))
+    assert pl["rx_rho"] == pytest.approx(np.max(off / np.diag(A)), rel=1e-14)
+    assert pl["rx_rho"] <= 0.5
+    assert np.array_equal(np.flatnonzero(pl["rx_air"][:n] >= 0), np.sort(pl["air_node"]))
+    assert np.array_equal(pl["rx_air"][pl["air_node"]], np.arange(pl["k"]))
+    rng = np.random.default_rng(zones + 1)
+    for trial in range(4):
+        g = rng.uniform(0.0, 900.0, pl["k"]) if trial else np.zeros(pl["k"])
+        Ag = A.copy()
+        Ag[pl["air_node"], pl["air_node"]] += g
+        xt = rng.uniform(280.0, 310.0, n)
+        b = Ag @ xt
+        x0 = xt + rng.normal(size=n) * (5.0 if trial < 2 else 50.0)
+        x, it, bound = relax_solve(pl, g, b, x0)
+        exact = np.linalg.solve(Ag, b)
+        err = np.max(np.abs(x - exact))
+        assert it < 64
+        assert err <= bound + 1e-12 * np.max(np.abs(exact))
+        assert err <= 1e-10 * np.max(np.abs(exact))
+
+
+def test_relax_rejects_weak_dominance(tmp_path):
+    """Scaling the diagonal down until rho > 1/2 must turn the relaxation form off
+    (the kernel then runs the LU plan), and the reason must say why."""
+    import scipy.sparse as sp
+
+    p, _ = golden_blob((41, 1), (10.0, 8.0, 499), tmp_path)
+    d = read_sbb(p)
+    n = d["solved"].size
+    A = sp.csc_matrix((d["A_system_data"], d["A_system_indices"], d["A_system_indptr"]), shape=(n, n))
+    off = np.asarray(abs(A).sum(1)).ravel() - np.abs(A.diagonal())
+    x = d["A_system_data"].copy()
+    for c in range(n):
+        for q in range(d["A_system_indptr"][c], d["A_system_indptr"][c + 1]):
+            if d["A_system_indices"][q] == c:
+                x[q] = off[c] * 1.5          # rho = 2/3 in every row
+    bad = tmp_path / "weak.sbb"
+    _rewrite(p, bad, A_system_data=x)
+    pl = E.plan_layout(bad, 64)
+    assert not pl["rx_ok"]
+    assert pl["rx_rho"] == pytest.approx(2.0 / 3.0)
