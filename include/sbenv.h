@@ -129,11 +129,12 @@ typedef struct SbxVecInfo {
     int n_envs;
     int n_layouts;
     int n_scenarios;
-    int block;              /* threads per env workgroup */
+    int block;              /* threads per workgroup (64 per env) */
     int lds_bytes;          /* dynamic LDS per workgroup */
     int max_nodes;
     double bytes_per_step;  /* algorithmic HBM bytes of one puf_step (all envs) */
     double flops_per_step;  /* fp64 flops of one puf_step's solves (all envs) */
+    int envs_per_block;     /* envs sharing a workgroup (one wavefront each) */
 } SbxVecInfo;
 void sbx_vec_info(Env* envs, SbxVecInfo* out);
 
@@ -155,6 +156,11 @@ float sbx_time_step(Env* envs, int iters);
  * duration over workgroups in microseconds. Advances the envs by one step and
  * synchronises. Returns the number of phases written. */
 int sbx_phase_times(Env* envs, double* mean_us, double* max_us, int n_phases);
+
+/* Runs one step and copies the raw wall-clock stamps of every env (SBK_NSTAMP
+ * = 16 per env, env-major; the phases above are stamps 0..12, unused stamps
+ * read 0). Returns the number written, or -1 when cap is below 16 * n. */
+int sbx_phase_stamps(Env* envs, unsigned long long* out, int cap);
 
 /* Runs one step recording the shader-clock duration of every solve pass of
  * env `env`'s workgroup (for a layout on the relaxation solver: the setup,

@@ -54,24 +54,84 @@ enum { SOLVER_LU = 0, SOLVER_RELAX = 1 };
 enum { PI_HWS_RUN = 0, PI_PUMP_RUN, PI_HWS_REQ, PI_STEP_INDEX, PI_STEP, PI_MT_IDX,
        PI_STEPS_TOTAL, PI_EPISODES };
 
-// LDS carve-up (byte offsets from the dynamic shared base).
+// Per-env LDS region (byte offsets from the env's base; a workgroup holds the
+// layout image first, then one region per env).
 struct LdsLayout {
     int state;        // state image (StateLayout offsets are relative to this)
-    int slots;        // f64[n_slots]: 0 zero, 1 sink, LU entries, vector
-    int mt;           // u32[625]; aliases the slot region (used after the solve)
+    int mt;           // u32[624] MT19937 words (staged with the record, which they follow)
+    int scen;         // scenario image (ScenImg offsets are relative to this)
+    int act;          // f32[SB_ACT] action row of the step
+    int slots;        // f64[n_slots]: 0 zero, 1 sink, LU entries, vector (relaxation: node heat)
     int zq;           // f64[nz] zone heat / zone mean temperature
     int vtmp;         // f64[3 * nv]: unrestricted flow, flow demand, reheat energy
     int g;            // f64[k] air-side conductance
     int tair;         // f64[k] supply air temperature
     int atmp;         // f64[8 * na]: wsum, atotal, satv, demand, fd sum, count
     int red;          // f64[64] reduction scratch
-    int misc;         // f64[32] scalars
+    int misc;         // f64[MS_SIZE] scalars
+    int obsx;         // f64[OX_AHU + 4 * na] per-step values the observation reads (OX_*)
     int iscr;         // i32[W + 8] scan scratch
     int prec;         // int4[n_pass] solve pass records (copied at kernel start)
-    int bytes;
+    int bytes;        // region size, 16-byte multiple
 };
 
-enum { MS_FFS = 0, MS_TOTAL_REHEAT, MS_TF, MS_REWARD, MS_COMFORT, MS_AMB };
+// Layout image: every per-layout table the step reads, packed (16-byte aligned
+// sections) so a workgroup copies it to LDS in one burst and its envs share it.
+struct ImgLayout {
+    int bytes;        // 16-byte multiple
+    // f64
+    int cap, mcoup, mret, mgain, solar_c, rx_diag;          // [n]
+    int zone_area;                                          // [nz]
+    int vav_area;                                           // [nv]
+    int vav_c, ahu_c;                                       // [9 nv], [9 na]
+    int act_mn, act_mx, act_mnr, act_mxr, act_hi;           // [n_act]
+    int f_mean, f_sd;                                       // [n_dev]
+    int f_src;                                              // u32 [n_dev], OBS_SRC_*
+    // i32
+    int rx_air, pos;                                        // [n]
+    int zone_cell_off, zone_cells, vz_off, vz_idx, vav_ahu, coupled, zone_col_off, zone_cols;
+    int act_src, act_dst, act_aux;                          // [n_act] (dst/aux: ACT_*)
+    int air_slot, air_node;                                 // [k]
+    // u8
+    int is_room;                                            // [n]
+    int act_disc, act_flags;                                // [n_act]
+};
+
+// Scenario image: per-scenario tables the step reads, staged per env.
+struct ScenImg {
+    int bytes;        // 16-byte multiple
+    int dirx;         // f64[n] dirichlet + exposure(h)
+    int elec_wk, elec_we, elec_co2;   // f64[24]
+    int gas_price;    // f64[12]
+};
+
+// misc scratch (f64[48]): step scalars, then the step's calendar values (rows
+// kk = the index before the step and j = kk + 1; RW_* offsets from MS_ROW),
+// then the aux-time row j (MS_AUX, n_aux - 1 values)
+enum { MS_FFS = 0, MS_TOTAL_REHEAT, MS_TF, MS_REWARD, MS_COMFORT, MS_AMB, MS_CMIN, MS_CMAX,
+       MS_ROW = 8, MS_AUX = 24, MS_SIZE = 48 };
+// Observation field source, resolved on the host: a value at a byte offset of
+// the env's LDS region (state image, obsx values) or of the layout image.
+#define OBS_SRC_IMG (1u << 31)   // offset into the layout image (else the env region)
+#define OBS_SRC_I32 (1u << 30)   // int32 value (else f64)
+#define OBS_SRC_OFF 0x3FFFFFFFu
+// Action target, resolved on the host (sb_sim.c:220-244 actuator routing): the
+// decoded value goes to a byte offset of the env's state image as f64, or as
+// int32 (value == 1) when ACT_I32; the aux word optionally also sets a u8 flag
+// to 1 (ACT_AUX_U8) or stores the same int32 (ACT_AUX_I32) at its offset.
+#define ACT_I32 (1u << 31)
+#define ACT_AUX_U8 (1u << 31)
+#define ACT_AUX_I32 (1u << 30)
+#define ACT_OFF 0x3FFFFFFFu
+// act_flags: clamp to [0, act_hi]; divide by the pump head's bar -> m factor
+enum { ACT_CLAMP = 1, ACT_PUMP_HEAD = 2 };
+
+// obsx: ambient of the observed row, pump differential pressure, then per AHU
+// a at OX_AHU + 4a: static pressure, delivered flow, flow fraction, outside-air flow
+enum { OX_AMB = 0, OX_DP = 1, OX_AHU = 2 };
+
+enum { RW_AMB_K = 0, RW_SOLAR_K, RW_COMF_K, RW_COMF_KM1, RW_HSP_K, RW_CSP_K, RW_AMB_J, RW_HSP_J, RW_CSP_J,
+       RW_OCC_HOUR_J, RW_OCC_WORK_J, RW_REW_HOUR_J, RW_REW_MONTH_J, RW_REW_WORK_J, RW_COUNT };
 
 // One layout (building structure): solve plan + HVAC topology + constant tables.
 struct DevLayout {
@@ -83,6 +143,8 @@ struct DevLayout {
     double rx_stop;                    // rho / (1 - rho)
     StateLayout st;
     LdsLayout lds;
+    ImgLayout img;
+    const SBK_C unsigned char* img_src;   // the layout image in HBM
     // relaxation tables, rows padded to SBK_RX_ROWS
     const SBK_C double* rx_diag;       // [SBK_RX_ROWS]
     const SBK_C int* rx_air;           // [SBK_RX_ROWS] air-side column or -1
@@ -141,6 +203,8 @@ struct DevLayout {
 struct DevScen {
     int layout;
     int n1;                      // calendar rows
+    ScenImg img;
+    const SBK_C unsigned char* img_src;   // the scenario image in HBM
     const SBK_C double* amb;
     const SBK_C double* solar_i;
     const SBK_C double* comfort;
@@ -182,9 +246,15 @@ struct EnvDesc {
 
 enum { KMODE_STEP = 0, KMODE_RESET = 1 };
 
+// A workgroup's envs: order[first .. first + count) all of one layout.
+struct Tile {
+    int layout, first, count, pad;
+};
+
 struct KParams {
     const SBK_C EnvDesc* envs;
-    const SBK_C int* order;      // block -> env
+    const SBK_C int* order;      // tile slot -> env
+    const SBK_C Tile* tiles;     // block -> tile
     const SBK_C DevLayout* layouts;
     const SBK_C DevScen* scens;
     unsigned char* state;
@@ -198,9 +268,10 @@ struct KParams {
     int n_envs;
     int mode;
     float reward_scale;
-    unsigned long long* phase_ts;   // null, or [n_blocks * SBK_NSTAMP] wall-clock stamps
-    unsigned long long* pass_ts;    // null, or [n_pass + 1] shader-clock stamps of one workgroup
-    int pass_ts_block;              // workgroup whose solve passes are stamped
+    int img_lds;                 // LDS bytes reserved for the layout image (max over layouts)
+    unsigned long long* phase_ts;   // null, or [n_envs * SBK_NSTAMP] wall-clock stamps
+    unsigned long long* pass_ts;    // null, or [n_pass + 1] shader-clock stamps of one env
+    int pass_ts_env;                // env whose solve passes are stamped
 };
 
 }  // namespace sbk

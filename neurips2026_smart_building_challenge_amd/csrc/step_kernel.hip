@@ -32,132 +32,148 @@ namespace sbk {
 
 enum { M_OFF = 0, M_HEAT = 1, M_COOL = 2, M_PASSIVE = 3 };
 
-// Phase stamp (wall clock, written by lane 0 only when phase timing is on).
+// Phase stamp of env c.e (wall clock, written by its lane 0 when phase timing is on).
 #define STAMP(i)                                                                        \
     do {                                                                                \
-        if (P.phase_ts && threadIdx.x == 0)                                             \
-            P.phase_ts[(size_t)blockIdx.x * SBK_NSTAMP + (i)] = wall_clock64();        \
+        if (P.phase_ts && (threadIdx.x & 63) == 0)                                      \
+            P.phase_ts[(size_t)c.e * SBK_NSTAMP + (i)] = wall_clock64();                \
     } while (0)
 
+// Orders this wave's LDS accesses before and after the point (the wave's DS
+// operations complete in issue order) without waiting for global loads, so
+// the next pass's term words stay in flight across the synchronisation.
+__device__ __forceinline__ void wave_lds_sync() {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0), vmcnt/expcnt untouched
+    __builtin_amdgcn_wave_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// Lane of the calling thread within its env's wavefront (a workgroup holds one
+// wavefront per env).
+__device__ __forceinline__ int ln() { return (int)(threadIdx.x & 63); }
+
+// Synchronisation point of one env: its wavefront's LDS writes before this
+// point are visible to its LDS reads after it.
+__device__ __forceinline__ void esync() { wave_lds_sync(); }
+
+// Wavefront reductions and scans on DPP lane moves (no LDS traffic). Every
+// lane of the wavefront must be active. The combination order is fixed:
+// pairs, quads, halves of a row, rows of 16 (quad_perm, row_half_mirror,
+// row_mirror), then rows 0+1 and 2+3 (row_bcast:15), then the two halves
+// (row_bcast:31); lane 63 ends with the total and is broadcast.
+enum {
+    DPP_QUAD_1032 = 0xB1,       // quad_perm [1,0,3,2]
+    DPP_QUAD_2301 = 0x4E,       // quad_perm [2,3,0,1]
+    DPP_ROW_SHR = 0x110,        // + 1..15
+    DPP_ROW_MIRROR = 0x140,
+    DPP_ROW_HALF_MIRROR = 0x141,
+    DPP_ROW_BCAST15 = 0x142,
+    DPP_ROW_BCAST31 = 0x143,
+};
+
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ int dpp_i(int old, int v) {
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROWS, 0xF, false);
+}
+
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ double dpp_d(double old, double v) {
+    const unsigned long long o = __double_as_longlong(old), x = __double_as_longlong(v);
+    const int lo = dpp_i<CTRL, ROWS>((int)(unsigned)o, (int)(unsigned)x);
+    const int hi = dpp_i<CTRL, ROWS>((int)(unsigned)(o >> 32), (int)(unsigned)(x >> 32));
+    return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}
+
+__device__ __forceinline__ double lane63_d(double v) {
+    const unsigned long long x = __double_as_longlong(v);
+    const unsigned lo = __builtin_amdgcn_readlane((int)(unsigned)x, 63);
+    const unsigned hi = __builtin_amdgcn_readlane((int)(unsigned)(x >> 32), 63);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+template <class Op>
+__device__ __forceinline__ double wave_reduce(double v, double ident, Op op) {
+    v = op(v, dpp_d<DPP_QUAD_1032>(ident, v));
+    v = op(v, dpp_d<DPP_QUAD_2301>(ident, v));
+    v = op(v, dpp_d<DPP_ROW_HALF_MIRROR>(ident, v));
+    v = op(v, dpp_d<DPP_ROW_MIRROR>(ident, v));
+    v = op(v, dpp_d<DPP_ROW_BCAST15, 0xA>(ident, v));
+    v = op(v, dpp_d<DPP_ROW_BCAST31, 0xC>(ident, v));
+    return lane63_d(v);
+}
+
 __device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
+    return wave_reduce(v, 0.0, [](double a, double b) { return a + b; });
 }
 
 __device__ __forceinline__ double wave_min(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmin(v, __shfl_xor(v, off, 64));
-    return v;
+    return wave_reduce(v, __longlong_as_double(0x7FF0000000000000ll), [](double a, double b) { return fmin(a, b); });
 }
 
 __device__ __forceinline__ double wave_max(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmax(v, __shfl_xor(v, off, 64));
-    return v;
+    return wave_reduce(v, __longlong_as_double((long long)0xFFF0000000000000ull), [](double a, double b) { return fmax(a, b); });
 }
 
 __device__ __forceinline__ int wave_isum(int v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    v += dpp_i<DPP_QUAD_1032>(0, v);
+    v += dpp_i<DPP_QUAD_2301>(0, v);
+    v += dpp_i<DPP_ROW_HALF_MIRROR>(0, v);
+    v += dpp_i<DPP_ROW_MIRROR>(0, v);
+    v += dpp_i<DPP_ROW_BCAST15, 0xA>(0, v);
+    v += dpp_i<DPP_ROW_BCAST31, 0xC>(0, v);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+// Inclusive prefix sum over the wavefront.
+__device__ __forceinline__ int wave_iscan(int v) {
+    v += dpp_i<DPP_ROW_SHR + 1>(0, v);
+    v += dpp_i<DPP_ROW_SHR + 2>(0, v);
+    v += dpp_i<DPP_ROW_SHR + 4>(0, v);
+    v += dpp_i<DPP_ROW_SHR + 8>(0, v);
+    v += dpp_i<DPP_ROW_BCAST15, 0xA>(0, v);
+    v += dpp_i<DPP_ROW_BCAST31, 0xC>(0, v);
     return v;
 }
 
-// Block-wide reductions; every lane receives the same value. The combination
-// order is fixed, so results are deterministic.
+// Env-wide reductions (one wavefront per env); every lane receives the value.
 template <int W>
-__device__ __forceinline__ double bsum(double v, double* red) {
-    v = wave_sum(v);
-    if constexpr (W == 64) {
-        return v;
-    } else {
-        __syncthreads();
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-        __syncthreads();
-        double s = red[0];
-#pragma unroll
-        for (int i = 1; i < W / 64; i++) s += red[i];
-        return s;
-    }
-}
+__device__ __forceinline__ double bsum(double v, double*) { return wave_sum(v); }
 
 template <int W>
-__device__ __forceinline__ double bmin(double v, double* red) {
-    v = wave_min(v);
-    if constexpr (W == 64) {
-        return v;
-    } else {
-        __syncthreads();
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-        __syncthreads();
-        double s = red[0];
-#pragma unroll
-        for (int i = 1; i < W / 64; i++) s = fmin(s, red[i]);
-        return s;
-    }
-}
+__device__ __forceinline__ double bmin(double v, double*) { return wave_min(v); }
 
 template <int W>
-__device__ __forceinline__ double bmax(double v, double* red) {
-    v = wave_max(v);
-    if constexpr (W == 64) {
-        return v;
-    } else {
-        __syncthreads();
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-        __syncthreads();
-        double s = red[0];
-#pragma unroll
-        for (int i = 1; i < W / 64; i++) s = fmax(s, red[i]);
-        return s;
-    }
-}
+__device__ __forceinline__ double bmax(double v, double*) { return wave_max(v); }
 
 template <int W>
-__device__ __forceinline__ int bisum(int v, double* red) {
-    v = wave_isum(v);
-    if constexpr (W == 64) {
-        return v;
-    } else {
-        int* r = reinterpret_cast<int*>(red);
-        __syncthreads();
-        if ((threadIdx.x & 63) == 0) r[threadIdx.x >> 6] = v;
-        __syncthreads();
-        int s = 0;
-#pragma unroll
-        for (int i = 0; i < W / 64; i++) s += r[i];
-        return s;
-    }
-}
+__device__ __forceinline__ int bisum(int v, double*) { return wave_isum(v); }
 
-// Block exclusive prefix sum of an int per lane; returns the prefix, *total
+// Exclusive prefix sum of an int per lane over the env's wavefront; *total
 // receives the sum.
 template <int W>
-__device__ __forceinline__ int bscan(int v, int* scr, int* total) {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    int inc = v;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        int t = __shfl_up(inc, off, 64);
-        if (lane >= off) inc += t;
-    }
-    __syncthreads();
-    if (lane == 63) scr[w] = inc;
-    __syncthreads();
-    int base = 0, tot = 0;
-#pragma unroll
-    for (int i = 0; i < W / 64; i++) {
-        if (i < w) base += scr[i];
-        tot += scr[i];
-    }
-    *total = tot;
-    return base + inc - v;
+__device__ __forceinline__ int bscan(int v, int*, int* total) {
+    const int inc = wave_iscan(v);
+    *total = __builtin_amdgcn_readlane(inc, 63);
+    return inc - v;
 }
+
+// Layout tables in the staged LDS image (shared by the envs of a workgroup).
+struct Tab {
+    const double *cap, *mcoup, *mret, *mgain, *solar_c, *rx_diag, *zone_area, *vav_area, *vav_c, *ahu_c;
+    const double *act_mn, *act_mx, *act_mnr, *act_mxr, *act_hi, *f_mean, *f_sd;
+    const int *rx_air, *pos, *zone_cell_off, *zone_cells, *vz_off, *vz_idx, *vav_ahu, *coupled;
+    const int *zone_col_off, *zone_cols, *act_src, *air_slot, *air_node;
+    const uint32_t *f_src, *act_dst, *act_aux;
+    const uint8_t *is_room, *act_disc, *act_flags;
+};
 
 struct Ctx {
     const SBK_C DevLayout* L;
     const SBK_C DevScen* S;
+    int e;                   // env index
     unsigned char* rec;      // HBM record of this env
+    Tab t;
     double *T, *M, *damper, *reheat, *ratio, *heatsp, *coolsp, *dcmd, *rcmd, *sensing;
     double *recirc, *sat, *fan, *flow, *plant;
     int *run, *coolreq, *ip;
@@ -167,11 +183,59 @@ struct Ctx {
     uint32_t* mt;
     int* iscr;
     unsigned char* prec;     // LDS copy of the solve pass records
+    const float* act;        // the step's action row (LDS)
+    const unsigned char* imgb;   // layout image (LDS)
+    unsigned char* envb;         // this env's LDS region
+    double* obsx;                // per-step values the observation reads (OX_*)
+    const double *dirx, *elec_wk, *elec_we, *elec_co2, *gas_price;   // scenario image (LDS)
 };
 
-__device__ __forceinline__ void bind(Ctx& c, unsigned char* lds) {
+// img: the workgroup's layout image; env: this env's LDS region.
+__device__ __forceinline__ void bind(Ctx& c, const unsigned char* img, unsigned char* env) {
     const SBK_C DevLayout* L = c.L;
-    unsigned char* s = lds + L->lds.state;
+    const ImgLayout g = L->img;
+    Tab& t = c.t;
+    t.cap = (const double*)(img + g.cap);
+    t.mcoup = (const double*)(img + g.mcoup);
+    t.mret = (const double*)(img + g.mret);
+    t.mgain = (const double*)(img + g.mgain);
+    t.solar_c = (const double*)(img + g.solar_c);
+    t.rx_diag = (const double*)(img + g.rx_diag);
+    t.zone_area = (const double*)(img + g.zone_area);
+    t.vav_area = (const double*)(img + g.vav_area);
+    t.vav_c = (const double*)(img + g.vav_c);
+    t.ahu_c = (const double*)(img + g.ahu_c);
+    t.act_mn = (const double*)(img + g.act_mn);
+    t.act_mx = (const double*)(img + g.act_mx);
+    t.act_mnr = (const double*)(img + g.act_mnr);
+    t.act_mxr = (const double*)(img + g.act_mxr);
+    t.act_hi = (const double*)(img + g.act_hi);
+    t.act_dst = (const uint32_t*)(img + g.act_dst);
+    t.act_aux = (const uint32_t*)(img + g.act_aux);
+    t.act_flags = img + g.act_flags;
+    t.f_mean = (const double*)(img + g.f_mean);
+    t.f_sd = (const double*)(img + g.f_sd);
+    t.rx_air = (const int*)(img + g.rx_air);
+    t.pos = (const int*)(img + g.pos);
+    t.zone_cell_off = (const int*)(img + g.zone_cell_off);
+    t.zone_cells = (const int*)(img + g.zone_cells);
+    t.vz_off = (const int*)(img + g.vz_off);
+    t.vz_idx = (const int*)(img + g.vz_idx);
+    t.vav_ahu = (const int*)(img + g.vav_ahu);
+    t.coupled = (const int*)(img + g.coupled);
+    t.zone_col_off = (const int*)(img + g.zone_col_off);
+    t.zone_cols = (const int*)(img + g.zone_cols);
+    t.act_src = (const int*)(img + g.act_src);
+    t.air_slot = (const int*)(img + g.air_slot);
+    t.air_node = (const int*)(img + g.air_node);
+    t.is_room = img + g.is_room;
+    t.act_disc = img + g.act_disc;
+    t.f_src = (const uint32_t*)(img + g.f_src);
+    c.imgb = img;
+    c.envb = env;
+    c.obsx = (double*)(env + L->lds.obsx);
+    const LdsLayout l = L->lds;
+    unsigned char* s = env + l.state;
     const StateLayout st = L->st;
     c.T = (double*)(s + st.T);
     c.M = (double*)(s + st.M);
@@ -197,37 +261,44 @@ __device__ __forceinline__ void bind(Ctx& c, unsigned char* lds) {
     c.rcmd_set = s + st.rcmd_set;
     c.occ_state = s + st.occ_state;
     c.occV = s + st.occV;
-    const LdsLayout l = L->lds;
-    c.slots = (double*)(lds + l.slots);
-    c.mt = (uint32_t*)(lds + l.mt);
-    c.zq = (double*)(lds + l.zq);
-    c.unres = (double*)(lds + l.vtmp);
+    c.mt = (uint32_t*)(env + l.mt);
+    const ScenImg si = c.S->img;
+    const unsigned char* sc = env + l.scen;
+    c.dirx = (const double*)(sc + si.dirx);
+    c.elec_wk = (const double*)(sc + si.elec_wk);
+    c.elec_we = (const double*)(sc + si.elec_we);
+    c.elec_co2 = (const double*)(sc + si.elec_co2);
+    c.gas_price = (const double*)(sc + si.gas_price);
+    c.act = (const float*)(env + l.act);
+    c.slots = (double*)(env + l.slots);
+    c.zq = (double*)(env + l.zq);
+    c.unres = (double*)(env + l.vtmp);
     c.fdem = c.unres + L->nv;
     c.rwen = c.fdem + L->nv;
-    c.g = (double*)(lds + l.g);
-    c.tair = (double*)(lds + l.tair);
-    double* a = (double*)(lds + l.atmp);
+    c.g = (double*)(env + l.g);
+    c.tair = (double*)(env + l.tair);
+    double* a = (double*)(env + l.atmp);
     c.wsum = a;
     c.atotal = a + L->na;
     c.satv = a + 2 * L->na;
     c.demand = a + 3 * L->na;
     c.fdsum = a + 4 * L->na;
-    c.red = (double*)(lds + l.red);
-    c.misc = (double*)(lds + l.misc);
-    c.iscr = (int*)(lds + l.iscr);
-    c.prec = lds + l.prec;
+    c.red = (double*)(env + l.red);
+    c.misc = (double*)(env + l.misc);
+    c.iscr = (int*)(env + l.iscr);
+    c.prec = env + l.prec;
 }
 
 // ------------------------------------------------------------------ helpers
 __device__ __forceinline__ double ahu_static(const Ctx& c, int a) {
     if (c.run[a] != 1) return 0.0;
-    double sp = c.fan[a], mn = c.L->ahu_c[a * 9 + 2];
+    double sp = c.fan[a], mn = c.t.ahu_c[a * 9 + 2];
     return sp > mn ? sp : mn;
 }
 
 __device__ __forceinline__ double vav_unrestricted(const Ctx& c, int v) {
-    const double* vc = c.L->vav_c + v * 9;
-    double d = c.damper[v] * vc[0] * sqrt(ahu_static(c, c.L->vav_ahu[v]) / vc[4]);
+    const double* vc = c.t.vav_c + v * 9;
+    double d = c.damper[v] * vc[0] * sqrt(ahu_static(c, c.t.vav_ahu[v]) / vc[4]);
     return d > 0.00001 ? d : 0.00001;
 }
 
@@ -250,10 +321,10 @@ __device__ __forceinline__ int default_mode(int cur, double zt, double hsp, doub
 template <int W>
 __device__ __forceinline__ void zone_means(Ctx& c, double* out) {
     const SBK_C DevLayout* L = c.L;
-    for (int z = threadIdx.x; z < L->nz; z += W) {
-        int a = L->zone_cell_off[z], b = L->zone_cell_off[z + 1];
+    for (int z = ln(); z < L->nz; z += W) {
+        int a = c.t.zone_cell_off[z], b = c.t.zone_cell_off[z + 1];
         double sum = 0.0;
-        for (int t = a; t < b; t++) sum += c.T[L->zone_cells[t]];
+        for (int t = a; t < b; t++) sum += c.T[c.t.zone_cells[t]];
         out[z] = sum / (double)(b - a);
     }
 }
@@ -262,71 +333,82 @@ __device__ __forceinline__ void zone_means(Ctx& c, double* out) {
 __device__ __forceinline__ double vav_temp(const Ctx& c, const double* zmean, int v, double* area_out) {
     const SBK_C DevLayout* L = c.L;
     double area = 0.0, wt = 0.0;
-    for (int t = L->vz_off[v]; t < L->vz_off[v + 1]; t++) {
-        int z = L->vz_idx[t];
-        area += L->zone_area[z];
-        wt += zmean[z] * L->zone_area[z];
+    for (int t = c.t.vz_off[v]; t < c.t.vz_off[v + 1]; t++) {
+        int z = c.t.vz_idx[t];
+        area += c.t.zone_area[z];
+        wt += zmean[z] * c.t.zone_area[z];
     }
     *area_out = area;
     return (area > 0.0) ? wt / area : 0.0;
 }
 
 // ------------------------------------------------------------------ observation
-__device__ __forceinline__ double obs_value(const Ctx& c, int kind, int idx, int id, int j) {
-    if (kind == 0) {
-        switch (id) {
-        case 0: return (double)c.coolreq[idx];
-        case 1: return ahu_static(c, idx);
-        case 2: return (c.run[idx] == 1) ? c.flow[idx] : 0.0;
-        case 3: return c.sat[idx];
-        case 4: return (double)c.run[idx];
-        case 5: return c.flow[idx] / c.L->ahu_c[idx * 9 + 1];
-        case 6: return (1.0 - c.recirc[idx]) * c.flow[idx];
-        case 7: return (double)c.run[idx];
-        case 8: return c.recirc[idx];
-        default: return c.S->amb[j];
-        }
+// Values the observation reads besides the state (sb_obs.c:49-64 device
+// fields): per AHU the static pressure, delivered flow, flow fraction and
+// outside-air flow; the pump differential pressure; the row's ambient.
+template <int W>
+__device__ __forceinline__ void obs_specials(Ctx& c, double amb) {
+#pragma clang fp contract(off)
+    const int l = ln();
+    double* ox = c.obsx;
+    if (l < c.L->na) {
+        const int a = l;
+        double* ax = ox + OX_AHU + 4 * a;
+        ax[0] = ahu_static(c, a);
+        ax[1] = (c.run[a] == 1) ? c.flow[a] : 0.0;
+        ax[2] = c.flow[a] / c.t.ahu_c[a * 9 + 1];
+        ax[3] = (1.0 - c.recirc[a]) * c.flow[a];
     }
-    if (kind == 1) {
-        switch (id) {
-        case 0: return c.reheat[idx];
-        case 1: return c.damper[idx];
-        case 2: return c.L->vav_c[idx * 9];
-        case 3: return c.coolsp[idx];
-        case 4: return c.heatsp[idx];
-        default: return c.sensing[idx];
-        }
+    if (l == 0) {
+        ox[OX_AMB] = amb;
+        ox[OX_DP] = (c.ip[PI_PUMP_RUN] == 1) ? 9.8 * 1000.0 * c.plant[PF_PUMP_HEAD] / 100000.0 : 0.0;
     }
-    double dp = (c.ip[PI_PUMP_RUN] == 1) ? 9.8 * 1000.0 * c.plant[PF_PUMP_HEAD] / 100000.0 : 0.0;
-    switch (id) {
-    case 0: return dp;
-    case 1: return c.plant[PF_BOILER_CUR];
-    case 2: return dp;
-    case 3: return (double)c.ip[PI_HWS_RUN];
-    case 4: return (double)c.ip[PI_HWS_REQ];
-    case 5: return (double)c.ip[PI_HWS_RUN];
-    default: return c.plant[PF_BOILER_SP];
-    }
+    esync();
 }
 
+// Observation row (sb_obs.c:49-64) at a calendar row whose ambient is `amb`
+// and aux-time values `aux` (n_aux - 1). Every device field is a gather from
+// its host-resolved source, normalised as (f32(v) - mean) / sd; fields are
+// taken four per lane at a time so their LDS reads overlap.
 template <int W>
-__device__ __forceinline__ void write_obs(Ctx& c, int j, float* row) {
+__device__ __forceinline__ void write_obs(Ctx& c, float* row, double amb, const double* aux) {
 #pragma clang fp contract(off)
+    obs_specials<W>(c, amb);
     const SBK_C DevLayout* L = c.L;
-    for (int i = threadIdx.x; i < L->n_dev; i += W) {
-        double v = obs_value(c, L->f_kind[i], L->f_idx[i], L->f_id[i], j);
-        double sd = L->f_sd[i];
-        float v32 = (float)v;
-        row[i] = (float)((sd > 0.0) ? ((double)v32 - L->f_mean[i]) / sd : 0.0);
+    const int nd = L->n_dev;
+    constexpr int U = 4;
+    for (int i0 = 0; i0 < nd; i0 += U * W) {
+        uint32_t src[U];
+        double mean[U], sd[U], v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = i0 + u * W + ln();
+            const int ic = i < nd ? i : nd - 1;
+            src[u] = c.t.f_src[ic];
+            mean[u] = c.t.f_mean[ic];
+            sd[u] = c.t.f_sd[ic];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const unsigned char* base = (src[u] & OBS_SRC_IMG) ? c.imgb : c.envb;
+            const unsigned char* p = base + (src[u] & OBS_SRC_OFF);
+            v[u] = (src[u] & OBS_SRC_I32) ? (double)*reinterpret_cast<const int*>(p)
+                                          : *reinterpret_cast<const double*>(p);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = i0 + u * W + ln();
+            const float v32 = (float)v[u];
+            if (i < nd) row[i] = (float)((sd[u] > 0.0) ? ((double)v32 - mean[u]) / sd[u] : 0.0);
+        }
     }
     const int na = L->n_aux;
-    const double* aux = c.S->aux_time + (size_t)j * (na - 1);
-    for (int i = threadIdx.x; i < na - 1; i += W) row[L->n_dev + i] = (float)aux[i];
+    for (int i = ln(); i < na - 1; i += W) row[L->n_dev + i] = (float)aux[i];
     int occ = 0;
-    for (int z = threadIdx.x; z < L->nz; z += W) occ += c.occV[z];
+    for (int z = ln(); z < L->nz; z += W) occ += c.occV[z];
     occ = bisum<W>(occ, c.red);
-    if (threadIdx.x == 0) row[L->n_dev + na - 1] = (float)occ;
-    for (int i = L->n_dev + na + threadIdx.x; i < 1024; i += W) row[i] = 0.0f;
+    if (ln() == 0) row[L->n_dev + na - 1] = (float)occ;
+    for (int i = L->n_dev + na + ln(); i < 1024; i += W) row[i] = 0.0f;
 }
 
 // ------------------------------------------------------------------ occupancy
@@ -357,20 +439,20 @@ __device__ __forceinline__ void mt_twist(uint32_t* mt) {
         const int lo = ph * 227, hi = ph == 2 ? 624 : lo + 227;
 #pragma unroll
         for (int r = 0; r < PER; r++) {
-            int i = lo + threadIdx.x + r * W;
+            int i = lo + ln() + r * W;
             if (i < hi) {
                 uint32_t nxt = (i == 623) ? mt[0] : mt[i + 1];
                 uint32_t far = (ph == 0) ? mt[i + 397] : mt[i - 227];
                 v[r] = mt_mix(mt[i], nxt, far);
             }
         }
-        __syncthreads();
+        esync();
 #pragma unroll
         for (int r = 0; r < PER; r++) {
-            int i = lo + threadIdx.x + r * W;
+            int i = lo + ln() + r * W;
             if (i < hi) mt[i] = v[r];
         }
-        __syncthreads();
+        esync();
     }
 }
 
@@ -406,7 +488,7 @@ __device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday)
     const int nocc = L->nz * L->nassign;
     constexpr int MAXC = 8;   // occupants per lane (nocc <= 8 * W, checked on the host)
     const int per = (nocc + W - 1) / W;
-    const int o0 = threadIdx.x * per;
+    const int o0 = ln() * per;
     int need[MAXC];
     int cnt = 0;
 #pragma unroll
@@ -425,22 +507,14 @@ __device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday)
     const int idx = c.ip[PI_MT_IDX];
     const int words = 2 * total;
     uint32_t* hbm_mt = (uint32_t*)(c.rec + L->st.mt);
-    bool twisted = false;
-    if (total > 0) {
-        if (idx + words > SBK_MT_N) {
-            // needs the rest of the current block and the start of the next
-            for (int i = threadIdx.x; i < SBK_MT_N; i += W) c.mt[i] = hbm_mt[i];
-            __syncthreads();
-            twisted = true;
-        }
-    }
-    // gather the tempered words: stream position s -> old[idx + s] or new[idx + s - 624]
-    // Words before the twist are read from the old state first, then the twist.
+    // the draws need the rest of the current block and the start of the next
+    const bool twisted = total > 0 && idx + words > SBK_MT_N;
+    // gather the tempered words: stream position s -> old[idx + s] or new[idx + s - 624];
+    // words before the twist are read from the old state (staged in LDS) first
     uint32_t w_old[2 * MAXC];
-    if (twisted) gather_words<MAXC>(c.mt, idx, first, need, w_old);     // LDS copy of the state
-    else gather_words<MAXC>(hbm_mt, idx, first, need, w_old);           // HBM record
+    gather_words<MAXC>(c.mt, idx, first, need, w_old);
     if (twisted) {
-        __syncthreads();
+        esync();
         mt_twist<W>(c.mt);
         int d = first;
 #pragma unroll
@@ -454,7 +528,7 @@ __device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday)
                 d++;
             }
         }
-        for (int i = threadIdx.x; i < SBK_MT_N; i += W) hbm_mt[i] = c.mt[i];
+        for (int i = ln(); i < SBK_MT_N; i += W) hbm_mt[i] = c.mt[i];
     }
     // apply the chain updates
 #pragma unroll
@@ -479,17 +553,17 @@ __device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday)
             c.occ_state[o] = (uint8_t)st;
         }
     }
-    __syncthreads();
-    if (threadIdx.x == 0 && total > 0) {
+    esync();
+    if (ln() == 0 && total > 0) {
         int ni = idx + words;
         c.ip[PI_MT_IDX] = twisted ? ni - SBK_MT_N : ni;
     }
-    for (int z = threadIdx.x; z < L->nz; z += W) {
+    for (int z = ln(); z < L->nz; z += W) {
         int s = 0;
         for (int a = 0; a < L->nassign; a++) s += c.occ_state[z * L->nassign + a];
         c.occV[z] = (uint8_t)s;
     }
-    __syncthreads();
+    esync();
 }
 
 // ------------------------------------------------------------------ reset
@@ -498,8 +572,8 @@ template <int W>
 __device__ __forceinline__ void sim_reset(Ctx& c, int start) {
     const SBK_C DevLayout* L = c.L;
     const SBK_C DevScen* S = c.S;
-    for (int a = threadIdx.x; a < L->na; a += W) {
-        const double* ac = L->ahu_c + a * 9;
+    for (int a = ln(); a < L->na; a += W) {
+        const double* ac = c.t.ahu_c + a * 9;
         c.run[a] = (int)ac[8];
         c.recirc[a] = ac[0];
         c.sat[a] = ac[6];
@@ -507,8 +581,8 @@ __device__ __forceinline__ void sim_reset(Ctx& c, int start) {
         c.flow[a] = 0.0;
         c.coolreq[a] = 0;
     }
-    for (int v = threadIdx.x; v < L->nv; v += W) {
-        const double* vc = L->vav_c + v * 9;
+    for (int v = ln(); v < L->nv; v += W) {
+        const double* vc = c.t.vav_c + v * 9;
         c.damper[v] = vc[7];
         c.reheat[v] = vc[8];
         c.ratio[v] = 1.0;
@@ -521,11 +595,11 @@ __device__ __forceinline__ void sim_reset(Ctx& c, int start) {
         c.dcmd[v] = 0.0;
         c.rcmd[v] = 0.0;
     }
-    for (int t = threadIdx.x; t < L->n; t += W) {
+    for (int t = ln(); t < L->n; t += W) {
         c.T[t] = S->temp_init[t];
         c.M[t] = S->mass_init[t];
     }
-    if (threadIdx.x == 0) {
+    if (ln() == 0) {
         c.ip[PI_HWS_REQ] = 0;
         c.ip[PI_HWS_RUN] = 1;
         c.ip[PI_PUMP_RUN] = 1;
@@ -536,14 +610,14 @@ __device__ __forceinline__ void sim_reset(Ctx& c, int start) {
         c.ip[PI_STEP_INDEX] = start;
         c.ip[PI_STEP] = 0;
     }
-    __syncthreads();
+    esync();
     zone_means<W>(c, c.zq);
-    __syncthreads();
-    for (int v = threadIdx.x; v < L->nv; v += W) {
+    esync();
+    for (int v = ln(); v < L->nv; v += W) {
         double area;
         c.sensing[v] = vav_temp(c, c.zq, v, &area);
     }
-    __syncthreads();
+    esync();
 }
 
 // puf_reset sequence (pufferlib_cpu_env.h:187-208) at the env's start offset.
@@ -552,78 +626,142 @@ __device__ __forceinline__ void env_reset(Ctx& c, int start, float* obs_row) {
     const SBK_C DevScen* S = c.S;
     sim_reset<W>(c, start);
     occupancy_advance<W>(c, S->hour_m1[start], S->work_m1[start]);
-    write_obs<W>(c, start, obs_row);
+    write_obs<W>(c, obs_row, S->amb[start], S->aux_time + (size_t)start * (c.L->n_aux - 1));
     occupancy_advance<W>(c, S->occ_hour[start], S->occ_work[start]);
 }
 
 // ------------------------------------------------------------------ step
+// The step's calendar values (row kk before the step, kk - 1 for the comfort
+// transition, row j = kk + 1 after it) and aux-time row j. row_issue only
+// issues the loads (the kernel overlaps them with the staging burst);
+// row_store puts them in the env's scratch. The host guarantees j < n1.
+struct RowVals {
+    double v[RW_COUNT];
+    double aux;
+};
+
 template <int W>
-__device__ __forceinline__ void decode_apply(Ctx& c, const float* act) {
-#pragma clang fp contract(off)
-    const SBK_C DevLayout* L = c.L;
-    for (int i = threadIdx.x; i < L->n_act; i += W) {
-        double nat;
-        float a = act[L->act_src[i]];
-        if (L->act_disc[i]) {
-            double dv = (double)a;
-            double m = (dv == 1.0) ? 1.0 : -1.0;
-            nat = (m - L->act_mnr[i]) / (L->act_mxr[i] - L->act_mnr[i]) * (L->act_mx[i] - L->act_mn[i])
-                  + L->act_mn[i];
-        } else {
-            float m = a > 1.0f ? 1.0f : (a < -1.0f ? -1.0f : a);
-            float span_in = (float)(L->act_mxr[i] - L->act_mnr[i]);
-            float span_out = (float)(L->act_mx[i] - L->act_mn[i]);
-            float r = (m - (float)L->act_mnr[i]) / span_in * span_out + (float)L->act_mn[i];
-            nat = (double)r;
-        }
-        const int idx = L->act_idx[i], ak = L->act_act[i];
-        switch (L->act_kind[i]) {
-        case 0:
-            if (ak == 0) c.sat[idx] = nat;
-            else if (ak == 1) c.fan[idx] = nat;
-            else if (ak == 2) {
-                double hi = L->ahu_c[idx * 9 + 3];
-                c.recirc[idx] = nat < 0.0 ? 0.0 : (nat > hi ? hi : nat);
-            } else c.run[idx] = (nat == 1.0) ? 1 : 0;
-            break;
-        case 1: {
-            double cl = nat < 0.0 ? 0.0 : (nat > 1.0 ? 1.0 : nat);
-            if (ak == 0) { c.dcmd[idx] = cl; c.dcmd_set[idx] = 1; }
-            else { c.rcmd[idx] = cl; c.rcmd_set[idx] = 1; }
-            break;
-        }
-        default:
-            if (ak == 0) c.plant[PF_BOILER_SP] = nat;
-            else if (ak == 1) c.plant[PF_PUMP_HEAD] = nat / (GRAV * RHO_W / PA_PER_BAR);
-            else { int on = (nat == 1.0) ? 1 : 0; c.ip[PI_HWS_RUN] = on; c.ip[PI_PUMP_RUN] = on; }
-        }
-    }
-    __syncthreads();
+__device__ __forceinline__ RowVals row_issue(const Ctx& c, int kk, int j) {
+    const SBK_C DevScen* S = c.S;
+    const int naux = c.L->n_aux - 1;
+    const int km1 = kk > 0 ? kk - 1 : 0;
+    RowVals r;
+    r.v[RW_AMB_K] = S->amb[kk];
+    r.v[RW_SOLAR_K] = S->solar_i[kk];
+    r.v[RW_COMF_K] = S->comfort[kk];
+    r.v[RW_COMF_KM1] = kk > 0 ? S->comfort[km1] : 0.0;
+    r.v[RW_HSP_K] = S->heat_sp[kk];
+    r.v[RW_CSP_K] = S->cool_sp[kk];
+    r.v[RW_AMB_J] = S->amb[j];
+    r.v[RW_HSP_J] = S->heat_sp[j];
+    r.v[RW_CSP_J] = S->cool_sp[j];
+    r.v[RW_OCC_HOUR_J] = (double)S->occ_hour[j];
+    r.v[RW_OCC_WORK_J] = (double)S->occ_work[j];
+    r.v[RW_REW_HOUR_J] = (double)S->rew_hour[j];
+    r.v[RW_REW_MONTH_J] = (double)S->rew_month[j];
+    r.v[RW_REW_WORK_J] = (double)S->rew_work[j];
+    const int l = ln();
+    r.aux = naux > 0 ? S->aux_time[(size_t)j * naux + (l < naux ? l : 0)] : 0.0;
+    return r;
 }
 
 template <int W>
-__device__ __forceinline__ void step_pre(Ctx& c) {
+__device__ __forceinline__ void row_store(Ctx& c, const RowVals& r) {
+    const int l = ln();
+    if (l == 0) {
+#pragma unroll
+        for (int i = 0; i < RW_COUNT; i++) c.misc[MS_ROW + i] = r.v[i];
+    }
+    if (l < c.L->n_aux - 1) c.misc[MS_AUX + l] = r.aux;
+}
+
+// Action decode and apply (sb_sim.c:557-576, :220-244): continuous actions
+// clamp to [-1, 1] and map through float32 (min, max) spans, discrete ones map
+// 1 -> max and anything else -> min in float64; the value then goes to its
+// host-resolved target. Both decodes are computed and one selected, so lanes
+// do not diverge; actions are taken four per lane at a time.
+template <int W>
+__device__ __forceinline__ void decode_apply(Ctx& c) {
+#pragma clang fp contract(off)
+    const int n = c.L->n_act;
+    const Tab& t = c.t;
+    constexpr int U = 4;
+    for (int i0 = 0; i0 < n; i0 += U * W) {
+        int src[U];
+        uint32_t dst[U], aux[U];
+        uint8_t disc[U], fl[U];
+        double mn[U], mx[U], mnr[U], mxr[U], hi[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = i0 + u * W + ln();
+            const int ic = i < n ? i : n - 1;
+            src[u] = t.act_src[ic];
+            dst[u] = t.act_dst[ic];
+            aux[u] = t.act_aux[ic];
+            disc[u] = t.act_disc[ic];
+            fl[u] = t.act_flags[ic];
+            mn[u] = t.act_mn[ic];
+            mx[u] = t.act_mx[ic];
+            mnr[u] = t.act_mnr[ic];
+            mxr[u] = t.act_mxr[ic];
+            hi[u] = t.act_hi[ic];
+        }
+        float a[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) a[u] = c.act[src[u]];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = i0 + u * W + ln();
+            // discrete: 1 -> +1, else -1, mapped in float64
+            const double m64 = ((double)a[u] == 1.0) ? 1.0 : -1.0;
+            const double nat_d = (m64 - mnr[u]) / (mxr[u] - mnr[u]) * (mx[u] - mn[u]) + mn[u];
+            // continuous: clamp, then the float32 span map
+            const float m = a[u] > 1.0f ? 1.0f : (a[u] < -1.0f ? -1.0f : a[u]);
+            const float span_in = (float)(mxr[u] - mnr[u]);
+            const float span_out = (float)(mx[u] - mn[u]);
+            const float r = (m - (float)mnr[u]) / span_in * span_out + (float)mn[u];
+            const double nat = disc[u] ? nat_d : (double)r;
+            double v = nat;
+            if (fl[u] & ACT_CLAMP) v = nat < 0.0 ? 0.0 : (nat > hi[u] ? hi[u] : nat);
+            if (fl[u] & ACT_PUMP_HEAD) v = nat / (GRAV * RHO_W / PA_PER_BAR);
+            if (i < n) {
+                unsigned char* p = c.envb + (dst[u] & ACT_OFF);
+                const int on = (nat == 1.0) ? 1 : 0;
+                if (dst[u] & ACT_I32) *reinterpret_cast<int*>(p) = on;
+                else *reinterpret_cast<double*>(p) = v;
+                unsigned char* q = c.envb + (aux[u] & ACT_OFF);
+                if (aux[u] & ACT_AUX_U8) *q = 1;
+                if (aux[u] & ACT_AUX_I32) *reinterpret_cast<int*>(q) = on;
+            }
+        }
+    }
+    esync();
+}
+
+template <int W>
+__device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
     const SBK_C DevLayout* L = c.L;
     const SBK_C DevScen* S = c.S;
-    const int kk = c.ip[PI_STEP_INDEX];
-    const double ambient = S->amb[kk];
-    const int comfort = (S->comfort[kk] != 0.0);
+    const double* rw = c.misc + MS_ROW;
+    const double ambient = rw[RW_AMB_K];
+    const int comfort = (rw[RW_COMF_K] != 0.0);
     const int na = L->na, nv = L->nv;
     zone_means<W>(c, c.zq);
-    __syncthreads();
+    esync();
+    STAMP(13);
     // sensing + thermostat + VAV settings (sb_sim.c:368-384, :316-355)
-    for (int v = threadIdx.x; v < nv; v += W) {
+    for (int v = ln(); v < nv; v += W) {
         double area;
         double sensing = vav_temp(c, c.zq, v, &area);
         c.sensing[v] = sensing;
         if (area <= 0.0) continue;
-        const double* vc = L->vav_c + v * 9;
-        double hsp = S->heat_sp[kk], csp = S->cool_sp[kk];
+        const double* vc = c.t.vav_c + v * 9;
+        double hsp = rw[RW_HSP_K], csp = rw[RW_CSP_K];
         c.heatsp[v] = hsp;
         c.coolsp[v] = csp;
         int mode = c.mode[v];
         if (comfort) mode = default_mode(mode, sensing, hsp, csp);
-        else if (c.prev_valid[v] && S->comfort[kk - 1] != 0.0) mode = M_PASSIVE;
+        else if (c.prev_valid[v] && rw[RW_COMF_KM1] != 0.0) mode = M_PASSIVE;
         else if (mode == M_PASSIVE && sensing > hsp && sensing < csp) mode = M_PASSIVE;
         else mode = default_mode(mode, sensing, hsp, csp);
         c.mode[v] = (uint8_t)mode;
@@ -637,25 +775,26 @@ __device__ __forceinline__ void step_pre(Ctx& c) {
         c.damper[v] = damper > vc[2] ? damper : vc[2];
         c.reheat[v] = reheat;
     }
-    __syncthreads();
+    esync();
+    STAMP(14);
     // AHU return-air means and supply temperatures (sb_sim.c:382-387, :253-265)
     double tmean = 0.0;
     if (S->conv_tmean) {
         double s = 0.0;
-        for (int t = threadIdx.x; t < L->n; t += W) s += c.T[t];
+        for (int t = ln(); t < L->n; t += W) s += c.T[t];
         tmean = bsum<W>(s, c.red) / (double)L->n;
     }
     double ffs_part = 0.0;
-    for (int v = threadIdx.x; v < nv; v += W) {
-        ffs_part += c.reheat[v] * L->vav_c[v * 9 + 1];
+    for (int v = ln(); v < nv; v += W) {
+        ffs_part += c.reheat[v] * c.t.vav_c[v * 9 + 1];
         c.unres[v] = vav_unrestricted(c, v);
     }
     const double ffs = bsum<W>(ffs_part, c.red);
     for (int a = 0; a < na; a++) {
         double ws = 0.0, at = 0.0, dm = 0.0;
-        for (int v = threadIdx.x; v < nv; v += W) {
-            if (L->vav_ahu[v] != a) continue;
-            double area = L->vav_area[v];
+        for (int v = ln(); v < nv; v += W) {
+            if (c.t.vav_ahu[v] != a) continue;
+            double area = c.t.vav_area[v];
             if (area > 0.0) {
                 ws += c.sensing[v] * area;
                 at += area;
@@ -665,39 +804,40 @@ __device__ __forceinline__ void step_pre(Ctx& c) {
         ws = bsum<W>(ws, c.red);
         at = bsum<W>(at, c.red);
         dm = bsum<W>(dm, c.red);
-        if (threadIdx.x == 0) {
+        if (ln() == 0) {
             double rt = (at > 0.0) ? ws / at : tmean;
             double mixed = c.recirc[a] * rt + (1.0 - c.recirc[a]) * ambient;
             c.satv[a] = (mixed > c.sat[a] && c.run[a] == 1) ? c.sat[a] : mixed;
             c.demand[a] = dm;
         }
     }
-    if (threadIdx.x == 0) {
+    if (ln() == 0) {
         c.misc[MS_FFS] = ffs;
         c.ip[PI_HWS_REQ] = nv;
     }
-    __syncthreads();
-    for (int v = threadIdx.x; v < nv; v += W) {
-        int a = L->vav_ahu[v];
+    esync();
+    for (int v = ln(); v < nv; v += W) {
+        int a = c.t.vav_ahu[v];
         double dm = c.demand[a];
         if (dm > 0.0) {
-            double r = L->ahu_c[a * 9 + 1] / dm;
+            double r = c.t.ahu_c[a * 9 + 1] / dm;
             c.ratio[v] = r < 1.0 ? r : 1.0;
         } else {
             c.ratio[v] = 1.0;
         }
     }
-    __syncthreads();
+    esync();
+    STAMP(15);
     const double tf = total_flow_rate(c);
     const double iwt = c.plant[PF_BOILER_CUR];
     // coupled columns: reheat energy, air-side conductance, AHU flow (sb_sim.c:410-436)
     double rw_part = 0.0;
-    for (int col = threadIdx.x; col < L->k; col += W) {
-        int v = L->coupled[col];
+    for (int col = ln(); col < L->k; col += W) {
+        int v = c.t.coupled[col];
         double g = 0.0, ta = 0.0, rw = 0.0, fd = 0.0;
-        if (L->vav_area[v] > 0.0) {
-            const double* vc = L->vav_c + v * 9;
-            int a = L->vav_ahu[v];
+        if (c.t.vav_area[v] > 0.0) {
+            const double* vc = c.t.vav_c + v * 9;
+            int a = c.t.vav_ahu[v];
             double sat = c.satv[a];
             ta = sat;
             fd = c.unres[v] * c.ratio[v];
@@ -734,8 +874,8 @@ __device__ __forceinline__ void step_pre(Ctx& c) {
     const double total_rw = bsum<W>(rw_part, c.red);
     // coil extreme for the boiler return temperature (sb_sim.c:495-499)
     double cmin = 1e308, cmax = -1e308;
-    for (int col = threadIdx.x; col < L->k; col += W) {
-        int v = L->coupled[col];
+    for (int col = ln(); col < L->k; col += W) {
+        int v = c.t.coupled[col];
         (void)v;
         cmin = fmin(cmin, c.tair[col]);
         cmax = fmax(cmax, c.tair[col]);
@@ -745,22 +885,22 @@ __device__ __forceinline__ void step_pre(Ctx& c) {
     for (int a = 0; a < na; a++) {
         double f = 0.0;
         int cnt = 0;
-        for (int col = threadIdx.x; col < L->k; col += W) {
-            int v = L->coupled[col];
-            if (L->vav_ahu[v] == a && L->vav_area[v] > 0.0 && c.fdem[col] > 0.0) {
+        for (int col = ln(); col < L->k; col += W) {
+            int v = c.t.coupled[col];
+            if (c.t.vav_ahu[v] == a && c.t.vav_area[v] > 0.0 && c.fdem[col] > 0.0) {
                 f += c.fdem[col];
                 cnt++;
             }
         }
         f = bsum<W>(f, c.red);
         cnt = bisum<W>(cnt, c.red);
-        if (threadIdx.x == 0) {
-            double mf = L->ahu_c[a * 9 + 1];
+        if (ln() == 0) {
+            double mf = c.t.ahu_c[a * 9 + 1];
             c.flow[a] = f > mf ? mf : f;
             c.coolreq[a] = cnt;
         }
     }
-    if (threadIdx.x == 0) {
+    if (ln() == 0) {
         c.misc[MS_TOTAL_REHEAT] = total_rw;
         c.misc[MS_TF] = tf;
         c.misc[6] = cmin;
@@ -771,33 +911,23 @@ __device__ __forceinline__ void step_pre(Ctx& c) {
     // zone heat: reheat share, internal and occupant gains (sb_sim.c:420-447)
     const double frac = comfort ? 1.0 : S->standby_frac;
     const double wpc = S->internal_w_m2 * S->cv_area * frac;
-    for (int z = threadIdx.x; z < L->nz; z += W) {
+    for (int z = ln(); z < L->nz; z += W) {
         double q = 0.0;
-        for (int t = L->zone_col_off[z]; t < L->zone_col_off[z + 1]; t++) {
-            int col = L->zone_cols[t];
-            int v = L->coupled[col];
-            if (L->vav_area[v] > 0.0 && c.damper[v] > 0.0 && L->vav_c[v * 9] > 0.0)
-                q += c.rwen[col] * L->zone_area[z] / L->vav_area[v];
+        for (int t = c.t.zone_col_off[z]; t < c.t.zone_col_off[z + 1]; t++) {
+            int col = c.t.zone_cols[t];
+            int v = c.t.coupled[col];
+            if (c.t.vav_area[v] > 0.0 && c.damper[v] > 0.0 && c.t.vav_c[v * 9] > 0.0)
+                q += c.rwen[col] * c.t.zone_area[z] / c.t.vav_area[v];
         }
-        int ncell = L->zone_cell_off[z + 1] - L->zone_cell_off[z];
+        int ncell = c.t.zone_cell_off[z + 1] - c.t.zone_cell_off[z];
         if (S->internal_w_m2 > 0.0) q += wpc * (double)ncell;
         if (S->occupant_w > 0.0) q += (double)c.occV[z] * S->occupant_w;
         c.zq[z] = q / (double)ncell;
     }
-    __syncthreads();
+    esync();
 }
 
 // ------------------------------------------------------------------ solve plan
-// Orders this wave's LDS accesses before and after the point (the wave's DS
-// operations complete in issue order) without waiting for global loads, so
-// the next pass's term words stay in flight across the synchronisation.
-__device__ __forceinline__ void wave_lds_sync() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0), vmcnt/expcnt untouched
-    __builtin_amdgcn_wave_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 struct PassRegs {
     uint64_t h;
     int nact, maxcnt, piv;
@@ -813,7 +943,7 @@ struct PassRegs {
 __device__ __forceinline__ void fetch_pass(const SBK_C DevLayout* L, int4 pi, PassRegs& r) {
     const int hdr_off = pi.x, word_off = pi.y;
     const int nact = pi.z & 0xff, maxcnt = (pi.z >> 8) & 0xff, has_pivot = (pi.z >> 16) & 1;
-    const int lane = threadIdx.x;
+    const int lane = ln();
     const bool act = lane < nact;
     r.nact = nact;
     r.maxcnt = maxcnt;
@@ -881,7 +1011,7 @@ __device__ __forceinline__ void run_pass(double* slots, const PassRegs& r) {
         for (int j = 0; j < CH; j++) acc -= x[j] * y[j];
     }
     acc *= scale;
-    if ((int)threadIdx.x < r.nact) slots[tgt] = acc;
+    if (ln() < r.nact) slots[tgt] = acc;
     if (r.piv) slots[invt] = recip(acc);
 }
 
@@ -934,7 +1064,7 @@ template <int K>
 __device__ __forceinline__ int relax_sweeps(const SBK_C DevLayout* L, double* x, int n, const double* bv,
                                             const double* iv, double* xv, double atol,
                                             unsigned long long* pts) {
-    const int lane = threadIdx.x;
+    const int lane = ln();
     double av[SBK_RX_RPL][K];
     int ci[SBK_RX_RPL][K];
 #pragma unroll
@@ -983,7 +1113,7 @@ __device__ __forceinline__ void relax_solve(Ctx& c, double ambient, double irr, 
     const SBK_C DevLayout* L = c.L;
     const SBK_C DevScen* S = c.S;
     const int n = L->n;
-    const int lane = threadIdx.x;
+    const int lane = ln();
     if (pts) pts[0] = clock64();
     double bv[SBK_RX_RPL], iv[SBK_RX_RPL], xv[SBK_RX_RPL];
     double xabs = 0.0;
@@ -994,10 +1124,10 @@ __device__ __forceinline__ void relax_solve(Ctx& c, double ambient, double irr, 
         iv[j] = 0.0;
         xv[j] = 0.0;
         if (t < n) {
-            const double qin = L->is_room[t] ? c.slots[t] + L->solar_c[t] * irr : L->solar_c[t] * irr;
-            double b = L->cap[t] * c.T[t] + qin + ambient * S->dirx[t] + L->mcoup[t] * c.M[t];
-            double d = L->rx_diag[t];
-            const int col = L->rx_air[t];
+            const double qin = c.t.is_room[t] ? c.slots[t] + c.t.solar_c[t] * irr : c.t.solar_c[t] * irr;
+            double b = c.t.cap[t] * c.T[t] + qin + ambient * c.dirx[t] + c.t.mcoup[t] * c.M[t];
+            double d = c.t.rx_diag[t];
+            const int col = c.t.rx_air[t];
             if (col >= 0) {
                 const double g = c.g[col];
                 b += g * c.tair[col];
@@ -1021,9 +1151,9 @@ __device__ __forceinline__ void relax_solve(Ctx& c, double ambient, double irr, 
 #pragma unroll
     for (int j = 0; j < SBK_RX_RPL; j++) {
         const int t = lane + 64 * j;
-        if (t < n) c.M[t] = c.M[t] * L->mret[t] + L->mgain[t] * xv[j];
+        if (t < n) c.M[t] = c.M[t] * c.t.mret[t] + c.t.mgain[t] * xv[j];
     }
-    __syncthreads();
+    esync();
 }
 
 // Field step: b = cap T + q + amb dirx + mc M (+ solar, + g T_air at the air
@@ -1033,61 +1163,60 @@ template <int W>
 __device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
     const SBK_C DevLayout* L = c.L;
     const SBK_C DevScen* S = c.S;
-    const int kk = c.ip[PI_STEP_INDEX];
-    const double ambient = S->amb[kk];
-    const double irr = S->solar_i[kk];
+    const double ambient = c.misc[MS_ROW + RW_AMB_K];
+    const double irr = c.misc[MS_ROW + RW_SOLAR_K];
     const int n = L->n;
     double* slots = c.slots;
     if (L->solver == SOLVER_RELAX) {
         // room cells carry their zone's heat (node-indexed scratch in the slot region)
-        for (int z = threadIdx.x; z < L->nz; z += W) {
+        for (int z = ln(); z < L->nz; z += W) {
             double qz = c.zq[z];
-            for (int t = L->zone_cell_off[z]; t < L->zone_cell_off[z + 1]; t++) slots[L->zone_cells[t]] = qz;
+            for (int t = c.t.zone_cell_off[z]; t < c.t.zone_cell_off[z + 1]; t++) slots[c.t.zone_cells[t]] = qz;
         }
-        __syncthreads();
+        esync();
         STAMP(4);
-        unsigned long long* pts = (P.pass_ts && blockIdx.x == P.pass_ts_block && threadIdx.x == 0) ? P.pass_ts : nullptr;
+        unsigned long long* pts = (P.pass_ts && c.e == P.pass_ts_env && ln() == 0) ? P.pass_ts : nullptr;
         relax_solve<W>(c, ambient, irr, pts);
         STAMP(5);
         return;
     }
     const int vb = L->vec_base;
-    for (int s = threadIdx.x; s < vb; s += W) slots[s] = L->slot_init[s];   // incl. 0.0 and 1.0 slots
+    for (int s = ln(); s < vb; s += W) slots[s] = L->slot_init[s];   // incl. 0.0 and 1.0 slots
     // room cells carry their zone's heat; every node then gets its solar gain
-    for (int z = threadIdx.x; z < L->nz; z += W) {
+    for (int z = ln(); z < L->nz; z += W) {
         double qz = c.zq[z];
-        for (int t = L->zone_cell_off[z]; t < L->zone_cell_off[z + 1]; t++) c.slots[vb + L->pos[L->zone_cells[t]]] = qz;
+        for (int t = c.t.zone_cell_off[z]; t < c.t.zone_cell_off[z + 1]; t++) c.slots[vb + c.t.pos[c.t.zone_cells[t]]] = qz;
     }
-    __syncthreads();
-    for (int t = threadIdx.x; t < n; t += W) {
-        const int ps = vb + L->pos[t];
-        double qin = L->is_room[t] ? slots[ps] + L->solar_c[t] * irr : L->solar_c[t] * irr;
-        slots[ps] = L->cap[t] * c.T[t] + qin + ambient * S->dirx[t] + L->mcoup[t] * c.M[t];
+    esync();
+    for (int t = ln(); t < n; t += W) {
+        const int ps = vb + c.t.pos[t];
+        double qin = c.t.is_room[t] ? slots[ps] + c.t.solar_c[t] * irr : c.t.solar_c[t] * irr;
+        slots[ps] = c.t.cap[t] * c.T[t] + qin + ambient * c.dirx[t] + c.t.mcoup[t] * c.M[t];
     }
-    __syncthreads();
-    for (int col = threadIdx.x; col < L->k; col += W) {
+    esync();
+    for (int col = ln(); col < L->k; col += W) {
         double g = c.g[col];
-        slots[L->air_slot[col]] += g;
-        slots[vb + L->pos[L->air_node[col]]] += g * c.tair[col];
+        slots[c.t.air_slot[col]] += g;
+        slots[vb + c.t.pos[c.t.air_node[col]]] += g * c.tair[col];
     }
-    __syncthreads();
+    esync();
     STAMP(4);
     // level schedule: LU of the permuted system, forward and backward solves
-    unsigned long long* pts = (P.pass_ts && blockIdx.x == P.pass_ts_block && threadIdx.x == 0) ? P.pass_ts : nullptr;
+    unsigned long long* pts = (P.pass_ts && c.e == P.pass_ts_env && ln() == 0) ? P.pass_ts : nullptr;
     run_plan<W>(L, slots, reinterpret_cast<const int4*>(c.prec), pts);
     STAMP(5);
-    for (int t = threadIdx.x; t < n; t += W) {
-        double y = slots[vb + L->pos[t]];
-        c.M[t] = c.M[t] * L->mret[t] + L->mgain[t] * y;
+    for (int t = ln(); t < n; t += W) {
+        double y = slots[vb + c.t.pos[t]];
+        c.M[t] = c.M[t] * c.t.mret[t] + c.t.mgain[t] * y;
         c.T[t] = y;
     }
-    __syncthreads();
+    esync();
 }
 
 // sb_sim_step_post (sb_sim.c:489-521), convection off.
 template <int W>
 __device__ __forceinline__ void step_post(Ctx& c) {
-    if (threadIdx.x == 0) {
+    if (ln() == 0) {
         const SBK_C DevScen* S = c.S;
         const double total_rw = c.misc[MS_TOTAL_REHEAT];
         double wcap = CP_W * RHO_W * c.misc[MS_TF];
@@ -1117,30 +1246,31 @@ __device__ __forceinline__ void step_post(Ctx& c) {
         c.plant[PF_BOILER_DSTEP] = cur - begin;
         c.ip[PI_STEP_INDEX] += 1;
     }
-    __syncthreads();
+    esync();
 }
 
 // 3C reward (sb_reward.c:31-155) on the post-step state and new occupancy.
 template <int W>
-__device__ __forceinline__ double reward(Ctx& c, int kv) {
+__device__ __forceinline__ double reward(Ctx& c) {
     const SBK_C DevLayout* L = c.L;
     const SBK_C DevScen* S = c.S;
     const double dt = S->dt_sec, inv_hour = 1.0 / 3600.0;
     zone_means<W>(c, c.zq);
-    __syncthreads();
-    const double ambient = S->amb[kv];
-    const int hour = S->rew_hour[kv], month = S->rew_month[kv], wd = S->rew_work[kv];
+    esync();
+    const double* rw = c.misc + MS_ROW;
+    const double ambient = rw[RW_AMB_J];
+    const int hour = (int)rw[RW_REW_HOUR_J], month = (int)rw[RW_REW_MONTH_J], wd = (int)rw[RW_REW_WORK_J];
     double tmean = 0.0;
     if (S->conv_tmean) {
         double s = 0.0;
-        for (int t = threadIdx.x; t < L->n; t += W) s += c.T[t];
+        for (int t = ln(); t < L->n; t += W) s += c.T[t];
         tmean = bsum<W>(s, c.red) / (double)L->n;
     }
     double intake = 0.0, exhaust = 0.0, cooling = 0.0;
     for (int a = 0; a < L->na; a++) {
         double ws = 0.0, at = 0.0;
-        for (int v = threadIdx.x; v < L->nv; v += W) {
-            if (L->vav_ahu[v] != a) continue;
+        for (int v = ln(); v < L->nv; v += W) {
+            if (c.t.vav_ahu[v] != a) continue;
             double area;
             double tv = vav_temp(c, c.zq, v, &area);
             if (area > 0.0) {
@@ -1152,13 +1282,13 @@ __device__ __forceinline__ double reward(Ctx& c, int kv) {
         at = bsum<W>(at, c.red);
         double rc = (at > 0.0) ? ws / at : tmean;
         double st = ahu_static(c, a);
-        double fe = L->ahu_c[a * 9 + 5];
+        double fe = c.t.ahu_c[a * 9 + 5];
         double flow = (c.run[a] == 1) ? c.flow[a] : 0.0;
         intake += flow * st / fe;
         exhaust += flow * (1.0 - c.recirc[a]) * st / fe;
         double mixed = c.recirc[a] * rc + (1.0 - c.recirc[a]) * ambient;
         double sat = (mixed > c.sat[a] && c.run[a] == 1) ? c.sat[a] : mixed;
-        cooling += flow * RHO_AIR * CP_AIR * (sat - mixed) / L->ahu_c[a * 9 + 4];
+        cooling += flow * RHO_AIR * CP_AIR * (sat - mixed) / c.t.ahu_c[a * 9 + 4];
     }
     const double blower = intake + exhaust;
     const double tf = total_flow_rate(c);
@@ -1179,9 +1309,9 @@ __device__ __forceinline__ double reward(Ctx& c, int kv) {
     }
     const double pump_e = tf * RHO_W * GRAV * c.plant[PF_PUMP_HEAD] / S->pump_eff;
     const double max_pph = S->rw[0], min_pph = S->rw[1], ref = S->rw[2];
-    const double hsp = S->heat_sp[kv], csp = S->cool_sp[kv];
+    const double hsp = rw[RW_HSP_J], csp = rw[RW_CSP_J];
     double occ_part = 0.0, cum_part = 0.0;
-    for (int z = threadIdx.x; z < L->nz; z += W) {
+    for (int z = ln(); z < L->nz; z += W) {
         double occ = (double)c.occV[z];
         occ_part += occ;
         double zt = c.zq[z];
@@ -1198,13 +1328,13 @@ __device__ __forceinline__ double reward(Ctx& c, int kv) {
     double npr = 0.0;
     if (total_occ > 0.0 && (max_prod - min_prod) != 0.0) npr = (cum - min_prod) / (max_prod - min_prod) - 1.0;
     const double elec_rate = blower + fabs(cooling) + pump_e;
-    const double price = wd ? S->elec_wk[hour] : S->elec_we[hour];
-    const double crate = S->elec_co2[hour];
+    const double price = wd ? c.elec_wk[hour] : c.elec_we[hour];
+    const double crate = c.elec_co2[hour];
     const double elec_cost = price * fabs(elec_rate) * dt;
     const double elec_cost_max = price * S->rw[3] * dt;
     const double elec_carb = crate * fabs(elec_rate) * dt;
     const double elec_carb_max = crate * S->rw[3] * dt;
-    const double gprice = S->gas_price[month - 1];
+    const double gprice = c.gas_price[month - 1];
     const double gg = gas_rate > 0.0 ? gas_rate : 0.0;
     const double gas_cost = gprice * gg * dt;
     const double gas_cost_max = gprice * S->rw[4] * dt;
@@ -1219,75 +1349,153 @@ __device__ __forceinline__ double reward(Ctx& c, int kv) {
     return raw / (pw + ew + cw);
 }
 
-// Loads/stores of the state image, 16 bytes per lane.
+// Store of the state image back to its HBM record, 16 bytes per lane.
 template <int W>
-__device__ __forceinline__ void copy16(unsigned char* dst, const unsigned char* src, int bytes) {
+__device__ __forceinline__ void store16(unsigned char* dst, const unsigned char* src, int bytes) {
     const int n16 = bytes >> 4;
-    for (int i = threadIdx.x; i < n16; i += W)
+    for (int i = ln(); i < n16; i += W)
         reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
 }
 
+// Staging burst: every thread issues all loads of a round (up to U vectors of
+// each part) before its first store, so the burst costs one memory latency
+// per round. Indices are clamped into the part (to vector 0 of a valid buffer
+// when the part is empty), so every load is unconditional and in bounds.
+template <int U, class Src>
+__device__ __forceinline__ void part_load(uint4 (&r)[U], Src src, int n16, int tid, int nthr, int base) {
+    const int last = n16 > 0 ? n16 - 1 : 0;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int i = base + u * nthr + tid;
+        r[u] = src[i < last ? i : last];
+    }
+}
+
+template <int U>
+__device__ __forceinline__ void part_store(const uint4 (&r)[U], uint4* dst, int n16, int tid, int nthr, int base) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const int i = base + u * nthr + tid;
+        if (i < n16) dst[i] = r[u];
+    }
+}
+
 template <int W>
-__global__ __launch_bounds__(W) void step_kernel(KParams P) {
+__global__ __launch_bounds__(512) void step_kernel(KParams P) {
+    static_assert(W == 64, "one wavefront per env");
     extern __shared__ __align__(16) unsigned char lds[];
-    const int e = P.order[blockIdx.x];
+    const Tile tl = P.tiles[blockIdx.x];
+    const SBK_C DevLayout* L = P.layouts + tl.layout;
+    const int slot = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));   // wave-uniform
+    const bool active = slot < tl.count;
+    const int e = P.order[tl.first + (active ? slot : 0)];
     const EnvDesc ed = P.envs[e];
     Ctx c;
-    c.L = P.layouts + ed.layout;
+    c.L = L;
     c.S = P.scens + ed.scen;
+    c.e = e;
     c.rec = P.state + ed.state_off;
-    bind(c, lds);
-    const SBK_C DevLayout* L = c.L;
+    unsigned char* env = lds + P.img_lds + slot * L->lds.bytes;
+    bind(c, lds, env);
     STAMP(0);
-    copy16<W>(lds + L->lds.state, c.rec, L->st.bytes);
-    if (P.mode == KMODE_STEP) {
-        const SBK_C uint4* src = reinterpret_cast<const SBK_C uint4*>(L->pinfo);
-        for (int i = threadIdx.x; i < L->n_pass; i += W) reinterpret_cast<uint4*>(c.prec)[i] = src[i];
+    {
+        // one burst: the layout image (whole block), and per env its record
+        // with the MT words, its scenario image and its action row
+        constexpr int UI = 12, UR = 12, US = 4, UA = 2;
+        const int nthr = (int)blockDim.x, tid = (int)threadIdx.x, l = ln();
+        const int img16 = L->img.bytes >> 4;
+        const int rec16 = active ? (L->st.bytes + 4 * SBK_MT_N) >> 4 : 0;
+        const int scn16 = active ? c.S->img.bytes >> 4 : 0;
+        const int act16 = (active && P.mode == KMODE_STEP) ? (4 * SB_ACT) >> 4 : 0;
+        const SBK_C uint4* isrc = reinterpret_cast<const SBK_C uint4*>(L->img_src);
+        const SBK_C uint4* ssrc = reinterpret_cast<const SBK_C uint4*>(c.S->img_src);
+        const uint4* rsrc = reinterpret_cast<const uint4*>(c.rec);
+        const uint4* asrc = reinterpret_cast<const uint4*>(P.actions + (size_t)e * SB_ACT);
+        uint4* idst = reinterpret_cast<uint4*>(lds);
+        uint4* rdst = reinterpret_cast<uint4*>(env + L->lds.state);
+        uint4* sdst = reinterpret_cast<uint4*>(env + L->lds.scen);
+        uint4* adst = reinterpret_cast<uint4*>(env + L->lds.act);
+        const int rounds = max(max((img16 + UI * nthr - 1) / (UI * nthr), (rec16 + UR * 64 - 1) / (UR * 64)),
+                               max((scn16 + US * 64 - 1) / (US * 64), (act16 + UA * 64 - 1) / (UA * 64)));
+        // the step's calendar position, read from the record in HBM so the
+        // calendar row loads go out while the burst is in flight
+        const bool stepping = active && P.mode == KMODE_STEP;
+        int kk = 0, j1 = 0;
+        if (stepping) {
+            const int* ipg = reinterpret_cast<const int*>(c.rec + L->st.iplant);
+            kk = ipg[PI_STEP_INDEX];
+            j1 = ed.start + ipg[PI_STEP] + 1;
+        }
+        for (int rd = 0; rd < rounds; rd++) {
+            uint4 pi[UI], pr[UR], ps[US], pa[UA];
+            part_load(pi, isrc, img16, tid, nthr, rd * UI * nthr);
+            part_load(pr, rsrc, rec16, l, 64, rd * UR * 64);
+            part_load(ps, ssrc, scn16, l, 64, rd * US * 64);
+            part_load(pa, asrc, act16, l, 64, rd * UA * 64);
+            if (rd == 0 && stepping) {
+                const RowVals rv = row_issue<W>(c, __builtin_amdgcn_readfirstlane(kk),
+                                                __builtin_amdgcn_readfirstlane(j1));
+                part_store(pi, idst, img16, tid, nthr, 0);
+                part_store(pr, rdst, rec16, l, 64, 0);
+                part_store(ps, sdst, scn16, l, 64, 0);
+                part_store(pa, adst, act16, l, 64, 0);
+                row_store<W>(c, rv);
+                continue;
+            }
+            part_store(pi, idst, img16, tid, nthr, rd * UI * nthr);
+            part_store(pr, rdst, rec16, l, 64, rd * UR * 64);
+            part_store(ps, sdst, scn16, l, 64, rd * US * 64);
+            part_store(pa, adst, act16, l, 64, rd * UA * 64);
+        }
+        if (active && P.mode == KMODE_STEP) {
+            const SBK_C uint4* src = reinterpret_cast<const SBK_C uint4*>(L->pinfo);
+            for (int i = l; i < L->n_pass; i += W) reinterpret_cast<uint4*>(c.prec)[i] = src[i];
+        }
     }
-    __syncthreads();
+    __syncthreads();   // the only workgroup barrier: the layout image is shared
+    if (!active) return;
     STAMP(1);
     float* obs_row = P.obs + (size_t)e * 1024;
     if (P.mode == KMODE_RESET) {
         env_reset<W>(c, ed.start, obs_row);
-        if (threadIdx.x == 0) {
+        if (ln() == 0) {
             c.ip[PI_STEP] = 0;
             c.ip[PI_STEPS_TOTAL] = 0;
             c.ip[PI_EPISODES] = 0;
             c.plant[PF_REW_SUM] = 0.0;
         }
-        __syncthreads();
-        copy16<W>(c.rec, lds + L->lds.state, L->st.bytes);
+        esync();
+        store16<W>(c.rec, env + L->lds.state, L->st.bytes);
         return;
     }
     // host-visible log fields (trainer may clear them between steps)
     Log* hlog = nullptr;
     float lg_ret = 0.f, lg_mean = 0.f;
-    if (P.host_env && threadIdx.x == 0) {
+    if (P.host_env && ln() == 0) {
         hlog = reinterpret_cast<Log*>(reinterpret_cast<unsigned char*>(P.host_env) + (size_t)e * P.env_stride
                                       + P.log_offset);
         lg_ret = __hip_atomic_load(&hlog->episode_return, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         lg_mean = __hip_atomic_load(&hlog->reward_mean, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
-    decode_apply<W>(c, P.actions + (size_t)e * 272);
+    decode_apply<W>(c);
     STAMP(2);
-    step_pre<W>(c);
+    step_pre<W>(c, P);
     STAMP(3);
     field_step<W>(c, P);
     STAMP(6);
     step_post<W>(c);
     STAMP(7);
     const int step = c.ip[PI_STEP] + 1;
-    const int j = ed.start + step;
-    write_obs<W>(c, j, obs_row);
-    __syncthreads();
+    write_obs<W>(c, obs_row, c.misc[MS_ROW + RW_AMB_J], c.misc + MS_AUX);
+    esync();
     STAMP(8);
-    occupancy_advance<W>(c, c.S->occ_hour[j], c.S->occ_work[j]);
+    occupancy_advance<W>(c, (int)c.misc[MS_ROW + RW_OCC_HOUR_J], (int)c.misc[MS_ROW + RW_OCC_WORK_J]);
     STAMP(9);
-    const double rew = reward<W>(c, j);
+    const double rew = reward<W>(c);
     STAMP(10);
     const float r = (float)rew;
     const int done = step >= ed.max_steps;
-    if (threadIdx.x == 0) {
+    if (ln() == 0) {
         P.rewards[e] = r * P.reward_scale;
         P.terminals[e] = done ? 1.0f : 0.0f;
         c.ip[PI_STEP] = step;
@@ -1313,11 +1521,11 @@ __global__ __launch_bounds__(W) void step_kernel(KParams P) {
         }
         if (done) c.ip[PI_EPISODES] += 1;
     }
-    __syncthreads();
+    esync();
     if (done) env_reset<W>(c, ed.start, obs_row);
-    __syncthreads();
+    esync();
     STAMP(11);
-    copy16<W>(c.rec, lds + L->lds.state, L->st.bytes);
+    store16<W>(c.rec, env + L->lds.state, L->st.bytes);
     STAMP(12);
 }
 
@@ -1364,10 +1572,11 @@ __global__ void gen_actions_kernel(float* actions, const int* n_cont, const int*
 }  // namespace sbk
 
 // ---------------------------------------------------------------- launchers
-extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int width, int lds_bytes, hipStream_t s) {
+// threads: 64 per env of a tile (at most 8 envs per workgroup).
+extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int threads, int lds_bytes, hipStream_t s) {
     using namespace sbk;
-    if (width != 64) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(step_kernel<64>, dim3(n_blocks), dim3(64), lds_bytes, s, *p);
+    if (threads < 64 || threads > 512 || threads % 64) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(step_kernel<64>, dim3(n_blocks), dim3(threads), lds_bytes, s, *p);
     return (int)hipGetLastError();
 }
 

@@ -25,7 +25,7 @@
 #include "sbenv.h"
 #include "sbenv_internal.h"
 
-extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int width, int lds_bytes, hipStream_t s);
+extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int threads, int lds_bytes, hipStream_t s);
 extern "C" int sbk_set_lds_limit(int width, int bytes);
 extern "C" int sbk_launch_gen_actions(float* actions, const int* n_cont, const int* n_disc, int n_envs,
                                       uint64_t seed, uint32_t step, hipStream_t s);
@@ -114,6 +114,23 @@ std::string structural_key(const sbh::Blob& b) {
 
 template <class T>
 std::vector<T> take(const T* p, uint64_t n) { return p ? std::vector<T>(p, p + n) : std::vector<T>(); }
+
+// Packs tables into one byte image with 16-byte aligned sections (the LDS
+// images the step kernel stages in one burst).
+struct ImgBuilder {
+    std::vector<unsigned char> bytes;
+    template <class T>
+    int add(const std::vector<T>& v) {
+        const size_t off = (bytes.size() + 15) & ~(size_t)15;
+        bytes.resize(off + v.size() * sizeof(T), 0);
+        if (!v.empty()) memcpy(bytes.data() + off, v.data(), v.size() * sizeof(T));
+        return (int)off;
+    }
+    int finish() {
+        bytes.resize((bytes.size() + 15) & ~(size_t)15, 0);
+        return (int)bytes.size();
+    }
+};
 
 enum { SOLVE_AUTO = 0, SOLVE_LU = 1, SOLVE_RELAX = 2 };
 
@@ -257,19 +274,24 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     S.bytes = align_up(o, 16);
     S.mt = S.bytes;
     S.record_bytes = align_up(S.bytes + 4 * SBK_MT_N, 256);
-    // LDS
+    // per-env LDS region: record image + MT words (one staged copy), scenario
+    // image, action row, then scratch
     sbk::LdsLayout& Ls = D.lds;
     int l = 0;
     Ls.state = 0; l = S.bytes;
+    Ls.mt = l; l += 4 * SBK_MT_N; l = align_up(l, 16);
+    Ls.scen = l; l += align_up(8 * n, 16) + 8 * 84;
+    Ls.act = l; l += 4 * SB_ACT;
     // slots: the LU entries and vector, or (relaxation) the node heat inputs
-    Ls.slots = l; Ls.mt = l; l += std::max(8 * (relax ? n : P.n_slots), 4 * (SBK_MT_N + 1)); l = align_up(l, 16);
+    Ls.slots = l; l += 8 * (relax ? n : P.n_slots); l = align_up(l, 16);
     Ls.zq = l; l += 8 * nz;
     Ls.vtmp = l; l += 8 * 3 * nv;
     Ls.g = l; l += 8 * std::max(k, 1);
     Ls.tair = l; l += 8 * std::max(k, 1);
     Ls.atmp = l; l += 8 * 8 * na;
     Ls.red = l; l += 8 * 64;
-    Ls.misc = l; l += 8 * 32;
+    Ls.misc = l; l += 8 * sbk::MS_SIZE;
+    Ls.obsx = l; l += 8 * (sbk::OX_AHU + 4 * na);
     Ls.iscr = l; l += 4 * (width / 64 + 8);
     l = align_up(l, 16);
     Ls.prec = l; l += 16 * D.n_pass;
@@ -335,12 +357,137 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     O["f_idx"] = A.vec(take(fi, n_dev));
     O["f_mean"] = A.vec(take(fm, n_dev));
     O["f_sd"] = A.vec(fsd);
+    // the layout image the step kernel stages into LDS (one copy per workgroup)
+    {
+        ImgBuilder I;
+        sbk::ImgLayout& G = D.img;
+        uint64_t c2 = 0;
+        const double* sc = b.f64("solar_gain_coeff", &c2);
+        std::vector<double> solar(n, 0.0);
+        if (sc && (int)c2 == n) solar.assign(sc, sc + n);
+        G.cap = I.add(take(b.f64("capacitance_rate"), n));
+        G.mcoup = I.add(take(b.f64("mass_coupling"), n));
+        G.mret = I.add(take(b.f64("mass_retained"), n));
+        G.mgain = I.add(take(b.f64("mass_gained"), n));
+        G.solar_c = I.add(solar);
+        G.rx_diag = I.add(R.ok ? std::vector<double>(R.diag.begin(), R.diag.begin() + n) : std::vector<double>(n, 1.0));
+        G.zone_area = I.add(take(zone_area, nz));
+        G.vav_area = I.add(vav_area);
+        G.vav_c = I.add(take(vav_c, 9 * nv));
+        G.ahu_c = I.add(take(ahu_c, 9 * na));
+        G.act_mn = I.add(take(mn, n_act));
+        G.act_mx = I.add(take(mx, n_act));
+        G.act_mnr = I.add(take(mnr, n_act));
+        G.act_mxr = I.add(take(mxr, n_act));
+        // action targets (complete_port/csim/sb_sim.c:220-244): AHU supply
+        // temperature / fan static / recirculation (clamped to its maximum) /
+        // run; VAV damper / reheat commands (clamped to [0, 1], with their set
+        // flags); boiler setpoint / pump head (bar -> m) / HWS and pump run
+        std::vector<uint32_t> adst(n_act), aaux(n_act, 0u);
+        std::vector<double> ahi(n_act, 0.0);
+        std::vector<uint8_t> aflag(n_act, 0);
+        for (int i = 0; i < n_act; i++) {
+            const int ix = aidx[i], ak = act[i];
+            if (kind[i] == 0) {
+                if (ix < 0 || ix >= na) return (*err = "action AHU index out of range"), false;
+                if (ak == 0) adst[i] = (uint32_t)(S.sat + 8 * ix);
+                else if (ak == 1) adst[i] = (uint32_t)(S.fan + 8 * ix);
+                else if (ak == 2) {
+                    adst[i] = (uint32_t)(S.recirc + 8 * ix);
+                    aflag[i] = sbk::ACT_CLAMP;
+                    ahi[i] = ahu_c[ix * 9 + 3];
+                } else adst[i] = (uint32_t)(S.run + 4 * ix) | ACT_I32;
+            } else if (kind[i] == 1) {
+                if (ix < 0 || ix >= nv) return (*err = "action VAV index out of range"), false;
+                aflag[i] = sbk::ACT_CLAMP;
+                ahi[i] = 1.0;
+                if (ak == 0) { adst[i] = (uint32_t)(S.dcmd + 8 * ix); aaux[i] = (uint32_t)(S.dcmd_set + ix) | ACT_AUX_U8; }
+                else { adst[i] = (uint32_t)(S.rcmd + 8 * ix); aaux[i] = (uint32_t)(S.rcmd_set + ix) | ACT_AUX_U8; }
+            } else {
+                if (ak == 0) adst[i] = (uint32_t)(S.plant + 8 * sbk::PF_BOILER_SP);
+                else if (ak == 1) { adst[i] = (uint32_t)(S.plant + 8 * sbk::PF_PUMP_HEAD); aflag[i] = sbk::ACT_PUMP_HEAD; }
+                else {
+                    adst[i] = (uint32_t)(S.iplant + 4 * sbk::PI_HWS_RUN) | ACT_I32;
+                    aaux[i] = (uint32_t)(S.iplant + 4 * sbk::PI_PUMP_RUN) | ACT_AUX_I32;
+                }
+            }
+        }
+        G.act_hi = I.add(ahi);
+        G.act_dst = I.add(adst);
+        G.act_aux = I.add(aaux);
+        G.act_flags = I.add(aflag);
+        G.f_mean = I.add(take(fm, n_dev));
+        G.f_sd = I.add(fsd);
+        G.rx_air = I.add(R.ok ? std::vector<int>(R.air_col.begin(), R.air_col.begin() + n) : std::vector<int>(n, -1));
+        G.pos = I.add(P.pos);
+        G.zone_cell_off = I.add(zoff);
+        G.zone_cells = I.add(zcells);
+        G.vz_off = I.add(take(vz_off, nv + 1));
+        G.vz_idx = I.add(take(vz_idx, vz_off[nv]));
+        G.vav_ahu = I.add(take(vav_ahu, nv));
+        G.coupled = I.add(take(coupled, k));
+        G.zone_col_off = I.add(zcol_off);
+        G.zone_cols = I.add(zcols);
+        G.act_src = I.add(src);
+        G.air_slot = I.add(P.air_slot);
+        G.air_node = I.add(P.air_node);
+        G.is_room = I.add(is_room);
+        G.act_disc = I.add(take(disc, n_act));
+        // observation sources (the value each field reads; sb_obs.c:49-64 and
+        // the device kinds of bake_env.py:228-248): AHU, VAV, then plant fields
+        std::vector<uint32_t> fsrc(n_dev);
+        for (int i = 0; i < n_dev; i++) {
+            const int kd = fk[i], id = fo[i], ix = fi[i];
+            auto env_f64 = [&](int off) { return (uint32_t)off; };
+            auto env_i32 = [&](int off) { return (uint32_t)off | OBS_SRC_I32; };
+            const int ox = Ls.obsx;
+            uint32_t v;
+            if (kd == 0) {
+                if (ix < 0 || ix >= na) return (*err = "observation AHU index out of range"), false;
+                const int ax = ox + 8 * (sbk::OX_AHU + 4 * ix);
+                switch (id) {
+                case 0: v = env_i32(S.coolreq + 4 * ix); break;
+                case 1: v = env_f64(ax); break;
+                case 2: v = env_f64(ax + 8); break;
+                case 3: v = env_f64(S.sat + 8 * ix); break;
+                case 4: case 7: v = env_i32(S.run + 4 * ix); break;
+                case 5: v = env_f64(ax + 16); break;
+                case 6: v = env_f64(ax + 24); break;
+                case 8: v = env_f64(S.recirc + 8 * ix); break;
+                default: v = env_f64(ox + 8 * sbk::OX_AMB);
+                }
+            } else if (kd == 1) {
+                if (ix < 0 || ix >= nv) return (*err = "observation VAV index out of range"), false;
+                switch (id) {
+                case 0: v = env_f64(S.reheat + 8 * ix); break;
+                case 1: v = env_f64(S.damper + 8 * ix); break;
+                case 2: v = (uint32_t)(G.vav_c + 8 * 9 * ix) | OBS_SRC_IMG; break;
+                case 3: v = env_f64(S.coolsp + 8 * ix); break;
+                case 4: v = env_f64(S.heatsp + 8 * ix); break;
+                default: v = env_f64(S.sensing + 8 * ix);
+                }
+            } else {
+                switch (id) {
+                case 0: case 2: v = env_f64(ox + 8 * sbk::OX_DP); break;
+                case 1: v = env_f64(S.plant + 8 * sbk::PF_BOILER_CUR); break;
+                case 3: case 5: v = env_i32(S.iplant + 4 * sbk::PI_HWS_RUN); break;
+                case 4: v = env_i32(S.iplant + 4 * sbk::PI_HWS_REQ); break;
+                default: v = env_f64(S.plant + 8 * sbk::PF_BOILER_SP);
+                }
+            }
+            fsrc[i] = v;
+        }
+        G.f_src = I.add(fsrc);
+        G.bytes = I.finish();
+        O["img"] = A.vec(I.bytes);
+    }
     return true;
 }
 
 void patch_layout(HostLayout* H, unsigned char* d) {
     sbk::DevLayout& D = H->dev;
     auto& O = H->off;
+    D.img_src = at<unsigned char>(d, O["img"]);
     D.rx_diag = at<double>(d, O["rx_diag"]);
     D.rx_air = at<int>(d, O["rx_air"]);
     D.rx_val = at<double>(d, O["rx_val"]);
@@ -478,6 +625,17 @@ bool make_scen(const sbh::Blob& b, const HostLayout& Lh, HostScen* H, Arena& A, 
     O["elec_we"] = A.vec(take(ewe, 24));
     O["elec_co2"] = A.vec(take(eco, 24));
     O["gas_price"] = A.vec(take(gp, 12));
+    {
+        ImgBuilder I;
+        D.img.dirx = I.add(dirx);
+        D.img.elec_wk = I.add(take(ewk, 24));
+        D.img.elec_we = I.add(take(ewe, 24));
+        D.img.elec_co2 = I.add(take(eco, 24));
+        D.img.gas_price = I.add(take(gp, 12));
+        D.img.bytes = I.finish();
+        if (D.img.bytes > align_up(8 * n, 16) + 8 * 84) return (*err = "scenario image larger than its LDS region"), false;
+        O["img"] = A.vec(I.bytes);
+    }
     D.n1 = (int)n1;
     D.gas_co2 = b.f64_1("gas_carbon_rate", 0.0);
     for (int i = 0; i < 8; i++) D.rw[i] = rw[i];
@@ -526,6 +684,7 @@ bool make_scen(const sbh::Blob& b, const HostLayout& Lh, HostScen* H, Arena& A, 
 void patch_scen(HostScen* H, unsigned char* d) {
     sbk::DevScen& D = H->dev;
     auto& O = H->off;
+    D.img_src = at<unsigned char>(d, O["img"]);
     D.amb = at<double>(d, O["amb"]);
     D.solar_i = at<double>(d, O["solar_i"]);
     D.comfort = at<double>(d, O["comfort"]);
@@ -551,6 +710,10 @@ void patch_scen(HostScen* H, unsigned char* d) {
 // ---------------------------------------------------------------- vec
 struct Vec {
     int n = 0, width = 64, lds_bytes = 0;
+    int epb = 4;                              // envs (wavefronts) per workgroup
+    int img_lds = 0;                          // LDS bytes of the largest layout image
+    std::vector<sbk::Tile> tiles;
+    sbk::Tile* d_tiles = nullptr;
     float reward_scale = 1.0f;
     Env* envs = nullptr;
     std::vector<std::string> paths;           // ordered scenario list
@@ -580,6 +743,8 @@ sbk::KParams params(Vec* v, int mode) {
     sbk::KParams p{};
     p.envs = v->d_envs;
     p.order = v->d_order;
+    p.tiles = v->d_tiles;
+    p.img_lds = v->img_lds;
     p.layouts = v->d_layouts;
     p.scens = v->d_scens;
     p.state = v->d_state;
@@ -596,11 +761,12 @@ sbk::KParams params(Vec* v, int mode) {
     return p;
 }
 
-void launch(Vec* v, int mode) {
-    sbk::KParams p = params(v, mode);
-    int rc = sbk_launch_step(&p, v->n, v->width, v->lds_bytes, g_stream);
+void launch_params(Vec* v, const sbk::KParams& p) {
+    int rc = sbk_launch_step(&p, (int)v->tiles.size(), v->width * v->epb, v->lds_bytes, g_stream);
     if (rc != 0) die(std::string("step kernel launch failed: ") + hipGetErrorString((hipError_t)rc));
 }
+
+void launch(Vec* v, int mode) { launch_params(v, params(v, mode)); }
 
 Vec* vec_of(Env* envs) {
     if (!envs || !envs[0].vec) die("env array was not created by puf_vec_create");
@@ -781,30 +947,54 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
         }
     }
     v->state_bytes = state_off;
-    // launch order: largest layouts first
+    // tiles: envs of one layout share a workgroup (one wavefront each) and the
+    // layout image it stages; largest layouts first, then by scenario
     v->order.resize(n);
     for (int i = 0; i < n; i++) v->order[i] = i;
     std::stable_sort(v->order.begin(), v->order.end(), [&](int a, int b) {
-        return v->layouts[v->desc[a].layout].dev.lds.bytes > v->layouts[v->desc[b].layout].dev.lds.bytes;
+        const sbk::EnvDesc &da = v->desc[a], &db = v->desc[b];
+        const int na_ = v->layouts[da.layout].dev.n, nb_ = v->layouts[db.layout].dev.n;
+        if (na_ != nb_) return na_ > nb_;
+        if (da.layout != db.layout) return da.layout < db.layout;
+        return da.scen < db.scen;
     });
+    {
+        const int epb_kw = (int)kw(kwargs, "envs_per_block", 4.0f);
+        if (epb_kw < 1 || epb_kw > 8) die("env.envs_per_block must be 1..8");
+        int img = 0, reg = 0;
+        for (auto& L : v->layouts) {
+            img = std::max(img, L.dev.img.bytes);
+            reg = std::max(reg, L.dev.lds.bytes);
+        }
+        const int limit = 160 * 1024;
+        int epb = epb_kw;
+        while (epb > 1 && img + epb * reg > limit) epb--;
+        if (img + reg > limit) die("layout needs more LDS than a workgroup has");
+        v->epb = epb;
+        v->img_lds = img;
+        v->lds_bytes = img + epb * reg;
+        for (int i = 0; i < n;) {
+            const int lay = v->desc[v->order[i]].layout;
+            int j = i;
+            while (j < n && j - i < epb && v->desc[v->order[j]].layout == lay) j++;
+            v->tiles.push_back(sbk::Tile{lay, i, j - i, 0});
+            i = j;
+        }
+    }
     // ---- upload tables
     hip_ok(hipMalloc(&v->d_arena, A.host.size()), "hipMalloc(tables)");
     hip_ok(hipMemcpy(v->d_arena, A.host.data(), A.host.size(), hipMemcpyHostToDevice), "upload tables");
     std::vector<sbk::DevLayout> dl;
-    int lds = 0;
     for (auto& L : v->layouts) {
         patch_layout(&L, v->d_arena);
         dl.push_back(L.dev);
-        lds = std::max(lds, L.dev.lds.bytes);
     }
     std::vector<sbk::DevScen> ds;
     for (auto& S : v->scens) {
         patch_scen(&S, v->d_arena);
         ds.push_back(S.dev);
     }
-    v->lds_bytes = lds;
-    if (lds > 160 * 1024) die("layout needs more LDS than a workgroup has");
-    if (lds > 64 * 1024) hip_ok((hipError_t)sbk_set_lds_limit(v->width, lds), "LDS limit");
+    if (v->lds_bytes > 64 * 1024) hip_ok((hipError_t)sbk_set_lds_limit(v->width, v->lds_bytes), "LDS limit");
     hip_ok(hipMalloc(&v->d_layouts, sizeof(sbk::DevLayout) * dl.size()), "hipMalloc(layouts)");
     hip_ok(hipMemcpy(v->d_layouts, dl.data(), sizeof(sbk::DevLayout) * dl.size(), hipMemcpyHostToDevice), "upload");
     hip_ok(hipMalloc(&v->d_scens, sizeof(sbk::DevScen) * ds.size()), "hipMalloc(scens)");
@@ -813,6 +1003,9 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
     hip_ok(hipMemcpy(v->d_envs, v->desc.data(), sizeof(sbk::EnvDesc) * n, hipMemcpyHostToDevice), "upload");
     hip_ok(hipMalloc(&v->d_order, sizeof(int) * n), "hipMalloc(order)");
     hip_ok(hipMemcpy(v->d_order, v->order.data(), sizeof(int) * n, hipMemcpyHostToDevice), "upload");
+    hip_ok(hipMalloc(&v->d_tiles, sizeof(sbk::Tile) * v->tiles.size()), "hipMalloc(tiles)");
+    hip_ok(hipMemcpy(v->d_tiles, v->tiles.data(), sizeof(sbk::Tile) * v->tiles.size(), hipMemcpyHostToDevice),
+           "upload");
     {
         std::vector<int> nc(n), nd(n);
         for (int i = 0; i < n; i++) {
@@ -912,6 +1105,7 @@ void puf_close(Env* envs) {
     (void)hipFree(v->d_scens);
     (void)hipFree(v->d_envs);
     (void)hipFree(v->d_order);
+    (void)hipFree(v->d_tiles);
     (void)hipFree(v->d_ncont);
     (void)hipFree(v->d_ndisc);
     (void)hipHostFree(v->envs);
@@ -978,8 +1172,9 @@ void sbx_vec_info(Env* envs, SbxVecInfo* out) {
     out->n_envs = v->n;
     out->n_layouts = (int)v->layouts.size();
     out->n_scenarios = (int)v->scens.size();
-    out->block = v->width;
+    out->block = v->width * v->epb;
     out->lds_bytes = v->lds_bytes;
+    out->envs_per_block = v->epb;
     for (auto& L : v->layouts) out->max_nodes = std::max(out->max_nodes, L.dev.n);
     out->bytes_per_step = v->bytes_per_step;
     out->flops_per_step = v->flops_per_step;
@@ -1032,8 +1227,7 @@ int sbx_phase_times(Env* envs, double* mean_us, double* max_us, int n_phases) {
     hip_ok(hipMemset(d, 0, count * sizeof(unsigned long long)), "memset(stamps)");
     sbk::KParams p = params(v, sbk::KMODE_STEP);
     p.phase_ts = d;
-    int rc = sbk_launch_step(&p, v->n, v->width, v->lds_bytes, g_stream);
-    if (rc != 0) die("step kernel launch failed");
+    launch_params(v, p);
     hip_ok(hipStreamSynchronize(g_stream), "stamps sync");
     std::vector<unsigned long long> h(count);
     hip_ok(hipMemcpy(h.data(), d, count * sizeof(unsigned long long), hipMemcpyDeviceToHost), "stamps copy");
@@ -1056,6 +1250,22 @@ int sbx_phase_times(Env* envs, double* mean_us, double* max_us, int n_phases) {
     return n_phases;
 }
 
+int sbx_phase_stamps(Env* envs, unsigned long long* out, int cap) {
+    Vec* v = vec_of(envs);
+    const size_t count = (size_t)v->n * SBK_NSTAMP;
+    if (!out || cap < (int)count) return -1;
+    unsigned long long* d = nullptr;
+    hip_ok(hipMalloc(&d, count * sizeof(unsigned long long)), "hipMalloc(stamps)");
+    hip_ok(hipMemset(d, 0, count * sizeof(unsigned long long)), "memset(stamps)");
+    sbk::KParams p = params(v, sbk::KMODE_STEP);
+    p.phase_ts = d;
+    launch_params(v, p);
+    hip_ok(hipStreamSynchronize(g_stream), "stamps sync");
+    hip_ok(hipMemcpy(out, d, count * sizeof(unsigned long long), hipMemcpyDeviceToHost), "stamps copy");
+    (void)hipFree(d);
+    return (int)count;
+}
+
 int sbx_pass_times(Env* envs, int env, long long* cycles, int cap) {
     Vec* v = vec_of(envs);
     if (env < 0 || env >= v->n) return -1;
@@ -1063,17 +1273,13 @@ int sbx_pass_times(Env* envs, int env, long long* cycles, int cap) {
     // relaxation: a stamp at entry, after the setup and after every sweep
     const int np = relax ? SBK_RX_MAXIT + 1 : v->layouts[v->desc[env].layout].dev.n_pass;
     if (cap < np) return -1;
-    int block = -1;
-    for (int b = 0; b < v->n; b++)
-        if (v->order[b] == env) block = b;
     unsigned long long* d = nullptr;
     hip_ok(hipMalloc(&d, (size_t)(np + 1) * sizeof(unsigned long long)), "hipMalloc(pass stamps)");
     hip_ok(hipMemset(d, 0, (size_t)(np + 1) * sizeof(unsigned long long)), "memset(pass stamps)");
     sbk::KParams p = params(v, sbk::KMODE_STEP);
     p.pass_ts = d;
-    p.pass_ts_block = block;
-    int rc = sbk_launch_step(&p, v->n, v->width, v->lds_bytes, g_stream);
-    if (rc != 0) die("step kernel launch failed");
+    p.pass_ts_env = env;
+    launch_params(v, p);
     hip_ok(hipStreamSynchronize(g_stream), "pass stamps sync");
     std::vector<unsigned long long> h(np + 1);
     hip_ok(hipMemcpy(h.data(), d, h.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost), "copy");

@@ -53,7 +53,8 @@ class Dict(ctypes.Structure):
 class SbxVecInfo(ctypes.Structure):
     _fields_ = [("n_envs", ctypes.c_int), ("n_layouts", ctypes.c_int), ("n_scenarios", ctypes.c_int),
                 ("block", ctypes.c_int), ("lds_bytes", ctypes.c_int), ("max_nodes", ctypes.c_int),
-                ("bytes_per_step", ctypes.c_double), ("flops_per_step", ctypes.c_double)]
+                ("bytes_per_step", ctypes.c_double), ("flops_per_step", ctypes.c_double),
+                ("envs_per_block", ctypes.c_int)]
 
 
 class SbxPlan(ctypes.Structure):
@@ -77,7 +78,7 @@ class SbxPlan(ctypes.Structure):
 EXPORTS = [
     "dict_find", "dict_set", "puf_vec_create", "puf_bind_stream", "puf_init", "puf_reset", "puf_step",
     "puf_render", "puf_close", "puf_log", "puf_live_log", "puf_mask_init", "sbx_gen_actions",
-    "sbx_vec_info", "sbx_env_state", "sbx_time_step", "sbx_phase_times", "sbx_pass_times", "sbx_solve_info",
+    "sbx_vec_info", "sbx_env_state", "sbx_time_step", "sbx_phase_times", "sbx_phase_stamps", "sbx_pass_times", "sbx_solve_info",
     "sbx_env_meta", "sbx_scenario_path",
     "sbx_plan_layout", "sbx_plan_free", "sbx_last_error", "sbx_version",
 ]
@@ -115,6 +116,8 @@ def lib() -> ctypes.CDLL:
         L.sbx_phase_times.restype = ctypes.c_int
         L.sbx_pass_times.argtypes = [ctypes.POINTER(Env), ctypes.c_int, P, ctypes.c_int]
         L.sbx_pass_times.restype = ctypes.c_int
+        L.sbx_phase_stamps.argtypes = [ctypes.POINTER(Env), P, ctypes.c_int]
+        L.sbx_phase_stamps.restype = ctypes.c_int
         L.sbx_solve_info.argtypes = [ctypes.POINTER(Env), ctypes.c_int, P]
         L.sbx_solve_info.restype = ctypes.c_int
         L.sbx_env_meta.argtypes = [ctypes.POINTER(Env), ctypes.c_int, ctypes.POINTER(ctypes.c_int),
@@ -263,6 +266,13 @@ class VecEnv:
         mean, mx = np.zeros(k), np.zeros(k)
         n = self.L.sbx_phase_times(self.envs, mean.ctypes.data_as(P), mx.ctypes.data_as(P), k)
         return {self.PHASES[i]: (float(mean[i]), float(mx[i])) for i in range(n)}
+
+    def phase_stamps(self) -> np.ndarray:
+        """Raw wall-clock stamps (n, 16) of one step; stamps 0..12 bound the phases."""
+        buf = np.zeros(self.n * 16, np.uint64)
+        if self.L.sbx_phase_stamps(self.envs, buf.ctypes.data_as(P), buf.size) < 0:
+            raise RuntimeError("sbx_phase_stamps failed")
+        return buf.reshape(self.n, 16)
 
     def pass_times(self, i: int) -> np.ndarray:
         """Shader-clock cycles of each solve pass of env i for one step."""

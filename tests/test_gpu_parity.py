@@ -271,11 +271,13 @@ def test_gpu_episode_total_vs_reference(golden_index, tmp_path, solver):
     vec.close()
 
 
-@pytest.mark.parametrize("solver", SOLVERS)
-def test_gpu_batch_invariance(mixed_dir, solver):
-    """An env steps bit-identically alone and inside a 60-env mixed batch."""
-    say(f"batch invariance ({solver})")
-    big = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=50, solver=solver)
+@pytest.mark.parametrize("solver,epb", [("relax", 4), ("lu", 4), ("relax", 1), ("relax", 8)])
+def test_gpu_batch_invariance(mixed_dir, solver, epb):
+    """An env steps bit-identically alone and inside a 60-env mixed batch whose
+    workgroups hold `epb` envs each (8 is cut to what LDS allows)."""
+    say(f"batch invariance ({solver}, {epb} envs per workgroup)")
+    big = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=50, solver=solver, envs_per_block=epb)
+    assert 1 <= big.info().envs_per_block <= epb
     path, _, _ = big.meta(0)
     small = E.VecEnv(1, blob=path, max_steps=50, solver=solver)
     big.reset()
