@@ -17,6 +17,7 @@
 #define SBK_NAUX_MAX 16
 #define SBK_KMAX 48      // terms per lane per pass (matches the planner)
 #define SBK_NSTAMP 16    // phase stamps per workgroup when phase timing is on
+#define SBK_VPL 4        // VAVs (and coupled columns) per lane: at most 256 per env
 #define SBK_RX_RPL 4     // relaxation rows per lane (matches the planner)
 #define SBK_RX_ROWS 256  // padded relaxation rows
 #define SBK_RX_TERMS 8   // relaxation off-diagonal entries per row
@@ -90,6 +91,8 @@ struct ImgLayout {
     // i32
     int rx_air, pos;                                        // [n]
     int zone_cell_off, zone_cells, vz_off, vz_idx, vav_ahu, coupled, zone_col_off, zone_cols;
+    int ahu_vav_off, ahu_vavs;     // [na + 1], [nv]: each AHU's VAVs, ascending
+    int ahu_col_off, ahu_cols;     // [na + 1], [k]: each AHU's coupled columns, ascending
     int act_src, act_dst, act_aux;                          // [n_act] (dst/aux: ACT_*)
     int air_slot, air_node;                                 // [k]
     // u8

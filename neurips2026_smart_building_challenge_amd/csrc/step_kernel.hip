@@ -125,6 +125,61 @@ __device__ __forceinline__ int wave_isum(int v) {
     return __builtin_amdgcn_readlane(v, 63);
 }
 
+// Sum, minimum and maximum of three per-lane values in one pass (the three
+// DPP chains are independent, so their latencies overlap).
+__device__ __forceinline__ void wave_sum_min_max(double& s, double& mn, double& mx) {
+    const double zero = 0.0, pinf = __longlong_as_double(0x7FF0000000000000ll);
+    const double ninf = __longlong_as_double((long long)0xFFF0000000000000ull);
+#define SBK_STEP3(CTRL, ROWS)                                 \
+    s = s + dpp_d<CTRL, ROWS>(zero, s);                       \
+    mn = fmin(mn, dpp_d<CTRL, ROWS>(pinf, mn));               \
+    mx = fmax(mx, dpp_d<CTRL, ROWS>(ninf, mx));
+    SBK_STEP3(DPP_QUAD_1032, 0xF)
+    SBK_STEP3(DPP_QUAD_2301, 0xF)
+    SBK_STEP3(DPP_ROW_HALF_MIRROR, 0xF)
+    SBK_STEP3(DPP_ROW_MIRROR, 0xF)
+    SBK_STEP3(DPP_ROW_BCAST15, 0xA)
+    SBK_STEP3(DPP_ROW_BCAST31, 0xC)
+#undef SBK_STEP3
+    s = lane63_d(s);
+    mn = lane63_d(mn);
+    mx = lane63_d(mx);
+}
+
+// Sums of three per-lane values in one pass.
+__device__ __forceinline__ void wave_sum3(double& a, double& b, double& d) {
+#define SBK_STEP3S(CTRL, ROWS)                \
+    a = a + dpp_d<CTRL, ROWS>(0.0, a);        \
+    b = b + dpp_d<CTRL, ROWS>(0.0, b);        \
+    d = d + dpp_d<CTRL, ROWS>(0.0, d);
+    SBK_STEP3S(DPP_QUAD_1032, 0xF)
+    SBK_STEP3S(DPP_QUAD_2301, 0xF)
+    SBK_STEP3S(DPP_ROW_HALF_MIRROR, 0xF)
+    SBK_STEP3S(DPP_ROW_MIRROR, 0xF)
+    SBK_STEP3S(DPP_ROW_BCAST15, 0xA)
+    SBK_STEP3S(DPP_ROW_BCAST31, 0xC)
+#undef SBK_STEP3S
+    a = lane63_d(a);
+    b = lane63_d(b);
+    d = lane63_d(d);
+}
+
+// Sums of two per-lane values in one pass.
+__device__ __forceinline__ void wave_sum2(double& a, double& b) {
+#define SBK_STEP2(CTRL, ROWS)                 \
+    a = a + dpp_d<CTRL, ROWS>(0.0, a);        \
+    b = b + dpp_d<CTRL, ROWS>(0.0, b);
+    SBK_STEP2(DPP_QUAD_1032, 0xF)
+    SBK_STEP2(DPP_QUAD_2301, 0xF)
+    SBK_STEP2(DPP_ROW_HALF_MIRROR, 0xF)
+    SBK_STEP2(DPP_ROW_MIRROR, 0xF)
+    SBK_STEP2(DPP_ROW_BCAST15, 0xA)
+    SBK_STEP2(DPP_ROW_BCAST31, 0xC)
+#undef SBK_STEP2
+    a = lane63_d(a);
+    b = lane63_d(b);
+}
+
 // Inclusive prefix sum over the wavefront.
 __device__ __forceinline__ int wave_iscan(int v) {
     v += dpp_i<DPP_ROW_SHR + 1>(0, v);
@@ -164,6 +219,7 @@ struct Tab {
     const double *act_mn, *act_mx, *act_mnr, *act_mxr, *act_hi, *f_mean, *f_sd;
     const int *rx_air, *pos, *zone_cell_off, *zone_cells, *vz_off, *vz_idx, *vav_ahu, *coupled;
     const int *zone_col_off, *zone_cols, *act_src, *air_slot, *air_node;
+    const int *ahu_vav_off, *ahu_vavs, *ahu_col_off, *ahu_cols;
     const uint32_t *f_src, *act_dst, *act_aux;
     const uint8_t *is_room, *act_disc, *act_flags;
 };
@@ -225,6 +281,10 @@ __device__ __forceinline__ void bind(Ctx& c, const unsigned char* img, unsigned 
     t.coupled = (const int*)(img + g.coupled);
     t.zone_col_off = (const int*)(img + g.zone_col_off);
     t.zone_cols = (const int*)(img + g.zone_cols);
+    t.ahu_vav_off = (const int*)(img + g.ahu_vav_off);
+    t.ahu_vavs = (const int*)(img + g.ahu_vavs);
+    t.ahu_col_off = (const int*)(img + g.ahu_col_off);
+    t.ahu_cols = (const int*)(img + g.ahu_cols);
     t.act_src = (const int*)(img + g.act_src);
     t.air_slot = (const int*)(img + g.air_slot);
     t.air_node = (const int*)(img + g.air_node);
@@ -777,33 +837,48 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
     }
     esync();
     STAMP(14);
-    // AHU return-air means and supply temperatures (sb_sim.c:382-387, :253-265)
+    // AHU return-air means and supply temperatures (sb_sim.c:382-387, :253-265):
+    // flow-factor sum over all VAVs, then one lane per AHU sums over its VAVs
+    // in VAV order (as csim accumulates them)
     double tmean = 0.0;
     if (S->conv_tmean) {
         double s = 0.0;
         for (int t = ln(); t < L->n; t += W) s += c.T[t];
         tmean = bsum<W>(s, c.red) / (double)L->n;
     }
+    // this lane's VAVs (v = lane + 64 r), kept in registers for the AHU sums
     double ffs_part = 0.0;
-    for (int v = ln(); v < nv; v += W) {
-        ffs_part += c.reheat[v] * c.t.vav_c[v * 9 + 1];
-        c.unres[v] = vav_unrestricted(c, v);
+    int vahu[SBK_VPL];
+    double vws[SBK_VPL], varea[SBK_VPL], vdm[SBK_VPL];
+#pragma unroll
+    for (int r = 0; r < SBK_VPL; r++) {
+        const int v = ln() + 64 * r;
+        vahu[r] = -1;
+        vws[r] = varea[r] = vdm[r] = 0.0;
+        if (v < nv) {
+            ffs_part += c.reheat[v] * c.t.vav_c[v * 9 + 1];
+            const double u = vav_unrestricted(c, v);
+            c.unres[v] = u;
+            const double area = c.t.vav_area[v];
+            vahu[r] = c.t.vav_ahu[v];
+            vdm[r] = u;
+            if (area > 0.0) {
+                vws[r] = c.sensing[v] * area;
+                varea[r] = area;
+            }
+        }
     }
     const double ffs = bsum<W>(ffs_part, c.red);
     for (int a = 0; a < na; a++) {
         double ws = 0.0, at = 0.0, dm = 0.0;
-        for (int v = ln(); v < nv; v += W) {
-            if (c.t.vav_ahu[v] != a) continue;
-            double area = c.t.vav_area[v];
-            if (area > 0.0) {
-                ws += c.sensing[v] * area;
-                at += area;
-            }
-            dm += c.unres[v];
+#pragma unroll
+        for (int r = 0; r < SBK_VPL; r++) {
+            const bool m = vahu[r] == a;
+            ws += m ? vws[r] : 0.0;
+            at += m ? varea[r] : 0.0;
+            dm += m ? vdm[r] : 0.0;
         }
-        ws = bsum<W>(ws, c.red);
-        at = bsum<W>(at, c.red);
-        dm = bsum<W>(dm, c.red);
+        wave_sum3(ws, at, dm);
         if (ln() == 0) {
             double rt = (at > 0.0) ? ws / at : tmean;
             double mixed = c.recirc[a] * rt + (1.0 - c.recirc[a]) * ambient;
@@ -830,8 +905,16 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
     STAMP(15);
     const double tf = total_flow_rate(c);
     const double iwt = c.plant[PF_BOILER_CUR];
-    // coupled columns: reheat energy, air-side conductance, AHU flow (sb_sim.c:410-436)
-    double rw_part = 0.0;
+    // coupled columns: reheat energy, air-side conductance, AHU flow (sb_sim.c:410-436),
+    // and the coil extremes for the boiler return temperature (sb_sim.c:495-499)
+    double total_rw = 0.0, cmin = 1e308, cmax = -1e308;
+    int cahu[SBK_VPL];
+    double cfd[SBK_VPL];
+#pragma unroll
+    for (int r = 0; r < SBK_VPL; r++) {
+        cahu[r] = -1;
+        cfd[r] = 0.0;
+    }
     for (int col = ln(); col < L->k; col += W) {
         int v = c.t.coupled[col];
         double g = 0.0, ta = 0.0, rw = 0.0, fd = 0.0;
@@ -869,42 +952,37 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
         c.tair[col] = ta;
         c.rwen[col] = rw;
         c.fdem[col] = fd;
-        rw_part += rw;
-    }
-    const double total_rw = bsum<W>(rw_part, c.red);
-    // coil extreme for the boiler return temperature (sb_sim.c:495-499)
-    double cmin = 1e308, cmax = -1e308;
-    for (int col = ln(); col < L->k; col += W) {
-        int v = c.t.coupled[col];
-        (void)v;
-        cmin = fmin(cmin, c.tair[col]);
-        cmax = fmax(cmax, c.tair[col]);
-    }
-    cmin = bmin<W>(cmin, c.red);
-    cmax = bmax<W>(cmax, c.red);
-    for (int a = 0; a < na; a++) {
-        double f = 0.0;
-        int cnt = 0;
-        for (int col = ln(); col < L->k; col += W) {
-            int v = c.t.coupled[col];
-            if (c.t.vav_ahu[v] == a && c.t.vav_area[v] > 0.0 && c.fdem[col] > 0.0) {
-                f += c.fdem[col];
-                cnt++;
-            }
+        total_rw += rw;
+        cmin = fmin(cmin, ta);
+        cmax = fmax(cmax, ta);
+        const int r = col >> 6;
+        if (c.t.vav_area[v] > 0.0 && fd > 0.0) {
+            cahu[r] = c.t.vav_ahu[v];
+            cfd[r] = fd;
         }
-        f = bsum<W>(f, c.red);
-        cnt = bisum<W>(cnt, c.red);
+    }
+    wave_sum_min_max(total_rw, cmin, cmax);
+    // AHU flow (clamped to the AHU's maximum) and cooling requests
+    for (int a = 0; a < na; a++) {
+        double f = 0.0, cnt = 0.0;
+#pragma unroll
+        for (int r = 0; r < SBK_VPL; r++) {
+            const bool m = cahu[r] == a;
+            f += m ? cfd[r] : 0.0;
+            cnt += m ? 1.0 : 0.0;
+        }
+        wave_sum2(f, cnt);
         if (ln() == 0) {
-            double mf = c.t.ahu_c[a * 9 + 1];
+            const double mf = c.t.ahu_c[a * 9 + 1];
             c.flow[a] = f > mf ? mf : f;
-            c.coolreq[a] = cnt;
+            c.coolreq[a] = (int)cnt;
         }
     }
     if (ln() == 0) {
         c.misc[MS_TOTAL_REHEAT] = total_rw;
         c.misc[MS_TF] = tf;
-        c.misc[6] = cmin;
-        c.misc[7] = cmax;
+        c.misc[MS_CMIN] = cmin;
+        c.misc[MS_CMAX] = cmax;
         c.misc[MS_AMB] = ambient;
         c.misc[MS_COMFORT] = comfort;
     }
@@ -1223,7 +1301,7 @@ __device__ __forceinline__ void step_post(Ctx& c) {
         if (wcap > 0.0 && c.L->k > 0) {
             double supply = c.plant[PF_BOILER_CUR];
             double rt = supply - total_rw / wcap;
-            double at = total_rw >= 0.0 ? c.misc[6] : c.misc[7];
+            double at = total_rw >= 0.0 ? c.misc[MS_CMIN] : c.misc[MS_CMAX];
             double lo = supply < at ? supply : at;
             double hi = supply > at ? supply : at;
             if (rt < lo) rt = lo;
@@ -1266,29 +1344,52 @@ __device__ __forceinline__ double reward(Ctx& c) {
         for (int t = ln(); t < L->n; t += W) s += c.T[t];
         tmean = bsum<W>(s, c.red) / (double)L->n;
     }
-    double intake = 0.0, exhaust = 0.0, cooling = 0.0;
-    for (int a = 0; a < L->na; a++) {
-        double ws = 0.0, at = 0.0;
-        for (int v = ln(); v < L->nv; v += W) {
-            if (c.t.vav_ahu[v] != a) continue;
+    // VAV temperatures (lanes over VAVs), then one lane per AHU: return-air
+    // mean over its VAVs in VAV order and its blower / cooling terms, which
+    // every lane then sums in AHU order (sb_reward.c:62-98)
+    int vahu[SBK_VPL];
+    double vws[SBK_VPL], varea[SBK_VPL];
+#pragma unroll
+    for (int r = 0; r < SBK_VPL; r++) {
+        const int v = ln() + 64 * r;
+        vahu[r] = -1;
+        vws[r] = varea[r] = 0.0;
+        if (v < L->nv) {
             double area;
-            double tv = vav_temp(c, c.zq, v, &area);
+            const double tv = vav_temp(c, c.zq, v, &area);
+            vahu[r] = c.t.vav_ahu[v];
             if (area > 0.0) {
-                ws += tv * area;
-                at += area;
+                vws[r] = tv * area;
+                varea[r] = area;
             }
         }
-        ws = bsum<W>(ws, c.red);
-        at = bsum<W>(at, c.red);
+    }
+    for (int a = 0; a < L->na; a++) {
+        double ws = 0.0, at = 0.0;
+#pragma unroll
+        for (int r = 0; r < SBK_VPL; r++) {
+            const bool m = vahu[r] == a;
+            ws += m ? vws[r] : 0.0;
+            at += m ? varea[r] : 0.0;
+        }
+        wave_sum2(ws, at);
+        if (ln() != a) continue;
         double rc = (at > 0.0) ? ws / at : tmean;
         double st = ahu_static(c, a);
         double fe = c.t.ahu_c[a * 9 + 5];
         double flow = (c.run[a] == 1) ? c.flow[a] : 0.0;
-        intake += flow * st / fe;
-        exhaust += flow * (1.0 - c.recirc[a]) * st / fe;
         double mixed = c.recirc[a] * rc + (1.0 - c.recirc[a]) * ambient;
         double sat = (mixed > c.sat[a] && c.run[a] == 1) ? c.sat[a] : mixed;
-        cooling += flow * RHO_AIR * CP_AIR * (sat - mixed) / c.t.ahu_c[a * 9 + 4];
+        c.wsum[a] = flow * st / fe;
+        c.atotal[a] = flow * (1.0 - c.recirc[a]) * st / fe;
+        c.fdsum[a] = flow * RHO_AIR * CP_AIR * (sat - mixed) / c.t.ahu_c[a * 9 + 4];
+    }
+    esync();
+    double intake = 0.0, exhaust = 0.0, cooling = 0.0;
+    for (int a = 0; a < L->na; a++) {
+        intake += c.wsum[a];
+        exhaust += c.atotal[a];
+        cooling += c.fdsum[a];
     }
     const double blower = intake + exhaust;
     const double tf = total_flow_rate(c);
@@ -1321,8 +1422,8 @@ __device__ __forceinline__ double reward(Ctx& c) {
         double sh = (dev <= ref) ? dev / ref : 1.0 + ((dev - ref) / ref) * ((dev - ref) / ref);
         cum_part += max_pph * (1.0 - sh) * occ * dt * inv_hour;
     }
-    const double total_occ = bsum<W>(occ_part, c.red);
-    const double cum = bsum<W>(cum_part, c.red);
+    double total_occ = occ_part, cum = cum_part;
+    wave_sum2(total_occ, cum);
     const double max_prod = max_pph * total_occ * dt * inv_hour;
     const double min_prod = min_pph * total_occ * dt * inv_hour;
     double npr = 0.0;

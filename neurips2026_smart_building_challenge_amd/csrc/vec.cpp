@@ -170,6 +170,7 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     const int k = P.k;
     if (k > 0 && !coupled) return (*err = "coupled_vav_idx missing"), false;
     if (k > nv) return (*err = "more coupled columns than VAVs"), false;
+    if (nv > 64 * SBK_VPL) return (*err = "more than 256 VAVs per building"), false;
     for (int c = 0; c < k; c++)
         if (coupled[c] < 0 || coupled[c] >= nv) return (*err = "coupled_vav_idx out of range"), false;
     for (int v = 0; v < nv; v++)
@@ -428,6 +429,21 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
         G.coupled = I.add(take(coupled, k));
         G.zone_col_off = I.add(zcol_off);
         G.zone_cols = I.add(zcols);
+        {
+            std::vector<int> voff(1, 0), vl, coff(1, 0), cl;
+            for (int a = 0; a < na; a++) {
+                for (int v = 0; v < nv; v++)
+                    if (vav_ahu[v] == a) vl.push_back(v);
+                voff.push_back((int)vl.size());
+                for (int c = 0; c < k; c++)
+                    if (vav_ahu[coupled[c]] == a) cl.push_back(c);
+                coff.push_back((int)cl.size());
+            }
+            G.ahu_vav_off = I.add(voff);
+            G.ahu_vavs = I.add(vl);
+            G.ahu_col_off = I.add(coff);
+            G.ahu_cols = I.add(cl);
+        }
         G.act_src = I.add(src);
         G.air_slot = I.add(P.air_slot);
         G.air_node = I.add(P.air_node);
