@@ -10,10 +10,12 @@ a full 8,640-step episode.
 
 roofline: algorithmic HBM bytes of one puf_step (per-env state record read and
 written, action row read, observation row + reward + terminal written; the
-shared per-layout/per-scenario tables are cache-resident and not counted)
-divided by the step kernel's average duration from HIP events recorded around
-back-to-back launches on the bound stream. traffic: measured HBM bytes per
-launch from rocprofv3 FETCH_SIZE/WRITE_SIZE when profiles/ holds them.
+shared per-layout/per-scenario tables are not counted) divided by the step
+kernel's mean duration, from HIP event pairs recorded on the bound stream around
+every 16th step-kernel launch of the timed region (bracketing every launch would
+add queue markers that slow the loop itself). traffic: HBM bytes per launch
+from rocprofv3 FETCH_SIZE / WRITE_SIZE passes, scaled by the same counters on a
+plain copy of known size (--calibrate-copy), when profiles/ holds them.
 
 cpu_baseline: the reference csim core (oracle/_ref, compiled from the
 reference sources) or, where it was not built, this repo's C restatement,
@@ -36,6 +38,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = "env-steps/sec at 960 mixed envs (fp64 physics); % of HBM roofline"
 HBM_PEAK_GBS = 8000.0
 SEED = 20260601
+TIMER_PERIOD = 16   # every 16th step-kernel launch of the timed region is bracketed by HIP events
 
 
 def log(msg: str) -> None:
@@ -96,12 +99,33 @@ def cpu_baseline(blob_dir: Path, n_envs: int, groups: int, target_s: float, thre
     per_step = secs / 4
     steps = max(4, min(G.EPISODE_STEPS, int(target_s / max(per_step, 1e-9))))
     secs, _ = po.run_batch(envs, ids, steps, SEED + 1, threads)
+    # one core: every 8th env (all 30 scenarios stay represented), about a third of the time
+    sub_envs, sub = envs[::8], ids[::8]
+    s1, _ = po.run_batch(sub_envs, sub, 2, SEED + 2, 1)
+    steps1 = max(2, int(target_s / 3 / max(s1 / 2, 1e-9)))
+    s1, _ = po.run_batch(sub_envs, sub, steps1, SEED + 3, 1)
     for e in envs:
         e.close()
     return {"value": n_envs * steps / secs, "unit": "env-steps/s", "cores": threads,
             "kind": "reference" if kind == "ref" else "port",
-            "sample": f"{n_envs} envs of the same workload x {steps} steps ({secs:.1f} s) on {threads} threads, "
-                      f"{'reference csim compiled from its sources' if kind == 'ref' else 'C restatement of csim'}"}
+            "value_single_core": len(sub) * steps1 / s1,
+            "sample": f"{n_envs} envs of the same workload x {steps} steps ({secs:.1f} s) on {threads} threads "
+                      f"(whole envs per thread); single core: {len(sub)} of the envs x {steps1} steps "
+                      f"({s1:.1f} s); {'reference csim compiled from its sources' if kind == 'ref' else 'C restatement of csim'}"}
+
+
+def calibrate_copy() -> int:
+    """A plain device-to-device copy of known size, for scaling the HBM counters."""
+    import torch
+
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").random_(0, 255)
+    dst = torch.empty_like(src)
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "copies": 10}), flush=True)
+    return 0
 
 
 def main() -> int:
@@ -110,10 +134,15 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=8640)
     ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--config", type=int, default=1)
-    ap.add_argument("--kernel-iters", type=int, default=1000)
+    ap.add_argument("--kernel-iters", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--solver", default="auto", choices=["auto", "relax", "lu"])
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain device copy of 256 MiB 10 times (counter calibration)")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        return calibrate_copy()
     if args.gpus != 1:
         log("bench.py measures one GPU: the env step has no cross-GPU exchange and this build runs "
             "on a single MI355X; --gpus above 1 is not supported")
@@ -129,7 +158,7 @@ def main() -> int:
     t0 = time.time()
     blob_dir = scenario_dir(args.config)
     log(f"scenarios ready in {time.time() - t0:.1f}s: {blob_dir}")
-    vec = E.VecEnv(n_envs, blob_dir=str(blob_dir), groups=groups, desync=int(desync))
+    vec = E.VecEnv(n_envs, blob_dir=str(blob_dir), groups=groups, desync=int(desync), solver=args.solver)
     info = vec.info()
     vec.reset()
     for s in range(args.warmup):
@@ -140,21 +169,24 @@ def main() -> int:
     stream = torch.cuda.current_stream()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    vec.kernel_timer(TIMER_PERIOD)
     ev0.record(stream)
     for s in range(args.steps):
         vec.gen_actions(SEED, args.warmup + s)
         vec.step()
     ev1.record(stream)
     torch.cuda.synchronize()
+    k_us, k_n = vec.kernel_timer(0)
     ms = ev0.elapsed_time(ev1)
     ms_per_step = ms / args.steps
     value = n_envs * args.steps / (ms / 1e3)
     log(f"timed {args.steps} steps: {ms_per_step * 1e3:.1f} us/step, {value:.4g} env-steps/s")
-    k_iters = max(1, args.kernel_iters)
-    k_ms = vec.time_step(k_iters) / k_iters
-    achieved = info.bytes_per_step / (k_ms * 1e-3) / 1e9
-    log(f"step kernel: {k_ms * 1e3:.1f} us/launch, {info.bytes_per_step / 1e6:.2f} MB algorithmic -> "
-        f"{achieved:.1f} GB/s")
+    achieved = info.bytes_per_step / (k_us * 1e-6) / 1e9
+    log(f"step kernel: {k_us:.1f} us/launch over {k_n} launches, {info.bytes_per_step / 1e6:.2f} MB "
+        f"algorithmic -> {achieved:.1f} GB/s")
+    b2b_us = vec.time_step(max(1, args.kernel_iters)) / max(1, args.kernel_iters) * 1e3
+    solver = vec.solve_info(0)
+    sweeps = [vec.solve_info(i)["sweeps"] for i in range(0, n_envs, max(1, n_envs // 64))]
     traffic = measured_traffic(args.config)
     phases = vec.phase_times()
     log("phase us (mean / max over workgroups): " +
@@ -177,11 +209,14 @@ def main() -> int:
                                f"climates), Beta(2,2) actions, fp64 physics"
                                + (", desynchronised starts" if desync else ""),
                    "n_envs": n_envs, "scenarios": groups, "episode_steps": G.EPISODE_STEPS,
+                   "solver": solver["solver"], "envs_per_workgroup": info.envs_per_block,
                    "block": info.block, "lds_bytes": info.lds_bytes},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
-                     "kernel_us": k_ms * 1e3, "algorithmic_bytes": info.bytes_per_step,
-                     "phase_us_max": {k: round(x, 2) for k, (m, x) in phases.items()}},
+                     "kernel_us": k_us, "kernel_launches_timed": k_n, "back_to_back_us": b2b_us,
+                     "algorithmic_bytes": info.bytes_per_step,
+                     "relax_sweeps_mean": (sum(sweeps) / len(sweeps)) if solver["solver"] == "relax" else None,
+                     "phase_us_mean": {k: round(m, 2) for k, (m, x) in phases.items()}},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

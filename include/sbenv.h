@@ -146,6 +146,13 @@ void sbx_vec_info(Env* envs, SbxVecInfo* out);
  * Returns the number of doubles written (<= cap), or -1. */
 int sbx_env_state(Env* envs, int i, double* out, int cap);
 
+/* Step-kernel timer on the bound stream: on = p > 0 clears it and makes every
+ * p-th following puf_step (the first, then every p launches) record a HIP
+ * event pair around its kernel launch (up to 16384 pairs); on = 0 stops it,
+ * synchronises and returns the mean per-launch duration in microseconds of the
+ * launches timed (*count of them). */
+double sbx_kernel_timer(Env* envs, int on, int* count);
+
 /* Launches the step kernel `iters` times back to back between two HIP events
  * on the bound stream and returns the elapsed milliseconds (synchronises). */
 float sbx_time_step(Env* envs, int iters);

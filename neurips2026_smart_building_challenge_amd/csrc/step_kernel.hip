@@ -1689,7 +1689,7 @@ extern "C" int sbk_set_lds_limit(int width, int bytes) {
 
 extern "C" int sbk_launch_gen_actions(float* actions, const int* n_cont, const int* n_disc, int n_envs,
                                       uint64_t seed, uint32_t step, hipStream_t s) {
-    hipLaunchKernelGGL(sbk::gen_actions_kernel, dim3(n_envs), dim3(64), 0, s, actions, n_cont, n_disc, n_envs,
+    hipLaunchKernelGGL(sbk::gen_actions_kernel, dim3(n_envs), dim3(256), 0, s, actions, n_cont, n_disc, n_envs,
                        seed, step);
     return (int)hipGetLastError();
 }

@@ -753,7 +753,12 @@ struct Vec {
     float* rewards = nullptr;
     float* terminals = nullptr;
     double bytes_per_step = 0.0, flops_per_step = 0.0;
+    // step-kernel timer: an event pair around each puf_step launch while on
+    std::vector<hipEvent_t> tev;
+    int t_on = 0, t_used = 0, t_seen = 0;   // t_on: sampling period (0 = off)
 };
+
+constexpr int kTimerPairs = 16384;
 
 sbk::KParams params(Vec* v, int mode) {
     sbk::KParams p{};
@@ -1107,7 +1112,17 @@ void puf_reset(Env* envs) {
     hip_ok(hipStreamSynchronize(g_stream), "reset");
 }
 
-void puf_step(Env* envs) { launch(vec_of(envs), sbk::KMODE_STEP); }
+void puf_step(Env* envs) {
+    Vec* v = vec_of(envs);
+    if (v->t_on && v->t_seen++ % v->t_on == 0 && v->t_used < kTimerPairs) {
+        hip_ok(hipEventRecord(v->tev[2 * v->t_used], g_stream), "timer event");
+        launch(v, sbk::KMODE_STEP);
+        hip_ok(hipEventRecord(v->tev[2 * v->t_used + 1], g_stream), "timer event");
+        v->t_used++;
+        return;
+    }
+    launch(v, sbk::KMODE_STEP);
+}
 
 void puf_render(Env* env) { (void)env; }
 
@@ -1122,6 +1137,7 @@ void puf_close(Env* envs) {
     (void)hipFree(v->d_envs);
     (void)hipFree(v->d_order);
     (void)hipFree(v->d_tiles);
+    for (hipEvent_t e : v->tev) (void)hipEventDestroy(e);
     (void)hipFree(v->d_ncont);
     (void)hipFree(v->d_ndisc);
     (void)hipHostFree(v->envs);
@@ -1316,6 +1332,32 @@ int sbx_pass_times(Env* envs, int env, long long* cycles, int cap) {
         for (int k = i; k < j; k++) cycles[k] = dt / (j - i);
     }
     return np;
+}
+
+double sbx_kernel_timer(Env* envs, int on, int* count) {
+    Vec* v = vec_of(envs);
+    if (on) {
+        if (v->tev.empty()) {
+            v->tev.resize(2 * kTimerPairs);
+            for (auto& e : v->tev) hip_ok(hipEventCreate(&e), "event");
+        }
+        v->t_used = 0;
+        v->t_seen = 0;
+        v->t_on = on;
+        if (count) *count = 0;
+        return 0.0;
+    }
+    v->t_on = 0;
+    if (count) *count = v->t_used;
+    if (v->t_used == 0) return 0.0;
+    hip_ok(hipEventSynchronize(v->tev[2 * v->t_used - 1]), "timer sync");
+    double sum = 0.0;
+    for (int i = 0; i < v->t_used; i++) {
+        float ms = 0.f;
+        hip_ok(hipEventElapsedTime(&ms, v->tev[2 * i], v->tev[2 * i + 1]), "elapsed");
+        sum += ms;
+    }
+    return sum * 1e3 / v->t_used;
 }
 
 float sbx_time_step(Env* envs, int iters) {

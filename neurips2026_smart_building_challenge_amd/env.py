@@ -78,7 +78,7 @@ class SbxPlan(ctypes.Structure):
 EXPORTS = [
     "dict_find", "dict_set", "puf_vec_create", "puf_bind_stream", "puf_init", "puf_reset", "puf_step",
     "puf_render", "puf_close", "puf_log", "puf_live_log", "puf_mask_init", "sbx_gen_actions",
-    "sbx_vec_info", "sbx_env_state", "sbx_time_step", "sbx_phase_times", "sbx_phase_stamps", "sbx_pass_times", "sbx_solve_info",
+    "sbx_vec_info", "sbx_env_state", "sbx_time_step", "sbx_phase_times", "sbx_phase_stamps", "sbx_kernel_timer", "sbx_pass_times", "sbx_solve_info",
     "sbx_env_meta", "sbx_scenario_path",
     "sbx_plan_layout", "sbx_plan_free", "sbx_last_error", "sbx_version",
 ]
@@ -116,6 +116,8 @@ def lib() -> ctypes.CDLL:
         L.sbx_phase_times.restype = ctypes.c_int
         L.sbx_pass_times.argtypes = [ctypes.POINTER(Env), ctypes.c_int, P, ctypes.c_int]
         L.sbx_pass_times.restype = ctypes.c_int
+        L.sbx_kernel_timer.argtypes = [ctypes.POINTER(Env), ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
+        L.sbx_kernel_timer.restype = ctypes.c_double
         L.sbx_phase_stamps.argtypes = [ctypes.POINTER(Env), P, ctypes.c_int]
         L.sbx_phase_stamps.restype = ctypes.c_int
         L.sbx_solve_info.argtypes = [ctypes.POINTER(Env), ctypes.c_int, P]
@@ -279,6 +281,13 @@ class VecEnv:
         buf = np.zeros(65536, np.int64)
         n = self.L.sbx_pass_times(self.envs, i, buf.ctypes.data_as(P), buf.size)
         return buf[:max(n, 0)].copy()
+
+    def kernel_timer(self, period: int) -> tuple[float, int]:
+        """period > 0 starts timing every period-th step-kernel launch; 0 stops and
+        returns (mean us per timed launch, launches timed)."""
+        n = ctypes.c_int(0)
+        us = self.L.sbx_kernel_timer(self.envs, int(period), ctypes.byref(n))
+        return float(us), int(n.value)
 
     def time_step(self, iters: int) -> float:
         return float(self.L.sbx_time_step(self.envs, iters))
