@@ -160,9 +160,19 @@ def main() -> int:
     log(f"scenarios ready in {time.time() - t0:.1f}s: {blob_dir}")
     vec = E.VecEnv(n_envs, blob_dir=str(blob_dir), groups=groups, desync=int(desync), solver=args.solver)
     info = vec.info()
+    rollout = args.config == 4
+    if rollout:
+        # the shared-policy MLP (fp32 MFMA) + Beta sampling makes every action row
+        vec.policy_bind(E.policy_weights(SEED))
+
+        def actions(s):
+            vec.policy_act(SEED, s)
+    else:
+        def actions(s):
+            vec.gen_actions(SEED, s)
     vec.reset()
     for s in range(args.warmup):
-        vec.gen_actions(SEED, s)
+        actions(s)
         vec.step()
     torch.cuda.synchronize()
     log(f"warmup done ({args.warmup} steps)")
@@ -172,7 +182,7 @@ def main() -> int:
     vec.kernel_timer(TIMER_PERIOD)
     ev0.record(stream)
     for s in range(args.steps):
-        vec.gen_actions(SEED, args.warmup + s)
+        actions(args.warmup + s)
         vec.step()
     ev1.record(stream)
     torch.cuda.synchronize()
@@ -206,8 +216,10 @@ def main() -> int:
         "vs_baseline": None, "dtype": "f64", "data": "synthetic",
         "config": {"workload": f"BASELINE config {args.config}: {n_envs} envs, {groups} scenarios "
                                f"({len({s[0].zones for s in scen})} layouts x {len({s[1].name for s in scen})} "
-                               f"climates), Beta(2,2) actions, fp64 physics"
-                               + (", desynchronised starts" if desync else ""),
+                               f"climates), "
+                               + ("shared-policy MLP 1024-128-128-544 (fp32 MFMA) + Beta sampling per step, "
+                                  if rollout else "Beta(2,2) actions, ")
+                               + "fp64 physics" + (", desynchronised starts" if desync else ""),
                    "n_envs": n_envs, "scenarios": groups, "episode_steps": G.EPISODE_STEPS,
                    "solver": solver["solver"], "envs_per_workgroup": info.envs_per_block,
                    "block": info.block, "lds_bytes": info.lds_bytes},

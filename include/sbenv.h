@@ -184,6 +184,38 @@ int sbx_pass_times(Env* envs, int env, long long* cycles, int cap);
  * 4, or -1. Synchronous. */
 int sbx_solve_info(Env* envs, int i, double* out);
 
+/* Shared-policy rollout step (the reference trainer's
+ * policy forward runs between env steps). fp32 MLP on MFMA over every env's
+ * observation row: h1 = tanh(obs W1 + b1), h2 = tanh(h1 W2 + b2),
+ * y = h2 W3 + b3 = (u[256], v[256], ud[16], vd[16]); head j draws
+ * x ~ Beta(softplus(u_j) + 1, softplus(v_j) + 1) (two Marsaglia-Tsang gamma
+ * draws on Philox4x32-10 keyed by seed, counter (env, step, 2j or 2j + 1,
+ * 1 + attempt)); continuous heads write 2x - 1, discrete heads x > 0.5 into the
+ * vec's action rows (0 past the env's n_cont / n_disc). Weights are caller-owned
+ * device memory, row-major [in][out]: W1 [1024][128], W2 [128][128],
+ * W3 [128][544], biases [128], [128], [544]. sbx_policy_bind stores them and
+ * allocates the activations (call it outside graph capture); sbx_policy_act
+ * launches on the bound stream and allocates nothing. sbx_policy_heads copies
+ * y of the last sbx_policy_act to host (synchronous). Return 0 / count, or -1. */
+#define SBX_POLICY_HIDDEN 128
+#define SBX_POLICY_HEADS 544
+typedef struct SbxPolicy {
+    const float* w1;
+    const float* b1;
+    const float* w2;
+    const float* b2;
+    const float* w3;
+    const float* b3;
+} SbxPolicy;
+int sbx_policy_bind(Env* envs, const SbxPolicy* p);
+int sbx_policy_act(Env* envs, uint64_t seed, uint32_t step);
+int sbx_policy_heads(Env* envs, float* out, int cap);
+
+/* The heads' Beta sampler alone: out[i] ~ Beta(alpha[i], beta[i]) for device
+ * arrays of n floats (alpha, beta >= 1), counter (i, 0, 0 or 1, 1 + attempt),
+ * on the bound stream. Returns 0, or -1. */
+int sbx_beta_sample(const float* alpha, const float* beta, float* out, int n, uint64_t seed);
+
 /* Scenario of env i (index into the sorted, round-robin ordered blob list),
  * its calendar start offset and occupancy seed. */
 int sbx_env_meta(Env* envs, int i, int* scenario, int* start, uint32_t* occ_seed);

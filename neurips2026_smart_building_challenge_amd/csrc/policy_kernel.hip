@@ -1,0 +1,196 @@
+// Shared-policy MLP forward + Beta action sampling for MI355X (gfx950), the
+// rollout-loop workload of BASELINE config 5: every env's observation row goes
+// through the same fp32 MLP
+//
+//   h1 = tanh(obs W1 + b1)   [n x 1024] x [1024 x 128]
+//   h2 = tanh(h1 W2 + b2)    [n x 128]  x [128 x 128]
+//   y  = h2 W3 + b3          [n x 128]  x [128 x 544] = (u[256], v[256], ud[16], vd[16])
+//
+// and each action head j draws x ~ Beta(softplus(u_j) + 1, softplus(v_j) + 1);
+// continuous heads write 2x - 1, discrete heads x > 0.5 into the action row the
+// next env step decodes.
+//
+// The three products run on fp32 MFMA (v_mfma_f32_16x16x4_f32): one workgroup
+// per 16 x 16 output tile, its K range split over up to four wavefronts whose
+// partial tiles are summed in LDS in a fixed order, then bias and activation.
+// Within a 16-wide K block, lane group g (lanes 16g .. 16g + 15) feeds the
+// k values 4g .. 4g + 3 over the four MFMA steps, so each lane reads its A
+// operand as one contiguous float4 (the product over a block is the same sum).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "sb_philox.h"
+
+namespace sbk {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kPolicyHidden = 128;
+constexpr int kPolicyHeads = 2 * 256 + 2 * 16;   // u, v of the continuous and the discrete heads
+constexpr int kObsWidth = 1024;
+constexpr int kActWidth = 272;
+
+// C[M x N] = act(A[M x K] B[K x N] + bias) with K = KW * (blockDim.x / 64):
+// wavefront w takes K range [w KW, (w + 1) KW) and issues every load of that
+// range before its first MFMA (one memory latency per tile). lda / ldc in
+// floats; N a multiple of 16. ACT: 0 identity, 1 tanh.
+template <int ACT, int KW>
+__global__ __launch_bounds__(256) void mlp_layer_kernel(const float* __restrict__ A, int lda,
+                                                        const float* __restrict__ B,
+                                                        const float* __restrict__ bias, float* __restrict__ C,
+                                                        int ldc, int M, int N) {
+    static_assert(KW % 16 == 0, "K per wavefront is a multiple of 16");
+    constexpr int NB = KW / 16;
+    __shared__ v4f part[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, ksplit = blockDim.x >> 6;
+    const int m0 = blockIdx.x * 16, n0 = blockIdx.y * 16;
+    const int g = lane >> 4, i = lane & 15;
+    const int m = m0 + i;
+    const int mc = m < M ? m : M - 1;   // rows past M read row M - 1; their outputs are dropped
+    const float* a_row = A + (size_t)mc * lda + w * KW + 4 * g;
+    const float* b_col = B + (size_t)(w * KW + 4 * g) * N + n0 + i;
+    float4 a[NB];
+    float b[NB][4];
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+        a[j] = *reinterpret_cast<const float4*>(a_row + 16 * j);
+        const float* bp = b_col + (size_t)(16 * j) * N;
+#pragma unroll
+        for (int s = 0; s < 4; s++) b[j][s] = bp[s * N];
+    }
+    // the empty asm "uses" every loaded register here, so the compiler keeps
+    // all loads ahead of the first MFMA instead of sinking each to its use
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+        asm volatile("" : "+v"(a[j].x), "+v"(a[j].y), "+v"(a[j].z), "+v"(a[j].w));
+        asm volatile("" : "+v"(b[j][0]), "+v"(b[j][1]), "+v"(b[j][2]), "+v"(b[j][3]));
+    }
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].x, b[j][0], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].y, b[j][1], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].z, b[j][2], acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].w, b[j][3], acc, 0, 0, 0);
+    }
+    if (ksplit > 1) {
+        part[w][lane] = acc;
+        __syncthreads();
+        if (w != 0) return;
+        for (int s = 1; s < ksplit; s++) acc += part[s][lane];
+    }
+    // lane holds C[4g + r][i] of the tile
+    const float bv = bias[n0 + i];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int row = m0 + 4 * g + r;
+        float v = acc[r] + bv;
+        if (ACT == 1) v = tanhf(v);
+        if (row < M) C[(size_t)row * ldc + n0 + i] = v;
+    }
+}
+
+__device__ __forceinline__ float softplus(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
+// Gamma(a) for a >= 1 (Marsaglia and Tsang, "A simple method for generating
+// gamma variables", ACM TOMS 26(3), 2000): d = a - 1/3, c = 1/sqrt(9d); draw
+// z ~ N(0, 1) (Box-Muller) and u ~ U(0, 1), v = (1 + cz)^3, accept d v when
+// v > 0 and u < 1 - 0.0331 z^4 or log u < z^2/2 + d (1 - v + log v). Attempt t
+// uses Philox block (env, step, stream, 1 + t); after 32 rejected attempts
+// (probability below 1e-40 for a >= 1) the mean a is returned. The sampler is
+// statistical, so it uses the hardware log2 / cos / sqrt.
+__device__ __forceinline__ float gamma_mt(float a, uint32_t env, uint32_t step, uint32_t stream, uint32_t k0,
+                                          uint32_t k1) {
+    const float d = a - (1.0f / 3.0f);
+    const float c = __frsqrt_rn(9.0f * d);
+    for (uint32_t t = 0; t < 32; t++) {
+        const Ctr4 r = philox4x32_10(Ctr4{env, step, stream, 1u + t}, k0, k1);
+        const float u1 = u24(r.x), u2 = u24(r.y), u = u24(r.z);
+        const float z = __fsqrt_rn(-2.0f * __logf(u1)) * __cosf(6.283185307f * u2);
+        float v = 1.0f + c * z;
+        if (v <= 0.0f) continue;
+        v = v * v * v;
+        const float z2 = z * z;
+        if (u < 1.0f - 0.0331f * z2 * z2) return d * v;
+        if (__logf(u) < 0.5f * z2 + d * (1.0f - v + __logf(v))) return d * v;
+    }
+    return a;
+}
+
+// Head h (< 272) of env e: continuous h < 256 (u, v at columns h, 256 + h),
+// discrete 256 + d (columns 512 + d, 528 + d). Stream 2h draws Ga, 2h + 1 Gb.
+__device__ __forceinline__ int head_col(int h, int which) {
+    return h < 256 ? h + 256 * which : 512 + (h - 256) + 16 * which;
+}
+
+// One thread per gamma draw: lanes 2t and 2t + 1 draw Ga and Gb of head t of
+// the flattened (env, head) index, and the even lane writes the action
+// x = Ga / (Ga + Gb): continuous 2x - 1, discrete x > 0.5; 0 past the env's
+// head counts.
+__global__ __launch_bounds__(256) void beta_heads_kernel(const float* __restrict__ y, float* __restrict__ actions,
+                                                         const int* __restrict__ n_cont,
+                                                         const int* __restrict__ n_disc, int n_envs,
+                                                         uint64_t seed, uint32_t step) {
+    const int gid = blockIdx.x * blockDim.x + threadIdx.x;
+    const int t = gid >> 1, which = gid & 1;
+    const int e = t / kActWidth, h = t - e * kActWidth;
+    const bool live = e < n_envs;
+    const int ec = live ? e : n_envs - 1;
+    const bool used = live && (h < 256 ? h < n_cont[ec] : h - 256 < n_disc[ec]);
+    float g = 1.0f;
+    if (used) {
+        const float a = softplus(y[(size_t)ec * kPolicyHeads + head_col(h, which)]) + 1.0f;
+        g = gamma_mt(a, (uint32_t)e, step, 2u * (uint32_t)h + (uint32_t)which, (uint32_t)seed,
+                     (uint32_t)(seed >> 32));
+    }
+    const float other = __shfl_xor(g, 1, 64);
+    if (live && which == 0) {
+        float v = 0.0f;
+        if (used) {
+            const float x = g / (g + other);
+            v = h < 256 ? 2.0f * x - 1.0f : (x > 0.5f ? 1.0f : 0.0f);
+        }
+        actions[(size_t)e * kActWidth + h] = v;
+    }
+}
+
+// Draws out[i] ~ Beta(alpha[i], beta[i]) with the heads' sampler (env = i, step 0, head 0).
+__global__ void beta_sample_kernel(const float* alpha, const float* beta, float* out, int n, uint64_t seed) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+    const float ga = gamma_mt(alpha[i], (uint32_t)i, 0u, 0u, k0, k1);
+    const float gb = gamma_mt(beta[i], (uint32_t)i, 0u, 1u, k0, k1);
+    out[i] = ga / (ga + gb);
+}
+
+}  // namespace sbk
+
+// ---------------------------------------------------------------- launchers
+// obs [n x 1024] -> h1, h2 [n x 128] -> y [n x 544] -> actions [n x 272], on stream s.
+extern "C" int sbk_launch_policy(const float* obs, const float* w1, const float* b1, const float* w2,
+                                 const float* b2, const float* w3, const float* b3, float* h1, float* h2, float* y,
+                                 float* actions, const int* n_cont, const int* n_disc, int n, uint64_t seed,
+                                 uint32_t step, hipStream_t s) {
+    using namespace sbk;
+    if (n <= 0) return (int)hipErrorInvalidValue;
+    const int mt = (n + 15) / 16;
+    // K split over 4 wavefronts (layer 1, K = 1024) or 2 (K = 128)
+    hipLaunchKernelGGL((mlp_layer_kernel<1, kObsWidth / 4>), dim3(mt, kPolicyHidden / 16), dim3(256), 0, s, obs,
+                       kObsWidth, w1, b1, h1, kPolicyHidden, n, kPolicyHidden);
+    hipLaunchKernelGGL((mlp_layer_kernel<1, kPolicyHidden / 2>), dim3(mt, kPolicyHidden / 16), dim3(128), 0, s, h1,
+                       kPolicyHidden, w2, b2, h2, kPolicyHidden, n, kPolicyHidden);
+    hipLaunchKernelGGL((mlp_layer_kernel<0, kPolicyHidden / 2>), dim3(mt, kPolicyHeads / 16), dim3(128), 0, s, h2,
+                       kPolicyHidden, w3, b3, y, kPolicyHeads, n, kPolicyHeads);
+    const long long draws = 2LL * n * kActWidth;
+    hipLaunchKernelGGL(beta_heads_kernel, dim3((unsigned)((draws + 255) / 256)), dim3(256), 0, s, y, actions, n_cont,
+                       n_disc, n, seed, step);
+    return (int)hipGetLastError();
+}
+
+extern "C" int sbk_launch_beta_sample(const float* alpha, const float* beta, float* out, int n, uint64_t seed,
+                                      hipStream_t s) {
+    if (n <= 0) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(sbk::beta_sample_kernel, dim3((n + 255) / 256), dim3(256), 0, s, alpha, beta, out, n, seed);
+    return (int)hipGetLastError();
+}

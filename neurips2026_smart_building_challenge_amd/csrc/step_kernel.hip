@@ -19,6 +19,7 @@
 
 #include "sbenv.h"
 #include "sbenv_internal.h"
+#include "sb_philox.h"
 
 namespace sbk {
 
@@ -1630,23 +1631,11 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
     STAMP(12);
 }
 
-// Beta(2,2) action rows (see sbx_gen_actions in sbenv.h).
-__device__ __forceinline__ float u24(uint32_t x) { return ((float)(x >> 8) + 0.5f) * (1.0f / 16777216.0f); }
-
+// Beta(2,2) action rows (see sbx_gen_actions in sbenv.h): the median of three
+// U(0,1) of one Philox4x32-10 block keyed by the seed, counter (env, step, slot, 0).
 __device__ __forceinline__ float beta22(uint64_t seed, uint32_t env, uint32_t step, uint32_t slot) {
-    uint32_t c0 = env, c1 = step, c2 = slot, c3 = 0u;
-    uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
-#pragma unroll
-    for (int r = 0; r < 10; r++) {
-        uint32_t hi0 = __umulhi(0xD2511F53u, c0), lo0 = 0xD2511F53u * c0;
-        uint32_t hi1 = __umulhi(0xCD9E8D57u, c2), lo1 = 0xCD9E8D57u * c2;
-        uint32_t n0 = hi1 ^ c1 ^ k0;
-        uint32_t n2 = hi0 ^ c3 ^ k1;
-        c0 = n0; c1 = lo1; c2 = n2; c3 = lo0;
-        k0 += 0x9E3779B9u;
-        k1 += 0xBB67AE85u;
-    }
-    float a = u24(c0), b = u24(c1), d = u24(c2);
+    const Ctr4 r = philox4x32_10(Ctr4{env, step, slot, 0u}, (uint32_t)seed, (uint32_t)(seed >> 32));
+    float a = u24(r.x), b = u24(r.y), d = u24(r.z);
     float lo = a < b ? a : b, hi = a < b ? b : a;
     return d < lo ? lo : (d > hi ? hi : d);
 }

@@ -27,6 +27,12 @@
 
 extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int threads, int lds_bytes, hipStream_t s);
 extern "C" int sbk_set_lds_limit(int width, int bytes);
+extern "C" int sbk_launch_policy(const float* obs, const float* w1, const float* b1, const float* w2,
+                                 const float* b2, const float* w3, const float* b3, float* h1, float* h2, float* y,
+                                 float* actions, const int* n_cont, const int* n_disc, int n, uint64_t seed,
+                                 uint32_t step, hipStream_t s);
+extern "C" int sbk_launch_beta_sample(const float* alpha, const float* beta, float* out, int n, uint64_t seed,
+                                      hipStream_t s);
 extern "C" int sbk_launch_gen_actions(float* actions, const int* n_cont, const int* n_disc, int n_envs,
                                       uint64_t seed, uint32_t step, hipStream_t s);
 
@@ -756,6 +762,9 @@ struct Vec {
     // step-kernel timer: an event pair around each puf_step launch while on
     std::vector<hipEvent_t> tev;
     int t_on = 0, t_used = 0, t_seen = 0;   // t_on: sampling period (0 = off)
+    // shared policy (sbx_policy_bind): caller-owned weights, library-owned activations
+    SbxPolicy pol{};
+    float *p_h1 = nullptr, *p_h2 = nullptr, *p_y = nullptr;
 };
 
 constexpr int kTimerPairs = 16384;
@@ -1138,6 +1147,9 @@ void puf_close(Env* envs) {
     (void)hipFree(v->d_order);
     (void)hipFree(v->d_tiles);
     for (hipEvent_t e : v->tev) (void)hipEventDestroy(e);
+    (void)hipFree(v->p_h1);
+    (void)hipFree(v->p_h2);
+    (void)hipFree(v->p_y);
     (void)hipFree(v->d_ncont);
     (void)hipFree(v->d_ndisc);
     (void)hipHostFree(v->envs);
@@ -1374,6 +1386,44 @@ float sbx_time_step(Env* envs, int iters) {
     (void)hipEventDestroy(a);
     (void)hipEventDestroy(b);
     return ms;
+}
+
+int sbx_policy_bind(Env* envs, const SbxPolicy* p) {
+    Vec* v = vec_of(envs);
+    if (!p || !p->w1 || !p->b1 || !p->w2 || !p->b2 || !p->w3 || !p->b3) { g_err = "null policy weight"; return -1; }
+    v->pol = *p;
+    if (!v->p_h1) {
+        hip_ok(hipMalloc(&v->p_h1, sizeof(float) * (size_t)v->n * SBX_POLICY_HIDDEN), "hipMalloc(policy)");
+        hip_ok(hipMalloc(&v->p_h2, sizeof(float) * (size_t)v->n * SBX_POLICY_HIDDEN), "hipMalloc(policy)");
+        hip_ok(hipMalloc(&v->p_y, sizeof(float) * (size_t)v->n * SBX_POLICY_HEADS), "hipMalloc(policy)");
+    }
+    return 0;
+}
+
+int sbx_policy_act(Env* envs, uint64_t seed, uint32_t step) {
+    Vec* v = vec_of(envs);
+    if (!v->p_h1) { g_err = "sbx_policy_act before sbx_policy_bind"; return -1; }
+    const SbxPolicy& p = v->pol;
+    int rc = sbk_launch_policy(v->obs, p.w1, p.b1, p.w2, p.b2, p.w3, p.b3, v->p_h1, v->p_h2, v->p_y, v->actions,
+                               v->d_ncont, v->d_ndisc, v->n, seed, step, g_stream);
+    if (rc != 0) die(std::string("policy launch failed: ") + hipGetErrorString((hipError_t)rc));
+    return 0;
+}
+
+int sbx_policy_heads(Env* envs, float* out, int cap) {
+    Vec* v = vec_of(envs);
+    const size_t count = (size_t)v->n * SBX_POLICY_HEADS;
+    if (!v->p_y || !out || cap < (int)count) return -1;
+    hip_ok(hipStreamSynchronize(g_stream), "policy sync");
+    hip_ok(hipMemcpy(out, v->p_y, count * sizeof(float), hipMemcpyDeviceToHost), "policy heads copy");
+    return (int)count;
+}
+
+int sbx_beta_sample(const float* alpha, const float* beta, float* out, int n, uint64_t seed) {
+    if (!alpha || !beta || !out || n <= 0) return -1;
+    int rc = sbk_launch_beta_sample(alpha, beta, out, n, seed, g_stream);
+    if (rc != 0) die(std::string("beta sample launch failed: ") + hipGetErrorString((hipError_t)rc));
+    return 0;
 }
 
 int sbx_solve_info(Env* envs, int i, double* out) {

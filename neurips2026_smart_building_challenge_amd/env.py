@@ -74,11 +74,19 @@ class SbxPlan(ctypes.Structure):
                 ("rx_val", ctypes.POINTER(ctypes.c_double)), ("rx_col", ctypes.POINTER(ctypes.c_int))]
 
 
+class SbxPolicy(ctypes.Structure):
+    _fields_ = [(k, ctypes.c_void_p) for k in ("w1", "b1", "w2", "b2", "w3", "b3")]
+
+
+POLICY_HIDDEN, POLICY_HEADS = 128, 544
+
+
 # every symbol include/sbenv.h declares
 EXPORTS = [
     "dict_find", "dict_set", "puf_vec_create", "puf_bind_stream", "puf_init", "puf_reset", "puf_step",
     "puf_render", "puf_close", "puf_log", "puf_live_log", "puf_mask_init", "sbx_gen_actions",
     "sbx_vec_info", "sbx_env_state", "sbx_time_step", "sbx_phase_times", "sbx_phase_stamps", "sbx_kernel_timer", "sbx_pass_times", "sbx_solve_info",
+    "sbx_policy_bind", "sbx_policy_act", "sbx_policy_heads", "sbx_beta_sample",
     "sbx_env_meta", "sbx_scenario_path",
     "sbx_plan_layout", "sbx_plan_free", "sbx_last_error", "sbx_version",
 ]
@@ -118,6 +126,10 @@ def lib() -> ctypes.CDLL:
         L.sbx_pass_times.restype = ctypes.c_int
         L.sbx_kernel_timer.argtypes = [ctypes.POINTER(Env), ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
         L.sbx_kernel_timer.restype = ctypes.c_double
+        L.sbx_policy_bind.argtypes = [ctypes.POINTER(Env), ctypes.POINTER(SbxPolicy)]
+        L.sbx_policy_act.argtypes = [ctypes.POINTER(Env), ctypes.c_uint64, ctypes.c_uint32]
+        L.sbx_policy_heads.argtypes = [ctypes.POINTER(Env), P, ctypes.c_int]
+        L.sbx_beta_sample.argtypes = [P, P, P, ctypes.c_int, ctypes.c_uint64]
         L.sbx_phase_stamps.argtypes = [ctypes.POINTER(Env), P, ctypes.c_int]
         L.sbx_phase_stamps.restype = ctypes.c_int
         L.sbx_solve_info.argtypes = [ctypes.POINTER(Env), ctypes.c_int, P]
@@ -197,6 +209,35 @@ def plan_layout(blob: str | Path, width: int = 64) -> dict[str, np.ndarray]:
     return out
 
 
+def policy_weights(seed: int, device: str = "cuda") -> dict:
+    """Random-init fp32 weights of the shared policy, row-major [in][out], drawn like
+    torch.nn.Linear's default init (U(-1/sqrt(fan_in), 1/sqrt(fan_in)))."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    out = {}
+    for name, (fi, fo) in {"1": (1024, POLICY_HIDDEN), "2": (POLICY_HIDDEN, POLICY_HIDDEN),
+                           "3": (POLICY_HIDDEN, POLICY_HEADS)}.items():
+        bound = 1.0 / fi ** 0.5
+        out["w" + name] = ((torch.rand(fi, fo, generator=g) * 2 - 1) * bound).to(device).contiguous()
+        out["b" + name] = ((torch.rand(fo, generator=g) * 2 - 1) * bound).to(device).contiguous()
+    return out
+
+
+def beta_sample(alpha, beta, seed: int):
+    """Device Beta(alpha, beta) draws with the policy heads' sampler (torch float32 tensors)."""
+    import torch
+
+    alpha = alpha.contiguous()
+    beta = beta.contiguous()
+    out = torch.empty_like(alpha)
+    L = lib()
+    L.puf_bind_stream(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    if L.sbx_beta_sample(alpha.data_ptr(), beta.data_ptr(), out.data_ptr(), alpha.numel(), seed) != 0:
+        raise RuntimeError("sbx_beta_sample failed")
+    return out
+
+
 class VecEnv:
     """n envs of the GPU env behind the PufferLib ABI, with torch-owned buffers."""
 
@@ -244,6 +285,25 @@ class VecEnv:
         s, st, sd = ctypes.c_int(), ctypes.c_int(), ctypes.c_uint32()
         self.L.sbx_env_meta(self.envs, i, ctypes.byref(s), ctypes.byref(st), ctypes.byref(sd))
         return self.L.sbx_scenario_path(self.envs, s.value).decode(), st.value, sd.value
+
+    def policy_bind(self, weights: dict) -> None:
+        """Binds caller-owned policy weights (device float32, [in][out]); see policy_weights."""
+        self._policy = weights   # keeps the tensors alive
+        p = SbxPolicy(*[ctypes.c_void_p(weights[k].data_ptr()) for k in ("w1", "b1", "w2", "b2", "w3", "b3")])
+        if self.L.sbx_policy_bind(self.envs, ctypes.byref(p)) != 0:
+            raise RuntimeError(self.L.sbx_last_error().decode())
+
+    def policy_act(self, seed: int, step: int) -> None:
+        """Policy forward + Beta sampling: writes every env's action row for the next step."""
+        if self.L.sbx_policy_act(self.envs, seed, step) != 0:
+            raise RuntimeError(self.L.sbx_last_error().decode())
+
+    def policy_heads(self) -> np.ndarray:
+        """Head outputs y (n, 544) of the last policy_act."""
+        buf = np.zeros(self.n * POLICY_HEADS, np.float32)
+        if self.L.sbx_policy_heads(self.envs, buf.ctypes.data_as(P), buf.size) < 0:
+            raise RuntimeError("sbx_policy_heads failed")
+        return buf.reshape(self.n, POLICY_HEADS)
 
     def solve_info(self, i: int) -> dict[str, float]:
         """Field solver of env i: kind ("lu"/"relax"), rho, sweeps of the last step, capped steps."""

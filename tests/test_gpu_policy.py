@@ -1,0 +1,122 @@
+"""Shared-policy rollout step on the GPU, through the C ABI.
+
+  - the MFMA MLP's head outputs against a float64 CPU evaluation of the same
+    weights on the same observations (fp32 products with K up to 1024:
+    within 2e-5 of the largest head value);
+  - the Beta sampler against the law it draws from (mean, variance,
+    Kolmogorov-Smirnov against scipy's Beta CDF), in (0, 1), deterministic;
+  - the action rows: continuous heads in [-1, 1], discrete heads in {0, 1},
+    zero past each env's action counts, a function of (seed, step) only;
+  - a rollout where the policy's actions drive the env: the oracle stepped
+    with the same action rows stays within the physics tolerance.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import pyoracle as po
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+from neurips2026_smart_building_challenge_amd import env as E  # noqa: E402
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    yield
+    torch.cuda.synchronize()
+
+
+def reference_heads(obs: np.ndarray, w: dict) -> np.ndarray:
+    W = {k: v.detach().cpu().double().numpy() for k, v in w.items()}
+    h1 = np.tanh(obs.astype(np.float64) @ W["w1"] + W["b1"])
+    h2 = np.tanh(h1 @ W["w2"] + W["b2"])
+    return h2 @ W["w3"] + W["b3"]
+
+
+def test_gpu_policy_heads_and_actions(mixed_dir):
+    print("policy: 60 mixed envs, heads vs float64 reference", flush=True)
+    vec = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=40)
+    w = E.policy_weights(123)
+    vec.policy_bind(w)
+    vec.reset()
+    for s in range(3):                       # a few steps so observations are not reset values only
+        vec.gen_actions(5, s)
+        vec.step()
+    vec.policy_act(7, 0)
+    torch.cuda.synchronize()
+    obs = vec.obs.cpu().numpy()
+    y = vec.policy_heads()
+    yr = reference_heads(obs, w)
+    err = np.max(np.abs(y - yr)) / max(1.0, np.max(np.abs(yr)))
+    assert err <= 2e-5, err
+    act = vec.actions.cpu().numpy()
+    for i in range(vec.n):
+        nc, nd = vec.envs[i].n_cont, vec.envs[i].n_disc
+        cont, disc = act[i, :256], act[i, 256:272]
+        assert np.all(np.abs(cont[:nc]) < 1.0) and np.all(cont[nc:] == 0.0)
+        assert set(np.unique(disc[:nd])) <= {0.0, 1.0} and np.all(disc[nd:] == 0.0)
+    first = act.copy()
+    vec.policy_act(7, 0)
+    torch.cuda.synchronize()
+    assert np.array_equal(vec.actions.cpu().numpy(), first), "actions are a function of (seed, step)"
+    vec.policy_act(7, 1)
+    torch.cuda.synchronize()
+    assert not np.array_equal(vec.actions.cpu().numpy()[:, :64], first[:, :64])
+    vec.close()
+
+
+@pytest.mark.parametrize("a,b", [(1.0, 1.0), (2.0, 2.0), (1.3, 5.0), (8.0, 1.5), (30.0, 30.0)])
+def test_gpu_beta_sampler_law(a, b):
+    from scipy import stats
+
+    n = 200_000
+    alpha = torch.full((n,), a, dtype=torch.float32, device="cuda")
+    beta = torch.full((n,), b, dtype=torch.float32, device="cuda")
+    x = E.beta_sample(alpha, beta, seed=11)
+    x2 = E.beta_sample(alpha, beta, seed=11)
+    torch.cuda.synchronize()
+    assert torch.equal(x, x2)
+    x = x.cpu().double().numpy()
+    assert np.all(x > 0.0) and np.all(x < 1.0)
+    mean = a / (a + b)
+    var = a * b / ((a + b) ** 2 * (a + b + 1))
+    assert abs(x.mean() - mean) < 5 * np.sqrt(var / n)
+    assert abs(x.var() - var) < 0.02 * var + 1e-4
+    assert stats.kstest(x, stats.beta(a, b).cdf).pvalue > 1e-4
+
+
+def test_gpu_policy_rollout_parity(mixed_dir):
+    """30 envs (one per scenario) driven by the policy for 70 steps (one auto-reset):
+    the oracle, stepped with the same action rows, agrees to the physics tolerance."""
+    print("policy rollout: 30 envs x 70 steps vs oracle", flush=True)
+    vec = E.VecEnv(30, blob_dir=str(mixed_dir), groups=30, max_steps=50)
+    vec.policy_bind(E.policy_weights(99))
+    twins = []
+    for i in range(vec.n):
+        path, start, seed = vec.meta(i)
+        twins.append(po.CpuEnv("oracle", path, seed, start=start, max_steps=50))
+    vec.reset()
+    for t in twins:
+        t.reset()
+    for s in range(70):
+        vec.policy_act(3, s)
+        torch.cuda.synchronize()
+        rows = vec.actions.cpu().numpy()
+        vec.step()
+        torch.cuda.synchronize()
+        rew = vec.rewards.cpu().numpy()
+        for i, t in enumerate(twins):
+            _, r, term, _ = t.step(rows[i])
+            assert abs(float(rew[i]) - r) <= 2 * np.spacing(np.float32(abs(r))) + 1e-12, (s, i)
+            if s % 10 == 9:
+                g, c = vec.state(i), t.state()
+                g = g[:len(c)]
+                fin = ~np.isnan(g)
+                rel = np.abs(g[fin] - c[fin]) / np.maximum(np.abs(c[fin]), 1.0)
+                assert rel.max() <= 1e-9, (s, i, rel.max())
+    vec.close()
