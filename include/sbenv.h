@@ -175,13 +175,16 @@ int sbx_phase_stamps(Env* envs, unsigned long long* out, int cap);
 int sbx_pass_times(Env* envs, int env, long long* cycles, int cap);
 
 /* Field solver of env i's layout and its counters: out[0] solver (0 LU plan,
- * 1 relaxation), out[1] the certified contraction bound rho (relaxation; 0
+ * 1 point relaxation, 2 block relaxation), out[1] the certified contraction
+ * bound rho (relaxation; 0
  * otherwise), out[2] relaxation sweeps of the env's last step, out[3] steps of
  * the env that stopped at the sweep cap (64) without meeting the error bound.
- * The solver is chosen per vec by kwargs "solver": "auto" (default:
- * relaxation for every layout where it is certified, rho <= 0.5, at most 256
- * solved cells and 8 off-diagonal entries per row), "lu" or "relax". Returns
- * 4, or -1. Synchronous. */
+ * The solver is chosen per vec by kwargs "solver": "auto" (default: block
+ * relaxation where it is certified — A an M-matrix, blocks of at most 3 nodes,
+ * at most 128 blocks and 8 off-block entries per block, rho <= 0.5 — else point
+ * relaxation where certified — rho <= 0.5, at most 256 solved cells and 8
+ * off-diagonal entries per row — else the LU plan), "relax" (the same without
+ * the LU fallback), "point" or "lu". Returns 4, or -1. Synchronous. */
 int sbx_solve_info(Env* envs, int i, double* out);
 
 /* Shared-policy rollout step (the reference trainer's
@@ -261,6 +264,23 @@ typedef struct SbxPlan {
     const int* rx_air;           /* [rx_rows] */
     const double* rx_val;        /* [rx_terms_max * rx_rows] */
     const int* rx_col;           /* [rx_terms_max * rx_rows] */
+    /* block-Jacobi form: blocks of at most bx_rows nodes; lane l owns blocks l
+     * and l + 64 (block slot q < bx_slots); tables lane-minor (64 lanes):
+     * bx_row / bx_diag / bx_air at (q * bx_rows + p) * 64 + l (node or -1, a_ii,
+     * air column or -1), bx_in at ((q * bx_rows + p) * bx_rows + p2) * 64 + l
+     * (a(row p, row p2), 0 on p == p2), and the block's off-block entries
+     * bx_val / bx_col / bx_trow at (q * bx_terms_max + t) * 64 + l (value,
+     * column, row within the block; (0.0, 0, 0) padding) */
+    int bx_ok;
+    int bx_rows, bx_slots, bx_terms_max, bx_terms, bx_blocks;
+    double bx_rho;               /* max_i sum_j (|A_BB^-1| |A_BO|)_ij */
+    const int* bx_row;
+    const double* bx_diag;
+    const int* bx_air;
+    const double* bx_in;
+    const double* bx_val;
+    const int* bx_col;
+    const int* bx_trow;
 } SbxPlan;
 int sbx_plan_layout(const char* blob_path, int width, SbxPlan* out);
 void sbx_plan_free(SbxPlan* p);

@@ -358,4 +358,171 @@ void build_relax(const Blob& b, const SolvePlan& lu, RelaxPlan* out) {
     R.ok = true;
 }
 
+namespace {
+
+// Inverse of a small dense matrix (row-major, m x m) by Gauss-Jordan with
+// partial pivoting; false if singular.
+bool invert_small(std::vector<double> a, int m, std::vector<double>* inv) {
+    std::vector<double>& r = *inv;
+    r.assign((size_t)m * m, 0.0);
+    for (int i = 0; i < m; i++) r[(size_t)i * m + i] = 1.0;
+    for (int c = 0; c < m; c++) {
+        int p = c;
+        for (int i = c + 1; i < m; i++)
+            if (std::fabs(a[(size_t)i * m + c]) > std::fabs(a[(size_t)p * m + c])) p = i;
+        if (a[(size_t)p * m + c] == 0.0) return false;
+        for (int j = 0; j < m; j++) {
+            std::swap(a[(size_t)c * m + j], a[(size_t)p * m + j]);
+            std::swap(r[(size_t)c * m + j], r[(size_t)p * m + j]);
+        }
+        const double d = a[(size_t)c * m + c];
+        for (int j = 0; j < m; j++) {
+            a[(size_t)c * m + j] /= d;
+            r[(size_t)c * m + j] /= d;
+        }
+        for (int i = 0; i < m; i++) {
+            if (i == c) continue;
+            const double f = a[(size_t)i * m + c];
+            if (f == 0.0) continue;
+            for (int j = 0; j < m; j++) {
+                a[(size_t)i * m + j] -= f * a[(size_t)c * m + j];
+                r[(size_t)i * m + j] -= f * r[(size_t)c * m + j];
+            }
+        }
+    }
+    return true;
+}
+
+}  // namespace
+
+void build_block(const Blob& b, const SolvePlan& lu, BlockPlan* out) {
+    BlockPlan& B = *out;
+    B = BlockPlan();
+    const int n = lu.n;
+    auto no = [&](const std::string& why) { B.ok = false; B.why = why; };
+    if (n > 64 * kBlockSlots * kBlockRows)
+        return no("more than " + std::to_string(64 * kBlockSlots * kBlockRows) + " solved cells");
+    uint64_t cnt = 0;
+    const int32_t* Ap = b.i32("A_system_indptr", &cnt);
+    const int32_t* Ai = b.i32("A_system_indices");
+    const double* Ax = b.f64("A_system_data");
+    if (!Ap || !Ai || !Ax || (int)cnt != n + 1) return no("blob lacks A_system");
+    std::vector<double> A((size_t)n * n, 0.0);
+    for (int c = 0; c < n; c++)
+        for (int p = Ap[c]; p < Ap[c + 1]; p++) {
+            if (Ai[p] < 0 || Ai[p] >= n) return no("A_system row index out of range");
+            A[(size_t)Ai[p] * n + c] += Ax[p];
+        }
+    auto a = [&](int i, int j) { return A[(size_t)i * n + j]; };
+    for (int i = 0; i < n; i++) {
+        if (!(a(i, i) > 0.0)) return no("a diagonal entry of A is not positive");
+        for (int j = 0; j < n; j++)
+            if (j != i && a(i, j) > 0.0) return no("A has a positive off-diagonal entry (not an M-matrix)");
+    }
+    // greedy partition: strongest couplings first, blocks of at most kBlockRows
+    struct Edge {
+        double s;
+        int i, j;
+    };
+    std::vector<Edge> edges;
+    for (int i = 0; i < n; i++)
+        for (int j = i + 1; j < n; j++) {
+            const double s = std::max(std::fabs(a(i, j)), std::fabs(a(j, i)));
+            if (s > 0.0) edges.push_back({s / std::min(a(i, i), a(j, j)), i, j});
+        }
+    std::stable_sort(edges.begin(), edges.end(), [](const Edge& x, const Edge& y) { return x.s > y.s; });
+    std::vector<int> parent(n), size(n, 1);
+    for (int i = 0; i < n; i++) parent[i] = i;
+    auto find = [&](int x) {
+        while (parent[x] != x) x = parent[x] = parent[parent[x]];
+        return x;
+    };
+    for (const Edge& e : edges) {
+        int x = find(e.i), y = find(e.j);
+        if (x == y || size[x] + size[y] > kBlockRows) continue;
+        if (y < x) std::swap(x, y);
+        parent[y] = x;
+        size[x] += size[y];
+    }
+    std::vector<int> bid(n, -1);
+    for (int i = 0; i < n; i++) {
+        const int r = find(i);
+        if (bid[r] < 0) {
+            bid[r] = (int)B.blocks.size();
+            B.blocks.push_back({});
+        }
+        B.blocks[bid[r]].push_back(i);
+        bid[i] = bid[r];
+    }
+    B.n_blocks = (int)B.blocks.size();
+    if (B.n_blocks > 64 * kBlockSlots) return no("more than " + std::to_string(64 * kBlockSlots) + " blocks");
+    // per-row bound and off-block terms
+    double rho = 0.0;
+    int terms = 0;
+    std::vector<std::vector<double>> binv(B.n_blocks);
+    for (int k = 0; k < B.n_blocks; k++) {
+        const auto& blk = B.blocks[k];
+        const int m = (int)blk.size();
+        std::vector<double> M((size_t)m * m);
+        for (int x = 0; x < m; x++)
+            for (int y = 0; y < m; y++) M[(size_t)x * m + y] = a(blk[x], blk[y]);
+        if (!invert_small(M, m, &binv[k])) return no("a diagonal block of A is singular");
+        double mx = 0.0;
+        for (double v : binv[k]) mx = std::max(mx, std::fabs(v));
+        for (double v : binv[k])
+            if (v < -1e-14 * mx) return no("a diagonal block of A has a negative inverse entry");
+        int t = 0;
+        for (int x = 0; x < m; x++) {
+            double s = 0.0;
+            for (int j = 0; j < n; j++) {
+                if (bid[j] == k) continue;
+                double col_sum = 0.0;
+                for (int y = 0; y < m; y++) col_sum += std::fabs(binv[k][(size_t)x * m + y]) * std::fabs(a(blk[y], j));
+                s += col_sum;
+                if (a(blk[x], j) != 0.0) t++;
+            }
+            rho = std::max(rho, s);
+        }
+        terms = std::max(terms, t);
+    }
+    B.rho = rho;
+    B.terms = terms;
+    if (terms > kBlockTerms) return no("a block has more than " + std::to_string(kBlockTerms) + " off-block entries");
+    if (!(rho <= kRelaxRhoMax)) return no("block bound too large (rho " + std::to_string(rho) + ")");
+    // tables
+    const int R = kBlockRows, T = kBlockTerms, Q = kBlockSlots;
+    B.row.assign((size_t)Q * R * 64, -1);
+    B.diag.assign((size_t)Q * R * 64, 1.0);
+    B.air.assign((size_t)Q * R * 64, -1);
+    B.in.assign((size_t)Q * R * R * 64, 0.0);
+    B.val.assign((size_t)Q * T * 64, 0.0);
+    B.col.assign((size_t)Q * T * 64, 0);
+    B.trow.assign((size_t)Q * T * 64, 0);
+    std::vector<int> air_of(n, -1);
+    for (int c = 0; c < lu.k; c++) air_of[lu.air_node[c]] = c;
+    for (int k = 0; k < B.n_blocks; k++) {
+        const auto& blk = B.blocks[k];
+        const int lane = k % 64, q = k / 64;
+        int t = 0;
+        for (int p = 0; p < (int)blk.size(); p++) {
+            const int i = blk[p];
+            const size_t at = (size_t)(q * R + p) * 64 + lane;
+            B.row[at] = i;
+            B.diag[at] = a(i, i);
+            B.air[at] = air_of[i];
+            for (int p2 = 0; p2 < (int)blk.size(); p2++)
+                if (p2 != p) B.in[((size_t)(q * R + p) * R + p2) * 64 + lane] = a(i, blk[p2]);
+            for (int j = 0; j < n; j++)
+                if (bid[j] != k && a(i, j) != 0.0) {
+                    const size_t e = (size_t)(q * T + t) * 64 + lane;
+                    B.val[e] = a(i, j);
+                    B.col[e] = j;
+                    B.trow[e] = p;
+                    t++;
+                }
+        }
+    }
+    B.ok = true;
+}
+
 }  // namespace sbh

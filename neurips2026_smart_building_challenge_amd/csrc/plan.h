@@ -78,4 +78,39 @@ struct RelaxPlan {
 // the relaxation form applies and out->why why not.
 void build_relax(const Blob& b, const SolvePlan& lu, RelaxPlan* out);
 
+// Block-Jacobi form: nodes grouped into blocks of at most kBlockRows (greedy,
+// strongest coupling |a_ij| / min(a_ii, a_jj) first), each block solved
+// exactly per sweep: x_B <- (A_BB + G_B)^-1 (b_B - A_BO x_O). When A is an
+// M-matrix (off-diagonal entries <= 0, every A_BB with a non-negative inverse),
+// adding g >= 0 to diagonals only shrinks |(A_BB + G_B)^-1| entrywise, so
+//   rho = max_i sum_j (|A_BB^-1| |A_BO|)_ij      (at g = 0)
+// bounds every step's iteration matrix in the infinity norm, with the same
+// a-posteriori stopping bound as the point form. Lane l owns blocks l and
+// l + 64 (block slot q = 0, 1). A block's off-block entries form one list of
+// at most kBlockTerms (value, column, row within the block), so the kernel can
+// fold the block inverse into them once per step and sweep with one gather per
+// entry.
+constexpr int kBlockRows = 3;
+constexpr int kBlockSlots = 2;
+constexpr int kBlockTerms = 8;                             // off-block entries per block
+
+struct BlockPlan {
+    bool ok = false;
+    std::string why;
+    int n_blocks = 0, terms = 0;            // terms: most off-block entries of one block
+    double rho = 0.0;
+    std::vector<std::vector<int>> blocks;   // node lists, ascending
+    // tables, lane-minor (64 lanes), q = block slot, p / p2 = row within the block,
+    // t = entry of the block's off-block list
+    std::vector<int> row;                   // [(q * R + p) * 64 + lane]: node or -1
+    std::vector<double> diag;               // same index: a_ii (1.0 for padding)
+    std::vector<int> air;                   // same index: air column or -1
+    std::vector<double> in;                 // [((q * R + p) * R + p2) * 64 + lane]: a(row p, row p2), 0 on p == p2
+    std::vector<double> val;                // [(q * T + t) * 64 + lane]: entry value (0.0 padding)
+    std::vector<int> col;                   // same index: its column (0 padding)
+    std::vector<int> trow;                  // same index: its row within the block (0 padding)
+};
+
+void build_block(const Blob& b, const SolvePlan& lu, BlockPlan* out);
+
 }  // namespace sbh

@@ -23,6 +23,9 @@
 #define SBK_RX_TERMS 8   // relaxation off-diagonal entries per row
 #define SBK_RX_MAXIT 64  // sweep cap (rho <= 1/2 contracts by 2^-64 before it)
 #define SBK_RX_TOL 1e-13 // stop when the error bound is below TOL * max |T|
+#define SBK_BX_ROWS 3    // block-Jacobi rows per block (matches the planner)
+#define SBK_BX_SLOTS 2   // block slots per lane
+#define SBK_BX_TERMS 8   // off-block entries per block
 
 namespace sbk {
 
@@ -95,6 +98,12 @@ struct ImgLayout {
     int ahu_col_off, ahu_cols;     // [na + 1], [k]: each AHU's coupled columns, ascending
     int act_src, act_dst, act_aux;                          // [n_act] (dst/aux: ACT_*)
     int air_slot, air_node;                                 // [k]
+    // block-Jacobi tables (block form only), chunk-major so lane l reading block
+    // b = q * 64 + l takes 16 consecutive bytes per chunk: bx_d double2[9][nb]
+    // = a_ii (3), in-block a(p, p2) for (0,1) (0,2) (1,0) (1,2) (2,0) (2,1), the
+    // 8 off-block entry values, 0; bx_i int4[3][nb] = row | air << 16 (3, each
+    // -1 as 0xffff / -1), 0, then col | row-in-block << 16 of the 8 entries
+    int bx_d, bx_i;
     // u8
     int is_room;                                            // [n]
     int act_disc, act_flags;                                // [n_act]
@@ -142,7 +151,8 @@ struct DevLayout {
     int n_slots, vec_base, n_pass, width;
     int max_room_cells;
     int solver;                        // SOLVER_LU or SOLVER_RELAX
-    int rx_terms;                      // longest off-diagonal row (relaxation)
+    int rx_terms;                      // longest off-diagonal (or off-block) row (relaxation)
+    int rx_block;                      // block-Jacobi form with 1 or 2 block slots per lane (bx_*), 0: point form (rx_*)
     double rx_stop;                    // rho / (1 - rho)
     StateLayout st;
     LdsLayout lds;
@@ -153,6 +163,7 @@ struct DevLayout {
     const SBK_C int* rx_air;           // [SBK_RX_ROWS] air-side column or -1
     const SBK_C double* rx_val;        // [SBK_RX_TERMS * SBK_RX_ROWS]
     const SBK_C int* rx_col;           // [SBK_RX_TERMS * SBK_RX_ROWS]
+    int bx_nb;                         // block-Jacobi blocks (tables in the layout image: bx_d, bx_i)
     // solve plan
     const SBK_C int* pinfo;            // [n_pass * 4]: hdr_off, word_off, nact | maxcnt << 8 | pivot << 16, 0
     const SBK_C uint64_t* hdr;         // per active lane: target | mul << 16 | inv_target << 32 | count << 48

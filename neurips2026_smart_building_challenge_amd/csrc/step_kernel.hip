@@ -40,14 +40,15 @@ enum { M_OFF = 0, M_HEAT = 1, M_COOL = 2, M_PASSIVE = 3 };
             P.phase_ts[(size_t)c.e * SBK_NSTAMP + (i)] = wall_clock64();                \
     } while (0)
 
-// Orders this wave's LDS accesses before and after the point (the wave's DS
-// operations complete in issue order) without waiting for global loads, so
-// the next pass's term words stay in flight across the synchronisation.
+// Orders this wavefront's LDS accesses before and after the point. A
+// wavefront's LDS operations are performed in issue order, so a wavefront-scope
+// fence needs no wait (nothing is emitted for it): it only keeps the compiler
+// from moving memory accesses across the point, and LDS reads and writes
+// still in flight stay in flight, as do global loads.
 __device__ __forceinline__ void wave_lds_sync() {
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0), vmcnt/expcnt untouched
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     __builtin_amdgcn_wave_barrier();
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 }
 
 // Lane of the calling thread within its env's wavefront (a workgroup holds one
@@ -179,6 +180,71 @@ __device__ __forceinline__ void wave_sum2(double& a, double& b) {
 #undef SBK_STEP2
     a = lane63_d(a);
     b = lane63_d(b);
+}
+
+// Sums of N per-lane values in one pass (N independent DPP chains).
+template <int N>
+__device__ __forceinline__ void wave_sum_n(double (&x)[N]) {
+#define SBK_STEPN(CTRL, ROWS)                                          \
+    _Pragma("unroll") for (int i = 0; i < N; i++) x[i] = x[i] + dpp_d<CTRL, ROWS>(0.0, x[i]);
+    SBK_STEPN(DPP_QUAD_1032, 0xF)
+    SBK_STEPN(DPP_QUAD_2301, 0xF)
+    SBK_STEPN(DPP_ROW_HALF_MIRROR, 0xF)
+    SBK_STEPN(DPP_ROW_MIRROR, 0xF)
+    SBK_STEPN(DPP_ROW_BCAST15, 0xA)
+    SBK_STEPN(DPP_ROW_BCAST31, 0xC)
+#undef SBK_STEPN
+#pragma unroll
+    for (int i = 0; i < N; i++) x[i] = lane63_d(x[i]);
+}
+
+// Per-AHU sums of NV per-lane values, Q AHUs (a0 .. a0 + Q - 1) per pass with
+// their reductions interleaved; lane l receives the sums of AHU l in mine[]
+// (lanes l outside the pass keep what they had).
+template <int NV, int Q>
+__device__ __forceinline__ void ahu_sums_pass(const int (&key)[SBK_VPL], const double (&vals)[SBK_VPL][NV], int a0,
+                                              double (&mine)[NV]) {
+    double x[Q * NV];
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+#pragma unroll
+        for (int k = 0; k < NV; k++) {
+            double acc = 0.0;
+#pragma unroll
+            for (int r = 0; r < SBK_VPL; r++) acc += key[r] == a0 + q ? vals[r][k] : 0.0;
+            x[q * NV + k] = acc;
+        }
+    }
+    wave_sum_n<Q * NV>(x);
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        const bool me = ln() == a0 + q;
+#pragma unroll
+        for (int k = 0; k < NV; k++) mine[k] = me ? x[q * NV + k] : mine[k];
+    }
+}
+
+// Per-AHU sums of NV per-lane values: lane a < na receives in mine[k] the
+// wavefront's sum of vals[r][k] over the slots r with key[r] == a. Every lane
+// of the wavefront must be active.
+template <int NV>
+__device__ __forceinline__ void ahu_sums(const int (&key)[SBK_VPL], const double (&vals)[SBK_VPL][NV], int na,
+                                         double (&mine)[NV]) {
+#pragma unroll
+    for (int k = 0; k < NV; k++) mine[k] = 0.0;
+    for (int a0 = 0; a0 < na;) {
+        const int left = na - a0;
+        if (left >= 3) {
+            ahu_sums_pass<NV, 4>(key, vals, a0, mine);
+            a0 += 4;
+        } else if (left == 2) {
+            ahu_sums_pass<NV, 2>(key, vals, a0, mine);
+            a0 += 2;
+        } else {
+            ahu_sums_pass<NV, 1>(key, vals, a0, mine);
+            a0 += 1;
+        }
+    }
 }
 
 // Inclusive prefix sum over the wavefront.
@@ -850,42 +916,35 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
     // this lane's VAVs (v = lane + 64 r), kept in registers for the AHU sums
     double ffs_part = 0.0;
     int vahu[SBK_VPL];
-    double vws[SBK_VPL], varea[SBK_VPL], vdm[SBK_VPL];
+    double vv[SBK_VPL][3];   // sensing * area, area (zone area > 0 only), unrestricted flow
 #pragma unroll
     for (int r = 0; r < SBK_VPL; r++) {
         const int v = ln() + 64 * r;
         vahu[r] = -1;
-        vws[r] = varea[r] = vdm[r] = 0.0;
+        vv[r][0] = vv[r][1] = vv[r][2] = 0.0;
         if (v < nv) {
             ffs_part += c.reheat[v] * c.t.vav_c[v * 9 + 1];
             const double u = vav_unrestricted(c, v);
             c.unres[v] = u;
             const double area = c.t.vav_area[v];
             vahu[r] = c.t.vav_ahu[v];
-            vdm[r] = u;
+            vv[r][2] = u;
             if (area > 0.0) {
-                vws[r] = c.sensing[v] * area;
-                varea[r] = area;
+                vv[r][0] = c.sensing[v] * area;
+                vv[r][1] = area;
             }
         }
     }
     const double ffs = bsum<W>(ffs_part, c.red);
-    for (int a = 0; a < na; a++) {
-        double ws = 0.0, at = 0.0, dm = 0.0;
-#pragma unroll
-        for (int r = 0; r < SBK_VPL; r++) {
-            const bool m = vahu[r] == a;
-            ws += m ? vws[r] : 0.0;
-            at += m ? varea[r] : 0.0;
-            dm += m ? vdm[r] : 0.0;
-        }
-        wave_sum3(ws, at, dm);
-        if (ln() == 0) {
-            double rt = (at > 0.0) ? ws / at : tmean;
-            double mixed = c.recirc[a] * rt + (1.0 - c.recirc[a]) * ambient;
-            c.satv[a] = (mixed > c.sat[a] && c.run[a] == 1) ? c.sat[a] : mixed;
-            c.demand[a] = dm;
-        }
+    double sums[3];
+    ahu_sums<3>(vahu, vv, na, sums);
+    if (ln() < na) {
+        const int a = ln();
+        const double ws = sums[0], at = sums[1], dm = sums[2];
+        double rt = (at > 0.0) ? ws / at : tmean;
+        double mixed = c.recirc[a] * rt + (1.0 - c.recirc[a]) * ambient;
+        c.satv[a] = (mixed > c.sat[a] && c.run[a] == 1) ? c.sat[a] : mixed;
+        c.demand[a] = dm;
     }
     if (ln() == 0) {
         c.misc[MS_FFS] = ffs;
@@ -910,11 +969,11 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
     // and the coil extremes for the boiler return temperature (sb_sim.c:495-499)
     double total_rw = 0.0, cmin = 1e308, cmax = -1e308;
     int cahu[SBK_VPL];
-    double cfd[SBK_VPL];
+    double cfd[SBK_VPL][2];   // flow demand, 1 (count) of columns with area > 0 and demand > 0
 #pragma unroll
     for (int r = 0; r < SBK_VPL; r++) {
         cahu[r] = -1;
-        cfd[r] = 0.0;
+        cfd[r][0] = cfd[r][1] = 0.0;
     }
     for (int col = ln(); col < L->k; col += W) {
         int v = c.t.coupled[col];
@@ -959,25 +1018,20 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
         const int r = col >> 6;
         if (c.t.vav_area[v] > 0.0 && fd > 0.0) {
             cahu[r] = c.t.vav_ahu[v];
-            cfd[r] = fd;
+            cfd[r][0] = fd;
+            cfd[r][1] = 1.0;
         }
     }
     wave_sum_min_max(total_rw, cmin, cmax);
     // AHU flow (clamped to the AHU's maximum) and cooling requests
-    for (int a = 0; a < na; a++) {
-        double f = 0.0, cnt = 0.0;
-#pragma unroll
-        for (int r = 0; r < SBK_VPL; r++) {
-            const bool m = cahu[r] == a;
-            f += m ? cfd[r] : 0.0;
-            cnt += m ? 1.0 : 0.0;
-        }
-        wave_sum2(f, cnt);
-        if (ln() == 0) {
-            const double mf = c.t.ahu_c[a * 9 + 1];
-            c.flow[a] = f > mf ? mf : f;
-            c.coolreq[a] = (int)cnt;
-        }
+    double fsum[2];
+    ahu_sums<2>(cahu, cfd, na, fsum);
+    if (ln() < na) {
+        const int a = ln();
+        const double f = fsum[0], cnt = fsum[1];
+        const double mf = c.t.ahu_c[a * 9 + 1];
+        c.flow[a] = f > mf ? mf : f;
+        c.coolreq[a] = (int)cnt;
     }
     if (ln() == 0) {
         c.misc[MS_TOTAL_REHEAT] = total_rw;
@@ -1155,7 +1209,8 @@ __device__ __forceinline__ int relax_sweeps(const SBK_C DevLayout* L, double* x,
             ci[j][m] = L->rx_col[m * SBK_RX_ROWS + t];
         }
     }
-    const double stop = L->rx_stop;
+    double stop = L->rx_stop;
+    asm volatile("" : "+v"(stop));   // keep it in a VGPR: no scalar reload (and lgkm wait) per sweep
     if (pts) pts[1] = clock64();
     int it = 0;
     bool done = false;
@@ -1235,6 +1290,206 @@ __device__ __forceinline__ void relax_solve(Ctx& c, double ambient, double irr, 
     esync();
 }
 
+// ------------------------------------------------------------------ block relaxation
+// Block-Jacobi form: lane l owns blocks l and l + 64 (block slot q < Q) of at
+// most three nodes. Once per step each block's matrix A_BB + G_B is inverted
+// in registers (Gauss-Jordan without pivoting: it is an M-matrix, so pivots
+// stay positive) and folded into the block's list of off-block entries:
+//   x_B = c0 - sum_t cf_t x[col_t],  c0 = (A_BB + G_B)^-1 b_B,
+//   cf_t = (A_BB + G_B)^-1 e_{row_t} a_t,
+// so a sweep is one LDS gather per off-block entry and a few FMAs per row.
+// Padding rows have c0 = cf = 0 and store to a per-lane sink. Same stopping
+// bound as the point form, with the host's block rho.
+constexpr int BXR = SBK_BX_ROWS, BXT = SBK_BX_TERMS;
+
+template <int Q>
+__device__ __forceinline__ int block_sweeps(double* x, const int (&col)[Q][BXT], const double (&cf)[Q][BXR][BXT],
+                                            const double (&c0)[Q][BXR], const int (&dst)[Q][BXR],
+                                            double (&xv)[Q][BXR], double stop, double atol,
+                                            unsigned long long* pts) {
+    asm volatile("" : "+v"(stop));   // keep it in a VGPR: no scalar reload (and lgkm wait) per sweep
+    if (pts) pts[1] = clock64();
+    int it = 0;
+    bool done = false;
+    while (!done) {
+        double xg[Q][BXT];
+#pragma unroll
+        for (int q = 0; q < Q; q++) {
+#pragma unroll
+            for (int t = 0; t < BXT; t++) xg[q][t] = x[col[q][t]];
+        }
+        double dmax = 0.0;
+#pragma unroll
+        for (int q = 0; q < Q; q++) {
+#pragma unroll
+            for (int p = 0; p < BXR; p++) {
+                double acc = c0[q][p];
+#pragma unroll
+                for (int t = 0; t < BXT; t++) acc -= cf[q][p][t] * xg[q][t];
+                dmax = fmax(dmax, fabs(acc - xv[q][p]));
+                xv[q][p] = acc;
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < Q; q++) {
+#pragma unroll
+            for (int p = 0; p < BXR; p++) x[dst[q][p]] = xv[q][p];
+        }
+        wave_lds_sync();
+        ++it;
+        done = __all(stop * dmax <= atol) || it >= SBK_RX_MAXIT;
+        if (pts) pts[1 + it] = clock64();
+    }
+    return it;
+}
+
+template <int Q>
+__device__ __forceinline__ void relax_block_solve(Ctx& c, double ambient, double irr, unsigned long long* pts) {
+    const SBK_C DevLayout* L = c.L;
+    const int lane = ln();
+    if (pts) pts[0] = clock64();
+    // per-lane sink for padding rows, as an index relative to the iterate
+    const int sink = (int)((c.red + lane) - c.T);
+    // block tables from the staged layout image: lane l takes block q * 64 + l
+    // (clamped into the table, and then turned into padding, past the last one)
+    static_assert(BXR == 3 && BXT == 8, "the chunk layout holds three rows and eight entries");
+    const int nb = L->bx_nb;
+    const double2* bxd = reinterpret_cast<const double2*>(c.imgb + L->img.bx_d);
+    const int4* bxi = reinterpret_cast<const int4*>(c.imgb + L->img.bx_i);
+    int row[Q][BXR], air[Q][BXR], col[Q][BXT], trow[Q][BXT];
+    double dia[Q][BXR], inm[Q][BXR][BXR], val[Q][BXT];
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        const int blk = q * 64 + lane;
+        const bool ok = blk < nb;
+        const int bc = ok ? blk : nb - 1;
+        double rd[18];
+        int ri[12];
+#pragma unroll
+        for (int j = 0; j < 9; j++) {
+            const double2 v = bxd[j * nb + bc];
+            rd[2 * j] = v.x;
+            rd[2 * j + 1] = v.y;
+        }
+#pragma unroll
+        for (int j = 0; j < 3; j++) {
+            const int4 v = bxi[j * nb + bc];
+            ri[4 * j] = v.x;
+            ri[4 * j + 1] = v.y;
+            ri[4 * j + 2] = v.z;
+            ri[4 * j + 3] = v.w;
+        }
+#pragma unroll
+        for (int p = 0; p < BXR; p++) {
+            row[q][p] = ok ? (ri[p] << 16) >> 16 : -1;
+            air[q][p] = ok ? ri[p] >> 16 : -1;
+            dia[q][p] = ok ? rd[p] : 1.0;
+            inm[q][p][p] = 0.0;
+        }
+        inm[q][0][1] = ok ? rd[3] : 0.0;
+        inm[q][0][2] = ok ? rd[4] : 0.0;
+        inm[q][1][0] = ok ? rd[5] : 0.0;
+        inm[q][1][2] = ok ? rd[6] : 0.0;
+        inm[q][2][0] = ok ? rd[7] : 0.0;
+        inm[q][2][1] = ok ? rd[8] : 0.0;
+#pragma unroll
+        for (int t = 0; t < BXT; t++) {
+            val[q][t] = ok ? rd[9 + t] : 0.0;
+            col[q][t] = ok ? ri[4 + t] & 0xffff : 0;
+            trow[q][t] = ok ? ri[4 + t] >> 16 : 0;
+        }
+    }
+    int dst[Q][BXR];
+    double xv[Q][BXR], c0[Q][BXR], cf[Q][BXR][BXT];
+    double xabs = 0.0;
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+        double m[BXR][BXR], bi[BXR][BXR], b[BXR];
+#pragma unroll
+        for (int p = 0; p < BXR; p++) {
+            const int t = row[q][p];
+            const int tc = t >= 0 ? t : 0;
+            double d = dia[q][p];
+            const double qin = c.t.is_room[tc] ? c.slots[tc] + c.t.solar_c[tc] * irr : c.t.solar_c[tc] * irr;
+            double bb = c.t.cap[tc] * c.T[tc] + qin + ambient * c.dirx[tc] + c.t.mcoup[tc] * c.M[tc];
+            const int ac = air[q][p];
+            if (ac >= 0) {
+                const double g = c.g[ac];
+                bb += g * c.tair[ac];
+                d += g;
+            }
+#pragma unroll
+            for (int p2 = 0; p2 < BXR; p2++) {
+                m[p][p2] = p2 == p ? d : inm[q][p][p2];
+                bi[p][p2] = p2 == p ? 1.0 : 0.0;
+            }
+            dst[q][p] = t >= 0 ? t : sink;
+            b[p] = t >= 0 ? bb : 0.0;
+            xv[q][p] = t >= 0 ? c.T[tc] : 0.0;
+            if (t >= 0) xabs = fmax(xabs, fabs(xv[q][p]));
+        }
+#pragma unroll
+        for (int k = 0; k < BXR; k++) {
+            const double rp = recip(m[k][k]);
+#pragma unroll
+            for (int j = 0; j < BXR; j++) {
+                m[k][j] *= rp;
+                bi[k][j] *= rp;
+            }
+#pragma unroll
+            for (int i = 0; i < BXR; i++) {
+                if (i == k) continue;
+                const double f = m[i][k];
+#pragma unroll
+                for (int j = 0; j < BXR; j++) {
+                    m[i][j] -= f * m[k][j];
+                    bi[i][j] -= f * bi[k][j];
+                }
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < BXR; p++) {
+            double acc = 0.0;
+#pragma unroll
+            for (int p2 = 0; p2 < BXR; p2++) acc += bi[p][p2] * b[p2];
+            c0[q][p] = acc;
+        }
+        // cf = bi * (entry value placed in its row): three plain selects and
+        // nine FMAs per entry (a select chain over the row index compiles to
+        // exec-mask branches)
+#pragma unroll
+        for (int t = 0; t < BXT; t++) {
+            const int r = trow[q][t];
+            double vr[BXR];
+#pragma unroll
+            for (int p2 = 0; p2 < BXR; p2++) vr[p2] = r == p2 ? val[q][t] : 0.0;
+#pragma unroll
+            for (int p = 0; p < BXR; p++) {
+                double acc = bi[p][0] * vr[0];
+#pragma unroll
+                for (int p2 = 1; p2 < BXR; p2++) acc = fma(bi[p][p2], vr[p2], acc);
+                cf[q][p][t] = acc;
+            }
+        }
+    }
+    static_assert(BXR == 3, "the entry-row select above assumes three rows per block");
+    const double atol = SBK_RX_TOL * wave_max(xabs);
+    const int it = block_sweeps<Q>(c.T, col, cf, c0, dst, xv, L->rx_stop, atol, pts);
+    if (lane == 0) {
+        c.plant[PF_SWEEPS] = (double)it;
+        if (it >= SBK_RX_MAXIT) c.plant[PF_CAPPED] += 1.0;
+    }
+#pragma unroll
+    for (int q = 0; q < Q; q++) {
+#pragma unroll
+        for (int p = 0; p < BXR; p++) {
+            const int t = row[q][p];
+            if (t >= 0) c.M[t] = c.M[t] * c.t.mret[t] + c.t.mgain[t] * xv[q][p];
+        }
+    }
+    esync();
+}
+
 // Field step: b = cap T + q + amb dirx + mc M (+ solar, + g T_air at the air
 // nodes), then (A + diag(g)) y = b by the plan (or by relaxation); mass and
 // field update.
@@ -1255,7 +1510,9 @@ __device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
         esync();
         STAMP(4);
         unsigned long long* pts = (P.pass_ts && c.e == P.pass_ts_env && ln() == 0) ? P.pass_ts : nullptr;
-        relax_solve<W>(c, ambient, irr, pts);
+        if (L->rx_block == 2) relax_block_solve<2>(c, ambient, irr, pts);
+        else if (L->rx_block == 1) relax_block_solve<1>(c, ambient, irr, pts);
+        else relax_solve<W>(c, ambient, irr, pts);
         STAMP(5);
         return;
     }
@@ -1349,32 +1606,27 @@ __device__ __forceinline__ double reward(Ctx& c) {
     // mean over its VAVs in VAV order and its blower / cooling terms, which
     // every lane then sums in AHU order (sb_reward.c:62-98)
     int vahu[SBK_VPL];
-    double vws[SBK_VPL], varea[SBK_VPL];
+    double vv[SBK_VPL][2];   // temperature * area, area (zone area > 0 only)
 #pragma unroll
     for (int r = 0; r < SBK_VPL; r++) {
         const int v = ln() + 64 * r;
         vahu[r] = -1;
-        vws[r] = varea[r] = 0.0;
+        vv[r][0] = vv[r][1] = 0.0;
         if (v < L->nv) {
             double area;
             const double tv = vav_temp(c, c.zq, v, &area);
             vahu[r] = c.t.vav_ahu[v];
             if (area > 0.0) {
-                vws[r] = tv * area;
-                varea[r] = area;
+                vv[r][0] = tv * area;
+                vv[r][1] = area;
             }
         }
     }
-    for (int a = 0; a < L->na; a++) {
-        double ws = 0.0, at = 0.0;
-#pragma unroll
-        for (int r = 0; r < SBK_VPL; r++) {
-            const bool m = vahu[r] == a;
-            ws += m ? vws[r] : 0.0;
-            at += m ? varea[r] : 0.0;
-        }
-        wave_sum2(ws, at);
-        if (ln() != a) continue;
+    double sums[2];
+    ahu_sums<2>(vahu, vv, L->na, sums);
+    if (ln() < L->na) {
+        const int a = ln();
+        const double ws = sums[0], at = sums[1];
         double rc = (at > 0.0) ? ws / at : tmean;
         double st = ahu_static(c, a);
         double fe = c.t.ahu_c[a * 9 + 5];
@@ -1483,7 +1735,7 @@ __device__ __forceinline__ void part_store(const uint4 (&r)[U], uint4* dst, int 
 }
 
 template <int W>
-__global__ __launch_bounds__(512) void step_kernel(KParams P) {
+__global__ __launch_bounds__(256) void step_kernel(KParams P) {
     static_assert(W == 64, "one wavefront per env");
     extern __shared__ __align__(16) unsigned char lds[];
     const Tile tl = P.tiles[blockIdx.x];
@@ -1503,7 +1755,7 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
     {
         // one burst: the layout image (whole block), and per env its record
         // with the MT words, its scenario image and its action row
-        constexpr int UI = 12, UR = 12, US = 4, UA = 2;
+        constexpr int UI = 16, UR = 16, US = 4, UA = 2;   // one round up to 64 KB of image, 16 KB of record
         const int nthr = (int)blockDim.x, tid = (int)threadIdx.x, l = ln();
         const int img16 = L->img.bytes >> 4;
         const int rec16 = active ? (L->st.bytes + 4 * SBK_MT_N) >> 4 : 0;
@@ -1662,10 +1914,10 @@ __global__ void gen_actions_kernel(float* actions, const int* n_cont, const int*
 }  // namespace sbk
 
 // ---------------------------------------------------------------- launchers
-// threads: 64 per env of a tile (at most 8 envs per workgroup).
+// threads: 64 per env of a tile (at most 4 envs per workgroup).
 extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int threads, int lds_bytes, hipStream_t s) {
     using namespace sbk;
-    if (threads < 64 || threads > 512 || threads % 64) return (int)hipErrorInvalidValue;
+    if (threads < 64 || threads > 256 || threads % 64) return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(step_kernel<64>, dim3(n_blocks), dim3(threads), lds_bytes, s, *p);
     return (int)hipGetLastError();
 }

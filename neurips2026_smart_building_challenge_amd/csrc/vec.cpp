@@ -83,6 +83,7 @@ struct HostLayout {
     std::string key;
     sbh::SolvePlan plan;
     sbh::RelaxPlan relax;
+    sbh::BlockPlan block;
     sbk::DevLayout dev{};   // sizes + layouts; pointers patched after upload
     std::map<std::string, size_t> off;
 };
@@ -138,18 +139,24 @@ struct ImgBuilder {
     }
 };
 
-enum { SOLVE_AUTO = 0, SOLVE_LU = 1, SOLVE_RELAX = 2 };
+enum { SOLVE_AUTO = 0, SOLVE_LU = 1, SOLVE_RELAX = 2, SOLVE_POINT = 3 };
 
 // Builds one layout's tables (everything shared by its scenarios). `solve`
-// picks the field solver: the relaxation form where it is certified (AUTO),
-// or the one named.
+// picks the field solver: AUTO takes block-Jacobi relaxation where it is
+// certified, else point Jacobi where that is, else the LU plan; RELAX the
+// same without the LU fallback; POINT and LU force those forms.
 bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena& A, std::string* err) {
     if (!sbh::build_plan(b, width, &H->plan, err)) return false;
     const sbh::SolvePlan& P = H->plan;
     sbh::build_relax(b, P, &H->relax);
+    sbh::build_block(b, P, &H->block);
     const sbh::RelaxPlan& R = H->relax;
-    if (solve == SOLVE_RELAX && !R.ok) return (*err = "relaxation solver not applicable: " + R.why), false;
-    const bool relax = solve == SOLVE_RELAX || (solve == SOLVE_AUTO && R.ok);
+    const sbh::BlockPlan& BP = H->block;
+    const bool use_block = (solve == SOLVE_AUTO || solve == SOLVE_RELAX) && BP.ok && (!R.ok || BP.rho < R.rho);
+    if (solve == SOLVE_RELAX && !BP.ok && !R.ok)
+        return (*err = "relaxation solver not applicable: " + R.why + "; " + BP.why), false;
+    if (solve == SOLVE_POINT && !R.ok) return (*err = "point relaxation not applicable: " + R.why), false;
+    const bool relax = use_block || solve == SOLVE_POINT || ((solve == SOLVE_AUTO || solve == SOLVE_RELAX) && R.ok);
     sbk::DevLayout& D = H->dev;
     uint64_t cnt = 0;
     const int n = P.n;
@@ -263,8 +270,9 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     D.n_slots = P.n_slots; D.vec_base = P.vec_base; D.n_pass = P.n_pass(); D.width = width;
     D.max_room_cells = max_cells;
     D.solver = relax ? sbk::SOLVER_RELAX : sbk::SOLVER_LU;
-    D.rx_terms = relax ? R.terms : 0;
-    D.rx_stop = relax ? R.rho / (1.0 - R.rho) : 0.0;
+    D.rx_block = use_block ? (BP.n_blocks > 64 ? 2 : 1) : 0;
+    D.rx_terms = use_block ? BP.terms : (relax ? R.terms : 0);
+    D.rx_stop = use_block ? BP.rho / (1.0 - BP.rho) : (relax ? R.rho / (1.0 - R.rho) : 0.0);
     if (relax) D.n_pass = 0;
     // state record
     sbk::StateLayout& S = D.st;
@@ -305,7 +313,12 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     Ls.bytes = align_up(l, 16);
     D.bytes_per_step = 2.0 * S.bytes + 4.0 * (ncont + ndisc) + 4.0 * SB_OBS + 8.0;
     D.solve_flops = 2.0 * (double)P.n_pairs + (double)P.n_divs;
-    if (relax) {   // per sweep: one multiply-subtract per off-diagonal entry, one scaling per row
+    if (use_block) {   // per sweep: off-block multiply-subtracts, then each block's inverse applied
+        long long nnz = 0, dense = 0;
+        for (double x : BP.val) nnz += x != 0.0;
+        for (const auto& blk : BP.blocks) dense += (long long)blk.size() * (long long)blk.size();
+        D.solve_flops = 2.0 * (double)(nnz + dense);
+    } else if (relax) {   // per sweep: one multiply-subtract per off-diagonal entry, one scaling per row
         long long nnz = 0;
         for (int i = 0; i < n; i++)
             for (int m = 0; m < sbh::kRelaxTerms; m++) nnz += R.val[(size_t)m * sbh::kRelaxRows + i] != 0.0;
@@ -453,6 +466,40 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
         G.act_src = I.add(src);
         G.air_slot = I.add(P.air_slot);
         G.air_node = I.add(P.air_node);
+        G.bx_d = G.bx_i = 0;
+        D.bx_nb = use_block ? BP.n_blocks : 0;
+        if (use_block) {
+            const int nb = BP.n_blocks, R = sbh::kBlockRows, T = sbh::kBlockTerms;
+            static_assert(sbh::kBlockRows == 3 && sbh::kBlockTerms == 8, "chunk layout of the block tables");
+            std::vector<double> bd((size_t)18 * nb, 0.0);
+            std::vector<int32_t> bi((size_t)12 * nb, 0);
+            for (int kb = 0; kb < nb; kb++) {
+                const int q = kb / 64, ln = kb % 64;
+                double rec[18] = {0.0};
+                int32_t irec[12] = {0};
+                static const int in_pairs[6][2] = {{0, 1}, {0, 2}, {1, 0}, {1, 2}, {2, 0}, {2, 1}};
+                for (int p = 0; p < R; p++) {
+                    const size_t at = (size_t)(q * R + p) * 64 + ln;
+                    rec[p] = BP.diag[at];
+                    irec[p] = (int32_t)(((uint32_t)BP.row[at] & 0xffffu) | ((uint32_t)BP.air[at] << 16));
+                }
+                for (int j = 0; j < 6; j++)
+                    rec[3 + j] = BP.in[((size_t)(q * R + in_pairs[j][0]) * R + in_pairs[j][1]) * 64 + ln];
+                for (int t = 0; t < T; t++) {
+                    const size_t e = (size_t)(q * T + t) * 64 + ln;
+                    rec[9 + t] = BP.val[e];
+                    irec[4 + t] = (int32_t)((uint32_t)BP.col[e] | ((uint32_t)BP.trow[e] << 16));
+                }
+                for (int j = 0; j < 9; j++) {
+                    bd[((size_t)j * nb + kb) * 2 + 0] = rec[2 * j];
+                    bd[((size_t)j * nb + kb) * 2 + 1] = rec[2 * j + 1];
+                }
+                for (int j = 0; j < 3; j++)
+                    for (int e = 0; e < 4; e++) bi[((size_t)j * nb + kb) * 4 + e] = irec[4 * j + e];
+            }
+            G.bx_d = I.add(bd);
+            G.bx_i = I.add(bi);
+        }
         G.is_room = I.add(is_room);
         G.act_disc = I.add(take(disc, n_act));
         // observation sources (the value each field reads; sb_obs.c:49-64 and
@@ -913,7 +960,8 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
     if (const char* sv = kws(kwargs, "solver")) {
         if (!strcmp(sv, "lu")) solve = SOLVE_LU;
         else if (!strcmp(sv, "relax")) solve = SOLVE_RELAX;
-        else if (strcmp(sv, "auto")) die(std::string("env.solver must be auto, lu or relax, not ") + sv);
+        else if (!strcmp(sv, "point")) solve = SOLVE_POINT;
+        else if (strcmp(sv, "auto")) die(std::string("env.solver must be auto, lu, relax or point, not ") + sv);
     }
     // ---- layouts + scenarios
     Arena A;
@@ -990,7 +1038,7 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
     });
     {
         const int epb_kw = (int)kw(kwargs, "envs_per_block", 4.0f);
-        if (epb_kw < 1 || epb_kw > 8) die("env.envs_per_block must be 1..8");
+        if (epb_kw < 1 || epb_kw > 4) die("env.envs_per_block must be 1..4");
         int img = 0, reg = 0;
         for (auto& L : v->layouts) {
             img = std::max(img, L.dev.img.bytes);
@@ -1435,8 +1483,8 @@ int sbx_solve_info(Env* envs, int i, double* out) {
     hip_ok(hipStreamSynchronize(g_stream), "state sync");
     hip_ok(hipMemcpy(pf, v->d_state + d.state_off + H.dev.st.plant, sizeof(pf), hipMemcpyDeviceToHost), "copy");
     const bool relax = H.dev.solver == sbk::SOLVER_RELAX;
-    out[0] = relax ? 1.0 : 0.0;
-    out[1] = relax ? H.relax.rho : 0.0;
+    out[0] = relax ? (H.dev.rx_block ? 2.0 : 1.0) : 0.0;
+    out[1] = relax ? (H.dev.rx_block ? H.block.rho : H.relax.rho) : 0.0;
     out[2] = pf[sbk::PF_SWEEPS];
     out[3] = pf[sbk::PF_CAPPED];
     return 4;
@@ -1460,6 +1508,7 @@ const char* sbx_scenario_path(Env* envs, int s) {
 struct PlanHolder {
     sbh::SolvePlan plan;
     sbh::RelaxPlan relax;
+    sbh::BlockPlan block;
 };
 static std::map<const void*, PlanHolder*> g_plans;
 
@@ -1505,6 +1554,24 @@ int sbx_plan_layout(const char* blob_path, int width, SbxPlan* out) {
         out->rx_air = R.air_col.data();
         out->rx_val = R.val.data();
         out->rx_col = R.col.data();
+    }
+    sbh::build_block(b, P, &h->block);
+    const sbh::BlockPlan& BP = h->block;
+    out->bx_ok = BP.ok ? 1 : 0;
+    out->bx_rows = sbh::kBlockRows;
+    out->bx_slots = sbh::kBlockSlots;
+    out->bx_terms_max = sbh::kBlockTerms;
+    out->bx_terms = BP.terms;
+    out->bx_blocks = BP.n_blocks;
+    out->bx_rho = BP.rho;
+    if (BP.ok) {
+        out->bx_row = BP.row.data();
+        out->bx_diag = BP.diag.data();
+        out->bx_air = BP.air.data();
+        out->bx_in = BP.in.data();
+        out->bx_val = BP.val.data();
+        out->bx_col = BP.col.data();
+        out->bx_trow = BP.trow.data();
     }
     g_plans[out->hdr] = h;
     return 0;

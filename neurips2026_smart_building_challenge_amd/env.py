@@ -71,7 +71,14 @@ class SbxPlan(ctypes.Structure):
                 ("rx_ok", ctypes.c_int), ("rx_rows", ctypes.c_int), ("rx_terms_max", ctypes.c_int),
                 ("rx_terms", ctypes.c_int), ("rx_rho", ctypes.c_double),
                 ("rx_diag", ctypes.POINTER(ctypes.c_double)), ("rx_air", ctypes.POINTER(ctypes.c_int)),
-                ("rx_val", ctypes.POINTER(ctypes.c_double)), ("rx_col", ctypes.POINTER(ctypes.c_int))]
+                ("rx_val", ctypes.POINTER(ctypes.c_double)), ("rx_col", ctypes.POINTER(ctypes.c_int)),
+                ("bx_ok", ctypes.c_int), ("bx_rows", ctypes.c_int), ("bx_slots", ctypes.c_int),
+                ("bx_terms_max", ctypes.c_int), ("bx_terms", ctypes.c_int), ("bx_blocks", ctypes.c_int),
+                ("bx_rho", ctypes.c_double),
+                ("bx_row", ctypes.POINTER(ctypes.c_int)), ("bx_diag", ctypes.POINTER(ctypes.c_double)),
+                ("bx_air", ctypes.POINTER(ctypes.c_int)), ("bx_in", ctypes.POINTER(ctypes.c_double)),
+                ("bx_val", ctypes.POINTER(ctypes.c_double)), ("bx_col", ctypes.POINTER(ctypes.c_int)),
+                ("bx_trow", ctypes.POINTER(ctypes.c_int))]
 
 
 class SbxPolicy(ctypes.Structure):
@@ -204,6 +211,18 @@ def plan_layout(blob: str | Path, width: int = 64) -> dict[str, np.ndarray]:
             out["rx_air"] = arr(p.rx_air, rows).astype(np.int64)
             out["rx_val"] = arr(p.rx_val, tm * rows).reshape(tm, rows)
             out["rx_col"] = arr(p.rx_col, tm * rows).reshape(tm, rows).astype(np.int64)
+        out.update({"bx_ok": bool(p.bx_ok), "bx_rho": p.bx_rho, "bx_terms": p.bx_terms,
+                    "bx_blocks": p.bx_blocks, "bx_rows": p.bx_rows, "bx_slots": p.bx_slots,
+                    "bx_terms_max": p.bx_terms_max})
+        if p.bx_ok:
+            Q, R_, T_ = p.bx_slots, p.bx_rows, p.bx_terms_max
+            out["bx_row"] = arr(p.bx_row, Q * R_ * 64).reshape(Q, R_, 64).astype(np.int64)
+            out["bx_diag"] = arr(p.bx_diag, Q * R_ * 64).reshape(Q, R_, 64)
+            out["bx_air"] = arr(p.bx_air, Q * R_ * 64).reshape(Q, R_, 64).astype(np.int64)
+            out["bx_in"] = arr(p.bx_in, Q * R_ * R_ * 64).reshape(Q, R_, R_, 64)
+            out["bx_val"] = arr(p.bx_val, Q * T_ * 64).reshape(Q, T_, 64)
+            out["bx_col"] = arr(p.bx_col, Q * T_ * 64).reshape(Q, T_, 64).astype(np.int64)
+            out["bx_trow"] = arr(p.bx_trow, Q * T_ * 64).reshape(Q, T_, 64).astype(np.int64)
     finally:
         L.sbx_plan_free(ctypes.byref(p))
     return out
@@ -306,11 +325,11 @@ class VecEnv:
         return buf.reshape(self.n, POLICY_HEADS)
 
     def solve_info(self, i: int) -> dict[str, float]:
-        """Field solver of env i: kind ("lu"/"relax"), rho, sweeps of the last step, capped steps."""
+        """Field solver of env i: kind ("lu"/"point"/"block"), rho, sweeps of the last step, capped steps."""
         out = np.zeros(4, np.float64)
         if self.L.sbx_solve_info(self.envs, i, out.ctypes.data_as(P)) != 4:
             raise RuntimeError("sbx_solve_info failed")
-        return {"solver": "relax" if out[0] == 1.0 else "lu", "rho": float(out[1]),
+        return {"solver": {0.0: "lu", 1.0: "point", 2.0: "block"}[float(out[0])], "rho": float(out[1]),
                 "sweeps": int(out[2]), "capped": int(out[3])}
 
     def log(self, i: int) -> dict[str, float]:

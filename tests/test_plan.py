@@ -189,3 +189,123 @@ def test_relax_rejects_weak_dominance(tmp_path):
     pl = E.plan_layout(bad, 64)
     assert not pl["rx_ok"]
     assert pl["rx_rho"] == pytest.approx(2.0 / 3.0)
+
+
+def block_parts(pl):
+    """Blocks as (block slot, lane, node list) read back from the exported tables."""
+    row = pl["bx_row"]
+    out = []
+    for q in range(row.shape[0]):
+        for lane in range(64):
+            nodes = [int(v) for v in row[q, :, lane] if v >= 0]
+            if nodes:
+                assert np.all(row[q, len(nodes):, lane] < 0)     # rows are packed at the front
+                out.append(((q, lane), nodes))
+    return out
+
+
+def block_entries(pl, q, lane):
+    """The block's off-block entry list: (row within the block, column, value)."""
+    v, c, r = pl["bx_val"][q, :, lane], pl["bx_col"][q, :, lane], pl["bx_trow"][q, :, lane]
+    return [(int(r[t]), int(c[t]), float(v[t])) for t in range(v.size) if v[t] != 0.0]
+
+
+def block_solve(pl, g, b, x0, tol=1e-13, cap=64):
+    """Block-Jacobi sweeps over the exported tables: each block's rows solved
+    exactly against the previous sweep's off-block values, stopped by the same
+    rho / (1 - rho) * max|x_m - x_m-1| <= tol * max|x0| rule as the point form."""
+    gd = np.zeros(pl["n"])
+    gd[pl["air_node"]] = g
+    parts = block_parts(pl)
+    stop = pl["bx_rho"] / (1.0 - pl["bx_rho"])
+    atol = tol * np.max(np.abs(x0))
+    x = x0.copy()
+    for it in range(1, cap + 1):
+        xn = x.copy()
+        for (q, lane), nodes in parts:
+            m = len(nodes)
+            M = pl["bx_in"][q, :m, :m, lane].copy()
+            M[np.arange(m), np.arange(m)] = pl["bx_diag"][q, :m, lane] + gd[nodes]
+            rhs = b[nodes].copy()
+            for r, c, v in block_entries(pl, q, lane):
+                rhs[r] -= v * x[c]
+            xn[nodes] = np.linalg.solve(M, rhs)
+        delta = np.max(np.abs(xn - x))
+        x = xn
+        if stop * delta <= atol:
+            return x, it, stop * delta
+    return x, cap, stop * delta
+
+
+@pytest.mark.parametrize("zones,ahus", G.LAYOUTS)
+def test_block_tables_and_bound(zones, ahus, tmp_path):
+    """The block tables partition the nodes and rebuild A exactly; rho_B is
+    max_i sum_j (|A_BB^-1| |A_BO|)_ij recomputed here from the partition, below
+    the point bound; block sweeps with the stopping rule land within their own
+    certified bound of the exact solution, in fewer sweeps than point sweeps."""
+    import scipy.sparse as sp
+
+    p, _ = golden_blob((zones, ahus), (10.0, 8.0, 499), tmp_path)
+    pl = E.plan_layout(p, 64)
+    assert pl["bx_ok"] and pl["rx_ok"]
+    d = read_sbb(p)
+    n = pl["n"]
+    A = sp.csc_matrix((d["A_system_data"], d["A_system_indices"], d["A_system_indptr"]), shape=(n, n)).toarray()
+    parts = block_parts(pl)
+    assert len(parts) == pl["bx_blocks"]
+    nodes = np.concatenate([np.array(b) for _, b in parts])
+    assert np.array_equal(np.sort(nodes), np.arange(n))
+    Rb = np.zeros((n, n))
+    rho = 0.0
+    for (q, lane), blk in parts:
+        inv = np.linalg.inv(A[np.ix_(blk, blk)])
+        assert np.all(inv >= -1e-14 * np.abs(inv).max())
+        other = np.setdiff1d(np.arange(n), blk)
+        rho = max(rho, (np.abs(inv) @ np.abs(A[np.ix_(blk, other)])).sum(1).max())
+        ents = block_entries(pl, q, lane)
+        assert len(ents) <= pl["bx_terms"] <= pl["bx_terms_max"]
+        for pp, i in enumerate(blk):
+            Rb[i, i] += pl["bx_diag"][q, pp, lane]
+            assert pl["bx_in"][q, pp, pp, lane] == 0.0
+            for p2, j in enumerate(blk):
+                if p2 != pp:
+                    Rb[i, j] += pl["bx_in"][q, pp, p2, lane]
+            a = pl["bx_air"][q, pp, lane]
+            assert a == (list(pl["air_node"]).index(i) if i in pl["air_node"] else -1)
+        for r, c, v in ents:
+            assert c not in blk
+            Rb[blk[r], c] += v
+    assert np.array_equal(Rb, A)
+    assert pl["bx_rho"] == pytest.approx(rho, rel=1e-12)
+    assert pl["bx_rho"] < pl["rx_rho"] <= 0.5
+    rng = np.random.default_rng(zones + 7)
+    for trial in range(3):
+        g = rng.uniform(0.0, 900.0, pl["k"]) if trial else np.zeros(pl["k"])
+        Ag = A.copy()
+        Ag[pl["air_node"], pl["air_node"]] += g
+        xt = rng.uniform(280.0, 310.0, n)
+        bvec = Ag @ xt
+        x0 = xt + rng.normal(size=n) * 5.0
+        x, it, bound = block_solve(pl, g, bvec, x0)
+        _, it_point, _ = relax_solve(pl, g, bvec, x0)
+        exact = np.linalg.solve(Ag, bvec)
+        err = np.max(np.abs(x - exact))
+        assert it < 64 and it <= it_point
+        assert err <= bound + 1e-12 * np.max(np.abs(exact))
+        assert err <= 1e-10 * np.max(np.abs(exact))
+
+
+def test_block_rejects_positive_coupling(tmp_path):
+    """A positive off-diagonal entry breaks the M-matrix property the block bound
+    rests on: the block form must turn off (point relaxation stays available)."""
+    p, _ = golden_blob((41, 1), (10.0, 8.0, 499), tmp_path)
+    d = read_sbb(p)
+    x = d["A_system_data"].copy()
+    Ap, Ai = d["A_system_indptr"], d["A_system_indices"]
+    q = next(q for q in range(Ap[0], Ap[1]) if Ai[q] != 0)
+    x[q] = -x[q]
+    bad = tmp_path / "pos.sbb"
+    _rewrite(p, bad, A_system_data=x)
+    pl = E.plan_layout(bad, 64)
+    assert not pl["bx_ok"]
+    assert pl["rx_ok"]
