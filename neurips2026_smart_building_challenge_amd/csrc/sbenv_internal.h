@@ -55,6 +55,10 @@ enum { PF_PUMP_HEAD = 0, PF_BOILER_SP, PF_BOILER_RET, PF_BOILER_CUR, PF_BOILER_D
        PF_REW_SUM, PF_SWEEPS, PF_CAPPED };
 
 enum { SOLVER_LU = 0, SOLVER_RELAX = 1 };
+// Step-kernel variants, one per field-solver form (each compiles only its own
+// solver, which keeps the instruction footprint of a launch small); a launch
+// covers the tiles whose layouts use that form.
+enum { KV_LU = 0, KV_POINT = 1, KV_BLOCK = 2, KV_COUNT = 3 };
 enum { PI_HWS_RUN = 0, PI_PUMP_RUN, PI_HWS_REQ, PI_STEP_INDEX, PI_STEP, PI_MT_IDX,
        PI_STEPS_TOTAL, PI_EPISODES };
 

@@ -444,16 +444,88 @@ __device__ __forceinline__ int default_mode(int cur, double zt, double hsp, doub
     return M_OFF;
 }
 
-// zone means of room cells (ascending), sb_sim.c:149-160
+// Passes of a U-slot loop: U = 1 serves counts up to 64 (one pass), U = 2
+// counts up to 64 * SBK_VPL (the callers dispatch on the count).
+template <int U>
+__device__ constexpr int upasses() { return U == 1 ? 1 : SBK_VPL / U; }
+
+// zone means of room cells (ascending), sb_sim.c:149-160. U zones per lane
+// per pass (lane + 64 u) with their cell chains interleaved.
+template <int U>
+__device__ __forceinline__ void zone_means_pass(Ctx& c, double* out) {
+    const int nz = c.L->nz, lane = ln();
+#pragma unroll
+    for (int pass = 0; pass < upasses<U>(); pass++) {
+        const int base = pass * 64 * U;
+        if (base >= nz) break;
+        int z[U], a[U], b[U];
+        bool ok[U];
+        double sum[U];
+        int len = 0;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int zz = base + 64 * u + lane;
+            ok[u] = zz < nz;
+            z[u] = ok[u] ? zz : nz - 1;
+            a[u] = c.t.zone_cell_off[z[u]];
+            b[u] = c.t.zone_cell_off[z[u] + 1];
+            sum[u] = 0.0;
+            len = max(len, b[u] - a[u]);
+        }
+        for (int i = 0; i < len; i++) {
+            double tv[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) tv[u] = c.T[c.t.zone_cells[a[u] + i < b[u] ? a[u] + i : a[u]]];
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                if (a[u] + i < b[u]) sum[u] += tv[u];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++)
+            if (ok[u]) out[z[u]] = sum[u] / (double)(b[u] - a[u]);
+    }
+}
+
 template <int W>
 __device__ __forceinline__ void zone_means(Ctx& c, double* out) {
-    const SBK_C DevLayout* L = c.L;
-    for (int z = ln(); z < L->nz; z += W) {
-        int a = c.t.zone_cell_off[z], b = c.t.zone_cell_off[z + 1];
-        double sum = 0.0;
-        for (int t = a; t < b; t++) sum += c.T[c.t.zone_cells[t]];
-        out[z] = sum / (double)(b - a);
+    if (c.L->nz > 64) zone_means_pass<2>(c, out);
+    else zone_means_pass<1>(c, out);
+}
+
+// area-weighted VAV temperatures from zone means (sb_sim.c:163-175) of the U
+// VAVs v[u], their zone chains interleaved (each VAV's zones in order)
+template <int U>
+__device__ __forceinline__ void vav_temps(const Ctx& c, const double* zmean, const int (&v)[U], double (&tv)[U],
+                                          double (&area)[U]) {
+    int a[U], b[U];
+    double wt[U];
+    int len = 0;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        a[u] = c.t.vz_off[v[u]];
+        b[u] = c.t.vz_off[v[u] + 1];
+        area[u] = 0.0;
+        wt[u] = 0.0;
+        len = max(len, b[u] - a[u]);
     }
+    for (int i = 0; i < len; i++) {
+        double za[U], zm[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int z = c.t.vz_idx[a[u] + i < b[u] ? a[u] + i : a[u]];
+            za[u] = c.t.zone_area[z];
+            zm[u] = zmean[z];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (a[u] + i < b[u]) {
+                area[u] += za[u];
+                wt[u] += zm[u] * za[u];
+            }
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) tv[u] = (area[u] > 0.0) ? wt[u] / area[u] : 0.0;
 }
 
 // area-weighted VAV temperature from zone means (sb_sim.c:163-175)
@@ -613,7 +685,7 @@ __device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday)
     const SBK_C DevLayout* L = c.L;
     const SBK_C DevScen* S = c.S;
     const int nocc = L->nz * L->nassign;
-    constexpr int MAXC = 8;   // occupants per lane (nocc <= 8 * W, checked on the host)
+    constexpr int MAXC = 5;   // occupants per lane (nocc <= 5 * W, checked on the host)
     const int per = (nocc + W - 1) / W;
     const int o0 = ln() * per;
     int need[MAXC];
@@ -752,9 +824,14 @@ template <int W>
 __device__ __forceinline__ void env_reset(Ctx& c, int start, float* obs_row) {
     const SBK_C DevScen* S = c.S;
     sim_reset<W>(c, start);
-    occupancy_advance<W>(c, S->hour_m1[start], S->work_m1[start]);
-    write_obs<W>(c, obs_row, S->amb[start], S->aux_time + (size_t)start * (c.L->n_aux - 1));
-    occupancy_advance<W>(c, S->occ_hour[start], S->occ_work[start]);
+    // two occupancy intervals around the first observation; one loop body so
+    // the (large) occupancy code is emitted once here
+#pragma nounroll
+    for (int k = 0; k < 2; k++) {
+        occupancy_advance<W>(c, k == 0 ? S->hour_m1[start] : S->occ_hour[start],
+                             k == 0 ? S->work_m1[start] : S->occ_work[start]);
+        if (k == 0) write_obs<W>(c, obs_row, S->amb[start], S->aux_time + (size_t)start * (c.L->n_aux - 1));
+    }
 }
 
 // ------------------------------------------------------------------ step
@@ -865,6 +942,252 @@ __device__ __forceinline__ void decode_apply(Ctx& c) {
     esync();
 }
 
+// VAV pass of the pre-step (sb_sim.c:368-384, :316-355, :382-387): sensed
+// temperature, thermostat mode, damper and reheat settings, unrestricted flow,
+// and the register slots r = pass * U + u (VAV lane + 64 r) the AHU sums read.
+// U VAVs per lane per pass, all loads of a pass before any store.
+template <int U>
+__device__ __forceinline__ void vav_pass(Ctx& c, int comfort, double& ffs_part, int (&vahu)[SBK_VPL],
+                                         double (&vv)[SBK_VPL][3]) {
+    const int nv = c.L->nv, lane = ln();
+    const double* rw = c.misc + MS_ROW;
+    const double hsp = rw[RW_HSP_K], csp = rw[RW_CSP_K];
+    const bool comf_km1 = rw[RW_COMF_KM1] != 0.0;
+#pragma unroll
+    for (int pass = 0; pass < upasses<U>(); pass++) {
+        const int base = pass * 64 * U;
+        if (base >= nv) break;
+        int v[U], a[U], mode[U], pv[U], dset[U], rset[U], run[U];
+        bool ok[U];
+        double tv[U], area[U], vc0[U], vc1[U], vc2[U], vc4[U], dcmd[U], rcmd[U], dmp[U], rht[U];
+        double fan[U], amin[U], varea[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int vv0 = base + 64 * u + lane;
+            ok[u] = vv0 < nv;
+            v[u] = ok[u] ? vv0 : nv - 1;
+        }
+        vav_temps<U>(c, c.zq, v, tv, area);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const double* vc = c.t.vav_c + v[u] * 9;
+            vc0[u] = vc[0];
+            vc1[u] = vc[1];
+            vc2[u] = vc[2];
+            vc4[u] = vc[4];
+            mode[u] = c.mode[v[u]];
+            pv[u] = c.prev_valid[v[u]];
+            dset[u] = c.dcmd_set[v[u]];
+            rset[u] = c.rcmd_set[v[u]];
+            dcmd[u] = c.dcmd[v[u]];
+            rcmd[u] = c.rcmd[v[u]];
+            dmp[u] = c.damper[v[u]];
+            rht[u] = c.reheat[v[u]];
+            a[u] = c.t.vav_ahu[v[u]];
+            varea[u] = c.t.vav_area[v[u]];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            run[u] = c.run[a[u]];
+            fan[u] = c.fan[a[u]];
+            amin[u] = c.t.ahu_c[a[u] * 9 + 2];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const double sensing = tv[u];
+            int md = mode[u];
+            double damper = dmp[u], reheat = rht[u];
+            const bool live = area[u] > 0.0;
+            if (live) {
+                if (comfort) md = default_mode(md, sensing, hsp, csp);
+                else if (pv[u] && comf_km1) md = M_PASSIVE;
+                else if (md == M_PASSIVE && sensing > hsp && sensing < csp) md = M_PASSIVE;
+                else md = default_mode(md, sensing, hsp, csp);
+                double d, h;
+                if (md == M_HEAT) { d = 1.0; h = 1.0; }
+                else if (md == M_COOL) { d = 1.0; h = 0.0; }
+                else { d = vc2[u]; h = 0.0; }
+                if (dset[u]) d = dcmd[u];
+                if (rset[u]) h = rcmd[u];
+                damper = d > vc2[u] ? d : vc2[u];
+                reheat = h;
+            }
+            // unrestricted flow (sb_sim.c:253-265) from the settings just made
+            const double st = run[u] != 1 ? 0.0 : (fan[u] > amin[u] ? fan[u] : amin[u]);
+            double un = damper * vc0[u] * sqrt(st / vc4[u]);
+            un = un > 0.00001 ? un : 0.00001;
+            if (ok[u]) {
+                c.sensing[v[u]] = sensing;
+                if (live) {
+                    c.heatsp[v[u]] = hsp;
+                    c.coolsp[v[u]] = csp;
+                    c.mode[v[u]] = (uint8_t)md;
+                    c.prev_valid[v[u]] = 1;
+                    c.damper[v[u]] = damper;
+                    c.reheat[v[u]] = reheat;
+                }
+                c.unres[v[u]] = un;
+                ffs_part += reheat * vc1[u];
+                const int r = pass * U + u;
+                vahu[r] = a[u];
+                vv[r][2] = un;
+                if (varea[u] > 0.0) {
+                    vv[r][0] = sensing * varea[u];
+                    vv[r][1] = varea[u];
+                }
+            }
+        }
+    }
+}
+
+// Coupled columns (sb_sim.c:410-436, :289-314): reheat energy, air-side
+// conductance and supply temperature per column, plus the wavefront's reheat
+// total and supply extremes and the register slots for the per-AHU flow sums.
+// U columns per lane per pass (lane + 64 u), all loads of a pass issued before
+// any store so the U chains overlap; out-of-range slots compute a clamped
+// column and drop their results.
+template <int U>
+__device__ __forceinline__ void coupled_columns(Ctx& c, double ffs, double tf, double iwt, double& total_rw,
+                                                double& cmin, double& cmax, int (&cahu)[SBK_VPL],
+                                                double (&cfd)[SBK_VPL][2]) {
+    const int k = c.L->k;
+    const int lane = ln();
+#pragma unroll
+    for (int pass = 0; pass < upasses<U>(); pass++) {
+        const int base = pass * 64 * U;
+        if (base >= k) break;
+        int col[U], v[U], a[U];
+        bool ok[U];
+        double area[U], vc0[U], vc1[U], vc3[U], rh[U], dmp[U], un[U], rt[U], sat[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int cc = base + 64 * u + lane;
+            ok[u] = cc < k;
+            col[u] = ok[u] ? cc : k - 1;
+            v[u] = c.t.coupled[col[u]];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const double* vc = c.t.vav_c + v[u] * 9;
+            area[u] = c.t.vav_area[v[u]];
+            a[u] = c.t.vav_ahu[v[u]];
+            vc0[u] = vc[0];
+            vc1[u] = vc[1];
+            vc3[u] = vc[3];
+            rh[u] = c.reheat[v[u]];
+            dmp[u] = c.damper[v[u]];
+            un[u] = c.unres[v[u]];
+            rt[u] = c.ratio[v[u]];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) sat[u] = c.satv[a[u]];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            double g = 0.0, ta = 0.0, rw = 0.0, fd = 0.0;
+            if (area[u] > 0.0) {
+                ta = sat[u];
+                fd = un[u] * rt[u];
+                // reheat_eff / reheat_energy (sb_sim.c:289-314)
+                double eff;
+                double air_cap = CP_AIR * RHO_AIR * fd;
+                if (air_cap <= 0.0) {
+                    eff = 0.0;
+                } else {
+                    double wflow = 0.0;
+                    if (ffs != 0.0) wflow = tf * ((rh[u] * vc1[u]) / ffs);
+                    double water_cap = CP_W * RHO_W * wflow;
+                    eff = water_cap / air_cap;
+                    if (eff > 1.0) eff = 1.0;
+                    double gap = iwt - ta;
+                    if (gap > 0.0) {
+                        double headroom = vc3[u] - ta;
+                        if (headroom <= 0.0) eff = 0.0;
+                        else {
+                            double hr = headroom / gap;
+                            if (hr < eff) eff = hr;
+                        }
+                    }
+                }
+                rw = eff * CP_AIR * RHO_AIR * fd * (iwt - ta);
+                if (dmp[u] > 0.0 && vc0[u] > 0.0) g = fd * RHO_AIR * CP_AIR;
+            }
+            if (ok[u]) {
+                c.g[col[u]] = g;
+                c.tair[col[u]] = ta;
+                c.rwen[col[u]] = rw;
+                c.fdem[col[u]] = fd;
+                total_rw += rw;
+                cmin = fmin(cmin, ta);
+                cmax = fmax(cmax, ta);
+                if (area[u] > 0.0 && fd > 0.0) {
+                    cahu[pass * U + u] = a[u];
+                    cfd[pass * U + u][0] = fd;
+                    cfd[pass * U + u][1] = 1.0;
+                }
+            }
+        }
+    }
+}
+
+// Zone heat (sb_sim.c:420-447): the reheat share of each coupled column of
+// the zone, internal and occupant gains, per room cell. U zones per lane per
+// pass with their column chains interleaved (each zone's columns in order).
+template <int U>
+__device__ __forceinline__ void zone_heat(Ctx& c, double wpc) {
+    const SBK_C DevScen* S = c.S;
+    const int nz = c.L->nz;
+    const int lane = ln();
+#pragma unroll
+    for (int pass = 0; pass < upasses<U>(); pass++) {
+        const int base = pass * 64 * U;
+        if (base >= nz) break;
+        int z[U], c0[U], c1[U], ncell[U], occ[U];
+        bool ok[U];
+        double za[U], q[U];
+        int len = 0;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int zz = base + 64 * u + lane;
+            ok[u] = zz < nz;
+            z[u] = ok[u] ? zz : nz - 1;
+            c0[u] = c.t.zone_col_off[z[u]];
+            c1[u] = c.t.zone_col_off[z[u] + 1];
+            ncell[u] = c.t.zone_cell_off[z[u] + 1] - c.t.zone_cell_off[z[u]];
+            za[u] = c.t.zone_area[z[u]];
+            occ[u] = c.occV[z[u]];
+            q[u] = 0.0;
+            len = max(len, c1[u] - c0[u]);
+        }
+        for (int i = 0; i < len; i++) {
+            int col[U], v[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                col[u] = c.t.zone_cols[c0[u] + i < c1[u] ? c0[u] + i : c0[u]];
+                v[u] = c.t.coupled[col[u]];
+            }
+            double area[U], dmp[U], vc0[U], rw[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                area[u] = c.t.vav_area[v[u]];
+                dmp[u] = c.damper[v[u]];
+                vc0[u] = c.t.vav_c[v[u] * 9];
+                rw[u] = c.rwen[col[u]];
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++)
+                if (c0[u] + i < c1[u] && area[u] > 0.0 && dmp[u] > 0.0 && vc0[u] > 0.0)
+                    q[u] += rw[u] * za[u] / area[u];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            double qq = q[u];
+            if (S->internal_w_m2 > 0.0) qq += wpc * (double)ncell[u];
+            if (S->occupant_w > 0.0) qq += (double)occ[u] * S->occupant_w;
+            if (ok[u]) c.zq[z[u]] = qq / (double)ncell[u];
+        }
+    }
+}
+
 template <int W>
 __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
     const SBK_C DevLayout* L = c.L;
@@ -876,34 +1199,6 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
     zone_means<W>(c, c.zq);
     esync();
     STAMP(13);
-    // sensing + thermostat + VAV settings (sb_sim.c:368-384, :316-355)
-    for (int v = ln(); v < nv; v += W) {
-        double area;
-        double sensing = vav_temp(c, c.zq, v, &area);
-        c.sensing[v] = sensing;
-        if (area <= 0.0) continue;
-        const double* vc = c.t.vav_c + v * 9;
-        double hsp = rw[RW_HSP_K], csp = rw[RW_CSP_K];
-        c.heatsp[v] = hsp;
-        c.coolsp[v] = csp;
-        int mode = c.mode[v];
-        if (comfort) mode = default_mode(mode, sensing, hsp, csp);
-        else if (c.prev_valid[v] && rw[RW_COMF_KM1] != 0.0) mode = M_PASSIVE;
-        else if (mode == M_PASSIVE && sensing > hsp && sensing < csp) mode = M_PASSIVE;
-        else mode = default_mode(mode, sensing, hsp, csp);
-        c.mode[v] = (uint8_t)mode;
-        c.prev_valid[v] = 1;
-        double damper, reheat;
-        if (mode == M_HEAT) { damper = 1.0; reheat = 1.0; }
-        else if (mode == M_COOL) { damper = 1.0; reheat = 0.0; }
-        else { damper = vc[2]; reheat = 0.0; }
-        if (c.dcmd_set[v]) damper = c.dcmd[v];
-        if (c.rcmd_set[v]) reheat = c.rcmd[v];
-        c.damper[v] = damper > vc[2] ? damper : vc[2];
-        c.reheat[v] = reheat;
-    }
-    esync();
-    STAMP(14);
     // AHU return-air means and supply temperatures (sb_sim.c:382-387, :253-265):
     // flow-factor sum over all VAVs, then one lane per AHU sums over its VAVs
     // in VAV order (as csim accumulates them)
@@ -913,28 +1208,19 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
         for (int t = ln(); t < L->n; t += W) s += c.T[t];
         tmean = bsum<W>(s, c.red) / (double)L->n;
     }
-    // this lane's VAVs (v = lane + 64 r), kept in registers for the AHU sums
+    // sensing, thermostat and VAV settings (sb_sim.c:368-384, :316-355), then
+    // this lane's VAVs (v = lane + 64 r) kept in registers for the AHU sums
     double ffs_part = 0.0;
     int vahu[SBK_VPL];
     double vv[SBK_VPL][3];   // sensing * area, area (zone area > 0 only), unrestricted flow
 #pragma unroll
     for (int r = 0; r < SBK_VPL; r++) {
-        const int v = ln() + 64 * r;
         vahu[r] = -1;
         vv[r][0] = vv[r][1] = vv[r][2] = 0.0;
-        if (v < nv) {
-            ffs_part += c.reheat[v] * c.t.vav_c[v * 9 + 1];
-            const double u = vav_unrestricted(c, v);
-            c.unres[v] = u;
-            const double area = c.t.vav_area[v];
-            vahu[r] = c.t.vav_ahu[v];
-            vv[r][2] = u;
-            if (area > 0.0) {
-                vv[r][0] = c.sensing[v] * area;
-                vv[r][1] = area;
-            }
-        }
     }
+    if (nv > 64) vav_pass<2>(c, comfort, ffs_part, vahu, vv);
+    else vav_pass<1>(c, comfort, ffs_part, vahu, vv);
+    STAMP(14);
     const double ffs = bsum<W>(ffs_part, c.red);
     double sums[3];
     ahu_sums<3>(vahu, vv, na, sums);
@@ -951,14 +1237,25 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
         c.ip[PI_HWS_REQ] = nv;
     }
     esync();
-    for (int v = ln(); v < nv; v += W) {
-        int a = c.t.vav_ahu[v];
-        double dm = c.demand[a];
-        if (dm > 0.0) {
-            double r = c.t.ahu_c[a * 9 + 1] / dm;
-            c.ratio[v] = r < 1.0 ? r : 1.0;
-        } else {
-            c.ratio[v] = 1.0;
+    // flow ratio per VAV from its AHU's demand, AHUs from the register slots
+    {
+        double rt[SBK_VPL];
+#pragma unroll
+        for (int r = 0; r < SBK_VPL; r++) {
+            rt[r] = 1.0;
+            if (64 * r < nv) {
+                const int a = vahu[r] >= 0 ? vahu[r] : 0;
+                const double dm = c.demand[a], mf = c.t.ahu_c[a * 9 + 1];
+                if (dm > 0.0) {
+                    const double q = mf / dm;
+                    rt[r] = q < 1.0 ? q : 1.0;
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < SBK_VPL; r++) {
+            const int v = ln() + 64 * r;
+            if (64 * r < nv && v < nv) c.ratio[v] = rt[r];
         }
     }
     esync();
@@ -975,53 +1272,8 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
         cahu[r] = -1;
         cfd[r][0] = cfd[r][1] = 0.0;
     }
-    for (int col = ln(); col < L->k; col += W) {
-        int v = c.t.coupled[col];
-        double g = 0.0, ta = 0.0, rw = 0.0, fd = 0.0;
-        if (c.t.vav_area[v] > 0.0) {
-            const double* vc = c.t.vav_c + v * 9;
-            int a = c.t.vav_ahu[v];
-            double sat = c.satv[a];
-            ta = sat;
-            fd = c.unres[v] * c.ratio[v];
-            // reheat_eff / reheat_energy (sb_sim.c:289-314)
-            double eff;
-            double air_cap = CP_AIR * RHO_AIR * fd;
-            if (air_cap <= 0.0) {
-                eff = 0.0;
-            } else {
-                double wflow = 0.0;
-                if (ffs != 0.0) wflow = tf * ((c.reheat[v] * vc[1]) / ffs);
-                double water_cap = CP_W * RHO_W * wflow;
-                eff = water_cap / air_cap;
-                if (eff > 1.0) eff = 1.0;
-                double gap = iwt - sat;
-                if (gap > 0.0) {
-                    double headroom = vc[3] - sat;
-                    if (headroom <= 0.0) eff = 0.0;
-                    else {
-                        double hr = headroom / gap;
-                        if (hr < eff) eff = hr;
-                    }
-                }
-            }
-            rw = eff * CP_AIR * RHO_AIR * fd * (iwt - sat);
-            if (c.damper[v] > 0.0 && vc[0] > 0.0) g = fd * RHO_AIR * CP_AIR;
-        }
-        c.g[col] = g;
-        c.tair[col] = ta;
-        c.rwen[col] = rw;
-        c.fdem[col] = fd;
-        total_rw += rw;
-        cmin = fmin(cmin, ta);
-        cmax = fmax(cmax, ta);
-        const int r = col >> 6;
-        if (c.t.vav_area[v] > 0.0 && fd > 0.0) {
-            cahu[r] = c.t.vav_ahu[v];
-            cfd[r][0] = fd;
-            cfd[r][1] = 1.0;
-        }
-    }
+    if (L->k > 64) coupled_columns<2>(c, ffs, tf, iwt, total_rw, cmin, cmax, cahu, cfd);
+    else coupled_columns<1>(c, ffs, tf, iwt, total_rw, cmin, cmax, cahu, cfd);
     wave_sum_min_max(total_rw, cmin, cmax);
     // AHU flow (clamped to the AHU's maximum) and cooling requests
     double fsum[2];
@@ -1044,19 +1296,8 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
     // zone heat: reheat share, internal and occupant gains (sb_sim.c:420-447)
     const double frac = comfort ? 1.0 : S->standby_frac;
     const double wpc = S->internal_w_m2 * S->cv_area * frac;
-    for (int z = ln(); z < L->nz; z += W) {
-        double q = 0.0;
-        for (int t = c.t.zone_col_off[z]; t < c.t.zone_col_off[z + 1]; t++) {
-            int col = c.t.zone_cols[t];
-            int v = c.t.coupled[col];
-            if (c.t.vav_area[v] > 0.0 && c.damper[v] > 0.0 && c.t.vav_c[v * 9] > 0.0)
-                q += c.rwen[col] * c.t.zone_area[z] / c.t.vav_area[v];
-        }
-        int ncell = c.t.zone_cell_off[z + 1] - c.t.zone_cell_off[z];
-        if (S->internal_w_m2 > 0.0) q += wpc * (double)ncell;
-        if (S->occupant_w > 0.0) q += (double)c.occV[z] * S->occupant_w;
-        c.zq[z] = q / (double)ncell;
-    }
+    if (L->nz > 64) zone_heat<2>(c, wpc);
+    else zone_heat<1>(c, wpc);
     esync();
 }
 
@@ -1493,7 +1734,7 @@ __device__ __forceinline__ void relax_block_solve(Ctx& c, double ambient, double
 // Field step: b = cap T + q + amb dirx + mc M (+ solar, + g T_air at the air
 // nodes), then (A + diag(g)) y = b by the plan (or by relaxation); mass and
 // field update.
-template <int W>
+template <int W, int KV>
 __device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
     const SBK_C DevLayout* L = c.L;
     const SBK_C DevScen* S = c.S;
@@ -1501,7 +1742,7 @@ __device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
     const double irr = c.misc[MS_ROW + RW_SOLAR_K];
     const int n = L->n;
     double* slots = c.slots;
-    if (L->solver == SOLVER_RELAX) {
+    if constexpr (KV != KV_LU) {
         // room cells carry their zone's heat (node-indexed scratch in the slot region)
         for (int z = ln(); z < L->nz; z += W) {
             double qz = c.zq[z];
@@ -1510,12 +1751,15 @@ __device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
         esync();
         STAMP(4);
         unsigned long long* pts = (P.pass_ts && c.e == P.pass_ts_env && ln() == 0) ? P.pass_ts : nullptr;
-        if (L->rx_block == 2) relax_block_solve<2>(c, ambient, irr, pts);
-        else if (L->rx_block == 1) relax_block_solve<1>(c, ambient, irr, pts);
-        else relax_solve<W>(c, ambient, irr, pts);
+        if constexpr (KV == KV_BLOCK) {
+            if (L->rx_block == 2) relax_block_solve<2>(c, ambient, irr, pts);
+            else relax_block_solve<1>(c, ambient, irr, pts);
+        } else {
+            relax_solve<W>(c, ambient, irr, pts);
+        }
         STAMP(5);
         return;
-    }
+    } else {
     const int vb = L->vec_base;
     for (int s = ln(); s < vb; s += W) slots[s] = L->slot_init[s];   // incl. 0.0 and 1.0 slots
     // room cells carry their zone's heat; every node then gets its solar gain
@@ -1547,6 +1791,7 @@ __device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
         c.T[t] = y;
     }
     esync();
+    }
 }
 
 // sb_sim_step_post (sb_sim.c:489-521), convection off.
@@ -1586,6 +1831,40 @@ __device__ __forceinline__ void step_post(Ctx& c) {
 }
 
 // 3C reward (sb_reward.c:31-155) on the post-step state and new occupancy.
+// VAV temperatures and areas of the reward's AHU terms (sb_reward.c:62-98)
+// into the register slots r = pass * U + u (VAV lane + 64 r).
+template <int U>
+__device__ __forceinline__ void reward_vavs(Ctx& c, int (&vahu)[SBK_VPL], double (&vv)[SBK_VPL][2]) {
+    const int nv = c.L->nv, lane = ln();
+#pragma unroll
+    for (int pass = 0; pass < upasses<U>(); pass++) {
+        const int base = pass * 64 * U;
+        if (base >= nv) break;
+        int v[U], a[U];
+        bool ok[U];
+        double tv[U], area[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int vv0 = base + 64 * u + lane;
+            ok[u] = vv0 < nv;
+            v[u] = ok[u] ? vv0 : nv - 1;
+            a[u] = c.t.vav_ahu[v[u]];
+        }
+        vav_temps<U>(c, c.zq, v, tv, area);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int r = pass * U + u;
+            if (ok[u]) {
+                vahu[r] = a[u];
+                if (area[u] > 0.0) {
+                    vv[r][0] = tv[u] * area[u];
+                    vv[r][1] = area[u];
+                }
+            }
+        }
+    }
+}
+
 template <int W>
 __device__ __forceinline__ double reward(Ctx& c) {
     const SBK_C DevLayout* L = c.L;
@@ -1609,19 +1888,11 @@ __device__ __forceinline__ double reward(Ctx& c) {
     double vv[SBK_VPL][2];   // temperature * area, area (zone area > 0 only)
 #pragma unroll
     for (int r = 0; r < SBK_VPL; r++) {
-        const int v = ln() + 64 * r;
         vahu[r] = -1;
         vv[r][0] = vv[r][1] = 0.0;
-        if (v < L->nv) {
-            double area;
-            const double tv = vav_temp(c, c.zq, v, &area);
-            vahu[r] = c.t.vav_ahu[v];
-            if (area > 0.0) {
-                vv[r][0] = tv * area;
-                vv[r][1] = area;
-            }
-        }
     }
+    if (L->nv > 64) reward_vavs<2>(c, vahu, vv);
+    else reward_vavs<1>(c, vahu, vv);
     double sums[2];
     ahu_sums<2>(vahu, vv, L->na, sums);
     if (ln() < L->na) {
@@ -1665,15 +1936,35 @@ __device__ __forceinline__ double reward(Ctx& c) {
     const double max_pph = S->rw[0], min_pph = S->rw[1], ref = S->rw[2];
     const double hsp = rw[RW_HSP_J], csp = rw[RW_CSP_J];
     double occ_part = 0.0, cum_part = 0.0;
-    for (int z = ln(); z < L->nz; z += W) {
-        double occ = (double)c.occV[z];
-        occ_part += occ;
-        double zt = c.zq[z];
-        double dev = zt - csp;
-        if (hsp - zt > dev) dev = hsp - zt;
-        if (dev < 0.0) dev = 0.0;
-        double sh = (dev <= ref) ? dev / ref : 1.0 + ((dev - ref) / ref) * ((dev - ref) / ref);
-        cum_part += max_pph * (1.0 - sh) * occ * dt * inv_hour;
+    {
+        // zones z = lane + 64 r: loads of every slot first, then the sums in
+        // slot order
+        double occv[SBK_VPL], ztv[SBK_VPL];
+#pragma unroll
+        for (int r = 0; r < SBK_VPL; r++) {
+            const int z = ln() + 64 * r;
+            const int zc = z < L->nz ? z : 0;
+            occv[r] = 0.0;
+            ztv[r] = 0.0;
+            if (64 * r < L->nz) {
+                occv[r] = (double)c.occV[zc];
+                ztv[r] = c.zq[zc];
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < SBK_VPL; r++) {
+            const int z = ln() + 64 * r;
+            if (64 * r < L->nz && z < L->nz) {
+                const double occ = occv[r];
+                occ_part += occ;
+                const double zt = ztv[r];
+                double dev = zt - csp;
+                if (hsp - zt > dev) dev = hsp - zt;
+                if (dev < 0.0) dev = 0.0;
+                double sh = (dev <= ref) ? dev / ref : 1.0 + ((dev - ref) / ref) * ((dev - ref) / ref);
+                cum_part += max_pph * (1.0 - sh) * occ * dt * inv_hour;
+            }
+        }
     }
     double total_occ = occ_part, cum = cum_part;
     wave_sum2(total_occ, cum);
@@ -1734,7 +2025,7 @@ __device__ __forceinline__ void part_store(const uint4 (&r)[U], uint4* dst, int 
     }
 }
 
-template <int W>
+template <int W, int KV>
 __global__ __launch_bounds__(256) void step_kernel(KParams P) {
     static_assert(W == 64, "one wavefront per env");
     extern __shared__ __align__(16) unsigned char lds[];
@@ -1810,18 +2101,11 @@ __global__ __launch_bounds__(256) void step_kernel(KParams P) {
     if (!active) return;
     STAMP(1);
     float* obs_row = P.obs + (size_t)e * 1024;
-    if (P.mode == KMODE_RESET) {
-        env_reset<W>(c, ed.start, obs_row);
-        if (ln() == 0) {
-            c.ip[PI_STEP] = 0;
-            c.ip[PI_STEPS_TOTAL] = 0;
-            c.ip[PI_EPISODES] = 0;
-            c.plant[PF_REW_SUM] = 0.0;
-        }
-        esync();
-        store16<W>(c.rec, env + L->lds.state, L->st.bytes);
-        return;
-    }
+    // the step (KMODE_STEP), then one shared reset path for puf_reset and for
+    // the auto-reset at the end of an episode
+    const bool reset_mode = P.mode == KMODE_RESET;
+    int done = 0;
+    if (!reset_mode) {
     // host-visible log fields (trainer may clear them between steps)
     Log* hlog = nullptr;
     float lg_ret = 0.f, lg_mean = 0.f;
@@ -1835,7 +2119,7 @@ __global__ __launch_bounds__(256) void step_kernel(KParams P) {
     STAMP(2);
     step_pre<W>(c, P);
     STAMP(3);
-    field_step<W>(c, P);
+    field_step<W, KV>(c, P);
     STAMP(6);
     step_post<W>(c);
     STAMP(7);
@@ -1848,7 +2132,7 @@ __global__ __launch_bounds__(256) void step_kernel(KParams P) {
     const double rew = reward<W>(c);
     STAMP(10);
     const float r = (float)rew;
-    const int done = step >= ed.max_steps;
+    done = step >= ed.max_steps;
     if (ln() == 0) {
         P.rewards[e] = r * P.reward_scale;
         P.terminals[e] = done ? 1.0f : 0.0f;
@@ -1876,7 +2160,16 @@ __global__ __launch_bounds__(256) void step_kernel(KParams P) {
         if (done) c.ip[PI_EPISODES] += 1;
     }
     esync();
-    if (done) env_reset<W>(c, ed.start, obs_row);
+    }
+    if (reset_mode || done) {
+        env_reset<W>(c, ed.start, obs_row);
+        if (reset_mode && ln() == 0) {
+            c.ip[PI_STEP] = 0;
+            c.ip[PI_STEPS_TOTAL] = 0;
+            c.ip[PI_EPISODES] = 0;
+            c.plant[PF_REW_SUM] = 0.0;
+        }
+    }
     esync();
     STAMP(11);
     store16<W>(c.rec, env + L->lds.state, L->st.bytes);
@@ -1915,17 +2208,33 @@ __global__ void gen_actions_kernel(float* actions, const int* n_cont, const int*
 
 // ---------------------------------------------------------------- launchers
 // threads: 64 per env of a tile (at most 4 envs per workgroup).
-extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int threads, int lds_bytes, hipStream_t s) {
+extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int threads, int lds_bytes, int variant,
+                               hipStream_t s) {
     using namespace sbk;
     if (threads < 64 || threads > 256 || threads % 64) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(step_kernel<64>, dim3(n_blocks), dim3(threads), lds_bytes, s, *p);
+    switch (variant) {
+    case KV_LU: hipLaunchKernelGGL((step_kernel<64, KV_LU>), dim3(n_blocks), dim3(threads), lds_bytes, s, *p); break;
+    case KV_POINT:
+        hipLaunchKernelGGL((step_kernel<64, KV_POINT>), dim3(n_blocks), dim3(threads), lds_bytes, s, *p);
+        break;
+    case KV_BLOCK:
+        hipLaunchKernelGGL((step_kernel<64, KV_BLOCK>), dim3(n_blocks), dim3(threads), lds_bytes, s, *p);
+        break;
+    default: return (int)hipErrorInvalidValue;
+    }
     return (int)hipGetLastError();
 }
 
 extern "C" int sbk_set_lds_limit(int width, int bytes) {
     using namespace sbk;
     if (width != 64) return (int)hipErrorInvalidValue;
-    return (int)hipFuncSetAttribute((const void*)step_kernel<64>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    const void* fns[KV_COUNT] = {(const void*)step_kernel<64, KV_LU>, (const void*)step_kernel<64, KV_POINT>,
+                                 (const void*)step_kernel<64, KV_BLOCK>};
+    for (const void* f : fns) {
+        const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+        if (e != hipSuccess) return (int)e;
+    }
+    return 0;
 }
 
 extern "C" int sbk_launch_gen_actions(float* actions, const int* n_cont, const int* n_disc, int n_envs,

@@ -25,7 +25,8 @@
 #include "sbenv.h"
 #include "sbenv_internal.h"
 
-extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int threads, int lds_bytes, hipStream_t s);
+extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int threads, int lds_bytes, int variant,
+                               hipStream_t s);
 extern "C" int sbk_set_lds_limit(int width, int bytes);
 extern "C" int sbk_launch_policy(const float* obs, const float* w1, const float* b1, const float* w2,
                                  const float* b2, const float* w3, const float* b3, float* h1, float* h2, float* y,
@@ -184,6 +185,7 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     if (k > 0 && !coupled) return (*err = "coupled_vav_idx missing"), false;
     if (k > nv) return (*err = "more coupled columns than VAVs"), false;
     if (nv > 64 * SBK_VPL) return (*err = "more than 256 VAVs per building"), false;
+    if (nz > 64 * SBK_VPL) return (*err = "more than 256 zones per building"), false;
     for (int c = 0; c < k; c++)
         if (coupled[c] < 0 || coupled[c] >= nv) return (*err = "coupled_vav_idx out of range"), false;
     for (int v = 0; v < nv; v++)
@@ -261,7 +263,7 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     const double* op = b.f64("occ_params");
     if (!op) return (*err = "occ_params missing"), false;
     const int nassign = (int)op[0];
-    if (nassign < 0 || nz * nassign > 312 || nz * nassign > 8 * width)
+    if (nassign < 0 || nz * nassign > 312 || nz * nassign > 5 * width)
         return (*err = "too many occupants per env"), false;
     if (b.f64_1("conv_p", 0.0) != 0.0) return (*err = "stochastic convection (conv_p > 0) is not supported"), false;
 
@@ -777,11 +779,21 @@ void patch_scen(HostScen* H, unsigned char* d) {
 }
 
 // ---------------------------------------------------------------- vec
+struct TileGroup {
+    int variant, first, count;
+};
+
+int kernel_variant(const sbk::DevLayout& d) {
+    if (d.solver == sbk::SOLVER_LU) return sbk::KV_LU;
+    return d.rx_block ? sbk::KV_BLOCK : sbk::KV_POINT;
+}
+
 struct Vec {
     int n = 0, width = 64, lds_bytes = 0;
     int epb = 4;                              // envs (wavefronts) per workgroup
     int img_lds = 0;                          // LDS bytes of the largest layout image
     std::vector<sbk::Tile> tiles;
+    std::vector<TileGroup> groups;            // consecutive tiles of one kernel variant
     sbk::Tile* d_tiles = nullptr;
     float reward_scale = 1.0f;
     Env* envs = nullptr;
@@ -838,9 +850,14 @@ sbk::KParams params(Vec* v, int mode) {
     return p;
 }
 
+// One launch per kernel variant present (tiles are grouped by variant).
 void launch_params(Vec* v, const sbk::KParams& p) {
-    int rc = sbk_launch_step(&p, (int)v->tiles.size(), v->width * v->epb, v->lds_bytes, g_stream);
-    if (rc != 0) die(std::string("step kernel launch failed: ") + hipGetErrorString((hipError_t)rc));
+    for (const TileGroup& g : v->groups) {
+        sbk::KParams q = p;
+        q.tiles = v->d_tiles + g.first;
+        int rc = sbk_launch_step(&q, g.count, v->width * v->epb, v->lds_bytes, g.variant, g_stream);
+        if (rc != 0) die(std::string("step kernel launch failed: ") + hipGetErrorString((hipError_t)rc));
+    }
 }
 
 void launch(Vec* v, int mode) { launch_params(v, params(v, mode)); }
@@ -1031,6 +1048,8 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
     for (int i = 0; i < n; i++) v->order[i] = i;
     std::stable_sort(v->order.begin(), v->order.end(), [&](int a, int b) {
         const sbk::EnvDesc &da = v->desc[a], &db = v->desc[b];
+        const int ka = kernel_variant(v->layouts[da.layout].dev), kb = kernel_variant(v->layouts[db.layout].dev);
+        if (ka != kb) return ka > kb;
         const int na_ = v->layouts[da.layout].dev.n, nb_ = v->layouts[db.layout].dev.n;
         if (na_ != nb_) return na_ > nb_;
         if (da.layout != db.layout) return da.layout < db.layout;
@@ -1056,6 +1075,10 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
             int j = i;
             while (j < n && j - i < epb && v->desc[v->order[j]].layout == lay) j++;
             v->tiles.push_back(sbk::Tile{lay, i, j - i, 0});
+            const int kv = kernel_variant(v->layouts[lay].dev);
+            if (v->groups.empty() || v->groups.back().variant != kv)
+                v->groups.push_back(TileGroup{kv, (int)v->tiles.size() - 1, 0});
+            v->groups.back().count++;
             i = j;
         }
     }
