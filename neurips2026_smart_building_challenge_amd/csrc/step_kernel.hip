@@ -2041,11 +2041,11 @@ __global__ __launch_bounds__(256) void step_kernel(KParams P) {
     c.e = e;
     c.rec = P.state + ed.state_off;
     unsigned char* env = lds + P.img_lds + slot * L->lds.bytes;
-    bind(c, lds, env);
     STAMP(0);
     {
         // one burst: the layout image (whole block), and per env its record
-        // with the MT words, its scenario image and its action row
+        // with the MT words, its scenario image and its action row; the LDS
+        // pointers are bound while the first round's loads are in flight
         constexpr int UI = 16, UR = 16, US = 4, UA = 2;   // one round up to 64 KB of image, 16 KB of record
         const int nthr = (int)blockDim.x, tid = (int)threadIdx.x, l = ln();
         const int img16 = L->img.bytes >> 4;
@@ -2071,13 +2071,14 @@ __global__ __launch_bounds__(256) void step_kernel(KParams P) {
             kk = ipg[PI_STEP_INDEX];
             j1 = ed.start + ipg[PI_STEP] + 1;
         }
-        for (int rd = 0; rd < rounds; rd++) {
+        {
             uint4 pi[UI], pr[UR], ps[US], pa[UA];
-            part_load(pi, isrc, img16, tid, nthr, rd * UI * nthr);
-            part_load(pr, rsrc, rec16, l, 64, rd * UR * 64);
-            part_load(ps, ssrc, scn16, l, 64, rd * US * 64);
-            part_load(pa, asrc, act16, l, 64, rd * UA * 64);
-            if (rd == 0 && stepping) {
+            part_load(pi, isrc, img16, tid, nthr, 0);
+            part_load(pr, rsrc, rec16, l, 64, 0);
+            part_load(ps, ssrc, scn16, l, 64, 0);
+            part_load(pa, asrc, act16, l, 64, 0);
+            bind(c, lds, env);
+            if (stepping) {
                 const RowVals rv = row_issue<W>(c, __builtin_amdgcn_readfirstlane(kk),
                                                 __builtin_amdgcn_readfirstlane(j1));
                 part_store(pi, idst, img16, tid, nthr, 0);
@@ -2085,8 +2086,19 @@ __global__ __launch_bounds__(256) void step_kernel(KParams P) {
                 part_store(ps, sdst, scn16, l, 64, 0);
                 part_store(pa, adst, act16, l, 64, 0);
                 row_store<W>(c, rv);
-                continue;
+            } else {
+                part_store(pi, idst, img16, tid, nthr, 0);
+                part_store(pr, rdst, rec16, l, 64, 0);
+                part_store(ps, sdst, scn16, l, 64, 0);
+                part_store(pa, adst, act16, l, 64, 0);
             }
+        }
+        for (int rd = 1; rd < rounds; rd++) {
+            uint4 pi[UI], pr[UR], ps[US], pa[UA];
+            part_load(pi, isrc, img16, tid, nthr, rd * UI * nthr);
+            part_load(pr, rsrc, rec16, l, 64, rd * UR * 64);
+            part_load(ps, ssrc, scn16, l, 64, rd * US * 64);
+            part_load(pa, asrc, act16, l, 64, rd * UA * 64);
             part_store(pi, idst, img16, tid, nthr, rd * UI * nthr);
             part_store(pr, rdst, rec16, l, 64, rd * UR * 64);
             part_store(ps, sdst, scn16, l, 64, rd * US * 64);
