@@ -260,13 +260,26 @@ struct EnvDesc {
     long long state_off;         // byte offset of the env's record
     int start;                   // calendar start offset
     int max_steps;
+    // staging burst inputs, copied from the scenario so the burst can be
+    // issued from this record alone
+    int scn16;                   // scenario image size in 16-byte units
+    int pad;
+    const SBK_C unsigned char* scen_src;   // scenario image in HBM
 };
 
 enum { KMODE_STEP = 0, KMODE_RESET = 1 };
 
-// A workgroup's envs: order[first .. first + count) all of one layout.
+// A workgroup's envs: order[first .. first + count) all of one layout, with
+// the layout's staging burst inputs (copied from its DevLayout so the burst
+// can be issued from the tile and env records alone).
 struct Tile {
-    int layout, first, count, pad;
+    int layout, first, count, lds_bytes;   // lds_bytes: one env's LDS region
+    int img16, rec16;                      // layout image, record + MT words, in 16-byte units
+    int lds_state, lds_scen, lds_act;      // LDS offsets within the env region
+    int st_iplant;                         // byte offset of the i32 plant counters in the record
+    int pad0, pad1;
+    const SBK_C unsigned char* img_src;    // layout image in HBM
+    long long pad2;
 };
 
 struct KParams {

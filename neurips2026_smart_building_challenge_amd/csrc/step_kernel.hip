@@ -2040,7 +2040,7 @@ __global__ __launch_bounds__(256) void step_kernel(KParams P) {
     c.S = P.scens + ed.scen;
     c.e = e;
     c.rec = P.state + ed.state_off;
-    unsigned char* env = lds + P.img_lds + slot * L->lds.bytes;
+    unsigned char* env = lds + P.img_lds + slot * tl.lds_bytes;
     STAMP(0);
     {
         // one burst: the layout image (whole block), and per env its record
@@ -2048,18 +2048,18 @@ __global__ __launch_bounds__(256) void step_kernel(KParams P) {
         // pointers are bound while the first round's loads are in flight
         constexpr int UI = 16, UR = 16, US = 4, UA = 2;   // one round up to 64 KB of image, 16 KB of record
         const int nthr = (int)blockDim.x, tid = (int)threadIdx.x, l = ln();
-        const int img16 = L->img.bytes >> 4;
-        const int rec16 = active ? (L->st.bytes + 4 * SBK_MT_N) >> 4 : 0;
-        const int scn16 = active ? c.S->img.bytes >> 4 : 0;
+        const int img16 = tl.img16;
+        const int rec16 = active ? tl.rec16 : 0;
+        const int scn16 = active ? ed.scn16 : 0;
         const int act16 = (active && P.mode == KMODE_STEP) ? (4 * SB_ACT) >> 4 : 0;
-        const SBK_C uint4* isrc = reinterpret_cast<const SBK_C uint4*>(L->img_src);
-        const SBK_C uint4* ssrc = reinterpret_cast<const SBK_C uint4*>(c.S->img_src);
+        const SBK_C uint4* isrc = reinterpret_cast<const SBK_C uint4*>(tl.img_src);
+        const SBK_C uint4* ssrc = reinterpret_cast<const SBK_C uint4*>(ed.scen_src);
         const uint4* rsrc = reinterpret_cast<const uint4*>(c.rec);
         const uint4* asrc = reinterpret_cast<const uint4*>(P.actions + (size_t)e * SB_ACT);
         uint4* idst = reinterpret_cast<uint4*>(lds);
-        uint4* rdst = reinterpret_cast<uint4*>(env + L->lds.state);
-        uint4* sdst = reinterpret_cast<uint4*>(env + L->lds.scen);
-        uint4* adst = reinterpret_cast<uint4*>(env + L->lds.act);
+        uint4* rdst = reinterpret_cast<uint4*>(env + tl.lds_state);
+        uint4* sdst = reinterpret_cast<uint4*>(env + tl.lds_scen);
+        uint4* adst = reinterpret_cast<uint4*>(env + tl.lds_act);
         const int rounds = max(max((img16 + UI * nthr - 1) / (UI * nthr), (rec16 + UR * 64 - 1) / (UR * 64)),
                                max((scn16 + US * 64 - 1) / (US * 64), (act16 + UA * 64 - 1) / (UA * 64)));
         // the step's calendar position, read from the record in HBM so the
@@ -2067,7 +2067,7 @@ __global__ __launch_bounds__(256) void step_kernel(KParams P) {
         const bool stepping = active && P.mode == KMODE_STEP;
         int kk = 0, j1 = 0;
         if (stepping) {
-            const int* ipg = reinterpret_cast<const int*>(c.rec + L->st.iplant);
+            const int* ipg = reinterpret_cast<const int*>(c.rec + tl.st_iplant);
             kk = ipg[PI_STEP_INDEX];
             j1 = ed.start + ipg[PI_STEP] + 1;
         }

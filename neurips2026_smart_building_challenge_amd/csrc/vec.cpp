@@ -1095,6 +1095,23 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
         patch_scen(&S, v->d_arena);
         ds.push_back(S.dev);
     }
+    // burst inputs of the tiles and env records (device pointers now known)
+    for (auto& t : v->tiles) {
+        const sbk::DevLayout& D = v->layouts[t.layout].dev;
+        t.lds_bytes = D.lds.bytes;
+        t.img16 = D.img.bytes >> 4;
+        t.rec16 = (D.st.bytes + 4 * SBK_MT_N) >> 4;
+        t.lds_state = D.lds.state;
+        t.lds_scen = D.lds.scen;
+        t.lds_act = D.lds.act;
+        t.st_iplant = D.st.iplant;
+        t.img_src = D.img_src;
+    }
+    for (auto& d : v->desc) {
+        const sbk::DevScen& S = v->scens[d.scen].dev;
+        d.scn16 = S.img.bytes >> 4;
+        d.scen_src = S.img_src;
+    }
     if (v->lds_bytes > 64 * 1024) hip_ok((hipError_t)sbk_set_lds_limit(v->width, v->lds_bytes), "LDS limit");
     hip_ok(hipMalloc(&v->d_layouts, sizeof(sbk::DevLayout) * dl.size()), "hipMalloc(layouts)");
     hip_ok(hipMemcpy(v->d_layouts, dl.data(), sizeof(sbk::DevLayout) * dl.size(), hipMemcpyHostToDevice), "upload");
