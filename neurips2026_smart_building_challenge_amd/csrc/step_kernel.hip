@@ -280,15 +280,55 @@ __device__ __forceinline__ int bscan(int v, int*, int* total) {
     return inc - v;
 }
 
-// Layout tables in the staged LDS image (shared by the envs of a workgroup).
+// Layout tables in the staged LDS image (shared by the envs of a workgroup):
+// each accessor adds the table's offset (constant memory, kept in the scalar
+// cache) to the image base, so no table pointer has to stay live in registers.
 struct Tab {
-    const double *cap, *mcoup, *mret, *mgain, *solar_c, *rx_diag, *zone_area, *vav_area, *vav_c, *ahu_c;
-    const double *act_mn, *act_mx, *act_mnr, *act_mxr, *act_hi, *f_mean, *f_sd;
-    const int *rx_air, *pos, *zone_cell_off, *zone_cells, *vz_off, *vz_idx, *vav_ahu, *coupled;
-    const int *zone_col_off, *zone_cols, *act_src, *air_slot, *air_node;
-    const int *ahu_vav_off, *ahu_vavs, *ahu_col_off, *ahu_cols;
-    const uint32_t *f_src, *act_dst, *act_aux;
-    const uint8_t *is_room, *act_disc, *act_flags;
+    const unsigned char* img;
+    const SBK_C ImgLayout* g;
+#define SBK_TAB(T, name) \
+    __device__ __forceinline__ const T* name() const { return reinterpret_cast<const T*>(img + g->name); }
+    SBK_TAB(double, cap)
+    SBK_TAB(double, mcoup)
+    SBK_TAB(double, mret)
+    SBK_TAB(double, mgain)
+    SBK_TAB(double, solar_c)
+    SBK_TAB(double, rx_diag)
+    SBK_TAB(double, zone_area)
+    SBK_TAB(double, vav_area)
+    SBK_TAB(double, vav_c)
+    SBK_TAB(double, ahu_c)
+    SBK_TAB(double, act_mn)
+    SBK_TAB(double, act_mx)
+    SBK_TAB(double, act_mnr)
+    SBK_TAB(double, act_mxr)
+    SBK_TAB(double, act_hi)
+    SBK_TAB(double, f_mean)
+    SBK_TAB(double, f_sd)
+    SBK_TAB(int, rx_air)
+    SBK_TAB(int, pos)
+    SBK_TAB(int, zone_cell_off)
+    SBK_TAB(int, zone_cells)
+    SBK_TAB(int, vz_off)
+    SBK_TAB(int, vz_idx)
+    SBK_TAB(int, vav_ahu)
+    SBK_TAB(int, coupled)
+    SBK_TAB(int, zone_col_off)
+    SBK_TAB(int, zone_cols)
+    SBK_TAB(int, act_src)
+    SBK_TAB(int, air_slot)
+    SBK_TAB(int, air_node)
+    SBK_TAB(int, ahu_vav_off)
+    SBK_TAB(int, ahu_vavs)
+    SBK_TAB(int, ahu_col_off)
+    SBK_TAB(int, ahu_cols)
+    SBK_TAB(uint32_t, f_src)
+    SBK_TAB(uint32_t, act_dst)
+    SBK_TAB(uint32_t, act_aux)
+    SBK_TAB(uint8_t, is_room)
+    SBK_TAB(uint8_t, act_disc)
+    SBK_TAB(uint8_t, act_flags)
+#undef SBK_TAB
 };
 
 struct Ctx {
@@ -316,48 +356,8 @@ struct Ctx {
 // img: the workgroup's layout image; env: this env's LDS region.
 __device__ __forceinline__ void bind(Ctx& c, const unsigned char* img, unsigned char* env) {
     const SBK_C DevLayout* L = c.L;
-    const ImgLayout g = L->img;
-    Tab& t = c.t;
-    t.cap = (const double*)(img + g.cap);
-    t.mcoup = (const double*)(img + g.mcoup);
-    t.mret = (const double*)(img + g.mret);
-    t.mgain = (const double*)(img + g.mgain);
-    t.solar_c = (const double*)(img + g.solar_c);
-    t.rx_diag = (const double*)(img + g.rx_diag);
-    t.zone_area = (const double*)(img + g.zone_area);
-    t.vav_area = (const double*)(img + g.vav_area);
-    t.vav_c = (const double*)(img + g.vav_c);
-    t.ahu_c = (const double*)(img + g.ahu_c);
-    t.act_mn = (const double*)(img + g.act_mn);
-    t.act_mx = (const double*)(img + g.act_mx);
-    t.act_mnr = (const double*)(img + g.act_mnr);
-    t.act_mxr = (const double*)(img + g.act_mxr);
-    t.act_hi = (const double*)(img + g.act_hi);
-    t.act_dst = (const uint32_t*)(img + g.act_dst);
-    t.act_aux = (const uint32_t*)(img + g.act_aux);
-    t.act_flags = img + g.act_flags;
-    t.f_mean = (const double*)(img + g.f_mean);
-    t.f_sd = (const double*)(img + g.f_sd);
-    t.rx_air = (const int*)(img + g.rx_air);
-    t.pos = (const int*)(img + g.pos);
-    t.zone_cell_off = (const int*)(img + g.zone_cell_off);
-    t.zone_cells = (const int*)(img + g.zone_cells);
-    t.vz_off = (const int*)(img + g.vz_off);
-    t.vz_idx = (const int*)(img + g.vz_idx);
-    t.vav_ahu = (const int*)(img + g.vav_ahu);
-    t.coupled = (const int*)(img + g.coupled);
-    t.zone_col_off = (const int*)(img + g.zone_col_off);
-    t.zone_cols = (const int*)(img + g.zone_cols);
-    t.ahu_vav_off = (const int*)(img + g.ahu_vav_off);
-    t.ahu_vavs = (const int*)(img + g.ahu_vavs);
-    t.ahu_col_off = (const int*)(img + g.ahu_col_off);
-    t.ahu_cols = (const int*)(img + g.ahu_cols);
-    t.act_src = (const int*)(img + g.act_src);
-    t.air_slot = (const int*)(img + g.air_slot);
-    t.air_node = (const int*)(img + g.air_node);
-    t.is_room = img + g.is_room;
-    t.act_disc = img + g.act_disc;
-    t.f_src = (const uint32_t*)(img + g.f_src);
+    c.t.img = img;
+    c.t.g = &L->img;
     c.imgb = img;
     c.envb = env;
     c.obsx = (double*)(env + L->lds.obsx);
@@ -419,13 +419,13 @@ __device__ __forceinline__ void bind(Ctx& c, const unsigned char* img, unsigned 
 // ------------------------------------------------------------------ helpers
 __device__ __forceinline__ double ahu_static(const Ctx& c, int a) {
     if (c.run[a] != 1) return 0.0;
-    double sp = c.fan[a], mn = c.t.ahu_c[a * 9 + 2];
+    double sp = c.fan[a], mn = c.t.ahu_c()[a * 9 + 2];
     return sp > mn ? sp : mn;
 }
 
 __device__ __forceinline__ double vav_unrestricted(const Ctx& c, int v) {
-    const double* vc = c.t.vav_c + v * 9;
-    double d = c.damper[v] * vc[0] * sqrt(ahu_static(c, c.t.vav_ahu[v]) / vc[4]);
+    const double* vc = c.t.vav_c() + v * 9;
+    double d = c.damper[v] * vc[0] * sqrt(ahu_static(c, c.t.vav_ahu()[v]) / vc[4]);
     return d > 0.00001 ? d : 0.00001;
 }
 
@@ -467,15 +467,15 @@ __device__ __forceinline__ void zone_means_pass(Ctx& c, double* out) {
             const int zz = base + 64 * u + lane;
             ok[u] = zz < nz;
             z[u] = ok[u] ? zz : nz - 1;
-            a[u] = c.t.zone_cell_off[z[u]];
-            b[u] = c.t.zone_cell_off[z[u] + 1];
+            a[u] = c.t.zone_cell_off()[z[u]];
+            b[u] = c.t.zone_cell_off()[z[u] + 1];
             sum[u] = 0.0;
             len = max(len, b[u] - a[u]);
         }
         for (int i = 0; i < len; i++) {
             double tv[U];
 #pragma unroll
-            for (int u = 0; u < U; u++) tv[u] = c.T[c.t.zone_cells[a[u] + i < b[u] ? a[u] + i : a[u]]];
+            for (int u = 0; u < U; u++) tv[u] = c.T[c.t.zone_cells()[a[u] + i < b[u] ? a[u] + i : a[u]]];
 #pragma unroll
             for (int u = 0; u < U; u++)
                 if (a[u] + i < b[u]) sum[u] += tv[u];
@@ -502,8 +502,8 @@ __device__ __forceinline__ void vav_temps(const Ctx& c, const double* zmean, con
     int len = 0;
 #pragma unroll
     for (int u = 0; u < U; u++) {
-        a[u] = c.t.vz_off[v[u]];
-        b[u] = c.t.vz_off[v[u] + 1];
+        a[u] = c.t.vz_off()[v[u]];
+        b[u] = c.t.vz_off()[v[u] + 1];
         area[u] = 0.0;
         wt[u] = 0.0;
         len = max(len, b[u] - a[u]);
@@ -512,8 +512,8 @@ __device__ __forceinline__ void vav_temps(const Ctx& c, const double* zmean, con
         double za[U], zm[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int z = c.t.vz_idx[a[u] + i < b[u] ? a[u] + i : a[u]];
-            za[u] = c.t.zone_area[z];
+            const int z = c.t.vz_idx()[a[u] + i < b[u] ? a[u] + i : a[u]];
+            za[u] = c.t.zone_area()[z];
             zm[u] = zmean[z];
         }
 #pragma unroll
@@ -532,10 +532,10 @@ __device__ __forceinline__ void vav_temps(const Ctx& c, const double* zmean, con
 __device__ __forceinline__ double vav_temp(const Ctx& c, const double* zmean, int v, double* area_out) {
     const SBK_C DevLayout* L = c.L;
     double area = 0.0, wt = 0.0;
-    for (int t = c.t.vz_off[v]; t < c.t.vz_off[v + 1]; t++) {
-        int z = c.t.vz_idx[t];
-        area += c.t.zone_area[z];
-        wt += zmean[z] * c.t.zone_area[z];
+    for (int t = c.t.vz_off()[v]; t < c.t.vz_off()[v + 1]; t++) {
+        int z = c.t.vz_idx()[t];
+        area += c.t.zone_area()[z];
+        wt += zmean[z] * c.t.zone_area()[z];
     }
     *area_out = area;
     return (area > 0.0) ? wt / area : 0.0;
@@ -555,7 +555,7 @@ __device__ __forceinline__ void obs_specials(Ctx& c, double amb) {
         double* ax = ox + OX_AHU + 4 * a;
         ax[0] = ahu_static(c, a);
         ax[1] = (c.run[a] == 1) ? c.flow[a] : 0.0;
-        ax[2] = c.flow[a] / c.t.ahu_c[a * 9 + 1];
+        ax[2] = c.flow[a] / c.t.ahu_c()[a * 9 + 1];
         ax[3] = (1.0 - c.recirc[a]) * c.flow[a];
     }
     if (l == 0) {
@@ -583,9 +583,9 @@ __device__ __forceinline__ void write_obs(Ctx& c, float* row, double amb, const 
         for (int u = 0; u < U; u++) {
             const int i = i0 + u * W + ln();
             const int ic = i < nd ? i : nd - 1;
-            src[u] = c.t.f_src[ic];
-            mean[u] = c.t.f_mean[ic];
-            sd[u] = c.t.f_sd[ic];
+            src[u] = c.t.f_src()[ic];
+            mean[u] = c.t.f_mean()[ic];
+            sd[u] = c.t.f_sd()[ic];
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
@@ -772,7 +772,7 @@ __device__ __forceinline__ void sim_reset(Ctx& c, int start) {
     const SBK_C DevLayout* L = c.L;
     const SBK_C DevScen* S = c.S;
     for (int a = ln(); a < L->na; a += W) {
-        const double* ac = c.t.ahu_c + a * 9;
+        const double* ac = c.t.ahu_c() + a * 9;
         c.run[a] = (int)ac[8];
         c.recirc[a] = ac[0];
         c.sat[a] = ac[6];
@@ -781,7 +781,7 @@ __device__ __forceinline__ void sim_reset(Ctx& c, int start) {
         c.coolreq[a] = 0;
     }
     for (int v = ln(); v < L->nv; v += W) {
-        const double* vc = c.t.vav_c + v * 9;
+        const double* vc = c.t.vav_c() + v * 9;
         c.damper[v] = vc[7];
         c.reheat[v] = vc[8];
         c.ratio[v] = 1.0;
@@ -899,16 +899,16 @@ __device__ __forceinline__ void decode_apply(Ctx& c) {
         for (int u = 0; u < U; u++) {
             const int i = i0 + u * W + ln();
             const int ic = i < n ? i : n - 1;
-            src[u] = t.act_src[ic];
-            dst[u] = t.act_dst[ic];
-            aux[u] = t.act_aux[ic];
-            disc[u] = t.act_disc[ic];
-            fl[u] = t.act_flags[ic];
-            mn[u] = t.act_mn[ic];
-            mx[u] = t.act_mx[ic];
-            mnr[u] = t.act_mnr[ic];
-            mxr[u] = t.act_mxr[ic];
-            hi[u] = t.act_hi[ic];
+            src[u] = t.act_src()[ic];
+            dst[u] = t.act_dst()[ic];
+            aux[u] = t.act_aux()[ic];
+            disc[u] = t.act_disc()[ic];
+            fl[u] = t.act_flags()[ic];
+            mn[u] = t.act_mn()[ic];
+            mx[u] = t.act_mx()[ic];
+            mnr[u] = t.act_mnr()[ic];
+            mxr[u] = t.act_mxr()[ic];
+            hi[u] = t.act_hi()[ic];
         }
         float a[U];
 #pragma unroll
@@ -970,7 +970,7 @@ __device__ __forceinline__ void vav_pass(Ctx& c, int comfort, double& ffs_part, 
         vav_temps<U>(c, c.zq, v, tv, area);
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const double* vc = c.t.vav_c + v[u] * 9;
+            const double* vc = c.t.vav_c() + v[u] * 9;
             vc0[u] = vc[0];
             vc1[u] = vc[1];
             vc2[u] = vc[2];
@@ -983,14 +983,14 @@ __device__ __forceinline__ void vav_pass(Ctx& c, int comfort, double& ffs_part, 
             rcmd[u] = c.rcmd[v[u]];
             dmp[u] = c.damper[v[u]];
             rht[u] = c.reheat[v[u]];
-            a[u] = c.t.vav_ahu[v[u]];
-            varea[u] = c.t.vav_area[v[u]];
+            a[u] = c.t.vav_ahu()[v[u]];
+            varea[u] = c.t.vav_area()[v[u]];
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
             run[u] = c.run[a[u]];
             fan[u] = c.fan[a[u]];
-            amin[u] = c.t.ahu_c[a[u] * 9 + 2];
+            amin[u] = c.t.ahu_c()[a[u] * 9 + 2];
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
@@ -1064,13 +1064,13 @@ __device__ __forceinline__ void coupled_columns(Ctx& c, double ffs, double tf, d
             const int cc = base + 64 * u + lane;
             ok[u] = cc < k;
             col[u] = ok[u] ? cc : k - 1;
-            v[u] = c.t.coupled[col[u]];
+            v[u] = c.t.coupled()[col[u]];
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const double* vc = c.t.vav_c + v[u] * 9;
-            area[u] = c.t.vav_area[v[u]];
-            a[u] = c.t.vav_ahu[v[u]];
+            const double* vc = c.t.vav_c() + v[u] * 9;
+            area[u] = c.t.vav_area()[v[u]];
+            a[u] = c.t.vav_ahu()[v[u]];
             vc0[u] = vc[0];
             vc1[u] = vc[1];
             vc3[u] = vc[3];
@@ -1150,10 +1150,10 @@ __device__ __forceinline__ void zone_heat(Ctx& c, double wpc) {
             const int zz = base + 64 * u + lane;
             ok[u] = zz < nz;
             z[u] = ok[u] ? zz : nz - 1;
-            c0[u] = c.t.zone_col_off[z[u]];
-            c1[u] = c.t.zone_col_off[z[u] + 1];
-            ncell[u] = c.t.zone_cell_off[z[u] + 1] - c.t.zone_cell_off[z[u]];
-            za[u] = c.t.zone_area[z[u]];
+            c0[u] = c.t.zone_col_off()[z[u]];
+            c1[u] = c.t.zone_col_off()[z[u] + 1];
+            ncell[u] = c.t.zone_cell_off()[z[u] + 1] - c.t.zone_cell_off()[z[u]];
+            za[u] = c.t.zone_area()[z[u]];
             occ[u] = c.occV[z[u]];
             q[u] = 0.0;
             len = max(len, c1[u] - c0[u]);
@@ -1162,15 +1162,15 @@ __device__ __forceinline__ void zone_heat(Ctx& c, double wpc) {
             int col[U], v[U];
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                col[u] = c.t.zone_cols[c0[u] + i < c1[u] ? c0[u] + i : c0[u]];
-                v[u] = c.t.coupled[col[u]];
+                col[u] = c.t.zone_cols()[c0[u] + i < c1[u] ? c0[u] + i : c0[u]];
+                v[u] = c.t.coupled()[col[u]];
             }
             double area[U], dmp[U], vc0[U], rw[U];
 #pragma unroll
             for (int u = 0; u < U; u++) {
-                area[u] = c.t.vav_area[v[u]];
+                area[u] = c.t.vav_area()[v[u]];
                 dmp[u] = c.damper[v[u]];
-                vc0[u] = c.t.vav_c[v[u] * 9];
+                vc0[u] = c.t.vav_c()[v[u] * 9];
                 rw[u] = c.rwen[col[u]];
             }
 #pragma unroll
@@ -1245,7 +1245,7 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
             rt[r] = 1.0;
             if (64 * r < nv) {
                 const int a = vahu[r] >= 0 ? vahu[r] : 0;
-                const double dm = c.demand[a], mf = c.t.ahu_c[a * 9 + 1];
+                const double dm = c.demand[a], mf = c.t.ahu_c()[a * 9 + 1];
                 if (dm > 0.0) {
                     const double q = mf / dm;
                     rt[r] = q < 1.0 ? q : 1.0;
@@ -1281,7 +1281,7 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
     if (ln() < na) {
         const int a = ln();
         const double f = fsum[0], cnt = fsum[1];
-        const double mf = c.t.ahu_c[a * 9 + 1];
+        const double mf = c.t.ahu_c()[a * 9 + 1];
         c.flow[a] = f > mf ? mf : f;
         c.coolreq[a] = (int)cnt;
     }
@@ -1499,10 +1499,10 @@ __device__ __forceinline__ void relax_solve(Ctx& c, double ambient, double irr, 
         iv[j] = 0.0;
         xv[j] = 0.0;
         if (t < n) {
-            const double qin = c.t.is_room[t] ? c.slots[t] + c.t.solar_c[t] * irr : c.t.solar_c[t] * irr;
-            double b = c.t.cap[t] * c.T[t] + qin + ambient * c.dirx[t] + c.t.mcoup[t] * c.M[t];
-            double d = c.t.rx_diag[t];
-            const int col = c.t.rx_air[t];
+            const double qin = c.t.is_room()[t] ? c.slots[t] + c.t.solar_c()[t] * irr : c.t.solar_c()[t] * irr;
+            double b = c.t.cap()[t] * c.T[t] + qin + ambient * c.dirx[t] + c.t.mcoup()[t] * c.M[t];
+            double d = c.t.rx_diag()[t];
+            const int col = c.t.rx_air()[t];
             if (col >= 0) {
                 const double g = c.g[col];
                 b += g * c.tair[col];
@@ -1526,7 +1526,7 @@ __device__ __forceinline__ void relax_solve(Ctx& c, double ambient, double irr, 
 #pragma unroll
     for (int j = 0; j < SBK_RX_RPL; j++) {
         const int t = lane + 64 * j;
-        if (t < n) c.M[t] = c.M[t] * c.t.mret[t] + c.t.mgain[t] * xv[j];
+        if (t < n) c.M[t] = c.M[t] * c.t.mret()[t] + c.t.mgain()[t] * xv[j];
     }
     esync();
 }
@@ -1651,8 +1651,8 @@ __device__ __forceinline__ void relax_block_solve(Ctx& c, double ambient, double
             const int t = row[q][p];
             const int tc = t >= 0 ? t : 0;
             double d = dia[q][p];
-            const double qin = c.t.is_room[tc] ? c.slots[tc] + c.t.solar_c[tc] * irr : c.t.solar_c[tc] * irr;
-            double bb = c.t.cap[tc] * c.T[tc] + qin + ambient * c.dirx[tc] + c.t.mcoup[tc] * c.M[tc];
+            const double qin = c.t.is_room()[tc] ? c.slots[tc] + c.t.solar_c()[tc] * irr : c.t.solar_c()[tc] * irr;
+            double bb = c.t.cap()[tc] * c.T[tc] + qin + ambient * c.dirx[tc] + c.t.mcoup()[tc] * c.M[tc];
             const int ac = air[q][p];
             if (ac >= 0) {
                 const double g = c.g[ac];
@@ -1725,7 +1725,7 @@ __device__ __forceinline__ void relax_block_solve(Ctx& c, double ambient, double
 #pragma unroll
         for (int p = 0; p < BXR; p++) {
             const int t = row[q][p];
-            if (t >= 0) c.M[t] = c.M[t] * c.t.mret[t] + c.t.mgain[t] * xv[q][p];
+            if (t >= 0) c.M[t] = c.M[t] * c.t.mret()[t] + c.t.mgain()[t] * xv[q][p];
         }
     }
     esync();
@@ -1746,7 +1746,7 @@ __device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
         // room cells carry their zone's heat (node-indexed scratch in the slot region)
         for (int z = ln(); z < L->nz; z += W) {
             double qz = c.zq[z];
-            for (int t = c.t.zone_cell_off[z]; t < c.t.zone_cell_off[z + 1]; t++) slots[c.t.zone_cells[t]] = qz;
+            for (int t = c.t.zone_cell_off()[z]; t < c.t.zone_cell_off()[z + 1]; t++) slots[c.t.zone_cells()[t]] = qz;
         }
         esync();
         STAMP(4);
@@ -1765,19 +1765,19 @@ __device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
     // room cells carry their zone's heat; every node then gets its solar gain
     for (int z = ln(); z < L->nz; z += W) {
         double qz = c.zq[z];
-        for (int t = c.t.zone_cell_off[z]; t < c.t.zone_cell_off[z + 1]; t++) c.slots[vb + c.t.pos[c.t.zone_cells[t]]] = qz;
+        for (int t = c.t.zone_cell_off()[z]; t < c.t.zone_cell_off()[z + 1]; t++) c.slots[vb + c.t.pos()[c.t.zone_cells()[t]]] = qz;
     }
     esync();
     for (int t = ln(); t < n; t += W) {
-        const int ps = vb + c.t.pos[t];
-        double qin = c.t.is_room[t] ? slots[ps] + c.t.solar_c[t] * irr : c.t.solar_c[t] * irr;
-        slots[ps] = c.t.cap[t] * c.T[t] + qin + ambient * c.dirx[t] + c.t.mcoup[t] * c.M[t];
+        const int ps = vb + c.t.pos()[t];
+        double qin = c.t.is_room()[t] ? slots[ps] + c.t.solar_c()[t] * irr : c.t.solar_c()[t] * irr;
+        slots[ps] = c.t.cap()[t] * c.T[t] + qin + ambient * c.dirx[t] + c.t.mcoup()[t] * c.M[t];
     }
     esync();
     for (int col = ln(); col < L->k; col += W) {
         double g = c.g[col];
-        slots[c.t.air_slot[col]] += g;
-        slots[vb + c.t.pos[c.t.air_node[col]]] += g * c.tair[col];
+        slots[c.t.air_slot()[col]] += g;
+        slots[vb + c.t.pos()[c.t.air_node()[col]]] += g * c.tair[col];
     }
     esync();
     STAMP(4);
@@ -1786,8 +1786,8 @@ __device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
     run_plan<W>(L, slots, reinterpret_cast<const int4*>(c.prec), pts);
     STAMP(5);
     for (int t = ln(); t < n; t += W) {
-        double y = slots[vb + c.t.pos[t]];
-        c.M[t] = c.M[t] * c.t.mret[t] + c.t.mgain[t] * y;
+        double y = slots[vb + c.t.pos()[t]];
+        c.M[t] = c.M[t] * c.t.mret()[t] + c.t.mgain()[t] * y;
         c.T[t] = y;
     }
     esync();
@@ -1848,7 +1848,7 @@ __device__ __forceinline__ void reward_vavs(Ctx& c, int (&vahu)[SBK_VPL], double
             const int vv0 = base + 64 * u + lane;
             ok[u] = vv0 < nv;
             v[u] = ok[u] ? vv0 : nv - 1;
-            a[u] = c.t.vav_ahu[v[u]];
+            a[u] = c.t.vav_ahu()[v[u]];
         }
         vav_temps<U>(c, c.zq, v, tv, area);
 #pragma unroll
@@ -1900,13 +1900,13 @@ __device__ __forceinline__ double reward(Ctx& c) {
         const double ws = sums[0], at = sums[1];
         double rc = (at > 0.0) ? ws / at : tmean;
         double st = ahu_static(c, a);
-        double fe = c.t.ahu_c[a * 9 + 5];
+        double fe = c.t.ahu_c()[a * 9 + 5];
         double flow = (c.run[a] == 1) ? c.flow[a] : 0.0;
         double mixed = c.recirc[a] * rc + (1.0 - c.recirc[a]) * ambient;
         double sat = (mixed > c.sat[a] && c.run[a] == 1) ? c.sat[a] : mixed;
         c.wsum[a] = flow * st / fe;
         c.atotal[a] = flow * (1.0 - c.recirc[a]) * st / fe;
-        c.fdsum[a] = flow * RHO_AIR * CP_AIR * (sat - mixed) / c.t.ahu_c[a * 9 + 4];
+        c.fdsum[a] = flow * RHO_AIR * CP_AIR * (sat - mixed) / c.t.ahu_c()[a * 9 + 4];
     }
     esync();
     double intake = 0.0, exhaust = 0.0, cooling = 0.0;
