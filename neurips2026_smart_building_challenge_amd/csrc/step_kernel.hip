@@ -596,6 +596,7 @@ __device__ __forceinline__ void write_obs(Ctx& c, float* row, double amb, const 
         }
 #pragma unroll
         for (int u = 0; u < U; u++) {
+            if (i0 + u * W >= nd) break;   // wave-uniform: slots past the field count
             const int i = i0 + u * W + ln();
             const float v32 = (float)v[u];
             if (i < nd) row[i] = (float)((sd[u] > 0.0) ? ((double)v32 - mean[u]) / sd[u] : 0.0);
@@ -915,16 +916,21 @@ __device__ __forceinline__ void decode_apply(Ctx& c) {
         for (int u = 0; u < U; u++) a[u] = c.act[src[u]];
 #pragma unroll
         for (int u = 0; u < U; u++) {
+            if (i0 + u * W >= n) break;   // wave-uniform: slots past the action count
             const int i = i0 + u * W + ln();
-            // discrete: 1 -> +1, else -1, mapped in float64
-            const double m64 = ((double)a[u] == 1.0) ? 1.0 : -1.0;
-            const double nat_d = (m64 - mnr[u]) / (mxr[u] - mnr[u]) * (mx[u] - mn[u]) + mn[u];
             // continuous: clamp, then the float32 span map
             const float m = a[u] > 1.0f ? 1.0f : (a[u] < -1.0f ? -1.0f : a[u]);
             const float span_in = (float)(mxr[u] - mnr[u]);
             const float span_out = (float)(mx[u] - mn[u]);
             const float r = (m - (float)mnr[u]) / span_in * span_out + (float)mn[u];
-            const double nat = disc[u] ? nat_d : (double)r;
+            double nat = (double)r;
+            // discrete: 1 -> +1, else -1, mapped in float64 (only where a lane holds one;
+            // discrete actions follow the continuous ones)
+            if (__any(disc[u] != 0)) {
+                const double m64 = ((double)a[u] == 1.0) ? 1.0 : -1.0;
+                const double nat_d = (m64 - mnr[u]) / (mxr[u] - mnr[u]) * (mx[u] - mn[u]) + mn[u];
+                nat = disc[u] ? nat_d : nat;
+            }
             double v = nat;
             if (fl[u] & ACT_CLAMP) v = nat < 0.0 ? 0.0 : (nat > hi[u] ? hi[u] : nat);
             if (fl[u] & ACT_PUMP_HEAD) v = nat / (GRAV * RHO_W / PA_PER_BAR);
