@@ -274,7 +274,7 @@ enum { KMODE_STEP = 0, KMODE_RESET = 1 };
 // can be issued from the tile and env records alone).
 struct Tile {
     int layout, first, count, lds_bytes;   // lds_bytes: one env's LDS region
-    int img16, rec16;                      // layout image, record + MT words, in 16-byte units
+    int img16, rec16;                      // layout image, record image (no MT words), in 16-byte units
     int lds_state, lds_scen, lds_act;      // LDS offsets within the env region
     int st_iplant;                         // byte offset of the i32 plant counters in the record
     int pad0, pad1;

@@ -710,10 +710,14 @@ __device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday)
     // the draws need the rest of the current block and the start of the next
     const bool twisted = total > 0 && idx + words > SBK_MT_N;
     // gather the tempered words: stream position s -> old[idx + s] or new[idx + s - 624];
-    // words before the twist are read from the old state (staged in LDS) first
+    // words before the twist are read from the old state in HBM (the state is
+    // not staged: most steps draw nothing), the rest after a twist in LDS
     uint32_t w_old[2 * MAXC];
-    gather_words<MAXC>(c.mt, idx, first, need, w_old);
+#pragma unroll
+    for (int r = 0; r < 2 * MAXC; r++) w_old[r] = 0;
+    if (total > 0) gather_words<MAXC>(hbm_mt, idx, first, need, w_old);
     if (twisted) {
+        for (int i = ln(); i < SBK_MT_N; i += W) c.mt[i] = hbm_mt[i];
         esync();
         mt_twist<W>(c.mt);
         int d = first;
@@ -729,6 +733,8 @@ __device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday)
             }
         }
         for (int i = ln(); i < SBK_MT_N; i += W) hbm_mt[i] = c.mt[i];
+        // a later draw of this kernel (the reset's second interval) reads these words back
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "agent");
     }
     // apply the chain updates
 #pragma unroll

@@ -1100,7 +1100,7 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
         const sbk::DevLayout& D = v->layouts[t.layout].dev;
         t.lds_bytes = D.lds.bytes;
         t.img16 = D.img.bytes >> 4;
-        t.rec16 = (D.st.bytes + 4 * SBK_MT_N) >> 4;
+        t.rec16 = D.st.bytes >> 4;
         t.lds_state = D.lds.state;
         t.lds_scen = D.lds.scen;
         t.lds_act = D.lds.act;
