@@ -599,7 +599,7 @@ __device__ __forceinline__ void write_obs(Ctx& c, float* row, double amb, const 
             if (i0 + u * W >= nd) break;   // wave-uniform: slots past the field count
             const int i = i0 + u * W + ln();
             const float v32 = (float)v[u];
-            if (i < nd) row[i] = (float)((sd[u] > 0.0) ? ((double)v32 - mean[u]) / sd[u] : 0.0);
+            if (i < nd) __builtin_nontemporal_store((float)((sd[u] > 0.0) ? ((double)v32 - mean[u]) / sd[u] : 0.0), row + i);
         }
     }
     const int na = L->n_aux;
@@ -608,7 +608,7 @@ __device__ __forceinline__ void write_obs(Ctx& c, float* row, double amb, const 
     for (int z = ln(); z < L->nz; z += W) occ += c.occV[z];
     occ = bisum<W>(occ, c.red);
     if (ln() == 0) row[L->n_dev + na - 1] = (float)occ;
-    for (int i = L->n_dev + na + ln(); i < 1024; i += W) row[i] = 0.0f;
+    for (int i = L->n_dev + na + ln(); i < 1024; i += W) __builtin_nontemporal_store(0.0f, row + i);
 }
 
 // ------------------------------------------------------------------ occupancy
@@ -2010,8 +2010,10 @@ __device__ __forceinline__ double reward(Ctx& c) {
 template <int W>
 __device__ __forceinline__ void store16(unsigned char* dst, const unsigned char* src, int bytes) {
     const int n16 = bytes >> 4;
+    // streaming stores: the record is read back only by the next step's burst
+    typedef unsigned int u4v __attribute__((ext_vector_type(4)));
     for (int i = ln(); i < n16; i += W)
-        reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(src)[i];
+        __builtin_nontemporal_store(reinterpret_cast<const u4v*>(src)[i], reinterpret_cast<u4v*>(dst) + i);
 }
 
 // Staging burst: every thread issues all loads of a round (up to U vectors of
