@@ -157,6 +157,14 @@ double sbx_kernel_timer(Env* envs, int on, int* count);
  * on the bound stream and returns the elapsed milliseconds (synchronises). */
 float sbx_time_step(Env* envs, int iters);
 
+/* puf_step with the step's action rows read from `actions` (device, n x
+ * NUM_ATNS floats, same layout as the bound buffer) instead of the buffer bound
+ * at puf_vec_create; the bound buffer is not touched. For drivers that keep a
+ * bank of pre-drawn action rows resident (the benchmark). No counterpart in the
+ * reference. Returns 0, or -1 for a null pointer. Asynchronous on the bound
+ * stream, capturable. */
+int sbx_step_actions(Env* envs, const float* actions);
+
 /* Runs one step with per-phase wall-clock stamps and reports, for phases
  * 0..n-1 (load, decode, HVAC pre, solve setup, solve, solve epilogue, post,
  * observation, occupancy, reward, bookkeeping, store), the mean and max

@@ -1209,17 +1209,21 @@ void puf_reset(Env* envs) {
     hip_ok(hipStreamSynchronize(g_stream), "reset");
 }
 
-void puf_step(Env* envs) {
-    Vec* v = vec_of(envs);
+// One step reading its action rows from `actions` (the bound buffer when null).
+void step_from(Vec* v, const float* actions) {
+    sbk::KParams p = params(v, sbk::KMODE_STEP);
+    if (actions) p.actions = actions;
     if (v->t_on && v->t_seen++ % v->t_on == 0 && v->t_used < kTimerPairs) {
         hip_ok(hipEventRecord(v->tev[2 * v->t_used], g_stream), "timer event");
-        launch(v, sbk::KMODE_STEP);
+        launch_params(v, p);
         hip_ok(hipEventRecord(v->tev[2 * v->t_used + 1], g_stream), "timer event");
         v->t_used++;
         return;
     }
-    launch(v, sbk::KMODE_STEP);
+    launch_params(v, p);
 }
+
+void puf_step(Env* envs) { step_from(vec_of(envs), nullptr); }
 
 void puf_render(Env* env) { (void)env; }
 
@@ -1458,6 +1462,12 @@ double sbx_kernel_timer(Env* envs, int on, int* count) {
         sum += ms;
     }
     return sum * 1e3 / v->t_used;
+}
+
+int sbx_step_actions(Env* envs, const float* actions) {
+    if (!actions) { g_err = "sbx_step_actions: null action rows"; return -1; }
+    step_from(vec_of(envs), actions);
+    return 0;
 }
 
 float sbx_time_step(Env* envs, int iters) {

@@ -92,7 +92,7 @@ POLICY_HIDDEN, POLICY_HEADS = 128, 544
 EXPORTS = [
     "dict_find", "dict_set", "puf_vec_create", "puf_bind_stream", "puf_init", "puf_reset", "puf_step",
     "puf_render", "puf_close", "puf_log", "puf_live_log", "puf_mask_init", "sbx_gen_actions",
-    "sbx_vec_info", "sbx_env_state", "sbx_time_step", "sbx_phase_times", "sbx_phase_stamps", "sbx_kernel_timer", "sbx_pass_times", "sbx_solve_info",
+    "sbx_vec_info", "sbx_env_state", "sbx_time_step", "sbx_step_actions", "sbx_phase_times", "sbx_phase_stamps", "sbx_kernel_timer", "sbx_pass_times", "sbx_solve_info",
     "sbx_policy_bind", "sbx_policy_act", "sbx_policy_heads", "sbx_beta_sample",
     "sbx_env_meta", "sbx_scenario_path",
     "sbx_plan_layout", "sbx_plan_free", "sbx_last_error", "sbx_version",
@@ -125,6 +125,8 @@ def lib() -> ctypes.CDLL:
         L.sbx_vec_info.argtypes = [ctypes.POINTER(Env), ctypes.POINTER(SbxVecInfo)]
         L.sbx_env_state.argtypes = [ctypes.POINTER(Env), ctypes.c_int, P, ctypes.c_int]
         L.sbx_env_state.restype = ctypes.c_int
+        L.sbx_step_actions.argtypes = [ctypes.POINTER(Env), P]
+        L.sbx_step_actions.restype = ctypes.c_int
         L.sbx_time_step.argtypes = [ctypes.POINTER(Env), ctypes.c_int]
         L.sbx_time_step.restype = ctypes.c_float
         L.sbx_phase_times.argtypes = [ctypes.POINTER(Env), P, P, ctypes.c_int]
@@ -292,6 +294,13 @@ class VecEnv:
 
     def step(self):
         self.L.puf_step(self.envs)
+
+    def step_actions(self, actions) -> None:
+        """One step reading its action rows from `actions` (device tensor, n x 272 float32)."""
+        assert actions.is_cuda and actions.dtype == self.torch.float32 and actions.is_contiguous()
+        assert tuple(actions.shape) == (self.n, SB_ACT)
+        if self.L.sbx_step_actions(self.envs, P(actions.data_ptr())) != 0:
+            raise RuntimeError(self.L.sbx_last_error().decode())
 
     def state(self, i: int) -> np.ndarray:
         buf = np.zeros(16384, np.float64)

@@ -327,6 +327,34 @@ def test_gpu_graph_replay_matches_eager(mixed_dir):
     graph.close()
 
 
+def test_gpu_step_actions_matches_bound_buffer(mixed_dir):
+    """sbx_step_actions with a per-step pointer into a bank of action rows steps
+    exactly like puf_step with the same rows copied into the bound buffer, and
+    leaves the bound buffer alone."""
+    say("step with explicit action rows")
+    a = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=25)
+    b = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=25)
+    a.reset()
+    b.reset()
+    bank = torch.empty((40, a.n, E.SB_ACT), dtype=torch.float32, device="cuda")
+    for s in range(40):
+        a.gen_actions(SEED, s)
+        bank[s].copy_(a.actions)
+    b.actions.fill_(0.25)
+    torch.cuda.synchronize()
+    for s in range(40):
+        a.actions.copy_(bank[s])
+        a.step()
+        b.step_actions(bank[s])
+        torch.cuda.synchronize()
+        assert torch.equal(a.obs, b.obs), s
+        assert torch.equal(a.rewards, b.rewards), s
+        assert torch.equal(a.terminals, b.terminals), s
+    assert torch.all(b.actions == 0.25)
+    a.close()
+    b.close()
+
+
 def test_gpu_log_matches_oracle(cfg0_dir):
     say("episode logs")
     vec = E.VecEnv(1, blob_dir=str(cfg0_dir), max_steps=25)
