@@ -66,7 +66,7 @@ enum { PI_HWS_RUN = 0, PI_PUMP_RUN, PI_HWS_REQ, PI_STEP_INDEX, PI_STEP, PI_MT_ID
 // layout image first, then one region per env).
 struct LdsLayout {
     int state;        // state image (StateLayout offsets are relative to this)
-    int mt;           // u32[624] MT19937 words (staged with the record, which they follow)
+    int mt;           // u32[624] MT19937 words (filled from HBM when a draw twists the state)
     int scen;         // scenario image (ScenImg offsets are relative to this)
     int act;          // f32[SB_ACT] action row of the step
     int slots;        // f64[n_slots]: 0 zero, 1 sink, LU entries, vector (relaxation: node heat)

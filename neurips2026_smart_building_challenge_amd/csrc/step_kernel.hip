@@ -2058,8 +2058,8 @@ __global__ __launch_bounds__(256) void step_kernel(KParams P) {
     STAMP(0);
     {
         // one burst: the layout image (whole block), and per env its record
-        // with the MT words, its scenario image and its action row; the LDS
-        // pointers are bound while the first round's loads are in flight
+        // image, its scenario image and its action row; the LDS pointers are
+        // bound while the first round's loads are in flight
         constexpr int UI = 16, UR = 16, US = 4, UA = 2;   // one round up to 64 KB of image, 16 KB of record
         const int nthr = (int)blockDim.x, tid = (int)threadIdx.x, l = ln();
         const int img16 = tl.img16;

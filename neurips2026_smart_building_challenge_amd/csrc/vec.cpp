@@ -291,8 +291,8 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     S.bytes = align_up(o, 16);
     S.mt = S.bytes;
     S.record_bytes = align_up(S.bytes + 4 * SBK_MT_N, 256);
-    // per-env LDS region: record image + MT words (one staged copy), scenario
-    // image, action row, then scratch
+    // per-env LDS region: record image, MT words (filled when a draw twists),
+    // scenario image, action row, then scratch
     sbk::LdsLayout& Ls = D.lds;
     int l = 0;
     Ls.state = 0; l = S.bytes;
