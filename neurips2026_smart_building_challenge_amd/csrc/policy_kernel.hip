@@ -10,9 +10,11 @@
 // continuous heads write 2x - 1, discrete heads x > 0.5 into the action row the
 // next env step decodes.
 //
-// The three products run on fp32 MFMA (v_mfma_f32_16x16x4_f32): one workgroup
-// per 16 x 16 output tile, its K range split over up to four wavefronts whose
-// partial tiles are summed in LDS in a fixed order, then bias and activation.
+// The three products run on fp32 MFMA (v_mfma_f32_16x16x4_f32). The two
+// hidden layers take one workgroup per 16 x 16 output tile, its K range split
+// over up to four wavefronts whose partial tiles are summed in LDS in a fixed
+// order, then bias and activation; the third layer is fused with the Beta
+// draws, one workgroup per (16 envs, 16 heads).
 // Within a 16-wide K block, lane group g (lanes 16g .. 16g + 15) feeds the
 // k values 4g .. 4g + 3 over the four MFMA steps, so each lane reads its A
 // operand as one contiguous float4 (the product over a block is the same sum).
@@ -117,40 +119,89 @@ __device__ __forceinline__ float gamma_mt(float a, uint32_t env, uint32_t step, 
     return a;
 }
 
-// Head h (< 272) of env e: continuous h < 256 (u, v at columns h, 256 + h),
-// discrete 256 + d (columns 512 + d, 528 + d). Stream 2h draws Ga, 2h + 1 Gb.
-__device__ __forceinline__ int head_col(int h, int which) {
-    return h < 256 ? h + 256 * which : 512 + (h - 256) + 16 * which;
-}
 
-// One thread per gamma draw: lanes 2t and 2t + 1 draw Ga and Gb of head t of
-// the flattened (env, head) index, and the even lane writes the action
-// x = Ga / (Ga + Gb): continuous 2x - 1, discrete x > 0.5; 0 past the env's
-// head counts.
-__global__ __launch_bounds__(256) void beta_heads_kernel(const float* __restrict__ y, float* __restrict__ actions,
-                                                         const int* __restrict__ n_cont,
-                                                         const int* __restrict__ n_disc, int n_envs,
-                                                         uint64_t seed, uint32_t step) {
-    const int gid = blockIdx.x * blockDim.x + threadIdx.x;
-    const int t = gid >> 1, which = gid & 1;
-    const int e = t / kActWidth, h = t - e * kActWidth;
-    const bool live = e < n_envs;
-    const int ec = live ? e : n_envs - 1;
-    const bool used = live && (h < 256 ? h < n_cont[ec] : h - 256 < n_disc[ec]);
-    float g = 1.0f;
-    if (used) {
-        const float a = softplus(y[(size_t)ec * kPolicyHeads + head_col(h, which)]) + 1.0f;
-        g = gamma_mt(a, (uint32_t)e, step, 2u * (uint32_t)h + (uint32_t)which, (uint32_t)seed,
-                     (uint32_t)(seed >> 32));
-    }
-    const float other = __shfl_xor(g, 1, 64);
-    if (live && which == 0) {
-        float v = 0.0f;
-        if (used) {
-            const float x = g / (g + other);
-            v = h < 256 ? 2.0f * x - 1.0f : (x > 0.5f ? 1.0f : 0.0f);
+// Third layer fused with the Beta draws: one workgroup per (16-env tile, group
+// of 16 heads). Waves 0 and 1 compute the group's u and v column tiles of
+// y = h2 W3 + b3 (K = 128, every load ahead of the first MFMA), the tile is
+// kept in LDS (and written to y for sbx_policy_heads), and the 256 threads then
+// take the group's 16 x 16 x 2 gamma draws, two each: lanes 2t and 2t + 1
+// draw Ga and Gb of one head and the even lane writes x = Ga / (Ga + Gb)
+// (continuous 2x - 1, discrete x > 0.5; 0 past the env's head counts).
+constexpr int kHeadGroups = kActWidth / 16;   // 16 continuous groups, 1 discrete
+
+__global__ __launch_bounds__(256) void heads_layer_kernel(const float* __restrict__ h2, const float* __restrict__ w3,
+                                                          const float* __restrict__ b3, float* __restrict__ y,
+                                                          float* __restrict__ actions, const int* __restrict__ n_cont,
+                                                          const int* __restrict__ n_disc, int n, uint64_t seed,
+                                                          uint32_t step) {
+    constexpr int H = kPolicyHidden;
+    __shared__ float ys[16][32 + 1];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int g = lane >> 4, i = lane & 15;
+    const int m0 = blockIdx.x * 16, q = blockIdx.y;
+    if (w < 2) {
+        const int which = w;
+        const int n0 = q < 16 ? 16 * q + 256 * which : 512 + 16 * which;
+        const int mc = m0 + i < n ? m0 + i : n - 1;
+        const float* a_row = h2 + (size_t)mc * H + 4 * g;
+        const float* b_col = w3 + (size_t)(4 * g) * kPolicyHeads + n0 + i;
+        float4 a[H / 16];
+        float b[H / 16][4];
+#pragma unroll
+        for (int j = 0; j < H / 16; j++) {
+            a[j] = *reinterpret_cast<const float4*>(a_row + 16 * j);
+#pragma unroll
+            for (int s = 0; s < 4; s++) b[j][s] = b_col[(size_t)(16 * j + s) * kPolicyHeads];
         }
-        actions[(size_t)e * kActWidth + h] = v;
+#pragma unroll
+        for (int j = 0; j < H / 16; j++) {
+            asm volatile("" : "+v"(a[j].x), "+v"(a[j].y), "+v"(a[j].z), "+v"(a[j].w));
+            asm volatile("" : "+v"(b[j][0]), "+v"(b[j][1]), "+v"(b[j][2]), "+v"(b[j][3]));
+        }
+        v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < H / 16; j++) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].x, b[j][0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].y, b[j][1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].z, b[j][2], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].w, b[j][3], acc, 0, 0, 0);
+        }
+        const float bv = b3[n0 + i];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int row = 4 * g + r;
+            const float v = acc[r] + bv;
+            ys[row][16 * which + i] = v;
+            if (m0 + row < n) y[(size_t)(m0 + row) * kPolicyHeads + n0 + i] = v;
+        }
+    }
+    __syncthreads();
+    // draw d = 2 (row * 16 + k) + which of this group: 512 draws, two per thread
+#pragma unroll
+    for (int d0 = 0; d0 < 16 * 16 * 2; d0 += 256) {
+        const int d = d0 + (int)threadIdx.x;
+        const int which = d & 1, p = d >> 1;
+        const int row = p >> 4, k = p & 15;
+        const int e = m0 + row;
+        const int h = 16 * q + k;
+        const bool live = e < n;
+        const int ec = live ? e : n - 1;
+        const bool used = live && (h < 256 ? h < n_cont[ec] : h - 256 < n_disc[ec]);
+        float gm = 1.0f;
+        if (used) {
+            const float a = softplus(ys[row][16 * which + k]) + 1.0f;
+            gm = gamma_mt(a, (uint32_t)e, step, 2u * (uint32_t)h + (uint32_t)which, (uint32_t)seed,
+                          (uint32_t)(seed >> 32));
+        }
+        const float other = __shfl_xor(gm, 1, 64);
+        if (live && which == 0) {
+            float v = 0.0f;
+            if (used) {
+                const float x = gm / (gm + other);
+                v = h < 256 ? 2.0f * x - 1.0f : (x > 0.5f ? 1.0f : 0.0f);
+            }
+            actions[(size_t)e * kActWidth + h] = v;
+        }
     }
 }
 
@@ -180,10 +231,8 @@ extern "C" int sbk_launch_policy(const float* obs, const float* w1, const float*
                        kObsWidth, w1, b1, h1, kPolicyHidden, n, kPolicyHidden);
     hipLaunchKernelGGL((mlp_layer_kernel<1, kPolicyHidden / 2>), dim3(mt, kPolicyHidden / 16), dim3(128), 0, s, h1,
                        kPolicyHidden, w2, b2, h2, kPolicyHidden, n, kPolicyHidden);
-    hipLaunchKernelGGL((mlp_layer_kernel<0, kPolicyHidden / 2>), dim3(mt, kPolicyHeads / 16), dim3(128), 0, s, h2,
-                       kPolicyHidden, w3, b3, y, kPolicyHeads, n, kPolicyHeads);
-    const long long draws = 2LL * n * kActWidth;
-    hipLaunchKernelGGL(beta_heads_kernel, dim3((unsigned)((draws + 255) / 256)), dim3(256), 0, s, y, actions, n_cont,
+    // third layer and the Beta draws in one launch per (env tile, head group)
+    hipLaunchKernelGGL(heads_layer_kernel, dim3(mt, kHeadGroups), dim3(256), 0, s, h2, w3, b3, y, actions, n_cont,
                        n_disc, n, seed, step);
     return (int)hipGetLastError();
 }
