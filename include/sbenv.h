@@ -129,12 +129,12 @@ typedef struct SbxVecInfo {
     int n_envs;
     int n_layouts;
     int n_scenarios;
-    int block;              /* threads per workgroup (64 per env) */
+    int block;              /* threads per workgroup (128 per env: two wavefronts) */
     int lds_bytes;          /* dynamic LDS per workgroup */
     int max_nodes;
     double bytes_per_step;  /* algorithmic HBM bytes of one puf_step (all envs) */
     double flops_per_step;  /* fp64 flops of one puf_step's solves (all envs) */
-    int envs_per_block;     /* envs sharing a workgroup (one wavefront each) */
+    int envs_per_block;     /* envs sharing a workgroup (two wavefronts each) */
 } SbxVecInfo;
 void sbx_vec_info(Env* envs, SbxVecInfo* out);
 

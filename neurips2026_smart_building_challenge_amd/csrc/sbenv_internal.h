@@ -16,7 +16,8 @@
 #define SBK_MT_N 624
 #define SBK_NAUX_MAX 16
 #define SBK_KMAX 48      // terms per lane per pass (matches the planner)
-#define SBK_NSTAMP 16    // phase stamps per workgroup when phase timing is on
+#define SBK_NSTAMP 20        // phase stamps per env when phase timing is on
+#define SBK_STAMP_HELPER 15  // stamps from here on are the env's helper wavefront's
 #define SBK_VPL 4        // VAVs (and coupled columns) per lane: at most 256 per env
 #define SBK_RX_RPL 4     // relaxation rows per lane (matches the planner)
 #define SBK_RX_ROWS 256  // padded relaxation rows
@@ -79,6 +80,8 @@ struct LdsLayout {
     int misc;         // f64[MS_SIZE] scalars
     int obsx;         // f64[OX_AHU + 4 * na] per-step values the observation reads (OX_*)
     int iscr;         // i32[W + 8] scan scratch
+    int occn;         // u8[nz * nassign + nz] the helper's new chain states and zone counts
+    int sync;         // i32[SY_WORDS] hand-off flags of the env's two wavefronts
     int prec;         // int4[n_pass] solve pass records (copied at kernel start)
     int bytes;        // region size, 16-byte multiple
 };
@@ -268,6 +271,10 @@ struct EnvDesc {
 };
 
 enum { KMODE_STEP = 0, KMODE_RESET = 1 };
+// Words of an env's hand-off area (LdsLayout::sync): flags posted by the first
+// wavefront (post-step state ready, observation written) and by the helper
+// (new occupancy, reward and bookkeeping done).
+enum { SY_POST = 0, SY_OBS = 1, SY_DONE = 2, SY_WORDS = 4 };
 
 // A workgroup's envs: order[first .. first + count) all of one layout, with
 // the layout's staging burst inputs (copied from its DevLayout so the burst

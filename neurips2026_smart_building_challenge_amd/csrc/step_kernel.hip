@@ -1,20 +1,25 @@
 // Fused Smart Buildings env step for MI355X (gfx950).
 //
-// One workgroup of W lanes owns one env for one step. The env's state record
-// is copied HBM -> LDS in one coalesced pass, every phase of the step runs out
-// of LDS, and the record is copied back at the end:
+// One workgroup steps a tile of up to four envs of one layout. The layout
+// image and each env's state record are copied HBM -> LDS in one burst, every
+// phase of the step runs out of LDS, and the record is copied back at the end.
+// Each env has two wavefronts: the first runs the physics chain, the second
+// (its helper) runs the work that does not feed that chain alongside it.
 //
+//   first wavefront
 //   decode + apply     complete_port/csim/sb_sim.c:557-576, :220-244
-//   HVAC pre           sb_sim.c:357-457 (lanes over VAVs / zones, block sums)
-//   field solve        sb_fdm.c:142-188 restated as (A + P G S) y = b + P G T_air
-//                      (Woodbury form of csim's air-side step): numeric LU of
-//                      the permuted system, forward and backward solves, all as
-//                      one host-built level schedule over LDS slots
+//   HVAC pre           sb_sim.c:357-457 (lanes over VAVs / zones, wave sums)
+//   field solve        sb_fdm.c:142-188 restated as (A + diag(g)) y = b: block
+//                      or point relaxation with a certified stop, or numeric
+//                      LU over a host-built level schedule
 //   post               sb_sim.c:489-521 (boiler return, ramp)
 //   observation        complete_port/csim/sb_obs.c:49-64
+//   auto-reset         complete_port/pufferlib_cpu_env.h:187-208, sb_sim.c:177-218
+//   helper wavefront
 //   occupancy          sb_occup.c:36-61, MT19937 draws assigned by prefix sum
-//   reward             sb_reward.c:31-155
-//   bookkeeping        complete_port/pufferlib_cpu_env.h:243-256 (+ auto-reset)
+//                      (during decode, HVAC pre and solve: it is exogenous)
+//   reward             sb_reward.c:31-155 (during the observation)
+//   bookkeeping        complete_port/pufferlib_cpu_env.h:243-256
 #include <hip/hip_runtime.h>
 
 #include "sbenv.h"
@@ -34,9 +39,10 @@ namespace sbk {
 enum { M_OFF = 0, M_HEAT = 1, M_COOL = 2, M_PASSIVE = 3 };
 
 // Phase stamp of env c.e (wall clock, written by its lane 0 when phase timing is on).
+// Stamps below SBK_STAMP_HELPER are the env's first wavefront's, the rest its helper's.
 #define STAMP(i)                                                                        \
     do {                                                                                \
-        if (P.phase_ts && (threadIdx.x & 63) == 0)                                      \
+        if (P.phase_ts && (threadIdx.x & 63) == 0 && c.helper == ((i) >= SBK_STAMP_HELPER)) \
             P.phase_ts[(size_t)c.e * SBK_NSTAMP + (i)] = wall_clock64();                \
     } while (0)
 
@@ -335,6 +341,7 @@ struct Ctx {
     const SBK_C DevLayout* L;
     const SBK_C DevScen* S;
     int e;                   // env index
+    bool helper;             // the env's second wavefront
     unsigned char* rec;      // HBM record of this env
     Tab t;
     double *T, *M, *damper, *reheat, *ratio, *heatsp, *coolsp, *dcmd, *rcmd, *sensing;
@@ -680,9 +687,10 @@ __device__ __forceinline__ void gather_words(Ptr src, int idx, int first, const 
 // Occupant o = z * nassign + a draws iff it is at home in the arrival window
 // or at work in the departure window of a workday; draws are taken from the
 // MT stream in occupant order, so occupant o uses the words at
-// 2 * (number of drawing occupants before o).
+// 2 * (number of drawing occupants before o). The new chain states go to
+// st_out (which may be c.occ_state itself) and the zone counts to v_out.
 template <int W>
-__device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday) {
+__device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday, uint8_t* st_out, uint8_t* v_out) {
     const SBK_C DevLayout* L = c.L;
     const SBK_C DevScen* S = c.S;
     const int nocc = L->nz * L->nassign;
@@ -756,7 +764,7 @@ __device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday)
                 double u = ((w_old[2 * r] >> 5) * 67108864.0 + (w_old[2 * r + 1] >> 6)) / 9007199254740992.0;
                 if (u < S->p_dep) st = 0;
             }
-            c.occ_state[o] = (uint8_t)st;
+            st_out[o] = (uint8_t)st;
         }
     }
     esync();
@@ -766,8 +774,8 @@ __device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday)
     }
     for (int z = ln(); z < L->nz; z += W) {
         int s = 0;
-        for (int a = 0; a < L->nassign; a++) s += c.occ_state[z * L->nassign + a];
-        c.occV[z] = (uint8_t)s;
+        for (int a = 0; a < L->nassign; a++) s += st_out[z * L->nassign + a];
+        v_out[z] = (uint8_t)s;
     }
     esync();
 }
@@ -836,7 +844,7 @@ __device__ __forceinline__ void env_reset(Ctx& c, int start, float* obs_row) {
 #pragma nounroll
     for (int k = 0; k < 2; k++) {
         occupancy_advance<W>(c, k == 0 ? S->hour_m1[start] : S->occ_hour[start],
-                             k == 0 ? S->work_m1[start] : S->occ_work[start]);
+                             k == 0 ? S->work_m1[start] : S->occ_work[start], c.occ_state, c.occV);
         if (k == 0) write_obs<W>(c, obs_row, S->amb[start], S->aux_time + (size_t)start * (c.L->n_aux - 1));
     }
 }
@@ -1210,7 +1218,7 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
     const int na = L->na, nv = L->nv;
     zone_means<W>(c, c.zq);
     esync();
-    STAMP(13);
+    STAMP(12);
     // AHU return-air means and supply temperatures (sb_sim.c:382-387, :253-265):
     // flow-factor sum over all VAVs, then one lane per AHU sums over its VAVs
     // in VAV order (as csim accumulates them)
@@ -1232,7 +1240,7 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
     }
     if (nv > 64) vav_pass<2>(c, comfort, ffs_part, vahu, vv);
     else vav_pass<1>(c, comfort, ffs_part, vahu, vv);
-    STAMP(14);
+    STAMP(13);
     const double ffs = bsum<W>(ffs_part, c.red);
     double sums[3];
     ahu_sums<3>(vahu, vv, na, sums);
@@ -1271,7 +1279,7 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
         }
     }
     esync();
-    STAMP(15);
+    STAMP(14);
     const double tf = total_flow_rate(c);
     const double iwt = c.plant[PF_BOILER_CUR];
     // coupled columns: reheat energy, air-side conductance, AHU flow (sb_sim.c:410-436),
@@ -1878,7 +1886,7 @@ __device__ __forceinline__ void reward_vavs(Ctx& c, int (&vahu)[SBK_VPL], double
 }
 
 template <int W>
-__device__ __forceinline__ double reward(Ctx& c) {
+__device__ __forceinline__ double reward(Ctx& c, const uint8_t* occ_v) {
     const SBK_C DevLayout* L = c.L;
     const SBK_C DevScen* S = c.S;
     const double dt = S->dt_sec, inv_hour = 1.0 / 3600.0;
@@ -1959,7 +1967,7 @@ __device__ __forceinline__ double reward(Ctx& c) {
             occv[r] = 0.0;
             ztv[r] = 0.0;
             if (64 * r < L->nz) {
-                occv[r] = (double)c.occV[zc];
+                occv[r] = (double)occ_v[zc];
                 ztv[r] = c.zq[zc];
             }
         }
@@ -2039,100 +2047,36 @@ __device__ __forceinline__ void part_store(const uint4 (&r)[U], uint4* dst, int 
     }
 }
 
-template <int W, int KV>
-__global__ __launch_bounds__(256) void step_kernel(KParams P) {
-    static_assert(W == 64, "one wavefront per env");
-    extern __shared__ __align__(16) unsigned char lds[];
-    const Tile tl = P.tiles[blockIdx.x];
-    const SBK_C DevLayout* L = P.layouts + tl.layout;
-    const int slot = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));   // wave-uniform
-    const bool active = slot < tl.count;
-    const int e = P.order[tl.first + (active ? slot : 0)];
-    const EnvDesc ed = P.envs[e];
-    Ctx c;
-    c.L = L;
-    c.S = P.scens + ed.scen;
-    c.e = e;
-    c.rec = P.state + ed.state_off;
-    unsigned char* env = lds + P.img_lds + slot * tl.lds_bytes;
-    STAMP(0);
-    {
-        // one burst: the layout image (whole block), and per env its record
-        // image, its scenario image and its action row; the LDS pointers are
-        // bound while the first round's loads are in flight
-        constexpr int UI = 16, UR = 16, US = 4, UA = 2;   // one round up to 64 KB of image, 16 KB of record
-        const int nthr = (int)blockDim.x, tid = (int)threadIdx.x, l = ln();
-        const int img16 = tl.img16;
-        const int rec16 = active ? tl.rec16 : 0;
-        const int scn16 = active ? ed.scn16 : 0;
-        const int act16 = (active && P.mode == KMODE_STEP) ? (4 * SB_ACT) >> 4 : 0;
-        const SBK_C uint4* isrc = reinterpret_cast<const SBK_C uint4*>(tl.img_src);
-        const SBK_C uint4* ssrc = reinterpret_cast<const SBK_C uint4*>(ed.scen_src);
-        const uint4* rsrc = reinterpret_cast<const uint4*>(c.rec);
-        const uint4* asrc = reinterpret_cast<const uint4*>(P.actions + (size_t)e * SB_ACT);
-        uint4* idst = reinterpret_cast<uint4*>(lds);
-        uint4* rdst = reinterpret_cast<uint4*>(env + tl.lds_state);
-        uint4* sdst = reinterpret_cast<uint4*>(env + tl.lds_scen);
-        uint4* adst = reinterpret_cast<uint4*>(env + tl.lds_act);
-        const int rounds = max(max((img16 + UI * nthr - 1) / (UI * nthr), (rec16 + UR * 64 - 1) / (UR * 64)),
-                               max((scn16 + US * 64 - 1) / (US * 64), (act16 + UA * 64 - 1) / (UA * 64)));
-        // the step's calendar position, read from the record in HBM so the
-        // calendar row loads go out while the burst is in flight
-        const bool stepping = active && P.mode == KMODE_STEP;
-        int kk = 0, j1 = 0;
-        if (stepping) {
-            const int* ipg = reinterpret_cast<const int*>(c.rec + tl.st_iplant);
-            kk = ipg[PI_STEP_INDEX];
-            j1 = ed.start + ipg[PI_STEP] + 1;
-        }
-        {
-            uint4 pi[UI], pr[UR], ps[US], pa[UA];
-            part_load(pi, isrc, img16, tid, nthr, 0);
-            part_load(pr, rsrc, rec16, l, 64, 0);
-            part_load(ps, ssrc, scn16, l, 64, 0);
-            part_load(pa, asrc, act16, l, 64, 0);
-            bind(c, lds, env);
-            if (stepping) {
-                const RowVals rv = row_issue<W>(c, __builtin_amdgcn_readfirstlane(kk),
-                                                __builtin_amdgcn_readfirstlane(j1));
-                part_store(pi, idst, img16, tid, nthr, 0);
-                part_store(pr, rdst, rec16, l, 64, 0);
-                part_store(ps, sdst, scn16, l, 64, 0);
-                part_store(pa, adst, act16, l, 64, 0);
-                row_store<W>(c, rv);
-            } else {
-                part_store(pi, idst, img16, tid, nthr, 0);
-                part_store(pr, rdst, rec16, l, 64, 0);
-                part_store(ps, sdst, scn16, l, 64, 0);
-                part_store(pa, adst, act16, l, 64, 0);
-            }
-        }
-        for (int rd = 1; rd < rounds; rd++) {
-            uint4 pi[UI], pr[UR], ps[US], pa[UA];
-            part_load(pi, isrc, img16, tid, nthr, rd * UI * nthr);
-            part_load(pr, rsrc, rec16, l, 64, rd * UR * 64);
-            part_load(ps, ssrc, scn16, l, 64, rd * US * 64);
-            part_load(pa, asrc, act16, l, 64, rd * UA * 64);
-            part_store(pi, idst, img16, tid, nthr, rd * UI * nthr);
-            part_store(pr, rdst, rec16, l, 64, rd * UR * 64);
-            part_store(ps, sdst, scn16, l, 64, rd * US * 64);
-            part_store(pa, adst, act16, l, 64, rd * UA * 64);
-        }
-        if (active && P.mode == KMODE_STEP) {
-            const SBK_C uint4* src = reinterpret_cast<const SBK_C uint4*>(L->pinfo);
-            for (int i = l; i < L->n_pass; i += W) reinterpret_cast<uint4*>(c.prec)[i] = src[i];
-        }
-    }
-    __syncthreads();   // the only workgroup barrier: the layout image is shared
-    if (!active) return;
-    STAMP(1);
-    float* obs_row = P.obs + (size_t)e * 1024;
-    // the step (KMODE_STEP), then one shared reset path for puf_reset and for
-    // the auto-reset at the end of an episode
-    const bool reset_mode = P.mode == KMODE_RESET;
-    int done = 0;
-    if (!reset_mode) {
-    // host-visible log fields (trainer may clear them between steps)
+// Cross-wavefront hand-off between an env's two wavefronts (same workgroup):
+// a workgroup-scope release waits for the wavefront's LDS operations
+// (lgkmcnt) before the flag is written, and the waiter polls the flag, so LDS
+// data written before env_post is visible to LDS reads after env_wait.
+__device__ __forceinline__ void env_post(int* flag, int v) {
+    esync();
+    if (ln() == 0) __hip_atomic_store(flag, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__device__ __forceinline__ void env_wait(int* flag, int v) {
+    while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) < v)
+        __builtin_amdgcn_s_sleep(1);
+}
+
+// The env's second wavefront during a step: the occupancy interval (exogenous:
+// it reads only the chain states, the MT stream and the calendar, so it runs
+// while the first wavefront decodes, runs the HVAC pre-step and solves), then
+// the reward once the post-step state is there (while the first wavefront
+// writes the observation), then, once the observation has read the old
+// counts, the new chain states and the bookkeeping of puf_step's tail
+// (pufferlib_cpu_env.h:243-256): reward and terminal, step counters, the
+// host-visible log. The host log fields are read first, so their latency
+// hides behind the occupancy work. Each wait is for a post the first
+// wavefront always makes.
+template <int W>
+__device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, unsigned char* env, int max_steps) {
+    const SBK_C DevLayout* L = c.L;
+    const int nocc = L->nz * L->nassign;
+    const int e = c.e;
+    // host-visible log fields (the trainer may clear them between steps)
     Log* hlog = nullptr;
     float lg_ret = 0.f, lg_mean = 0.f;
     if (P.host_env && ln() == 0) {
@@ -2141,30 +2085,27 @@ __global__ __launch_bounds__(256) void step_kernel(KParams P) {
         lg_ret = __hip_atomic_load(&hlog->episode_return, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         lg_mean = __hip_atomic_load(&hlog->reward_mean, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
-    decode_apply<W>(c);
-    STAMP(2);
-    step_pre<W>(c, P);
-    STAMP(3);
-    field_step<W, KV>(c, P);
-    STAMP(6);
-    step_post<W>(c);
-    STAMP(7);
-    const int step = c.ip[PI_STEP] + 1;
-    write_obs<W>(c, obs_row, c.misc[MS_ROW + RW_AMB_J], c.misc + MS_AUX);
-    esync();
-    STAMP(8);
-    occupancy_advance<W>(c, (int)c.misc[MS_ROW + RW_OCC_HOUR_J], (int)c.misc[MS_ROW + RW_OCC_WORK_J]);
-    STAMP(9);
-    const double rew = reward<W>(c);
-    STAMP(10);
-    const float r = (float)rew;
-    done = step >= ed.max_steps;
+    uint8_t* st_new = env + L->lds.occn;
+    uint8_t* v_new = st_new + nocc;
+    occupancy_advance<W>(c, (int)c.misc[MS_ROW + RW_OCC_HOUR_J], (int)c.misc[MS_ROW + RW_OCC_WORK_J], st_new, v_new);
+    STAMP(15);
+    env_wait(sy + SY_POST, 1);
+    STAMP(16);
+    const double rew = reward<W>(c, v_new);
+    STAMP(17);
+    env_wait(sy + SY_OBS, 1);
+    for (int i = ln(); i < nocc; i += W) c.occ_state[i] = st_new[i];
+    for (int z = ln(); z < L->nz; z += W) c.occV[z] = v_new[z];
     if (ln() == 0) {
+        const float r = (float)rew;
+        const int step = c.ip[PI_STEP] + 1;
+        const int done = step >= max_steps;
         P.rewards[e] = r * P.reward_scale;
         P.terminals[e] = done ? 1.0f : 0.0f;
         c.ip[PI_STEP] = step;
         c.plant[PF_REW_SUM] += rew;
         c.ip[PI_STEPS_TOTAL] += 1;
+        if (done) c.ip[PI_EPISODES] += 1;
         if (hlog) {
             float ret = lg_ret + r;
             float mean = lg_mean + (r - lg_mean) / (float)step;
@@ -2183,9 +2124,136 @@ __global__ __launch_bounds__(256) void step_kernel(KParams P) {
                 __hip_atomic_store(&lf[5], nn + 1.0f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             }
         }
-        if (done) c.ip[PI_EPISODES] += 1;
     }
-    esync();
+    env_post(sy + SY_DONE, 1);
+    STAMP(18);
+}
+
+// One workgroup per tile of E envs of one layout, two wavefronts per env:
+// wavefronts [0, E) step the envs, wavefronts [E, 2E) are their helpers (the
+// helper of env slot s is wavefront E + (s + E - E/2) % E, on another SIMD
+// than its env's first wavefront).
+template <int W, int KV>
+__global__ __launch_bounds__(512) void step_kernel(KParams P) {
+    static_assert(W == 64, "one wavefront per env");
+    extern __shared__ __align__(16) unsigned char lds[];
+    const Tile tl = P.tiles[blockIdx.x];
+    const SBK_C DevLayout* L = P.layouts + tl.layout;
+    const int E = (int)(blockDim.x >> 7);
+    const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));   // wave-uniform
+    const bool helper = wv >= E;
+    const int slot = helper ? (wv - E + (E >> 1)) % E : wv;
+    const bool active = slot < tl.count;
+    const int e = P.order[tl.first + (active ? slot : 0)];
+    const EnvDesc ed = P.envs[e];
+    Ctx c;
+    c.L = L;
+    c.S = P.scens + ed.scen;
+    c.e = e;
+    c.helper = helper;
+    c.rec = P.state + ed.state_off;
+    unsigned char* env = lds + P.img_lds + slot * tl.lds_bytes;
+    int* sy = reinterpret_cast<int*>(env + L->lds.sync);
+    STAMP(0);
+    {
+        // one burst: the layout image (whole block, every thread), and per env
+        // (its two wavefronts) its record image, its scenario image and its
+        // action row; the LDS pointers are bound while the first round's loads
+        // are in flight
+        constexpr int UI = 8, UR = 8, US = 2, UA = 1;   // one round: 64 KB of image, 16 KB of record
+        constexpr int ET = 2 * W;                        // threads per env
+        const int nthr = (int)blockDim.x, tid = (int)threadIdx.x;
+        const int et = (helper ? W : 0) + ln();
+        const int img16 = tl.img16;
+        const int rec16 = active ? tl.rec16 : 0;
+        const int scn16 = active ? ed.scn16 : 0;
+        const int act16 = (active && P.mode == KMODE_STEP) ? (4 * SB_ACT) >> 4 : 0;
+        const SBK_C uint4* isrc = reinterpret_cast<const SBK_C uint4*>(tl.img_src);
+        const SBK_C uint4* ssrc = reinterpret_cast<const SBK_C uint4*>(ed.scen_src);
+        const uint4* rsrc = reinterpret_cast<const uint4*>(c.rec);
+        const uint4* asrc = reinterpret_cast<const uint4*>(P.actions + (size_t)e * SB_ACT);
+        uint4* idst = reinterpret_cast<uint4*>(lds);
+        uint4* rdst = reinterpret_cast<uint4*>(env + tl.lds_state);
+        uint4* sdst = reinterpret_cast<uint4*>(env + tl.lds_scen);
+        uint4* adst = reinterpret_cast<uint4*>(env + tl.lds_act);
+        const int rounds = max(max((img16 + UI * nthr - 1) / (UI * nthr), (rec16 + UR * ET - 1) / (UR * ET)),
+                               max((scn16 + US * ET - 1) / (US * ET), (act16 + UA * ET - 1) / (UA * ET)));
+        // the step's calendar position, read from the record in HBM so the
+        // calendar row loads (first wavefront) go out while the burst is in flight
+        const bool rows = active && !helper && P.mode == KMODE_STEP;
+        int kk = 0, j1 = 0;
+        if (rows) {
+            const int* ipg = reinterpret_cast<const int*>(c.rec + tl.st_iplant);
+            kk = ipg[PI_STEP_INDEX];
+            j1 = ed.start + ipg[PI_STEP] + 1;
+        }
+        {
+            uint4 pi[UI], pr[UR], ps[US], pa[UA];
+            part_load(pi, isrc, img16, tid, nthr, 0);
+            part_load(pr, rsrc, rec16, et, ET, 0);
+            part_load(ps, ssrc, scn16, et, ET, 0);
+            part_load(pa, asrc, act16, et, ET, 0);
+            bind(c, lds, env);
+            if (rows) {
+                const RowVals rv = row_issue<W>(c, __builtin_amdgcn_readfirstlane(kk),
+                                                __builtin_amdgcn_readfirstlane(j1));
+                part_store(pi, idst, img16, tid, nthr, 0);
+                part_store(pr, rdst, rec16, et, ET, 0);
+                part_store(ps, sdst, scn16, et, ET, 0);
+                part_store(pa, adst, act16, et, ET, 0);
+                row_store<W>(c, rv);
+            } else {
+                part_store(pi, idst, img16, tid, nthr, 0);
+                part_store(pr, rdst, rec16, et, ET, 0);
+                part_store(ps, sdst, scn16, et, ET, 0);
+                part_store(pa, adst, act16, et, ET, 0);
+            }
+        }
+        for (int rd = 1; rd < rounds; rd++) {
+            uint4 pi[UI], pr[UR], ps[US], pa[UA];
+            part_load(pi, isrc, img16, tid, nthr, rd * UI * nthr);
+            part_load(pr, rsrc, rec16, et, ET, rd * UR * ET);
+            part_load(ps, ssrc, scn16, et, ET, rd * US * ET);
+            part_load(pa, asrc, act16, et, ET, rd * UA * ET);
+            part_store(pi, idst, img16, tid, nthr, rd * UI * nthr);
+            part_store(pr, rdst, rec16, et, ET, rd * UR * ET);
+            part_store(ps, sdst, scn16, et, ET, rd * US * ET);
+            part_store(pa, adst, act16, et, ET, rd * UA * ET);
+        }
+        if (rows) {
+            const SBK_C uint4* src = reinterpret_cast<const SBK_C uint4*>(L->pinfo);
+            for (int i = ln(); i < L->n_pass; i += W) reinterpret_cast<uint4*>(c.prec)[i] = src[i];
+        }
+        if (active && !helper && ln() < SY_WORDS) sy[ln()] = 0;
+    }
+    __syncthreads();   // the only workgroup barrier: the layout image is shared
+    if (!active) return;
+    const bool reset_mode = P.mode == KMODE_RESET;
+    if (helper) {
+        if (!reset_mode) helper_step<W>(c, P, sy, env, ed.max_steps);
+        return;
+    }
+    STAMP(1);
+    float* obs_row = P.obs + (size_t)e * 1024;
+    // the step (KMODE_STEP), then one shared reset path for puf_reset and for
+    // the auto-reset at the end of an episode
+    int done = 0;
+    if (!reset_mode) {
+        decode_apply<W>(c);
+        STAMP(2);
+        step_pre<W>(c, P);
+        STAMP(3);
+        field_step<W, KV>(c, P);
+        STAMP(6);
+        step_post<W>(c);
+        env_post(sy + SY_POST, 1);   // the helper's reward reads the post-step state
+        STAMP(7);
+        done = c.ip[PI_STEP] + 1 >= ed.max_steps;   // read before the helper advances the counter
+        write_obs<W>(c, obs_row, c.misc[MS_ROW + RW_AMB_J], c.misc + MS_AUX);
+        env_post(sy + SY_OBS, 1);    // the observation has read the old occupant counts
+        STAMP(8);
+        env_wait(sy + SY_DONE, 1);   // new occupancy, reward and bookkeeping from the helper
+        STAMP(9);
     }
     if (reset_mode || done) {
         env_reset<W>(c, ed.start, obs_row);
@@ -2197,9 +2265,9 @@ __global__ __launch_bounds__(256) void step_kernel(KParams P) {
         }
     }
     esync();
-    STAMP(11);
+    STAMP(10);
     store16<W>(c.rec, env + L->lds.state, L->st.bytes);
-    STAMP(12);
+    STAMP(11);
 }
 
 // Beta(2,2) action rows (see sbx_gen_actions in sbenv.h): the median of three
@@ -2233,11 +2301,11 @@ __global__ void gen_actions_kernel(float* actions, const int* n_cont, const int*
 }  // namespace sbk
 
 // ---------------------------------------------------------------- launchers
-// threads: 64 per env of a tile (at most 4 envs per workgroup).
+// threads: 128 per env of a tile (two wavefronts; at most 4 envs per workgroup).
 extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int threads, int lds_bytes, int variant,
                                hipStream_t s) {
     using namespace sbk;
-    if (threads < 64 || threads > 256 || threads % 64) return (int)hipErrorInvalidValue;
+    if (threads < 128 || threads > 512 || threads % 128) return (int)hipErrorInvalidValue;
     switch (variant) {
     case KV_LU: hipLaunchKernelGGL((step_kernel<64, KV_LU>), dim3(n_blocks), dim3(threads), lds_bytes, s, *p); break;
     case KV_POINT:

@@ -311,6 +311,10 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     Ls.obsx = l; l += 8 * (sbk::OX_AHU + 4 * na);
     Ls.iscr = l; l += 4 * (width / 64 + 8);
     l = align_up(l, 16);
+    Ls.occn = l; l += nz * nassign + nz;
+    l = align_up(l, 16);
+    Ls.sync = l; l += 4 * sbk::SY_WORDS;
+    l = align_up(l, 16);
     Ls.prec = l; l += 16 * D.n_pass;
     Ls.bytes = align_up(l, 16);
     D.bytes_per_step = 2.0 * S.bytes + 4.0 * (ncont + ndisc) + 4.0 * SB_OBS + 8.0;
@@ -855,7 +859,7 @@ void launch_params(Vec* v, const sbk::KParams& p) {
     for (const TileGroup& g : v->groups) {
         sbk::KParams q = p;
         q.tiles = v->d_tiles + g.first;
-        int rc = sbk_launch_step(&q, g.count, v->width * v->epb, v->lds_bytes, g.variant, g_stream);
+        int rc = sbk_launch_step(&q, g.count, 2 * v->width * v->epb, v->lds_bytes, g.variant, g_stream);
         if (rc != 0) die(std::string("step kernel launch failed: ") + hipGetErrorString((hipError_t)rc));
     }
 }
@@ -1042,7 +1046,7 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
         }
     }
     v->state_bytes = state_off;
-    // tiles: envs of one layout share a workgroup (one wavefront each) and the
+    // tiles: envs of one layout share a workgroup (two wavefronts each) and the
     // layout image it stages; largest layouts first, then by scenario
     v->order.resize(n);
     for (int i = 0; i < n; i++) v->order[i] = i;
@@ -1308,7 +1312,7 @@ void sbx_vec_info(Env* envs, SbxVecInfo* out) {
     out->n_envs = v->n;
     out->n_layouts = (int)v->layouts.size();
     out->n_scenarios = (int)v->scens.size();
-    out->block = v->width * v->epb;
+    out->block = 2 * v->width * v->epb;
     out->lds_bytes = v->lds_bytes;
     out->envs_per_block = v->epb;
     for (auto& L : v->layouts) out->max_nodes = std::max(out->max_nodes, L.dev.n);

@@ -348,7 +348,8 @@ class VecEnv:
         return read_dict(d)
 
     PHASES = ["load", "decode", "hvac_pre", "solve_setup", "solve", "solve_epilogue", "post",
-              "observation", "occupancy", "reward", "bookkeeping", "store"]
+              "observation", "helper_wait", "auto_reset", "store"]
+    N_STAMPS = 20   # per env: 0..11 bound PHASES, 12..14 the HVAC pre sub-phases, 15..18 the helper's
 
     def phase_times(self) -> dict[str, tuple[float, float]]:
         """(mean, max) microseconds per kernel phase over workgroups, for one step."""
@@ -358,11 +359,13 @@ class VecEnv:
         return {self.PHASES[i]: (float(mean[i]), float(mx[i])) for i in range(n)}
 
     def phase_stamps(self) -> np.ndarray:
-        """Raw wall-clock stamps (n, 16) of one step; stamps 0..12 bound the phases."""
-        buf = np.zeros(self.n * 16, np.uint64)
+        """Raw wall-clock stamps (n, N_STAMPS) of one step: 0..11 bound PHASES on the
+        env's first wavefront; its helper wavefront stamps 15 (occupancy done),
+        16 (post-step state seen), 17 (reward done) and 18 (hand-off posted)."""
+        buf = np.zeros(self.n * self.N_STAMPS, np.uint64)
         if self.L.sbx_phase_stamps(self.envs, buf.ctypes.data_as(P), buf.size) < 0:
             raise RuntimeError("sbx_phase_stamps failed")
-        return buf.reshape(self.n, 16)
+        return buf.reshape(self.n, self.N_STAMPS)
 
     def pass_times(self, i: int) -> np.ndarray:
         """Shader-clock cycles of each solve pass of env i for one step."""
