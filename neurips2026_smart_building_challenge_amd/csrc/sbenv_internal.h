@@ -81,7 +81,9 @@ struct LdsLayout {
     int obsx;         // f64[OX_AHU + 4 * na] per-step values the observation reads (OX_*)
     int iscr;         // i32[W + 8] scan scratch
     int occn;         // u8[nz * nassign + nz] the helper's new chain states and zone counts
-    int sync;         // i32[SY_WORDS] hand-off flags of the env's two wavefronts
+    int hzq;          // f64[nz] the helper's zone means
+    int sync;         // i32[SY_WORDS] hand-off area of the env's two wavefronts
+    int stamps;       // u64[SBK_NSTAMP] phase stamps (phase timing only)
     int prec;         // int4[n_pass] solve pass records (copied at kernel start)
     int bytes;        // region size, 16-byte multiple
 };
@@ -272,9 +274,11 @@ struct EnvDesc {
 
 enum { KMODE_STEP = 0, KMODE_RESET = 1 };
 // Words of an env's hand-off area (LdsLayout::sync): flags posted by the first
-// wavefront (post-step state ready, observation written) and by the helper
-// (new occupancy, reward and bookkeeping done).
-enum { SY_POST = 0, SY_OBS = 1, SY_DONE = 2, SY_WORDS = 4 };
+// wavefront (state after the HVAC pre-step and boiler update ready, new field
+// ready) and by the helper (observation written, new occupancy committed,
+// reward half ready); the helper's reward half (4 f64 from SY_PART) and the
+// host log fields it read (2 f32 from SY_LOG).
+enum { SY_PRE = 0, SY_POST = 1, SY_HALF = 2, SY_PART = 4, SY_LOG = 12, SY_WORDS = 16 };
 
 // A workgroup's envs: order[first .. first + count) all of one layout, with
 // the layout's staging burst inputs (copied from its DevLayout so the burst

@@ -38,12 +38,14 @@ namespace sbk {
 
 enum { M_OFF = 0, M_HEAT = 1, M_COOL = 2, M_PASSIVE = 3 };
 
-// Phase stamp of env c.e (wall clock, written by its lane 0 when phase timing is on).
+// Phase stamp of env c.e (wall clock, taken by its lane 0 when phase timing is
+// on). Stamps go to the env's LDS area and are copied out by stamps_flush at
+// the end of the wavefront, so taking one adds no wait on global stores.
 // Stamps below SBK_STAMP_HELPER are the env's first wavefront's, the rest its helper's.
 #define STAMP(i)                                                                        \
     do {                                                                                \
         if (P.phase_ts && (threadIdx.x & 63) == 0 && c.helper == ((i) >= SBK_STAMP_HELPER)) \
-            P.phase_ts[(size_t)c.e * SBK_NSTAMP + (i)] = wall_clock64();                \
+            c.stamps[(i)] = wall_clock64();                                             \
     } while (0)
 
 // Orders this wavefront's LDS accesses before and after the point. A
@@ -342,6 +344,7 @@ struct Ctx {
     const SBK_C DevScen* S;
     int e;                   // env index
     bool helper;             // the env's second wavefront
+    unsigned long long* stamps;   // phase stamps (LDS)
     unsigned char* rec;      // HBM record of this env
     Tab t;
     double *T, *M, *damper, *reheat, *ratio, *heatsp, *coolsp, *dcmd, *rcmd, *sensing;
@@ -1769,7 +1772,7 @@ __device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
             for (int t = c.t.zone_cell_off()[z]; t < c.t.zone_cell_off()[z + 1]; t++) slots[c.t.zone_cells()[t]] = qz;
         }
         esync();
-        STAMP(4);
+        STAMP(5);
         unsigned long long* pts = (P.pass_ts && c.e == P.pass_ts_env && ln() == 0) ? P.pass_ts : nullptr;
         if constexpr (KV == KV_BLOCK) {
             if (L->rx_block == 2) relax_block_solve<2>(c, ambient, irr, pts);
@@ -1777,7 +1780,7 @@ __device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
         } else {
             relax_solve<W>(c, ambient, irr, pts);
         }
-        STAMP(5);
+        STAMP(6);
         return;
     } else {
     const int vb = L->vec_base;
@@ -1800,11 +1803,11 @@ __device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
         slots[vb + c.t.pos()[c.t.air_node()[col]]] += g * c.tair[col];
     }
     esync();
-    STAMP(4);
+    STAMP(5);
     // level schedule: LU of the permuted system, forward and backward solves
     unsigned long long* pts = (P.pass_ts && c.e == P.pass_ts_env && ln() == 0) ? P.pass_ts : nullptr;
     run_plan<W>(L, slots, reinterpret_cast<const int4*>(c.prec), pts);
-    STAMP(5);
+    STAMP(6);
     for (int t = ln(); t < n; t += W) {
         double y = slots[vb + c.t.pos()[t]];
         c.M[t] = c.M[t] * c.t.mret()[t] + c.t.mgain()[t] * y;
@@ -1854,7 +1857,7 @@ __device__ __forceinline__ void step_post(Ctx& c) {
 // VAV temperatures and areas of the reward's AHU terms (sb_reward.c:62-98)
 // into the register slots r = pass * U + u (VAV lane + 64 r).
 template <int U>
-__device__ __forceinline__ void reward_vavs(Ctx& c, int (&vahu)[SBK_VPL], double (&vv)[SBK_VPL][2]) {
+__device__ __forceinline__ void reward_vavs(Ctx& c, const double* zm, int (&vahu)[SBK_VPL], double (&vv)[SBK_VPL][2]) {
     const int nv = c.L->nv, lane = ln();
 #pragma unroll
     for (int pass = 0; pass < upasses<U>(); pass++) {
@@ -1870,7 +1873,7 @@ __device__ __forceinline__ void reward_vavs(Ctx& c, int (&vahu)[SBK_VPL], double
             v[u] = ok[u] ? vv0 : nv - 1;
             a[u] = c.t.vav_ahu()[v[u]];
         }
-        vav_temps<U>(c, c.zq, v, tv, area);
+        vav_temps<U>(c, zm, v, tv, area);
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int r = pass * U + u;
@@ -1885,16 +1888,21 @@ __device__ __forceinline__ void reward_vavs(Ctx& c, int (&vahu)[SBK_VPL], double
     }
 }
 
+// The reward is computed in two halves on the env's two wavefronts, each on
+// its own zone means of the post-step field: the AHU half (blower and cooling
+// power) and the rest (boiler gas, pump, occupant productivity), combined by
+// reward_combine in csim's order of operations.
+struct RewardPart {
+    double gas_rate, pump_e, total_occ, cum;
+};
+
+// AHU half (sb_reward.c:62-98): `zm` holds the zone means of the post-step
+// field. Returns blower (intake + exhaust) and cooling power.
 template <int W>
-__device__ __forceinline__ double reward(Ctx& c, const uint8_t* occ_v) {
+__device__ __forceinline__ void reward_ahu(Ctx& c, const double* zm, double& blower, double& cooling) {
     const SBK_C DevLayout* L = c.L;
     const SBK_C DevScen* S = c.S;
-    const double dt = S->dt_sec, inv_hour = 1.0 / 3600.0;
-    zone_means<W>(c, c.zq);
-    esync();
-    const double* rw = c.misc + MS_ROW;
-    const double ambient = rw[RW_AMB_J];
-    const int hour = (int)rw[RW_REW_HOUR_J], month = (int)rw[RW_REW_MONTH_J], wd = (int)rw[RW_REW_WORK_J];
+    const double ambient = c.misc[MS_ROW + RW_AMB_J];
     double tmean = 0.0;
     if (S->conv_tmean) {
         double s = 0.0;
@@ -1911,8 +1919,8 @@ __device__ __forceinline__ double reward(Ctx& c, const uint8_t* occ_v) {
         vahu[r] = -1;
         vv[r][0] = vv[r][1] = 0.0;
     }
-    if (L->nv > 64) reward_vavs<2>(c, vahu, vv);
-    else reward_vavs<1>(c, vahu, vv);
+    if (L->nv > 64) reward_vavs<2>(c, zm, vahu, vv);
+    else reward_vavs<1>(c, zm, vahu, vv);
     double sums[2];
     ahu_sums<2>(vahu, vv, L->na, sums);
     if (ln() < L->na) {
@@ -1929,16 +1937,29 @@ __device__ __forceinline__ double reward(Ctx& c, const uint8_t* occ_v) {
         c.fdsum[a] = flow * RHO_AIR * CP_AIR * (sat - mixed) / c.t.ahu_c()[a * 9 + 4];
     }
     esync();
-    double intake = 0.0, exhaust = 0.0, cooling = 0.0;
+    double intake = 0.0, exhaust = 0.0, cool = 0.0;
     for (int a = 0; a < L->na; a++) {
         intake += c.wsum[a];
         exhaust += c.atotal[a];
-        cooling += c.fdsum[a];
+        cool += c.fdsum[a];
     }
-    const double blower = intake + exhaust;
+    blower = intake + exhaust;
+    cooling = cool;
+}
+
+// The rest (sb_reward.c:12-29, :99-130): boiler gas rate (log(r2/c6)/c8 +
+// 1/c4/r2 precomputed on the host), pump power and the occupant productivity
+// sums over zones (`zm` zone means of the post-step field, `occ_v` the new
+// occupant counts).
+template <int W>
+__device__ __forceinline__ RewardPart reward_rest(Ctx& c, const double* zm, const uint8_t* occ_v) {
+    const SBK_C DevLayout* L = c.L;
+    const SBK_C DevScen* S = c.S;
+    const double dt = S->dt_sec, inv_hour = 1.0 / 3600.0;
+    const double* rw = c.misc + MS_ROW;
+    const double ambient = rw[RW_AMB_J];
     const double tf = total_flow_rate(c);
-    // boiler gas rate (sb_reward.c:12-29); log(r2/c6)/c8 + 1/c4/r2 from the host
-    double gas_rate;
+    RewardPart out;
     {
         const double* bc = S->boiler_c;
         double rwt = c.plant[PF_BOILER_RET];
@@ -1950,10 +1971,10 @@ __device__ __forceinline__ double reward(Ctx& c, const uint8_t* occ_v) {
         double tank = 0.0;
         if (dt > 0.0) tank = CP_W * RHO_W * bc[7] * c.plant[PF_BOILER_DSTEP] / dt;
         double tot = flow + diss + tank;
-        gas_rate = tot > 0.0 ? tot : 0.0;
+        out.gas_rate = tot > 0.0 ? tot : 0.0;
     }
-    const double pump_e = tf * RHO_W * GRAV * c.plant[PF_PUMP_HEAD] / S->pump_eff;
-    const double max_pph = S->rw[0], min_pph = S->rw[1], ref = S->rw[2];
+    out.pump_e = tf * RHO_W * GRAV * c.plant[PF_PUMP_HEAD] / S->pump_eff;
+    const double max_pph = S->rw[0], ref = S->rw[2];
     const double hsp = rw[RW_HSP_J], csp = rw[RW_CSP_J];
     double occ_part = 0.0, cum_part = 0.0;
     {
@@ -1968,7 +1989,7 @@ __device__ __forceinline__ double reward(Ctx& c, const uint8_t* occ_v) {
             ztv[r] = 0.0;
             if (64 * r < L->nz) {
                 occv[r] = (double)occ_v[zc];
-                ztv[r] = c.zq[zc];
+                ztv[r] = zm[zc];
             }
         }
 #pragma unroll
@@ -1986,13 +2007,26 @@ __device__ __forceinline__ double reward(Ctx& c, const uint8_t* occ_v) {
             }
         }
     }
-    double total_occ = occ_part, cum = cum_part;
-    wave_sum2(total_occ, cum);
+    wave_sum2(occ_part, cum_part);
+    out.total_occ = occ_part;
+    out.cum = cum_part;
+    return out;
+}
+
+// Normalised productivity, cost and carbon, and the weighted reward
+// (sb_reward.c:99-155).
+__device__ __forceinline__ double reward_combine(const Ctx& c, double blower, double cooling, const RewardPart& p) {
+    const SBK_C DevScen* S = c.S;
+    const double dt = S->dt_sec, inv_hour = 1.0 / 3600.0;
+    const double* rw = c.misc + MS_ROW;
+    const int hour = (int)rw[RW_REW_HOUR_J], month = (int)rw[RW_REW_MONTH_J], wd = (int)rw[RW_REW_WORK_J];
+    const double max_pph = S->rw[0], min_pph = S->rw[1];
+    const double total_occ = p.total_occ, cum = p.cum;
     const double max_prod = max_pph * total_occ * dt * inv_hour;
     const double min_prod = min_pph * total_occ * dt * inv_hour;
     double npr = 0.0;
     if (total_occ > 0.0 && (max_prod - min_prod) != 0.0) npr = (cum - min_prod) / (max_prod - min_prod) - 1.0;
-    const double elec_rate = blower + fabs(cooling) + pump_e;
+    const double elec_rate = blower + fabs(cooling) + p.pump_e;
     const double price = wd ? c.elec_wk[hour] : c.elec_we[hour];
     const double crate = c.elec_co2[hour];
     const double elec_cost = price * fabs(elec_rate) * dt;
@@ -2000,7 +2034,7 @@ __device__ __forceinline__ double reward(Ctx& c, const uint8_t* occ_v) {
     const double elec_carb = crate * fabs(elec_rate) * dt;
     const double elec_carb_max = crate * S->rw[3] * dt;
     const double gprice = c.gas_price[month - 1];
-    const double gg = gas_rate > 0.0 ? gas_rate : 0.0;
+    const double gg = p.gas_rate > 0.0 ? p.gas_rate : 0.0;
     const double gas_cost = gprice * gg * dt;
     const double gas_cost_max = gprice * S->rw[4] * dt;
     const double gas_carb = S->gas_co2 * gg * dt;
@@ -2047,6 +2081,15 @@ __device__ __forceinline__ void part_store(const uint4 (&r)[U], uint4* dst, int 
     }
 }
 
+// Copies this wavefront's phase stamps to the host-visible array.
+__device__ __forceinline__ void stamps_flush(const KParams& P, const Ctx& c) {
+    if (!P.phase_ts) return;
+    esync();
+    const int i = ln();
+    if (i < SBK_NSTAMP && c.helper == (i >= SBK_STAMP_HELPER))
+        P.phase_ts[(size_t)c.e * SBK_NSTAMP + i] = c.stamps[i];
+}
+
 // Cross-wavefront hand-off between an env's two wavefronts (same workgroup):
 // a workgroup-scope release waits for the wavefront's LDS operations
 // (lgkmcnt) before the flag is written, and the waiter polls the flag, so LDS
@@ -2061,72 +2104,56 @@ __device__ __forceinline__ void env_wait(int* flag, int v) {
         __builtin_amdgcn_s_sleep(1);
 }
 
-// The env's second wavefront during a step: the occupancy interval (exogenous:
-// it reads only the chain states, the MT stream and the calendar, so it runs
-// while the first wavefront decodes, runs the HVAC pre-step and solves), then
-// the reward once the post-step state is there (while the first wavefront
-// writes the observation), then, once the observation has read the old
-// counts, the new chain states and the bookkeeping of puf_step's tail
-// (pufferlib_cpu_env.h:243-256): reward and terminal, step counters, the
-// host-visible log. The host log fields are read first, so their latency
-// hides behind the occupancy work. Each wait is for a post the first
-// wavefront always makes.
+// The env's second wavefront during a step. The occupancy interval is
+// exogenous (it reads only the chain states, the MT stream and the calendar),
+// so it runs while the first wavefront decodes and runs the HVAC pre-step.
+// The observation reads nothing the field solve writes (the post-step boiler
+// update does not read the field either, so the first wavefront runs it before
+// the solve), so it is written while the first wavefront solves; the new chain
+// states are committed after it has read the old counts. Once the field is
+// there, the reward's non-AHU half (gas, pump, productivity) goes to the first
+// wavefront, which computes the AHU half meanwhile. The host log fields are
+// read first, so their latency hides behind the occupancy work. Each wait is
+// for a post the first wavefront always makes.
 template <int W>
-__device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, unsigned char* env, int max_steps) {
+__device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, unsigned char* env, float* obs_row) {
     const SBK_C DevLayout* L = c.L;
     const int nocc = L->nz * L->nassign;
-    const int e = c.e;
     // host-visible log fields (the trainer may clear them between steps)
-    Log* hlog = nullptr;
     float lg_ret = 0.f, lg_mean = 0.f;
     if (P.host_env && ln() == 0) {
-        hlog = reinterpret_cast<Log*>(reinterpret_cast<unsigned char*>(P.host_env) + (size_t)e * P.env_stride
-                                      + P.log_offset);
+        Log* hlog = reinterpret_cast<Log*>(reinterpret_cast<unsigned char*>(P.host_env) + (size_t)c.e * P.env_stride
+                                           + P.log_offset);
         lg_ret = __hip_atomic_load(&hlog->episode_return, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         lg_mean = __hip_atomic_load(&hlog->reward_mean, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
     uint8_t* st_new = env + L->lds.occn;
     uint8_t* v_new = st_new + nocc;
     occupancy_advance<W>(c, (int)c.misc[MS_ROW + RW_OCC_HOUR_J], (int)c.misc[MS_ROW + RW_OCC_WORK_J], st_new, v_new);
+    if (ln() == 0) {
+        float* lg = reinterpret_cast<float*>(sy + SY_LOG);
+        lg[0] = lg_ret;
+        lg[1] = lg_mean;
+    }
     STAMP(15);
-    env_wait(sy + SY_POST, 1);
-    STAMP(16);
-    const double rew = reward<W>(c, v_new);
-    STAMP(17);
-    env_wait(sy + SY_OBS, 1);
+    env_wait(sy + SY_PRE, 1);
+    write_obs<W>(c, obs_row, c.misc[MS_ROW + RW_AMB_J], c.misc + MS_AUX);
     for (int i = ln(); i < nocc; i += W) c.occ_state[i] = st_new[i];
     for (int z = ln(); z < L->nz; z += W) c.occV[z] = v_new[z];
-    if (ln() == 0) {
-        const float r = (float)rew;
-        const int step = c.ip[PI_STEP] + 1;
-        const int done = step >= max_steps;
-        P.rewards[e] = r * P.reward_scale;
-        P.terminals[e] = done ? 1.0f : 0.0f;
-        c.ip[PI_STEP] = step;
-        c.plant[PF_REW_SUM] += rew;
-        c.ip[PI_STEPS_TOTAL] += 1;
-        if (done) c.ip[PI_EPISODES] += 1;
-        if (hlog) {
-            float ret = lg_ret + r;
-            float mean = lg_mean + (r - lg_mean) / (float)step;
-            __hip_atomic_store(&hlog->episode_return, ret, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            __hip_atomic_store(&hlog->reward_mean, mean, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            if (done) {
-                float m = ret / (float)step;
-                float* lf = reinterpret_cast<float*>(hlog);
-                float perf = __hip_atomic_load(&lf[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                float score = __hip_atomic_load(&lf[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                float elen = __hip_atomic_load(&lf[3], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                float nn = __hip_atomic_load(&lf[5], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                __hip_atomic_store(&lf[0], perf + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                __hip_atomic_store(&lf[1], score + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                __hip_atomic_store(&lf[3], elen + (float)step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                __hip_atomic_store(&lf[5], nn + 1.0f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            }
-        }
-    }
-    env_post(sy + SY_DONE, 1);
+    STAMP(16);
+    env_wait(sy + SY_POST, 1);
+    STAMP(17);
+    double* hzq = reinterpret_cast<double*>(env + L->lds.hzq);
+    zone_means<W>(c, hzq);
+    esync();
+    const RewardPart part = reward_rest<W>(c, hzq, v_new);
+    if (ln() == 0) *reinterpret_cast<RewardPart*>(sy + SY_PART) = part;
+    // the observation row's stores are complete before the first wavefront
+    // may overwrite the row with an auto-reset observation
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    env_post(sy + SY_HALF, 1);
     STAMP(18);
+    stamps_flush(P, c);
 }
 
 // One workgroup per tile of E envs of one layout, two wavefronts per env:
@@ -2154,6 +2181,7 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
     c.rec = P.state + ed.state_off;
     unsigned char* env = lds + P.img_lds + slot * tl.lds_bytes;
     int* sy = reinterpret_cast<int*>(env + L->lds.sync);
+    c.stamps = reinterpret_cast<unsigned long long*>(env + L->lds.stamps);
     STAMP(0);
     {
         // one burst: the layout image (whole block, every thread), and per env
@@ -2230,7 +2258,7 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
     if (!active) return;
     const bool reset_mode = P.mode == KMODE_RESET;
     if (helper) {
-        if (!reset_mode) helper_step<W>(c, P, sy, env, ed.max_steps);
+        if (!reset_mode) helper_step<W>(c, P, sy, env, P.obs + (size_t)e * 1024);
         return;
     }
     STAMP(1);
@@ -2243,17 +2271,54 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
         STAMP(2);
         step_pre<W>(c, P);
         STAMP(3);
+        step_post<W>(c);             // boiler update: reads the pre-step results, not the field
+        env_post(sy + SY_PRE, 1);    // the helper's observation reads the state as of here
+        STAMP(4);
         field_step<W, KV>(c, P);
-        STAMP(6);
-        step_post<W>(c);
-        env_post(sy + SY_POST, 1);   // the helper's reward reads the post-step state
+        env_post(sy + SY_POST, 1);   // the helper's reward half reads the new field
         STAMP(7);
-        done = c.ip[PI_STEP] + 1 >= ed.max_steps;   // read before the helper advances the counter
-        write_obs<W>(c, obs_row, c.misc[MS_ROW + RW_AMB_J], c.misc + MS_AUX);
-        env_post(sy + SY_OBS, 1);    // the observation has read the old occupant counts
+        zone_means<W>(c, c.zq);
+        esync();
+        double blower, cooling;
+        reward_ahu<W>(c, c.zq, blower, cooling);
         STAMP(8);
-        env_wait(sy + SY_DONE, 1);   // new occupancy, reward and bookkeeping from the helper
+        env_wait(sy + SY_HALF, 1);   // the helper's reward half, observation and new occupancy
         STAMP(9);
+        const RewardPart part = *reinterpret_cast<const RewardPart*>(sy + SY_PART);
+        const double rew = reward_combine(c, blower, cooling, part);
+        const float r = (float)rew;
+        const int step = c.ip[PI_STEP] + 1;
+        done = step >= ed.max_steps;
+        if (ln() == 0) {
+            P.rewards[e] = r * P.reward_scale;
+            P.terminals[e] = done ? 1.0f : 0.0f;
+            c.ip[PI_STEP] = step;
+            c.plant[PF_REW_SUM] += rew;
+            c.ip[PI_STEPS_TOTAL] += 1;
+            if (done) c.ip[PI_EPISODES] += 1;
+            if (P.host_env) {
+                Log* hlog = reinterpret_cast<Log*>(reinterpret_cast<unsigned char*>(P.host_env)
+                                                   + (size_t)e * P.env_stride + P.log_offset);
+                const float* lg = reinterpret_cast<const float*>(sy + SY_LOG);
+                float ret = lg[0] + r;
+                float mean = lg[1] + (r - lg[1]) / (float)step;
+                __hip_atomic_store(&hlog->episode_return, ret, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                __hip_atomic_store(&hlog->reward_mean, mean, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                if (done) {
+                    float m = ret / (float)step;
+                    float* lf = reinterpret_cast<float*>(hlog);
+                    float perf = __hip_atomic_load(&lf[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    float score = __hip_atomic_load(&lf[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    float elen = __hip_atomic_load(&lf[3], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    float nn = __hip_atomic_load(&lf[5], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    __hip_atomic_store(&lf[0], perf + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    __hip_atomic_store(&lf[1], score + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    __hip_atomic_store(&lf[3], elen + (float)step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                    __hip_atomic_store(&lf[5], nn + 1.0f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+                }
+            }
+        }
+        esync();
     }
     if (reset_mode || done) {
         env_reset<W>(c, ed.start, obs_row);
@@ -2268,6 +2333,7 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
     STAMP(10);
     store16<W>(c.rec, env + L->lds.state, L->st.bytes);
     STAMP(11);
+    stamps_flush(P, c);
 }
 
 // Beta(2,2) action rows (see sbx_gen_actions in sbenv.h): the median of three

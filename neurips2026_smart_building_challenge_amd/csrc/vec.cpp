@@ -313,8 +313,11 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     l = align_up(l, 16);
     Ls.occn = l; l += nz * nassign + nz;
     l = align_up(l, 16);
+    Ls.hzq = l; l += 8 * nz;
+    l = align_up(l, 16);
     Ls.sync = l; l += 4 * sbk::SY_WORDS;
     l = align_up(l, 16);
+    Ls.stamps = l; l += 8 * SBK_NSTAMP;
     Ls.prec = l; l += 16 * D.n_pass;
     Ls.bytes = align_up(l, 16);
     D.bytes_per_step = 2.0 * S.bytes + 4.0 * (ncont + ndisc) + 4.0 * SB_OBS + 8.0;

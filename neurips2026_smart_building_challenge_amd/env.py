@@ -347,8 +347,8 @@ class VecEnv:
         self.L.puf_log(ctypes.byref(self.envs[i].log), ctypes.byref(d))
         return read_dict(d)
 
-    PHASES = ["load", "decode", "hvac_pre", "solve_setup", "solve", "solve_epilogue", "post",
-              "observation", "helper_wait", "auto_reset", "store"]
+    PHASES = ["load", "decode", "hvac_pre", "post", "solve_setup", "solve", "solve_epilogue", "reward_ahu",
+              "helper_wait", "bookkeeping_reset", "store"]
     N_STAMPS = 20   # per env: 0..11 bound PHASES, 12..14 the HVAC pre sub-phases, 15..18 the helper's
 
     def phase_times(self) -> dict[str, tuple[float, float]]:
@@ -361,7 +361,7 @@ class VecEnv:
     def phase_stamps(self) -> np.ndarray:
         """Raw wall-clock stamps (n, N_STAMPS) of one step: 0..11 bound PHASES on the
         env's first wavefront; its helper wavefront stamps 15 (occupancy done),
-        16 (post-step state seen), 17 (reward done) and 18 (hand-off posted)."""
+        16 (observation written), 17 (new field seen) and 18 (reward half posted)."""
         buf = np.zeros(self.n * self.N_STAMPS, np.uint64)
         if self.L.sbx_phase_stamps(self.envs, buf.ctypes.data_as(P), buf.size) < 0:
             raise RuntimeError("sbx_phase_stamps failed")
