@@ -2072,6 +2072,15 @@ __device__ __forceinline__ void part_load(uint4 (&r)[U], Src src, int n16, int t
     }
 }
 
+// Marks the loaded vectors as used here, so the compiler cannot sink each load
+// down to its (conditional) store and wait for it there: every load of the
+// round is issued before the first wait.
+template <int U>
+__device__ __forceinline__ void part_pin(uint4 (&r)[U]) {
+#pragma unroll
+    for (int u = 0; u < U; u++) asm volatile("" : "+v"(r[u].x), "+v"(r[u].y), "+v"(r[u].z), "+v"(r[u].w));
+}
+
 template <int U>
 __device__ __forceinline__ void part_store(const uint4 (&r)[U], uint4* dst, int n16, int tid, int nthr, int base) {
 #pragma unroll
@@ -2209,12 +2218,8 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
         // the step's calendar position, read from the record in HBM so the
         // calendar row loads (first wavefront) go out while the burst is in flight
         const bool rows = active && !helper && P.mode == KMODE_STEP;
-        int kk = 0, j1 = 0;
-        if (rows) {
-            const int* ipg = reinterpret_cast<const int*>(c.rec + tl.st_iplant);
-            kk = ipg[PI_STEP_INDEX];
-            j1 = ed.start + ipg[PI_STEP] + 1;
-        }
+        static_assert(PI_STEP == PI_STEP_INDEX + 1, "calendar index and step are adjacent i32s");
+        const int2 kst = *reinterpret_cast<const int2*>(c.rec + tl.st_iplant + 4 * PI_STEP_INDEX);
         {
             uint4 pi[UI], pr[UR], ps[US], pa[UA];
             part_load(pi, isrc, img16, tid, nthr, 0);
@@ -2223,14 +2228,23 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
             part_load(pa, asrc, act16, et, ET, 0);
             bind(c, lds, env);
             if (rows) {
-                const RowVals rv = row_issue<W>(c, __builtin_amdgcn_readfirstlane(kk),
-                                                __builtin_amdgcn_readfirstlane(j1));
+                const int kk = __builtin_amdgcn_readfirstlane(kst.x);
+                const int j1 = __builtin_amdgcn_readfirstlane(ed.start + kst.y + 1);
+                const RowVals rv = row_issue<W>(c, kk, j1);
+                part_pin(pi);
+                part_pin(pr);
+                part_pin(ps);
+                part_pin(pa);
                 part_store(pi, idst, img16, tid, nthr, 0);
                 part_store(pr, rdst, rec16, et, ET, 0);
                 part_store(ps, sdst, scn16, et, ET, 0);
                 part_store(pa, adst, act16, et, ET, 0);
                 row_store<W>(c, rv);
             } else {
+                part_pin(pi);
+                part_pin(pr);
+                part_pin(ps);
+                part_pin(pa);
                 part_store(pi, idst, img16, tid, nthr, 0);
                 part_store(pr, rdst, rec16, et, ET, 0);
                 part_store(ps, sdst, scn16, et, ET, 0);
@@ -2243,6 +2257,10 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
             part_load(pr, rsrc, rec16, et, ET, rd * UR * ET);
             part_load(ps, ssrc, scn16, et, ET, rd * US * ET);
             part_load(pa, asrc, act16, et, ET, rd * UA * ET);
+            part_pin(pi);
+            part_pin(pr);
+            part_pin(ps);
+            part_pin(pa);
             part_store(pi, idst, img16, tid, nthr, rd * UI * nthr);
             part_store(pr, rdst, rec16, et, ET, rd * UR * ET);
             part_store(ps, sdst, scn16, et, ET, rd * US * ET);
