@@ -17,7 +17,8 @@
 #define SBK_NAUX_MAX 16
 #define SBK_KMAX 48      // terms per lane per pass (matches the planner)
 #define SBK_NSTAMP 20        // phase stamps per env when phase timing is on
-#define SBK_STAMP_HELPER 15  // stamps from here on are the env's helper wavefront's
+#define SBK_STAMP_HELPER 15  // stamps 15..18 are the env's helper wavefront's
+#define SBK_STAMP_ENTRY 19   // the first wavefront's entry into the kernel
 #define SBK_VPL 4        // VAVs (and coupled columns) per lane: at most 256 per env
 #define SBK_RX_RPL 4     // relaxation rows per lane (matches the planner)
 #define SBK_RX_ROWS 256  // padded relaxation rows

@@ -38,13 +38,18 @@ namespace sbk {
 
 enum { M_OFF = 0, M_HEAT = 1, M_COOL = 2, M_PASSIVE = 3 };
 
+// Stamps SBK_STAMP_HELPER .. SBK_STAMP_ENTRY - 1 are the helper's.
+__device__ __forceinline__ constexpr bool stamp_is_helpers(int i) {
+    return i >= SBK_STAMP_HELPER && i < SBK_STAMP_ENTRY;
+}
+
 // Phase stamp of env c.e (wall clock, taken by its lane 0 when phase timing is
 // on). Stamps go to the env's LDS area and are copied out by stamps_flush at
 // the end of the wavefront, so taking one adds no wait on global stores.
 // Stamps below SBK_STAMP_HELPER are the env's first wavefront's, the rest its helper's.
 #define STAMP(i)                                                                        \
     do {                                                                                \
-        if (P.phase_ts && (threadIdx.x & 63) == 0 && c.helper == ((i) >= SBK_STAMP_HELPER)) \
+        if (P.phase_ts && (threadIdx.x & 63) == 0 && c.helper == stamp_is_helpers(i))     \
             c.stamps[(i)] = wall_clock64();                                             \
     } while (0)
 
@@ -744,8 +749,13 @@ __device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday,
             }
         }
         for (int i = ln(); i < SBK_MT_N; i += W) hbm_mt[i] = c.mt[i];
-        // a later draw of this kernel (the reset's second interval) reads these words back
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "agent");
+        // the only reader of these words within this kernel is this env's
+        // reset path (the reset's second interval), on a wavefront of this
+        // workgroup, after a hand-off or in program order: a workgroup-scope
+        // fence orders it (an agent-scope one would write back and invalidate
+        // the whole L2 of the XCD); later launches see the words across the
+        // kernel boundary
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
     }
     // apply the chain updates
 #pragma unroll
@@ -2095,7 +2105,7 @@ __device__ __forceinline__ void stamps_flush(const KParams& P, const Ctx& c) {
     if (!P.phase_ts) return;
     esync();
     const int i = ln();
-    if (i < SBK_NSTAMP && c.helper == (i >= SBK_STAMP_HELPER))
+    if (i < SBK_NSTAMP && c.helper == stamp_is_helpers(i))
         P.phase_ts[(size_t)c.e * SBK_NSTAMP + i] = c.stamps[i];
 }
 
@@ -2173,6 +2183,7 @@ template <int W, int KV>
 __global__ __launch_bounds__(512) void step_kernel(KParams P) {
     static_assert(W == 64, "one wavefront per env");
     extern __shared__ __align__(16) unsigned char lds[];
+    const unsigned long long t_entry = P.phase_ts ? wall_clock64() : 0ull;
     const Tile tl = P.tiles[blockIdx.x];
     const SBK_C DevLayout* L = P.layouts + tl.layout;
     const int E = (int)(blockDim.x >> 7);
@@ -2192,6 +2203,7 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
     int* sy = reinterpret_cast<int*>(env + L->lds.sync);
     c.stamps = reinterpret_cast<unsigned long long*>(env + L->lds.stamps);
     STAMP(0);
+    if (P.phase_ts && ln() == 0 && !helper) c.stamps[SBK_STAMP_ENTRY] = t_entry;
     {
         // one burst: the layout image (whole block, every thread), and per env
         // (its two wavefronts) its record image, its scenario image and its
