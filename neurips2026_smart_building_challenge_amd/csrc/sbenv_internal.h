@@ -276,10 +276,10 @@ struct EnvDesc {
 enum { KMODE_STEP = 0, KMODE_RESET = 1 };
 // Words of an env's hand-off area (LdsLayout::sync): flags posted by the first
 // wavefront (state after the HVAC pre-step and boiler update ready, new field
-// ready) and by the helper (observation written, new occupancy committed,
-// reward half ready); the helper's reward half (4 f64 from SY_PART) and the
-// host log fields it read (2 f32 from SY_LOG).
-enum { SY_PRE = 0, SY_POST = 1, SY_HALF = 2, SY_PART = 4, SY_LOG = 12, SY_WORDS = 16 };
+// ready) and by the helper (VAV sensed temperatures ready; observation
+// written, new occupancy committed and reward half ready); the helper's reward
+// half (4 f64 from SY_PART) and the host log fields it read (2 f32 from SY_LOG).
+enum { SY_PRE = 0, SY_POST = 1, SY_HALF = 2, SY_SENS = 3, SY_PART = 4, SY_LOG = 12, SY_WORDS = 16 };
 
 // A workgroup's envs: order[first .. first + count) all of one layout, with
 // the layout's staging burst inputs (copied from its DevLayout so the burst

@@ -64,13 +64,27 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 }
 
-// Lane of the calling thread within its env's wavefront (a workgroup holds one
-// wavefront per env).
+// Lane of the calling thread within its wavefront (a workgroup holds two
+// wavefronts per env).
 __device__ __forceinline__ int ln() { return (int)(threadIdx.x & 63); }
 
 // Synchronisation point of one env: its wavefront's LDS writes before this
 // point are visible to its LDS reads after it.
 __device__ __forceinline__ void esync() { wave_lds_sync(); }
+
+// Cross-wavefront hand-off between an env's two wavefronts (same workgroup):
+// a workgroup-scope release waits for the wavefront's LDS operations
+// (lgkmcnt) before the flag is written, and the waiter polls the flag, so LDS
+// data written before env_post is visible to LDS reads after env_wait.
+__device__ __forceinline__ void env_post(int* flag, int v) {
+    esync();
+    if (ln() == 0) __hip_atomic_store(flag, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__device__ __forceinline__ void env_wait(int* flag, int v) {
+    while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) < v)
+        __builtin_amdgcn_s_sleep(1);
+}
 
 // Wavefront reductions and scans on DPP lane moves (no LDS traffic). Every
 // lane of the wavefront must be active. The combination order is fixed:
@@ -560,6 +574,38 @@ __device__ __forceinline__ double vav_temp(const Ctx& c, const double* zmean, in
 // Values the observation reads besides the state (sb_obs.c:49-64 device
 // fields): per AHU the static pressure, delivered flow, flow fraction and
 // outside-air flow; the pump differential pressure; the row's ambient.
+// VAV sensed temperatures of the step (area-weighted zone means of the field
+// before the step, sb_sim.c:368-377), computed by the helper wavefront for
+// the first wavefront's VAV pass: the temperature goes to c.sensing, and
+// c.fdem (scratch until the coupled-column pass) holds the VAV's zone area,
+// whose sign says whether the VAV senses a zone at all.
+template <int U>
+__device__ __forceinline__ void vav_sensing(Ctx& c) {
+    const int nv = c.L->nv, lane = ln();
+#pragma unroll
+    for (int pass = 0; pass < upasses<U>(); pass++) {
+        const int base = pass * 64 * U;
+        if (base >= nv) break;
+        int v[U];
+        bool ok[U];
+        double tv[U], area[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int vv0 = base + 64 * u + lane;
+            ok[u] = vv0 < nv;
+            v[u] = ok[u] ? vv0 : nv - 1;
+        }
+        vav_temps<U>(c, c.zq, v, tv, area);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            if (ok[u]) {
+                c.sensing[v[u]] = tv[u];
+                c.fdem[v[u]] = area[u];
+            }
+        }
+    }
+}
+
 template <int W>
 __device__ __forceinline__ void obs_specials(Ctx& c, double amb) {
 #pragma clang fp contract(off)
@@ -1000,7 +1046,11 @@ __device__ __forceinline__ void vav_pass(Ctx& c, int comfort, double& ffs_part, 
             ok[u] = vv0 < nv;
             v[u] = ok[u] ? vv0 : nv - 1;
         }
-        vav_temps<U>(c, c.zq, v, tv, area);
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            tv[u] = c.sensing[v[u]];
+            area[u] = c.fdem[v[u]];
+        }
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const double* vc = c.t.vav_c() + v[u] * 9;
@@ -1050,7 +1100,6 @@ __device__ __forceinline__ void vav_pass(Ctx& c, int comfort, double& ffs_part, 
             double un = damper * vc0[u] * sqrt(st / vc4[u]);
             un = un > 0.00001 ? un : 0.00001;
             if (ok[u]) {
-                c.sensing[v[u]] = sensing;
                 if (live) {
                     c.heatsp[v[u]] = hsp;
                     c.coolsp[v[u]] = csp;
@@ -1222,15 +1271,16 @@ __device__ __forceinline__ void zone_heat(Ctx& c, double wpc) {
 }
 
 template <int W>
-__device__ __forceinline__ void step_pre(Ctx& c, const KParams& P) {
+__device__ __forceinline__ void step_pre(Ctx& c, const KParams& P, int* sy) {
     const SBK_C DevLayout* L = c.L;
     const SBK_C DevScen* S = c.S;
     const double* rw = c.misc + MS_ROW;
     const double ambient = rw[RW_AMB_K];
     const int comfort = (rw[RW_COMF_K] != 0.0);
     const int na = L->na, nv = L->nv;
-    zone_means<W>(c, c.zq);
-    esync();
+    // the zone means and VAV sensed temperatures come from the helper
+    // wavefront, which computes them while this one decodes the actions
+    env_wait(sy + SY_SENS, 1);
     STAMP(12);
     // AHU return-air means and supply temperatures (sb_sim.c:382-387, :253-265):
     // flow-factor sum over all VAVs, then one lane per AHU sums over its VAVs
@@ -2109,19 +2159,6 @@ __device__ __forceinline__ void stamps_flush(const KParams& P, const Ctx& c) {
         P.phase_ts[(size_t)c.e * SBK_NSTAMP + i] = c.stamps[i];
 }
 
-// Cross-wavefront hand-off between an env's two wavefronts (same workgroup):
-// a workgroup-scope release waits for the wavefront's LDS operations
-// (lgkmcnt) before the flag is written, and the waiter polls the flag, so LDS
-// data written before env_post is visible to LDS reads after env_wait.
-__device__ __forceinline__ void env_post(int* flag, int v) {
-    esync();
-    if (ln() == 0) __hip_atomic_store(flag, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-
-__device__ __forceinline__ void env_wait(int* flag, int v) {
-    while (__builtin_amdgcn_readfirstlane(__hip_atomic_load(flag, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP)) < v)
-        __builtin_amdgcn_s_sleep(1);
-}
 
 // The env's second wavefront during a step. The occupancy interval is
 // exogenous (it reads only the chain states, the MT stream and the calendar),
@@ -2146,6 +2183,13 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
         lg_ret = __hip_atomic_load(&hlog->episode_return, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         lg_mean = __hip_atomic_load(&hlog->reward_mean, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
+    // zone means and VAV sensed temperatures of the field before the step,
+    // while the first wavefront decodes the actions
+    zone_means<W>(c, c.zq);
+    esync();
+    if (L->nv > 64) vav_sensing<2>(c);
+    else vav_sensing<1>(c);
+    env_post(sy + SY_SENS, 1);
     uint8_t* st_new = env + L->lds.occn;
     uint8_t* v_new = st_new + nocc;
     occupancy_advance<W>(c, (int)c.misc[MS_ROW + RW_OCC_HOUR_J], (int)c.misc[MS_ROW + RW_OCC_WORK_J], st_new, v_new);
@@ -2299,7 +2343,7 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
     if (!reset_mode) {
         decode_apply<W>(c);
         STAMP(2);
-        step_pre<W>(c, P);
+        step_pre<W>(c, P, sy);
         STAMP(3);
         step_post<W>(c);             // boiler update: reads the pre-step results, not the field
         env_post(sy + SY_PRE, 1);    // the helper's observation reads the state as of here
