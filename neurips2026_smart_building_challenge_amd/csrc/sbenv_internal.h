@@ -40,6 +40,9 @@ struct StateLayout {
     int damper, reheat, ratio, heatsp, coolsp, dcmd, rcmd, sensing;  // [nv]
     int recirc, sat, fan, flow;                 // [na]
     int plant;                                  // f64[8], see PF_*
+    int cal, cal_n;                             // f64[2][cal_n]: a step's calendar values (RW_*, then
+                                                // the aux-time row), in section (calendar index & 1),
+                                                // prefetched by the step before (or the reset)
     // i32 arrays
     int run, coolreq;                           // [na]
     int iplant;                                 // i32[8], see PI_*
@@ -127,11 +130,8 @@ struct ScenImg {
     int gas_price;    // f64[12]
 };
 
-// misc scratch (f64[48]): step scalars, then the step's calendar values (rows
-// kk = the index before the step and j = kk + 1; RW_* offsets from MS_ROW),
-// then the aux-time row j (MS_AUX, n_aux - 1 values)
-enum { MS_FFS = 0, MS_TOTAL_REHEAT, MS_TF, MS_REWARD, MS_COMFORT, MS_AMB, MS_CMIN, MS_CMAX,
-       MS_ROW = 8, MS_AUX = 24, MS_SIZE = 48 };
+// misc scratch (f64[MS_SIZE]): step scalars
+enum { MS_FFS = 0, MS_TOTAL_REHEAT, MS_TF, MS_REWARD, MS_COMFORT, MS_AMB, MS_CMIN, MS_CMAX, MS_SIZE };
 // Observation field source, resolved on the host: a value at a byte offset of
 // the env's LDS region (state image, obsx values) or of the layout image.
 #define OBS_SRC_IMG (1u << 31)   // offset into the layout image (else the env region)
@@ -152,6 +152,8 @@ enum { ACT_CLAMP = 1, ACT_PUMP_HEAD = 2 };
 // a at OX_AHU + 4a: static pressure, delivered flow, flow fraction, outside-air flow
 enum { OX_AMB = 0, OX_DP = 1, OX_AHU = 2 };
 
+// A step's calendar values (StateLayout::cal): rows kk = the calendar index
+// before the step and j = kk + 1 (RW_*), then the aux-time row j.
 enum { RW_AMB_K = 0, RW_SOLAR_K, RW_COMF_K, RW_COMF_KM1, RW_HSP_K, RW_CSP_K, RW_AMB_J, RW_HSP_J, RW_CSP_J,
        RW_OCC_HOUR_J, RW_OCC_WORK_J, RW_REW_HOUR_J, RW_REW_MONTH_J, RW_REW_WORK_J, RW_COUNT };
 

@@ -372,6 +372,8 @@ struct Ctx {
     uint8_t *mode, *prev_valid, *dcmd_set, *rcmd_set, *occ_state, *occV;
     double *slots, *zq, *unres, *fdem, *rwen, *g, *tair;
     double *wsum, *atotal, *satv, *demand, *fdsum, *red, *misc;
+    double* cal;             // the two calendar sections of the state image
+    const double* row;       // this step's calendar values (RW_*), the aux-time row after them
     uint32_t* mt;
     int* iscr;
     unsigned char* prec;     // LDS copy of the solve pass records
@@ -408,6 +410,7 @@ __device__ __forceinline__ void bind(Ctx& c, const unsigned char* img, unsigned 
     c.fan = (double*)(s + st.fan);
     c.flow = (double*)(s + st.flow);
     c.plant = (double*)(s + st.plant);
+    c.cal = (double*)(s + st.cal);
     c.run = (int*)(s + st.run);
     c.coolreq = (int*)(s + st.coolreq);
     c.ip = (int*)(s + st.iplant);
@@ -839,6 +842,54 @@ __device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday,
     esync();
 }
 
+// ------------------------------------------------------------------ step
+// A step's calendar values (row kk before the step, kk - 1 for the comfort
+// transition, row j = kk + 1 after it) and aux-time row j. row_issue only
+// issues the loads; row_store puts them in a calendar section of the state
+// image. The host guarantees j < n1 for every step of an episode.
+struct RowVals {
+    double v[RW_COUNT];
+    double aux;
+};
+
+template <int W>
+__device__ __forceinline__ RowVals row_issue(const Ctx& c, int kk, int j) {
+    const SBK_C DevScen* S = c.S;
+    const int naux = c.L->n_aux - 1;
+    const int km1 = kk > 0 ? kk - 1 : 0;
+    RowVals r;
+    r.v[RW_AMB_K] = S->amb[kk];
+    r.v[RW_SOLAR_K] = S->solar_i[kk];
+    r.v[RW_COMF_K] = S->comfort[kk];
+    r.v[RW_COMF_KM1] = kk > 0 ? S->comfort[km1] : 0.0;
+    r.v[RW_HSP_K] = S->heat_sp[kk];
+    r.v[RW_CSP_K] = S->cool_sp[kk];
+    r.v[RW_AMB_J] = S->amb[j];
+    r.v[RW_HSP_J] = S->heat_sp[j];
+    r.v[RW_CSP_J] = S->cool_sp[j];
+    r.v[RW_OCC_HOUR_J] = (double)S->occ_hour[j];
+    r.v[RW_OCC_WORK_J] = (double)S->occ_work[j];
+    r.v[RW_REW_HOUR_J] = (double)S->rew_hour[j];
+    r.v[RW_REW_MONTH_J] = (double)S->rew_month[j];
+    r.v[RW_REW_WORK_J] = (double)S->rew_work[j];
+    const int l = ln();
+    r.aux = naux > 0 ? S->aux_time[(size_t)j * naux + (l < naux ? l : 0)] : 0.0;
+    return r;
+}
+
+template <int W>
+__device__ __forceinline__ void row_store(Ctx& c, const RowVals& r, double* dst) {
+    const int l = ln();
+    if (l == 0) {
+#pragma unroll
+        for (int i = 0; i < RW_COUNT; i++) dst[i] = r.v[i];
+    }
+    if (l < c.L->n_aux - 1) dst[RW_COUNT + l] = r.aux;
+}
+
+// The calendar section of calendar index kk.
+__device__ __forceinline__ double* cal_section(const Ctx& c, int kk) { return c.cal + (kk & 1) * c.L->st.cal_n; }
+
 // ------------------------------------------------------------------ reset
 // sb_sim_reset (sb_sim.c:177-218) on the LDS image; pump head is not reset.
 template <int W>
@@ -897,6 +948,7 @@ __device__ __forceinline__ void sim_reset(Ctx& c, int start) {
 template <int W>
 __device__ __forceinline__ void env_reset(Ctx& c, int start, float* obs_row) {
     const SBK_C DevScen* S = c.S;
+    const RowVals first = row_issue<W>(c, start, start + 1);   // the new episode's first step
     sim_reset<W>(c, start);
     // two occupancy intervals around the first observation; one loop body so
     // the (large) occupancy code is emitted once here
@@ -906,52 +958,10 @@ __device__ __forceinline__ void env_reset(Ctx& c, int start, float* obs_row) {
                              k == 0 ? S->work_m1[start] : S->occ_work[start], c.occ_state, c.occV);
         if (k == 0) write_obs<W>(c, obs_row, S->amb[start], S->aux_time + (size_t)start * (c.L->n_aux - 1));
     }
+    row_store<W>(c, first, cal_section(c, start));
+    esync();
 }
 
-// ------------------------------------------------------------------ step
-// The step's calendar values (row kk before the step, kk - 1 for the comfort
-// transition, row j = kk + 1 after it) and aux-time row j. row_issue only
-// issues the loads (the kernel overlaps them with the staging burst);
-// row_store puts them in the env's scratch. The host guarantees j < n1.
-struct RowVals {
-    double v[RW_COUNT];
-    double aux;
-};
-
-template <int W>
-__device__ __forceinline__ RowVals row_issue(const Ctx& c, int kk, int j) {
-    const SBK_C DevScen* S = c.S;
-    const int naux = c.L->n_aux - 1;
-    const int km1 = kk > 0 ? kk - 1 : 0;
-    RowVals r;
-    r.v[RW_AMB_K] = S->amb[kk];
-    r.v[RW_SOLAR_K] = S->solar_i[kk];
-    r.v[RW_COMF_K] = S->comfort[kk];
-    r.v[RW_COMF_KM1] = kk > 0 ? S->comfort[km1] : 0.0;
-    r.v[RW_HSP_K] = S->heat_sp[kk];
-    r.v[RW_CSP_K] = S->cool_sp[kk];
-    r.v[RW_AMB_J] = S->amb[j];
-    r.v[RW_HSP_J] = S->heat_sp[j];
-    r.v[RW_CSP_J] = S->cool_sp[j];
-    r.v[RW_OCC_HOUR_J] = (double)S->occ_hour[j];
-    r.v[RW_OCC_WORK_J] = (double)S->occ_work[j];
-    r.v[RW_REW_HOUR_J] = (double)S->rew_hour[j];
-    r.v[RW_REW_MONTH_J] = (double)S->rew_month[j];
-    r.v[RW_REW_WORK_J] = (double)S->rew_work[j];
-    const int l = ln();
-    r.aux = naux > 0 ? S->aux_time[(size_t)j * naux + (l < naux ? l : 0)] : 0.0;
-    return r;
-}
-
-template <int W>
-__device__ __forceinline__ void row_store(Ctx& c, const RowVals& r) {
-    const int l = ln();
-    if (l == 0) {
-#pragma unroll
-        for (int i = 0; i < RW_COUNT; i++) c.misc[MS_ROW + i] = r.v[i];
-    }
-    if (l < c.L->n_aux - 1) c.misc[MS_AUX + l] = r.aux;
-}
 
 // Action decode and apply (sb_sim.c:557-576, :220-244): continuous actions
 // clamp to [-1, 1] and map through float32 (min, max) spans, discrete ones map
@@ -1029,7 +1039,7 @@ template <int U>
 __device__ __forceinline__ void vav_pass(Ctx& c, int comfort, double& ffs_part, int (&vahu)[SBK_VPL],
                                          double (&vv)[SBK_VPL][3]) {
     const int nv = c.L->nv, lane = ln();
-    const double* rw = c.misc + MS_ROW;
+    const double* rw = c.row;
     const double hsp = rw[RW_HSP_K], csp = rw[RW_CSP_K];
     const bool comf_km1 = rw[RW_COMF_KM1] != 0.0;
 #pragma unroll
@@ -1274,7 +1284,7 @@ template <int W>
 __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P, int* sy) {
     const SBK_C DevLayout* L = c.L;
     const SBK_C DevScen* S = c.S;
-    const double* rw = c.misc + MS_ROW;
+    const double* rw = c.row;
     const double ambient = rw[RW_AMB_K];
     const int comfort = (rw[RW_COMF_K] != 0.0);
     const int na = L->na, nv = L->nv;
@@ -1821,8 +1831,8 @@ template <int W, int KV>
 __device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
     const SBK_C DevLayout* L = c.L;
     const SBK_C DevScen* S = c.S;
-    const double ambient = c.misc[MS_ROW + RW_AMB_K];
-    const double irr = c.misc[MS_ROW + RW_SOLAR_K];
+    const double ambient = c.row[RW_AMB_K];
+    const double irr = c.row[RW_SOLAR_K];
     const int n = L->n;
     double* slots = c.slots;
     if constexpr (KV != KV_LU) {
@@ -1962,7 +1972,7 @@ template <int W>
 __device__ __forceinline__ void reward_ahu(Ctx& c, const double* zm, double& blower, double& cooling) {
     const SBK_C DevLayout* L = c.L;
     const SBK_C DevScen* S = c.S;
-    const double ambient = c.misc[MS_ROW + RW_AMB_J];
+    const double ambient = c.row[RW_AMB_J];
     double tmean = 0.0;
     if (S->conv_tmean) {
         double s = 0.0;
@@ -2016,7 +2026,7 @@ __device__ __forceinline__ RewardPart reward_rest(Ctx& c, const double* zm, cons
     const SBK_C DevLayout* L = c.L;
     const SBK_C DevScen* S = c.S;
     const double dt = S->dt_sec, inv_hour = 1.0 / 3600.0;
-    const double* rw = c.misc + MS_ROW;
+    const double* rw = c.row;
     const double ambient = rw[RW_AMB_J];
     const double tf = total_flow_rate(c);
     RewardPart out;
@@ -2078,7 +2088,7 @@ __device__ __forceinline__ RewardPart reward_rest(Ctx& c, const double* zm, cons
 __device__ __forceinline__ double reward_combine(const Ctx& c, double blower, double cooling, const RewardPart& p) {
     const SBK_C DevScen* S = c.S;
     const double dt = S->dt_sec, inv_hour = 1.0 / 3600.0;
-    const double* rw = c.misc + MS_ROW;
+    const double* rw = c.row;
     const int hour = (int)rw[RW_REW_HOUR_J], month = (int)rw[RW_REW_MONTH_J], wd = (int)rw[RW_REW_WORK_J];
     const double max_pph = S->rw[0], min_pph = S->rw[1];
     const double total_occ = p.total_occ, cum = p.cum;
@@ -2172,9 +2182,11 @@ __device__ __forceinline__ void stamps_flush(const KParams& P, const Ctx& c) {
 // read first, so their latency hides behind the occupancy work. Each wait is
 // for a post the first wavefront always makes.
 template <int W>
-__device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, unsigned char* env, float* obs_row) {
+__device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, unsigned char* env, float* obs_row,
+                                            int kk, int j) {
     const SBK_C DevLayout* L = c.L;
     const int nocc = L->nz * L->nassign;
+
     // host-visible log fields (the trainer may clear them between steps)
     float lg_ret = 0.f, lg_mean = 0.f;
     if (P.host_env && ln() == 0) {
@@ -2192,15 +2204,25 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
     env_post(sy + SY_SENS, 1);
     uint8_t* st_new = env + L->lds.occn;
     uint8_t* v_new = st_new + nocc;
-    occupancy_advance<W>(c, (int)c.misc[MS_ROW + RW_OCC_HOUR_J], (int)c.misc[MS_ROW + RW_OCC_WORK_J], st_new, v_new);
+    occupancy_advance<W>(c, (int)c.row[RW_OCC_HOUR_J], (int)c.row[RW_OCC_WORK_J], st_new, v_new);
     if (ln() == 0) {
         float* lg = reinterpret_cast<float*>(sy + SY_LOG);
         lg[0] = lg_ret;
         lg[1] = lg_mean;
     }
     STAMP(15);
-    env_wait(sy + SY_PRE, 1);
-    write_obs<W>(c, obs_row, c.misc[MS_ROW + RW_AMB_J], c.misc + MS_AUX);
+    {
+        // the next step's calendar values (rows kk + 1 and j + 1) into the
+        // other calendar section of the state image, loaded while this
+        // wavefront waits for the pre-step state; after the last step of an
+        // episode the reset path writes the new episode's own, so clamping to
+        // the tables is enough there
+        const int n1 = c.S->n1;
+        const RowVals next = row_issue<W>(c, min(kk + 1, n1 - 1), min(j + 1, n1 - 1));
+        env_wait(sy + SY_PRE, 1);
+        row_store<W>(c, next, cal_section(c, kk + 1));
+    }
+    write_obs<W>(c, obs_row, c.row[RW_AMB_J], c.row + RW_COUNT);
     for (int i = ln(); i < nocc; i += W) c.occ_state[i] = st_new[i];
     for (int z = ln(); z < L->nz; z += W) c.occV[z] = v_new[z];
     STAMP(16);
@@ -2271,11 +2293,6 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
         uint4* adst = reinterpret_cast<uint4*>(env + tl.lds_act);
         const int rounds = max(max((img16 + UI * nthr - 1) / (UI * nthr), (rec16 + UR * ET - 1) / (UR * ET)),
                                max((scn16 + US * ET - 1) / (US * ET), (act16 + UA * ET - 1) / (UA * ET)));
-        // the step's calendar position, read from the record in HBM so the
-        // calendar row loads (first wavefront) go out while the burst is in flight
-        const bool rows = active && !helper && P.mode == KMODE_STEP;
-        static_assert(PI_STEP == PI_STEP_INDEX + 1, "calendar index and step are adjacent i32s");
-        const int2 kst = *reinterpret_cast<const int2*>(c.rec + tl.st_iplant + 4 * PI_STEP_INDEX);
         {
             uint4 pi[UI], pr[UR], ps[US], pa[UA];
             part_load(pi, isrc, img16, tid, nthr, 0);
@@ -2283,29 +2300,14 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
             part_load(ps, ssrc, scn16, et, ET, 0);
             part_load(pa, asrc, act16, et, ET, 0);
             bind(c, lds, env);
-            if (rows) {
-                const int kk = __builtin_amdgcn_readfirstlane(kst.x);
-                const int j1 = __builtin_amdgcn_readfirstlane(ed.start + kst.y + 1);
-                const RowVals rv = row_issue<W>(c, kk, j1);
-                part_pin(pi);
-                part_pin(pr);
-                part_pin(ps);
-                part_pin(pa);
-                part_store(pi, idst, img16, tid, nthr, 0);
-                part_store(pr, rdst, rec16, et, ET, 0);
-                part_store(ps, sdst, scn16, et, ET, 0);
-                part_store(pa, adst, act16, et, ET, 0);
-                row_store<W>(c, rv);
-            } else {
-                part_pin(pi);
-                part_pin(pr);
-                part_pin(ps);
-                part_pin(pa);
-                part_store(pi, idst, img16, tid, nthr, 0);
-                part_store(pr, rdst, rec16, et, ET, 0);
-                part_store(ps, sdst, scn16, et, ET, 0);
-                part_store(pa, adst, act16, et, ET, 0);
-            }
+            part_pin(pi);
+            part_pin(pr);
+            part_pin(ps);
+            part_pin(pa);
+            part_store(pi, idst, img16, tid, nthr, 0);
+            part_store(pr, rdst, rec16, et, ET, 0);
+            part_store(ps, sdst, scn16, et, ET, 0);
+            part_store(pa, adst, act16, et, ET, 0);
         }
         for (int rd = 1; rd < rounds; rd++) {
             uint4 pi[UI], pr[UR], ps[US], pa[UA];
@@ -2322,7 +2324,7 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
             part_store(ps, sdst, scn16, et, ET, rd * US * ET);
             part_store(pa, adst, act16, et, ET, rd * UA * ET);
         }
-        if (rows) {
+        if (active && !helper && P.mode == KMODE_STEP) {
             const SBK_C uint4* src = reinterpret_cast<const SBK_C uint4*>(L->pinfo);
             for (int i = ln(); i < L->n_pass; i += W) reinterpret_cast<uint4*>(c.prec)[i] = src[i];
         }
@@ -2331,8 +2333,12 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
     __syncthreads();   // the only workgroup barrier: the layout image is shared
     if (!active) return;
     const bool reset_mode = P.mode == KMODE_RESET;
+    // the step's calendar index and step count, read before either wavefront
+    // changes them (the first one advances the index after SY_SENS)
+    const int kk0 = c.ip[PI_STEP_INDEX], st0 = c.ip[PI_STEP];
+    c.row = cal_section(c, kk0);
     if (helper) {
-        if (!reset_mode) helper_step<W>(c, P, sy, env, P.obs + (size_t)e * 1024);
+        if (!reset_mode) helper_step<W>(c, P, sy, env, P.obs + (size_t)e * 1024, kk0, ed.start + st0 + 1);
         return;
     }
     STAMP(1);

@@ -285,6 +285,8 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     S.coolsp = f64a(nv); S.dcmd = f64a(nv); S.rcmd = f64a(nv); S.sensing = f64a(nv);
     S.recirc = f64a(na); S.sat = f64a(na); S.fan = f64a(na); S.flow = f64a(na);
     S.plant = f64a(8);
+    S.cal_n = sbk::RW_COUNT + std::max(n_aux - 1, 0);
+    S.cal = f64a(2 * S.cal_n);
     S.run = o; o += 4 * na; S.coolreq = o; o += 4 * na; S.iplant = o; o += 32;
     S.mode = o; o += nv; S.prev_valid = o; o += nv; S.dcmd_set = o; o += nv; S.rcmd_set = o; o += nv;
     S.occ_state = o; o += nz * nassign; S.occV = o; o += nz;
@@ -320,7 +322,9 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     Ls.stamps = l; l += 8 * SBK_NSTAMP;
     Ls.prec = l; l += 16 * D.n_pass;
     Ls.bytes = align_up(l, 16);
-    D.bytes_per_step = 2.0 * S.bytes + 4.0 * (ncont + ndisc) + 4.0 * SB_OBS + 8.0;
+    // algorithmic bytes: the state image without the calendar prefetch, which
+    // is a copy of shared per-scenario tables
+    D.bytes_per_step = 2.0 * (S.bytes - 16.0 * S.cal_n) + 4.0 * (ncont + ndisc) + 4.0 * SB_OBS + 8.0;
     D.solve_flops = 2.0 * (double)P.n_pairs + (double)P.n_divs;
     if (use_block) {   // per sweep: off-block multiply-subtracts, then each block's inverse applied
         long long nnz = 0, dense = 0;
