@@ -16,9 +16,9 @@
 #define SBK_MT_N 624
 #define SBK_NAUX_MAX 16
 #define SBK_KMAX 48      // terms per lane per pass (matches the planner)
-#define SBK_NSTAMP 20        // phase stamps per env when phase timing is on
+#define SBK_NSTAMP 32        // phase stamps per env when phase timing is on
 #define SBK_STAMP_HELPER 15  // stamps 15..18 are the env's helper wavefront's
-#define SBK_STAMP_ENTRY 19   // the first wavefront's entry into the kernel
+#define SBK_STAMP_ENTRY 19   // the first wavefront's entry into the kernel (20.. finer stamps of its HVAC pre-step)
 #define SBK_VPL 4        // VAVs (and coupled columns) per lane: at most 256 per env
 #define SBK_RX_RPL 4     // relaxation rows per lane (matches the planner)
 #define SBK_RX_ROWS 256  // padded relaxation rows
@@ -278,10 +278,11 @@ struct EnvDesc {
 enum { KMODE_STEP = 0, KMODE_RESET = 1 };
 // Words of an env's hand-off area (LdsLayout::sync): flags posted by the first
 // wavefront (state after the HVAC pre-step and boiler update ready, new field
-// ready) and by the helper (VAV sensed temperatures ready; observation
+// ready) and by the helper (VAV sensed temperatures ready; AHU return-air
+// sums ready; observation
 // written, new occupancy committed and reward half ready); the helper's reward
 // half (4 f64 from SY_PART) and the host log fields it read (2 f32 from SY_LOG).
-enum { SY_PRE = 0, SY_POST = 1, SY_HALF = 2, SY_SENS = 3, SY_PART = 4, SY_LOG = 12, SY_WORDS = 16 };
+enum { SY_PRE = 0, SY_POST = 1, SY_HALF = 2, SY_SENS = 3, SY_PART = 4, SY_LOG = 12, SY_RET = 14, SY_WORDS = 16 };
 
 // A workgroup's envs: order[first .. first + count) all of one layout, with
 // the layout's staging burst inputs (copied from its DevLayout so the burst

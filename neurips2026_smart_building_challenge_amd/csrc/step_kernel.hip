@@ -228,7 +228,7 @@ __device__ __forceinline__ void wave_sum_n(double (&x)[N]) {
 // Per-AHU sums of NV per-lane values, Q AHUs (a0 .. a0 + Q - 1) per pass with
 // their reductions interleaved; lane l receives the sums of AHU l in mine[]
 // (lanes l outside the pass keep what they had).
-template <int NV, int Q>
+template <int NV, int Q, int R>
 __device__ __forceinline__ void ahu_sums_pass(const int (&key)[SBK_VPL], const double (&vals)[SBK_VPL][NV], int a0,
                                               double (&mine)[NV]) {
     double x[Q * NV];
@@ -238,7 +238,7 @@ __device__ __forceinline__ void ahu_sums_pass(const int (&key)[SBK_VPL], const d
         for (int k = 0; k < NV; k++) {
             double acc = 0.0;
 #pragma unroll
-            for (int r = 0; r < SBK_VPL; r++) acc += key[r] == a0 + q ? vals[r][k] : 0.0;
+            for (int r = 0; r < R; r++) acc += key[r] == a0 + q ? vals[r][k] : 0.0;
             x[q * NV + k] = acc;
         }
     }
@@ -252,26 +252,35 @@ __device__ __forceinline__ void ahu_sums_pass(const int (&key)[SBK_VPL], const d
 }
 
 // Per-AHU sums of NV per-lane values: lane a < na receives in mine[k] the
-// wavefront's sum of vals[r][k] over the slots r with key[r] == a. Every lane
-// of the wavefront must be active.
-template <int NV>
-__device__ __forceinline__ void ahu_sums(const int (&key)[SBK_VPL], const double (&vals)[SBK_VPL][NV], int na,
-                                         double (&mine)[NV]) {
+// wavefront's sum of vals[r][k] over the slots r < R with key[r] == a (the
+// slots past R must not hold keys). Every lane of the wavefront must be active.
+template <int NV, int R>
+__device__ __forceinline__ void ahu_sums_r(const int (&key)[SBK_VPL], const double (&vals)[SBK_VPL][NV], int na,
+                                           double (&mine)[NV]) {
 #pragma unroll
     for (int k = 0; k < NV; k++) mine[k] = 0.0;
     for (int a0 = 0; a0 < na;) {
         const int left = na - a0;
         if (left >= 3) {
-            ahu_sums_pass<NV, 4>(key, vals, a0, mine);
+            ahu_sums_pass<NV, 4, R>(key, vals, a0, mine);
             a0 += 4;
         } else if (left == 2) {
-            ahu_sums_pass<NV, 2>(key, vals, a0, mine);
+            ahu_sums_pass<NV, 2, R>(key, vals, a0, mine);
             a0 += 2;
         } else {
-            ahu_sums_pass<NV, 1>(key, vals, a0, mine);
+            ahu_sums_pass<NV, 1, R>(key, vals, a0, mine);
             a0 += 1;
         }
     }
+}
+
+// ahu_sums_r over every register slot (`items`, the VAV or column count, is
+// not used to trim them: one instantiation keeps the code small).
+template <int NV>
+__device__ __forceinline__ void ahu_sums(const int (&key)[SBK_VPL], const double (&vals)[SBK_VPL][NV], int na,
+                                         int items, double (&mine)[NV]) {
+    (void)items;
+    ahu_sums_r<NV, SBK_VPL>(key, vals, na, mine);
 }
 
 // Inclusive prefix sum over the wavefront.
@@ -582,21 +591,25 @@ __device__ __forceinline__ double vav_temp(const Ctx& c, const double* zmean, in
 // the first wavefront's VAV pass: the temperature goes to c.sensing, and
 // c.fdem (scratch until the coupled-column pass) holds the VAV's zone area,
 // whose sign says whether the VAV senses a zone at all.
+// The VAVs' terms of their AHU's return-air mean go to the register slots
+// r = pass * U + u: key vahu[r], values sensing * area and area (VAV area > 0).
 template <int U>
-__device__ __forceinline__ void vav_sensing(Ctx& c) {
+__device__ __forceinline__ void vav_sensing(Ctx& c, int (&vahu)[SBK_VPL], double (&vv)[SBK_VPL][2]) {
     const int nv = c.L->nv, lane = ln();
 #pragma unroll
     for (int pass = 0; pass < upasses<U>(); pass++) {
         const int base = pass * 64 * U;
         if (base >= nv) break;
-        int v[U];
+        int v[U], a[U];
         bool ok[U];
-        double tv[U], area[U];
+        double tv[U], area[U], varea[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int vv0 = base + 64 * u + lane;
             ok[u] = vv0 < nv;
             v[u] = ok[u] ? vv0 : nv - 1;
+            a[u] = c.t.vav_ahu()[v[u]];
+            varea[u] = c.t.vav_area()[v[u]];
         }
         vav_temps<U>(c, c.zq, v, tv, area);
 #pragma unroll
@@ -604,6 +617,12 @@ __device__ __forceinline__ void vav_sensing(Ctx& c) {
             if (ok[u]) {
                 c.sensing[v[u]] = tv[u];
                 c.fdem[v[u]] = area[u];
+                const int r = pass * U + u;
+                vahu[r] = a[u];
+                if (varea[u] > 0.0) {
+                    vv[r][0] = tv[u] * varea[u];
+                    vv[r][1] = varea[u];
+                }
             }
         }
     }
@@ -1037,7 +1056,7 @@ __device__ __forceinline__ void decode_apply(Ctx& c) {
 // U VAVs per lane per pass, all loads of a pass before any store.
 template <int U>
 __device__ __forceinline__ void vav_pass(Ctx& c, int comfort, double& ffs_part, int (&vahu)[SBK_VPL],
-                                         double (&vv)[SBK_VPL][3]) {
+                                         double (&vv)[SBK_VPL][1]) {
     const int nv = c.L->nv, lane = ln();
     const double* rw = c.row;
     const double hsp = rw[RW_HSP_K], csp = rw[RW_CSP_K];
@@ -1122,11 +1141,7 @@ __device__ __forceinline__ void vav_pass(Ctx& c, int comfort, double& ffs_part, 
                 ffs_part += reheat * vc1[u];
                 const int r = pass * U + u;
                 vahu[r] = a[u];
-                vv[r][2] = un;
-                if (varea[u] > 0.0) {
-                    vv[r][0] = sensing * varea[u];
-                    vv[r][1] = varea[u];
-                }
+                vv[r][0] = un;
             }
         }
     }
@@ -1305,21 +1320,24 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P, int* sy) {
     // this lane's VAVs (v = lane + 64 r) kept in registers for the AHU sums
     double ffs_part = 0.0;
     int vahu[SBK_VPL];
-    double vv[SBK_VPL][3];   // sensing * area, area (zone area > 0 only), unrestricted flow
+    double vv[SBK_VPL][1];   // unrestricted flow
 #pragma unroll
     for (int r = 0; r < SBK_VPL; r++) {
         vahu[r] = -1;
-        vv[r][0] = vv[r][1] = vv[r][2] = 0.0;
+        vv[r][0] = 0.0;
     }
     if (nv > 64) vav_pass<2>(c, comfort, ffs_part, vahu, vv);
     else vav_pass<1>(c, comfort, ffs_part, vahu, vv);
     STAMP(13);
     const double ffs = bsum<W>(ffs_part, c.red);
-    double sums[3];
-    ahu_sums<3>(vahu, vv, na, sums);
+    STAMP(20);
+    double sums[1];
+    ahu_sums<1>(vahu, vv, na, nv, sums);
+    env_wait(sy + SY_RET, 1);   // the helper's return-air sums
+    STAMP(21);
     if (ln() < na) {
         const int a = ln();
-        const double ws = sums[0], at = sums[1], dm = sums[2];
+        const double ws = c.wsum[a], at = c.atotal[a], dm = sums[0];
         double rt = (at > 0.0) ? ws / at : tmean;
         double mixed = c.recirc[a] * rt + (1.0 - c.recirc[a]) * ambient;
         c.satv[a] = (mixed > c.sat[a] && c.run[a] == 1) ? c.sat[a] : mixed;
@@ -1367,10 +1385,13 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P, int* sy) {
     }
     if (L->k > 64) coupled_columns<2>(c, ffs, tf, iwt, total_rw, cmin, cmax, cahu, cfd);
     else coupled_columns<1>(c, ffs, tf, iwt, total_rw, cmin, cmax, cahu, cfd);
+    STAMP(22);
     wave_sum_min_max(total_rw, cmin, cmax);
+    STAMP(23);
     // AHU flow (clamped to the AHU's maximum) and cooling requests
     double fsum[2];
-    ahu_sums<2>(cahu, cfd, na, fsum);
+    ahu_sums<2>(cahu, cfd, na, L->k, fsum);
+    STAMP(24);
     if (ln() < na) {
         const int a = ln();
         const double f = fsum[0], cnt = fsum[1];
@@ -1389,6 +1410,7 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P, int* sy) {
     // zone heat: reheat share, internal and occupant gains (sb_sim.c:420-447)
     const double frac = comfort ? 1.0 : S->standby_frac;
     const double wpc = S->internal_w_m2 * S->cv_area * frac;
+    STAMP(25);
     if (L->nz > 64) zone_heat<2>(c, wpc);
     else zone_heat<1>(c, wpc);
     esync();
@@ -1992,7 +2014,7 @@ __device__ __forceinline__ void reward_ahu(Ctx& c, const double* zm, double& blo
     if (L->nv > 64) reward_vavs<2>(c, zm, vahu, vv);
     else reward_vavs<1>(c, zm, vahu, vv);
     double sums[2];
-    ahu_sums<2>(vahu, vv, L->na, sums);
+    ahu_sums<2>(vahu, vv, L->na, L->nv, sums);
     if (ln() < L->na) {
         const int a = ln();
         const double ws = sums[0], at = sums[1];
@@ -2199,9 +2221,28 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
     // while the first wavefront decodes the actions
     zone_means<W>(c, c.zq);
     esync();
-    if (L->nv > 64) vav_sensing<2>(c);
-    else vav_sensing<1>(c);
-    env_post(sy + SY_SENS, 1);
+    {
+        int vahu[SBK_VPL];
+        double vv[SBK_VPL][2];
+#pragma unroll
+        for (int r = 0; r < SBK_VPL; r++) {
+            vahu[r] = -1;
+            vv[r][0] = vv[r][1] = 0.0;
+        }
+        if (L->nv > 64) vav_sensing<2>(c, vahu, vv);
+        else vav_sensing<1>(c, vahu, vv);
+        env_post(sy + SY_SENS, 1);
+        // each AHU's return-air sums over its VAVs (sb_sim.c:382-387), for the
+        // first wavefront's supply temperatures (c.wsum / c.atotal: reward
+        // scratch, free until then)
+        double sums[2];
+        ahu_sums<2>(vahu, vv, L->na, L->nv, sums);
+        if (ln() < L->na) {
+            c.wsum[ln()] = sums[0];
+            c.atotal[ln()] = sums[1];
+        }
+        env_post(sy + SY_RET, 1);
+    }
     uint8_t* st_new = env + L->lds.occn;
     uint8_t* v_new = st_new + nocc;
     occupancy_advance<W>(c, (int)c.row[RW_OCC_HOUR_J], (int)c.row[RW_OCC_WORK_J], st_new, v_new);

@@ -349,7 +349,7 @@ class VecEnv:
 
     PHASES = ["load", "decode", "hvac_pre", "post", "solve_setup", "solve", "solve_epilogue", "reward_ahu",
               "helper_wait", "bookkeeping_reset", "store"]
-    N_STAMPS = 20   # per env: 0..11 bound PHASES, 12..14 the HVAC pre sub-phases, 15..18 the helper's
+    N_STAMPS = 32   # per env: 0..11 bound PHASES, 12..14 and 20..25 HVAC pre sub-phases, 15..18 the helper's, 19 entry
 
     def phase_times(self) -> dict[str, tuple[float, float]]:
         """(mean, max) microseconds per kernel phase over workgroups, for one step."""
