@@ -2201,22 +2201,16 @@ __device__ __forceinline__ void stamps_flush(const KParams& P, const Ctx& c) {
 // states are committed after it has read the old counts. Once the field is
 // there, the reward's non-AHU half (gas, pump, productivity) goes to the first
 // wavefront, which computes the AHU half meanwhile. The host log fields are
-// read first, so their latency hides behind the occupancy work. Each wait is
-// for a post the first wavefront always makes.
+// read over the host link after the wavefront's last other global load has been
+// issued (loads complete in issue order, so a wait for an earlier load never
+// waits for them), while it waits for the pre-step state; they are used only at
+// the end. Each wait is for a post the first wavefront always makes.
 template <int W>
 __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, unsigned char* env, float* obs_row,
                                             int kk, int j) {
     const SBK_C DevLayout* L = c.L;
     const int nocc = L->nz * L->nassign;
 
-    // host-visible log fields (the trainer may clear them between steps)
-    float lg_ret = 0.f, lg_mean = 0.f;
-    if (P.host_env && ln() == 0) {
-        Log* hlog = reinterpret_cast<Log*>(reinterpret_cast<unsigned char*>(P.host_env) + (size_t)c.e * P.env_stride
-                                           + P.log_offset);
-        lg_ret = __hip_atomic_load(&hlog->episode_return, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        lg_mean = __hip_atomic_load(&hlog->reward_mean, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    }
     // zone means and VAV sensed temperatures of the field before the step,
     // while the first wavefront decodes the actions
     zone_means<W>(c, c.zq);
@@ -2246,12 +2240,9 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
     uint8_t* st_new = env + L->lds.occn;
     uint8_t* v_new = st_new + nocc;
     occupancy_advance<W>(c, (int)c.row[RW_OCC_HOUR_J], (int)c.row[RW_OCC_WORK_J], st_new, v_new);
-    if (ln() == 0) {
-        float* lg = reinterpret_cast<float*>(sy + SY_LOG);
-        lg[0] = lg_ret;
-        lg[1] = lg_mean;
-    }
     STAMP(15);
+    // host-visible log fields (the trainer may clear them between steps)
+    float lg_ret = 0.f, lg_mean = 0.f;
     {
         // the next step's calendar values (rows kk + 1 and j + 1) into the
         // other calendar section of the state image, loaded while this
@@ -2260,6 +2251,12 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
         // the tables is enough there
         const int n1 = c.S->n1;
         const RowVals next = row_issue<W>(c, min(kk + 1, n1 - 1), min(j + 1, n1 - 1));
+        if (P.host_env && ln() == 0) {
+            Log* hlog = reinterpret_cast<Log*>(reinterpret_cast<unsigned char*>(P.host_env)
+                                               + (size_t)c.e * P.env_stride + P.log_offset);
+            lg_ret = __hip_atomic_load(&hlog->episode_return, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            lg_mean = __hip_atomic_load(&hlog->reward_mean, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        }
         env_wait(sy + SY_PRE, 1);
         row_store<W>(c, next, cal_section(c, kk + 1));
     }
@@ -2273,7 +2270,12 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
     zone_means<W>(c, hzq);
     esync();
     const RewardPart part = reward_rest<W>(c, hzq, v_new);
-    if (ln() == 0) *reinterpret_cast<RewardPart*>(sy + SY_PART) = part;
+    if (ln() == 0) {
+        *reinterpret_cast<RewardPart*>(sy + SY_PART) = part;
+        float* lg = reinterpret_cast<float*>(sy + SY_LOG);
+        lg[0] = lg_ret;
+        lg[1] = lg_mean;
+    }
     // the observation row's stores are complete before the first wavefront
     // may overwrite the row with an auto-reset observation
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
