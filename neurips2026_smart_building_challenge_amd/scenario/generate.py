@@ -131,8 +131,51 @@ def layout(spec: LayoutSpec) -> tuple[Building, dict]:
     return _LAYOUT_CACHE[key]
 
 
+@dataclass(frozen=True)
+class ConvSpec:
+    """Stochastic convection (complete_port/csim/sb_convect.c:39-73): each step,
+    every cell of a convection room starts a swap with probability p with one of
+    its candidates (cells of the same room within `distance` grid columns; -1:
+    the whole room); the swaps are shuffled and applied to the field."""
+    p: float = 0.05
+    distance: int = 2
+    seed: int = 9001
+
+    @property
+    def tag(self) -> str:
+        return f"cv{int(round(self.p * 1000)):03d}d{self.distance}"
+
+
+def conv_tables(b: Building, distance: int):
+    """Convection rooms of a synthetic layout: the zones of one grid row of one
+    floor form an open-plan strip, and a strip's room cells are its zones' air
+    cells (grid row 0, column z) in column order. Tables in the reference
+    baker's form (complete_port/pysim/bake_scenario.py:162-186): room offsets
+    into the cell list, cells as (row, col), and per cell a CSR list of its
+    candidates as cell positions in that list."""
+    rooms: dict[tuple[int, int], list[tuple[int, int]]] = {}
+    for z in range(b.n_zones):
+        fl, r, c = (int(x) for x in b.zone_pos[z])
+        rooms.setdefault((fl, r), []).append((c, z))
+    off, cells, cand_off, cand_idx = [0], [], [], []
+    for key in sorted(rooms):
+        strip = sorted(rooms[key])
+        base = len(cells)
+        for c, z in strip:
+            cells.append((0, z))
+        off.append(len(cells))
+        for i, (c, _) in enumerate(strip):
+            cand_off.append(len(cand_idx))
+            for j, (c2, _) in enumerate(strip):
+                if j != i and (distance < 0 or abs(c2 - c) <= distance):
+                    cand_idx.append(base + j)
+    cand_off.append(len(cand_idx))
+    return (np.asarray(off, np.int64), np.asarray(cells, np.int64).reshape(-1),
+            np.asarray(cand_off, np.int64), np.asarray(cand_idx, np.int64))
+
+
 def scenario_writer(spec: LayoutSpec, clim: ClimateSpec, table_steps: int,
-                    occ_seed: int) -> SbbWriter:
+                    occ_seed: int, conv: ConvSpec | None = None) -> SbbWriter:
     b, f = layout(spec)
     Z, A, N = b.n_zones, b.n_ahu, b.n_nodes
     n1 = table_steps + 1
@@ -185,14 +228,24 @@ def scenario_writer(spec: LayoutSpec, clim: ClimateSpec, table_steps: int,
     w.add("air_side_sensed_indptr", ind, "i32")
     w.add("air_side_sensed_indices", np.arange(k), "i32")
     w.add("air_side_sensed_data", np.ones(k), "f64")
-    # ---- convection: present but off ----
-    w.scalar_f64("conv_p", 0.0)
-    w.scalar_f64("conv_distance", 0.0)
-    w.scalar_i64("conv_seed", 0)
-    w.add("conv_room_offsets", [0], "i32")
-    w.add("conv_room_cells", np.zeros(0), "i32")
-    w.add("conv_cand_offsets", [0], "i32")
-    w.add("conv_cand_idx", np.zeros(0), "i32")
+    # ---- convection: off (the BASELINE configs), or on with open-plan strips ----
+    if conv is None:
+        w.scalar_f64("conv_p", 0.0)
+        w.scalar_f64("conv_distance", 0.0)
+        w.scalar_i64("conv_seed", 0)
+        w.add("conv_room_offsets", [0], "i32")
+        w.add("conv_room_cells", np.zeros(0), "i32")
+        w.add("conv_cand_offsets", [0], "i32")
+        w.add("conv_cand_idx", np.zeros(0), "i32")
+    else:
+        c_off, c_cells, c_coff, c_idx = conv_tables(b, conv.distance)
+        w.scalar_f64("conv_p", conv.p)
+        w.scalar_f64("conv_distance", float(conv.distance))
+        w.scalar_i64("conv_seed", conv.seed)
+        w.add("conv_room_offsets", c_off, "i32")
+        w.add("conv_room_cells", c_cells, "i32")
+        w.add("conv_cand_offsets", c_coff, "i32")
+        w.add("conv_cand_idx", c_idx, "i32")
     # ---- zones / rooms / VAVs ----
     w.add("zone_area", b.zone_area, "f64")
     w.add("phys_room_idx", np.arange(Z), "i32")
@@ -282,14 +335,19 @@ def config_scenarios(config: int) -> tuple[list[tuple[LayoutSpec, ClimateSpec]],
 
 
 def write_scenarios(scen: list[tuple[LayoutSpec, ClimateSpec]], out_dir,
-                    table_steps: int = 2 * EPISODE_STEPS, occ_seed_base: int = 17321) -> list[Path]:
+                    table_steps: int = 2 * EPISODE_STEPS, occ_seed_base: int = 17321,
+                    conv: ConvSpec | None = None) -> list[Path]:
+    """Writes one blob per scenario; with `conv`, every blob has stochastic
+    convection on (scenario i gets conv seed conv.seed + 7 i)."""
     out = Path(out_dir)
     out.mkdir(parents=True, exist_ok=True)
     paths = []
     for i, (l, c) in enumerate(scen):
-        p = out / f"{l.name}__{c.name}.sbb"
+        cv = None if conv is None else ConvSpec(conv.p, conv.distance, conv.seed + 7 * i)
+        tag = "" if conv is None else "__" + conv.tag
+        p = out / f"{l.name}__{c.name}{tag}.sbb"
         if not p.exists():
-            scenario_writer(l, c, table_steps, occ_seed_base + 101 * i).write(p)
+            scenario_writer(l, c, table_steps, occ_seed_base + 101 * i, cv).write(p)
         paths.append(p)
     meta = {"scenarios": [p.name for p in paths], "table_steps": table_steps,
             "episode_steps": EPISODE_STEPS}
@@ -297,6 +355,6 @@ def write_scenarios(scen: list[tuple[LayoutSpec, ClimateSpec]], out_dir,
     return paths
 
 
-def write_config(config: int, out_dir) -> tuple[list[Path], int, bool]:
+def write_config(config: int, out_dir, conv: ConvSpec | None = None) -> tuple[list[Path], int, bool]:
     scen, n, desync = config_scenarios(config)
-    return write_scenarios(scen, out_dir), n, desync
+    return write_scenarios(scen, out_dir, conv=conv), n, desync

@@ -34,7 +34,7 @@ class _Lib:
         L = self.lib
         if prefix == "ref":
             L.ref_open.restype = P
-            L.ref_open.argtypes = [ctypes.c_char_p, ctypes.c_uint32, ctypes.c_int, ctypes.c_int]
+            L.ref_open.argtypes = [ctypes.c_char_p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int, ctypes.c_int]
             self.open_fn = L.ref_open
             self.close_fn = L.ref_close
             self.reset_fn, self.step_fn, self.state_fn = L.ref_reset, L.ref_step, L.ref_state
@@ -52,7 +52,7 @@ class _Lib:
             L.sbo_scen_open.argtypes = [P, ctypes.c_char_p]
             L.sbo_scen_close.argtypes = [P]
             L.sbo_env_new.restype = P
-            L.sbo_env_new.argtypes = [P, ctypes.c_uint32, ctypes.c_int, ctypes.c_int]
+            L.sbo_env_new.argtypes = [P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int, ctypes.c_int]
             self.close_fn = L.sbo_env_free
             self.reset_fn, self.step_fn, self.state_fn = L.sbo_env_reset, L.sbo_env_step, L.sbo_env_state
             self.batch_fn = L.sbo_run_batch
@@ -67,6 +67,8 @@ class _Lib:
             L.sbo_mt_u32.restype = ctypes.c_uint32
             L.sbo_mt_double.argtypes = [P]
             L.sbo_mt_double.restype = ctypes.c_double
+            L.sbo_mt_interval.argtypes = [P, ctypes.c_uint32]
+            L.sbo_mt_interval.restype = ctypes.c_uint32
         self.close_fn.argtypes = [P]
         self.reset_fn.argtypes = [P, P]
         self.step_fn.argtypes = [P, P, P, P, P]
@@ -124,19 +126,40 @@ def scenario(path) -> _Scen:
     return _SCEN_CACHE[key]
 
 
+_SEEDS: dict[str, tuple[int, int]] = {}
+
+
+def default_conv_seed(path, occ_seed: int) -> int:
+    """The convection stream seed of the env whose occupancy seed is occ_seed:
+    the blob's conv_seed offset by the env's index within its scenario (the
+    GPU vec seeds env j of a scenario with occ_seed + j and conv_seed + j)."""
+    key = str(path)
+    if key not in _SEEDS:
+        from neurips2026_smart_building_challenge_amd.scenario.sbb import read_sbb
+
+        b = read_sbb(path)
+        _SEEDS[key] = (int(b["occ_seed"][0]), int(b["conv_seed"][0]))
+    occ0, conv0 = _SEEDS[key]
+    return (conv0 + int(occ_seed) - occ0) & 0xFFFFFFFF
+
+
 class CpuEnv:
     """One env of either oracle, stepping with the reference CPU env protocol."""
 
-    def __init__(self, kind: str, path, occ_seed: int, start: int = 0, max_steps: int = 8640):
+    def __init__(self, kind: str, path, occ_seed: int, start: int = 0, max_steps: int = 8640,
+                 conv_seed: int | None = None):
         self.kind = kind
         self.L = lib(kind)
+        if conv_seed is None:
+            conv_seed = default_conv_seed(path, occ_seed)
         if kind == "ref":
-            self.h = self.L.open_fn(str(path).encode(), occ_seed, start, max_steps)
+            self.h = self.L.open_fn(str(path).encode(), occ_seed, conv_seed, start, max_steps)
             self.n_cont = self.L.lib.ref_n_cont(self.h)
             self.n_disc = self.L.lib.ref_n_disc(self.h)
         else:
             self.scen = scenario(path)
-            self.h = self.L.lib.sbo_env_new(ctypes.addressof(self.scen.buf), occ_seed, start, max_steps)
+            self.h = self.L.lib.sbo_env_new(ctypes.addressof(self.scen.buf), occ_seed, conv_seed, start,
+                                            max_steps)
             if self.h:
                 self.n_cont = self.L.lib.sbo_env_n_cont(self.h)
                 self.n_disc = self.L.lib.sbo_env_n_disc(self.h)

@@ -63,7 +63,7 @@ static void write_obs(RefEnv* e, int j, float* out) {
     if (out) memcpy(out, e->obs, sizeof(float) * SB_OBS);
 }
 
-RefEnv* ref_open(const char* path, uint32_t occ_seed, int start, int max_steps) {
+RefEnv* ref_open(const char* path, uint32_t occ_seed, uint32_t conv_seed, int start, int max_steps) {
     RefEnv* e = (RefEnv*)calloc(1, sizeof(RefEnv));
     if (!e) return NULL;
     if (sb_open(&e->blob, path) != 0) { free(e); return NULL; }
@@ -75,6 +75,7 @@ RefEnv* ref_open(const char* path, uint32_t occ_seed, int start, int max_steps) 
         return NULL;
     }
     sb_rng_seed(&e->occ.rng, occ_seed);
+    sb_rng_seed(&e->conv.rng, conv_seed);
     e->is_disc = sb_u8(&e->blob, "act_is_discrete");
     e->n_act = e->sim.n_action;
     for (int i = 0; i < e->n_act; i++) {

@@ -91,6 +91,11 @@ typedef struct {
     double gas_co2;
     uint8_t* is_room;
     int episode_steps;
+    /* stochastic convection (sb_convect.h); off when conv_p == 0 or conv_dist == 0 */
+    double conv_p;
+    int conv_dist, cv_rooms, cv_max_room;
+    int64_t conv_seed;
+    const int32_t *cv_off, *cv_cells, *cv_coff, *cv_cidx;
 } SboScen;
 
 int sbo_scen_open(SboScen* s, const char* path);
@@ -123,6 +128,9 @@ typedef struct {
     uint8_t* occ_state;
     double* occV;
     SboMt mt;
+    /* convection stream and swap lists */
+    SboMt cmt;
+    int *cv_left, *cv_right;
     /* scratch */
     double *rhs, *y, *yr, *r, *work, *power, *mat;
     /* bookkeeping (pufferlib_cpu_env.h Env) */
@@ -134,7 +142,7 @@ typedef struct {
     float obs[SBO_OBS];
 } SboEnv;
 
-SboEnv* sbo_env_new(const SboScen* sc, uint32_t occ_seed, int start, int max_steps);
+SboEnv* sbo_env_new(const SboScen* sc, uint32_t occ_seed, uint32_t conv_seed, int start, int max_steps);
 void sbo_env_free(SboEnv* e);
 void sbo_env_reset(SboEnv* e, float* obs_out);
 int sbo_env_step(SboEnv* e, const float* actions, float* obs_out, float* reward, float* terminal);
@@ -149,6 +157,8 @@ void sbo_env_log(const SboEnv* e, float* out);
 void sbo_mt_seed(SboMt* r, uint32_t seed);
 uint32_t sbo_mt_u32(SboMt* r);
 double sbo_mt_double(SboMt* r);
+uint32_t sbo_mt_interval(SboMt* r, uint32_t max);
+void sbo_conv_apply(const SboScen* sc, SboMt* r, int* left, int* right, double* temp);
 void sbo_decode(const SboScen* sc, const double* cont, const double* disc, double* native);
 void sbo_lu_solve(const SboScen* sc, const double* b, double* x, double* work);
 int sbo_dense_solve(int k, double* M, double* b);

@@ -58,6 +58,61 @@ double sbo_mt_double(SboMt* r) {
     return (a * 67108864.0 + b) / 9007199254740992.0;
 }
 
+/* Uniform integer in [0, max] by masked rejection (numpy's legacy
+ * rk_interval); complete_port/csim/sb_rng.c:45-54. */
+uint32_t sbo_mt_interval(SboMt* r, uint32_t max) {
+    if (max == 0) return 0;
+    uint32_t mask = max;
+    mask |= mask >> 1;
+    mask |= mask >> 2;
+    mask |= mask >> 4;
+    mask |= mask >> 8;
+    mask |= mask >> 16;
+    uint32_t v;
+    do {
+        v = sbo_mt_u32(r) & mask;
+    } while (v > max);
+    return v;
+}
+
+/* ------------------------------------------------------------ convection */
+/* sb_conv_apply, complete_port/csim/sb_convect.c:39-73: per room, every cell
+ * draws u and, when u <= p and it has candidates, picks one of them; the
+ * (cell, candidate) pairs are shuffled by Fisher-Yates from the last pair
+ * down and the temperatures of each pair are swapped in that order. */
+void sbo_conv_apply(const SboScen* s, SboMt* r, int* left, int* right, double* temp) {
+    if (s->conv_p == 0.0 || s->conv_dist == 0) return;
+    for (int rm = 0; rm < s->cv_rooms; rm++) {
+        const int base = s->cv_off[rm], n = s->cv_off[rm + 1] - base;
+        int m = 0;
+        for (int j = 0; j < n; j++) {
+            if (sbo_mt_double(r) > s->conv_p) continue;
+            const int cg = base + j, c0 = s->cv_coff[cg], c1 = s->cv_coff[cg + 1];
+            if (c1 <= c0) continue;
+            left[m] = cg;
+            right[m] = s->cv_cidx[c0 + (int)sbo_mt_interval(r, (uint32_t)(c1 - c0 - 1))];
+            m++;
+        }
+        for (int t = m - 1; t > 0; t--) {
+            const int j2 = (int)sbo_mt_interval(r, (uint32_t)t);
+            int x = left[t];
+            left[t] = left[j2];
+            left[j2] = x;
+            x = right[t];
+            right[t] = right[j2];
+            right[j2] = x;
+        }
+        for (int t = 0; t < m; t++) {
+            const int a = left[t], b = right[t];
+            const int ia = s->cv_cells[2 * a] * s->nc + s->cv_cells[2 * a + 1];
+            const int ib = s->cv_cells[2 * b] * s->nc + s->cv_cells[2 * b + 1];
+            const double held = temp[ia];
+            temp[ia] = temp[ib];
+            temp[ib] = held;
+        }
+    }
+}
+
 /* ------------------------------------------------------------ LU replay */
 /* complete_port/csim/sb_lu.c:5-33 (diagonal lookup, inverse row perm) */
 static int lu_prepare(SboScen* s) {
@@ -267,9 +322,20 @@ int sbo_scen_open(SboScen* s, const char* path) {
     for (int rm = 0; rm < s->n_rooms; rm++)
         for (int t = s->room_off[rm]; t < s->room_off[rm + 1]; t++)
             s->is_room[s->room_cells[2 * t] * s->nc + s->room_cells[2 * t + 1]] = 1;
-    if (sbo_f64_1(b, "conv_p", 0.0) != 0.0) {
-        fprintf(stderr, "sbo: convection (conv_p > 0) is outside the oracle's scope\n");
-        return -1;
+    /* convection tables (sb_convect.c:6-31) */
+    s->conv_p = sbo_f64_1(b, "conv_p", 0.0);
+    s->conv_dist = (int)sbo_f64_1(b, "conv_distance", -1.0);
+    s->conv_seed = sbo_i64_1(b, "conv_seed", 0);
+    s->cv_off = sbo_i32(b, "conv_room_offsets");
+    s->cv_cells = sbo_i32(b, "conv_room_cells");
+    s->cv_coff = sbo_i32(b, "conv_cand_offsets");
+    s->cv_cidx = sbo_i32(b, "conv_cand_idx");
+    if (!s->cv_off || !s->cv_cells || !s->cv_coff || !s->cv_cidx) return -1;
+    s->cv_rooms = (int)sbo_sec(b, "conv_room_offsets")->count - 1;
+    s->cv_max_room = 0;
+    for (int i = 0; i < s->cv_rooms; i++) {
+        const int m = s->cv_off[i + 1] - s->cv_off[i];
+        if (m > s->cv_max_room) s->cv_max_room = m;
     }
     return 0;
 }
@@ -637,9 +703,10 @@ static void field_step(SboEnv* e) {
 /* sb_sim_step_post, sb_sim.c:459-521. The post-solve sensed-mean block
  * (:462-487) writes only zone_q/input_q/sensed_mean, which the next step_pre
  * rewrites before any read, so it has no observable effect and is omitted.
- * Convection is off (conv_p == 0, sb_convect.c:40). */
+ * Convection (sb_sim.c:489) permutes the new field within its rooms. */
 static void step_post(SboEnv* e) {
     const SboScen* s = e->sc;
+    sbo_conv_apply(s, &e->cmt, e->cv_left, e->cv_right, e->T);
     double wcap = CP_W * RHO_W * total_flow_rate(e);
     if (wcap > 0.0 && s->k > 0) {
         double supply = e->boiler_cur;
@@ -861,7 +928,7 @@ static double reward(SboEnv* e, int kv) {
 /* ------------------------------------------------------------ env API */
 static void* zalloc(size_t n, size_t sz) { return calloc(n ? n : 1, sz); }
 
-SboEnv* sbo_env_new(const SboScen* s, uint32_t occ_seed, int start, int max_steps) {
+SboEnv* sbo_env_new(const SboScen* s, uint32_t occ_seed, uint32_t conv_seed, int start, int max_steps) {
     SboEnv* e = (SboEnv*)calloc(1, sizeof(SboEnv));
     if (!e) return NULL;
     int na = s->n_ahu, nv = s->n_vav, nz = s->n_zones, n = s->n, k = s->k;
@@ -884,6 +951,9 @@ SboEnv* sbo_env_new(const SboScen* s, uint32_t occ_seed, int start, int max_step
     e->work = zalloc(n, 8); e->power = zalloc(k, 8); e->mat = zalloc((size_t)k * (size_t)k, 8);
     e->pump_head = s->pump_head0;
     sbo_mt_seed(&e->mt, occ_seed);
+    sbo_mt_seed(&e->cmt, conv_seed);
+    e->cv_left = zalloc((size_t)s->cv_max_room, 4);
+    e->cv_right = zalloc((size_t)s->cv_max_room, 4);
     e->start = start;
     e->max_steps = max_steps;
     return e;
@@ -896,7 +966,7 @@ void sbo_env_free(SboEnv* e) {
                     e->ratio, e->heatsp, e->coolsp, e->dcmd, e->rcmd, e->sensing, e->vav_area,
                     e->mode, e->prev_valid, e->dcmd_set, e->rcmd_set, e->avg_temp, e->zone_q,
                     e->input_q, e->air_g, e->air_T, e->coil, e->occ_state, e->occV, e->rhs, e->y,
-                    e->yr, e->r, e->work, e->power, e->mat};
+                    e->yr, e->r, e->work, e->power, e->mat, e->cv_left, e->cv_right};
     for (size_t i = 0; i < sizeof(ptrs) / sizeof(ptrs[0]); i++) free(ptrs[i]);
     free(e);
 }

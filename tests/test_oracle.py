@@ -217,3 +217,67 @@ def test_oracle_matches_reference_core(zones, ahus, tmp_path):
         assert a.last_reward_f64() == b.last_reward_f64()
         assert np.array_equal(a.state().view(np.uint64), b.state().view(np.uint64)), s
     assert np.array_equal(a.log(), b.log())
+
+
+@pytest.mark.parametrize("seed,top", [(5, 1), (17321, 6), (2**31 + 7, 13), (99, 1000)])
+def test_mt_interval_matches_numpy_randint(seed, top):
+    """Masked rejection in [0, top] (sb_rng.c:45-54) is numpy's legacy
+    RandomState.randint stream: a dropped rejection or a wrong mask width fails."""
+    L = po.lib("oracle").lib
+    r = _mt(seed)
+    ours = np.array([L.sbo_mt_interval(ctypes.byref(r), top) for _ in range(3000)])
+    ref = np.random.RandomState(seed).randint(0, top + 1, size=3000)
+    assert np.array_equal(ours, ref)
+
+
+def _conv_blob(zones, ahus, tmp_path, conv):
+    lay = G.LayoutSpec(zones, ahus)
+    clim = G.ClimateSpec(12.0, 8.0, seed=502)
+    p = tmp_path / f"{lay.name}__{clim.name}__{conv.tag}.sbb"
+    G.scenario_writer(lay, clim, 2 * G.EPISODE_STEPS, 17321, conv).write(p)
+    return p
+
+
+@pytest.mark.skipif(not po.ref_available(), reason="oracle/_ref needs /root/reference")
+@pytest.mark.parametrize("zones,ahus", [(41, 1), (81, 4)])
+def test_oracle_convection_matches_reference_core(zones, ahus, tmp_path):
+    """Stochastic convection (sb_convect.c:39-73) on: restatement vs the compiled
+    reference csim, bit for bit, through an auto-reset (the stream persists)."""
+    p = _conv_blob(zones, ahus, tmp_path, G.ConvSpec(p=0.08, distance=2, seed=4242))
+    a = po.CpuEnv("ref", p, 17321 + 3, start=5, max_steps=40)
+    b = po.CpuEnv("oracle", p, 17321 + 3, start=5, max_steps=40)
+    assert np.array_equal(a.reset().view(np.uint32), b.reset().view(np.uint32))
+    for s in range(90):
+        row = po.action_row(11, 2, s, a.n_cont, a.n_disc)
+        ra, rb = a.step(row), b.step(row)
+        assert np.array_equal(ra[0].view(np.uint32), rb[0].view(np.uint32)), s
+        assert a.last_reward_f64() == b.last_reward_f64()
+        assert np.array_equal(a.state().view(np.uint64), b.state().view(np.uint64)), s
+    assert np.array_equal(a.log(), b.log())
+
+
+def test_oracle_convection_swaps_room_temperatures(tmp_path):
+    """One step with convection permutes zone-air temperatures within strips:
+    against the same step with p = 0 the multiset of air temperatures of every
+    strip is the same and some cells moved (a swap applied to the wrong cells or
+    rooms fails the first; an apply that does nothing fails the second)."""
+    on = _conv_blob(57, 2, tmp_path, G.ConvSpec(p=0.5, distance=-1, seed=7))
+    off = _conv_blob(57, 2, tmp_path, G.ConvSpec(p=0.0, distance=-1, seed=7))
+    b_on = read_sbb(on)
+    a = po.CpuEnv("oracle", on, 17321, start=0, max_steps=100)
+    b = po.CpuEnv("oracle", off, 17321, start=0, max_steps=100)
+    a.reset()
+    b.reset()
+    row = po.action_row(3, 0, 0, a.n_cont, a.n_disc)
+    a.step(row)
+    b.step(row)
+    Z = 57
+    ta, tb = a.state()[:Z], b.state()[:Z]   # grid row 0: the zone air cells
+    off_ = b_on["conv_room_offsets"]
+    cells = b_on["conv_room_cells"].reshape(-1, 2)
+    moved = 0
+    for rm in range(off_.size - 1):
+        cols = cells[off_[rm]:off_[rm + 1], 1]
+        assert np.array_equal(np.sort(ta[cols]), np.sort(tb[cols]))
+        moved += int(np.sum(ta[cols] != tb[cols]))
+    assert moved > 0
