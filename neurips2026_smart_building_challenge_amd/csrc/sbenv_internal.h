@@ -28,6 +28,8 @@
 #define SBK_BX_ROWS 3    // block-Jacobi rows per block (matches the planner)
 #define SBK_BX_SLOTS 2   // block slots per lane
 #define SBK_BX_TERMS 8   // off-block entries per block
+#define SBK_CV_WIN 256   // tempered convection words held in LDS at a time
+#define SBK_CV_ROOM 64   // cells per convection room (one draw round per wavefront)
 
 namespace sbk {
 
@@ -52,7 +54,8 @@ struct StateLayout {
     int occV;                                   // [nz]
     // MT19937 words live after the image in HBM (loaded only when drawn from)
     int mt;                                     // u32[624], HBM offset
-    int record_bytes;                           // image + mt, 256-byte aligned
+    int cmt;                                    // u32[624] convection stream, HBM offset (0: no convection tables)
+    int record_bytes;                           // image + mt (+ cmt), 256-byte aligned
 };
 
 // PF_SWEEPS: relaxation sweeps of the last step; PF_CAPPED: steps that hit the sweep cap
@@ -65,7 +68,7 @@ enum { SOLVER_LU = 0, SOLVER_RELAX = 1 };
 // covers the tiles whose layouts use that form.
 enum { KV_LU = 0, KV_POINT = 1, KV_BLOCK = 2, KV_COUNT = 3 };
 enum { PI_HWS_RUN = 0, PI_PUMP_RUN, PI_HWS_REQ, PI_STEP_INDEX, PI_STEP, PI_MT_IDX,
-       PI_STEPS_TOTAL, PI_EPISODES };
+       PI_STEPS_TOTAL, PI_EPISODES, PI_CONV_IDX, PI_COUNT = 16 };
 
 // Per-env LDS region (byte offsets from the env's base; a workgroup holds the
 // layout image first, then one region per env).
@@ -89,6 +92,11 @@ struct LdsLayout {
     int sync;         // i32[SY_WORDS] hand-off area of the env's two wavefronts
     int stamps;       // u64[SBK_NSTAMP] phase stamps (phase timing only)
     int prec;         // int4[n_pass] solve pass records (copied at kernel start)
+    // convection (layouts with convection tables only): tempered stream words,
+    // the step's permutation of the room cells, one room's swap pairs
+    int cvwin;        // u32[SBK_CV_WIN]
+    int cvsig;        // i32[cv_cells]
+    int cvl, cvr;     // i32[cv_max_room]
     int bytes;        // region size, 16-byte multiple
 };
 
@@ -117,6 +125,10 @@ struct ImgLayout {
     // 8 off-block entry values, 0; bx_i int4[3][nb] = row | air << 16 (3, each
     // -1 as 0xffff / -1), 0, then col | row-in-block << 16 of the 8 entries
     int bx_d, bx_i;
+    // convection rooms (sb_convect.h): room offsets [cv_rooms + 1] into the
+    // cell list, each cell's node [cv_cells], its candidates as CSR over cell
+    // positions [cv_cells + 1], [candidates]
+    int cv_off, cv_node, cv_coff, cv_cidx;
     // u8
     int is_room;                                            // [n]
     int act_disc, act_flags;                                // [n_act]
@@ -176,6 +188,7 @@ struct DevLayout {
     const SBK_C double* rx_val;        // [SBK_RX_TERMS * SBK_RX_ROWS]
     const SBK_C int* rx_col;           // [SBK_RX_TERMS * SBK_RX_ROWS]
     int bx_nb;                         // block-Jacobi blocks (tables in the layout image: bx_d, bx_i)
+    int cv_rooms, cv_cells, cv_max_room;   // convection rooms and cells (tables in the layout image: cv_*)
     // solve plan
     const SBK_C int* pinfo;            // [n_pass * 4]: hdr_off, word_off, nact | maxcnt << 8 | pivot << 16, 0
     const SBK_C uint64_t* hdr;         // per active lane: target | mul << 16 | inv_target << 32 | count << 48
@@ -260,6 +273,8 @@ struct DevScen {
     double p_arr, p_dep;
     int ea, la, ed, ld;
     int conv_tmean;              // 1 if some AHU may need the field mean
+    int conv_on;                 // stochastic convection: conv_p != 0 and conv_distance != 0
+    double conv_p;
 };
 
 struct EnvDesc {
@@ -281,8 +296,10 @@ enum { KMODE_STEP = 0, KMODE_RESET = 1 };
 // ready) and by the helper (VAV sensed temperatures ready; AHU return-air
 // sums ready; observation
 // written, new occupancy committed and reward half ready); the helper's reward
-// half (4 f64 from SY_PART) and the host log fields it read (2 f32 from SY_LOG).
-enum { SY_PRE = 0, SY_POST = 1, SY_HALF = 2, SY_SENS = 3, SY_PART = 4, SY_LOG = 12, SY_RET = 14, SY_WORDS = 16 };
+// half (4 f64 from SY_PART) and the host log fields it read (2 f32 from SY_LOG);
+// the helper's convection permutation of the step (SY_CONV).
+enum { SY_PRE = 0, SY_POST = 1, SY_HALF = 2, SY_SENS = 3, SY_PART = 4, SY_LOG = 12, SY_RET = 14, SY_CONV = 15,
+       SY_WORDS = 16 };
 
 // A workgroup's envs: order[first .. first + count) all of one layout, with
 // the layout's staging burst inputs (copied from its DevLayout so the burst

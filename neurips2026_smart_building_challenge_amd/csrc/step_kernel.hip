@@ -358,6 +358,10 @@ struct Tab {
     SBK_TAB(int, ahu_vavs)
     SBK_TAB(int, ahu_col_off)
     SBK_TAB(int, ahu_cols)
+    SBK_TAB(int, cv_off)
+    SBK_TAB(int, cv_node)
+    SBK_TAB(int, cv_coff)
+    SBK_TAB(int, cv_cidx)
     SBK_TAB(uint32_t, f_src)
     SBK_TAB(uint32_t, act_dst)
     SBK_TAB(uint32_t, act_aux)
@@ -372,6 +376,7 @@ struct Ctx {
     const SBK_C DevScen* S;
     int e;                   // env index
     bool helper;             // the env's second wavefront
+    bool conv;               // stochastic convection on (read with the env's records, before the burst)
     unsigned long long* stamps;   // phase stamps (LDS)
     unsigned char* rec;      // HBM record of this env
     Tab t;
@@ -857,6 +862,207 @@ __device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday,
         int s = 0;
         for (int a = 0; a < L->nassign; a++) s += st_out[z * L->nassign + a];
         v_out[z] = (uint8_t)s;
+    }
+    esync();
+}
+
+// ------------------------------------------------------------------ convection
+// Stochastic convection (complete_port/csim/sb_convect.c:39-73) splits into a
+// plan and an apply. Which cells swap depends only on the convection stream,
+// never on temperatures, so the helper wavefront draws the step's swaps while
+// the first wavefront runs the HVAC pre-step and the solve, and hands over the
+// permutation they compose to; the first wavefront applies it to the new
+// field after the solve (sb_sim.c:489).
+//
+// Stream words come from a window of SBK_CV_WIN tempered words in LDS at
+// stream positions [wb, wb + SBK_CV_WIN); positions count from the start of
+// the state block in c.mt (the env's state, staged from HBM), and a fill that
+// runs past the block's end twists the state and rebases every position by
+// -624. A round reads ahead of what it consumes, so the step may end before
+// the first word of a block it twisted into (a negative position): the HBM
+// state then stays the block before (twisting writes that block to HBM first
+// when it is not the one staged).
+struct CvStream {
+    uint32_t* win;
+    uint32_t* hbm;   // the env's stream state in its HBM record
+    int wb, pos;
+    bool twisted;
+};
+
+// Refills the window to start at s.pos: words still in the old window are
+// kept, the rest tempered from the state (twisting it when they run past the
+// block's end).
+template <int W>
+__device__ __forceinline__ void cv_fill(CvStream& s, uint32_t* mt) {
+    constexpr int PER = SBK_CV_WIN / W;
+    uint32_t v[PER];
+    const int old_end = s.wb + SBK_CV_WIN;
+#pragma unroll
+    for (int r = 0; r < PER; r++) {
+        const int q = s.pos + ln() + r * W;
+        v[r] = 0u;
+        if (q < old_end) v[r] = s.win[q - s.wb];
+        else if (q < SBK_MT_N) v[r] = mt_temper(mt[q]);
+    }
+    const bool tw = s.pos + SBK_CV_WIN > SBK_MT_N;
+    if (tw) {
+        if (s.twisted)
+            for (int i = ln(); i < SBK_MT_N; i += W) s.hbm[i] = mt[i];
+        esync();
+        mt_twist<W>(mt);
+#pragma unroll
+        for (int r = 0; r < PER; r++) {
+            const int q = s.pos + ln() + r * W;
+            if (q >= SBK_MT_N && q >= old_end) v[r] = mt_temper(mt[q - SBK_MT_N]);
+        }
+    }
+    esync();
+#pragma unroll
+    for (int r = 0; r < PER; r++) s.win[ln() + r * W] = v[r];
+    esync();
+    s.wb = s.pos;
+    if (tw) {
+        s.wb -= SBK_MT_N;
+        s.pos -= SBK_MT_N;
+        s.twisted = true;
+    }
+}
+
+// Next stream word (wave-uniform).
+template <int W>
+__device__ __forceinline__ uint32_t cv_next(CvStream& s, uint32_t* mt) {
+    if (s.pos >= s.wb + SBK_CV_WIN) cv_fill<W>(s, mt);
+    return __builtin_amdgcn_readfirstlane(s.win[s.pos++ - s.wb]);
+}
+
+// Uniform integer in [0, max] by masked rejection (sb_rng.c:45-54).
+template <int W>
+__device__ __forceinline__ int cv_interval(CvStream& s, uint32_t* mt, uint32_t max) {
+    if (max == 0u) return 0;
+    uint32_t mask = max;
+    mask |= mask >> 1;
+    mask |= mask >> 2;
+    mask |= mask >> 4;
+    mask |= mask >> 8;
+    mask |= mask >> 16;
+    uint32_t v;
+    do {
+        v = cv_next<W>(s, mt) & mask;
+    } while (v > max);
+    return (int)v;
+}
+
+// The helper's half: draws the step's swaps room by room in the stream order
+// of sb_conv_apply and composes them into the permutation sig of the room
+// cells (the new field at cell s is the old field at cell sig[s]). Within a
+// room, the candidate draws of one round are taken in parallel: lane i reads
+// the u of the room's i-th undecided cell as if no cell before it had drawn a
+// candidate, and the first cell that swaps fixes where the stream continues.
+template <int W>
+__device__ __forceinline__ void conv_plan(Ctx& c) {
+    const SBK_C DevLayout* L = c.L;
+    const double p = c.S->conv_p;
+    uint32_t* mt = c.mt;
+    const uint32_t* hbm_mt = reinterpret_cast<const uint32_t*>(c.rec + L->st.cmt);
+    int* sig = reinterpret_cast<int*>(c.envb + L->lds.cvsig);
+    int* lft = reinterpret_cast<int*>(c.envb + L->lds.cvl);
+    int* rgt = reinterpret_cast<int*>(c.envb + L->lds.cvr);
+    const int* off = c.t.cv_off();
+    const int* coff = c.t.cv_coff();
+    const int* cidx = c.t.cv_cidx();
+    for (int i = ln(); i < SBK_MT_N; i += W) mt[i] = hbm_mt[i];
+    for (int i = ln(); i < L->cv_cells; i += W) sig[i] = i;
+    esync();
+    CvStream s;
+    s.win = reinterpret_cast<uint32_t*>(c.envb + L->lds.cvwin);
+    s.hbm = reinterpret_cast<uint32_t*>(c.rec + L->st.cmt);
+    s.pos = c.ip[PI_CONV_IDX];
+    s.wb = s.pos - SBK_CV_WIN;   // empty window
+    s.twisted = false;
+    cv_fill<W>(s, mt);
+    for (int rm = 0; rm < L->cv_rooms; rm++) {
+        const int base = off[rm], n = off[rm + 1] - base;
+        int m = 0, j = 0;
+        while (j < n) {
+            // one round over the undecided cells j .. n - 1 (at most 64)
+            if (s.pos + 2 * (n - j) > s.wb + SBK_CV_WIN) cv_fill<W>(s, mt);
+            const int i = ln();
+            bool sel = false;
+            if (i < n - j) {
+                const uint32_t a = s.win[s.pos - s.wb + 2 * i], b = s.win[s.pos - s.wb + 2 * i + 1];
+                const double u = ((a >> 5) * 67108864.0 + (b >> 6)) / 9007199254740992.0;
+                const int cg = base + j + i;
+                sel = !(u > p) && coff[cg + 1] > coff[cg];
+            }
+            const uint64_t bal = __ballot(sel);
+            if (bal == 0ull) {
+                s.pos += 2 * (n - j);
+                break;
+            }
+            const int first = __builtin_ctzll(bal);
+            const int cg = base + j + first;
+            s.pos += 2 * (first + 1);
+            const int c0 = coff[cg], c1 = coff[cg + 1];
+            const int pick = cv_interval<W>(s, mt, (uint32_t)(c1 - c0 - 1));
+            if (ln() == 0) {
+                lft[m] = cg;
+                rgt[m] = cidx[c0 + pick];
+            }
+            m++;
+            j += first + 1;
+        }
+        // Fisher-Yates over the pairs, last first (sb_convect.c:60-64)
+        for (int t = m - 1; t > 0; t--) {
+            const int j2 = cv_interval<W>(s, mt, (uint32_t)t);
+            if (ln() == 0) {
+                const int l0 = lft[t], r0 = rgt[t];
+                lft[t] = lft[j2];
+                rgt[t] = rgt[j2];
+                lft[j2] = l0;
+                rgt[j2] = r0;
+            }
+        }
+        // the swaps in order, composed into sig (sb_convect.c:65-71)
+        if (ln() == 0) {
+            for (int t = 0; t < m; t++) {
+                const int a = lft[t], b = rgt[t];
+                const int x = sig[a];
+                sig[a] = sig[b];
+                sig[b] = x;
+            }
+        }
+        esync();
+    }
+    // the state of the block holding the next unread position: the twisted
+    // one, or (a negative position) the block before, already in HBM
+    if (s.twisted && s.pos >= 0)
+        for (int i = ln(); i < SBK_MT_N; i += W) s.hbm[i] = mt[i];
+    // read again only by later launches (across the kernel boundary)
+    if (s.twisted) __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    if (ln() == 0) c.ip[PI_CONV_IDX] = s.pos < 0 ? s.pos + SBK_MT_N : s.pos;
+    esync();
+}
+
+// The first wavefront's half: the new field of room cell s is the field at
+// cell sig[s] after the solve.
+template <int W>
+__device__ __forceinline__ void conv_apply(Ctx& c) {
+    const SBK_C DevLayout* L = c.L;
+    const int* node = c.t.cv_node();
+    const int* sig = reinterpret_cast<const int*>(c.envb + L->lds.cvsig);
+    constexpr int PER = 4;   // room cells per lane (at most 256, checked on the host)
+    double v[PER];
+#pragma unroll
+    for (int r = 0; r < PER; r++) {
+        const int i = ln() + r * W;
+        v[r] = 0.0;
+        if (i < L->cv_cells) v[r] = c.T[node[sig[i]]];
+    }
+    esync();
+#pragma unroll
+    for (int r = 0; r < PER; r++) {
+        const int i = ln() + r * W;
+        if (i < L->cv_cells) c.T[node[i]] = v[r];
     }
     esync();
 }
@@ -2240,6 +2446,10 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
     uint8_t* st_new = env + L->lds.occn;
     uint8_t* v_new = st_new + nocc;
     occupancy_advance<W>(c, (int)c.row[RW_OCC_HOUR_J], (int)c.row[RW_OCC_WORK_J], st_new, v_new);
+    if (c.conv) {
+        conv_plan<W>(c);
+        env_post(sy + SY_CONV, 1);
+    }
     STAMP(15);
     // host-visible log fields (the trainer may clear them between steps)
     float lg_ret = 0.f, lg_mean = 0.f;
@@ -2307,6 +2517,7 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
     c.S = P.scens + ed.scen;
     c.e = e;
     c.helper = helper;
+    c.conv = c.S->conv_on != 0;
     c.rec = P.state + ed.state_off;
     unsigned char* env = lds + P.img_lds + slot * tl.lds_bytes;
     int* sy = reinterpret_cast<int*>(env + L->lds.sync);
@@ -2398,6 +2609,10 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
         env_post(sy + SY_PRE, 1);    // the helper's observation reads the state as of here
         STAMP(4);
         field_step<W, KV>(c, P);
+        if (c.conv) {
+            env_wait(sy + SY_CONV, 1);   // the helper's permutation of the room cells
+            conv_apply<W>(c);
+        }
         env_post(sy + SY_POST, 1);   // the helper's reward half reads the new field
         STAMP(7);
         zone_means<W>(c, c.zq);

@@ -97,6 +97,7 @@ struct HostScen {
     int n1 = 0;
     int episode_steps = 0;
     int64_t occ_seed = 17321;
+    int64_t conv_seed = 0;
     int hour_m1_rows = 0;
     int n_cont = 0, n_disc = 0;
 };
@@ -109,7 +110,8 @@ const char* kStructural[] = {
     "room_cells", "vav_zone_offsets", "vav_zone_idx", "vav_ahu_idx", "coupled_vav_idx", "ahu_const",
     "vav_const", "act_owner_kind", "act_owner_index", "act_actuator", "act_is_discrete", "act_min_native",
     "act_max_native", "act_min_norm", "act_max_norm", "f_dev_kind", "f_dev_idx", "f_obs_id", "f_norm_mean",
-    "f_norm_var", "n_dev", "n_aux", "occ_params", nullptr};
+    "f_norm_var", "n_dev", "n_aux", "occ_params", "conv_room_offsets", "conv_room_cells", "conv_cand_offsets",
+    "conv_cand_idx", nullptr};
 
 std::string structural_key(const sbh::Blob& b) {
     std::string k;
@@ -265,7 +267,41 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     const int nassign = (int)op[0];
     if (nassign < 0 || nz * nassign > 312 || nz * nassign > 5 * width)
         return (*err = "too many occupants per env"), false;
-    if (b.f64_1("conv_p", 0.0) != 0.0) return (*err = "stochastic convection (conv_p > 0) is not supported"), false;
+    // convection rooms (complete_port/csim/sb_convect.c:6-31): cells -> nodes,
+    // candidates as positions in the cell list
+    std::vector<int> cv_off, cv_node, cv_coff, cv_cidx;
+    int cv_max_room = 0;
+    {
+        uint64_t c_off = 0, c_cells = 0, c_coff = 0, c_idx = 0;
+        const int32_t* ro = b.i32("conv_room_offsets", &c_off);
+        const int32_t* rc = b.i32("conv_room_cells", &c_cells);
+        const int32_t* co = b.i32("conv_cand_offsets", &c_coff);
+        const int32_t* ci = b.i32("conv_cand_idx", &c_idx);
+        if (!ro || !co || c_off < 1 || c_coff < 1) return (*err = "convection tables missing"), false;
+        const int nrooms = (int)c_off - 1, ncells = (int)c_coff - 1;
+        if (ro[0] != 0 || ro[nrooms] != ncells || (int)c_cells != 2 * ncells || co[0] != 0 || co[ncells] != (int)c_idx)
+            return (*err = "convection tables inconsistent"), false;
+        if (ncells > 0) {
+            cv_off.assign(ro, ro + nrooms + 1);
+            cv_coff.assign(co, co + ncells + 1);
+            for (int r = 0; r < nrooms; r++) {
+                if (ro[r + 1] < ro[r]) return (*err = "convection room offsets decrease"), false;
+                cv_max_room = std::max(cv_max_room, ro[r + 1] - ro[r]);
+            }
+            if (cv_max_room > SBK_CV_ROOM) return (*err = "convection room with more than 64 cells"), false;
+            if (ncells > 4 * 64) return (*err = "more than 256 convection cells per building"), false;
+            for (int j = 0; j < ncells; j++) {
+                const int p = rc[2 * j] * nc_grid + rc[2 * j + 1];
+                if (p < 0 || p >= n) return (*err = "convection cell outside the solved field"), false;
+                cv_node.push_back(p);
+                if (co[j + 1] < co[j]) return (*err = "convection candidate offsets decrease"), false;
+            }
+            for (uint64_t j = 0; j < c_idx; j++) {
+                if (ci[j] < 0 || ci[j] >= ncells) return (*err = "convection candidate out of range"), false;
+                cv_cidx.push_back(ci[j]);
+            }
+        }
+    }
 
     D.n = n; D.nz = nz; D.nv = nv; D.na = na; D.k = k; D.n_act = n_act; D.n_cont = ncont; D.n_disc = ndisc;
     D.n_dev = n_dev; D.n_aux = n_aux; D.nassign = nassign;
@@ -287,12 +323,13 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     S.plant = f64a(8);
     S.cal_n = sbk::RW_COUNT + std::max(n_aux - 1, 0);
     S.cal = f64a(2 * S.cal_n);
-    S.run = o; o += 4 * na; S.coolreq = o; o += 4 * na; S.iplant = o; o += 32;
+    S.run = o; o += 4 * na; S.coolreq = o; o += 4 * na; S.iplant = o; o += 4 * sbk::PI_COUNT;
     S.mode = o; o += nv; S.prev_valid = o; o += nv; S.dcmd_set = o; o += nv; S.rcmd_set = o; o += nv;
     S.occ_state = o; o += nz * nassign; S.occV = o; o += nz;
     S.bytes = align_up(o, 16);
     S.mt = S.bytes;
-    S.record_bytes = align_up(S.bytes + 4 * SBK_MT_N, 256);
+    S.cmt = cv_node.empty() ? 0 : S.mt + 4 * SBK_MT_N;
+    S.record_bytes = align_up(S.bytes + 4 * SBK_MT_N * (cv_node.empty() ? 1 : 2), 256);
     // per-env LDS region: record image, MT words (filled when a draw twists),
     // scenario image, action row, then scratch
     sbk::LdsLayout& Ls = D.lds;
@@ -321,10 +358,22 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     l = align_up(l, 16);
     Ls.stamps = l; l += 8 * SBK_NSTAMP;
     Ls.prec = l; l += 16 * D.n_pass;
+    Ls.cvwin = Ls.cvsig = Ls.cvl = Ls.cvr = 0;
+    if (!cv_node.empty()) {
+        l = align_up(l, 16);
+        Ls.cvwin = l; l += 4 * SBK_CV_WIN;
+        Ls.cvsig = l; l += 4 * (int)cv_node.size();
+        Ls.cvl = l; l += 4 * cv_max_room;
+        Ls.cvr = l; l += 4 * cv_max_room;
+    }
     Ls.bytes = align_up(l, 16);
+    D.cv_rooms = cv_node.empty() ? 0 : (int)cv_off.size() - 1;
+    D.cv_cells = (int)cv_node.size();
+    D.cv_max_room = cv_max_room;
     // algorithmic bytes: the state image without the calendar prefetch, which
     // is a copy of shared per-scenario tables
     D.bytes_per_step = 2.0 * (S.bytes - 16.0 * S.cal_n) + 4.0 * (ncont + ndisc) + 4.0 * SB_OBS + 8.0;
+    if (S.cmt) D.bytes_per_step += 4.0 * SBK_MT_N;   // the convection stream state, read every step
     D.solve_flops = 2.0 * (double)P.n_pairs + (double)P.n_divs;
     if (use_block) {   // per sweep: off-block multiply-subtracts, then each block's inverse applied
         long long nnz = 0, dense = 0;
@@ -513,6 +562,10 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
             G.bx_d = I.add(bd);
             G.bx_i = I.add(bi);
         }
+        G.cv_off = I.add(cv_off);
+        G.cv_node = I.add(cv_node);
+        G.cv_coff = I.add(cv_coff);
+        G.cv_cidx = I.add(cv_cidx);
         G.is_room = I.add(is_room);
         G.act_disc = I.add(take(disc, n_act));
         // observation sources (the value each field reads; sb_obs.c:49-64 and
@@ -758,6 +811,12 @@ bool make_scen(const sbh::Blob& b, const HostLayout& Lh, HostScen* H, Arena& A, 
     const double* meta = b.f64("obs_meta", &c);
     H->episode_steps = (meta && c >= 4) ? (int)meta[3] : 0;
     H->occ_seed = b.i64_1("occ_seed", 17321);
+    // stochastic convection (sb_convect.c:12-14, :40): on when p != 0 and the
+    // distance is not 0; the stream is seeded per env from conv_seed
+    D.conv_p = b.f64_1("conv_p", 0.0);
+    D.conv_on = (D.conv_p != 0.0 && (int)b.f64_1("conv_distance", -1.0) != 0) ? 1 : 0;
+    if (D.conv_on && L.cv_cells == 0) D.conv_on = 0;   // no rooms: nothing to draw (sb_convect.c:42)
+    H->conv_seed = b.i64_1("conv_seed", 0);
     H->n_cont = L.n_cont;
     H->n_disc = L.n_disc;
     return true;
@@ -814,6 +873,7 @@ struct Vec {
     std::vector<sbk::EnvDesc> desc;
     std::vector<int> order;
     std::vector<uint32_t> seeds;
+    std::vector<uint32_t> conv_seeds;
     std::vector<int> env_scen_local;
     unsigned char* d_arena = nullptr;
     unsigned char* d_state = nullptr;
@@ -1048,6 +1108,7 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
             d.start = start;
             v->desc.push_back(d);
             v->seeds.push_back((uint32_t)(S.occ_seed + (per_env_seed ? j : 0)));
+            v->conv_seeds.push_back((uint32_t)(S.conv_seed + (per_env_seed ? j : 0)));
             v->env_scen_local.push_back(j);
             state_off += (size_t)L.dev.st.record_bytes;
         }
@@ -1156,6 +1217,10 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
             reinterpret_cast<double*>(r + L.st.plant)[sbk::PF_PUMP_HEAD] = v->scens[d.scen].dev.pump_head0;
             reinterpret_cast<int*>(r + L.st.iplant)[sbk::PI_MT_IDX] = SBK_MT_N;
             mt_seed(reinterpret_cast<uint32_t*>(r + L.st.mt), v->seeds[i]);
+            if (L.st.cmt) {
+                reinterpret_cast<int*>(r + L.st.iplant)[sbk::PI_CONV_IDX] = SBK_MT_N;
+                mt_seed(reinterpret_cast<uint32_t*>(r + L.st.cmt), v->conv_seeds[i]);
+            }
             v->bytes_per_step += L.bytes_per_step;
             v->flops_per_step += L.solve_flops;
         }

@@ -54,3 +54,17 @@ def cfg0_dir(tmp_path_factory) -> Path:
     d = tmp_path_factory.mktemp("cfg0")
     G.write_config(0, d)
     return d
+
+
+def conv_scenarios(out_dir: Path, p: float, distance: int, seed: int) -> Path:
+    """The 6 layouts under one climate with stochastic convection on."""
+    from neurips2026_smart_building_challenge_amd.scenario import generate as G
+
+    scen = [(G.LayoutSpec(z, a), G.ClimateSpec(12.0, 8.0, seed=502)) for z, a in G.LAYOUTS]
+    G.write_scenarios(scen, out_dir, conv=G.ConvSpec(p, distance, seed))
+    return out_dir
+
+
+@pytest.fixture(scope="session")
+def conv_dir(tmp_path_factory) -> Path:
+    return conv_scenarios(tmp_path_factory.mktemp("conv"), 0.08, 2, 4242)
