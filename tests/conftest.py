@@ -25,14 +25,16 @@ def golden_index() -> dict:
     return json.loads((GOLDEN / "golden.json").read_text())
 
 
-def golden_blob(layout, climate, out_dir: Path) -> tuple[Path, str]:
-    """Regenerates the blob of a golden case; returns (path, sha256)."""
+def golden_blob(layout, climate, out_dir: Path, conv=None) -> tuple[Path, str]:
+    """Regenerates the blob of a golden case (conv: (p, distance, seed) or None);
+    returns (path, sha256)."""
     from neurips2026_smart_building_challenge_amd.scenario import generate as G
 
     spec = G.LayoutSpec(*layout)
     clim = G.ClimateSpec(climate[0], climate[1], seed=climate[2])
-    p = out_dir / f"{spec.name}__{clim.name}.sbb"
-    data = G.scenario_writer(spec, clim, 2 * G.EPISODE_STEPS, 17321).tobytes()
+    cv = None if conv is None else G.ConvSpec(*conv)
+    p = out_dir / f"{spec.name}__{clim.name}{'' if cv is None else '__' + cv.tag}.sbb"
+    data = G.scenario_writer(spec, clim, 2 * G.EPISODE_STEPS, 17321, cv).tobytes()
     p.write_bytes(data)
     return p, hashlib.sha256(data).hexdigest()
 

@@ -72,3 +72,33 @@ def test_gpu_convection_batch_invariant(conv_dir):
         assert np.array_equal(big.state(0)[:-2], small.state(0)[:-2], equal_nan=True), s
     big.close()
     small.close()
+
+
+def test_gpu_convection_vs_reference_fixture(golden_index, tmp_path):
+    """The reference csim core's own trajectory with convection on (golden
+    fixture z65_convection, written by the compiled reference): per-step float
+    rewards within two float32 steps, recorded states within 1e-9, through
+    two auto-resets."""
+    from conftest import golden_blob
+    import pyoracle as po
+    from pathlib import Path
+
+    case = golden_index["cases"]["z65_convection"]
+    path, sha = golden_blob(case["layout"], case["climate"], tmp_path, case["conv"])
+    assert sha == case["blob_sha256"], "generator output changed: regenerate tests/golden"
+    fx = np.load(str(Path(__file__).parent / "golden" / "z65_convection.npz"))
+    say("convection vs reference fixture: 1 env, 96 steps")
+    vec = E.VecEnv(1, blob=str(path), max_steps=case["max_steps"])
+    assert vec.meta(0)[1] == case["start"] and vec.meta(0)[2] == case["occ_seed"]
+    vec.reset()
+    seed = golden_index["action_seed"]
+    for s in range(case["steps"]):
+        vec.actions[0].copy_(torch.from_numpy(po.action_row(seed, 0, s, vec.envs[0].n_cont, vec.envs[0].n_disc)))
+        vec.step()
+        torch.cuda.synchronize()
+        r = float(fx["reward_f32"][s])
+        assert abs(float(host(vec.rewards)[0]) - r) <= 2 * np.spacing(np.float32(abs(r))) + 1e-12, s
+        if s + 1 in case["record"]:
+            ref = fx[f"state_{s + 1}"]
+            state_close(vec.state(0), ref, f"step {s + 1}")
+    vec.close()

@@ -170,10 +170,10 @@ def _run_case(kind, path, case, seed):
     return rewards, rec, h_obs.hexdigest(), h_state.hexdigest()
 
 
-@pytest.mark.parametrize("name", ["z81_autoreset", "z57_offset", "z49_weekend", "cfg0_episode"])
+@pytest.mark.parametrize("name", ["z81_autoreset", "z57_offset", "z49_weekend", "cfg0_episode", "z65_convection"])
 def test_oracle_matches_golden(name, golden_index, tmp_path):
     case = golden_index["cases"][name]
-    path, sha = golden_blob(case["layout"], case["climate"], tmp_path)
+    path, sha = golden_blob(case["layout"], case["climate"], tmp_path, case.get("conv"))
     assert sha == case["blob_sha256"], "generator output changed: regenerate tests/golden"
     rewards, rec, ho, hs = _run_case("oracle", path, case, golden_index["action_seed"])
     fx = np.load(pytest.importorskip("pathlib").Path(__file__).parent / "golden" / f"{name}.npz")
