@@ -1,6 +1,6 @@
 """Benchmark of the MI355X env step: env-steps/s at 960 mixed envs (fp64 physics).
 
-    python bench.py [--steps K] [--warmup W] [--config 1] [--gpus 1] [--no-cpu]
+    python bench.py [--steps K] [--warmup W] [--config 1] [--gpus 1] [--no-cpu] [--conv P]
 
 Workload (BASELINE config index 1): 960 envs over 30 seeded synthetic scenarios
 (6 layouts of 41..81 zones x 5 climates, 32 envs each), Beta(2,2) actions from
@@ -51,11 +51,14 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def scenario_dir(config: int) -> Path:
+def scenario_dir(config: int, conv: float = 0.0) -> Path:
+    """The config's blobs; conv > 0 turns stochastic convection on in every blob
+    (probability conv per room cell and step, candidates within 2 columns)."""
     from neurips2026_smart_building_challenge_amd.scenario import generate as G
 
-    d = Path(tempfile.gettempdir()) / f"sbenv_bench_cfg{config}"
-    G.write_config(config, d)
+    cv = G.ConvSpec(conv, 2, 9001) if conv > 0 else None
+    d = Path(tempfile.gettempdir()) / (f"sbenv_bench_cfg{config}" + (f"_{cv.tag}" if cv else ""))
+    G.write_config(config, d, conv=cv)
     return d
 
 
@@ -144,6 +147,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--solver", default="auto", choices=["auto", "relax", "point", "lu"])
+    ap.add_argument("--conv", type=float, default=0.0,
+                    help="stochastic convection on with this swap probability (not a BASELINE config)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of 256 MiB 10 times (counter calibration)")
     args = ap.parse_args()
@@ -162,7 +167,7 @@ def main() -> int:
     scen, n_envs, desync = G.config_scenarios(args.config)
     groups = len(scen)
     t0 = time.time()
-    blob_dir = scenario_dir(args.config)
+    blob_dir = scenario_dir(args.config, args.conv)
     log(f"scenarios ready in {time.time() - t0:.1f}s: {blob_dir}")
     vec = E.VecEnv(n_envs, blob_dir=str(blob_dir), groups=groups, desync=int(desync), solver=args.solver)
     info = vec.info()
@@ -237,7 +242,7 @@ def main() -> int:
     b2b_us = vec.time_step(max(1, args.kernel_iters)) / max(1, args.kernel_iters) * 1e3
     solver = vec.solve_info(0)
     sweeps = [vec.solve_info(i)["sweeps"] for i in range(0, n_envs, max(1, n_envs // 64))]
-    traffic = measured_traffic(args.config)
+    traffic = measured_traffic(args.config) if args.conv <= 0 else None
     phases = vec.phase_times()
     log("phase us (mean / max over workgroups): " +
         ", ".join(f"{k} {m:.1f}/{x:.1f}" for k, (m, x) in phases.items()))
@@ -259,7 +264,8 @@ def main() -> int:
                                f"climates), "
                                + ("shared-policy MLP 1024-128-128-544 (fp32 MFMA) + Beta sampling per step, "
                                   if rollout else "Beta(2,2) actions, ")
-                               + "fp64 physics" + (", desynchronised starts" if desync else ""),
+                               + "fp64 physics" + (", desynchronised starts" if desync else "")
+                               + (f", stochastic convection p={args.conv}" if args.conv > 0 else ""),
                    "n_envs": n_envs, "scenarios": groups, "episode_steps": G.EPISODE_STEPS,
                    "solver": solver["solver"], "envs_per_workgroup": info.envs_per_block,
                    "block": info.block, "lds_bytes": info.lds_bytes},

@@ -770,8 +770,9 @@ __device__ __forceinline__ void gather_words(Ptr src, int idx, int first, const 
 // MT stream in occupant order, so occupant o uses the words at
 // 2 * (number of drawing occupants before o). The new chain states go to
 // st_out (which may be c.occ_state itself) and the zone counts to v_out.
+// Returns whether the draws twisted the state (staged through c.mt).
 template <int W>
-__device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday, uint8_t* st_out, uint8_t* v_out) {
+__device__ __forceinline__ bool occupancy_advance(Ctx& c, int hour, int workday, uint8_t* st_out, uint8_t* v_out) {
     const SBK_C DevLayout* L = c.L;
     const SBK_C DevScen* S = c.S;
     const int nocc = L->nz * L->nassign;
@@ -864,6 +865,7 @@ __device__ __forceinline__ void occupancy_advance(Ctx& c, int hour, int workday,
         v_out[z] = (uint8_t)s;
     }
     esync();
+    return twisted;
 }
 
 // ------------------------------------------------------------------ convection
@@ -952,14 +954,16 @@ __device__ __forceinline__ int cv_interval(CvStream& s, uint32_t* mt, uint32_t m
     return (int)v;
 }
 
-// The helper's half: draws the step's swaps room by room in the stream order
-// of sb_conv_apply and composes them into the permutation sig of the room
-// cells (the new field at cell s is the old field at cell sig[s]). Within a
-// room, the candidate draws of one round are taken in parallel: lane i reads
-// the u of the room's i-th undecided cell as if no cell before it had drawn a
-// candidate, and the first cell that swaps fixes where the stream continues.
+// The helper's half: draws the step's swaps in the stream order of
+// sb_conv_apply and composes them into the permutation sig of the room
+// cells (the new field at cell s is the old field at cell sig[s]). The stream
+// state arrives in c.mt with the staging burst; `restage` reloads it from HBM
+// (the occupancy draws of this step twisted their own state through c.mt).
+// A round reads the u of up to 64 undecided cells in parallel, each at the
+// position it has if no cell before it swaps; the first cell that swaps fixes
+// where the stream continues.
 template <int W>
-__device__ __forceinline__ void conv_plan(Ctx& c) {
+__device__ __forceinline__ void conv_plan(Ctx& c, bool restage) {
     const SBK_C DevLayout* L = c.L;
     const double p = c.S->conv_p;
     uint32_t* mt = c.mt;
@@ -970,7 +974,8 @@ __device__ __forceinline__ void conv_plan(Ctx& c) {
     const int* off = c.t.cv_off();
     const int* coff = c.t.cv_coff();
     const int* cidx = c.t.cv_cidx();
-    for (int i = ln(); i < SBK_MT_N; i += W) mt[i] = hbm_mt[i];
+    if (restage)
+        for (int i = ln(); i < SBK_MT_N; i += W) mt[i] = hbm_mt[i];
     for (int i = ln(); i < L->cv_cells; i += W) sig[i] = i;
     esync();
     CvStream s;
@@ -980,59 +985,82 @@ __device__ __forceinline__ void conv_plan(Ctx& c) {
     s.wb = s.pos - SBK_CV_WIN;   // empty window
     s.twisted = false;
     cv_fill<W>(s, mt);
-    for (int rm = 0; rm < L->cv_rooms; rm++) {
-        const int base = off[rm], n = off[rm + 1] - base;
-        int m = 0, j = 0;
-        while (j < n) {
-            // one round over the undecided cells j .. n - 1 (at most 64)
-            if (s.pos + 2 * (n - j) > s.wb + SBK_CV_WIN) cv_fill<W>(s, mt);
-            const int i = ln();
-            bool sel = false;
-            if (i < n - j) {
-                const uint32_t a = s.win[s.pos - s.wb + 2 * i], b = s.win[s.pos - s.wb + 2 * i + 1];
-                const double u = ((a >> 5) * 67108864.0 + (b >> 6)) / 9007199254740992.0;
-                const int cg = base + j + i;
-                sel = !(u > p) && coff[cg + 1] > coff[cg];
-            }
-            const uint64_t bal = __ballot(sel);
-            if (bal == 0ull) {
-                s.pos += 2 * (n - j);
-                break;
-            }
+    // rounds over the cells in stream order, across rooms while the current
+    // room holds no pair yet (a room's end then draws nothing), else up to its
+    // end (where its pairs are shuffled). Room ends (lane r: the end of room r)
+    // and which cells have candidates (bit c % 64 of word c / 64) stay in
+    // registers, so a round's only LDS reads are its stream words.
+    const int ncells = L->cv_cells, nrooms = L->cv_rooms;
+    const int rend_l = ln() < nrooms ? off[ln() + 1] : 0x7fffffff;
+    uint64_t hasc[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int cg = ln() + W * r;
+        hasc[r] = __ballot(cg < ncells && coff[cg + 1] > coff[cg]);
+    }
+    // the room holding cell x (rooms are consecutive; empty ones hold none)
+    auto room_of = [&](int x) { return __popcll(__ballot(rend_l <= x)); };
+    int g = 0, m = 0;
+    while (g < ncells) {
+        const int room = room_of(g);
+        const int rend = __builtin_amdgcn_readlane(rend_l, room);
+        const int h = min(m == 0 ? ncells : rend, g + W);
+        if (s.pos + 2 * (h - g) > s.wb + SBK_CV_WIN) cv_fill<W>(s, mt);
+        const int i = ln();
+        bool sel = false;
+        if (i < h - g) {
+            const uint32_t a = s.win[s.pos - s.wb + 2 * i], b = s.win[s.pos - s.wb + 2 * i + 1];
+            const double u = ((a >> 5) * 67108864.0 + (b >> 6)) / 9007199254740992.0;
+            const int cg = g + i, q = cg >> 6;
+            const uint64_t hw = q == 0 ? hasc[0] : (q == 1 ? hasc[1] : (q == 2 ? hasc[2] : hasc[3]));
+            sel = !(u > p) && ((hw >> (cg & 63)) & 1ull);
+        }
+        const uint64_t bal = __ballot(sel);
+        bool close = false;   // the current room's pairs are complete after this round
+        if (bal == 0ull) {
+            s.pos += 2 * (h - g);
+            close = rend <= h;
+            g = h;
+        } else {
             const int first = __builtin_ctzll(bal);
-            const int cg = base + j + first;
+            const int gs = g + first;
             s.pos += 2 * (first + 1);
-            const int c0 = coff[cg], c1 = coff[cg + 1];
+            const int grend = __builtin_amdgcn_readlane(rend_l, room_of(gs));   // rooms passed held no pair
+            const int c0 = coff[gs], c1 = coff[gs + 1];
             const int pick = cv_interval<W>(s, mt, (uint32_t)(c1 - c0 - 1));
             if (ln() == 0) {
-                lft[m] = cg;
+                lft[m] = gs;
                 rgt[m] = cidx[c0 + pick];
             }
             m++;
-            j += first + 1;
+            g = gs + 1;
+            close = g == grend;
         }
-        // Fisher-Yates over the pairs, last first (sb_convect.c:60-64)
-        for (int t = m - 1; t > 0; t--) {
-            const int j2 = cv_interval<W>(s, mt, (uint32_t)t);
+        if (close && m > 0) {
+            // Fisher-Yates over the room's pairs, last first (sb_convect.c:60-64),
+            // then the swaps in order composed into sig (:65-71)
+            for (int t = m - 1; t > 0; t--) {
+                const int j2 = cv_interval<W>(s, mt, (uint32_t)t);
+                if (ln() == 0) {
+                    const int l0 = lft[t], r0 = rgt[t];
+                    lft[t] = lft[j2];
+                    rgt[t] = rgt[j2];
+                    lft[j2] = l0;
+                    rgt[j2] = r0;
+                }
+            }
             if (ln() == 0) {
-                const int l0 = lft[t], r0 = rgt[t];
-                lft[t] = lft[j2];
-                rgt[t] = rgt[j2];
-                lft[j2] = l0;
-                rgt[j2] = r0;
+                for (int t = 0; t < m; t++) {
+                    const int a = lft[t], b = rgt[t];
+                    const int x = sig[a];
+                    sig[a] = sig[b];
+                    sig[b] = x;
+                }
             }
+            m = 0;
         }
-        // the swaps in order, composed into sig (sb_convect.c:65-71)
-        if (ln() == 0) {
-            for (int t = 0; t < m; t++) {
-                const int a = lft[t], b = rgt[t];
-                const int x = sig[a];
-                sig[a] = sig[b];
-                sig[b] = x;
-            }
-        }
-        esync();
     }
+    esync();
     // the state of the block holding the next unread position: the twisted
     // one, or (a negative position) the block before, already in HBM
     if (s.twisted && s.pos >= 0)
@@ -2445,9 +2473,10 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
     }
     uint8_t* st_new = env + L->lds.occn;
     uint8_t* v_new = st_new + nocc;
-    occupancy_advance<W>(c, (int)c.row[RW_OCC_HOUR_J], (int)c.row[RW_OCC_WORK_J], st_new, v_new);
+    const bool occ_twisted = occupancy_advance<W>(c, (int)c.row[RW_OCC_HOUR_J], (int)c.row[RW_OCC_WORK_J], st_new,
+                                                  v_new);
     if (c.conv) {
-        conv_plan<W>(c);
+        conv_plan<W>(c, occ_twisted);
         env_post(sy + SY_CONV, 1);
     }
     STAMP(15);
@@ -2522,8 +2551,10 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
     unsigned char* env = lds + P.img_lds + slot * tl.lds_bytes;
     int* sy = reinterpret_cast<int*>(env + L->lds.sync);
     c.stamps = reinterpret_cast<unsigned long long*>(env + L->lds.stamps);
-    STAMP(0);
-    if (P.phase_ts && ln() == 0 && !helper) c.stamps[SBK_STAMP_ENTRY] = t_entry;
+    // an inactive slot's region may lie past the workgroup's LDS (a layout's
+    // tiles hold only the envs that fit): it touches no LDS but the shared image
+    if (active) STAMP(0);
+    if (P.phase_ts && ln() == 0 && !helper && active) c.stamps[SBK_STAMP_ENTRY] = t_entry;
     {
         // one burst: the layout image (whole block, every thread), and per env
         // (its two wavefronts) its record image, its scenario image and its

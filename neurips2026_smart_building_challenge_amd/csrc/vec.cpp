@@ -290,6 +290,7 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
             }
             if (cv_max_room > SBK_CV_ROOM) return (*err = "convection room with more than 64 cells"), false;
             if (ncells > 4 * 64) return (*err = "more than 256 convection cells per building"), false;
+            if (nrooms > 64) return (*err = "more than 64 convection rooms per building"), false;
             for (int j = 0; j < ncells; j++) {
                 const int p = rc[2 * j] * nc_grid + rc[2 * j + 1];
                 if (p < 0 || p >= n) return (*err = "convection cell outside the solved field"), false;
@@ -327,8 +328,11 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     S.mode = o; o += nv; S.prev_valid = o; o += nv; S.dcmd_set = o; o += nv; S.rcmd_set = o; o += nv;
     S.occ_state = o; o += nz * nassign; S.occV = o; o += nz;
     S.bytes = align_up(o, 16);
-    S.mt = S.bytes;
-    S.cmt = cv_node.empty() ? 0 : S.mt + 4 * SBK_MT_N;
+    // HBM record: the image, then (convection) the convection stream state,
+    // which the staging burst copies with the image into the env's MT scratch
+    // in LDS (it follows the image there too), then the occupancy stream state
+    S.cmt = cv_node.empty() ? 0 : S.bytes;
+    S.mt = S.bytes + (cv_node.empty() ? 0 : 4 * SBK_MT_N);
     S.record_bytes = align_up(S.bytes + 4 * SBK_MT_N * (cv_node.empty() ? 1 : 2), 256);
     // per-env LDS region: record image, MT words (filled when a draw twists),
     // scenario image, action row, then scratch
@@ -1130,22 +1134,28 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
     {
         const int epb_kw = (int)kw(kwargs, "envs_per_block", 4.0f);
         if (epb_kw < 1 || epb_kw > 4) die("env.envs_per_block must be 1..4");
-        int img = 0, reg = 0;
-        for (auto& L : v->layouts) {
-            img = std::max(img, L.dev.img.bytes);
-            reg = std::max(reg, L.dev.lds.bytes);
-        }
+        // every workgroup holds the largest layout image, then its envs'
+        // regions; a layout's tiles take as many envs as fit (at most
+        // envs_per_block), the launch is shaped for the largest tile
+        int img = 0;
+        for (auto& L : v->layouts) img = std::max(img, L.dev.img.bytes);
         const int limit = 160 * 1024;
-        int epb = epb_kw;
-        while (epb > 1 && img + epb * reg > limit) epb--;
-        if (img + reg > limit) die("layout needs more LDS than a workgroup has");
+        std::vector<int> per(v->layouts.size());
+        int epb = 1, lds = 0;
+        for (size_t li = 0; li < v->layouts.size(); li++) {
+            const int reg = v->layouts[li].dev.lds.bytes;
+            if (img + reg > limit) die("layout needs more LDS than a workgroup has");
+            per[li] = std::min(epb_kw, (limit - img) / reg);
+            epb = std::max(epb, per[li]);
+            lds = std::max(lds, img + per[li] * reg);
+        }
         v->epb = epb;
         v->img_lds = img;
-        v->lds_bytes = img + epb * reg;
+        v->lds_bytes = lds;
         for (int i = 0; i < n;) {
             const int lay = v->desc[v->order[i]].layout;
             int j = i;
-            while (j < n && j - i < epb && v->desc[v->order[j]].layout == lay) j++;
+            while (j < n && j - i < per[lay] && v->desc[v->order[j]].layout == lay) j++;
             v->tiles.push_back(sbk::Tile{lay, i, j - i, 0});
             const int kv = kernel_variant(v->layouts[lay].dev);
             if (v->groups.empty() || v->groups.back().variant != kv)
@@ -1172,7 +1182,7 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
         const sbk::DevLayout& D = v->layouts[t.layout].dev;
         t.lds_bytes = D.lds.bytes;
         t.img16 = D.img.bytes >> 4;
-        t.rec16 = D.st.bytes >> 4;
+        t.rec16 = (D.st.bytes + (D.st.cmt ? 4 * SBK_MT_N : 0)) >> 4;   // the image (and the convection state)
         t.lds_state = D.lds.state;
         t.lds_scen = D.lds.scen;
         t.lds_act = D.lds.act;
