@@ -222,6 +222,26 @@ int sbx_policy_bind(Env* envs, const SbxPolicy* p);
 int sbx_policy_act(Env* envs, uint64_t seed, uint32_t step);
 int sbx_policy_heads(Env* envs, float* out, int cap);
 
+/* Rollout-buffer side of the Beta heads (complete_port/patches/
+ * pufferlib_core.diff:944-1000, beta_continuous_head; the trainer stores each
+ * draw with its log-probability and entropy). With a = softplus(u) + 1,
+ * b = softplus(v) + 1 (float, as the sampler maps them), a head's draw x has
+ * log p = (a - 1) log x + (b - 1) log(1 - x) - ln B(a, b) (x clamped to
+ * [2^-24, 1 - 2^-24]) and entropy H = ln B(a, b) - (a - 1) psi(a) - (b - 1) psi(b)
+ * + (a + b - 2) psi(a + b), evaluated in f64 and stored as float.
+ * sbx_policy_act_logp: sbx_policy_act (same draws and action rows) that also
+ * writes draws [n][272] (each used head's x in (0, 1), 0 elsewhere) and the
+ * per-env sums over used heads logp [n] and entropy [n] (fixed summation
+ * order). sbx_beta_eval: the same sums for given heads y [n][544] (the layout of
+ * sbx_policy_heads) and draws [n][272], and, when grad is not null, grad
+ * [n][4][272] = d log p / du, d log p / dv, d H / du, d H / dv per head (0 for
+ * unused heads). Continuous head h reads u = y[h], v = y[256 + h]; discrete
+ * head d (column 256 + d) reads u = y[512 + d], v = y[528 + d]. Device
+ * pointers, caller-owned; both need sbx_policy_bind first (its scratch), launch
+ * on the bound stream and allocate nothing. Return 0, or -1. */
+int sbx_policy_act_logp(Env* envs, uint64_t seed, uint32_t step, float* draws, float* logp, float* entropy);
+int sbx_beta_eval(Env* envs, const float* y, const float* draws, float* logp, float* entropy, float* grad);
+
 /* The heads' Beta sampler alone: out[i] ~ Beta(alpha[i], beta[i]) for device
  * arrays of n floats (alpha, beta >= 1), counter (i, 0, 0 or 1, 1 + attempt),
  * on the bound stream. Returns 0, or -1. */

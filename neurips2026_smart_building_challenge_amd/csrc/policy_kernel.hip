@@ -21,6 +21,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "sb_betamath.h"
 #include "sb_philox.h"
 
 namespace sbk {
@@ -126,14 +127,17 @@ __device__ __forceinline__ float gamma_mt(float a, uint32_t env, uint32_t step, 
 // kept in LDS (and written to y for sbx_policy_heads), and the 256 threads then
 // take the group's 16 x 16 x 2 gamma draws, two each: lanes 2t and 2t + 1
 // draw Ga and Gb of one head and the even lane writes x = Ga / (Ga + Gb)
-// (continuous 2x - 1, discrete x > 0.5; 0 past the env's head counts).
+// (continuous 2x - 1, discrete x > 0.5; 0 past the env's head counts). With
+// `draws` set, the even lane also stores x and the head's log-density at x and
+// entropy (hlp, hent; 0 past the head counts) for the rollout buffer.
 constexpr int kHeadGroups = kActWidth / 16;   // 16 continuous groups, 1 discrete
 
 __global__ __launch_bounds__(256) void heads_layer_kernel(const float* __restrict__ h2, const float* __restrict__ w3,
                                                           const float* __restrict__ b3, float* __restrict__ y,
                                                           float* __restrict__ actions, const int* __restrict__ n_cont,
                                                           const int* __restrict__ n_disc, int n, uint64_t seed,
-                                                          uint32_t step) {
+                                                          uint32_t step, float* __restrict__ draws,
+                                                          float* __restrict__ hlp, float* __restrict__ hent) {
     constexpr int H = kPolicyHidden;
     __shared__ float ys[16][32 + 1];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -195,13 +199,80 @@ __global__ __launch_bounds__(256) void heads_layer_kernel(const float* __restric
         }
         const float other = __shfl_xor(gm, 1, 64);
         if (live && which == 0) {
-            float v = 0.0f;
+            float v = 0.0f, x = 0.0f;
             if (used) {
-                const float x = gm / (gm + other);
+                x = gm / (gm + other);
                 v = h < 256 ? 2.0f * x - 1.0f : (x > 0.5f ? 1.0f : 0.0f);
             }
             actions[(size_t)e * kActWidth + h] = v;
+            if (draws) {
+                const size_t o = (size_t)e * kActWidth + h;
+                draws[o] = x;
+                float lp = 0.0f, en = 0.0f;
+                if (used) {
+                    const BetaHead bh = beta_head(ys[row][k], ys[row][16 + k], x);
+                    lp = (float)bh.logp;
+                    en = (float)bh.entropy;
+                }
+                hlp[o] = lp;
+                hent[o] = en;
+            }
         }
+    }
+}
+
+// Rollout-buffer evaluation of given draws (complete_port/patches/
+// pufferlib_core.diff:944-1000): thread (e, h) takes head h of env e, u and v
+// from y (continuous head h: columns h and 256 + h; discrete head d = h - 256:
+// columns 512 + d and 528 + d) and its draw x; writes the head's log-density,
+// entropy and grad[e][k][h] (k: d logp/du, d logp/dv, d H/du, d H/dv), zeros
+// past the env's head counts.
+__global__ void beta_eval_kernel(const float* __restrict__ y, const float* __restrict__ draws,
+                                 const int* __restrict__ n_cont, const int* __restrict__ n_disc, int n,
+                                 float* __restrict__ hlp, float* __restrict__ hent, float* __restrict__ grad) {
+    const int e = blockIdx.x, h = threadIdx.x;
+    if (e >= n || h >= kActWidth) return;
+    const bool used = h < 256 ? h < n_cont[e] : h - 256 < n_disc[e];
+    const size_t o = (size_t)e * kActWidth + h;
+    float lp = 0.0f, en = 0.0f, g[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (used) {
+        const float* ye = y + (size_t)e * kPolicyHeads;
+        const float u = h < 256 ? ye[h] : ye[512 + (h - 256)];
+        const float v = h < 256 ? ye[256 + h] : ye[528 + (h - 256)];
+        const BetaHead bh = beta_head(u, v, draws[o]);
+        lp = (float)bh.logp;
+        en = (float)bh.entropy;
+#pragma unroll
+        for (int k = 0; k < 4; k++) g[k] = (float)bh.g[k];
+    }
+    hlp[o] = lp;
+    hent[o] = en;
+    if (grad) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) grad[((size_t)e * 4 + k) * kActWidth + h] = g[k];
+    }
+}
+
+// Per-env sums of the heads' log-densities and entropies, one wavefront per env
+// in a fixed order (lane-strided partial sums, then a butterfly), so a sum does
+// not depend on the batch it is in.
+__global__ void beta_sum_kernel(const float* __restrict__ hlp, const float* __restrict__ hent, int n,
+                                float* __restrict__ logp, float* __restrict__ entropy) {
+    const int e = blockIdx.x, lane = threadIdx.x;
+    if (e >= n) return;
+    float a = 0.0f, b = 0.0f;
+    for (int h = lane; h < kActWidth; h += 64) {
+        a += hlp[(size_t)e * kActWidth + h];
+        b += hent[(size_t)e * kActWidth + h];
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) {
+        a += __shfl_xor(a, m, 64);
+        b += __shfl_xor(b, m, 64);
+    }
+    if (lane == 0) {
+        logp[e] = a;
+        entropy[e] = b;
     }
 }
 
@@ -219,10 +290,13 @@ __global__ void beta_sample_kernel(const float* alpha, const float* beta, float*
 
 // ---------------------------------------------------------------- launchers
 // obs [n x 1024] -> h1, h2 [n x 128] -> y [n x 544] -> actions [n x 272], on stream s.
+// With draws set, also the rollout buffer's draws, per-head log-densities and
+// entropies (hlp, hent [n x 272]) and their per-env sums (logp, entropy [n]).
 extern "C" int sbk_launch_policy(const float* obs, const float* w1, const float* b1, const float* w2,
                                  const float* b2, const float* w3, const float* b3, float* h1, float* h2, float* y,
                                  float* actions, const int* n_cont, const int* n_disc, int n, uint64_t seed,
-                                 uint32_t step, hipStream_t s) {
+                                 uint32_t step, float* draws, float* hlp, float* hent, float* logp, float* entropy,
+                                 hipStream_t s) {
     using namespace sbk;
     if (n <= 0) return (int)hipErrorInvalidValue;
     const int mt = (n + 15) / 16;
@@ -233,7 +307,20 @@ extern "C" int sbk_launch_policy(const float* obs, const float* w1, const float*
                        kPolicyHidden, w2, b2, h2, kPolicyHidden, n, kPolicyHidden);
     // third layer and the Beta draws in one launch per (env tile, head group)
     hipLaunchKernelGGL(heads_layer_kernel, dim3(mt, kHeadGroups), dim3(256), 0, s, h2, w3, b3, y, actions, n_cont,
-                       n_disc, n, seed, step);
+                       n_disc, n, seed, step, draws, hlp, hent);
+    if (draws) hipLaunchKernelGGL(beta_sum_kernel, dim3(n), dim3(64), 0, s, hlp, hent, n, logp, entropy);
+    return (int)hipGetLastError();
+}
+
+// Log-densities, entropies and their gradients of given draws under heads y.
+extern "C" int sbk_launch_beta_eval(const float* y, const float* draws, const int* n_cont, const int* n_disc, int n,
+                                    float* hlp, float* hent, float* grad, float* logp, float* entropy,
+                                    hipStream_t s) {
+    using namespace sbk;
+    if (n <= 0) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(beta_eval_kernel, dim3(n), dim3(kActWidth + 16), 0, s, y, draws, n_cont, n_disc, n, hlp,
+                       hent, grad);
+    hipLaunchKernelGGL(beta_sum_kernel, dim3(n), dim3(64), 0, s, hlp, hent, n, logp, entropy);
     return (int)hipGetLastError();
 }
 

@@ -31,7 +31,11 @@ extern "C" int sbk_set_lds_limit(int width, int bytes);
 extern "C" int sbk_launch_policy(const float* obs, const float* w1, const float* b1, const float* w2,
                                  const float* b2, const float* w3, const float* b3, float* h1, float* h2, float* y,
                                  float* actions, const int* n_cont, const int* n_disc, int n, uint64_t seed,
-                                 uint32_t step, hipStream_t s);
+                                 uint32_t step, float* draws, float* hlp, float* hent, float* logp, float* entropy,
+                                 hipStream_t s);
+extern "C" int sbk_launch_beta_eval(const float* y, const float* draws, const int* n_cont, const int* n_disc, int n,
+                                    float* hlp, float* hent, float* grad, float* logp, float* entropy,
+                                    hipStream_t s);
 extern "C" int sbk_launch_beta_sample(const float* alpha, const float* beta, float* out, int n, uint64_t seed,
                                       hipStream_t s);
 extern "C" int sbk_launch_gen_actions(float* actions, const int* n_cont, const int* n_disc, int n_envs,
@@ -899,6 +903,7 @@ struct Vec {
     // shared policy (sbx_policy_bind): caller-owned weights, library-owned activations
     SbxPolicy pol{};
     float *p_h1 = nullptr, *p_h2 = nullptr, *p_y = nullptr;
+    float *p_hlp = nullptr, *p_hent = nullptr;   // per-head log-densities and entropies [n][SB_ACT]
 };
 
 constexpr int kTimerPairs = 16384;
@@ -1328,6 +1333,8 @@ void puf_close(Env* envs) {
     (void)hipFree(v->p_h1);
     (void)hipFree(v->p_h2);
     (void)hipFree(v->p_y);
+    (void)hipFree(v->p_hlp);
+    (void)hipFree(v->p_hent);
     (void)hipFree(v->d_ncont);
     (void)hipFree(v->d_ndisc);
     (void)hipHostFree(v->envs);
@@ -1580,6 +1587,8 @@ int sbx_policy_bind(Env* envs, const SbxPolicy* p) {
         hip_ok(hipMalloc(&v->p_h1, sizeof(float) * (size_t)v->n * SBX_POLICY_HIDDEN), "hipMalloc(policy)");
         hip_ok(hipMalloc(&v->p_h2, sizeof(float) * (size_t)v->n * SBX_POLICY_HIDDEN), "hipMalloc(policy)");
         hip_ok(hipMalloc(&v->p_y, sizeof(float) * (size_t)v->n * SBX_POLICY_HEADS), "hipMalloc(policy)");
+        hip_ok(hipMalloc(&v->p_hlp, sizeof(float) * (size_t)v->n * SB_ACT), "hipMalloc(policy)");
+        hip_ok(hipMalloc(&v->p_hent, sizeof(float) * (size_t)v->n * SB_ACT), "hipMalloc(policy)");
     }
     return 0;
 }
@@ -1589,8 +1598,31 @@ int sbx_policy_act(Env* envs, uint64_t seed, uint32_t step) {
     if (!v->p_h1) { g_err = "sbx_policy_act before sbx_policy_bind"; return -1; }
     const SbxPolicy& p = v->pol;
     int rc = sbk_launch_policy(v->obs, p.w1, p.b1, p.w2, p.b2, p.w3, p.b3, v->p_h1, v->p_h2, v->p_y, v->actions,
-                               v->d_ncont, v->d_ndisc, v->n, seed, step, g_stream);
+                               v->d_ncont, v->d_ndisc, v->n, seed, step, nullptr, nullptr, nullptr, nullptr, nullptr,
+                               g_stream);
     if (rc != 0) die(std::string("policy launch failed: ") + hipGetErrorString((hipError_t)rc));
+    return 0;
+}
+
+int sbx_policy_act_logp(Env* envs, uint64_t seed, uint32_t step, float* draws, float* logp, float* entropy) {
+    Vec* v = vec_of(envs);
+    if (!v->p_h1) { g_err = "sbx_policy_act_logp before sbx_policy_bind"; return -1; }
+    if (!draws || !logp || !entropy) { g_err = "sbx_policy_act_logp: null output"; return -1; }
+    const SbxPolicy& p = v->pol;
+    int rc = sbk_launch_policy(v->obs, p.w1, p.b1, p.w2, p.b2, p.w3, p.b3, v->p_h1, v->p_h2, v->p_y, v->actions,
+                               v->d_ncont, v->d_ndisc, v->n, seed, step, draws, v->p_hlp, v->p_hent, logp, entropy,
+                               g_stream);
+    if (rc != 0) die(std::string("policy launch failed: ") + hipGetErrorString((hipError_t)rc));
+    return 0;
+}
+
+int sbx_beta_eval(Env* envs, const float* y, const float* draws, float* logp, float* entropy, float* grad) {
+    Vec* v = vec_of(envs);
+    if (!v->p_hlp) { g_err = "sbx_beta_eval before sbx_policy_bind"; return -1; }
+    if (!y || !draws || !logp || !entropy) { g_err = "sbx_beta_eval: null argument"; return -1; }
+    int rc = sbk_launch_beta_eval(y, draws, v->d_ncont, v->d_ndisc, v->n, v->p_hlp, v->p_hent, grad, logp, entropy,
+                                  g_stream);
+    if (rc != 0) die(std::string("beta eval launch failed: ") + hipGetErrorString((hipError_t)rc));
     return 0;
 }
 

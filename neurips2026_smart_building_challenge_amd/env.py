@@ -94,6 +94,7 @@ EXPORTS = [
     "puf_render", "puf_close", "puf_log", "puf_live_log", "puf_mask_init", "sbx_gen_actions",
     "sbx_vec_info", "sbx_env_state", "sbx_time_step", "sbx_step_actions", "sbx_phase_times", "sbx_phase_stamps", "sbx_kernel_timer", "sbx_pass_times", "sbx_solve_info",
     "sbx_policy_bind", "sbx_policy_act", "sbx_policy_heads", "sbx_beta_sample",
+    "sbx_policy_act_logp", "sbx_beta_eval",
     "sbx_env_meta", "sbx_scenario_path",
     "sbx_plan_layout", "sbx_plan_free", "sbx_last_error", "sbx_version",
 ]
@@ -139,6 +140,8 @@ def lib() -> ctypes.CDLL:
         L.sbx_policy_act.argtypes = [ctypes.POINTER(Env), ctypes.c_uint64, ctypes.c_uint32]
         L.sbx_policy_heads.argtypes = [ctypes.POINTER(Env), P, ctypes.c_int]
         L.sbx_beta_sample.argtypes = [P, P, P, ctypes.c_int, ctypes.c_uint64]
+        L.sbx_policy_act_logp.argtypes = [ctypes.POINTER(Env), ctypes.c_uint64, ctypes.c_uint32, P, P, P]
+        L.sbx_beta_eval.argtypes = [ctypes.POINTER(Env), P, P, P, P, P]
         L.sbx_phase_stamps.argtypes = [ctypes.POINTER(Env), P, ctypes.c_int]
         L.sbx_phase_stamps.restype = ctypes.c_int
         L.sbx_solve_info.argtypes = [ctypes.POINTER(Env), ctypes.c_int, P]
@@ -325,6 +328,32 @@ class VecEnv:
         """Policy forward + Beta sampling: writes every env's action row for the next step."""
         if self.L.sbx_policy_act(self.envs, seed, step) != 0:
             raise RuntimeError(self.L.sbx_last_error().decode())
+
+    def policy_act_logp(self, seed: int, step: int):
+        """policy_act that also returns the rollout buffer's draws (n, 272) and
+        per-env log-probability and entropy (n,) as device tensors."""
+        t = self.torch
+        draws = t.empty((self.n, SB_ACT), dtype=t.float32, device=self.obs.device)
+        logp = t.empty(self.n, dtype=t.float32, device=self.obs.device)
+        ent = t.empty(self.n, dtype=t.float32, device=self.obs.device)
+        if self.L.sbx_policy_act_logp(self.envs, seed, step, P(draws.data_ptr()), P(logp.data_ptr()),
+                                      P(ent.data_ptr())) != 0:
+            raise RuntimeError(self.L.sbx_last_error().decode())
+        return draws, logp, ent
+
+    def beta_eval(self, y, draws, grad: bool = True):
+        """Per-env log-probability and entropy (n,) of draws (n, 272) under heads
+        y (n, 544), and the per-head gradients (n, 4, 272) when grad."""
+        t = self.torch
+        y = y.contiguous()
+        draws = draws.contiguous()
+        logp = t.empty(self.n, dtype=t.float32, device=self.obs.device)
+        ent = t.empty(self.n, dtype=t.float32, device=self.obs.device)
+        g = t.empty((self.n, 4, SB_ACT), dtype=t.float32, device=self.obs.device) if grad else None
+        if self.L.sbx_beta_eval(self.envs, P(y.data_ptr()), P(draws.data_ptr()), P(logp.data_ptr()),
+                                P(ent.data_ptr()), P(g.data_ptr()) if grad else None) != 0:
+            raise RuntimeError(self.L.sbx_last_error().decode())
+        return logp, ent, g
 
     def policy_heads(self) -> np.ndarray:
         """Head outputs y (n, 544) of the last policy_act."""

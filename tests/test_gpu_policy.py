@@ -120,3 +120,84 @@ def test_gpu_policy_rollout_parity(mixed_dir):
                 rel = np.abs(g[fin] - c[fin]) / np.maximum(np.abs(c[fin]), 1.0)
                 assert rel.max() <= 1e-9, (s, i, rel.max())
     vec.close()
+
+
+def _softplus32(x: np.ndarray) -> np.ndarray:
+    x = x.astype(np.float32)
+    return np.where(x > 20.0, x, np.log1p(np.exp(x)).astype(np.float32)).astype(np.float32)
+
+
+def _beta_ref(u, v, x):
+    """float64 log-density and entropy (scipy) at the float32 shapes."""
+    from scipy import stats
+
+    a = (_softplus32(u) + np.float32(1.0)).astype(np.float64)
+    b = (_softplus32(v) + np.float32(1.0)).astype(np.float64)
+    xc = np.clip(x.astype(np.float64), 2.0**-24, 1.0 - 2.0**-24)
+    return stats.beta.logpdf(xc, a, b), stats.beta.entropy(a, b)
+
+
+def test_gpu_beta_eval_matches_scipy(mixed_dir):
+    """sbx_beta_eval against scipy.stats.beta: per-env sums of log-densities and
+    entropies over the used heads, and the per-head derivatives in u and v
+    against central differences of scipy's log-density and entropy."""
+    print("beta eval: 30 envs vs scipy", flush=True)
+    vec = E.VecEnv(30, blob_dir=str(mixed_dir), groups=30)
+    vec.policy_bind(E.policy_weights(3))
+    rng = np.random.default_rng(11)
+    y = rng.normal(0.0, 2.0, (vec.n, E.POLICY_HEADS)).astype(np.float32)
+    y[:, :8] = [-30.0, -5.0, 0.0, 5.0, 19.9, 20.1, 30.0, 1e-3]   # both softplus branches, flat and peaked heads
+    x = rng.uniform(0.0, 1.0, (vec.n, E.SB_ACT)).astype(np.float32)
+    x[:, :3] = [0.0, 1.0, 0.5]                                   # the clamp at both ends
+    yt, xt = torch.from_numpy(y).cuda(), torch.from_numpy(x).cuda()
+    logp, ent, g = vec.beta_eval(yt, xt)
+    torch.cuda.synchronize()
+    logp, ent, g = logp.cpu().numpy(), ent.cpu().numpy(), g.cpu().numpy()
+    for i in range(vec.n):
+        nc, nd = vec.envs[i].n_cont, vec.envs[i].n_disc
+        heads = list(range(nc)) + [256 + d for d in range(nd)]
+        u = np.array([y[i, h] if h < 256 else y[i, 512 + h - 256] for h in heads], np.float32)
+        v = np.array([y[i, 256 + h] if h < 256 else y[i, 528 + h - 256] for h in heads], np.float32)
+        lp, en = _beta_ref(u, v, x[i, heads])
+        assert abs(logp[i] - lp.sum()) <= 2e-5 * max(1.0, np.abs(lp).sum()), (i, logp[i], lp.sum())
+        assert abs(ent[i] - en.sum()) <= 2e-5 * max(1.0, np.abs(en).sum()), (i, ent[i], en.sum())
+        unused = np.setdiff1d(np.arange(E.SB_ACT), heads)
+        assert np.all(g[i][:, unused] == 0.0)
+        if i < 3:
+            hh = 1e-3
+            for which, k_lp, k_en in ((0, 0, 2), (1, 1, 3)):
+                up, um = (u + hh, u - hh) if which == 0 else (u, u)
+                vp, vm = (v, v) if which == 0 else (v + hh, v - hh)
+                lpp, enp = _beta_ref(up.astype(np.float64), vp.astype(np.float64), x[i, heads])
+                lpm, enm = _beta_ref(um.astype(np.float64), vm.astype(np.float64), x[i, heads])
+                for got, want in ((g[i][k_lp, heads], (lpp - lpm) / (2 * hh)), (g[i][k_en, heads], (enp - enm) / (2 * hh))):
+                    assert np.all(np.abs(got - want) <= 2e-3 * np.maximum(1.0, np.abs(want))), (i, which)
+    vec.close()
+
+
+def test_gpu_policy_act_logp_consistent(mixed_dir):
+    """sbx_policy_act_logp draws exactly what sbx_policy_act draws (same action
+    rows), records the draws behind them (continuous 2x - 1, discrete x > 0.5)
+    and their log-probability and entropy, which equal sbx_beta_eval of the
+    same heads and draws."""
+    print("policy act with log-probabilities: 60 envs", flush=True)
+    vec = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=40)
+    vec.policy_bind(E.policy_weights(5))
+    vec.reset()
+    vec.policy_act(9, 4)
+    a_plain = vec.actions.clone()
+    draws, logp, ent = vec.policy_act_logp(9, 4)
+    torch.cuda.synchronize()
+    assert torch.equal(vec.actions, a_plain)
+    y = torch.from_numpy(vec.policy_heads()).cuda()
+    lp2, en2, _ = vec.beta_eval(y, draws, grad=False)
+    torch.cuda.synchronize()
+    assert torch.allclose(logp, lp2, rtol=1e-6, atol=1e-5) and torch.allclose(ent, en2, rtol=1e-6, atol=1e-5)
+    d, a = draws.cpu().numpy(), vec.actions.cpu().numpy()
+    for i in range(vec.n):
+        nc, nd = vec.envs[i].n_cont, vec.envs[i].n_disc
+        assert np.all((d[i, :nc] > 0.0) & (d[i, :nc] < 1.0))
+        assert np.array_equal(a[i, :nc], (np.float32(2.0) * d[i, :nc] - np.float32(1.0)).astype(np.float32))
+        assert np.array_equal(a[i, 256:256 + nd], (d[i, 256:256 + nd] > 0.5).astype(np.float32))
+        assert np.all(d[i, nc:256] == 0.0) and np.all(d[i, 256 + nd:] == 0.0)
+    vec.close()
