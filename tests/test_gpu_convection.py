@@ -102,3 +102,41 @@ def test_gpu_convection_vs_reference_fixture(golden_index, tmp_path):
             ref = fx[f"state_{s + 1}"]
             state_close(vec.state(0), ref, f"step {s + 1}")
     vec.close()
+
+
+def test_gpu_convection_graph_replay(conv_dir):
+    """puf_step with convection on, captured in a hipGraph: every replay equals
+    eager stepping (the stream state and its position live in the env records,
+    written by the kernel itself; no memset node)."""
+    say("convection graph replay: 24 envs, 45 replays")
+    eager = E.VecEnv(24, blob_dir=str(conv_dir), groups=6, max_steps=30)
+    graph = E.VecEnv(24, blob_dir=str(conv_dir), groups=6, max_steps=30)
+    eager.reset()
+    graph.reset()
+    g = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        graph.L.puf_bind_stream(E.P(torch.cuda.current_stream().cuda_stream))
+        graph.step()
+    graph.L.puf_bind_stream(E.P(torch.cuda.current_stream().cuda_stream))
+    for s in range(45):
+        eager.gen_actions(SEED, s)
+        graph.actions.copy_(eager.actions)
+        torch.cuda.synchronize()
+        eager.step()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(eager.obs, graph.obs), s
+        assert torch.equal(eager.rewards, graph.rewards), s
+    eager.close()
+    graph.close()
+
+
+def test_gpu_convection_desync_parity(conv_dir):
+    """Desynchronised starts with convection on: every env at its own calendar
+    offset, its own occupancy and convection streams."""
+    say("convection parity, desync: 24 envs, 70 steps")
+    vec = E.VecEnv(24, blob_dir=str(conv_dir), groups=6, max_steps=50, desync=1, desync_seed=5)
+    twins = [Twin(vec, i, 50) for i in range(0, vec.n, 2)]
+    _run_parity(vec, twins, 70, "conv desync")
+    vec.close()
