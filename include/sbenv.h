@@ -107,6 +107,8 @@ void dict_set(Dict* d, const char* key, float value);
 /* ---- PufferLib env ABI ---- */
 Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions,
                     float* rewards, float* terminals);
+/* NULL binds the null stream (the binding before any call); the reference
+ * ignores NULL instead, which would leave a stale stream bound. */
 void puf_bind_stream(void* stream /* hipStream_t */);
 void puf_init(Env* env, Dict* kwargs);
 void puf_reset(Env* envs);

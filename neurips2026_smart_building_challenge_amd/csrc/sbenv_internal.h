@@ -302,16 +302,19 @@ enum { SY_PRE = 0, SY_POST = 1, SY_HALF = 2, SY_SENS = 3, SY_PART = 4, SY_LOG = 
        SY_WORDS = 16 };
 
 // A workgroup's envs: order[first .. first + count) all of one layout, with
-// the layout's staging burst inputs (copied from its DevLayout so the burst
-// can be issued from the tile and env records alone).
+// the layout's staging burst inputs (copied from its DevLayout) and each
+// slot's env index and record (copied from the env table; a slot past count
+// repeats the first), so the burst is issued after reading this record alone.
 struct Tile {
     int layout, first, count, lds_bytes;   // lds_bytes: one env's LDS region
-    int img16, rec16;                      // layout image, record image (no MT words), in 16-byte units
+    int img16, rec16;                      // layout image, record image (+ convection state), 16-byte units
     int lds_state, lds_scen, lds_act;      // LDS offsets within the env region
     int st_iplant;                         // byte offset of the i32 plant counters in the record
     int pad0, pad1;
     const SBK_C unsigned char* img_src;    // layout image in HBM
     long long pad2;
+    int env[4];                            // env index of each slot
+    EnvDesc desc[4];                       // its env record
 };
 
 struct KParams {

@@ -2532,15 +2532,15 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
     static_assert(W == 64, "one wavefront per env");
     extern __shared__ __align__(16) unsigned char lds[];
     const unsigned long long t_entry = P.phase_ts ? wall_clock64() : 0ull;
-    const Tile tl = P.tiles[blockIdx.x];
+    const SBK_C Tile& tl = P.tiles[blockIdx.x];
     const SBK_C DevLayout* L = P.layouts + tl.layout;
     const int E = (int)(blockDim.x >> 7);
     const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));   // wave-uniform
     const bool helper = wv >= E;
     const int slot = helper ? (wv - E + (E >> 1)) % E : wv;
     const bool active = slot < tl.count;
-    const int e = P.order[tl.first + (active ? slot : 0)];
-    const EnvDesc ed = P.envs[e];
+    const int e = tl.env[slot];
+    const EnvDesc ed = tl.desc[slot];
     Ctx c;
     c.L = L;
     c.S = P.scens + ed.scen;

@@ -1199,6 +1199,11 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
         d.scn16 = S.img.bytes >> 4;
         d.scen_src = S.img_src;
     }
+    for (auto& t : v->tiles)
+        for (int sl = 0; sl < 4; sl++) {
+            t.env[sl] = v->order[t.first + (sl < t.count ? sl : 0)];
+            t.desc[sl] = v->desc[t.env[sl]];
+        }
     if (v->lds_bytes > 64 * 1024) hip_ok((hipError_t)sbk_set_lds_limit(v->width, v->lds_bytes), "LDS limit");
     hip_ok(hipMalloc(&v->d_layouts, sizeof(sbk::DevLayout) * dl.size()), "hipMalloc(layouts)");
     hip_ok(hipMemcpy(v->d_layouts, dl.data(), sizeof(sbk::DevLayout) * dl.size(), hipMemcpyHostToDevice), "upload");
@@ -1271,10 +1276,10 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
     return out;
 }
 
-void puf_bind_stream(void* s) {
-    if (s == nullptr) return;
-    g_stream = (hipStream_t)s;
-}
+// The reference ignores a NULL stream (smart_buildings.cu:2887-2890); here
+// NULL binds the null stream, the binding before any call, so a caller that
+// bound another stream (a graph capture's, say) can return to the default one.
+void puf_bind_stream(void* s) { g_stream = (hipStream_t)s; }
 
 void puf_init(Env* env, Dict* kwargs) {
     (void)kwargs;

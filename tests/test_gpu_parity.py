@@ -401,3 +401,22 @@ def test_gpu_full_size_properties(config, tmp_path):
         outs.append((obs.copy(), rew.copy()))
         vec.close()
     assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+
+
+def test_gpu_bind_null_stream_returns_to_default(mixed_dir):
+    """puf_bind_stream(NULL) binds the null stream again after another stream was
+    bound (a graph capture's): the env's launches are then ordered with torch's
+    default-stream copies, with no device-wide synchronisation in between."""
+    say("stream binding: side stream, then NULL")
+    vec = E.VecEnv(30, blob_dir=str(mixed_dir), groups=30)
+    side = torch.cuda.Stream()
+    vec.L.puf_bind_stream(E.P(side.cuda_stream))
+    vec.L.puf_bind_stream(None)
+    for step in (3, 777):
+        vec.gen_actions(SEED, step)
+        a = host(vec.actions)                  # a default-stream copy, ordered after the launch
+        for i in range(vec.n):
+            e = vec.envs[i]
+            want = po.action_row(SEED, i, step, e.n_cont, e.n_disc)
+            assert np.array_equal(a[i].view(np.uint32), want.view(np.uint32)), (i, step)
+    vec.close()
