@@ -91,3 +91,32 @@ def test_configs():
     assert n == 16384 and desync
     scen, n, _ = G.config_scenarios(2)
     assert n == 4096 and all(s[0].zones == 81 for s in scen)
+
+
+def test_convection_tables_are_open_plan_strips():
+    """Convection rooms of a synthetic layout: each room is one grid row of one
+    floor (its zones' air cells, in column order), every candidate lies in the
+    cell's own room within the distance and is not the cell itself, and the
+    candidate relation is symmetric (csim draws candidates per cell,
+    sb_convect.c:49-55)."""
+    for zones, ahus in G.LAYOUTS:
+        b, _ = G.layout(G.LayoutSpec(zones, ahus))
+        for dist in (1, 2, -1):
+            off, cells, coff, cidx = G.conv_tables(b, dist)
+            cells = cells.reshape(-1, 2)
+            assert off[0] == 0 and off[-1] == cells.shape[0] == zones
+            assert np.array_equal(np.sort(cells[:, 1]), np.arange(zones)) and np.all(cells[:, 0] == 0)
+            room = np.repeat(np.arange(off.size - 1), np.diff(off))
+            pairs = set()
+            for c in range(cells.shape[0]):
+                fl, r, col = b.zone_pos[cells[c, 1]]
+                for k in cidx[coff[c]:coff[c + 1]]:
+                    assert k != c and room[k] == room[c]
+                    fl2, r2, col2 = b.zone_pos[cells[k, 1]]
+                    assert (fl2, r2) == (fl, r)
+                    assert dist < 0 or abs(int(col2) - int(col)) <= dist
+                    pairs.add((c, int(k)))
+            assert all((k, c) in pairs for c, k in pairs)
+            for rm in range(off.size - 1):
+                cols = [b.zone_pos[z][2] for z in cells[off[rm]:off[rm + 1], 1]]
+                assert cols == sorted(cols)
