@@ -420,3 +420,41 @@ def test_gpu_bind_null_stream_returns_to_default(mixed_dir):
             want = po.action_row(SEED, i, step, e.n_cont, e.n_disc)
             assert np.array_equal(a[i].view(np.uint32), want.view(np.uint32)), (i, step)
     vec.close()
+
+
+def test_gpu_decode_edge_values(cfg0_dir):
+    """Action decode at its edges, bit for bit against the oracle's decode
+    (pufferlib_cpu_env.h:218-225 clamp, sb_sim.c:557-576 float32 span map,
+    sb_sim.c:220-244 routing clamps): exact end points, out-of-range values,
+    -0, a float32 subnormal, values one float step inside the ends, discrete
+    values other than 0 and 1, and NaN (which the reference's comparisons pass
+    through to the commands)."""
+    say("decode edge values: 3 envs, 2 steps")
+    vec = E.VecEnv(3, blob_dir=str(cfg0_dir), max_steps=50)
+    twins = [Twin(vec, i, 50) for i in range(vec.n)]
+    vec.reset()
+    for tw in twins:
+        tw.cpu.reset()
+    nc, nd = vec.envs[0].n_cont, vec.envs[0].n_disc
+    f1 = np.float32(1.0)
+    cont = np.array([-1.0, 1.0, 7.0, -7.0, -0.0, 1e-40, np.nextafter(f1, 0), -np.nextafter(f1, 0), 0.25, np.inf,
+                     -np.inf], np.float32)
+    disc = np.array([0.0, 1.0, 0.5, 2.0, -1.0, np.nextafter(f1, 2)], np.float32)
+    for s in range(2):
+        rows = np.zeros((vec.n, E.SB_ACT), np.float32)
+        for i in range(vec.n):
+            rows[i, :nc] = np.roll(cont, 3 * i + s)[np.arange(nc) % cont.size]
+            rows[i, 256:256 + nd] = np.roll(disc, i + s)[np.arange(nd) % disc.size]
+        rows[2, 5:nc:7] = np.nan              # env 2: NaN in some continuous slots
+        rows[2, 256] = np.nan
+        vec.actions.copy_(torch.from_numpy(rows))
+        vec.step()
+        torch.cuda.synchronize()
+        for tw in twins:
+            tw.cpu.step(rows[tw.i])
+            gs, cs = vec.state(tw.i), tw.cpu.state()
+            ix = tw.exact_state
+            assert np.array_equal(gs[ix], cs[ix], equal_nan=True), (s, tw.i, ix[~((gs[ix] == cs[ix]) | (np.isnan(gs[ix]) & np.isnan(cs[ix])))][:8])
+            if tw.i < 2:
+                state_close(gs, cs, f"decode edges step {s} env {tw.i}")
+    vec.close()
