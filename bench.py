@@ -11,12 +11,14 @@ own rows (sbx_step_actions, puf_step with a per-step action pointer), as the
 reference's bench feeds recorded action traces to its step. The JSON also
 reports the generator + step pair launched in turn (generator_and_step_us).
 K defaults to a full 8,640-step episode. Config 4 times the rollout: policy
-forward + Beta sampling, then puf_step, each step.
+forward + Beta sampling, then puf_step, each step. Configs 0-3 are timed a
+second time with the per-env sparse LU as the field solver (the "lu" record).
 
-roofline: algorithmic HBM bytes of one puf_step (per-env state record read and
-written, action row read, observation row + reward + terminal written; the
-shared per-layout/per-scenario tables are not counted) divided by the step
-kernel's mean duration: the timed region itself (it launches only step
+roofline: algorithmic HBM bytes of one puf_step (per env: the persistent state
+read and written -- T, per-VAV and per-AHU state, plant scalars, occupancy,
+interior mass -- the action row read, the observation prefix, reward and
+terminal written; the shared per-layout/per-scenario tables are not counted)
+divided by the step kernel's mean duration: the timed region itself (it launches only step
 kernels, back to back on the bound stream) for configs 0-3; for config 4, HIP
 event pairs recorded around every 16th step-kernel launch (bracketing every
 launch would add queue markers that slow the loop itself). traffic: HBM bytes per launch
@@ -146,6 +148,7 @@ def main() -> int:
     ap.add_argument("--kernel-iters", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-lu", action="store_true", help="skip the second timing under the LU solver")
     ap.add_argument("--solver", default="auto", choices=["auto", "relax", "point", "lu"])
     ap.add_argument("--conv", type=float, default=0.0,
                     help="stochastic convection on with this swap probability (not a BASELINE config)")
@@ -164,12 +167,12 @@ def main() -> int:
     from neurips2026_smart_building_challenge_amd import env as E
     from neurips2026_smart_building_challenge_amd.scenario import generate as G
 
-    scen, n_envs, desync = G.config_scenarios(args.config)
+    scen, n_envs, offsets = G.config_scenarios(args.config)
     groups = len(scen)
     t0 = time.time()
     blob_dir = scenario_dir(args.config, args.conv)
     log(f"scenarios ready in {time.time() - t0:.1f}s: {blob_dir}")
-    vec = E.VecEnv(n_envs, blob_dir=str(blob_dir), groups=groups, desync=int(desync), solver=args.solver)
+    vec = E.VecEnv(n_envs, blob_dir=str(blob_dir), groups=groups, start_offsets=int(offsets), solver=args.solver)
     info = vec.info()
     rollout = args.config == 4
     if rollout:
@@ -213,6 +216,33 @@ def main() -> int:
     ev1.record(stream)
     torch.cuda.synchronize()
     ms = ev0.elapsed_time(ev1)
+    lu = None
+    if not rollout and args.solver == "auto" and not args.no_lu:
+        # the north star's per-env sparse LU (numeric refactorization + both
+        # triangular solves every step) on the same envs and action rows
+        lvec = E.VecEnv(n_envs, blob_dir=str(blob_dir), groups=groups, start_offsets=int(offsets), solver="lu")
+        lvec.reset()
+        for s in range(args.warmup):
+            lvec.gen_actions(SEED, s)
+            lvec.step()
+        torch.cuda.synchronize()
+        ev0.record(stream)
+        for s in range(args.steps):
+            lvec.step_actions(bank[s])
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        lms = ev0.elapsed_time(ev1)
+        linfo = lvec.info()
+        l_us = lms / args.steps * 1e3
+        l_ach = linfo.bytes_per_step / (l_us * 1e-6) / 1e9
+        lu = {"solver": "lu", "ms_per_step": lms / args.steps, "value": n_envs * args.steps / (lms / 1e3),
+              "unit": "env-steps/s", "steps": args.steps,
+              "roofline": {"bound": "hbm", "achieved": l_ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": l_ach / HBM_PEAK_GBS, "kernel_us": l_us,
+                           "algorithmic_bytes": linfo.bytes_per_step},
+              "solve_flops_per_step": linfo.flops_per_step}
+        log(f"LU solver: {l_us:.1f} us/step, {lu['value']:.4g} env-steps/s")
+        lvec.close()
     if rollout:
         k_us, k_n = vec.kernel_timer(0)
         k_src = "HIP event pairs around every 16th step-kernel launch of the timed region"
@@ -250,9 +280,13 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu:
-        threads = min(16, os.cpu_count() or 1)
-        log(f"cpu baseline on {threads} threads ...")
+        # every core the process may run on, up to the 16-core CPU share a
+        # one-GPU box of this pool grants a job (a process pool must not exceed it)
+        visible = len(os.sched_getaffinity(0))
+        threads = min(16, visible)
+        log(f"cpu baseline on {threads} threads ({visible} cores visible) ...")
         cpu = cpu_baseline(blob_dir, n_envs, groups, args.cpu_seconds, threads)
+        cpu["cores_visible"] = visible
         log(f"cpu baseline: {cpu['value']:.4g} env-steps/s ({cpu['kind']})")
 
     out = {
@@ -264,7 +298,7 @@ def main() -> int:
                                f"climates), "
                                + ("shared-policy MLP 1024-128-128-544 (fp32 MFMA) + Beta sampling per step, "
                                   if rollout else "Beta(2,2) actions, ")
-                               + "fp64 physics" + (", desynchronised starts" if desync else "")
+                               + "fp64 physics" + (", desynchronised starts (seeded per-env calendar offsets)" if offsets else "")
                                + (f", stochastic convection p={args.conv}" if args.conv > 0 else ""),
                    "n_envs": n_envs, "scenarios": groups, "episode_steps": G.EPISODE_STEPS,
                    "solver": solver["solver"], "envs_per_workgroup": info.envs_per_block,
@@ -275,9 +309,11 @@ def main() -> int:
                      "back_to_back_us": b2b_us,
                      "generator_and_step_us": gen_step_us,
                      "algorithmic_bytes": info.bytes_per_step,
+                     "record_bytes": info.record_bytes_per_step,
                      "relax_sweeps_mean": (sum(sweeps) / len(sweeps)) if solver["solver"] != "lu" else None,
                      "phase_us_mean": {k: round(m, 2) for k, (m, x) in phases.items()}},
         "cpu_baseline": cpu,
+        "lu": lu,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -104,7 +104,18 @@ typedef struct Dict {
 DictItem* dict_find(Dict* d, const char* key);
 void dict_set(Dict* d, const char* key, float value);
 
-/* ---- PufferLib env ABI ---- */
+/* ---- PufferLib env ABI ----
+ * puf_vec_create kwargs ([env] section): blob | blob_dir (or SB_BLOB_DIR),
+ * groups, max_steps, reward_scale (<= 0 means 1), desync (1: each env's first
+ * episode ends at a hashed step in [1, episode length] and stays out of the
+ * episode log; smart_buildings.cu:2583-2590, 2808-2815, 1990-1993), and the
+ * reference keys this env does not implement, accepted only at 0 (random_start,
+ * rew_norm, rew_center, canonical, residual, plant_pair, guard_d1, guard_hot,
+ * comfort_shape, zone_*, ahu_critic, interleave, prestart_explore, probe).
+ * Extras: start_offsets (1: every env starts its episodes at its own seeded
+ * calendar offset, start_seed), shard_base (this vec's first env index in a
+ * batch sharded over several vecs), per_env_seed (occupancy / convection seed
+ * + index within the scenario, default 1), solver, envs_per_block. */
 Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions,
                     float* rewards, float* terminals);
 /* NULL binds the null stream (the binding before any call); the reference
@@ -134,9 +145,14 @@ typedef struct SbxVecInfo {
     int block;              /* threads per workgroup (128 per env: two wavefronts) */
     int lds_bytes;          /* dynamic LDS per workgroup */
     int max_nodes;
-    double bytes_per_step;  /* algorithmic HBM bytes of one puf_step (all envs) */
+    double bytes_per_step;  /* algorithmic HBM bytes of one puf_step (all envs): per env the
+                               persistent state read and written (T, per-VAV and per-AHU
+                               state, plant scalars, occupancy; interior mass where present),
+                               the action row, the observation prefix, reward and terminal */
     double flops_per_step;  /* fp64 flops of one puf_step's solves (all envs) */
     int envs_per_block;     /* envs sharing a workgroup (two wavefronts each) */
+    double record_bytes_per_step;   /* what the kernel's per-env record round trip moves for
+                                       the same (its record image is wider than the state) */
 } SbxVecInfo;
 void sbx_vec_info(Env* envs, SbxVecInfo* out);
 
@@ -246,8 +262,9 @@ int sbx_beta_eval(Env* envs, const float* y, const float* draws, float* logp, fl
 
 /* The heads' Beta sampler alone: out[i] ~ Beta(alpha[i], beta[i]) for device
  * arrays of n floats (alpha, beta >= 1), counter (i, 0, 0 or 1, 1 + attempt),
- * on the bound stream. Returns 0, or -1. */
-int sbx_beta_sample(const float* alpha, const float* beta, float* out, int n, uint64_t seed);
+ * on `stream` (hipStream_t; NULL = the null stream). Leaves the stream bound
+ * by puf_bind_stream alone. Returns 0, or -1. */
+int sbx_beta_sample(const float* alpha, const float* beta, float* out, int n, uint64_t seed, void* stream);
 
 /* Scenario of env i (index into the sorted, round-robin ordered blob list),
  * its calendar start offset and occupancy seed. */

@@ -1,6 +1,7 @@
 // Internal layout shared by the host planner (vec.cpp, plan.cpp) and the HIP
 // step kernel (step_kernel.hip). Not part of the public ABI.
 #pragma once
+#include <stddef.h>
 #include <stdint.h>
 
 // Read-only device tables live in the constant address space when compiled for
@@ -67,8 +68,10 @@ enum { SOLVER_LU = 0, SOLVER_RELAX = 1 };
 // solver, which keeps the instruction footprint of a launch small); a launch
 // covers the tiles whose layouts use that form.
 enum { KV_LU = 0, KV_POINT = 1, KV_BLOCK = 2, KV_COUNT = 3 };
+// PI_FIRST_DONE: 1 once the env's first episode after puf_vec_create has
+// ended (puf_reset leaves it; the first episode is the one desync truncates)
 enum { PI_HWS_RUN = 0, PI_PUMP_RUN, PI_HWS_REQ, PI_STEP_INDEX, PI_STEP, PI_MT_IDX,
-       PI_STEPS_TOTAL, PI_EPISODES, PI_CONV_IDX, PI_COUNT = 16 };
+       PI_STEPS_TOTAL, PI_EPISODES, PI_CONV_IDX, PI_FIRST_DONE, PI_COUNT = 16 };
 
 // Per-env LDS region (byte offsets from the env's base; a workgroup holds the
 // layout image first, then one region per env).
@@ -233,8 +236,11 @@ struct DevLayout {
     const SBK_C int* f_idx;
     const SBK_C double* f_mean;
     const SBK_C double* f_sd;          // sqrt(var) or 0 when var <= 0
-    // bytes of algorithmic traffic per env-step
+    // bytes of algorithmic traffic per env-step (the persistent state, the
+    // action row, the observation prefix, reward and terminal), and what the
+    // kernel's record image round trip moves for them
     double bytes_per_step;
+    double record_bytes_per_step;
     double solve_flops;
 };
 
@@ -286,7 +292,8 @@ struct EnvDesc {
     // staging burst inputs, copied from the scenario so the burst can be
     // issued from this record alone
     int scn16;                   // scenario image size in 16-byte units
-    int pad;
+    int first_steps;             // length of the env's first episode after puf_vec_create (desync
+                                 // truncates it; = max_steps otherwise)
     const SBK_C unsigned char* scen_src;   // scenario image in HBM
 };
 
@@ -339,5 +346,20 @@ struct KParams {
     unsigned long long* pass_ts;    // null, or [n_pass + 1] shader-clock stamps of one env
     int pass_ts_env;                // env whose solve passes are stamped
 };
+
+// The host (g++) and the device (hipcc) compile these structs separately and
+// exchange them byte for byte: both builds check the same sizes and offsets.
+static_assert(sizeof(EnvDesc) == 40 && offsetof(EnvDesc, state_off) == 8 && offsetof(EnvDesc, first_steps) == 28
+              && offsetof(EnvDesc, scen_src) == 32, "EnvDesc layout");
+static_assert(sizeof(Tile) == 240 && offsetof(Tile, img_src) == 48 && offsetof(Tile, env) == 64
+              && offsetof(Tile, desc) == 80, "Tile layout");
+static_assert(sizeof(StateLayout) == 120 && sizeof(LdsLayout) == 96 && sizeof(ImgLayout) == 188
+              && sizeof(ScenImg) == 24, "table layouts");
+static_assert(sizeof(DevLayout) == 888 && offsetof(DevLayout, st) == 88 && offsetof(DevLayout, img_src) == 496
+              && offsetof(DevLayout, bytes_per_step) == 864, "DevLayout layout");
+static_assert(sizeof(DevScen) == 472 && offsetof(DevScen, img_src) == 32 && offsetof(DevScen, gas_co2) == 200
+              && offsetof(DevScen, conv_p) == 464, "DevScen layout");
+static_assert(sizeof(KParams) == 136 && offsetof(KParams, host_env) == 80 && offsetof(KParams, phase_ts) == 112
+              && offsetof(KParams, pass_ts_env) == 128, "KParams layout");
 
 }  // namespace sbk

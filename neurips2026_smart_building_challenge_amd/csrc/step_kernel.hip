@@ -658,7 +658,7 @@ __device__ __forceinline__ void obs_specials(Ctx& c, double amb) {
 // its host-resolved source, normalised as (f32(v) - mean) / sd; fields are
 // taken four per lane at a time so their LDS reads overlap.
 template <int W>
-__device__ __forceinline__ void write_obs(Ctx& c, float* row, double amb, const double* aux) {
+__device__ __forceinline__ void write_obs(Ctx& c, float* row, double amb, const double* aux, bool tail) {
 #pragma clang fp contract(off)
     obs_specials<W>(c, amb);
     const SBK_C DevLayout* L = c.L;
@@ -696,7 +696,10 @@ __device__ __forceinline__ void write_obs(Ctx& c, float* row, double amb, const 
     for (int z = ln(); z < L->nz; z += W) occ += c.occV[z];
     occ = bisum<W>(occ, c.red);
     if (ln() == 0) row[L->n_dev + na - 1] = (float)occ;
-    for (int i = L->n_dev + na + ln(); i < 1024; i += W) __builtin_nontemporal_store(0.0f, row + i);
+    // the row's padding past the observation is zeroed by puf_reset only: no
+    // step writes there afterwards (the reference GPU env writes obs_len floats)
+    if (tail)
+        for (int i = L->n_dev + na + ln(); i < 1024; i += W) __builtin_nontemporal_store(0.0f, row + i);
 }
 
 // ------------------------------------------------------------------ occupancy
@@ -1197,9 +1200,10 @@ __device__ __forceinline__ void sim_reset(Ctx& c, int start) {
     esync();
 }
 
-// puf_reset sequence (pufferlib_cpu_env.h:187-208) at the env's start offset.
+// puf_reset sequence (pufferlib_cpu_env.h:187-208) at the env's start offset;
+// tail: also zero the observation row's padding (puf_reset, not auto-reset).
 template <int W>
-__device__ __forceinline__ void env_reset(Ctx& c, int start, float* obs_row) {
+__device__ __forceinline__ void env_reset(Ctx& c, int start, float* obs_row, bool tail) {
     const SBK_C DevScen* S = c.S;
     const RowVals first = row_issue<W>(c, start, start + 1);   // the new episode's first step
     sim_reset<W>(c, start);
@@ -1209,7 +1213,7 @@ __device__ __forceinline__ void env_reset(Ctx& c, int start, float* obs_row) {
     for (int k = 0; k < 2; k++) {
         occupancy_advance<W>(c, k == 0 ? S->hour_m1[start] : S->occ_hour[start],
                              k == 0 ? S->work_m1[start] : S->occ_work[start], c.occ_state, c.occV);
-        if (k == 0) write_obs<W>(c, obs_row, S->amb[start], S->aux_time + (size_t)start * (c.L->n_aux - 1));
+        if (k == 0) write_obs<W>(c, obs_row, S->amb[start], S->aux_time + (size_t)start * (c.L->n_aux - 1), tail);
     }
     row_store<W>(c, first, cal_section(c, start));
     esync();
@@ -2499,7 +2503,7 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
         env_wait(sy + SY_PRE, 1);
         row_store<W>(c, next, cal_section(c, kk + 1));
     }
-    write_obs<W>(c, obs_row, c.row[RW_AMB_J], c.row + RW_COUNT);
+    write_obs<W>(c, obs_row, c.row[RW_AMB_J], c.row + RW_COUNT, false);
     for (int i = ln(); i < nocc; i += W) c.occ_state[i] = st_new[i];
     for (int z = ln(); z < L->nz; z += W) c.occV[z] = v_new[z];
     STAMP(16);
@@ -2657,15 +2661,23 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
         const double rew = reward_combine(c, blower, cooling, part);
         const float r = (float)rew;
         const int step = c.ip[PI_STEP] + 1;
-        done = step >= ed.max_steps;
+        // the first episode after puf_vec_create may be cut short (desync); a
+        // cut episode is a truncation and stays out of the episode log
+        // (complete_port/gpu/smart_buildings.cu:1990-1993, 2043)
+        const bool first = c.ip[PI_FIRST_DONE] == 0;
+        const bool cut = first && ed.first_steps < ed.max_steps;
+        done = step >= (first ? ed.first_steps : ed.max_steps);
         if (ln() == 0) {
             P.rewards[e] = r * P.reward_scale;
             P.terminals[e] = done ? 1.0f : 0.0f;
             c.ip[PI_STEP] = step;
             c.plant[PF_REW_SUM] += rew;
             c.ip[PI_STEPS_TOTAL] += 1;
-            if (done) c.ip[PI_EPISODES] += 1;
-            if (P.host_env) {
+            if (done) {
+                c.ip[PI_EPISODES] += 1;
+                c.ip[PI_FIRST_DONE] = 1;
+            }
+            if (P.host_env && !cut) {
                 Log* hlog = reinterpret_cast<Log*>(reinterpret_cast<unsigned char*>(P.host_env)
                                                    + (size_t)e * P.env_stride + P.log_offset);
                 const float* lg = reinterpret_cast<const float*>(sy + SY_LOG);
@@ -2690,7 +2702,7 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
         esync();
     }
     if (reset_mode || done) {
-        env_reset<W>(c, ed.start, obs_row);
+        env_reset<W>(c, ed.start, obs_row, reset_mode);
         if (reset_mode && ln() == 0) {
             c.ip[PI_STEP] = 0;
             c.ip[PI_STEPS_TOTAL] = 0;
@@ -2733,9 +2745,45 @@ __global__ void gen_actions_kernel(float* actions, const int* n_cont, const int*
     }
 }
 
+// puf_live_log's totals over every env in one workgroup: out[0] the f64 sum
+// of rewards since puf_reset, out[1] env-steps since puf_reset, out[2]
+// episodes ended since puf_reset. Each thread sums envs t, t + 256, ... in
+// ascending order, then a fixed tree: the result does not depend on timing.
+__global__ __launch_bounds__(256) void live_sums_kernel(const EnvDesc* envs, const DevLayout* layouts,
+                                                        const unsigned char* state, int n, double* out) {
+    __shared__ double red[3][256];
+    const int t = (int)threadIdx.x;
+    double rs = 0.0, st = 0.0, ep = 0.0;
+    for (int i = t; i < n; i += 256) {
+        const EnvDesc& d = envs[i];
+        const DevLayout* L = layouts + d.layout;
+        const unsigned char* r = state + d.state_off;
+        rs += reinterpret_cast<const double*>(r + L->st.plant)[PF_REW_SUM];
+        const int* ip = reinterpret_cast<const int*>(r + L->st.iplant);
+        st += (double)ip[PI_STEPS_TOTAL];
+        ep += (double)ip[PI_EPISODES];
+    }
+    red[0][t] = rs;
+    red[1][t] = st;
+    red[2][t] = ep;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if (t < w)
+            for (int q = 0; q < 3; q++) red[q][t] += red[q][t + w];
+        __syncthreads();
+    }
+    if (t < 3) out[t] = red[t][0];
+}
+
 }  // namespace sbk
 
 // ---------------------------------------------------------------- launchers
+extern "C" int sbk_launch_live_sums(const sbk::EnvDesc* envs, const sbk::DevLayout* layouts,
+                                    const unsigned char* state, int n, double* out, hipStream_t s) {
+    hipLaunchKernelGGL(sbk::live_sums_kernel, dim3(1), dim3(256), 0, s, envs, layouts, state, n, out);
+    return (int)hipGetLastError();
+}
+
 // threads: 128 per env of a tile (two wavefronts; at most 4 envs per workgroup).
 extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int threads, int lds_bytes, int variant,
                                hipStream_t s) {

@@ -38,6 +38,8 @@ extern "C" int sbk_launch_beta_eval(const float* y, const float* draws, const in
                                     hipStream_t s);
 extern "C" int sbk_launch_beta_sample(const float* alpha, const float* beta, float* out, int n, uint64_t seed,
                                       hipStream_t s);
+extern "C" int sbk_launch_live_sums(const sbk::EnvDesc* envs, const sbk::DevLayout* layouts,
+                                    const unsigned char* state, int n, double* out, hipStream_t s);
 extern "C" int sbk_launch_gen_actions(float* actions, const int* n_cont, const int* n_disc, int n_envs,
                                       uint64_t seed, uint32_t step, hipStream_t s);
 
@@ -378,10 +380,27 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     D.cv_rooms = cv_node.empty() ? 0 : (int)cv_off.size() - 1;
     D.cv_cells = (int)cv_node.size();
     D.cv_max_room = cv_max_room;
-    // algorithmic bytes: the state image without the calendar prefetch, which
-    // is a copy of shared per-scenario tables
-    D.bytes_per_step = 2.0 * (S.bytes - 16.0 * S.cal_n) + 4.0 * (ncont + ndisc) + 4.0 * SB_OBS + 8.0;
-    if (S.cmt) D.bytes_per_step += 4.0 * SBK_MT_N;   // the convection stream state, read every step
+    // algorithmic bytes of one env-step: the persistent state a step must read
+    // and write (T [8n], per VAV 7 f64 and a flag byte [57 nv], per AHU 3 f64
+    // and a flag byte [25 na], 48 B of plant scalars, occupant counts [nz] and
+    // chain bits [nz * nassign / 8]; interior mass [8n] where any node has
+    // it), the action row read, the observation prefix (n_dev + n_aux floats),
+    // reward and terminal written; shared per-layout and per-scenario tables
+    // are not counted (one copy serves every env of the layout or scenario)
+    {
+        bool mass = false;
+        const double* mc = b.f64("mass_coupling");
+        const double* mg = b.f64("mass_gained");
+        for (int t = 0; t < n && !mass; t++) mass = mc[t] != 0.0 || mg[t] != 0.0;
+        const double state = 8.0 * n + 57.0 * nv + 25.0 * na + 48.0 + nz + (nz * nassign + 7) / 8 + (mass ? 8.0 * n : 0.0);
+        D.bytes_per_step = 2.0 * state + 4.0 * n_act + 4.0 * (n_dev + n_aux) + 8.0;
+        if (S.cmt) D.bytes_per_step += 4.0 * SBK_MT_N;   // the convection stream state, read every step
+    }
+    // what this kernel actually moves for it: the record image (without the
+    // calendar prefetch, a copy of shared per-scenario tables) read and
+    // written, the action row, the observation prefix, reward and terminal
+    D.record_bytes_per_step = 2.0 * (S.bytes - 16.0 * S.cal_n) + 4.0 * (ncont + ndisc) + 4.0 * (n_dev + n_aux) + 8.0;
+    if (S.cmt) D.record_bytes_per_step += 4.0 * SBK_MT_N;
     D.solve_flops = 2.0 * (double)P.n_pairs + (double)P.n_divs;
     if (use_block) {   // per sweep: off-block multiply-subtracts, then each block's inverse applied
         long long nnz = 0, dense = 0;
@@ -896,7 +915,7 @@ struct Vec {
     float* actions = nullptr;
     float* rewards = nullptr;
     float* terminals = nullptr;
-    double bytes_per_step = 0.0, flops_per_step = 0.0;
+    double bytes_per_step = 0.0, record_bytes_per_step = 0.0, flops_per_step = 0.0;
     // step-kernel timer: an event pair around each puf_step launch while on
     std::vector<hipEvent_t> tev;
     int t_on = 0, t_used = 0, t_seen = 0;   // t_on: sampling period (0 = off)
@@ -904,6 +923,8 @@ struct Vec {
     SbxPolicy pol{};
     float *p_h1 = nullptr, *p_h2 = nullptr, *p_y = nullptr;
     float *p_hlp = nullptr, *p_hent = nullptr;   // per-head log-densities and entropies [n][SB_ACT]
+    double* d_live = nullptr;                    // puf_live_log totals (device, 3 f64)
+    double* h_live = nullptr;                    // and their pinned host copy
 };
 
 constexpr int kTimerPairs = 16384;
@@ -992,6 +1013,30 @@ const char* kws(Dict* d, const char* key) {
     return (it && it->str && it->str[0]) ? it->str : nullptr;
 }
 
+// [env] keys of the reference GPU env (complete_port/gpu/smart_buildings.cu:
+// 2590-2720, complete_port/config/smart_buildings.ini [env]) whose behaviour
+// this build does not have: each is accepted at its inert value (0, as the
+// reference ini ships them) and aborts with a message otherwise, so a trainer
+// config never gets a different environment without notice. Keys that only
+// parameterise one of these (center_beta, plant_eps, res_scale, res_dscale,
+// guard_d0, shape_gamma, random_start_seed) and merge_weathers (how the
+// reference groups scenarios for its solver: no effect on results) are
+// accepted at any value.
+void check_env_keys(Dict* d) {
+    static const char* const unsupported[] = {
+        "random_start", "rew_norm", "rew_center", "canonical", "residual", "plant_pair", "guard_d1",
+        "guard_hot", "comfort_shape", "zone_memory", "interleave", "zone_adv", "zone_critic", "ahu_critic",
+        "zone_command", "prestart_explore", "probe", "zone_signed", "zone_night_share",
+    };
+    if (!d) return;
+    for (const char* k : unsupported) {
+        DictItem* it = dict_find(d, k);
+        if (it && it->value != 0.0f)
+            die(std::string("env.") + k + " = " + std::to_string(it->value)
+                + " is not supported by this env (only its default, 0)");
+    }
+}
+
 void mt_seed(uint32_t* mt, uint32_t seed) {
     mt[0] = seed;
     for (int i = 1; i < SBK_MT_N; i++) mt[i] = 1812433253u * (mt[i - 1] ^ (mt[i - 1] >> 30)) + (uint32_t)i;
@@ -1032,7 +1077,12 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
     v->terminals = terminals;
     v->width = (int)kw(kwargs, "block", 64.0f);
     if (v->width != 64) die("env.block must be 64 (one wavefront per env)");
-    v->reward_scale = kw(kwargs, "reward_scale", 1.0f);
+    // a reward_scale <= 0 means 1 (complete_port/gpu/smart_buildings.cu:2595-2596)
+    {
+        const float rs = kw(kwargs, "reward_scale", 1.0f);
+        v->reward_scale = rs > 0.0f ? rs : 1.0f;
+    }
+    check_env_keys(kwargs);
     // ---- scenario list
     std::vector<std::string> files;
     if (const char* one = kws(kwargs, "blob")) {
@@ -1089,8 +1139,19 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
     }
     // ---- envs
     const int max_steps_kw = (int)kw(kwargs, "max_steps", 0.0f);
+    // desync = 1: every env's first episode ends at a hashed step in
+    // [1, episode length]; later episodes have the full length
+    // (complete_port/gpu/smart_buildings.cu:2583-2590, 2808-2815)
     const int desync = (int)kw(kwargs, "desync", 0.0f);
-    const uint64_t desync_seed = (uint64_t)kw(kwargs, "desync_seed", 7.0f);
+    // start_offsets = 1: every env starts its episodes at its own seeded
+    // calendar offset (the BASELINE's desynchronised starts; no reference key)
+    const int start_offsets = (int)kw(kwargs, "start_offsets", 0.0f);
+    const uint64_t start_seed = (uint64_t)kw(kwargs, "start_seed", 7.0f);
+    // shard_base: index of this vec's first env in a batch sharded over
+    // several vecs, so env-keyed draws (desync, start offsets) match the whole
+    // batch's
+    const int shard_base = (int)kw(kwargs, "shard_base", 0.0f);
+    if (shard_base < 0) die("env.shard_base must be >= 0");
     const int per_env_seed = (int)kw(kwargs, "per_env_seed", 1.0f);
     size_t state_off = 0;
     int e = 0;
@@ -1105,12 +1166,21 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
             d.layout = S.layout;
             d.max_steps = ms;
             d.state_off = (long long)state_off;
+            const uint64_t gid = (uint64_t)shard_base + (uint64_t)e;   // env index in the whole batch
             int start = 0;
-            if (desync) {
+            if (start_offsets) {
                 int range = S.n1 - 1 - ms + 1;
-                if (range < 1) die(S.path + ": calendar too short for desynchronised starts");
+                if (range < 1) die(S.path + ": calendar too short for start offsets");
                 range = std::min(range, std::max(S.episode_steps, 1));
-                start = (int)(splitmix64(desync_seed * 0x100000001B3ull + (uint64_t)e) % (uint64_t)range);
+                start = (int)(splitmix64(start_seed * 0x100000001B3ull + gid) % (uint64_t)range);
+            }
+            d.first_steps = ms;
+            if (desync) {
+                uint64_t h = 0x9E3779B97F4A7C15ull * (gid + 1);
+                h ^= h >> 31;
+                h *= 0xBF58476D1CE4E5B9ull;
+                h ^= h >> 29;
+                d.first_steps = 1 + (int)(h % (uint64_t)ms);
             }
             if (start + ms > S.n1 - 1) die(S.path + ": calendar tables shorter than the episode");
             if (start >= S.hour_m1_rows) die(S.path + ": occ_hour_m1 has no row for the start offset");
@@ -1242,11 +1312,14 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
                 mt_seed(reinterpret_cast<uint32_t*>(r + L.st.cmt), v->conv_seeds[i]);
             }
             v->bytes_per_step += L.bytes_per_step;
+            v->record_bytes_per_step += L.record_bytes_per_step;
             v->flops_per_step += L.solve_flops;
         }
         hip_ok(hipMalloc(&v->d_state, v->state_bytes), "hipMalloc(state)");
         hip_ok(hipMemcpy(v->d_state, rec.data(), v->state_bytes, hipMemcpyHostToDevice), "upload state");
     }
+    hip_ok(hipMalloc(&v->d_live, 3 * sizeof(double)), "hipMalloc(live log)");
+    hip_ok(hipHostMalloc(&v->h_live, 3 * sizeof(double), hipHostMallocDefault), "hipHostMalloc(live log)");
     // ---- Env array (host memory the device can write: logs)
     void* envmem = nullptr;
     hip_ok(hipHostMalloc(&envmem, sizeof(Env) * (size_t)n, hipHostMallocCoherent), "hipHostMalloc(envs)");
@@ -1342,6 +1415,8 @@ void puf_close(Env* envs) {
     (void)hipFree(v->p_hent);
     (void)hipFree(v->d_ncont);
     (void)hipFree(v->d_ndisc);
+    (void)hipFree(v->d_live);
+    (void)hipHostFree(v->h_live);
     (void)hipHostFree(v->envs);
     if (g_last == v) g_last = nullptr;
     delete v;
@@ -1356,26 +1431,19 @@ void puf_log(Log* log, Dict* out) {
     dict_set(out, "n", log->n);
 }
 
+// Totals over every env since puf_reset (complete_port/gpu/smart_buildings.cu:
+// 3069-3100 reports the same kind of live counters): one device reduction and
+// one 24-byte copy on the bound stream, then a synchronisation.
 void puf_live_log(Env* envs, Dict* out) {
     Vec* v = vec_of(envs);
+    int rc = sbk_launch_live_sums(v->d_envs, v->d_layouts, v->d_state, v->n, v->d_live, g_stream);
+    if (rc != 0) die("live log kernel launch failed");
+    hip_ok(hipMemcpyAsync(v->h_live, v->d_live, 3 * sizeof(double), hipMemcpyDeviceToHost, g_stream), "live log");
     hip_ok(hipStreamSynchronize(g_stream), "live log");
-    double rs = 0.0;
-    long long st = 0, eps = 0;
-    std::vector<unsigned char> img;
-    for (int i = 0; i < v->n; i++) {
-        const sbk::EnvDesc& d = v->desc[i];
-        const sbk::DevLayout& L = v->layouts[d.layout].dev;
-        double pf[8];
-        int ip[8];
-        hip_ok(hipMemcpy(pf, v->d_state + d.state_off + L.st.plant, sizeof(pf), hipMemcpyDeviceToHost), "copy");
-        hip_ok(hipMemcpy(ip, v->d_state + d.state_off + L.st.iplant, sizeof(ip), hipMemcpyDeviceToHost), "copy");
-        rs += pf[sbk::PF_REW_SUM];
-        st += ip[sbk::PI_STEPS_TOTAL];
-        eps += ip[sbk::PI_EPISODES];
-    }
+    const double rs = v->h_live[0], st = v->h_live[1], eps = v->h_live[2];
     dict_set(out, "env_steps", (float)st);
     dict_set(out, "episodes", (float)eps);
-    dict_set(out, "reward_mean", st ? (float)(rs / (double)st) : 0.0f);
+    dict_set(out, "reward_mean", st > 0.0 ? (float)(rs / st) : 0.0f);
 }
 
 void puf_mask_init(unsigned char* mask, int width, int nagents) {
@@ -1411,6 +1479,7 @@ void sbx_vec_info(Env* envs, SbxVecInfo* out) {
     out->envs_per_block = v->epb;
     for (auto& L : v->layouts) out->max_nodes = std::max(out->max_nodes, L.dev.n);
     out->bytes_per_step = v->bytes_per_step;
+    out->record_bytes_per_step = v->record_bytes_per_step;
     out->flops_per_step = v->flops_per_step;
 }
 
@@ -1640,9 +1709,9 @@ int sbx_policy_heads(Env* envs, float* out, int cap) {
     return (int)count;
 }
 
-int sbx_beta_sample(const float* alpha, const float* beta, float* out, int n, uint64_t seed) {
+int sbx_beta_sample(const float* alpha, const float* beta, float* out, int n, uint64_t seed, void* stream) {
     if (!alpha || !beta || !out || n <= 0) return -1;
-    int rc = sbk_launch_beta_sample(alpha, beta, out, n, seed, g_stream);
+    int rc = sbk_launch_beta_sample(alpha, beta, out, n, seed, (hipStream_t)stream);
     if (rc != 0) die(std::string("beta sample launch failed: ") + hipGetErrorString((hipError_t)rc));
     return 0;
 }

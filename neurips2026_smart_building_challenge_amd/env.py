@@ -4,7 +4,7 @@ Mirrors the PufferLib GPU env binding the reference exports
 (complete_port/gpu/smart_buildings.cu:3307-3323): `VecEnv` owns the trainer-side
 device buffers (torch tensors on the GPU), creates the env vec through
 puf_vec_create with the same kwargs (blob / blob_dir / groups / max_steps /
-desync / reward_scale ...), and steps it with puf_step on a bound stream.
+desync / start_offsets / reward_scale ...), and steps it with puf_step on a bound stream.
 
 There is no CPU fallback: loading fails loudly when libsbenv.so is missing.
 """
@@ -54,7 +54,7 @@ class SbxVecInfo(ctypes.Structure):
     _fields_ = [("n_envs", ctypes.c_int), ("n_layouts", ctypes.c_int), ("n_scenarios", ctypes.c_int),
                 ("block", ctypes.c_int), ("lds_bytes", ctypes.c_int), ("max_nodes", ctypes.c_int),
                 ("bytes_per_step", ctypes.c_double), ("flops_per_step", ctypes.c_double),
-                ("envs_per_block", ctypes.c_int)]
+                ("envs_per_block", ctypes.c_int), ("record_bytes_per_step", ctypes.c_double)]
 
 
 class SbxPlan(ctypes.Structure):
@@ -139,7 +139,7 @@ def lib() -> ctypes.CDLL:
         L.sbx_policy_bind.argtypes = [ctypes.POINTER(Env), ctypes.POINTER(SbxPolicy)]
         L.sbx_policy_act.argtypes = [ctypes.POINTER(Env), ctypes.c_uint64, ctypes.c_uint32]
         L.sbx_policy_heads.argtypes = [ctypes.POINTER(Env), P, ctypes.c_int]
-        L.sbx_beta_sample.argtypes = [P, P, P, ctypes.c_int, ctypes.c_uint64]
+        L.sbx_beta_sample.argtypes = [P, P, P, ctypes.c_int, ctypes.c_uint64, P]
         L.sbx_policy_act_logp.argtypes = [ctypes.POINTER(Env), ctypes.c_uint64, ctypes.c_uint32, P, P, P]
         L.sbx_beta_eval.argtypes = [ctypes.POINTER(Env), P, P, P, P, P]
         L.sbx_phase_stamps.argtypes = [ctypes.POINTER(Env), P, ctypes.c_int]
@@ -256,8 +256,8 @@ def beta_sample(alpha, beta, seed: int):
     beta = beta.contiguous()
     out = torch.empty_like(alpha)
     L = lib()
-    L.puf_bind_stream(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
-    if L.sbx_beta_sample(alpha.data_ptr(), beta.data_ptr(), out.data_ptr(), alpha.numel(), seed) != 0:
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    if L.sbx_beta_sample(alpha.data_ptr(), beta.data_ptr(), out.data_ptr(), alpha.numel(), seed, stream) != 0:
         raise RuntimeError("sbx_beta_sample failed")
     return out
 
@@ -361,6 +361,13 @@ class VecEnv:
         if self.L.sbx_policy_heads(self.envs, buf.ctypes.data_as(P), buf.size) < 0:
             raise RuntimeError("sbx_policy_heads failed")
         return buf.reshape(self.n, POLICY_HEADS)
+
+    def live_log(self) -> dict[str, float]:
+        """puf_live_log: env-steps, episodes and mean reward since puf_reset over every env."""
+        items = (DictItem * 8)()
+        d = Dict(ctypes.cast(items, ctypes.POINTER(DictItem)), 0, 8)
+        self.L.puf_live_log(self.envs, ctypes.byref(d))
+        return read_dict(d)
 
     def solve_info(self, i: int) -> dict[str, float]:
         """Field solver of env i: kind ("lu"/"point"/"block"), rho, sweeps of the last step, capped steps."""

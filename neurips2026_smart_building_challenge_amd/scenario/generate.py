@@ -13,7 +13,7 @@ csim ignores:
 
 Calendar tables hold `table_steps + 1` rows so that an episode of
 `episode_steps` may start at any offset in [0, table_steps - episode_steps]
-(desynchronised starts). occ_hour_m1 / occ_workday_m1 hold one row per start
+(per-env start offsets, the env kwarg start_offsets). occ_hour_m1 / occ_workday_m1 hold one row per start
 offset: the hour/workday of the interval before that start.
 """
 from __future__ import annotations
@@ -320,7 +320,9 @@ def climates() -> list[ClimateSpec]:
 
 
 def config_scenarios(config: int) -> tuple[list[tuple[LayoutSpec, ClimateSpec]], int, bool]:
-    """(scenarios, n_envs, desync) for the BASELINE configs 0..4 (0-based)."""
+    """(scenarios, n_envs, start_offsets) for the BASELINE configs 0..4 (0-based);
+    start_offsets: every env starts at its own seeded calendar offset (config 3,
+    BASELINE's "desync on")."""
     lays = [LayoutSpec(z, a) for z, a in LAYOUTS]
     if config == 0:
         return [(LayoutSpec(41, 1), ClimateSpec(10.0, 8.0, seed=499))], 1, False
@@ -356,5 +358,5 @@ def write_scenarios(scen: list[tuple[LayoutSpec, ClimateSpec]], out_dir,
 
 
 def write_config(config: int, out_dir, conv: ConvSpec | None = None) -> tuple[list[Path], int, bool]:
-    scen, n, desync = config_scenarios(config)
-    return write_scenarios(scen, out_dir, conv=conv), n, desync
+    scen, n, offsets = config_scenarios(config)
+    return write_scenarios(scen, out_dir, conv=conv), n, offsets

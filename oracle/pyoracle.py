@@ -62,6 +62,7 @@ class _Lib:
             for f in (L.sbo_env_obs_len, L.sbo_env_n_cont, L.sbo_env_n_disc):
                 f.argtypes = [P]
             L.sbo_env_log.argtypes = [P, P]
+            L.sbo_env_set_first_steps.argtypes = [P, ctypes.c_int]
             L.sbo_mt_seed.argtypes = [P, ctypes.c_uint32]
             L.sbo_mt_u32.argtypes = [P]
             L.sbo_mt_u32.restype = ctypes.c_uint32
@@ -147,7 +148,7 @@ class CpuEnv:
     """One env of either oracle, stepping with the reference CPU env protocol."""
 
     def __init__(self, kind: str, path, occ_seed: int, start: int = 0, max_steps: int = 8640,
-                 conv_seed: int | None = None):
+                 conv_seed: int | None = None, first_steps: int | None = None):
         self.kind = kind
         self.L = lib(kind)
         if conv_seed is None:
@@ -165,6 +166,10 @@ class CpuEnv:
                 self.n_disc = self.L.lib.sbo_env_n_disc(self.h)
         if not self.h:
             raise RuntimeError(f"cannot open env on {path}")
+        if first_steps is not None and first_steps != max_steps:
+            if kind == "ref":
+                raise ValueError("first-episode truncation is a GPU-env feature the reference CPU core lacks")
+            self.L.lib.sbo_env_set_first_steps(self.h, int(first_steps))
         self.obs = np.zeros(SB_OBS, np.float32)
         self._r = np.zeros(1, np.float32)
         self._t = np.zeros(1, np.float32)
@@ -209,6 +214,18 @@ class CpuEnv:
     def state(self) -> np.ndarray:
         n = self.L.state_fn(self.h, _ptr(self._st))
         return self._st[:n].copy()
+
+
+def desync_first_steps(env_index: int, episode_steps: int) -> int:
+    """Length of env `env_index`'s first episode under the GPU env's desync
+    (complete_port/gpu/smart_buildings.cu:2808-2815): a splitmix-style hash of
+    the env index mapped into [1, episode_steps]."""
+    m = (1 << 64) - 1
+    h = (0x9E3779B97F4A7C15 * (env_index + 1)) & m
+    h ^= h >> 31
+    h = (h * 0xBF58476D1CE4E5B9) & m
+    h ^= h >> 29
+    return 1 + h % episode_steps
 
 
 def action_row(seed: int, env: int, step: int, n_cont: int, n_disc: int, kind: str = "oracle") -> np.ndarray:

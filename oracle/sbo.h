@@ -135,6 +135,7 @@ typedef struct {
     double *rhs, *y, *yr, *r, *work, *power, *mat;
     /* bookkeeping (pufferlib_cpu_env.h Env) */
     int step, max_steps, start;
+    int first_steps, first_done;   /* first episode's length (desync truncation), 1 once it ended */
     float log[6];
     double native[SBO_CONT + SBO_DISC];
     double parts[12];
@@ -144,6 +145,7 @@ typedef struct {
 
 SboEnv* sbo_env_new(const SboScen* sc, uint32_t occ_seed, uint32_t conv_seed, int start, int max_steps);
 void sbo_env_free(SboEnv* e);
+void sbo_env_set_first_steps(SboEnv* e, int first_steps);
 void sbo_env_reset(SboEnv* e, float* obs_out);
 int sbo_env_step(SboEnv* e, const float* actions, float* obs_out, float* reward, float* terminal);
 int sbo_env_state(const SboEnv* e, double* out);

@@ -956,8 +956,14 @@ SboEnv* sbo_env_new(const SboScen* s, uint32_t occ_seed, uint32_t conv_seed, int
     e->cv_right = zalloc((size_t)s->cv_max_room, 4);
     e->start = start;
     e->max_steps = max_steps;
+    e->first_steps = max_steps;
     return e;
 }
+
+/* The GPU env's desync (complete_port/gpu/smart_buildings.cu:2808-2815): the
+ * env's first episode ends after first_steps steps, a truncation that leaves
+ * the episode log alone (:1990-1993); later episodes have max_steps. */
+void sbo_env_set_first_steps(SboEnv* e, int first_steps) { e->first_steps = first_steps; }
 
 void sbo_env_free(SboEnv* e) {
     if (!e) return;
@@ -1006,17 +1012,23 @@ int sbo_env_step(SboEnv* e, const float* act, float* obs_out, float* reward_out,
     double rew = reward(e, j);
     e->last_rew = rew;
     float r = (float)rew;
-    int done = e->step >= e->max_steps;
+    const int cut = !e->first_done && e->first_steps < e->max_steps;
+    int done = e->step >= (e->first_done ? e->max_steps : e->first_steps);
     if (reward_out) *reward_out = r;
     if (term_out) *term_out = done ? 1.0f : 0.0f;
-    e->log[2] += r;
-    e->log[4] += (r - e->log[4]) / (float)e->step;
+    if (!cut) {
+        e->log[2] += r;
+        e->log[4] += (r - e->log[4]) / (float)e->step;
+    }
     if (done) {
-        float mean = e->log[2] / (float)e->step;
-        e->log[0] += mean;
-        e->log[1] += mean;
-        e->log[3] += (float)e->step;
-        e->log[5] += 1.0f;
+        if (!cut) {
+            float mean = e->log[2] / (float)e->step;
+            e->log[0] += mean;
+            e->log[1] += mean;
+            e->log[3] += (float)e->step;
+            e->log[5] += 1.0f;
+        }
+        e->first_done = 1;
         sbo_env_reset(e, NULL);
     }
     if (obs_out) memcpy(obs_out, e->obs, sizeof(float) * SBO_OBS);

@@ -43,3 +43,25 @@ def test_struct_layout_matches_header():
     assert ctypes.sizeof(E.Log) == 24
     assert E.Env.log.offset == 0
     assert E.lib().sbx_version().startswith(b"sbenv")
+
+
+def test_unsupported_env_key_aborts():
+    """A reference [env] key this env does not implement, set to anything but its
+    default, stops puf_vec_create with a message before any device call."""
+    import subprocess
+    import sys
+
+    code = ("import ctypes; from neurips2026_smart_building_challenge_amd import env as E; "
+            "kw = E.Kwargs(blob='/nonexistent.sbb', {key}={val}); "
+            "E.lib().puf_vec_create(1, kw.ptr(), ctypes.c_void_p(64), ctypes.c_void_p(64), "
+            "ctypes.c_void_p(64), ctypes.c_void_p(64)); print('created')")
+    root = str(Path(__file__).resolve().parents[1])
+    for key in ("rew_norm", "canonical", "random_start", "zone_memory", "comfort_shape"):
+        r = subprocess.run([sys.executable, "-c", code.format(key=key, val=1)], cwd=root, capture_output=True,
+                           text=True, timeout=120)
+        assert r.returncode != 0 and "created" not in r.stdout, (key, r.stdout, r.stderr)
+        assert f"env.{key}" in r.stderr and "not supported" in r.stderr, (key, r.stderr)
+    # at the default the key passes the check (the missing blob is the next error)
+    r = subprocess.run([sys.executable, "-c", code.format(key="rew_norm", val=0)], cwd=root, capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode != 0 and "not supported" not in r.stderr and "nonexistent" in r.stderr, r.stderr

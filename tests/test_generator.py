@@ -85,10 +85,10 @@ def test_calendar_and_weather():
 
 
 def test_configs():
-    scen, n, desync = G.config_scenarios(1)
-    assert n == 960 and len(scen) == 30 and not desync
-    scen, n, desync = G.config_scenarios(3)
-    assert n == 16384 and desync
+    scen, n, offsets = G.config_scenarios(1)
+    assert n == 960 and len(scen) == 30 and not offsets
+    scen, n, offsets = G.config_scenarios(3)
+    assert n == 16384 and offsets
     scen, n, _ = G.config_scenarios(2)
     assert n == 4096 and all(s[0].zones == 81 for s in scen)
 

@@ -136,7 +136,7 @@ def test_gpu_convection_desync_parity(conv_dir):
     """Desynchronised starts with convection on: every env at its own calendar
     offset, its own occupancy and convection streams."""
     say("convection parity, desync: 24 envs, 70 steps")
-    vec = E.VecEnv(24, blob_dir=str(conv_dir), groups=6, max_steps=50, desync=1, desync_seed=5)
+    vec = E.VecEnv(24, blob_dir=str(conv_dir), groups=6, max_steps=50, start_offsets=1, start_seed=5)
     twins = [Twin(vec, i, 50) for i in range(0, vec.n, 2)]
     _run_parity(vec, twins, 70, "conv desync")
     vec.close()

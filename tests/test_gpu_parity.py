@@ -22,6 +22,7 @@ run under all three forms.
 from __future__ import annotations
 
 import sys
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -56,11 +57,11 @@ def _gpu():
 class Twin:
     """Oracle env mirroring GPU env i of a vec (same scenario, seed, start)."""
 
-    def __init__(self, vec: E.VecEnv, i: int, max_steps: int):
+    def __init__(self, vec: E.VecEnv, i: int, max_steps: int, first_steps: int | None = None):
         path, start, seed = vec.meta(i)
         self.i = i
         self.path = path
-        self.cpu = po.CpuEnv("oracle", path, seed, start=start, max_steps=max_steps)
+        self.cpu = po.CpuEnv("oracle", path, seed, start=start, max_steps=max_steps, first_steps=first_steps)
         d = read_sbb(path)
         self.obs_len = int(d["n_dev"][0] + d["n_aux"][0])
         self.n_dev = int(d["n_dev"][0])
@@ -206,15 +207,81 @@ def test_gpu_step_parity_mixed_layouts(mixed_dir, solver):
 
 
 @pytest.mark.parametrize("solver", SOLVERS)
-def test_gpu_step_parity_desync(mixed_dir, solver):
-    """Desynchronised calendar starts: every env at its own seeded offset."""
-    say(f"parity ({solver}): 60 envs, desync, 90 steps")
-    vec = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=40, desync=1, desync_seed=99, solver=solver)
+def test_gpu_step_parity_start_offsets(mixed_dir, solver):
+    """Desynchronised calendar starts (start_offsets): every env at its own seeded offset."""
+    say(f"parity ({solver}): 60 envs, start offsets, 90 steps")
+    vec = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=40, start_offsets=1, start_seed=99,
+                   solver=solver)
     starts = {vec.meta(i)[1] for i in range(vec.n)}
     assert len(starts) > 40
     twins = [Twin(vec, i, 40) for i in range(0, vec.n, 3)]
-    _run_parity(vec, twins, 90, "desync")
+    _run_parity(vec, twins, 90, "start offsets")
     vec.close()
+
+
+LOG_NAMES = ["perf", "score", "episode_return", "episode_length", "reward_mean", "n"]
+
+
+def test_gpu_desync_truncation_parity(mixed_dir):
+    """desync = 1 (the reference GPU env's meaning, smart_buildings.cu:2808-2815):
+    env i's first episode ends after 1 + hash(i) mod 40 steps, later ones after 40;
+    the cut episode is a truncation that stays out of the episode log. Terminals,
+    rewards, states and logs against the oracle with the same first-episode lengths."""
+    say("desync truncation: 60 envs, 100 steps")
+    vec = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=40, desync=1)
+    firsts = [po.desync_first_steps(i, 40) for i in range(vec.n)]
+    assert len(set(firsts)) > 20 and min(firsts) >= 1 and max(firsts) <= 40
+    twins = [Twin(vec, i, 40, first_steps=firsts[i]) for i in range(0, vec.n, 2)]
+    _run_parity(vec, twins, 100, "desync")
+    for tw in twins:
+        got, want = vec.log(tw.i), tw.cpu.log()
+        for k, name in enumerate(LOG_NAMES):
+            assert abs(got[name] - float(want[k])) <= 1e-5 * max(1.0, abs(float(want[k]))), (tw.i, name, got, want)
+        # full episodes only: the cut first episode (if shorter than 40) is not counted
+        full = (100 - firsts[tw.i]) // 40 + (firsts[tw.i] == 40)
+        assert got["n"] == full, (tw.i, firsts[tw.i], got)
+    vec.close()
+
+
+def test_gpu_reset_isolation(mixed_dir):
+    """Envs of one batch end their episodes on different steps (desync truncates each
+    env's first episode at its own step); each env steps bit-identically inside the
+    batch and alone (a one-env vec keyed as the same batch index via shard_base),
+    through its own resets and its neighbours'."""
+    say("reset isolation: 60 envs with staggered episode ends vs solo runs")
+    big = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=30, desync=1, per_env_seed=0)
+    picks = [0, 7, 13, 29, 44, 59]
+    firsts = [po.desync_first_steps(i, 30) for i in picks]
+    assert len(set(firsts)) >= 4, firsts
+    solos = [E.VecEnv(1, blob=big.meta(i)[0], max_steps=30, desync=1, per_env_seed=0, shard_base=i) for i in picks]
+    big.reset()
+    for v in solos:
+        v.reset()
+    torch.cuda.synchronize()
+    for k, i in enumerate(picks):
+        assert torch.equal(big.obs[i], solos[k].obs[0]), ("reset", i)
+    ends = {i: [] for i in picks}
+    for s in range(75):
+        big.gen_actions(SEED, s)
+        for k, i in enumerate(picks):
+            solos[k].actions[0].copy_(big.actions[i])
+        big.step()
+        for v in solos:
+            v.step()
+        torch.cuda.synchronize()
+        for k, i in enumerate(picks):
+            assert torch.equal(big.obs[i], solos[k].obs[0]), (s, i)
+            assert torch.equal(big.rewards[i], solos[k].rewards[0]), (s, i)
+            assert torch.equal(big.terminals[i], solos[k].terminals[0]), (s, i)
+            if float(big.terminals[i]) == 1.0:
+                ends[i].append(s + 1)
+    for k, i in enumerate(picks):
+        assert np.array_equal(big.state(i)[:-2], solos[k].state(0)[:-2], equal_nan=True), i
+        assert ends[i][0] == firsts[k] and all(b - a == 30 for a, b in zip(ends[i], ends[i][1:])), (i, ends[i])
+    assert len({tuple(e) for e in ends.values()}) == len(picks)
+    big.close()
+    for v in solos:
+        v.close()
 
 
 def test_gpu_occupancy_exact(mixed_dir):
@@ -377,48 +444,182 @@ def test_gpu_log_matches_oracle(cfg0_dir):
 
 @pytest.mark.parametrize("config", [2, 3])
 def test_gpu_full_size_properties(config, tmp_path):
-    """BASELINE sizes (4,096 x 81 zones; 16,384 mixed desync): finite outputs, zero padding,
-    deterministic replay of the same vec configuration."""
+    """BASELINE sizes (config 2: 4,096 x 81 zones; config 3: 16,384 mixed with seeded
+    start offsets), 110 steps of 100-step episodes, so every env crosses its first
+    auto-reset (and, from a midnight start, the 07:00-09:00 arrivals):
+      - the observation row's padding past each env's obs_len is zero on every step;
+      - every env's terminal is set exactly on step 100 and nowhere else;
+      - a sample of envs across the batch matches the oracle (rewards, terminals and
+        observations every step, including the auto-reset observation; state at the end);
+      - replaying the same vec configuration is bit-identical."""
     from neurips2026_smart_building_challenge_amd.scenario import generate as G
 
     say(f"full size config {config}")
     G.write_config(config, tmp_path)
-    scen, n, desync = G.config_scenarios(config)
+    scen, n, offsets = G.config_scenarios(config)
+    sample = list(range(0, n, n // 8))[:8] + [n - 1]
     outs = []
     for rep in range(2):
-        vec = E.VecEnv(n, blob_dir=str(tmp_path), desync=int(desync))
+        vec = E.VecEnv(n, blob_dir=str(tmp_path), start_offsets=int(offsets), max_steps=100)
+        obs_len = {}
+        lens = np.zeros(n, np.int64)
+        for i in range(n):
+            pth = vec.meta(i)[0]
+            if pth not in obs_len:
+                d = read_sbb(pth)
+                obs_len[pth] = int(d["n_dev"][0] + d["n_aux"][0])
+            lens[i] = obs_len[pth]
+        pad = np.arange(E.SB_OBS)[None, :] >= lens[:, None]
+        twins = [Twin(vec, i, 100) for i in sample] if rep == 0 else []
         vec.reset()
-        for s in range(6):
+        for tw in twins:
+            tw.cpu.reset()
+        torch.cuda.synchronize()
+        assert np.all(host(vec.obs)[pad] == 0.0)
+        rew_trace = []
+        for s in range(110):
             vec.gen_actions(SEED, s)
             vec.step()
-        torch.cuda.synchronize()
-        obs = host(vec.obs)
-        rew = host(vec.rewards)
-        assert np.isfinite(obs).all() and np.isfinite(rew).all()
-        assert not host(vec.terminals).any()
-        lens = np.array([vec.envs[i].n_cont for i in range(n)])
-        assert lens.min() > 0
-        outs.append((obs.copy(), rew.copy()))
+            torch.cuda.synchronize()
+            obs, rew, term = host(vec.obs), host(vec.rewards), host(vec.terminals)
+            assert np.isfinite(obs).all() and np.isfinite(rew).all(), s
+            assert np.all(obs[pad] == 0.0), f"padding written at step {s}"
+            if s + 1 == 100:
+                assert np.all(term == 1.0), s
+            else:
+                assert not term.any(), s
+            rew_trace.append(rew.copy())
+            for tw in twins:
+                ob, r, t = tw.step(SEED, s)
+                where = f"full size config {config} step {s} env {tw.i}"
+                assert abs(float(rew[tw.i]) - r) <= 2 * np.spacing(np.float32(abs(r))) + 1e-12, where
+                assert term[tw.i] == t, where
+                obs_close(obs[tw.i], tw, ob, where)
+        for tw in twins:
+            state_close(vec.state(tw.i), tw.cpu.state(), f"full size config {config} env {tw.i}")
+        outs.append((host(vec.obs).copy(), np.array(rew_trace)))
         vec.close()
     assert np.array_equal(outs[0][0], outs[1][0]) and np.array_equal(outs[0][1], outs[1][1])
+
+
+@pytest.mark.parametrize("solver", ["relax", "lu"])
+def test_gpu_episode_totals_all_layouts(golden_index, tmp_path, solver):
+    """The north star's episode bar on every layout: one vec of the 12 scenarios whose
+    full 8,640-step reward totals the reference csim core wrote (6 layouts x 2
+    climates), each env driven by the action rows the reference run used; every env's
+    f64 episode total within 1e-6 relative of the reference core's, the terminal set
+    on step 8,640 only."""
+    from neurips2026_smart_building_challenge_amd.scenario import generate as G
+
+    totals = golden_index["totals"]
+    assert len(totals) == 12
+    want = {}
+    for t in totals:
+        path, sha = golden_blob(t["layout"], t["climate"], tmp_path)
+        assert sha == t["blob_sha256"], path
+        want[path.name] = t["total"]
+    steps = G.EPISODE_STEPS
+    vec = E.VecEnv(12, blob_dir=str(tmp_path), groups=12, max_steps=steps, solver=solver)
+    names = [Path(vec.meta(i)[0]).name for i in range(vec.n)]
+    assert sorted(names) == sorted(want)
+    # the reference run drove each scenario with the action rows of env 0
+    seed = golden_index["action_seed"]
+    rows = {}
+    bank = np.zeros((steps, vec.n, E.SB_ACT), np.float32)
+    for i in range(vec.n):
+        key = (vec.envs[i].n_cont, vec.envs[i].n_disc)
+        if key not in rows:
+            rows[key] = np.stack([po.action_row(seed, 0, s, *key) for s in range(steps)])
+        bank[:, i] = rows[key]
+    dbank = torch.from_numpy(bank).to("cuda")
+    say(f"episode totals ({solver}): 12 envs x {steps} steps")
+    vec.reset()
+    terms = torch.zeros(vec.n, dtype=torch.float32, device="cuda")
+    for s in range(steps):
+        vec.step_actions(dbank[s])
+        if s + 1 < steps:
+            terms += vec.terminals
+    torch.cuda.synchronize()
+    assert not host(terms).any()
+    assert np.all(host(vec.terminals) == 1.0)
+    worst = 0.0
+    for i in range(vec.n):
+        gs = vec.state(i)
+        assert gs[-1] == steps
+        ref = want[names[i]]
+        rel = abs(gs[-2] - ref) / abs(ref)
+        worst = max(worst, rel)
+        assert rel <= 1e-6, (names[i], gs[-2], ref, rel)
+    say(f"episode totals ({solver}): worst relative error {worst:.3e}")
+    check_solver(vec, solver)
+    vec.close()
 
 
 def test_gpu_bind_null_stream_returns_to_default(mixed_dir):
     """puf_bind_stream(NULL) binds the null stream again after another stream was
     bound (a graph capture's): the env's launches are then ordered with torch's
-    default-stream copies, with no device-wide synchronisation in between."""
-    say("stream binding: side stream, then NULL")
+    default-stream copies. The side stream is held busy by a spin kernel, so a
+    launch left on it would still be pending when the default-stream copy reads."""
+    say("stream binding: side stream held busy, then NULL")
     vec = E.VecEnv(30, blob_dir=str(mixed_dir), groups=30)
     side = torch.cuda.Stream()
-    vec.L.puf_bind_stream(E.P(side.cuda_stream))
-    vec.L.puf_bind_stream(None)
+    torch.cuda.synchronize()
     for step in (3, 777):
+        vec.actions.fill_(-5.0)
+        torch.cuda.synchronize()
+        with torch.cuda.stream(side):
+            torch.cuda._sleep(200_000_000)      # ~0.1 s of spinning on the side stream
+        vec.L.puf_bind_stream(E.P(side.cuda_stream))
+        vec.L.puf_bind_stream(None)
         vec.gen_actions(SEED, step)
         a = host(vec.actions)                  # a default-stream copy, ordered after the launch
         for i in range(vec.n):
             e = vec.envs[i]
             want = po.action_row(SEED, i, step, e.n_cont, e.n_disc)
             assert np.array_equal(a[i].view(np.uint32), want.view(np.uint32)), (i, step)
+        torch.cuda.synchronize()
+    vec.close()
+
+
+def test_gpu_reward_scale(cfg0_dir):
+    """reward_scale multiplies the reward handed to the trainer; a value <= 0 means 1
+    (complete_port/gpu/smart_buildings.cu:2595-2596)."""
+    say("reward_scale 1, 0, -2, 0.5")
+    vecs = {rs: E.VecEnv(3, blob_dir=str(cfg0_dir), reward_scale=rs) for rs in (1.0, 0.0, -2.0, 0.5)}
+    for v in vecs.values():
+        v.reset()
+    for s in range(4):
+        for v in vecs.values():
+            v.gen_actions(SEED, s)
+            v.step()
+        torch.cuda.synchronize()
+        base = host(vecs[1.0].rewards)
+        assert np.any(base != 0.0)
+        assert np.array_equal(host(vecs[0.0].rewards), base) and np.array_equal(host(vecs[-2.0].rewards), base)
+        assert np.array_equal(host(vecs[0.5].rewards), (base * np.float32(0.5)).astype(np.float32))
+    for v in vecs.values():
+        v.close()
+
+
+def test_gpu_live_log_totals(mixed_dir):
+    """puf_live_log's device reduction equals the per-env counters read one by one."""
+    say("live log: 90 envs, 70 steps")
+    vec = E.VecEnv(90, blob_dir=str(mixed_dir), groups=30, max_steps=25, desync=1)
+    vec.reset()
+    for s in range(70):
+        vec.gen_actions(SEED, s)
+        vec.step()
+    got = vec.live_log()
+    rs = st = 0.0
+    for i in range(vec.n):
+        g = vec.state(i)
+        rs += g[-2]
+        st += g[-1]
+    assert got["env_steps"] == 90 * 70 == st
+    firsts = [po.desync_first_steps(i, 25) for i in range(vec.n)]
+    eps = sum(1 + (70 - f) // 25 for f in firsts)
+    assert got["episodes"] == eps
+    assert abs(got["reward_mean"] - rs / st) <= 1e-6 * abs(rs / st)
     vec.close()
 
 

@@ -281,3 +281,37 @@ def test_oracle_convection_swaps_room_temperatures(tmp_path):
         assert np.array_equal(np.sort(ta[cols]), np.sort(tb[cols]))
         moved += int(np.sum(ta[cols] != tb[cols]))
     assert moved > 0
+
+
+def test_oracle_first_episode_truncation(tmp_path):
+    """The GPU env's desync (first episode cut at first_steps, smart_buildings.cu:
+    2808-2815) in the oracle: up to step 2f - 1 the env is step for step the same as
+    one whose every episode has f steps (the cut, then the same reset and streams);
+    the cut episode leaves the log at zero; the next episode has the full length and
+    is logged."""
+    paths, _, _ = G.write_config(0, tmp_path)
+    f, full = 7, 25
+    cut = po.CpuEnv("oracle", paths[0], 17321, max_steps=full, first_steps=f)
+    short = po.CpuEnv("oracle", paths[0], 17321, max_steps=f)
+    assert np.array_equal(cut.reset(), short.reset())
+    for s in range(2 * f - 1):
+        row = po.action_row(5, 0, s, cut.n_cont, cut.n_disc)
+        oa, ra, ta, _ = cut.step(row)
+        ob, rb, tb, _ = short.step(row)
+        assert np.array_equal(oa.view(np.uint32), ob.view(np.uint32)) and ra == rb and ta == tb, s
+        assert ta == (1.0 if s + 1 == f else 0.0), s
+        if s + 1 <= f:
+            assert not cut.log().any(), s
+    for s in range(2 * f - 1, f + full):
+        _, _, t, _ = cut.step(po.action_row(5, 0, s, cut.n_cont, cut.n_disc))
+        assert t == (1.0 if s + 1 == f + full else 0.0), s
+    lg = cut.log()
+    assert lg[5] == 1.0 and lg[3] == float(full)
+
+
+def test_desync_first_steps_range():
+    """The hashed first-episode length lies in [1, episode length] and spreads over it."""
+    firsts = [po.desync_first_steps(i, 8640) for i in range(4096)]
+    assert min(firsts) >= 1 and max(firsts) <= 8640
+    assert len(set(firsts)) > 3100   # 4,096 uniform draws from 8,640 values: about 3,262 distinct
+    assert abs(np.mean(firsts) - 4320.5) < 200
