@@ -238,6 +238,17 @@ typedef struct SbxPolicy {
 } SbxPolicy;
 int sbx_policy_bind(Env* envs, const SbxPolicy* p);
 int sbx_policy_act(Env* envs, uint64_t seed, uint32_t step);
+/* sbx_policy_act for callers that cannot allocate device memory (code under
+ * hipGraph capture, tight serving loops, harnesses that forbid hipMalloc); no
+ * counterpart in the reference. Needs no sbx_policy_bind: the weights come with
+ * the call, and the activations live in a file-scope device array of the
+ * library (12.5 MiB per GPU, held until the process ends) that fits at most
+ * SBX_NOALLOC_MAX_ENVS envs; a larger vec is rejected (-1, message in
+ * sbx_last_error). Same kernels and action rows as sbx_policy_act; launches on
+ * the bound stream, no allocation, no synchronisation. Every call on one GPU
+ * shares that array: calls that overlap on one GPU race. Returns 0, or -1. */
+#define SBX_NOALLOC_MAX_ENVS 4096
+int sbx_policy_act_noalloc(Env* envs, const SbxPolicy* p, uint64_t seed, uint32_t step);
 int sbx_policy_heads(Env* envs, float* out, int cap);
 
 /* Rollout-buffer side of the Beta heads (complete_port/patches/

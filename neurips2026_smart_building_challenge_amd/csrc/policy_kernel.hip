@@ -21,6 +21,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "sb_betamath.h"
 #include "sb_philox.h"
 
@@ -329,4 +331,58 @@ extern "C" int sbk_launch_beta_sample(const float* alpha, const float* beta, flo
     if (n <= 0) return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(sbk::beta_sample_kernel, dim3((n + 255) / 256), dim3(256), 0, s, alpha, beta, out, n, seed);
     return (int)hipGetLastError();
+}
+
+// ------------------------------------------------- allocation-free policy step
+// Activations of sbk_launch_policy_noalloc (h1 [n][128], h2 [n][128] and
+// y [n][544], at most kNoAllocEnvs envs: 12.5 MiB) in a file-scope device
+// array. Each GPU the library runs on holds its own copy until the process
+// ends. Every call on a GPU uses that GPU's copy: calls that overlap on one GPU
+// race. Nothing in it needs clearing between calls: each layer writes every
+// element of its output rows before the next layer reads them.
+namespace {
+constexpr int kNoAllocEnvs = 4096;
+constexpr size_t kNoAllocFloats = (size_t)kNoAllocEnvs * (2 * sbk::kPolicyHidden + sbk::kPolicyHeads);
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kMaxDevices] = {};
+}  // namespace
+
+static __device__ __align__(256) float scratch[kNoAllocFloats];
+
+// The device address of this GPU's scratch, looked up once per device with
+// that device current (the array's name is only a host-side stand-in).
+static int scratch_of_device(float** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    if (dev < 0 || dev >= kMaxDevices) return (int)hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        g_scratch[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch[dev];
+    return 0;
+}
+
+extern "C" int sbk_noalloc_max_envs(void) { return kNoAllocEnvs; }
+
+// sbk_launch_policy without the rollout-buffer outputs, its activations in the
+// scratch array: launches only, no allocation.
+extern "C" int sbk_launch_policy_noalloc(const float* obs, const float* w1, const float* b1, const float* w2,
+                                         const float* b2, const float* w3, const float* b3, float* actions,
+                                         const int* n_cont, const int* n_disc, int n, uint64_t seed, uint32_t step,
+                                         hipStream_t s) {
+    if (n <= 0 || n > kNoAllocEnvs) return (int)hipErrorInvalidValue;
+    float* base = nullptr;
+    const int rc = scratch_of_device(&base);
+    if (rc != 0) return rc;
+    float* h1 = base;
+    float* h2 = h1 + (size_t)kNoAllocEnvs * sbk::kPolicyHidden;
+    float* y = h2 + (size_t)kNoAllocEnvs * sbk::kPolicyHidden;
+    return sbk_launch_policy(obs, w1, b1, w2, b2, w3, b3, h1, h2, y, actions, n_cont, n_disc, n, seed, step,
+                             nullptr, nullptr, nullptr, nullptr, nullptr, s);
 }

@@ -38,6 +38,11 @@ extern "C" int sbk_launch_beta_eval(const float* y, const float* draws, const in
                                     hipStream_t s);
 extern "C" int sbk_launch_beta_sample(const float* alpha, const float* beta, float* out, int n, uint64_t seed,
                                       hipStream_t s);
+extern "C" int sbk_noalloc_max_envs(void);
+extern "C" int sbk_launch_policy_noalloc(const float* obs, const float* w1, const float* b1, const float* w2,
+                                         const float* b2, const float* w3, const float* b3, float* actions,
+                                         const int* n_cont, const int* n_disc, int n, uint64_t seed, uint32_t step,
+                                         hipStream_t s);
 extern "C" int sbk_launch_live_sums(const sbk::EnvDesc* envs, const sbk::DevLayout* layouts,
                                     const unsigned char* state, int n, double* out, hipStream_t s);
 extern "C" int sbk_launch_gen_actions(float* actions, const int* n_cont, const int* n_disc, int n_envs,
@@ -1675,6 +1680,23 @@ int sbx_policy_act(Env* envs, uint64_t seed, uint32_t step) {
                                v->d_ncont, v->d_ndisc, v->n, seed, step, nullptr, nullptr, nullptr, nullptr, nullptr,
                                g_stream);
     if (rc != 0) die(std::string("policy launch failed: ") + hipGetErrorString((hipError_t)rc));
+    return 0;
+}
+
+int sbx_policy_act_noalloc(Env* envs, const SbxPolicy* p, uint64_t seed, uint32_t step) {
+    Vec* v = vec_of(envs);
+    if (!p || !p->w1 || !p->b1 || !p->w2 || !p->b2 || !p->w3 || !p->b3) { g_err = "null policy weight"; return -1; }
+    if (v->n > sbk_noalloc_max_envs()) {
+        g_err = "sbx_policy_act_noalloc: " + std::to_string(v->n) + " envs, at most "
+                + std::to_string(sbk_noalloc_max_envs());
+        return -1;
+    }
+    int rc = sbk_launch_policy_noalloc(v->obs, p->w1, p->b1, p->w2, p->b2, p->w3, p->b3, v->actions, v->d_ncont,
+                                       v->d_ndisc, v->n, seed, step, g_stream);
+    if (rc != 0) {
+        g_err = std::string("sbx_policy_act_noalloc: ") + hipGetErrorString((hipError_t)rc);
+        return -1;
+    }
     return 0;
 }
 

@@ -93,7 +93,7 @@ EXPORTS = [
     "dict_find", "dict_set", "puf_vec_create", "puf_bind_stream", "puf_init", "puf_reset", "puf_step",
     "puf_render", "puf_close", "puf_log", "puf_live_log", "puf_mask_init", "sbx_gen_actions",
     "sbx_vec_info", "sbx_env_state", "sbx_time_step", "sbx_step_actions", "sbx_phase_times", "sbx_phase_stamps", "sbx_kernel_timer", "sbx_pass_times", "sbx_solve_info",
-    "sbx_policy_bind", "sbx_policy_act", "sbx_policy_heads", "sbx_beta_sample",
+    "sbx_policy_bind", "sbx_policy_act", "sbx_policy_act_noalloc", "sbx_policy_heads", "sbx_beta_sample",
     "sbx_policy_act_logp", "sbx_beta_eval",
     "sbx_env_meta", "sbx_scenario_path",
     "sbx_plan_layout", "sbx_plan_free", "sbx_last_error", "sbx_version",
@@ -138,6 +138,8 @@ def lib() -> ctypes.CDLL:
         L.sbx_kernel_timer.restype = ctypes.c_double
         L.sbx_policy_bind.argtypes = [ctypes.POINTER(Env), ctypes.POINTER(SbxPolicy)]
         L.sbx_policy_act.argtypes = [ctypes.POINTER(Env), ctypes.c_uint64, ctypes.c_uint32]
+        L.sbx_policy_act_noalloc.argtypes = [ctypes.POINTER(Env), ctypes.POINTER(SbxPolicy), ctypes.c_uint64,
+                                             ctypes.c_uint32]
         L.sbx_policy_heads.argtypes = [ctypes.POINTER(Env), P, ctypes.c_int]
         L.sbx_beta_sample.argtypes = [P, P, P, ctypes.c_int, ctypes.c_uint64, P]
         L.sbx_policy_act_logp.argtypes = [ctypes.POINTER(Env), ctypes.c_uint64, ctypes.c_uint32, P, P, P]
@@ -327,6 +329,12 @@ class VecEnv:
     def policy_act(self, seed: int, step: int) -> None:
         """Policy forward + Beta sampling: writes every env's action row for the next step."""
         if self.L.sbx_policy_act(self.envs, seed, step) != 0:
+            raise RuntimeError(self.L.sbx_last_error().decode())
+
+    def policy_act_noalloc(self, weights: dict, seed: int, step: int) -> None:
+        """policy_act through the allocation-free entry point (weights per call, no bind)."""
+        p = SbxPolicy(*[ctypes.c_void_p(weights[k].data_ptr()) for k in ("w1", "b1", "w2", "b2", "w3", "b3")])
+        if self.L.sbx_policy_act_noalloc(self.envs, ctypes.byref(p), seed, step) != 0:
             raise RuntimeError(self.L.sbx_last_error().decode())
 
     def policy_act_logp(self, seed: int, step: int):
