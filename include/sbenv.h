@@ -217,9 +217,10 @@ int sbx_solve_info(Env* envs, int i, double* out);
  * policy forward runs between env steps). fp32 MLP on MFMA over every env's
  * observation row: h1 = tanh(obs W1 + b1), h2 = tanh(h1 W2 + b2),
  * y = h2 W3 + b3 = (u[256], v[256], ud[16], vd[16]); head j draws
- * x ~ Beta(softplus(u_j) + 1, softplus(v_j) + 1) (two Marsaglia-Tsang gamma
- * draws on Philox4x32-10 keyed by seed, counter (env, step, 2j or 2j + 1,
- * 1 + attempt)); continuous heads write 2x - 1, discrete heads x > 0.5 into the
+ * x ~ Beta(softplus(u_j) + f, softplus(v_j) + f) (f = beta_floor; two
+ * Marsaglia-Tsang gamma draws on Philox4x32-10 keyed by seed, counter (env,
+ * step, 2j or 2j + 1, 1 + attempt), a shape below 1 boosted as
+ * G(k + 1) U^(1/k)); continuous heads write 2x - 1, discrete heads x > 0.5 into the
  * vec's action rows (0 past the env's n_cont / n_disc). Weights are caller-owned
  * device memory, row-major [in][out]: W1 [1024][128], W2 [128][128],
  * W3 [128][544], biases [128], [128], [544]. sbx_policy_bind stores them and
@@ -235,6 +236,9 @@ typedef struct SbxPolicy {
     const float* b2;
     const float* w3;
     const float* b3;
+    float beta_floor;   /* shape floor f: a = softplus(u) + f (the reference's policy.beta_floor);
+                           1 gives shapes >= 1, below 1 shapes may fall under 1 (boosted gamma
+                           draws); finite, >= 0 */
 } SbxPolicy;
 int sbx_policy_bind(Env* envs, const SbxPolicy* p);
 int sbx_policy_act(Env* envs, uint64_t seed, uint32_t step);
@@ -253,8 +257,9 @@ int sbx_policy_heads(Env* envs, float* out, int cap);
 
 /* Rollout-buffer side of the Beta heads (complete_port/patches/
  * pufferlib_core.diff:944-1000, beta_continuous_head; the trainer stores each
- * draw with its log-probability and entropy). With a = softplus(u) + 1,
- * b = softplus(v) + 1 (float, as the sampler maps them), a head's draw x has
+ * draw with its log-probability and entropy). With a = softplus(u) + f,
+ * b = softplus(v) + f (float, as the sampler maps them; f the bound policy's
+ * beta_floor), a head's draw x has
  * log p = (a - 1) log x + (b - 1) log(1 - x) - ln B(a, b) (x clamped to
  * [2^-24, 1 - 2^-24]) and entropy H = ln B(a, b) - (a - 1) psi(a) - (b - 1) psi(b)
  * + (a + b - 2) psi(a + b), evaluated in f64 and stored as float.
@@ -271,8 +276,33 @@ int sbx_policy_heads(Env* envs, float* out, int cap);
 int sbx_policy_act_logp(Env* envs, uint64_t seed, uint32_t step, float* draws, float* logp, float* entropy);
 int sbx_beta_eval(Env* envs, const float* y, const float* draws, float* logp, float* entropy, float* grad);
 
+/* PPO side of the Beta heads, one minibatch row per env (the reference's PPO
+ * loss, complete_port/patches/pufferlib_core.diff:1205-1252, with its
+ * ratio_per_dim, :539-543, and beta_kl, :1008-1014). Inputs (device, caller
+ * owned): the new and the old policy's heads y_new, y_old [n][544] (the layout
+ * of sbx_policy_heads), the rollout draws [n][272], the stored log-probability
+ * logp_old [n] and advantages adv [n]. Over the env's D used heads, summed in
+ * f64 in a fixed order: logp = sum log p_new(x), H = sum of the new heads'
+ * entropies, KL = sum KL(old head || new head). lr = (logp - logp_old) / D
+ * when ratio_per_dim (the geometric-mean ratio) else logp - logp_old,
+ * non-finite -> 0, clamped to [-20, 20]; r = exp(lr);
+ * pg = s max(-A r, -A clamp(r, 1 - clip, 1 + clip)), s = D when ratio_per_dim
+ * else 1. out [n][6] = logp, H, KL, r, pg, lr. grad [n][2][272] (or NULL): the
+ * derivative of pg - ent_coef H in each used head's u and v (0 elsewhere), with
+ * d pg / d logp = -A r, or 0 where the clipped term is the larger and r lies
+ * outside the clip range. Launches on the bound stream, allocates nothing.
+ * Returns 0, or -1. */
+typedef struct SbxPpo {
+    float clip_coef;
+    float ent_coef;
+    int ratio_per_dim;
+    float beta_floor;
+} SbxPpo;
+int sbx_ppo_beta(Env* envs, const float* y_new, const float* y_old, const float* draws, const float* logp_old,
+                 const float* adv, const SbxPpo* args, float* out, float* grad);
+
 /* The heads' Beta sampler alone: out[i] ~ Beta(alpha[i], beta[i]) for device
- * arrays of n floats (alpha, beta >= 1), counter (i, 0, 0 or 1, 1 + attempt),
+ * arrays of n floats (alpha, beta > 0), counter (i, 0, 0 or 1, 1 + attempt),
  * on `stream` (hipStream_t; NULL = the null stream). Leaves the stream bound
  * by puf_bind_stream alone. Returns 0, or -1. */
 int sbx_beta_sample(const float* alpha, const float* beta, float* out, int n, uint64_t seed, void* stream);

@@ -6,7 +6,8 @@
 //   h2 = tanh(h1 W2 + b2)    [n x 128]  x [128 x 128]
 //   y  = h2 W3 + b3          [n x 128]  x [128 x 544] = (u[256], v[256], ud[16], vd[16])
 //
-// and each action head j draws x ~ Beta(softplus(u_j) + 1, softplus(v_j) + 1);
+// and each action head j draws x ~ Beta(softplus(u_j) + f, softplus(v_j) + f)
+// (f the policy's shape floor, 1 by default);
 // continuous heads write 2x - 1, discrete heads x > 0.5 into the action row the
 // next env step decodes.
 //
@@ -95,33 +96,49 @@ __global__ __launch_bounds__(256) void mlp_layer_kernel(const float* __restrict_
     }
 }
 
-__device__ __forceinline__ float softplus(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
-
-// Gamma(a) for a >= 1 (Marsaglia and Tsang, "A simple method for generating
-// gamma variables", ACM TOMS 26(3), 2000): d = a - 1/3, c = 1/sqrt(9d); draw
-// z ~ N(0, 1) (Box-Muller) and u ~ U(0, 1), v = (1 + cz)^3, accept d v when
-// v > 0 and u < 1 - 0.0331 z^4 or log u < z^2/2 + d (1 - v + log v). Attempt t
-// uses Philox block (env, step, stream, 1 + t); after 32 rejected attempts
-// (probability below 1e-40 for a >= 1) the mean a is returned. The sampler is
-// statistical, so it uses the hardware log2 / cos / sqrt.
+// Gamma(a), a > 0 (Marsaglia and Tsang, "A simple method for generating gamma
+// variables", ACM TOMS 26(3), 2000): for k = a (a >= 1) or k = a + 1 (a < 1),
+// d = k - 1/3, c = 1/sqrt(9d); draw z ~ N(0, 1) (Box-Muller) and u ~ U(0, 1),
+// t = (1 + cz)^3, accept d t when cz > -1 and u < 1 - 0.0331 z^4 or
+// log u < z^2/2 + d (1 - t + log t). With w = cz the last term is written
+// 1 - t = -w (3 + 3w + w^2) and log t = 3 log1p(w), which keeps its precision
+// when d is large and t is close to 1 (where 1 - t + log t cancels). For
+// a < 1 the draw is boosted, G(a) = G(a + 1) U^(1/a) (the paper's section 6),
+// with U from Philox block (env, step, stream, 0xffffffff). Attempt t uses
+// Philox block (env, step, stream, 1 + t); after 32 rejected attempts
+// (probability below 1e-40) the mean a is returned. The sampler is statistical,
+// so it uses the hardware log2 / cos / sqrt for the proposal.
 __device__ __forceinline__ float gamma_mt(float a, uint32_t env, uint32_t step, uint32_t stream, uint32_t k0,
                                           uint32_t k1) {
-    const float d = a - (1.0f / 3.0f);
+    const bool boost = a < 1.0f;
+    const float k = boost ? a + 1.0f : a;
+    const float d = k - (1.0f / 3.0f);
     const float c = __frsqrt_rn(9.0f * d);
     for (uint32_t t = 0; t < 32; t++) {
         const Ctr4 r = philox4x32_10(Ctr4{env, step, stream, 1u + t}, k0, k1);
         const float u1 = u24(r.x), u2 = u24(r.y), u = u24(r.z);
         const float z = __fsqrt_rn(-2.0f * __logf(u1)) * __cosf(6.283185307f * u2);
-        float v = 1.0f + c * z;
-        if (v <= 0.0f) continue;
-        v = v * v * v;
+        const float w = c * z;
+        if (w <= -1.0f) continue;
+        const float v = 1.0f + w;
+        const float cube = v * v * v;
         const float z2 = z * z;
-        if (u < 1.0f - 0.0331f * z2 * z2) return d * v;
-        if (__logf(u) < 0.5f * z2 + d * (1.0f - v + __logf(v))) return d * v;
+        bool ok = u < 1.0f - 0.0331f * z2 * z2;
+        if (!ok) {
+            const float one_minus_t = -w * (3.0f + w * (3.0f + w));
+            ok = __logf(u) < 0.5f * z2 + d * (one_minus_t + 3.0f * log1pf(w));
+        }
+        if (ok) {
+            float g = d * cube;
+            if (boost) {
+                const Ctr4 rb = philox4x32_10(Ctr4{env, step, stream, 0xffffffffu}, k0, k1);
+                g *= powf(u24(rb.x), 1.0f / a);
+            }
+            return g;
+        }
     }
     return a;
 }
-
 
 // Third layer fused with the Beta draws: one workgroup per (16-env tile, group
 // of 16 heads). Waves 0 and 1 compute the group's u and v column tiles of
@@ -139,7 +156,8 @@ __global__ __launch_bounds__(256) void heads_layer_kernel(const float* __restric
                                                           float* __restrict__ actions, const int* __restrict__ n_cont,
                                                           const int* __restrict__ n_disc, int n, uint64_t seed,
                                                           uint32_t step, float* __restrict__ draws,
-                                                          float* __restrict__ hlp, float* __restrict__ hent) {
+                                                          float* __restrict__ hlp, float* __restrict__ hent,
+                                                          float floor) {
     constexpr int H = kPolicyHidden;
     __shared__ float ys[16][32 + 1];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -195,7 +213,7 @@ __global__ __launch_bounds__(256) void heads_layer_kernel(const float* __restric
         const bool used = live && (h < 256 ? h < n_cont[ec] : h - 256 < n_disc[ec]);
         float gm = 1.0f;
         if (used) {
-            const float a = softplus(ys[row][16 * which + k]) + 1.0f;
+            const float a = beta_shape(ys[row][16 * which + k], floor);
             gm = gamma_mt(a, (uint32_t)e, step, 2u * (uint32_t)h + (uint32_t)which, (uint32_t)seed,
                           (uint32_t)(seed >> 32));
         }
@@ -212,7 +230,7 @@ __global__ __launch_bounds__(256) void heads_layer_kernel(const float* __restric
                 draws[o] = x;
                 float lp = 0.0f, en = 0.0f;
                 if (used) {
-                    const BetaHead bh = beta_head(ys[row][k], ys[row][16 + k], x);
+                    const BetaHead bh = beta_head(ys[row][k], ys[row][16 + k], x, floor);
                     lp = (float)bh.logp;
                     en = (float)bh.entropy;
                 }
@@ -231,7 +249,8 @@ __global__ __launch_bounds__(256) void heads_layer_kernel(const float* __restric
 // past the env's head counts.
 __global__ void beta_eval_kernel(const float* __restrict__ y, const float* __restrict__ draws,
                                  const int* __restrict__ n_cont, const int* __restrict__ n_disc, int n,
-                                 float* __restrict__ hlp, float* __restrict__ hent, float* __restrict__ grad) {
+                                 float* __restrict__ hlp, float* __restrict__ hent, float* __restrict__ grad,
+                                 float floor) {
     const int e = blockIdx.x, h = threadIdx.x;
     if (e >= n || h >= kActWidth) return;
     const bool used = h < 256 ? h < n_cont[e] : h - 256 < n_disc[e];
@@ -241,7 +260,7 @@ __global__ void beta_eval_kernel(const float* __restrict__ y, const float* __res
         const float* ye = y + (size_t)e * kPolicyHeads;
         const float u = h < 256 ? ye[h] : ye[512 + (h - 256)];
         const float v = h < 256 ? ye[256 + h] : ye[528 + (h - 256)];
-        const BetaHead bh = beta_head(u, v, draws[o]);
+        const BetaHead bh = beta_head(u, v, draws[o], floor);
         lp = (float)bh.logp;
         en = (float)bh.entropy;
 #pragma unroll
@@ -288,6 +307,89 @@ __global__ void beta_sample_kernel(const float* alpha, const float* beta, float*
     out[i] = ga / (ga + gb);
 }
 
+// The PPO side of the Beta heads for one minibatch row per env
+// (complete_port/patches/pufferlib_core.diff:1205-1252 ppo loss and its
+// ratio_per_dim, :539-543, :1008-1014 beta_kl): one workgroup per env, thread h takes
+// head h. Over the env's used heads (D of them), in f64 and a fixed summation
+// order: logp = sum log p_new(x), H = sum entropies under the new heads,
+// KL = sum KL(old head || new head). Then
+//   r = exp(clamp(lr, -20, 20)), lr = (logp - logp_old) / (D if per_dim else 1)
+//   pg = s * max(-A r, -A clamp(r, 1 - eps, 1 + eps)),  s = D if per_dim else 1
+// (a non-finite lr counts as 0), and the gradient of pg - ent_coef * H in each
+// head's raw outputs: d pg / d logp = g_r r with g_r = -A, or 0 where the
+// clipped term is the larger and r lies outside the clip range; the per-dim
+// scale s cancels the 1/D of the ratio. out[e][0..5] = logp, H, KL, r, pg, lr;
+// grad[e][0][h] = d / du, grad[e][1][h] = d / dv (0 for unused heads).
+__global__ __launch_bounds__(320) void ppo_beta_kernel(const float* __restrict__ y_new, const float* __restrict__ y_old,
+                                                       const float* __restrict__ draws,
+                                                       const float* __restrict__ logp_old, const float* __restrict__ adv,
+                                                       const int* __restrict__ n_cont, const int* __restrict__ n_disc,
+                                                       int n, float floor, float clip, float ent_coef, int per_dim,
+                                                       float* __restrict__ out, float* __restrict__ grad) {
+    __shared__ double red[3][512];
+    __shared__ float dlp;
+    const int e = blockIdx.x, t = (int)threadIdx.x;
+    if (e >= n) return;
+    const int nc = n_cont[e], nd = n_disc[e];
+    const int h = t;
+    const bool used = h < kActWidth && (h < 256 ? h < nc : h - 256 < nd);
+    double lp = 0.0, en = 0.0, kl = 0.0;
+    double g[4] = {0.0, 0.0, 0.0, 0.0};
+    if (used) {
+        const float* yn = y_new + (size_t)e * kPolicyHeads;
+        const float* yo = y_old + (size_t)e * kPolicyHeads;
+        const int cu = h < 256 ? h : 512 + (h - 256), cv = h < 256 ? 256 + h : 528 + (h - 256);
+        const BetaHead bh = beta_head(yn[cu], yn[cv], draws[(size_t)e * kActWidth + h], floor);
+        lp = bh.logp;
+        en = bh.entropy;
+#pragma unroll
+        for (int k = 0; k < 4; k++) g[k] = bh.g[k];
+        kl = beta_kl(beta_shape(yo[cu], floor), beta_shape(yo[cv], floor), beta_shape(yn[cu], floor),
+                     beta_shape(yn[cv], floor));
+    }
+    for (int i = t; i < 512; i += (int)blockDim.x) {
+        const bool mine = i == t;
+        red[0][i] = mine ? lp : 0.0;
+        red[1][i] = mine ? en : 0.0;
+        red[2][i] = mine ? kl : 0.0;
+    }
+    __syncthreads();
+    for (int w = 256; w > 0; w >>= 1) {
+        for (int i = t; i < w; i += (int)blockDim.x)
+            for (int q = 0; q < 3; q++) red[q][i] += red[q][i + w];
+        __syncthreads();
+    }
+    if (t == 0) {
+        const double lps = red[0][0], ens = red[1][0], kls = red[2][0];
+        const int D = nc + nd;
+        double lr = lps - (double)logp_old[e];
+        if (per_dim) lr /= (double)(D > 0 ? D : 1);
+        if (!isfinite(lr)) lr = 0.0;
+        lr = fmin(20.0, fmax(-20.0, lr));
+        const double r = exp(lr);
+        const double A = (double)adv[e];
+        const double lo = 1.0 - (double)clip, hi = 1.0 + (double)clip;
+        const double l1 = -A * r, l2 = -A * fmin(hi, fmax(lo, r));
+        double gr = -A;
+        if (l2 > l1 && (r < lo || r > hi)) gr = 0.0;
+        const double s = per_dim ? (double)(D > 0 ? D : 1) : 1.0;
+        float* o = out + (size_t)e * 6;
+        o[0] = (float)lps;
+        o[1] = (float)ens;
+        o[2] = (float)kls;
+        o[3] = (float)r;
+        o[4] = (float)(s * fmax(l1, l2));
+        o[5] = (float)lr;
+        dlp = (float)(gr * r);
+    }
+    __syncthreads();
+    if (grad && h < kActWidth) {
+        const double d = (double)dlp;
+        grad[((size_t)e * 2 + 0) * kActWidth + h] = used ? (float)(d * g[0] - (double)ent_coef * g[2]) : 0.0f;
+        grad[((size_t)e * 2 + 1) * kActWidth + h] = used ? (float)(d * g[1] - (double)ent_coef * g[3]) : 0.0f;
+    }
+}
+
 }  // namespace sbk
 
 // ---------------------------------------------------------------- launchers
@@ -298,7 +400,7 @@ extern "C" int sbk_launch_policy(const float* obs, const float* w1, const float*
                                  const float* b2, const float* w3, const float* b3, float* h1, float* h2, float* y,
                                  float* actions, const int* n_cont, const int* n_disc, int n, uint64_t seed,
                                  uint32_t step, float* draws, float* hlp, float* hent, float* logp, float* entropy,
-                                 hipStream_t s) {
+                                 float floor, hipStream_t s) {
     using namespace sbk;
     if (n <= 0) return (int)hipErrorInvalidValue;
     const int mt = (n + 15) / 16;
@@ -309,20 +411,29 @@ extern "C" int sbk_launch_policy(const float* obs, const float* w1, const float*
                        kPolicyHidden, w2, b2, h2, kPolicyHidden, n, kPolicyHidden);
     // third layer and the Beta draws in one launch per (env tile, head group)
     hipLaunchKernelGGL(heads_layer_kernel, dim3(mt, kHeadGroups), dim3(256), 0, s, h2, w3, b3, y, actions, n_cont,
-                       n_disc, n, seed, step, draws, hlp, hent);
+                       n_disc, n, seed, step, draws, hlp, hent, floor);
     if (draws) hipLaunchKernelGGL(beta_sum_kernel, dim3(n), dim3(64), 0, s, hlp, hent, n, logp, entropy);
     return (int)hipGetLastError();
 }
 
 // Log-densities, entropies and their gradients of given draws under heads y.
 extern "C" int sbk_launch_beta_eval(const float* y, const float* draws, const int* n_cont, const int* n_disc, int n,
-                                    float* hlp, float* hent, float* grad, float* logp, float* entropy,
+                                    float* hlp, float* hent, float* grad, float* logp, float* entropy, float floor,
                                     hipStream_t s) {
     using namespace sbk;
     if (n <= 0) return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(beta_eval_kernel, dim3(n), dim3(kActWidth + 16), 0, s, y, draws, n_cont, n_disc, n, hlp,
-                       hent, grad);
+                       hent, grad, floor);
     hipLaunchKernelGGL(beta_sum_kernel, dim3(n), dim3(64), 0, s, hlp, hent, n, logp, entropy);
+    return (int)hipGetLastError();
+}
+
+extern "C" int sbk_launch_ppo_beta(const float* y_new, const float* y_old, const float* draws, const float* logp_old,
+                                   const float* adv, const int* n_cont, const int* n_disc, int n, float floor,
+                                   float clip, float ent_coef, int per_dim, float* out, float* grad, hipStream_t s) {
+    if (n <= 0) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(sbk::ppo_beta_kernel, dim3(n), dim3(320), 0, s, y_new, y_old, draws, logp_old, adv, n_cont,
+                       n_disc, n, floor, clip, ent_coef, per_dim, out, grad);
     return (int)hipGetLastError();
 }
 
@@ -375,7 +486,7 @@ extern "C" int sbk_noalloc_max_envs(void) { return kNoAllocEnvs; }
 extern "C" int sbk_launch_policy_noalloc(const float* obs, const float* w1, const float* b1, const float* w2,
                                          const float* b2, const float* w3, const float* b3, float* actions,
                                          const int* n_cont, const int* n_disc, int n, uint64_t seed, uint32_t step,
-                                         hipStream_t s) {
+                                         float floor, hipStream_t s) {
     if (n <= 0 || n > kNoAllocEnvs) return (int)hipErrorInvalidValue;
     float* base = nullptr;
     const int rc = scratch_of_device(&base);
@@ -384,5 +495,5 @@ extern "C" int sbk_launch_policy_noalloc(const float* obs, const float* w1, cons
     float* h2 = h1 + (size_t)kNoAllocEnvs * sbk::kPolicyHidden;
     float* y = h2 + (size_t)kNoAllocEnvs * sbk::kPolicyHidden;
     return sbk_launch_policy(obs, w1, b1, w2, b2, w3, b3, h1, h2, y, actions, n_cont, n_disc, n, seed, step,
-                             nullptr, nullptr, nullptr, nullptr, nullptr, s);
+                             nullptr, nullptr, nullptr, nullptr, nullptr, floor, s);
 }

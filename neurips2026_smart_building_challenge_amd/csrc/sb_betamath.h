@@ -1,7 +1,9 @@
 // Beta policy head math for the rollout buffer of the shared-policy loop: the
 // log-density of a draw, the entropy, and their derivatives with respect to the
-// head's raw outputs (u, v), for shapes a = softplus(u) + 1, b = softplus(v) + 1
-// (complete_port/patches/pufferlib_core.diff:944-1000, beta_continuous_head).
+// head's raw outputs (u, v), for shapes a = softplus(u) + f, b = softplus(v) + f
+// with the policy's shape floor f (1 by default; below 1 the shapes may be
+// below 1) (complete_port/patches/pufferlib_core.diff:944-1000,
+// beta_continuous_head; :1008-1014 beta_kl).
 //
 //   log p(x)  = (a - 1) log x + (b - 1) log(1 - x) - ln B(a, b)
 //   H         = ln B(a, b) - (a - 1) psi(a) - (b - 1) psi(b) + (a + b - 2) psi(a + b)
@@ -11,7 +13,12 @@
 //
 // ln B from the device libm's lgamma; psi and psi' by upward recurrence to
 // x >= 10 and the asymptotic series of Abramowitz & Stegun 6.3.18 / 6.4.12
-// (truncation below 1e-15 relative there). Shapes are at least 1 here.
+// (truncation below 1e-15 relative there); shapes are positive.
+//
+//   KL(Beta(a1, b1) || Beta(a2, b2)) = ln B(a2, b2) - ln B(a1, b1) + (a1 - a2) psi(a1)
+//                                      + (b1 - b2) psi(b1) + (a2 - a1 + b2 - b1) psi(a1 + b1)
+// (the difference of the cross-entropy E_1[-log p_2] and the entropy of p_1,
+// with E_1[log x] = psi(a1) - psi(a1 + b1) and E_1[log(1 - x)] = psi(b1) - psi(a1 + b1)).
 #pragma once
 #include <hip/hip_runtime.h>
 
@@ -46,7 +53,9 @@ __device__ __forceinline__ double beta_trigamma(double x) {
 }
 
 // The sampler's shape map (float, as the draws use it) and its derivative.
-__device__ __forceinline__ float beta_shape(float raw) { return (raw > 20.0f ? raw : log1pf(expf(raw))) + 1.0f; }
+__device__ __forceinline__ float beta_shape(float raw, float floor) {
+    return (raw > 20.0f ? raw : log1pf(expf(raw))) + floor;
+}
 __device__ __forceinline__ double beta_shape_grad(float raw) {
     return raw > 20.0f ? 1.0 : 1.0 / (1.0 + exp(-(double)raw));
 }
@@ -63,8 +72,8 @@ struct BetaHead {
     double g[4];   // d logp / du, d logp / dv, d H / du, d H / dv
 };
 
-__device__ __forceinline__ BetaHead beta_head(float u, float v, float x) {
-    const double a = beta_shape(u), b = beta_shape(v), s = a + b;
+__device__ __forceinline__ BetaHead beta_head(float u, float v, float x, float floor) {
+    const double a = beta_shape(u, floor), b = beta_shape(v, floor), s = a + b;
     const double xc = beta_clamp_x(x);
     const double lx = log(xc), l1 = log1p(-xc);
     const double lnb = lgamma(a) + lgamma(b) - lgamma(s);
@@ -79,6 +88,14 @@ __device__ __forceinline__ BetaHead beta_head(float u, float v, float x) {
     h.g[2] = (-(a - 1.0) * ta + (s - 2.0) * ts) * su;
     h.g[3] = (-(b - 1.0) * tb + (s - 2.0) * ts) * sv;
     return h;
+}
+
+__device__ __forceinline__ double beta_lnb(double a, double b) { return lgamma(a) + lgamma(b) - lgamma(a + b); }
+
+__device__ __forceinline__ double beta_kl(double a1, double b1, double a2, double b2) {
+    const double s1 = a1 + b1;
+    return beta_lnb(a2, b2) - beta_lnb(a1, b1) + (a1 - a2) * beta_digamma(a1) + (b1 - b2) * beta_digamma(b1)
+           + (a2 - a1 + b2 - b1) * beta_digamma(s1);
 }
 
 }  // namespace sbk

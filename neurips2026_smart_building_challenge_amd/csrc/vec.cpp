@@ -15,6 +15,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <cmath>
 #include <map>
 #include <memory>
 #include <string>
@@ -32,17 +33,20 @@ extern "C" int sbk_launch_policy(const float* obs, const float* w1, const float*
                                  const float* b2, const float* w3, const float* b3, float* h1, float* h2, float* y,
                                  float* actions, const int* n_cont, const int* n_disc, int n, uint64_t seed,
                                  uint32_t step, float* draws, float* hlp, float* hent, float* logp, float* entropy,
-                                 hipStream_t s);
+                                 float floor, hipStream_t s);
 extern "C" int sbk_launch_beta_eval(const float* y, const float* draws, const int* n_cont, const int* n_disc, int n,
-                                    float* hlp, float* hent, float* grad, float* logp, float* entropy,
+                                    float* hlp, float* hent, float* grad, float* logp, float* entropy, float floor,
                                     hipStream_t s);
+extern "C" int sbk_launch_ppo_beta(const float* y_new, const float* y_old, const float* draws, const float* logp_old,
+                                   const float* adv, const int* n_cont, const int* n_disc, int n, float floor,
+                                   float clip, float ent_coef, int per_dim, float* out, float* grad, hipStream_t s);
 extern "C" int sbk_launch_beta_sample(const float* alpha, const float* beta, float* out, int n, uint64_t seed,
                                       hipStream_t s);
 extern "C" int sbk_noalloc_max_envs(void);
 extern "C" int sbk_launch_policy_noalloc(const float* obs, const float* w1, const float* b1, const float* w2,
                                          const float* b2, const float* w3, const float* b3, float* actions,
                                          const int* n_cont, const int* n_disc, int n, uint64_t seed, uint32_t step,
-                                         hipStream_t s);
+                                         float floor, hipStream_t s);
 extern "C" int sbk_launch_live_sums(const sbk::EnvDesc* envs, const sbk::DevLayout* layouts,
                                     const unsigned char* state, int n, double* out, hipStream_t s);
 extern "C" int sbk_launch_gen_actions(float* actions, const int* n_cont, const int* n_disc, int n_envs,
@@ -1658,9 +1662,18 @@ float sbx_time_step(Env* envs, int iters) {
     return ms;
 }
 
+static bool policy_ok(const SbxPolicy* p) {
+    if (!p || !p->w1 || !p->b1 || !p->w2 || !p->b2 || !p->w3 || !p->b3) { g_err = "null policy weight"; return false; }
+    if (!(p->beta_floor >= 0.0f) || !std::isfinite(p->beta_floor)) {
+        g_err = "policy beta_floor must be finite and >= 0";
+        return false;
+    }
+    return true;
+}
+
 int sbx_policy_bind(Env* envs, const SbxPolicy* p) {
     Vec* v = vec_of(envs);
-    if (!p || !p->w1 || !p->b1 || !p->w2 || !p->b2 || !p->w3 || !p->b3) { g_err = "null policy weight"; return -1; }
+    if (!policy_ok(p)) return -1;
     v->pol = *p;
     if (!v->p_h1) {
         hip_ok(hipMalloc(&v->p_h1, sizeof(float) * (size_t)v->n * SBX_POLICY_HIDDEN), "hipMalloc(policy)");
@@ -1678,21 +1691,21 @@ int sbx_policy_act(Env* envs, uint64_t seed, uint32_t step) {
     const SbxPolicy& p = v->pol;
     int rc = sbk_launch_policy(v->obs, p.w1, p.b1, p.w2, p.b2, p.w3, p.b3, v->p_h1, v->p_h2, v->p_y, v->actions,
                                v->d_ncont, v->d_ndisc, v->n, seed, step, nullptr, nullptr, nullptr, nullptr, nullptr,
-                               g_stream);
+                               p.beta_floor, g_stream);
     if (rc != 0) die(std::string("policy launch failed: ") + hipGetErrorString((hipError_t)rc));
     return 0;
 }
 
 int sbx_policy_act_noalloc(Env* envs, const SbxPolicy* p, uint64_t seed, uint32_t step) {
     Vec* v = vec_of(envs);
-    if (!p || !p->w1 || !p->b1 || !p->w2 || !p->b2 || !p->w3 || !p->b3) { g_err = "null policy weight"; return -1; }
+    if (!policy_ok(p)) return -1;
     if (v->n > sbk_noalloc_max_envs()) {
         g_err = "sbx_policy_act_noalloc: " + std::to_string(v->n) + " envs, at most "
                 + std::to_string(sbk_noalloc_max_envs());
         return -1;
     }
     int rc = sbk_launch_policy_noalloc(v->obs, p->w1, p->b1, p->w2, p->b2, p->w3, p->b3, v->actions, v->d_ncont,
-                                       v->d_ndisc, v->n, seed, step, g_stream);
+                                       v->d_ndisc, v->n, seed, step, p->beta_floor, g_stream);
     if (rc != 0) {
         g_err = std::string("sbx_policy_act_noalloc: ") + hipGetErrorString((hipError_t)rc);
         return -1;
@@ -1707,7 +1720,7 @@ int sbx_policy_act_logp(Env* envs, uint64_t seed, uint32_t step, float* draws, f
     const SbxPolicy& p = v->pol;
     int rc = sbk_launch_policy(v->obs, p.w1, p.b1, p.w2, p.b2, p.w3, p.b3, v->p_h1, v->p_h2, v->p_y, v->actions,
                                v->d_ncont, v->d_ndisc, v->n, seed, step, draws, v->p_hlp, v->p_hent, logp, entropy,
-                               g_stream);
+                               p.beta_floor, g_stream);
     if (rc != 0) die(std::string("policy launch failed: ") + hipGetErrorString((hipError_t)rc));
     return 0;
 }
@@ -1717,8 +1730,25 @@ int sbx_beta_eval(Env* envs, const float* y, const float* draws, float* logp, fl
     if (!v->p_hlp) { g_err = "sbx_beta_eval before sbx_policy_bind"; return -1; }
     if (!y || !draws || !logp || !entropy) { g_err = "sbx_beta_eval: null argument"; return -1; }
     int rc = sbk_launch_beta_eval(y, draws, v->d_ncont, v->d_ndisc, v->n, v->p_hlp, v->p_hent, grad, logp, entropy,
-                                  g_stream);
+                                  v->pol.beta_floor, g_stream);
     if (rc != 0) die(std::string("beta eval launch failed: ") + hipGetErrorString((hipError_t)rc));
+    return 0;
+}
+
+int sbx_ppo_beta(Env* envs, const float* y_new, const float* y_old, const float* draws, const float* logp_old,
+                 const float* adv, const SbxPpo* args, float* out, float* grad) {
+    Vec* v = vec_of(envs);
+    if (!y_new || !y_old || !draws || !logp_old || !adv || !args || !out) {
+        g_err = "sbx_ppo_beta: null argument";
+        return -1;
+    }
+    if (!(args->beta_floor >= 0.0f) || !std::isfinite(args->beta_floor) || !(args->clip_coef >= 0.0f)) {
+        g_err = "sbx_ppo_beta: beta_floor and clip_coef must be >= 0";
+        return -1;
+    }
+    int rc = sbk_launch_ppo_beta(y_new, y_old, draws, logp_old, adv, v->d_ncont, v->d_ndisc, v->n, args->beta_floor,
+                                 args->clip_coef, args->ent_coef, args->ratio_per_dim, out, grad, g_stream);
+    if (rc != 0) die(std::string("ppo beta launch failed: ") + hipGetErrorString((hipError_t)rc));
     return 0;
 }
 

@@ -82,7 +82,17 @@ class SbxPlan(ctypes.Structure):
 
 
 class SbxPolicy(ctypes.Structure):
-    _fields_ = [(k, ctypes.c_void_p) for k in ("w1", "b1", "w2", "b2", "w3", "b3")]
+    _fields_ = [(k, ctypes.c_void_p) for k in ("w1", "b1", "w2", "b2", "w3", "b3")] + [("beta_floor", ctypes.c_float)]
+
+
+class SbxPpo(ctypes.Structure):
+    _fields_ = [("clip_coef", ctypes.c_float), ("ent_coef", ctypes.c_float), ("ratio_per_dim", ctypes.c_int),
+                ("beta_floor", ctypes.c_float)]
+
+
+def policy_struct(weights: dict, beta_floor: float = 1.0) -> SbxPolicy:
+    return SbxPolicy(*[ctypes.c_void_p(weights[k].data_ptr()) for k in ("w1", "b1", "w2", "b2", "w3", "b3")],
+                     float(beta_floor))
 
 
 POLICY_HIDDEN, POLICY_HEADS = 128, 544
@@ -94,7 +104,7 @@ EXPORTS = [
     "puf_render", "puf_close", "puf_log", "puf_live_log", "puf_mask_init", "sbx_gen_actions",
     "sbx_vec_info", "sbx_env_state", "sbx_time_step", "sbx_step_actions", "sbx_phase_times", "sbx_phase_stamps", "sbx_kernel_timer", "sbx_pass_times", "sbx_solve_info",
     "sbx_policy_bind", "sbx_policy_act", "sbx_policy_act_noalloc", "sbx_policy_heads", "sbx_beta_sample",
-    "sbx_policy_act_logp", "sbx_beta_eval",
+    "sbx_policy_act_logp", "sbx_beta_eval", "sbx_ppo_beta",
     "sbx_env_meta", "sbx_scenario_path",
     "sbx_plan_layout", "sbx_plan_free", "sbx_last_error", "sbx_version",
 ]
@@ -144,6 +154,7 @@ def lib() -> ctypes.CDLL:
         L.sbx_beta_sample.argtypes = [P, P, P, ctypes.c_int, ctypes.c_uint64, P]
         L.sbx_policy_act_logp.argtypes = [ctypes.POINTER(Env), ctypes.c_uint64, ctypes.c_uint32, P, P, P]
         L.sbx_beta_eval.argtypes = [ctypes.POINTER(Env), P, P, P, P, P]
+        L.sbx_ppo_beta.argtypes = [ctypes.POINTER(Env), P, P, P, P, P, ctypes.POINTER(SbxPpo), P, P]
         L.sbx_phase_stamps.argtypes = [ctypes.POINTER(Env), P, ctypes.c_int]
         L.sbx_phase_stamps.restype = ctypes.c_int
         L.sbx_solve_info.argtypes = [ctypes.POINTER(Env), ctypes.c_int, P]
@@ -319,10 +330,10 @@ class VecEnv:
         self.L.sbx_env_meta(self.envs, i, ctypes.byref(s), ctypes.byref(st), ctypes.byref(sd))
         return self.L.sbx_scenario_path(self.envs, s.value).decode(), st.value, sd.value
 
-    def policy_bind(self, weights: dict) -> None:
+    def policy_bind(self, weights: dict, beta_floor: float = 1.0) -> None:
         """Binds caller-owned policy weights (device float32, [in][out]); see policy_weights."""
         self._policy = weights   # keeps the tensors alive
-        p = SbxPolicy(*[ctypes.c_void_p(weights[k].data_ptr()) for k in ("w1", "b1", "w2", "b2", "w3", "b3")])
+        p = policy_struct(weights, beta_floor)
         if self.L.sbx_policy_bind(self.envs, ctypes.byref(p)) != 0:
             raise RuntimeError(self.L.sbx_last_error().decode())
 
@@ -331,9 +342,9 @@ class VecEnv:
         if self.L.sbx_policy_act(self.envs, seed, step) != 0:
             raise RuntimeError(self.L.sbx_last_error().decode())
 
-    def policy_act_noalloc(self, weights: dict, seed: int, step: int) -> None:
+    def policy_act_noalloc(self, weights: dict, seed: int, step: int, beta_floor: float = 1.0) -> None:
         """policy_act through the allocation-free entry point (weights per call, no bind)."""
-        p = SbxPolicy(*[ctypes.c_void_p(weights[k].data_ptr()) for k in ("w1", "b1", "w2", "b2", "w3", "b3")])
+        p = policy_struct(weights, beta_floor)
         if self.L.sbx_policy_act_noalloc(self.envs, ctypes.byref(p), seed, step) != 0:
             raise RuntimeError(self.L.sbx_last_error().decode())
 
@@ -362,6 +373,21 @@ class VecEnv:
                                 P(ent.data_ptr()), P(g.data_ptr()) if grad else None) != 0:
             raise RuntimeError(self.L.sbx_last_error().decode())
         return logp, ent, g
+
+    def ppo_beta(self, y_new, y_old, draws, logp_old, adv, clip_coef: float = 0.2, ent_coef: float = 0.0,
+                 ratio_per_dim: bool = True, beta_floor: float = 1.0, grad: bool = True):
+        """PPO side of the Beta heads (sbx_ppo_beta): per-env out (n, 6) = logp, entropy,
+        KL(old || new), ratio, pg loss, log-ratio; grad (n, 2, 272) of pg - ent_coef H in u, v."""
+        t = self.torch
+        dev = self.obs.device
+        args = [a.contiguous() for a in (y_new, y_old, draws, logp_old, adv)]
+        out = t.empty((self.n, 6), dtype=t.float32, device=dev)
+        g = t.empty((self.n, 2, SB_ACT), dtype=t.float32, device=dev) if grad else None
+        a = SbxPpo(float(clip_coef), float(ent_coef), int(bool(ratio_per_dim)), float(beta_floor))
+        if self.L.sbx_ppo_beta(self.envs, *[P(x.data_ptr()) for x in args], ctypes.byref(a), P(out.data_ptr()),
+                               P(g.data_ptr()) if grad else None) != 0:
+            raise RuntimeError(self.L.sbx_last_error().decode())
+        return out, g
 
     def policy_heads(self) -> np.ndarray:
         """Head outputs y (n, 544) of the last policy_act."""

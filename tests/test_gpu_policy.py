@@ -70,8 +70,11 @@ def test_gpu_policy_heads_and_actions(mixed_dir):
     vec.close()
 
 
-@pytest.mark.parametrize("a,b", [(1.0, 1.0), (2.0, 2.0), (1.3, 5.0), (8.0, 1.5), (30.0, 30.0)])
+@pytest.mark.parametrize("a,b", [(1.0, 1.0), (2.0, 2.0), (1.3, 5.0), (8.0, 1.5), (30.0, 30.0),
+                                 (0.3, 0.5), (0.6, 2.5), (4.0, 0.45), (150.0, 300.0), (400.0, 90.0), (700.0, 650.0)])
 def test_gpu_beta_sampler_law(a, b):
+    """Shapes below 1 (boosted draws) and in the hundreds (where 1 - t + log t would
+    cancel) included."""
     from scipy import stats
 
     n = 200_000
@@ -82,7 +85,10 @@ def test_gpu_beta_sampler_law(a, b):
     torch.cuda.synchronize()
     assert torch.equal(x, x2)
     x = x.cpu().double().numpy()
-    assert np.all(x > 0.0) and np.all(x < 1.0)
+    if min(a, b) >= 1.0:
+        assert np.all(x > 0.0) and np.all(x < 1.0)
+    else:
+        assert np.all(x >= 0.0) and np.all(x <= 1.0)
     mean = a / (a + b)
     var = a * b / ((a + b) ** 2 * (a + b + 1))
     assert abs(x.mean() - mean) < 5 * np.sqrt(var / n)
@@ -127,12 +133,12 @@ def _softplus32(x: np.ndarray) -> np.ndarray:
     return np.where(x > 20.0, x, np.log1p(np.exp(x)).astype(np.float32)).astype(np.float32)
 
 
-def _beta_ref(u, v, x):
+def _beta_ref(u, v, x, floor=1.0):
     """float64 log-density and entropy (scipy) at the float32 shapes."""
     from scipy import stats
 
-    a = (_softplus32(u) + np.float32(1.0)).astype(np.float64)
-    b = (_softplus32(v) + np.float32(1.0)).astype(np.float64)
+    a = (_softplus32(u) + np.float32(floor)).astype(np.float64)
+    b = (_softplus32(v) + np.float32(floor)).astype(np.float64)
     xc = np.clip(x.astype(np.float64), 2.0**-24, 1.0 - 2.0**-24)
     return stats.beta.logpdf(xc, a, b), stats.beta.entropy(a, b)
 
@@ -200,4 +206,121 @@ def test_gpu_policy_act_logp_consistent(mixed_dir):
         assert np.array_equal(a[i, :nc], (np.float32(2.0) * d[i, :nc] - np.float32(1.0)).astype(np.float32))
         assert np.array_equal(a[i, 256:256 + nd], (d[i, 256:256 + nd] > 0.5).astype(np.float32))
         assert np.all(d[i, nc:256] == 0.0) and np.all(d[i, 256 + nd:] == 0.0)
+    vec.close()
+
+
+def _heads_of(vec, i):
+    nc, nd = vec.envs[i].n_cont, vec.envs[i].n_disc
+    heads = list(range(nc)) + [256 + d for d in range(nd)]
+    cu = np.array([h if h < 256 else 512 + h - 256 for h in heads])
+    cv = np.array([256 + h if h < 256 else 528 + h - 256 for h in heads])
+    return np.array(heads), cu, cv
+
+
+def _shapes(y, floor):
+    return (_softplus32(y) + np.float32(floor)).astype(np.float64)
+
+
+def _ppo_ref(yn, yo, x, lp_old, adv, floor, clip, ent_coef, per_dim):
+    """float64 restatement from scipy.stats.beta (log-density, entropy), the KL
+    closed form (pinned against quadrature in tests/test_policy_math.py) and the
+    clipped surrogate of Schulman et al. 2017: (logp, H, KL, r, pg, lr, loss)."""
+    from scipy import stats
+
+    from test_policy_math import beta_kl
+
+    an, bn = _shapes(yn[0], floor), _shapes(yn[1], floor)
+    ao, bo = _shapes(yo[0], floor), _shapes(yo[1], floor)
+    xc = np.clip(x.astype(np.float64), 2.0**-24, 1.0 - 2.0**-24)
+    lp = stats.beta.logpdf(xc, an, bn).sum()
+    en = stats.beta.entropy(an, bn).sum()
+    kl = beta_kl(ao, bo, an, bn).sum()
+    D = len(x)
+    lr = (lp - lp_old) / (D if per_dim else 1)
+    lr = min(20.0, max(-20.0, lr))
+    r = np.exp(lr)
+    pg = (D if per_dim else 1) * max(-adv * r, -adv * min(1 + clip, max(1 - clip, r)))
+    return lp, en, kl, r, pg, lr, pg - ent_coef * en
+
+
+@pytest.mark.parametrize("floor,per_dim", [(1.0, True), (1.0, False), (0.25, True)])
+def test_gpu_ppo_beta_matches_reference(mixed_dir, floor, per_dim):
+    """sbx_ppo_beta against a float64 evaluation: per-env log-probability, entropy,
+    KL(old || new), ratio, clipped surrogate and log-ratio; the per-head gradients of
+    pg - ent_coef H in u and v against central differences of that evaluation (on
+    heads whose ratio is inside and outside the clip range). floor 0.25 exercises
+    shapes below 1."""
+    print(f"ppo beta: floor {floor}, ratio_per_dim {per_dim}", flush=True)
+    vec = E.VecEnv(30, blob_dir=str(mixed_dir), groups=30)
+    rng = np.random.default_rng(5)
+    yn = rng.normal(0.0, 1.5, (vec.n, E.POLICY_HEADS)).astype(np.float32)
+    yo = (yn + rng.normal(0.0, 0.05, yn.shape)).astype(np.float32)
+    x = rng.uniform(0.02, 0.98, (vec.n, E.SB_ACT)).astype(np.float32)
+    clip, ent_coef = 0.2, 0.01
+    lp_old = np.zeros(vec.n, np.float32)
+    adv = rng.normal(0.0, 1.0, vec.n).astype(np.float32)
+    refs = []
+    for i in range(vec.n):
+        heads, cu, cv = _heads_of(vec, i)
+        ref0 = _ppo_ref((yn[i, cu], yn[i, cv]), (yo[i, cu], yo[i, cv]), x[i, heads], 0.0, adv[i], floor, clip,
+                        ent_coef, per_dim)
+        # stored log-probabilities that put half the envs' ratios outside the clip range
+        shift = (0.5 if i % 2 else 0.02) * (len(heads) if per_dim else 1)
+        lp_old[i] = np.float32(ref0[0] + (shift if i % 4 < 2 else -shift))
+        refs.append((heads, cu, cv))
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    out, g = vec.ppo_beta(T(yn), T(yo), T(x), T(lp_old), T(adv), clip, ent_coef, per_dim, floor)
+    torch.cuda.synchronize()
+    out, g = out.cpu().numpy(), g.cpu().numpy()
+    clipped = 0
+    for i in range(vec.n):
+        heads, cu, cv = refs[i]
+        ref = _ppo_ref((yn[i, cu], yn[i, cv]), (yo[i, cu], yo[i, cv]), x[i, heads], float(lp_old[i]), float(adv[i]),
+                       floor, clip, ent_coef, per_dim)
+        for k in range(6):
+            tol = 2e-5 * max(1.0, abs(ref[k])) if k != 3 else 1e-4 * ref[3]
+            assert abs(out[i, k] - ref[k]) <= tol, (i, k, out[i, k], ref[k])
+        clipped += abs(ref[3] - 1.0) > clip
+        unused = np.setdiff1d(np.arange(E.SB_ACT), heads)
+        assert np.all(g[i][:, unused] == 0.0)
+        if i < 6:
+            hh = 1e-3
+            for which, cols in ((0, cu), (1, cv)):
+                for j in range(0, len(heads), 7):
+                    yp, ym = yn[i].astype(np.float64), yn[i].astype(np.float64)
+                    yp, ym = yp.copy(), ym.copy()
+                    yp[cols[j]] += hh
+                    ym[cols[j]] -= hh
+                    fp = _ppo_ref((yp[cu], yp[cv]), (yo[i, cu], yo[i, cv]), x[i, heads], float(lp_old[i]),
+                                  float(adv[i]), floor, clip, ent_coef, per_dim)[6]
+                    fm = _ppo_ref((ym[cu], ym[cv]), (yo[i, cu], yo[i, cv]), x[i, heads], float(lp_old[i]),
+                                  float(adv[i]), floor, clip, ent_coef, per_dim)[6]
+                    want = (fp - fm) / (2 * hh)
+                    assert abs(g[i, which, heads[j]] - want) <= 2e-3 * max(1.0, abs(want)), (i, which, j)
+    assert 0 < clipped < vec.n
+    vec.close()
+
+
+def test_gpu_beta_eval_floor_below_one(mixed_dir):
+    """sbx_beta_eval with a shape floor of 0.25 (shapes below 1) against scipy."""
+    print("beta eval, floor 0.25", flush=True)
+    vec = E.VecEnv(30, blob_dir=str(mixed_dir), groups=30)
+    vec.policy_bind(E.policy_weights(3), beta_floor=0.25)
+    rng = np.random.default_rng(12)
+    y = rng.normal(-1.0, 2.0, (vec.n, E.POLICY_HEADS)).astype(np.float32)
+    x = rng.uniform(0.0, 1.0, (vec.n, E.SB_ACT)).astype(np.float32)
+    logp, ent, _ = vec.beta_eval(torch.from_numpy(y).cuda(), torch.from_numpy(x).cuda())
+    torch.cuda.synchronize()
+    logp, ent = logp.cpu().numpy(), ent.cpu().numpy()
+    for i in range(vec.n):
+        heads, cu, cv = _heads_of(vec, i)
+        lp, en = _beta_ref(y[i, cu], y[i, cv], x[i, heads], floor=0.25)
+        assert abs(logp[i] - lp.sum()) <= 2e-5 * max(1.0, np.abs(lp).sum()), (i, logp[i], lp.sum())
+        assert abs(ent[i] - en.sum()) <= 2e-5 * max(1.0, np.abs(en).sum()), (i, ent[i], en.sum())
+    # the policy with that floor draws inside [0, 1] and writes legal action rows
+    vec.reset()
+    vec.policy_act(3, 0)
+    torch.cuda.synchronize()
+    act = vec.actions.cpu().numpy()
+    assert np.all(np.abs(act[:, :256]) <= 1.0) and set(np.unique(act[:, 256:])) <= {0.0, 1.0}
     vec.close()
