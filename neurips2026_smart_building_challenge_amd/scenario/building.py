@@ -43,6 +43,29 @@ VAV_FIELDS = 6    # ids 0..5
 HWS_FIELDS = 7    # ids 0..6
 N_AUX = 7         # hod cos/sin, dow cos/sin, comfort now/soon, occupants
 
+# Observation field names (the env's field_names, bake_env.py:112-113): device
+# fields are "<device>_<measurement>", one measurement name per id of the maps
+# at bake_env.py:228-250 (where two names share an id, the sensor's).
+AHU_MEAS = ["cooling_request_count", "supply_air_static_pressure_sensor", "supply_air_flowrate_sensor",
+            "supply_air_temperature_setpoint", "supply_fan_run_command", "supply_fan_speed_percentage_command",
+            "outside_air_flowrate_sensor", "supervisor_run_command", "recirculation_percentage_command",
+            "outside_air_temperature_sensor"]
+VAV_MEAS = ["reheat_valve_percentage_command", "supply_air_damper_percentage_command",
+            "supply_air_flowrate_setpoint", "zone_air_cooling_temperature_setpoint_sensor",
+            "zone_air_heating_temperature_setpoint_sensor", "zone_air_temperature_sensor"]
+HWS_MEAS = ["differential_pressure_setpoint", "supply_water_temperature_sensor", "differential_pressure_sensor",
+            "supervisor_run_command", "heating_request_count", "run_status", "supply_water_temperature_setpoint"]
+AUX_NAMES = ["hod_cos_000", "hod_sin_000", "dow_cos_000", "dow_sin_000", "comfort_mode_now", "comfort_mode_soon",
+             "num_occupants"]
+
+
+def field_name(kind: int, idx: int, obs_id: int) -> str:
+    if kind == 2:
+        return "hws_" + HWS_MEAS[obs_id]
+    if kind == 0:
+        return f"ahs_ahu_{idx + 1}_" + AHU_MEAS[obs_id]
+    return f"VAV_{idx + 1}_" + VAV_MEAS[obs_id]
+
 
 @dataclass
 class Building:
@@ -268,21 +291,24 @@ def make_building(n_zones: int, n_ahu: int, seed: int, name: str | None = None) 
                              2.0, 0.6, 1.5, 0.05, 0.05])
     pump_const = np.array([10.0, 0.7])
 
-    # ---- actions: per VAV damper+reheat, per AHU sat/static/recirc/run, HWS ----
+    # ---- actions: per AHU sat/static/recirc/run, HWS, per VAV damper+reheat ----
+    # (the order of the competition env's action names: the discrete actions
+    # are the AHU run commands in AHU order, then the hot-water run command,
+    # which its baseline controllers index by position)
     kind, idx, act, disc, amin, amax = [], [], [], [], [], []
 
     def add_act(k, i, a, d, lo, hi):
         kind.append(k); idx.append(i); act.append(a); disc.append(d)
         amin.append(lo); amax.append(hi)
 
-    add_act(2, 0, 0, 0, T0 + 35.0, T0 + 75.0)     # supply water temperature setpoint
-    add_act(2, 0, 1, 0, 0.3, 2.0)                 # differential pressure setpoint (bar)
-    add_act(2, 0, 2, 1, 0.0, 1.0)                 # HWS run
     for a in range(A):
         add_act(0, a, 0, 0, T0 + 12.0, T0 + 24.0)  # supply air temperature setpoint
         add_act(0, a, 1, 0, 100.0, 1000.0)         # static pressure setpoint
         add_act(0, a, 2, 0, 0.0, 1.0)              # recirculation command
         add_act(0, a, 3, 1, 0.0, 1.0)              # run command
+    add_act(2, 0, 0, 0, T0 + 35.0, T0 + 75.0)     # supply water temperature setpoint
+    add_act(2, 0, 1, 0, 0.3, 2.0)                 # differential pressure setpoint (bar)
+    add_act(2, 0, 2, 1, 0.0, 1.0)                 # HWS run
     for v in range(Z):
         add_act(1, v, 0, 0, 0.0, 1.0)              # damper command
         add_act(1, v, 1, 0, 0.0, 1.0)              # reheat valve command

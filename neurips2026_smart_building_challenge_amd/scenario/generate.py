@@ -26,7 +26,7 @@ from pathlib import Path
 
 import numpy as np
 
-from .building import DT_SEC, N_AUX, T0, Building, make_building
+from .building import AUX_NAMES, DT_SEC, N_AUX, T0, Building, field_name, make_building
 from .factor import factorize
 from .sbb import SbbWriter
 
@@ -63,6 +63,11 @@ class ClimateSpec:
         return f"m{self.mean_c:+05.1f}a{self.amp_c:04.1f}".replace("+", "p").replace("-", "n")
 
 
+COMFORT_HOURS = (6, 19)      # comfort mode on workdays from 06:00 to 19:00
+COMFORT_SP = (21.0, 24.0)    # heating / cooling setpoints (C) in comfort mode
+ECO_SP = (15.0, 29.0)        # ... and outside it
+
+
 def calendar_tables(n1: int) -> dict[str, np.ndarray]:
     k = np.arange(n1)
     day = k // STEPS_PER_DAY
@@ -71,13 +76,14 @@ def calendar_tables(n1: int) -> dict[str, np.ndarray]:
     dow = day % 7
     workday = (dow < 5).astype(np.uint8)
     month = np.array([(START_DATE + _dt.timedelta(days=int(d))).month for d in range(int(day[-1]) + 1)])[day]
-    comfort = ((workday == 1) & (hour >= 6) & (hour < 19)).astype(np.float64)
+    h0, h1 = COMFORT_HOURS
+    comfort = ((workday == 1) & (hour >= h0) & (hour < h1)).astype(np.float64)
     k_soon = k + 12
     day_s = k_soon // STEPS_PER_DAY
     hour_s = (k_soon % STEPS_PER_DAY) // 12
-    comfort_soon = (((day_s % 7) < 5) & (hour_s >= 6) & (hour_s < 19)).astype(np.float64)
-    heat = np.where(comfort > 0, T0 + 21.0, T0 + 15.0)
-    cool = np.where(comfort > 0, T0 + 24.0, T0 + 29.0)
+    comfort_soon = (((day_s % 7) < 5) & (hour_s >= h0) & (hour_s < h1)).astype(np.float64)
+    heat = np.where(comfort > 0, T0 + COMFORT_SP[0], T0 + ECO_SP[0])
+    cool = np.where(comfort > 0, T0 + COMFORT_SP[1], T0 + ECO_SP[1])
     km1 = k - 1
     day_m1 = np.floor_divide(km1, STEPS_PER_DAY)
     hour_m1 = (km1 % STEPS_PER_DAY) // 12
@@ -284,6 +290,12 @@ def scenario_writer(spec: LayoutSpec, clim: ClimateSpec, table_steps: int,
     w.add("f_norm_var", b.f_norm_var, "f64")
     w.scalar_i64("n_dev", b.f_dev_kind.size)
     w.scalar_i64("n_aux", N_AUX)
+    names = [field_name(int(k), int(i), int(o)) for k, i, o in zip(b.f_dev_kind, b.f_dev_idx, b.f_obs_id)]
+    w.text("field_names", "\n".join(names + AUX_NAMES))
+    # schedule (bake_env.py:103-108): morning / evening start hour, comfort and
+    # eco (heating, cooling) windows, as calendar_tables draws them
+    w.add("sched_scalars", [float(COMFORT_HOURS[0]), float(COMFORT_HOURS[1]), T0 + COMFORT_SP[0], T0 + COMFORT_SP[1],
+                            T0 + ECO_SP[0], T0 + ECO_SP[1]], "f64")
     w.add("obs_meta", [1.0, 1.0, 1.0, float(EPISODE_STEPS), DT_SEC], "f64")
     # ---- calendar / weather / occupancy ----
     cal = calendar_tables(n1)

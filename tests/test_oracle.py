@@ -136,13 +136,13 @@ def test_decode_end_points(tmp_path):
     n, nv, na = 123, 41, 1
     sat = st[2 * n + 4 * nv + na]            # ahu_sat after apply
     mn = d["act_min_native"][d["act_is_discrete"] == 0]
-    # AHU 0 supply temperature is the third continuous action (after the two HWS setpoints)
-    assert sat == float(np.float32(mn[2]))
+    # AHU 0 supply temperature is the first continuous action
+    assert sat == float(np.float32(mn[0]))
     row[:env.n_cont] = 7.0                    # clamps to +1
     env.step(row)
     st = env.state()
     mx = d["act_max_native"][d["act_is_discrete"] == 0]
-    want = np.float32(np.float32(2.0) / np.float32(2.0) * np.float32(mx[2] - mn[2]) + np.float32(mn[2]))
+    want = np.float32(np.float32(2.0) / np.float32(2.0) * np.float32(mx[0] - mn[0]) + np.float32(mn[0]))
     assert st[2 * n + 4 * nv + na] == float(want)
 
 
