@@ -319,13 +319,14 @@ def make_building(n_zones: int, n_ahu: int, seed: int, name: str | None = None) 
                 (float(Z), 0.0), (0.9, 0.09), (T0 + 55.0, 100.0)]
     for i, (m, s2) in enumerate(hws_norm):
         fk.append(2); fi.append(0); fo.append(i); fm.append(m); fv.append(s2)
+    # one (mean, variance) per measurement name, as the env's normalizer keeps
+    # them (bake_env.py:125-131), from the building's average air handler
+    nserv = Z / A
+    mflow = float(ahu_const[:, 1].mean())
+    ahu_norm = [(nserv / 2.0, nserv * nserv / 8.0), (400.0, 4.0e4), (0.5 * mflow, 0.1 * mflow ** 2),
+                (T0 + 15.0, 9.0), (0.9, 0.09), (0.5, 0.08), (0.15 * mflow, 0.02 * mflow ** 2),
+                (0.9, 0.09), (0.6, 0.06), (T0 + 10.0, 120.0)]
     for a in range(A):
-        nserv = int((vav_ahu == a).sum())
-        ahu_norm = [(nserv / 2.0, nserv * nserv / 8.0), (400.0, 4.0e4),
-                    (0.5 * ahu_const[a, 1], 0.1 * ahu_const[a, 1] ** 2),
-                    (T0 + 15.0, 9.0), (0.9, 0.09), (0.5, 0.08),
-                    (0.15 * ahu_const[a, 1], 0.02 * ahu_const[a, 1] ** 2),
-                    (0.9, 0.09), (0.6, 0.06), (T0 + 10.0, 120.0)]
         for i, (m, s2) in enumerate(ahu_norm):
             fk.append(0); fi.append(a); fo.append(i); fm.append(m); fv.append(s2)
     for v in range(Z):

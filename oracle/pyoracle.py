@@ -216,6 +216,69 @@ class CpuEnv:
         return self._st[:n].copy()
 
 
+CN_OBS, CN_ACT = 983, 219
+
+
+class Canon:
+    """The oracle's canonical layout of one blob (oracle/sbo_canon.c): the
+    pid_water base controller, the canonical observation, the comfort guard
+    and the residual / absolute action decode, one env and one step at a time."""
+
+    def __init__(self, path):
+        L = lib("oracle").lib
+        L.sbo_canon_size.restype = ctypes.c_size_t
+        L.sbo_canon_open.argtypes = [P, ctypes.c_char_p]
+        L.sbo_canon_base.argtypes = [P, P, P, P, P]
+        L.sbo_canon_features.argtypes = [P, P, P, P, P, P]
+        L.sbo_canon_trust.argtypes = [P, P, ctypes.c_float, ctypes.c_float, ctypes.c_int, P]
+        L.sbo_canon_decode.argtypes = [P, P, P, P, ctypes.c_int, ctypes.c_float, ctypes.c_float, P]
+        self.L = L
+        self.buf = ctypes.create_string_buffer(int(L.sbo_canon_size()))
+        rc = L.sbo_canon_open(ctypes.addressof(self.buf), str(path).encode())
+        if rc != 0:
+            raise ValueError(f"canonical layout not available for {path} ({rc})")
+        ints = np.frombuffer(self.buf, np.int32, count=4)
+        self.K, self.n_act, self.n_cont, self.n_disc = (int(v) for v in ints)
+        L.sbo_canon_slot.argtypes = [P, ctypes.c_int]
+        self.slot_of_action = np.array([L.sbo_canon_slot(self._p(), i) for i in range(self.n_act)])
+
+    def _p(self):
+        return ctypes.addressof(self.buf)
+
+    def base(self, obs: np.ndarray, pid: np.ndarray):
+        """pid (float64 [18]) is updated in place; returns (base [n_act] float32, ahu_info [18] float32)."""
+        o = np.ascontiguousarray(obs, np.float32)
+        assert pid.dtype == np.float64 and pid.size >= 18 and pid.flags.c_contiguous
+        base = np.zeros(self.n_act, np.float32)
+        ai = np.zeros(18, np.float32)
+        self.L.sbo_canon_base(self._p(), _ptr(o), _ptr(pid), _ptr(base), _ptr(ai))
+        return base, ai
+
+    def features(self, obs, base, ahu_info, pid) -> np.ndarray:
+        o = np.ascontiguousarray(obs, np.float32)
+        x = np.zeros(CN_OBS, np.float32)
+        self.L.sbo_canon_features(self._p(), _ptr(o), _ptr(np.ascontiguousarray(base, np.float32)),
+                                  _ptr(np.ascontiguousarray(ahu_info, np.float32)),
+                                  _ptr(np.ascontiguousarray(pid, np.float64)), _ptr(x))
+        return x
+
+    def trust(self, obs, d0: float, d1: float, hot: int) -> np.ndarray:
+        o = np.ascontiguousarray(obs, np.float32)
+        w = np.zeros(self.n_act, np.float32)
+        self.L.sbo_canon_trust(self._p(), _ptr(o), d0, d1, int(hot), _ptr(w))
+        return w
+
+    def decode(self, base, p_row, trust, resid: int, scale: float, dscale: float) -> np.ndarray:
+        """The native action row (272 floats) the env step decodes."""
+        row = np.zeros(SB_CONT + SB_DISC, np.float32)
+        pr = np.zeros(SB_CONT + SB_DISC, np.float32)
+        pr[:len(p_row)] = p_row
+        tr = None if trust is None else np.ascontiguousarray(trust, np.float32)
+        self.L.sbo_canon_decode(self._p(), _ptr(np.ascontiguousarray(base, np.float32)), _ptr(pr),
+                                _ptr(tr) if tr is not None else None, int(resid), scale, dscale, _ptr(row))
+        return row
+
+
 def desync_first_steps(env_index: int, episode_steps: int) -> int:
     """Length of env `env_index`'s first episode under the GPU env's desync
     (complete_port/gpu/smart_buildings.cu:2808-2815): a splitmix-style hash of

@@ -13,6 +13,7 @@
  */
 #ifndef SBO_H
 #define SBO_H
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -164,6 +165,46 @@ void sbo_conv_apply(const SboScen* sc, SboMt* r, int* left, int* right, double* 
 void sbo_decode(const SboScen* sc, const double* cont, const double* disc, double* native);
 void sbo_lu_solve(const SboScen* sc, const double* b, double* x, double* work);
 int sbo_dense_solve(int k, double* M, double* b);
+
+/* ---------------- canonical layout, pid_water base, residual decode ---------
+ * (sbo_canon.c; slot constants of complete_port/gpu/sb_gpu_base.inc:31-45) */
+#define SBO_CN_K 9
+#define SBO_CN_ZPA 10
+#define SBO_CN_ZS (SBO_CN_K * SBO_CN_ZPA)
+#define SBO_CN_OBS 983
+#define SBO_CN_ACT 219
+typedef struct {
+    int K, n_act, n_cont, n_disc;
+    int zc[SBO_CN_K];
+    /* zone slots: observation fields (temperature, heating / cooling setpoint,
+     * damper / reheat command) and native actions (damper, reheat); -1 absent */
+    int zT[SBO_CN_ZS], zH[SBO_CN_ZS], zC[SBO_CN_ZS], zD[SBO_CN_ZS], zR[SBO_CN_ZS], zAd[SBO_CN_ZS], zAr[SBO_CN_ZS];
+    /* AHU k: fields outside-air temp, static pressure, supply flow, outside-air
+     * flow, supply temp setpoint, recirculation, cooling requests, run command */
+    int aObs[SBO_CN_K][8];
+    int aT[SBO_CN_K], aP[SBO_CN_K], aRec[SBO_CN_K], aRun[SBO_CN_K];
+    /* hot water: supply temp, its setpoint, dP, dP setpoint, run status, requests */
+    int hObs[6];
+    int hW, hDPa, hRun;
+    int g[19];   /* hod sin x4, hod cos x4, dow sin x4, dow cos x4, comfort now, soon, occupants */
+    float tmean, tstd;
+    float fmean[SBO_OBS], fstd[SBO_OBS];
+    double comfort_lo, comfort_hi, eco_lo, eco_hi;
+    int morning, evening;
+    int slot_of_action[SBO_CONT + SBO_DISC];
+    int act_col[SBO_CONT + SBO_DISC];
+    uint8_t act_disc[SBO_CONT + SBO_DISC];
+} SboCanon;
+/* 0 ok, -1 a section is missing, -2 the building exceeds the canonical slots */
+int sbo_canon_open(SboCanon* c, const char* blob_path);
+size_t sbo_canon_size(void);
+int sbo_canon_slot(const SboCanon* c, int native_action);
+void sbo_canon_base(const SboCanon* c, const float* obs, double* pid, float* base, float* ahu_info);
+void sbo_canon_features(const SboCanon* c, const float* obs, const float* base, const float* ahu_info,
+                        const double* pid, float* out);
+void sbo_canon_trust(const SboCanon* c, const float* obs, float d0, float d1, int hot, float* trust);
+void sbo_canon_decode(const SboCanon* c, const float* base, const float* p_row, const float* trust, int resid,
+                      float scale, float dscale, float* native_row);
 
 double sbo_run_batch(SboEnv** envs, const int* env_ids, int n, int steps, uint64_t seed,
                      int nthreads, double* reward_sum);
