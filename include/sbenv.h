@@ -109,8 +109,10 @@ void dict_set(Dict* d, const char* key, float value);
  * groups, max_steps, reward_scale (<= 0 means 1), desync (1: each env's first
  * episode ends at a hashed step in [1, episode length] and stays out of the
  * episode log; smart_buildings.cu:2583-2590, 2808-2815, 1990-1993), and the
- * reference keys this env does not implement, accepted only at 0 (random_start,
- * rew_norm, rew_center, canonical, residual, plant_pair, guard_d1, guard_hot,
+ * canonical / residual / res_scale / res_dscale / guard_d0 / guard_d1 / guard_hot
+ * (the canonical policy interface over the on-device pid_water base, see
+ * sbx_canon_state), and the reference keys this env does not implement,
+ * accepted only at 0 (random_start, rew_norm, rew_center, plant_pair,
  * comfort_shape, zone_*, ahu_critic, interleave, prestart_explore, probe).
  * Extras: start_offsets (1: every env starts its episodes at its own seeded
  * calendar offset, start_seed), shard_base (this vec's first env index in a
@@ -306,6 +308,17 @@ int sbx_ppo_beta(Env* envs, const float* y_new, const float* y_old, const float*
  * on `stream` (hipStream_t; NULL = the null stream). Leaves the stream bound
  * by puf_bind_stream alone. Returns 0, or -1. */
 int sbx_beta_sample(const float* alpha, const float* beta, float* out, int n, uint64_t seed, void* stream);
+
+/* Canonical interface (kwargs canonical = 1, residual, res_scale, res_dscale,
+ * guard_d0/d1/hot; complete_port/gpu/sb_gpu_base.inc): the trainer's rows hold
+ * the canonical observation (983 floats) and canonical action heads (219,
+ * SBC_ACT; Env.n_cont reads 219, n_disc 0); the env keeps its own observation
+ * row internally and runs the pid_water base controller on it. Synchronous
+ * copy of env i's own observation row (SB_OBS floats), the base proposal per
+ * native action (SB_ACT floats) and the PID state (18 doubles: integral,
+ * previous error per AHU slot); each pointer may be NULL. Returns the env's
+ * native action count, or -1 (not canonical). */
+int sbx_canon_state(Env* envs, int i, float* raw_obs, float* base, double* pid);
 
 /* Scenario of env i (index into the sorted, round-robin ordered blob list),
  * its calendar start offset and occupancy seed. */

@@ -43,7 +43,7 @@ def build_product() -> Path:
     tmp = PKG / "_build"
     tmp.mkdir(exist_ok=True)
     inc = ["-I", str(ROOT / "include"), "-I", str(CSRC)]
-    for src in ["step_kernel.hip", "policy_kernel.hip"]:
+    for src in ["step_kernel.hip", "policy_kernel.hip", "canon_kernel.hip"]:
         o = tmp / (Path(src).stem + ".o")
         _run([hipcc, *HIP_FLAGS, *inc, "-c", str(CSRC / src), "-o", str(o)])
         objs.append(o)

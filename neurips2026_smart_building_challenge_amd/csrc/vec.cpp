@@ -21,6 +21,7 @@
 #include <string>
 #include <vector>
 
+#include "canon.h"
 #include "plan.h"
 #include "sbb_reader.h"
 #include "sbenv.h"
@@ -47,6 +48,7 @@ extern "C" int sbk_launch_policy_noalloc(const float* obs, const float* w1, cons
                                          const float* b2, const float* w3, const float* b3, float* actions,
                                          const int* n_cont, const int* n_disc, int n, uint64_t seed, uint32_t step,
                                          float floor, hipStream_t s);
+extern "C" int sbk_launch_canon(const sbk::CanonArgs* a, int post, hipStream_t s);
 extern "C" int sbk_launch_live_sums(const sbk::EnvDesc* envs, const sbk::DevLayout* layouts,
                                     const unsigned char* state, int n, double* out, hipStream_t s);
 extern "C" int sbk_launch_gen_actions(float* actions, const int* n_cont, const int* n_disc, int n_envs,
@@ -102,6 +104,7 @@ struct HostLayout {
     sbh::BlockPlan block;
     sbk::DevLayout dev{};   // sizes + layouts; pointers patched after upload
     std::map<std::string, size_t> off;
+    std::unique_ptr<sbk::CanonTab> canon;   // canonical maps (canonical mode only)
 };
 
 struct HostScen {
@@ -126,7 +129,7 @@ const char* kStructural[] = {
     "vav_const", "act_owner_kind", "act_owner_index", "act_actuator", "act_is_discrete", "act_min_native",
     "act_max_native", "act_min_norm", "act_max_norm", "f_dev_kind", "f_dev_idx", "f_obs_id", "f_norm_mean",
     "f_norm_var", "n_dev", "n_aux", "occ_params", "conv_room_offsets", "conv_room_cells", "conv_cand_offsets",
-    "conv_cand_idx", nullptr};
+    "conv_cand_idx", "field_names", "sched_scalars", nullptr};
 
 std::string structural_key(const sbh::Blob& b) {
     std::string k;
@@ -135,6 +138,150 @@ std::string structural_key(const sbh::Blob& b) {
         k += std::to_string(s.size()) + ":" + s;
     }
     return k;
+}
+
+// The canonical maps of one layout, found by name in the blob's observation
+// field names and its action owner tables as the reference does
+// (complete_port/gpu/smart_buildings.cu:844-1000 sb_canon_setup): zone slots
+// in the order the VAV temperature fields appear, slot 10 k + j on AHU k.
+bool make_canon(const sbh::Blob& b, sbk::CanonTab* C, std::string* err) {
+    memset(C, 0, sizeof(*C));
+    const sbh::Section* fs = b.find("field_names");
+    uint64_t cnt = 0;
+    const uint8_t* fk = b.u8("f_dev_kind");
+    const int32_t* fi = b.i32("f_dev_idx");
+    const uint8_t* fo = b.u8("f_obs_id");
+    const double* fmn = b.f64("f_norm_mean");
+    const double* fvr = b.f64("f_norm_var");
+    const int32_t* vai = b.i32("vav_ahu_idx", &cnt);
+    const int nv = (int)cnt;
+    const double* sc = b.f64("sched_scalars", &cnt);
+    if (!fs || fs->dtype != sbh::STR || !fk || !fi || !fo || !fmn || !fvr || !vai || !sc || cnt < 6)
+        return (*err = "canonical mode needs the blob's field_names and sched_scalars"), false;
+    const uint8_t* ok_ = b.u8("act_owner_kind", &cnt);
+    const int n_act = (int)cnt;
+    const int32_t* oi = b.i32("act_owner_index");
+    const uint8_t* oa = b.u8("act_actuator");
+    const uint8_t* isd = b.u8("act_is_discrete");
+    const double* ahu = b.f64("ahu_const", &cnt);
+    if (!ok_ || !oi || !oa || !isd || !ahu) return (*err = "action tables missing"), false;
+    const int n_dev = (int)b.i64_1("n_dev", 0);
+    std::vector<std::string> names;
+    {
+        std::string cur;
+        for (uint64_t i = 0; i < fs->count; i++) {
+            const char ch = (char)fs->data[i];
+            if (ch == '\n') { names.push_back(cur); cur.clear(); } else cur += ch;
+        }
+        names.push_back(cur);
+    }
+    auto find = [&](const std::string& nm) -> int {
+        for (size_t i = 0; i < names.size(); i++)
+            if (names[i] == nm) return (int)i;
+        return -1;
+    };
+    C->K = (int)(cnt / 9);
+    C->n_act = n_act;
+    if (C->K > SBC_K) return (*err = "more AHUs than the canonical slots (9)"), false;
+    for (int i = 0; i < SBC_ZS; i++) C->zT[i] = C->zH[i] = C->zC[i] = C->zD[i] = C->zR[i] = C->zAd[i] = C->zAr[i] = -1;
+    for (int k = 0; k < SBC_K; k++) {
+        for (int m = 0; m < 8; m++) C->aObs[k][m] = -1;
+        C->aT[k] = C->aP[k] = C->aRec[k] = C->aRun[k] = -1;
+    }
+    C->hW = C->hDPa = C->hRun = -1;
+    std::vector<int> vav_slot(nv, -1);
+    const std::string zsuf = "zone_air_temperature_sensor";
+    for (int i = 0; i < n_dev && i < (int)names.size(); i++) {
+        if (fk[i] != 1 || fo[i] != 5) continue;
+        const int v = fi[i];
+        if (v < 0 || v >= nv) return (*err = "observation field of an unknown VAV"), false;
+        const int a = vai[v];
+        if (a < 0 || a >= SBC_K || C->zc[a] >= SBC_ZPA)
+            return (*err = "an AHU serves more zones than the canonical slots (10)"), false;
+        const int sl = SBC_ZPA * a + C->zc[a]++;
+        vav_slot[v] = sl;
+        const std::string& full = names[i];
+        if (full.size() < zsuf.size()) return (*err = "bad zone temperature field name"), false;
+        const std::string pre = full.substr(0, full.size() - zsuf.size());
+        C->zT[sl] = i;
+        C->zH[sl] = find(pre + "zone_air_heating_temperature_setpoint_sensor");
+        C->zC[sl] = find(pre + "zone_air_cooling_temperature_setpoint_sensor");
+        C->zD[sl] = find(pre + "supply_air_damper_percentage_command");
+        C->zR[sl] = find(pre + "reheat_valve_percentage_command");
+    }
+    static const char* ahu_meas[8] = {"outside_air_temperature_sensor", "supply_air_static_pressure_sensor",
+                                      "supply_air_flowrate_sensor", "outside_air_flowrate_sensor",
+                                      "supply_air_temperature_setpoint", "recirculation_percentage_command",
+                                      "cooling_request_count", "supervisor_run_command"};
+    for (int k = 0; k < C->K; k++)
+        for (int m = 0; m < 8; m++) C->aObs[k][m] = find("ahs_ahu_" + std::to_string(k + 1) + "_" + ahu_meas[m]);
+    static const char* hws[6] = {"hws_supply_water_temperature_sensor", "hws_supply_water_temperature_setpoint",
+                                 "hws_differential_pressure_sensor", "hws_differential_pressure_setpoint",
+                                 "hws_run_status", "hws_heating_request_count"};
+    for (int m = 0; m < 6; m++) C->hObs[m] = find(hws[m]);
+    for (int h = 0; h < 4; h++) {
+        char buf[32];
+        snprintf(buf, sizeof buf, "hod_sin_%03d", h); C->g[h] = find(buf);
+        snprintf(buf, sizeof buf, "hod_cos_%03d", h); C->g[4 + h] = find(buf);
+        snprintf(buf, sizeof buf, "dow_sin_%03d", h); C->g[8 + h] = find(buf);
+        snprintf(buf, sizeof buf, "dow_cos_%03d", h); C->g[12 + h] = find(buf);
+    }
+    C->g[16] = find("comfort_mode_now");
+    C->g[17] = find("comfort_mode_soon");
+    C->g[18] = find("num_occupants");
+    if (C->g[0] < 0 || C->g[4] < 0 || C->g[8] < 0 || C->g[12] < 0)
+        return (*err = "canonical mode needs the hod/dow time features"), false;
+    for (int i = 0; i < SB_OBS; i++) {
+        C->fmean[i] = 0.0f;
+        C->fstd[i] = 1.0f;
+    }
+    for (int i = 0; i < n_dev && i < SB_OBS; i++)
+        if (fvr[i] > 0.0) {
+            C->fmean[i] = (float)fmn[i];
+            C->fstd[i] = (float)sqrt(fvr[i]);
+        }
+    for (int sl = 0; sl < SBC_ZS; sl++)
+        if (C->zT[sl] >= 0) {
+            C->tmean = C->fmean[C->zT[sl]];
+            C->tstd = C->fstd[C->zT[sl]];
+            break;
+        }
+    C->morning = (int)sc[0];
+    C->evening = (int)sc[1];
+    C->comfort_lo = sc[2];
+    C->comfort_hi = sc[3];
+    C->eco_lo = sc[4];
+    C->eco_hi = sc[5];
+    for (int c = 0; c < SB_ACT; c++) C->act_of_col[c] = -1;
+    int nc = 0, nd = 0;
+    for (int a = 0; a < n_act; a++) {
+        C->act_disc[a] = isd[a] ? 1 : 0;
+        const int col = isd[a] ? SB_CONT + nd++ : nc++;
+        if (col >= SB_ACT || (isd[a] && nd > SB_DISC) || (!isd[a] && nc > SB_CONT))
+            return (*err = "too many actions"), false;
+        C->act_of_col[col] = a;
+        C->slot_of_action[a] = -1;
+        if (ok_[a] == 1) {
+            const int sl = (oi[a] >= 0 && oi[a] < nv) ? vav_slot[oi[a]] : -1;
+            if (sl < 0) continue;
+            if (oa[a] == 0) { C->zAd[sl] = a; C->slot_of_action[a] = 2 * sl; }
+            else { C->zAr[sl] = a; C->slot_of_action[a] = 2 * sl + 1; }
+        } else if (ok_[a] == 0) {
+            const int k = oi[a];
+            if (k < 0 || k >= SBC_K || oa[a] > 3) continue;
+            if (oa[a] == 0) C->aT[k] = a;
+            else if (oa[a] == 1) C->aP[k] = a;
+            else if (oa[a] == 2) C->aRec[k] = a;
+            else C->aRun[k] = a;
+            C->slot_of_action[a] = SBC_AA + 4 * k + oa[a];
+        } else if (oa[a] <= 2) {
+            if (oa[a] == 0) C->hW = a;
+            else if (oa[a] == 1) C->hDPa = a;
+            else C->hRun = a;
+            C->slot_of_action[a] = SBC_AH + oa[a];
+        }
+    }
+    return true;
 }
 
 template <class T>
@@ -934,6 +1081,16 @@ struct Vec {
     float *p_hlp = nullptr, *p_hent = nullptr;   // per-head log-densities and entropies [n][SB_ACT]
     double* d_live = nullptr;                    // puf_live_log totals (device, 3 f64)
     double* h_live = nullptr;                    // and their pinned host copy
+    // canonical policy interface (kwargs canonical / residual / res_* / guard_*)
+    int canonical = 0, resid = 0, guard = 0, guard_hot = 0;
+    float res_scale = 0.5f, res_dscale = 1.5f, guard_d0 = 1.0f, guard_d1 = 0.0f;
+    sbk::CanonTab* d_canon = nullptr;            // per layout
+    float* d_raw = nullptr;                      // [n][SB_OBS] the env's own observation rows
+    float* d_native = nullptr;                   // [n][SB_ACT] native action rows the step decodes
+    float* d_cbase = nullptr;                    // [n][SB_ACT] base proposal per native action
+    float* d_ctrust = nullptr;                   // [n][SB_ACT] guard trust per native action
+    double* d_cpid = nullptr;                    // [n][2 * SBC_K] PID state
+    float* d_cinfo = nullptr;                    // [n][2 * SBC_K] effort, mean zone temperature per AHU
 };
 
 constexpr int kTimerPairs = 16384;
@@ -970,7 +1127,51 @@ void launch_params(Vec* v, const sbk::KParams& p) {
     }
 }
 
-void launch(Vec* v, int mode) { launch_params(v, params(v, mode)); }
+// The canonical interface's kernels around a step or reset (post) / before a
+// step (pre, reading the trainer's canonical action rows `actions`).
+void launch_canon(Vec* v, int post, int reset, const float* actions) {
+    sbk::CanonArgs a{};
+    a.tabs = v->d_canon;
+    a.envs = v->d_envs;
+    a.raw_obs = v->d_raw;
+    a.obs = v->obs;
+    a.actions = actions;
+    a.native = v->d_native;
+    a.terminals = v->terminals;
+    a.pid = v->d_cpid;
+    a.base = v->d_cbase;
+    a.trust = v->d_ctrust;
+    a.ainfo = v->d_cinfo;
+    a.n = v->n;
+    a.reset = reset;
+    a.resid = v->resid;
+    a.scale = v->res_scale;
+    a.dscale = v->res_dscale;
+    a.guard = v->guard;
+    a.d0 = v->guard_d0;
+    a.d1 = v->guard_d1;
+    a.hot = v->guard_hot;
+    const int rc = sbk_launch_canon(&a, post, g_stream);
+    if (rc != 0) die(std::string("canonical kernel launch failed: ") + hipGetErrorString((hipError_t)rc));
+}
+
+// One step or reset of every env: in canonical mode the step kernel reads the
+// native action rows the pre kernel decoded and writes the env's own
+// observation rows, from which the post kernel makes the canonical ones.
+void run_env(Vec* v, sbk::KParams p, const float* actions) {
+    const bool reset = p.mode == sbk::KMODE_RESET;
+    if (v->canonical) {
+        if (!reset) launch_canon(v, 0, 0, actions ? actions : v->actions);
+        p.actions = v->d_native;
+        p.obs = v->d_raw;
+    } else if (actions) {
+        p.actions = actions;
+    }
+    launch_params(v, p);
+    if (v->canonical) launch_canon(v, 1, reset ? 1 : 0, nullptr);
+}
+
+void launch(Vec* v, int mode) { run_env(v, params(v, mode), nullptr); }
 
 Vec* vec_of(Env* envs) {
     if (!envs || !envs[0].vec) die("env array was not created by puf_vec_create");
@@ -1027,14 +1228,15 @@ const char* kws(Dict* d, const char* key) {
 // this build does not have: each is accepted at its inert value (0, as the
 // reference ini ships them) and aborts with a message otherwise, so a trainer
 // config never gets a different environment without notice. Keys that only
-// parameterise one of these (center_beta, plant_eps, res_scale, res_dscale,
-// guard_d0, shape_gamma, random_start_seed) and merge_weathers (how the
-// reference groups scenarios for its solver: no effect on results) are
-// accepted at any value.
+// parameterise one of these (center_beta, plant_eps, shape_gamma,
+// random_start_seed) and merge_weathers (how the reference groups scenarios
+// for its solver: no effect on results) are accepted at any value. The
+// canonical interface (canonical, residual, res_scale, res_dscale, guard_*)
+// is implemented.
 void check_env_keys(Dict* d) {
     static const char* const unsupported[] = {
-        "random_start", "rew_norm", "rew_center", "canonical", "residual", "plant_pair", "guard_d1",
-        "guard_hot", "comfort_shape", "zone_memory", "interleave", "zone_adv", "zone_critic", "ahu_critic",
+        "random_start", "rew_norm", "rew_center", "plant_pair", "comfort_shape", "zone_memory", "interleave",
+        "zone_adv", "zone_critic", "ahu_critic",
         "zone_command", "prestart_explore", "probe", "zone_signed", "zone_night_share",
     };
     if (!d) return;
@@ -1111,6 +1313,23 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
     v->paths = files;
     std::vector<int> scnt(G);
     for (int i = 0; i < G; i++) scnt[i] = n / G + (i < n % G ? 1 : 0);
+    // ---- canonical policy interface (complete_port/gpu/smart_buildings.cu:2611-2660, 2717)
+    v->canonical = (int)kw(kwargs, "canonical", 0.0f) != 0;
+    v->resid = (int)kw(kwargs, "residual", 0.0f) != 0;
+    if (v->resid && !v->canonical) die("env.residual needs env.canonical = 1");
+    {
+        const float rs = kw(kwargs, "res_scale", 0.5f), rd = kw(kwargs, "res_dscale", 1.5f);
+        if (rs > 0.0f) v->res_scale = rs;
+        if (rd > 0.0f) v->res_dscale = rd;
+        const float d0 = kw(kwargs, "guard_d0", 1.0f);
+        if (d0 >= 0.0f) v->guard_d0 = d0;
+        v->guard_d1 = kw(kwargs, "guard_d1", 0.0f);
+        v->guard_hot = (int)kw(kwargs, "guard_hot", 0.0f) != 0;
+        if (!v->resid) v->guard_d1 = 0.0f;     // the guard scales residuals only
+        v->guard = v->guard_d1 > 0.0f;
+        if ((v->guard_d1 != 0.0f || v->guard_hot) && !v->canonical)
+            die("env.guard_d1 / env.guard_hot need env.canonical = 1 and env.residual = 1");
+    }
     // ---- field solver: "auto" (relaxation where certified), "lu" or "relax"
     int solve = SOLVE_AUTO;
     if (const char* sv = kws(kwargs, "solver")) {
@@ -1133,6 +1352,10 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
             HostLayout H;
             H.key = key;
             if (!make_layout(b, v->width, solve, &H, A, &err)) die(files[i] + ": " + err);
+            if (v->canonical) {
+                H.canon = std::make_unique<sbk::CanonTab>();
+                if (!make_canon(b, H.canon.get(), &err)) die(files[i] + ": canonical layout: " + err);
+            }
             li = (int)v->layouts.size();
             v->layouts.push_back(std::move(H));
             layout_of_key[key] = li;
@@ -1296,10 +1519,11 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
     hip_ok(hipMemcpy(v->d_tiles, v->tiles.data(), sizeof(sbk::Tile) * v->tiles.size(), hipMemcpyHostToDevice),
            "upload");
     {
+        // the trainer's heads: the native actions, or (canonical) the canonical slots
         std::vector<int> nc(n), nd(n);
         for (int i = 0; i < n; i++) {
-            nc[i] = v->layouts[v->desc[i].layout].dev.n_cont;
-            nd[i] = v->layouts[v->desc[i].layout].dev.n_disc;
+            nc[i] = v->canonical ? SBC_ACT : v->layouts[v->desc[i].layout].dev.n_cont;
+            nd[i] = v->canonical ? 0 : v->layouts[v->desc[i].layout].dev.n_disc;
         }
         hip_ok(hipMalloc(&v->d_ncont, sizeof(int) * n), "hipMalloc");
         hip_ok(hipMalloc(&v->d_ndisc, sizeof(int) * n), "hipMalloc");
@@ -1327,6 +1551,26 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
         hip_ok(hipMalloc(&v->d_state, v->state_bytes), "hipMalloc(state)");
         hip_ok(hipMemcpy(v->d_state, rec.data(), v->state_bytes, hipMemcpyHostToDevice), "upload state");
     }
+    if (v->canonical) {
+        std::vector<sbk::CanonTab> tabs(v->layouts.size());
+        for (size_t li = 0; li < v->layouts.size(); li++) tabs[li] = *v->layouts[li].canon;
+        hip_ok(hipMalloc(&v->d_canon, sizeof(sbk::CanonTab) * tabs.size()), "hipMalloc(canonical maps)");
+        hip_ok(hipMemcpy(v->d_canon, tabs.data(), sizeof(sbk::CanonTab) * tabs.size(), hipMemcpyHostToDevice),
+               "upload");
+        const size_t na = (size_t)n * SB_ACT, ns = (size_t)n * 2 * SBC_K;
+        hip_ok(hipMalloc(&v->d_raw, sizeof(float) * (size_t)n * SB_OBS), "hipMalloc(canonical)");
+        hip_ok(hipMalloc(&v->d_native, sizeof(float) * na), "hipMalloc(canonical)");
+        hip_ok(hipMalloc(&v->d_cbase, sizeof(float) * na), "hipMalloc(canonical)");
+        hip_ok(hipMalloc(&v->d_ctrust, sizeof(float) * na), "hipMalloc(canonical)");
+        hip_ok(hipMalloc(&v->d_cpid, sizeof(double) * ns), "hipMalloc(canonical)");
+        hip_ok(hipMalloc(&v->d_cinfo, sizeof(float) * ns), "hipMalloc(canonical)");
+        hip_ok(hipMemset(v->d_raw, 0, sizeof(float) * (size_t)n * SB_OBS), "clear");
+        hip_ok(hipMemset(v->d_native, 0, sizeof(float) * na), "clear");
+        hip_ok(hipMemset(v->d_cbase, 0, sizeof(float) * na), "clear");
+        hip_ok(hipMemset(v->d_ctrust, 0, sizeof(float) * na), "clear");
+        hip_ok(hipMemset(v->d_cpid, 0, sizeof(double) * ns), "clear");
+        hip_ok(hipMemset(v->d_cinfo, 0, sizeof(float) * ns), "clear");
+    }
     hip_ok(hipMalloc(&v->d_live, 3 * sizeof(double)), "hipMalloc(live log)");
     hip_ok(hipHostMalloc(&v->h_live, 3 * sizeof(double), hipHostMallocDefault), "hipHostMalloc(live log)");
     // ---- Env array (host memory the device can write: logs)
@@ -1344,9 +1588,9 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
         E.num_agents = 1;
         E.max_steps = v->desc[i].max_steps;
         E.start_offset = v->desc[i].start;
-        E.n_act = L.n_act;
-        E.n_cont = L.n_cont;
-        E.n_disc = L.n_disc;
+        E.n_act = v->canonical ? SBC_ACT : L.n_act;
+        E.n_cont = v->canonical ? SBC_ACT : L.n_cont;
+        E.n_disc = v->canonical ? 0 : L.n_disc;
         E.loaded = 1;
         E.index = i;
         E.vec = v.get();
@@ -1389,16 +1633,15 @@ void puf_reset(Env* envs) {
 
 // One step reading its action rows from `actions` (the bound buffer when null).
 void step_from(Vec* v, const float* actions) {
-    sbk::KParams p = params(v, sbk::KMODE_STEP);
-    if (actions) p.actions = actions;
+    const sbk::KParams p = params(v, sbk::KMODE_STEP);
     if (v->t_on && v->t_seen++ % v->t_on == 0 && v->t_used < kTimerPairs) {
         hip_ok(hipEventRecord(v->tev[2 * v->t_used], g_stream), "timer event");
-        launch_params(v, p);
+        run_env(v, p, actions);
         hip_ok(hipEventRecord(v->tev[2 * v->t_used + 1], g_stream), "timer event");
         v->t_used++;
         return;
     }
-    launch_params(v, p);
+    run_env(v, p, actions);
 }
 
 void puf_step(Env* envs) { step_from(vec_of(envs), nullptr); }
@@ -1426,6 +1669,9 @@ void puf_close(Env* envs) {
     (void)hipFree(v->d_ndisc);
     (void)hipFree(v->d_live);
     (void)hipHostFree(v->h_live);
+    for (void* p : {(void*)v->d_canon, (void*)v->d_raw, (void*)v->d_native, (void*)v->d_cbase, (void*)v->d_ctrust,
+                    (void*)v->d_cpid, (void*)v->d_cinfo})
+        (void)hipFree(p);
     (void)hipHostFree(v->envs);
     if (g_last == v) g_last = nullptr;
     delete v;
@@ -1455,13 +1701,27 @@ void puf_live_log(Env* envs, Dict* out) {
     dict_set(out, "reward_mean", st > 0.0 ? (float)(rs / st) : 0.0f);
 }
 
+// The action mask of every agent (complete_port/gpu/smart_buildings.cu:3230-
+// 3300): the env's continuous heads and both categories of its discrete heads,
+// or (canonical) the canonical slots the building has. The mask may be device
+// or host memory: it is built on the host and copied.
 void puf_mask_init(unsigned char* mask, int width, int nagents) {
     Vec* v = g_last;
-    if (!v || !mask) return;
+    if (!v || !mask || nagents <= 0) return;
+    if (width < 1 || width > SB_MASK_WIDTH) die("puf_mask_init: width " + std::to_string(width) + " out of range");
+    std::vector<unsigned char> host((size_t)nagents * width, 0);
     for (int a = 0; a < nagents; a++) {
-        unsigned char* m = mask + (size_t)a * width;
-        const Env& E = v->envs[a < v->n ? a : v->n - 1];
-        for (int h = 0; h < width; h++) m[h] = 0;
+        unsigned char* m = host.data() + (size_t)a * width;
+        const int i = a < v->n ? a : v->n - 1;
+        const Env& E = v->envs[i];
+        if (v->canonical) {
+            const sbk::CanonTab& C = *v->layouts[v->desc[i].layout].canon;
+            for (int j = 0; j < C.n_act; j++) {
+                const int sl = C.slot_of_action[j];
+                if (sl >= 0 && sl < width) m[sl] = 1;
+            }
+            continue;
+        }
         for (int h = 0; h < SB_CONT && h < width; h++) m[h] = (h < E.n_cont) ? 1 : 0;
         for (int h = 0; h < SB_DISC && SB_CONT + 2 * h + 1 < width; h++) {
             unsigned char b = (h < E.n_disc) ? 1 : 0;
@@ -1469,6 +1729,7 @@ void puf_mask_init(unsigned char* mask, int width, int nagents) {
             m[SB_CONT + 2 * h + 1] = b;
         }
     }
+    hip_ok(hipMemcpy(mask, host.data(), host.size(), hipMemcpyDefault), "puf_mask_init copy");
 }
 
 void sbx_gen_actions(Env* envs, uint64_t seed, uint32_t step) {
@@ -1539,7 +1800,7 @@ int sbx_phase_times(Env* envs, double* mean_us, double* max_us, int n_phases) {
     hip_ok(hipMemset(d, 0, count * sizeof(unsigned long long)), "memset(stamps)");
     sbk::KParams p = params(v, sbk::KMODE_STEP);
     p.phase_ts = d;
-    launch_params(v, p);
+    run_env(v, p, nullptr);
     hip_ok(hipStreamSynchronize(g_stream), "stamps sync");
     std::vector<unsigned long long> h(count);
     hip_ok(hipMemcpy(h.data(), d, count * sizeof(unsigned long long), hipMemcpyDeviceToHost), "stamps copy");
@@ -1571,7 +1832,7 @@ int sbx_phase_stamps(Env* envs, unsigned long long* out, int cap) {
     hip_ok(hipMemset(d, 0, count * sizeof(unsigned long long)), "memset(stamps)");
     sbk::KParams p = params(v, sbk::KMODE_STEP);
     p.phase_ts = d;
-    launch_params(v, p);
+    run_env(v, p, nullptr);
     hip_ok(hipStreamSynchronize(g_stream), "stamps sync");
     hip_ok(hipMemcpy(out, d, count * sizeof(unsigned long long), hipMemcpyDeviceToHost), "stamps copy");
     (void)hipFree(d);
@@ -1591,7 +1852,7 @@ int sbx_pass_times(Env* envs, int env, long long* cycles, int cap) {
     sbk::KParams p = params(v, sbk::KMODE_STEP);
     p.pass_ts = d;
     p.pass_ts_env = env;
-    launch_params(v, p);
+    run_env(v, p, nullptr);
     hip_ok(hipStreamSynchronize(g_stream), "pass stamps sync");
     std::vector<unsigned long long> h(np + 1);
     hip_ok(hipMemcpy(h.data(), d, h.size() * sizeof(unsigned long long), hipMemcpyDeviceToHost), "copy");
@@ -1782,6 +2043,20 @@ int sbx_solve_info(Env* envs, int i, double* out) {
     out[2] = pf[sbk::PF_SWEEPS];
     out[3] = pf[sbk::PF_CAPPED];
     return 4;
+}
+
+int sbx_canon_state(Env* envs, int i, float* raw_obs, float* base, double* pid) {
+    Vec* v = vec_of(envs);
+    if (!v->canonical || i < 0 || i >= v->n) return -1;
+    hip_ok(hipStreamSynchronize(g_stream), "canonical state");
+    if (raw_obs)
+        hip_ok(hipMemcpy(raw_obs, v->d_raw + (size_t)i * SB_OBS, sizeof(float) * SB_OBS, hipMemcpyDeviceToHost), "copy");
+    if (base)
+        hip_ok(hipMemcpy(base, v->d_cbase + (size_t)i * SB_ACT, sizeof(float) * SB_ACT, hipMemcpyDeviceToHost), "copy");
+    if (pid)
+        hip_ok(hipMemcpy(pid, v->d_cpid + (size_t)i * 2 * SBC_K, sizeof(double) * 2 * SBC_K, hipMemcpyDeviceToHost),
+               "copy");
+    return v->layouts[v->desc[i].layout].canon->n_act;
 }
 
 int sbx_env_meta(Env* envs, int i, int* scenario, int* start, uint32_t* occ_seed) {

@@ -105,7 +105,7 @@ EXPORTS = [
     "sbx_vec_info", "sbx_env_state", "sbx_time_step", "sbx_step_actions", "sbx_phase_times", "sbx_phase_stamps", "sbx_kernel_timer", "sbx_pass_times", "sbx_solve_info",
     "sbx_policy_bind", "sbx_policy_act", "sbx_policy_act_noalloc", "sbx_policy_heads", "sbx_beta_sample",
     "sbx_policy_act_logp", "sbx_beta_eval", "sbx_ppo_beta",
-    "sbx_env_meta", "sbx_scenario_path",
+    "sbx_env_meta", "sbx_scenario_path", "sbx_canon_state",
     "sbx_plan_layout", "sbx_plan_free", "sbx_last_error", "sbx_version",
 ]
 
@@ -159,6 +159,8 @@ def lib() -> ctypes.CDLL:
         L.sbx_phase_stamps.restype = ctypes.c_int
         L.sbx_solve_info.argtypes = [ctypes.POINTER(Env), ctypes.c_int, P]
         L.sbx_solve_info.restype = ctypes.c_int
+        L.sbx_canon_state.argtypes = [ctypes.POINTER(Env), ctypes.c_int, P, P, P]
+        L.sbx_canon_state.restype = ctypes.c_int
         L.sbx_env_meta.argtypes = [ctypes.POINTER(Env), ctypes.c_int, ctypes.POINTER(ctypes.c_int),
                                    ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_uint32)]
         L.sbx_scenario_path.argtypes = [ctypes.POINTER(Env), ctypes.c_int]
@@ -324,6 +326,18 @@ class VecEnv:
         if m < 0:
             raise RuntimeError("sbx_env_state failed")
         return buf[:m].copy()
+
+    def canon_state(self, i: int):
+        """Canonical mode: env i's own observation row, base proposal per native action
+        (first n_act entries) and PID state."""
+        raw = np.zeros(SB_OBS, np.float32)
+        base = np.zeros(SB_ACT, np.float32)
+        pid = np.zeros(18, np.float64)
+        n = self.L.sbx_canon_state(self.envs, i, raw.ctypes.data_as(P), base.ctypes.data_as(P),
+                                   pid.ctypes.data_as(P))
+        if n < 0:
+            raise RuntimeError("sbx_canon_state failed (not a canonical vec?)")
+        return raw, base[:n], pid
 
     def meta(self, i: int) -> tuple[str, int, int]:
         s, st, sd = ctypes.c_int(), ctypes.c_int(), ctypes.c_uint32()

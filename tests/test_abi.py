@@ -56,7 +56,7 @@ def test_unsupported_env_key_aborts():
             "E.lib().puf_vec_create(1, kw.ptr(), ctypes.c_void_p(64), ctypes.c_void_p(64), "
             "ctypes.c_void_p(64), ctypes.c_void_p(64)); print('created')")
     root = str(Path(__file__).resolve().parents[1])
-    for key in ("rew_norm", "canonical", "random_start", "zone_memory", "comfort_shape"):
+    for key in ("rew_norm", "plant_pair", "random_start", "zone_memory", "comfort_shape"):
         r = subprocess.run([sys.executable, "-c", code.format(key=key, val=1)], cwd=root, capture_output=True,
                            text=True, timeout=120)
         assert r.returncode != 0 and "created" not in r.stdout, (key, r.stdout, r.stderr)
@@ -65,3 +65,24 @@ def test_unsupported_env_key_aborts():
     r = subprocess.run([sys.executable, "-c", code.format(key="rew_norm", val=0)], cwd=root, capture_output=True,
                        text=True, timeout=120)
     assert r.returncode != 0 and "not supported" not in r.stderr and "nonexistent" in r.stderr, r.stderr
+
+
+def test_canonical_rejects_buildings_beyond_the_slots(tmp_path):
+    """canonical = 1 on a building with more than 10 zones on one AHU (41 zones, one AHU)
+    stops puf_vec_create with the reason, before any device call; residual without
+    canonical is refused too."""
+    import subprocess
+    import sys
+
+    from neurips2026_smart_building_challenge_amd.scenario import generate as G
+
+    paths, _, _ = G.write_config(0, tmp_path)
+    root = str(Path(__file__).resolve().parents[1])
+    code = ("import ctypes; from neurips2026_smart_building_challenge_amd import env as E; "
+            "kw = E.Kwargs(blob={blob!r}, {extra}); "
+            "E.lib().puf_vec_create(1, kw.ptr(), ctypes.c_void_p(64), ctypes.c_void_p(64), "
+            "ctypes.c_void_p(64), ctypes.c_void_p(64)); print('created')")
+    for extra, msg in (("canonical=1", "more zones than the canonical slots"), ("residual=1", "needs env.canonical")):
+        r = subprocess.run([sys.executable, "-c", code.format(blob=str(paths[0]), extra=extra)], cwd=root,
+                           capture_output=True, text=True, timeout=120)
+        assert r.returncode != 0 and "created" not in r.stdout and msg in r.stderr, (extra, r.stderr)

@@ -1,0 +1,145 @@
+"""The canonical policy interface on the GPU (kwargs canonical / residual / guard_*),
+through the C ABI, against the oracle's canonical layout (oracle/sbo_canon.c, pinned
+bit-exactly to the reference submission's Python in tests/test_canonical_oracle.py).
+
+Every step, for every env of a mixed batch (4, 5 and 9 air handlers):
+  - the base proposal, the PID state and the canonical observation the trainer
+    receives equal, bit for bit, what the oracle computes from the env's own
+    observation row (read back with sbx_canon_state) and its own PID state;
+  - the oracle env, stepped with the native actions the oracle decodes from the
+    trainer's canonical action row and that base (residual, comfort guard on), keeps
+    the decoded commands exactly and the physics within the state tolerance of the
+    GPU env;
+through episode ends (the PID state restarts with the episode)."""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+import pyoracle as po
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+from neurips2026_smart_building_challenge_amd import env as E  # noqa: E402
+from neurips2026_smart_building_challenge_amd.scenario import generate as G  # noqa: E402
+
+SEED = 31337
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    yield
+    torch.cuda.synchronize()
+
+
+@pytest.fixture(scope="module")
+def canon_dir(tmp_path_factory):
+    d = tmp_path_factory.mktemp("canon")
+    scen = [(G.LayoutSpec(36, 4), G.ClimateSpec(2.0, 7.0, seed=611)),
+            (G.LayoutSpec(45, 5), G.ClimateSpec(24.0, 8.0, seed=613)),
+            (G.LayoutSpec(81, 9), G.ClimateSpec(-4.0, 6.0, seed=612))]
+    G.write_scenarios(scen, d)
+    return d
+
+
+def _state_close(g, c, where):
+    m = len(c)
+    g = g[:m]
+    fin = ~np.isnan(g)
+    err = np.abs(g[fin] - c[fin]) / np.maximum(np.abs(c[fin]), 1.0)
+    assert err.max() <= 1e-9, f"{where}: state rel err {err.max():.3e}"
+
+
+@pytest.mark.parametrize("mode", ["residual_guard", "residual", "absolute"])
+def test_gpu_canonical_matches_oracle(canon_dir, mode):
+    kw = dict(canonical=1, max_steps=40)
+    guard = None
+    if mode.startswith("residual"):
+        kw.update(residual=1, res_scale=0.5, res_dscale=1.5)
+    if mode == "residual_guard":
+        kw.update(guard_d0=0.5, guard_d1=1.5, guard_hot=1)
+        guard = (0.5, 1.5, 1)
+    resid = 1 if mode.startswith("residual") else 0
+    say(f"canonical ({mode}): 9 envs, 90 steps")
+    vec = E.VecEnv(9, blob_dir=str(canon_dir), groups=3, **kw)
+    assert all(vec.envs[i].n_cont == po.CN_ACT and vec.envs[i].n_disc == 0 for i in range(vec.n))
+    twins = []
+    for i in range(vec.n):
+        path, start, seed = vec.meta(i)
+        twins.append({"env": po.CpuEnv("oracle", path, seed, start=start, max_steps=40), "canon": po.Canon(path),
+                      "pid": np.zeros(18, np.float64)})
+    vec.reset()
+    for t in twins:
+        t["env"].reset()
+    torch.cuda.synchronize()
+
+    def check_observation(where, fresh):
+        obs = vec.obs.cpu().numpy()
+        for i, t in enumerate(twins):
+            c = t["canon"]
+            raw, gbase, gpid = vec.canon_state(i)
+            n_obs = t["env"].obs_len
+            if fresh[i]:
+                t["pid"][:] = 0.0
+            base, ai = c.base(raw[:n_obs], t["pid"])
+            assert np.array_equal(gbase.view(np.uint32), base.view(np.uint32)), f"{where} env {i}: base"
+            assert np.array_equal(gpid, t["pid"]), f"{where} env {i}: PID state"
+            x = c.features(raw[:n_obs], base, ai, t["pid"])
+            assert np.array_equal(obs[i, :po.CN_OBS].view(np.uint32), x.view(np.uint32)), f"{where} env {i}: obs"
+            assert np.all(obs[i, po.CN_OBS:] == 0.0), f"{where} env {i}: padding"
+            t["base"] = base
+            t["raw"] = raw[:n_obs]
+
+    check_observation("reset", [True] * vec.n)
+    for s in range(90):
+        vec.gen_actions(SEED, s)
+        prow = vec.actions.cpu().numpy()
+        vec.step()
+        torch.cuda.synchronize()
+        term = vec.terminals.cpu().numpy()
+        rew = vec.rewards.cpu().numpy()
+        for i, t in enumerate(twins):
+            c = t["canon"]
+            trust = c.trust(t["raw"], *guard) if guard else None
+            row = c.decode(t["base"], prow[i, :po.CN_ACT], trust, resid, 0.5, 1.5)
+            _, r, tt, _ = t["env"].step(row)
+            assert tt == term[i], (s, i)
+            assert abs(float(rew[i]) - r) <= 2 * np.spacing(np.float32(abs(r))) + 1e-12, (s, i)
+            _state_close(vec.state(i), t["env"].state(), f"{mode} step {s} env {i}")
+        check_observation(f"{mode} step {s}", [bool(x) for x in term])
+    vec.close()
+
+
+def test_gpu_canonical_mask_and_policy(canon_dir):
+    """puf_mask_init marks exactly the canonical slots each building has, into device
+    memory; the shared policy reads the canonical observation and writes 219 heads."""
+    say("canonical mask and policy")
+    vec = E.VecEnv(6, blob_dir=str(canon_dir), groups=3, canonical=1, residual=1)
+    mask = torch.full((vec.n, 288), 7, dtype=torch.uint8, device="cuda")   # SB_MASK_WIDTH
+    vec.L.puf_mask_init(E.P(mask.data_ptr()), mask.shape[1], vec.n)
+    m = mask.cpu().numpy()
+    for i in range(vec.n):
+        c = po.Canon(vec.meta(i)[0])
+        want = np.zeros(mask.shape[1], np.uint8)
+        sl = c.slot_of_action[c.slot_of_action >= 0]
+        want[sl] = 1
+        assert np.array_equal(m[i], want), i
+        assert want.sum() == c.n_act
+    vec.policy_bind(E.policy_weights(4))
+    vec.reset()
+    vec.policy_act(5, 0)
+    vec.step()
+    torch.cuda.synchronize()
+    a = vec.actions.cpu().numpy()
+    assert np.all(np.abs(a[:, :po.CN_ACT]) < 1.0) and np.all(a[:, po.CN_ACT:] == 0.0)
+    vec.close()
