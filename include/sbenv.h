@@ -192,9 +192,9 @@ int sbx_step_actions(Env* envs, const float* actions);
  * synchronises. Returns the number of phases written. */
 int sbx_phase_times(Env* envs, double* mean_us, double* max_us, int n_phases);
 
-/* Runs one step and copies the raw wall-clock stamps of every env (SBK_NSTAMP
- * = 16 per env, env-major; the phases above are stamps 0..12, unused stamps
- * read 0). Returns the number written, or -1 when cap is below 16 * n. */
+/* Runs one step and copies the raw wall-clock stamps of every env (32 per
+ * env, env-major; the phases above are stamps 0..12, unused stamps read 0).
+ * Returns the number written, or -1 when cap is below 32 * n. */
 int sbx_phase_stamps(Env* envs, unsigned long long* out, int cap);
 
 /* Runs one step recording the shader-clock duration of every solve pass of
@@ -385,6 +385,51 @@ typedef struct SbxPlan {
 } SbxPlan;
 int sbx_plan_layout(const char* blob_path, int width, SbxPlan* out);
 void sbx_plan_free(SbxPlan* p);
+
+/* ---- Building-scale field step ------------------------------------------
+ * The reference core's FDM step (complete_port/csim/sb_fdm.h:60-68,
+ * sb_fdm_step_batch; sb_fdm.c:142-270) for G envs that share one blob's baked
+ * factorization, on the device: forcing, the L and U sweeps of the SuperLU
+ * factors, the air-side correction (sensed dots, the dense k x k solve, the
+ * applied heat, a second solve), interior mass and the field. Results are
+ * those of G sequential sb_fdm_step calls, bit for bit. The blob needs only
+ * the field sections (grid, solved, capacitance_rate, dirichlet_conductance,
+ * mass_*, temp_init, horizontal, vertical, solver_conductivity,
+ * ambient_face_areas_0/1, lu_L/lu_U/lu_perm_r/lu_perm_c, applied, sensed).
+ * Envs are grouped in blocks of envs_per_block lanes (a power of two up to 64;
+ * 0 picks 64 or fewer for small G); each block runs every level of a factor on
+ * one workgroup. */
+typedef struct SbxFdm SbxFdm;
+typedef struct {
+    int n_cvs, n_solved, k;       /* cells, solved cells, air-side columns */
+    int n_envs, envs_per_block, n_blocks;
+    int levels_l, levels_u;       /* level-schedule depth of the two sweeps */
+    long long nnz_l, nnz_u;       /* off-diagonal factor entries */
+    double bytes_per_step;        /* algorithmic HBM bytes of one batched step */
+    double flops_per_step;        /* multiply-subtracts x 2 of both solves */
+} SbxFdmInfo;
+/* sb_fdm_init for every env: the blob's initial fields, S = sensed A^-1 applied
+ * (solved on the device). NULL on error (sbx_last_error). */
+SbxFdm* sbx_fdm_open(const char* blob_path, int n_envs, int envs_per_block);
+void sbx_fdm_close(SbxFdm* f);
+int sbx_fdm_info(const SbxFdm* f, SbxFdmInfo* out);
+/* One step of every env on `stream` (asynchronous). Device arrays: input_q
+ * [n_cvs][G] (heat per cell, the G envs of one cell adjacent), ambient and h
+ * [G] (ambient temperature, convection coefficient), air_g and air_T [G][k]
+ * (air-side conductance and supply temperature per coupled column; an env
+ * whose k conductances are all 0 has no air side this step). */
+int sbx_fdm_step(SbxFdm* f, const double* input_q, const double* ambient, const double* h, const double* air_g,
+                 const double* air_T, void* stream);
+/* Every env back to the blob's initial fields. */
+int sbx_fdm_reset(SbxFdm* f, void* stream);
+/* Host arrays, env-major: temp [G][n_cvs], mass_temp [G][n_solved]. Synchronise. */
+int sbx_fdm_get_state(SbxFdm* f, double* temp, double* mass_temp);
+int sbx_fdm_set_state(SbxFdm* f, const double* temp, const double* mass_temp);
+/* S [k][k] (host). */
+int sbx_fdm_sensed_response(SbxFdm* f, double* out);
+/* x = A^-1 b through the baked factors on the device (sb_lu_solve,
+ * sb_lu.c:38-63), for n_rhs host columns b, x [n_rhs][n_solved]. */
+int sbx_fdm_lu_solve(SbxFdm* f, const double* b, double* x, int n_rhs);
 
 /* Message of the last failing sbx_* call. */
 const char* sbx_last_error(void);

@@ -2161,3 +2161,6 @@ const char* sbx_last_error(void) { return g_err.c_str(); }
 const char* sbx_version(void) { return "sbenv 0.1 gfx950"; }
 
 }  // extern "C"
+
+// Error text for the other host files of the library (field step).
+void sbx_set_error(const std::string& msg) { g_err = msg; }

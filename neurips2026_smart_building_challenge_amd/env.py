@@ -106,7 +106,10 @@ EXPORTS = [
     "sbx_policy_bind", "sbx_policy_act", "sbx_policy_act_noalloc", "sbx_policy_heads", "sbx_beta_sample",
     "sbx_policy_act_logp", "sbx_beta_eval", "sbx_ppo_beta",
     "sbx_env_meta", "sbx_scenario_path", "sbx_canon_state",
-    "sbx_plan_layout", "sbx_plan_free", "sbx_last_error", "sbx_version",
+    "sbx_plan_layout", "sbx_plan_free",
+    "sbx_fdm_open", "sbx_fdm_close", "sbx_fdm_info", "sbx_fdm_step", "sbx_fdm_reset", "sbx_fdm_get_state",
+    "sbx_fdm_set_state", "sbx_fdm_sensed_response", "sbx_fdm_lu_solve",
+    "sbx_last_error", "sbx_version",
 ]
 
 _LIB = None

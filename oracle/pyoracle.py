@@ -305,3 +305,107 @@ def run_batch(envs: list[CpuEnv], env_ids, steps: int, seed: int, nthreads: int)
     acc = np.zeros(1, np.float64)
     secs = lib(kind).batch_fn(ctypes.cast(arr, P), _ptr(ids), len(envs), steps, seed, nthreads, _ptr(acc))
     return float(secs), float(acc[0])
+
+
+class Fdm:
+    """The building-scale field model alone, G envs of one blob:
+    kind "oracle" is this repo's restatement (sbo_fdm.c), kind "ref" the
+    reference core's sb_fdm (oracle/_ref). Fields are host arrays: T (G, n_cvs),
+    M (G, n_solved)."""
+
+    def __init__(self, kind: str, path, G: int):
+        self.kind, self.G = kind, G
+        L = lib(kind).lib
+        self.L = L
+        dims = np.zeros(5, np.int32)
+        if kind == "ref":
+            L.ref_fdm_open.restype = P
+            L.ref_fdm_open.argtypes = [ctypes.c_char_p, ctypes.c_int]
+            for f in (L.ref_fdm_dims, L.ref_fdm_sensed_response):
+                f.argtypes = [P, P]
+            L.ref_fdm_lu_solve.argtypes = [P, P, P]
+            L.ref_fdm_get.argtypes = [P, ctypes.c_int, P, P]
+            L.ref_fdm_set.argtypes = [P, ctypes.c_int, P, P]
+            L.ref_fdm_step_batch.argtypes = [P, P, P, P, P, P]
+            L.ref_fdm_close.argtypes = [P]
+            self.h = L.ref_fdm_open(str(path).encode(), G)
+            if not self.h:
+                raise RuntimeError(f"ref_fdm_open failed for {path}")
+            L.ref_fdm_dims(self.h, _ptr(dims))
+        else:
+            L.sbo_fdm_open.restype = P
+            L.sbo_fdm_open.argtypes = [ctypes.c_char_p]
+            L.sbo_fdm_dims.argtypes = [P, P]
+            L.sbo_fdm_sensed_response.restype = ctypes.POINTER(ctypes.c_double)
+            L.sbo_fdm_sensed_response.argtypes = [P]
+            L.sbo_fdm_init_state.argtypes = [P, P, P]
+            L.sbo_fdm_lu_solve.argtypes = [P, P, P]
+            L.sbo_fdm_step_batch.argtypes = [P, ctypes.c_int, P, P, P, P, P, P, P]
+            L.sbo_fdm_step_batch.restype = ctypes.c_int
+            L.sbo_fdm_close.argtypes = [P]
+            self.h = L.sbo_fdm_open(str(path).encode())
+            if not self.h:
+                raise RuntimeError(f"sbo_fdm_open failed for {path}")
+            L.sbo_fdm_dims(self.h, _ptr(dims))
+        self.n_cvs, self.n, self.k, self.rows, self.cols = (int(x) for x in dims)
+        if kind == "oracle":
+            self.T = np.zeros((G, self.n_cvs))
+            self.M = np.zeros((G, self.n))
+            for g in range(G):
+                L.sbo_fdm_init_state(self.h, _ptr(self.T[g]), _ptr(self.M[g]))
+
+    def close(self):
+        if self.h:
+            (self.L.ref_fdm_close if self.kind == "ref" else self.L.sbo_fdm_close)(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def sensed_response(self) -> np.ndarray:
+        if self.kind == "ref":
+            out = np.zeros(self.k * self.k)
+            self.L.ref_fdm_sensed_response(self.h, _ptr(out))
+            return out.reshape(self.k, self.k)
+        p = self.L.sbo_fdm_sensed_response(self.h)
+        return np.ctypeslib.as_array(p, (self.k * self.k,)).copy().reshape(self.k, self.k)
+
+    def lu_solve(self, b: np.ndarray) -> np.ndarray:
+        b = np.ascontiguousarray(b, np.float64)
+        x = np.zeros(self.n)
+        (self.L.ref_fdm_lu_solve if self.kind == "ref" else self.L.sbo_fdm_lu_solve)(self.h, _ptr(b), _ptr(x))
+        return x
+
+    def state(self) -> tuple[np.ndarray, np.ndarray]:
+        if self.kind == "oracle":
+            return self.T.copy(), self.M.copy()
+        T = np.zeros((self.G, self.n_cvs))
+        M = np.zeros((self.G, self.n))
+        for g in range(self.G):
+            self.L.ref_fdm_get(self.h, g, _ptr(T[g]), _ptr(M[g]))
+        return T, M
+
+    def set_state(self, T: np.ndarray, M: np.ndarray):
+        T = np.ascontiguousarray(T, np.float64)
+        M = np.ascontiguousarray(M, np.float64)
+        if self.kind == "oracle":
+            self.T[...] = T
+            self.M[...] = M
+            return
+        for g in range(self.G):
+            self.L.ref_fdm_set(self.h, g, _ptr(T[g]), _ptr(M[g]))
+
+    def step(self, inp: dict):
+        q = np.ascontiguousarray(inp["input_q"], np.float64)
+        amb = np.ascontiguousarray(inp["ambient"], np.float64)
+        h = np.ascontiguousarray(inp["h"], np.float64)
+        g = np.ascontiguousarray(inp["air_g"], np.float64)
+        t = np.ascontiguousarray(inp["air_T"], np.float64)
+        if self.kind == "ref":
+            self.L.ref_fdm_step_batch(self.h, _ptr(q), _ptr(amb), _ptr(h), _ptr(g), _ptr(t))
+        elif self.L.sbo_fdm_step_batch(self.h, self.G, _ptr(self.T), _ptr(self.M), _ptr(q), _ptr(amb), _ptr(h),
+                                       _ptr(g), _ptr(t)) != 0:
+            raise MemoryError("sbo_fdm_step_batch")

@@ -276,3 +276,86 @@ double ref_run_batch(RefEnv** envs, const int* env_ids, int n, int steps, uint64
 void ref_action_row(uint64_t seed, uint32_t env, uint32_t step, int n_cont, int n_disc, float* row) {
     sbo_action_row_philox(seed, env, step, n_cont, n_disc, row, SB_CONT, SB_DISC);
 }
+
+/* ---- the reference's field model alone (sb_fdm.h), for the FDM-scale plans:
+ * G envs of one blob, each its own SbFdm (sb_fdm_init, sb_fdm.c:40-118) over
+ * the one loaded blob, stepped together by sb_fdm_step_batch (sb_fdm.c:190-270). */
+typedef struct {
+    SbBlob blob;
+    int G;
+    SbFdm* f;
+    SbFdm** fp;
+    double *rhs, *sol, *work;
+} RefFdm;
+
+void ref_fdm_close(RefFdm* r) {
+    if (!r) return;
+    for (int g = 0; g < r->G; g++) sb_fdm_free(&r->f[g]);
+    free(r->f); free(r->fp); free(r->rhs); free(r->sol); free(r->work);
+    free(r);
+}
+
+RefFdm* ref_fdm_open(const char* path, int G) {
+    RefFdm* r = (RefFdm*)calloc(1, sizeof(RefFdm));
+    if (!r || G < 1) { free(r); return NULL; }
+    if (sb_open(&r->blob, path) != 0) { free(r); return NULL; }
+    r->f = (SbFdm*)calloc((size_t)G, sizeof(SbFdm));
+    r->fp = (SbFdm**)calloc((size_t)G, sizeof(SbFdm*));
+    if (!r->f || !r->fp) { ref_fdm_close(r); return NULL; }
+    for (int g = 0; g < G; g++) {
+        if (sb_fdm_init(&r->f[g], &r->blob) != 0) { r->G = g; ref_fdm_close(r); return NULL; }
+        r->G = g + 1;
+        r->fp[g] = &r->f[g];
+    }
+    const size_t n = (size_t)r->f[0].n_solved;
+    r->rhs = (double*)malloc(sizeof(double) * n * G);
+    r->sol = (double*)malloc(sizeof(double) * n * G);
+    r->work = (double*)malloc(sizeof(double) * n * G);
+    if (!r->rhs || !r->sol || !r->work) { ref_fdm_close(r); return NULL; }
+    return r;
+}
+
+void ref_fdm_dims(const RefFdm* r, int* out) {
+    out[0] = r->f[0].n_cvs;
+    out[1] = r->f[0].n_solved;
+    out[2] = r->f[0].k;
+    out[3] = r->f[0].nr;
+    out[4] = r->f[0].nc;
+}
+
+void ref_fdm_sensed_response(const RefFdm* r, double* out) {
+    const int k = r->f[0].k;
+    memcpy(out, r->f[0].sensed_response, sizeof(double) * (size_t)k * k);
+}
+
+void ref_fdm_lu_solve(const RefFdm* r, const double* b, double* x) {
+    sb_lu_solve(&r->f[0].lu, b, x, r->work);
+}
+
+/* env g's fields: T [n_cvs], M [n_solved] */
+void ref_fdm_get(const RefFdm* r, int g, double* T, double* M) {
+    memcpy(T, r->f[g].temp, sizeof(double) * (size_t)r->f[g].n_cvs);
+    memcpy(M, r->f[g].mass_temp, sizeof(double) * (size_t)r->f[g].n_solved);
+}
+
+void ref_fdm_set(RefFdm* r, int g, const double* T, const double* M) {
+    memcpy(r->f[g].temp, T, sizeof(double) * (size_t)r->f[g].n_cvs);
+    memcpy(r->f[g].mass_temp, M, sizeof(double) * (size_t)r->f[g].n_solved);
+}
+
+/* input_q [G][n_cvs], ambient / h [G], air_g / air_T [G][k] */
+void ref_fdm_step_batch(RefFdm* r, const double* input_q, const double* ambient, const double* h,
+                        const double* air_g, const double* air_T) {
+    const int G = r->G;
+    const size_t nc = (size_t)r->f[0].n_cvs, k = (size_t)r->f[0].k;
+    const double** q = (const double**)malloc(sizeof(double*) * G);
+    const double** ag = (const double**)malloc(sizeof(double*) * G);
+    const double** at = (const double**)malloc(sizeof(double*) * G);
+    for (int g = 0; g < G; g++) {
+        q[g] = input_q + g * nc;
+        ag[g] = air_g + g * k;
+        at[g] = air_T + g * k;
+    }
+    sb_fdm_step_batch(r->fp, G, q, ambient, h, ag, at, r->rhs, r->sol, r->work);
+    free(q); free(ag); free(at);
+}

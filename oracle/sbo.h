@@ -210,6 +210,20 @@ double sbo_run_batch(SboEnv** envs, const int* env_ids, int n, int steps, uint64
                      int nthreads, double* reward_sum);
 void sbo_action_row(uint64_t seed, uint32_t env, uint32_t step, int n_cont, int n_disc, float* row);
 
+/* ---------------- building-scale field step (sbo_fdm.c) ---------------- */
+typedef struct SboFdm SboFdm;
+SboFdm* sbo_fdm_open(const char* path);
+void sbo_fdm_close(SboFdm* f);
+void sbo_fdm_dims(const SboFdm* f, int* out);   /* n_cvs, n_solved, k, rows, cols */
+const double* sbo_fdm_sensed_response(const SboFdm* f);
+void sbo_fdm_init_state(const SboFdm* f, double* T, double* M);
+void sbo_fdm_lu_solve(const SboFdm* f, const double* b, double* x);
+void sbo_fdm_exposure(const SboFdm* f, double h, double* out);
+int sbo_fdm_step(const SboFdm* f, double* T, double* M, const double* input_q, double ambient, double h,
+                 const double* air_g, const double* air_T);
+int sbo_fdm_step_batch(const SboFdm* f, int G, double* T, double* M, const double* input_q, const double* ambient,
+                       const double* h, const double* air_g, const double* air_T);
+
 #ifdef __cplusplus
 }
 #endif
