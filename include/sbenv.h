@@ -392,13 +392,13 @@ void sbx_plan_free(SbxPlan* p);
  * factorization, on the device: forcing, the L and U sweeps of the SuperLU
  * factors, the air-side correction (sensed dots, the dense k x k solve, the
  * applied heat, a second solve), interior mass and the field. Results are
- * those of G sequential sb_fdm_step calls, bit for bit. The blob needs only
+ * those of G sequential sb_fdm_step calls (bit for bit with SBX_FDM_EXACT,
+ * to rounding otherwise). The blob needs only
  * the field sections (grid, solved, capacitance_rate, dirichlet_conductance,
  * mass_*, temp_init, horizontal, vertical, solver_conductivity,
  * ambient_face_areas_0/1, lu_L/lu_U/lu_perm_r/lu_perm_c, applied, sensed).
- * Envs are grouped in blocks of envs_per_block lanes (a power of two up to 64;
- * 0 picks 64 or fewer for small G); each block runs every level of a factor on
- * one workgroup. */
+ * Envs are grouped in blocks of envs_per_block lanes (a power of two up to
+ * 64); each block runs every level of a factor on one workgroup. */
 typedef struct SbxFdm SbxFdm;
 typedef struct {
     int n_cvs, n_solved, k;       /* cells, solved cells, air-side columns */
@@ -407,10 +407,23 @@ typedef struct {
     long long nnz_l, nnz_u;       /* off-diagonal factor entries */
     double bytes_per_step;        /* algorithmic HBM bytes of one batched step */
     double flops_per_step;        /* multiply-subtracts x 2 of both solves */
+    int tail_rows_l, tail_rows_u;       /* rows of each sweep's LDS run (0: exact mode) */
+    int tail_levels_l, tail_levels_u;   /* levels of the LDS run */
+    int chunked_levels_l, chunked_levels_u;   /* levels after it solved chunked from HBM */
 } SbxFdmInfo;
+/* Flags of sbx_fdm_open. Default: each sweep's longest run of narrow levels
+ * (at most 64 rows each: the separators at the top of the elimination tree,
+ * as many as fit) runs with its rows in LDS, and the levels after it with
+ * each row's terms spread over lanes; row sums are formed in another order,
+ * so results agree with the reference to rounding, far inside 1e-9
+ * relative. SBX_FDM_EXACT: every level from HBM in the reference's order,
+ * bit-identical results. envs_per_block 0 picks 1 (default) or up to 64
+ * (exact). */
+#define SBX_FDM_EXACT 1
 /* sb_fdm_init for every env: the blob's initial fields, S = sensed A^-1 applied
- * (solved on the device). NULL on error (sbx_last_error). */
-SbxFdm* sbx_fdm_open(const char* blob_path, int n_envs, int envs_per_block);
+ * (solved on the device, in the reference's order). NULL on error
+ * (sbx_last_error). */
+SbxFdm* sbx_fdm_open(const char* blob_path, int n_envs, int envs_per_block, int flags);
 void sbx_fdm_close(SbxFdm* f);
 int sbx_fdm_info(const SbxFdm* f, SbxFdmInfo* out);
 /* One step of every env on `stream` (asynchronous). Device arrays: input_q

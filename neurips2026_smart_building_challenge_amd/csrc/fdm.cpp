@@ -17,6 +17,7 @@
 extern "C" int sbf_launch_step(const sbf::Tables* t, const sbf::Group* g, const sbf::StepIn* in, hipStream_t s);
 extern "C" int sbf_launch_init(const sbf::Tables* t, const sbf::Group* g, const double* temp_init,
                                const double* mass_init, hipStream_t s);
+extern "C" int sbf_run_lds_limit(int bytes);
 extern "C" int sbf_launch_solve_cols(const sbf::Tables* t, const sbf::Group* g, const double* b, double* x,
                                      double* S, hipStream_t s);
 
@@ -65,28 +66,35 @@ struct TriHost {
 void level_order(const std::vector<std::vector<std::pair<int, double>>>& terms, const std::vector<double>* diag,
                  bool upper, TriHost* out) {
     const int n = (int)terms.size();
+    // a row of the unit lower factor without terms keeps its value: it is
+    // left out of the schedule (level -1)
+    auto skip = [&](int i) { return !upper && terms[i].empty(); };
     std::vector<int> lvl(n, 0);
     int nlev = 0;
     for (int s = 0; s < n; s++) {
         const int i = upper ? n - 1 - s : s;
-        int l = 0;
+        int l = skip(i) ? -1 : 0;
         for (const auto& e : terms[i]) l = std::max(l, lvl[e.first] + 1);
         lvl[i] = l;
         nlev = std::max(nlev, l + 1);
     }
     std::vector<int> cnt(nlev + 1, 0);
-    for (int i = 0; i < n; i++) cnt[lvl[i] + 1]++;
+    for (int i = 0; i < n; i++)
+        if (lvl[i] >= 0) cnt[lvl[i] + 1]++;
     for (int l = 0; l < nlev; l++) cnt[l + 1] += cnt[l];
+    const int nr = cnt[nlev];
     out->nlev = nlev;
     out->lev = cnt;
-    out->rows.assign(n, 0);
+    out->rows.assign(std::max(nr, 1), 0);
     std::vector<int> fill(cnt.begin(), cnt.end() - 1);
-    for (int i = 0; i < n; i++) out->rows[fill[lvl[i]]++] = i;   // ascending i within a level
-    out->ptr.assign(n + 1, 0);
+    for (int i = 0; i < n; i++)
+        if (lvl[i] >= 0) out->rows[fill[lvl[i]]++] = i;   // ascending i within a level
+    out->rows.resize(nr);
+    out->ptr.assign(nr + 1, 0);
     out->col.clear();
     out->val.clear();
     out->diag.clear();
-    for (int q = 0; q < n; q++) {
+    for (int q = 0; q < nr; q++) {
         const int i = out->rows[q];
         for (const auto& e : terms[i]) {
             out->col.push_back(e.first);
@@ -101,6 +109,131 @@ void level_order(const std::vector<std::vector<std::pair<int, double>>>& terms, 
         out->val.push_back(0.0);
     }
     if (out->diag.empty()) out->diag.push_back(1.0);
+}
+
+// Runs of the default mode (see sbf::Tail and sbf::Sweep). The LDS run is the
+// longest run of consecutive levels with at most kTailRows rows each, cut from
+// its side that borders wider levels until its row values and one level's
+// chunk partials fit in kRunLds bytes for Gl envs.
+constexpr int kTailRows = 64;
+constexpr size_t kRunLds = 152 * 1024;
+constexpr int kWaveFinishRows = 16;   // levels with more rows (some long) finish one row per lane
+
+struct RunHost {
+    int lds = 0, lev0 = 0, m = 0, nlev = 0, max_chunks = 0;
+    std::vector<int> rows, hptr, hcol, trow, tchunk, tmode, rchunk, cpos;
+    std::vector<double> diag, hval, cval;
+    size_t need(int Gl) const { return (size_t)((lds ? m : 0) + max_chunks) * Gl * 8; }
+};
+
+struct LevelOf {
+    // level of a row (-1: not scheduled, final from the start), its position in level order
+    std::vector<int> lvl, q_of;
+    LevelOf(const TriHost& T, int n) : lvl(n, -1), q_of(n, -1) {
+        for (int l = 0; l < T.nlev; l++)
+            for (int q = T.lev[l]; q < T.lev[l + 1]; q++) lvl[T.rows[q]] = l;
+        for (size_t q = 0; q < T.rows.size(); q++) q_of[T.rows[q]] = (int)q;
+    }
+};
+
+void lay_run(const TriHost& T, const LevelOf& V, int lev0, int lev1, bool lds, int Gl, RunHost* out) {
+    const int nr = (int)T.rows.size();
+    const int q0 = T.lev[lev0];
+    RunHost& o = *out;
+    o = RunHost();
+    o.lds = lds;
+    o.lev0 = lev0;
+    o.m = T.lev[lev1] - q0;
+    o.nlev = lev1 - lev0;
+    o.hptr.push_back(0);
+    o.rchunk.push_back(0);
+    for (int t = 0; t < o.nlev; t++) {
+        o.trow.push_back(T.lev[lev0 + t] - q0);
+        o.tchunk.push_back((int)o.cpos.size() / sbf::kChunk);
+        int most = 0;
+        for (int q = T.lev[lev0 + t]; q < T.lev[lev0 + t + 1]; q++) {
+            o.rows.push_back(T.rows[q]);
+            if ((int)T.diag.size() == nr) o.diag.push_back(T.diag[q]);
+            int cnt = 0;
+            for (int e = T.ptr[q]; e < T.ptr[q + 1]; e++) {
+                const int j = T.col[e];
+                if (!lds) {
+                    o.cpos.push_back(j);
+                } else if (V.lvl[j] >= lev0) {   // a row reads earlier levels only: lvl[j] < lev0 + t
+                    o.cpos.push_back(V.q_of[j] - q0);
+                } else {
+                    o.hcol.push_back(j);
+                    o.hval.push_back(T.val[e]);
+                    continue;
+                }
+                o.cval.push_back(T.val[e]);
+                cnt++;
+            }
+            while (cnt % sbf::kChunk) {
+                o.cpos.push_back(0);
+                o.cval.push_back(0.0);
+                cnt++;
+            }
+            o.hptr.push_back((int)o.hcol.size());
+            o.rchunk.push_back((int)o.cpos.size() / sbf::kChunk);
+            most = std::max(most, cnt / sbf::kChunk);
+        }
+        const int nrows = T.lev[lev0 + t + 1] - T.lev[lev0 + t];
+        const int mode = most <= 1 ? 0 : nrows > kWaveFinishRows ? 1 : most > 64 / Gl ? 2 : 3;
+        o.tmode.push_back(mode);
+        if (mode == 1 || mode == 2)
+            o.max_chunks = std::max(o.max_chunks, (int)o.cpos.size() / sbf::kChunk - o.tchunk.back());
+    }
+    o.trow.push_back(o.m);
+    o.tchunk.push_back((int)o.cpos.size() / sbf::kChunk);
+    for (auto* v : {&o.rows, &o.hcol, &o.cpos, &o.tmode})
+        if (v->empty()) v->push_back(0);
+    for (auto* v : {&o.diag, &o.hval, &o.cval})
+        if (v->empty()) v->push_back(1.0);
+}
+
+struct SweepHost {
+    int pre_end = 0, post_begin = 0, pre_chunked = 0, post_chunked = 0;
+    RunHost pre, mid, post;
+};
+
+void plan_sweep(const TriHost& T, int n, int Gl, SweepHost* out) {
+    const LevelOf V(T, n);
+    auto narrow = [&](int l) { return T.lev[l + 1] - T.lev[l] <= kTailRows; };
+    int a = 0, b = 0;   // the longest run [a, b) of narrow levels
+    for (int l = 0; l < T.nlev;) {
+        if (!narrow(l)) { l++; continue; }
+        int e = l;
+        while (e < T.nlev && narrow(e)) e++;
+        if (e - l > b - a) { a = l; b = e; }
+        l = e;
+    }
+    RunHost& mid = out->mid;
+    auto need = [&](int lo, int hi) {
+        lay_run(T, V, lo, hi, true, Gl, &mid);
+        return mid.need(Gl);
+    };
+    if (b > a && need(a, b) > kRunLds) {
+        // cut the side that borders wider levels (for the L sweep the run ends
+        // the schedule, for the U sweep it starts it); fewer levels need less
+        // LDS, so bisect for the longest run that fits
+        const bool keep_end = b == T.nlev;
+        int lo = 0, hi = b - a;   // levels kept
+        while (lo < hi) {
+            const int mid_n = lo + (hi - lo + 1) / 2;
+            if (need(keep_end ? b - mid_n : a, keep_end ? b : a + mid_n) <= kRunLds) lo = mid_n;
+            else hi = mid_n - 1;
+        }
+        if (keep_end) a = b - lo;
+        else b = a + lo;
+    }
+    lay_run(T, V, a, b, true, Gl, &mid);
+    out->pre_end = a;
+    out->post_begin = b;
+    lay_run(T, V, 0, a, false, Gl, &out->pre);
+    out->pre_chunked = out->pre.nlev > 0 && out->pre.need(Gl) <= kRunLds;
+    lay_run(T, V, b, T.nlev, false, Gl, &out->post);
+    out->post_chunked = out->post.nlev > 0 && out->post.need(Gl) <= kRunLds;
 }
 
 bool csc_ok(const sbh::Blob& b, const char* name, int n_rows, int n_cols, const int32_t** p, const int32_t** ix,
@@ -170,7 +303,7 @@ bool hip_check(hipError_t e, const char* what) {
     return fail(std::string(what) + ": " + hipGetErrorString(e));
 }
 
-bool build(SbxFdm* f, const char* path, int G, int epb) {
+bool build(SbxFdm* f, const char* path, int G, int epb, int flags) {
     sbh::Blob b;
     std::string err;
     if (!b.open(path, &err)) return fail(err);
@@ -326,6 +459,47 @@ bool build(SbxFdm* f, const char* path, int G, int epb) {
     };
     put_tri(&T.L, L);
     put_tri(&T.U, U);
+    // envs per block: as asked; by default one (the default mode keeps a run's
+    // rows in LDS per env) or, in exact mode, up to 64
+    const bool exact = (flags & SBX_FDM_EXACT) != 0;
+    const int gl = std::min(64, next_pow2(std::min(G, epb > 0 ? epb : (exact ? 64 : 1))));
+    T.fast = exact ? 0 : 1;
+    SweepHost sl, su;
+    if (T.fast) {
+        plan_sweep(L, n, gl, &sl);
+        plan_sweep(U, n, gl, &su);
+    }
+    auto put_run = [&](sbf::Tail* d, const RunHost& h) {
+        d->lds = h.lds;
+        d->lev0 = h.lev0;
+        d->m = h.m;
+        d->nlev = h.nlev;
+        d->max_chunks = h.max_chunks;
+        put((const void**)&d->rows, A.vec(h.rows));
+        put((const void**)&d->diag, A.vec(h.diag));
+        put((const void**)&d->hptr, A.vec(h.hptr));
+        put((const void**)&d->hcol, A.vec(h.hcol));
+        put((const void**)&d->hval, A.vec(h.hval));
+        put((const void**)&d->trow, A.vec(h.trow));
+        put((const void**)&d->tchunk, A.vec(h.tchunk));
+        put((const void**)&d->tmode, A.vec(h.tmode));
+        put((const void**)&d->rchunk, A.vec(h.rchunk));
+        put((const void**)&d->cpos, A.vec(h.cpos));
+        put((const void**)&d->cval, A.vec(h.cval));
+    };
+    auto put_sweep = [&](sbf::Sweep* d, const SweepHost& h) {
+        d->pre_end = h.pre_end;
+        d->post_begin = h.post_begin;
+        d->pre_chunked = h.pre_chunked;
+        d->post_chunked = h.post_chunked;
+        put_run(&d->mid, h.mid);
+        if (h.pre_chunked) put_run(&d->pre, h.pre);
+        if (h.post_chunked) put_run(&d->post, h.post);
+    };
+    if (T.fast) {
+        put_sweep(&T.SL, sl);
+        put_sweep(&T.SU, su);
+    }
     put((const void**)&T.sn_p, A.add(sp, 4 * (size_t)(k + 1)));
     put((const void**)&T.sn_w, A.vec(snw));
     put((const void**)&T.sn_x, A.add(sx, 8 * (size_t)std::max<uint64_t>(nnzS, 1)));
@@ -338,6 +512,7 @@ bool build(SbxFdm* f, const char* path, int G, int epb) {
     if (!hip_check(hipMemcpy(f->d_tables, A.host.data(), A.host.size(), hipMemcpyHostToDevice), "upload field tables"))
         return false;
     for (auto& e : fix) *e.first = f->d_tables + e.second;
+    if (T.fast && !hip_check((hipError_t)sbf_run_lds_limit((int)kRunLds), "run LDS limit")) return false;
     if (!hip_check(hipMalloc(&f->d_temp_init, 8 * (size_t)n_cvs), "hipMalloc(temp_init)")) return false;
     if (!hip_check(hipMalloc(&f->d_mass_init, 8 * (size_t)n), "hipMalloc(mass_temp_init)")) return false;
     if (!hip_check(hipMemcpy(f->d_temp_init, tinit, 8 * (size_t)n_cvs, hipMemcpyHostToDevice), "upload temp_init")
@@ -348,8 +523,7 @@ bool build(SbxFdm* f, const char* path, int G, int epb) {
     // columns solved as a group of k envs
     if (k > 0) {
         sbf::Group sg{};
-        const int gl = std::min(64, next_pow2(k));
-        if (!make_group(f, k, gl, false, &sg)) return false;
+        if (!make_group(f, k, std::min(64, next_pow2(k)), false, &sg)) return false;
         if (!hip_check((hipError_t)sbf_launch_solve_cols(&T, &sg, nullptr, nullptr, (double*)T.S, nullptr),
                        "sensed response")
             || !hip_check(hipDeviceSynchronize(), "sensed response"))
@@ -359,7 +533,6 @@ bool build(SbxFdm* f, const char* path, int G, int epb) {
             f->owned.erase(std::find(f->owned.begin(), f->owned.end(), p));
         }
     }
-    const int gl = std::min(64, next_pow2(std::min(G, epb > 0 ? epb : 64)));
     if (!make_group(f, G, gl, true, &f->grp)) return false;
     if (!hip_check((hipError_t)sbf_launch_init(&T, &f->grp, f->d_temp_init, f->d_mass_init, nullptr), "field init")
         || !hip_check(hipDeviceSynchronize(), "field init"))
@@ -376,6 +549,12 @@ bool build(SbxFdm* f, const char* path, int G, int epb) {
     I.levels_u = U.nlev;
     I.nnz_l = L.nnz;
     I.nnz_u = U.nnz;
+    I.tail_rows_l = T.fast ? sl.mid.m : 0;
+    I.tail_rows_u = T.fast ? su.mid.m : 0;
+    I.tail_levels_l = T.fast ? sl.mid.nlev : 0;
+    I.tail_levels_u = T.fast ? su.mid.nlev : 0;
+    I.chunked_levels_l = T.fast && sl.post_chunked ? sl.post.nlev : 0;
+    I.chunked_levels_u = T.fast && su.post_chunked ? su.post.nlev : 0;
     // algorithmic HBM bytes of one batched step: per block, both factors read
     // once per solve (value + column per term, U's diagonal, row ids and row
     // pointers); per env the heat input, the field read (solved cells) and
@@ -392,13 +571,13 @@ bool build(SbxFdm* f, const char* path, int G, int epb) {
 
 extern "C" {
 
-SbxFdm* sbx_fdm_open(const char* blob_path, int n_envs, int envs_per_block) {
-    if (!blob_path || n_envs < 1 || envs_per_block < 0) {
-        sbx_set_error("sbx_fdm_open: blob path, n_envs >= 1 and envs_per_block >= 0 required");
+SbxFdm* sbx_fdm_open(const char* blob_path, int n_envs, int envs_per_block, int flags) {
+    if (!blob_path || n_envs < 1 || envs_per_block < 0 || (flags & ~SBX_FDM_EXACT)) {
+        sbx_set_error("sbx_fdm_open: blob path, n_envs >= 1, envs_per_block >= 0 and known flags required");
         return nullptr;
     }
     SbxFdm* f = new SbxFdm();
-    if (!build(f, blob_path, n_envs, envs_per_block)) {
+    if (!build(f, blob_path, n_envs, envs_per_block, flags)) {
         sbx_fdm_close(f);
         return nullptr;
     }

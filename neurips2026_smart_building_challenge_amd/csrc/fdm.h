@@ -29,6 +29,54 @@ struct Tri {
     const double* diag;
 };
 
+// A run of consecutive levels lev0 .. lev0 + nlev - 1 of a factor's Tri,
+// solved level by level by one workgroup per block with each row's terms cut
+// into chunks of kChunk spread over the lanes (partial sums in LDS, then one
+// wavefront per row, or one lane per row where no row of the level has more
+// than one chunk, adds them and finishes the row). Two kinds:
+//   lds = 1: the run's own row values live in LDS for its duration (the narrow
+//     levels at the top of the elimination tree: the last levels of the L
+//     sweep, the first of the U sweep); terms on earlier levels ("head" terms,
+//     final before the run starts) per row in [hptr[r], hptr[r + 1]) of
+//     (hcol, hval) are applied first, and chunk positions index the run;
+//   lds = 0: values stay in HBM and chunk positions are row ids.
+// Rows in level order r = 0 .. m-1 (rows[r]); level t spans chunks
+// [tchunk[t], tchunk[t + 1]) and rows [trow[t], trow[t + 1]); row r's chunks
+// are [rchunk[r], rchunk[r + 1]). tmode[t]: 0 no row of the level has more
+// than one chunk (each lane finishes its rows directly, no partials); 1 and 2
+// chunks spread over all lanes, partials in LDS, rows finished one lane each
+// (1, wide levels) or one wavefront each (2, a few rows longer than a
+// wavefront's lanes); 3 one wavefront per row, no partials. Padding terms are
+// (0, 0.0).
+constexpr int kChunk = 8;
+
+struct Tail {
+    int lds;
+    int lev0, m, nlev, max_chunks;
+    const int* rows;
+    const double* diag;     // [m] U's diagonal (unused for L)
+    const int* hptr;
+    const int* hcol;
+    const double* hval;
+    const int* trow;
+    const int* tchunk;
+    const int* tmode;
+    const int* rchunk;
+    const int* cpos;        // [chunks * kChunk]
+    const double* cval;     // [chunks * kChunk]
+};
+
+// How one factor's sweep runs in the default (non-exact) mode: the levels
+// before the LDS run, the LDS run, the levels after it; the levels before and
+// after run chunked from HBM when one level's partials fit in LDS, else as
+// plain row solves.
+struct Sweep {
+    int pre_end;            // levels [0, pre_end) before the LDS run
+    int post_begin;         // levels [post_begin, nlev) after it
+    int pre_chunked, post_chunked;
+    Tail pre, mid, post;    // (mid.nlev may be 0)
+};
+
 struct Tables {
     int n, n_cvs, k, n_unsolved;
     const int* ir;          // [n] row of the permuted vector -> solved index t
@@ -38,6 +86,8 @@ struct Tables {
     const double *cap, *dir, *mcoup, *mret, *mgain;   // [n] by t
     const double *a0, *a1, *hz, *vt, *cd;             // [n] by t: exterior face areas, half widths, conductivity
     Tri L, U;
+    int fast;               // chunked runs (reassociated sums) instead of every level in order
+    Sweep SL, SU;
     // sensed rows (k): entries p in [sn_p[i], sn_p[i + 1]) weigh row sn_w[p] of the solution
     const int* sn_p;
     const int* sn_w;

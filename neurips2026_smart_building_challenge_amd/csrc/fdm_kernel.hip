@@ -23,6 +23,8 @@
 #include <math.h>
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "fdm.h"
 
 namespace {
@@ -38,7 +40,8 @@ __device__ __forceinline__ size_t gstride() { return (size_t)gridDim.x * blockDi
 // whose solution is not used) returns at once. GL lanes per row (the block's
 // envs), 64 / GL rows per wavefront.
 template <bool UPPER, int GL>
-__global__ __launch_bounds__(kSolveThreads) void solve_kernel(sbf::Tri tri, int n, double* W, const int* bact) {
+__global__ __launch_bounds__(kSolveThreads) void solve_kernel(sbf::Tri tri, int lev_begin, int lev_end, int n,
+                                                              double* W, const int* bact) {
     constexpr int R = 64 / GL;
     constexpr int STEP = (kSolveThreads / 64) * R;
     const int b = blockIdx.x;
@@ -46,7 +49,7 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(sbf::Tri tri, int 
     double* Wb = W + (size_t)b * n * GL;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int gl = lane % GL, rs = lane / GL;
-    for (int l = 0; l < tri.nlev; l++) {
+    for (int l = lev_begin; l < lev_end; l++) {
         const int lo = tri.lev[l], hi = tri.lev[l + 1];
         for (int q = lo + wave * R + rs; q < hi; q += STEP) {
             const int i = tri.rows[q];
@@ -59,6 +62,212 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(sbf::Tri tri, int 
         }
         __syncthreads();
     }
+}
+
+// Sum over a wavefront's lanes that share an env (lanes l, l + GL, ...), in a
+// fixed order; every lane gets the total.
+template <int GL>
+__device__ __forceinline__ double lane_sum(double v) {
+#pragma unroll
+    for (int off = GL; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Head terms of the tail rows (columns finished before the tail's first
+// level): W[row] -= their sum, one wavefront per (block, tail row), the terms
+// spread over the lanes of each env.
+template <int GL>
+__global__ __launch_bounds__(256) void head_kernel(sbf::Tail tl, int n, int nblk, double* W, const int* bact) {
+    constexpr int S = 64 / GL;
+    const int lane = threadIdx.x & 63;
+    const int gl = lane % GL, s = lane / GL;
+    const size_t nw = (size_t)gridDim.x * (blockDim.x >> 6);
+    for (size_t x = (size_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); x < (size_t)nblk * tl.m; x += nw) {
+        const int b = (int)(x / tl.m), r = (int)(x % tl.m);
+        if (bact && !bact[b]) continue;
+        double* Wb = W + (size_t)b * n * GL;
+        double acc = 0.0;
+        const int e1 = tl.hptr[r + 1];
+        for (int e = tl.hptr[r] + s; e < e1; e += S) acc += tl.hval[e] * Wb[(size_t)tl.hcol[e] * GL + gl];
+        acc = lane_sum<GL>(acc);
+        if (s == 0) Wb[(size_t)tl.rows[r] * GL + gl] -= acc;
+    }
+}
+
+// Workgroup barrier ordering LDS accesses only: global loads in flight (the
+// next level's chunks) stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// The levels of one run (sbf::Tail) of one block (one workgroup), in order:
+//   tmode 0 (no row has more than one chunk): each lane takes a row, forms its
+//     chunk's sum and finishes it;
+//   tmode 1 and 2: each lane forms the partial sum of one chunk of kChunk
+//     terms into LDS, then, after an LDS barrier, rows are finished from their
+//     chunks' partials, one lane per row (tmode 1, wide levels) or one
+//     wavefront per row (tmode 2, a few long rows);
+//   tmode 3 (a few rows, each with no more chunks than a wavefront has lanes
+//     per env): each wavefront takes a row, its lanes sum the row's chunks and
+//     the wavefront adds the lanes' sums.
+// Each level starts by loading the first chunk each lane uses in the next
+// level and, in HBM runs, the value of the first row it will finish there.
+// LDSW: the run's row values live in LDS (loaded at the start, stored at the
+// end), chunk positions index the run and levels are separated by LDS
+// barriers; otherwise values are read from and written to HBM, positions are
+// row ids and levels are separated by full workgroup barriers.
+typedef const __attribute__((address_space(4))) int* cint_ptr;
+
+template <bool UPPER, int GL, bool LDSW>
+__global__ __launch_bounds__(kSolveThreads) void run_kernel(sbf::Tail tl, int n, double* W, const int* bact) {
+    extern __shared__ double lds[];
+    // level metadata is uniform: read through the scalar (constant) path, so
+    // these reads do not queue behind the vector loads of the prefetch
+    const cint_ptr trow = (cint_ptr)tl.trow;
+    const cint_ptr tchunk = (cint_ptr)tl.tchunk;
+    const cint_ptr tmode = (cint_ptr)tl.tmode;
+    constexpr int NS = kSolveThreads / GL;   // lane slots of the workgroup per env
+    constexpr int NW = kSolveThreads / 64;
+    constexpr int S = 64 / GL;
+    constexpr int K = sbf::kChunk;
+    const int b = blockIdx.x;
+    if (bact && !bact[b]) return;
+    double* Wb = W + (size_t)b * n * GL;
+    double* Wt = lds;
+    double* P = LDSW ? lds + (size_t)tl.m * GL : lds;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int gl = tid % GL, slot = tid / GL;
+    const int s = lane / GL;
+    if (LDSW)
+        for (int x = tid; x < tl.m * GL; x += kSolveThreads) Wt[x] = Wb[(size_t)tl.rows[x / GL] * GL + x % GL];
+    struct Chunk {
+        int4 a0, a1;
+        double v[K];
+    };
+    auto fetch = [&](int c, Chunk& ch) {
+        const int4* cp = reinterpret_cast<const int4*>(tl.cpos + (size_t)K * c);
+        const double2* cv = reinterpret_cast<const double2*>(tl.cval + (size_t)K * c);
+        ch.a0 = cp[0];
+        ch.a1 = cp[1];
+#pragma unroll
+        for (int j = 0; j < K / 2; j++) {
+            const double2 d = cv[j];
+            ch.v[2 * j] = d.x;
+            ch.v[2 * j + 1] = d.y;
+        }
+    };
+    auto val = [&](int pos) -> double { return LDSW ? Wt[pos * GL + gl] : Wb[(size_t)pos * GL + gl]; };
+    auto part = [&](const Chunk& ch) {
+        const int pos[K] = {ch.a0.x, ch.a0.y, ch.a0.z, ch.a0.w, ch.a1.x, ch.a1.y, ch.a1.z, ch.a1.w};
+        double w[K];
+#pragma unroll
+        for (int j = 0; j < K; j++) w[j] = val(pos[j]);
+        double acc = ch.v[0] * w[0];
+#pragma unroll
+        for (int j = 1; j < K; j++) acc += ch.v[j] * w[j];
+        return acc;
+    };
+    auto own_ref = [&](int r) -> double* { return LDSW ? &Wt[r * GL + gl] : &Wb[(size_t)tl.rows[r] * GL + gl]; };
+    auto finish = [&](int r, double own, double acc) {
+        double w = own - acc;
+        if (UPPER) w = w / tl.diag[r];
+        *own_ref(r) = w;
+    };
+    // the first row this lane finishes in level t (-1: none) and the chunk it
+    // starts the level with (-1: none)
+    auto first_row = [&](int t) -> int {
+        const int mode = tmode[t];
+        const bool by_wave = mode >= 2;
+        const int r = trow[t] + (by_wave ? wave : slot);
+        return (r < trow[t + 1] && (!by_wave || s == 0)) ? r : -1;
+    };
+    auto first_chunk = [&](int t) -> int {
+        const int mode = tmode[t];
+        if (mode == 1 || mode == 2) {
+            const int c = tchunk[t] + slot;
+            return c < tchunk[t + 1] ? c : -1;
+        }
+        const int r = trow[t] + (mode == 3 ? wave : slot);
+        if (r >= trow[t + 1]) return -1;
+        const int c = tl.rchunk[r] + (mode == 3 ? s : 0);
+        return c < tl.rchunk[r + 1] ? c : -1;
+    };
+    // this level's first chunk and row value (cur*), the next level's (nxt*)
+    Chunk cur, nxt;
+    int curc = -1, curr = -1, nxtc = -1, nxtr = -1;
+    double curo = 0.0, nxto = 0.0;
+    // loads issued whether or not the lane uses them (index 0 when not), so
+    // the compiler can wait for exactly the ones a use needs
+    auto load_first = [&](int t, Chunk& ch, int& c, int& r, double& o) {
+        c = first_chunk(t);
+        fetch(c >= 0 ? c : 0, ch);
+        if (!LDSW) {
+            r = first_row(t);
+            o = Wb[(size_t)tl.rows[r >= 0 ? r : 0] * GL + gl];
+        }
+    };
+    auto own_of = [&](int r) -> double {
+        if (r == curr) {
+            curr = -1;
+            return curo;
+        }
+        return *own_ref(r);
+    };
+    auto chunk_of = [&](int c, Chunk& tmp) -> const Chunk& {
+        if (c == curc) return cur;
+        fetch(c, tmp);
+        return tmp;
+    };
+    if (tl.nlev > 0) load_first(0, cur, curc, curr, curo);
+    __syncthreads();
+    for (int t = 0; t < tl.nlev; t++) {
+        if (t + 1 < tl.nlev) load_first(t + 1, nxt, nxtc, nxtr, nxto);
+        const int clo = tchunk[t], chi = tchunk[t + 1];
+        const int mode = tmode[t];
+        Chunk tmp;
+        if (mode == 0) {
+            for (int r = trow[t] + slot; r < trow[t + 1]; r += NS) {
+                double acc = 0.0;
+                if (tl.rchunk[r] < tl.rchunk[r + 1]) acc = part(chunk_of(tl.rchunk[r], tmp));
+                finish(r, own_of(r), acc);
+            }
+        } else if (mode == 1 || mode == 2) {
+            for (int c = clo + slot; c < chi; c += NS) P[(size_t)(c - clo) * GL + gl] = part(chunk_of(c, tmp));
+            lds_barrier();
+            if (mode == 1) {
+                for (int r = trow[t] + slot; r < trow[t + 1]; r += NS) {
+                    double acc = 0.0;
+                    for (int c = tl.rchunk[r]; c < tl.rchunk[r + 1]; c++) acc += P[(size_t)(c - clo) * GL + gl];
+                    finish(r, own_of(r), acc);
+                }
+            } else {
+                for (int r = trow[t] + wave; r < trow[t + 1]; r += NW) {
+                    const int c1 = tl.rchunk[r + 1] - clo;
+                    double acc = 0.0;
+                    for (int c = tl.rchunk[r] - clo + s; c < c1; c += S) acc += P[(size_t)c * GL + gl];
+                    acc = lane_sum<GL>(acc);
+                    if (s == 0) finish(r, own_of(r), acc);
+                }
+            }
+        } else {
+            for (int r = trow[t] + wave; r < trow[t + 1]; r += NW) {
+                double acc = 0.0;
+                for (int c = tl.rchunk[r] + s; c < tl.rchunk[r + 1]; c += S) acc += part(chunk_of(c, tmp));
+                acc = lane_sum<GL>(acc);
+                if (s == 0) finish(r, own_of(r), acc);
+            }
+        }
+        cur = nxt;
+        curc = nxtc;
+        curr = nxtr;
+        curo = nxto;
+        if (LDSW) lds_barrier();
+        else __syncthreads();
+    }
+    if (LDSW)
+        for (int x = tid; x < tl.m * GL; x += kSolveThreads) Wb[(size_t)tl.rows[x / GL] * GL + x % GL] = Wt[x];
 }
 
 // sum_p x[p] * W[row w[p]] over [p0, p1) in order, 8 terms per round trip
@@ -122,6 +331,22 @@ __global__ void sensed_kernel(sbf::Tables t, sbf::Group g, sbf::StepIn in) {
         const int b = env / Gl, l = env % Gl;
         const double acc = sensed_dot(t.sn_w, t.sn_x, t.sn_p[i], t.sn_p[i + 1], g.W1 + (size_t)b * t.n * Gl, Gl, l);
         g.pw[x] = in.g[x] * (in.airT[x] - acc);
+    }
+}
+
+// The same with each dot spread over a wavefront's 64 lanes (one wavefront per
+// env and row; the sum in another, fixed, order).
+__global__ __launch_bounds__(256) void sensed_wide_kernel(sbf::Tables t, sbf::Group g, sbf::StepIn in) {
+    const int k = t.k, Gl = g.Gl, lane = threadIdx.x & 63;
+    const size_t nw = (size_t)gridDim.x * (blockDim.x >> 6);
+    for (size_t x = (size_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); x < (size_t)g.G * k; x += nw) {
+        const int env = (int)(x / k), i = (int)(x % k);
+        const int b = env / Gl, l = env % Gl;
+        const double* Wb = g.W1 + (size_t)b * t.n * Gl;
+        double acc = 0.0;
+        for (int p = t.sn_p[i] + lane; p < t.sn_p[i + 1]; p += 64) acc += t.sn_x[p] * Wb[(size_t)t.sn_w[p] * Gl + l];
+        acc = lane_sum<1>(acc);
+        if (lane == 0) g.pw[x] = in.g[x] * (in.airT[x] - acc);
     }
 }
 
@@ -307,24 +532,77 @@ int elt_grid(size_t total) {
     return (int)(b < 1 ? 1 : (b > 16384 ? 16384 : b));
 }
 
-template <int GL>
-void solve_gl(const sbf::Tables& t, const sbf::Group& g, double* W, const int* bact, hipStream_t s) {
-    hipLaunchKernelGGL((solve_kernel<false, GL>), dim3(g.nblk), dim3(kSolveThreads), 0, s, t.L, t.n, W, bact);
-    hipLaunchKernelGGL((solve_kernel<true, GL>), dim3(g.nblk), dim3(kSolveThreads), 0, s, t.U, t.n, W, bact);
+template <bool UPPER, int GL>
+void sweep(const sbf::Tri& tri, const sbf::Sweep* sw, const sbf::Group& g, int n, double* W, const int* bact,
+           hipStream_t s) {
+    auto plain = [&](int l0, int l1) {
+        if (l1 > l0)
+            hipLaunchKernelGGL((solve_kernel<UPPER, GL>), dim3(g.nblk), dim3(kSolveThreads), 0, s, tri, l0, l1, n, W,
+                               bact);
+    };
+    if (!sw) {
+        plain(0, tri.nlev);
+        return;
+    }
+    // levels before the LDS run; the run's head terms and the run; the levels after it
+    if (sw->pre_chunked) {
+        const size_t lds = (size_t)sw->pre.max_chunks * GL * sizeof(double);
+        hipLaunchKernelGGL((run_kernel<UPPER, GL, false>), dim3(g.nblk), dim3(kSolveThreads), lds, s, sw->pre, n, W,
+                           bact);
+    } else {
+        plain(0, sw->pre_end);
+    }
+    const sbf::Tail& mid = sw->mid;
+    if (mid.nlev > 0) {
+        if (mid.lev0 > 0) {
+            const size_t waves = (size_t)g.nblk * mid.m;
+            const int grid = (int)std::min<size_t>((waves + 3) / 4, 8192);
+            hipLaunchKernelGGL((head_kernel<GL>), dim3(grid), dim3(256), 0, s, mid, n, g.nblk, W, bact);
+        }
+        const size_t lds = (size_t)(mid.m + mid.max_chunks) * GL * sizeof(double);
+        hipLaunchKernelGGL((run_kernel<UPPER, GL, true>), dim3(g.nblk), dim3(kSolveThreads), lds, s, mid, n, W, bact);
+    }
+    if (sw->post_chunked) {
+        const size_t lds = (size_t)sw->post.max_chunks * GL * sizeof(double);
+        hipLaunchKernelGGL((run_kernel<UPPER, GL, false>), dim3(g.nblk), dim3(kSolveThreads), lds, s, sw->post, n, W,
+                           bact);
+    } else {
+        plain(sw->post_begin, tri.nlev);
+    }
 }
 
-int solve(const sbf::Tables& t, const sbf::Group& g, double* W, const int* bact, hipStream_t s) {
+template <int GL>
+void solve_gl(const sbf::Tables& t, const sbf::Group& g, double* W, const int* bact, bool exact, hipStream_t s) {
+    const bool fast = t.fast && !exact;
+    sweep<false, GL>(t.L, fast ? &t.SL : nullptr, g, t.n, W, bact, s);
+    sweep<true, GL>(t.U, fast ? &t.SU : nullptr, g, t.n, W, bact, s);
+}
+
+// The L then U sweep of every block's columns of W; exact: every level in the
+// reference's order (the tails are laid out for the step's group only).
+int solve(const sbf::Tables& t, const sbf::Group& g, double* W, const int* bact, bool exact, hipStream_t s) {
     switch (g.Gl) {
-    case 1: solve_gl<1>(t, g, W, bact, s); break;
-    case 2: solve_gl<2>(t, g, W, bact, s); break;
-    case 4: solve_gl<4>(t, g, W, bact, s); break;
-    case 8: solve_gl<8>(t, g, W, bact, s); break;
-    case 16: solve_gl<16>(t, g, W, bact, s); break;
-    case 32: solve_gl<32>(t, g, W, bact, s); break;
-    case 64: solve_gl<64>(t, g, W, bact, s); break;
+    case 1: solve_gl<1>(t, g, W, bact, exact, s); break;
+    case 2: solve_gl<2>(t, g, W, bact, exact, s); break;
+    case 4: solve_gl<4>(t, g, W, bact, exact, s); break;
+    case 8: solve_gl<8>(t, g, W, bact, exact, s); break;
+    case 16: solve_gl<16>(t, g, W, bact, exact, s); break;
+    case 32: solve_gl<32>(t, g, W, bact, exact, s); break;
+    case 64: solve_gl<64>(t, g, W, bact, exact, s); break;
     default: return (int)hipErrorInvalidValue;
     }
     return (int)hipGetLastError();
+}
+
+template <int GL>
+hipError_t run_limit(int bytes) {
+    const void* fns[4] = {(const void*)run_kernel<false, GL, true>, (const void*)run_kernel<true, GL, true>,
+                          (const void*)run_kernel<false, GL, false>, (const void*)run_kernel<true, GL, false>};
+    for (const void* f : fns) {
+        const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 }  // namespace
@@ -333,15 +611,28 @@ int solve(const sbf::Tables& t, const sbf::Group& g, double* W, const int* bact,
 extern "C" int sbf_launch_step(const sbf::Tables* t, const sbf::Group* g, const sbf::StepIn* in, hipStream_t s) {
     const size_t rows = (size_t)g->nblk * t->n * g->Gl;
     hipLaunchKernelGGL(forcing_kernel, dim3(elt_grid(rows)), dim3(kEltThreads), 0, s, *t, *g, *in);
-    if (int e = solve(*t, *g, g->W1, nullptr, s)) return e;
+    if (int e = solve(*t, *g, g->W1, nullptr, false, s)) return e;
     if (t->k > 0) {
-        hipLaunchKernelGGL(sensed_kernel, dim3(elt_grid((size_t)g->G * t->k)), dim3(kEltThreads), 0, s, *t, *g, *in);
+        if (t->fast)
+            hipLaunchKernelGGL(sensed_wide_kernel, dim3((int)std::min<size_t>(((size_t)g->G * t->k + 3) / 4, 16384)),
+                               dim3(256), 0, s, *t, *g, *in);
+        else
+            hipLaunchKernelGGL(sensed_kernel, dim3(elt_grid((size_t)g->G * t->k)), dim3(kEltThreads), 0, s, *t, *g,
+                               *in);
         hipLaunchKernelGGL(dense_kernel, dim3(g->G), dim3(64), 0, s, *t, *g, *in);
         hipLaunchKernelGGL(applied_kernel, dim3(elt_grid(rows)), dim3(kEltThreads), 0, s, *t, *g);
-        if (int e = solve(*t, *g, g->W2, g->bact, s)) return e;
+        if (int e = solve(*t, *g, g->W2, g->bact, false, s)) return e;
     }
     hipLaunchKernelGGL(update_kernel, dim3(elt_grid(rows)), dim3(kEltThreads), 0, s, *t, *g, *in);
     return (int)hipGetLastError();
+}
+
+// Lets the run kernels use `bytes` of dynamic LDS.
+extern "C" int sbf_run_lds_limit(int bytes) {
+    for (hipError_t e : {run_limit<1>(bytes), run_limit<2>(bytes), run_limit<4>(bytes), run_limit<8>(bytes),
+                         run_limit<16>(bytes), run_limit<32>(bytes), run_limit<64>(bytes)})
+        if (e != hipSuccess) return (int)e;
+    return 0;
 }
 
 extern "C" int sbf_launch_init(const sbf::Tables* t, const sbf::Group* g, const double* temp_init,
@@ -357,7 +648,7 @@ extern "C" int sbf_launch_solve_cols(const sbf::Tables* t, const sbf::Group* g, 
                                      double* S, hipStream_t s) {
     const size_t rows = (size_t)g->nblk * t->n * g->Gl;
     hipLaunchKernelGGL(rhs_kernel, dim3(elt_grid(rows)), dim3(kEltThreads), 0, s, *t, *g, b);
-    if (int e = solve(*t, *g, g->W1, nullptr, s)) return e;
+    if (int e = solve(*t, *g, g->W1, nullptr, true, s)) return e;
     if (x) hipLaunchKernelGGL(sol_kernel, dim3(elt_grid((size_t)g->G * t->n)), dim3(kEltThreads), 0, s, *t, *g, x);
     if (S) hipLaunchKernelGGL(sresp_kernel, dim3(elt_grid((size_t)t->k * t->k)), dim3(kEltThreads), 0, s, *t, *g, S);
     return (int)hipGetLastError();

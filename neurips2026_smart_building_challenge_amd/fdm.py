@@ -29,7 +29,12 @@ class SbxFdmInfo(ctypes.Structure):
                 ("n_envs", ctypes.c_int), ("envs_per_block", ctypes.c_int), ("n_blocks", ctypes.c_int),
                 ("levels_l", ctypes.c_int), ("levels_u", ctypes.c_int),
                 ("nnz_l", ctypes.c_longlong), ("nnz_u", ctypes.c_longlong),
-                ("bytes_per_step", ctypes.c_double), ("flops_per_step", ctypes.c_double)]
+                ("bytes_per_step", ctypes.c_double), ("flops_per_step", ctypes.c_double),
+                ("tail_rows_l", ctypes.c_int), ("tail_rows_u", ctypes.c_int),
+                ("tail_levels_l", ctypes.c_int), ("tail_levels_u", ctypes.c_int),
+                ("chunked_levels_l", ctypes.c_int), ("chunked_levels_u", ctypes.c_int)]
+
+EXACT = 1   # SBX_FDM_EXACT: every level in the reference's order, bit-identical results
 
 
 _BOUND = False
@@ -40,7 +45,7 @@ def _lib() -> ctypes.CDLL:
     L = E.lib()
     if not _BOUND:
         L.sbx_fdm_open.restype = P
-        L.sbx_fdm_open.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int]
+        L.sbx_fdm_open.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         L.sbx_fdm_close.argtypes = [P]
         L.sbx_fdm_info.argtypes = [P, ctypes.POINTER(SbxFdmInfo)]
         L.sbx_fdm_step.argtypes = [P, P, P, P, P, P, P]
@@ -66,13 +71,13 @@ def cell_major(a: np.ndarray) -> np.ndarray:
 
 
 class FieldGroup:
-    def __init__(self, blob: str | Path, n_envs: int, envs_per_block: int = 0):
+    def __init__(self, blob: str | Path, n_envs: int, envs_per_block: int = 0, exact: bool = False):
         import torch
 
         torch.cuda.init()   # torch's HIP runtime state before the library's first HIP call
         L = _lib()
         self.L = L
-        self.h = L.sbx_fdm_open(str(blob).encode(), int(n_envs), int(envs_per_block))
+        self.h = L.sbx_fdm_open(str(blob).encode(), int(n_envs), int(envs_per_block), EXACT if exact else 0)
         if not self.h:
             raise RuntimeError(f"sbx_fdm_open: {L.sbx_last_error().decode()}")
         info = SbxFdmInfo()
