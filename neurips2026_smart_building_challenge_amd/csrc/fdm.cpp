@@ -555,14 +555,15 @@ bool build(SbxFdm* f, const char* path, int G, int epb, int flags) {
     I.tail_levels_u = T.fast ? su.mid.nlev : 0;
     I.chunked_levels_l = T.fast && sl.post_chunked ? sl.post.nlev : 0;
     I.chunked_levels_u = T.fast && su.post_chunked ? su.post.nlev : 0;
-    // algorithmic HBM bytes of one batched step: per block, both factors read
-    // once per solve (value + column per term, U's diagonal, row ids and row
-    // pointers); per env the heat input, the field read (solved cells) and
+    // algorithmic HBM bytes of one batched step: both factors read once per
+    // solve for the whole group (value + column per term, U's diagonal, row
+    // ids and row pointers: shared by every env, however the blocks re-read
+    // them); per env the heat input, the field read (solved cells) and
     // written (all cells), the mass read and written, and each solve's vector
     // read and written once per sweep
     const double per_solve = 12.0 * (double)(L.nnz + U.nnz) + 8.0 * n + 2.0 * 8.0 * n;
     const double per_env = 8.0 * ((double)n_cvs + n + n_cvs + 2.0 * n) + 2.0 * (2.0 * 2.0 * 8.0 * n);
-    I.bytes_per_step = (double)f->grp.nblk * 2.0 * per_solve + (double)G * per_env;
+    I.bytes_per_step = 2.0 * per_solve + (double)G * per_env;
     I.flops_per_step = (double)G * 2.0 * 2.0 * (double)(L.nnz + U.nnz);
     return true;
 }
