@@ -152,7 +152,7 @@ def fdm_leg(envs: int, steps: int, cpu: bool, cpu_threads: int) -> dict:
     import numpy as np
     import torch
 
-    from neurips2026_smart_building_challenge_amd.fdm import FieldGroup, cell_major
+    from neurips2026_smart_building_challenge_amd.fdm import FieldGroup
     from neurips2026_smart_building_challenge_amd.scenario import fdm as F
 
     spec = F.FdmSpec()
@@ -164,7 +164,7 @@ def fdm_leg(envs: int, steps: int, cpu: bool, cpu_threads: int) -> dict:
     inf = f.info
     inp = F.step_inputs(plan, 8, SEED, 0)
     rep = lambda a: np.ascontiguousarray(np.concatenate([a] * (envs // a.shape[0] + 1))[:envs])
-    dev = [torch.from_numpy(x).cuda() for x in (cell_major(rep(inp["input_q"])), rep(inp["ambient"]), rep(inp["h"]),
+    dev = [torch.from_numpy(x).cuda() for x in (rep(inp["input_q"]), rep(inp["ambient"]), rep(inp["h"]),
                                                   rep(inp["air_g"]), rep(inp["air_T"]))]
     f.step(*dev)
     torch.cuda.synchronize()

@@ -426,11 +426,11 @@ typedef struct {
 SbxFdm* sbx_fdm_open(const char* blob_path, int n_envs, int envs_per_block, int flags);
 void sbx_fdm_close(SbxFdm* f);
 int sbx_fdm_info(const SbxFdm* f, SbxFdmInfo* out);
-/* One step of every env on `stream` (asynchronous). Device arrays: input_q
- * [n_cvs][G] (heat per cell, the G envs of one cell adjacent), ambient and h
- * [G] (ambient temperature, convection coefficient), air_g and air_T [G][k]
- * (air-side conductance and supply temperature per coupled column; an env
- * whose k conductances are all 0 has no air side this step). */
+/* One step of every env on `stream` (asynchronous). Device arrays, env-major
+ * like the reference's per-env arguments: input_q [G][n_cvs] (heat per cell),
+ * ambient and h [G] (ambient temperature, convection coefficient), air_g and
+ * air_T [G][k] (air-side conductance and supply temperature per coupled
+ * column; an env whose k conductances are all 0 has no air side this step). */
 int sbx_fdm_step(SbxFdm* f, const double* input_q, const double* ambient, const double* h, const double* air_g,
                  const double* air_T, void* stream);
 /* Every env back to the blob's initial fields. */

@@ -435,6 +435,11 @@ bool build(SbxFdm* f, const char* path, int G, int epb, int flags) {
     T.n_unsolved = n_unsolved;
     auto put = [&](const void** dst, size_t off) { fix.push_back({dst, off}); };
     put((const void**)&T.ir, A.vec(ir));
+    {
+        std::vector<int> ipr(n);
+        for (int i = 0; i < n; i++) ipr[ir[i]] = i;
+        put((const void**)&T.ipr, A.vec(ipr));
+    }
     put((const void**)&T.pc, A.vec(pcv));
     put((const void**)&T.solved, A.vec(sol));
     put((const void**)&T.unsolved, A.vec(unsolved));

@@ -79,8 +79,9 @@ struct Sweep {
 
 struct Tables {
     int n, n_cvs, k, n_unsolved;
-    const int* ir;          // [n] row of the permuted vector -> solved index t
-    const int* pc;          // [n] solved index t -> row of the permuted vector
+    const int* ir;          // [n] row of the permuted vector -> solved index t of its right-hand side
+    const int* ipr;         // [n] solved index t -> that row (the inverse of ir)
+    const int* pc;          // [n] solved index t -> row of the permuted solution
     const int* solved;      // [n] t -> cell p
     const int* unsolved;    // [n_unsolved] cells held at the ambient temperature
     const double *cap, *dir, *mcoup, *mret, *mgain;   // [n] by t
@@ -112,8 +113,8 @@ struct Group {
     int* bact;              // [nblk] some env of the block has
 };
 
-// One batched step's inputs (device): input_q [n_cvs][G] (the G envs' heat of
-// one cell adjacent), ambient / h [G], air_g / air_T [G][k].
+// One batched step's inputs (device): input_q [G][n_cvs], ambient / h [G],
+// air_g / air_T [G][k].
 struct StepIn {
     const double* q;
     const double* amb;

@@ -293,19 +293,20 @@ __device__ __forceinline__ double sensed_dot(const int* wrow, const double* x, i
     return acc;
 }
 
-// Forcing (sb_fdm.c:147-151, exposure :126-140) written to the permuted row
-// i = the row of solved cell ir[i]; clears the blocks' air-side flags.
+// Forcing (sb_fdm.c:147-151, exposure :126-140) of every solved cell t, in
+// the cells' order (the field, the heat input and the mass read in order),
+// written to its row ipr[t] of the permuted vector; clears the blocks'
+// air-side flags.
 __global__ void forcing_kernel(sbf::Tables t, sbf::Group g, sbf::StepIn in) {
     const int n = t.n, Gl = g.Gl, G = g.G;
     const size_t total = (size_t)g.nblk * n * Gl;
     for (size_t x = gtid(); x < total; x += gstride()) {
         const int l = (int)(x % Gl);
-        const size_t bi = x / Gl;
-        const int i = (int)(bi % n), b = (int)(bi / n);
+        const size_t bt = x / Gl;
+        const int tt = (int)(bt % n), b = (int)(bt / n);
         const int env = b * Gl + l;
         double w = 0.0;
         if (env < G) {
-            const int tt = t.ir[i];
             const int p = t.solved[tt];
             const double h = in.h[env];
             double e = 0.0;
@@ -313,10 +314,10 @@ __global__ void forcing_kernel(sbf::Tables t, sbf::Group g, sbf::StepIn in) {
             if (a0 > 0.0) e += h * a0 / (1.0 + h * 0.5 * t.hz[tt] / t.cd[tt]);
             const double a1 = t.a1[tt];
             if (a1 > 0.0) e += h * a1 / (1.0 + h * 0.5 * t.vt[tt] / t.cd[tt]);
-            w = t.cap[tt] * g.T[((size_t)b * t.n_cvs + p) * Gl + l] + in.q[(size_t)p * G + env]
-                + in.amb[env] * (t.dir[tt] + e) + t.mcoup[tt] * g.M[((size_t)b * n + tt) * Gl + l];
+            w = t.cap[tt] * g.T[((size_t)b * t.n_cvs + p) * Gl + l] + in.q[(size_t)env * t.n_cvs + p]
+                + in.amb[env] * (t.dir[tt] + e) + t.mcoup[tt] * g.M[x];
         }
-        g.W1[x] = w;
+        g.W1[((size_t)b * n + t.ipr[tt]) * Gl + l] = w;
     }
     if (gtid() < (size_t)g.nblk) g.bact[gtid()] = 0;
 }

@@ -8,9 +8,8 @@ stays on the device between steps.
     f.step(input_q, ambient, h, air_g, air_T)   # torch float64 cuda tensors
     temp, mass = f.state()                        # host copies, env-major
 
-input_q is (n_cvs, G) (the G envs of one cell adjacent; a (G, n_cvs) host array
-can be passed through `cell_major`), ambient and h are (G,), air_g and air_T
-are (G, k).
+input_q is (G, n_cvs), ambient and h are (G,), air_g and air_T are (G, k)
+(env-major, as the reference's per-env arguments).
 """
 from __future__ import annotations
 
@@ -65,11 +64,6 @@ def _ptr(a: np.ndarray):
     return a.ctypes.data_as(P)
 
 
-def cell_major(a: np.ndarray) -> np.ndarray:
-    """(G, n_cvs) env-major heat rows -> the (n_cvs, G) layout sbx_fdm_step reads."""
-    return np.ascontiguousarray(np.asarray(a, np.float64).T)
-
-
 class FieldGroup:
     def __init__(self, blob: str | Path, n_envs: int, envs_per_block: int = 0, exact: bool = False):
         import torch
@@ -105,7 +99,7 @@ class FieldGroup:
         import torch
 
         G, k = self.G, self.k
-        args = [(input_q, (self.n_cvs, G)), (ambient, (G,)), (h, (G,)), (air_g, (G, k)), (air_T, (G, k))]
+        args = [(input_q, (G, self.n_cvs)), (ambient, (G,)), (h, (G,)), (air_g, (G, k)), (air_T, (G, k))]
         for t, shape in args:
             if not (isinstance(t, torch.Tensor) and t.is_cuda and t.dtype == torch.float64 and t.is_contiguous()
                     and tuple(t.shape) == shape):

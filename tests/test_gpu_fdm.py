@@ -29,7 +29,6 @@ import numpy as np
 import pytest
 
 import pyoracle as po
-from neurips2026_smart_building_challenge_amd.fdm import cell_major
 from neurips2026_smart_building_challenge_amd.scenario import fdm as F
 from neurips2026_smart_building_challenge_amd.scenario.sbb import read_sbb
 
@@ -86,7 +85,7 @@ def device_inputs(inp: dict):
     import torch
 
     d = "cuda:0"
-    return (torch.from_numpy(cell_major(inp["input_q"])).to(d), torch.from_numpy(inp["ambient"]).to(d),
+    return (torch.from_numpy(np.ascontiguousarray(inp["input_q"])).to(d), torch.from_numpy(inp["ambient"]).to(d),
             torch.from_numpy(inp["h"]).to(d), torch.from_numpy(np.ascontiguousarray(inp["air_g"])).to(d),
             torch.from_numpy(np.ascontiguousarray(inp["air_T"])).to(d))
 
