@@ -1845,27 +1845,52 @@ __device__ __forceinline__ void relax_solve(Ctx& c, double ambient, double irr, 
     if (pts) pts[0] = clock64();
     double bv[SBK_RX_RPL], iv[SBK_RX_RPL], xv[SBK_RX_RPL];
     double xabs = 0.0;
+    // the forcing of this lane's rows: every LDS read issued before the first
+    // use, then selects (rows past n read node 0 and rows without an air
+    // column read column 0; both are dropped by the selects)
+    const uint8_t* isroom = c.t.is_room();
+    const double *solar = c.t.solar_c(), *cap = c.t.cap(), *mcoup = c.t.mcoup(), *rxd = c.t.rx_diag();
+    const int* rxa = c.t.rx_air();
+    int fcol[SBK_RX_RPL];
+    uint8_t fr[SBK_RX_RPL];
+    double fs[SBK_RX_RPL], fo[SBK_RX_RPL], fc[SBK_RX_RPL], ft[SBK_RX_RPL], fd[SBK_RX_RPL], fm[SBK_RX_RPL],
+        fM[SBK_RX_RPL], fdi[SBK_RX_RPL];
 #pragma unroll
     for (int j = 0; j < SBK_RX_RPL; j++) {
-        const int t = lane + 64 * j;
-        bv[j] = 0.0;
-        iv[j] = 0.0;
-        xv[j] = 0.0;
-        if (t < n) {
-            const double qin = c.t.is_room()[t] ? c.slots[t] + c.t.solar_c()[t] * irr : c.t.solar_c()[t] * irr;
-            double b = c.t.cap()[t] * c.T[t] + qin + ambient * c.dirx[t] + c.t.mcoup()[t] * c.M[t];
-            double d = c.t.rx_diag()[t];
-            const int col = c.t.rx_air()[t];
-            if (col >= 0) {
-                const double g = c.g[col];
-                b += g * c.tair[col];
-                d += g;
-            }
-            bv[j] = b;
-            iv[j] = recip(d);
-            xv[j] = c.T[t];
-            xabs = fmax(xabs, fabs(xv[j]));
-        }
+        const int t = lane + 64 * j < n ? lane + 64 * j : 0;
+        fr[j] = isroom[t];
+        fs[j] = c.slots[t];
+        fo[j] = solar[t];
+        fc[j] = cap[t];
+        ft[j] = c.T[t];
+        fd[j] = c.dirx[t];
+        fm[j] = mcoup[t];
+        fM[j] = c.M[t];
+        fdi[j] = rxd[t];
+        fcol[j] = rxa[t];
+    }
+    double fg[SBK_RX_RPL], fa[SBK_RX_RPL];
+#pragma unroll
+    for (int j = 0; j < SBK_RX_RPL; j++) {
+        const int col = fcol[j] >= 0 ? fcol[j] : 0;
+        fg[j] = c.g[col];
+        fa[j] = c.tair[col];
+    }
+#pragma unroll
+    for (int j = 0; j < SBK_RX_RPL; j++) {
+        const bool ok = lane + 64 * j < n;
+        const double qr = fs[j] + fo[j] * irr, qo = fo[j] * irr;
+        const double qin = fr[j] ? qr : qo;
+        double b = fc[j] * ft[j] + qin + ambient * fd[j] + fm[j] * fM[j];
+        double d = fdi[j];
+        const bool ha = fcol[j] >= 0;
+        const double bg = b + fg[j] * fa[j], dg = d + fg[j];
+        b = ha ? bg : b;
+        d = ha ? dg : d;
+        bv[j] = ok ? b : 0.0;
+        iv[j] = ok ? recip(d) : 0.0;
+        xv[j] = ok ? ft[j] : 0.0;
+        xabs = fmax(xabs, fabs(xv[j]));
     }
     const double atol = SBK_RX_TOL * wave_max(xabs);
     const int nt = L->rx_terms;
@@ -1950,10 +1975,71 @@ __device__ __forceinline__ void relax_block_solve(Ctx& c, double ambient, double
     const int nb = L->bx_nb;
     const double2* bxd = reinterpret_cast<const double2*>(c.imgb + L->img.bx_d);
     const int4* bxi = reinterpret_cast<const int4*>(c.imgb + L->img.bx_i);
-    int row[Q][BXR], air[Q][BXR], col[Q][BXT], trow[Q][BXT];
-    double dia[Q][BXR], inm[Q][BXR][BXR], val[Q][BXT];
+    int row[Q][BXR], col[Q][BXT];
+    int dst[Q][BXR];
+    double xv[Q][BXR], c0[Q][BXR], cf[Q][BXR][BXT];
+    double xabs = 0.0;
+    // the forcing b = cap T + q + amb dirx + mc M of every node into the slot
+    // region (which holds each room cell's zone heat), node-major: lane l
+    // takes nodes l + 64 j, three per round with every read of a round
+    // issued before the first use (n <= 192 Q: every node sits in one of at
+    // most 64 Q blocks of at most three)
+    {
+        const int n = L->n;
+        const uint8_t* isroom = c.t.is_room();
+        const double *solar = c.t.solar_c(), *cap = c.t.cap(), *mcoup = c.t.mcoup();
+        constexpr int NR = 3;
+#pragma unroll
+        for (int j0 = 0; j0 < BXR * Q; j0 += NR) {
+            if (64 * j0 >= n) break;
+            uint8_t fr[NR];
+            double fs[NR], fo[NR], fc[NR], ft[NR], fd[NR], fm[NR], fM[NR];
+#pragma unroll
+            for (int j = 0; j < NR; j++) {
+                const int t0 = lane + 64 * (j0 + j);
+                const int t = t0 < n ? t0 : 0;
+                fr[j] = isroom[t];
+                fs[j] = c.slots[t];
+                fo[j] = solar[t];
+                fc[j] = cap[t];
+                ft[j] = c.T[t];
+                fd[j] = c.dirx[t];
+                fm[j] = mcoup[t];
+                fM[j] = c.M[t];
+            }
+#pragma unroll
+            for (int j = 0; j < NR; j++) {
+                const int t0 = lane + 64 * (j0 + j);
+                const double qr = fs[j] + fo[j] * irr, qo = fo[j] * irr;
+                const double qin = fr[j] ? qr : qo;
+                const double bb = fc[j] * ft[j] + qin + ambient * fd[j] + fm[j] * fM[j];
+                if (t0 < n) c.slots[t0] = bb;
+            }
+        }
+        esync();
+        // the air side: b += g T_air at each column's node (every node has
+        // at most one column)
+        const int k = L->k;
+        const int* an = c.t.air_node();
+#pragma unroll
+        for (int c0i = 0; c0i < 2; c0i++) {
+            if (64 * c0i >= k) break;
+            const int cc0 = lane + 64 * c0i;
+            const int cc = cc0 < k ? cc0 : 0;
+            const int node = an[cc];
+            const double gv = c.g[cc], tv = c.tair[cc];
+            const double bb = c.slots[node];
+            const double bg = bb + gv * tv;
+            if (cc0 < k) c.slots[node] = bg;
+        }
+        esync();
+    }
+    // one slot at a time (its tables, then its rows' forcing, conductance and
+    // temperature, then its matrix)
 #pragma unroll
     for (int q = 0; q < Q; q++) {
+        int air[BXR], trow[BXT];
+        double dia[BXR], inm[BXR][BXR], val[BXT];
         const int blk = q * 64 + lane;
         const bool ok = blk < nb;
         const int bc = ok ? blk : nb - 1;
@@ -1976,51 +2062,48 @@ __device__ __forceinline__ void relax_block_solve(Ctx& c, double ambient, double
 #pragma unroll
         for (int p = 0; p < BXR; p++) {
             row[q][p] = ok ? (ri[p] << 16) >> 16 : -1;
-            air[q][p] = ok ? ri[p] >> 16 : -1;
-            dia[q][p] = ok ? rd[p] : 1.0;
-            inm[q][p][p] = 0.0;
+            air[p] = ok ? ri[p] >> 16 : -1;
+            dia[p] = ok ? rd[p] : 1.0;
+            inm[p][p] = 0.0;
         }
-        inm[q][0][1] = ok ? rd[3] : 0.0;
-        inm[q][0][2] = ok ? rd[4] : 0.0;
-        inm[q][1][0] = ok ? rd[5] : 0.0;
-        inm[q][1][2] = ok ? rd[6] : 0.0;
-        inm[q][2][0] = ok ? rd[7] : 0.0;
-        inm[q][2][1] = ok ? rd[8] : 0.0;
+        inm[0][1] = ok ? rd[3] : 0.0;
+        inm[0][2] = ok ? rd[4] : 0.0;
+        inm[1][0] = ok ? rd[5] : 0.0;
+        inm[1][2] = ok ? rd[6] : 0.0;
+        inm[2][0] = ok ? rd[7] : 0.0;
+        inm[2][1] = ok ? rd[8] : 0.0;
 #pragma unroll
         for (int t = 0; t < BXT; t++) {
-            val[q][t] = ok ? rd[9 + t] : 0.0;
+            val[t] = ok ? rd[9 + t] : 0.0;
             col[q][t] = ok ? ri[4 + t] & 0xffff : 0;
-            trow[q][t] = ok ? ri[4 + t] >> 16 : 0;
+            trow[t] = ok ? ri[4 + t] >> 16 : 0;
         }
-    }
-    int dst[Q][BXR];
-    double xv[Q][BXR], c0[Q][BXR], cf[Q][BXR][BXT];
-    double xabs = 0.0;
+        // padding rows read node 0 and rows without an air column column 0;
+        // the selects drop both
+        double fb[BXR], fg[BXR], ft[BXR];
 #pragma unroll
-    for (int q = 0; q < Q; q++) {
+        for (int p = 0; p < BXR; p++) {
+            const int tc = row[q][p] >= 0 ? row[q][p] : 0;
+            const int ac = air[p] >= 0 ? air[p] : 0;
+            fb[p] = c.slots[tc];
+            fg[p] = c.g[ac];
+            ft[p] = c.T[tc];
+        }
         double m[BXR][BXR], bi[BXR][BXR], b[BXR];
 #pragma unroll
         for (int p = 0; p < BXR; p++) {
             const int t = row[q][p];
-            const int tc = t >= 0 ? t : 0;
-            double d = dia[q][p];
-            const double qin = c.t.is_room()[tc] ? c.slots[tc] + c.t.solar_c()[tc] * irr : c.t.solar_c()[tc] * irr;
-            double bb = c.t.cap()[tc] * c.T[tc] + qin + ambient * c.dirx[tc] + c.t.mcoup()[tc] * c.M[tc];
-            const int ac = air[q][p];
-            if (ac >= 0) {
-                const double g = c.g[ac];
-                bb += g * c.tair[ac];
-                d += g;
-            }
+            const double dg = dia[p] + fg[p];
+            const double d = air[p] >= 0 ? dg : dia[p];
 #pragma unroll
             for (int p2 = 0; p2 < BXR; p2++) {
-                m[p][p2] = p2 == p ? d : inm[q][p][p2];
+                m[p][p2] = p2 == p ? d : inm[p][p2];
                 bi[p][p2] = p2 == p ? 1.0 : 0.0;
             }
             dst[q][p] = t >= 0 ? t : sink;
-            b[p] = t >= 0 ? bb : 0.0;
-            xv[q][p] = t >= 0 ? c.T[tc] : 0.0;
-            if (t >= 0) xabs = fmax(xabs, fabs(xv[q][p]));
+            b[p] = t >= 0 ? fb[p] : 0.0;
+            xv[q][p] = t >= 0 ? ft[p] : 0.0;
+            xabs = fmax(xabs, fabs(xv[q][p]));
         }
 #pragma unroll
         for (int k = 0; k < BXR; k++) {
@@ -2053,10 +2136,10 @@ __device__ __forceinline__ void relax_block_solve(Ctx& c, double ambient, double
         // exec-mask branches)
 #pragma unroll
         for (int t = 0; t < BXT; t++) {
-            const int r = trow[q][t];
+            const int r = trow[t];
             double vr[BXR];
 #pragma unroll
-            for (int p2 = 0; p2 < BXR; p2++) vr[p2] = r == p2 ? val[q][t] : 0.0;
+            for (int p2 = 0; p2 < BXR; p2++) vr[p2] = r == p2 ? val[t] : 0.0;
 #pragma unroll
             for (int p = 0; p < BXR; p++) {
                 double acc = bi[p][0] * vr[0];
