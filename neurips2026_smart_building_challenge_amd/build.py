@@ -30,9 +30,9 @@ HIP_FLAGS = [
 ]
 
 
-# the field step is bit-exact to the reference core only with products rounded
-# before they are added
-EXTRA = {"fdm_kernel.hip": ["-ffp-contract=off"]}
+# the field step and the field envs' HVAC lanes are bit-exact to the reference
+# core only with products rounded before they are added
+EXTRA = {"fdm_kernel.hip": ["-ffp-contract=off"], "field_env_kernel.hip": ["-ffp-contract=off"]}
 
 
 def _run(cmd: list[str], cwd: Path | None = None) -> None:
@@ -48,12 +48,12 @@ def build_product() -> Path:
     tmp = PKG / "_build"
     tmp.mkdir(exist_ok=True)
     inc = ["-I", str(ROOT / "include"), "-I", str(CSRC)]
-    for src in ["step_kernel.hip", "policy_kernel.hip", "canon_kernel.hip", "fdm_kernel.hip"]:
+    for src in ["step_kernel.hip", "policy_kernel.hip", "canon_kernel.hip", "fdm_kernel.hip", "field_env_kernel.hip"]:
         o = tmp / (Path(src).stem + ".o")
         _run([hipcc, *HIP_FLAGS, *EXTRA.get(src, []), *inc, "-c", str(CSRC / src), "-o", str(o)])
         objs.append(o)
     rocm = Path(hipcc).resolve().parent.parent
-    for src in ["vec.cpp", "plan.cpp", "sbb_reader.cpp", "fdm.cpp"]:
+    for src in ["vec.cpp", "plan.cpp", "sbb_reader.cpp", "fdm.cpp", "field_env.cpp"]:
         # host-only C++ (HIP runtime API calls, no device code)
         o = tmp / (Path(src).stem + ".o")
         _run(["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__",

@@ -11,27 +11,16 @@
 #include <vector>
 
 #include "fdm.h"
+#include "fdm_host.h"
 #include "sbb_reader.h"
 #include "sbenv.h"
 
-extern "C" int sbf_launch_step(const sbf::Tables* t, const sbf::Group* g, const sbf::StepIn* in, hipStream_t s);
-extern "C" int sbf_launch_init(const sbf::Tables* t, const sbf::Group* g, const double* temp_init,
-                               const double* mass_init, hipStream_t s);
 extern "C" int sbf_run_lds_limit(int bytes);
 extern "C" int sbf_launch_solve_cols(const sbf::Tables* t, const sbf::Group* g, const double* b, double* x,
                                      double* S, hipStream_t s);
 
 void sbx_set_error(const std::string& msg);
 
-struct SbxFdm {
-    sbf::Tables tab{};
-    sbf::Group grp{};
-    SbxFdmInfo info{};
-    unsigned char* d_tables = nullptr;
-    double* d_temp_init = nullptr;
-    double* d_mass_init = nullptr;
-    std::vector<void*> owned;     // device buffers of the group
-};
 
 namespace {
 
@@ -405,6 +394,35 @@ bool build(SbxFdm* f, const char* path, int G, int epb, int flags) {
         vtt[t] = vt[p];
         cdt[t] = cd[p];
     }
+    // zones (env scenarios): the zone whose heat each solved cell carries
+    std::vector<int> czone;
+    int nz = 0;
+    {
+        uint64_t nzc = 0, nro = 0, nrc = 0;
+        const double* za = b.f64("zone_area", &nzc);
+        const int32_t* phys = b.i32("phys_room_idx");
+        const int32_t* ro = b.i32("room_offsets", &nro);
+        const int32_t* rc = b.i32("room_cells", &nrc);
+        if (za && phys && ro && rc && nro >= 1) {
+            nz = (int)nzc;
+            std::vector<int> tof(n_cvs, -1);
+            for (int t = 0; t < n; t++) tof[solved[t]] = t;
+            czone.assign(n, -1);
+            const int nrooms = (int)nro - 1;
+            for (int z = 0; z < nz; z++) {
+                const int rm = phys[z];
+                if (rm < 0 || rm >= nrooms || ro[rm] < 0 || ro[rm + 1] < ro[rm] || 2 * (uint64_t)ro[rm + 1] > nrc)
+                    return fail("zone rooms out of range");
+                for (int q = ro[rm]; q < ro[rm + 1]; q++) {
+                    const long long cell = (long long)rc[2 * q] * grid[1] + rc[2 * q + 1];
+                    if (rc[2 * q] < 0 || rc[2 * q] >= grid[0] || rc[2 * q + 1] < 0 || rc[2 * q + 1] >= grid[1]
+                        || tof[cell] < 0)
+                        return fail("room cell outside the solved field");
+                    czone[tof[cell]] = z;
+                }
+            }
+        }
+    }
     // sensed rows over the permuted solution; applied columns transposed per
     // permuted row, ascending column (sb_fdm.c:173-176 scatters them in that order)
     std::vector<int> snw(std::max<uint64_t>(nnzS, 1), 0);
@@ -453,6 +471,9 @@ bool build(SbxFdm* f, const char* path, int G, int epb, int flags) {
     put((const void**)&T.hz, A.vec(hzt));
     put((const void**)&T.vt, A.vec(vtt));
     put((const void**)&T.cd, A.vec(cdt));
+    T.nz = nz;
+    T.czone = nullptr;
+    if (nz > 0) put((const void**)&T.czone, A.vec(czone));
     auto put_tri = [&](sbf::Tri* d, const TriHost& h) {
         d->nlev = h.nlev;
         put((const void**)&d->lev, A.vec(h.lev));
@@ -612,7 +633,7 @@ int sbx_fdm_step(SbxFdm* f, const double* input_q, const double* ambient, const 
         sbx_set_error("sbx_fdm_step: null argument");
         return -1;
     }
-    sbf::StepIn in{input_q, ambient, h, air_g, air_T};
+    sbf::StepIn in{input_q, ambient, h, air_g, air_T, nullptr};
     const int e = sbf_launch_step(&f->tab, &f->grp, &in, (hipStream_t)stream);
     if (e) {
         sbx_set_error(std::string("sbx_fdm_step: ") + hipGetErrorString((hipError_t)e));

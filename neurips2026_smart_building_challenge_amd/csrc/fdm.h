@@ -99,6 +99,11 @@ struct Tables {
     const int* at_j;
     const double* at_x;
     const double* S;        // [k][k] sensed A^-1 applied
+    // blobs with zones (full env scenarios): the zone whose heat each solved
+    // cell t carries, or -1 (a zone's heat goes to its room's cells; a cell of
+    // two zones' rooms takes the later zone's, as csim assigns input_q)
+    const int* czone;       // [n] or null
+    int nz;
 };
 
 struct Group {
@@ -114,13 +119,15 @@ struct Group {
 };
 
 // One batched step's inputs (device): input_q [G][n_cvs], ambient / h [G],
-// air_g / air_T [G][k].
+// air_g / air_T [G][k]. With q null, each cell's input_q is its zone's heat
+// per cell qz [G][nz] (Tables::czone; 0 outside the rooms).
 struct StepIn {
     const double* q;
     const double* amb;
     const double* h;
     const double* g;
     const double* airT;
+    const double* qz;
 };
 
 }  // namespace sbf

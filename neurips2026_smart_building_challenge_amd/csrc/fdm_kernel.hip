@@ -314,8 +314,15 @@ __global__ void forcing_kernel(sbf::Tables t, sbf::Group g, sbf::StepIn in) {
             if (a0 > 0.0) e += h * a0 / (1.0 + h * 0.5 * t.hz[tt] / t.cd[tt]);
             const double a1 = t.a1[tt];
             if (a1 > 0.0) e += h * a1 / (1.0 + h * 0.5 * t.vt[tt] / t.cd[tt]);
-            w = t.cap[tt] * g.T[((size_t)b * t.n_cvs + p) * Gl + l] + in.q[(size_t)env * t.n_cvs + p]
-                + in.amb[env] * (t.dir[tt] + e) + t.mcoup[tt] * g.M[x];
+            double q;
+            if (in.q) {
+                q = in.q[(size_t)env * t.n_cvs + p];
+            } else {
+                const int z = t.czone[tt];
+                q = z >= 0 ? in.qz[(size_t)env * t.nz + z] : 0.0;
+            }
+            w = t.cap[tt] * g.T[((size_t)b * t.n_cvs + p) * Gl + l] + q + in.amb[env] * (t.dir[tt] + e)
+                + t.mcoup[tt] * g.M[x];
         }
         g.W1[((size_t)b * n + t.ipr[tt]) * Gl + l] = w;
     }

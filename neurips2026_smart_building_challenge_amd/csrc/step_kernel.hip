@@ -2105,23 +2105,25 @@ __device__ __forceinline__ void relax_block_solve(Ctx& c, double ambient, double
             xv[q][p] = t >= 0 ? ft[p] : 0.0;
             xabs = fmax(xabs, fabs(xv[q][p]));
         }
-#pragma unroll
-        for (int k = 0; k < BXR; k++) {
-            const double rp = recip(m[k][k]);
-#pragma unroll
-            for (int j = 0; j < BXR; j++) {
-                m[k][j] *= rp;
-                bi[k][j] *= rp;
-            }
+        {
+            // the inverse as adjugate / determinant (one reciprocal; the block
+            // is an M-matrix, so the determinant is positive and the cofactor
+            // differences do not cancel badly)
+            double adj[BXR][BXR];
 #pragma unroll
             for (int i = 0; i < BXR; i++) {
-                if (i == k) continue;
-                const double f = m[i][k];
 #pragma unroll
                 for (int j = 0; j < BXR; j++) {
-                    m[i][j] -= f * m[k][j];
-                    bi[i][j] -= f * bi[k][j];
+                    const int r0 = (j + 1) % 3, r1 = (j + 2) % 3, c0i = (i + 1) % 3, c1i = (i + 2) % 3;
+                    adj[i][j] = m[r0][c0i] * m[r1][c1i] - m[r0][c1i] * m[r1][c0i];
                 }
+            }
+            const double det = m[0][0] * adj[0][0] + m[0][1] * adj[1][0] + m[0][2] * adj[2][0];
+            const double rd = recip(det);
+#pragma unroll
+            for (int i = 0; i < BXR; i++) {
+#pragma unroll
+                for (int j = 0; j < BXR; j++) bi[i][j] = adj[i][j] * rd;
             }
         }
 #pragma unroll
@@ -2840,6 +2842,7 @@ __global__ __launch_bounds__(256) void live_sums_kernel(const EnvDesc* envs, con
     for (int i = t; i < n; i += 256) {
         const EnvDesc& d = envs[i];
         const DevLayout* L = layouts + d.layout;
+        if (L->st.bytes == 0) continue;   // a field scenario's env (its totals are added after)
         const unsigned char* r = state + d.state_off;
         rs += reinterpret_cast<const double*>(r + L->st.plant)[PF_REW_SUM];
         const int* ip = reinterpret_cast<const int*>(r + L->st.iplant);

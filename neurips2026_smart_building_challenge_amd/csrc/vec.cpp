@@ -22,6 +22,7 @@
 #include <vector>
 
 #include "canon.h"
+#include "field_host.h"
 #include "plan.h"
 #include "sbb_reader.h"
 #include "sbenv.h"
@@ -105,6 +106,7 @@ struct HostLayout {
     sbk::DevLayout dev{};   // sizes + layouts; pointers patched after upload
     std::map<std::string, size_t> off;
     std::unique_ptr<sbk::CanonTab> canon;   // canonical maps (canonical mode only)
+    int field = -1;         // a field scenario's stand-in (counts only; its envs are not tiled)
 };
 
 struct HostScen {
@@ -118,6 +120,7 @@ struct HostScen {
     int64_t conv_seed = 0;
     int hour_m1_rows = 0;
     int n_cont = 0, n_disc = 0;
+    int field = -1;         // index into Vec::fields (FDM-scale scenario)
 };
 
 const char* kStructural[] = {
@@ -1091,6 +1094,11 @@ struct Vec {
     float* d_ctrust = nullptr;                   // [n][SB_ACT] guard trust per native action
     double* d_cpid = nullptr;                    // [n][2 * SBC_K] PID state
     float* d_cinfo = nullptr;                    // [n][2 * SBC_K] effort, mean zone temperature per AHU
+    // field scenarios (FDM-scale fields): one per scenario, its envs as slots
+    std::vector<FieldScen*> fields;
+    std::vector<std::vector<sbe::Slot>> field_slots;
+    std::vector<int> field_of;                   // [n] field scenario of env i, or -1
+    std::vector<int> slot_of;                    // [n] its slot there
 };
 
 constexpr int kTimerPairs = 16384;
@@ -1169,6 +1177,12 @@ void run_env(Vec* v, sbk::KParams p, const float* actions) {
     }
     launch_params(v, p);
     if (v->canonical) launch_canon(v, 1, reset ? 1 : 0, nullptr);
+    if (!v->fields.empty()) {
+        FieldIo io{p.actions, p.obs, p.rewards, p.terminals, p.host_env, p.env_stride, p.log_offset, p.reward_scale};
+        std::string err;
+        for (FieldScen* f : v->fields)
+            if (!field_step(f, io, reset, g_stream, &err)) die("field scenario step: " + err);
+    }
 }
 
 void launch(Vec* v, int mode) { run_env(v, params(v, mode), nullptr); }
@@ -1345,6 +1359,35 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
         sbh::Blob b;
         std::string err;
         if (!b.open(files[i], &err)) die(err);
+        if (field_blob(b)) {
+            // FDM-scale field: HVAC lanes around the field group's solve
+            if (v->canonical) die(files[i] + ": the canonical interface is not supported for field scenarios");
+            FieldScen* F = field_open(b, &err);
+            if (!F) die(files[i] + ": " + err);
+            const FieldCounts fc = field_counts(F);
+            HostLayout H;
+            H.key = "field:" + files[i];
+            H.field = (int)v->fields.size();
+            H.dev.n_act = fc.n_act;
+            H.dev.n_cont = fc.n_cont;
+            H.dev.n_disc = fc.n_disc;
+            H.dev.nz = fc.nz;
+            const int li = (int)v->layouts.size();
+            v->layouts.push_back(std::move(H));
+            HostScen S;
+            S.path = files[i];
+            S.layout = li;
+            S.field = (int)v->fields.size();
+            S.n1 = fc.n1;
+            S.episode_steps = fc.episode_steps;
+            S.occ_seed = fc.occ_seed;
+            S.hour_m1_rows = fc.hour_m1_rows;
+            S.dev.layout = li;
+            v->scens.push_back(std::move(S));
+            v->fields.push_back(F);
+            v->field_slots.emplace_back();
+            continue;
+        }
         std::string key = structural_key(b);
         int li;
         auto it = layout_of_key.find(key);
@@ -1417,6 +1460,15 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
             if (start + ms > S.n1 - 1) die(S.path + ": calendar tables shorter than the episode");
             if (start >= S.hour_m1_rows) die(S.path + ": occ_hour_m1 has no row for the start offset");
             d.start = start;
+            if (S.field >= 0) {
+                v->field_of.push_back(S.field);
+                v->slot_of.push_back((int)v->field_slots[S.field].size());
+                v->field_slots[S.field].push_back(
+                    sbe::Slot{e, start, ms, d.first_steps, (uint32_t)(S.occ_seed + (per_env_seed ? j : 0)), {0, 0, 0}});
+            } else {
+                v->field_of.push_back(-1);
+                v->slot_of.push_back(-1);
+            }
             v->desc.push_back(d);
             v->seeds.push_back((uint32_t)(S.occ_seed + (per_env_seed ? j : 0)));
             v->conv_seeds.push_back((uint32_t)(S.conv_seed + (per_env_seed ? j : 0)));
@@ -1427,8 +1479,9 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
     v->state_bytes = state_off;
     // tiles: envs of one layout share a workgroup (two wavefronts each) and the
     // layout image it stages; largest layouts first, then by scenario
-    v->order.resize(n);
-    for (int i = 0; i < n; i++) v->order[i] = i;
+    for (int i = 0; i < n; i++)
+        if (v->field_of[i] < 0) v->order.push_back(i);
+    const int n_rc = (int)v->order.size();
     std::stable_sort(v->order.begin(), v->order.end(), [&](int a, int b) {
         const sbk::EnvDesc &da = v->desc[a], &db = v->desc[b];
         const int ka = kernel_variant(v->layouts[da.layout].dev), kb = kernel_variant(v->layouts[db.layout].dev);
@@ -1447,9 +1500,10 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
         int img = 0;
         for (auto& L : v->layouts) img = std::max(img, L.dev.img.bytes);
         const int limit = 160 * 1024;
-        std::vector<int> per(v->layouts.size());
+        std::vector<int> per(v->layouts.size(), 1);
         int epb = 1, lds = 0;
         for (size_t li = 0; li < v->layouts.size(); li++) {
+            if (v->layouts[li].field >= 0) continue;
             const int reg = v->layouts[li].dev.lds.bytes;
             if (img + reg > limit) die("layout needs more LDS than a workgroup has");
             per[li] = std::min(epb_kw, (limit - img) / reg);
@@ -1459,10 +1513,10 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
         v->epb = epb;
         v->img_lds = img;
         v->lds_bytes = lds;
-        for (int i = 0; i < n;) {
+        for (int i = 0; i < n_rc;) {
             const int lay = v->desc[v->order[i]].layout;
             int j = i;
-            while (j < n && j - i < per[lay] && v->desc[v->order[j]].layout == lay) j++;
+            while (j < n_rc && j - i < per[lay] && v->desc[v->order[j]].layout == lay) j++;
             v->tiles.push_back(sbk::Tile{lay, i, j - i, 0});
             const int kv = kernel_variant(v->layouts[lay].dev);
             if (v->groups.empty() || v->groups.back().variant != kv)
@@ -1513,8 +1567,8 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
     hip_ok(hipMemcpy(v->d_scens, ds.data(), sizeof(sbk::DevScen) * ds.size(), hipMemcpyHostToDevice), "upload");
     hip_ok(hipMalloc(&v->d_envs, sizeof(sbk::EnvDesc) * n), "hipMalloc(envs)");
     hip_ok(hipMemcpy(v->d_envs, v->desc.data(), sizeof(sbk::EnvDesc) * n, hipMemcpyHostToDevice), "upload");
-    hip_ok(hipMalloc(&v->d_order, sizeof(int) * n), "hipMalloc(order)");
-    hip_ok(hipMemcpy(v->d_order, v->order.data(), sizeof(int) * n, hipMemcpyHostToDevice), "upload");
+    hip_ok(hipMalloc(&v->d_order, sizeof(int) * std::max(n_rc, 1)), "hipMalloc(order)");
+    hip_ok(hipMemcpy(v->d_order, v->order.data(), sizeof(int) * n_rc, hipMemcpyHostToDevice), "upload");
     hip_ok(hipMalloc(&v->d_tiles, sizeof(sbk::Tile) * v->tiles.size()), "hipMalloc(tiles)");
     hip_ok(hipMemcpy(v->d_tiles, v->tiles.data(), sizeof(sbk::Tile) * v->tiles.size(), hipMemcpyHostToDevice),
            "upload");
@@ -1534,6 +1588,7 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
     {
         std::vector<unsigned char> rec(v->state_bytes, 0);
         for (int i = 0; i < n; i++) {
+            if (v->field_of[i] >= 0) continue;
             const sbk::EnvDesc& d = v->desc[i];
             const sbk::DevLayout& L = v->layouts[d.layout].dev;
             unsigned char* r = rec.data() + d.state_off;
@@ -1548,7 +1603,7 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
             v->record_bytes_per_step += L.record_bytes_per_step;
             v->flops_per_step += L.solve_flops;
         }
-        hip_ok(hipMalloc(&v->d_state, v->state_bytes), "hipMalloc(state)");
+        hip_ok(hipMalloc(&v->d_state, std::max<size_t>(v->state_bytes, 16)), "hipMalloc(state)");
         hip_ok(hipMemcpy(v->d_state, rec.data(), v->state_bytes, hipMemcpyHostToDevice), "upload state");
     }
     if (v->canonical) {
@@ -1594,6 +1649,23 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
         E.loaded = 1;
         E.index = i;
         E.vec = v.get();
+    }
+    // field scenarios: tables, field group, per-env records
+    {
+        const int fexact = (int)kw(kwargs, "field_exact", 0.0f) != 0;
+        const int fepb = (int)kw(kwargs, "field_envs_per_block", 0.0f);
+        if (fepb < 0) die("env.field_envs_per_block must be >= 0");
+        // (every scenario holds at least one env: G <= n)
+        for (size_t fi = 0; fi < v->fields.size(); fi++) {
+            std::string err, path;
+            for (auto& S : v->scens)
+                if (S.field == (int)fi) path = S.path;
+            if (!field_attach(v->fields[fi], path, v->field_slots[fi], fexact ? SBX_FDM_EXACT : 0, fepb, &err))
+                die(path + ": " + err);
+            v->bytes_per_step += field_bytes_per_step(v->fields[fi]);
+            v->record_bytes_per_step += field_bytes_per_step(v->fields[fi]);
+            v->flops_per_step += field_flops_per_step(v->fields[fi]);
+        }
     }
     hip_ok(hipDeviceSynchronize(), "sync after create");
     g_last = v.get();
@@ -1672,6 +1744,7 @@ void puf_close(Env* envs) {
     for (void* p : {(void*)v->d_canon, (void*)v->d_raw, (void*)v->d_native, (void*)v->d_cbase, (void*)v->d_ctrust,
                     (void*)v->d_cpid, (void*)v->d_cinfo})
         (void)hipFree(p);
+    for (FieldScen* f : v->fields) field_close(f);
     (void)hipHostFree(v->envs);
     if (g_last == v) g_last = nullptr;
     delete v;
@@ -1693,6 +1766,8 @@ void puf_live_log(Env* envs, Dict* out) {
     Vec* v = vec_of(envs);
     int rc = sbk_launch_live_sums(v->d_envs, v->d_layouts, v->d_state, v->n, v->d_live, g_stream);
     if (rc != 0) die("live log kernel launch failed");
+    for (FieldScen* f : v->fields)
+        if (!field_live(f, v->d_live, g_stream)) die("live log kernel launch failed (field scenario)");
     hip_ok(hipMemcpyAsync(v->h_live, v->d_live, 3 * sizeof(double), hipMemcpyDeviceToHost, g_stream), "live log");
     hip_ok(hipStreamSynchronize(g_stream), "live log");
     const double rs = v->h_live[0], st = v->h_live[1], eps = v->h_live[2];
@@ -1756,6 +1831,10 @@ void sbx_vec_info(Env* envs, SbxVecInfo* out) {
 int sbx_env_state(Env* envs, int i, double* out, int cap) {
     Vec* v = vec_of(envs);
     if (i < 0 || i >= v->n) return -1;
+    if (v->field_of[i] >= 0) {
+        hip_ok(hipStreamSynchronize(g_stream), "state sync");
+        return field_state(v->fields[v->field_of[i]], v->slot_of[i], out, cap);
+    }
     const sbk::EnvDesc& d = v->desc[i];
     const sbk::DevLayout& L = v->layouts[d.layout].dev;
     std::vector<unsigned char> r(L.st.bytes);
@@ -1841,7 +1920,7 @@ int sbx_phase_stamps(Env* envs, unsigned long long* out, int cap) {
 
 int sbx_pass_times(Env* envs, int env, long long* cycles, int cap) {
     Vec* v = vec_of(envs);
-    if (env < 0 || env >= v->n) return -1;
+    if (env < 0 || env >= v->n || v->field_of[env] >= 0) return -1;
     const bool relax = v->layouts[v->desc[env].layout].dev.solver == sbk::SOLVER_RELAX;
     // relaxation: a stamp at entry, after the setup and after every sweep
     const int np = relax ? SBK_RX_MAXIT + 1 : v->layouts[v->desc[env].layout].dev.n_pass;
@@ -2031,7 +2110,7 @@ int sbx_beta_sample(const float* alpha, const float* beta, float* out, int n, ui
 
 int sbx_solve_info(Env* envs, int i, double* out) {
     Vec* v = vec_of(envs);
-    if (i < 0 || i >= v->n || !out) return -1;
+    if (i < 0 || i >= v->n || !out || v->field_of[i] >= 0) return -1;
     const sbk::EnvDesc& d = v->desc[i];
     const HostLayout& H = v->layouts[d.layout];
     double pf[8];

@@ -324,11 +324,13 @@ class VecEnv:
             raise RuntimeError(self.L.sbx_last_error().decode())
 
     def state(self, i: int) -> np.ndarray:
-        buf = np.zeros(16384, np.float64)
-        m = self.L.sbx_env_state(self.envs, i, buf.ctypes.data_as(P), buf.size)
-        if m < 0:
-            raise RuntimeError("sbx_env_state failed")
-        return buf[:m].copy()
+        """Env i's state in the oracle's order (an FDM-scale field takes a larger buffer)."""
+        for cap in (16384, 1 << 22):
+            buf = np.zeros(cap, np.float64)
+            m = self.L.sbx_env_state(self.envs, i, buf.ctypes.data_as(P), buf.size)
+            if m >= 0:
+                return buf[:m].copy()
+        raise RuntimeError("sbx_env_state failed")
 
     def canon_state(self, i: int):
         """Canonical mode: env i's own observation row, base proposal per native action

@@ -252,11 +252,24 @@ def scenario_writer(spec: LayoutSpec, clim: ClimateSpec, table_steps: int,
         w.add("conv_room_cells", c_cells, "i32")
         w.add("conv_cand_offsets", c_coff, "i32")
         w.add("conv_cand_idx", c_idx, "i32")
-    # ---- zones / rooms / VAVs ----
-    w.add("zone_area", b.zone_area, "f64")
+    # ---- zones / rooms / VAVs: zone z is the air cell of column z ----
+    rooms = (np.arange(Z + 1), np.stack([np.zeros(Z, dtype=np.int64), np.arange(Z)], 1).reshape(-1))
+    hvac_sections(w, b, Z, clim, table_steps, occ_seed, b.zone_area, b.cv_size_cm, rooms, b.solar_coeff)
+    return w
+
+
+def hvac_sections(w: SbbWriter, b: Building, Z: int, clim: ClimateSpec, table_steps: int, occ_seed: int,
+                  zone_area: np.ndarray, cv_size_cm: float, rooms, solar_coeff) -> None:
+    """The sections past the field: zones (one VAV per zone, zone z in room
+    z), the rooms' cells when `rooms` = (offsets, cells) is given, the HVAC
+    plant of `b`, actions, observation, calendar and weather (with the solar
+    gain coefficients when given), occupancy and reward tables."""
+    n1 = table_steps + 1
+    w.add("zone_area", zone_area, "f64")
     w.add("phys_room_idx", np.arange(Z), "i32")
-    w.add("room_offsets", np.arange(Z + 1), "i32")
-    w.add("room_cells", np.stack([np.zeros(Z, dtype=np.int64), np.arange(Z)], 1).reshape(-1), "i32")
+    if rooms is not None:
+        w.add("room_offsets", rooms[0], "i32")
+        w.add("room_cells", rooms[1], "i32")
     w.add("vav_zone_offsets", np.arange(Z + 1), "i32")
     w.add("vav_zone_idx", np.arange(Z), "i32")
     w.add("zone_vav_offsets", np.arange(Z + 1), "i32")
@@ -272,7 +285,7 @@ def scenario_writer(spec: LayoutSpec, clim: ClimateSpec, table_steps: int,
     w.scalar_f64("internal_gain_w_per_m2", b.internal_w_m2)
     w.scalar_f64("internal_gain_standby_fraction", b.standby_frac)
     w.scalar_f64("occupant_sensible_heat_w", b.occupant_w)
-    w.scalar_f64("cv_size_cm", b.cv_size_cm)
+    w.scalar_f64("cv_size_cm", cv_size_cm)
     # ---- actions ----
     w.add("act_owner_kind", b.act_kind, "u8")
     w.add("act_owner_index", b.act_index, "i32")
@@ -302,7 +315,8 @@ def scenario_writer(spec: LayoutSpec, clim: ClimateSpec, table_steps: int,
     wt = weather_tables(clim, n1)
     w.add("weather_ambient", wt["weather_ambient"], "f64")
     w.add("solar_irradiance", wt["solar_irradiance"], "f64")
-    w.add("solar_gain_coeff", b.solar_coeff, "f64")
+    if solar_coeff is not None:
+        w.add("solar_gain_coeff", solar_coeff, "f64")
     for name in ("sched_comfort", "sched_heat_sp", "sched_cool_sp"):
         w.add(name, cal[name], "f64")
     w.add("occ_hour", cal["occ_hour"], "i64")
@@ -322,7 +336,6 @@ def scenario_writer(spec: LayoutSpec, clim: ClimateSpec, table_steps: int,
         w.add(name, p[name], "f64")
     w.scalar_f64("gas_carbon_rate", p["gas_carbon_rate"])
     w.scalar_i64("table_steps", table_steps)
-    return w
 
 
 # ---------------------------------------------------------------- configs ----
@@ -372,3 +385,47 @@ def write_scenarios(scen: list[tuple[LayoutSpec, ClimateSpec]], out_dir,
 def write_config(config: int, out_dir, conv: ConvSpec | None = None) -> tuple[list[Path], int, bool]:
     scen, n, offsets = config_scenarios(config)
     return write_scenarios(scen, out_dir, conv=conv), n, offsets
+
+
+# ------------------------------------------------------ FDM-scale buildings --
+
+@dataclass(frozen=True)
+class FieldEnvSpec:
+    """A building whose field is an FDM plan (scenario/fdm.py) and whose HVAC
+    plant serves one VAV per room: the zones are the plan's rooms, the plant
+    constants those of a seeded RC layout with as many zones and `ahus` AHUs."""
+    field: "object"           # fdm.FdmSpec
+    ahus: int = 3
+
+    @property
+    def seed(self) -> int:
+        return 5000 + 31 * self.field.rooms + self.ahus + 7 * self.field.seed
+
+    @property
+    def name(self) -> str:
+        return f"{self.field.name}_a{self.ahus}"
+
+
+def field_env_writer(spec: FieldEnvSpec, clim: ClimateSpec, table_steps: int, occ_seed: int) -> SbbWriter:
+    """One FDM-scale env scenario: the plan's field sections (fdm.fdm_writer,
+    with its rooms' cells and area-weighted air-side columns), convection
+    off, and hvac_sections with the rooms as zones (zone area = the room's
+    floor area, internal gains per cell of the plan's cell size). No solar
+    gain section: the reference core has no solar input."""
+    from .fdm import fdm_writer, make_plan
+
+    plan = make_plan(spec.field)
+    w = fdm_writer(plan)
+    Z = plan.k
+    b = make_building(Z, spec.ahus, spec.seed, name=spec.name)
+    w.scalar_f64("conv_p", 0.0)
+    w.scalar_f64("conv_distance", 0.0)
+    w.scalar_i64("conv_seed", 0)
+    w.add("conv_room_offsets", [0], "i32")
+    w.add("conv_room_cells", np.zeros(0), "i32")
+    w.add("conv_cand_offsets", [0], "i32")
+    w.add("conv_cand_idx", np.zeros(0), "i32")
+    cv = spec.field.cv_m
+    zone_area = np.array([c.size for c in plan.room_cells], np.float64) * cv * cv
+    hvac_sections(w, b, Z, clim, table_steps, occ_seed, zone_area, cv * 100.0, None, None)
+    return w

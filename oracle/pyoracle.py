@@ -130,6 +130,21 @@ def scenario(path) -> _Scen:
 _SEEDS: dict[str, tuple[int, int]] = {}
 
 
+_CAPS: dict[str, int] = {}
+
+
+def _state_cap(path) -> int:
+    """Doubles a state snapshot may hold: the field (every cell and the
+    solved cells' interior mass) plus at most 8192 of HVAC state."""
+    key = str(path)
+    if key not in _CAPS:
+        from neurips2026_smart_building_challenge_amd.scenario.sbb import read_sbb
+
+        b = read_sbb(path)
+        _CAPS[key] = int(np.prod(b["grid"])) + int(b["solved"].size) + 8192
+    return _CAPS[key]
+
+
 def default_conv_seed(path, occ_seed: int) -> int:
     """The convection stream seed of the env whose occupancy seed is occ_seed:
     the blob's conv_seed offset by the env's index within its scenario (the
@@ -173,7 +188,7 @@ class CpuEnv:
         self.obs = np.zeros(SB_OBS, np.float32)
         self._r = np.zeros(1, np.float32)
         self._t = np.zeros(1, np.float32)
-        self._st = np.zeros(8192, np.float64)
+        self._st = np.zeros(_state_cap(path), np.float64)
 
     def close(self):
         if self.h:
