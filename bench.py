@@ -14,7 +14,8 @@ K defaults to a full 8,640-step episode. Config 4 times the rollout: policy
 forward + Beta sampling, then puf_step, each step. Configs 0-3 are timed a
 second time with the per-env sparse LU as the field solver (the "lu" record).
 Config 1 also times the building-scale field step (the "fdm" record, see
-fdm_leg; --fdm-only runs just that).
+fdm_leg; --fdm-only runs just that) and whole env steps of FDM-scale
+scenarios through the same ABI (the "field_env" record, see field_env_leg).
 
 roofline: algorithmic HBM bytes of one puf_step (per env: the persistent state
 read and written -- T, per-VAV and per-AHU state, plant scalars, occupancy,
@@ -207,6 +208,70 @@ def fdm_leg(envs: int, steps: int, cpu: bool, cpu_threads: int) -> dict:
     return rec
 
 
+def field_env_leg(envs: int, steps: int, cpu: bool, cpu_threads: int) -> dict:
+    """Whole env steps (puf_step on pre-drawn resident action rows) of an
+    FDM-scale scenario: the field of building_train_1's size (606 x 339 cells,
+    39 rooms; fdm.FdmSpec()) with one VAV per room and 3 AHUs
+    (generate.field_env_writer), `envs` envs, `steps` timed steps after one
+    untimed step. cpu: the reference core's env (oracle/_ref; this repo's
+    restatement where that is not built) on `cpu_threads` threads, one env
+    each, 2 steps."""
+    import torch
+
+    from neurips2026_smart_building_challenge_amd import env as E
+    from neurips2026_smart_building_challenge_amd.scenario import fdm as F
+    from neurips2026_smart_building_challenge_amd.scenario import generate as G
+
+    spec = G.FieldEnvSpec(F.FdmSpec(), 3)
+    td = Path(tempfile.mkdtemp(prefix="sb_field_env_"))
+    path = td / f"{spec.name}.sbb"
+    path.write_bytes(G.field_env_writer(spec, G.climates()[2], G.EPISODE_STEPS + 256, 17321).tobytes())
+    vec = E.VecEnv(envs, blob=str(path))
+    info = vec.info()
+    vec.reset()
+    rows = torch.empty((steps + 1, envs, 272), dtype=torch.float32, device="cuda")
+    for s in range(steps + 1):
+        vec.gen_actions(SEED, s)
+        rows[s].copy_(vec.actions)
+    vec.step_actions(rows[0])
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for s in range(steps):
+        vec.step_actions(rows[s + 1])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    rec = {"workload": f"FDM-scale env scenario: {spec.field.rows} x {spec.field.cols} cells, {spec.field.rooms} rooms "
+                       f"(one VAV each), {spec.ahus} AHUs; {envs} envs through puf_step",
+           "n_envs": envs, "steps": steps, "ms_per_step": ms, "value": envs / (ms / 1e3), "unit": "env-steps/s",
+           "algorithmic_bytes": info.bytes_per_step, "achieved_gbs": info.bytes_per_step / (ms / 1e3) / 1e9}
+    vec.close()
+    log(f"field env step: {ms:.2f} ms/step at {envs} envs, {rec['value']:.4g} env-steps/s")
+    if cpu:
+        sys.path.insert(0, str(ROOT / "oracle"))
+        import pyoracle as po
+        from concurrent.futures import ThreadPoolExecutor
+
+        kind = "ref" if po.ref_available() else "oracle"
+        es = [po.CpuEnv(kind, path, 17321 + j) for j in range(cpu_threads)]
+        for e in es:
+            e.reset()
+        row = po.action_row(SEED, 0, 0, es[0].n_cont, es[0].n_disc)
+        t0 = time.time()
+        with ThreadPoolExecutor(cpu_threads) as ex:
+            list(ex.map(lambda e: [e.step(row) for _ in range(2)], es))
+        dt = time.time() - t0
+        rec["cpu_baseline"] = {"value": 2 * cpu_threads / dt, "unit": "env-steps/s", "cores": cpu_threads,
+                               "kind": "reference" if kind == "ref" else "port",
+                               "sample": f"{cpu_threads} envs x 2 steps, one env per thread"}
+        log(f"field env cpu baseline: {rec['cpu_baseline']['value']:.4g} env-steps/s on {cpu_threads} threads ({kind})")
+        for e in es:
+            e.close()
+    return rec
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -222,6 +287,9 @@ def main() -> int:
                     help="stochastic convection on with this swap probability (not a BASELINE config)")
     ap.add_argument("--fdm-envs", type=int, default=256, help="envs of the building-scale field-step record (0: skip)")
     ap.add_argument("--fdm-only", action="store_true", help="only the building-scale field-step record")
+    ap.add_argument("--field-env-envs", type=int, default=256,
+                    help="envs of the FDM-scale env-scenario record (0: skip)")
+    ap.add_argument("--field-env-only", action="store_true", help="only the FDM-scale env-scenario record")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of 256 MiB 10 times (counter calibration)")
     args = ap.parse_args()
@@ -240,6 +308,11 @@ def main() -> int:
     if args.fdm_only:
         visible = len(os.sched_getaffinity(0))
         print(json.dumps(fdm_leg(max(1, args.fdm_envs), 5, not args.no_cpu, min(16, visible))), flush=True)
+        return 0
+    if args.field_env_only:
+        visible = len(os.sched_getaffinity(0))
+        print(json.dumps(field_env_leg(max(1, args.field_env_envs), 5, not args.no_cpu, min(16, visible))),
+              flush=True)
         return 0
     scen, n_envs, offsets = G.config_scenarios(args.config)
     groups = len(scen)
@@ -363,9 +436,11 @@ def main() -> int:
         cpu["cores_visible"] = visible
         log(f"cpu baseline: {cpu['value']:.4g} env-steps/s ({cpu['kind']})")
 
-    fdm = None
+    fdm = field_env = None
     if args.fdm_envs > 0 and args.config == 1 and args.conv <= 0:
         fdm = fdm_leg(args.fdm_envs, 5, not args.no_cpu, min(16, len(os.sched_getaffinity(0))))
+    if args.field_env_envs > 0 and args.config == 1 and args.conv <= 0:
+        field_env = field_env_leg(args.field_env_envs, 5, not args.no_cpu, min(16, len(os.sched_getaffinity(0))))
 
     out = {
         "metric": METRIC, "value": value, "unit": "env-steps/s", "n_gpus": 1, "steps": args.steps,
@@ -393,6 +468,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "lu": lu,
         "fdm": fdm,
+        "field_env": field_env,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -652,16 +652,29 @@ __global__ void fe_pre_kernel(Args a) {
     step_pre(e, a, s);
 }
 
-// Zone means of the new field: lane per (env, zone), the room's cells in order.
+// Zone means of the new field: lane per (zone, env), envs of one zone on
+// adjacent lanes (they read the same cells), the room's cells in order, eight
+// loads in flight ahead of the sequential sum.
 __global__ void fe_means_kernel(Args a) {
     const int x = (int)(blockIdx.x * blockDim.x + threadIdx.x);
     const int nz = a.t.nz;
     if (x >= a.G * nz) return;
-    const int s = x / nz, z = x % nz;
+    const int z = x / a.G, s = x % a.G;
     const size_t b = (size_t)(s / a.Gl), l = (size_t)(s % a.Gl);
+    const double* T = a.T + b * (size_t)a.t.n_cvs * a.Gl + l;
+    const int* cells = a.t.zcells;
     const int c0 = a.t.zoff[z], c1 = a.t.zoff[z + 1];
     double sum = 0.0;
-    for (int q = c0; q < c1; q++) sum += a.T[(b * a.t.n_cvs + a.t.zcells[q]) * a.Gl + l];
+    int q = c0;
+    constexpr int U = 8;
+    for (; q + U <= c1; q += U) {
+        double v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = T[(size_t)cells[q + u] * a.Gl];
+#pragma unroll
+        for (int u = 0; u < U; u++) sum += v[u];
+    }
+    for (; q < c1; q++) sum += T[(size_t)cells[q] * a.Gl];
     unsigned char* rec = a.state + (size_t)s * a.st.bytes;
     reinterpret_cast<double*>(rec + a.st.avg_temp)[z] = sum / (double)(c1 - c0);
 }
