@@ -181,7 +181,7 @@ def fdm_leg(envs: int, steps: int, cpu: bool, cpu_threads: int) -> dict:
                        f"({inf.nnz_l} + {inf.nnz_u} off-diagonal, {inf.levels_l}/{inf.levels_u} levels), "
                        f"{envs} envs, air side on",
            "n_envs": envs, "steps": steps, "ms_per_step": ms, "value": envs / (ms / 1e3), "unit": "env-steps/s",
-           "mode": "default (LDS runs of the narrow levels, chunked levels)",
+           "mode": "default (LDS runs of the narrow levels, chunked levels, air-side correction from the applied columns' responses)",
            "lds_run_rows": [inf.tail_rows_l, inf.tail_rows_u], "lds_run_levels": [inf.tail_levels_l, inf.tail_levels_u],
            "algorithmic_bytes": inf.bytes_per_step,
            "achieved_gbs": inf.bytes_per_step / (ms / 1e3) / 1e9}

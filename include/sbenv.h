@@ -406,7 +406,7 @@ typedef struct {
     int levels_l, levels_u;       /* level-schedule depth of the two sweeps */
     long long nnz_l, nnz_u;       /* off-diagonal factor entries */
     double bytes_per_step;        /* algorithmic HBM bytes of one batched step */
-    double flops_per_step;        /* multiply-subtracts x 2 of both solves */
+    double flops_per_step;        /* multiply-adds x 2 of the solves and the air-side combination */
     int tail_rows_l, tail_rows_u;       /* rows of each sweep's LDS run (0: exact mode) */
     int tail_levels_l, tail_levels_u;   /* levels of the LDS run */
     int chunked_levels_l, chunked_levels_u;   /* levels after it solved chunked from HBM */
@@ -418,7 +418,9 @@ typedef struct {
  * so results agree with the reference to rounding, far inside 1e-9
  * relative. SBX_FDM_EXACT: every level from HBM in the reference's order,
  * bit-identical results. envs_per_block 0 picks 1 (default) or up to 64
- * (exact). */
+ * (exact). The default mode also takes the air-side correction from the
+ * responses of the applied columns (sbx_fdm_air_responses) instead of a
+ * second solve per step. */
 #define SBX_FDM_EXACT 1
 /* sb_fdm_init for every env: the blob's initial fields, S = sensed A^-1 applied
  * (solved on the device, in the reference's order). NULL on error
@@ -440,6 +442,14 @@ int sbx_fdm_get_state(SbxFdm* f, double* temp, double* mass_temp);
 int sbx_fdm_set_state(SbxFdm* f, const double* temp, const double* mass_temp);
 /* S [k][k] (host). */
 int sbx_fdm_sensed_response(SbxFdm* f, double* out);
+/* The default mode's air-side responses R [k][n_solved] (host): row j is
+ * A^-1 applied_j by solved index, solved at open in the reference's order
+ * (sb_fdm.c:104-108 solves the same columns for S). A step's air-side
+ * correction (sb_fdm.c:171-178: the applied heat of the dense solve's q,
+ * solved again) is then the combination sum_j q_j R[j] (linear in q: equal
+ * to rounding). Returns 1 (and writes nothing) in exact mode, which solves
+ * the correction as the reference does, or when k = 0. */
+int sbx_fdm_air_responses(SbxFdm* f, double* out);
 /* x = A^-1 b through the baked factors on the device (sb_lu_solve,
  * sb_lu.c:38-63), for n_rhs host columns b, x [n_rhs][n_solved]. */
 int sbx_fdm_lu_solve(SbxFdm* f, const double* b, double* x, int n_rhs);

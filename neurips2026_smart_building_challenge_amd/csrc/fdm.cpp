@@ -274,7 +274,8 @@ bool make_group(SbxFdm* f, int G, int Gl, bool fields, sbf::Group* g) {
     g->nblk = (G + Gl - 1) / Gl;
     const size_t lanes = (size_t)g->nblk * Gl;
     g->W1 = (double*)dalloc(f, sizeof(double) * lanes * t.n);
-    g->W2 = fields ? (double*)dalloc(f, sizeof(double) * lanes * t.n) : nullptr;
+    const bool w2 = fields && !t.R;   // the second solve's vector (exact mode)
+    g->W2 = w2 ? (double*)dalloc(f, sizeof(double) * lanes * t.n) : nullptr;
     g->T = fields ? (double*)dalloc(f, sizeof(double) * lanes * t.n_cvs) : nullptr;
     g->M = fields ? (double*)dalloc(f, sizeof(double) * lanes * t.n) : nullptr;
     const size_t k = std::max(t.k, 1);
@@ -282,7 +283,7 @@ bool make_group(SbxFdm* f, int G, int Gl, bool fields, sbf::Group* g) {
     g->mat = fields ? (double*)dalloc(f, sizeof(double) * G * k * k) : nullptr;
     g->eact = (int*)dalloc(f, sizeof(int) * G);
     g->bact = (int*)dalloc(f, sizeof(int) * g->nblk);
-    if (!g->W1 || !g->pw || !g->eact || !g->bact || (fields && (!g->W2 || !g->T || !g->M || !g->mat)))
+    if (!g->W1 || !g->pw || !g->eact || !g->bact || (w2 && !g->W2) || (fields && (!g->T || !g->M || !g->mat)))
         return fail("hipMalloc failed for the field buffers");
     return true;
 }
@@ -546,14 +547,23 @@ bool build(SbxFdm* f, const char* path, int G, int epb, int flags) {
         return false;
 
     // S = sensed A^-1 applied (sb_fdm.c:104-116), on the device: the applied
-    // columns solved as a group of k envs
+    // columns solved as a group of k envs (in exact mode, as the reference
+    // solves them); the default mode keeps the solutions themselves (R) for
+    // its air-side corrections
+    T.R = nullptr;
     if (k > 0) {
         sbf::Group sg{};
         if (!make_group(f, k, std::min(64, next_pow2(k)), false, &sg)) return false;
-        if (!hip_check((hipError_t)sbf_launch_solve_cols(&T, &sg, nullptr, nullptr, (double*)T.S, nullptr),
+        double* R = nullptr;
+        if (T.fast) {
+            R = (double*)dalloc(f, sizeof(double) * (size_t)k * n);
+            if (!R) return fail("hipMalloc failed for the air-side responses");
+        }
+        if (!hip_check((hipError_t)sbf_launch_solve_cols(&T, &sg, nullptr, R, (double*)T.S, nullptr),
                        "sensed response")
             || !hip_check(hipDeviceSynchronize(), "sensed response"))
             return false;
+        T.R = R;
         for (void* p : {(void*)sg.W1, (void*)sg.pw, (void*)sg.eact, (void*)sg.bact}) {
             (void)hipFree(p);
             f->owned.erase(std::find(f->owned.begin(), f->owned.end(), p));
@@ -587,10 +597,14 @@ bool build(SbxFdm* f, const char* path, int G, int epb, int flags) {
     // them); per env the heat input, the field read (solved cells) and
     // written (all cells), the mass read and written, and each solve's vector
     // read and written once per sweep
+    // (two solves in exact mode; in the default mode one, plus R read once and
+    // its k-term combination per env and solved cell)
+    const double solves = T.R ? 1.0 : 2.0;
     const double per_solve = 12.0 * (double)(L.nnz + U.nnz) + 8.0 * n + 2.0 * 8.0 * n;
-    const double per_env = 8.0 * ((double)n_cvs + n + n_cvs + 2.0 * n) + 2.0 * (2.0 * 2.0 * 8.0 * n);
-    I.bytes_per_step = 2.0 * per_solve + (double)G * per_env;
-    I.flops_per_step = (double)G * 2.0 * 2.0 * (double)(L.nnz + U.nnz);
+    const double per_env = 8.0 * ((double)n_cvs + n + n_cvs + 2.0 * n) + solves * (2.0 * 2.0 * 8.0 * n);
+    const double r_bytes = T.R ? 8.0 * (double)k * n : 0.0;
+    I.bytes_per_step = solves * per_solve + r_bytes + (double)G * per_env;
+    I.flops_per_step = (double)G * (solves * 2.0 * (double)(L.nnz + U.nnz) + (T.R ? 2.0 * (double)k * n : 0.0));
     return true;
 }
 
@@ -693,6 +707,13 @@ int sbx_fdm_sensed_response(SbxFdm* f, double* out) {
     const int k = f->tab.k;
     if (k == 0) return 0;
     return hip_check(hipMemcpy(out, f->tab.S, 8 * (size_t)k * k, hipMemcpyDeviceToHost), "copy S") ? 0 : -1;
+}
+
+int sbx_fdm_air_responses(SbxFdm* f, double* out) {
+    if (!f || !out) return -1;
+    const sbf::Tables& t = f->tab;
+    if (!t.R || t.k == 0) return 1;
+    return hip_check(hipMemcpy(out, t.R, 8 * (size_t)t.k * t.n, hipMemcpyDeviceToHost), "copy R") ? 0 : -1;
 }
 
 int sbx_fdm_lu_solve(SbxFdm* f, const double* b, double* x, int n_rhs) {

@@ -10,6 +10,7 @@
 // vector of the baked factorization (SuperLU convention, complete_port/csim/
 // sb_lu.c:38-63): w[i] = b[ir[i]], L w' = w, U z = w', x[t] = z[pc[t]].
 #pragma once
+#include <stddef.h>
 #include <stdint.h>
 
 namespace sbf {
@@ -99,6 +100,11 @@ struct Tables {
     const int* at_j;
     const double* at_x;
     const double* S;        // [k][k] sensed A^-1 applied
+    // default mode: R [k][n], row j the solution A^-1 applied_j of applied
+    // column j by solved index t (exact-mode solves at open), so a step's
+    // air-side correction A^-1 (applied q) is the combination R^T q instead of
+    // a second solve; null in exact mode
+    const double* R;
     // blobs with zones (full env scenarios): the zone whose heat each solved
     // cell t carries, or -1 (a zone's heat goes to its room's cells; a cell of
     // two zones' rooms takes the later zone's, as csim assigns input_q)
@@ -111,7 +117,7 @@ struct Group {
     double* T;              // [nblk][n_cvs][Gl]
     double* M;              // [nblk][n][Gl]
     double* W1;             // [nblk][n][Gl] the forcing solve
-    double* W2;             // [nblk][n][Gl] the air-side correction
+    double* W2;             // [nblk][n][Gl] the air-side correction (exact mode; null with Tables::R)
     double* pw;             // [G][k] air-side power, then the dense solve's result
     double* mat;            // [G][k][k] I + diag(g) S
     int* eact;              // [G] env has a nonzero air-side conductance this step
@@ -129,5 +135,12 @@ struct StepIn {
     const double* airT;
     const double* qz;
 };
+
+// The host (g++) and the device (hipcc) compile these structs separately and
+// exchange them byte for byte: both builds check the same sizes and offsets.
+static_assert(sizeof(Tri) == 56 && sizeof(Tail) == 112 && sizeof(Sweep) == 352, "Tri / Tail / Sweep layout");
+static_assert(sizeof(Tables) == 1040 && offsetof(Tables, S) == 1008 && offsetof(Tables, R) == 1016
+              && offsetof(Tables, nz) == 1032, "Tables layout");
+static_assert(sizeof(Group) == 80 && sizeof(StepIn) == 48, "Group / StepIn layout");
 
 }  // namespace sbf

@@ -480,6 +480,69 @@ __global__ void update_kernel(sbf::Tables t, sbf::Group g, sbf::StepIn in) {
     }
 }
 
+// Default mode with the air side: y = the forcing solve + R^T q, R's rows the
+// solutions of the applied columns (solved once at open), q the dense solve's
+// result per env; the same y as sb_fdm.c:171-178's second solve of the
+// applied heat up to rounding (the correction is linear in q). Then the
+// interior mass and the field (sb_fdm.c:183-187). A block is 64 solved cells
+// (a lane each) by 4 wavefronts of kREnvs envs; each R value loaded is used
+// for kREnvs envs, and an env's q row is wave-uniform (scalar loads). The
+// correction of an env sums j = 0 .. k-1 in order.
+constexpr int kREnvs = 16;
+
+__global__ __launch_bounds__(256) void update_r_kernel(sbf::Tables t, sbf::Group g, sbf::StepIn in) {
+    const int n = t.n, k = t.k, Gl = g.Gl, G = g.G;
+    const int lane = (int)(threadIdx.x & 63), wv = (int)(threadIdx.x >> 6);
+    const int egs = (G + 4 * kREnvs - 1) / (4 * kREnvs);
+    const int tile = (int)blockIdx.x / egs, eg = (int)blockIdx.x % egs;
+    const int e0 = (eg * 4 + wv) * kREnvs;
+    const int tt = tile * 64 + lane;
+    if (e0 < G && tile * 64 < n) {
+        const bool ok = tt < n;
+        const int tc = ok ? tt : n - 1;
+        double acc[kREnvs];
+#pragma unroll
+        for (int e = 0; e < kREnvs; e++) acc[e] = 0.0;
+        for (int j0 = 0; j0 < k; j0 += 8) {
+            double r[8];
+#pragma unroll
+            for (int jj = 0; jj < 8; jj++) r[jj] = j0 + jj < k ? t.R[(size_t)(j0 + jj) * n + tc] : 0.0;
+#pragma unroll
+            for (int e = 0; e < kREnvs; e++) {
+                const int env = e0 + e < G ? e0 + e : G - 1;
+                const double* qv = g.pw + (size_t)env * k + j0;
+#pragma unroll
+                for (int jj = 0; jj < 8; jj++)
+                    if (j0 + jj < k) acc[e] = fma(r[jj], qv[jj], acc[e]);   // j0, jj, k wave-uniform
+            }
+        }
+        if (ok) {
+            const int pcv = t.pc[tc], cell = t.solved[tc];
+            const double mr = t.mret[tc], mg = t.mgain[tc];
+#pragma unroll
+            for (int e = 0; e < kREnvs; e++) {
+                const int env = e0 + e;
+                if (env >= G) break;
+                const int b = env / Gl, l = env % Gl;
+                double y = g.W1[((size_t)b * n + pcv) * Gl + l];
+                if (g.eact[env]) y += acc[e];
+                const size_t mi = ((size_t)b * n + tc) * Gl + l;
+                g.M[mi] = g.M[mi] * mr + mg * y;
+                g.T[((size_t)b * t.n_cvs + cell) * Gl + l] = y;
+            }
+        }
+    }
+    const size_t tu = (size_t)g.nblk * t.n_unsolved * Gl;
+    for (size_t x = gtid(); x < tu; x += gstride()) {
+        const int l = (int)(x % Gl);
+        const size_t bu = x / Gl;
+        const int u = (int)(bu % t.n_unsolved), b = (int)(bu / t.n_unsolved);
+        const int env = b * Gl + l;
+        if (env >= G) continue;
+        g.T[((size_t)b * t.n_cvs + t.unsolved[u]) * Gl + l] = in.amb[env];
+    }
+}
+
 // Every env's fields from the blob's initial fields.
 __global__ void init_kernel(sbf::Tables t, sbf::Group g, const double* temp_init, const double* mass_init) {
     const int Gl = g.Gl;
@@ -628,6 +691,12 @@ extern "C" int sbf_launch_step(const sbf::Tables* t, const sbf::Group* g, const 
             hipLaunchKernelGGL(sensed_kernel, dim3(elt_grid((size_t)g->G * t->k)), dim3(kEltThreads), 0, s, *t, *g,
                                *in);
         hipLaunchKernelGGL(dense_kernel, dim3(g->G), dim3(64), 0, s, *t, *g, *in);
+        if (t->R) {
+            // the correction as R^T q, fused with the mass and field update
+            const size_t tiles = ((size_t)t->n + 63) / 64, egs = ((size_t)g->G + 4 * kREnvs - 1) / (4 * kREnvs);
+            hipLaunchKernelGGL(update_r_kernel, dim3((unsigned)(tiles * egs)), dim3(256), 0, s, *t, *g, *in);
+            return (int)hipGetLastError();
+        }
         hipLaunchKernelGGL(applied_kernel, dim3(elt_grid(rows)), dim3(kEltThreads), 0, s, *t, *g);
         if (int e = solve(*t, *g, g->W2, g->bact, false, s)) return e;
     }

@@ -108,7 +108,7 @@ EXPORTS = [
     "sbx_env_meta", "sbx_scenario_path", "sbx_canon_state",
     "sbx_plan_layout", "sbx_plan_free",
     "sbx_fdm_open", "sbx_fdm_close", "sbx_fdm_info", "sbx_fdm_step", "sbx_fdm_reset", "sbx_fdm_get_state",
-    "sbx_fdm_set_state", "sbx_fdm_sensed_response", "sbx_fdm_lu_solve",
+    "sbx_fdm_set_state", "sbx_fdm_sensed_response", "sbx_fdm_air_responses", "sbx_fdm_lu_solve",
     "sbx_last_error", "sbx_version",
 ]
 

@@ -52,9 +52,10 @@ def _lib() -> ctypes.CDLL:
         L.sbx_fdm_get_state.argtypes = [P, P, P]
         L.sbx_fdm_set_state.argtypes = [P, P, P]
         L.sbx_fdm_sensed_response.argtypes = [P, P]
+        L.sbx_fdm_air_responses.argtypes = [P, P]
         L.sbx_fdm_lu_solve.argtypes = [P, P, P, ctypes.c_int]
         for f in (L.sbx_fdm_info, L.sbx_fdm_step, L.sbx_fdm_reset, L.sbx_fdm_get_state, L.sbx_fdm_set_state,
-                  L.sbx_fdm_sensed_response, L.sbx_fdm_lu_solve):
+                  L.sbx_fdm_sensed_response, L.sbx_fdm_air_responses, L.sbx_fdm_lu_solve):
             f.restype = ctypes.c_int
         _BOUND = True
     return L
@@ -129,6 +130,15 @@ class FieldGroup:
         S = np.zeros((self.k, self.k))
         self._check(self.L.sbx_fdm_sensed_response(self.h, _ptr(S)), "sbx_fdm_sensed_response")
         return S
+
+    def air_responses(self) -> np.ndarray | None:
+        """R [k][n_solved] of the default mode (None in exact mode or without an air side)."""
+        R = np.zeros((self.k, self.info.n_solved))
+        rc = self.L.sbx_fdm_air_responses(self.h, _ptr(R))
+        if rc == 1:
+            return None
+        self._check(rc, "sbx_fdm_air_responses")
+        return R
 
     def lu_solve(self, b: np.ndarray) -> np.ndarray:
         b = np.ascontiguousarray(np.atleast_2d(b), np.float64)

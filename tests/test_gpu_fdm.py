@@ -13,6 +13,9 @@ deep end of each sweep solved in LDS with reassociated sums):
     nonempty LDS tail on both plans;
   - the sensed response S (solved on the device at open) and the factor solve
     of the baker's reference right-hand side, bit-identical to the oracle's;
+  - the default mode's air-side responses (the applied columns solved at
+    open; its steps combine them instead of solving the correction again),
+    bit-identical to the oracle's solves of those columns;
   - steps where no env, or only some envs, have an air side (the correction
     skipped per env and per block);
   - at 64 envs of the full-size plan: a permutation of the envs permutes the
@@ -108,6 +111,33 @@ def test_gpu_fdm_sensed_response_and_solve(small):
     X = f.lu_solve(B)
     for r in range(B.shape[0]):
         assert np.array_equal(X[r], o.lu_solve(B[r])), r
+    assert f.air_responses() is None, "exact mode solves the correction itself"
+    f.close()
+
+
+def test_gpu_fdm_air_responses(small):
+    """The default mode's air-side responses: row j is the oracle's solve of
+    applied column j (sb_fdm.c:104-108), bit for bit; S is sensed times them."""
+    plan, path, _ = small
+    say("air-side responses of the default mode, small plan")
+    f = gpu_group(path, 2, 0, exact=False)
+    R = f.air_responses()
+    o = po.Fdm("oracle", path, 1)
+    d = read_sbb(path)
+    n, k = (int(v) for v in d["applied_shape"])
+    assert R.shape == (k, n) and k == plan.k
+    ap_p, ap_i, ap_x = d["applied_indptr"], d["applied_indices"], d["applied_data"]
+    cols = np.zeros((k, n))
+    for j in range(k):
+        cols[j, ap_i[ap_p[j]:ap_p[j + 1]]] = ap_x[ap_p[j]:ap_p[j + 1]]
+    for j in range(k):
+        assert np.array_equal(R[j], o.lu_solve(cols[j])), j
+    sn_p, sn_i, sn_x = d["sensed_indptr"], d["sensed_indices"], d["sensed_data"]
+    S = f.sensed_response()
+    for i in range(k):
+        w = np.zeros(n)
+        w[sn_i[sn_p[i]:sn_p[i + 1]]] = sn_x[sn_p[i]:sn_p[i + 1]]
+        assert np.allclose(S[i], R @ w, rtol=1e-12, atol=1e-15), i
     f.close()
 
 
