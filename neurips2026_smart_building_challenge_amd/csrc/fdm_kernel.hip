@@ -492,7 +492,9 @@ constexpr int kREnvs = 16;
 
 __global__ __launch_bounds__(256) void update_r_kernel(sbf::Tables t, sbf::Group g, sbf::StepIn in) {
     const int n = t.n, k = t.k, Gl = g.Gl, G = g.G;
-    const int lane = (int)(threadIdx.x & 63), wv = (int)(threadIdx.x >> 6);
+    // the wavefront index through readfirstlane: the compiler then knows the
+    // envs (and their q rows) are wave-uniform and reads q with scalar loads
+    const int lane = (int)(threadIdx.x & 63), wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int egs = (G + 4 * kREnvs - 1) / (4 * kREnvs);
     const int tile = (int)blockIdx.x / egs, eg = (int)blockIdx.x % egs;
     const int e0 = (eg * 4 + wv) * kREnvs;
@@ -503,17 +505,26 @@ __global__ __launch_bounds__(256) void update_r_kernel(sbf::Tables t, sbf::Group
         double acc[kREnvs];
 #pragma unroll
         for (int e = 0; e < kREnvs; e++) acc[e] = 0.0;
-        for (int j0 = 0; j0 < k; j0 += 8) {
+        // columns eight at a time, then one at a time (j0 and k are wave-uniform)
+        int j0 = 0;
+        for (; j0 + 8 <= k; j0 += 8) {
             double r[8];
 #pragma unroll
-            for (int jj = 0; jj < 8; jj++) r[jj] = j0 + jj < k ? t.R[(size_t)(j0 + jj) * n + tc] : 0.0;
+            for (int jj = 0; jj < 8; jj++) r[jj] = t.R[(size_t)(j0 + jj) * n + tc];
 #pragma unroll
             for (int e = 0; e < kREnvs; e++) {
                 const int env = e0 + e < G ? e0 + e : G - 1;
                 const double* qv = g.pw + (size_t)env * k + j0;
 #pragma unroll
-                for (int jj = 0; jj < 8; jj++)
-                    if (j0 + jj < k) acc[e] = fma(r[jj], qv[jj], acc[e]);   // j0, jj, k wave-uniform
+                for (int jj = 0; jj < 8; jj++) acc[e] = fma(r[jj], qv[jj], acc[e]);
+            }
+        }
+        for (; j0 < k; j0++) {
+            const double r = t.R[(size_t)j0 * n + tc];
+#pragma unroll
+            for (int e = 0; e < kREnvs; e++) {
+                const int env = e0 + e < G ? e0 + e : G - 1;
+                acc[e] = fma(r, g.pw[(size_t)env * k + j0], acc[e]);
             }
         }
         if (ok) {
