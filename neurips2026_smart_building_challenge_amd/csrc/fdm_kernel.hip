@@ -30,6 +30,10 @@
 namespace {
 
 constexpr int kSolveThreads = 1024;
+// the chunked runs: a level's chain (chunk sums, LDS barrier, row finishes,
+// barrier) is shorter with 8 wavefronts than with 16 (16.4 ms with 4, 15.2
+// with 8, 17.9 with 16 per step at 256 envs of the 205K-cell plan)
+constexpr int kRunThreads = 512;
 constexpr int kEltThreads = 256;
 
 __device__ __forceinline__ size_t gtid() { return (size_t)blockIdx.x * blockDim.x + threadIdx.x; }
@@ -121,15 +125,15 @@ __device__ __forceinline__ void lds_barrier() {
 typedef const __attribute__((address_space(4))) int* cint_ptr;
 
 template <bool UPPER, int GL, bool LDSW>
-__global__ __launch_bounds__(kSolveThreads) void run_kernel(sbf::Tail tl, int n, double* W, const int* bact) {
+__global__ __launch_bounds__(kRunThreads) void run_kernel(sbf::Tail tl, int n, double* W, const int* bact) {
     extern __shared__ double lds[];
     // level metadata is uniform: read through the scalar (constant) path, so
     // these reads do not queue behind the vector loads of the prefetch
     const cint_ptr trow = (cint_ptr)tl.trow;
     const cint_ptr tchunk = (cint_ptr)tl.tchunk;
     const cint_ptr tmode = (cint_ptr)tl.tmode;
-    constexpr int NS = kSolveThreads / GL;   // lane slots of the workgroup per env
-    constexpr int NW = kSolveThreads / 64;
+    constexpr int NS = kRunThreads / GL;   // lane slots of the workgroup per env
+    constexpr int NW = kRunThreads / 64;
     constexpr int S = 64 / GL;
     constexpr int K = sbf::kChunk;
     const int b = blockIdx.x;
@@ -141,7 +145,7 @@ __global__ __launch_bounds__(kSolveThreads) void run_kernel(sbf::Tail tl, int n,
     const int gl = tid % GL, slot = tid / GL;
     const int s = lane / GL;
     if (LDSW)
-        for (int x = tid; x < tl.m * GL; x += kSolveThreads) Wt[x] = Wb[(size_t)tl.rows[x / GL] * GL + x % GL];
+        for (int x = tid; x < tl.m * GL; x += kRunThreads) Wt[x] = Wb[(size_t)tl.rows[x / GL] * GL + x % GL];
     struct Chunk {
         int4 a0, a1;
         double v[K];
@@ -267,7 +271,7 @@ __global__ __launch_bounds__(kSolveThreads) void run_kernel(sbf::Tail tl, int n,
         else __syncthreads();
     }
     if (LDSW)
-        for (int x = tid; x < tl.m * GL; x += kSolveThreads) Wb[(size_t)tl.rows[x / GL] * GL + x % GL] = Wt[x];
+        for (int x = tid; x < tl.m * GL; x += kRunThreads) Wb[(size_t)tl.rows[x / GL] * GL + x % GL] = Wt[x];
 }
 
 // sum_p x[p] * W[row w[p]] over [p0, p1) in order, 8 terms per round trip
@@ -629,7 +633,7 @@ void sweep(const sbf::Tri& tri, const sbf::Sweep* sw, const sbf::Group& g, int n
     // levels before the LDS run; the run's head terms and the run; the levels after it
     if (sw->pre_chunked) {
         const size_t lds = (size_t)sw->pre.max_chunks * GL * sizeof(double);
-        hipLaunchKernelGGL((run_kernel<UPPER, GL, false>), dim3(g.nblk), dim3(kSolveThreads), lds, s, sw->pre, n, W,
+        hipLaunchKernelGGL((run_kernel<UPPER, GL, false>), dim3(g.nblk), dim3(kRunThreads), lds, s, sw->pre, n, W,
                            bact);
     } else {
         plain(0, sw->pre_end);
@@ -642,11 +646,11 @@ void sweep(const sbf::Tri& tri, const sbf::Sweep* sw, const sbf::Group& g, int n
             hipLaunchKernelGGL((head_kernel<GL>), dim3(grid), dim3(256), 0, s, mid, n, g.nblk, W, bact);
         }
         const size_t lds = (size_t)(mid.m + mid.max_chunks) * GL * sizeof(double);
-        hipLaunchKernelGGL((run_kernel<UPPER, GL, true>), dim3(g.nblk), dim3(kSolveThreads), lds, s, mid, n, W, bact);
+        hipLaunchKernelGGL((run_kernel<UPPER, GL, true>), dim3(g.nblk), dim3(kRunThreads), lds, s, mid, n, W, bact);
     }
     if (sw->post_chunked) {
         const size_t lds = (size_t)sw->post.max_chunks * GL * sizeof(double);
-        hipLaunchKernelGGL((run_kernel<UPPER, GL, false>), dim3(g.nblk), dim3(kSolveThreads), lds, s, sw->post, n, W,
+        hipLaunchKernelGGL((run_kernel<UPPER, GL, false>), dim3(g.nblk), dim3(kRunThreads), lds, s, sw->post, n, W,
                            bact);
     } else {
         plain(sw->post_begin, tri.nlev);
