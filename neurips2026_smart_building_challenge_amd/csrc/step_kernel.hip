@@ -2515,6 +2515,9 @@ __device__ __forceinline__ void stamps_flush(const KParams& P, const Ctx& c) {
 }
 
 
+static_assert(offsetof(Log, episode_return) == 8 && offsetof(Log, reward_mean) == 16 && sizeof(Log) == 24,
+              "the helper's 16-byte log read covers episode_return, episode_length, reward_mean and n");
+
 // The env's second wavefront during a step. The occupancy interval is
 // exogenous (it reads only the chain states, the MT stream and the calendar),
 // so it runs while the first wavefront decodes and runs the HVAC pre-step.
@@ -2569,8 +2572,13 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
         env_post(sy + SY_CONV, 1);
     }
     STAMP(15);
-    // host-visible log fields (the trainer may clear them between steps)
-    float lg_ret = 0.f, lg_mean = 0.f;
+    // host-visible log fields (the trainer may clear them between steps):
+    // episode_return .. n in one 16-byte system-coherent load, one request
+    // over the host link per env (those requests queue there when thousands
+    // of envs step at once). The compiler does not count an inline load, so
+    // the explicit wait before the fields are used covers it.
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    f4v lgv = {0.f, 0.f, 0.f, 0.f};
     {
         // the next step's calendar values (rows kk + 1 and j + 1) into the
         // other calendar section of the state image, loaded while this
@@ -2580,10 +2588,10 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
         const int n1 = c.S->n1;
         const RowVals next = row_issue<W>(c, min(kk + 1, n1 - 1), min(j + 1, n1 - 1));
         if (P.host_env && ln() == 0) {
-            Log* hlog = reinterpret_cast<Log*>(reinterpret_cast<unsigned char*>(P.host_env)
-                                               + (size_t)c.e * P.env_stride + P.log_offset);
-            lg_ret = __hip_atomic_load(&hlog->episode_return, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            lg_mean = __hip_atomic_load(&hlog->reward_mean, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            const Log* hlog = reinterpret_cast<const Log*>(reinterpret_cast<const unsigned char*>(P.host_env)
+                                                           + (size_t)c.e * P.env_stride + P.log_offset);
+            const float* lp = &hlog->episode_return;
+            asm volatile("global_load_dwordx4 %0, %1, off sc0 sc1" : "=v"(lgv) : "v"(lp) : "memory");
         }
         env_wait(sy + SY_PRE, 1);
         row_store<W>(c, next, cal_section(c, kk + 1));
@@ -2598,11 +2606,12 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
     zone_means<W>(c, hzq);
     esync();
     const RewardPart part = reward_rest<W>(c, hzq, v_new);
+    asm volatile("s_waitcnt vmcnt(0)" : "+v"(lgv) : : "memory");   // the log fields' load
     if (ln() == 0) {
         *reinterpret_cast<RewardPart*>(sy + SY_PART) = part;
         float* lg = reinterpret_cast<float*>(sy + SY_LOG);
-        lg[0] = lg_ret;
-        lg[1] = lg_mean;
+        lg[0] = lgv.x;   // episode_return
+        lg[1] = lgv.z;   // reward_mean
     }
     // the observation row's stores are complete before the first wavefront
     // may overwrite the row with an auto-reset observation
