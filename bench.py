@@ -208,6 +208,19 @@ def fdm_leg(envs: int, steps: int, cpu: bool, cpu_threads: int) -> dict:
     return rec
 
 
+def with_more_envs(leg, envs: int, cpu: bool, cpu_threads: int, more=(512,)) -> dict:
+    """A building-scale record at `envs` envs, with the same leg timed (3
+    steps, no CPU baseline) at each of `more` envs beside it: the reference's
+    published GPU figures are quoted at 256 and 512 envs."""
+    rec = leg(envs, 5, cpu, cpu_threads)
+    rec["more_envs"] = []
+    for m in more:
+        if m != envs:
+            r = leg(m, 3, False, 1)
+            rec["more_envs"].append({k: r[k] for k in ("n_envs", "steps", "ms_per_step", "value")})
+    return rec
+
+
 def field_env_leg(envs: int, steps: int, cpu: bool, cpu_threads: int) -> dict:
     """Whole env steps (puf_step on pre-drawn resident action rows) of an
     FDM-scale scenario: the field of building_train_1's size (606 x 339 cells,
@@ -307,12 +320,13 @@ def main() -> int:
 
     if args.fdm_only:
         visible = len(os.sched_getaffinity(0))
-        print(json.dumps(fdm_leg(max(1, args.fdm_envs), 5, not args.no_cpu, min(16, visible))), flush=True)
+        print(json.dumps(with_more_envs(fdm_leg, max(1, args.fdm_envs), not args.no_cpu, min(16, visible))),
+              flush=True)
         return 0
     if args.field_env_only:
         visible = len(os.sched_getaffinity(0))
-        print(json.dumps(field_env_leg(max(1, args.field_env_envs), 5, not args.no_cpu, min(16, visible))),
-              flush=True)
+        print(json.dumps(with_more_envs(field_env_leg, max(1, args.field_env_envs), not args.no_cpu,
+                                        min(16, visible))), flush=True)
         return 0
     scen, n_envs, offsets = G.config_scenarios(args.config)
     groups = len(scen)
@@ -438,9 +452,10 @@ def main() -> int:
 
     fdm = field_env = None
     if args.fdm_envs > 0 and args.config == 1 and args.conv <= 0:
-        fdm = fdm_leg(args.fdm_envs, 5, not args.no_cpu, min(16, len(os.sched_getaffinity(0))))
+        fdm = with_more_envs(fdm_leg, args.fdm_envs, not args.no_cpu, min(16, len(os.sched_getaffinity(0))))
     if args.field_env_envs > 0 and args.config == 1 and args.conv <= 0:
-        field_env = field_env_leg(args.field_env_envs, 5, not args.no_cpu, min(16, len(os.sched_getaffinity(0))))
+        field_env = with_more_envs(field_env_leg, args.field_env_envs, not args.no_cpu,
+                                   min(16, len(os.sched_getaffinity(0))))
 
     out = {
         "metric": METRIC, "value": value, "unit": "env-steps/s", "n_gpus": 1, "steps": args.steps,

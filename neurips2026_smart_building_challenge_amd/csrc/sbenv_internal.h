@@ -304,9 +304,10 @@ enum { KMODE_STEP = 0, KMODE_RESET = 1 };
 // sums ready; observation
 // written, new occupancy committed and reward half ready); the helper's reward
 // half (4 f64 from SY_PART) and the host log fields it read (2 f32 from SY_LOG);
+// the helper's stores of the record's leading arrays complete (SY_STORED);
 // the helper's convection permutation of the step (SY_CONV).
 enum { SY_PRE = 0, SY_POST = 1, SY_HALF = 2, SY_SENS = 3, SY_PART = 4, SY_LOG = 12, SY_RET = 14, SY_CONV = 15,
-       SY_WORDS = 16 };
+       SY_STORED = 16, SY_WORDS = 17 };
 
 // A workgroup's envs: order[first .. first + count) all of one layout, with
 // the layout's staging burst inputs (copied from its DevLayout) and each

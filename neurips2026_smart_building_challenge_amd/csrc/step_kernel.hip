@@ -2463,13 +2463,13 @@ __device__ __forceinline__ double reward_combine(const Ctx& c, double blower, do
     return raw / (pw + ew + cw);
 }
 
-// Store of the state image back to its HBM record, 16 bytes per lane.
+// Store of bytes [begin, end) (16-byte multiples) of the state image back to
+// its HBM record, 16 bytes per lane.
 template <int W>
-__device__ __forceinline__ void store16(unsigned char* dst, const unsigned char* src, int bytes) {
-    const int n16 = bytes >> 4;
+__device__ __forceinline__ void store16(unsigned char* dst, const unsigned char* src, int begin, int end) {
     // streaming stores: the record is read back only by the next step's burst
     typedef unsigned int u4v __attribute__((ext_vector_type(4)));
-    for (int i = ln(); i < n16; i += W)
+    for (int i = (begin >> 4) + ln(); i < (end >> 4); i += W)
         __builtin_nontemporal_store(reinterpret_cast<const u4v*>(src)[i], reinterpret_cast<u4v*>(dst) + i);
 }
 
@@ -2618,6 +2618,13 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     env_post(sy + SY_HALF, 1);
     STAMP(18);
+    // the record's field, mass, VAV and AHU arrays [0, early) are final (the
+    // first wavefront changes them after this only when the episode ends,
+    // and then stores them again after SY_STORED): stored here, beside its
+    // bookkeeping, so the end of the step stores only the rest
+    store16<W>(c.rec, env + L->lds.state, 0, L->st.plant & ~15);
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0): complete before the first wavefront may store them again
+    env_post(sy + SY_STORED, 1);
     stamps_flush(P, c);
 }
 
@@ -2729,6 +2736,7 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
     // the step (KMODE_STEP), then one shared reset path for puf_reset and for
     // the auto-reset at the end of an episode
     int done = 0;
+    const int early = L->st.plant & ~15;   // the part of the record stored after the field step
     if (!reset_mode) {
         decode_apply<W>(c);
         STAMP(2);
@@ -2806,7 +2814,11 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
     }
     esync();
     STAMP(10);
-    store16<W>(c.rec, env + L->lds.state, L->st.bytes);
+    // the helper has stored the record's field, mass, VAV and AHU arrays
+    // [0, early); an episode that ended rewrote them (the reset), so once the
+    // helper's stores are complete they are stored again
+    if (!reset_mode && done) env_wait(sy + SY_STORED, 1);
+    store16<W>(c.rec, env + L->lds.state, (reset_mode || done) ? 0 : early, L->st.bytes);
     STAMP(11);
     stamps_flush(P, c);
 }
