@@ -68,13 +68,36 @@ __global__ __launch_bounds__(kSolveThreads) void solve_kernel(sbf::Tri tri, int 
     }
 }
 
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ double dpp_d(double v) {
+    const unsigned long long x = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)x, CTRL, ROWS, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(x >> 32), CTRL, ROWS, 0xF, false);
+    return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}
+
 // Sum over a wavefront's lanes that share an env (lanes l, l + GL, ...), in a
-// fixed order; every lane gets the total.
+// fixed order; every lane gets the total. One env per wavefront (GL = 1): DPP
+// lane moves (quad permutes, row mirrors, row broadcasts; no LDS traffic),
+// the total read from lane 63; otherwise a butterfly over the env's lanes.
 template <int GL>
 __device__ __forceinline__ double lane_sum(double v) {
+    if constexpr (GL == 1) {
+        v += dpp_d<0xB1>(v);          // quad_perm [1,0,3,2]
+        v += dpp_d<0x4E>(v);          // quad_perm [2,3,0,1]
+        v += dpp_d<0x141>(v);         // row_half_mirror
+        v += dpp_d<0x140>(v);         // row_mirror
+        v += dpp_d<0x142, 0xA>(v);    // row_bcast:15
+        v += dpp_d<0x143, 0xC>(v);    // row_bcast:31
+        const unsigned long long x = __double_as_longlong(v);
+        const unsigned lo = __builtin_amdgcn_readlane((int)(unsigned)x, 63);
+        const unsigned hi = __builtin_amdgcn_readlane((int)(unsigned)(x >> 32), 63);
+        return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+    } else {
 #pragma unroll
-    for (int off = GL; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
-    return v;
+        for (int off = GL; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
+        return v;
+    }
 }
 
 // Head terms of the tail rows (columns finished before the tail's first
@@ -242,8 +265,16 @@ __global__ __launch_bounds__(kRunThreads) void run_kernel(sbf::Tail tl, int n, d
             lds_barrier();
             if (mode == 1) {
                 for (int r = trow[t] + slot; r < trow[t + 1]; r += NS) {
+                    // the row's partials four reads at a time, summed in order
+                    const int c0 = tl.rchunk[r] - clo, c1 = tl.rchunk[r + 1] - clo;
                     double acc = 0.0;
-                    for (int c = tl.rchunk[r]; c < tl.rchunk[r + 1]; c++) acc += P[(size_t)(c - clo) * GL + gl];
+                    for (int c = c0; c < c1; c += 4) {
+                        double pv[4];
+#pragma unroll
+                        for (int j = 0; j < 4; j++) pv[j] = P[(size_t)(c + j < c1 ? c + j : c1 - 1) * GL + gl];
+#pragma unroll
+                        for (int j = 0; j < 4; j++) acc += c + j < c1 ? pv[j] : 0.0;
+                    }
                     finish(r, own_of(r), acc);
                 }
             } else {
