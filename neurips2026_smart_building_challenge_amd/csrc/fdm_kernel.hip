@@ -197,11 +197,7 @@ __global__ __launch_bounds__(kRunThreads) void run_kernel(sbf::Tail tl, int n, d
         return acc;
     };
     auto own_ref = [&](int r) -> double* { return LDSW ? &Wt[r * GL + gl] : &Wb[(size_t)tl.rows[r] * GL + gl]; };
-    auto finish = [&](int r, double own, double acc) {
-        double w = own - acc;
-        if (UPPER) w = w / tl.diag[r];
-        *own_ref(r) = w;
-    };
+
     // the first row this lane finishes in level t (-1: none) and the chunk it
     // starts the level with (-1: none)
     auto first_row = [&](int t) -> int {
@@ -221,36 +217,46 @@ __global__ __launch_bounds__(kRunThreads) void run_kernel(sbf::Tail tl, int n, d
         const int c = tl.rchunk[r] + (mode == 3 ? s : 0);
         return c < tl.rchunk[r + 1] ? c : -1;
     };
-    // this level's first chunk and row value (cur*), the next level's (nxt*)
+    // this level's first chunk, row value (HBM runs) and diagonal (U) of the
+    // first row this lane finishes (cur*), the next level's (nxt*)
     Chunk cur, nxt;
     int curc = -1, curr = -1, nxtc = -1, nxtr = -1;
-    double curo = 0.0, nxto = 0.0;
+    double curo = 0.0, nxto = 0.0, curd = 1.0, nxtd = 1.0;
     // loads issued whether or not the lane uses them (index 0 when not), so
     // the compiler can wait for exactly the ones a use needs
-    auto load_first = [&](int t, Chunk& ch, int& c, int& r, double& o) {
+    auto load_first = [&](int t, Chunk& ch, int& c, int& r, double& o, double& d) {
         c = first_chunk(t);
         fetch(c >= 0 ? c : 0, ch);
-        if (!LDSW) {
-            r = first_row(t);
-            o = Wb[(size_t)tl.rows[r >= 0 ? r : 0] * GL + gl];
-        }
+        if (!LDSW || UPPER) r = first_row(t);
+        if (!LDSW) o = Wb[(size_t)tl.rows[r >= 0 ? r : 0] * GL + gl];
+        if (UPPER) d = tl.diag[r >= 0 ? r : 0];
     };
-    auto own_of = [&](int r) -> double {
+    // row r's value from its own value less the sum of its terms (divided by
+    // U's diagonal), with the prefetched own value and diagonal where r is
+    // the lane's first row of the level
+    auto finish_row = [&](int r, double acc) {
+        double own, dg = 1.0;
         if (r == curr) {
+            own = LDSW ? *own_ref(r) : curo;
+            dg = curd;
             curr = -1;
-            return curo;
+        } else {
+            own = *own_ref(r);
+            if (UPPER) dg = tl.diag[r];
         }
-        return *own_ref(r);
+        double w = own - acc;
+        if (UPPER) w = w / dg;
+        *own_ref(r) = w;
     };
     auto chunk_of = [&](int c, Chunk& tmp) -> const Chunk& {
         if (c == curc) return cur;
         fetch(c, tmp);
         return tmp;
     };
-    if (tl.nlev > 0) load_first(0, cur, curc, curr, curo);
+    if (tl.nlev > 0) load_first(0, cur, curc, curr, curo, curd);
     __syncthreads();
     for (int t = 0; t < tl.nlev; t++) {
-        if (t + 1 < tl.nlev) load_first(t + 1, nxt, nxtc, nxtr, nxto);
+        if (t + 1 < tl.nlev) load_first(t + 1, nxt, nxtc, nxtr, nxto, nxtd);
         const int clo = tchunk[t], chi = tchunk[t + 1];
         const int mode = tmode[t];
         Chunk tmp;
@@ -258,7 +264,7 @@ __global__ __launch_bounds__(kRunThreads) void run_kernel(sbf::Tail tl, int n, d
             for (int r = trow[t] + slot; r < trow[t + 1]; r += NS) {
                 double acc = 0.0;
                 if (tl.rchunk[r] < tl.rchunk[r + 1]) acc = part(chunk_of(tl.rchunk[r], tmp));
-                finish(r, own_of(r), acc);
+                finish_row(r, acc);
             }
         } else if (mode == 1 || mode == 2) {
             for (int c = clo + slot; c < chi; c += NS) P[(size_t)(c - clo) * GL + gl] = part(chunk_of(c, tmp));
@@ -275,7 +281,7 @@ __global__ __launch_bounds__(kRunThreads) void run_kernel(sbf::Tail tl, int n, d
 #pragma unroll
                         for (int j = 0; j < 4; j++) acc += c + j < c1 ? pv[j] : 0.0;
                     }
-                    finish(r, own_of(r), acc);
+                    finish_row(r, acc);
                 }
             } else {
                 for (int r = trow[t] + wave; r < trow[t + 1]; r += NW) {
@@ -283,7 +289,7 @@ __global__ __launch_bounds__(kRunThreads) void run_kernel(sbf::Tail tl, int n, d
                     double acc = 0.0;
                     for (int c = tl.rchunk[r] - clo + s; c < c1; c += S) acc += P[(size_t)c * GL + gl];
                     acc = lane_sum<GL>(acc);
-                    if (s == 0) finish(r, own_of(r), acc);
+                    if (s == 0) finish_row(r, acc);
                 }
             }
         } else {
@@ -291,13 +297,14 @@ __global__ __launch_bounds__(kRunThreads) void run_kernel(sbf::Tail tl, int n, d
                 double acc = 0.0;
                 for (int c = tl.rchunk[r] + s; c < tl.rchunk[r + 1]; c += S) acc += part(chunk_of(c, tmp));
                 acc = lane_sum<GL>(acc);
-                if (s == 0) finish(r, own_of(r), acc);
+                if (s == 0) finish_row(r, acc);
             }
         }
         cur = nxt;
         curc = nxtc;
         curr = nxtr;
         curo = nxto;
+        curd = nxtd;
         if (LDSW) lds_barrier();
         else __syncthreads();
     }
