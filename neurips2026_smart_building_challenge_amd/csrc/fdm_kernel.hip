@@ -164,7 +164,10 @@ __global__ __launch_bounds__(kRunThreads) void run_kernel(sbf::Tail tl, int n, d
     double* Wb = W + (size_t)b * n * GL;
     double* Wt = lds;
     double* P = LDSW ? lds + (size_t)tl.m * GL : lds;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wavefront index through readfirstlane: a row taken by a whole
+    // wavefront is then known to be wave-uniform, so its chunk bounds and
+    // metadata are read with scalar loads
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int gl = tid % GL, slot = tid / GL;
     const int s = lane / GL;
     if (LDSW)

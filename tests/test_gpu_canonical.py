@@ -56,7 +56,7 @@ def _state_close(g, c, where):
     m = len(c)
     g = g[:m]
     fin = ~np.isnan(g)
-    err = np.abs(g[fin] - c[fin]) / np.maximum(np.abs(c[fin]), 1.0)
+    err = np.abs(g[fin] - c[fin]) / np.maximum(np.abs(c[fin]), 1e-6)
     assert err.max() <= 1e-9, f"{where}: state rel err {err.max():.3e}"
 
 

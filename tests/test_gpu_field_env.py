@@ -135,7 +135,7 @@ def run_against_oracle(vec, twins, steps, exact: bool, tag: str):
             else:
                 obs_close(obs[tw.i], tw, ob, where)
                 assert abs(float(rew[tw.i]) - r) <= 2 * np.spacing(np.float32(abs(r))) + 1e-12, f"{where}: reward"
-                err = np.abs(gs - cs) / np.maximum(np.abs(cs), 1.0)
+                err = np.abs(gs - cs) / np.maximum(np.abs(cs), 1e-6)
                 assert err.max() <= STATE_RTOL, f"{where}: state rel err {err.max():.3e} at {err.argmax()}"
     return done_seen
 
@@ -224,7 +224,7 @@ def test_gpu_field_env_mixed_with_rc(small_blob, tmp_path):
             cs = tw.cpu.state()
             gs = vec.state(tw.i)[:cs.size]
             fin = ~np.isnan(gs)
-            err = np.abs(gs[fin] - cs[fin]) / np.maximum(np.abs(cs[fin]), 1.0)
+            err = np.abs(gs[fin] - cs[fin]) / np.maximum(np.abs(cs[fin]), 1e-6)
             assert err.max() <= STATE_RTOL, f"{where}: state rel err {err.max():.3e}"
             assert abs(float(rew[tw.i]) - r) <= 4 * np.spacing(np.float32(abs(r))) + 1e-12, where
     vec.close()

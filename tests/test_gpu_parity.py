@@ -3,7 +3,8 @@
 Bars (from the hot-path contract):
   - action generation, reset observations, action decode and observation
     indexing: bit-exact;
-  - fp64 physics: per-step state within 1e-9 relative; 8,640-step episode
+  - fp64 physics: per-step state within 1e-9 relative (denominator
+    max(|oracle|, 1e-6): relative for every value above 1e-6); 8,640-step episode
     reward totals within 1e-6 relative (also against the reference core's
     total stored in the golden fixtures);
   - observations computed from physics: equal up to the float32 quantization
@@ -38,6 +39,10 @@ from neurips2026_smart_building_challenge_amd.scenario.sbb import read_sbb  # no
 
 SEED = 424242
 STATE_RTOL = 1e-9
+# the relative bound's floor: values at or above it are held to STATE_RTOL
+# relative, smaller ones (exact zeros of the oracle among them) to
+# STATE_RTOL * STATE_FLOOR absolute
+STATE_FLOOR = 1e-6
 
 
 def say(msg: str) -> None:
@@ -121,7 +126,7 @@ def state_close(gs: np.ndarray, cs: np.ndarray, where: str) -> None:
     m = len(cs)
     g = gs[:m]
     fin = ~np.isnan(g)
-    err = np.abs(g[fin] - cs[fin]) / np.maximum(np.abs(cs[fin]), 1.0)
+    err = np.abs(g[fin] - cs[fin]) / np.maximum(np.abs(cs[fin]), STATE_FLOOR)
     assert err.max() <= STATE_RTOL, f"{where}: state rel err {err.max():.3e} at {np.nonzero(fin)[0][err.argmax()]}"
 
 

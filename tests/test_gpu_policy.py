@@ -123,7 +123,7 @@ def test_gpu_policy_rollout_parity(mixed_dir):
                 g, c = vec.state(i), t.state()
                 g = g[:len(c)]
                 fin = ~np.isnan(g)
-                rel = np.abs(g[fin] - c[fin]) / np.maximum(np.abs(c[fin]), 1.0)
+                rel = np.abs(g[fin] - c[fin]) / np.maximum(np.abs(c[fin]), 1e-6)
                 assert rel.max() <= 1e-9, (s, i, rel.max())
     vec.close()
 
