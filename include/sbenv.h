@@ -417,8 +417,8 @@ typedef struct {
  * each row's terms spread over lanes; row sums are formed in another order,
  * so results agree with the reference to rounding, far inside 1e-9
  * relative. SBX_FDM_EXACT: every level from HBM in the reference's order,
- * bit-identical results. envs_per_block 0 picks 1 (default) or up to 64
- * (exact). The default mode also takes the air-side correction from the
+ * bit-identical results. envs_per_block 0 picks 1 (default; 2 when there
+ * are more envs than the GPU has compute units) or up to 64 (exact). The default mode also takes the air-side correction from the
  * responses of the applied columns (sbx_fdm_air_responses) instead of a
  * second solve per step. */
 #define SBX_FDM_EXACT 1
