@@ -69,9 +69,11 @@ enum { SOLVER_LU = 0, SOLVER_RELAX = 1 };
 // covers the tiles whose layouts use that form.
 enum { KV_LU = 0, KV_POINT = 1, KV_BLOCK = 2, KV_COUNT = 3 };
 // PI_FIRST_DONE: 1 once the env's first episode after puf_vec_create has
-// ended (puf_reset leaves it; the first episode is the one desync truncates)
+// ended (puf_reset leaves it; the first episode is the one desync truncates).
+// PI_EP_RET, PI_EP_MEAN (float bits): the episode's running return and mean
+// reward when the log is written at episode ends only (env key log_at_end)
 enum { PI_HWS_RUN = 0, PI_PUMP_RUN, PI_HWS_REQ, PI_STEP_INDEX, PI_STEP, PI_MT_IDX,
-       PI_STEPS_TOTAL, PI_EPISODES, PI_CONV_IDX, PI_FIRST_DONE, PI_COUNT = 16 };
+       PI_STEPS_TOTAL, PI_EPISODES, PI_CONV_IDX, PI_FIRST_DONE, PI_EP_RET, PI_EP_MEAN, PI_COUNT = 16 };
 
 // Per-env LDS region (byte offsets from the env's base; a workgroup holds the
 // layout image first, then one region per env).
@@ -346,6 +348,7 @@ struct KParams {
     unsigned long long* phase_ts;   // null, or [n_envs * SBK_NSTAMP] wall-clock stamps
     unsigned long long* pass_ts;    // null, or [n_pass + 1] shader-clock stamps of one env
     int pass_ts_env;                // env whose solve passes are stamped
+    int log_at_end;                 // 1: the host Log only at episode ends, running sums in the record
 };
 
 // The host (g++) and the device (hipcc) compile these structs separately and
@@ -361,6 +364,6 @@ static_assert(sizeof(DevLayout) == 888 && offsetof(DevLayout, st) == 88 && offse
 static_assert(sizeof(DevScen) == 472 && offsetof(DevScen, img_src) == 32 && offsetof(DevScen, gas_co2) == 200
               && offsetof(DevScen, conv_p) == 464, "DevScen layout");
 static_assert(sizeof(KParams) == 136 && offsetof(KParams, host_env) == 80 && offsetof(KParams, phase_ts) == 112
-              && offsetof(KParams, pass_ts_env) == 128, "KParams layout");
+              && offsetof(KParams, pass_ts_env) == 128 && offsetof(KParams, log_at_end) == 132, "KParams layout");
 
 }  // namespace sbk

@@ -2587,7 +2587,7 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
         // the tables is enough there
         const int n1 = c.S->n1;
         const RowVals next = row_issue<W>(c, min(kk + 1, n1 - 1), min(j + 1, n1 - 1));
-        if (P.host_env && ln() == 0) {
+        if (P.host_env && !P.log_at_end && ln() == 0) {
             const Log* hlog = reinterpret_cast<const Log*>(reinterpret_cast<const unsigned char*>(P.host_env)
                                                            + (size_t)c.e * P.env_stride + P.log_offset);
             const float* lp = &hlog->episode_return;
@@ -2631,10 +2631,13 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
 // One workgroup per tile of E envs of one layout, two wavefronts per env:
 // wavefronts [0, E) step the envs, wavefronts [E, 2E) are their helpers (the
 // helper of env slot s is wavefront E + (s + E - E/2) % E, on another SIMD
-// than its env's first wavefront).
-template <int W, int KV>
-__global__ __launch_bounds__(512) void step_kernel(KParams P) {
+// than its env's first wavefront). LE: KParams::log_at_end as a compile-time
+// constant, so each log form compiles without the other's code.
+template <int W, int KV, bool LE>
+__global__ __launch_bounds__(512) void step_kernel(KParams P0) {
     static_assert(W == 64, "one wavefront per env");
+    KParams P = P0;
+    P.log_at_end = LE ? 1 : 0;
     extern __shared__ __align__(16) unsigned char lds[];
     const unsigned long long t_entry = P.phase_ts ? wall_clock64() : 0ull;
     const SBK_C Tile& tl = P.tiles[blockIdx.x];
@@ -2779,16 +2782,34 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
                 c.ip[PI_EPISODES] += 1;
                 c.ip[PI_FIRST_DONE] = 1;
             }
-            if (P.host_env && !cut) {
+            // log_at_end: the episode's running return and mean in the record
+            // (the CPU env's per-step arithmetic), added to the host Log when
+            // the episode ends, so the step reads nothing over the host link
+            float er = 0.0f, em = 0.0f;
+            if (P.log_at_end) {
+                float* ep = reinterpret_cast<float*>(c.ip + PI_EP_RET);
+                er = ep[0] + r;
+                em = ep[1] + (r - ep[1]) / (float)step;
+                ep[0] = done ? 0.0f : er;
+                ep[1] = done ? 0.0f : em;
+            }
+            if (P.host_env && !cut && (!P.log_at_end || done)) {
                 Log* hlog = reinterpret_cast<Log*>(reinterpret_cast<unsigned char*>(P.host_env)
                                                    + (size_t)e * P.env_stride + P.log_offset);
-                const float* lg = reinterpret_cast<const float*>(sy + SY_LOG);
-                float ret = lg[0] + r;
-                float mean = lg[1] + (r - lg[1]) / (float)step;
+                float ret, mean, m;
+                if (P.log_at_end) {
+                    ret = __hip_atomic_load(&hlog->episode_return, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) + er;
+                    mean = __hip_atomic_load(&hlog->reward_mean, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) + em;
+                    m = er / (float)step;
+                } else {
+                    const float* lg = reinterpret_cast<const float*>(sy + SY_LOG);
+                    ret = lg[0] + r;
+                    mean = lg[1] + (r - lg[1]) / (float)step;
+                    m = ret / (float)step;
+                }
                 __hip_atomic_store(&hlog->episode_return, ret, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
                 __hip_atomic_store(&hlog->reward_mean, mean, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
                 if (done) {
-                    float m = ret / (float)step;
                     float* lf = reinterpret_cast<float*>(hlog);
                     float perf = __hip_atomic_load(&lf[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
                     float score = __hip_atomic_load(&lf[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -2809,6 +2830,8 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P) {
             c.ip[PI_STEP] = 0;
             c.ip[PI_STEPS_TOTAL] = 0;
             c.ip[PI_EPISODES] = 0;
+            c.ip[PI_EP_RET] = 0;
+            c.ip[PI_EP_MEAN] = 0;
             c.plant[PF_REW_SUM] = 0.0;
         }
     }
@@ -2896,13 +2919,20 @@ extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int threads,
                                hipStream_t s) {
     using namespace sbk;
     if (threads < 128 || threads > 512 || threads % 128) return (int)hipErrorInvalidValue;
+    const dim3 g(n_blocks), b(threads);
+    const bool le = p->log_at_end != 0;
     switch (variant) {
-    case KV_LU: hipLaunchKernelGGL((step_kernel<64, KV_LU>), dim3(n_blocks), dim3(threads), lds_bytes, s, *p); break;
+    case KV_LU:
+        if (le) hipLaunchKernelGGL((step_kernel<64, KV_LU, true>), g, b, lds_bytes, s, *p);
+        else hipLaunchKernelGGL((step_kernel<64, KV_LU, false>), g, b, lds_bytes, s, *p);
+        break;
     case KV_POINT:
-        hipLaunchKernelGGL((step_kernel<64, KV_POINT>), dim3(n_blocks), dim3(threads), lds_bytes, s, *p);
+        if (le) hipLaunchKernelGGL((step_kernel<64, KV_POINT, true>), g, b, lds_bytes, s, *p);
+        else hipLaunchKernelGGL((step_kernel<64, KV_POINT, false>), g, b, lds_bytes, s, *p);
         break;
     case KV_BLOCK:
-        hipLaunchKernelGGL((step_kernel<64, KV_BLOCK>), dim3(n_blocks), dim3(threads), lds_bytes, s, *p);
+        if (le) hipLaunchKernelGGL((step_kernel<64, KV_BLOCK, true>), g, b, lds_bytes, s, *p);
+        else hipLaunchKernelGGL((step_kernel<64, KV_BLOCK, false>), g, b, lds_bytes, s, *p);
         break;
     default: return (int)hipErrorInvalidValue;
     }
@@ -2912,8 +2942,10 @@ extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int threads,
 extern "C" int sbk_set_lds_limit(int width, int bytes) {
     using namespace sbk;
     if (width != 64) return (int)hipErrorInvalidValue;
-    const void* fns[KV_COUNT] = {(const void*)step_kernel<64, KV_LU>, (const void*)step_kernel<64, KV_POINT>,
-                                 (const void*)step_kernel<64, KV_BLOCK>};
+    const void* fns[2 * KV_COUNT] = {
+        (const void*)step_kernel<64, KV_LU, false>, (const void*)step_kernel<64, KV_POINT, false>,
+        (const void*)step_kernel<64, KV_BLOCK, false>, (const void*)step_kernel<64, KV_LU, true>,
+        (const void*)step_kernel<64, KV_POINT, true>, (const void*)step_kernel<64, KV_BLOCK, true>};
     for (const void* f : fns) {
         const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
         if (e != hipSuccess) return (int)e;

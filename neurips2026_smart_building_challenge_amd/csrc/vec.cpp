@@ -1052,6 +1052,7 @@ struct Vec {
     std::vector<TileGroup> groups;            // consecutive tiles of one kernel variant
     sbk::Tile* d_tiles = nullptr;
     float reward_scale = 1.0f;
+    int log_at_end = 0;                       // env key log_at_end: the host Log at episode ends only
     Env* envs = nullptr;
     std::vector<std::string> paths;           // ordered scenario list
     std::vector<HostLayout> layouts;
@@ -1122,6 +1123,7 @@ sbk::KParams params(Vec* v, int mode) {
     p.n_envs = v->n;
     p.mode = mode;
     p.reward_scale = v->reward_scale;
+    p.log_at_end = v->log_at_end;
     return p;
 }
 
@@ -1307,6 +1309,13 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
         const float rs = kw(kwargs, "reward_scale", 1.0f);
         v->reward_scale = rs > 0.0f ? rs : 1.0f;
     }
+    // log_at_end = 1: each env's running episode return and mean reward stay
+    // in its device record and are added to its host Log when the episode
+    // ends (as the reference GPU env fills Log at episode ends,
+    // complete_port/gpu/smart_buildings.cu:123-125), so puf_step reads no host
+    // memory; 0 (default): the CPU env's per-step Log, read and written every
+    // step (pufferlib_cpu_env.h:247-248), which sees a trainer's mid-episode clears
+    v->log_at_end = (int)kw(kwargs, "log_at_end", 0.0f) != 0;
     check_env_keys(kwargs);
     // ---- scenario list
     std::vector<std::string> files;
@@ -1378,6 +1387,7 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
             S.path = files[i];
             S.layout = li;
             S.field = (int)v->fields.size();
+            if (v->log_at_end) die("env.log_at_end applies to RC layouts only (a field scenario logs every step)");
             S.n1 = fc.n1;
             S.episode_steps = fc.episode_steps;
             S.occ_seed = fc.occ_seed;

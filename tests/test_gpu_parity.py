@@ -664,3 +664,53 @@ def test_gpu_decode_edge_values(cfg0_dir):
             if tw.i < 2:
                 state_close(gs, cs, f"decode edges step {s} env {tw.i}")
     vec.close()
+
+
+def test_gpu_log_at_end(mixed_dir):
+    """log_at_end = 1: each env's running episode return and mean reward stay in
+    its record and reach the host Log only when an episode ends (desync-cut
+    first episodes excluded). The Log after 100 steps against the same float32
+    arithmetic replayed on the host from the rewards and terminals the vec
+    returned; the episode count and lengths exactly."""
+    say("log at episode ends: 60 envs, 100 steps")
+    vec = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=40, desync=1, log_at_end=1)
+    firsts = [po.desync_first_steps(i, 40) for i in range(vec.n)]
+    vec.reset()
+    f32 = np.float32
+    run = np.zeros((vec.n, 2), np.float32)   # running return, mean
+    steps = np.zeros(vec.n, np.int64)
+    first = np.ones(vec.n, bool)
+    want = {k: np.zeros(vec.n, np.float32) for k in ("perf", "score", "episode_return", "episode_length",
+                                                        "reward_mean", "n")}
+    for s in range(100):
+        vec.gen_actions(SEED, s)
+        vec.step()
+        r = vec.rewards.cpu().numpy()
+        term = vec.terminals.cpu().numpy()
+        for i in range(vec.n):
+            steps[i] += 1
+            st = f32(steps[i])
+            er = f32(run[i, 0] + r[i])
+            em = f32(run[i, 1] + f32(f32(r[i] - run[i, 1]) / st))
+            run[i] = (er, em)
+            if term[i]:
+                assert steps[i] == (firsts[i] if first[i] else 40), (i, s, steps[i])
+                if not (first[i] and firsts[i] < 40):
+                    m = f32(er / st)
+                    want["perf"][i] = f32(want["perf"][i] + m)
+                    want["score"][i] = f32(want["score"][i] + m)
+                    want["episode_return"][i] = f32(want["episode_return"][i] + er)
+                    want["reward_mean"][i] = f32(want["reward_mean"][i] + em)
+                    want["episode_length"][i] = f32(want["episode_length"][i] + st)
+                    want["n"][i] = f32(want["n"][i] + 1)
+                run[i] = 0.0
+                steps[i] = 0
+                first[i] = False
+    torch.cuda.synchronize()
+    for i in range(vec.n):
+        got = vec.log(i)
+        assert got["n"] == want["n"][i] and got["episode_length"] == want["episode_length"][i], (i, got)
+        for k in ("perf", "score", "episode_return", "reward_mean"):
+            assert abs(got[k] - float(want[k][i])) <= 1e-6 * max(1.0, abs(float(want[k][i]))), (i, k, got, want[k][i])
+    assert sum(vec.log(i)["n"] for i in range(vec.n)) > 60
+    vec.close()
