@@ -117,7 +117,12 @@ void dict_set(Dict* d, const char* key, float value);
  * Extras: start_offsets (1: every env starts its episodes at its own seeded
  * calendar offset, start_seed), shard_base (this vec's first env index in a
  * batch sharded over several vecs), per_env_seed (occupancy / convection seed
- * + index within the scenario, default 1), solver, envs_per_block. */
+ * + index within the scenario, default 1), solver, envs_per_block, log_at_end
+ * (1: each env's running episode return and mean reward stay on the device
+ * and are added to its Log when the episode ends, as the reference GPU env
+ * fills Log at episode ends (smart_buildings.cu:123-125), so puf_step reads no
+ * host memory; 0, the default: the CPU env's per-step Log, read and written
+ * every step, which sees a trainer's mid-episode clears; RC layouts only). */
 Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions,
                     float* rewards, float* terminals);
 /* NULL binds the null stream (the binding before any call); the reference
