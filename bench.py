@@ -285,6 +285,69 @@ def field_env_leg(envs: int, steps: int, cpu: bool, cpu_threads: int) -> dict:
     return rec
 
 
+def config_leg(config: int, steps: int, warmup: int) -> dict:
+    """One other BASELINE config (index 0, 2, 3 or 4) timed the headline's way:
+    action rows of every timed step drawn before the timed region (config 4:
+    the shared-policy forward + Beta sampling, then puf_step, each step), the
+    env step's mean duration over the timed region. Reported beside the
+    headline so every config is timed by the same run."""
+    import torch
+
+    from neurips2026_smart_building_challenge_amd import env as E
+    from neurips2026_smart_building_challenge_amd.scenario import generate as G
+
+    scen, n_envs, offsets = G.config_scenarios(config)
+    groups = len(scen)
+    blob_dir = scenario_dir(config)
+    vec = E.VecEnv(n_envs, blob_dir=str(blob_dir), groups=groups, start_offsets=int(offsets))
+    info = vec.info()
+    rollout = config == 4
+    if rollout:
+        vec.policy_bind(E.policy_weights(SEED))
+    vec.reset()
+    for s in range(warmup):
+        if rollout:
+            vec.policy_act(SEED, s)
+        else:
+            vec.gen_actions(SEED, s)
+        vec.step()
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    bank = None
+    if not rollout:
+        bank = torch.empty((steps, n_envs, E.SB_ACT), dtype=torch.float32, device="cuda")
+        for s in range(steps):
+            vec.gen_actions(SEED, warmup + s)
+            bank[s].copy_(vec.actions)
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    for s in range(steps):
+        if rollout:
+            vec.policy_act(SEED, warmup + s)
+            vec.step()
+        else:
+            vec.step_actions(bank[s])
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1)
+    vec.close()
+    del bank
+    us = ms / steps * 1e3
+    value = n_envs * steps / (ms / 1e3)
+    ach = info.bytes_per_step / (us * 1e-6) / 1e9
+    rec = {"config": config, "n_envs": n_envs, "scenarios": groups, "steps": steps, "warmup": warmup,
+           "workload": f"BASELINE config {config}: {n_envs} envs, {groups} scenarios"
+                       + (", desynchronised starts" if offsets else "")
+                       + (", shared-policy MLP + Beta sampling then puf_step per step" if rollout
+                          else ", Beta(2,2) action rows resident, puf_step per step"),
+           "ms_per_step": ms / steps, "value": value, "unit": "env-steps/s",
+           "roofline": None if rollout else {"bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                              "frac": ach / HBM_PEAK_GBS, "kernel_us": us,
+                                              "algorithmic_bytes": info.bytes_per_step}}
+    log(f"config {config}: {us:.1f} us/step over {steps} steps, {value:.4g} env-steps/s")
+    return rec
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -307,6 +370,11 @@ def main() -> int:
     ap.add_argument("--field-env-envs", type=int, default=256,
                     help="envs of the FDM-scale env-scenario record (0: skip)")
     ap.add_argument("--field-env-only", action="store_true", help="only the FDM-scale env-scenario record")
+    ap.add_argument("--other-configs", type=str, default="0,2,3,4",
+                    help="comma-separated other BASELINE configs timed after the headline (config 1 runs only); "
+                         "'' for none")
+    ap.add_argument("--other-steps", type=int, default=200,
+                    help="timed steps of each other config (at most --steps)")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain device copy of 256 MiB 10 times (counter calibration)")
     args = ap.parse_args()
@@ -463,6 +531,12 @@ def main() -> int:
         field_env = with_more_envs(field_env_leg, args.field_env_envs, not args.no_cpu,
                                    min(16, len(os.sched_getaffinity(0))), more)
 
+    others = []
+    if args.config == 1 and args.conv <= 0:
+        for c in (int(x) for x in args.other_configs.split(",") if x.strip()):
+            if c != 1:
+                others.append(config_leg(c, max(1, min(args.steps, args.other_steps)), min(args.warmup, 20)))
+
     out = {
         "metric": METRIC, "value": value, "unit": "env-steps/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
@@ -491,6 +565,7 @@ def main() -> int:
         "lu": lu,
         "fdm": fdm,
         "field_env": field_env,
+        "other_configs": others,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -245,7 +245,8 @@ typedef struct SbxPolicy {
     const float* b3;
     float beta_floor;   /* shape floor f: a = softplus(u) + f (the reference's policy.beta_floor);
                            1 gives shapes >= 1, below 1 shapes may fall under 1 (boosted gamma
-                           draws); finite, >= 0 */
+                           draws); finite and > 0, as the reference trainer requires
+                           (pufferlib_core.diff:5204-5208); -1 otherwise */
 } SbxPolicy;
 int sbx_policy_bind(Env* envs, const SbxPolicy* p);
 int sbx_policy_act(Env* envs, uint64_t seed, uint32_t step);
@@ -303,7 +304,7 @@ typedef struct SbxPpo {
     float clip_coef;
     float ent_coef;
     int ratio_per_dim;
-    float beta_floor;
+    float beta_floor;   /* finite and > 0 (as SbxPolicy.beta_floor) */
 } SbxPpo;
 int sbx_ppo_beta(Env* envs, const float* y_new, const float* y_old, const float* draws, const float* logp_old,
                  const float* adv, const SbxPpo* args, float* out, float* grad);

@@ -14,6 +14,7 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
@@ -35,6 +36,10 @@ HIP_FLAGS = [
 EXTRA = {"fdm_kernel.hip": ["-ffp-contract=off"], "field_env_kernel.hip": ["-ffp-contract=off"]}
 
 
+HIP_SOURCES = ["step_kernel.hip", "policy_kernel.hip", "canon_kernel.hip", "fdm_kernel.hip", "field_env_kernel.hip"]
+HOST_SOURCES = ["vec.cpp", "plan.cpp", "sbb_reader.cpp", "fdm.cpp", "field_env.cpp"]
+
+
 def _run(cmd: list[str], cwd: Path | None = None) -> None:
     r = subprocess.run(cmd, cwd=cwd, capture_output=True, text=True)
     if r.returncode != 0:
@@ -44,21 +49,24 @@ def _run(cmd: list[str], cwd: Path | None = None) -> None:
 
 def build_product() -> Path:
     hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
-    objs = []
     tmp = PKG / "_build"
     tmp.mkdir(exist_ok=True)
     inc = ["-I", str(ROOT / "include"), "-I", str(CSRC)]
-    for src in ["step_kernel.hip", "policy_kernel.hip", "canon_kernel.hip", "fdm_kernel.hip", "field_env_kernel.hip"]:
-        o = tmp / (Path(src).stem + ".o")
-        _run([hipcc, *HIP_FLAGS, *EXTRA.get(src, []), *inc, "-c", str(CSRC / src), "-o", str(o)])
-        objs.append(o)
     rocm = Path(hipcc).resolve().parent.parent
-    for src in ["vec.cpp", "plan.cpp", "sbb_reader.cpp", "fdm.cpp", "field_env.cpp"]:
+    jobs = []   # (command, object): every translation unit compiles independently
+    for src in HIP_SOURCES:
+        o = tmp / (Path(src).stem + ".o")
+        jobs.append(([hipcc, *HIP_FLAGS, *EXTRA.get(src, []), *inc, "-c", str(CSRC / src), "-o", str(o)], o))
+    for src in HOST_SOURCES:
         # host-only C++ (HIP runtime API calls, no device code)
         o = tmp / (Path(src).stem + ".o")
-        _run(["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__",
-              "-I", str(rocm / "include"), *inc, "-c", str(CSRC / src), "-o", str(o)])
-        objs.append(o)
+        jobs.append((["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__",
+                      "-I", str(rocm / "include"), *inc, "-c", str(CSRC / src), "-o", str(o)], o))
+    workers = max(1, min(len(jobs), os.cpu_count() or 1, 8))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        for f in [pool.submit(_run, cmd) for cmd, _ in jobs]:
+            f.result()
+    objs = [o for _, o in jobs]
     out_tmp = LIB.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(out_tmp)])
     out_tmp.replace(LIB)

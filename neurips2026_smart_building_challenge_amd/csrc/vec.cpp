@@ -2014,16 +2014,19 @@ float sbx_time_step(Env* envs, int iters) {
 
 static bool policy_ok(const SbxPolicy* p) {
     if (!p || !p->w1 || !p->b1 || !p->w2 || !p->b2 || !p->w3 || !p->b3) { g_err = "null policy weight"; return false; }
-    if (!(p->beta_floor >= 0.0f) || !std::isfinite(p->beta_floor)) {
-        g_err = "policy beta_floor must be finite and >= 0";
+    // the reference trainer aborts unless policy.beta_floor > 0
+    // (complete_port/patches/pufferlib_core.diff:5204-5208): at 0 a shape can
+    // underflow to exactly 0, where lgamma and the boosted draw give inf/NaN
+    if (!(p->beta_floor > 0.0f) || !std::isfinite(p->beta_floor)) {
+        g_err = "policy beta_floor must be finite and > 0";
         return false;
     }
     return true;
 }
 
 int sbx_policy_bind(Env* envs, const SbxPolicy* p) {
-    Vec* v = vec_of(envs);
     if (!policy_ok(p)) return -1;
+    Vec* v = vec_of(envs);
     v->pol = *p;
     if (!v->p_h1) {
         hip_ok(hipMalloc(&v->p_h1, sizeof(float) * (size_t)v->n * SBX_POLICY_HIDDEN), "hipMalloc(policy)");
@@ -2047,8 +2050,8 @@ int sbx_policy_act(Env* envs, uint64_t seed, uint32_t step) {
 }
 
 int sbx_policy_act_noalloc(Env* envs, const SbxPolicy* p, uint64_t seed, uint32_t step) {
-    Vec* v = vec_of(envs);
     if (!policy_ok(p)) return -1;
+    Vec* v = vec_of(envs);
     if (v->n > sbk_noalloc_max_envs()) {
         g_err = "sbx_policy_act_noalloc: " + std::to_string(v->n) + " envs, at most "
                 + std::to_string(sbk_noalloc_max_envs());
@@ -2087,15 +2090,15 @@ int sbx_beta_eval(Env* envs, const float* y, const float* draws, float* logp, fl
 
 int sbx_ppo_beta(Env* envs, const float* y_new, const float* y_old, const float* draws, const float* logp_old,
                  const float* adv, const SbxPpo* args, float* out, float* grad) {
-    Vec* v = vec_of(envs);
     if (!y_new || !y_old || !draws || !logp_old || !adv || !args || !out) {
         g_err = "sbx_ppo_beta: null argument";
         return -1;
     }
-    if (!(args->beta_floor >= 0.0f) || !std::isfinite(args->beta_floor) || !(args->clip_coef >= 0.0f)) {
-        g_err = "sbx_ppo_beta: beta_floor and clip_coef must be >= 0";
+    if (!(args->beta_floor > 0.0f) || !std::isfinite(args->beta_floor) || !(args->clip_coef >= 0.0f)) {
+        g_err = "sbx_ppo_beta: beta_floor must be finite and > 0, clip_coef >= 0";
         return -1;
     }
+    Vec* v = vec_of(envs);
     int rc = sbk_launch_ppo_beta(y_new, y_old, draws, logp_old, adv, v->d_ncont, v->d_ndisc, v->n, args->beta_floor,
                                  args->clip_coef, args->ent_coef, args->ratio_per_dim, out, grad, g_stream);
     if (rc != 0) die(std::string("ppo beta launch failed: ") + hipGetErrorString((hipError_t)rc));

@@ -86,3 +86,20 @@ def test_canonical_rejects_buildings_beyond_the_slots(tmp_path):
         r = subprocess.run([sys.executable, "-c", code.format(blob=str(paths[0]), extra=extra)], cwd=root,
                            capture_output=True, text=True, timeout=120)
         assert r.returncode != 0 and "created" not in r.stdout and msg in r.stderr, (extra, r.stderr)
+
+
+def test_beta_floor_must_be_positive():
+    """A shape floor of 0 (or below, or non-finite) is refused with -1 and a message
+    before the env array is read, as the reference trainer aborts unless
+    policy.beta_floor > 0 (pufferlib_core.diff:5204-5208): at 0 a shape can
+    underflow to exactly 0, where the log-density and the boosted draw are NaN."""
+    L = E.lib()
+    for bad in (0.0, -0.5, float("nan"), float("inf")):
+        p = E.SbxPolicy(*([64] * 6), bad)
+        assert L.sbx_policy_bind(None, ctypes.byref(p)) == -1
+        assert b"beta_floor" in L.sbx_last_error()
+        assert L.sbx_policy_act_noalloc(None, ctypes.byref(p), 1, 0) == -1
+        ppo = E.SbxPpo(0.2, 0.01, 1, bad)
+        buf = ctypes.c_void_p(64)
+        assert L.sbx_ppo_beta(None, buf, buf, buf, buf, buf, ctypes.byref(ppo), buf, buf) == -1
+        assert b"beta_floor" in L.sbx_last_error()
