@@ -8,6 +8,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <map>
 #include <string>
 #include <vector>
 
@@ -17,8 +18,7 @@
 #include "sbenv.h"
 
 extern "C" int sbe_launch(const sbe::Args* a, int which, hipStream_t s);
-extern "C" int sbe_launch_field_reset(double* T, double* M, int n_cvs, int n, int G, int Gl, const int* mask,
-                                      const double* temp_init, const double* mass_init, hipStream_t s);
+extern "C" int sbe_lds_limit(int bytes);
 extern "C" SbxFdm* sbx_fdm_open(const char* blob_path, int n_envs, int envs_per_block, int flags);
 extern "C" void sbx_fdm_close(SbxFdm* f);
 extern "C" const char* sbx_last_error(void);
@@ -60,7 +60,13 @@ struct FieldScen {
     sbe::Slot* d_slots = nullptr;
     unsigned char* d_state = nullptr;
     double *d_qz = nullptr, *d_amb = nullptr, *d_hh = nullptr, *d_g = nullptr, *d_airT = nullptr;
-    int* d_mask = nullptr;
+    int lds_bytes = 0;            // the HVAC kernels' dynamic LDS
+    // convection: the step's moves, their count and values, pair overflow
+    unsigned long long* d_moves = nullptr;
+    int* d_count = nullptr;
+    double* d_vals = nullptr;
+    unsigned int* d_spill = nullptr;
+    int lds_pairs = 0;
     SbxFdm* fdm = nullptr;
 };
 
@@ -147,6 +153,28 @@ FieldScen* field_open(const sbh::Blob& b, std::string* err) {
         for (int q = 0; q < na; q++)
             if (!(at[q] > 0.0)) return bad("an AHU serves no zone area (not supported for field scenarios)");
     }
+    // each AHU's VAVs and columns in ascending order; each zone's heating
+    // columns in column order (a column heats every zone of its VAV)
+    std::vector<int> av_off(1, 0), av_idx, ac_off(1, 0), ac_idx, zc_off(1, 0), zc_idx;
+    {
+        std::vector<std::vector<int>> zc(nz);
+        for (int col = 0; col < k; col++) {
+            const int v = coupled[col];
+            for (int q = vz_off[v]; q < vz_off[v + 1]; q++) zc[vz_idx[q]].push_back(col);
+        }
+        for (int q = 0; q < na; q++) {
+            for (int v = 0; v < nv; v++)
+                if (vav_ahu[v] == q) av_idx.push_back(v);
+            av_off.push_back((int)av_idx.size());
+            for (int col = 0; col < k; col++)
+                if (vav_ahu[coupled[col]] == q) ac_idx.push_back(col);
+            ac_off.push_back((int)ac_idx.size());
+        }
+        for (int z = 0; z < nz; z++) {
+            zc_idx.insert(zc_idx.end(), zc[z].begin(), zc[z].end());
+            zc_off.push_back((int)zc_idx.size());
+        }
+    }
     // zones -> their room's cells, in the room's order; zone means of temp_init
     const double* tinit = b.f64("temp_init", &c);
     if (!tinit || (int64_t)c != f.t.n_cvs) return bad("temp_init missing");
@@ -168,8 +196,62 @@ FieldScen* field_open(const sbh::Blob& b, std::string* err) {
         zoff.push_back((int)zcells.size());
         zm[z] = sum / (double)(zoff[z + 1] - zoff[z]);
     }
+    // ---- stochastic convection (sb_convect.c:5-31, applied at :39-73): on
+    // when conv_p != 0 and conv_distance != 0; the rooms' candidates must lie
+    // in their own room (the reference baker's tables, bake_scenario.py:162-186)
+    std::vector<int> cv_off(1, 0), cv_cell, cv_coff;
+    std::vector<uint8_t> cv_ncand;
+    std::vector<uint16_t> cv_cidx;
+    const double conv_p = b.f64_1("conv_p", 0.0);
+    const int conv_dist = (int)b.f64_1("conv_distance", -1.0);
+    f.t.cv_max_room = 0;
+    if (conv_p != 0.0 && conv_dist != 0) {
+        uint64_t nco = 0, ncc = 0, ncf = 0, nci = 0;
+        const int32_t* co = b.i32("conv_room_offsets", &nco);
+        const int32_t* cc = b.i32("conv_room_cells", &ncc);
+        const int32_t* cf = b.i32("conv_cand_offsets", &ncf);
+        const int32_t* ci = b.i32("conv_cand_idx", &nci);
+        if (!co || !cc || !cf || !ci || nco < 1) return bad("convection tables missing");
+        const int rooms = (int)nco - 1, cells = co[rooms];
+        if (co[0] != 0 || cells < 0 || 2 * (uint64_t)cells > ncc || ncf != (uint64_t)cells + 1)
+            return bad("convection room tables inconsistent");
+        for (int rm = 0; rm < rooms; rm++) {
+            const int r0 = co[rm], r1 = co[rm + 1];
+            if (r1 < r0) return bad("convection room offsets decrease");
+            if (r1 - r0 > 65535) return bad("a convection room has more than 65535 cells");
+            f.t.cv_max_room = std::max(f.t.cv_max_room, r1 - r0);
+            for (int q = r0; q < r1; q++) {
+                const int r = cc[2 * q], c2 = cc[2 * q + 1];
+                if (r < 0 || r >= nr || c2 < 0 || c2 >= ncol) return bad("convection cell outside the grid");
+                cv_cell.push_back(r * ncol + c2);
+                const int a0 = cf[q], a1 = cf[q + 1];
+                if (a0 < 0 || a1 < a0 || (uint64_t)a1 > nci) return bad("convection candidate offsets inconsistent");
+                if (a1 - a0 > 255) return bad("a convection cell has more than 255 candidates");
+                cv_ncand.push_back((uint8_t)(a1 - a0));
+                for (int x = a0; x < a1; x++) {
+                    if (ci[x] < r0 || ci[x] >= r1) return bad("a convection candidate lies outside its room");
+                    cv_cidx.push_back((uint16_t)(ci[x] - r0));
+                }
+            }
+            cv_off.push_back(r1);
+        }
+        cv_coff.assign(cf, cf + cells + 1);
+        f.t.cv_rooms = rooms;
+        f.t.cv_cells = cells;
+        // csim swaps when its 53-bit draw u / 2^53 <= p (sb_convect.c:47)
+        if (!(conv_p > 0.0)) {
+            f.t.cv_thr_hi = 0xFFFFFFFFu;   // never (p < 0; NaN is refused below)
+            f.t.cv_thr_lo = 0;
+        } else {
+            const uint64_t thr = conv_p >= 1.0 ? (1ull << 53) : (uint64_t)floor(conv_p * 9007199254740992.0);
+            f.t.cv_thr_hi = (uint32_t)(thr >> 32);
+            f.t.cv_thr_lo = (uint32_t)thr;
+        }
+        if (conv_p != conv_p) return bad("conv_p is NaN");
+    }
+    if (cv_coff.empty()) cv_coff.push_back(0);
+    f.c.conv_seed = b.i64_1("conv_seed", 0);
     // ---- features this path does not carry
-    if (b.f64_1("conv_p", 0.0) != 0.0) return bad("stochastic convection is not supported for field scenarios");
     {
         uint64_t cs = 0;
         const double* sc = b.f64("solar_gain_coeff", &cs);
@@ -194,6 +276,23 @@ FieldScen* field_open(const sbh::Blob& b, std::string* err) {
         if (kind[i] < 2 && (aidx[i] < 0 || aidx[i] >= lim)) return bad("action owner index out of range");
     }
     if (ncont > SB_CONT || ndisc > SB_DISC) return bad("scenario has more actions than SB_CONT/SB_DISC");
+    // each action's trainer column and target; the sequential apply
+    // (sb_sim.c:220-244) keeps the last action written to a target
+    std::vector<int> act_col(std::max<uint64_t>(n_act, 1), 0), act_tgt(std::max<uint64_t>(n_act, 1), 0);
+    std::vector<uint8_t> act_live(std::max<uint64_t>(n_act, 1), 0);
+    {
+        int ci = 0, di = 0;
+        std::map<int, int> last;
+        for (uint64_t i = 0; i < n_act; i++) {
+            act_col[i] = disc[i] ? SB_CONT + di++ : ci++;
+            const int kd = kind[i] > 2 ? 2 : kind[i];
+            const int ac = kd == 0 ? std::min<int>(act[i], 3) : (kd == 1 ? (act[i] == 0 ? 0 : 1) : std::min<int>(act[i], 2));
+            const int ix = kd == 2 ? 0 : aidx[i];
+            act_tgt[i] = kd | (ac << 4) | (ix << 8);
+            last[act_tgt[i]] = (int)i;
+        }
+        for (auto& kv : last) act_live[kv.second] = 1;
+    }
     // ---- observation
     const int n_dev = (int)b.i64_1("n_dev", 0), n_aux = (int)b.i64_1("n_aux", 0);
     if (n_aux < 1 || n_dev < 0 || n_dev + n_aux > SB_OBS) return bad("observation size out of range");
@@ -314,24 +413,34 @@ FieldScen* field_open(const sbh::Blob& b, std::string* err) {
     f.c.nz = nz;
     sbe::StateLayout& S = f.st;
     int o = 0;
-    auto f64a = [&](int count) { const int r = o; o += 8 * count; return r; };
-    S.recirc = f64a(na); S.sat = f64a(na); S.fan = f64a(na); S.flow = f64a(na);
-    S.wsum = f64a(na); S.atotal = f64a(na); S.satv = f64a(na);
+    auto f64a = [&](int count) { const int r = o; o += 8 * std::max(count, 1); return r; };
+    S.recirc = f64a(na); S.sat = f64a(na); S.fan = f64a(na); S.flow = f64a(na); S.satv = f64a(na);
     S.damper = f64a(nv); S.reheat = f64a(nv); S.ratio = f64a(nv); S.heatsp = f64a(nv); S.coolsp = f64a(nv);
-    S.dcmd = f64a(nv); S.rcmd = f64a(nv); S.sensing = f64a(nv); S.vav_area = f64a(nv);
+    S.dcmd = f64a(nv); S.rcmd = f64a(nv); S.sensing = f64a(nv); S.vav_area = f64a(nv); S.unres = f64a(nv);
     S.avg_temp = f64a(nz); S.zone_q = f64a(nz); S.occV = f64a(nz);
-    S.air_g = f64a(k); S.air_T = f64a(k); S.coil = f64a(k);
+    S.air_g = f64a(k); S.air_T = f64a(k); S.coil = f64a(k); S.rwen = f64a(k);
     S.plant = f64a(sbe::PL_COUNT);
-    auto i32a = [&](int count) { const int r = o; o += 4 * count; return r; };
+    auto i32a = [&](int count) { const int r = o; o += 4 * std::max(count, 1); return r; };
     S.run = i32a(na); S.coolreq = i32a(na);
     S.mode = i32a(nv); S.prev_valid = i32a(nv); S.dcmd_set = i32a(nv); S.rcmd_set = i32a(nv);
     S.ip = i32a(sbe::IP_COUNT);
+    S.ep = i32a(sbe::EP_COUNT);
     S.occ_state = o;
-    o += nz * nassign;
+    o += std::max(nz * nassign, 1);
     o = (o + 15) & ~15;
     S.mt = o;
-    o += 4 * 624;
-    S.bytes = (o + 255) & ~255;
+    o += 4 * SBE_MT_N;
+    S.bytes = (o + 15) & ~15;
+    S.cmt = f.t.cv_rooms > 0 ? S.bytes : 0;
+    S.record = (S.bytes + (S.cmt ? 4 * SBE_MT_N : 0) + 255) & ~255;
+    // the HVAC kernels' LDS: the image, then f64 scratch for the pre-step
+    // (AHU demand, column flow demand), the reward (VAV sums, AHU terms, zone
+    // terms) or one MT block
+    {
+        const int scratch = std::max({8 * (na + k), 8 * (nv + 3 * na + nz), 4 * SBE_MT_N});
+        f.lds_bytes = S.bytes + ((scratch + 15) & ~15);
+        if (f.lds_bytes > 160 * 1024) return bad("an env's HVAC state does not fit in LDS");
+    }
 
     // ---- device tables (host image; pointers patched at attach)
     Arena& A = f.A;
@@ -345,13 +454,19 @@ FieldScen* field_open(const sbh::Blob& b, std::string* err) {
     sec((const void**)&f.t.vz_idx, vz_idx, 4 * std::max<uint64_t>(nvz, 1));
     sec((const void**)&f.t.vav_ahu, vav_ahu, 4 * (size_t)nv);
     sec((const void**)&f.t.coupled, coupled, 4 * (size_t)std::max(k, 1));
+    sec((const void**)&f.t.av_off, av_off.data(), 4 * av_off.size());
+    sec((const void**)&f.t.av_idx, av_idx.data(), 4 * std::max<size_t>(av_idx.size(), 1));
+    sec((const void**)&f.t.ac_off, ac_off.data(), 4 * ac_off.size());
+    sec((const void**)&f.t.ac_idx, ac_idx.data(), 4 * std::max<size_t>(ac_idx.size(), 1));
+    sec((const void**)&f.t.zc_off, zc_off.data(), 4 * zc_off.size());
+    sec((const void**)&f.t.zc_idx, zc_idx.data(), 4 * std::max<size_t>(zc_idx.size(), 1));
     sec((const void**)&f.t.vav_c, vav_c, 8 * 9 * (size_t)nv);
     sec((const void**)&f.t.ahu_c, ahu_c, 8 * 9 * (size_t)na);
     sec((const void**)&f.t.boiler_c, boiler.data(), 8 * boiler.size());
-    sec((const void**)&f.t.act_kind, kind, n_act);
-    sec((const void**)&f.t.act_act, act, n_act);
+    sec((const void**)&f.t.act_col, act_col.data(), 4 * act_col.size());
+    sec((const void**)&f.t.act_tgt, act_tgt.data(), 4 * act_tgt.size());
+    sec((const void**)&f.t.act_live, act_live.data(), act_live.size());
     sec((const void**)&f.t.act_disc, disc, n_act);
-    sec((const void**)&f.t.act_idx, aidx, 4 * n_act);
     sec((const void**)&f.t.act_mn, mn, 8 * n_act);
     sec((const void**)&f.t.act_mx, mx, 8 * n_act);
     sec((const void**)&f.t.act_mnr, mnr, 8 * n_act);
@@ -378,10 +493,56 @@ FieldScen* field_open(const sbh::Blob& b, std::string* err) {
     sec((const void**)&f.t.elec_we, ewe, 8 * 24);
     sec((const void**)&f.t.elec_co2, eco2, 8 * 24);
     sec((const void**)&f.t.gas_price, gp, 8 * 12);
+    sec((const void**)&f.t.temp_init, tinit, 8 * (size_t)f.t.n_cvs);
+    {
+        const double* mi = b.f64("mass_temp_init", &c);
+        if (!mi || c != n_solved) return bad("mass_temp_init missing");
+        sec((const void**)&f.t.mass_init, mi, 8 * (size_t)n_solved);
+    }
+    f.t.n_solved = (int)n_solved;
+    sec((const void**)&f.t.cv_off, cv_off.data(), 4 * cv_off.size());
+    sec((const void**)&f.t.cv_cell, cv_cell.data(), 4 * std::max<size_t>(cv_cell.size(), 1));
+    sec((const void**)&f.t.cv_ncand, cv_ncand.data(), std::max<size_t>(cv_ncand.size(), 1));
+    sec((const void**)&f.t.cv_coff, cv_coff.data(), 4 * cv_coff.size());
+    sec((const void**)&f.t.cv_cidx, cv_cidx.data(), 2 * std::max<size_t>(cv_cidx.size(), 1));
     return F;
 }
 
 FieldCounts field_counts(const FieldScen* f) { return f->c; }
+
+namespace {
+
+// MT19937 initialisation (sb_rng.c:9-16)
+void mt_seed(uint32_t* mt, uint32_t seed) {
+    mt[0] = seed;
+    for (int i = 1; i < SBE_MT_N; i++) mt[i] = 1812433253u * (mt[i - 1] ^ (mt[i - 1] >> 30)) + (uint32_t)i;
+}
+
+sbe::Args base_args(const FieldScen* f) {
+    sbe::Args a{};
+    a.t = f->t;
+    a.st = f->st;
+    a.state = f->d_state;
+    a.slots = f->d_slots;
+    a.G = f->G;
+    a.lds_bytes = f->lds_bytes;
+    a.qz = f->d_qz;
+    a.amb = f->d_amb;
+    a.hh = f->d_hh;
+    a.g = f->d_g;
+    a.airT = f->d_airT;
+    a.T = f->fdm->grp.T;
+    a.M = f->fdm->grp.M;
+    a.Gl = f->fdm->grp.Gl;
+    a.cv_moves = f->d_moves;
+    a.cv_count = f->d_count;
+    a.cv_vals = f->d_vals;
+    a.cv_spill = f->d_spill;
+    a.cv_lds_pairs = f->lds_pairs;
+    return a;
+}
+
+}  // namespace
 
 bool field_attach(FieldScen* f, const std::string& path, const std::vector<sbe::Slot>& slots, int flags,
                   int envs_per_block, std::string* err) {
@@ -397,38 +558,58 @@ bool field_attach(FieldScen* f, const std::string& path, const std::vector<sbe::
     f->A.host.shrink_to_fit();
     f->fdm = sbx_fdm_open(path.c_str(), G, envs_per_block, flags);
     if (!f->fdm) return (*err = std::string("field group: ") + sbx_last_error()), false;
-    if (f->fdm->tab.k != f->t.k || f->fdm->tab.nz != f->t.nz)
-        return (*err = "the field's air side or zones do not match the HVAC tables"), false;
+    if (f->fdm->tab.k != f->t.k || f->fdm->tab.nz != f->t.nz || f->fdm->tab.n != f->t.n_solved)
+        return (*err = "the field's air side, zones or solved cells do not match the HVAC tables"), false;
+    // the records: zero, the streams seeded (sb_rng.c:9-16; position 624: the
+    // first draw twists), the pump head at its constant
+    const sbe::StateLayout& S = f->st;
+    std::vector<unsigned char> rec((size_t)S.record * G, 0);
+    for (int s = 0; s < G; s++) {
+        unsigned char* r = rec.data() + (size_t)s * S.record;
+        int* ip = reinterpret_cast<int*>(r + S.ip);
+        mt_seed(reinterpret_cast<uint32_t*>(r + S.mt), slots[s].occ_seed);
+        ip[sbe::IP_MT_IDX] = SBE_MT_N;
+        if (S.cmt) {
+            mt_seed(reinterpret_cast<uint32_t*>(r + S.cmt), slots[s].conv_seed);
+            ip[sbe::IP_CMT_IDX] = SBE_MT_N;
+        }
+        reinterpret_cast<double*>(r + S.plant)[sbe::PL_PUMP_HEAD] = f->t.pump_head0;
+    }
     const size_t nz = (size_t)f->t.nz, k = (size_t)std::max(f->t.k, 1);
     if (!hip_ok(hipMalloc(&f->d_slots, sizeof(sbe::Slot) * G), "hipMalloc(field slots)", err)
         || !hip_ok(hipMemcpy(f->d_slots, slots.data(), sizeof(sbe::Slot) * G, hipMemcpyHostToDevice), "upload", err)
-        || !hip_ok(hipMalloc(&f->d_state, (size_t)f->st.bytes * G), "hipMalloc(field env state)", err)
-        || !hip_ok(hipMemset(f->d_state, 0, (size_t)f->st.bytes * G), "clear", err)
+        || !hip_ok(hipMalloc(&f->d_state, rec.size()), "hipMalloc(field env state)", err)
+        || !hip_ok(hipMemcpy(f->d_state, rec.data(), rec.size(), hipMemcpyHostToDevice), "upload", err)
         || !hip_ok(hipMalloc(&f->d_qz, 8 * nz * G), "hipMalloc", err)
         || !hip_ok(hipMalloc(&f->d_amb, 8 * (size_t)G), "hipMalloc", err)
         || !hip_ok(hipMalloc(&f->d_hh, 8 * (size_t)G), "hipMalloc", err)
         || !hip_ok(hipMalloc(&f->d_g, 8 * k * G), "hipMalloc", err)
-        || !hip_ok(hipMalloc(&f->d_airT, 8 * k * G), "hipMalloc", err)
-        || !hip_ok(hipMalloc(&f->d_mask, 4 * (size_t)G), "hipMalloc", err)
-        || !hip_ok(hipMemset(f->d_mask, 0, 4 * (size_t)G), "clear", err))
+        || !hip_ok(hipMalloc(&f->d_airT, 8 * k * G), "hipMalloc", err))
         return false;
-    sbe::Args a{};
-    a.t = f->t;
-    a.st = f->st;
-    a.state = f->d_state;
-    a.slots = f->d_slots;
-    a.G = G;
-    const int rc = sbe_launch(&a, 3, nullptr);
-    return hip_ok((hipError_t)rc, "field env seed", err) && hip_ok(hipDeviceSynchronize(), "field env seed", err);
+    int lds = f->lds_bytes;
+    if (f->t.cv_rooms > 0) {
+        // the plan kernel keeps two MT blocks (raw and tempered), the room's
+        // inverse permutation (u16) and candidate counts (u8) in LDS, and as
+        // many of the room's pairs as fit beside them (the rest in HBM)
+        const int fixed = 4 * 4 * SBE_MT_N + 3 * f->t.cv_max_room + 16;
+        const int room = 160 * 1024 - fixed;
+        if (room < 4 * 1024) return (*err = "a convection room is too large for the plan kernel's LDS"), false;
+        f->lds_pairs = std::min(f->t.cv_max_room, room / 4);
+        lds = std::max(lds, fixed + 4 * f->lds_pairs);
+        const size_t cells = (size_t)std::max(f->t.cv_cells, 1), mr = (size_t)std::max(f->t.cv_max_room, 1);
+        if (!hip_ok(hipMalloc(&f->d_moves, 8 * cells * G), "hipMalloc(convection moves)", err)
+            || !hip_ok(hipMalloc(&f->d_vals, 8 * cells * G), "hipMalloc(convection values)", err)
+            || !hip_ok(hipMalloc(&f->d_count, 4 * (size_t)G), "hipMalloc", err)
+            || !hip_ok(hipMemset(f->d_count, 0, 4 * (size_t)G), "clear", err)
+            || !hip_ok(hipMalloc(&f->d_spill, 4 * mr * G), "hipMalloc(convection pairs)", err))
+            return false;
+    }
+    if (lds > 64 * 1024 && !hip_ok((hipError_t)sbe_lds_limit(lds), "field env LDS limit", err)) return false;
+    return true;
 }
 
 bool field_step(FieldScen* f, const FieldIo& io, bool reset, hipStream_t s, std::string* err) {
-    sbe::Args a{};
-    a.t = f->t;
-    a.st = f->st;
-    a.state = f->d_state;
-    a.slots = f->d_slots;
-    a.G = f->G;
+    sbe::Args a = base_args(f);
     a.mode = reset ? sbe::FE_RESET : sbe::FE_STEP;
     a.actions = io.actions;
     a.obs = io.obs;
@@ -438,14 +619,6 @@ bool field_step(FieldScen* f, const FieldIo& io, bool reset, hipStream_t s, std:
     a.env_stride = io.env_stride;
     a.log_offset = io.log_offset;
     a.reward_scale = io.reward_scale;
-    a.qz = f->d_qz;
-    a.amb = f->d_amb;
-    a.hh = f->d_hh;
-    a.g = f->d_g;
-    a.airT = f->d_airT;
-    a.reset_mask = f->d_mask;
-    a.T = f->fdm->grp.T;
-    a.Gl = f->fdm->grp.Gl;
     const sbf::Tables& T = f->fdm->tab;
     const sbf::Group& g = f->fdm->grp;
     if (reset) {
@@ -453,14 +626,14 @@ bool field_step(FieldScen* f, const FieldIo& io, bool reset, hipStream_t s, std:
                       "field init", err)
                && hip_ok((hipError_t)sbe_launch(&a, 0, s), "field env reset", err);
     }
+    const bool conv = f->t.cv_rooms > 0;
     const sbf::StepIn in{nullptr, f->d_amb, f->d_hh, f->d_g, f->d_airT, f->d_qz};
     return hip_ok((hipError_t)sbe_launch(&a, 0, s), "field env pre-step", err)
+           && (!conv || hip_ok((hipError_t)sbe_launch(&a, 4, s), "convection plan", err))
            && hip_ok((hipError_t)sbf_launch_step(&T, &g, &in, s), "field step", err)
+           && (!conv || hip_ok((hipError_t)sbe_launch(&a, 5, s), "convection moves", err))
            && hip_ok((hipError_t)sbe_launch(&a, 1, s), "field zone means", err)
-           && hip_ok((hipError_t)sbe_launch(&a, 2, s), "field env post-step", err)
-           && hip_ok((hipError_t)sbe_launch_field_reset(g.T, g.M, T.n_cvs, T.n, g.G, g.Gl, f->d_mask,
-                                                        f->fdm->d_temp_init, f->fdm->d_mass_init, s),
-                     "field reset", err);
+           && hip_ok((hipError_t)sbe_launch(&a, 2, s), "field env post-step", err);
 }
 
 int field_state(FieldScen* f, int slot, double* out, int cap) {
@@ -473,7 +646,7 @@ int field_state(FieldScen* f, int slot, double* out, int cap) {
     const size_t b = (size_t)(slot / g.Gl), l = (size_t)(slot % g.Gl);
     std::vector<double> blk((size_t)std::max(n_cvs, n) * g.Gl);
     if (hipDeviceSynchronize() != hipSuccess) return -1;
-    if (hipMemcpy(r.data(), f->d_state + (size_t)slot * S.bytes, S.bytes, hipMemcpyDeviceToHost) != hipSuccess)
+    if (hipMemcpy(r.data(), f->d_state + (size_t)slot * S.record, S.bytes, hipMemcpyDeviceToHost) != hipSuccess)
         return -1;
     std::vector<double> o;
     if (hipMemcpy(blk.data(), g.T + b * n_cvs * g.Gl, 8 * (size_t)n_cvs * g.Gl, hipMemcpyDeviceToHost) != hipSuccess)
@@ -510,13 +683,9 @@ int field_state(FieldScen* f, int slot, double* out, int cap) {
 }
 
 bool field_live(FieldScen* f, double* out, hipStream_t s) {
-    sbe::Args a{};
-    a.t = f->t;
-    a.st = f->st;
-    a.state = f->d_state;
-    a.G = f->G;
+    sbe::Args a = base_args(f);
     a.live = out;
-    return sbe_launch(&a, 4, s) == 0;
+    return sbe_launch(&a, 3, s) == 0;
 }
 
 double field_bytes_per_step(const FieldScen* f) {
@@ -532,7 +701,8 @@ void field_close(FieldScen* f) {
     if (!f) return;
     (void)hipDeviceSynchronize();
     for (void* p : {(void*)f->d_tables, (void*)f->d_slots, (void*)f->d_state, (void*)f->d_qz, (void*)f->d_amb,
-                    (void*)f->d_hh, (void*)f->d_g, (void*)f->d_airT, (void*)f->d_mask})
+                    (void*)f->d_hh, (void*)f->d_g, (void*)f->d_airT, (void*)f->d_moves, (void*)f->d_count,
+                    (void*)f->d_vals, (void*)f->d_spill})
         (void)hipFree(p);
     if (f->fdm) sbx_fdm_close(f->fdm);
     delete f;

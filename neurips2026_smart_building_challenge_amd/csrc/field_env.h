@@ -1,51 +1,60 @@
 // Field envs: scenarios whose field is FDM-scale (10^5-10^6 cells, general
 // area-weighted air side), stepped behind the same PufferLib ABI as the RC
-// envs. The HVAC plant, actions, observation, occupancy, reward and episode
-// bookkeeping run in field_env_kernel.hip, one lane per env (O(zones + VAVs +
-// fields) work per env-step); the field solve runs in fdm_kernel.hip on the
-// scenario's group of envs (envs as lanes of its level-ordered row solves).
-// Shared by the host (vec.cpp) and the device; not part of the public ABI.
+// envs. Shared by the host (field_env.cpp, vec.cpp) and the device
+// (field_env_kernel.hip); not part of the public ABI.
 //
-// One env-step of a field scenario, on the bound stream:
-//   fe_pre    decode + sb_sim_apply_native + sb_sim_step_pre from the zone
-//             means of the current field (kept per env): each zone's heat per
-//             room cell, the air-side conductance and supply temperature per
-//             coupled column, the ambient temperature and h, into the field
-//             step's inputs (complete_port/csim/sb_sim.c:357-457);
-//   field     the FDM step (forcing, LU replay, air side, mass, field update;
-//             complete_port/csim/sb_fdm.c:126-188) on every env of the group;
-//   fe_means  each zone's mean over its room's cells of the new field, in the
-//             room's cell order (sb_sim.c:149-160);
-//   fe_post   sb_sim_step_post (boiler), the observation, the occupancy
-//             interval, the 3C reward from the new zone means, the Log and
-//             the auto-reset (complete_port/pufferlib_cpu_env.h:211-257); an
-//             env that resets marks its field for re-initialisation;
-//   fe_field_reset  temp_init / mass_temp_init into the marked envs' fields.
+// Work split of one env-step of a field scenario (G envs), on the bound stream:
+//   hvac(pre)   one 64-lane wavefront per env, its record staged in LDS:
+//               actions decoded and applied, VAV / AHU / column / zone
+//               passes with lanes over the entities and every csim
+//               accumulation kept in its operand order by giving each sum to
+//               one lane (per AHU over its VAVs, per zone over its columns),
+//               the boiler update (it reads only pre-step values), and the
+//               field step's inputs: heat per room cell of each zone, air-side
+//               conductance and supply temperature per column, ambient, h;
+//   conv plan   (stochastic convection on) one wavefront per env: the
+//               convection stream's swap decisions of the step, which depend
+//               on no temperature, composed per room into a permutation and
+//               listed as (cell, source cell) moves;
+//   field       the FDM step on the whole group (fdm_kernel.hip);
+//   conv apply  the listed moves, gathered then scattered;
+//   means       each zone's mean over its room's cells, lane per (zone, env);
+//   hvac(post)  one wavefront per env: observation (lanes over fields),
+//               occupancy draws (lanes over chains, positions in the MT
+//               stream from a wavefront prefix sum), 3C reward, bookkeeping,
+//               the Log at episode ends and the auto-reset (which also
+//               re-initialises the env's field).
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
 
+#define SBE_MT_N 624
+
 namespace sbe {
 
-// Per-env state record (one block per env, envs of a scenario back to back),
-// byte offsets. f64 arrays first, then i32, then u8, then the MT19937 words.
+// Per-env record (HBM, envs of a scenario back to back, stride `record`).
+// [0, bytes) is the image the HVAC kernels stage into LDS and store back;
+// the convection stream follows it (read only by the plan kernel).
 struct StateLayout {
-    int bytes;
+    int bytes;        // staged image (16-byte multiple)
+    int record;       // record stride (256-byte multiple)
     // f64 [na]
-    int recirc, sat, fan, flow, wsum, atotal, satv;
+    int recirc, sat, fan, flow, satv;
     // f64 [nv]
-    int damper, reheat, ratio, heatsp, coolsp, dcmd, rcmd, sensing, vav_area;
+    int damper, reheat, ratio, heatsp, coolsp, dcmd, rcmd, sensing, vav_area, unres;
     // f64 [nz]
     int avg_temp, zone_q, occV;
     // f64 [k]
-    int air_g, air_T, coil;
+    int air_g, air_T, coil, rwen;
     int plant;        // f64 [PL_COUNT]
     // i32
-    int run, coolreq;                         // [na]
-    int mode, prev_valid, dcmd_set, rcmd_set; // [nv]
-    int ip;                                   // [IP_COUNT]
-    int occ_state;                            // u8 [nz * nassign]
-    int mt;                                   // u32 [624]
+    int run, coolreq;                          // [na]
+    int mode, prev_valid, dcmd_set, rcmd_set;  // [nv]
+    int ip;                                    // [IP_COUNT]
+    int ep;                                    // f32 [EP_COUNT] running episode sums
+    int occ_state;                             // u8 [nz * nassign]
+    int mt;                                    // u32 [624] occupancy stream (in the image)
+    int cmt;                                   // u32 [624] convection stream (after the image; 0: none)
 };
 
 enum {
@@ -67,35 +76,47 @@ enum {
     IP_STEP_INDEX,       // calendar row of the next step
     IP_STEP,             // steps into the episode
     IP_FIRST_DONE,       // the first episode after puf_vec_create has ended
-    IP_MT_IDX,
+    IP_MT_IDX,           // occupancy stream position in its block (624: twist before the next draw)
     IP_STEPS_TOTAL,      // env-steps since puf_reset
     IP_EPISODES,         // episodes ended since puf_reset
-    IP_COUNT
+    IP_CMT_IDX,          // convection stream position in its block
+    IP_COUNT = 12
 };
+
+// Running episode sums (float, as the reference GPU env keeps them)
+enum { EP_RET = 0, EP_MEAN = 1, EP_COUNT = 4 };
 
 // Read-only tables of one field scenario (device pointers).
 struct Tabs {
     int n_cvs, nz, nv, na, k, n_act, n_dev, n_aux, nassign, n1;
-    // zone z's room cells (cell ids r * cols + c, the room's order) are
+    // zone z's room cells (field cell ids r * cols + c, the room's order) are
     // zcells[zoff[z] .. zoff[z + 1])
     const int* zoff;
     const int* zcells;
     const double* zone_area;      // [nz]
-    const double* zm_init;        // [nz] zone means of temp_init (host, the same order)
+    const double* zm_init;        // [nz] zone means of temp_init (host, the room's order)
     const int* vz_off;            // [nv + 1] VAV -> zones
     const int* vz_idx;
     const int* vav_ahu;           // [nv]
     const int* coupled;           // [k] column -> VAV
+    const int* av_off;            // [na + 1] AHU -> its VAVs, ascending
+    const int* av_idx;
+    const int* ac_off;            // [na + 1] AHU -> the columns of its VAVs, ascending
+    const int* ac_idx;
+    const int* zc_off;            // [nz + 1] zone -> the columns that heat it, in column order
+    const int* zc_idx;
     const double* vav_c;          // [nv * 9]
     const double* ahu_c;          // [na * 9]
     const double* boiler_c;       // [10]
     double pump_head0, pump_eff, header_res, internal_w_m2, standby_frac, occupant_w, cv_area, dt_sec, h;
     double gas_den;               // log(r2 / c6) / c8 + 1 / c4 / r2 (sb_reward.c:19-23)
-    // actions
-    const uint8_t* act_kind;
-    const uint8_t* act_act;
+    // actions: per action its trainer column (continuous block or SB_CONT + d),
+    // its target (kind | actuator << 4 | owner index << 8) and whether it is
+    // the last action writing that target (the one the sequential apply keeps)
+    const int* act_col;
+    const int* act_tgt;
+    const uint8_t* act_live;
     const uint8_t* act_disc;
-    const int* act_idx;
     const double* act_mn;
     const double* act_mx;
     const double* act_mnr;
@@ -129,17 +150,32 @@ struct Tabs {
     const double* elec_co2;
     const double* gas_price;
     double gas_co2;
+    // field re-initialisation at an auto-reset
+    const double* temp_init;      // [n_cvs]
+    const double* mass_init;      // [n]
+    int n_solved;
+    // stochastic convection (sb_convect.c): rooms [cv_rooms + 1] offsets into
+    // the cell list, each cell's field id, its candidate count (u8) and CSR
+    // candidates as room-local positions
+    int cv_rooms, cv_cells, cv_max_room;
+    uint32_t cv_thr_hi, cv_thr_lo;   // swap when the 53-bit draw is <= this (hi:lo); hi = 0xFFFFFFFF: never
+    const int* cv_off;
+    const int* cv_cell;
+    const uint8_t* cv_ncand;
+    const int* cv_coff;
+    const uint16_t* cv_cidx;
 };
 
 // One env of a field group: its index in the vec, its calendar start, episode
-// lengths and its occupancy stream seed.
+// lengths, its occupancy and convection stream seeds.
 struct Slot {
     int env;
     int start;
     int max_steps;
     int first_steps;
     uint32_t occ_seed;
-    int pad[3];
+    uint32_t conv_seed;
+    int pad[2];
 };
 
 enum { FE_STEP = 0, FE_RESET = 1 };
@@ -147,7 +183,7 @@ enum { FE_STEP = 0, FE_RESET = 1 };
 struct Args {
     Tabs t;
     StateLayout st;
-    unsigned char* state;         // [G][st.bytes]
+    unsigned char* state;         // [G][st.record]
     const Slot* slots;            // [G]
     int G;
     int mode;
@@ -159,6 +195,7 @@ struct Args {
     void* host_env;               // Env array (host-coherent), or null
     int env_stride, log_offset;
     float reward_scale;
+    int lds_bytes;                // dynamic LDS of the HVAC kernels (image + scratch)
     // the field step's inputs: per env the heat per room cell of each zone,
     // the ambient temperature, h, per column the air-side conductance and
     // supply temperature
@@ -167,18 +204,28 @@ struct Args {
     double* hh;                   // [G]
     double* g;                    // [G][k]
     double* airT;                 // [G][k]
-    int* reset_mask;              // [G] fe_post marks envs whose field is re-initialised
     // the group's field: cell p of env b * Gl + l at T[(b * n_cvs + p) * Gl + l]
-    const double* T;
+    double* T;
+    double* M;                    // interior mass, [(b * n + q) * Gl + l]
     int Gl;
-    double* live;                 // fe_live adds the totals since puf_reset to live[0..2]
+    double* live;                 // the live-sums kernel adds the totals since puf_reset to live[0..2]
+    // convection moves of the step: per env at most cv_cells (field id << 32 |
+    // source field id) words, their count, the gathered values; pair overflow
+    // past the plan kernel's LDS
+    unsigned long long* cv_moves; // [G][cv_cells]
+    int* cv_count;                // [G]
+    double* cv_vals;              // [G][cv_cells]
+    unsigned int* cv_spill;       // [G][cv_max_room]
+    int cv_lds_pairs;             // pairs the plan kernel keeps in LDS
 };
 
 // The host (g++) and the device (hipcc) compile these structs separately and
 // exchange them byte for byte: both builds check the same sizes and offsets.
-static_assert(sizeof(Tabs) == 488 && offsetof(Tabs, gas_co2) == 480, "Tabs layout");
-static_assert(sizeof(StateLayout) == 132 && sizeof(Slot) == 32, "StateLayout / Slot layout");
-static_assert(sizeof(Args) == 776 && offsetof(Args, st) == 488 && offsetof(Args, state) == 624
-              && offsetof(Args, live) == 768, "Args layout");
+static_assert(sizeof(StateLayout) == 144 && offsetof(StateLayout, cmt) == 140, "StateLayout layout");
+static_assert(sizeof(Slot) == 32, "Slot layout");
+static_assert(offsetof(Tabs, gas_co2) == 528 && offsetof(Tabs, temp_init) == 536 && offsetof(Tabs, cv_off) == 576
+              && sizeof(Tabs) == 616, "Tabs layout");
+static_assert(offsetof(Args, st) == 616 && offsetof(Args, state) == 760 && offsetof(Args, qz) == 840
+              && offsetof(Args, live) == 904 && sizeof(Args) == 952, "Args layout");
 
 }  // namespace sbe

@@ -19,6 +19,7 @@ struct FieldCounts {
     int episode_steps;
     int hour_m1_rows;
     int64_t occ_seed;
+    int64_t conv_seed;      // the convection stream's seed (env j of the scenario: + j, as the occupancy one)
     int n_cvs, n_solved, nz;
 };
 
@@ -31,8 +32,8 @@ FieldScen* field_open(const sbh::Blob& b, std::string* err);
 FieldCounts field_counts(const FieldScen* f);
 
 // Device tables, the field group (sbx_fdm with `flags`, `envs_per_block`) and
-// the per-env records of the scenario's envs (slots in vec order); seeds the
-// occupancy streams.
+// the per-env records of the scenario's envs (slots in vec order), with their
+// occupancy and convection streams seeded.
 bool field_attach(FieldScen* f, const std::string& path, const std::vector<sbe::Slot>& slots, int flags,
                   int envs_per_block, std::string* err);
 

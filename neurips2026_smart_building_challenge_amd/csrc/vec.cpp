@@ -1391,6 +1391,7 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
             S.n1 = fc.n1;
             S.episode_steps = fc.episode_steps;
             S.occ_seed = fc.occ_seed;
+            S.conv_seed = fc.conv_seed;
             S.hour_m1_rows = fc.hour_m1_rows;
             S.dev.layout = li;
             v->scens.push_back(std::move(S));
@@ -1474,7 +1475,8 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
                 v->field_of.push_back(S.field);
                 v->slot_of.push_back((int)v->field_slots[S.field].size());
                 v->field_slots[S.field].push_back(
-                    sbe::Slot{e, start, ms, d.first_steps, (uint32_t)(S.occ_seed + (per_env_seed ? j : 0)), {0, 0, 0}});
+                    sbe::Slot{e, start, ms, d.first_steps, (uint32_t)(S.occ_seed + (per_env_seed ? j : 0)),
+                              (uint32_t)(S.conv_seed + (per_env_seed ? j : 0)), {0, 0}});
             } else {
                 v->field_of.push_back(-1);
                 v->slot_of.push_back(-1);

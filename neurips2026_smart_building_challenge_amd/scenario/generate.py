@@ -406,25 +406,72 @@ class FieldEnvSpec:
         return f"{self.field.name}_a{self.ahus}"
 
 
-def field_env_writer(spec: FieldEnvSpec, clim: ClimateSpec, table_steps: int, occ_seed: int) -> SbbWriter:
+def field_conv_tables(plan, distance: int):
+    """Convection rooms of an FDM plan: every room, its cells in row-major
+    order, and per cell its candidates, the room's other cells within
+    Chebyshev distance `distance` in row-major order (the reference baker's
+    table form, complete_port/pysim/bake_scenario.py:162-186: room offsets
+    into the cell list, cells as (row, col), candidates as CSR over cell
+    positions in that list)."""
+    cols = plan.spec.cols
+    off, cells, cand_off, cand_idx = [0], [], [np.zeros(1, np.int64)], []
+    for rc in plan.room_cells:
+        p = plan.solved[rc]
+        r, c = p // cols, p % cols
+        r0, c0 = int(r.min()), int(c.min())
+        h, w = int(r.max()) - r0 + 1, int(c.max()) - c0 + 1
+        if h * w != rc.size:
+            raise ValueError("convection rooms must be rectangles of the plan")
+        base = off[-1]
+        cells.append(np.stack([r, c], 1))
+        off.append(base + rc.size)
+        lr, lc = (r - r0)[:, None], (c - c0)[:, None]
+        offs = [(dr, dc) for dr in range(-distance, distance + 1) for dc in range(-distance, distance + 1)
+                if (dr, dc) != (0, 0)]
+        dr = np.array([o[0] for o in offs])[None, :]
+        dc = np.array([o[1] for o in offs])[None, :]
+        nr, nc = lr + dr, lc + dc
+        ok = (nr >= 0) & (nr < h) & (nc >= 0) & (nc < w)
+        cand = np.where(ok, base + nr * w + nc, -1)
+        cnt = ok.sum(1)
+        cand_idx.append(cand[ok])
+        cand_off.append(cand_off[-1][-1] + np.cumsum(cnt))
+    return (np.asarray(off, np.int64), np.concatenate(cells).reshape(-1).astype(np.int64),
+            np.concatenate(cand_off).astype(np.int64), np.concatenate(cand_idx).astype(np.int64))
+
+
+def field_env_writer(spec: FieldEnvSpec, clim: ClimateSpec, table_steps: int, occ_seed: int,
+                     conv: ConvSpec | None = None) -> SbbWriter:
     """One FDM-scale env scenario: the plan's field sections (fdm.fdm_writer,
-    with its rooms' cells and area-weighted air-side columns), convection
-    off, and hvac_sections with the rooms as zones (zone area = the room's
-    floor area, internal gains per cell of the plan's cell size). No solar
-    gain section: the reference core has no solar input."""
+    with its rooms' cells and area-weighted air-side columns), stochastic
+    convection off or, with `conv`, on in every room (the shipped buildings
+    all carry p = 0.1, distance 2: data/blob_meta/*.json "conv"), and
+    hvac_sections with the rooms as zones (zone area = the room's floor area,
+    internal gains per cell of the plan's cell size). No solar gain section:
+    the reference core has no solar input."""
     from .fdm import fdm_writer, make_plan
 
     plan = make_plan(spec.field)
     w = fdm_writer(plan)
     Z = plan.k
     b = make_building(Z, spec.ahus, spec.seed, name=spec.name)
-    w.scalar_f64("conv_p", 0.0)
-    w.scalar_f64("conv_distance", 0.0)
-    w.scalar_i64("conv_seed", 0)
-    w.add("conv_room_offsets", [0], "i32")
-    w.add("conv_room_cells", np.zeros(0), "i32")
-    w.add("conv_cand_offsets", [0], "i32")
-    w.add("conv_cand_idx", np.zeros(0), "i32")
+    if conv is None:
+        w.scalar_f64("conv_p", 0.0)
+        w.scalar_f64("conv_distance", 0.0)
+        w.scalar_i64("conv_seed", 0)
+        w.add("conv_room_offsets", [0], "i32")
+        w.add("conv_room_cells", np.zeros(0), "i32")
+        w.add("conv_cand_offsets", [0], "i32")
+        w.add("conv_cand_idx", np.zeros(0), "i32")
+    else:
+        c_off, c_cells, c_coff, c_idx = field_conv_tables(plan, conv.distance)
+        w.scalar_f64("conv_p", conv.p)
+        w.scalar_f64("conv_distance", float(conv.distance))
+        w.scalar_i64("conv_seed", conv.seed)
+        w.add("conv_room_offsets", c_off, "i32")
+        w.add("conv_room_cells", c_cells, "i32")
+        w.add("conv_cand_offsets", c_coff, "i32")
+        w.add("conv_cand_idx", c_idx, "i32")
     cv = spec.field.cv_m
     zone_area = np.array([c.size for c in plan.room_cells], np.float64) * cv * cv
     hvac_sections(w, b, Z, clim, table_steps, occ_seed, zone_area, cv * 100.0, None, None)

@@ -33,13 +33,19 @@ from neurips2026_smart_building_challenge_amd.scenario import generate as G  # n
 OUT = Path(__file__).resolve().parent / "field_env.json"
 ACTION_SEED = 20261202
 TABLE_STEPS = G.EPISODE_STEPS + 256
-# name, field spec, AHUs, climate index, occ_seed, env index (action rows), start, max_steps, steps.
-# The cases at start 0 use the blob's occupancy seed (17321), as the first env
-# of a vec on the blob does.
+# name, field spec, AHUs, climate index, occ_seed, env index (action rows), start, max_steps, steps,
+# stochastic convection (p, distance, seed) or None. The cases at start 0 use the
+# blob's occupancy seed (17321), as the first env of a vec on the blob does (its
+# convection stream then has the blob's conv_seed). The convection cases use the
+# shipped buildings' setting, p = 0.1 within distance 2 (data/blob_meta/*.json).
+SHIPPED_CONV = (0.1, 2, 5)
 CASES = [
-    ("field_small", dict(rows=120, cols=90, rooms=7, margin=6, seed=3), 2, 1, 17321, 0, 0, 40, 60),
-    ("field_small_offset", dict(rows=120, cols=90, rooms=7, margin=6, seed=3), 2, 1, 78, 1, 200, 30, 45),
-    ("field_train1_size", dict(), 3, 3, 17321, 0, 0, 8640, 3),
+    ("field_small", dict(rows=120, cols=90, rooms=7, margin=6, seed=3), 2, 1, 17321, 0, 0, 40, 60, None),
+    ("field_small_offset", dict(rows=120, cols=90, rooms=7, margin=6, seed=3), 2, 1, 78, 1, 200, 30, 45, None),
+    ("field_train1_size", dict(), 3, 3, 17321, 0, 0, 8640, 3, None),
+    ("field_small_conv", dict(rows=120, cols=90, rooms=7, margin=6, seed=3), 2, 1, 17321, 0, 0, 30, 45,
+     SHIPPED_CONV),
+    ("field_train1_conv", dict(), 3, 3, 17321, 0, 0, 8640, 4, SHIPPED_CONV),
 ]
 
 
@@ -47,10 +53,11 @@ def spec_of(field: dict, ahus: int) -> G.FieldEnvSpec:
     return G.FieldEnvSpec(F.FdmSpec(**field), ahus)
 
 
-def blob(field: dict, ahus: int, clim: int, tmp: Path) -> tuple[Path, str]:
+def blob(field: dict, ahus: int, clim: int, tmp: Path, conv=None) -> tuple[Path, str]:
     spec = spec_of(field, ahus)
-    data = G.field_env_writer(spec, G.climates()[clim], TABLE_STEPS, 17321).tobytes()
-    p = tmp / f"{spec.name}__c{clim}.sbb"
+    cv = None if conv is None else G.ConvSpec(*conv)
+    data = G.field_env_writer(spec, G.climates()[clim], TABLE_STEPS, 17321, cv).tobytes()
+    p = tmp / f"{spec.name}__c{clim}{'' if cv is None else '__' + cv.tag}.sbb"
     p.write_bytes(data)
     return p, hashlib.sha256(data).hexdigest()
 
@@ -87,11 +94,11 @@ def main() -> None:
         raise SystemExit("oracle/_ref is not built (needs /root/reference)")
     out = {"action_seed": ACTION_SEED, "table_steps": TABLE_STEPS, "cases": {}}
     with tempfile.TemporaryDirectory() as td:
-        for name, field, ahus, clim, occ, env, start, ms, steps in CASES:
-            path, sha = blob(field, ahus, clim, Path(td))
+        for name, field, ahus, clim, occ, env, start, ms, steps, conv in CASES:
+            path, sha = blob(field, ahus, clim, Path(td), conv)
             rec = run_case("ref", path, occ, env, start, ms, steps)
             rec.update({"field": field, "ahus": ahus, "climate": clim, "occ_seed": occ, "env": env, "start": start,
-                        "max_steps": ms, "steps": steps, "blob_sha256": sha})
+                        "max_steps": ms, "steps": steps, "blob_sha256": sha, "conv": conv})
             out["cases"][name] = rec
             print(name, "ok", flush=True)
     OUT.write_text(json.dumps(out, indent=1))

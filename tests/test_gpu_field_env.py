@@ -15,7 +15,11 @@ and the reference core's fixture (tests/golden/field_env.json):
     observations within float32 quantization of the physics fields, rewards
     within 2 float32 ulps;
   - a vec mixing RC layouts and a field scenario: every env against its
-    oracle twin (RC envs at the RC tolerances).
+    oracle twin (RC envs at the RC tolerances);
+  - stochastic convection on (the shipped buildings' p = 0.1 within distance
+    2, and p = 0.6 in a room of 45,384 cells, whose swap pairs outgrow the
+    plan kernel's LDS): the same bit-identity in exact mode, the tolerances in
+    default mode, and the reference core's fixture at 205,434 cells.
 """
 from __future__ import annotations
 
@@ -57,10 +61,15 @@ def _gpu():
     torch.cuda.synchronize()
 
 
-def field_blob(tmp: Path, field: dict, ahus: int, clim: int, table_steps: int = G.EPISODE_STEPS + 256) -> Path:
+SHIPPED_CONV = (0.1, 2, 5)
+
+
+def field_blob(tmp: Path, field: dict, ahus: int, clim: int, table_steps: int = G.EPISODE_STEPS + 256,
+               conv=None) -> Path:
     spec = G.FieldEnvSpec(F.FdmSpec(**field), ahus)
-    data = G.field_env_writer(spec, G.climates()[clim], table_steps, 17321).tobytes()
-    p = tmp / f"{spec.name}__c{clim}.sbb"
+    cv = None if conv is None else G.ConvSpec(*conv)
+    data = G.field_env_writer(spec, G.climates()[clim], table_steps, 17321, cv).tobytes()
+    p = tmp / f"{spec.name}__c{clim}{'' if cv is None else '__' + cv.tag}.sbb"
     p.write_bytes(data)
     return p
 
@@ -68,6 +77,11 @@ def field_blob(tmp: Path, field: dict, ahus: int, clim: int, table_steps: int = 
 @pytest.fixture(scope="module")
 def small_blob(tmp_path_factory):
     return field_blob(tmp_path_factory.mktemp("field_small"), SMALL, 2, 1)
+
+
+@pytest.fixture(scope="module")
+def small_conv_blob(tmp_path_factory):
+    return field_blob(tmp_path_factory.mktemp("field_small_conv"), SMALL, 2, 1, conv=SHIPPED_CONV)
 
 
 def host(t) -> np.ndarray:
@@ -140,9 +154,11 @@ def run_against_oracle(vec, twins, steps, exact: bool, tag: str):
     return done_seen
 
 
-def test_gpu_field_env_exact_matches_oracle(small_blob):
-    say("3 envs, 7-room FDM plan, exact field mode, 60 steps (auto-reset at 40)")
-    vec = E.VecEnv(3, blob=str(small_blob), max_steps=40, field_exact=1)
+@pytest.mark.parametrize("conv", [False, True])
+def test_gpu_field_env_exact_matches_oracle(small_blob, small_conv_blob, conv):
+    blob = small_conv_blob if conv else small_blob
+    say(f"3 envs, 7-room FDM plan{' with convection' if conv else ''}, exact field mode, 60 steps (auto-reset at 40)")
+    vec = E.VecEnv(3, blob=str(blob), max_steps=40, field_exact=1)
     twins = [Twin(vec, i, 40) for i in range(3)]
     assert len({tw.cpu.n_cont for tw in twins}) == 1
     done = run_against_oracle(vec, twins, 60, True, "exact")
@@ -157,19 +173,20 @@ def test_gpu_field_env_exact_matches_oracle(small_blob):
     vec.close()
 
 
-def test_gpu_field_env_default_mode(small_blob):
-    say("3 envs, 7-room FDM plan, default field mode, 50 steps")
-    vec = E.VecEnv(3, blob=str(small_blob), max_steps=30)
+@pytest.mark.parametrize("conv", [False, True])
+def test_gpu_field_env_default_mode(small_blob, small_conv_blob, conv):
+    say(f"3 envs, 7-room FDM plan{' with convection' if conv else ''}, default field mode, 50 steps")
+    vec = E.VecEnv(3, blob=str(small_conv_blob if conv else small_blob), max_steps=30)
     twins = [Twin(vec, i, 30) for i in range(3)]
     run_against_oracle(vec, twins, 50, False, "default")
     vec.close()
 
 
-@pytest.mark.parametrize("name", ["field_small", "field_train1_size"])
+@pytest.mark.parametrize("name", ["field_small", "field_train1_size", "field_small_conv", "field_train1_conv"])
 def test_gpu_field_env_reference_fixture(name, tmp_path):
     fx = json.loads((GOLDEN / "field_env.json").read_text())
     case = fx["cases"][name]
-    path = field_blob(tmp_path, case["field"], case["ahus"], case["climate"], fx["table_steps"])
+    path = field_blob(tmp_path, case["field"], case["ahus"], case["climate"], fx["table_steps"], case.get("conv"))
     assert hashlib.sha256(path.read_bytes()).hexdigest() == case["blob_sha256"], "stale fixture"
     say(f"{name}: reference fixture, {case['steps']} steps, exact field mode")
     vec = E.VecEnv(1, blob=str(path), max_steps=case["max_steps"], field_exact=1)
@@ -227,4 +244,20 @@ def test_gpu_field_env_mixed_with_rc(small_blob, tmp_path):
             err = np.abs(gs[fin] - cs[fin]) / np.maximum(np.abs(cs[fin]), 1e-6)
             assert err.max() <= STATE_RTOL, f"{where}: state rel err {err.max():.3e}"
             assert abs(float(rew[tw.i]) - r) <= 4 * np.spacing(np.float32(abs(r))) + 1e-12, where
+    vec.close()
+
+
+def test_gpu_field_env_conv_big_room(tmp_path):
+    """Two rooms, the larger of 45,384 cells, with p = 0.6: about 27,000 swap
+    pairs a step there, more than the plan kernel holds in LDS beside the
+    room's permutation (the rest go to its HBM overflow), and room-local
+    indices in the upper half of the 16-bit range. Exact mode, bit-identical
+    to the oracle every step."""
+    field = dict(rows=310, cols=260, rooms=2, margin=6, seed=4)
+    blob = field_blob(tmp_path, field, 2, 2, conv=(0.6, 2, 9))
+    assert int(np.diff(read_sbb(blob)["conv_room_offsets"]).max()) == 45384
+    say("3 envs, rooms of 45,384 and 26,108 cells, convection p = 0.6, exact field mode, 6 steps")
+    vec = E.VecEnv(3, blob=str(blob), max_steps=100, field_exact=1)
+    twins = [Twin(vec, i, 100) for i in range(3)]
+    run_against_oracle(vec, twins, 6, True, "big room")
     vec.close()
