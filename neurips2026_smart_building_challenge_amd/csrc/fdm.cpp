@@ -487,19 +487,16 @@ bool build(SbxFdm* f, const char* path, int G, int epb, int flags) {
     put_tri(&T.L, L);
     put_tri(&T.U, U);
     // envs per block: as asked; by default one (the default mode keeps a run's
-    // rows in LDS per env), two once the group has more envs than the GPU has
-    // compute units (a block's level chain then serves two envs: 512 envs of
-    // a 205K-cell plan 18.6 -> 17.5 ms per step, 1,024 envs 28.2 ms; four
-    // were slower), or, in exact mode, up to 64
+    // rows in LDS per env), two once the group has more than 256 envs, the
+    // MI355X's compute-unit count (a block's level chain then serves two envs:
+    // 512 envs of a 205K-cell plan 18.6 -> 17.5 ms per step, 1,024 envs
+    // 28.2 ms; four were slower), or, in exact mode, up to 64. The threshold
+    // is a constant, not the device's count: the default mode's sums are
+    // reassociated by the block width, so an env's rounding depends on the
+    // group size only (both widths are held to the reference within 1e-9)
     const bool exact = (flags & SBX_FDM_EXACT) != 0;
-    int cus = 256;
-    {
-        int dev = 0;
-        hipDeviceProp_t pr;
-        if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&pr, dev) == hipSuccess)
-            cus = pr.multiProcessorCount;
-    }
-    const int dflt = exact ? 64 : (G > cus ? 2 : 1);
+    constexpr int kTwoPerBlockAbove = 256;
+    const int dflt = exact ? 64 : (G > kTwoPerBlockAbove ? 2 : 1);
     const int gl = std::min(64, next_pow2(std::min(G, epb > 0 ? epb : dflt)));
     T.fast = exact ? 0 : 1;
     SweepHost sl, su;

@@ -76,13 +76,21 @@ bool field_blob(const sbh::Blob& b) {
     if ((int64_t)n > kFieldMinSolved) return true;
     // air side: one applied and one sensed entry per column, unit weight, on
     // the same node, no node twice (what the RC plans fold into diag(g))
-    const int64_t* ss = b.i64("sensed_shape");
-    const int k = ss ? (int)ss[0] : 0;
-    const int32_t *ap = b.i32("applied_indptr"), *ai = b.i32("applied_indices");
-    const int32_t *sp = b.i32("sensed_indptr"), *si = b.i32("sensed_indices");
-    const double *ax = b.f64("applied_data"), *sx = b.f64("sensed_data");
-    if (k == 0) return false;
-    if (!ap || !ai || !sp || !si || !ax || !sx) return false;
+    uint64_t nss = 0, nap = 0, nai = 0, nsp = 0, nsi = 0, nax = 0, nsx = 0;
+    const int64_t* ss = b.i64("sensed_shape", &nss);
+    const int k = (ss && nss >= 1) ? (int)ss[0] : 0;
+    const int32_t *ap = b.i32("applied_indptr", &nap), *ai = b.i32("applied_indices", &nai);
+    const int32_t *sp = b.i32("sensed_indptr", &nsp), *si = b.i32("sensed_indices", &nsi);
+    const double *ax = b.f64("applied_data", &nax), *sx = b.f64("sensed_data", &nsx);
+    if (k <= 0) return false;
+    // a malformed air side goes to the field path, whose open checks it with
+    // a message (the tests below read only inside the sections)
+    if (!ap || !ai || !sp || !si || !ax || !sx) return true;
+    if (nap != (uint64_t)k + 1 || nsp != (uint64_t)k + 1 || nax < nai || nsx < nsi) return true;
+    for (int c = 0; c < k; c++)
+        if (ap[c] < 0 || ap[c + 1] < ap[c] || (uint64_t)ap[c + 1] > nai || sp[c] < 0 || sp[c + 1] < sp[c]
+            || (uint64_t)sp[c + 1] > nsi)
+            return true;
     std::vector<char> seen(n, 0);
     for (int c = 0; c < k; c++) {
         if (ap[c + 1] - ap[c] != 1 || sp[c + 1] - sp[c] != 1) return true;

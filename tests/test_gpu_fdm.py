@@ -243,3 +243,33 @@ def test_gpu_fdm_full_size_batch_properties(full):
     assert close(Ta[:2], To) and close(Ma[:2], Mo)
     f.close()
     g2.close()
+
+
+@pytest.mark.parametrize("G", [40, 300])
+def test_gpu_fdm_full_size_default_every_cell(full, G):
+    """The default configuration (envs_per_block 0, default mode) at
+    building_train_1's size: one env per block at 40 envs, two per block at
+    300 (more envs than the GPU's compute units). Every cell of the field and
+    of the interior mass of seven envs (the first block, the middle, the last
+    ones) within 1e-9 of the oracle after each of 3 steps with air sides on;
+    envs are independent, so the oracle steps just those envs."""
+    import torch
+
+    plan, path, _ = full
+    sel = [0, 1, G // 2, G // 2 + 1, G - 3, G - 2, G - 1]
+    say(f"full-size plan, {G} envs, default configuration, every cell of envs {sel}, 3 steps")
+    f = gpu_group(path, G, 0, exact=False)
+    assert f.info.tail_rows_l > 0 and f.info.tail_rows_u > 0
+    o = po.Fdm("oracle", path, len(sel))
+    for s in range(3):
+        inp = F.step_inputs(plan, G, 300 + G, s)
+        inp["air_g"][sel[2]] = np.where(inp["air_g"][sel[2]] > 0.0, inp["air_g"][sel[2]], 25.0)   # every column on
+        f.step(*device_inputs(inp))
+        o.step({k: (v[sel] if v.ndim else v) for k, v in inp.items()})
+        torch.cuda.synchronize()
+        Tg, Mg = f.state()
+        To, Mo = o.state()
+        for i, g in enumerate(sel):
+            assert close(Tg[g], To[i]), (G, s, g, "T", np.abs(Tg[g] - To[i]).max())
+            assert close(Mg[g], Mo[i]), (G, s, g, "M", np.abs(Mg[g] - Mo[i]).max())
+    f.close()

@@ -261,3 +261,20 @@ def test_gpu_field_env_conv_big_room(tmp_path):
     twins = [Twin(vec, i, 100) for i in range(3)]
     run_against_oracle(vec, twins, 6, True, "big room")
     vec.close()
+
+
+def test_gpu_field_env_default_mode_full_size(tmp_path):
+    """building_train_1's size (205,434 cells) with the shipped buildings'
+    convection, default field mode, 300 envs (the field group then runs two
+    envs per block), episodes of 3 steps: four envs against their oracle twins
+    every step through two auto-resets: state within 1e-9, observations within
+    float32 quantisation of the physics fields, rewards within 2 float32 ulps."""
+    blob = field_blob(tmp_path, {}, 3, 3, conv=SHIPPED_CONV)
+    G = 300
+    say(f"{G} envs at 205,434 cells with convection, default field mode, 7 steps (resets after 3 and 6)")
+    vec = E.VecEnv(G, blob=str(blob), max_steps=3)
+    picks = [0, 1, 150, G - 1]
+    twins = [Twin(vec, i, 3) for i in picks]
+    done = run_against_oracle(vec, twins, 7, False, "full size")
+    assert done == 2 * len(picks)
+    vec.close()
