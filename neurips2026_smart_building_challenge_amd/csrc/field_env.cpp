@@ -67,6 +67,11 @@ struct FieldScen {
     double* d_vals = nullptr;
     unsigned int* d_spill = nullptr;
     int lds_pairs = 0;
+    double conv_p = 0.0;
+    // the plan kernel runs on its own stream, forked from the bound stream at
+    // the start of a step and joined before the moves (it reads no field)
+    hipStream_t side = nullptr;
+    hipEvent_t fork = nullptr, join = nullptr;
     SbxFdm* fdm = nullptr;
 };
 
@@ -258,6 +263,7 @@ FieldScen* field_open(const sbh::Blob& b, std::string* err) {
         if (conv_p != conv_p) return bad("conv_p is NaN");
     }
     if (cv_coff.empty()) cv_coff.push_back(0);
+    f.conv_p = conv_p;
     f.c.conv_seed = b.i64_1("conv_seed", 0);
     // ---- features this path does not carry
     {
@@ -440,7 +446,7 @@ FieldScen* field_open(const sbh::Blob& b, std::string* err) {
     o += 4 * SBE_MT_N;
     S.bytes = (o + 15) & ~15;
     S.cmt = f.t.cv_rooms > 0 ? S.bytes : 0;
-    S.record = (S.bytes + (S.cmt ? 4 * SBE_MT_N : 0) + 255) & ~255;
+    S.record = (S.bytes + (S.cmt ? 4 * (SBE_MT_N + 4) : 0) + 255) & ~255;
     // the HVAC kernels' LDS: the image, then f64 scratch for the pre-step
     // (AHU demand, column flow demand), the reward (VAV sums, AHU terms, zone
     // terms) or one MT block
@@ -578,8 +584,9 @@ bool field_attach(FieldScen* f, const std::string& path, const std::vector<sbe::
         mt_seed(reinterpret_cast<uint32_t*>(r + S.mt), slots[s].occ_seed);
         ip[sbe::IP_MT_IDX] = SBE_MT_N;
         if (S.cmt) {
-            mt_seed(reinterpret_cast<uint32_t*>(r + S.cmt), slots[s].conv_seed);
-            ip[sbe::IP_CMT_IDX] = SBE_MT_N;
+            uint32_t* cmt = reinterpret_cast<uint32_t*>(r + S.cmt);
+            mt_seed(cmt, slots[s].conv_seed);
+            cmt[SBE_MT_N] = SBE_MT_N;   // position: the first draw twists
         }
         reinterpret_cast<double*>(r + S.plant)[sbe::PL_PUMP_HEAD] = f->t.pump_head0;
     }
@@ -597,19 +604,25 @@ bool field_attach(FieldScen* f, const std::string& path, const std::vector<sbe::
     int lds = f->lds_bytes;
     if (f->t.cv_rooms > 0) {
         // the plan kernel keeps two MT blocks (raw and tempered), the room's
-        // inverse permutation (u16) and candidate counts (u8) in LDS, and as
-        // many of the room's pairs as fit beside them (the rest in HBM)
+        // inverse permutation (u16) and candidate counts (u8) in LDS, and the
+        // room's first pairs (the rest in HBM): room for 1.5 times the
+        // expected count of the largest room, at least 2,048, so that two plan
+        // wavefronts and a field-solve workgroup fit on one compute unit
         const int fixed = 4 * 4 * SBE_MT_N + 3 * f->t.cv_max_room + 16;
         const int room = 160 * 1024 - fixed;
-        if (room < 4 * 1024) return (*err = "a convection room is too large for the plan kernel's LDS"), false;
-        f->lds_pairs = std::min(f->t.cv_max_room, room / 4);
-        lds = std::max(lds, fixed + 4 * f->lds_pairs);
+        if (room < 6 * 1024) return (*err = "a convection room is too large for the plan kernel's LDS"), false;
+        const double expect = 1.5 * std::min(std::max(f->conv_p, 0.0), 1.0) * f->t.cv_max_room;
+        f->lds_pairs = std::min({f->t.cv_max_room, room / 6, std::max(2048, (int)expect)});
+        lds = std::max(lds, fixed + 6 * f->lds_pairs);
         const size_t cells = (size_t)std::max(f->t.cv_cells, 1), mr = (size_t)std::max(f->t.cv_max_room, 1);
         if (!hip_ok(hipMalloc(&f->d_moves, 8 * cells * G), "hipMalloc(convection moves)", err)
             || !hip_ok(hipMalloc(&f->d_vals, 8 * cells * G), "hipMalloc(convection values)", err)
             || !hip_ok(hipMalloc(&f->d_count, 4 * (size_t)G), "hipMalloc", err)
             || !hip_ok(hipMemset(f->d_count, 0, 4 * (size_t)G), "clear", err)
-            || !hip_ok(hipMalloc(&f->d_spill, 4 * mr * G), "hipMalloc(convection pairs)", err))
+            || !hip_ok(hipMalloc(&f->d_spill, 8 * mr * G), "hipMalloc(convection pairs)", err)
+            || !hip_ok(hipStreamCreateWithFlags(&f->side, hipStreamNonBlocking), "convection stream", err)
+            || !hip_ok(hipEventCreateWithFlags(&f->fork, hipEventDisableTiming), "event", err)
+            || !hip_ok(hipEventCreateWithFlags(&f->join, hipEventDisableTiming), "event", err))
             return false;
     }
     if (lds > 64 * 1024 && !hip_ok((hipError_t)sbe_lds_limit(lds), "field env LDS limit", err)) return false;
@@ -636,9 +649,16 @@ bool field_step(FieldScen* f, const FieldIo& io, bool reset, hipStream_t s, std:
     }
     const bool conv = f->t.cv_rooms > 0;
     const sbf::StepIn in{nullptr, f->d_amb, f->d_hh, f->d_g, f->d_airT, f->d_qz};
+    // convection plan on the side stream, beside the pre-step and the field
+    // step; the bound stream waits for it before the moves
+    if (conv && !(hip_ok(hipEventRecord(f->fork, s), "fork", err)
+                  && hip_ok(hipStreamWaitEvent(f->side, f->fork, 0), "fork", err)
+                  && hip_ok((hipError_t)sbe_launch(&a, 4, f->side), "convection plan", err)
+                  && hip_ok(hipEventRecord(f->join, f->side), "join", err)))
+        return false;
     return hip_ok((hipError_t)sbe_launch(&a, 0, s), "field env pre-step", err)
-           && (!conv || hip_ok((hipError_t)sbe_launch(&a, 4, s), "convection plan", err))
            && hip_ok((hipError_t)sbf_launch_step(&T, &g, &in, s), "field step", err)
+           && (!conv || hip_ok(hipStreamWaitEvent(s, f->join, 0), "join", err))
            && (!conv || hip_ok((hipError_t)sbe_launch(&a, 5, s), "convection moves", err))
            && hip_ok((hipError_t)sbe_launch(&a, 1, s), "field zone means", err)
            && hip_ok((hipError_t)sbe_launch(&a, 2, s), "field env post-step", err);
@@ -708,6 +728,9 @@ double field_flops_per_step(const FieldScen* f) { return f->fdm->info.flops_per_
 void field_close(FieldScen* f) {
     if (!f) return;
     (void)hipDeviceSynchronize();
+    if (f->fork) (void)hipEventDestroy(f->fork);
+    if (f->join) (void)hipEventDestroy(f->join);
+    if (f->side) (void)hipStreamDestroy(f->side);
     for (void* p : {(void*)f->d_tables, (void*)f->d_slots, (void*)f->d_state, (void*)f->d_qz, (void*)f->d_amb,
                     (void*)f->d_hh, (void*)f->d_g, (void*)f->d_airT, (void*)f->d_moves, (void*)f->d_count,
                     (void*)f->d_vals, (void*)f->d_spill})

@@ -34,7 +34,9 @@ namespace sbe {
 
 // Per-env record (HBM, envs of a scenario back to back, stride `record`).
 // [0, bytes) is the image the HVAC kernels stage into LDS and store back;
-// the convection stream follows it (read only by the plan kernel).
+// the convection stream follows it (624 words, then its position in the
+// block), read and written only by the plan kernel, which may run beside the
+// HVAC kernels on another stream.
 struct StateLayout {
     int bytes;        // staged image (16-byte multiple)
     int record;       // record stride (256-byte multiple)
@@ -54,7 +56,7 @@ struct StateLayout {
     int ep;                                    // f32 [EP_COUNT] running episode sums
     int occ_state;                             // u8 [nz * nassign]
     int mt;                                    // u32 [624] occupancy stream (in the image)
-    int cmt;                                   // u32 [624] convection stream (after the image; 0: none)
+    int cmt;                                   // u32 [624 + 4] convection stream and position (after the image; 0: none)
 };
 
 enum {
@@ -79,7 +81,6 @@ enum {
     IP_MT_IDX,           // occupancy stream position in its block (624: twist before the next draw)
     IP_STEPS_TOTAL,      // env-steps since puf_reset
     IP_EPISODES,         // episodes ended since puf_reset
-    IP_CMT_IDX,          // convection stream position in its block
     IP_COUNT = 12
 };
 
@@ -209,13 +210,13 @@ struct Args {
     double* M;                    // interior mass, [(b * n + q) * Gl + l]
     int Gl;
     double* live;                 // the live-sums kernel adds the totals since puf_reset to live[0..2]
-    // convection moves of the step: per env at most cv_cells (field id << 32 |
-    // source field id) words, their count, the gathered values; pair overflow
-    // past the plan kernel's LDS
+    // convection moves of the step: per env at most cv_cells (convection cell
+    // << 32 | source convection cell) words, their count, the gathered values;
+    // pair overflow past the plan kernel's LDS
     unsigned long long* cv_moves; // [G][cv_cells]
     int* cv_count;                // [G]
     double* cv_vals;              // [G][cv_cells]
-    unsigned int* cv_spill;       // [G][cv_max_room]
+    unsigned int* cv_spill;       // [G][2][cv_max_room]: pairs, then shuffle draws, past the LDS
     int cv_lds_pairs;             // pairs the plan kernel keeps in LDS
 };
 

@@ -109,14 +109,35 @@ __device__ __forceinline__ uint32_t mt_temper(uint32_t y) {
     return y;
 }
 
-__device__ void mt_next_block(const uint32_t* src, uint32_t* dst) {
-    for (int i = lane(); i < 227; i += W) dst[i] = mt_mix(src[i], src[i + 1], src[i + 397]);
-    wsync();
-    for (int i = 227 + lane(); i < 454; i += W) dst[i] = mt_mix(src[i], src[i + 1], dst[i - 227]);
-    wsync();
-    for (int i = 454 + lane(); i < SBE_MT_N; i += W)
-        dst[i] = mt_mix(src[i], i + 1 < SBE_MT_N ? src[i + 1] : dst[0], dst[i - 227]);
-    wsync();
+// Each range: every lane's loads (at most four words per lane) issued before
+// its first store, so a range costs one LDS round trip. `tw`, if given,
+// receives the tempered words of the new block as well.
+__device__ void mt_next_block(const uint32_t* src, uint32_t* dst, uint32_t* tw = nullptr) {
+    auto range = [&](int lo, int hi, bool far_new) {
+        uint32_t a[4], b[4], f[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = lo + u * W + lane();
+            const bool ok = i < hi;
+            const int ic = ok ? i : lo;
+            a[u] = src[ic];
+            b[u] = ic + 1 < SBE_MT_N ? src[ic + 1] : dst[0];
+            f[u] = far_new ? dst[ic - 227] : src[ic + 397];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int i = lo + u * W + lane();
+            if (i < hi) {
+                const uint32_t x = mt_mix(a[u], b[u], f[u]);
+                dst[i] = x;
+                if (tw) tw[i] = mt_temper(x);
+            }
+        }
+        wsync();
+    };
+    range(0, 227, false);
+    range(227, 454, true);
+    range(454, SBE_MT_N, true);
 }
 
 // numpy's random_sample from two consecutive words (sb_rng.c:39-43)
@@ -854,9 +875,7 @@ struct Stream {
         while (q >= base + SBE_MT_N * (have_next ? 2 : 1)) {
             if (!have_next) {
                 const int nb = cur ^ 1;
-                mt_next_block(raw + cur * SBE_MT_N, raw + nb * SBE_MT_N);
-                for (int i = lane(); i < SBE_MT_N; i += W) tw[nb * SBE_MT_N + i] = mt_temper(raw[nb * SBE_MT_N + i]);
-                wsync();
+                mt_next_block(raw + cur * SBE_MT_N, raw + nb * SBE_MT_N, tw + nb * SBE_MT_N);
                 have_next = true;
             } else {
                 base += SBE_MT_N;
@@ -891,9 +910,18 @@ __global__ __launch_bounds__(W) void fe_conv_plan_kernel(Args a) {
     uint8_t* ncand = reinterpret_cast<uint8_t*>(qinv + t.cv_max_room);    // [cv_max_room]
     unsigned char* g = a.state + (size_t)s * a.st.record;
     uint32_t* gmt = reinterpret_cast<uint32_t*>(g + a.st.cmt);
-    int* gip = reinterpret_cast<int*>(g + a.st.ip);
-    unsigned int* spill = a.cv_spill + (size_t)s * t.cv_max_room;
+    int* gidx = reinterpret_cast<int*>(gmt + SBE_MT_N);   // the stream's position in its block
+    unsigned int* spill = a.cv_spill + (size_t)s * 2 * t.cv_max_room;
     const int cap = a.cv_lds_pairs;
+    // the room's Fisher-Yates draws: u16 in LDS beside the pairs, past the
+    // LDS pairs in the HBM overflow area's second half
+    uint16_t* jd = reinterpret_cast<uint16_t*>(lds + ((ncand + t.cv_max_room - lds + 3) & ~3));
+    unsigned int* jspill = spill + t.cv_max_room;
+    auto jd_st = [&](int i, uint32_t v) {
+        if (i < cap) jd[i] = (uint16_t)v;
+        else jspill[i - cap] = v;
+    };
+    auto jd_ld = [&](int i) -> uint32_t { return i < cap ? (uint32_t)jd[i] : jspill[i - cap]; };
     auto pr_ld = [&](int i) -> uint32_t { return i < cap ? pr[i] : spill[i - cap]; };
     auto pr_st = [&](int i, uint32_t v) {
         if (i < cap) pr[i] = v;
@@ -905,7 +933,7 @@ __global__ __launch_bounds__(W) void fe_conv_plan_kernel(Args a) {
         S.tw[i] = mt_temper(w);
     }
     S.base = 0;
-    S.pos = gip[IP_CMT_IDX];
+    S.pos = *gidx;
     S.cur = 0;
     S.have_next = false;
     wsync();
@@ -915,58 +943,117 @@ __global__ __launch_bounds__(W) void fe_conv_plan_kernel(Args a) {
     int count = 0;
     for (int rm = 0; rm < t.cv_rooms; rm++) {
         const int b0 = t.cv_off[rm], n = t.cv_off[rm + 1] - b0;
-        for (int i = lane(); i < n; i += W) {
-            ncand[i] = t.cv_ncand[b0 + i];
-            qinv[i] = (uint16_t)i;
-        }
-        wsync();
-        // cells: rounds that end at the first cell that swaps
-        int m = 0;
-        for (int j = 0; j < n;) {
-            S.ensure(S.pos + 2 * W + 1);
-            const int c = j + lane();
-            const bool ok = c < n;
-            const long long p = S.pos + 2 * lane();
-            const uint32_t w0 = S.word(p), w1 = S.word(p + 1), w2 = S.word(p + 2);
-            const int nc = ok ? ncand[c] : 0;
-            const uint64_t u53 = ((uint64_t)(w0 >> 5) << 26) | (uint64_t)(w1 >> 6);
-            const unsigned long long acc = ballot(ok && nc > 0 && !never && u53 <= thr);
-            if (acc == 0ull) {
-                const int adv = min(W, n - j);
-                S.pos += 2 * adv;
-                j += adv;
-                continue;
+        // the room's candidate counts, eight loads in flight per lane
+        for (int i0 = 0; i0 < n; i0 += 8 * W) {
+            uint8_t c8[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = i0 + u * W + lane();
+                c8[u] = i < n ? t.cv_ncand[b0 + i] : 0;
             }
-            const int f = first_lane(acc);
-            S.pos += 2 * f + 2;
-            const int cell = j + f;
-            j = cell + 1;
-            const uint32_t mx = (uint32_t)__builtin_amdgcn_readlane(nc, f) - 1u;
-            uint32_t pick = 0;
-            if (mx != 0u) {
-                const uint32_t mask = smear(mx);
-                const uint32_t first = lane_u32(w2, f) & mask;
-                if (first <= mx) {
-                    pick = first;
-                    S.pos += 1;
-                } else {
-                    S.pos += 1;
-                    for (;;) {
-                        S.ensure(S.pos + W - 1);
-                        const uint32_t v = S.word(S.pos + lane()) & mask;
-                        const unsigned long long okm = ballot(v <= mx);
-                        if (okm) {
-                            const int gl = first_lane(okm);
-                            pick = lane_u32(v, gl);
-                            S.pos += gl + 1;
-                            break;
-                        }
-                        S.pos += W;
-                    }
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const int i = i0 + u * W + lane();
+                if (i < n) {
+                    ncand[i] = c8[u];
+                    qinv[i] = (uint16_t)i;
                 }
             }
-            if (lane() == 0) pr_st(m, (uint32_t)cell | (pick << 16));
-            m++;
+        }
+        wsync();
+        // cells, in windows of 128 stream words: lane i holds the words at
+        // offsets 2i, 2i + 1, 2i + 2 of the window, so for either parity of the
+        // drift (the words the window's swapping cells have taken beyond two
+        // per cell) the swap bit of cell i is one ballot (P0, P1), and a drift
+        // of 2t + par shifts those bits by t cells; each swap's candidate
+        // draw reads its words from the same registers
+        int m = 0;
+        for (int j = 0; j < n;) {
+            S.ensure(S.pos + 2 * W);
+            const long long p = S.pos + 2 * lane();
+            const uint32_t w0 = S.word(p), w1 = S.word(p + 1), w2 = S.word(p + 2);
+            const int nc = (j + lane() < n) ? ncand[j + lane()] : 0;
+            const uint64_t u0 = ((uint64_t)(w0 >> 5) << 26) | (uint64_t)(w1 >> 6);
+            const uint64_t u1 = ((uint64_t)(w1 >> 5) << 26) | (uint64_t)(w2 >> 6);
+            const unsigned long long P0 = ballot(!never && u0 <= thr), P1 = ballot(!never && u1 <= thr);
+            const unsigned long long HC = ballot(nc > 0);
+            // the window's pairs collect in one register (lane k: its k-th pair)
+            uint32_t wp = 0;
+            int npair = 0;
+            int c = 0, drift = 0;
+            bool slow = false;           // a candidate draw ran past the window
+            uint32_t smax = 0;
+            while (true) {
+                const int tt = drift >> 1, par = drift & 1;
+                if (c + tt >= W) break;
+                const unsigned long long cand = ((par ? P1 : P0) >> tt) & HC & (~0ull << c);
+                if (cand == 0ull) {
+                    c = W - tt;
+                    break;
+                }
+                const int cc = first_lane(cand);
+                const uint32_t mx = (uint32_t)__builtin_amdgcn_readlane(nc, cc) - 1u;
+                int q = 2 * (cc + tt) + par + 2;   // the candidate draw's first word
+                uint32_t pick = 0;
+                if (mx != 0u) {
+                    const uint32_t mask = smear(mx);
+                    for (;;) {
+                        if (q >= 2 * W) {
+                            slow = true;
+                            break;
+                        }
+                        const uint32_t wa = lane_u32(w0, q >> 1), wb = lane_u32(w1, q >> 1);
+                        const uint32_t v = ((q & 1) ? wb : wa) & mask;
+                        q++;
+                        if (v <= mx) {
+                            pick = v;
+                            break;
+                        }
+                    }
+                }
+                if (slow) {
+                    // the draw continues past the window: finish it from LDS
+                    S.pos += q;
+                    j += cc;
+                    smax = mx;
+                    break;
+                }
+                wp = lane() == npair ? ((uint32_t)(j + cc) | (pick << 16)) : wp;
+                npair++;
+                drift = q - 2 * (cc + 1);
+                c = cc + 1;
+            }
+            if (npair > 0) {
+                if (m + W <= cap) {
+                    if (lane() < npair) pr[m + lane()] = wp;
+                } else if (lane() < npair) {
+                    pr_st(m + lane(), wp);
+                }
+                m += npair;
+            }
+            if (slow) {
+                const uint32_t mask = smear(smax);
+                uint32_t pick = 0;
+                for (;;) {
+                    S.ensure(S.pos + W - 1);
+                    const uint32_t v = S.word(S.pos + lane()) & mask;
+                    const unsigned long long okm = ballot(v <= smax);
+                    if (okm) {
+                        const int gl = first_lane(okm);
+                        pick = lane_u32(v, gl);
+                        S.pos += gl + 1;
+                        break;
+                    }
+                    S.pos += W;
+                }
+                if (lane() == 0) pr_st(m, (uint32_t)j | (pick << 16));
+                m++;
+                j += 1;
+                continue;
+            }
+            const int ce = min(c, n - j);   // the window's cells past the room draw nothing
+            S.pos += 2 * ce + drift;
+            j += ce;
         }
         wsync();
         // each pair's candidate as a room-local cell
@@ -977,14 +1064,10 @@ __global__ __launch_bounds__(W) void fe_conv_plan_kernel(Args a) {
             pr_st(i, (uint32_t)cell | (right << 16));
         }
         wsync();
-        // Fisher-Yates from the top; pair t is final once the shuffle has
-        // passed it and is composed into q right away
-        auto compose = [&](uint32_t y) {
-            const int ca = (int)(y & 0xffffu), cb = (int)(y >> 16);
-            const uint16_t qa = qinv[ca], qb = qinv[cb];
-            qinv[ca] = qb;
-            qinv[cb] = qa;
-        };
+        // Fisher-Yates from the top: every draw resolved first (64 stream
+        // words per ballot pass; draw t into jd[t]), then lane 0 applies them,
+        // each final pair composed into q (q <- q o (a b)); the composition of
+        // one pair overlaps the loads of the next, one LDS round trip a draw
         for (int tt = m - 1; tt > 0;) {
             S.ensure(S.pos + W - 1);
             const uint32_t w = S.word(S.pos + lane());
@@ -997,30 +1080,59 @@ __global__ __launch_bounds__(W) void fe_conv_plan_kernel(Args a) {
                     break;
                 }
                 const int gl = first_lane(okm);
-                const int j2 = (int)(lane_u32(w, gl) & mask);
+                if (lane() == 0) jd_st(tt, (lane_u32(w, gl) & mask));
                 kx = gl + 1;
-                if (lane() == 0) {
-                    const uint32_t x = pr_ld(tt), y = pr_ld(j2);
-                    pr_st(j2, x);
-                    compose(y);
-                }
                 tt--;
             }
             S.pos += kx;
         }
-        if (m > 0 && lane() == 0) compose(pr_ld(0));
         wsync();
-        // moves: cell i's value goes to cell q[i]
+        for (int top = m - 1; top > 0; top -= W) {
+            const int mine = top - lane();
+            const uint32_t jl = mine > 0 ? jd_ld(mine) : 0u;
+            if (lane() == 0) {
+                const int cnt = min(W, top);
+                uint32_t held = 0;
+                bool have = false;
+                for (int l = 0; l < cnt; l++) {
+                    const int t2 = top - l;
+                    const int j2 = (int)lane_u32(jl, l);
+                    const uint32_t x = pr_ld(t2), y = pr_ld(j2);
+                    if (have) {
+                        const int ca = (int)(held & 0xffffu), cb = (int)(held >> 16);
+                        const uint16_t qa = qinv[ca], qb = qinv[cb];
+                        qinv[ca] = qb;
+                        qinv[cb] = qa;
+                    }
+                    pr_st(j2, x);
+                    held = y;
+                    have = true;
+                }
+                if (have) {
+                    const int ca = (int)(held & 0xffffu), cb = (int)(held >> 16);
+                    const uint16_t qa = qinv[ca], qb = qinv[cb];
+                    qinv[ca] = qb;
+                    qinv[cb] = qa;
+                }
+            }
+            wsync();
+        }
+        if (m > 0 && lane() == 0) {
+            const uint32_t y = pr_ld(0);
+            const int ca = (int)(y & 0xffffu), cb = (int)(y >> 16);
+            const uint16_t qa = qinv[ca], qb = qinv[cb];
+            qinv[ca] = qb;
+            qinv[cb] = qa;
+        }
+        wsync();
+        // moves: cell i's value goes to cell q[i] (convection-cell indices;
+        // the move kernels map them to field cells)
         for (int i0 = 0; i0 < n; i0 += W) {
             const int i = i0 + lane();
             const int q = i < n ? (int)qinv[i] : i;
             const bool mv = i < n && q != i;
             const unsigned long long mm = ballot(mv);
-            if (mv) {
-                const unsigned long long dst = (unsigned long long)(unsigned)t.cv_cell[b0 + q];
-                const unsigned long long src = (unsigned long long)(unsigned)t.cv_cell[b0 + i];
-                moves[count + below_me(mm)] = (dst << 32) | src;
-            }
+            if (mv) moves[count + below_me(mm)] = ((unsigned long long)(unsigned)(b0 + q) << 32) | (unsigned)(b0 + i);
             count += __popcll(mm);
         }
         wsync();
@@ -1030,7 +1142,7 @@ __global__ __launch_bounds__(W) void fe_conv_plan_kernel(Args a) {
     const int blkx = d > SBE_MT_N ? (S.cur ^ 1) : S.cur;
     for (int i = lane(); i < SBE_MT_N; i += W) gmt[i] = S.raw[blkx * SBE_MT_N + i];
     if (lane() == 0) {
-        gip[IP_CMT_IDX] = (int)(d > SBE_MT_N ? d - SBE_MT_N : d);
+        *gidx = (int)(d > SBE_MT_N ? d - SBE_MT_N : d);
         a.cv_count[s] = count;
     }
 }
@@ -1045,7 +1157,7 @@ __global__ void fe_conv_gather_kernel(Args a) {
     const unsigned long long* mv = a.cv_moves + (size_t)s * a.t.cv_cells;
     double* val = a.cv_vals + (size_t)s * a.t.cv_cells;
     for (int i = (int)(blockIdx.x * blockDim.x + threadIdx.x); i < cnt; i += (int)(gridDim.x * blockDim.x))
-        val[i] = T[(size_t)(unsigned)(mv[i] & 0xffffffffull) * Gl];
+        val[i] = T[(size_t)(unsigned)a.t.cv_cell[(unsigned)(mv[i] & 0xffffffffull)] * Gl];
 }
 
 __global__ void fe_conv_scatter_kernel(Args a) {
@@ -1056,7 +1168,7 @@ __global__ void fe_conv_scatter_kernel(Args a) {
     const unsigned long long* mv = a.cv_moves + (size_t)s * a.t.cv_cells;
     const double* val = a.cv_vals + (size_t)s * a.t.cv_cells;
     for (int i = (int)(blockIdx.x * blockDim.x + threadIdx.x); i < cnt; i += (int)(gridDim.x * blockDim.x))
-        T[(size_t)(unsigned)(mv[i] >> 32) * Gl] = val[i];
+        T[(size_t)(unsigned)a.t.cv_cell[(unsigned)(mv[i] >> 32)] * Gl] = val[i];
 }
 
 // Adds the group's f64 reward sum, env-steps and episodes since puf_reset to
@@ -1101,7 +1213,7 @@ extern "C" int sbe_launch(const sbe::Args* a, int which, hipStream_t s) {
     case 2: hipLaunchKernelGGL(fe_post_kernel, dim3(G), dim3(64), a->lds_bytes, s, *a); break;
     case 3: hipLaunchKernelGGL(fe_live_kernel, dim3(1), dim3(64), 0, s, *a); break;
     case 4: {
-        const size_t lds = 4 * 4 * SBE_MT_N + 4 * (size_t)a->cv_lds_pairs + 3 * (size_t)a->t.cv_max_room + 16;
+        const size_t lds = 4 * 4 * SBE_MT_N + 6 * (size_t)a->cv_lds_pairs + 3 * (size_t)a->t.cv_max_room + 16;
         hipLaunchKernelGGL(fe_conv_plan_kernel, dim3(G), dim3(64), lds, s, *a);
         break;
     }
