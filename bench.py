@@ -376,8 +376,6 @@ def main() -> int:
     ap.add_argument("--kernel-iters", type=int, default=200)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--log-at-end", action="store_true",
-                    help="env key log_at_end=1: the host Log written at episode ends only (no host reads per step)")
     ap.add_argument("--no-lu", action="store_true", help="skip the second timing under the LU solver")
     ap.add_argument("--solver", default="auto", choices=["auto", "relax", "point", "lu"])
     ap.add_argument("--conv", type=float, default=0.0,
@@ -425,8 +423,7 @@ def main() -> int:
     t0 = time.time()
     blob_dir = scenario_dir(args.config, args.conv)
     log(f"scenarios ready in {time.time() - t0:.1f}s: {blob_dir}")
-    vec = E.VecEnv(n_envs, blob_dir=str(blob_dir), groups=groups, start_offsets=int(offsets), solver=args.solver,
-                   log_at_end=int(args.log_at_end))
+    vec = E.VecEnv(n_envs, blob_dir=str(blob_dir), groups=groups, start_offsets=int(offsets), solver=args.solver)
     info = vec.info()
     rollout = args.config == 4
     if rollout:
@@ -566,8 +563,7 @@ def main() -> int:
                                + ("shared-policy MLP 1024-128-128-544 (fp32 MFMA) + Beta sampling per step, "
                                   if rollout else "Beta(2,2) actions, ")
                                + "fp64 physics" + (", desynchronised starts (seeded per-env calendar offsets)" if offsets else "")
-                               + (f", stochastic convection p={args.conv}" if args.conv > 0 else "")
-                               + (", log_at_end=1 (host Log at episode ends)" if args.log_at_end else ""),
+                               + (f", stochastic convection p={args.conv}" if args.conv > 0 else ""),
                    "n_envs": n_envs, "scenarios": groups, "episode_steps": G.EPISODE_STEPS,
                    "solver": solver["solver"], "envs_per_workgroup": info.envs_per_block,
                    "block": info.block, "lds_bytes": info.lds_bytes},

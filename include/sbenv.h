@@ -51,13 +51,30 @@ extern "C" {
 
 typedef float obs_t;
 
-/* Episode log, complete_port/pufferlib_cpu_env.h:82-89 (n is the last field). */
+/* Episode log of the reference GPU env this library replaces,
+ * complete_port/gpu/smart_buildings.cu:101-115 (n is the last field, as the
+ * trainer's log aggregation requires). Filled when an episode ends
+ * (finalize_k, :1936-2047): the trainer may clear it between steps, so the
+ * running sums stay on the device. Every field but n is a sum over the
+ * episodes logged since the last clear: perf and score the episode's mean
+ * reward, episode_return and episode_length, the episode means of the
+ * per-step mean zone deviation from the comfort band (comfort_dev_K), of the
+ * fraction of zones outside it (out_of_band_frac), of the normalized
+ * productivity term, energy cost and carbon, the episode's worst zone
+ * deviation (worst_dev_K), and its electricity and gas kWh. */
 typedef struct Log {
     float perf;
     float score;
     float episode_return;
     float episode_length;
-    float reward_mean;
+    float comfort_dev_K;
+    float worst_dev_K;
+    float out_of_band_frac;
+    float productivity;
+    float energy_cost_norm;
+    float carbon_norm;
+    float elec_kwh;
+    float gas_kwh;
     float n;
 } Log;
 
@@ -117,12 +134,9 @@ void dict_set(Dict* d, const char* key, float value);
  * Extras: start_offsets (1: every env starts its episodes at its own seeded
  * calendar offset, start_seed), shard_base (this vec's first env index in a
  * batch sharded over several vecs), per_env_seed (occupancy / convection seed
- * + index within the scenario, default 1), solver, envs_per_block, log_at_end
- * (1: each env's running episode return and mean reward stay on the device
- * and are added to its Log when the episode ends, as the reference GPU env
- * fills Log at episode ends (smart_buildings.cu:123-125), so puf_step reads no
- * host memory; 0, the default: the CPU env's per-step Log, read and written
- * every step, which sees a trainer's mid-episode clears; RC layouts only). */
+ * + index within the scenario, default 1), solver, envs_per_block. The Log
+ * is filled at episode ends (the reference GPU env's form); the key log_at_end
+ * is accepted at 1 only (the per-step Log of earlier versions is gone). */
 Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions,
                     float* rewards, float* terminals);
 /* NULL binds the null stream (the binding before any call); the reference
@@ -133,7 +147,14 @@ void puf_reset(Env* envs);
 void puf_step(Env* envs);
 void puf_render(Env* env);
 void puf_close(Env* envs);
+/* Every Log field under its name (smart_buildings.cu:3044-3066). */
 void puf_log(Log* log, Dict* out);
+/* Totals since the previous call (a device reduction, then one sync):
+ * env_steps, episodes, reward_mean over every env, and, when the vec holds
+ * more than one scenario, scenario/<name>/reward and
+ * scenario/<name>/comfort_dev_K, the scenario's mean reward and mean zone
+ * deviation per env-step of the window (smart_buildings.cu:3069-3100; <name>
+ * is the blob's file name without .sbb). */
 void puf_live_log(Env* envs, Dict* out);
 void puf_mask_init(unsigned char* mask, int width, int nagents);
 

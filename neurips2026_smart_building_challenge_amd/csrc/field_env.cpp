@@ -451,7 +451,7 @@ FieldScen* field_open(const sbh::Blob& b, std::string* err) {
     // (AHU demand, column flow demand), the reward (VAV sums, AHU terms, zone
     // terms) or one MT block
     {
-        const int scratch = std::max({8 * (na + k), 8 * (nv + 3 * na + nz), 4 * SBE_MT_N});
+        const int scratch = std::max({8 * (na + k), 8 * (nv + 3 * na + 2 * nz), 4 * SBE_MT_N});
         f.lds_bytes = S.bytes + ((scratch + 15) & ~15);
         if (f.lds_bytes > 160 * 1024) return bad("an env's HVAC state does not fit in LDS");
     }
@@ -710,9 +710,10 @@ int field_state(FieldScen* f, int slot, double* out, int cap) {
     return (int)o.size();
 }
 
-bool field_live(FieldScen* f, double* out, hipStream_t s) {
+bool field_live(FieldScen* f, double* out, int scen, hipStream_t s) {
     sbe::Args a = base_args(f);
     a.live = out;
+    a.live_scen = scen;
     return sbe_launch(&a, 3, s) == 0;
 }
 

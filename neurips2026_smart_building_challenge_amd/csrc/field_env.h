@@ -68,6 +68,7 @@ enum {
     PL_BOILER_DSTEP,
     PL_PUMP_HEAD,
     PL_REW_SUM,          // f64 sum of rewards since puf_reset
+    PL_DEV_SUM,          // f64 sum since puf_reset of each step's mean zone deviation from the comfort band
     PL_COUNT
 };
 
@@ -84,8 +85,12 @@ enum {
     IP_COUNT = 12
 };
 
-// Running episode sums (float, as the reference GPU env keeps them)
-enum { EP_RET = 0, EP_MEAN = 1, EP_COUNT = 4 };
+// The reference GPU env's running episode sums, float (complete_port/gpu/
+// smart_buildings.cu:118-121, 1965-1971): the reward, the 8 per-step
+// diagnostics (productivity term, normalized energy cost, normalized carbon,
+// mean zone deviation, worst zone deviation (its sum unused), out-of-band
+// fraction, electricity kWh, gas kWh), then the worst deviation as a maximum
+enum { EP_RET = 0, EP_PART = 1, EP_WORST = 9, EP_COUNT = 10 };
 
 // Read-only tables of one field scenario (device pointers).
 struct Tabs {
@@ -210,6 +215,7 @@ struct Args {
     double* M;                    // interior mass, [(b * n + q) * Gl + l]
     int Gl;
     double* live;                 // the live-sums kernel adds the totals since puf_reset to live[0..2]
+    int live_scen;                //   and the scenario's to live[3 + 3 live_scen ..]
     // convection moves of the step: per env at most cv_cells (convection cell
     // << 32 | source convection cell) words, their count, the gathered values;
     // pair overflow past the plan kernel's LDS
@@ -227,6 +233,6 @@ static_assert(sizeof(Slot) == 32, "Slot layout");
 static_assert(offsetof(Tabs, gas_co2) == 528 && offsetof(Tabs, temp_init) == 536 && offsetof(Tabs, cv_off) == 576
               && sizeof(Tabs) == 616, "Tabs layout");
 static_assert(offsetof(Args, st) == 616 && offsetof(Args, state) == 760 && offsetof(Args, qz) == 840
-              && offsetof(Args, live) == 904 && sizeof(Args) == 952, "Args layout");
+              && offsetof(Args, live) == 904 && sizeof(Args) == 960, "Args layout");
 
 }  // namespace sbe

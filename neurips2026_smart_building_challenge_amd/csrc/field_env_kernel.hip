@@ -562,12 +562,15 @@ __device__ void occupancy(const Tabs& t, Rec& r, int hour, int workday, uint32_t
 // ------------------------------------------------------------------ reward
 // 3C reward at calendar row kv from the zone means of the new field
 // (sb_reward.c:31-155; the tank dissipation's denominator precomputed on the
-// host). `scr` is f64 scratch of at least 2 nv + 3 na + nz.
-__device__ double reward(const Tabs& t, Rec& r, double* scr, int kv) {
+// host), and in `dg` (lane 0) the reference GPU env's 8 per-step diagnostics
+// (complete_port/gpu/sb_gpu_kernels.cuh:1409-1473). `scr` is f64 scratch of
+// at least nv + 3 na + 2 nz.
+__device__ double reward(const Tabs& t, Rec& r, double* scr, int kv, double (&dg)[8]) {
     const int na = t.na, nv = t.nv, nz = t.nz;
     double* vwt = scr;                 // [nv] VAV mean * area (area > 0)
     double* ahu_terms = scr + nv;      // [3 na] intake, exhaust, cooling
     double* zterm = ahu_terms + 3 * na;   // [nz] productivity term
+    double* zdev = zterm + nz;            // [nz] deviation from the comfort band
     const double dt = t.dt_sec, inv_hour = 1.0 / 3600.0;
     const double ambient = t.amb[kv];
     for (int v = lane(); v < nv; v += W) {
@@ -584,6 +587,7 @@ __device__ double reward(const Tabs& t, Rec& r, double* scr, int kv) {
         if (dev < 0.0) dev = 0.0;
         const double sh = (dev <= ref) ? dev / ref : 1.0 + ((dev - ref) / ref) * ((dev - ref) / ref);
         zterm[z] = max_pph * (1.0 - sh) * r.occV[z] * dt * inv_hour;
+        zdev[z] = dev;
     }
     wsync();
     for (int q = lane(); q < na; q += W) {
@@ -614,10 +618,14 @@ __device__ double reward(const Tabs& t, Rec& r, double* scr, int kv) {
             exhaust += ahu_terms[3 * q + 1];
             cooling += ahu_terms[3 * q + 2];
         }
-        double total_occ = 0.0, cum = 0.0;
+        double total_occ = 0.0, cum = 0.0, dsum = 0.0, dmax = 0.0;
+        int n_oob = 0;
         for (int z = 0; z < nz; z++) {
             total_occ += r.occV[z];
             cum += zterm[z];
+            dsum += zdev[z];
+            if (zdev[z] > dmax) dmax = zdev[z];
+            if (zdev[z] > 0.0) n_oob++;
         }
         const double tf = water_flow(t, r);
         const double* bc = t.boiler_c;
@@ -643,6 +651,14 @@ __device__ double reward(const Tabs& t, Rec& r, double* scr, int kv) {
         const double ncar = (den_c > 0.0) ? (crate * fabs(elec) * dt + t.gas_co2 * gas * dt) / den_c : 0.0;
         const double pw = t.rw[5], ew = t.rw[6], cw = t.rw[7];
         rew = (npr * pw - nec * ew - ncar * cw) / (pw + ew + cw);
+        dg[0] = npr;
+        dg[1] = nec;
+        dg[2] = ncar;
+        dg[3] = nz > 0 ? dsum / nz : 0.0;
+        dg[4] = dmax;
+        dg[5] = nz > 0 ? (double)n_oob / nz : 0.0;
+        dg[6] = fabs(elec) * dt / 3.6e6;
+        dg[7] = gas * dt / 3.6e6;
     }
     wsync();
     return rew;
@@ -714,26 +730,25 @@ __device__ void env_reset(const Tabs& t, Rec& r, const Slot& sl, float* obs_row,
     }
 }
 
-// The env's Log fields as the CPU env updates them (pufferlib_cpu_env.h:243-255):
-// the running return and mean every step, the episode's mean return, length
-// and count at its end.
-__device__ void log_step(const Args& a, int env, float r, int step, bool done) {
-    Log* lg = reinterpret_cast<Log*>(reinterpret_cast<unsigned char*>(a.host_env) + (size_t)env * a.env_stride
-                                     + a.log_offset);
-    float* lf = reinterpret_cast<float*>(lg);
-    const float ret = __hip_atomic_load(&lg->episode_return, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) + r;
-    const float m0 = __hip_atomic_load(&lg->reward_mean, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    __hip_atomic_store(&lg->episode_return, ret, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    __hip_atomic_store(&lg->reward_mean, m0 + (r - m0) / (float)step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    if (!done) return;
-    const float m = ret / (float)step;
-    const int add_at[4] = {0, 1, 3, 5};
-    const float add[4] = {m, m, (float)step, 1.0f};
-    for (int i = 0; i < 4; i++) {
-        const float x = __hip_atomic_load(&lf[add_at[i]], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        __hip_atomic_store(&lf[add_at[i]], x + add[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+// A whole episode's sums added to the env's host-visible Log (the reference
+// GPU env's finalize_k, complete_port/gpu/smart_buildings.cu:2002-2036), each
+// field read and written with system-scope accesses (the trainer may clear
+// the Log between steps). ep: EP_* running sums, st: the episode's length.
+__device__ void log_episode(const Args& a, int env, const float* ep, int st) {
+    float* f = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(a.host_env) + (size_t)env * a.env_stride
+                                        + a.log_offset);
+    const float s = (float)st;
+    const float mean = ep[EP_RET] / s;
+    const float add[13] = {mean, mean, ep[EP_RET], s,
+                           ep[EP_PART + 3] / s, ep[EP_WORST], ep[EP_PART + 5] / s,
+                           ep[EP_PART + 0] / s, ep[EP_PART + 1] / s, ep[EP_PART + 2] / s,
+                           ep[EP_PART + 6], ep[EP_PART + 7], 1.0f};
+    for (int i = 0; i < 13; i++) {
+        const float x = __hip_atomic_load(&f[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(&f[i], x + add[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     }
 }
+static_assert(sizeof(Log) == 52 && offsetof(Log, n) == 48, "log_episode writes the reference GPU env's Log");
 
 }  // namespace
 
@@ -758,6 +773,7 @@ __global__ __launch_bounds__(W) void fe_pre_kernel(Args a) {
             r.ip[IP_STEPS_TOTAL] = 0;
             r.ip[IP_EPISODES] = 0;
             r.pl[PL_REW_SUM] = 0.0;
+            r.pl[PL_DEV_SUM] = 0.0;
             for (int i = 0; i < EP_COUNT; i++) r.ep[i] = 0.0f;
         }
     } else {
@@ -813,7 +829,8 @@ __global__ __launch_bounds__(W) void fe_post_kernel(Args a) {
     write_obs(t, r, obs_row, j);
     wsync();
     occupancy(t, r, (int)t.occ_hour[j], (int)t.occ_work[j], blk);
-    const double rew = reward(t, r, scr, j);
+    double dg[8];
+    const double rew = reward(t, r, scr, j, dg);
     // the first episode after puf_vec_create may be cut short (desync); a cut
     // episode is a truncation and stays out of the episode log
     // (complete_port/gpu/smart_buildings.cu:1990-1993, 2043)
@@ -826,11 +843,18 @@ __global__ __launch_bounds__(W) void fe_post_kernel(Args a) {
         a.terminals[sl.env] = done ? 1.0f : 0.0f;
         r.ip[IP_STEP] = step;
         r.pl[PL_REW_SUM] += rew;
+        r.pl[PL_DEV_SUM] += dg[3];
         r.ip[IP_STEPS_TOTAL] += 1;
-        if (a.host_env && !cut) log_step(a, sl.env, rf, step, done);
+        // the episode's running sums in float (smart_buildings.cu:1965-1971),
+        // into the host Log when a whole episode ends
+        r.ep[EP_RET] += rf;
+        for (int k = 0; k < 8; k++) r.ep[EP_PART + k] += (float)dg[k];
+        if ((float)dg[4] > r.ep[EP_WORST]) r.ep[EP_WORST] = (float)dg[4];
         if (done) {
             r.ip[IP_EPISODES] += 1;
             r.ip[IP_FIRST_DONE] = 1;
+            if (a.host_env && !cut) log_episode(a, sl.env, r.ep, step);
+            for (int k = 0; k < EP_COUNT; k++) r.ep[k] = 0.0f;
         }
     }
     wsync();
@@ -1175,11 +1199,13 @@ __global__ void fe_conv_scatter_kernel(Args a) {
 // live[0..2]: lane l sums envs l, l + 64, ... in order, lane 0 the lanes' sums
 // in lane order (independent of timing).
 __global__ __launch_bounds__(W) void fe_live_kernel(Args a) {
-    __shared__ double part[3][W];
-    double rs = 0.0, st = 0.0, ep = 0.0;
+    __shared__ double part[4][W];
+    double rs = 0.0, st = 0.0, ep = 0.0, dv = 0.0;
     for (int s = lane(); s < a.G; s += W) {
         const unsigned char* rec = a.state + (size_t)s * a.st.record;
-        rs += reinterpret_cast<const double*>(rec + a.st.plant)[PL_REW_SUM];
+        const double* pl = reinterpret_cast<const double*>(rec + a.st.plant);
+        rs += pl[PL_REW_SUM];
+        dv += pl[PL_DEV_SUM];
         const int* ip = reinterpret_cast<const int*>(rec + a.st.ip);
         st += (double)ip[IP_STEPS_TOTAL];
         ep += (double)ip[IP_EPISODES];
@@ -1187,11 +1213,17 @@ __global__ __launch_bounds__(W) void fe_live_kernel(Args a) {
     part[0][lane()] = rs;
     part[1][lane()] = st;
     part[2][lane()] = ep;
+    part[3][lane()] = dv;
     __syncthreads();
-    if (lane() < 3) {
+    if (lane() < 4) {
         double x = 0.0;
         for (int i = 0; i < W; i++) x += part[lane()][i];
-        a.live[lane()] += x;
+        if (lane() < 3) a.live[lane()] += x;
+        if (a.live_scen >= 0) {
+            // the scenario's (reward sum, deviation sum, env-steps)
+            const int slot = lane() == 0 ? 0 : (lane() == 3 ? 1 : (lane() == 1 ? 2 : -1));
+            if (slot >= 0) a.live[3 + 3 * a.live_scen + slot] += x;
+        }
     }
 }
 

@@ -57,8 +57,9 @@ bool field_step(FieldScen* f, const FieldIo& io, bool reset, hipStream_t s, std:
 int field_state(FieldScen* f, int slot, double* out, int cap);
 
 // Adds the scenario's totals since puf_reset (reward sum, env-steps,
-// episodes) to out[0..2] (device, stream-ordered).
-bool field_live(FieldScen* f, double* out, hipStream_t s);
+// episodes) to out[0..2] and (reward sum, mean zone deviation sum, env-steps)
+// to out[3 + 3 scen ..] (device, stream-ordered).
+bool field_live(FieldScen* f, double* out, int scen, hipStream_t s);
 
 double field_bytes_per_step(const FieldScen* f);
 double field_flops_per_step(const FieldScen* f);

@@ -42,13 +42,13 @@ struct StateLayout {
     int T, M;                                   // [n]
     int damper, reheat, ratio, heatsp, coolsp, dcmd, rcmd, sensing;  // [nv]
     int recirc, sat, fan, flow;                 // [na]
-    int plant;                                  // f64[8], see PF_*
+    int plant;                                  // f64[PF_COUNT], see PF_*
     int cal, cal_n;                             // f64[2][cal_n]: a step's calendar values (RW_*, then
                                                 // the aux-time row), in section (calendar index & 1),
                                                 // prefetched by the step before (or the reset)
     // i32 arrays
     int run, coolreq;                           // [na]
-    int iplant;                                 // i32[8], see PI_*
+    int iplant;                                 // i32[PI_COUNT], see PI_*
     // u8 arrays
     int mode, prev_valid, dcmd_set, rcmd_set;   // [nv]
     int occ_state;                              // [nz * nassign]
@@ -59,9 +59,10 @@ struct StateLayout {
     int record_bytes;                           // image + mt (+ cmt), 256-byte aligned
 };
 
-// PF_SWEEPS: relaxation sweeps of the last step; PF_CAPPED: steps that hit the sweep cap
+// PF_SWEEPS: relaxation sweeps of the last step; PF_CAPPED: steps that hit the sweep cap;
+// PF_DEV_SUM: sum since puf_reset of each step's mean zone deviation from the comfort band
 enum { PF_PUMP_HEAD = 0, PF_BOILER_SP, PF_BOILER_RET, PF_BOILER_CUR, PF_BOILER_DSTEP,
-       PF_REW_SUM, PF_SWEEPS, PF_CAPPED };
+       PF_REW_SUM, PF_SWEEPS, PF_CAPPED, PF_DEV_SUM, PF_COUNT };
 
 enum { SOLVER_LU = 0, SOLVER_RELAX = 1 };
 // Step-kernel variants, one per field-solver form (each compiles only its own
@@ -70,10 +71,16 @@ enum { SOLVER_LU = 0, SOLVER_RELAX = 1 };
 enum { KV_LU = 0, KV_POINT = 1, KV_BLOCK = 2, KV_COUNT = 3 };
 // PI_FIRST_DONE: 1 once the env's first episode after puf_vec_create has
 // ended (puf_reset leaves it; the first episode is the one desync truncates).
-// PI_EP_RET, PI_EP_MEAN (float bits): the episode's running return and mean
-// reward when the log is written at episode ends only (env key log_at_end)
+// PI_EP .. PI_EP + EP_COUNT - 1 (float bits): the episode's running sums that
+// fill the Log when it ends (EP_*)
 enum { PI_HWS_RUN = 0, PI_PUMP_RUN, PI_HWS_REQ, PI_STEP_INDEX, PI_STEP, PI_MT_IDX,
-       PI_STEPS_TOTAL, PI_EPISODES, PI_CONV_IDX, PI_FIRST_DONE, PI_EP_RET, PI_EP_MEAN, PI_COUNT = 16 };
+       PI_STEPS_TOTAL, PI_EPISODES, PI_CONV_IDX, PI_FIRST_DONE, PI_EP, PI_COUNT = 20 };
+// The reference GPU env's running episode sums (complete_port/gpu/smart_buildings.cu:
+// 118-121, 1965-1971): the float reward, the 8 per-step diagnostics (productivity
+// term, normalized energy cost, normalized carbon, mean zone deviation, worst zone
+// deviation (its sum unused), out-of-band fraction, electricity kWh, gas kWh),
+// then the worst deviation as a maximum
+enum { EP_RET = 0, EP_PART = 1, EP_WORST = 9, EP_COUNT = 10 };
 
 // Per-env LDS region (byte offsets from the env's base; a workgroup holds the
 // layout image first, then one region per env).
@@ -305,11 +312,11 @@ enum { KMODE_STEP = 0, KMODE_RESET = 1 };
 // ready) and by the helper (VAV sensed temperatures ready; AHU return-air
 // sums ready; observation
 // written, new occupancy committed and reward half ready); the helper's reward
-// half (4 f64 from SY_PART) and the host log fields it read (2 f32 from SY_LOG);
-// the helper's stores of the record's leading arrays complete (SY_STORED);
-// the helper's convection permutation of the step (SY_CONV).
-enum { SY_PRE = 0, SY_POST = 1, SY_HALF = 2, SY_SENS = 3, SY_PART = 4, SY_LOG = 12, SY_RET = 14, SY_CONV = 15,
-       SY_STORED = 16, SY_WORDS = 17 };
+// half (7 f64 from SY_PART); the helper's stores of the record's leading
+// arrays complete (SY_STORED); the helper's convection permutation of the
+// step (SY_CONV).
+enum { SY_PRE = 0, SY_POST = 1, SY_HALF = 2, SY_SENS = 3, SY_PART = 4, SY_RET = 18, SY_CONV = 19,
+       SY_STORED = 20, SY_WORDS = 21 };
 
 // A workgroup's envs: order[first .. first + count) all of one layout, with
 // the layout's staging burst inputs (copied from its DevLayout) and each
@@ -348,7 +355,7 @@ struct KParams {
     unsigned long long* phase_ts;   // null, or [n_envs * SBK_NSTAMP] wall-clock stamps
     unsigned long long* pass_ts;    // null, or [n_pass + 1] shader-clock stamps of one env
     int pass_ts_env;                // env whose solve passes are stamped
-    int log_at_end;                 // 1: the host Log only at episode ends, running sums in the record
+    int pad_le;
 };
 
 // The host (g++) and the device (hipcc) compile these structs separately and
@@ -364,6 +371,6 @@ static_assert(sizeof(DevLayout) == 888 && offsetof(DevLayout, st) == 88 && offse
 static_assert(sizeof(DevScen) == 472 && offsetof(DevScen, img_src) == 32 && offsetof(DevScen, gas_co2) == 200
               && offsetof(DevScen, conv_p) == 464, "DevScen layout");
 static_assert(sizeof(KParams) == 136 && offsetof(KParams, host_env) == 80 && offsetof(KParams, phase_ts) == 112
-              && offsetof(KParams, pass_ts_env) == 128 && offsetof(KParams, log_at_end) == 132, "KParams layout");
+              && offsetof(KParams, pass_ts_env) == 128, "KParams layout");
 
 }  // namespace sbk

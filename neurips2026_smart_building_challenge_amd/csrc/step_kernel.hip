@@ -2309,7 +2309,9 @@ __device__ __forceinline__ void reward_vavs(Ctx& c, const double* zm, int (&vahu
 // reward_combine in csim's order of operations.
 struct RewardPart {
     double gas_rate, pump_e, total_occ, cum;
+    double dev_sum, dev_max, oob;   // comfort diagnostics: zone deviations from the band
 };
+static_assert(sizeof(RewardPart) == 4 * (SY_RET - SY_PART), "the helper's reward half fills SY_PART..SY_RET");
 
 // AHU half (sb_reward.c:62-98): `zm` holds the zone means of the post-step
 // field. Returns blower (intake + exhaust) and cooling power.
@@ -2391,7 +2393,7 @@ __device__ __forceinline__ RewardPart reward_rest(Ctx& c, const double* zm, cons
     out.pump_e = tf * RHO_W * GRAV * c.plant[PF_PUMP_HEAD] / S->pump_eff;
     const double max_pph = S->rw[0], ref = S->rw[2];
     const double hsp = rw[RW_HSP_J], csp = rw[RW_CSP_J];
-    double occ_part = 0.0, cum_part = 0.0;
+    double occ_part = 0.0, cum_part = 0.0, dsum = 0.0, dmax = 0.0, noob = 0.0;
     {
         // zones z = lane + 64 r: loads of every slot first, then the sums in
         // slot order
@@ -2417,20 +2419,33 @@ __device__ __forceinline__ RewardPart reward_rest(Ctx& c, const double* zm, cons
                 double dev = zt - csp;
                 if (hsp - zt > dev) dev = hsp - zt;
                 if (dev < 0.0) dev = 0.0;
+                dsum += dev;
+                dmax = fmax(dmax, dev);
+                noob += dev > 0.0 ? 1.0 : 0.0;
                 double sh = (dev <= ref) ? dev / ref : 1.0 + ((dev - ref) / ref) * ((dev - ref) / ref);
                 cum_part += max_pph * (1.0 - sh) * occ * dt * inv_hour;
             }
         }
     }
     wave_sum2(occ_part, cum_part);
+    wave_sum2(dsum, noob);
     out.total_occ = occ_part;
     out.cum = cum_part;
+    out.dev_sum = dsum;
+    out.dev_max = wave_max(dmax);
+    out.oob = noob;
     return out;
 }
 
 // Normalised productivity, cost and carbon, and the weighted reward
 // (sb_reward.c:99-155).
-__device__ __forceinline__ double reward_combine(const Ctx& c, double blower, double cooling, const RewardPart& p) {
+// The step's 8 diagnostics of the reference GPU env (sb_gpu_kernels.cuh:1466-1473).
+struct StepParts {
+    double v[8];
+};
+
+__device__ __forceinline__ double reward_combine(const Ctx& c, double blower, double cooling, const RewardPart& p,
+                                                 StepParts& sp) {
     const SBK_C DevScen* S = c.S;
     const double dt = S->dt_sec, inv_hour = 1.0 / 3600.0;
     const double* rw = c.row;
@@ -2460,6 +2475,15 @@ __device__ __forceinline__ double reward_combine(const Ctx& c, double blower, do
     const double ncar = (den_c > 0.0) ? (elec_carb + gas_carb) / den_c : 0.0;
     const double pw = S->rw[5], ew = S->rw[6], cw = S->rw[7];
     const double raw = npr * pw - nec * ew - ncar * cw;
+    const double nz = (double)c.L->nz;
+    sp.v[0] = npr;
+    sp.v[1] = nec;
+    sp.v[2] = ncar;
+    sp.v[3] = p.dev_sum / nz;
+    sp.v[4] = p.dev_max;
+    sp.v[5] = p.oob / nz;
+    sp.v[6] = fabs(elec_rate) * dt / 3.6e6;
+    sp.v[7] = gg * dt / 3.6e6;
     return raw / (pw + ew + cw);
 }
 
@@ -2515,8 +2539,28 @@ __device__ __forceinline__ void stamps_flush(const KParams& P, const Ctx& c) {
 }
 
 
-static_assert(offsetof(Log, episode_return) == 8 && offsetof(Log, reward_mean) == 16 && sizeof(Log) == 24,
-              "the helper's 16-byte log read covers episode_return, episode_length, reward_mean and n");
+// A whole episode's sums added to the env's host-visible Log (the reference GPU
+// env's finalize_k, complete_port/gpu/smart_buildings.cu:2002-2036): each
+// field read and written with system-scope accesses (the trainer may clear the
+// Log between steps). ep: EP_* running sums, st: the episode's length.
+__device__ void log_episode(const KParams& P, int e, const float* ep, int st) {
+    Log* lg = reinterpret_cast<Log*>(reinterpret_cast<unsigned char*>(P.host_env) + (size_t)e * P.env_stride
+                                     + P.log_offset);
+    const float s = (float)st;
+    const float mean = ep[EP_RET] / s;
+    const float add[13] = {mean, mean, ep[EP_RET], s,
+                           ep[EP_PART + 3] / s, ep[EP_WORST], ep[EP_PART + 5] / s,
+                           ep[EP_PART + 0] / s, ep[EP_PART + 1] / s, ep[EP_PART + 2] / s,
+                           ep[EP_PART + 6], ep[EP_PART + 7], 1.0f};
+    float* f = reinterpret_cast<float*>(lg);
+#pragma unroll
+    for (int i = 0; i < 13; i++) {
+        const float x = __hip_atomic_load(&f[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(&f[i], x + add[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+}
+static_assert(sizeof(Log) == 52 && offsetof(Log, comfort_dev_K) == 16 && offsetof(Log, n) == 48,
+              "log_episode writes the reference GPU env's Log field order");
 
 // The env's second wavefront during a step. The occupancy interval is
 // exogenous (it reads only the chain states, the MT stream and the calendar),
@@ -2572,13 +2616,6 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
         env_post(sy + SY_CONV, 1);
     }
     STAMP(15);
-    // host-visible log fields (the trainer may clear them between steps):
-    // episode_return .. n in one 16-byte system-coherent load, one request
-    // over the host link per env (those requests queue there when thousands
-    // of envs step at once). The compiler does not count an inline load, so
-    // the explicit wait before the fields are used covers it.
-    typedef float f4v __attribute__((ext_vector_type(4)));
-    f4v lgv = {0.f, 0.f, 0.f, 0.f};
     {
         // the next step's calendar values (rows kk + 1 and j + 1) into the
         // other calendar section of the state image, loaded while this
@@ -2587,12 +2624,6 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
         // the tables is enough there
         const int n1 = c.S->n1;
         const RowVals next = row_issue<W>(c, min(kk + 1, n1 - 1), min(j + 1, n1 - 1));
-        if (P.host_env && !P.log_at_end && ln() == 0) {
-            const Log* hlog = reinterpret_cast<const Log*>(reinterpret_cast<const unsigned char*>(P.host_env)
-                                                           + (size_t)c.e * P.env_stride + P.log_offset);
-            const float* lp = &hlog->episode_return;
-            asm volatile("global_load_dwordx4 %0, %1, off sc0 sc1" : "=v"(lgv) : "v"(lp) : "memory");
-        }
         env_wait(sy + SY_PRE, 1);
         row_store<W>(c, next, cal_section(c, kk + 1));
     }
@@ -2606,13 +2637,7 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
     zone_means<W>(c, hzq);
     esync();
     const RewardPart part = reward_rest<W>(c, hzq, v_new);
-    asm volatile("s_waitcnt vmcnt(0)" : "+v"(lgv) : : "memory");   // the log fields' load
-    if (ln() == 0) {
-        *reinterpret_cast<RewardPart*>(sy + SY_PART) = part;
-        float* lg = reinterpret_cast<float*>(sy + SY_LOG);
-        lg[0] = lgv.x;   // episode_return
-        lg[1] = lgv.z;   // reward_mean
-    }
+    if (ln() == 0) *reinterpret_cast<RewardPart*>(sy + SY_PART) = part;
     // the observation row's stores are complete before the first wavefront
     // may overwrite the row with an auto-reset observation
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
@@ -2631,13 +2656,11 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
 // One workgroup per tile of E envs of one layout, two wavefronts per env:
 // wavefronts [0, E) step the envs, wavefronts [E, 2E) are their helpers (the
 // helper of env slot s is wavefront E + (s + E - E/2) % E, on another SIMD
-// than its env's first wavefront). LE: KParams::log_at_end as a compile-time
-// constant, so each log form compiles without the other's code.
-template <int W, int KV, bool LE>
+// than its env's first wavefront).
+template <int W, int KV>
 __global__ __launch_bounds__(512) void step_kernel(KParams P0) {
     static_assert(W == 64, "one wavefront per env");
-    KParams P = P0;
-    P.log_at_end = LE ? 1 : 0;
+    const KParams P = P0;
     extern __shared__ __align__(16) unsigned char lds[];
     const unsigned long long t_entry = P.phase_ts ? wall_clock64() : 0ull;
     const SBK_C Tile& tl = P.tiles[blockIdx.x];
@@ -2763,7 +2786,8 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P0) {
         env_wait(sy + SY_HALF, 1);   // the helper's reward half, observation and new occupancy
         STAMP(9);
         const RewardPart part = *reinterpret_cast<const RewardPart*>(sy + SY_PART);
-        const double rew = reward_combine(c, blower, cooling, part);
+        StepParts sp;
+        const double rew = reward_combine(c, blower, cooling, part, sp);
         const float r = (float)rew;
         const int step = c.ip[PI_STEP] + 1;
         // the first episode after puf_vec_create may be cut short (desync); a
@@ -2777,49 +2801,25 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P0) {
             P.terminals[e] = done ? 1.0f : 0.0f;
             c.ip[PI_STEP] = step;
             c.plant[PF_REW_SUM] += rew;
+            c.plant[PF_DEV_SUM] += sp.v[3];
             c.ip[PI_STEPS_TOTAL] += 1;
             if (done) {
                 c.ip[PI_EPISODES] += 1;
                 c.ip[PI_FIRST_DONE] = 1;
             }
-            // log_at_end: the episode's running return and mean in the record
-            // (the CPU env's per-step arithmetic), added to the host Log when
-            // the episode ends, so the step reads nothing over the host link
-            float er = 0.0f, em = 0.0f;
-            if (P.log_at_end) {
-                float* ep = reinterpret_cast<float*>(c.ip + PI_EP_RET);
-                er = ep[0] + r;
-                em = ep[1] + (r - ep[1]) / (float)step;
-                ep[0] = done ? 0.0f : er;
-                ep[1] = done ? 0.0f : em;
-            }
-            if (P.host_env && !cut && (!P.log_at_end || done)) {
-                Log* hlog = reinterpret_cast<Log*>(reinterpret_cast<unsigned char*>(P.host_env)
-                                                   + (size_t)e * P.env_stride + P.log_offset);
-                float ret, mean, m;
-                if (P.log_at_end) {
-                    ret = __hip_atomic_load(&hlog->episode_return, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) + er;
-                    mean = __hip_atomic_load(&hlog->reward_mean, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM) + em;
-                    m = er / (float)step;
-                } else {
-                    const float* lg = reinterpret_cast<const float*>(sy + SY_LOG);
-                    ret = lg[0] + r;
-                    mean = lg[1] + (r - lg[1]) / (float)step;
-                    m = ret / (float)step;
-                }
-                __hip_atomic_store(&hlog->episode_return, ret, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                __hip_atomic_store(&hlog->reward_mean, mean, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                if (done) {
-                    float* lf = reinterpret_cast<float*>(hlog);
-                    float perf = __hip_atomic_load(&lf[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                    float score = __hip_atomic_load(&lf[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                    float elen = __hip_atomic_load(&lf[3], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                    float nn = __hip_atomic_load(&lf[5], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                    __hip_atomic_store(&lf[0], perf + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                    __hip_atomic_store(&lf[1], score + m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                    __hip_atomic_store(&lf[3], elen + (float)step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                    __hip_atomic_store(&lf[5], nn + 1.0f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-                }
+            // the episode's running sums in float, as the reference GPU env
+            // keeps them (smart_buildings.cu:1965-1971); added to the host Log
+            // when a whole episode ends (:2002-2036), so a step reads nothing
+            // over the host link
+            float* ep = reinterpret_cast<float*>(c.ip + PI_EP);
+            ep[EP_RET] += r;
+#pragma unroll
+            for (int k = 0; k < 8; k++) ep[EP_PART + k] += (float)sp.v[k];
+            if ((float)sp.v[4] > ep[EP_WORST]) ep[EP_WORST] = (float)sp.v[4];
+            if (done) {
+                if (P.host_env && !cut) log_episode(P, e, ep, step);
+#pragma unroll
+                for (int k = 0; k < EP_COUNT; k++) ep[k] = 0.0f;
             }
         }
         esync();
@@ -2830,9 +2830,10 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P0) {
             c.ip[PI_STEP] = 0;
             c.ip[PI_STEPS_TOTAL] = 0;
             c.ip[PI_EPISODES] = 0;
-            c.ip[PI_EP_RET] = 0;
-            c.ip[PI_EP_MEAN] = 0;
+#pragma unroll
+            for (int k = 0; k < EP_COUNT; k++) c.ip[PI_EP + k] = 0;
             c.plant[PF_REW_SUM] = 0.0;
+            c.plant[PF_DEV_SUM] = 0.0;
         }
     }
     esync();
@@ -2874,43 +2875,54 @@ __global__ void gen_actions_kernel(float* actions, const int* n_cont, const int*
     }
 }
 
-// puf_live_log's totals over every env in one workgroup: out[0] the f64 sum
-// of rewards since puf_reset, out[1] env-steps since puf_reset, out[2]
-// episodes ended since puf_reset. Each thread sums envs t, t + 256, ... in
-// ascending order, then a fixed tree: the result does not depend on timing.
+// puf_live_log's totals: workgroup 0 over every env, out[0] the f64 sum of
+// rewards since puf_reset, out[1] env-steps since puf_reset, out[2] episodes
+// ended since puf_reset; workgroup 1 + g over scenario g's envs, out[3 + 3g]
+// its reward sum, out[4 + 3g] its sum of per-step mean zone deviations, out[5
+// + 3g] its env-steps. Each thread sums envs t, t + 256, ... in ascending
+// order, then a fixed tree: the result does not depend on timing. Field
+// scenarios' envs are added after, by their own kernel.
 __global__ __launch_bounds__(256) void live_sums_kernel(const EnvDesc* envs, const DevLayout* layouts,
                                                         const unsigned char* state, int n, double* out) {
     __shared__ double red[3][256];
     const int t = (int)threadIdx.x;
-    double rs = 0.0, st = 0.0, ep = 0.0;
+    const int g = (int)blockIdx.x - 1;   // -1: every env
+    double a0 = 0.0, a1 = 0.0, a2 = 0.0;
     for (int i = t; i < n; i += 256) {
         const EnvDesc& d = envs[i];
         const DevLayout* L = layouts + d.layout;
         if (L->st.bytes == 0) continue;   // a field scenario's env (its totals are added after)
+        if (g >= 0 && d.scen != g) continue;
         const unsigned char* r = state + d.state_off;
-        rs += reinterpret_cast<const double*>(r + L->st.plant)[PF_REW_SUM];
+        const double* pf = reinterpret_cast<const double*>(r + L->st.plant);
         const int* ip = reinterpret_cast<const int*>(r + L->st.iplant);
-        st += (double)ip[PI_STEPS_TOTAL];
-        ep += (double)ip[PI_EPISODES];
+        a0 += pf[PF_REW_SUM];
+        if (g < 0) {
+            a1 += (double)ip[PI_STEPS_TOTAL];
+            a2 += (double)ip[PI_EPISODES];
+        } else {
+            a1 += pf[PF_DEV_SUM];
+            a2 += (double)ip[PI_STEPS_TOTAL];
+        }
     }
-    red[0][t] = rs;
-    red[1][t] = st;
-    red[2][t] = ep;
+    red[0][t] = a0;
+    red[1][t] = a1;
+    red[2][t] = a2;
     __syncthreads();
     for (int w = 128; w > 0; w >>= 1) {
         if (t < w)
             for (int q = 0; q < 3; q++) red[q][t] += red[q][t + w];
         __syncthreads();
     }
-    if (t < 3) out[t] = red[t][0];
+    if (t < 3) out[(g < 0 ? 0 : 3 + 3 * g) + t] = red[t][0];
 }
 
 }  // namespace sbk
 
 // ---------------------------------------------------------------- launchers
 extern "C" int sbk_launch_live_sums(const sbk::EnvDesc* envs, const sbk::DevLayout* layouts,
-                                    const unsigned char* state, int n, double* out, hipStream_t s) {
-    hipLaunchKernelGGL(sbk::live_sums_kernel, dim3(1), dim3(256), 0, s, envs, layouts, state, n, out);
+                                    const unsigned char* state, int n, int n_scen, double* out, hipStream_t s) {
+    hipLaunchKernelGGL(sbk::live_sums_kernel, dim3(1 + n_scen), dim3(256), 0, s, envs, layouts, state, n, out);
     return (int)hipGetLastError();
 }
 
@@ -2920,20 +2932,10 @@ extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int threads,
     using namespace sbk;
     if (threads < 128 || threads > 512 || threads % 128) return (int)hipErrorInvalidValue;
     const dim3 g(n_blocks), b(threads);
-    const bool le = p->log_at_end != 0;
     switch (variant) {
-    case KV_LU:
-        if (le) hipLaunchKernelGGL((step_kernel<64, KV_LU, true>), g, b, lds_bytes, s, *p);
-        else hipLaunchKernelGGL((step_kernel<64, KV_LU, false>), g, b, lds_bytes, s, *p);
-        break;
-    case KV_POINT:
-        if (le) hipLaunchKernelGGL((step_kernel<64, KV_POINT, true>), g, b, lds_bytes, s, *p);
-        else hipLaunchKernelGGL((step_kernel<64, KV_POINT, false>), g, b, lds_bytes, s, *p);
-        break;
-    case KV_BLOCK:
-        if (le) hipLaunchKernelGGL((step_kernel<64, KV_BLOCK, true>), g, b, lds_bytes, s, *p);
-        else hipLaunchKernelGGL((step_kernel<64, KV_BLOCK, false>), g, b, lds_bytes, s, *p);
-        break;
+    case KV_LU: hipLaunchKernelGGL((step_kernel<64, KV_LU>), g, b, lds_bytes, s, *p); break;
+    case KV_POINT: hipLaunchKernelGGL((step_kernel<64, KV_POINT>), g, b, lds_bytes, s, *p); break;
+    case KV_BLOCK: hipLaunchKernelGGL((step_kernel<64, KV_BLOCK>), g, b, lds_bytes, s, *p); break;
     default: return (int)hipErrorInvalidValue;
     }
     return (int)hipGetLastError();
@@ -2942,10 +2944,8 @@ extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int threads,
 extern "C" int sbk_set_lds_limit(int width, int bytes) {
     using namespace sbk;
     if (width != 64) return (int)hipErrorInvalidValue;
-    const void* fns[2 * KV_COUNT] = {
-        (const void*)step_kernel<64, KV_LU, false>, (const void*)step_kernel<64, KV_POINT, false>,
-        (const void*)step_kernel<64, KV_BLOCK, false>, (const void*)step_kernel<64, KV_LU, true>,
-        (const void*)step_kernel<64, KV_POINT, true>, (const void*)step_kernel<64, KV_BLOCK, true>};
+    const void* fns[KV_COUNT] = {(const void*)step_kernel<64, KV_LU>, (const void*)step_kernel<64, KV_POINT>,
+                                 (const void*)step_kernel<64, KV_BLOCK>};
     for (const void* f : fns) {
         const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
         if (e != hipSuccess) return (int)e;

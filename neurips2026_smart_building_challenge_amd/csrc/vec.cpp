@@ -51,7 +51,7 @@ extern "C" int sbk_launch_policy_noalloc(const float* obs, const float* w1, cons
                                          float floor, hipStream_t s);
 extern "C" int sbk_launch_canon(const sbk::CanonArgs* a, int post, hipStream_t s);
 extern "C" int sbk_launch_live_sums(const sbk::EnvDesc* envs, const sbk::DevLayout* layouts,
-                                    const unsigned char* state, int n, double* out, hipStream_t s);
+                                    const unsigned char* state, int n, int n_scen, double* out, hipStream_t s);
 extern "C" int sbk_launch_gen_actions(float* actions, const int* n_cont, const int* n_disc, int n_envs,
                                       uint64_t seed, uint32_t step, hipStream_t s);
 
@@ -486,7 +486,7 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     S.damper = f64a(nv); S.reheat = f64a(nv); S.ratio = f64a(nv); S.heatsp = f64a(nv);
     S.coolsp = f64a(nv); S.dcmd = f64a(nv); S.rcmd = f64a(nv); S.sensing = f64a(nv);
     S.recirc = f64a(na); S.sat = f64a(na); S.fan = f64a(na); S.flow = f64a(na);
-    S.plant = f64a(8);
+    S.plant = f64a(sbk::PF_COUNT);
     S.cal_n = sbk::RW_COUNT + std::max(n_aux - 1, 0);
     S.cal = f64a(2 * S.cal_n);
     S.run = o; o += 4 * na; S.coolreq = o; o += 4 * na; S.iplant = o; o += 4 * sbk::PI_COUNT;
@@ -1052,7 +1052,6 @@ struct Vec {
     std::vector<TileGroup> groups;            // consecutive tiles of one kernel variant
     sbk::Tile* d_tiles = nullptr;
     float reward_scale = 1.0f;
-    int log_at_end = 0;                       // env key log_at_end: the host Log at episode ends only
     Env* envs = nullptr;
     std::vector<std::string> paths;           // ordered scenario list
     std::vector<HostLayout> layouts;
@@ -1083,8 +1082,10 @@ struct Vec {
     SbxPolicy pol{};
     float *p_h1 = nullptr, *p_h2 = nullptr, *p_y = nullptr;
     float *p_hlp = nullptr, *p_hent = nullptr;   // per-head log-densities and entropies [n][SB_ACT]
-    double* d_live = nullptr;                    // puf_live_log totals (device, 3 f64)
+    double* d_live = nullptr;                    // puf_live_log totals (device: 3 f64, then 3 per scenario)
     double* h_live = nullptr;                    // and their pinned host copy
+    std::vector<double> live_prev;               // per scenario: the totals at the previous puf_live_log
+    std::vector<std::string> live_keys;          // per scenario: its two live keys (Dict keeps the pointers)
     // canonical policy interface (kwargs canonical / residual / res_* / guard_*)
     int canonical = 0, resid = 0, guard = 0, guard_hot = 0;
     float res_scale = 0.5f, res_dscale = 1.5f, guard_d0 = 1.0f, guard_d1 = 0.0f;
@@ -1123,7 +1124,6 @@ sbk::KParams params(Vec* v, int mode) {
     p.n_envs = v->n;
     p.mode = mode;
     p.reward_scale = v->reward_scale;
-    p.log_at_end = v->log_at_end;
     return p;
 }
 
@@ -1309,13 +1309,10 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
         const float rs = kw(kwargs, "reward_scale", 1.0f);
         v->reward_scale = rs > 0.0f ? rs : 1.0f;
     }
-    // log_at_end = 1: each env's running episode return and mean reward stay
-    // in its device record and are added to its host Log when the episode
-    // ends (as the reference GPU env fills Log at episode ends,
-    // complete_port/gpu/smart_buildings.cu:123-125), so puf_step reads no host
-    // memory; 0 (default): the CPU env's per-step Log, read and written every
-    // step (pufferlib_cpu_env.h:247-248), which sees a trainer's mid-episode clears
-    v->log_at_end = (int)kw(kwargs, "log_at_end", 0.0f) != 0;
+    // the Log is filled at episode ends (the reference GPU env's form); the
+    // key of earlier versions that chose it is accepted at 1 only
+    if (kw(kwargs, "log_at_end", 1.0f) != 1.0f)
+        die("env.log_at_end: the per-step Log is not supported (the Log fills at episode ends)");
     check_env_keys(kwargs);
     // ---- scenario list
     std::vector<std::string> files;
@@ -1387,7 +1384,6 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
             S.path = files[i];
             S.layout = li;
             S.field = (int)v->fields.size();
-            if (v->log_at_end) die("env.log_at_end applies to RC layouts only (a field scenario logs every step)");
             S.n1 = fc.n1;
             S.episode_steps = fc.episode_steps;
             S.occ_seed = fc.occ_seed;
@@ -1638,8 +1634,18 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
         hip_ok(hipMemset(v->d_cpid, 0, sizeof(double) * ns), "clear");
         hip_ok(hipMemset(v->d_cinfo, 0, sizeof(float) * ns), "clear");
     }
-    hip_ok(hipMalloc(&v->d_live, 3 * sizeof(double)), "hipMalloc(live log)");
-    hip_ok(hipHostMalloc(&v->h_live, 3 * sizeof(double), hipHostMallocDefault), "hipHostMalloc(live log)");
+    {
+        const size_t nl = 3 + 3 * v->scens.size();
+        hip_ok(hipMalloc(&v->d_live, nl * sizeof(double)), "hipMalloc(live log)");
+        hip_ok(hipHostMalloc(&v->h_live, nl * sizeof(double), hipHostMallocDefault), "hipHostMalloc(live log)");
+        v->live_prev.assign(3 * v->scens.size(), 0.0);
+        for (const HostScen& S : v->scens) {
+            std::string name = S.path.substr(S.path.find_last_of('/') + 1);
+            if (ends_with(name, ".sbb")) name.resize(name.size() - 4);
+            v->live_keys.push_back("scenario/" + name + "/reward");
+            v->live_keys.push_back("scenario/" + name + "/comfort_dev_K");
+        }
+    }
     // ---- Env array (host memory the device can write: logs)
     void* envmem = nullptr;
     hip_ok(hipHostMalloc(&envmem, sizeof(Env) * (size_t)n, hipHostMallocCoherent), "hipHostMalloc(envs)");
@@ -1713,6 +1719,7 @@ void puf_reset(Env* envs) {
     }
     launch(v, sbk::KMODE_RESET);
     hip_ok(hipStreamSynchronize(g_stream), "reset");
+    std::fill(v->live_prev.begin(), v->live_prev.end(), 0.0);   // the per-env sums restart at 0
 }
 
 // One step reading its action rows from `actions` (the bound buffer when null).
@@ -1767,25 +1774,50 @@ void puf_log(Log* log, Dict* out) {
     dict_set(out, "score", log->score);
     dict_set(out, "episode_return", log->episode_return);
     dict_set(out, "episode_length", log->episode_length);
-    dict_set(out, "reward_mean", log->reward_mean);
+    dict_set(out, "comfort_dev_K", log->comfort_dev_K);
+    dict_set(out, "worst_dev_K", log->worst_dev_K);
+    dict_set(out, "out_of_band_frac", log->out_of_band_frac);
+    dict_set(out, "productivity", log->productivity);
+    dict_set(out, "energy_cost_norm", log->energy_cost_norm);
+    dict_set(out, "carbon_norm", log->carbon_norm);
+    dict_set(out, "elec_kwh", log->elec_kwh);
+    dict_set(out, "gas_kwh", log->gas_kwh);
     dict_set(out, "n", log->n);
 }
 
-// Totals over every env since puf_reset (complete_port/gpu/smart_buildings.cu:
-// 3069-3100 reports the same kind of live counters): one device reduction and
-// one 24-byte copy on the bound stream, then a synchronisation.
+// Totals over every env since puf_reset (env_steps, episodes, reward_mean)
+// and, for a vec of several scenarios, each scenario's mean reward and mean
+// zone deviation per env-step since the previous call (the reference's
+// scenario/<name>/* keys, complete_port/gpu/smart_buildings.cu:3069-3100):
+// one device reduction and one copy on the bound stream, then a sync.
 void puf_live_log(Env* envs, Dict* out) {
     Vec* v = vec_of(envs);
-    int rc = sbk_launch_live_sums(v->d_envs, v->d_layouts, v->d_state, v->n, v->d_live, g_stream);
+    const int ns = (int)v->scens.size();
+    int rc = sbk_launch_live_sums(v->d_envs, v->d_layouts, v->d_state, v->n, ns, v->d_live, g_stream);
     if (rc != 0) die("live log kernel launch failed");
-    for (FieldScen* f : v->fields)
-        if (!field_live(f, v->d_live, g_stream)) die("live log kernel launch failed (field scenario)");
-    hip_ok(hipMemcpyAsync(v->h_live, v->d_live, 3 * sizeof(double), hipMemcpyDeviceToHost, g_stream), "live log");
+    for (size_t fi = 0; fi < v->fields.size(); fi++) {
+        int scen = -1;
+        for (int g = 0; g < ns; g++)
+            if (v->scens[g].field == (int)fi) scen = g;
+        if (!field_live(v->fields[fi], v->d_live, scen, g_stream)) die("live log kernel launch failed (field scenario)");
+    }
+    const size_t nl = 3 + 3 * (size_t)ns;
+    hip_ok(hipMemcpyAsync(v->h_live, v->d_live, nl * sizeof(double), hipMemcpyDeviceToHost, g_stream), "live log");
     hip_ok(hipStreamSynchronize(g_stream), "live log");
     const double rs = v->h_live[0], st = v->h_live[1], eps = v->h_live[2];
     dict_set(out, "env_steps", (float)st);
     dict_set(out, "episodes", (float)eps);
     dict_set(out, "reward_mean", st > 0.0 ? (float)(rs / st) : 0.0f);
+    for (int g = 0; g < ns; g++) {
+        const double* cur = v->h_live + 3 + 3 * g;
+        double* prev = v->live_prev.data() + 3 * g;
+        const double dn = cur[2] - prev[2];
+        if (ns > 1 && dn > 0.0) {
+            dict_set(out, v->live_keys[2 * g].c_str(), (float)((cur[0] - prev[0]) / dn));
+            dict_set(out, v->live_keys[2 * g + 1].c_str(), (float)((cur[1] - prev[1]) / dn));
+        }
+        for (int q = 0; q < 3; q++) prev[q] = cur[q];
+    }
 }
 
 // The action mask of every agent (complete_port/gpu/smart_buildings.cu:3230-

@@ -22,10 +22,13 @@ SB_ACT = SB_CONT + SB_DISC
 P = ctypes.c_void_p
 
 
+LOG_FIELDS = ("perf", "score", "episode_return", "episode_length", "comfort_dev_K", "worst_dev_K",
+              "out_of_band_frac", "productivity", "energy_cost_norm", "carbon_norm", "elec_kwh", "gas_kwh", "n")
+
+
 class Log(ctypes.Structure):
-    _fields_ = [("perf", ctypes.c_float), ("score", ctypes.c_float),
-                ("episode_return", ctypes.c_float), ("episode_length", ctypes.c_float),
-                ("reward_mean", ctypes.c_float), ("n", ctypes.c_float)]
+    """The reference GPU env's episode log (include/sbenv.h), n last."""
+    _fields_ = [(k, ctypes.c_float) for k in LOG_FIELDS]
 
 
 class Agent(ctypes.Structure):
@@ -416,9 +419,12 @@ class VecEnv:
         return buf.reshape(self.n, POLICY_HEADS)
 
     def live_log(self) -> dict[str, float]:
-        """puf_live_log: env-steps, episodes and mean reward since puf_reset over every env."""
-        items = (DictItem * 8)()
-        d = Dict(ctypes.cast(items, ctypes.POINTER(DictItem)), 0, 8)
+        """puf_live_log: env-steps, episodes and mean reward over every env since
+        the previous call, and per scenario (vecs of several) its mean reward and
+        comfort deviation per env-step."""
+        cap = 8 + 2 * 4096
+        items = (DictItem * cap)()
+        d = Dict(ctypes.cast(items, ctypes.POINTER(DictItem)), 0, cap)
         self.L.puf_live_log(self.envs, ctypes.byref(d))
         return read_dict(d)
 
@@ -431,8 +437,8 @@ class VecEnv:
                 "sweeps": int(out[2]), "capped": int(out[3])}
 
     def log(self, i: int) -> dict[str, float]:
-        items = (DictItem * 8)()
-        d = Dict(ctypes.cast(items, ctypes.POINTER(DictItem)), 0, 8)
+        items = (DictItem * 16)()
+        d = Dict(ctypes.cast(items, ctypes.POINTER(DictItem)), 0, 16)
         self.L.puf_log(ctypes.byref(self.envs[i].log), ctypes.byref(d))
         return read_dict(d)
 

@@ -62,6 +62,7 @@ class _Lib:
             for f in (L.sbo_env_obs_len, L.sbo_env_n_cont, L.sbo_env_n_disc):
                 f.argtypes = [P]
             L.sbo_env_log.argtypes = [P, P]
+            L.sbo_env_parts.argtypes = [P, P]
             L.sbo_env_set_first_steps.argtypes = [P, ctypes.c_int]
             L.sbo_mt_seed.argtypes = [P, ctypes.c_uint32]
             L.sbo_mt_u32.argtypes = [P]
@@ -229,6 +230,78 @@ class CpuEnv:
     def state(self) -> np.ndarray:
         n = self.L.state_fn(self.h, _ptr(self._st))
         return self._st[:n].copy()
+
+    def parts(self) -> np.ndarray:
+        """The last step's reward parts: sb_reward's 12 (npr, nec, ncar, electricity
+        and gas cost, blower, cooling, pump power, price, dt, hour, workday); the
+        oracle adds the reference GPU env's comfort diagnostics (mean and worst
+        zone deviation, out-of-band fraction) and the gas rate."""
+        if self.kind == "ref":
+            out = np.zeros(12, np.float64)
+            self.L.lib.ref_parts(self.h, _ptr(out))
+        else:
+            out = np.zeros(16, np.float64)
+            self.L.lib.sbo_env_parts(self.h, _ptr(out))
+        return out
+
+
+LOG_KEYS = ["perf", "score", "episode_return", "episode_length", "comfort_dev_K", "worst_dev_K", "out_of_band_frac",
+            "productivity", "energy_cost_norm", "carbon_norm", "elec_kwh", "gas_kwh", "n"]
+
+
+class GpuEnvLog:
+    """The reference GPU env's episode log (complete_port/gpu/smart_buildings.cu:
+    101-115, filled by finalize_k :1936-2047), replayed in float32 from an env's
+    per-step float32 reward and the oracle's reward parts: running sums of the
+    reward and of 8 diagnostics (productivity term, normalized cost, normalized
+    carbon, mean zone deviation, the worst deviation as a maximum,
+    out-of-band fraction, electricity and gas kWh), added to the Log when a full
+    episode ends (a desync-cut first episode is dropped), then cleared."""
+
+    def __init__(self):
+        self.log = {k: np.float32(0.0) for k in LOG_KEYS}
+        self.ret = np.float32(0.0)
+        self.part = np.zeros(8, np.float32)
+        self.worst = np.float32(0.0)
+
+    @staticmethod
+    def step_parts(pt: np.ndarray) -> np.ndarray:
+        """The GPU env's 8 per-step diagnostics (sb_gpu_kernels.cuh:1466-1473) from the
+        oracle's 16 parts."""
+        dt = pt[9]
+        elec = pt[5] + abs(pt[6]) + pt[7]
+        return np.array([pt[0], pt[1], pt[2], pt[12], pt[13], pt[14], abs(elec) * dt / 3.6e6, pt[15] * dt / 3.6e6])
+
+    def step(self, r: float, pt: np.ndarray, step: int, done: bool, cut: bool):
+        f = np.float32
+        rp = self.step_parts(pt)
+        self.ret = f(self.ret + f(r))
+        for k in range(8):
+            self.part[k] = f(self.part[k] + f(rp[k]))
+        if f(rp[4]) > self.worst:
+            self.worst = f(rp[4])
+        if not done:
+            return
+        if not cut:
+            st = f(step)
+            L = self.log
+            mean = f(self.ret / st)
+            L["perf"] = f(L["perf"] + mean)
+            L["score"] = f(L["score"] + mean)
+            L["episode_return"] = f(L["episode_return"] + self.ret)
+            L["episode_length"] = f(L["episode_length"] + st)
+            L["productivity"] = f(L["productivity"] + f(self.part[0] / st))
+            L["energy_cost_norm"] = f(L["energy_cost_norm"] + f(self.part[1] / st))
+            L["carbon_norm"] = f(L["carbon_norm"] + f(self.part[2] / st))
+            L["comfort_dev_K"] = f(L["comfort_dev_K"] + f(self.part[3] / st))
+            L["worst_dev_K"] = f(L["worst_dev_K"] + self.worst)
+            L["out_of_band_frac"] = f(L["out_of_band_frac"] + f(self.part[5] / st))
+            L["elec_kwh"] = f(L["elec_kwh"] + self.part[6])
+            L["gas_kwh"] = f(L["gas_kwh"] + self.part[7])
+            L["n"] = f(L["n"] + 1)
+        self.ret = np.float32(0.0)
+        self.part[:] = 0.0
+        self.worst = np.float32(0.0)
 
 
 CN_OBS, CN_ACT = 983, 219

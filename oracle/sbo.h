@@ -139,7 +139,8 @@ typedef struct {
     int first_steps, first_done;   /* first episode's length (desync truncation), 1 once it ended */
     float log[6];
     double native[SBO_CONT + SBO_DISC];
-    double parts[12];
+    double parts[16];   /* sb_reward's 12 (sb_reward.c:148-151), then the GPU env's comfort
+                           diagnostics (mean, worst, out-of-band fraction) and the gas rate */
     double last_rew;
     float obs[SBO_OBS];
 } SboEnv;
@@ -155,6 +156,7 @@ int sbo_env_obs_len(const SboEnv* e);
 int sbo_env_n_cont(const SboEnv* e);
 int sbo_env_n_disc(const SboEnv* e);
 void sbo_env_log(const SboEnv* e, float* out);
+void sbo_env_parts(const SboEnv* e, double* out);
 
 /* core pieces (exposed for unit tests) */
 void sbo_mt_seed(SboMt* r, uint32_t seed);

@@ -883,6 +883,8 @@ static double reward(SboEnv* e, int kv) {
     double pump_e = tf * RHO_W * GRAV * e->pump_head / s->pump_eff;
     double max_pph = s->rw[0], min_pph = s->rw[1], ref = s->rw[2];
     double total_occ = 0.0, cum = 0.0;
+    double dsum = 0.0, dmax = 0.0;   /* comfort diagnostics of the reference GPU env */
+    int n_oob = 0;                   /* (complete_port/gpu/sb_gpu_kernels.cuh:1409-1473) */
     for (int z = 0; z < nz; z++) {
         double occ = e->occV[z];
         total_occ += occ;
@@ -891,6 +893,9 @@ static double reward(SboEnv* e, int kv) {
         double dev = zt - csp;
         if (hsp - zt > dev) dev = hsp - zt;
         if (dev < 0.0) dev = 0.0;
+        dsum += dev;
+        if (dev > dmax) dmax = dev;
+        if (dev > 0.0) n_oob++;
         double sh = (dev <= ref) ? dev / ref : 1.0 + ((dev - ref) / ref) * ((dev - ref) / ref);
         cum += max_pph * (1.0 - sh) * occ * dt * inv_hour;
     }
@@ -920,6 +925,11 @@ static double reward(SboEnv* e, int kv) {
     pt[0] = npr; pt[1] = nec; pt[2] = ncar; pt[3] = elec_cost; pt[4] = gas_cost;
     pt[5] = blower; pt[6] = cooling; pt[7] = pump_e; pt[8] = price; pt[9] = dt;
     pt[10] = (double)hour; pt[11] = (double)wd;
+    /* the reference GPU env's per-step diagnostics (sb_gpu_kernels.cuh:1469-1473):
+     * mean and worst zone deviation from the band, fraction of zones outside
+     * it, and the gas rate behind pt[4] */
+    pt[12] = nz > 0 ? dsum / nz : 0.0; pt[13] = dmax; pt[14] = nz > 0 ? (double)n_oob / nz : 0.0;
+    pt[15] = g;
     double pw = s->rw[5], ew = s->rw[6], cw = s->rw[7];
     double raw = npr * pw - nec * ew - ncar * cw;
     return raw / (pw + ew + cw);
@@ -1065,3 +1075,4 @@ int sbo_env_obs_len(const SboEnv* e) { return e->sc->n_dev + e->sc->n_aux; }
 int sbo_env_n_cont(const SboEnv* e) { return e->sc->n_cont; }
 int sbo_env_n_disc(const SboEnv* e) { return e->sc->n_disc; }
 void sbo_env_log(const SboEnv* e, float* out) { memcpy(out, e->log, sizeof(e->log)); }
+void sbo_env_parts(const SboEnv* e, double* out) { memcpy(out, e->parts, sizeof(e->parts)); }

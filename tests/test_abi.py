@@ -40,7 +40,14 @@ def test_dict_helpers():
 
 
 def test_struct_layout_matches_header():
-    assert ctypes.sizeof(E.Log) == 24
+    """The Log is the reference GPU env's (smart_buildings.cu:101-115): 13
+    floats in its order, n last; puf_log names every field."""
+    assert ctypes.sizeof(E.Log) == 52 and E.Log.n.offset == 48 and E.Log.comfort_dev_K.offset == 16
+    log = E.Log(*[float(i + 1) for i in range(13)])
+    items = (E.DictItem * 16)()
+    d = E.Dict(ctypes.cast(items, ctypes.POINTER(E.DictItem)), 0, 16)
+    E.lib().puf_log(ctypes.byref(log), ctypes.byref(d))
+    assert E.read_dict(d) == {k: float(i + 1) for i, k in enumerate(E.LOG_FIELDS)}
     assert E.Env.log.offset == 0
     assert E.lib().sbx_version().startswith(b"sbenv")
 
@@ -56,6 +63,10 @@ def test_unsupported_env_key_aborts():
             "E.lib().puf_vec_create(1, kw.ptr(), ctypes.c_void_p(64), ctypes.c_void_p(64), "
             "ctypes.c_void_p(64), ctypes.c_void_p(64)); print('created')")
     root = str(Path(__file__).resolve().parents[1])
+    # the per-step Log of earlier versions is gone: log_at_end is accepted at 1 only
+    r = subprocess.run([sys.executable, "-c", code.format(key="log_at_end", val=0)], cwd=root, capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode != 0 and "per-step Log is not supported" in r.stderr, r.stderr
     for key in ("rew_norm", "plant_pair", "random_start", "zone_memory", "comfort_shape"):
         r = subprocess.run([sys.executable, "-c", code.format(key=key, val=1)], cwd=root, capture_output=True,
                            text=True, timeout=120)

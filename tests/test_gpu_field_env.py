@@ -8,7 +8,8 @@ and the reference core's fixture (tests/golden/field_env.json):
     terminals and the full state (field, interior mass, HVAC state, air side,
     occupancy, plant) bit-identical to the oracle after every step, through an
     auto-reset, for three envs of one scenario (their occupancy streams differ);
-    the episode Log and puf_live_log totals equal the oracle's;
+    the episode Log (the reference GPU env's 13 fields, replayed from the
+    oracle's rewards and diagnostics) bit-equal, the puf_live_log totals equal;
   - the reference core's fixture (obs / state SHA-256, reward bits) on the
     7-room plan and on a plan at building_train_1's size (205,434 cells);
   - default field mode: state within the per-step bar (1e-9 relative),
@@ -106,8 +107,17 @@ class Twin:
         self.mean[:n_dev] = d["f_norm_mean"]
         self.sd[:n_dev] = np.sqrt(np.maximum(d["f_norm_var"], 0.0))
 
+        # the reference GPU env's episode log, replayed from the oracle's steps
+        self.glog = po.GpuEnvLog()
+        self.steps = 0
+
     def step(self, s):
-        return self.cpu.step(po.action_row(SEED, self.i, s, self.cpu.n_cont, self.cpu.n_disc))
+        out = self.cpu.step(po.action_row(SEED, self.i, s, self.cpu.n_cont, self.cpu.n_disc))
+        self.steps += 1
+        self.glog.step(out[1], self.cpu.parts(), self.steps, bool(out[2]), False)
+        if out[2]:
+            self.steps = 0
+        return out
 
 
 def obs_close(g: np.ndarray, tw: Twin, c: np.ndarray, where: str):
@@ -164,10 +174,11 @@ def test_gpu_field_env_exact_matches_oracle(small_blob, small_conv_blob, conv):
     done = run_against_oracle(vec, twins, 60, True, "exact")
     assert done == 3, "every env ended its first episode at step 40"
     for tw in twins:
-        got, want = vec.log(tw.i), tw.cpu.log()
-        names = ["perf", "score", "episode_return", "episode_length", "reward_mean", "n"]
-        for k, name in enumerate(names):
-            assert np.float32(got[name]) == np.float32(want[k]), (tw.i, name, got, want)
+        # exact mode: the env's diagnostics are the oracle's to the bit, so is the Log
+        got = vec.log(tw.i)
+        want = {k: float(v) for k, v in tw.glog.log.items()}
+        assert got == want, (tw.i, got, want)
+        assert got["n"] == 1.0 and got["episode_length"] == 40.0
     live = vec.live_log()
     assert live["env_steps"] == 180.0 and live["episodes"] == 3.0
     vec.close()

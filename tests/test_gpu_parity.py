@@ -99,12 +99,36 @@ class Twin:
         exact += [o, o + 2, o + 3, o + 4]                    # boiler current, setpoint, pump head, index
         self.exact_state = np.array(exact)
         self.state_len = o + 5
+        # the reference GPU env's episode log, replayed from the oracle's steps
+        self.glog = po.GpuEnvLog()
+        self.max_steps = max_steps
+        self.first_steps = max_steps if first_steps is None else first_steps
+        self.steps = 0
+        self.first = True
 
-    def step(self, seed, s):
-        row = po.action_row(seed, self.i, s, self.cpu.n_cont, self.cpu.n_disc)
+    def step(self, seed, s, row=None):
+        if row is None:
+            row = po.action_row(seed, self.i, s, self.cpu.n_cont, self.cpu.n_disc)
         ob, r, t, _ = self.cpu.step(row)
         self.rew_sum += self.cpu.last_reward_f64()
+        self.steps += 1
+        done = bool(t)
+        cut = self.first and self.first_steps < self.max_steps
+        self.glog.step(r, self.cpu.parts(), self.steps, done, cut)
+        if done:
+            self.steps = 0
+            self.first = False
         return ob, r, t
+
+
+def log_close(got: dict, tw: Twin, where: str, rtol: float = 1e-5) -> None:
+    """Every field of the GPU env's Log against the reference GPU env's episode
+    accumulation replayed from the oracle twin's float rewards and diagnostics."""
+    want = tw.glog.log
+    assert set(got) == set(po.LOG_KEYS), (where, sorted(got))
+    for k in po.LOG_KEYS:
+        w = float(want[k])
+        assert abs(got[k] - w) <= rtol * max(1.0, abs(w)), (where, k, got[k], w)
 
 
 def obs_close(gpu_row: np.ndarray, twin: Twin, cpu_row: np.ndarray, where: str) -> None:
@@ -224,9 +248,6 @@ def test_gpu_step_parity_start_offsets(mixed_dir, solver):
     vec.close()
 
 
-LOG_NAMES = ["perf", "score", "episode_return", "episode_length", "reward_mean", "n"]
-
-
 def test_gpu_desync_truncation_parity(mixed_dir):
     """desync = 1 (the reference GPU env's meaning, smart_buildings.cu:2808-2815):
     env i's first episode ends after 1 + hash(i) mod 40 steps, later ones after 40;
@@ -239,9 +260,8 @@ def test_gpu_desync_truncation_parity(mixed_dir):
     twins = [Twin(vec, i, 40, first_steps=firsts[i]) for i in range(0, vec.n, 2)]
     _run_parity(vec, twins, 100, "desync")
     for tw in twins:
-        got, want = vec.log(tw.i), tw.cpu.log()
-        for k, name in enumerate(LOG_NAMES):
-            assert abs(got[name] - float(want[k])) <= 1e-5 * max(1.0, abs(float(want[k]))), (tw.i, name, got, want)
+        got = vec.log(tw.i)
+        log_close(got, tw, f"desync env {tw.i}")
         # full episodes only: the cut first episode (if shorter than 40) is not counted
         full = (100 - firsts[tw.i]) // 40 + (firsts[tw.i] == 40)
         assert got["n"] == full, (tw.i, firsts[tw.i], got)
@@ -439,11 +459,10 @@ def test_gpu_log_matches_oracle(cfg0_dir):
         tw.step(SEED, s)
     torch.cuda.synchronize()
     got = vec.log(0)
-    want = tw.cpu.log()
-    names = ["perf", "score", "episode_return", "episode_length", "reward_mean", "n"]
-    for k, name in enumerate(names):
-        assert abs(got[name] - float(want[k])) <= 1e-5 * max(1.0, abs(float(want[k]))), (name, got, want)
+    log_close(got, tw, "one env")
     assert got["n"] == 2.0 and got["episode_length"] == 50.0
+    assert got["comfort_dev_K"] > 0.0 and got["worst_dev_K"] >= got["comfort_dev_K"] / 2.0
+    assert got["elec_kwh"] > 0.0 and got["gas_kwh"] >= 0.0 and 0.0 <= got["out_of_band_frac"] <= 2.0
     vec.close()
 
 
@@ -607,22 +626,43 @@ def test_gpu_reward_scale(cfg0_dir):
 
 
 def test_gpu_live_log_totals(mixed_dir):
-    """puf_live_log's device reduction equals the per-env counters read one by one."""
-    say("live log: 90 envs, 70 steps")
+    """puf_live_log: the totals since puf_reset equal the per-env counters read
+    one by one; the per-scenario keys (scenario/<blob>/reward and
+    comfort_dev_K, the reference's live metrics) equal the oracle twins' mean
+    reward and mean zone deviation per env-step over the window since the
+    previous call (two windows)."""
+    say("live log: 90 envs, 70 + 10 steps")
     vec = E.VecEnv(90, blob_dir=str(mixed_dir), groups=30, max_steps=25, desync=1)
+    firsts = [po.desync_first_steps(i, 25) for i in range(vec.n)]
+    twins = [Twin(vec, i, 25, first_steps=firsts[i]) for i in range(vec.n)]
     vec.reset()
-    for s in range(70):
-        vec.gen_actions(SEED, s)
-        vec.step()
-    got = vec.live_log()
+    for tw in twins:
+        tw.cpu.reset()
+    for window, steps in enumerate((70, 10)):
+        acc = {}
+        for s in range(steps):
+            s0 = 70 * window + s
+            vec.gen_actions(SEED, s0)
+            vec.step()
+            for tw in twins:
+                tw.step(SEED, s0)
+                name = tw.path.rsplit("/", 1)[-1][:-4]
+                a = acc.setdefault(name, [0.0, 0.0, 0])
+                a[0] += tw.cpu.last_reward_f64()
+                a[1] += tw.cpu.parts()[12]
+                a[2] += 1
+        got = vec.live_log()
+        for name, (r, dv, n) in acc.items():
+            assert abs(got[f"scenario/{name}/reward"] - r / n) <= 1e-5 * max(1.0, abs(r / n)), (window, name)
+            assert abs(got[f"scenario/{name}/comfort_dev_K"] - dv / n) <= 1e-5 * max(1.0, dv / n), (window, name)
+        assert len([k for k in got if k.startswith("scenario/")]) == 2 * 30
     rs = st = 0.0
     for i in range(vec.n):
         g = vec.state(i)
         rs += g[-2]
         st += g[-1]
-    assert got["env_steps"] == 90 * 70 == st
-    firsts = [po.desync_first_steps(i, 25) for i in range(vec.n)]
-    eps = sum(1 + (70 - f) // 25 for f in firsts)
+    assert got["env_steps"] == 90 * 80 == st
+    eps = sum(1 + (80 - f) // 25 for f in firsts)
     assert got["episodes"] == eps
     assert abs(got["reward_mean"] - rs / st) <= 1e-6 * abs(rs / st)
     vec.close()
@@ -666,51 +706,27 @@ def test_gpu_decode_edge_values(cfg0_dir):
     vec.close()
 
 
-def test_gpu_log_at_end(mixed_dir):
-    """log_at_end = 1: each env's running episode return and mean reward stay in
-    its record and reach the host Log only when an episode ends (desync-cut
-    first episodes excluded). The Log after 100 steps against the same float32
-    arithmetic replayed on the host from the rewards and terminals the vec
-    returned; the episode count and lengths exactly."""
+def test_gpu_log_at_episode_ends_every_env(mixed_dir):
+    """The Log of all 60 envs of a desynchronised batch (first episodes cut at
+    hashed steps, later ones after 40) after 100 steps: every field against the
+    reference GPU env's accumulation replayed from each env's oracle twin
+    (desync-cut episodes stay out), the episode counts exactly."""
     say("log at episode ends: 60 envs, 100 steps")
-    vec = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=40, desync=1, log_at_end=1)
+    vec = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=40, desync=1)
     firsts = [po.desync_first_steps(i, 40) for i in range(vec.n)]
+    twins = [Twin(vec, i, 40, first_steps=firsts[i]) for i in range(vec.n)]
     vec.reset()
-    f32 = np.float32
-    run = np.zeros((vec.n, 2), np.float32)   # running return, mean
-    steps = np.zeros(vec.n, np.int64)
-    first = np.ones(vec.n, bool)
-    want = {k: np.zeros(vec.n, np.float32) for k in ("perf", "score", "episode_return", "episode_length",
-                                                        "reward_mean", "n")}
+    for tw in twins:
+        tw.cpu.reset()
     for s in range(100):
         vec.gen_actions(SEED, s)
         vec.step()
-        r = vec.rewards.cpu().numpy()
-        term = vec.terminals.cpu().numpy()
-        for i in range(vec.n):
-            steps[i] += 1
-            st = f32(steps[i])
-            er = f32(run[i, 0] + r[i])
-            em = f32(run[i, 1] + f32(f32(r[i] - run[i, 1]) / st))
-            run[i] = (er, em)
-            if term[i]:
-                assert steps[i] == (firsts[i] if first[i] else 40), (i, s, steps[i])
-                if not (first[i] and firsts[i] < 40):
-                    m = f32(er / st)
-                    want["perf"][i] = f32(want["perf"][i] + m)
-                    want["score"][i] = f32(want["score"][i] + m)
-                    want["episode_return"][i] = f32(want["episode_return"][i] + er)
-                    want["reward_mean"][i] = f32(want["reward_mean"][i] + em)
-                    want["episode_length"][i] = f32(want["episode_length"][i] + st)
-                    want["n"][i] = f32(want["n"][i] + 1)
-                run[i] = 0.0
-                steps[i] = 0
-                first[i] = False
+        for tw in twins:
+            tw.step(SEED, s)
     torch.cuda.synchronize()
-    for i in range(vec.n):
-        got = vec.log(i)
-        assert got["n"] == want["n"][i] and got["episode_length"] == want["episode_length"][i], (i, got)
-        for k in ("perf", "score", "episode_return", "reward_mean"):
-            assert abs(got[k] - float(want[k][i])) <= 1e-6 * max(1.0, abs(float(want[k][i]))), (i, k, got, want[k][i])
+    for tw in twins:
+        got = vec.log(tw.i)
+        log_close(got, tw, f"env {tw.i}")
+        assert got["n"] == float(tw.glog.log["n"])
     assert sum(vec.log(i)["n"] for i in range(vec.n)) > 60
     vec.close()

@@ -315,3 +315,52 @@ def test_desync_first_steps_range():
     assert min(firsts) >= 1 and max(firsts) <= 8640
     assert len(set(firsts)) > 3100   # 4,096 uniform draws from 8,640 values: about 3,262 distinct
     assert abs(np.mean(firsts) - 4320.5) < 200
+
+
+@pytest.mark.parametrize("zones,ahus", [(41, 1), (81, 4)])
+def test_oracle_gpu_env_diagnostics(zones, ahus, tmp_path):
+    """The oracle's reward parts 12..15, the reference GPU env's per-step
+    diagnostics (complete_port/gpu/sb_gpu_kernels.cuh:1409-1473), recomputed
+    independently with numpy every step: each zone's mean over its room's cells
+    of the field the oracle exports, its deviation from the [heat, cool]
+    setpoint band at the step's calendar row, then the mean, the worst and the
+    fraction of zones outside the band; the gas rate times price and dt gives
+    the gas cost of part 4, which the reference core's own parts pin (they are
+    compared with the compiled reference core where it is built)."""
+    spec = G.LayoutSpec(zones, ahus)
+    clim = G.ClimateSpec(-5.0, 8.0, seed=41)
+    path = tmp_path / f"{spec.name}.sbb"
+    path.write_bytes(G.scenario_writer(spec, clim, 2 * G.EPISODE_STEPS, 17321).tobytes())
+    d = read_sbb(path)
+    nr, nc = (int(x) for x in d["grid"])
+    ro, rc, phys = d["room_offsets"], d["room_cells"].reshape(-1, 2), d["phys_room_idx"]
+    e = po.CpuEnv("oracle", path, 17321, start=0, max_steps=500)
+    ref = po.CpuEnv("ref", path, 17321, start=0, max_steps=500) if po.ref_available() else None
+    e.reset()
+    if ref:
+        ref.reset()
+    seen_out = 0
+    for s in range(120):
+        row = po.action_row(11, 0, s, e.n_cont, e.n_disc)
+        e.step(row)
+        pt = e.parts()
+        T = e.state()[:nr * nc]
+        j = s + 1
+        hsp, csp = d["sched_heat_sp"][j], d["sched_cool_sp"][j]
+        devs = []
+        for z in range(phys.size):
+            cells = rc[ro[phys[z]]:ro[phys[z] + 1]]
+            zt = T[cells[:, 0] * nc + cells[:, 1]].mean()
+            devs.append(max(zt - csp, hsp - zt, 0.0))
+        devs = np.array(devs)
+        assert abs(pt[12] - devs.mean()) <= 1e-9 * max(1.0, devs.mean()), s
+        assert abs(pt[13] - devs.max()) <= 1e-9 * max(1.0, devs.max()), s
+        assert pt[14] == np.count_nonzero(devs > 1e-12) / devs.size, s
+        seen_out += int(pt[14] > 0)
+        month = int(d["rew_month"][j])
+        gp = d["gas_month_price"][month - 1]
+        assert pt[15] >= 0.0 and abs(gp * pt[15] * pt[9] - pt[4]) <= 1e-12 * max(1.0, abs(pt[4])), s
+        if ref:
+            ref.step(row)
+            assert np.array_equal(ref.parts(), pt[:12]), s
+    assert seen_out > 0, "some step must leave the band (the diagnostics are not trivially zero)"
