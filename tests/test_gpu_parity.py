@@ -461,7 +461,6 @@ def test_gpu_log_matches_oracle(cfg0_dir):
     got = vec.log(0)
     log_close(got, tw, "one env")
     assert got["n"] == 2.0 and got["episode_length"] == 50.0
-    assert got["comfort_dev_K"] > 0.0 and got["worst_dev_K"] >= got["comfort_dev_K"] / 2.0
     assert got["elec_kwh"] > 0.0 and got["gas_kwh"] >= 0.0 and 0.0 <= got["out_of_band_frac"] <= 2.0
     vec.close()
 
@@ -729,4 +728,6 @@ def test_gpu_log_at_episode_ends_every_env(mixed_dir):
         log_close(got, tw, f"env {tw.i}")
         assert got["n"] == float(tw.glog.log["n"])
     assert sum(vec.log(i)["n"] for i in range(vec.n)) > 60
+    # some envs leave the comfort band in a logged episode (cold climates at dawn)
+    assert sum(vec.log(i)["comfort_dev_K"] > 0.0 for i in range(vec.n)) >= 3
     vec.close()
