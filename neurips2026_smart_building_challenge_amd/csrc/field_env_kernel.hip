@@ -743,10 +743,12 @@ __device__ void log_episode(const Args& a, int env, const float* ep, int st) {
                            ep[EP_PART + 3] / s, ep[EP_WORST], ep[EP_PART + 5] / s,
                            ep[EP_PART + 0] / s, ep[EP_PART + 1] / s, ep[EP_PART + 2] / s,
                            ep[EP_PART + 6], ep[EP_PART + 7], 1.0f};
-    for (int i = 0; i < 13; i++) {
-        const float x = __hip_atomic_load(&f[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        __hip_atomic_store(&f[i], x + add[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-    }
+    // every read issued before the first write: one round trip over the host link
+    float x[13];
+#pragma unroll
+    for (int i = 0; i < 13; i++) x[i] = __hip_atomic_load(&f[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+#pragma unroll
+    for (int i = 0; i < 13; i++) __hip_atomic_store(&f[i], x[i] + add[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 static_assert(sizeof(Log) == 52 && offsetof(Log, n) == 48, "log_episode writes the reference GPU env's Log");
 

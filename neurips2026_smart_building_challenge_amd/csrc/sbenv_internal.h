@@ -290,6 +290,8 @@ struct DevScen {
     int conv_tmean;              // 1 if some AHU may need the field mean
     int conv_on;                 // stochastic convection: conv_p != 0 and conv_distance != 0
     double conv_p;
+    double inv_nz;               // 1 / zones (the per-step comfort diagnostics are zone means)
+    double kwh_per_w;            // dt / 3.6e6: one step's energy in kWh per W
 };
 
 struct EnvDesc {
@@ -368,7 +370,7 @@ static_assert(sizeof(StateLayout) == 120 && sizeof(LdsLayout) == 96 && sizeof(Im
               && sizeof(ScenImg) == 24, "table layouts");
 static_assert(sizeof(DevLayout) == 888 && offsetof(DevLayout, st) == 88 && offsetof(DevLayout, img_src) == 496
               && offsetof(DevLayout, bytes_per_step) == 864, "DevLayout layout");
-static_assert(sizeof(DevScen) == 472 && offsetof(DevScen, img_src) == 32 && offsetof(DevScen, gas_co2) == 200
+static_assert(sizeof(DevScen) == 488 && offsetof(DevScen, img_src) == 32 && offsetof(DevScen, gas_co2) == 200
               && offsetof(DevScen, conv_p) == 464, "DevScen layout");
 static_assert(sizeof(KParams) == 136 && offsetof(KParams, host_env) == 80 && offsetof(KParams, phase_ts) == 112
               && offsetof(KParams, pass_ts_env) == 128, "KParams layout");

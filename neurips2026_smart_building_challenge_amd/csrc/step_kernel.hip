@@ -209,6 +209,29 @@ __device__ __forceinline__ void wave_sum2(double& a, double& b) {
     b = lane63_d(b);
 }
 
+// Sums of four per-lane values and the maximum of a fifth in one pass.
+__device__ __forceinline__ void wave_sum4_max(double& a, double& b, double& d, double& e, double& mx) {
+    const double ninf = __longlong_as_double((long long)0xFFF0000000000000ull);
+#define SBK_STEP5(CTRL, ROWS)                               \
+    a = a + dpp_d<CTRL, ROWS>(0.0, a);                      \
+    b = b + dpp_d<CTRL, ROWS>(0.0, b);                      \
+    d = d + dpp_d<CTRL, ROWS>(0.0, d);                      \
+    e = e + dpp_d<CTRL, ROWS>(0.0, e);                      \
+    mx = fmax(mx, dpp_d<CTRL, ROWS>(ninf, mx));
+    SBK_STEP5(DPP_QUAD_1032, 0xF)
+    SBK_STEP5(DPP_QUAD_2301, 0xF)
+    SBK_STEP5(DPP_ROW_HALF_MIRROR, 0xF)
+    SBK_STEP5(DPP_ROW_MIRROR, 0xF)
+    SBK_STEP5(DPP_ROW_BCAST15, 0xA)
+    SBK_STEP5(DPP_ROW_BCAST31, 0xC)
+#undef SBK_STEP5
+    a = lane63_d(a);
+    b = lane63_d(b);
+    d = lane63_d(d);
+    e = lane63_d(e);
+    mx = lane63_d(mx);
+}
+
 // Sums of N per-lane values in one pass (N independent DPP chains).
 template <int N>
 __device__ __forceinline__ void wave_sum_n(double (&x)[N]) {
@@ -2427,12 +2450,11 @@ __device__ __forceinline__ RewardPart reward_rest(Ctx& c, const double* zm, cons
             }
         }
     }
-    wave_sum2(occ_part, cum_part);
-    wave_sum2(dsum, noob);
+    wave_sum4_max(occ_part, cum_part, dsum, noob, dmax);
     out.total_occ = occ_part;
     out.cum = cum_part;
     out.dev_sum = dsum;
-    out.dev_max = wave_max(dmax);
+    out.dev_max = dmax;
     out.oob = noob;
     return out;
 }
@@ -2475,15 +2497,14 @@ __device__ __forceinline__ double reward_combine(const Ctx& c, double blower, do
     const double ncar = (den_c > 0.0) ? (elec_carb + gas_carb) / den_c : 0.0;
     const double pw = S->rw[5], ew = S->rw[6], cw = S->rw[7];
     const double raw = npr * pw - nec * ew - ncar * cw;
-    const double nz = (double)c.L->nz;
     sp.v[0] = npr;
     sp.v[1] = nec;
     sp.v[2] = ncar;
-    sp.v[3] = p.dev_sum / nz;
+    sp.v[3] = p.dev_sum * S->inv_nz;
     sp.v[4] = p.dev_max;
-    sp.v[5] = p.oob / nz;
-    sp.v[6] = fabs(elec_rate) * dt / 3.6e6;
-    sp.v[7] = gg * dt / 3.6e6;
+    sp.v[5] = p.oob * S->inv_nz;
+    sp.v[6] = fabs(elec_rate) * S->kwh_per_w;
+    sp.v[7] = gg * S->kwh_per_w;
     return raw / (pw + ew + cw);
 }
 
@@ -2543,21 +2564,28 @@ __device__ __forceinline__ void stamps_flush(const KParams& P, const Ctx& c) {
 // env's finalize_k, complete_port/gpu/smart_buildings.cu:2002-2036): each
 // field read and written with system-scope accesses (the trainer may clear the
 // Log between steps). ep: EP_* running sums, st: the episode's length.
-__device__ void log_episode(const KParams& P, int e, const float* ep, int st) {
-    Log* lg = reinterpret_cast<Log*>(reinterpret_cast<unsigned char*>(P.host_env) + (size_t)e * P.env_stride
-                                     + P.log_offset);
+__device__ __forceinline__ void log_episode(const KParams& P, int e, const float* ep, int st) {
+    // Log field i by lane i, so the 13 read-modify-writes over the host link
+    // are in flight together
+    const int i = ln();
+    if (i >= 13) return;
     const float s = (float)st;
-    const float mean = ep[EP_RET] / s;
-    const float add[13] = {mean, mean, ep[EP_RET], s,
-                           ep[EP_PART + 3] / s, ep[EP_WORST], ep[EP_PART + 5] / s,
-                           ep[EP_PART + 0] / s, ep[EP_PART + 1] / s, ep[EP_PART + 2] / s,
-                           ep[EP_PART + 6], ep[EP_PART + 7], 1.0f};
-    float* f = reinterpret_cast<float*>(lg);
-#pragma unroll
-    for (int i = 0; i < 13; i++) {
-        const float x = __hip_atomic_load(&f[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        __hip_atomic_store(&f[i], x + add[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    float a;
+    switch (i) {
+    case 0: case 1: a = ep[EP_RET] / s; break;          // perf, score: the episode's mean reward
+    case 2: a = ep[EP_RET]; break;
+    case 3: a = s; break;
+    case 4: a = ep[EP_PART + 3] / s; break;             // comfort_dev_K
+    case 5: a = ep[EP_WORST]; break;
+    case 6: a = ep[EP_PART + 5] / s; break;             // out_of_band_frac
+    case 7: case 8: case 9: a = ep[EP_PART + i - 7] / s; break;   // productivity, energy cost, carbon
+    case 10: case 11: a = ep[EP_PART + i - 4]; break;   // elec_kwh, gas_kwh
+    default: a = 1.0f; break;                           // n
     }
+    float* f = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(P.host_env) + (size_t)e * P.env_stride
+                                        + P.log_offset) + i;
+    const float x = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(f, x + a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 static_assert(sizeof(Log) == 52 && offsetof(Log, comfort_dev_K) == 16 && offsetof(Log, n) == 48,
               "log_episode writes the reference GPU env's Log field order");
@@ -2569,12 +2597,9 @@ static_assert(sizeof(Log) == 52 && offsetof(Log, comfort_dev_K) == 16 && offseto
 // update does not read the field either, so the first wavefront runs it before
 // the solve), so it is written while the first wavefront solves; the new chain
 // states are committed after it has read the old counts. Once the field is
-// there, the reward's non-AHU half (gas, pump, productivity) goes to the first
-// wavefront, which computes the AHU half meanwhile. The host log fields are
-// read over the host link after the wavefront's last other global load has been
-// issued (loads complete in issue order, so a wait for an earlier load never
-// waits for them), while it waits for the pre-step state; they are used only at
-// the end. Each wait is for a post the first wavefront always makes.
+// there, the reward's non-AHU half (gas, pump, productivity and the comfort
+// diagnostics) goes to the first wavefront, which computes the AHU half
+// meanwhile. Each wait is for a post the first wavefront always makes.
 template <int W>
 __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, unsigned char* env, float* obs_row,
                                             int kk, int j) {
@@ -2807,20 +2832,27 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P0) {
                 c.ip[PI_EPISODES] += 1;
                 c.ip[PI_FIRST_DONE] = 1;
             }
-            // the episode's running sums in float, as the reference GPU env
-            // keeps them (smart_buildings.cu:1965-1971); added to the host Log
-            // when a whole episode ends (:2002-2036), so a step reads nothing
-            // over the host link
-            float* ep = reinterpret_cast<float*>(c.ip + PI_EP);
-            ep[EP_RET] += r;
+        }
+        // the episode's running sums in float, as the reference GPU env keeps
+        // them (smart_buildings.cu:1965-1971), lane k updating sum k; added to
+        // the host Log when a whole episode ends (:2002-2036), so a step reads
+        // nothing over the host link
+        float* ep = reinterpret_cast<float*>(c.ip + PI_EP);
+        {
+            const int k = ln();
+            float x = r;
 #pragma unroll
-            for (int k = 0; k < 8; k++) ep[EP_PART + k] += (float)sp.v[k];
-            if ((float)sp.v[4] > ep[EP_WORST]) ep[EP_WORST] = (float)sp.v[4];
-            if (done) {
-                if (P.host_env && !cut) log_episode(P, e, ep, step);
-#pragma unroll
-                for (int k = 0; k < EP_COUNT; k++) ep[k] = 0.0f;
+            for (int q = 0; q < 8; q++) x = k == EP_PART + q ? (float)sp.v[q] : x;
+            if (k < EP_COUNT) {
+                const float o = ep[k];
+                ep[k] = k == EP_WORST ? ((float)sp.v[4] > o ? (float)sp.v[4] : o) : o + x;
             }
+        }
+        esync();
+        if (done) {
+            if (P.host_env && !cut) log_episode(P, e, ep, step);
+            esync();
+            if (ln() < EP_COUNT) ep[ln()] = 0.0f;
         }
         esync();
     }

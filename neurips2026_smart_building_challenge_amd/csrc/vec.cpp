@@ -983,6 +983,8 @@ bool make_scen(const sbh::Blob& b, const HostLayout& Lh, HostScen* H, Arena& A, 
     }
     const double* op = b.f64("occ_params");
     D.dt_sec = op[5];
+    D.inv_nz = 1.0 / L.nz;
+    D.kwh_per_w = op[5] / 3.6e6;
     D.ea = (int)op[1]; D.la = (int)op[2]; D.ed = (int)op[3]; D.ld = (int)op[4];
     D.p_arr = 1.0 / ((D.la - D.ea) * 3600.0 / op[5] / 2.0);
     D.p_dep = 1.0 / ((D.ld - D.ed) * 3600.0 / op[5] / 2.0);
