@@ -21,14 +21,25 @@
 // stores it to the lane's reciprocal slot (the sink for other tasks).
 //
 // A task's level is one more than the levels of everything it reads; tasks of
-// one level are independent, sorted by term count (descending) and cut into
-// passes of `width` lanes. A pass stores one 64-bit header per active lane and
-// its terms row by row: row m holds term m of every active lane (lanes whose
-// count is m or less hold the (0, 0) term, which reads the zero slot), so term
-// m of lane l sits at word_off + m * nact + l and each row is one coalesced read
-// whose address needs nothing but the pass record.
-// Dot products longer than kPlanKmax terms become a chain of tasks on the same
-// slot; only the last one divides.
+// one level are independent. A task runs on a segment of S lanes (S a power of
+// two up to kPlanSegMax, aligned, so the segment lies in one 16-lane row):
+// lane j of the segment takes the task's terms j, j + S, j + 2S, ..., the
+// segment's first lane (its leader) starts from the target's value and the
+// others from 0, and a butterfly over the segment (partners lane ^ 1, ^ 2,
+// ^ 4, ^ 8) leaves the sum in every lane; the leader stores it. A level's
+// tasks, sorted by term count (descending), fill passes of `width` lanes with
+// the narrowest segments that keep every lane at kPlanKmax terms or fewer;
+// lanes a pass leaves free then widen the segment of its longest lane load,
+// one doubling at a time, as long as that shortens the pass. A pass stores one
+// 64-bit header for each of the `width` lanes (idle lanes included) and its
+// terms lane by lane: lane l's terms sit at word_off + l * stride + m, stride =
+// maxcnt rounded up to 4 (a lane's terms past its count are the (0, 0) term,
+// which reads the zero slot), so a lane reads its pass with four 16-byte loads
+// whose addresses need nothing but the pass record, and no loaded value is
+// inspected before the pass runs. The pass count is padded with empty passes
+// to a multiple of kPlanDepth, the kernel's prefetch depth.
+// Dot products longer than kPlanKmax * kPlanSegMax terms become a chain of
+// tasks on the same slot; only the last one divides.
 //
 // build_relax prepares the alternative used for strongly diagonally dominant
 // systems: Jacobi sweeps with a certified contraction bound (see plan.h).
@@ -192,13 +203,14 @@ bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
     // slot to produce (or kSlotSink), terms, extra dependency level
     auto add_task = [&](int target, int mul, int inv_target, std::vector<std::pair<int, int>>&& terms,
                         int extra_level) {
-        // split into chains of at most kPlanKmax terms; the last piece scales
-        // and produces the reciprocal
+        // split into chains of at most kTaskTerms terms; the last piece
+        // scales and produces the reciprocal
+        constexpr size_t kTaskTerms = (size_t)kPlanKmax * kPlanSegMax;
         size_t nt = terms.size();
-        size_t pieces = nt == 0 ? 1 : (nt + kPlanKmax - 1) / kPlanKmax;
+        size_t pieces = nt == 0 ? 1 : (nt + kTaskTerms - 1) / kTaskTerms;
         int prev = extra_level;
         for (size_t pc = 0; pc < pieces; pc++) {
-            size_t lo = pc * kPlanKmax, hi = std::min(nt, lo + (size_t)kPlanKmax);
+            size_t lo = pc * kTaskTerms, hi = std::min(nt, lo + kTaskTerms);
             std::vector<std::pair<int, int>> part(terms.begin() + lo, terms.begin() + hi);
             int lv = prev;
             for (auto& t : part) lv = std::max(lv, std::max(slot_level[t.first], slot_level[t.second]));
@@ -253,7 +265,7 @@ bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
         add_task(vb + i, ib + i, kSlotSink, std::move(terms), lv0);
     }
 
-    // levels -> passes
+    // levels -> passes of lane segments
     int maxlv = 0;
     for (auto& t : tasks) maxlv = std::max(maxlv, t.level);
     P.n_levels = maxlv;
@@ -261,41 +273,98 @@ bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
     std::vector<std::vector<int>> by_level(maxlv + 1);
     for (int t = 0; t < (int)tasks.size(); t++) by_level[tasks[t].level].push_back(t);
     long long npairs = 0, ndiv = 0;
+    auto load = [&](int id, int seg) { return ((int)tasks[id].terms.size() + seg - 1) / seg; };
     for (int lv = 1; lv <= maxlv; lv++) {
         auto& ids = by_level[lv];
         std::stable_sort(ids.begin(), ids.end(), [&](int a, int c) {
             if (tasks[a].terms.size() != tasks[c].terms.size()) return tasks[a].terms.size() > tasks[c].terms.size();
             return tasks[a].target < tasks[c].target;
         });
-        for (size_t s = 0; s < ids.size(); s += (size_t)width) {
-            size_t e = std::min(ids.size(), s + (size_t)width);
+        size_t s = 0;
+        while (s < ids.size()) {
+            // the pass's tasks at their narrowest segments
+            std::vector<int> pid, seg;
+            int used = 0;
+            while (s < ids.size()) {
+                int sg = 1;
+                while (load(ids[s], sg) > kPlanKmax) sg *= 2;
+                if (used + sg > width) break;
+                pid.push_back(ids[s]);
+                seg.push_back(sg);
+                used += sg;
+                s++;
+            }
+            // widen the longest lane load while lanes are free
+            for (;;) {
+                int best = -1;
+                for (size_t q = 0; q < pid.size(); q++)
+                    if (best < 0 || load(pid[q], seg[q]) > load(pid[best], seg[best])) best = (int)q;
+                if (best < 0 || load(pid[best], seg[best]) <= 1 || seg[best] >= kPlanSegMax
+                    || used + seg[best] > width)
+                    break;
+                used += seg[best];
+                seg[best] *= 2;
+            }
+            // place segments widest first (power-of-two sizes in descending
+            // order land on aligned offsets)
+            std::vector<int> ord(pid.size());
+            for (size_t q = 0; q < ord.size(); q++) ord[q] = (int)q;
+            std::stable_sort(ord.begin(), ord.end(), [&](int a, int c) { return seg[a] > seg[c]; });
+            struct Lane {
+                int task, j, seg;
+            };
+            std::vector<Lane> lanes;
+            for (int q : ord)
+                for (int j = 0; j < seg[q]; j++) lanes.push_back(Lane{pid[q], j, seg[q]});
+            const int nact = (int)lanes.size();
+            int maxcnt = 0, piv = 0;
             PassInfo pi{};
             pi.hdr_off = (int)P.hdr.size();
             pi.word_off = (int)P.words.size();
-            const int nact = (int)(e - s);
-            const int maxcnt = (int)tasks[ids[s]].terms.size();
-            int piv = 0;
-            for (size_t id = s; id < e; id++) {
-                const Task& t = tasks[ids[id]];
-                P.hdr.push_back((uint64_t)(uint32_t)t.target | ((uint64_t)(uint32_t)t.mul << 16)
-                                | ((uint64_t)(uint32_t)t.inv_target << 32) | ((uint64_t)t.terms.size() << 48));
-                npairs += (long long)t.terms.size();
-                ndiv += t.inv_target != kSlotSink ? 1 : 0;
-                if (t.inv_target != kSlotSink) piv = 1;
+            for (const Lane& l : lanes) {
+                const Task& t = tasks[l.task];
+                const int cnt = ((int)t.terms.size() - l.j + l.seg - 1) / l.seg;
+                maxcnt = std::max(maxcnt, cnt);
+                int lg = 0;
+                while ((1 << lg) < l.seg) lg++;
+                const bool lead = l.j == 0;
+                const uint64_t flags = (uint64_t)lg | ((uint64_t)(lead ? 1 : 0) << 3) | ((uint64_t)cnt << 4);
+                const int tgt = lead ? t.target : kSlotZero;
+                const int mul = lead ? t.mul : kSlotOne;
+                const int inv = lead ? t.inv_target : kSlotSink;
+                P.hdr.push_back((uint64_t)(uint32_t)tgt | ((uint64_t)(uint32_t)mul << 16)
+                                | ((uint64_t)(uint32_t)inv << 32) | (flags << 48));
+                if (lead) {
+                    npairs += (long long)t.terms.size();
+                    ndiv += t.inv_target != kSlotSink ? 1 : 0;
+                    if (t.inv_target != kSlotSink) piv = 1;
+                }
             }
-            pi.packed = nact | (maxcnt << 8) | (piv << 16);
-            for (int m = 0; m < maxcnt; m++) {
-                for (size_t id = s; id < e; id++) {
-                    const Task& t = tasks[ids[id]];
-                    P.words.push_back((int)t.terms.size() > m
-                                      ? (uint32_t)t.terms[m].first | ((uint32_t)t.terms[m].second << 16)
+            for (int l = nact; l < width; l++) P.hdr.push_back(kIdleHeader);
+            const int wide = (int)lanes.size() > (int)pid.size() ? 1 : 0;
+            pi.packed = nact | (maxcnt << 8) | (piv << 16) | (wide << 17);
+            const int stride = (maxcnt + 3) & ~3;
+            for (const Lane& l : lanes) {
+                const Task& t = tasks[l.task];
+                for (int m = 0; m < stride; m++) {
+                    const size_t q = (size_t)l.j + (size_t)m * l.seg;
+                    P.words.push_back(q < t.terms.size()
+                                      ? (uint32_t)t.terms[q].first | ((uint32_t)t.terms[q].second << 16)
                                       : 0u);
                 }
             }
             P.passes.push_back(pi);
         }
     }
-    P.words.resize(P.words.size() + (size_t)kWordTailRows * width, 0u);
+    // empty passes up to a multiple of the prefetch depth: no lane leads, no pivot
+    while (P.passes.size() % kPlanDepth) {
+        PassInfo pi{};
+        pi.hdr_off = (int)P.hdr.size();
+        pi.word_off = (int)P.words.size();
+        for (int l = 0; l < width; l++) P.hdr.push_back(kIdleHeader);
+        P.passes.push_back(pi);
+    }
+    P.words.resize(P.words.size() + kWordTail, 0u);
     P.n_pairs = npairs;
     P.n_divs = ndiv;
     return true;

@@ -10,23 +10,33 @@
 
 namespace sbh {
 
-// Maximum terms one lane handles in one pass (longer dot products are split
-// into continuation tasks in later passes). The kernel keeps a pass's terms in
-// registers, so this bounds its register arrays.
-constexpr int kPlanKmax = 48;
+// Maximum terms one lane handles in one pass, and lanes one task may span (a
+// segment within a 16-lane row, summed by a butterfly). Longer dot products
+// are split into continuation tasks in later passes. The kernel keeps a pass's
+// terms in registers, so kPlanKmax bounds its register arrays.
+constexpr int kPlanKmax = 16;
+constexpr int kPlanSegMax = 16;
 
-// Per-pass record, 16 bytes: hdr_off, word_off, nact | maxcnt << 8 | has_pivot << 16, 0.
+// Per-pass record, 16 bytes: hdr_off, word_off, nact | maxcnt << 8 | has_pivot << 16 | wide << 17, 0.
+// nact: lanes used; wide: some task spans more than one lane. Lane header: target | mul << 16 | inv_target << 32 | flags << 48,
+// flags = log2(segment lanes) | leader << 3 | terms << 4; a lane that is not its
+// segment's leader has target kSlotZero, mul kSlotOne and inv_target kSlotSink.
 struct PassInfo {
     int hdr_off, word_off, packed, pad;
     int nact() const { return packed & 0xff; }
     int maxcnt() const { return (packed >> 8) & 0xff; }
     int has_pivot() const { return (packed >> 16) & 1; }
+    int wide() const { return (packed >> 17) & 1; }
 };
 
 // Fixed slots: 0 holds 0.0 (padding terms read it), 1 is a write sink, 2 holds 1.0.
 constexpr int kSlotZero = 0, kSlotSink = 1, kSlotOne = 2;
-// Rows of padding after the last pass, so chunked reads of 8 rows stay inside the array.
-constexpr int kWordTailRows = 8;
+// An idle lane's header: target and reciprocal target the sink, multiplier the zero slot, not a leader.
+constexpr uint64_t kIdleHeader = 0x0000000100000001ull;
+// Words of padding after the last pass: a lane reads kPlanKmax words from its start.
+constexpr int kWordTail = 16;
+// Passes the kernel loads ahead of the one it runs plus one; the pass count is a multiple of it.
+constexpr int kPlanDepth = 4;
 
 struct SolvePlan {
     int n = 0, k = 0, width = 0;
@@ -37,8 +47,8 @@ struct SolvePlan {
     std::vector<double> slot_init;   // [n_slots]
     std::vector<int> air_slot, air_node;   // [k]
     std::vector<PassInfo> passes;
-    std::vector<uint64_t> hdr;       // per active lane: target | mul << 16 | inv_target << 32 | count << 48
-    std::vector<uint32_t> words;     // rows of nact words: term m of lane l at word_off + m * nact + l
+    std::vector<uint64_t> hdr;       // per lane: target | mul << 16 | inv_target << 32 | flags << 48
+    std::vector<uint32_t> words;     // term m of lane l at word_off + l * stride + m, stride = maxcnt rounded up to 4
     int n_pass() const { return (int)passes.size(); }
 };
 

@@ -16,7 +16,8 @@
 #define SBK_MAX_AHU 16
 #define SBK_MT_N 624
 #define SBK_NAUX_MAX 16
-#define SBK_KMAX 48      // terms per lane per pass (matches the planner)
+#define SBK_KMAX 16      // terms per lane per pass (matches the planner)
+#define SBK_PLAN_DEPTH 4 // pass count multiple and prefetch depth (matches the planner)
 #define SBK_NSTAMP 32        // phase stamps per env when phase timing is on
 #define SBK_STAMP_HELPER 15  // stamps 15..18 are the env's helper wavefront's
 #define SBK_STAMP_ENTRY 19   // the first wavefront's entry into the kernel (20.. finer stamps of its HVAC pre-step)

@@ -1680,47 +1680,39 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P, int* sy) {
 // ------------------------------------------------------------------ solve plan
 struct PassRegs {
     uint64_t h;
-    int nact, maxcnt, piv;
     uint32_t w[SBK_KMAX];
 };
 
-// Issues the loads of one pass's header and term words into registers. Term m
-// of lane l is at word_off + m * nact + l: every address comes from the pass
-// record alone, so all loads of a pass go out back to back. Rows are read in
-// chunks of 8 without per-row branches; rows past maxcnt (the next pass's
-// words, or the array's tail padding) and lanes past nact read in-bounds words
-// that are then replaced by the (0, 0) term.
+// Pass record fields (nact | maxcnt << 8 | has_pivot << 16 | wide << 17).
+__device__ __forceinline__ int pass_maxcnt(int4 pi) { return (pi.z >> 8) & 0xff; }
+__device__ __forceinline__ bool pass_pivot(int4 pi) { return (pi.z >> 16) & 1; }
+__device__ __forceinline__ bool pass_wide(int4 pi) { return (pi.z >> 17) & 1; }
+
+// Issues the loads of one pass's lane header and terms into registers: the
+// header of this lane (every lane has one, idle lanes included) and four
+// 16-byte words from the lane's start (word_off + lane * stride; idle lanes
+// read lane 0's). Words past the lane's stride belong to the next lane or pass
+// and are masked when the pass runs, so nothing here waits for a load.
 __device__ __forceinline__ void fetch_pass(const SBK_C DevLayout* L, int4 pi, PassRegs& r) {
+    typedef unsigned int u4v __attribute__((ext_vector_type(4)));
     const int hdr_off = pi.x, word_off = pi.y;
-    const int nact = pi.z & 0xff, maxcnt = (pi.z >> 8) & 0xff, has_pivot = (pi.z >> 16) & 1;
+    const int nact = pi.z & 0xff, stride = (pass_maxcnt(pi) + 3) & ~3;
     const int lane = ln();
-    const bool act = lane < nact;
-    r.nact = nact;
-    r.maxcnt = maxcnt;
-    r.piv = has_pivot;
-    const uint64_t hv = L->hdr[hdr_off + (act ? lane : 0)];
-    // idle lanes: target and reciprocal target both the sink (slot 1), multiplier slot 0
-    r.h = act ? hv : 0x0000000100000001ull;
-    const SBK_C uint32_t* wp = L->words + word_off + lane;
+    r.h = L->hdr[hdr_off + lane];
+    const u4v* wp = reinterpret_cast<const u4v*>(L->words + word_off + (lane < nact ? lane : 0) * stride);
 #pragma unroll
-    for (int m0 = 0; m0 < SBK_KMAX; m0 += 8) {
-        if (m0 < maxcnt) {
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const int m = m0 + j;
-                const uint32_t v = wp[m * nact];
-                r.w[m] = (m < maxcnt && act) ? v : 0u;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; j++) r.w[m0 + j] = 0;
-        }
+    for (int q = 0; q < SBK_KMAX / 4; q++) {
+        const u4v v = wp[q];
+        r.w[4 * q + 0] = v.x;
+        r.w[4 * q + 1] = v.y;
+        r.w[4 * q + 2] = v.z;
+        r.w[4 * q + 3] = v.w;
     }
 }
 
 // Waits for a fetched pass here: the empty asm "uses" every register, so the
 // compiler places the memory wait at this point instead of at the first use
-// inside the next pass (where the loads of the pass after it are in flight).
+// inside the pass (where the loads of the passes after it are in flight).
 __device__ __forceinline__ void settle_pass(PassRegs& r) {
     asm volatile("" : "+v"(r.h));
 #pragma unroll
@@ -1736,20 +1728,31 @@ __device__ __forceinline__ double recip(double x) {
     return fma(r, e, r);
 }
 
-// One pass: every active lane computes slot[target] = (slot[target] - sum of
-// its terms) * slot[mul]; in a pass holding pivots, lanes also store the
-// reciprocal of their result to slot[inv_target] (the sink for non-pivots).
-// Missing terms are (0, 0) and read slot 0 = 0.
-__device__ __forceinline__ void run_pass(double* slots, const PassRegs& r) {
-    constexpr int CH = 8;
+// One pass: every task computes slot[target] = (slot[target] - sum of its
+// terms) * slot[mul] on its segment of lanes. Each lane subtracts its own terms
+// (the leader from slot[target], the others from 0), a butterfly over the
+// segment (lane ^ 1, ^ 2, then the other quad and the other half-row, whose
+// lanes hold equal sums by then) gives every lane of the segment the same
+// total, and the leader stores it. In a pass holding pivots, lanes also store
+// the reciprocal of their result to slot[inv_target] (the sink for non-pivots,
+// non-leaders and idle lanes). Terms run in groups of 4 up to the pass's
+// longest lane (its stride is that rounded up to 4, so a group never reaches
+// another lane's words); terms past a lane's count are (0, 0) and read slot
+// 0 = 0.
+__device__ __forceinline__ void run_pass(double* slots, const PassRegs& r, int4 pi) {
+    constexpr int CH = 4;
+    const int maxcnt = pass_maxcnt(pi);
     const int tgt = (int)(r.h & 0xffffu);
     const int mul = (int)((r.h >> 16) & 0xffffu);
     const int invt = (int)((r.h >> 32) & 0xffffu);
+    const int flags = (int)(r.h >> 48);
+    const int lg = flags & 7;
+    const bool lead = (flags >> 3) & 1;
     double acc = slots[tgt];
     const double scale = slots[mul];
 #pragma unroll
     for (int m0 = 0; m0 < SBK_KMAX; m0 += CH) {
-        if (m0 >= r.maxcnt) break;
+        if (m0 >= maxcnt) break;
         double x[CH], y[CH];
 #pragma unroll
         for (int j = 0; j < CH; j++) {
@@ -1760,38 +1763,47 @@ __device__ __forceinline__ void run_pass(double* slots, const PassRegs& r) {
 #pragma unroll
         for (int j = 0; j < CH; j++) acc -= x[j] * y[j];
     }
+    if (pass_wide(pi)) {
+        double t = dpp_d<DPP_QUAD_1032>(0.0, acc);
+        acc = lg >= 1 ? acc + t : acc;
+        t = dpp_d<DPP_QUAD_2301>(0.0, acc);
+        acc = lg >= 2 ? acc + t : acc;
+        t = dpp_d<DPP_ROW_HALF_MIRROR>(0.0, acc);
+        acc = lg >= 3 ? acc + t : acc;
+        t = dpp_d<DPP_ROW_MIRROR>(0.0, acc);
+        acc = lg >= 4 ? acc + t : acc;
+    }
     acc *= scale;
-    if (ln() < r.nact) slots[tgt] = acc;
-    if (r.piv) slots[invt] = recip(acc);
+    if (lead) slots[tgt] = acc;
+    if (pass_pivot(pi)) slots[invt] = recip(acc);
 }
 
-// All passes. Pass p+1's words are loaded while pass p computes and settled
-// after it; pass records are read two passes ahead.
+// All passes, in groups of SBK_PLAN_DEPTH (the pass count is a multiple of
+// it): a group's loads go out together and its passes wait for their own in
+// turn, and the next group's first pass is loaded before the group's last one
+// runs. Only that one pass's loads are in flight across the loop's back edge,
+// so the compiler's memory waits stay exact (a wait for pass k of a group
+// leaves the later passes' loads in flight).
 template <int W>
 __device__ __forceinline__ void run_plan(const SBK_C DevLayout* L, double* slots, const int4* rec,
                                          unsigned long long* pts) {
     static_assert(W == 64, "the solve plan runs on one wavefront");
+    constexpr int D = SBK_PLAN_DEPTH;
     const int np = L->n_pass;
     if (np == 0) return;
-    const int last = np - 1;
-    PassRegs A, B;
-    int4 q1 = rec[min(1, last)];
-    fetch_pass(L, rec[0], A);
-    settle_pass(A);
-    for (int p = 0; p < np; p += 2) {
+    PassRegs R[D];
+    fetch_pass(L, rec[0], R[0]);
+    for (int p = 0; p < np; p += D) {
         if (pts) pts[p] = clock64();
-        const int4 q2 = rec[min(p + 2, last)];
-        if (p + 1 < np) fetch_pass(L, q1, B);
-        run_pass(slots, A);
-        wave_lds_sync();
-        if (p + 1 >= np) break;
-        settle_pass(B);
-        const int4 q3 = rec[min(p + 3, last)];
-        if (p + 2 < np) fetch_pass(L, q2, A);
-        run_pass(slots, B);
-        wave_lds_sync();
-        settle_pass(A);
-        q1 = q3;
+#pragma unroll
+        for (int k = 1; k < D; k++) fetch_pass(L, rec[p + k], R[k]);
+#pragma unroll
+        for (int k = 0; k < D; k++) {
+            if (k == D - 1) fetch_pass(L, rec[min(p + D, np - 1)], R[0]);
+            settle_pass(R[k]);
+            run_pass(slots, R[k], rec[p + k]);
+            wave_lds_sync();
+        }
     }
     if (pts) pts[np] = clock64();
 }

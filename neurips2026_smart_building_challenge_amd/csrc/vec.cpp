@@ -28,6 +28,9 @@
 #include "sbenv.h"
 #include "sbenv_internal.h"
 
+static_assert(sbh::kPlanKmax == SBK_KMAX && sbh::kPlanDepth == SBK_PLAN_DEPTH && sbh::kWordTail >= SBK_KMAX,
+              "the kernel's pass registers and prefetch depth match the planner's");
+
 extern "C" int sbk_launch_step(const sbk::KParams* p, int n_blocks, int threads, int lds_bytes, int variant,
                                hipStream_t s);
 extern "C" int sbk_set_lds_limit(int width, int bytes);
@@ -1990,10 +1993,10 @@ int sbx_pass_times(Env* envs, int env, long long* cycles, int cap) {
         }
         return m;
     }
-    // stamps are taken at even passes (and after the last): split each
-    // two-pass interval evenly
-    for (int i = 0; i < np; i += 2) {
-        const int j = std::min(i + 2, np);
+    // stamps are taken every SBK_PLAN_DEPTH passes (and after the last):
+    // split each interval evenly
+    for (int i = 0; i < np; i += SBK_PLAN_DEPTH) {
+        const int j = std::min(i + SBK_PLAN_DEPTH, np);
         const long long dt = (long long)(h[j] - h[i]);
         for (int k = i; k < j; k++) cycles[k] = dt / (j - i);
     }

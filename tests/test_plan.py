@@ -13,25 +13,46 @@ from neurips2026_smart_building_challenge_amd.scenario.sbb import SbbWriter, rea
 
 
 def run_plan(pl, slots):
-    """Executes the exported plan pass by pass, as the kernel does."""
+    """Executes the exported plan pass by pass, as the kernel does: each task on
+    an aligned segment of lanes, lane j taking its terms j, j + S, ..., the
+    leader starting from the target, a butterfly summing the segment."""
+    assert pl["n_pass"] % 4 == 0, "passes padded to the prefetch depth"
+    assert pl["hdr"].size == 64 * pl["n_pass"]
     for pi in pl["pass_info"]:
         ho, wo, packed = (int(x) for x in pi[:3])
-        nact, maxcnt, piv = packed & 0xFF, (packed >> 8) & 0xFF, (packed >> 16) & 1
+        nact, maxcnt, piv, wide = packed & 0xFF, (packed >> 8) & 0xFF, (packed >> 16) & 1, (packed >> 17) & 1
+        assert ho % 64 == 0 and wo % 4 == 0, "a header per lane; 16-byte aligned lane words"
+        stride = (maxcnt + 3) & ~3
+        assert wo + max(nact - 1, 0) * stride + 16 <= pl["words"].size, "a lane's four 16-byte reads stay in the array"
+        assert np.all(pl["hdr"][ho + nact:ho + 64] == 0x0000000100000001), "idle lanes' headers"
         h = pl["hdr"][ho:ho + nact].astype(np.uint64)
         tgt = (h & 0xFFFF).astype(np.int64)
         mul = ((h >> 16) & 0xFFFF).astype(np.int64)
         invt = ((h >> 32) & 0xFFFF).astype(np.int64)
-        cnt = (h >> 48).astype(np.int64)
-        assert np.all(np.diff(cnt) <= 0), "lanes must be sorted by term count"
-        assert len(set(tgt.tolist())) == nact, "one task per target in a pass"
+        fl = (h >> 48).astype(np.int64)
+        lg, lead, cnt = fl & 7, (fl >> 3) & 1, fl >> 4
+        lanes = np.arange(nact)
+        seg = 1 << lg
+        assert np.all(seg <= 16) and np.all(lead == (lanes % seg == 0)), "aligned segments within a 16-lane row"
+        for l in np.flatnonzero(lead):
+            assert np.all(lg[l:l + seg[l]] == lg[l]), "a segment's lanes share its width"
+        assert np.all(tgt[lead == 0] == 0) and np.all(mul[lead == 0] == 2) and np.all(invt[lead == 0] == 1)
+        assert wide == int(np.any(seg > 1))
+        assert len(set(tgt[lead == 1].tolist())) == int(lead.sum()), "one task per target in a pass"
         assert piv == int(np.any(invt != 1))
-        acc = slots[tgt].copy()
+        assert cnt.max(initial=0) == maxcnt
+        acc = np.where(lead == 1, slots[tgt], 0.0)
+        W = pl["words"][wo:wo + nact * stride].astype(np.int64).reshape(nact, stride)
         for m in range(maxcnt):
-            w = pl["words"][wo + m * nact:wo + (m + 1) * nact].astype(np.int64)
+            w = W[:, m]
             assert np.all(w[cnt <= m] == 0), "terms past a lane's count must be (0, 0)"
-            acc -= slots[w & 0xFFFF] * slots[w >> 16]
-        acc *= slots[mul]
-        slots[tgt] = acc
+            acc = acc - slots[w & 0xFFFF] * slots[w >> 16]
+        assert np.all(W[:, maxcnt:] == 0)
+        for k in range(4):
+            partner = np.minimum(lanes ^ (1 << k), nact - 1)
+            acc = np.where(lg > k, acc + acc[partner], acc)
+        acc = acc * slots[mul]
+        slots[tgt[lead == 1]] = acc[lead == 1]
         if piv:
             with np.errstate(divide="ignore"):
                 slots[invt] = 1.0 / acc
