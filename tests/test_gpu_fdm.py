@@ -273,3 +273,34 @@ def test_gpu_fdm_full_size_default_every_cell(full, G):
             assert close(Tg[g], To[i]), (G, s, g, "T", np.abs(Tg[g] - To[i]).max())
             assert close(Mg[g], Mo[i]), (G, s, g, "M", np.abs(Mg[g] - Mo[i]).max())
     f.close()
+
+
+def test_gpu_fdm_largest_shipped_size(tmp_path):
+    """A plan at the largest shipped building's size (building_30025__singapore_5:
+    1622 x 653 cells, 82 rooms; 926,266 solved): exact mode bit-identical to
+    the oracle (field and interior mass, 2 envs x 2 steps), the default
+    configuration within 1e-9 of it (3 envs x 2 steps, every column of one
+    env's air side on)."""
+    import torch
+
+    spec = F.FdmSpec(rows=1622, cols=653, rooms=82, seed=3)
+    plan, path, _ = write_blob(spec, tmp_path)
+    say(f"largest shipped size: {plan.n_cvs} cells, {plan.n} solved, {plan.k} rooms")
+    assert plan.n_cvs == 1622 * 653 and plan.k == 82
+    for exact, G in ((True, 2), (False, 3)):
+        f = gpu_group(path, G, 0, exact=exact)
+        o = po.Fdm("oracle", path, G)
+        for s in range(2):
+            inp = F.step_inputs(plan, G, 41, s)
+            inp["air_g"][G - 1] = np.where(inp["air_g"][G - 1] > 0.0, inp["air_g"][G - 1], 25.0)
+            f.step(*device_inputs(inp))
+            o.step(inp)
+            torch.cuda.synchronize()
+            Tg, Mg = f.state()
+            To, Mo = o.state()
+            if exact:
+                assert np.array_equal(Tg, To) and np.array_equal(Mg, Mo), (s, np.abs(Tg - To).max())
+            else:
+                assert close(Tg, To) and close(Mg, Mo), (s, np.abs(Tg - To).max())
+        f.close()
+    path.unlink()

@@ -289,3 +289,27 @@ def test_gpu_field_env_default_mode_full_size(tmp_path):
     done = run_against_oracle(vec, twins, 7, False, "full size")
     assert done == 2 * len(picks)
     vec.close()
+
+
+LARGEST = dict(rows=1622, cols=653, rooms=82, seed=3)   # building_30025__singapore_5's grid and rooms
+
+
+@pytest.fixture(scope="module")
+def largest_blob(tmp_path_factory):
+    p = field_blob(tmp_path_factory.mktemp("field_largest"), LARGEST, 4, 3, table_steps=64, conv=SHIPPED_CONV)
+    yield p
+    p.unlink()
+
+
+@pytest.mark.parametrize("exact", [True, False])
+def test_gpu_field_env_largest_shipped_size(largest_blob, exact):
+    """The largest shipped building's size (1,059,166 cells, 926,266 solved,
+    82 rooms, 4 AHUs) with the shipped convection (p 0.1, distance 2): two envs
+    against their oracle twins through an auto-reset, bit-identical in exact
+    field mode, within the per-step bars in the default one."""
+    say(f"2 envs at 1,059,166 cells with convection, {'exact' if exact else 'default'} field mode, 4 steps")
+    vec = E.VecEnv(2, blob=str(largest_blob), max_steps=3, field_exact=1 if exact else 0)
+    twins = [Twin(vec, i, 3) for i in range(2)]
+    done = run_against_oracle(vec, twins, 4, exact, "largest")
+    assert done == 2
+    vec.close()
