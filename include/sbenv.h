@@ -134,7 +134,10 @@ void dict_set(Dict* d, const char* key, float value);
  * Extras: start_offsets (1: every env starts its episodes at its own seeded
  * calendar offset, start_seed), shard_base (this vec's first env index in a
  * batch sharded over several vecs), per_env_seed (occupancy / convection seed
- * + index within the scenario, default 1), solver, envs_per_block. The Log
+ * + index within the scenario, default 1), solver, envs_per_block,
+ * trace_air (1: each step also stores every env's air side, air_g and air_T
+ * as the reference core's state holds them, so sbx_env_state reports them;
+ * without it the RC scenarios' snapshots carry NaN there). The Log
  * is filled at episode ends (the reference GPU env's form); the key log_at_end
  * is accepted at 1 only (the per-step Log of earlier versions is gone). */
 Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions,
@@ -188,8 +191,10 @@ void sbx_vec_info(Env* envs, SbxVecInfo* out);
  * VAV damper/reheat/ratio/sensing, AHU flow/sat/recirc/fan, air_g, air_T,
  * occupancy, boiler current/return/setpoint, pump head, calendar index),
  * followed by two extras: the f64 sum of rewards and the number of steps since
- * puf_reset. air_g / air_T are not kept between steps and read as NaN.
- * Returns the number of doubles written (<= cap), or -1. */
+ * puf_reset. On RC scenarios air_g / air_T are the last step's under the
+ * kwarg trace_air (zero before the first step) and NaN without it; field
+ * scenarios keep them in their records. Returns the number of doubles written
+ * (<= cap), or -1. */
 int sbx_env_state(Env* envs, int i, double* out, int cap);
 
 /* Step-kernel timer on the bound stream: on = p > 0 clears it and makes every

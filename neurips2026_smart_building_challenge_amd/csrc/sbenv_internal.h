@@ -358,7 +358,8 @@ struct KParams {
     unsigned long long* phase_ts;   // null, or [n_envs * SBK_NSTAMP] wall-clock stamps
     unsigned long long* pass_ts;    // null, or [n_pass + 1] shader-clock stamps of one env
     int pass_ts_env;                // env whose solve passes are stamped
-    int pad_le;
+    int air_stride;                 // doubles per env half of air_trace (the largest k)
+    double* air_trace;              // null, or [n_envs][2][air_stride]: the step's air_g, then air_T
 };
 
 // The host (g++) and the device (hipcc) compile these structs separately and
@@ -373,7 +374,7 @@ static_assert(sizeof(DevLayout) == 888 && offsetof(DevLayout, st) == 88 && offse
               && offsetof(DevLayout, bytes_per_step) == 864, "DevLayout layout");
 static_assert(sizeof(DevScen) == 488 && offsetof(DevScen, img_src) == 32 && offsetof(DevScen, gas_co2) == 200
               && offsetof(DevScen, conv_p) == 464, "DevScen layout");
-static_assert(sizeof(KParams) == 136 && offsetof(KParams, host_env) == 80 && offsetof(KParams, phase_ts) == 112
-              && offsetof(KParams, pass_ts_env) == 128, "KParams layout");
+static_assert(sizeof(KParams) == 144 && offsetof(KParams, host_env) == 80 && offsetof(KParams, phase_ts) == 112
+              && offsetof(KParams, pass_ts_env) == 128 && offsetof(KParams, air_trace) == 136, "KParams layout");
 
 }  // namespace sbk

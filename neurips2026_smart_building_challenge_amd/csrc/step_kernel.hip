@@ -2804,6 +2804,14 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P0) {
         decode_apply<W>(c);
         STAMP(2);
         step_pre<W>(c, P, sy);
+        if (P.air_trace) {
+            // the step's air side as the reference core's state holds it (air_g, air_T)
+            double* at = P.air_trace + (size_t)e * 2 * P.air_stride;
+            for (int col = ln(); col < L->k; col += W) {
+                at[col] = c.g[col];
+                at[P.air_stride + col] = c.tair[col];
+            }
+        }
         STAMP(3);
         step_post<W>(c);             // boiler update: reads the pre-step results, not the field
         env_post(sy + SY_PRE, 1);    // the helper's observation reads the state as of here

@@ -1087,6 +1087,8 @@ struct Vec {
     SbxPolicy pol{};
     float *p_h1 = nullptr, *p_h2 = nullptr, *p_y = nullptr;
     float *p_hlp = nullptr, *p_hent = nullptr;   // per-head log-densities and entropies [n][SB_ACT]
+    double* d_air = nullptr;                     // kwarg trace_air: [n][2][air_stride] each step's air_g, air_T
+    int air_stride = 0;
     double* d_live = nullptr;                    // puf_live_log totals (device: 3 f64, then 3 per scenario)
     double* h_live = nullptr;                    // and their pinned host copy
     std::vector<double> live_prev;               // per scenario: the totals at the previous puf_live_log
@@ -1129,6 +1131,8 @@ sbk::KParams params(Vec* v, int mode) {
     p.n_envs = v->n;
     p.mode = mode;
     p.reward_scale = v->reward_scale;
+    p.air_trace = v->d_air;
+    p.air_stride = v->air_stride;
     return p;
 }
 
@@ -1597,6 +1601,14 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
         hip_ok(hipMemcpy(v->d_ncont, nc.data(), sizeof(int) * n, hipMemcpyHostToDevice), "upload");
         hip_ok(hipMemcpy(v->d_ndisc, nd.data(), sizeof(int) * n, hipMemcpyHostToDevice), "upload");
     }
+    if (kw(kwargs, "trace_air", 0.0f) != 0.0f) {
+        // every step also stores each env's air side, so state snapshots hold it
+        for (const HostLayout& L : v->layouts) v->air_stride = std::max(v->air_stride, L.dev.k);
+        v->air_stride = std::max(v->air_stride, 1);
+        const size_t bytes = sizeof(double) * 2 * (size_t)v->air_stride * n;
+        hip_ok(hipMalloc(&v->d_air, bytes), "hipMalloc(air trace)");
+        hip_ok(hipMemset(v->d_air, 0, bytes), "memset(air trace)");
+    }
     // ---- initial state records: pump head, seeded MT19937 (index 624)
     {
         std::vector<unsigned char> rec(v->state_bytes, 0);
@@ -1764,6 +1776,7 @@ void puf_close(Env* envs) {
     (void)hipFree(v->d_ncont);
     (void)hipFree(v->d_ndisc);
     (void)hipFree(v->d_live);
+    (void)hipFree(v->d_air);
     (void)hipHostFree(v->h_live);
     for (void* p : {(void*)v->d_canon, (void*)v->d_raw, (void*)v->d_native, (void*)v->d_cbase, (void*)v->d_ctrust,
                     (void*)v->d_cpid, (void*)v->d_cinfo})
@@ -1902,7 +1915,16 @@ int sbx_env_state(Env* envs, int i, double* out, int cap) {
     for (int a = 0; a < L.na; a++) o.push_back(f(L.st.sat)[a]);
     for (int a = 0; a < L.na; a++) o.push_back(f(L.st.recirc)[a]);
     for (int a = 0; a < L.na; a++) o.push_back(f(L.st.fan)[a]);
-    for (int c = 0; c < 2 * L.k; c++) o.push_back(NAN);   // air_g / air_T are not kept between steps
+    if (v->d_air) {
+        // the last step's air side (zero before the first step, as in a new reference env)
+        std::vector<double> at(2 * (size_t)v->air_stride);
+        hip_ok(hipMemcpy(at.data(), v->d_air + (size_t)i * at.size(), at.size() * sizeof(double),
+                         hipMemcpyDeviceToHost), "air copy");
+        for (int c = 0; c < L.k; c++) o.push_back(at[c]);
+        for (int c = 0; c < L.k; c++) o.push_back(at[v->air_stride + c]);
+    } else {
+        for (int c = 0; c < 2 * L.k; c++) o.push_back(NAN);   // kept only under trace_air
+    }
     for (int z = 0; z < L.nz; z++) o.push_back((double)s[L.st.occV + z]);
     const double* pf = f(L.st.plant);
     const int* ip = reinterpret_cast<const int*>(s + L.st.iplant);

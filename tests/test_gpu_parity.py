@@ -146,9 +146,13 @@ def obs_close(gpu_row: np.ndarray, twin: Twin, cpu_row: np.ndarray, where: str) 
     assert worst <= 1.0, f"{where}: obs beyond float32 quantization (x{worst:.2f})"
 
 
-def state_close(gs: np.ndarray, cs: np.ndarray, where: str) -> None:
+def state_close(gs: np.ndarray, cs: np.ndarray, where: str, air: bool = False) -> None:
+    """Every state entry within STATE_RTOL; air: the vec keeps the air side
+    (trace_air), so no entry may be missing (NaN)."""
     m = len(cs)
     g = gs[:m]
+    if air:
+        assert not np.isnan(g).any(), f"{where}: air side missing"
     fin = ~np.isnan(g)
     err = np.abs(g[fin] - cs[fin]) / np.maximum(np.abs(cs[fin]), STATE_FLOOR)
     assert err.max() <= STATE_RTOL, f"{where}: state rel err {err.max():.3e} at {np.nonzero(fin)[0][err.argmax()]}"
@@ -183,7 +187,7 @@ def test_gpu_reset_obs_bit_exact(mixed_dir):
     vec.close()
 
 
-def _run_parity(vec, twins, steps, label):
+def _run_parity(vec, twins, steps, label, air=False):
     vec.reset()
     for tw in twins:
         tw.cpu.reset()
@@ -201,7 +205,7 @@ def _run_parity(vec, twins, steps, label):
             gs = vec.state(tw.i)
             cs = tw.cpu.state()
             assert len(cs) == tw.state_len
-            state_close(gs, cs, where)
+            state_close(gs, cs, where, air)
             # decoded commands, occupancy and the boiler ramp carry no physics: exact
             ix = tw.exact_state
             bad = ix[gs[ix] != cs[ix]]
@@ -226,11 +230,12 @@ SOLVERS = ["relax", "point", "lu"]
 
 @pytest.mark.parametrize("solver", SOLVERS)
 def test_gpu_step_parity_mixed_layouts(mixed_dir, solver):
-    """30 scenarios (6 layouts x 5 climates), episodes of 60 steps, 130 steps (two auto-resets)."""
+    """30 scenarios (6 layouts x 5 climates), episodes of 60 steps, 130 steps (two
+    auto-resets); the air side (air_g, air_T) kept and compared too."""
     say(f"parity ({solver}): 30 envs, one per scenario, 130 steps")
-    vec = E.VecEnv(30, blob_dir=str(mixed_dir), groups=30, max_steps=60, solver=solver)
+    vec = E.VecEnv(30, blob_dir=str(mixed_dir), groups=30, max_steps=60, solver=solver, trace_air=1)
     twins = [Twin(vec, i, 60) for i in range(vec.n)]
-    _run_parity(vec, twins, 130, "mixed")
+    _run_parity(vec, twins, 130, "mixed", air=True)
     check_solver(vec, solver)
     vec.close()
 
@@ -240,11 +245,11 @@ def test_gpu_step_parity_start_offsets(mixed_dir, solver):
     """Desynchronised calendar starts (start_offsets): every env at its own seeded offset."""
     say(f"parity ({solver}): 60 envs, start offsets, 90 steps")
     vec = E.VecEnv(60, blob_dir=str(mixed_dir), groups=30, max_steps=40, start_offsets=1, start_seed=99,
-                   solver=solver)
+                   solver=solver, trace_air=1)
     starts = {vec.meta(i)[1] for i in range(vec.n)}
     assert len(starts) > 40
     twins = [Twin(vec, i, 40) for i in range(0, vec.n, 3)]
-    _run_parity(vec, twins, 90, "start offsets")
+    _run_parity(vec, twins, 90, "start offsets", air=True)
     vec.close()
 
 
