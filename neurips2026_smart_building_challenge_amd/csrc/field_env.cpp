@@ -425,6 +425,7 @@ FieldScen* field_open(const sbh::Blob& b, std::string* err) {
     f.c.hour_m1_rows = (int)std::min(cm1, cw1);
     f.c.occ_seed = b.i64_1("occ_seed", 17321);
     f.c.nz = nz;
+    f.c.n_obs = n_dev + n_aux;
     sbe::StateLayout& S = f.st;
     int o = 0;
     auto f64a = [&](int count) { const int r = o; o += 8 * std::max(count, 1); return r; };

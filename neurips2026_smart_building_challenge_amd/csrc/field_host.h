@@ -21,6 +21,7 @@ struct FieldCounts {
     int64_t occ_seed;
     int64_t conv_seed;      // the convection stream's seed (env j of the scenario: + j, as the occupancy one)
     int n_cvs, n_solved, nz;
+    int n_obs;              // observation prefix (n_dev + n_aux floats)
 };
 
 // A blob the RC step kernel cannot hold: more solved cells than its LDS plans

@@ -38,46 +38,56 @@ constexpr int kActWidth = 272;
 
 // C[M x N] = act(A[M x K] B[K x N] + bias) with K = KW * (blockDim.x / 64):
 // wavefront w takes K range [w KW, (w + 1) KW) and issues every load of that
-// range before its first MFMA (one memory latency per tile). lda / ldc in
-// floats; N a multiple of 16. ACT: 0 identity, 1 tanh.
+// range before its first MFMA (one memory latency per tile). Columns of A at
+// kmax and beyond are zero (an observation row's tail), so a wavefront skips
+// its 16-wide K blocks that start there: their products add exactly nothing,
+// and the fixed K partition keeps every result independent of kmax. lda / ldc
+// in floats; N a multiple of 16. ACT: 0 identity, 1 tanh.
 template <int ACT, int KW>
-__global__ __launch_bounds__(256) void mlp_layer_kernel(const float* __restrict__ A, int lda,
+__global__ __launch_bounds__(512) void mlp_layer_kernel(const float* __restrict__ A, int lda,
                                                         const float* __restrict__ B,
                                                         const float* __restrict__ bias, float* __restrict__ C,
-                                                        int ldc, int M, int N) {
+                                                        int ldc, int M, int N, int kmax) {
     static_assert(KW % 16 == 0, "K per wavefront is a multiple of 16");
     constexpr int NB = KW / 16;
-    __shared__ v4f part[4][64];
+    __shared__ v4f part[8][64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, ksplit = blockDim.x >> 6;
     const int m0 = blockIdx.x * 16, n0 = blockIdx.y * 16;
     const int g = lane >> 4, i = lane & 15;
     const int m = m0 + i;
     const int mc = m < M ? m : M - 1;   // rows past M read row M - 1; their outputs are dropped
+    const int nb = min(NB, max(0, (kmax - w * KW + 15) / 16));   // wave-uniform
     const float* a_row = A + (size_t)mc * lda + w * KW + 4 * g;
     const float* b_col = B + (size_t)(w * KW + 4 * g) * N + n0 + i;
     float4 a[NB];
     float b[NB][4];
 #pragma unroll
     for (int j = 0; j < NB; j++) {
-        a[j] = *reinterpret_cast<const float4*>(a_row + 16 * j);
-        const float* bp = b_col + (size_t)(16 * j) * N;
+        if (j < nb) {
+            a[j] = *reinterpret_cast<const float4*>(a_row + 16 * j);
+            const float* bp = b_col + (size_t)(16 * j) * N;
 #pragma unroll
-        for (int s = 0; s < 4; s++) b[j][s] = bp[s * N];
+            for (int s = 0; s < 4; s++) b[j][s] = bp[s * N];
+        }
     }
     // the empty asm "uses" every loaded register here, so the compiler keeps
     // all loads ahead of the first MFMA instead of sinking each to its use
 #pragma unroll
     for (int j = 0; j < NB; j++) {
-        asm volatile("" : "+v"(a[j].x), "+v"(a[j].y), "+v"(a[j].z), "+v"(a[j].w));
-        asm volatile("" : "+v"(b[j][0]), "+v"(b[j][1]), "+v"(b[j][2]), "+v"(b[j][3]));
+        if (j < nb) {
+            asm volatile("" : "+v"(a[j].x), "+v"(a[j].y), "+v"(a[j].z), "+v"(a[j].w));
+            asm volatile("" : "+v"(b[j][0]), "+v"(b[j][1]), "+v"(b[j][2]), "+v"(b[j][3]));
+        }
     }
     v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < NB; j++) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].x, b[j][0], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].y, b[j][1], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].z, b[j][2], acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].w, b[j][3], acc, 0, 0, 0);
+        if (j < nb) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].x, b[j][0], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].y, b[j][1], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].z, b[j][2], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j].w, b[j][3], acc, 0, 0, 0);
+        }
     }
     if (ksplit > 1) {
         part[w][lane] = acc;
@@ -394,21 +404,25 @@ __global__ __launch_bounds__(320) void ppo_beta_kernel(const float* __restrict__
 
 // ---------------------------------------------------------------- launchers
 // obs [n x 1024] -> h1, h2 [n x 128] -> y [n x 544] -> actions [n x 272], on stream s.
+// obs_cols: every observation row is zero from this column on (the longest
+// observation prefix of the vec's envs).
 // With draws set, also the rollout buffer's draws, per-head log-densities and
 // entropies (hlp, hent [n x 272]) and their per-env sums (logp, entropy [n]).
 extern "C" int sbk_launch_policy(const float* obs, const float* w1, const float* b1, const float* w2,
                                  const float* b2, const float* w3, const float* b3, float* h1, float* h2, float* y,
                                  float* actions, const int* n_cont, const int* n_disc, int n, uint64_t seed,
                                  uint32_t step, float* draws, float* hlp, float* hent, float* logp, float* entropy,
-                                 float floor, hipStream_t s) {
+                                 float floor, int obs_cols, hipStream_t s) {
     using namespace sbk;
     if (n <= 0) return (int)hipErrorInvalidValue;
+    if (obs_cols < 1 || obs_cols > kObsWidth) return (int)hipErrorInvalidValue;
     const int mt = (n + 15) / 16;
-    // K split over 4 wavefronts (layer 1, K = 1024) or 2 (K = 128)
-    hipLaunchKernelGGL((mlp_layer_kernel<1, kObsWidth / 4>), dim3(mt, kPolicyHidden / 16), dim3(256), 0, s, obs,
-                       kObsWidth, w1, b1, h1, kPolicyHidden, n, kPolicyHidden);
+    // K split over 8 wavefronts (layer 1, K = 1024; the observation's zero
+    // tail past obs_cols skipped) or 2 (K = 128)
+    hipLaunchKernelGGL((mlp_layer_kernel<1, kObsWidth / 8>), dim3(mt, kPolicyHidden / 16), dim3(512), 0, s, obs,
+                       kObsWidth, w1, b1, h1, kPolicyHidden, n, kPolicyHidden, obs_cols);
     hipLaunchKernelGGL((mlp_layer_kernel<1, kPolicyHidden / 2>), dim3(mt, kPolicyHidden / 16), dim3(128), 0, s, h1,
-                       kPolicyHidden, w2, b2, h2, kPolicyHidden, n, kPolicyHidden);
+                       kPolicyHidden, w2, b2, h2, kPolicyHidden, n, kPolicyHidden, kPolicyHidden);
     // third layer and the Beta draws in one launch per (env tile, head group)
     hipLaunchKernelGGL(heads_layer_kernel, dim3(mt, kHeadGroups), dim3(256), 0, s, h2, w3, b3, y, actions, n_cont,
                        n_disc, n, seed, step, draws, hlp, hent, floor);
@@ -486,7 +500,7 @@ extern "C" int sbk_noalloc_max_envs(void) { return kNoAllocEnvs; }
 extern "C" int sbk_launch_policy_noalloc(const float* obs, const float* w1, const float* b1, const float* w2,
                                          const float* b2, const float* w3, const float* b3, float* actions,
                                          const int* n_cont, const int* n_disc, int n, uint64_t seed, uint32_t step,
-                                         float floor, hipStream_t s) {
+                                         float floor, int obs_cols, hipStream_t s) {
     if (n <= 0 || n > kNoAllocEnvs) return (int)hipErrorInvalidValue;
     float* base = nullptr;
     const int rc = scratch_of_device(&base);
@@ -495,5 +509,5 @@ extern "C" int sbk_launch_policy_noalloc(const float* obs, const float* w1, cons
     float* h2 = h1 + (size_t)kNoAllocEnvs * sbk::kPolicyHidden;
     float* y = h2 + (size_t)kNoAllocEnvs * sbk::kPolicyHidden;
     return sbk_launch_policy(obs, w1, b1, w2, b2, w3, b3, h1, h2, y, actions, n_cont, n_disc, n, seed, step,
-                             nullptr, nullptr, nullptr, nullptr, nullptr, floor, s);
+                             nullptr, nullptr, nullptr, nullptr, nullptr, floor, obs_cols, s);
 }

@@ -38,7 +38,7 @@ extern "C" int sbk_launch_policy(const float* obs, const float* w1, const float*
                                  const float* b2, const float* w3, const float* b3, float* h1, float* h2, float* y,
                                  float* actions, const int* n_cont, const int* n_disc, int n, uint64_t seed,
                                  uint32_t step, float* draws, float* hlp, float* hent, float* logp, float* entropy,
-                                 float floor, hipStream_t s);
+                                 float floor, int obs_cols, hipStream_t s);
 extern "C" int sbk_launch_beta_eval(const float* y, const float* draws, const int* n_cont, const int* n_disc, int n,
                                     float* hlp, float* hent, float* grad, float* logp, float* entropy, float floor,
                                     hipStream_t s);
@@ -51,7 +51,7 @@ extern "C" int sbk_noalloc_max_envs(void);
 extern "C" int sbk_launch_policy_noalloc(const float* obs, const float* w1, const float* b1, const float* w2,
                                          const float* b2, const float* w3, const float* b3, float* actions,
                                          const int* n_cont, const int* n_disc, int n, uint64_t seed, uint32_t step,
-                                         float floor, hipStream_t s);
+                                         float floor, int obs_cols, hipStream_t s);
 extern "C" int sbk_launch_canon(const sbk::CanonArgs* a, int post, hipStream_t s);
 extern "C" int sbk_launch_live_sums(const sbk::EnvDesc* envs, const sbk::DevLayout* layouts,
                                     const unsigned char* state, int n, int n_scen, double* out, hipStream_t s);
@@ -1087,6 +1087,7 @@ struct Vec {
     SbxPolicy pol{};
     float *p_h1 = nullptr, *p_h2 = nullptr, *p_y = nullptr;
     float *p_hlp = nullptr, *p_hent = nullptr;   // per-head log-densities and entropies [n][SB_ACT]
+    int obs_cols = SB_OBS;                       // observation rows are zero from this column on (every env)
     double* d_air = nullptr;                     // kwarg trace_air: [n][2][air_stride] each step's air_g, air_T
     int air_stride = 0;
     double* d_live = nullptr;                    // puf_live_log totals (device: 3 f64, then 3 per scenario)
@@ -1582,6 +1583,14 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
     hip_ok(hipMemcpy(v->d_layouts, dl.data(), sizeof(sbk::DevLayout) * dl.size(), hipMemcpyHostToDevice), "upload");
     hip_ok(hipMalloc(&v->d_scens, sizeof(sbk::DevScen) * ds.size()), "hipMalloc(scens)");
     hip_ok(hipMemcpy(v->d_scens, ds.data(), sizeof(sbk::DevScen) * ds.size(), hipMemcpyHostToDevice), "upload");
+    // the longest observation prefix: the shared policy's first layer skips the zero tail past it
+    v->obs_cols = 1;
+    for (int i = 0; i < n; i++) {
+        const int w = v->canonical ? SB_OBS
+                      : v->field_of[i] >= 0 ? field_counts(v->fields[v->field_of[i]]).n_obs
+                                            : v->layouts[v->desc[i].layout].dev.n_dev + v->layouts[v->desc[i].layout].dev.n_aux;
+        v->obs_cols = std::max(v->obs_cols, std::min(w, SB_OBS));
+    }
     hip_ok(hipMalloc(&v->d_envs, sizeof(sbk::EnvDesc) * n), "hipMalloc(envs)");
     hip_ok(hipMemcpy(v->d_envs, v->desc.data(), sizeof(sbk::EnvDesc) * n, hipMemcpyHostToDevice), "upload");
     hip_ok(hipMalloc(&v->d_order, sizeof(int) * std::max(n_rc, 1)), "hipMalloc(order)");
@@ -2105,7 +2114,7 @@ int sbx_policy_act(Env* envs, uint64_t seed, uint32_t step) {
     const SbxPolicy& p = v->pol;
     int rc = sbk_launch_policy(v->obs, p.w1, p.b1, p.w2, p.b2, p.w3, p.b3, v->p_h1, v->p_h2, v->p_y, v->actions,
                                v->d_ncont, v->d_ndisc, v->n, seed, step, nullptr, nullptr, nullptr, nullptr, nullptr,
-                               p.beta_floor, g_stream);
+                               p.beta_floor, v->obs_cols, g_stream);
     if (rc != 0) die(std::string("policy launch failed: ") + hipGetErrorString((hipError_t)rc));
     return 0;
 }
@@ -2119,7 +2128,7 @@ int sbx_policy_act_noalloc(Env* envs, const SbxPolicy* p, uint64_t seed, uint32_
         return -1;
     }
     int rc = sbk_launch_policy_noalloc(v->obs, p->w1, p->b1, p->w2, p->b2, p->w3, p->b3, v->actions, v->d_ncont,
-                                       v->d_ndisc, v->n, seed, step, p->beta_floor, g_stream);
+                                       v->d_ndisc, v->n, seed, step, p->beta_floor, v->obs_cols, g_stream);
     if (rc != 0) {
         g_err = std::string("sbx_policy_act_noalloc: ") + hipGetErrorString((hipError_t)rc);
         return -1;
@@ -2134,7 +2143,7 @@ int sbx_policy_act_logp(Env* envs, uint64_t seed, uint32_t step, float* draws, f
     const SbxPolicy& p = v->pol;
     int rc = sbk_launch_policy(v->obs, p.w1, p.b1, p.w2, p.b2, p.w3, p.b3, v->p_h1, v->p_h2, v->p_y, v->actions,
                                v->d_ncont, v->d_ndisc, v->n, seed, step, draws, v->p_hlp, v->p_hent, logp, entropy,
-                               p.beta_floor, g_stream);
+                               p.beta_floor, v->obs_cols, g_stream);
     if (rc != 0) die(std::string("policy launch failed: ") + hipGetErrorString((hipError_t)rc));
     return 0;
 }
