@@ -1175,9 +1175,10 @@ void launch_canon(Vec* v, int post, int reset, const float* actions) {
     if (rc != 0) die(std::string("canonical kernel launch failed: ") + hipGetErrorString((hipError_t)rc));
 }
 
-// One step or reset of every env: in canonical mode the step kernel reads the
-// native action rows the pre kernel decoded and writes the env's own
-// observation rows, from which the post kernel makes the canonical ones.
+// One step or reset of every env: in canonical mode the step kernels (RC
+// tiles and field scenarios) read the native action rows the pre kernel
+// decoded and write the envs' own observation rows, from which the post
+// kernel then makes the canonical ones.
 void run_env(Vec* v, sbk::KParams p, const float* actions) {
     const bool reset = p.mode == sbk::KMODE_RESET;
     if (v->canonical) {
@@ -1188,13 +1189,13 @@ void run_env(Vec* v, sbk::KParams p, const float* actions) {
         p.actions = actions;
     }
     launch_params(v, p);
-    if (v->canonical) launch_canon(v, 1, reset ? 1 : 0, nullptr);
     if (!v->fields.empty()) {
         FieldIo io{p.actions, p.obs, p.rewards, p.terminals, p.host_env, p.env_stride, p.log_offset, p.reward_scale};
         std::string err;
         for (FieldScen* f : v->fields)
             if (!field_step(f, io, reset, g_stream, &err)) die("field scenario step: " + err);
     }
+    if (v->canonical) launch_canon(v, 1, reset ? 1 : 0, nullptr);
 }
 
 void launch(Vec* v, int mode) { run_env(v, params(v, mode), nullptr); }
@@ -1377,13 +1378,17 @@ Env* puf_vec_create(int n, Dict* kwargs, obs_t* observations, float* actions, fl
         if (!b.open(files[i], &err)) die(err);
         if (field_blob(b)) {
             // FDM-scale field: HVAC lanes around the field group's solve
-            if (v->canonical) die(files[i] + ": the canonical interface is not supported for field scenarios");
             FieldScen* F = field_open(b, &err);
             if (!F) die(files[i] + ": " + err);
             const FieldCounts fc = field_counts(F);
             HostLayout H;
             H.key = "field:" + files[i];
             H.field = (int)v->fields.size();
+            if (v->canonical) {
+                // the canonical maps read only the blob's observation map and topology
+                H.canon = std::make_unique<sbk::CanonTab>();
+                if (!make_canon(b, H.canon.get(), &err)) die(files[i] + ": canonical layout: " + err);
+            }
             H.dev.n_act = fc.n_act;
             H.dev.n_cont = fc.n_cont;
             H.dev.n_disc = fc.n_disc;

@@ -60,24 +60,14 @@ def _state_close(g, c, where):
     assert err.max() <= 1e-9, f"{where}: state rel err {err.max():.3e}"
 
 
-@pytest.mark.parametrize("mode", ["residual_guard", "residual", "absolute"])
-def test_gpu_canonical_matches_oracle(canon_dir, mode):
-    kw = dict(canonical=1, max_steps=40)
-    guard = None
-    if mode.startswith("residual"):
-        kw.update(residual=1, res_scale=0.5, res_dscale=1.5)
-    if mode == "residual_guard":
-        kw.update(guard_d0=0.5, guard_d1=1.5, guard_hot=1)
-        guard = (0.5, 1.5, 1)
-    resid = 1 if mode.startswith("residual") else 0
-    say(f"canonical ({mode}): 9 envs, 90 steps")
-    vec = E.VecEnv(9, blob_dir=str(canon_dir), groups=3, **kw)
-    assert all(vec.envs[i].n_cont == po.CN_ACT and vec.envs[i].n_disc == 0 for i in range(vec.n))
+def _run_canonical(vec, twins_of, guard, resid, steps, max_steps, tag):
+    """Steps vec with generated canonical action rows and checks every env
+    against its oracle twin and the oracle's canonical layout every step."""
     twins = []
     for i in range(vec.n):
         path, start, seed = vec.meta(i)
-        twins.append({"env": po.CpuEnv("oracle", path, seed, start=start, max_steps=40), "canon": po.Canon(path),
-                      "pid": np.zeros(18, np.float64)})
+        twins.append({"env": po.CpuEnv("oracle", path, seed, start=start, max_steps=max_steps),
+                      "canon": po.Canon(path), "pid": np.zeros(18, np.float64)})
     vec.reset()
     for t in twins:
         t["env"].reset()
@@ -100,8 +90,9 @@ def test_gpu_canonical_matches_oracle(canon_dir, mode):
             t["base"] = base
             t["raw"] = raw[:n_obs]
 
-    check_observation("reset", [True] * vec.n)
-    for s in range(90):
+    check_observation(f"{tag} reset", [True] * vec.n)
+    ends = 0
+    for s in range(steps):
         vec.gen_actions(SEED, s)
         prow = vec.actions.cpu().numpy()
         vec.step()
@@ -113,10 +104,51 @@ def test_gpu_canonical_matches_oracle(canon_dir, mode):
             trust = c.trust(t["raw"], *guard) if guard else None
             row = c.decode(t["base"], prow[i, :po.CN_ACT], trust, resid, 0.5, 1.5)
             _, r, tt, _ = t["env"].step(row)
-            assert tt == term[i], (s, i)
-            assert abs(float(rew[i]) - r) <= 2 * np.spacing(np.float32(abs(r))) + 1e-12, (s, i)
-            _state_close(vec.state(i), t["env"].state(), f"{mode} step {s} env {i}")
-        check_observation(f"{mode} step {s}", [bool(x) for x in term])
+            assert tt == term[i], (tag, s, i)
+            ends += int(tt)
+            assert abs(float(rew[i]) - r) <= 2 * np.spacing(np.float32(abs(r))) + 1e-12, (tag, s, i)
+            _state_close(vec.state(i), t["env"].state(), f"{tag} step {s} env {i}")
+        check_observation(f"{tag} step {s}", [bool(x) for x in term])
+    return ends
+
+
+@pytest.mark.parametrize("mode", ["residual_guard", "residual", "absolute"])
+def test_gpu_canonical_matches_oracle(canon_dir, mode):
+    kw = dict(canonical=1, max_steps=40)
+    guard = None
+    if mode.startswith("residual"):
+        kw.update(residual=1, res_scale=0.5, res_dscale=1.5)
+    if mode == "residual_guard":
+        kw.update(guard_d0=0.5, guard_d1=1.5, guard_hot=1)
+        guard = (0.5, 1.5, 1)
+    resid = 1 if mode.startswith("residual") else 0
+    say(f"canonical ({mode}): 9 envs, 90 steps")
+    vec = E.VecEnv(9, blob_dir=str(canon_dir), groups=3, **kw)
+    assert all(vec.envs[i].n_cont == po.CN_ACT and vec.envs[i].n_disc == 0 for i in range(vec.n))
+    _run_canonical(vec, None, guard, resid, 90, 40, mode)
+    vec.close()
+
+
+def test_gpu_canonical_field_scenario(tmp_path):
+    """The canonical interface on an FDM-scale field scenario (7 rooms on 2 air
+    handlers, the shipped convection) beside an RC layout in one vec, exact
+    field mode: base, PID state and canonical observation bit-exact every step,
+    the oracle env stepped with the oracle-decoded rows within the state
+    tolerance, through auto-resets (residual, comfort guard on)."""
+    from neurips2026_smart_building_challenge_amd.scenario import fdm as F
+
+    d = tmp_path / "mix"
+    d.mkdir()
+    spec = G.FieldEnvSpec(F.FdmSpec(rows=120, cols=90, rooms=7, margin=6, seed=3), 2)
+    (d / "field7.sbb").write_bytes(G.field_env_writer(spec, G.climates()[1], G.EPISODE_STEPS + 256, 17321,
+                                                      G.ConvSpec(0.1, 2, 5)).tobytes())
+    G.write_scenarios([(G.LayoutSpec(36, 4), G.ClimateSpec(2.0, 7.0, seed=611))], d)
+    say("canonical on a field scenario + an RC layout: 4 envs, 45 steps")
+    vec = E.VecEnv(4, blob_dir=str(d), groups=2, canonical=1, residual=1, res_scale=0.5, res_dscale=1.5,
+                   guard_d0=0.5, guard_d1=1.5, guard_hot=1, max_steps=20, field_exact=1)
+    assert sum(1 for i in range(vec.n) if "field7" in vec.meta(i)[0]) == 2
+    ends = _run_canonical(vec, None, (0.5, 1.5, 1), 1, 45, 20, "field")
+    assert ends == 2 * vec.n
     vec.close()
 
 
