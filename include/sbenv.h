@@ -42,7 +42,16 @@ extern "C" {
 #endif
 
 #define SB_OBS 1024
+/* Action row: SB_CONT continuous heads, then SB_DISC discrete ones. Built with
+ * -DSB_CONT_BIG (libsbenv_big.so) the row holds 320 continuous heads, for
+ * buildings with more than 256 continuous actions, as the reference GPU env
+ * built with SB_CONT_BIG (complete_port/gpu/smart_buildings.cu:35-61); a
+ * trainer compiled against one layout links the matching library. */
+#ifdef SB_CONT_BIG
+#define SB_CONT 320
+#else
 #define SB_CONT 256
+#endif
 #define SB_DISC 16
 #define SB_ACT (SB_CONT + SB_DISC)
 #define SB_MASK_WIDTH (SB_CONT + 2 * SB_DISC)
@@ -261,7 +270,7 @@ int sbx_solve_info(Env* envs, int i, double* out);
  * launches on the bound stream and allocates nothing. sbx_policy_heads copies
  * y of the last sbx_policy_act to host (synchronous). Return 0 / count, or -1. */
 #define SBX_POLICY_HIDDEN 128
-#define SBX_POLICY_HEADS 544
+#define SBX_POLICY_HEADS (2 * SB_ACT)
 typedef struct SbxPolicy {
     const float* w1;
     const float* b1;
@@ -489,6 +498,10 @@ int sbx_fdm_lu_solve(SbxFdm* f, const double* b, double* x, int n_rhs);
 /* Message of the last failing sbx_* call. */
 const char* sbx_last_error(void);
 const char* sbx_version(void);
+/* SB_CONT of this build (256, or 320 for libsbenv_big.so), so a binding can
+ * check it loaded the library its action rows are laid out for. No
+ * counterpart in the reference, whose layout is fixed at compile time. */
+int sbx_cont_width(void);
 
 #ifdef __cplusplus
 }

@@ -4,7 +4,9 @@
 
 Outputs, in-tree so they travel with the repository snapshot:
     neurips2026_smart_building_challenge_amd/libsbenv.so   product (HIP + C ABI)
-    oracle/liboracle.so                                    C restatement (tests)
+    neurips2026_smart_building_challenge_amd/libsbenv_big.so   the same with SB_CONT_BIG
+                                                           (320 continuous action heads)
+    oracle/liboracle.so, liboracle_big.so                  C restatement (tests)
     oracle/_ref/libcsim_ref.so                             reference csim (tests,
                                                            only where /root/reference exists)
 """
@@ -21,6 +23,7 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libsbenv.so"
+LIB_BIG = PKG / "libsbenv_big.so"   # SB_CONT_BIG: 320 continuous action heads
 ARCH = os.environ.get("SBENV_ARCH", "gfx950")
 REF_CSIM = Path("/root/reference/complete_port/csim")
 
@@ -48,28 +51,34 @@ def _run(cmd: list[str], cwd: Path | None = None) -> None:
 
 
 def build_product() -> Path:
+    """Both libraries: libsbenv.so (256 + 16 action heads) and libsbenv_big.so
+    (-DSB_CONT_BIG: 320 + 16, the reference GPU env's SB_CONT_BIG layout)."""
     hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
-    tmp = PKG / "_build"
-    tmp.mkdir(exist_ok=True)
     inc = ["-I", str(ROOT / "include"), "-I", str(CSRC)]
     rocm = Path(hipcc).resolve().parent.parent
-    jobs = []   # (command, object): every translation unit compiles independently
-    for src in HIP_SOURCES:
-        o = tmp / (Path(src).stem + ".o")
-        jobs.append(([hipcc, *HIP_FLAGS, *EXTRA.get(src, []), *inc, "-c", str(CSRC / src), "-o", str(o)], o))
-    for src in HOST_SOURCES:
-        # host-only C++ (HIP runtime API calls, no device code)
-        o = tmp / (Path(src).stem + ".o")
-        jobs.append((["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__",
-                      "-I", str(rocm / "include"), *inc, "-c", str(CSRC / src), "-o", str(o)], o))
+    jobs, links = [], []   # (command, object): every translation unit compiles independently
+    for lib, tmp, defs in ((LIB, PKG / "_build", []), (LIB_BIG, PKG / "_build_big", ["-DSB_CONT_BIG"])):
+        tmp.mkdir(exist_ok=True)
+        objs = []
+        for src in HIP_SOURCES:
+            o = tmp / (Path(src).stem + ".o")
+            jobs.append([hipcc, *HIP_FLAGS, *EXTRA.get(src, []), *defs, *inc, "-c", str(CSRC / src), "-o", str(o)])
+            objs.append(o)
+        for src in HOST_SOURCES:
+            # host-only C++ (HIP runtime API calls, no device code)
+            o = tmp / (Path(src).stem + ".o")
+            jobs.append(["g++", "-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__", *defs,
+                         "-I", str(rocm / "include"), *inc, "-c", str(CSRC / src), "-o", str(o)])
+            objs.append(o)
+        links.append((lib, objs))
     workers = max(1, min(len(jobs), os.cpu_count() or 1, 8))
     with ThreadPoolExecutor(max_workers=workers) as pool:
-        for f in [pool.submit(_run, cmd) for cmd, _ in jobs]:
+        for f in [pool.submit(_run, cmd) for cmd in jobs]:
             f.result()
-    objs = [o for _, o in jobs]
-    out_tmp = LIB.with_suffix(".so.tmp")
-    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(out_tmp)])
-    out_tmp.replace(LIB)
+    for lib, objs in links:
+        out_tmp = lib.with_suffix(".so.tmp")
+        _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(out_tmp)])
+        out_tmp.replace(lib)
     return LIB
 
 

@@ -193,7 +193,7 @@ struct Args {
     const Slot* slots;            // [G]
     int G;
     int mode;
-    // the trainer's buffers (rows of 1024 / 272 floats)
+    // the trainer's buffers (rows of SB_OBS / SB_ACT floats)
     const float* actions;
     float* obs;
     float* rewards;

@@ -4,7 +4,7 @@
 //
 //   h1 = tanh(obs W1 + b1)   [n x 1024] x [1024 x 128]
 //   h2 = tanh(h1 W2 + b2)    [n x 128]  x [128 x 128]
-//   y  = h2 W3 + b3          [n x 128]  x [128 x 544] = (u[256], v[256], ud[16], vd[16])
+//   y  = h2 W3 + b3          [n x 128]  x [128 x 2 SB_ACT] = (u[SB_CONT], v[SB_CONT], ud[16], vd[16])
 //
 // and each action head j draws x ~ Beta(softplus(u_j) + f, softplus(v_j) + f)
 // (f the policy's shape floor, 1 by default);
@@ -26,15 +26,23 @@
 
 #include "sb_betamath.h"
 #include "sb_philox.h"
+#include "sbenv.h"
 
 namespace sbk {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int kPolicyHidden = 128;
-constexpr int kPolicyHeads = 2 * 256 + 2 * 16;   // u, v of the continuous and the discrete heads
+constexpr int kPolicyHeads = 2 * SB_ACT;   // u, v of the continuous and the discrete heads
 constexpr int kObsWidth = 1024;
-constexpr int kActWidth = 272;
+constexpr int kActWidth = SB_ACT;
+static_assert(SB_CONT % 16 == 0 && SB_DISC == 16, "head groups of 16: the continuous block, then one discrete group");
+// y column of head h's u (which 0) or v (which 1): continuous heads h < SB_CONT
+// at h and SB_CONT + h, discrete head d = h - SB_CONT at 2 SB_CONT + d and
+// 2 SB_CONT + SB_DISC + d
+__device__ __forceinline__ int head_col(int h, int which) {
+    return h < SB_CONT ? h + SB_CONT * which : 2 * SB_CONT + SB_DISC * which + (h - SB_CONT);
+}
 
 // C[M x N] = act(A[M x K] B[K x N] + bias) with K = KW * (blockDim.x / 64):
 // wavefront w takes K range [w KW, (w + 1) KW) and issues every load of that
@@ -175,7 +183,7 @@ __global__ __launch_bounds__(256) void heads_layer_kernel(const float* __restric
     const int m0 = blockIdx.x * 16, q = blockIdx.y;
     if (w < 2) {
         const int which = w;
-        const int n0 = q < 16 ? 16 * q + 256 * which : 512 + 16 * which;
+        const int n0 = head_col(16 * q, which);
         const int mc = m0 + i < n ? m0 + i : n - 1;
         const float* a_row = h2 + (size_t)mc * H + 4 * g;
         const float* b_col = w3 + (size_t)(4 * g) * kPolicyHeads + n0 + i;
@@ -220,7 +228,7 @@ __global__ __launch_bounds__(256) void heads_layer_kernel(const float* __restric
         const int h = 16 * q + k;
         const bool live = e < n;
         const int ec = live ? e : n - 1;
-        const bool used = live && (h < 256 ? h < n_cont[ec] : h - 256 < n_disc[ec]);
+        const bool used = live && (h < SB_CONT ? h < n_cont[ec] : h - SB_CONT < n_disc[ec]);
         float gm = 1.0f;
         if (used) {
             const float a = beta_shape(ys[row][16 * which + k], floor);
@@ -232,7 +240,7 @@ __global__ __launch_bounds__(256) void heads_layer_kernel(const float* __restric
             float v = 0.0f, x = 0.0f;
             if (used) {
                 x = gm / (gm + other);
-                v = h < 256 ? 2.0f * x - 1.0f : (x > 0.5f ? 1.0f : 0.0f);
+                v = h < SB_CONT ? 2.0f * x - 1.0f : (x > 0.5f ? 1.0f : 0.0f);
             }
             actions[(size_t)e * kActWidth + h] = v;
             if (draws) {
@@ -253,8 +261,7 @@ __global__ __launch_bounds__(256) void heads_layer_kernel(const float* __restric
 
 // Rollout-buffer evaluation of given draws (complete_port/patches/
 // pufferlib_core.diff:944-1000): thread (e, h) takes head h of env e, u and v
-// from y (continuous head h: columns h and 256 + h; discrete head d = h - 256:
-// columns 512 + d and 528 + d) and its draw x; writes the head's log-density,
+// from y (head_col) and its draw x; writes the head's log-density,
 // entropy and grad[e][k][h] (k: d logp/du, d logp/dv, d H/du, d H/dv), zeros
 // past the env's head counts.
 __global__ void beta_eval_kernel(const float* __restrict__ y, const float* __restrict__ draws,
@@ -263,13 +270,13 @@ __global__ void beta_eval_kernel(const float* __restrict__ y, const float* __res
                                  float floor) {
     const int e = blockIdx.x, h = threadIdx.x;
     if (e >= n || h >= kActWidth) return;
-    const bool used = h < 256 ? h < n_cont[e] : h - 256 < n_disc[e];
+    const bool used = h < SB_CONT ? h < n_cont[e] : h - SB_CONT < n_disc[e];
     const size_t o = (size_t)e * kActWidth + h;
     float lp = 0.0f, en = 0.0f, g[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (used) {
         const float* ye = y + (size_t)e * kPolicyHeads;
-        const float u = h < 256 ? ye[h] : ye[512 + (h - 256)];
-        const float v = h < 256 ? ye[256 + h] : ye[528 + (h - 256)];
+        const float u = ye[head_col(h, 0)];
+        const float v = ye[head_col(h, 1)];
         const BetaHead bh = beta_head(u, v, draws[o], floor);
         lp = (float)bh.logp;
         en = (float)bh.entropy;
@@ -317,6 +324,9 @@ __global__ void beta_sample_kernel(const float* alpha, const float* beta, float*
     out[i] = ga / (ga + gb);
 }
 
+constexpr int kPpoThreads = (kActWidth + 63) / 64 * 64;   // one thread per head
+static_assert(kPpoThreads <= 512, "the PPO reduction sums 512 slots");
+
 // The PPO side of the Beta heads for one minibatch row per env
 // (complete_port/patches/pufferlib_core.diff:1205-1252 ppo loss and its
 // ratio_per_dim, :539-543, :1008-1014 beta_kl): one workgroup per env, thread h takes
@@ -330,7 +340,7 @@ __global__ void beta_sample_kernel(const float* alpha, const float* beta, float*
 // clipped term is the larger and r lies outside the clip range; the per-dim
 // scale s cancels the 1/D of the ratio. out[e][0..5] = logp, H, KL, r, pg, lr;
 // grad[e][0][h] = d / du, grad[e][1][h] = d / dv (0 for unused heads).
-__global__ __launch_bounds__(320) void ppo_beta_kernel(const float* __restrict__ y_new, const float* __restrict__ y_old,
+__global__ __launch_bounds__(kPpoThreads) void ppo_beta_kernel(const float* __restrict__ y_new, const float* __restrict__ y_old,
                                                        const float* __restrict__ draws,
                                                        const float* __restrict__ logp_old, const float* __restrict__ adv,
                                                        const int* __restrict__ n_cont, const int* __restrict__ n_disc,
@@ -342,13 +352,13 @@ __global__ __launch_bounds__(320) void ppo_beta_kernel(const float* __restrict__
     if (e >= n) return;
     const int nc = n_cont[e], nd = n_disc[e];
     const int h = t;
-    const bool used = h < kActWidth && (h < 256 ? h < nc : h - 256 < nd);
+    const bool used = h < kActWidth && (h < SB_CONT ? h < nc : h - SB_CONT < nd);
     double lp = 0.0, en = 0.0, kl = 0.0;
     double g[4] = {0.0, 0.0, 0.0, 0.0};
     if (used) {
         const float* yn = y_new + (size_t)e * kPolicyHeads;
         const float* yo = y_old + (size_t)e * kPolicyHeads;
-        const int cu = h < 256 ? h : 512 + (h - 256), cv = h < 256 ? 256 + h : 528 + (h - 256);
+        const int cu = head_col(h, 0), cv = head_col(h, 1);
         const BetaHead bh = beta_head(yn[cu], yn[cv], draws[(size_t)e * kActWidth + h], floor);
         lp = bh.logp;
         en = bh.entropy;
@@ -403,11 +413,11 @@ __global__ __launch_bounds__(320) void ppo_beta_kernel(const float* __restrict__
 }  // namespace sbk
 
 // ---------------------------------------------------------------- launchers
-// obs [n x 1024] -> h1, h2 [n x 128] -> y [n x 544] -> actions [n x 272], on stream s.
+// obs [n x 1024] -> h1, h2 [n x 128] -> y [n x 2 SB_ACT] -> actions [n x SB_ACT], on stream s.
 // obs_cols: every observation row is zero from this column on (the longest
 // observation prefix of the vec's envs).
 // With draws set, also the rollout buffer's draws, per-head log-densities and
-// entropies (hlp, hent [n x 272]) and their per-env sums (logp, entropy [n]).
+// entropies (hlp, hent [n x SB_ACT]) and their per-env sums (logp, entropy [n]).
 extern "C" int sbk_launch_policy(const float* obs, const float* w1, const float* b1, const float* w2,
                                  const float* b2, const float* w3, const float* b3, float* h1, float* h2, float* y,
                                  float* actions, const int* n_cont, const int* n_disc, int n, uint64_t seed,
@@ -446,7 +456,7 @@ extern "C" int sbk_launch_ppo_beta(const float* y_new, const float* y_old, const
                                    const float* adv, const int* n_cont, const int* n_disc, int n, float floor,
                                    float clip, float ent_coef, int per_dim, float* out, float* grad, hipStream_t s) {
     if (n <= 0) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(sbk::ppo_beta_kernel, dim3(n), dim3(320), 0, s, y_new, y_old, draws, logp_old, adv, n_cont,
+    hipLaunchKernelGGL(sbk::ppo_beta_kernel, dim3(n), dim3(sbk::kPpoThreads), 0, s, y_new, y_old, draws, logp_old, adv, n_cont,
                        n_disc, n, floor, clip, ent_coef, per_dim, out, grad);
     return (int)hipGetLastError();
 }
@@ -460,7 +470,7 @@ extern "C" int sbk_launch_beta_sample(const float* alpha, const float* beta, flo
 
 // ------------------------------------------------- allocation-free policy step
 // Activations of sbk_launch_policy_noalloc (h1 [n][128], h2 [n][128] and
-// y [n][544], at most kNoAllocEnvs envs: 12.5 MiB) in a file-scope device
+// y [n][2 SB_ACT], at most kNoAllocEnvs envs: 12.5 MiB, 14.5 MiB with SB_CONT_BIG) in a file-scope device
 // array. Each GPU the library runs on holds its own copy until the process
 // ends. Every call on a GPU uses that GPU's copy: calls that overlap on one GPU
 // race. Nothing in it needs clearing between calls: each layer writes every

@@ -2914,13 +2914,13 @@ __global__ void gen_actions_kernel(float* actions, const int* n_cont, const int*
     const int e = blockIdx.x;
     if (e >= n_envs) return;
     const int nc = n_cont[e], nd = n_disc[e];
-    float* row = actions + (size_t)e * 272;
-    for (int i = threadIdx.x; i < 272; i += blockDim.x) {
+    float* row = actions + (size_t)e * SB_ACT;
+    for (int i = threadIdx.x; i < SB_ACT; i += blockDim.x) {
         float v = 0.0f;
-        if (i < 256) {
+        if (i < SB_CONT) {
             if (i < nc) v = 2.0f * beta22(seed, (uint32_t)e, step, (uint32_t)i) - 1.0f;
         } else {
-            int d = i - 256;
+            int d = i - SB_CONT;
             if (d < nd) v = beta22(seed, (uint32_t)e, step, (uint32_t)i) > 0.5f ? 1.0f : 0.0f;
         }
         row[i] = v;

@@ -2325,7 +2325,9 @@ void sbx_plan_free(SbxPlan* p) {
 
 const char* sbx_last_error(void) { return g_err.c_str(); }
 
-const char* sbx_version(void) { return "sbenv 0.1 gfx950"; }
+const char* sbx_version(void) { return SB_CONT == 256 ? "sbenv 0.1 gfx950" : "sbenv 0.1 gfx950 cont320"; }
+
+int sbx_cont_width(void) { return SB_CONT; }
 
 }  // extern "C"
 

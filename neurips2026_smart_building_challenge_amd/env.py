@@ -11,13 +11,17 @@ There is no CPU fallback: loading fails loudly when libsbenv.so is missing.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 import numpy as np
 
 PKG = Path(__file__).resolve().parent
-LIB_PATH = PKG / "libsbenv.so"
-SB_OBS, SB_CONT, SB_DISC = 1024, 256, 16
+# SBENV_CONT_BIG=1 selects the SB_CONT_BIG build (320 continuous action heads,
+# libsbenv_big.so), as a trainer compiled with -DSB_CONT_BIG links it
+CONT_BIG = os.environ.get("SBENV_CONT_BIG", "0") not in ("", "0")
+LIB_PATH = PKG / ("libsbenv_big.so" if CONT_BIG else "libsbenv.so")
+SB_OBS, SB_CONT, SB_DISC = 1024, (320 if CONT_BIG else 256), 16
 SB_ACT = SB_CONT + SB_DISC
 P = ctypes.c_void_p
 
@@ -98,7 +102,7 @@ def policy_struct(weights: dict, beta_floor: float = 1.0) -> SbxPolicy:
                      float(beta_floor))
 
 
-POLICY_HIDDEN, POLICY_HEADS = 128, 544
+POLICY_HIDDEN, POLICY_HEADS = 128, 2 * SB_ACT
 
 
 # every symbol include/sbenv.h declares
@@ -112,7 +116,7 @@ EXPORTS = [
     "sbx_plan_layout", "sbx_plan_free",
     "sbx_fdm_open", "sbx_fdm_close", "sbx_fdm_info", "sbx_fdm_step", "sbx_fdm_reset", "sbx_fdm_get_state",
     "sbx_fdm_set_state", "sbx_fdm_sensed_response", "sbx_fdm_air_responses", "sbx_fdm_lu_solve",
-    "sbx_last_error", "sbx_version",
+    "sbx_last_error", "sbx_version", "sbx_cont_width",
 ]
 
 _LIB = None
@@ -126,6 +130,8 @@ def lib() -> ctypes.CDLL:
             raise RuntimeError(f"{LIB_PATH} is missing: build it with "
                                "python -m neurips2026_smart_building_challenge_amd.build")
         L = ctypes.CDLL(str(LIB_PATH))
+        if L.sbx_cont_width() != SB_CONT:
+            raise RuntimeError(f"{LIB_PATH} lays out {L.sbx_cont_width()} continuous heads, this binding {SB_CONT}")
         L.dict_find.restype = ctypes.POINTER(DictItem)
         L.dict_find.argtypes = [ctypes.POINTER(Dict), ctypes.c_char_p]
         L.dict_set.argtypes = [ctypes.POINTER(Dict), ctypes.c_char_p, ctypes.c_float]
@@ -320,7 +326,7 @@ class VecEnv:
         self.L.puf_step(self.envs)
 
     def step_actions(self, actions) -> None:
-        """One step reading its action rows from `actions` (device tensor, n x 272 float32)."""
+        """One step reading its action rows from `actions` (device tensor, n x SB_ACT float32)."""
         assert actions.is_cuda and actions.dtype == self.torch.float32 and actions.is_contiguous()
         assert tuple(actions.shape) == (self.n, SB_ACT)
         if self.L.sbx_step_actions(self.envs, P(actions.data_ptr())) != 0:
@@ -371,7 +377,7 @@ class VecEnv:
             raise RuntimeError(self.L.sbx_last_error().decode())
 
     def policy_act_logp(self, seed: int, step: int):
-        """policy_act that also returns the rollout buffer's draws (n, 272) and
+        """policy_act that also returns the rollout buffer's draws (n, SB_ACT) and
         per-env log-probability and entropy (n,) as device tensors."""
         t = self.torch
         draws = t.empty((self.n, SB_ACT), dtype=t.float32, device=self.obs.device)
@@ -383,8 +389,8 @@ class VecEnv:
         return draws, logp, ent
 
     def beta_eval(self, y, draws, grad: bool = True):
-        """Per-env log-probability and entropy (n,) of draws (n, 272) under heads
-        y (n, 544), and the per-head gradients (n, 4, 272) when grad."""
+        """Per-env log-probability and entropy (n,) of draws (n, SB_ACT) under heads
+        y (n, 2 SB_ACT), and the per-head gradients (n, 4, SB_ACT) when grad."""
         t = self.torch
         y = y.contiguous()
         draws = draws.contiguous()
@@ -399,7 +405,7 @@ class VecEnv:
     def ppo_beta(self, y_new, y_old, draws, logp_old, adv, clip_coef: float = 0.2, ent_coef: float = 0.0,
                  ratio_per_dim: bool = True, beta_floor: float = 1.0, grad: bool = True):
         """PPO side of the Beta heads (sbx_ppo_beta): per-env out (n, 6) = logp, entropy,
-        KL(old || new), ratio, pg loss, log-ratio; grad (n, 2, 272) of pg - ent_coef H in u, v."""
+        KL(old || new), ratio, pg loss, log-ratio; grad (n, 2, SB_ACT) of pg - ent_coef H in u, v."""
         t = self.torch
         dev = self.obs.device
         args = [a.contiguous() for a in (y_new, y_old, draws, logp_old, adv)]
@@ -412,7 +418,7 @@ class VecEnv:
         return out, g
 
     def policy_heads(self) -> np.ndarray:
-        """Head outputs y (n, 544) of the last policy_act."""
+        """Head outputs y (n, 2 SB_ACT) of the last policy_act."""
         buf = np.zeros(self.n * POLICY_HEADS, np.float32)
         if self.L.sbx_policy_heads(self.envs, buf.ctypes.data_as(P), buf.size) < 0:
             raise RuntimeError("sbx_policy_heads failed")

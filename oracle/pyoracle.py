@@ -12,14 +12,18 @@ cpu_baseline leg may import this module.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-ORACLE_SO = HERE / "liboracle.so"
+# SBENV_CONT_BIG=1: the SB_CONT_BIG action row (320 continuous slots), as the
+# env library of the same process (libsbenv_big.so) lays it out
+CONT_BIG = os.environ.get("SBENV_CONT_BIG", "0") not in ("", "0")
+ORACLE_SO = HERE / ("liboracle_big.so" if CONT_BIG else "liboracle.so")
 REF_SO = HERE / "_ref" / "libcsim_ref.so"
-SB_OBS, SB_CONT, SB_DISC = 1024, 256, 16
+SB_OBS, SB_CONT, SB_DISC = 1024, (320 if CONT_BIG else 256), 16
 P = ctypes.c_void_p
 
 
@@ -88,6 +92,8 @@ _LIBS: dict[str, _Lib] = {}
 
 def lib(kind: str) -> _Lib:
     if kind not in _LIBS:
+        if kind == "ref" and CONT_BIG:
+            raise RuntimeError("the reference core's driver lays out 256 continuous slots, not SB_CONT_BIG's 320")
         path = REF_SO if kind == "ref" else ORACLE_SO
         if not path.exists():
             raise FileNotFoundError(f"{path} is not built (run __graft_entry__.build())")
@@ -96,7 +102,7 @@ def lib(kind: str) -> _Lib:
 
 
 def ref_available() -> bool:
-    return REF_SO.exists()
+    return REF_SO.exists() and not CONT_BIG
 
 
 class _Scen:
@@ -192,7 +198,7 @@ class CpuEnv:
         self._st = np.zeros(_state_cap(path), np.float64)
 
     def close(self):
-        if self.h:
+        if getattr(self, "h", None):
             self.L.close_fn(self.h)
             self.h = None
 

@@ -21,7 +21,14 @@ extern "C" {
 #endif
 
 #define SBO_OBS 1024
+/* action row: SBO_CONT continuous slots, then SBO_DISC discrete ones; 320
+ * continuous slots when built with SB_CONT_BIG (the reference GPU env's
+ * SB_CONT_BIG layout, complete_port/gpu/smart_buildings.cu:35-40) */
+#ifdef SB_CONT_BIG
+#define SBO_CONT 320
+#else
 #define SBO_CONT 256
+#endif
 #define SBO_DISC 16
 
 /* ---------------- blob ---------------- */

@@ -282,6 +282,7 @@ int sbo_scen_open(SboScen* s, const char* path) {
     for (int i = 0; i < s->n_act; i++) {
         if (s->act_disc[i]) s->n_disc++; else s->n_cont++;
     }
+    if (s->n_cont > SBO_CONT || s->n_disc > SBO_DISC) return -1;   /* the action row has no room for them */
     s->amb = sbo_f64(b, "weather_ambient");
     s->comfort = sbo_f64(b, "sched_comfort");
     s->heat_sp = sbo_f64(b, "sched_heat_sp");

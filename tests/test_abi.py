@@ -3,8 +3,11 @@ include/sbenv.h declares; the host-only helpers work without device calls."""
 from __future__ import annotations
 
 import ctypes
+import os
 import re
 from pathlib import Path
+
+import pytest
 
 from neurips2026_smart_building_challenge_amd import env as E
 
@@ -114,3 +117,42 @@ def test_beta_floor_must_be_positive():
         buf = ctypes.c_void_p(64)
         assert L.sbx_ppo_beta(None, buf, buf, buf, buf, buf, ctypes.byref(ppo), buf, buf) == -1
         assert b"beta_floor" in L.sbx_last_error()
+
+
+def test_cont_big_build_layout(tmp_path):
+    """libsbenv_big.so and liboracle_big.so (SB_CONT_BIG: 320 continuous heads)
+    load in a process with SBENV_CONT_BIG=1 and report that layout; a field
+    scenario with 260 continuous actions opens and steps in the big oracle,
+    and the default oracle refuses it (its action row holds 256)."""
+    import subprocess
+    import sys
+
+    import pyoracle as po
+    from neurips2026_smart_building_challenge_amd.scenario import fdm as F
+    from neurips2026_smart_building_challenge_amd.scenario import generate as G
+
+    spec = G.FieldEnvSpec(F.FdmSpec(rows=200, cols=200, rooms=120, margin=6, seed=3), 6)
+    p = tmp_path / "field120.sbb"
+    p.write_bytes(G.field_env_writer(spec, G.climates()[1], 64, 17321).tobytes())
+    with pytest.raises(RuntimeError):
+        po.CpuEnv("oracle", p, 17321, start=0, max_steps=3)
+    code = f"""
+import sys
+sys.path[:0] = [{str(Path(__file__).resolve().parents[1])!r}, {str(Path(__file__).resolve().parents[1] / 'oracle')!r}]
+import numpy as np
+import pyoracle as po
+from neurips2026_smart_building_challenge_amd import env as E
+assert E.SB_CONT == 320 and E.SB_ACT == 336 and E.POLICY_HEADS == 672
+assert E.lib().sbx_cont_width() == 320 and b"cont320" in E.lib().sbx_version()
+e = po.CpuEnv("oracle", {str(p)!r}, 17321, start=0, max_steps=3)
+assert e.n_cont == 260, e.n_cont
+e.reset()
+for s in range(4):
+    row = po.action_row(7, 0, s, e.n_cont, e.n_disc)
+    assert row.size == 336
+    e.step(row)
+print("ok")
+"""
+    r = subprocess.run([sys.executable, "-c", code], env={**os.environ, "SBENV_CONT_BIG": "1"},
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), (r.stdout, r.stderr)

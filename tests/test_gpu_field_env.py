@@ -313,3 +313,18 @@ def test_gpu_field_env_largest_shipped_size(largest_blob, exact):
     done = run_against_oracle(vec, twins, 4, exact, "largest")
     assert done == 2
     vec.close()
+
+
+def test_gpu_cont_big_build():
+    """The SB_CONT_BIG build (320 continuous heads) steps a field scenario with
+    260 continuous actions beside an RC layout, against the oracle built the
+    same way, and runs the shared policy over 336-wide action rows; the build
+    is chosen at import, so tests/cont_big_check.py runs in a child process."""
+    import os
+    import subprocess
+    import sys
+
+    say("SB_CONT_BIG build: field scenario with 260 continuous actions + RC layout, child process")
+    r = subprocess.run([sys.executable, "-u", str(Path(__file__).resolve().parent / "cont_big_check.py")],
+                       env={**os.environ, "SBENV_CONT_BIG": "1"}, capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0 and "cont_big ok" in r.stdout, (r.stdout[-3000:], r.stderr[-3000:])
