@@ -736,3 +736,46 @@ def test_gpu_log_at_episode_ends_every_env(mixed_dir):
     # some envs leave the comfort band in a logged episode (cold climates at dawn)
     assert sum(vec.log(i)["comfort_dev_K"] > 0.0 for i in range(vec.n)) >= 3
     vec.close()
+
+
+def test_gpu_headline_config_full_episode(tmp_path):
+    """BASELINE config 1 as the bench runs it (960 envs, 30 scenarios, episodes of
+    8,640 steps) for one whole episode, one env of each scenario against its
+    oracle twin: rewards within two float32 steps and terminals every step, the
+    state (air side included) within 1e-9 every 960 steps and at the end, the
+    episode's f64 reward total within 1e-6, and its Log within the Log bar."""
+    from neurips2026_smart_building_challenge_amd.scenario import generate as G
+
+    say("config 1: 960 envs x 8,640 steps, 30 twins")
+    G.write_config(1, tmp_path)
+    scen, n, offsets = G.config_scenarios(1)
+    vec = E.VecEnv(n, blob_dir=str(tmp_path), groups=len(scen), start_offsets=int(offsets), trace_air=1)
+    paths = {}
+    for i in range(n):
+        paths.setdefault(vec.meta(i)[0], i)
+    assert len(paths) == 30
+    twins = [Twin(vec, i, 8640) for i in sorted(paths.values())]
+    vec.reset()
+    for tw in twins:
+        tw.cpu.reset()
+    for s in range(8640):
+        vec.gen_actions(SEED, s)
+        vec.step()
+        torch.cuda.synchronize()
+        rew, term = host(vec.rewards), host(vec.terminals)
+        for tw in twins:
+            _, r, t = tw.step(SEED, s)
+            where = f"config 1 step {s} env {tw.i}"
+            assert abs(float(rew[tw.i]) - r) <= 2 * np.spacing(np.float32(abs(r))) + 1e-12, where
+            assert term[tw.i] == t, where
+            if (s + 1) % 960 == 0 and s + 1 < 8640:
+                state_close(vec.state(tw.i), tw.cpu.state(), where, air=True)
+    assert np.all(host(vec.terminals) == 1.0)
+    for tw in twins:
+        where = f"config 1 env {tw.i} end of episode"
+        gs = vec.state(tw.i)
+        assert gs[-1] == 8640, where
+        assert abs(gs[-2] - tw.rew_sum) <= 1e-6 * abs(tw.rew_sum), (where, gs[-2], tw.rew_sum)
+        state_close(gs, tw.cpu.state(), where, air=True)
+        log_close(vec.log(tw.i), tw, where)
+    vec.close()
