@@ -341,8 +341,11 @@ bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
                 }
             }
             for (int l = nact; l < width; l++) P.hdr.push_back(kIdleHeader);
-            const int wide = (int)lanes.size() > (int)pid.size() ? 1 : 0;
-            pi.packed = nact | (maxcnt << 8) | (piv << 16) | (wide << 17);
+            // butterfly steps the pass needs: log2 of its widest segment
+            int lgmax = 0;
+            for (const Lane& l : lanes)
+                while ((1 << lgmax) < l.seg) lgmax++;
+            pi.packed = nact | (maxcnt << 8) | (piv << 16) | (lgmax << 17);
             const int stride = (maxcnt + 3) & ~3;
             for (const Lane& l : lanes) {
                 const Task& t = tasks[l.task];

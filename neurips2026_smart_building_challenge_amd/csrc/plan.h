@@ -17,8 +17,9 @@ namespace sbh {
 constexpr int kPlanKmax = 16;
 constexpr int kPlanSegMax = 16;
 
-// Per-pass record, 16 bytes: hdr_off, word_off, nact | maxcnt << 8 | has_pivot << 16 | wide << 17, 0.
-// nact: lanes used; wide: some task spans more than one lane. Lane header: target | mul << 16 | inv_target << 32 | flags << 48,
+// Per-pass record, 16 bytes: hdr_off, word_off, nact | maxcnt << 8 | has_pivot << 16 | lgmax << 17, 0.
+// nact: lanes used; lgmax: log2 of the pass's widest segment (the butterfly steps it runs).
+// Lane header: target | mul << 16 | inv_target << 32 | flags << 48,
 // flags = log2(segment lanes) | leader << 3 | terms << 4; a lane that is not its
 // segment's leader has target kSlotZero, mul kSlotOne and inv_target kSlotSink.
 struct PassInfo {
@@ -26,7 +27,7 @@ struct PassInfo {
     int nact() const { return packed & 0xff; }
     int maxcnt() const { return (packed >> 8) & 0xff; }
     int has_pivot() const { return (packed >> 16) & 1; }
-    int wide() const { return (packed >> 17) & 1; }
+    int lgmax() const { return (packed >> 17) & 7; }
 };
 
 // Fixed slots: 0 holds 0.0 (padding terms read it), 1 is a write sink, 2 holds 1.0.

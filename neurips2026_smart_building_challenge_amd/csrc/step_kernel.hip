@@ -1681,22 +1681,27 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P, int* sy) {
 struct PassRegs {
     uint64_t h;
     uint32_t w[SBK_KMAX];
+    int meta;   // the pass record's field word (wave-uniform, kept in a scalar register)
 };
 
-// Pass record fields (nact | maxcnt << 8 | has_pivot << 16 | wide << 17).
-__device__ __forceinline__ int pass_maxcnt(int4 pi) { return (pi.z >> 8) & 0xff; }
-__device__ __forceinline__ bool pass_pivot(int4 pi) { return (pi.z >> 16) & 1; }
-__device__ __forceinline__ bool pass_wide(int4 pi) { return (pi.z >> 17) & 1; }
+// Pass record fields (nact | maxcnt << 8 | has_pivot << 16 | lgmax << 17;
+// lgmax: log2 of the pass's widest segment).
+__device__ __forceinline__ int pass_maxcnt(int meta) { return (meta >> 8) & 0xff; }
+__device__ __forceinline__ bool pass_pivot(int meta) { return (meta >> 16) & 1; }
+__device__ __forceinline__ int pass_lgmax(int meta) { return (meta >> 17) & 7; }
 
 // Issues the loads of one pass's lane header and terms into registers: the
 // header of this lane (every lane has one, idle lanes included) and four
 // 16-byte words from the lane's start (word_off + lane * stride; idle lanes
 // read lane 0's). Words past the lane's stride belong to the next lane or pass
-// and are masked when the pass runs, so nothing here waits for a load.
+// and are masked when the pass runs, so nothing here waits for a load. The
+// record's field word stays in a register, so the pass reads no LDS before its
+// terms.
 __device__ __forceinline__ void fetch_pass(const SBK_C DevLayout* L, int4 pi, PassRegs& r) {
     typedef unsigned int u4v __attribute__((ext_vector_type(4)));
     const int hdr_off = pi.x, word_off = pi.y;
-    const int nact = pi.z & 0xff, stride = (pass_maxcnt(pi) + 3) & ~3;
+    r.meta = __builtin_amdgcn_readfirstlane(pi.z);
+    const int nact = r.meta & 0xff, stride = (pass_maxcnt(r.meta) + 3) & ~3;
     const int lane = ln();
     r.h = L->hdr[hdr_off + lane];
     const u4v* wp = reinterpret_cast<const u4v*>(L->words + word_off + (lane < nact ? lane : 0) * stride);
@@ -1710,9 +1715,9 @@ __device__ __forceinline__ void fetch_pass(const SBK_C DevLayout* L, int4 pi, Pa
     }
 }
 
-// Waits for a fetched pass here: the empty asm "uses" every register, so the
-// compiler places the memory wait at this point instead of at the first use
-// inside the pass (where the loads of the passes after it are in flight).
+// Waits for a fetched pass here: the empty asm "uses" every loaded register,
+// so the compiler places the memory wait at this point instead of at the first
+// use inside the pass (where the loads of the passes after it are in flight).
 __device__ __forceinline__ void settle_pass(PassRegs& r) {
     asm volatile("" : "+v"(r.h));
 #pragma unroll
@@ -1728,6 +1733,25 @@ __device__ __forceinline__ double recip(double x) {
     return fma(r, e, r);
 }
 
+// One group of 4 terms: the slot reads (issued early) and the products
+// subtracted in term order.
+struct TermGroup {
+    double x[4], y[4];
+};
+__device__ __forceinline__ void load_terms(const double* slots, const PassRegs& r, int m0, TermGroup& g) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t w = r.w[m0 + j];
+        g.x[j] = slots[w & 0xffffu];
+        g.y[j] = slots[w >> 16];
+    }
+}
+__device__ __forceinline__ double sub_terms(double acc, const TermGroup& g) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc = fma(-g.x[j], g.y[j], acc);
+    return acc;
+}
+
 // One pass: every task computes slot[target] = (slot[target] - sum of its
 // terms) * slot[mul] on its segment of lanes. Each lane subtracts its own terms
 // (the leader from slot[target], the others from 0), a butterfly over the
@@ -1739,9 +1763,8 @@ __device__ __forceinline__ double recip(double x) {
 // longest lane (its stride is that rounded up to 4, so a group never reaches
 // another lane's words); terms past a lane's count are (0, 0) and read slot
 // 0 = 0.
-__device__ __forceinline__ void run_pass(double* slots, const PassRegs& r, int4 pi) {
-    constexpr int CH = 4;
-    const int maxcnt = pass_maxcnt(pi);
+__device__ __forceinline__ void run_pass(double* slots, const PassRegs& r) {
+    const int meta = r.meta;
     const int tgt = (int)(r.h & 0xffffu);
     const int mul = (int)((r.h >> 16) & 0xffffu);
     const int invt = (int)((r.h >> 32) & 0xffffu);
@@ -1750,32 +1773,48 @@ __device__ __forceinline__ void run_pass(double* slots, const PassRegs& r, int4 
     const bool lead = (flags >> 3) & 1;
     double acc = slots[tgt];
     const double scale = slots[mul];
-#pragma unroll
-    for (int m0 = 0; m0 < SBK_KMAX; m0 += CH) {
-        if (m0 >= maxcnt) break;
-        double x[CH], y[CH];
-#pragma unroll
-        for (int j = 0; j < CH; j++) {
-            const uint32_t w = r.w[m0 + j];
-            x[j] = slots[w & 0xffffu];
-            y[j] = slots[w >> 16];
+    // groups of 4 terms, the reads of the next group issued before the
+    // products of the current one (the group count is wave-uniform)
+    static_assert(SBK_KMAX == 16, "term groups below are written for 16 terms a lane");
+    const int ng = (pass_maxcnt(meta) + 3) >> 2;
+    if (ng > 0) {
+        TermGroup ga, gb;
+        load_terms(slots, r, 0, ga);
+        if (ng > 1) load_terms(slots, r, 4, gb);
+        acc = sub_terms(acc, ga);
+        if (ng > 1) {
+            if (ng > 2) load_terms(slots, r, 8, ga);
+            acc = sub_terms(acc, gb);
+            if (ng > 2) {
+                if (ng > 3) load_terms(slots, r, 12, gb);
+                acc = sub_terms(acc, ga);
+                if (ng > 3) acc = sub_terms(acc, gb);
+            }
         }
-#pragma unroll
-        for (int j = 0; j < CH; j++) acc -= x[j] * y[j];
     }
-    if (pass_wide(pi)) {
-        double t = dpp_d<DPP_QUAD_1032>(0.0, acc);
+    // only the butterfly steps the pass's widest segment needs (wave-uniform);
+    // every lane of a step's row pattern is a source, so the moves need no
+    // fill value
+    const int lgmax = pass_lgmax(meta);
+    if (lgmax >= 1) {
+        double t = dpp_d<DPP_QUAD_1032>(acc, acc);
         acc = lg >= 1 ? acc + t : acc;
-        t = dpp_d<DPP_QUAD_2301>(0.0, acc);
-        acc = lg >= 2 ? acc + t : acc;
-        t = dpp_d<DPP_ROW_HALF_MIRROR>(0.0, acc);
-        acc = lg >= 3 ? acc + t : acc;
-        t = dpp_d<DPP_ROW_MIRROR>(0.0, acc);
-        acc = lg >= 4 ? acc + t : acc;
+        if (lgmax >= 2) {
+            t = dpp_d<DPP_QUAD_2301>(acc, acc);
+            acc = lg >= 2 ? acc + t : acc;
+            if (lgmax >= 3) {
+                t = dpp_d<DPP_ROW_HALF_MIRROR>(acc, acc);
+                acc = lg >= 3 ? acc + t : acc;
+                if (lgmax >= 4) {
+                    t = dpp_d<DPP_ROW_MIRROR>(acc, acc);
+                    acc = lg >= 4 ? acc + t : acc;
+                }
+            }
+        }
     }
     acc *= scale;
     if (lead) slots[tgt] = acc;
-    if (pass_pivot(pi)) slots[invt] = recip(acc);
+    if (pass_pivot(meta)) slots[invt] = recip(acc);
 }
 
 // All passes, in groups of SBK_PLAN_DEPTH (the pass count is a multiple of
@@ -1797,15 +1836,49 @@ __device__ __forceinline__ void run_plan(const SBK_C DevLayout* L, double* slots
         if (pts) pts[p] = clock64();
 #pragma unroll
         for (int k = 1; k < D; k++) fetch_pass(L, rec[p + k], R[k]);
+        // the group's loads are issued before the first pass waits for its
+        // own (the scheduler may not move them below this point)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int k = 0; k < D; k++) {
-            if (k == D - 1) fetch_pass(L, rec[min(p + D, np - 1)], R[0]);
+            if (k == D - 1) {
+                fetch_pass(L, rec[min(p + D, np - 1)], R[0]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
             settle_pass(R[k]);
-            run_pass(slots, R[k], rec[p + k]);
+            run_pass(slots, R[k]);
             wave_lds_sync();
         }
     }
     if (pts) pts[np] = clock64();
+}
+
+// The LU slots' starting values (the permuted matrix, the zero and one slots)
+// copied HBM -> LDS in 16-byte vectors, every load of a round (8 KB per
+// wavefront) issued before the round's first store, so the copy costs about
+// one memory latency per round instead of one per 512 bytes.
+__device__ __forceinline__ void copy_slot_init(double* dst, const SBK_C double* src, int count) {
+    constexpr int U = 8, W = 64;
+    typedef unsigned int u4v __attribute__((ext_vector_type(4)));
+    const int n16 = count >> 1, lane = ln();
+    const SBK_C u4v* s = reinterpret_cast<const SBK_C u4v*>(src);
+    u4v* d = reinterpret_cast<u4v*>(dst);
+    for (int base = 0; base < n16; base += U * W) {
+        u4v r[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = min(base + u * W + lane, n16 - 1);
+            r[u] = s[i];
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) asm volatile("" : "+v"(r[u]));
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = base + u * W + lane;
+            if (i < n16) d[i] = r[u];
+        }
+    }
+    if ((count & 1) && lane == 0) dst[count - 1] = src[count - 1];
 }
 
 // ------------------------------------------------------------------ relaxation
@@ -2234,7 +2307,7 @@ __device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
         return;
     } else {
     const int vb = L->vec_base;
-    for (int s = ln(); s < vb; s += W) slots[s] = L->slot_init[s];   // incl. 0.0 and 1.0 slots
+    copy_slot_init(slots, L->slot_init, vb);   // incl. 0.0 and 1.0 slots
     // room cells carry their zone's heat; every node then gets its solar gain
     for (int z = ln(); z < L->nz; z += W) {
         double qz = c.zq[z];

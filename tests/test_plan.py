@@ -20,7 +20,7 @@ def run_plan(pl, slots):
     assert pl["hdr"].size == 64 * pl["n_pass"]
     for pi in pl["pass_info"]:
         ho, wo, packed = (int(x) for x in pi[:3])
-        nact, maxcnt, piv, wide = packed & 0xFF, (packed >> 8) & 0xFF, (packed >> 16) & 1, (packed >> 17) & 1
+        nact, maxcnt, piv, lgmax = packed & 0xFF, (packed >> 8) & 0xFF, (packed >> 16) & 1, (packed >> 17) & 7
         assert ho % 64 == 0 and wo % 4 == 0, "a header per lane; 16-byte aligned lane words"
         stride = (maxcnt + 3) & ~3
         assert wo + max(nact - 1, 0) * stride + 16 <= pl["words"].size, "a lane's four 16-byte reads stay in the array"
@@ -37,7 +37,7 @@ def run_plan(pl, slots):
         for l in np.flatnonzero(lead):
             assert np.all(lg[l:l + seg[l]] == lg[l]), "a segment's lanes share its width"
         assert np.all(tgt[lead == 0] == 0) and np.all(mul[lead == 0] == 2) and np.all(invt[lead == 0] == 1)
-        assert wide == int(np.any(seg > 1))
+        assert lgmax == int(lg.max(initial=0)), "the pass runs as many butterfly steps as its widest segment needs"
         assert len(set(tgt[lead == 1].tolist())) == int(lead.sum()), "one task per target in a pass"
         assert piv == int(np.any(invt != 1))
         assert cnt.max(initial=0) == maxcnt
@@ -48,7 +48,7 @@ def run_plan(pl, slots):
             assert np.all(w[cnt <= m] == 0), "terms past a lane's count must be (0, 0)"
             acc = acc - slots[w & 0xFFFF] * slots[w >> 16]
         assert np.all(W[:, maxcnt:] == 0)
-        for k in range(4):
+        for k in range(lgmax):
             partner = np.minimum(lanes ^ (1 << k), nact - 1)
             acc = np.where(lg > k, acc + acc[partner], acc)
         acc = acc * slots[mul]
