@@ -779,3 +779,52 @@ def test_gpu_headline_config_full_episode(tmp_path):
         state_close(gs, tw.cpu.state(), where, air=True)
         log_close(vec.log(tw.i), tw, where)
     vec.close()
+
+
+@pytest.mark.parametrize("config", [2, 3])
+def test_gpu_large_config_full_episode(config, tmp_path):
+    """BASELINE configs 2 (4,096 envs of the 81-zone layout, 5 climates) and 3
+    (16,384 mixed envs, each from its own seeded calendar offset) for one whole
+    8,640-step episode at full batch, one env of each scenario (taken from the
+    end of the batch, so from the last tiles) against its oracle twin: rewards
+    within two float32 steps and terminals every step, the state (air side
+    included) within 1e-9 every 2,160 steps and at the end, the f64 reward total
+    within 1e-6 and the episode Log within the Log bar."""
+    from neurips2026_smart_building_challenge_amd.scenario import generate as G
+
+    G.write_config(config, tmp_path)
+    scen, n, offsets = G.config_scenarios(config)
+    say(f"config {config}: {n} envs x 8,640 steps, {len(scen)} twins")
+    vec = E.VecEnv(n, blob_dir=str(tmp_path), groups=len(scen), start_offsets=int(offsets), trace_air=1)
+    paths = {}
+    for i in range(n - 1, -1, -1):
+        paths.setdefault(vec.meta(i)[0], i)
+    assert len(paths) == len(scen)
+    twins = [Twin(vec, i, 8640) for i in sorted(paths.values())]
+    if offsets:
+        assert len({vec.meta(tw.i)[1] for tw in twins}) > 1, "the sampled envs start at different offsets"
+    vec.reset()
+    for tw in twins:
+        tw.cpu.reset()
+    idx = torch.as_tensor([tw.i for tw in twins], device=vec.rewards.device)
+    for s in range(8640):
+        vec.gen_actions(SEED, s)
+        vec.step()
+        torch.cuda.synchronize()
+        rew, term = host(vec.rewards[idx]), host(vec.terminals[idx])
+        for j, tw in enumerate(twins):
+            _, r, t = tw.step(SEED, s)
+            where = f"config {config} step {s} env {tw.i}"
+            assert abs(float(rew[j]) - r) <= 2 * np.spacing(np.float32(abs(r))) + 1e-12, where
+            assert term[j] == t, where
+            if (s + 1) % 2160 == 0 and s + 1 < 8640:
+                state_close(vec.state(tw.i), tw.cpu.state(), where, air=True)
+    assert np.all(host(vec.terminals) == 1.0)
+    for tw in twins:
+        where = f"config {config} env {tw.i} end of episode"
+        gs = vec.state(tw.i)
+        assert gs[-1] == 8640, where
+        assert abs(gs[-2] - tw.rew_sum) <= 1e-6 * abs(tw.rew_sum), (where, gs[-2], tw.rew_sum)
+        state_close(gs, tw.cpu.state(), where, air=True)
+        log_close(vec.log(tw.i), tw, where)
+    vec.close()
