@@ -232,78 +232,38 @@ __device__ __forceinline__ void wave_sum4_max(double& a, double& b, double& d, d
     mx = lane63_d(mx);
 }
 
-// Sums of N per-lane values in one pass (N independent DPP chains).
-template <int N>
-__device__ __forceinline__ void wave_sum_n(double (&x)[N]) {
-#define SBK_STEPN(CTRL, ROWS)                                          \
-    _Pragma("unroll") for (int i = 0; i < N; i++) x[i] = x[i] + dpp_d<CTRL, ROWS>(0.0, x[i]);
-    SBK_STEPN(DPP_QUAD_1032, 0xF)
-    SBK_STEPN(DPP_QUAD_2301, 0xF)
-    SBK_STEPN(DPP_ROW_HALF_MIRROR, 0xF)
-    SBK_STEPN(DPP_ROW_MIRROR, 0xF)
-    SBK_STEPN(DPP_ROW_BCAST15, 0xA)
-    SBK_STEPN(DPP_ROW_BCAST31, 0xC)
-#undef SBK_STEPN
+// Per-AHU sums by one lane each: lane a (< na) adds vals[idx[t]] over its list
+// entries t in [off[a], off[a + 1]) in list order (an AHU's VAVs or coupled
+// columns, ascending: the order csim accumulates them in), eight entries'
+// loads issued before their adds; with COUNT also the number of entries whose
+// value is > 0. The values are in LDS, written by the calling wavefront before
+// an esync().
+template <bool COUNT>
+__device__ __forceinline__ double ahu_list_sum(const int* off, const int* idx, const double* vals, int a, int& npos) {
+    double s = 0.0;
+    int np = 0;
+    const int t1 = off[a + 1];
+    int t = off[a];
+    for (; t + 8 <= t1; t += 8) {
+        int i8[8];
+        double v8[8];
 #pragma unroll
-    for (int i = 0; i < N; i++) x[i] = lane63_d(x[i]);
-}
-
-// Per-AHU sums of NV per-lane values, Q AHUs (a0 .. a0 + Q - 1) per pass with
-// their reductions interleaved; lane l receives the sums of AHU l in mine[]
-// (lanes l outside the pass keep what they had).
-template <int NV, int Q, int R>
-__device__ __forceinline__ void ahu_sums_pass(const int (&key)[SBK_VPL], const double (&vals)[SBK_VPL][NV], int a0,
-                                              double (&mine)[NV]) {
-    double x[Q * NV];
+        for (int u = 0; u < 8; u++) i8[u] = idx[t + u];
 #pragma unroll
-    for (int q = 0; q < Q; q++) {
+        for (int u = 0; u < 8; u++) v8[u] = vals[i8[u]];
 #pragma unroll
-        for (int k = 0; k < NV; k++) {
-            double acc = 0.0;
-#pragma unroll
-            for (int r = 0; r < R; r++) acc += key[r] == a0 + q ? vals[r][k] : 0.0;
-            x[q * NV + k] = acc;
+        for (int u = 0; u < 8; u++) {
+            s += v8[u];
+            if (COUNT) np += v8[u] > 0.0 ? 1 : 0;
         }
     }
-    wave_sum_n<Q * NV>(x);
-#pragma unroll
-    for (int q = 0; q < Q; q++) {
-        const bool me = ln() == a0 + q;
-#pragma unroll
-        for (int k = 0; k < NV; k++) mine[k] = me ? x[q * NV + k] : mine[k];
+    for (; t < t1; t++) {
+        const double x = vals[idx[t]];
+        s += x;
+        if (COUNT) np += x > 0.0 ? 1 : 0;
     }
-}
-
-// Per-AHU sums of NV per-lane values: lane a < na receives in mine[k] the
-// wavefront's sum of vals[r][k] over the slots r < R with key[r] == a (the
-// slots past R must not hold keys). Every lane of the wavefront must be active.
-template <int NV, int R>
-__device__ __forceinline__ void ahu_sums_r(const int (&key)[SBK_VPL], const double (&vals)[SBK_VPL][NV], int na,
-                                           double (&mine)[NV]) {
-#pragma unroll
-    for (int k = 0; k < NV; k++) mine[k] = 0.0;
-    for (int a0 = 0; a0 < na;) {
-        const int left = na - a0;
-        if (left >= 3) {
-            ahu_sums_pass<NV, 4, R>(key, vals, a0, mine);
-            a0 += 4;
-        } else if (left == 2) {
-            ahu_sums_pass<NV, 2, R>(key, vals, a0, mine);
-            a0 += 2;
-        } else {
-            ahu_sums_pass<NV, 1, R>(key, vals, a0, mine);
-            a0 += 1;
-        }
-    }
-}
-
-// ahu_sums_r over every register slot (`items`, the VAV or column count, is
-// not used to trim them: one instantiation keeps the code small).
-template <int NV>
-__device__ __forceinline__ void ahu_sums(const int (&key)[SBK_VPL], const double (&vals)[SBK_VPL][NV], int na,
-                                         int items, double (&mine)[NV]) {
-    (void)items;
-    ahu_sums_r<NV, SBK_VPL>(key, vals, na, mine);
+    npos = np;
+    return s;
 }
 
 // Inclusive prefix sum over the wavefront.
@@ -619,16 +579,18 @@ __device__ __forceinline__ double vav_temp(const Ctx& c, const double* zmean, in
 // the first wavefront's VAV pass: the temperature goes to c.sensing, and
 // c.fdem (scratch until the coupled-column pass) holds the VAV's zone area,
 // whose sign says whether the VAV senses a zone at all.
-// The VAVs' terms of their AHU's return-air mean go to the register slots
-// r = pass * U + u: key vahu[r], values sensing * area and area (VAV area > 0).
+// The VAVs' terms of their AHU's return-air mean: sensing * area into c.rwen
+// (every VAV has zone area: the host refuses one without; the coupled-column
+// pass writes c.rwen only after the first wavefront has waited for these
+// sums).
 template <int U>
-__device__ __forceinline__ void vav_sensing(Ctx& c, int (&vahu)[SBK_VPL], double (&vv)[SBK_VPL][2]) {
+__device__ __forceinline__ void vav_sensing(Ctx& c) {
     const int nv = c.L->nv, lane = ln();
 #pragma unroll
     for (int pass = 0; pass < upasses<U>(); pass++) {
         const int base = pass * 64 * U;
         if (base >= nv) break;
-        int v[U], a[U];
+        int v[U];
         bool ok[U];
         double tv[U], area[U], varea[U];
 #pragma unroll
@@ -636,7 +598,6 @@ __device__ __forceinline__ void vav_sensing(Ctx& c, int (&vahu)[SBK_VPL], double
             const int vv0 = base + 64 * u + lane;
             ok[u] = vv0 < nv;
             v[u] = ok[u] ? vv0 : nv - 1;
-            a[u] = c.t.vav_ahu()[v[u]];
             varea[u] = c.t.vav_area()[v[u]];
         }
         vav_temps<U>(c, c.zq, v, tv, area);
@@ -645,12 +606,7 @@ __device__ __forceinline__ void vav_sensing(Ctx& c, int (&vahu)[SBK_VPL], double
             if (ok[u]) {
                 c.sensing[v[u]] = tv[u];
                 c.fdem[v[u]] = area[u];
-                const int r = pass * U + u;
-                vahu[r] = a[u];
-                if (varea[u] > 0.0) {
-                    vv[r][0] = tv[u] * varea[u];
-                    vv[r][1] = varea[u];
-                }
+                c.rwen[v[u]] = tv[u] * varea[u];
             }
         }
     }
@@ -1312,12 +1268,12 @@ __device__ __forceinline__ void decode_apply(Ctx& c) {
 }
 
 // VAV pass of the pre-step (sb_sim.c:368-384, :316-355, :382-387): sensed
-// temperature, thermostat mode, damper and reheat settings, unrestricted flow,
-// and the register slots r = pass * U + u (VAV lane + 64 r) the AHU sums read.
+// temperature, thermostat mode, damper and reheat settings, unrestricted flow
+// (c.unres, which the AHUs' demand sums read), and each VAV's AHU in the
+// register slots r = pass * U + u (VAV lane + 64 r) for the flow ratios.
 // U VAVs per lane per pass, all loads of a pass before any store.
 template <int U>
-__device__ __forceinline__ void vav_pass(Ctx& c, int comfort, double& ffs_part, int (&vahu)[SBK_VPL],
-                                         double (&vv)[SBK_VPL][1]) {
+__device__ __forceinline__ void vav_pass(Ctx& c, int comfort, double& ffs_part, int (&vahu)[SBK_VPL]) {
     const int nv = c.L->nv, lane = ln();
     const double* rw = c.row;
     const double hsp = rw[RW_HSP_K], csp = rw[RW_CSP_K];
@@ -1400,9 +1356,7 @@ __device__ __forceinline__ void vav_pass(Ctx& c, int comfort, double& ffs_part, 
                 }
                 c.unres[v[u]] = un;
                 ffs_part += reheat * vc1[u];
-                const int r = pass * U + u;
-                vahu[r] = a[u];
-                vv[r][0] = un;
+                vahu[pass * U + u] = a[u];
             }
         }
     }
@@ -1416,8 +1370,7 @@ __device__ __forceinline__ void vav_pass(Ctx& c, int comfort, double& ffs_part, 
 // column and drop their results.
 template <int U>
 __device__ __forceinline__ void coupled_columns(Ctx& c, double ffs, double tf, double iwt, double& total_rw,
-                                                double& cmin, double& cmax, int (&cahu)[SBK_VPL],
-                                                double (&cfd)[SBK_VPL][2]) {
+                                                double& cmin, double& cmax) {
     const int k = c.L->k;
     const int lane = ln();
 #pragma unroll
@@ -1487,11 +1440,6 @@ __device__ __forceinline__ void coupled_columns(Ctx& c, double ffs, double tf, d
                 total_rw += rw;
                 cmin = fmin(cmin, ta);
                 cmax = fmax(cmax, ta);
-                if (area[u] > 0.0 && fd > 0.0) {
-                    cahu[pass * U + u] = a[u];
-                    cfd[pass * U + u][0] = fd;
-                    cfd[pass * U + u][1] = 1.0;
-                }
             }
         }
     }
@@ -1581,24 +1529,25 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P, int* sy) {
     // this lane's VAVs (v = lane + 64 r) kept in registers for the AHU sums
     double ffs_part = 0.0;
     int vahu[SBK_VPL];
-    double vv[SBK_VPL][1];   // unrestricted flow
 #pragma unroll
-    for (int r = 0; r < SBK_VPL; r++) {
-        vahu[r] = -1;
-        vv[r][0] = 0.0;
-    }
-    if (nv > 64) vav_pass<2>(c, comfort, ffs_part, vahu, vv);
-    else vav_pass<1>(c, comfort, ffs_part, vahu, vv);
+    for (int r = 0; r < SBK_VPL; r++) vahu[r] = -1;
+    if (nv > 64) vav_pass<2>(c, comfort, ffs_part, vahu);
+    else vav_pass<1>(c, comfort, ffs_part, vahu);
     STAMP(13);
     const double ffs = bsum<W>(ffs_part, c.red);
     STAMP(20);
-    double sums[1];
-    ahu_sums<1>(vahu, vv, na, nv, sums);
+    // each AHU's flow demand: the unrestricted flows of its VAVs, by lane a
+    esync();
+    double dm = 0.0;
+    if (ln() < na) {
+        int unused;
+        dm = ahu_list_sum<false>(c.t.ahu_vav_off(), c.t.ahu_vavs(), c.unres, ln(), unused);
+    }
     env_wait(sy + SY_RET, 1);   // the helper's return-air sums
     STAMP(21);
     if (ln() < na) {
         const int a = ln();
-        const double ws = c.wsum[a], at = c.atotal[a], dm = sums[0];
+        const double ws = c.wsum[a], at = c.atotal[a];
         double rt = (at > 0.0) ? ws / at : tmean;
         double mixed = c.recirc[a] * rt + (1.0 - c.recirc[a]) * ambient;
         c.satv[a] = (mixed > c.sat[a] && c.run[a] == 1) ? c.sat[a] : mixed;
@@ -1637,28 +1586,24 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P, int* sy) {
     // coupled columns: reheat energy, air-side conductance, AHU flow (sb_sim.c:410-436),
     // and the coil extremes for the boiler return temperature (sb_sim.c:495-499)
     double total_rw = 0.0, cmin = 1e308, cmax = -1e308;
-    int cahu[SBK_VPL];
-    double cfd[SBK_VPL][2];   // flow demand, 1 (count) of columns with area > 0 and demand > 0
-#pragma unroll
-    for (int r = 0; r < SBK_VPL; r++) {
-        cahu[r] = -1;
-        cfd[r][0] = cfd[r][1] = 0.0;
-    }
-    if (L->k > 64) coupled_columns<2>(c, ffs, tf, iwt, total_rw, cmin, cmax, cahu, cfd);
-    else coupled_columns<1>(c, ffs, tf, iwt, total_rw, cmin, cmax, cahu, cfd);
+    if (L->k > 64) coupled_columns<2>(c, ffs, tf, iwt, total_rw, cmin, cmax);
+    else coupled_columns<1>(c, ffs, tf, iwt, total_rw, cmin, cmax);
     STAMP(22);
+    esync();
+    // AHU flow (clamped to the AHU's maximum) and cooling requests: by lane a
+    // over its columns' flow demands (c.fdem; 0 where the VAV has no zone
+    // area), the requests its columns with a demand > 0
+    double f = 0.0;
+    int cnt = 0;
+    if (ln() < na) f = ahu_list_sum<true>(c.t.ahu_col_off(), c.t.ahu_cols(), c.fdem, ln(), cnt);
     wave_sum_min_max(total_rw, cmin, cmax);
     STAMP(23);
-    // AHU flow (clamped to the AHU's maximum) and cooling requests
-    double fsum[2];
-    ahu_sums<2>(cahu, cfd, na, L->k, fsum);
     STAMP(24);
     if (ln() < na) {
         const int a = ln();
-        const double f = fsum[0], cnt = fsum[1];
         const double mf = c.t.ahu_c()[a * 9 + 1];
         c.flow[a] = f > mf ? mf : f;
-        c.coolreq[a] = (int)cnt;
+        c.coolreq[a] = cnt;
     }
     if (ln() == 0) {
         c.misc[MS_TOTAL_REHEAT] = total_rw;
@@ -2377,16 +2322,17 @@ __device__ __forceinline__ void step_post(Ctx& c) {
 }
 
 // 3C reward (sb_reward.c:31-155) on the post-step state and new occupancy.
-// VAV temperatures and areas of the reward's AHU terms (sb_reward.c:62-98)
-// into the register slots r = pass * U + u (VAV lane + 64 r).
+// VAV temperatures and areas of the reward's AHU terms (sb_reward.c:62-98):
+// temperature * area into c.unres and area into c.fdem (both 0 for a VAV
+// without zone area; the pre-step's scratch, free by now).
 template <int U>
-__device__ __forceinline__ void reward_vavs(Ctx& c, const double* zm, int (&vahu)[SBK_VPL], double (&vv)[SBK_VPL][2]) {
+__device__ __forceinline__ void reward_vavs(Ctx& c, const double* zm) {
     const int nv = c.L->nv, lane = ln();
 #pragma unroll
     for (int pass = 0; pass < upasses<U>(); pass++) {
         const int base = pass * 64 * U;
         if (base >= nv) break;
-        int v[U], a[U];
+        int v[U];
         bool ok[U];
         double tv[U], area[U];
 #pragma unroll
@@ -2394,18 +2340,14 @@ __device__ __forceinline__ void reward_vavs(Ctx& c, const double* zm, int (&vahu
             const int vv0 = base + 64 * u + lane;
             ok[u] = vv0 < nv;
             v[u] = ok[u] ? vv0 : nv - 1;
-            a[u] = c.t.vav_ahu()[v[u]];
         }
         vav_temps<U>(c, zm, v, tv, area);
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int r = pass * U + u;
             if (ok[u]) {
-                vahu[r] = a[u];
-                if (area[u] > 0.0) {
-                    vv[r][0] = tv[u] * area[u];
-                    vv[r][1] = area[u];
-                }
+                const bool live = area[u] > 0.0;
+                c.unres[v[u]] = live ? tv[u] * area[u] : 0.0;
+                c.fdem[v[u]] = live ? area[u] : 0.0;
             }
         }
     }
@@ -2437,20 +2379,14 @@ __device__ __forceinline__ void reward_ahu(Ctx& c, const double* zm, double& blo
     // VAV temperatures (lanes over VAVs), then one lane per AHU: return-air
     // mean over its VAVs in VAV order and its blower / cooling terms, which
     // every lane then sums in AHU order (sb_reward.c:62-98)
-    int vahu[SBK_VPL];
-    double vv[SBK_VPL][2];   // temperature * area, area (zone area > 0 only)
-#pragma unroll
-    for (int r = 0; r < SBK_VPL; r++) {
-        vahu[r] = -1;
-        vv[r][0] = vv[r][1] = 0.0;
-    }
-    if (L->nv > 64) reward_vavs<2>(c, zm, vahu, vv);
-    else reward_vavs<1>(c, zm, vahu, vv);
-    double sums[2];
-    ahu_sums<2>(vahu, vv, L->na, L->nv, sums);
+    if (L->nv > 64) reward_vavs<2>(c, zm);
+    else reward_vavs<1>(c, zm);
+    esync();
     if (ln() < L->na) {
         const int a = ln();
-        const double ws = sums[0], at = sums[1];
+        int unused;
+        const double ws = ahu_list_sum<false>(c.t.ahu_vav_off(), c.t.ahu_vavs(), c.unres, a, unused);
+        const double at = ahu_list_sum<false>(c.t.ahu_vav_off(), c.t.ahu_vavs(), c.fdem, a, unused);
         double rc = (at > 0.0) ? ws / at : tmean;
         double st = ahu_static(c, a);
         double fe = c.t.ahu_c()[a * 9 + 5];
@@ -2696,24 +2632,18 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
     zone_means<W>(c, c.zq);
     esync();
     {
-        int vahu[SBK_VPL];
-        double vv[SBK_VPL][2];
-#pragma unroll
-        for (int r = 0; r < SBK_VPL; r++) {
-            vahu[r] = -1;
-            vv[r][0] = vv[r][1] = 0.0;
-        }
-        if (L->nv > 64) vav_sensing<2>(c, vahu, vv);
-        else vav_sensing<1>(c, vahu, vv);
+        if (L->nv > 64) vav_sensing<2>(c);
+        else vav_sensing<1>(c);
         env_post(sy + SY_SENS, 1);
-        // each AHU's return-air sums over its VAVs (sb_sim.c:382-387), for the
-        // first wavefront's supply temperatures (c.wsum / c.atotal: reward
-        // scratch, free until then)
-        double sums[2];
-        ahu_sums<2>(vahu, vv, L->na, L->nv, sums);
+        // each AHU's return-air sums over its VAVs in VAV order (sb_sim.c:
+        // 382-387) by lane a, for the first wavefront's supply temperatures
+        // (c.wsum / c.atotal: reward scratch, free until then)
+        esync();
         if (ln() < L->na) {
-            c.wsum[ln()] = sums[0];
-            c.atotal[ln()] = sums[1];
+            const int a = ln();
+            int unused;
+            c.wsum[a] = ahu_list_sum<false>(c.t.ahu_vav_off(), c.t.ahu_vavs(), c.rwen, a, unused);
+            c.atotal[a] = ahu_list_sum<false>(c.t.ahu_vav_off(), c.t.ahu_vavs(), c.t.vav_area(), a, unused);
         }
         env_post(sy + SY_RET, 1);
     }
