@@ -92,7 +92,7 @@ struct LdsLayout {
     int act;          // f32[SB_ACT] action row of the step
     int slots;        // f64[n_slots]: 0 zero, 1 sink, LU entries, vector (relaxation: node heat)
     int zq;           // f64[nz] zone heat / zone mean temperature
-    int vtmp;         // f64[3 * nv]: unrestricted flow, flow demand, reheat energy
+    int vtmp;         // f64[4 * nv]: unrestricted flow, flow demand, reheat energy, per-AHU list values
     int g;            // f64[k] air-side conductance
     int tair;         // f64[k] supply air temperature
     int atmp;         // f64[8 * na]: wsum, atotal, satv, demand, fd sum, count
@@ -121,6 +121,7 @@ struct ImgLayout {
     int cap, mcoup, mret, mgain, solar_c, rx_diag;          // [n]
     int zone_area;                                          // [nz]
     int vav_area;                                           // [nv]
+    int ahu_area;                                           // [na]: its VAVs' areas summed in ascending VAV order
     int vav_c, ahu_c;                                       // [9 nv], [9 na]
     int act_mn, act_mx, act_mnr, act_mxr, act_hi;           // [n_act]
     int f_mean, f_sd;                                       // [n_dev]
@@ -130,6 +131,7 @@ struct ImgLayout {
     int zone_cell_off, zone_cells, vz_off, vz_idx, vav_ahu, coupled, zone_col_off, zone_cols;
     int ahu_vav_off, ahu_vavs;     // [na + 1], [nv]: each AHU's VAVs, ascending
     int ahu_col_off, ahu_cols;     // [na + 1], [k]: each AHU's coupled columns, ascending
+    int vav_lpos, col_lpos;        // [nv], [k]: each VAV's position in ahu_vavs, each column's in ahu_cols
     int act_src, act_dst, act_aux;                          // [n_act] (dst/aux: ACT_*)
     int air_slot, air_node;                                 // [k]
     // block-Jacobi tables (block form only), chunk-major so lane l reading block
@@ -368,10 +370,10 @@ static_assert(sizeof(EnvDesc) == 40 && offsetof(EnvDesc, state_off) == 8 && offs
               && offsetof(EnvDesc, scen_src) == 32, "EnvDesc layout");
 static_assert(sizeof(Tile) == 240 && offsetof(Tile, img_src) == 48 && offsetof(Tile, env) == 64
               && offsetof(Tile, desc) == 80, "Tile layout");
-static_assert(sizeof(StateLayout) == 120 && sizeof(LdsLayout) == 96 && sizeof(ImgLayout) == 188
+static_assert(sizeof(StateLayout) == 120 && sizeof(LdsLayout) == 96 && sizeof(ImgLayout) == 200
               && sizeof(ScenImg) == 24, "table layouts");
-static_assert(sizeof(DevLayout) == 888 && offsetof(DevLayout, st) == 88 && offsetof(DevLayout, img_src) == 496
-              && offsetof(DevLayout, bytes_per_step) == 864, "DevLayout layout");
+static_assert(sizeof(DevLayout) == 896 && offsetof(DevLayout, st) == 88 && offsetof(DevLayout, img_src) == 504
+              && offsetof(DevLayout, bytes_per_step) == 872, "DevLayout layout");
 static_assert(sizeof(DevScen) == 488 && offsetof(DevScen, img_src) == 32 && offsetof(DevScen, gas_co2) == 200
               && offsetof(DevScen, conv_p) == 464, "DevScen layout");
 static_assert(sizeof(KParams) == 144 && offsetof(KParams, host_env) == 80 && offsetof(KParams, phase_ts) == 112

@@ -232,35 +232,30 @@ __device__ __forceinline__ void wave_sum4_max(double& a, double& b, double& d, d
     mx = lane63_d(mx);
 }
 
-// Per-AHU sums by one lane each: lane a (< na) adds vals[idx[t]] over its list
-// entries t in [off[a], off[a + 1]) in list order (an AHU's VAVs or coupled
-// columns, ascending: the order csim accumulates them in), eight entries'
-// loads issued before their adds; with COUNT also the number of entries whose
-// value is > 0. The values are in LDS, written by the calling wavefront before
-// an esync().
+// Per-AHU sums by one lane each: lane a (< na) adds vals[t] over its list
+// positions t in [off[a], off[a + 1]) in order. The per-AHU terms were written
+// at their entry's position in the AHU's list (ascending VAVs or columns: the
+// order csim accumulates them in), so an AHU's terms are contiguous and a
+// batch of eight loads goes out before its adds; with COUNT also the number of
+// terms > 0. The terms are non-negative (flows, temperatures in K times
+// areas). The calling wavefront wrote them before an esync().
 template <bool COUNT>
-__device__ __forceinline__ double ahu_list_sum(const int* off, const int* idx, const double* vals, int a, int& npos) {
+__device__ __forceinline__ double ahu_range_sum(const double* vals, const int* off, int a, int& npos) {
     double s = 0.0;
     int np = 0;
     const int t1 = off[a + 1];
-    int t = off[a];
-    for (; t + 8 <= t1; t += 8) {
-        int i8[8];
+    for (int t = off[a]; t < t1; t += 8) {
+        // past the list's end the loads repeat its last term and the adds take
+        // +0.0, which leaves the (non-negative) sum unchanged
         double v8[8];
 #pragma unroll
-        for (int u = 0; u < 8; u++) i8[u] = idx[t + u];
-#pragma unroll
-        for (int u = 0; u < 8; u++) v8[u] = vals[i8[u]];
+        for (int u = 0; u < 8; u++) v8[u] = vals[min(t + u, t1 - 1)];
 #pragma unroll
         for (int u = 0; u < 8; u++) {
-            s += v8[u];
-            if (COUNT) np += v8[u] > 0.0 ? 1 : 0;
+            const double x = t + u < t1 ? v8[u] : 0.0;
+            s += x;
+            if (COUNT) np += x > 0.0 ? 1 : 0;
         }
-    }
-    for (; t < t1; t++) {
-        const double x = vals[idx[t]];
-        s += x;
-        if (COUNT) np += x > 0.0 ? 1 : 0;
     }
     npos = np;
     return s;
@@ -341,6 +336,9 @@ struct Tab {
     SBK_TAB(int, ahu_vavs)
     SBK_TAB(int, ahu_col_off)
     SBK_TAB(int, ahu_cols)
+    SBK_TAB(int, vav_lpos)
+    SBK_TAB(int, col_lpos)
+    SBK_TAB(double, ahu_area)
     SBK_TAB(int, cv_off)
     SBK_TAB(int, cv_node)
     SBK_TAB(int, cv_coff)
@@ -367,7 +365,7 @@ struct Ctx {
     double *recirc, *sat, *fan, *flow, *plant;
     int *run, *coolreq, *ip;
     uint8_t *mode, *prev_valid, *dcmd_set, *rcmd_set, *occ_state, *occV;
-    double *slots, *zq, *unres, *fdem, *rwen, *g, *tair;
+    double *slots, *zq, *unres, *fdem, *rwen, *lsum, *g, *tair;
     double *wsum, *atotal, *satv, *demand, *fdsum, *red, *misc;
     double* cal;             // the two calendar sections of the state image
     const double* row;       // this step's calendar values (RW_*), the aux-time row after them
@@ -431,6 +429,7 @@ __device__ __forceinline__ void bind(Ctx& c, const unsigned char* img, unsigned 
     c.unres = (double*)(env + l.vtmp);
     c.fdem = c.unres + L->nv;
     c.rwen = c.fdem + L->nv;
+    c.lsum = c.rwen + L->nv;
     c.g = (double*)(env + l.g);
     c.tair = (double*)(env + l.tair);
     double* a = (double*)(env + l.atmp);
@@ -580,9 +579,10 @@ __device__ __forceinline__ double vav_temp(const Ctx& c, const double* zmean, in
 // c.fdem (scratch until the coupled-column pass) holds the VAV's zone area,
 // whose sign says whether the VAV senses a zone at all.
 // The VAVs' terms of their AHU's return-air mean: sensing * area into c.rwen
-// (every VAV has zone area: the host refuses one without; the coupled-column
-// pass writes c.rwen only after the first wavefront has waited for these
-// sums).
+// at the VAV's position in its AHU's list (the coupled-column pass writes
+// c.rwen only after the first wavefront has waited for these sums); the
+// areas' per-AHU sums are a layout table (every VAV has zone area: the host
+// refuses one without).
 template <int U>
 __device__ __forceinline__ void vav_sensing(Ctx& c) {
     const int nv = c.L->nv, lane = ln();
@@ -606,7 +606,7 @@ __device__ __forceinline__ void vav_sensing(Ctx& c) {
             if (ok[u]) {
                 c.sensing[v[u]] = tv[u];
                 c.fdem[v[u]] = area[u];
-                c.rwen[v[u]] = tv[u] * varea[u];
+                c.rwen[c.t.vav_lpos()[v[u]]] = tv[u] * varea[u];
             }
         }
     }
@@ -1269,8 +1269,9 @@ __device__ __forceinline__ void decode_apply(Ctx& c) {
 
 // VAV pass of the pre-step (sb_sim.c:368-384, :316-355, :382-387): sensed
 // temperature, thermostat mode, damper and reheat settings, unrestricted flow
-// (c.unres, which the AHUs' demand sums read), and each VAV's AHU in the
-// register slots r = pass * U + u (VAV lane + 64 r) for the flow ratios.
+// (c.unres by VAV for the column pass, c.lsum at the VAV's position in its
+// AHU's list for the AHUs' demand sums), and each VAV's AHU in the register
+// slots r = pass * U + u (VAV lane + 64 r) for the flow ratios.
 // U VAVs per lane per pass, all loads of a pass before any store.
 template <int U>
 __device__ __forceinline__ void vav_pass(Ctx& c, int comfort, double& ffs_part, int (&vahu)[SBK_VPL]) {
@@ -1282,7 +1283,7 @@ __device__ __forceinline__ void vav_pass(Ctx& c, int comfort, double& ffs_part, 
     for (int pass = 0; pass < upasses<U>(); pass++) {
         const int base = pass * 64 * U;
         if (base >= nv) break;
-        int v[U], a[U], mode[U], pv[U], dset[U], rset[U], run[U];
+        int v[U], a[U], lp[U], mode[U], pv[U], dset[U], rset[U], run[U];
         bool ok[U];
         double tv[U], area[U], vc0[U], vc1[U], vc2[U], vc4[U], dcmd[U], rcmd[U], dmp[U], rht[U];
         double fan[U], amin[U], varea[U];
@@ -1313,6 +1314,7 @@ __device__ __forceinline__ void vav_pass(Ctx& c, int comfort, double& ffs_part, 
             dmp[u] = c.damper[v[u]];
             rht[u] = c.reheat[v[u]];
             a[u] = c.t.vav_ahu()[v[u]];
+            lp[u] = c.t.vav_lpos()[v[u]];
             varea[u] = c.t.vav_area()[v[u]];
         }
 #pragma unroll
@@ -1355,6 +1357,7 @@ __device__ __forceinline__ void vav_pass(Ctx& c, int comfort, double& ffs_part, 
                     c.reheat[v[u]] = reheat;
                 }
                 c.unres[v[u]] = un;
+                c.lsum[lp[u]] = un;
                 ffs_part += reheat * vc1[u];
                 vahu[pass * U + u] = a[u];
             }
@@ -1436,7 +1439,7 @@ __device__ __forceinline__ void coupled_columns(Ctx& c, double ffs, double tf, d
                 c.g[col[u]] = g;
                 c.tair[col[u]] = ta;
                 c.rwen[col[u]] = rw;
-                c.fdem[col[u]] = fd;
+                c.fdem[c.t.col_lpos()[col[u]]] = fd;
                 total_rw += rw;
                 cmin = fmin(cmin, ta);
                 cmax = fmax(cmax, ta);
@@ -1541,7 +1544,7 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P, int* sy) {
     double dm = 0.0;
     if (ln() < na) {
         int unused;
-        dm = ahu_list_sum<false>(c.t.ahu_vav_off(), c.t.ahu_vavs(), c.unres, ln(), unused);
+        dm = ahu_range_sum<false>(c.lsum, c.t.ahu_vav_off(), ln(), unused);
     }
     env_wait(sy + SY_RET, 1);   // the helper's return-air sums
     STAMP(21);
@@ -1591,11 +1594,12 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P, int* sy) {
     STAMP(22);
     esync();
     // AHU flow (clamped to the AHU's maximum) and cooling requests: by lane a
-    // over its columns' flow demands (c.fdem; 0 where the VAV has no zone
-    // area), the requests its columns with a demand > 0
+    // over its columns' flow demands (c.fdem at each column's position in the
+    // AHU's list; 0 where the VAV has no zone area), the requests its columns
+    // with a demand > 0
     double f = 0.0;
     int cnt = 0;
-    if (ln() < na) f = ahu_list_sum<true>(c.t.ahu_col_off(), c.t.ahu_cols(), c.fdem, ln(), cnt);
+    if (ln() < na) f = ahu_range_sum<true>(c.fdem, c.t.ahu_col_off(), ln(), cnt);
     wave_sum_min_max(total_rw, cmin, cmax);
     STAMP(23);
     STAMP(24);
@@ -2322,9 +2326,9 @@ __device__ __forceinline__ void step_post(Ctx& c) {
 }
 
 // 3C reward (sb_reward.c:31-155) on the post-step state and new occupancy.
-// VAV temperatures and areas of the reward's AHU terms (sb_reward.c:62-98):
-// temperature * area into c.unres and area into c.fdem (both 0 for a VAV
-// without zone area; the pre-step's scratch, free by now).
+// VAV temperatures of the reward's AHU terms (sb_reward.c:62-98): temperature
+// * area into c.unres at the VAV's position in its AHU's list (the pre-step's
+// scratch, free by now); the areas' per-AHU sums are a layout table.
 template <int U>
 __device__ __forceinline__ void reward_vavs(Ctx& c, const double* zm) {
     const int nv = c.L->nv, lane = ln();
@@ -2344,11 +2348,7 @@ __device__ __forceinline__ void reward_vavs(Ctx& c, const double* zm) {
         vav_temps<U>(c, zm, v, tv, area);
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            if (ok[u]) {
-                const bool live = area[u] > 0.0;
-                c.unres[v[u]] = live ? tv[u] * area[u] : 0.0;
-                c.fdem[v[u]] = live ? area[u] : 0.0;
-            }
+            if (ok[u]) c.unres[c.t.vav_lpos()[v[u]]] = tv[u] * area[u];
         }
     }
 }
@@ -2385,8 +2385,8 @@ __device__ __forceinline__ void reward_ahu(Ctx& c, const double* zm, double& blo
     if (ln() < L->na) {
         const int a = ln();
         int unused;
-        const double ws = ahu_list_sum<false>(c.t.ahu_vav_off(), c.t.ahu_vavs(), c.unres, a, unused);
-        const double at = ahu_list_sum<false>(c.t.ahu_vav_off(), c.t.ahu_vavs(), c.fdem, a, unused);
+        const double ws = ahu_range_sum<false>(c.unres, c.t.ahu_vav_off(), a, unused);
+        const double at = c.t.ahu_area()[a];
         double rc = (at > 0.0) ? ws / at : tmean;
         double st = ahu_static(c, a);
         double fe = c.t.ahu_c()[a * 9 + 5];
@@ -2642,8 +2642,8 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
         if (ln() < L->na) {
             const int a = ln();
             int unused;
-            c.wsum[a] = ahu_list_sum<false>(c.t.ahu_vav_off(), c.t.ahu_vavs(), c.rwen, a, unused);
-            c.atotal[a] = ahu_list_sum<false>(c.t.ahu_vav_off(), c.t.ahu_vavs(), c.t.vav_area(), a, unused);
+            c.wsum[a] = ahu_range_sum<false>(c.rwen, c.t.ahu_vav_off(), a, unused);
+            c.atotal[a] = c.t.ahu_area()[a];
         }
         env_post(sy + SY_RET, 1);
     }

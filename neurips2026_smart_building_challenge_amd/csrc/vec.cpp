@@ -513,7 +513,7 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     // slots: the LU entries and vector, or (relaxation) the node heat inputs
     Ls.slots = l; l += 8 * (relax ? n : P.n_slots); l = align_up(l, 16);
     Ls.zq = l; l += 8 * nz;
-    Ls.vtmp = l; l += 8 * 3 * nv;
+    Ls.vtmp = l; l += 8 * 4 * nv;
     Ls.g = l; l += 8 * std::max(k, 1);
     Ls.tair = l; l += 8 * std::max(k, 1);
     Ls.atmp = l; l += 8 * 8 * na;
@@ -713,6 +713,22 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
             G.ahu_vavs = I.add(vl);
             G.ahu_col_off = I.add(coff);
             G.ahu_cols = I.add(cl);
+            // each entry's position in its AHU's list (the step writes per-AHU
+            // sum terms there, so an AHU's terms are contiguous), and each
+            // AHU's VAV area in the order the step would sum it
+            std::vector<int> vpos(nv, -1), cpos(k, -1);
+            for (int t = 0; t < (int)vl.size(); t++) vpos[vl[t]] = t;
+            for (int t = 0; t < (int)cl.size(); t++) cpos[cl[t]] = t;
+            for (int v = 0; v < nv; v++)
+                if (vpos[v] < 0) return (*err = "VAV without an AHU"), false;
+            for (int c = 0; c < k; c++)
+                if (cpos[c] < 0) return (*err = "coupled column without an AHU"), false;
+            std::vector<double> aarea(na, 0.0);
+            for (int a = 0; a < na; a++)
+                for (int t = voff[a]; t < voff[a + 1]; t++) aarea[a] += vav_area[vl[t]];
+            G.vav_lpos = I.add(vpos);
+            G.col_lpos = I.add(cpos);
+            G.ahu_area = I.add(aarea);
         }
         G.act_src = I.add(src);
         G.air_slot = I.add(P.air_slot);
