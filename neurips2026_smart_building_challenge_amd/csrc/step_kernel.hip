@@ -261,6 +261,32 @@ __device__ __forceinline__ double ahu_range_sum(const double* vals, const int* o
     return s;
 }
 
+// Per-AHU sums of the list-ordered terms: lane a (< na) receives AHU a's. A
+// single AHU (a layout's whole VAV or column list, 40-128 terms) is summed over
+// the whole wavefront (one load a lane, a DPP tree); with more AHUs (fewer
+// terms each) one lane per AHU adds its terms in list order (ahu_range_sum).
+// Every lane of the wavefront must call it.
+template <bool COUNT>
+__device__ __forceinline__ double ahu_sums_of(const double* vals, const int* off, int na, int& npos) {
+    double sv = 0.0;
+    int np = 0;
+    if (na == 1) {
+        const int t1 = off[1];
+        int k = 0;
+        for (int t = ln(); t < t1; t += 64) {
+            const double v = vals[t];
+            sv += v;
+            if (COUNT) k += v > 0.0 ? 1 : 0;
+        }
+        sv = wave_sum(sv);
+        if (COUNT) np = wave_isum(k);
+    } else if (ln() < na) {
+        sv = ahu_range_sum<COUNT>(vals, off, ln(), np);
+    }
+    npos = np;
+    return sv;
+}
+
 // Inclusive prefix sum over the wavefront.
 __device__ __forceinline__ int wave_iscan(int v) {
     v += dpp_i<DPP_ROW_SHR + 1>(0, v);
@@ -1541,11 +1567,8 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P, int* sy) {
     STAMP(20);
     // each AHU's flow demand: the unrestricted flows of its VAVs, by lane a
     esync();
-    double dm = 0.0;
-    if (ln() < na) {
-        int unused;
-        dm = ahu_range_sum<false>(c.lsum, c.t.ahu_vav_off(), ln(), unused);
-    }
+    int unused_dm;
+    const double dm = ahu_sums_of<false>(c.lsum, c.t.ahu_vav_off(), na, unused_dm);
     env_wait(sy + SY_RET, 1);   // the helper's return-air sums
     STAMP(21);
     if (ln() < na) {
@@ -1597,9 +1620,8 @@ __device__ __forceinline__ void step_pre(Ctx& c, const KParams& P, int* sy) {
     // over its columns' flow demands (c.fdem at each column's position in the
     // AHU's list; 0 where the VAV has no zone area), the requests its columns
     // with a demand > 0
-    double f = 0.0;
-    int cnt = 0;
-    if (ln() < na) f = ahu_range_sum<true>(c.fdem, c.t.ahu_col_off(), ln(), cnt);
+    int cnt;
+    const double f = ahu_sums_of<true>(c.fdem, c.t.ahu_col_off(), na, cnt);
     wave_sum_min_max(total_rw, cmin, cmax);
     STAMP(23);
     STAMP(24);
@@ -2382,10 +2404,10 @@ __device__ __forceinline__ void reward_ahu(Ctx& c, const double* zm, double& blo
     if (L->nv > 64) reward_vavs<2>(c, zm);
     else reward_vavs<1>(c, zm);
     esync();
+    int unused;
+    const double ws = ahu_sums_of<false>(c.unres, c.t.ahu_vav_off(), L->na, unused);
     if (ln() < L->na) {
         const int a = ln();
-        int unused;
-        const double ws = ahu_range_sum<false>(c.unres, c.t.ahu_vav_off(), a, unused);
         const double at = c.t.ahu_area()[a];
         double rc = (at > 0.0) ? ws / at : tmean;
         double st = ahu_static(c, a);
@@ -2639,11 +2661,11 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
         // 382-387) by lane a, for the first wavefront's supply temperatures
         // (c.wsum / c.atotal: reward scratch, free until then)
         esync();
+        int unused;
+        const double ws = ahu_sums_of<false>(c.rwen, c.t.ahu_vav_off(), L->na, unused);
         if (ln() < L->na) {
-            const int a = ln();
-            int unused;
-            c.wsum[a] = ahu_range_sum<false>(c.rwen, c.t.ahu_vav_off(), a, unused);
-            c.atotal[a] = c.t.ahu_area()[a];
+            c.wsum[ln()] = ws;
+            c.atotal[ln()] = c.t.ahu_area()[ln()];
         }
         env_post(sy + SY_RET, 1);
     }
