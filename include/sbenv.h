@@ -370,11 +370,14 @@ const char* sbx_scenario_path(Env* envs, int scenario);
  * schedule the step kernel runs for the numeric LU of A + diag(g) plus both
  * triangular solves. Slot 0 holds 0.0, slot 1 is a write sink, slot 2 holds
  * 1.0; inv_base.. hold pivot reciprocals. Pass p is pass_info[4p..4p+3] =
- * {hdr_off, word_off, nact | maxcnt << 8 | has_pivot << 16, 0}: lane l < nact runs task
- * hdr[hdr_off + l] = target | mul << 16 | inv_target << 32 | count << 48 as
+ * {hdr_off, word_off, nact | maxcnt << 8 | has_pivot << 16 | lgmax << 17, 0}:
+ * lane l < nact holds hdr[hdr_off + l] = target | mul << 16 | inv_target << 32
+ * | flags << 48 (flags = log2 segment width | leader << 3 | count << 4) and
+ * terms words[word_off + l * stride + m], stride = maxcnt rounded up to 4
+ * ((0, 0) past the count); a task's segment of lanes computes
  * slot[target] = (slot[target] - sum_m slot[a_m] * slot[b_m]) * slot[mul],
- * then, when has_pivot, slot[inv_target] = 1 / slot[target]; term m is
- * words[word_off + m * nact + l] = a_m | b_m << 16 ((0, 0) past the count).
+ * then, when has_pivot, slot[inv_target] = 1 / slot[target]. A term word is
+ * a_m | b_m << 16, or with term_bits 12 three factors (below).
  * Arrays are owned by the library until sbx_plan_free. */
 typedef struct SbxPlan {
     int n;               /* unknowns */
@@ -423,6 +426,13 @@ typedef struct SbxPlan {
     const double* bx_val;
     const int* bx_col;
     const int* bx_trow;
+    /* term word format: 16 = a | b << 16 as above; 12 = a | b << 12 | v << 24,
+     * the product slot[a] * slot[scale_base + v] * slot[b] (slot scale_base
+     * holds 1.0, scale_base + 1 + k the reciprocal of pivot k = inv_base + k),
+     * used where n <= 255 and n_slots <= 4096: L is then stored unscaled
+     * (L[i][k] * U[k][k]) and its readers multiply by the reciprocal */
+    int term_bits;
+    int scale_base;
 } SbxPlan;
 int sbx_plan_layout(const char* blob_path, int width, SbxPlan* out);
 void sbx_plan_free(SbxPlan* p);

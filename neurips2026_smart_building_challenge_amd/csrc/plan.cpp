@@ -15,6 +15,18 @@
 //   y_i = w_i - sum_{k<i} L[i][k] y_k                          (forward)
 //   x_i = (y_i - sum_{j>i} U[i][j] x_j) * r_i                  (backward, in place)
 //
+// With compact terms (systems of at most 255 unknowns and 4,096 slots) L is
+// kept unscaled, L'[i][j] = L[i][j] * U[j][j], and every product that reads it
+// takes the reciprocal as a third factor:
+//
+//   U[i][j]  = S[i][j] - sum_{k<i} L'[i][k] r_k U[k][j]
+//   L'[i][j] = S[i][j] - sum_{k<j} L'[i][k] r_k U[k][j]
+//   y_i      = w_i - sum_{k<i} L'[i][k] r_k y_k
+//
+// so an L entry no longer waits for its column's pivot: a column costs one
+// level of the dependency chain instead of two (81 zones: 140 levels -> 94).
+// L'[i][k] * r_k rounds to the value the scaled form stores for L[i][k].
+//
 // Every task multiplies its result by a slot (the pivot reciprocal, or the
 // constant 1.0), so a pass runs without divergent branches; a pass holding a
 // diagonal task also computes the reciprocal of every lane's result and
@@ -53,13 +65,28 @@ namespace sbh {
 
 namespace {
 
+// One product of a task's sum: slot[a] * slot[r] * slot[b] (r = kSlotOne when
+// the product has two factors).
+struct Term {
+    int a, b, r;
+};
+
 struct Task {
     int target;
     int mul;          // slot multiplying the result (reciprocal or kSlotOne)
     int inv_target;   // slot receiving 1/result (kSlotSink unless a pivot)
     int level;
-    std::vector<std::pair<int, int>> terms;
+    std::vector<Term> terms;
 };
+
+// a | b << 16 (16-bit terms, r always kSlotOne), or a | b << 12 | v << 24
+// (compact terms), v = r - scale_base: 0 reads the scale base's 1.0, k + 1 the
+// reciprocal of pivot k
+uint32_t term_word(const SolvePlan& P, const Term& t) {
+    if (P.term_bits == 16) return (uint32_t)t.a | ((uint32_t)t.b << 16);
+    const int v = t.r == kSlotOne ? 0 : t.r - P.scale_base;
+    return (uint32_t)t.a | ((uint32_t)t.b << 12) | ((uint32_t)v << 24);
+}
 
 bool fail(std::string* err, const std::string& msg) {
     *err = msg;
@@ -129,7 +156,8 @@ bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
     }
 
     // slots: 0 zero, 1 sink, 2 one, then per k: U row k (diagonal first),
-    // L column k; then the n pivot reciprocals; then the vector
+    // L column k; then a second 1.0 (the scale base), the n pivot reciprocals,
+    // the vector
     std::unordered_map<long long, int> slot;
     slot.reserve(8 * n);
     auto key = [n](int i, int j) { return (long long)i * n + j; };
@@ -139,10 +167,16 @@ bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
         for (int j : Urow[k]) slot[key(k, j)] = ns_++;
         for (int i : Lcol[k]) slot[key(i, k)] = ns_++;
     }
-    P.inv_base = ns_;
-    P.vec_base = ns_ + n;
-    P.n_slots = ns_ + 2 * n;
+    P.scale_base = ns_;
+    P.inv_base = ns_ + 1;
+    P.vec_base = P.inv_base + n;
+    P.n_slots = P.vec_base + n;
     if (P.n_slots > 65535) return fail(err, "system too large for 16-bit slots");
+    // compact terms (12-bit slots and the 8-bit scale index) where they fit:
+    // L then stays unscaled and each product reading it takes the column's
+    // reciprocal as its third factor
+    P.term_bits = (P.n_slots <= (1 << 12) && n <= 255) ? 12 : 16;
+    const bool defer = P.term_bits == 12;
 
     // fill closure: every update target must be structural
     for (int k = 0; k < n; k++)
@@ -153,6 +187,7 @@ bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
     // initial values: permuted A
     P.slot_init.assign(P.n_slots, 0.0);
     P.slot_init[kSlotOne] = 1.0;
+    P.slot_init[P.scale_base] = 1.0;
     for (int c = 0; c < n; c++)
         for (int p = Ap[c]; p < Ap[c + 1]; p++) {
             int r = Ai[p];
@@ -201,7 +236,7 @@ bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
     std::vector<int> ks;
     // target, multiplier slot (reciprocal to depend on, or kSlotOne), reciprocal
     // slot to produce (or kSlotSink), terms, extra dependency level
-    auto add_task = [&](int target, int mul, int inv_target, std::vector<std::pair<int, int>>&& terms,
+    auto add_task = [&](int target, int mul, int inv_target, std::vector<Term>&& terms,
                         int extra_level) {
         // split into chains of at most kTaskTerms terms; the last piece
         // scales and produces the reciprocal
@@ -211,9 +246,10 @@ bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
         int prev = extra_level;
         for (size_t pc = 0; pc < pieces; pc++) {
             size_t lo = pc * kTaskTerms, hi = std::min(nt, lo + kTaskTerms);
-            std::vector<std::pair<int, int>> part(terms.begin() + lo, terms.begin() + hi);
+            std::vector<Term> part(terms.begin() + lo, terms.begin() + hi);
             int lv = prev;
-            for (auto& t : part) lv = std::max(lv, std::max(slot_level[t.first], slot_level[t.second]));
+            for (auto& t : part)
+                lv = std::max(lv, std::max(slot_level[t.a], std::max(slot_level[t.b], slot_level[t.r])));
             const bool last = pc + 1 == pieces;
             if (last) lv = std::max(lv, slot_level[mul]);
             lv += 1;
@@ -235,32 +271,34 @@ bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
             intersect(Lrow[r], Ucol[j], r, ks);
             const bool diag = j == r;
             if (ks.empty() && !diag) continue;   // slot already holds its value
-            std::vector<std::pair<int, int>> terms;
-            for (int m : ks) terms.push_back({slot[key(r, m)], slot[key(m, j)]});
+            std::vector<Term> terms;
+            for (int m : ks) terms.push_back({slot[key(r, m)], slot[key(m, j)], defer ? ib + m : kSlotOne});
             add_task(slot[key(r, j)], kSlotOne, diag ? ib + r : kSlotSink, std::move(terms), 0);
         }
-        // L column r (i > r): terms over k < r, scaled by 1/U[r][r]
+        // L column r (i > r): terms over k < r, scaled by 1/U[r][r] (compact
+        // terms: left unscaled, L[i][r] * U[r][r], so the task does not wait
+        // for the pivot; its readers multiply by the reciprocal)
         for (int i : Lcol[r]) {
             intersect(Lrow[i], Ucol[r], r, ks);
-            std::vector<std::pair<int, int>> terms;
-            for (int m : ks) terms.push_back({slot[key(i, m)], slot[key(m, r)]});
-            add_task(slot[key(i, r)], ib + r, kSlotSink, std::move(terms), 0);
+            std::vector<Term> terms;
+            for (int m : ks) terms.push_back({slot[key(i, m)], slot[key(m, r)], defer ? ib + m : kSlotOne});
+            add_task(slot[key(i, r)], defer ? kSlotOne : ib + r, kSlotSink, std::move(terms), 0);
         }
     }
     // forward solve
     std::vector<int> y_read_max(n, 0);
     for (int i = 0; i < n; i++) {
         if (Lrow[i].empty()) continue;
-        std::vector<std::pair<int, int>> terms;
-        for (int m : Lrow[i]) terms.push_back({slot[key(i, m)], vb + m});
+        std::vector<Term> terms;
+        for (int m : Lrow[i]) terms.push_back({slot[key(i, m)], vb + m, defer ? ib + m : kSlotOne});
         add_task(vb + i, kSlotOne, kSlotSink, std::move(terms), 0);
         for (int m : Lrow[i]) y_read_max[m] = std::max(y_read_max[m], slot_level[vb + i]);
     }
     // backward solve, in place over y; a slot is overwritten only after its
     // last forward reader
     for (int i = n - 1; i >= 0; i--) {
-        std::vector<std::pair<int, int>> terms;
-        for (int j : Urow[i]) terms.push_back({slot[key(i, j)], vb + j});
+        std::vector<Term> terms;
+        for (int j : Urow[i]) terms.push_back({slot[key(i, j)], vb + j, kSlotOne});
         int lv0 = std::max(slot_level[vb + i], y_read_max[i]);
         add_task(vb + i, ib + i, kSlotSink, std::move(terms), lv0);
     }
@@ -351,9 +389,7 @@ bool build_plan(const Blob& b, int width, SolvePlan* out, std::string* err) {
                 const Task& t = tasks[l.task];
                 for (int m = 0; m < stride; m++) {
                     const size_t q = (size_t)l.j + (size_t)m * l.seg;
-                    P.words.push_back(q < t.terms.size()
-                                      ? (uint32_t)t.terms[q].first | ((uint32_t)t.terms[q].second << 16)
-                                      : 0u);
+                    P.words.push_back(q < t.terms.size() ? term_word(P, t.terms[q]) : 0u);
                 }
             }
             P.passes.push_back(pi);

@@ -42,6 +42,10 @@ constexpr int kPlanDepth = 4;
 struct SolvePlan {
     int n = 0, k = 0, width = 0;
     int n_slots = 0, vec_base = 0, inv_base = 0, n_levels = 0, n_tasks = 0;
+    // term word format: 16 (a | b << 16) or 12 (a | b << 12 | v << 24, the
+    // product slot[a] * slot[scale_base + v] * slot[b]); scale_base holds 1.0
+    // and precedes the reciprocals (inv_base = scale_base + 1)
+    int term_bits = 16, scale_base = 0;
     long long n_pairs = 0;           // multiply-subtract terms
     long long n_divs = 0;
     std::vector<int> pos;            // node -> permuted position
@@ -50,6 +54,7 @@ struct SolvePlan {
     std::vector<PassInfo> passes;
     std::vector<uint64_t> hdr;       // per lane: target | mul << 16 | inv_target << 32 | flags << 48
     std::vector<uint32_t> words;     // term m of lane l at word_off + l * stride + m, stride = maxcnt rounded up to 4
+                                     // (format: term_bits)
     int n_pass() const { return (int)passes.size(); }
 };
 

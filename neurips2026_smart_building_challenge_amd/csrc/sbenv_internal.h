@@ -192,6 +192,8 @@ struct DevLayout {
     int solver;                        // SOLVER_LU or SOLVER_RELAX
     int rx_terms;                      // longest off-diagonal (or off-block) row (relaxation)
     int rx_block;                      // block-Jacobi form with 1 or 2 block slots per lane (bx_*), 0: point form (rx_*)
+    int lu_sbase;                      // compact LU terms (a | b << 12 | v << 24): the 1.0 slot before the
+                                       // reciprocals, third factor slot[lu_sbase + v]; 0: terms a | b << 16
     double rx_stop;                    // rho / (1 - rho)
     StateLayout st;
     LdsLayout lds;

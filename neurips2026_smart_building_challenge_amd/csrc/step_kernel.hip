@@ -1705,21 +1705,37 @@ __device__ __forceinline__ double recip(double x) {
 }
 
 // One group of 4 terms: the slot reads (issued early) and the products
-// subtracted in term order.
+// subtracted in term order. A term word is a | b << 16 (C3 false: the product
+// slot[a] * slot[b]) or a | b << 12 | v << 24 (C3: slot[a] * rs[v] * slot[b],
+// rs[0] = 1.0 and rs[k + 1] the reciprocal of pivot k, which unscaled L
+// entries take when they are read).
+template <bool C3>
 struct TermGroup {
-    double x[4], y[4];
+    double x[4], y[4], z[C3 ? 4 : 1];
 };
-__device__ __forceinline__ void load_terms(const double* slots, const PassRegs& r, int m0, TermGroup& g) {
+template <bool C3>
+__device__ __forceinline__ void load_terms(const double* slots, const double* rs, const PassRegs& r, int m0,
+                                           TermGroup<C3>& g) {
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const uint32_t w = r.w[m0 + j];
-        g.x[j] = slots[w & 0xffffu];
-        g.y[j] = slots[w >> 16];
+        if constexpr (C3) {
+            g.x[j] = slots[w & 0xfffu];
+            g.y[j] = slots[(w >> 12) & 0xfffu];
+            g.z[j] = rs[w >> 24];
+        } else {
+            g.x[j] = slots[w & 0xffffu];
+            g.y[j] = slots[w >> 16];
+        }
     }
 }
-__device__ __forceinline__ double sub_terms(double acc, const TermGroup& g) {
+template <bool C3>
+__device__ __forceinline__ double sub_terms(double acc, const TermGroup<C3>& g) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) acc = fma(-g.x[j], g.y[j], acc);
+    for (int j = 0; j < 4; j++) {
+        if constexpr (C3) acc = fma(-(g.x[j] * g.z[j]), g.y[j], acc);
+        else acc = fma(-g.x[j], g.y[j], acc);
+    }
     return acc;
 }
 
@@ -1734,7 +1750,8 @@ __device__ __forceinline__ double sub_terms(double acc, const TermGroup& g) {
 // longest lane (its stride is that rounded up to 4, so a group never reaches
 // another lane's words); terms past a lane's count are (0, 0) and read slot
 // 0 = 0.
-__device__ __forceinline__ void run_pass(double* slots, const PassRegs& r) {
+template <bool C3>
+__device__ __forceinline__ void run_pass(double* slots, const double* rs, const PassRegs& r) {
     const int meta = r.meta;
     const int tgt = (int)(r.h & 0xffffu);
     const int mul = (int)((r.h >> 16) & 0xffffu);
@@ -1749,17 +1766,17 @@ __device__ __forceinline__ void run_pass(double* slots, const PassRegs& r) {
     static_assert(SBK_KMAX == 16, "term groups below are written for 16 terms a lane");
     const int ng = (pass_maxcnt(meta) + 3) >> 2;
     if (ng > 0) {
-        TermGroup ga, gb;
-        load_terms(slots, r, 0, ga);
-        if (ng > 1) load_terms(slots, r, 4, gb);
-        acc = sub_terms(acc, ga);
+        TermGroup<C3> ga, gb;
+        load_terms<C3>(slots, rs, r, 0, ga);
+        if (ng > 1) load_terms<C3>(slots, rs, r, 4, gb);
+        acc = sub_terms<C3>(acc, ga);
         if (ng > 1) {
-            if (ng > 2) load_terms(slots, r, 8, ga);
-            acc = sub_terms(acc, gb);
+            if (ng > 2) load_terms<C3>(slots, rs, r, 8, ga);
+            acc = sub_terms<C3>(acc, gb);
             if (ng > 2) {
-                if (ng > 3) load_terms(slots, r, 12, gb);
-                acc = sub_terms(acc, ga);
-                if (ng > 3) acc = sub_terms(acc, gb);
+                if (ng > 3) load_terms<C3>(slots, rs, r, 12, gb);
+                acc = sub_terms<C3>(acc, ga);
+                if (ng > 3) acc = sub_terms<C3>(acc, gb);
             }
         }
     }
@@ -1794,13 +1811,14 @@ __device__ __forceinline__ void run_pass(double* slots, const PassRegs& r) {
 // runs. Only that one pass's loads are in flight across the loop's back edge,
 // so the compiler's memory waits stay exact (a wait for pass k of a group
 // leaves the later passes' loads in flight).
-template <int W>
+template <int W, bool C3>
 __device__ __forceinline__ void run_plan(const SBK_C DevLayout* L, double* slots, const int4* rec,
                                          unsigned long long* pts) {
     static_assert(W == 64, "the solve plan runs on one wavefront");
     constexpr int D = SBK_PLAN_DEPTH;
     const int np = L->n_pass;
     if (np == 0) return;
+    const double* rs = slots + L->lu_sbase;
     PassRegs R[D];
     fetch_pass(L, rec[0], R[0]);
     for (int p = 0; p < np; p += D) {
@@ -1817,7 +1835,7 @@ __device__ __forceinline__ void run_plan(const SBK_C DevLayout* L, double* slots
                 __builtin_amdgcn_sched_barrier(0);
             }
             settle_pass(R[k]);
-            run_pass(slots, R[k]);
+            run_pass<C3>(slots, rs, R[k]);
             wave_lds_sync();
         }
     }
@@ -2300,7 +2318,8 @@ __device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
     STAMP(5);
     // level schedule: LU of the permuted system, forward and backward solves
     unsigned long long* pts = (P.pass_ts && c.e == P.pass_ts_env && ln() == 0) ? P.pass_ts : nullptr;
-    run_plan<W>(L, slots, reinterpret_cast<const int4*>(c.prec), pts);
+    if (L->lu_sbase) run_plan<W, true>(L, slots, reinterpret_cast<const int4*>(c.prec), pts);
+    else run_plan<W, false>(L, slots, reinterpret_cast<const int4*>(c.prec), pts);
     STAMP(6);
     for (int t = ln(); t < n; t += W) {
         double y = slots[vb + c.t.pos()[t]];

@@ -475,6 +475,7 @@ bool make_layout(const sbh::Blob& b, int width, int solve, HostLayout* H, Arena&
     D.n = n; D.nz = nz; D.nv = nv; D.na = na; D.k = k; D.n_act = n_act; D.n_cont = ncont; D.n_disc = ndisc;
     D.n_dev = n_dev; D.n_aux = n_aux; D.nassign = nassign;
     D.n_slots = P.n_slots; D.vec_base = P.vec_base; D.n_pass = P.n_pass(); D.width = width;
+    D.lu_sbase = P.term_bits == 12 ? P.scale_base : 0;
     D.max_room_cells = max_cells;
     D.solver = relax ? sbk::SOLVER_RELAX : sbk::SOLVER_LU;
     D.rx_block = use_block ? (BP.n_blocks > 64 ? 2 : 1) : 0;
@@ -2279,6 +2280,8 @@ int sbx_plan_layout(const char* blob_path, int width, SbxPlan* out) {
     out->n_slots = P.n_slots;
     out->vec_base = P.vec_base;
     out->inv_base = P.inv_base;
+    out->term_bits = P.term_bits;
+    out->scale_base = P.scale_base;
     out->n_pass = P.n_pass();
     out->n_levels = P.n_levels;
     out->n_tasks = P.n_tasks;

@@ -85,7 +85,8 @@ class SbxPlan(ctypes.Structure):
                 ("bx_row", ctypes.POINTER(ctypes.c_int)), ("bx_diag", ctypes.POINTER(ctypes.c_double)),
                 ("bx_air", ctypes.POINTER(ctypes.c_int)), ("bx_in", ctypes.POINTER(ctypes.c_double)),
                 ("bx_val", ctypes.POINTER(ctypes.c_double)), ("bx_col", ctypes.POINTER(ctypes.c_int)),
-                ("bx_trow", ctypes.POINTER(ctypes.c_int))]
+                ("bx_trow", ctypes.POINTER(ctypes.c_int)),
+                ("term_bits", ctypes.c_int), ("scale_base", ctypes.c_int)]
 
 
 class SbxPolicy(ctypes.Structure):
@@ -227,7 +228,7 @@ def plan_layout(blob: str | Path, width: int = 64) -> dict[str, np.ndarray]:
         out = {
             "n": p.n, "width": p.width, "n_slots": p.n_slots, "vec_base": p.vec_base, "inv_base": p.inv_base,
             "n_pass": p.n_pass, "n_levels": p.n_levels, "n_tasks": p.n_tasks, "n_pairs": p.n_pairs,
-            "kmax": p.kmax, "k": p.k,
+            "kmax": p.kmax, "k": p.k, "term_bits": p.term_bits, "scale_base": p.scale_base,
             "pass_info": arr(p.pass_info, 4 * p.n_pass).reshape(-1, 4),
             "hdr": arr(p.hdr, p.n_hdr),
             "words": arr(p.words, p.n_words),

@@ -46,7 +46,12 @@ def run_plan(pl, slots):
         for m in range(maxcnt):
             w = W[:, m]
             assert np.all(w[cnt <= m] == 0), "terms past a lane's count must be (0, 0)"
-            acc = acc - slots[w & 0xFFFF] * slots[w >> 16]
+            if pl["term_bits"] == 12:
+                # slot[a] * (1.0 or a pivot reciprocal) * slot[b]
+                z = slots[pl["scale_base"] + (w >> 24)]
+                acc = acc - (slots[w & 0xFFF] * z) * slots[(w >> 12) & 0xFFF]
+            else:
+                acc = acc - slots[w & 0xFFFF] * slots[w >> 16]
         assert np.all(W[:, maxcnt:] == 0)
         for k in range(lgmax):
             partner = np.minimum(lanes ^ (1 << k), nact - 1)
@@ -57,7 +62,7 @@ def run_plan(pl, slots):
             with np.errstate(divide="ignore"):
                 slots[invt] = 1.0 / acc
         slots[1] = 0.0
-    assert slots[0] == 0.0 and slots[2] == 1.0
+    assert slots[0] == 0.0 and slots[2] == 1.0 and slots[pl["scale_base"]] == 1.0
 
 
 def solve_by_plan(pl, g, b):
@@ -91,6 +96,62 @@ def test_plan_solves_system(zones, ahus, tmp_path):
         assert np.max(np.abs(x - xt)) <= 1e-12 * np.max(np.abs(xt))
     assert pl["n_pairs"] > 0 and pl["n_levels"] <= pl["n_pass"]
     assert ((pl["pass_info"][:, 2] >> 8) & 0xFF).max() <= pl["kmax"]
+    # these systems fit the compact terms: L unscaled, reciprocals read by its users
+    assert pl["term_bits"] == 12 and pl["scale_base"] == pl["inv_base"] - 1
+    assert pl["n_slots"] <= 4096 and n <= 255
+
+
+def _elimination_height(pl, d):
+    """Height of the elimination tree of the baked permuted pattern (longest
+    chain of columns j -> parent(j) = first row below j in L's column j)."""
+    n = pl["n"]
+    Lp, Li = d["lu_L_indptr"], d["lu_L_indices"]
+    parent = np.full(n, -1)
+    for j in range(n):
+        below = Li[Lp[j]:Lp[j + 1]]
+        below = below[below > j]
+        if below.size:
+            parent[j] = below.min()
+    h = np.ones(n, dtype=np.int64)
+    for j in range(n):
+        if parent[j] >= 0:
+            h[parent[j]] = max(h[parent[j]], h[j] + 1)
+    return int(h.max())
+
+
+@pytest.mark.parametrize("zones,ahus", [(41, 1), (81, 4)])
+def test_plan_depth_follows_elimination_tree(zones, ahus, tmp_path):
+    """With unscaled L a column adds one level to the factorization's chain, so
+    the level count is at most about twice the elimination tree's height (one
+    factorization level and one back-substitution level per column of the
+    longest chain, plus the extra levels of long dot products split into
+    pieces); the scaled form needs about three per column."""
+    p, _ = golden_blob((zones, ahus), (10.0, 8.0, 499), tmp_path)
+    pl = E.plan_layout(p, 64)
+    h = _elimination_height(pl, read_sbb(p))
+    assert pl["term_bits"] == 12
+    assert 2 * h - 2 <= pl["n_levels"] <= 2 * h + 4, (pl["n_levels"], h)
+
+
+def test_plan_wide_terms_above_compact_limits(tmp_path):
+    """A system above 255 unknowns keeps 16-bit terms with scaled L, and the
+    plan still solves it."""
+    import scipy.sparse as sp
+
+    p, _ = golden_blob((97, 4), (10.0, 8.0, 499), tmp_path)
+    pl = E.plan_layout(p, 64)
+    d = read_sbb(p)
+    n = pl["n"]
+    assert n > 255 and pl["term_bits"] == 16
+    A = sp.csc_matrix((d["A_system_data"], d["A_system_indices"], d["A_system_indptr"]), shape=(n, n)).toarray()
+    rng = np.random.default_rng(97)
+    g = rng.uniform(0.0, 900.0, pl["k"])
+    b = rng.normal(size=n) * 1e4
+    x = solve_by_plan(pl, g, b)
+    Ag = A.copy()
+    Ag[pl["air_node"], pl["air_node"]] += g
+    xt = np.linalg.solve(Ag, b)
+    assert np.max(np.abs(x - xt)) <= 1e-12 * np.max(np.abs(xt))
 
 
 def _rewrite(src, dst, **over):
