@@ -253,6 +253,20 @@ def test_gpu_step_parity_start_offsets(mixed_dir, solver):
     vec.close()
 
 
+def test_gpu_lu_wide_terms_parity(tmp_path):
+    """A 97-zone layout (291 unknowns, 4,669 LU slots) is past the compact term
+    words, so its LU plan keeps 16-bit two-factor terms with L scaled at its
+    own task; solver=lu against the oracle twins over an auto-reset."""
+    p, _ = golden_blob((97, 4), (5.0, 7.0, 501), tmp_path)
+    assert E.plan_layout(p, 64)["term_bits"] == 16
+    say("parity (lu, 16-bit terms): 2 envs of 97 zones, 60 steps")
+    vec = E.VecEnv(2, blob=str(p), max_steps=40, solver="lu", trace_air=1)
+    twins = [Twin(vec, i, 40) for i in range(vec.n)]
+    _run_parity(vec, twins, 60, "lu wide", air=True)
+    check_solver(vec, "lu")
+    vec.close()
+
+
 def test_gpu_desync_truncation_parity(mixed_dir):
     """desync = 1 (the reference GPU env's meaning, smart_buildings.cu:2808-2815):
     env i's first episode ends after 1 + hash(i) mod 40 steps, later ones after 40;
