@@ -323,7 +323,7 @@ enum { KMODE_STEP = 0, KMODE_RESET = 1 };
 // arrays complete (SY_STORED); the helper's convection permutation of the
 // step (SY_CONV).
 enum { SY_PRE = 0, SY_POST = 1, SY_HALF = 2, SY_SENS = 3, SY_PART = 4, SY_RET = 18, SY_CONV = 19,
-       SY_STORED = 20, SY_WORDS = 21 };
+       SY_STORED = 20, SY_SLOTS = 21, SY_WORDS = 22 };
 
 // A workgroup's envs: order[first .. first + count) all of one layout, with
 // the layout's staging burst inputs (copied from its DevLayout) and each

@@ -2270,7 +2270,7 @@ __device__ __forceinline__ void relax_block_solve(Ctx& c, double ambient, double
 // nodes), then (A + diag(g)) y = b by the plan (or by relaxation); mass and
 // field update.
 template <int W, int KV>
-__device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
+__device__ __forceinline__ void field_step(Ctx& c, const KParams& P, int* sy) {
     const SBK_C DevLayout* L = c.L;
     const SBK_C DevScen* S = c.S;
     const double ambient = c.row[RW_AMB_K];
@@ -2296,7 +2296,7 @@ __device__ __forceinline__ void field_step(Ctx& c, const KParams& P) {
         return;
     } else {
     const int vb = L->vec_base;
-    copy_slot_init(slots, L->slot_init, vb);   // incl. 0.0 and 1.0 slots
+    env_wait(sy + SY_SLOTS, 1);   // the helper's copy of the slots' starting values [0, vb)
     // room cells carry their zone's heat; every node then gets its solar gain
     for (int z = ln(); z < L->nz; z += W) {
         double qz = c.zq[z];
@@ -2662,7 +2662,7 @@ static_assert(sizeof(Log) == 52 && offsetof(Log, comfort_dev_K) == 16 && offseto
 // there, the reward's non-AHU half (gas, pump, productivity and the comfort
 // diagnostics) goes to the first wavefront, which computes the AHU half
 // meanwhile. Each wait is for a post the first wavefront always makes.
-template <int W>
+template <int W, int KV>
 __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, unsigned char* env, float* obs_row,
                                             int kk, int j) {
     const SBK_C DevLayout* L = c.L;
@@ -2687,6 +2687,13 @@ __device__ __forceinline__ void helper_step(Ctx& c, const KParams& P, int* sy, u
             c.atotal[ln()] = c.t.ahu_area()[ln()];
         }
         env_post(sy + SY_RET, 1);
+    }
+    if constexpr (KV == KV_LU) {
+        // the LU slots' starting values (the permuted matrix, the zero and
+        // one slots), copied while the first wavefront runs the pre-step; its
+        // field step waits for this post instead of copying them
+        copy_slot_init(c.slots, L->slot_init, L->vec_base);
+        env_post(sy + SY_SLOTS, 1);
     }
     uint8_t* st_new = env + L->lds.occn;
     uint8_t* v_new = st_new + nocc;
@@ -2835,7 +2842,7 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P0) {
     const int kk0 = c.ip[PI_STEP_INDEX], st0 = c.ip[PI_STEP];
     c.row = cal_section(c, kk0);
     if (helper) {
-        if (!reset_mode) helper_step<W>(c, P, sy, env, P.obs + (size_t)e * 1024, kk0, ed.start + st0 + 1);
+        if (!reset_mode) helper_step<W, KV>(c, P, sy, env, P.obs + (size_t)e * 1024, kk0, ed.start + st0 + 1);
         return;
     }
     STAMP(1);
@@ -2860,7 +2867,7 @@ __global__ __launch_bounds__(512) void step_kernel(KParams P0) {
         step_post<W>(c);             // boiler update: reads the pre-step results, not the field
         env_post(sy + SY_PRE, 1);    // the helper's observation reads the state as of here
         STAMP(4);
-        field_step<W, KV>(c, P);
+        field_step<W, KV>(c, P, sy);
         if (c.conv) {
             env_wait(sy + SY_CONV, 1);   // the helper's permutation of the room cells
             conv_apply<W>(c);
