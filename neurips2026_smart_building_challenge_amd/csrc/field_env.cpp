@@ -73,6 +73,7 @@ struct FieldScen {
     hipStream_t side = nullptr;
     hipEvent_t fork = nullptr, join = nullptr;
     SbxFdm* fdm = nullptr;
+    int exact = 0;                // SBX_FDM_EXACT: the zone means sum in the reference's order too
 };
 
 bool field_blob(const sbh::Blob& b) {
@@ -554,6 +555,7 @@ sbe::Args base_args(const FieldScen* f) {
     a.cv_vals = f->d_vals;
     a.cv_spill = f->d_spill;
     a.cv_lds_pairs = f->lds_pairs;
+    a.exact = f->exact;
     return a;
 }
 
@@ -571,6 +573,7 @@ bool field_attach(FieldScen* f, const std::string& path, const std::vector<sbe::
     for (auto& e : f->fix) *e.first = f->d_tables + e.second;
     f->A.host.clear();
     f->A.host.shrink_to_fit();
+    f->exact = (flags & SBX_FDM_EXACT) ? 1 : 0;
     f->fdm = sbx_fdm_open(path.c_str(), G, envs_per_block, flags);
     if (!f->fdm) return (*err = std::string("field group: ") + sbx_last_error()), false;
     if (f->fdm->tab.k != f->t.k || f->fdm->tab.nz != f->t.nz || f->fdm->tab.n != f->t.n_solved)

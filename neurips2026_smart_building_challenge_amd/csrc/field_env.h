@@ -224,6 +224,7 @@ struct Args {
     double* cv_vals;              // [G][cv_cells]
     unsigned int* cv_spill;       // [G][2][cv_max_room]: pairs, then shuffle draws, past the LDS
     int cv_lds_pairs;             // pairs the plan kernel keeps in LDS
+    int exact;                    // the field group runs in exact mode (SBX_FDM_EXACT): sums in the reference's order
 };
 
 // The host (g++) and the device (hipcc) compile these structs separately and

@@ -785,31 +785,88 @@ __global__ __launch_bounds__(W) void fe_pre_kernel(Args a) {
     stage_out(g, lds, a.st.bytes);
 }
 
-// Zone means of the new field: lane per (zone, env), envs of one zone on
-// adjacent lanes (they read the same cells), the room's cells in order, eight
-// loads in flight ahead of the sequential sum.
-__global__ void fe_means_kernel(Args a) {
-    const int x = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+// Zone means of the new field: one wavefront per (zone, env), the pairs
+// zone-major (the envs of a zone read the same cell list). The lanes load
+// 8 x 64 consecutive entries of the room's cell list a round (the next round's
+// in flight while the current one is summed). In exact mode lane 0 adds them
+// from LDS in the list's order, so the sum is the sequential one over the
+// room's cells (csim's); otherwise each lane sums its own entries and a
+// wavefront tree combines the lanes (reassociated, as the default mode's
+// field solve is: its results agree with the reference within rounding).
+constexpr int kMeansWaves = 4, kMeansChunks = 8;
+__device__ __forceinline__ void means_load(double (&v)[kMeansChunks], const double* T, const int* cells, int q,
+                                           int c1, int ln, int Gl) {
+    int c[kMeansChunks];
+#pragma unroll
+    for (int u = 0; u < kMeansChunks; u++) {
+        const int i = q + 64 * u + ln;
+        c[u] = i < c1 ? cells[i] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < kMeansChunks; u++) v[u] = c[u] >= 0 ? T[(size_t)c[u] * Gl] : 0.0;
+}
+__device__ __forceinline__ void wave_order() {
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+}
+__global__ __launch_bounds__(64 * kMeansWaves) void fe_means_kernel(Args a) {
+    constexpr int R = 64 * kMeansChunks;
+    __shared__ __align__(16) double buf[kMeansWaves][R];
+    const int w = (int)(threadIdx.x >> 6), ln = (int)(threadIdx.x & 63);
+    const int p = (int)blockIdx.x * kMeansWaves + w;
     const int nz = a.t.nz;
-    if (x >= a.G * nz) return;
-    const int z = x / a.G, s = x % a.G;
+    if (p >= a.G * nz) return;   // wave-uniform; the kernel has no workgroup barrier
+    const int z = p / a.G, s = p % a.G;
     const size_t b = (size_t)(s / a.Gl), l = (size_t)(s % a.Gl);
     const double* T = a.T + b * (size_t)a.t.n_cvs * a.Gl + l;
     const int* cells = a.t.zcells;
     const int c0 = a.t.zoff[z], c1 = a.t.zoff[z + 1];
+    double* bw = buf[w];
     double sum = 0.0;
-    int q = c0;
-    constexpr int U = 8;
-    for (; q + U <= c1; q += U) {
-        double v[U];
+    double v[kMeansChunks], vn[kMeansChunks];
+    means_load(v, T, cells, c0, c1, ln, a.Gl);
+    if (!a.exact) {
+        for (int q = c0; q < c1; q += R) {
+            if (q + R < c1) means_load(vn, T, cells, q + R, c1, ln, a.Gl);
 #pragma unroll
-        for (int u = 0; u < U; u++) v[u] = T[(size_t)cells[q + u] * a.Gl];
+            for (int u = 0; u < kMeansChunks; u++) sum += v[u];
 #pragma unroll
-        for (int u = 0; u < U; u++) sum += v[u];
+            for (int u = 0; u < kMeansChunks; u++) v[u] = vn[u];
+        }
+        for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+        if (ln == 0) {
+            unsigned char* rec = a.state + (size_t)s * a.st.record;
+            reinterpret_cast<double*>(rec + a.st.avg_temp)[z] = sum / (double)(c1 - c0);
+        }
+        return;
     }
-    for (; q < c1; q++) sum += T[(size_t)cells[q] * a.Gl];
-    unsigned char* rec = a.state + (size_t)s * a.st.record;
-    reinterpret_cast<double*>(rec + a.st.avg_temp)[z] = sum / (double)(c1 - c0);
+    for (int q = c0; q < c1; q += R) {
+        if (q + R < c1) means_load(vn, T, cells, q + R, c1, ln, a.Gl);
+#pragma unroll
+        for (int u = 0; u < kMeansChunks; u++) bw[64 * u + ln] = v[u];
+        wave_order();
+        if (ln == 0) {
+            const int m = c1 - q;
+            if (m >= R) {
+#pragma unroll 8
+                for (int i = 0; i < R; i += 2) {
+                    const double2 t = *reinterpret_cast<const double2*>(bw + i);
+                    sum += t.x;
+                    sum += t.y;
+                }
+            } else {
+                for (int i = 0; i < m; i++) sum += bw[i];
+            }
+        }
+        wave_order();
+#pragma unroll
+        for (int u = 0; u < kMeansChunks; u++) v[u] = vn[u];
+    }
+    if (ln == 0) {
+        unsigned char* rec = a.state + (size_t)s * a.st.record;
+        reinterpret_cast<double*>(rec + a.st.avg_temp)[z] = sum / (double)(c1 - c0);
+    }
 }
 
 // After the field step and the zone means: observation, occupancy, reward,
@@ -1240,8 +1297,8 @@ extern "C" int sbe_launch(const sbe::Args* a, int which, hipStream_t s) {
     switch (which) {
     case 0: hipLaunchKernelGGL(fe_pre_kernel, dim3(G), dim3(64), a->lds_bytes, s, *a); break;
     case 1: {
-        const int n = G * a->t.nz;
-        hipLaunchKernelGGL(fe_means_kernel, dim3((n + 63) / 64), dim3(64), 0, s, *a);
+        const int n = G * a->t.nz;   // (zone, env) pairs, one wavefront each
+        hipLaunchKernelGGL(fe_means_kernel, dim3((n + kMeansWaves - 1) / kMeansWaves), dim3(64 * kMeansWaves), 0, s, *a);
         break;
     }
     case 2: hipLaunchKernelGGL(fe_post_kernel, dim3(G), dim3(64), a->lds_bytes, s, *a); break;
