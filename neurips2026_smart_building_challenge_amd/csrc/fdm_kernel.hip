@@ -474,6 +474,107 @@ __global__ __launch_bounds__(64) void dense_kernel(sbf::Tables t, sbf::Group g, 
     }
 }
 
+// The same solve per env with M, the power row and the step's row factors in
+// LDS, one workgroup of kDenseThreads per env (k <= kDenseLdsK). Every value
+// sees the operations of sb_fdm.c:9-38 in their order: the pivot is the first
+// row reaching the largest |M[r][c]| over r >= c (NaNs never win; row c stays
+// when |M[c][c]| is NaN), as the sequential strictly-greater scan picks it;
+// the rows' factors f = M[r][c] / d are taken before the step's updates;
+// M[r][j] -= f M[c][j] for j >= c (the product rounded: this file is built
+// without contraction) and b[r] -= f b[c], rows with f == 0 skipped; then
+// lane 0 back-substitutes row by row, each row's terms in ascending column.
+constexpr int kDenseThreads = 256, kDenseLdsK = 89;
+__global__ __launch_bounds__(kDenseThreads) void dense_lds_kernel(sbf::Tables t, sbf::Group g, sbf::StepIn in) {
+    extern __shared__ __align__(16) double dl[];
+    __shared__ int s_piv, s_sing;
+    const int env = blockIdx.x, k = t.k, tid = threadIdx.x;
+    const double* gv = in.g + (size_t)env * k;
+    int any = 0;
+    for (int i = tid; i < k; i += kDenseThreads) any |= gv[i] != 0.0;
+    any = __syncthreads_or(any);
+    if (tid == 0) {
+        g.eact[env] = any;
+        if (any) atomicOr(&g.bact[env / g.Gl], 1);
+    }
+    if (!any) return;   // workgroup-uniform
+    double* M = dl;             // [k][k]
+    double* bv = dl + k * k;    // [k]
+    double* fr = bv + k;        // [k]: the step's row factors
+    double* pw = g.pw + (size_t)env * k;
+    for (int x = tid; x < k * k; x += kDenseThreads) {
+        const int i = x / k, j = x % k;
+        M[x] = (i == j ? 1.0 : 0.0) + gv[i] * t.S[x];
+    }
+    for (int i = tid; i < k; i += kDenseThreads) bv[i] = pw[i];
+    __syncthreads();
+    for (int c = 0; c < k; c++) {
+        if (tid < 64) {
+            double m = -1.0;
+            for (int r = c + tid; r < k; r += 64) {
+                const double v = fabs(M[r * k + c]);
+                if (v > m) m = v;
+            }
+            for (int o = 32; o > 0; o >>= 1) m = fmax(m, __shfl_xor(m, o));
+            int first = k;
+            for (int r = c + tid; r < k; r += 64)
+                if (fabs(M[r * k + c]) == m) {
+                    first = r;
+                    break;
+                }
+            for (int o = 32; o > 0; o >>= 1) first = min(first, __shfl_xor(first, o));
+            if (tid == 0) {
+                const double vc = fabs(M[c * k + c]);
+                const bool nan_c = vc != vc;
+                s_piv = nan_c ? c : first;
+                s_sing = !nan_c && m == 0.0;
+            }
+        }
+        __syncthreads();
+        if (s_sing) {
+            // the reference returns here, leaving the partly reduced row
+            for (int i = tid; i < k; i += kDenseThreads) pw[i] = bv[i];
+            return;
+        }
+        const int piv = s_piv;
+        if (piv != c) {
+            for (int j = c + tid; j < k; j += kDenseThreads) {
+                const double x = M[c * k + j];
+                M[c * k + j] = M[piv * k + j];
+                M[piv * k + j] = x;
+            }
+            if (tid == 0) {
+                const double x = bv[c];
+                bv[c] = bv[piv];
+                bv[piv] = x;
+            }
+            __syncthreads();
+        }
+        const double d = M[c * k + c];
+        for (int r = c + 1 + tid; r < k; r += kDenseThreads) fr[r] = M[r * k + c] / d;
+        __syncthreads();
+        const int nc = k - c, nx = (k - c - 1) * nc;
+        for (int x = tid; x < nx; x += kDenseThreads) {
+            const int r = c + 1 + x / nc, j = c + x % nc;
+            const double f = fr[r];
+            if (f != 0.0) M[r * k + j] -= f * M[c * k + j];
+        }
+        for (int r = c + 1 + tid; r < k; r += kDenseThreads) {
+            const double f = fr[r];
+            if (f != 0.0) bv[r] -= f * bv[c];
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        for (int r = k - 1; r >= 0; r--) {
+            double s = bv[r];
+            for (int j = r + 1; j < k; j++) s -= M[r * k + j] * bv[j];
+            bv[r] = s / M[r * k + r];
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < k; i += kDenseThreads) pw[i] = bv[i];
+}
+
 // The applied heat of the solved powers (sb_fdm.c:171-177), permuted into the
 // correction's right-hand side; zero for envs without an air side.
 __global__ void applied_kernel(sbf::Tables t, sbf::Group g) {
@@ -746,7 +847,11 @@ extern "C" int sbf_launch_step(const sbf::Tables* t, const sbf::Group* g, const 
         else
             hipLaunchKernelGGL(sensed_kernel, dim3(elt_grid((size_t)g->G * t->k)), dim3(kEltThreads), 0, s, *t, *g,
                                *in);
-        hipLaunchKernelGGL(dense_kernel, dim3(g->G), dim3(64), 0, s, *t, *g, *in);
+        if (t->k <= kDenseLdsK)
+            hipLaunchKernelGGL(dense_lds_kernel, dim3(g->G), dim3(kDenseThreads),
+                               sizeof(double) * ((size_t)t->k * t->k + 2 * (size_t)t->k), s, *t, *g, *in);
+        else
+            hipLaunchKernelGGL(dense_kernel, dim3(g->G), dim3(64), 0, s, *t, *g, *in);
         if (t->R) {
             // the correction as R^T q, fused with the mass and field update
             const size_t tiles = ((size_t)t->n + 63) / 64, egs = ((size_t)g->G + 4 * kREnvs - 1) / (4 * kREnvs);
