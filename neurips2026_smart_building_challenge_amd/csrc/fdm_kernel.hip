@@ -101,23 +101,50 @@ __device__ __forceinline__ double lane_sum(double v) {
 }
 
 // Head terms of the tail rows (columns finished before the tail's first
-// level): W[row] -= their sum, one wavefront per (block, tail row), the terms
-// spread over the lanes of each env.
+// level): W[row] -= their sum, one wavefront per (group of kHeadBlocks blocks,
+// tail row), block groups outermost (each block's vector stays in the caches
+// from row to row), the terms spread over the lanes of each env. A term's
+// value and column are loaded once for the group's blocks, so the factor's
+// head terms are read once per kHeadBlocks blocks; every env's sum has the
+// same terms per lane, order and lane tree as with one block per wavefront.
+constexpr int kHeadBlocks = 8;
 template <int GL>
 __global__ __launch_bounds__(256) void head_kernel(sbf::Tail tl, int n, int nblk, double* W, const int* bact) {
-    constexpr int S = 64 / GL;
+    constexpr int S = 64 / GL, E = kHeadBlocks;
     const int lane = threadIdx.x & 63;
     const int gl = lane % GL, s = lane / GL;
+    const int nbg = (nblk + E - 1) / E;
     const size_t nw = (size_t)gridDim.x * (blockDim.x >> 6);
-    for (size_t x = (size_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); x < (size_t)nblk * tl.m; x += nw) {
-        const int b = (int)(x / tl.m), r = (int)(x % tl.m);
-        if (bact && !bact[b]) continue;
-        double* Wb = W + (size_t)b * n * GL;
-        double acc = 0.0;
+    for (size_t x = (size_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); x < (size_t)nbg * tl.m; x += nw) {
+        const int bg = (int)(x / tl.m), r = (int)(x % tl.m);
+        bool on[E];
+        double* Wb[E];
+        double acc[E];
+        bool any = false;
+#pragma unroll
+        for (int k = 0; k < E; k++) {
+            const int b = bg * E + k;
+            on[k] = b < nblk && (!bact || bact[b]);   // wavefront-uniform
+            any |= on[k];
+            Wb[k] = W + (size_t)(b < nblk ? b : 0) * n * GL;
+            acc[k] = 0.0;
+        }
+        if (!any) continue;
         const int e1 = tl.hptr[r + 1];
-        for (int e = tl.hptr[r] + s; e < e1; e += S) acc += tl.hval[e] * Wb[(size_t)tl.hcol[e] * GL + gl];
-        acc = lane_sum<GL>(acc);
-        if (s == 0) Wb[(size_t)tl.rows[r] * GL + gl] -= acc;
+        for (int e = tl.hptr[r] + s; e < e1; e += S) {
+            const double v = tl.hval[e];
+            const size_t c = (size_t)tl.hcol[e] * GL + gl;
+#pragma unroll
+            for (int k = 0; k < E; k++)
+                if (on[k]) acc[k] += v * Wb[k][c];
+        }
+        const size_t row = (size_t)tl.rows[r] * GL + gl;
+#pragma unroll
+        for (int k = 0; k < E; k++) {
+            if (!on[k]) continue;
+            const double t = lane_sum<GL>(acc[k]);
+            if (s == 0) Wb[k][row] -= t;
+        }
     }
 }
 
@@ -783,7 +810,7 @@ void sweep(const sbf::Tri& tri, const sbf::Sweep* sw, const sbf::Group& g, int n
     const sbf::Tail& mid = sw->mid;
     if (mid.nlev > 0) {
         if (mid.lev0 > 0) {
-            const size_t waves = (size_t)g.nblk * mid.m;
+            const size_t waves = (size_t)((g.nblk + kHeadBlocks - 1) / kHeadBlocks) * mid.m;
             const int grid = (int)std::min<size_t>((waves + 3) / 4, 8192);
             hipLaunchKernelGGL((head_kernel<GL>), dim3(grid), dim3(256), 0, s, mid, n, g.nblk, W, bact);
         }
