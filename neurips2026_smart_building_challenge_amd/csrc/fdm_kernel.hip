@@ -367,36 +367,42 @@ __device__ __forceinline__ double sensed_dot(const int* wrow, const double* x, i
 
 // Forcing (sb_fdm.c:147-151, exposure :126-140) of every solved cell t, in
 // the cells' order (the field, the heat input and the mass read in order),
-// written to its row ipr[t] of the permuted vector; clears the blocks'
-// air-side flags.
+// written to its row ipr[t] of the permuted vector; one thread per (group of
+// kForceBlocks blocks, cell, lane), so the cell's tables are read once for the
+// group's envs; clears the blocks' air-side flags.
+constexpr int kForceBlocks = 8;
 __global__ void forcing_kernel(sbf::Tables t, sbf::Group g, sbf::StepIn in) {
     const int n = t.n, Gl = g.Gl, G = g.G;
-    const size_t total = (size_t)g.nblk * n * Gl;
+    const int nbg = (g.nblk + kForceBlocks - 1) / kForceBlocks;
+    const size_t total = (size_t)nbg * n * Gl;
     for (size_t x = gtid(); x < total; x += gstride()) {
         const int l = (int)(x % Gl);
         const size_t bt = x / Gl;
-        const int tt = (int)(bt % n), b = (int)(bt / n);
-        const int env = b * Gl + l;
-        double w = 0.0;
-        if (env < G) {
-            const int p = t.solved[tt];
-            const double h = in.h[env];
-            double e = 0.0;
-            const double a0 = t.a0[tt];
-            if (a0 > 0.0) e += h * a0 / (1.0 + h * 0.5 * t.hz[tt] / t.cd[tt]);
-            const double a1 = t.a1[tt];
-            if (a1 > 0.0) e += h * a1 / (1.0 + h * 0.5 * t.vt[tt] / t.cd[tt]);
-            double q;
-            if (in.q) {
-                q = in.q[(size_t)env * t.n_cvs + p];
-            } else {
-                const int z = t.czone[tt];
-                q = z >= 0 ? in.qz[(size_t)env * t.nz + z] : 0.0;
+        const int tt = (int)(bt % n), bg = (int)(bt / n);
+        const int p = t.solved[tt];
+        const double a0 = t.a0[tt], a1 = t.a1[tt], hz = t.hz[tt], vt = t.vt[tt], cd = t.cd[tt];
+        const double cap = t.cap[tt], dir = t.dir[tt], mcoup = t.mcoup[tt];
+        const int z = in.q ? -1 : t.czone[tt];
+        const int row = t.ipr[tt];
+#pragma unroll
+        for (int k = 0; k < kForceBlocks; k++) {
+            const int b = bg * kForceBlocks + k;
+            if (b >= g.nblk) break;
+            const int env = b * Gl + l;
+            double w = 0.0;
+            if (env < G) {
+                const double h = in.h[env];
+                double e = 0.0;
+                if (a0 > 0.0) e += h * a0 / (1.0 + h * 0.5 * hz / cd);
+                if (a1 > 0.0) e += h * a1 / (1.0 + h * 0.5 * vt / cd);
+                double q;
+                if (in.q) q = in.q[(size_t)env * t.n_cvs + p];
+                else q = z >= 0 ? in.qz[(size_t)env * t.nz + z] : 0.0;
+                w = cap * g.T[((size_t)b * t.n_cvs + p) * Gl + l] + q + in.amb[env] * (dir + e)
+                    + mcoup * g.M[((size_t)b * n + tt) * Gl + l];
             }
-            w = t.cap[tt] * g.T[((size_t)b * t.n_cvs + p) * Gl + l] + q + in.amb[env] * (t.dir[tt] + e)
-                + t.mcoup[tt] * g.M[x];
+            g.W1[((size_t)b * n + row) * Gl + l] = w;
         }
-        g.W1[((size_t)b * n + t.ipr[tt]) * Gl + l] = w;
     }
     if (gtid() < (size_t)g.nblk) g.bact[gtid()] = 0;
 }
@@ -865,7 +871,8 @@ hipError_t run_limit(int bytes) {
 // One batched step of a group (all launches on stream s).
 extern "C" int sbf_launch_step(const sbf::Tables* t, const sbf::Group* g, const sbf::StepIn* in, hipStream_t s) {
     const size_t rows = (size_t)g->nblk * t->n * g->Gl;
-    hipLaunchKernelGGL(forcing_kernel, dim3(elt_grid(rows)), dim3(kEltThreads), 0, s, *t, *g, *in);
+    const size_t fitems = (size_t)((g->nblk + kForceBlocks - 1) / kForceBlocks) * t->n * g->Gl;
+    hipLaunchKernelGGL(forcing_kernel, dim3(elt_grid(fitems)), dim3(kEltThreads), 0, s, *t, *g, *in);
     if (int e = solve(*t, *g, g->W1, nullptr, false, s)) return e;
     if (t->k > 0) {
         if (t->fast)
