@@ -428,10 +428,10 @@ extern "C" int sbk_launch_policy(const float* obs, const float* w1, const float*
     if (obs_cols < 1 || obs_cols > kObsWidth) return (int)hipErrorInvalidValue;
     const int mt = (n + 15) / 16;
     // K split over 8 wavefronts (layer 1, K = 1024; the observation's zero
-    // tail past obs_cols skipped) or 2 (K = 128)
+    // tail past obs_cols skipped) or 4 (K = 128)
     hipLaunchKernelGGL((mlp_layer_kernel<1, kObsWidth / 8>), dim3(mt, kPolicyHidden / 16), dim3(512), 0, s, obs,
                        kObsWidth, w1, b1, h1, kPolicyHidden, n, kPolicyHidden, obs_cols);
-    hipLaunchKernelGGL((mlp_layer_kernel<1, kPolicyHidden / 2>), dim3(mt, kPolicyHidden / 16), dim3(128), 0, s, h1,
+    hipLaunchKernelGGL((mlp_layer_kernel<1, kPolicyHidden / 4>), dim3(mt, kPolicyHidden / 16), dim3(256), 0, s, h1,
                        kPolicyHidden, w2, b2, h2, kPolicyHidden, n, kPolicyHidden, kPolicyHidden);
     // third layer and the Beta draws in one launch per (env tile, head group)
     hipLaunchKernelGGL(heads_layer_kernel, dim3(mt, kHeadGroups), dim3(256), 0, s, h2, w3, b3, y, actions, n_cont,
